@@ -1,0 +1,197 @@
+"""Deterministic synthetic inputs for the packed-weight hot path.
+
+There is no checkpoint to load, so every workload is built from seeded
+generators with the shapes and distributions of the reference codecs:
+
+* expert matrices: Mach-1 K=1.5/V=8 trellis, 24 u16 words per 16x16 tile,
+  uniform random words; f16 `su` (per input column), `sv` (per output row) and
+  `wave_gamma` (per anti-diagonal tile wave) drawn lognormal(0, 0.5);
+* non-expert matrices: K=4/V=2 trellis, 64 u16 words per tile, uniform random
+  words; +-1 int8 `SU`/`SV`; one lognormal(0, 0.5) f32 `Wscale`;
+* codebooks: expert TLUT 32768x8 and NE TLUT 512x2 f32, uniform in [-1, 1);
+* int5_g64 output head: uniform packed bytes, f16 per-64-column scales
+  lognormal(0, 0.5), optional bf16 protected rows;
+* router and shared-expert gate: f32 N(0, 0.02) rounded to bf16 (RNE);
+* hidden states N(0, 1) f32;
+* prefill routing skew: fp32 logit bias -s*ln(rank_e) with rank a seeded
+  permutation of 1..experts (s = 1.1), added after the router matvec.
+
+f16 rounding uses numpy's float16 conversion (round-to-nearest-even with
+subnormals), which equals the reference's f32_to_f16 on finite values.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+import numpy as np
+
+EXPERT_WORDS_PER_TILE = 24
+NE_WORDS_PER_TILE = 64
+SEED_BASE = 0xAD1C0000
+
+
+def f16_bits(values: np.ndarray) -> np.ndarray:
+    return np.asarray(values, np.float32).astype(np.float16).view(np.uint16)
+
+
+def bf16_bits_rne(values: np.ndarray) -> np.ndarray:
+    bits = np.ascontiguousarray(values, np.float32).view(np.uint32).astype(np.uint64)
+    rounding = 0x7FFF + ((bits >> 16) & 1)
+    return ((bits + rounding) >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, np.uint32) << 16).view(np.float32)
+
+
+def f16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
+
+
+@dataclass
+class ExpertMatrix:
+    rows: int
+    columns: int
+    trellis: np.ndarray        # u16 [tiles*24]
+    su_f16: np.ndarray         # u16 [columns]
+    sv_f16: np.ndarray         # u16 [rows]
+    wave_gamma_f16: np.ndarray # u16 [rows/16 + columns/16]
+    tlut: np.ndarray           # f32 [32768*8]
+
+
+@dataclass
+class NeMatrix:
+    rows: int
+    columns: int
+    trellis: np.ndarray  # u16 [tiles*64]
+    su: np.ndarray       # i8 [columns]
+    sv: np.ndarray       # i8 [rows]
+    weight_scale: float
+    tlut: np.ndarray     # f32 [512*2]
+
+
+@dataclass
+class HeadChunk:
+    rows: int
+    columns: int
+    packed: np.ndarray           # u8 [rows*columns/8*5]
+    group_scale_f16: np.ndarray  # u16 [rows*columns/64]
+    protected_rows: Optional[np.ndarray] = None  # u32 [p]
+    protected_bf16: Optional[np.ndarray] = None  # u16 [p*columns]
+
+
+@dataclass
+class MoeLayer:
+    hidden: int
+    expert_hidden: int
+    experts: int
+    router_bf16: np.ndarray              # u16 [experts, hidden]
+    shared_expert_gate_bf16: np.ndarray  # u16 [1, hidden]
+    gate: List[ExpertMatrix] = field(default_factory=list)
+    up: List[ExpertMatrix] = field(default_factory=list)
+    down: List[ExpertMatrix] = field(default_factory=list)
+    shared_gate: Optional[NeMatrix] = None
+    shared_up: Optional[NeMatrix] = None
+    shared_down: Optional[NeMatrix] = None
+    expert_tlut: Optional[np.ndarray] = None
+    ne_tlut: Optional[np.ndarray] = None
+
+
+def rng_for(config_index: int, salt: int = 0) -> np.random.Generator:
+    return np.random.default_rng([SEED_BASE + config_index, salt])
+
+
+def lognormal_f16(rng: np.random.Generator, count: int) -> np.ndarray:
+    return f16_bits(rng.lognormal(0.0, 0.5, count).astype(np.float32))
+
+
+def expert_tlut(rng: np.random.Generator) -> np.ndarray:
+    return rng.uniform(-1.0, 1.0, 32768 * 8).astype(np.float32)
+
+
+def ne_tlut(rng: np.random.Generator) -> np.ndarray:
+    return rng.uniform(-1.0, 1.0, 512 * 2).astype(np.float32)
+
+
+def uniform_words(rng: np.random.Generator, count: int) -> np.ndarray:
+    return rng.integers(0, 1 << 16, count, dtype=np.uint32).astype(np.uint16)
+
+
+def expert_matrix(rng, rows: int, columns: int, tlut: np.ndarray) -> ExpertMatrix:
+    tiles = (rows // 16) * (columns // 16)
+    return ExpertMatrix(
+        rows, columns,
+        uniform_words(rng, tiles * EXPERT_WORDS_PER_TILE),
+        lognormal_f16(rng, columns),
+        lognormal_f16(rng, rows),
+        lognormal_f16(rng, rows // 16 + columns // 16),
+        tlut,
+    )
+
+
+def ne_matrix(rng, rows: int, columns: int, tlut: np.ndarray) -> NeMatrix:
+    tiles = (rows // 16) * (columns // 16)
+    signs = lambda n: np.where(rng.integers(0, 2, n) == 0, -1, 1).astype(np.int8)
+    return NeMatrix(
+        rows, columns,
+        uniform_words(rng, tiles * NE_WORDS_PER_TILE),
+        signs(columns), signs(rows),
+        float(np.float32(rng.lognormal(0.0, 0.5))),
+        tlut,
+    )
+
+
+def head_chunk(rng, rows: int, columns: int, protected: int = 0) -> HeadChunk:
+    packed = rng.integers(0, 256, rows * columns // 8 * 5, dtype=np.uint32).astype(np.uint8)
+    scales = lognormal_f16(rng, rows * (columns // 64))
+    head = HeadChunk(rows, columns, packed, scales)
+    if protected:
+        head.protected_rows = np.sort(rng.choice(rows, protected, replace=False)).astype(np.uint32)
+        head.protected_bf16 = bf16_bits_rne(rng.normal(0.0, 0.02, protected * columns).astype(np.float32))
+    return head
+
+
+def hidden_states(rng, batch: int, hidden: int) -> np.ndarray:
+    return rng.standard_normal((batch, hidden)).astype(np.float32)
+
+
+def rms_normalized(x: np.ndarray, epsilon: float = 1e-6) -> np.ndarray:
+    """RMSNorm with unit weight (bf16 zero weight plus offset 1.0, as the
+    model applies its final norm), in the reference's order: a sequential
+    fp32 sum of squares, then x*scale*1.0 (src/kernels.cpp:1052-1073)."""
+    out = np.empty_like(x, dtype=np.float32)
+    for b in range(x.shape[0]):
+        row = x[b].astype(np.float32)
+        squares = np.float32(0.0)
+        for v in row:
+            squares = np.float32(squares + np.float32(v * v))
+        scale = np.float32(1.0) / np.sqrt(np.float32(squares / np.float32(row.size) + np.float32(epsilon)))
+        out[b] = (row * scale) * np.float32(1.0)
+    return out
+
+
+def zipf_bias(rng, experts: int, s: float = 1.1) -> np.ndarray:
+    ranks = rng.permutation(experts) + 1
+    return (-np.float32(s) * np.log(ranks.astype(np.float32))).astype(np.float32)
+
+
+def moe_layer(rng, hidden: int = 2048, expert_hidden: int = 512, experts: int = 256,
+              etlut: Optional[np.ndarray] = None,
+              ntlut: Optional[np.ndarray] = None) -> MoeLayer:
+    etlut = expert_tlut(rng) if etlut is None else etlut
+    ntlut = ne_tlut(rng) if ntlut is None else ntlut
+    layer = MoeLayer(
+        hidden, expert_hidden, experts,
+        bf16_bits_rne(rng.normal(0.0, 0.02, (experts, hidden)).astype(np.float32)),
+        bf16_bits_rne(rng.normal(0.0, 0.02, (1, hidden)).astype(np.float32)),
+        expert_tlut=etlut, ne_tlut=ntlut,
+    )
+    for _ in range(experts):
+        layer.gate.append(expert_matrix(rng, expert_hidden, hidden, etlut))
+        layer.up.append(expert_matrix(rng, expert_hidden, hidden, etlut))
+        layer.down.append(expert_matrix(rng, hidden, expert_hidden, etlut))
+    layer.shared_gate = ne_matrix(rng, expert_hidden, hidden, ntlut)
+    layer.shared_up = ne_matrix(rng, expert_hidden, hidden, ntlut)
+    layer.shared_down = ne_matrix(rng, hidden, expert_hidden, ntlut)
+    return layer

@@ -1,0 +1,172 @@
+/*
+ * adi_oracle.h -- CPU restatement of ADI's packed-weight hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker that the HIP path is
+ * compared against; it is never part of the product path. Only tests,
+ * the smoke check and the benchmark's CPU-baseline leg may load it.
+ *
+ * Every function restates the arithmetic of the reference CPU path in its
+ * scalar order (the order every SIMD variant of the reference reproduces bit
+ * for bit), citing the reference file:line it follows. The two reductions whose
+ * order depends on the CPU ISA in the reference (int5 head dot, bf16 dot) take
+ * an explicit lane count: 1 = scalar, 8 = AVX2, 16 = AVX-512.
+ *
+ * Built with -ffp-contract=off: a fused multiply-add rounds differently from
+ * the reference's separate multiply and add.
+ */
+#ifndef ADI_ORACLE_H
+#define ADI_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    AO_OK = 0,
+    AO_INVALID_ARGUMENT = -1,
+    AO_OUT_OF_MEMORY = -2,
+};
+
+/* Mirrors adi::MachExpertMatrix (include/adi/kernels.hpp:9-20). */
+typedef struct {
+    uint32_t rows;
+    uint32_t columns;
+    const uint16_t *trellis;        /* (rows/16)*(columns/16)*24 words */
+    const uint16_t *su_f16;         /* columns */
+    const uint16_t *sv_f16;         /* rows */
+    const uint16_t *wave_gamma_f16; /* rows/16 + columns/16 */
+    const float *tlut;              /* 32768*8 */
+    const float *state_values;      /* optional 65536*8 cache, NULL = build */
+} ao_expert_matrix;
+
+/* Mirrors adi::MachNeMatrix (include/adi/kernels.hpp:42-52). */
+typedef struct {
+    uint32_t rows;
+    uint32_t columns;
+    const uint16_t *trellis;   /* (rows/16)*(columns/16)*64 words */
+    const int8_t *su;          /* columns, +-1 */
+    const int8_t *sv;          /* rows, +-1 */
+    float weight_scale;
+    const float *tlut;         /* 512*2 */
+    const float *state_values; /* optional 65536*2 cache, NULL = build */
+} ao_ne_matrix;
+
+/* Mirrors adi::MachHeadChunk (include/adi/kernels.hpp:64-71). */
+typedef struct {
+    uint32_t rows;
+    uint32_t columns;
+    const uint8_t *packed;           /* rows*columns/8*5 bytes */
+    const uint16_t *group_scale_f16; /* rows*columns/64 */
+    const uint32_t *protected_rows;  /* protected_count */
+    const uint16_t *protected_bf16;  /* protected_count*columns */
+    uint32_t protected_count;
+} ao_head_chunk;
+
+/* Mirrors adi::Bf16Matrix (include/adi/kernels.hpp:73-77). */
+typedef struct {
+    uint32_t rows;
+    uint32_t columns;
+    const uint16_t *values;
+} ao_bf16_matrix;
+
+/* One MoE block: the fields moe_forward reads from the model's layer
+ * descriptor (src/executor.cpp:254, 270-288, 300-324). */
+typedef struct {
+    uint32_t hidden;
+    uint32_t expert_hidden;
+    uint32_t experts;
+    ao_bf16_matrix router;             /* experts x hidden */
+    ao_bf16_matrix shared_expert_gate; /* 1 x hidden */
+    const ao_expert_matrix *expert_matrices; /* experts*3: gate, up, down */
+    ao_ne_matrix shared_gate;          /* expert_hidden x hidden */
+    ao_ne_matrix shared_up;            /* expert_hidden x hidden */
+    ao_ne_matrix shared_down;          /* hidden x expert_hidden */
+} ao_moe_layer;
+
+/* Conversions (src/kernels.cpp:309-383). */
+float ao_f16_to_f32(uint16_t bits);
+uint16_t ao_f32_to_f16(float value);
+float ao_bf16_to_f32(uint16_t bits);
+
+/* Trellis walks (src/expert_trellis.hpp:44-59, src/ne_trellis.hpp:27-41). */
+void ao_expert_tile_states(const uint16_t *words, uint16_t *states /*32*/);
+void ao_ne_tile_states(const uint16_t *words, uint16_t *states /*128*/);
+
+/* Codec caches (src/codec_cache.cpp:33-147). */
+void ao_build_expert_state_values(const float *tlut, float *out /*65536*8*/);
+void ao_build_ne_state_values(const float *tlut, float *out /*65536*2*/);
+void ao_build_ne_signed_tlut(const float *tlut, float *out /*1024*2*/);
+int ao_build_wave_indexes(uint32_t tile_rows, uint32_t tile_columns,
+                          uint16_t *out /*tile_rows*tile_columns*/);
+
+/* Normalised fast Walsh-Hadamard transform (src/simd.cpp:48-63). */
+int ao_hadamard(float *values, uint32_t count);
+
+/* Dense decoded weights of one projection, W[row][column], before su/sv and
+ * the Hadamard rotations (expert: includes the tile gamma as a separate
+ * output; NE: V*Wscale). Used to cross-check the tile walk by brute force. */
+int ao_expert_decode_tiles(const ao_expert_matrix *matrix, float *values /*rows*columns*/);
+int ao_ne_decode_tiles(const ao_ne_matrix *matrix, float *values /*rows*columns*/);
+
+/* Projections (src/kernels.cpp:385-800). Inputs [batch, columns] and outputs
+ * [batch, rows], batch-major. Scalar reference order. */
+int ao_expert_matmul(const ao_expert_matrix *matrix, const float *inputs,
+                     uint32_t batch, float *outputs);
+int ao_ne_matmul(const ao_ne_matrix *matrix, const float *inputs,
+                 uint32_t batch, float *outputs);
+
+/* Pre-Hadamard row sums Z (the tile accumulation alone, src/kernels.cpp:103-264,
+ * 433-482): inputs are already transformed (x_hat). */
+int ao_expert_accumulate(const ao_expert_matrix *matrix, const float *x_hat,
+                         uint32_t batch, float *row_sums);
+int ao_ne_accumulate(const ao_ne_matrix *matrix, const float *x_hat,
+                     uint32_t batch, float *row_sums);
+
+/* int5_g64 output head (src/kernels.cpp:847-979, src/simd.cpp:65-86,
+ * src/simd_x86_avx2.cpp:101-120, src/simd_x86_avx512.cpp:87-107). */
+int ao_head_matmul(const ao_head_chunk *head, const float *inputs,
+                   uint32_t batch, float *outputs, uint32_t lanes);
+
+/* bf16 dense (src/kernels.cpp:981-1050, src/simd.cpp:88-96,
+ * src/simd_x86_avx2.cpp:172-193, src/simd_x86_avx512.cpp:109-130). */
+float ao_bf16_dot(const uint16_t *weights, const float *input, uint32_t count,
+                  uint32_t lanes);
+int ao_bf16_matmul(const ao_bf16_matrix *matrix, const float *inputs,
+                   uint32_t batch, float *outputs, uint32_t lanes);
+
+/* RMS norm (src/kernels.cpp:1052-1073). */
+int ao_rms_norm(const float *input, const uint16_t *weight_bf16, uint32_t count,
+                float weight_offset, float epsilon, float *output);
+
+float ao_silu(float value);    /* src/kernels.cpp:1089-1091 */
+float ao_sigmoid(float value); /* src/kernels.cpp:1093-1095 */
+
+/* top_experts (src/executor.cpp:193-229). */
+int ao_top_experts(const float *logits, uint32_t count, uint32_t *experts,
+                   float *weights);
+
+/* Routing + stable counting sort of a batch (src/executor.cpp:1221-1258).
+ * logits [batch, experts]; route_expert/route_weight [batch*8];
+ * counts [experts]; offsets [experts+1]; grouped_batch and
+ * route_to_grouped [batch*8]. */
+int ao_moe_route(const float *logits, uint32_t batch, uint32_t experts,
+                 uint32_t *route_expert, float *route_weight, uint32_t *counts,
+                 uint32_t *offsets, uint32_t *grouped_batch,
+                 uint32_t *route_to_grouped);
+
+/* MoE block for a batch (src/executor.cpp:1181-1453; batch 1 equals
+ * moe_forward, src/executor.cpp:242-330). logit_bias (nullable, [experts]) is
+ * added to the router logits before top_experts. route_expert/route_weight
+ * (nullable) receive the routes. threads: 0 = OpenMP default. */
+int ao_moe_forward(const ao_moe_layer *layer, const float *inputs,
+                   uint32_t batch, const float *logit_bias, uint32_t lanes,
+                   float *outputs, uint32_t *route_expert, float *route_weight,
+                   int threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,334 @@
+"""ctypes bindings for the CPU checkers (TEST INFRASTRUCTURE ONLY).
+
+`liboracle.so` is the C restatement in adi_oracle.c; `_ref/libadi_ref.so` is
+the reference's own CPU path compiled from its sources (optional: present only
+where it was built). Only tests, the smoke check and the benchmark's
+CPU-baseline leg use this module; the product path never does.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Optional
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_PATH = os.path.join(HERE, "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libadi_ref.so")
+
+u16p = C.POINTER(C.c_uint16)
+u32p = C.POINTER(C.c_uint32)
+f32p = C.POINTER(C.c_float)
+i8p = C.POINTER(C.c_int8)
+u8p = C.POINTER(C.c_uint8)
+
+
+class ExpertMatrix(C.Structure):
+    _fields_ = [
+        ("rows", C.c_uint32), ("columns", C.c_uint32),
+        ("trellis", u16p), ("su_f16", u16p), ("sv_f16", u16p),
+        ("wave_gamma_f16", u16p), ("tlut", f32p), ("state_values", f32p),
+    ]
+
+
+class NeMatrix(C.Structure):
+    _fields_ = [
+        ("rows", C.c_uint32), ("columns", C.c_uint32),
+        ("trellis", u16p), ("su", i8p), ("sv", i8p),
+        ("weight_scale", C.c_float), ("tlut", f32p), ("state_values", f32p),
+    ]
+
+
+class HeadChunk(C.Structure):
+    _fields_ = [
+        ("rows", C.c_uint32), ("columns", C.c_uint32),
+        ("packed", u8p), ("group_scale_f16", u16p),
+        ("protected_rows", u32p), ("protected_bf16", u16p),
+        ("protected_count", C.c_uint32),
+    ]
+
+
+class Bf16Matrix(C.Structure):
+    _fields_ = [("rows", C.c_uint32), ("columns", C.c_uint32), ("values", u16p)]
+
+
+class MoeLayer(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_uint32), ("expert_hidden", C.c_uint32), ("experts", C.c_uint32),
+        ("router", Bf16Matrix), ("shared_expert_gate", Bf16Matrix),
+        ("expert_matrices", C.POINTER(ExpertMatrix)),
+        ("shared_gate", NeMatrix), ("shared_up", NeMatrix), ("shared_down", NeMatrix),
+    ]
+
+
+def ptr(array: Optional[np.ndarray], ctype):
+    if array is None:
+        return C.cast(None, C.POINTER(ctype))
+    assert array.flags["C_CONTIGUOUS"], "oracle arrays must be contiguous"
+    return array.ctypes.data_as(C.POINTER(ctype))
+
+
+def _declare(lib, name, restype, *argtypes):
+    fn = getattr(lib, name)
+    fn.restype = restype
+    fn.argtypes = list(argtypes)
+    return fn
+
+
+class _Common:
+    """Signatures shared by the oracle (ao_*) and the reference shim (ref_*)."""
+
+
+def load_oracle() -> C.CDLL:
+    if not os.path.exists(ORACLE_PATH):
+        raise RuntimeError(f"{ORACLE_PATH} is not built; run `make -C oracle`")
+    lib = C.CDLL(ORACLE_PATH)
+    _declare(lib, "ao_f16_to_f32", C.c_float, C.c_uint16)
+    _declare(lib, "ao_f32_to_f16", C.c_uint16, C.c_float)
+    _declare(lib, "ao_bf16_to_f32", C.c_float, C.c_uint16)
+    _declare(lib, "ao_expert_tile_states", None, u16p, u16p)
+    _declare(lib, "ao_ne_tile_states", None, u16p, u16p)
+    _declare(lib, "ao_build_expert_state_values", None, f32p, f32p)
+    _declare(lib, "ao_build_ne_state_values", None, f32p, f32p)
+    _declare(lib, "ao_build_ne_signed_tlut", None, f32p, f32p)
+    _declare(lib, "ao_build_wave_indexes", C.c_int, C.c_uint32, C.c_uint32, u16p)
+    _declare(lib, "ao_hadamard", C.c_int, f32p, C.c_uint32)
+    _declare(lib, "ao_expert_decode_tiles", C.c_int, C.POINTER(ExpertMatrix), f32p)
+    _declare(lib, "ao_ne_decode_tiles", C.c_int, C.POINTER(NeMatrix), f32p)
+    _declare(lib, "ao_expert_matmul", C.c_int, C.POINTER(ExpertMatrix), f32p, C.c_uint32, f32p)
+    _declare(lib, "ao_ne_matmul", C.c_int, C.POINTER(NeMatrix), f32p, C.c_uint32, f32p)
+    _declare(lib, "ao_expert_accumulate", C.c_int, C.POINTER(ExpertMatrix), f32p, C.c_uint32, f32p)
+    _declare(lib, "ao_ne_accumulate", C.c_int, C.POINTER(NeMatrix), f32p, C.c_uint32, f32p)
+    _declare(lib, "ao_head_matmul", C.c_int, C.POINTER(HeadChunk), f32p, C.c_uint32, f32p, C.c_uint32)
+    _declare(lib, "ao_bf16_dot", C.c_float, u16p, f32p, C.c_uint32, C.c_uint32)
+    _declare(lib, "ao_bf16_matmul", C.c_int, C.POINTER(Bf16Matrix), f32p, C.c_uint32, f32p, C.c_uint32)
+    _declare(lib, "ao_rms_norm", C.c_int, f32p, u16p, C.c_uint32, C.c_float, C.c_float, f32p)
+    _declare(lib, "ao_silu", C.c_float, C.c_float)
+    _declare(lib, "ao_sigmoid", C.c_float, C.c_float)
+    _declare(lib, "ao_top_experts", C.c_int, f32p, C.c_uint32, u32p, f32p)
+    _declare(lib, "ao_moe_route", C.c_int, f32p, C.c_uint32, C.c_uint32, u32p, f32p,
+             u32p, u32p, u32p, u32p)
+    _declare(lib, "ao_moe_forward", C.c_int, C.POINTER(MoeLayer), f32p, C.c_uint32, f32p,
+             C.c_uint32, f32p, u32p, f32p, C.c_int)
+    return lib
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_PATH)
+
+
+def load_ref() -> C.CDLL:
+    if not ref_available():
+        raise RuntimeError(f"{REF_PATH} is not built; run `make -C oracle ref`")
+    lib = C.CDLL(REF_PATH)
+    _declare(lib, "ref_selected_isa_lanes", C.c_int)
+    _declare(lib, "ref_force_isa_lanes", None, C.c_int)
+    _declare(lib, "ref_avx512_vbmi", C.c_int)
+    _declare(lib, "ref_worker_threads", C.c_uint32)
+    _declare(lib, "ref_f16_to_f32", C.c_float, C.c_uint16)
+    _declare(lib, "ref_f32_to_f16", C.c_uint16, C.c_float)
+    _declare(lib, "ref_silu", C.c_float, C.c_float)
+    _declare(lib, "ref_sigmoid", C.c_float, C.c_float)
+    _declare(lib, "ref_expert_tile_states", None, u16p, u16p)
+    _declare(lib, "ref_expert_row_states", None, u16p, u16p)
+    _declare(lib, "ref_ne_tile_states", None, u16p, u16p)
+    _declare(lib, "ref_ne_row_states", None, u16p, u16p)
+    _declare(lib, "ref_build_expert_state_values", None, f32p, f32p)
+    _declare(lib, "ref_build_ne_state_values", None, f32p, f32p)
+    _declare(lib, "ref_build_ne_signed_tlut", None, f32p, f32p)
+    _declare(lib, "ref_build_wave_indexes", C.c_int, C.c_uint32, C.c_uint32, u16p)
+    _declare(lib, "ref_hadamard", None, f32p, C.c_uint32)
+    _declare(lib, "ref_expert_matmul", C.c_int, C.POINTER(ExpertMatrix), f32p, C.c_uint32, f32p)
+    _declare(lib, "ref_ne_matmul", C.c_int, C.POINTER(NeMatrix), f32p, C.c_uint32, f32p)
+    _declare(lib, "ref_head_matmul", C.c_int, C.POINTER(HeadChunk), f32p, C.c_uint32, f32p)
+    _declare(lib, "ref_bf16_matmul", C.c_int, C.POINTER(Bf16Matrix), f32p, C.c_uint32, f32p)
+    _declare(lib, "ref_rms_norm", C.c_int, f32p, u16p, C.c_uint32, C.c_float, C.c_float, f32p)
+    _declare(lib, "ref_top_experts", C.c_int, f32p, C.c_uint32, u32p, f32p)
+    _declare(lib, "ref_moe_layer_create", C.c_void_p, C.POINTER(MoeLayer))
+    _declare(lib, "ref_moe_layer_destroy", None, C.c_void_p)
+    _declare(lib, "ref_moe_forward", C.c_int, C.c_void_p, f32p, C.c_uint32, f32p, f32p, u32p, f32p)
+    return lib
+
+
+# ---- struct builders over numpy arrays (the caller keeps the arrays alive) --
+
+def expert_struct(m, state_values: Optional[np.ndarray] = None) -> ExpertMatrix:
+    return ExpertMatrix(
+        m.rows, m.columns, ptr(m.trellis, C.c_uint16), ptr(m.su_f16, C.c_uint16),
+        ptr(m.sv_f16, C.c_uint16), ptr(m.wave_gamma_f16, C.c_uint16),
+        ptr(m.tlut, C.c_float), ptr(state_values, C.c_float))
+
+
+def ne_struct(m, state_values: Optional[np.ndarray] = None) -> NeMatrix:
+    return NeMatrix(
+        m.rows, m.columns, ptr(m.trellis, C.c_uint16), ptr(m.su, C.c_int8),
+        ptr(m.sv, C.c_int8), C.c_float(m.weight_scale), ptr(m.tlut, C.c_float),
+        ptr(state_values, C.c_float))
+
+
+def head_struct(h) -> HeadChunk:
+    count = 0 if h.protected_rows is None else int(h.protected_rows.size)
+    return HeadChunk(
+        h.rows, h.columns, ptr(h.packed, C.c_uint8), ptr(h.group_scale_f16, C.c_uint16),
+        ptr(h.protected_rows, C.c_uint32), ptr(h.protected_bf16, C.c_uint16), count)
+
+
+def bf16_struct(values: np.ndarray) -> Bf16Matrix:
+    rows, columns = values.shape
+    return Bf16Matrix(rows, columns, ptr(values, C.c_uint16))
+
+
+class MoeLayerStruct:
+    """Holds a MoeLayer struct and the arrays/structs it points into."""
+
+    def __init__(self, layer):
+        self.layer = layer
+        experts = layer.experts
+        self._experts = (ExpertMatrix * (experts * 3))()
+        for e in range(experts):
+            for p, m in enumerate((layer.gate[e], layer.up[e], layer.down[e])):
+                self._experts[e * 3 + p] = expert_struct(m)
+        self.struct = MoeLayer(
+            layer.hidden, layer.expert_hidden, experts,
+            bf16_struct(layer.router_bf16), bf16_struct(layer.shared_expert_gate_bf16),
+            C.cast(self._experts, C.POINTER(ExpertMatrix)),
+            ne_struct(layer.shared_gate), ne_struct(layer.shared_up), ne_struct(layer.shared_down))
+
+
+# ---- numpy-level helpers ----------------------------------------------------
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        raise ValueError(f"{what} failed with status {status}")
+
+
+def expert_matmul(lib, m, inputs: np.ndarray, prefix="ao") -> np.ndarray:
+    inputs = np.ascontiguousarray(inputs, dtype=np.float32).reshape(-1, m.columns)
+    out = np.zeros((inputs.shape[0], m.rows), np.float32)
+    s = expert_struct(m)
+    check(getattr(lib, f"{prefix}_expert_matmul")(C.byref(s), ptr(inputs, C.c_float),
+                                                  inputs.shape[0], ptr(out, C.c_float)),
+          "expert_matmul")
+    return out
+
+
+def ne_matmul(lib, m, inputs: np.ndarray, prefix="ao") -> np.ndarray:
+    inputs = np.ascontiguousarray(inputs, dtype=np.float32).reshape(-1, m.columns)
+    out = np.zeros((inputs.shape[0], m.rows), np.float32)
+    s = ne_struct(m)
+    check(getattr(lib, f"{prefix}_ne_matmul")(C.byref(s), ptr(inputs, C.c_float),
+                                              inputs.shape[0], ptr(out, C.c_float)),
+          "ne_matmul")
+    return out
+
+
+def head_matmul(lib, h, inputs: np.ndarray, isa: int = 16, prefix="ao") -> np.ndarray:
+    inputs = np.ascontiguousarray(inputs, dtype=np.float32).reshape(-1, h.columns)
+    out = np.zeros((inputs.shape[0], h.rows), np.float32)
+    s = head_struct(h)
+    if prefix == "ao":
+        status = lib.ao_head_matmul(C.byref(s), ptr(inputs, C.c_float), inputs.shape[0],
+                                    ptr(out, C.c_float), isa)
+    else:
+        status = lib.ref_head_matmul(C.byref(s), ptr(inputs, C.c_float), inputs.shape[0],
+                                     ptr(out, C.c_float))
+    check(status, "head_matmul")
+    return out
+
+
+def bf16_matmul(lib, values: np.ndarray, inputs: np.ndarray, isa: int = 16,
+                prefix="ao") -> np.ndarray:
+    rows, columns = values.shape
+    inputs = np.ascontiguousarray(inputs, dtype=np.float32).reshape(-1, columns)
+    out = np.zeros((inputs.shape[0], rows), np.float32)
+    s = bf16_struct(np.ascontiguousarray(values))
+    if prefix == "ao":
+        status = lib.ao_bf16_matmul(C.byref(s), ptr(inputs, C.c_float), inputs.shape[0],
+                                    ptr(out, C.c_float), isa)
+    else:
+        status = lib.ref_bf16_matmul(C.byref(s), ptr(inputs, C.c_float), inputs.shape[0],
+                                     ptr(out, C.c_float))
+    check(status, "bf16_matmul")
+    return out
+
+
+def top_experts(lib, logits: np.ndarray, prefix="ao"):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    experts = np.zeros(8, np.uint32)
+    weights = np.zeros(8, np.float32)
+    check(getattr(lib, f"{prefix}_top_experts")(ptr(logits, C.c_float), logits.size,
+                                                ptr(experts, C.c_uint32),
+                                                ptr(weights, C.c_float)), "top_experts")
+    return experts, weights
+
+
+def moe_route(lib, logits: np.ndarray):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    batch, experts = logits.shape
+    out = dict(
+        route_expert=np.zeros(batch * 8, np.uint32),
+        route_weight=np.zeros(batch * 8, np.float32),
+        counts=np.zeros(experts, np.uint32),
+        offsets=np.zeros(experts + 1, np.uint32),
+        grouped_batch=np.zeros(batch * 8, np.uint32),
+        route_to_grouped=np.zeros(batch * 8, np.uint32),
+    )
+    check(lib.ao_moe_route(ptr(logits, C.c_float), batch, experts,
+                           ptr(out["route_expert"], C.c_uint32), ptr(out["route_weight"], C.c_float),
+                           ptr(out["counts"], C.c_uint32), ptr(out["offsets"], C.c_uint32),
+                           ptr(out["grouped_batch"], C.c_uint32),
+                           ptr(out["route_to_grouped"], C.c_uint32)), "moe_route")
+    return out
+
+
+def moe_forward(lib, layer, inputs: np.ndarray, isa: int = 16,
+                logit_bias: Optional[np.ndarray] = None, threads: int = 0):
+    inputs = np.ascontiguousarray(inputs, dtype=np.float32).reshape(-1, layer.hidden)
+    batch = inputs.shape[0]
+    out = np.zeros((batch, layer.hidden), np.float32)
+    route_expert = np.zeros(batch * 8, np.uint32)
+    route_weight = np.zeros(batch * 8, np.float32)
+    holder = MoeLayerStruct(layer)
+    bias = None if logit_bias is None else np.ascontiguousarray(logit_bias, np.float32)
+    check(lib.ao_moe_forward(C.byref(holder.struct), ptr(inputs, C.c_float), batch,
+                             ptr(bias, C.c_float), isa, ptr(out, C.c_float),
+                             ptr(route_expert, C.c_uint32), ptr(route_weight, C.c_float),
+                             threads), "moe_forward")
+    return out, route_expert.reshape(batch, 8), route_weight.reshape(batch, 8)
+
+
+class RefMoeLayer:
+    """A layer prepared inside the reference library (its codec caches built
+    once, as the model does at load)."""
+
+    def __init__(self, ref_lib, layer):
+        self.lib = ref_lib
+        self.layer = layer
+        self.holder = MoeLayerStruct(layer)
+        self.handle = ref_lib.ref_moe_layer_create(C.byref(self.holder.struct))
+        if not self.handle:
+            raise RuntimeError("reference MoE layer preparation failed")
+
+    def forward(self, inputs: np.ndarray, logit_bias: Optional[np.ndarray] = None,
+                out: Optional[np.ndarray] = None):
+        inputs = np.ascontiguousarray(inputs, dtype=np.float32).reshape(-1, self.layer.hidden)
+        batch = inputs.shape[0]
+        if out is None:
+            out = np.zeros((batch, self.layer.hidden), np.float32)
+        route_expert = np.zeros(batch * 8, np.uint32)
+        route_weight = np.zeros(batch * 8, np.float32)
+        bias = None if logit_bias is None else np.ascontiguousarray(logit_bias, np.float32)
+        check(self.lib.ref_moe_forward(self.handle, ptr(inputs, C.c_float), batch,
+                                       ptr(bias, C.c_float), ptr(out, C.c_float),
+                                       ptr(route_expert, C.c_uint32),
+                                       ptr(route_weight, C.c_float)), "ref_moe_forward")
+        return out, route_expert.reshape(batch, 8), route_weight.reshape(batch, 8)
+
+    def close(self):
+        if self.handle:
+            self.lib.ref_moe_layer_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
