@@ -1,0 +1,153 @@
+// context.hpp -- the context object behind adi_hip_context and the launch,
+// workspace and error plumbing every entry point shares.
+#pragma once
+
+#include "common.hpp"
+
+#include <cmath>
+#include <exception>
+#include <new>
+#include <string>
+#include <utility>
+#include <vector>
+
+struct adi_hip_codebook {
+    enum Kind { expert, ne } kind;
+    int device;
+    void *data;    // expert: u16[16384][8]; ne: u16[1024][2]
+    size_t bytes;
+};
+
+namespace adi_hip {
+
+struct KernelStat {
+    std::string name;
+    uint64_t launches = 0;
+    double total_ms = 0.0;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
+};
+
+// Grow-only device arena; reserve() hands out 256-byte aligned slices of one
+// allocation, reset per call.
+struct Workspace {
+    void *base = nullptr;
+    size_t capacity = 0;
+    size_t used = 0;
+
+    void ensure(size_t bytes) {
+        if (bytes <= capacity) {
+            return;
+        }
+        if (base != nullptr) {
+            check_hip(hipDeviceSynchronize(), "workspace synchronize");
+            check_hip(hipFree(base), "workspace free");
+            base = nullptr;
+            capacity = 0;
+        }
+        check_hip(hipMalloc(&base, bytes), "workspace allocation");
+        capacity = bytes;
+    }
+
+    template <typename T>
+    T *take(size_t count) {
+        const size_t bytes = (count * sizeof(T) + 255) & ~size_t(255);
+        if (used + bytes > capacity) {
+            fail(ADI_HIP_OUT_OF_MEMORY, "workspace plan exceeded its reservation");
+        }
+        T *p = reinterpret_cast<T *>(static_cast<char *>(base) + used);
+        used += bytes;
+        return p;
+    }
+
+    static size_t round(size_t bytes) { return (bytes + 255) & ~size_t(255); }
+};
+
+}  // namespace adi_hip
+
+struct adi_hip_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    uint32_t isa_lanes = 16;
+    int cu_count = 256;
+    std::string last_error;
+    adi_hip::Workspace workspace;
+    bool profiling = false;
+    std::vector<adi_hip::KernelStat> stats;
+};
+
+namespace adi_hip {
+
+// Selects the context's device for the duration of a call.
+class DeviceScope {
+  public:
+    explicit DeviceScope(int device) {
+        check_hip(hipGetDevice(&previous_), "hipGetDevice");
+        if (previous_ != device) {
+            check_hip(hipSetDevice(device), "hipSetDevice");
+        }
+        device_ = device;
+    }
+    ~DeviceScope() {
+        if (previous_ != device_) {
+            (void)hipSetDevice(previous_);
+        }
+    }
+    DeviceScope(const DeviceScope &) = delete;
+    DeviceScope &operator=(const DeviceScope &) = delete;
+
+  private:
+    int previous_ = 0;
+    int device_ = 0;
+};
+
+template <typename F>
+int guarded(adi_hip_context *ctx, F &&function) {
+    if (ctx == nullptr) {
+        return ADI_HIP_INVALID_ARGUMENT;
+    }
+    try {
+        DeviceScope scope(ctx->device);
+        function();
+        ctx->last_error.clear();
+        return ADI_HIP_OK;
+    } catch (const Failure &failure) {
+        ctx->last_error = failure.message;
+        return failure.status;
+    } catch (const std::bad_alloc &) {
+        ctx->last_error = "host allocation failed";
+        return ADI_HIP_OUT_OF_MEMORY;
+    } catch (const std::exception &error) {
+        ctx->last_error = error.what();
+        return ADI_HIP_DEVICE_ERROR;
+    }
+}
+
+KernelStat &stat_for(adi_hip_context *ctx, const char *name);
+
+// Launches `kernel` on the context stream, timing it with events when
+// profiling is on.
+template <typename Kernel, typename... Args>
+void launch(adi_hip_context *ctx, const char *name, Kernel kernel, dim3 grid,
+            dim3 block, size_t lds_bytes, Args... args) {
+    if (grid.x == 0 || grid.y == 0 || grid.z == 0) {
+        return;
+    }
+    hipEvent_t start = nullptr, stop = nullptr;
+    if (ctx->profiling) {
+        check_hip(hipEventCreate(&start), "hipEventCreate");
+        check_hip(hipEventCreate(&stop), "hipEventCreate");
+        check_hip(hipEventRecord(start, ctx->stream), "hipEventRecord");
+    }
+    hipLaunchKernelGGL(kernel, grid, block, lds_bytes, ctx->stream, args...);
+    check_hip(hipGetLastError(), name);
+    if (ctx->profiling) {
+        check_hip(hipEventRecord(stop, ctx->stream), "hipEventRecord");
+        stat_for(ctx, name).pending.emplace_back(start, stop);
+    }
+}
+
+inline uint32_t ceil_div(uint64_t a, uint64_t b) {
+    return static_cast<uint32_t>((a + b - 1) / b);
+}
+
+}  // namespace adi_hip

@@ -1,0 +1,412 @@
+// dense.hip -- bf16 dense products in the CPU's reduction order, RMS norm,
+// top_experts and the stable counting sort of the MoE dispatch.
+//
+// Routing must be bit-identical with the CPU path, so the router logits are
+// computed in exactly the order of the CPU ISA the host build selects
+// (src/simd.cpp:88-96, src/simd_x86_avx2.cpp:172-193,
+// src/simd_x86_avx512.cpp:109-130): `lanes` independent sums, lane j taking
+// columns j, j+lanes, ..., then the lane sums added 0..lanes-1 from 0.0f, then
+// any trailing columns. The AVX-512 build of the reference fuses each lane's
+// multiply-add (GCC contracts the intrinsics' mul+add), the AVX2 and scalar
+// builds do not. Contraction is switched off in this file and the fused form
+// is written as fmaf.
+#include "dense.hpp"
+
+namespace adi_hip {
+namespace {
+
+constexpr uint32_t kTokensPerThread = 4;
+
+template <int LANES, bool FUSED>
+__device__ __forceinline__ float lane_step(float acc, float w, float x) {
+#pragma clang fp contract(off)
+    if constexpr (FUSED) {
+        return fmaf(w, x, acc);
+    } else {
+        return acc + w * x;
+    }
+}
+
+// Block of 256 threads = 256/LANES rows x LANES lanes; each thread carries
+// kTokensPerThread tokens.
+template <int LANES, bool FUSED>
+__global__ __launch_bounds__(256) void k_bf16_ordered(
+    const uint16_t *__restrict__ w, uint32_t rows, uint32_t columns,
+    const float *__restrict__ x, uint32_t batch, float *__restrict__ out) {
+#pragma clang fp contract(off)
+    constexpr uint32_t rows_per_block = 256 / LANES;
+    __shared__ float lanes[kTokensPerThread][256];
+    const uint32_t lane = threadIdx.x % LANES;
+    const uint32_t local_row = threadIdx.x / LANES;
+    const uint32_t row = blockIdx.x * rows_per_block + local_row;
+    const uint32_t t0 = blockIdx.y * kTokensPerThread;
+    const bool row_ok = row < rows;
+    const uint32_t full = columns / LANES * LANES;
+
+    float acc[kTokensPerThread];
+#pragma unroll
+    for (uint32_t t = 0; t < kTokensPerThread; ++t) {
+        acc[t] = 0.0f;
+    }
+    if (row_ok) {
+        const uint16_t *wr = w + static_cast<size_t>(row) * columns;
+        for (uint32_t base = 0; base < full; base += LANES) {
+            const uint32_t k = base + lane;
+            const float wk = bf16_bits_to_float(wr[k]);
+#pragma unroll
+            for (uint32_t t = 0; t < kTokensPerThread; ++t) {
+                if (t0 + t < batch) {
+                    acc[t] = lane_step<LANES, FUSED>(acc[t], wk,
+                                                     x[static_cast<size_t>(t0 + t) * columns + k]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (uint32_t t = 0; t < kTokensPerThread; ++t) {
+        lanes[t][threadIdx.x] = acc[t];
+    }
+    __syncthreads();
+    if (!row_ok || lane >= kTokensPerThread) {
+        return;
+    }
+    // Lane t of the row finishes token t0 + t: ordered lane sum, then tail.
+    const uint32_t t = lane;
+    if (t0 + t >= batch) {
+        return;
+    }
+    float sum = 0.0f;
+    for (uint32_t j = 0; j < LANES; ++j) {
+        sum = sum + lanes[t][local_row * LANES + j];
+    }
+    const uint16_t *wr = w + static_cast<size_t>(row) * columns;
+    const float *xr = x + static_cast<size_t>(t0 + t) * columns;
+    for (uint32_t k = full; k < columns; ++k) {
+        sum = lane_step<LANES, FUSED>(sum, bf16_bits_to_float(wr[k]), xr[k]);
+    }
+    out[static_cast<size_t>(t0 + t) * rows + row] = sum;
+}
+
+// The scalar order has one lane per row; its "lane sum" is 0 + the row sum,
+// so the generic kernel with LANES = 1 would need four lanes to finish four
+// tokens. This variant gives each thread one (row, token).
+__global__ __launch_bounds__(256) void k_bf16_scalar(
+    const uint16_t *__restrict__ w, uint32_t rows, uint32_t columns,
+    const float *__restrict__ x, uint32_t batch, float *__restrict__ out) {
+#pragma clang fp contract(off)
+    const uint32_t row = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t t = blockIdx.y;
+    if (row >= rows || t >= batch) {
+        return;
+    }
+    const uint16_t *wr = w + static_cast<size_t>(row) * columns;
+    const float *xr = x + static_cast<size_t>(t) * columns;
+    float sum = 0.0f;
+    for (uint32_t k = 0; k < columns; ++k) {
+        sum = sum + bf16_bits_to_float(wr[k]) * xr[k];
+    }
+    out[static_cast<size_t>(t) * rows + row] = sum;
+}
+
+// rms_norm (src/kernels.cpp:1052-1073): a sequential fp32 sum of squares,
+// then x * scale * (offset + w), each rounded as written. One wave per row;
+// the sum is carried by lane 0 so that it rounds exactly as the CPU loop.
+__global__ __launch_bounds__(64) void k_rms_norm(
+    const float *__restrict__ x, const uint16_t *__restrict__ weight, uint32_t count,
+    float offset, float epsilon, float *__restrict__ out) {
+#pragma clang fp contract(off)
+    __shared__ float scale_shared;
+    const float *row = x + static_cast<size_t>(blockIdx.x) * count;
+    if (threadIdx.x == 0) {
+        float squares = 0.0f;
+        for (uint32_t i = 0; i < count; ++i) {
+            squares = squares + row[i] * row[i];
+        }
+        scale_shared = 1.0f / sqrtf(squares / static_cast<float>(count) + epsilon);
+    }
+    __syncthreads();
+    const float scale = scale_shared;
+    float *dst = out + static_cast<size_t>(blockIdx.x) * count;
+    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
+        dst[i] = row[i] * scale * (offset + bf16_bits_to_float(weight[i]));
+    }
+}
+
+// Larger logit first, lower index on ties: the comparator of top_experts
+// (src/executor.cpp:202-211).
+__device__ __forceinline__ bool route_before(float a, uint32_t ia, float b, uint32_t ib) {
+    return a == b ? ia < ib : a > b;
+}
+
+// One wave per logit row. Lane l holds experts l, l+64, ...; eight rounds of
+// a wave-wide arg-max by the comparator pick the routes in order. The softmax
+// over the eight then runs on lane 0 in the reference's order
+// (src/executor.cpp:213-227).
+__global__ __launch_bounds__(64) void k_top_experts(
+    const float *__restrict__ logits, const float *__restrict__ bias, uint32_t experts,
+    uint32_t *__restrict__ route_expert, float *__restrict__ route_weight) {
+#pragma clang fp contract(off)
+    constexpr uint32_t per_lane = kMaxExperts / 64;
+    const uint32_t lane = threadIdx.x;
+    const float *row = logits + static_cast<size_t>(blockIdx.x) * experts;
+    float value[per_lane];
+    uint32_t used = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < per_lane; ++i) {
+        const uint32_t e = lane + 64u * i;
+        value[i] = 0.0f;
+        if (e < experts) {
+            value[i] = row[e];
+            if (bias != nullptr) {
+                value[i] = value[i] + bias[e];
+            }
+        } else {
+            used |= 1u << i;
+        }
+    }
+    float chosen_value[8];
+    uint32_t chosen_index[8];
+    for (int round = 0; round < 8; ++round) {
+        float best = 0.0f;
+        uint32_t best_index = 0xFFFFFFFFu;
+#pragma unroll
+        for (uint32_t i = 0; i < per_lane; ++i) {
+            const uint32_t e = lane + 64u * i;
+            if (!(used & (1u << i)) &&
+                (best_index == 0xFFFFFFFFu || route_before(value[i], e, best, best_index))) {
+                best = value[i];
+                best_index = e;
+            }
+        }
+        for (int offset = 32; offset >= 1; offset >>= 1) {
+            const float other = __shfl_xor(best, offset);
+            const uint32_t other_index = static_cast<uint32_t>(
+                __shfl_xor(static_cast<int>(best_index), offset));
+            if (other_index != 0xFFFFFFFFu &&
+                (best_index == 0xFFFFFFFFu || route_before(other, other_index, best, best_index))) {
+                best = other;
+                best_index = other_index;
+            }
+        }
+        chosen_value[round] = best;
+        chosen_index[round] = best_index;
+        if (best_index % 64u == lane) {
+            used |= 1u << (best_index / 64u);
+        }
+    }
+    if (lane == 0) {
+        const float maximum = chosen_value[0];
+        float selected[8];
+        float sum = 0.0f;
+        for (int i = 0; i < 8; ++i) {
+            selected[i] = expf(chosen_value[i] - maximum);
+            sum = sum + selected[i];
+        }
+        sum = fmaxf(sum, 6.103515625e-5f);
+        for (int i = 0; i < 8; ++i) {
+            route_expert[blockIdx.x * 8u + i] = chosen_index[i];
+            route_weight[blockIdx.x * 8u + i] = selected[i] / sum;
+        }
+    }
+}
+
+// Counting sort of moe_forward_batch (src/executor.cpp:1235-1258) in one
+// wave: counts by LDS integer atomics, an exclusive scan for offsets, then the
+// (token, route) slots are placed 64 at a time in order; lanes that share an
+// expert in a chunk find their rank among earlier lanes with ballots, so each
+// expert's cursor advances exactly as the sequential loop's does.
+__global__ __launch_bounds__(64) void k_route_sort(RouteSort a) {
+    __shared__ uint32_t counts[kMaxExperts];
+    __shared__ uint32_t cursor[kMaxExperts];
+    const uint32_t lane = threadIdx.x;
+    for (uint32_t e = lane; e < a.experts; e += 64u) {
+        counts[e] = 0u;
+    }
+    __syncthreads();
+    for (uint32_t i = lane; i < a.positions; i += 64u) {
+        atomicAdd(&counts[a.route_expert[i]], 1u);
+    }
+    __syncthreads();
+    // exclusive scan over experts: each lane owns a contiguous run
+    const uint32_t per_lane = (a.experts + 63u) / 64u;
+    const uint32_t first = lane * per_lane;
+    uint32_t local = 0;
+    for (uint32_t e = first; e < first + per_lane && e < a.experts; ++e) {
+        local += counts[e];
+    }
+    uint32_t inclusive = local;
+    for (int offset = 1; offset < 64; offset <<= 1) {
+        const uint32_t other = static_cast<uint32_t>(__shfl_up(static_cast<int>(inclusive), offset));
+        if (lane >= static_cast<uint32_t>(offset)) {
+            inclusive += other;
+        }
+    }
+    uint32_t running = inclusive - local;
+    for (uint32_t e = first; e < first + per_lane && e < a.experts; ++e) {
+        cursor[e] = running;
+        a.offsets[e] = running;
+        a.counts[e] = counts[e];
+        if (a.position_expert != nullptr) {
+            for (uint32_t p = running; p < running + counts[e]; ++p) {
+                a.position_expert[p] = e;
+            }
+        }
+        running += counts[e];
+    }
+    if (lane == 63) {
+        a.offsets[a.experts] = inclusive;
+    }
+    // ascending list of active experts
+    if (a.active != nullptr) {
+        uint32_t base = 0;
+        for (uint32_t e0 = 0; e0 < a.experts; e0 += 64u) {
+            const uint32_t e = e0 + lane;
+            const bool on = e < a.experts && counts[e] != 0u;
+            const uint64_t mask = __ballot(on);
+            if (on) {
+                a.active[base + __popcll(mask & ((1ull << lane) - 1ull))] = e;
+            }
+            base += __popcll(mask);
+        }
+        if (lane == 0 && a.active_count != nullptr) {
+            *a.active_count = base;
+        }
+    }
+    __syncthreads();
+    const uint64_t below = (1ull << lane) - 1ull;
+    for (uint32_t c = 0; c < a.positions; c += 64u) {
+        const uint32_t i = c + lane;
+        const bool valid = i < a.positions;
+        const uint32_t e = valid ? a.route_expert[i] : 0u;
+        uint64_t peers = __ballot(valid);
+        if (!valid) {
+            peers = ~peers;
+        }
+        for (uint32_t bit = 0; bit < 10u; ++bit) {
+            const bool set = (e >> bit) & 1u;
+            const uint64_t vote = __ballot(set);
+            peers &= set ? vote : ~vote;
+        }
+        const uint32_t rank = __popcll(peers & below);
+        const uint32_t total = __popcll(peers);
+        uint32_t position = 0;
+        if (valid) {
+            position = cursor[e] + rank;
+        }
+        __syncthreads();
+        if (valid) {
+            a.grouped_batch[position] = i / 8u;
+            a.route_to_grouped[i] = position;
+            if (rank == 0) {
+                cursor[e] += total;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace
+
+void launch_bf16_ordered(adi_hip_context *ctx, const uint16_t *w, uint32_t rows,
+                         uint32_t columns, const float *x, uint32_t batch,
+                         float *out, uint32_t lanes) {
+    switch (lanes) {
+    case 1:
+        launch(ctx, "bf16_ordered", k_bf16_scalar, dim3(ceil_div(rows, 256), batch), dim3(256), 0,
+               w, rows, columns, x, batch, out);
+        break;
+    case 8:
+        launch(ctx, "bf16_ordered", k_bf16_ordered<8, false>,
+               dim3(ceil_div(rows, 256 / 8), ceil_div(batch, kTokensPerThread)), dim3(256), 0, w,
+               rows, columns, x, batch, out);
+        break;
+    default:
+        launch(ctx, "bf16_ordered", k_bf16_ordered<16, true>,
+               dim3(ceil_div(rows, 256 / 16), ceil_div(batch, kTokensPerThread)), dim3(256), 0, w,
+               rows, columns, x, batch, out);
+        break;
+    }
+}
+
+void launch_top_experts(adi_hip_context *ctx, const float *logits, const float *bias,
+                        uint32_t batch, uint32_t experts, uint32_t *route_expert,
+                        float *route_weight) {
+    launch(ctx, "top_experts", k_top_experts, dim3(batch), dim3(64), 0, logits, bias, experts,
+           route_expert, route_weight);
+}
+
+void launch_route_sort(adi_hip_context *ctx, const RouteSort &args) {
+    launch(ctx, "route_sort", k_route_sort, dim3(1), dim3(64), 0, args);
+}
+
+}  // namespace adi_hip
+
+using namespace adi_hip;
+
+extern "C" {
+
+int adi_hip_bf16_matmul(adi_hip_context *ctx, const adi_hip_bf16_matrix *m,
+                        const float *inputs, uint32_t batch, float *outputs) {
+    return guarded(ctx, [&] {
+        require(m != nullptr && m->values != nullptr, "BF16 matrix is null");
+        require(batch > 0 && m->rows > 0 && m->columns > 0, "BF16 matrix batch shape mismatch");
+        require(inputs != nullptr && outputs != nullptr, "BF16 vector is null");
+        launch_bf16_ordered(ctx, m->values, m->rows, m->columns, inputs, batch, outputs,
+                            ctx->isa_lanes);
+    });
+}
+
+int adi_hip_bf16_matvec(adi_hip_context *ctx, const adi_hip_bf16_matrix *m,
+                        const float *input, float *output) {
+    return adi_hip_bf16_matmul(ctx, m, input, 1, output);
+}
+
+int adi_hip_rms_norm(adi_hip_context *ctx, const float *input, const uint16_t *weight_bf16,
+                     uint32_t count, uint32_t rows, float weight_offset, float epsilon,
+                     float *output) {
+    return guarded(ctx, [&] {
+        require(count > 0 && rows > 0, "RMS norm shape mismatch");
+        require(input != nullptr && weight_bf16 != nullptr && output != nullptr,
+                "RMS norm vector is null");
+        launch(ctx, "rms_norm", k_rms_norm, dim3(rows), dim3(64), 0, input, weight_bf16, count,
+               weight_offset, epsilon, output);
+    });
+}
+
+int adi_hip_top_experts(adi_hip_context *ctx, const float *logits, uint32_t batch,
+                        uint32_t experts, uint32_t *route_expert, float *route_weight) {
+    return guarded(ctx, [&] {
+        require(experts >= 8, "MoE routing requires at least eight experts");
+        require(experts <= kMaxExperts, "MoE routing supports at most 1024 experts");
+        require(batch > 0 && logits != nullptr && route_expert != nullptr &&
+                    route_weight != nullptr,
+                "MoE routing shape mismatch");
+        launch_top_experts(ctx, logits, nullptr, batch, experts, route_expert, route_weight);
+    });
+}
+
+int adi_hip_moe_route(adi_hip_context *ctx, const float *logits, const float *logit_bias,
+                      uint32_t batch, uint32_t experts, uint32_t *route_expert,
+                      float *route_weight, uint32_t *counts, uint32_t *offsets,
+                      uint32_t *grouped_batch, uint32_t *route_to_grouped) {
+    return guarded(ctx, [&] {
+        require(experts >= 8, "MoE routing requires at least eight experts");
+        require(experts <= kMaxExperts, "MoE routing supports at most 1024 experts");
+        require(batch > 0 && logits != nullptr && route_expert != nullptr &&
+                    route_weight != nullptr && counts != nullptr && offsets != nullptr &&
+                    grouped_batch != nullptr && route_to_grouped != nullptr,
+                "MoE routing shape mismatch");
+        launch_top_experts(ctx, logits, logit_bias, batch, experts, route_expert, route_weight);
+        RouteSort s{};
+        s.route_expert = route_expert;
+        s.positions = batch * 8u;
+        s.experts = experts;
+        s.counts = counts;
+        s.offsets = offsets;
+        s.grouped_batch = grouped_batch;
+        s.route_to_grouped = route_to_grouped;
+        launch_route_sort(ctx, s);
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,36 @@
+// dense.hpp -- ISA-ordered bf16 matmul and routing launchers.
+#pragma once
+
+#include "context.hpp"
+
+namespace adi_hip {
+
+// out[b][r] = bf16 row r . x[b] in the CPU reduction order `lanes`.
+// `bias` (nullable, [rows]) is added to each result afterwards in fp32.
+void launch_bf16_ordered(adi_hip_context *ctx, const uint16_t *w, uint32_t rows,
+                         uint32_t columns, const float *x, uint32_t batch,
+                         float *out, uint32_t lanes);
+
+// Top-8 routes per logit row (bias nullable, [experts]).
+void launch_top_experts(adi_hip_context *ctx, const float *logits,
+                        const float *bias, uint32_t batch, uint32_t experts,
+                        uint32_t *route_expert, float *route_weight);
+
+// Stable counting sort of the batch's routes (one block).
+struct RouteSort {
+    const uint32_t *route_expert; // [positions]
+    uint32_t positions;           // batch * 8
+    uint32_t experts;
+    uint32_t *counts;             // [experts]
+    uint32_t *offsets;            // [experts + 1]
+    uint32_t *active;             // [experts] active experts ascending (nullable)
+    uint32_t *active_count;       // [1] (nullable)
+    uint32_t *position_expert;    // [positions] (nullable)
+    uint32_t *grouped_batch;      // [positions]
+    uint32_t *route_to_grouped;   // [positions]
+};
+void launch_route_sort(adi_hip_context *ctx, const RouteSort &args);
+
+constexpr uint32_t kMaxExperts = 1024;
+
+}  // namespace adi_hip

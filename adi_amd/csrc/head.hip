@@ -1,0 +1,505 @@
+// head.hip -- int5_g64 output head (src/kernels.cpp:847-979,
+// src/simd.cpp:65-86) and the certified greedy arg-max over its logits.
+//
+// Logits. Each row is columns/8 five-byte blocks, i.e. a little-endian bit
+// stream of 5-bit codes u; the weight is (u - 16) * scale of its 64-column
+// group. A lane owns 32 consecutive columns ("quad" of 4 blocks, 20 bytes,
+// half a scale group) of a row: it loads its 20 bytes as 5 dwords (the lanes
+// of a wave cover contiguous bytes), keeps its 32 x values per token in
+// registers, and computes scale * (sum u*x - 16 * sum x) with the 32-column x
+// sums precomputed per token. Lanes sharing a row add their parts with wave
+// shuffles. Waves walk the rows grid-stride.
+//
+// Certified arg-max. GPU and CPU sum the same exact products w_k*x_k (w_k is
+// exact in fp32: a 5-bit integer times an f16) in different orders, so each
+// is within (n + 80) * 2^-24 * sum|w_k x_k| of the exact sum, and
+// sum|w_k x_k| <= sum_k 16*scale*|x_k| =: A (computed per row alongside the
+// logit). A row can be the CPU's first maximum only if its GPU logit plus
+// its bound reaches the top GPU logit minus that row's bound; those
+// candidates are re-evaluated in the CPU order (ISA lanes, fused or not, as
+// the bf16 dot) and the first maximum among them is the CPU's greedy token
+// (std::max_element, src/generation.cpp:177-180).
+#include "context.hpp"
+#include "dense.hpp"
+
+#include <algorithm>
+
+namespace adi_hip {
+namespace {
+
+constexpr uint32_t kQuadColumns = 32;
+
+// x sums per 32-column quad: sum x and sum |x|.
+__global__ __launch_bounds__(256) void k_head_sums(const float *__restrict__ x, uint32_t columns,
+                                                   float *__restrict__ sums,
+                                                   float *__restrict__ abs_sums) {
+#pragma clang fp contract(off)
+    const uint32_t quads = columns / kQuadColumns;
+    const uint32_t b = blockIdx.x;
+    for (uint32_t q = threadIdx.x; q < quads; q += blockDim.x) {
+        const float *src = x + static_cast<size_t>(b) * columns + q * kQuadColumns;
+        float s = 0.0f, a = 0.0f;
+        for (uint32_t k = 0; k < kQuadColumns; ++k) {
+            s += src[k];
+            a += fabsf(src[k]);
+        }
+        sums[static_cast<size_t>(b) * quads + q] = s;
+        abs_sums[static_cast<size_t>(b) * quads + q] = a;
+    }
+}
+
+template <int K>
+__device__ __forceinline__ float code_at(const uint32_t (&d)[6]) {
+    constexpr int bit = 5 * K;
+    constexpr int w = bit / 32;
+    constexpr int s = bit % 32;
+    if constexpr (s <= 27) {
+        return static_cast<float>(__builtin_amdgcn_ubfe(d[w], s, 5));
+    } else {
+        return static_cast<float>(__builtin_amdgcn_alignbit(d[w + 1], d[w], s) & 31u);
+    }
+}
+
+// quads = columns/32 must be a power of two <= 64 (columns 64..2048).
+template <int NT>
+__global__ __launch_bounds__(256) void k_head_gemv(
+    const uint8_t *__restrict__ packed, const uint16_t *__restrict__ scales, uint32_t rows,
+    uint32_t columns, const float *__restrict__ x, const float *__restrict__ sums,
+    const float *__restrict__ abs_sums, uint32_t batch, float *__restrict__ logits,
+    float *__restrict__ bounds) {
+    const uint32_t quads = columns / kQuadColumns;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t quad = lane % quads;
+    const uint32_t rows_per_wave = 64u / quads;
+    const uint32_t wave_global = blockIdx.x * (blockDim.x / 64u) + (threadIdx.x >> 6);
+    const uint32_t wave_count = gridDim.x * (blockDim.x / 64u);
+    const uint32_t groups = columns / 64u;
+
+    for (uint32_t t0 = 0; t0 < batch; t0 += NT) {
+        float xv[NT][kQuadColumns];
+        float sx[NT], sa[NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const bool ok = t0 + j < batch;
+            const float4 *src = reinterpret_cast<const float4 *>(
+                x + static_cast<size_t>(ok ? t0 + j : t0) * columns + quad * kQuadColumns);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float4 v = src[q];
+                xv[j][4 * q] = v.x;
+                xv[j][4 * q + 1] = v.y;
+                xv[j][4 * q + 2] = v.z;
+                xv[j][4 * q + 3] = v.w;
+            }
+            const size_t si = static_cast<size_t>(ok ? t0 + j : t0) * quads + quad;
+            sx[j] = sums[si];
+            sa[j] = abs_sums[si];
+        }
+        for (uint32_t row0 = wave_global * rows_per_wave; row0 < rows;
+             row0 += wave_count * rows_per_wave) {
+            const uint32_t row = row0 + lane / quads;
+            const bool ok = row < rows;
+            uint32_t d[6] = {0u, 0u, 0u, 0u, 0u, 0u};
+            float scale = 0.0f;
+            if (ok) {
+                const uint32_t *src = reinterpret_cast<const uint32_t *>(packed) +
+                                      (static_cast<size_t>(row) * quads + quad) * 5u;
+#pragma unroll
+                for (int i = 0; i < 5; ++i) {
+                    d[i] = __builtin_nontemporal_load(src + i);
+                }
+                scale = half_bits_to_float(scales[static_cast<size_t>(row) * groups + quad / 2u]);
+            }
+            float u[kQuadColumns];
+#define ADI_CODE(K) u[K] = code_at<K>(d);
+            ADI_CODE(0) ADI_CODE(1) ADI_CODE(2) ADI_CODE(3) ADI_CODE(4) ADI_CODE(5) ADI_CODE(6)
+            ADI_CODE(7) ADI_CODE(8) ADI_CODE(9) ADI_CODE(10) ADI_CODE(11) ADI_CODE(12)
+            ADI_CODE(13) ADI_CODE(14) ADI_CODE(15) ADI_CODE(16) ADI_CODE(17) ADI_CODE(18)
+            ADI_CODE(19) ADI_CODE(20) ADI_CODE(21) ADI_CODE(22) ADI_CODE(23) ADI_CODE(24)
+            ADI_CODE(25) ADI_CODE(26) ADI_CODE(27) ADI_CODE(28) ADI_CODE(29) ADI_CODE(30)
+            ADI_CODE(31)
+#undef ADI_CODE
+            float val[NT], bnd[NT];
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 32; k += 2) {
+                    acc0 = fmaf(u[k], xv[j][k], acc0);
+                    acc1 = fmaf(u[k + 1], xv[j][k + 1], acc1);
+                }
+                val[j] = scale * ((acc0 + acc1) - 16.0f * sx[j]);
+                bnd[j] = 16.0f * scale * sa[j];
+            }
+            for (uint32_t off = 1; off < quads; off <<= 1) {
+#pragma unroll
+                for (int j = 0; j < NT; ++j) {
+                    val[j] += __shfl_xor(val[j], static_cast<int>(off));
+                    bnd[j] += __shfl_xor(bnd[j], static_cast<int>(off));
+                }
+            }
+            if (ok && quad == 0) {
+#pragma unroll
+                for (int j = 0; j < NT; ++j) {
+                    if (t0 + j < batch) {
+                        logits[static_cast<size_t>(t0 + j) * rows + row] = val[j];
+                        if (bounds != nullptr) {
+                            bounds[static_cast<size_t>(t0 + j) * rows + row] = bnd[j];
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// A row's dot in the CPU order: weights of lane j are columns j, j+LANES,
+// ...; lane sums added 0..LANES-1 from 0; then the tail (columns % LANES).
+// `weight(k)` supplies w_k. Runs on one wave; the result is valid on lane 0.
+template <int LANES, bool FUSED, typename Weight>
+__device__ float ordered_row_dot(uint32_t columns, const float *__restrict__ x, Weight weight) {
+#pragma clang fp contract(off)
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t full = columns / LANES * LANES;
+    float acc = 0.0f;
+    if (lane < LANES) {
+        for (uint32_t base = 0; base < full; base += LANES) {
+            const uint32_t k = base + lane;
+            if constexpr (FUSED) {
+                acc = fmaf(weight(k), x[k], acc);
+            } else {
+                acc = acc + weight(k) * x[k];
+            }
+        }
+    }
+    float sum = 0.0f;
+    for (int j = 0; j < LANES; ++j) {
+        sum = sum + __shfl(acc, j);
+    }
+    for (uint32_t k = full; k < columns; ++k) {
+        if constexpr (FUSED) {
+            sum = fmaf(weight(k), x[k], sum);
+        } else {
+            sum = sum + weight(k) * x[k];
+        }
+    }
+    return sum;
+}
+
+struct HeadView {
+    const uint8_t *packed;
+    const uint16_t *scales;
+    const uint32_t *protected_rows;
+    const uint16_t *protected_bf16;
+    uint32_t protected_count;
+    uint32_t rows;
+    uint32_t columns;
+};
+
+template <int LANES, bool FUSED>
+__device__ float exact_logit(const HeadView &h, uint32_t row, const float *x) {
+    for (uint32_t p = 0; p < h.protected_count; ++p) {
+        if (h.protected_rows[p] == row) {
+            const uint16_t *w = h.protected_bf16 + static_cast<size_t>(p) * h.columns;
+            return ordered_row_dot<LANES, FUSED>(
+                h.columns, x, [&](uint32_t k) { return bf16_bits_to_float(w[k]); });
+        }
+    }
+    const uint8_t *rb = h.packed + static_cast<size_t>(row) * (h.columns / 8u * 5u);
+    const uint16_t *rs = h.scales + static_cast<size_t>(row) * (h.columns / 64u);
+    return ordered_row_dot<LANES, FUSED>(h.columns, x, [&](uint32_t k) {
+        const uint32_t block = k >> 3, index = k & 7u;
+        const uint8_t *bytes = rb + block * 5u;
+        uint64_t word = 0;
+        for (int i = 0; i < 5; ++i) {
+            word |= static_cast<uint64_t>(bytes[i]) << (8 * i);
+        }
+        const int code = static_cast<int>((word >> (5u * index)) & 31u) - 16;
+        return static_cast<float>(code) * half_bits_to_float(rs[k >> 6]);
+    });
+}
+
+// Protected rows: their logits are the bf16 dot in CPU order, exactly.
+template <int LANES, bool FUSED>
+__global__ __launch_bounds__(64) void k_head_protected(HeadView h, const float *__restrict__ x,
+                                                       float *__restrict__ logits,
+                                                       float *__restrict__ bounds) {
+    const uint32_t p = blockIdx.x, b = blockIdx.y;
+    const uint16_t *w = h.protected_bf16 + static_cast<size_t>(p) * h.columns;
+    const float v = ordered_row_dot<LANES, FUSED>(
+        h.columns, x + static_cast<size_t>(b) * h.columns,
+        [&](uint32_t k) { return bf16_bits_to_float(w[k]); });
+    const uint32_t row = h.protected_rows[p];
+    if (threadIdx.x == 0 && row < h.rows) {  // rows out of range are ignored
+        const size_t at = static_cast<size_t>(b) * h.rows + row;
+        logits[at] = v;
+        if (bounds != nullptr) {
+            bounds[at] = 0.0f;
+        }
+    }
+}
+
+// Every row in CPU order (fallback for widths the fast kernel does not tile).
+template <int LANES, bool FUSED>
+__global__ __launch_bounds__(64) void k_head_exact_rows(HeadView h, const float *__restrict__ x,
+                                                        float *__restrict__ logits,
+                                                        float *__restrict__ bounds) {
+    const uint32_t row = blockIdx.x, b = blockIdx.y;
+    const float v = exact_logit<LANES, FUSED>(h, row, x + static_cast<size_t>(b) * h.columns);
+    if (threadIdx.x == 0) {
+        logits[static_cast<size_t>(b) * h.rows + row] = v;
+        if (bounds != nullptr) {
+            bounds[static_cast<size_t>(b) * h.rows + row] = 0.0f;
+        }
+    }
+}
+
+__device__ __forceinline__ bool first_max_before(float a, uint32_t ia, float b, uint32_t ib) {
+    return a == b ? ia < ib : a > b;
+}
+
+constexpr uint32_t kArgmaxThreads = 1024;
+constexpr uint32_t kCandidateCap = 2048;
+
+// One block per row of logits: top GPU logit, candidate rows, exact
+// re-evaluation, first maximum.
+template <int LANES, bool FUSED>
+__global__ __launch_bounds__(kArgmaxThreads) void k_head_argmax(
+    HeadView h, const float *__restrict__ x, const float *__restrict__ logits,
+    const float *__restrict__ bounds, float factor, uint32_t *__restrict__ argmax) {
+    __shared__ float best_value[kArgmaxThreads / 64];
+    __shared__ uint32_t best_index[kArgmaxThreads / 64];
+    __shared__ uint32_t candidates[kCandidateCap];
+    __shared__ uint32_t candidate_count;
+    __shared__ float threshold;
+    const uint32_t b = blockIdx.x;
+    const float *row_logits = logits + static_cast<size_t>(b) * h.rows;
+    const float *row_bounds = bounds + static_cast<size_t>(b) * h.rows;
+    const float *xb = x + static_cast<size_t>(b) * h.columns;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t waves = kArgmaxThreads / 64;
+
+    // 1. first maximum of the GPU logits
+    float v = -INFINITY;
+    uint32_t vi = 0xFFFFFFFFu;
+    for (uint32_t r = threadIdx.x; r < h.rows; r += kArgmaxThreads) {
+        const float c = row_logits[r];
+        if (vi == 0xFFFFFFFFu || first_max_before(c, r, v, vi)) {
+            v = c;
+            vi = r;
+        }
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(v, off);
+        const uint32_t oi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(vi), off));
+        if (oi != 0xFFFFFFFFu && (vi == 0xFFFFFFFFu || first_max_before(ov, oi, v, vi))) {
+            v = ov;
+            vi = oi;
+        }
+    }
+    if (lane == 0) {
+        best_value[wave] = v;
+        best_index[wave] = vi;
+    }
+    if (threadIdx.x == 0) {
+        candidate_count = 0;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float bv = best_value[0];
+        uint32_t bi = best_index[0];
+        for (uint32_t w = 1; w < waves; ++w) {
+            if (best_index[w] != 0xFFFFFFFFu && first_max_before(best_value[w], best_index[w], bv, bi)) {
+                bv = best_value[w];
+                bi = best_index[w];
+            }
+        }
+        threshold = bv - factor * row_bounds[bi];
+    }
+    __syncthreads();
+    // 2. candidates: rows whose bound interval reaches the threshold
+    const float t = threshold;
+    for (uint32_t r = threadIdx.x; r < h.rows; r += kArgmaxThreads) {
+        if (row_logits[r] + factor * row_bounds[r] >= t) {
+            const uint32_t slot = atomicAdd(&candidate_count, 1u);
+            if (slot < kCandidateCap) {
+                candidates[slot] = r;
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t count = candidate_count;
+    const bool overflow = count > kCandidateCap;
+    const uint32_t work = overflow ? h.rows : count;
+    // 3. exact re-evaluation, one wave per candidate
+    float wv = -INFINITY;
+    uint32_t wi = 0xFFFFFFFFu;
+    for (uint32_t c = wave; c < work; c += waves) {
+        const uint32_t r = overflow ? c : candidates[c];
+        const float e = exact_logit<LANES, FUSED>(h, r, xb);
+        if (wi == 0xFFFFFFFFu || first_max_before(e, r, wv, wi)) {
+            wv = e;
+            wi = r;
+        }
+    }
+    __syncthreads();
+    if (lane == 0) {
+        best_value[wave] = wv;
+        best_index[wave] = wi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float bv = best_value[0];
+        uint32_t bi = best_index[0];
+        for (uint32_t w = 1; w < waves; ++w) {
+            if (best_index[w] != 0xFFFFFFFFu &&
+                (bi == 0xFFFFFFFFu || first_max_before(best_value[w], best_index[w], bv, bi))) {
+                bv = best_value[w];
+                bi = best_index[w];
+            }
+        }
+        argmax[b] = bi;
+    }
+}
+
+void validate_head(const adi_hip_head_chunk *h) {
+    require(h != nullptr, "Mach output head is null");
+    require(h->rows > 0 && h->columns > 0 && h->columns % 64u == 0,
+            "Mach output head shape mismatch");
+    require(h->packed != nullptr && h->group_scale_f16 != nullptr,
+            "Mach output head tensor is null");
+    require(h->protected_count == 0 ||
+                (h->protected_rows != nullptr && h->protected_bf16 != nullptr),
+            "Mach protected output row shape mismatch");
+}
+
+bool fast_width(uint32_t columns) {
+    const uint32_t quads = columns / kQuadColumns;
+    return columns % 64u == 0 && is_power_of_two(quads) && quads <= 64u;
+}
+
+HeadView view_of(const adi_hip_head_chunk *h) {
+    return HeadView{h->packed,         h->group_scale_f16, h->protected_rows,
+                    h->protected_bf16, h->protected_count, h->rows,
+                    h->columns};
+}
+
+template <int LANES, bool FUSED>
+void launch_exact_parts(adi_hip_context *ctx, const HeadView &v, const float *x, uint32_t batch,
+                        float *logits, float *bounds, bool all_rows) {
+    if (all_rows) {
+        launch(ctx, "head_exact", k_head_exact_rows<LANES, FUSED>, dim3(v.rows, batch), dim3(64),
+               0, v, x, logits, bounds);
+    } else if (v.protected_count > 0) {
+        launch(ctx, "head_protected", k_head_protected<LANES, FUSED>,
+               dim3(v.protected_count, batch), dim3(64), 0, v, x, logits, bounds);
+    }
+}
+
+void head_logits(adi_hip_context *ctx, const adi_hip_head_chunk *h, const float *x,
+                 uint32_t batch, float *logits, float *bounds) {
+    const HeadView v = view_of(h);
+    const bool fast = fast_width(h->columns);
+    if (fast) {
+        const uint32_t quads = h->columns / kQuadColumns;
+        auto &ws = ctx->workspace;
+        float *sums = ws.take<float>(size_t(batch) * quads);
+        float *abs_sums = ws.take<float>(size_t(batch) * quads);
+        launch(ctx, "head_sums", k_head_sums, dim3(batch), dim3(256), 0, x, h->columns, sums,
+               abs_sums);
+        const uint32_t rows_per_block = 4u * (64u / quads);
+        const uint32_t blocks = std::min<uint32_t>(ceil_div(h->rows, rows_per_block),
+                                                   static_cast<uint32_t>(ctx->cu_count) * 8u);
+        if (batch == 1) {
+            launch(ctx, "head_gemv", k_head_gemv<1>, dim3(blocks), dim3(256), 0, h->packed,
+                   h->group_scale_f16, h->rows, h->columns, x, static_cast<const float *>(sums),
+                   static_cast<const float *>(abs_sums), batch, logits, bounds);
+        } else {
+            launch(ctx, "head_gemv", k_head_gemv<4>, dim3(blocks), dim3(256), 0, h->packed,
+                   h->group_scale_f16, h->rows, h->columns, x, static_cast<const float *>(sums),
+                   static_cast<const float *>(abs_sums), batch, logits, bounds);
+        }
+    }
+    switch (ctx->isa_lanes) {
+    case 1:
+        launch_exact_parts<1, false>(ctx, v, x, batch, logits, bounds, !fast);
+        break;
+    case 8:
+        launch_exact_parts<8, false>(ctx, v, x, batch, logits, bounds, !fast);
+        break;
+    default:
+        launch_exact_parts<16, true>(ctx, v, x, batch, logits, bounds, !fast);
+        break;
+    }
+}
+
+size_t head_workspace(const adi_hip_head_chunk *h, uint32_t batch, bool with_logits,
+                      bool with_bounds) {
+    const size_t quads = h->columns / kQuadColumns;
+    return Workspace::round(batch * quads * 4) * 2 +
+           (with_logits ? Workspace::round(size_t(batch) * h->rows * 4) : 0) +
+           (with_bounds ? Workspace::round(size_t(batch) * h->rows * 4) : 0);
+}
+
+}  // namespace
+}  // namespace adi_hip
+
+using namespace adi_hip;
+
+extern "C" {
+
+int adi_hip_head_matmul(adi_hip_context *ctx, const adi_hip_head_chunk *h, const float *inputs,
+                        uint32_t batch, float *outputs) {
+    return guarded(ctx, [&] {
+        validate_head(h);
+        require(batch > 0 && inputs != nullptr && outputs != nullptr,
+                "Mach output head batch shape mismatch");
+        auto &ws = ctx->workspace;
+        ws.used = 0;
+        ws.ensure(head_workspace(h, batch, false, false));
+        head_logits(ctx, h, inputs, batch, outputs, nullptr);
+    });
+}
+
+int adi_hip_head_matvec(adi_hip_context *ctx, const adi_hip_head_chunk *h, const float *input,
+                        float *output) {
+    return adi_hip_head_matmul(ctx, h, input, 1, output);
+}
+
+int adi_hip_head_argmax(adi_hip_context *ctx, const adi_hip_head_chunk *h, const float *inputs,
+                        uint32_t batch, float *logits, uint32_t *argmax) {
+    return guarded(ctx, [&] {
+        validate_head(h);
+        require(batch > 0 && inputs != nullptr && argmax != nullptr,
+                "Mach output head batch shape mismatch");
+        auto &ws = ctx->workspace;
+        ws.used = 0;
+        ws.ensure(head_workspace(h, batch, logits == nullptr, true));
+        float *out = logits != nullptr ? logits : ws.take<float>(size_t(batch) * h->rows);
+        float *bounds = ws.take<float>(size_t(batch) * h->rows);
+        head_logits(ctx, h, inputs, batch, out, bounds);
+        // Both orders are within (n + 80) * 2^-24 * A of the exact sum; the
+        // 1.25 margin also covers the rounding of A itself.
+        const float factor = 2.5f * static_cast<float>(h->columns + 80u) * 5.9604645e-8f;
+        const HeadView v = view_of(h);
+        switch (ctx->isa_lanes) {
+        case 1:
+            launch(ctx, "head_argmax", k_head_argmax<1, false>, dim3(batch), dim3(kArgmaxThreads),
+                   0, v, inputs, static_cast<const float *>(out),
+                   static_cast<const float *>(bounds), factor, argmax);
+            break;
+        case 8:
+            launch(ctx, "head_argmax", k_head_argmax<8, false>, dim3(batch), dim3(kArgmaxThreads),
+                   0, v, inputs, static_cast<const float *>(out),
+                   static_cast<const float *>(bounds), factor, argmax);
+            break;
+        default:
+            launch(ctx, "head_argmax", k_head_argmax<16, true>, dim3(batch), dim3(kArgmaxThreads),
+                   0, v, inputs, static_cast<const float *>(out),
+                   static_cast<const float *>(bounds), factor, argmax);
+            break;
+        }
+    });
+}
+
+}  // extern "C"

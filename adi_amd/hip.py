@@ -1,0 +1,346 @@
+"""ctypes binding of libadi_hip.so, the C ABI in include/adi_hip.h.
+
+torch is used only to own device memory and to hand its current stream to the
+library; every computation runs in the library's HIP kernels. Loading fails
+loudly when the library is not built: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY = os.path.join(HERE, "libadi_hip.so")
+
+OK = 0
+INVALID_ARGUMENT = -1
+OUT_OF_MEMORY = -2
+DEVICE_ERROR = -3
+
+vp = C.c_void_p
+u32 = C.c_uint32
+f32 = C.c_float
+
+
+class ExpertMatrix(C.Structure):
+    _fields_ = [("rows", u32), ("columns", u32), ("trellis", vp), ("su_f16", vp),
+                ("sv_f16", vp), ("wave_gamma_f16", vp), ("codebook", vp)]
+
+
+class NeMatrix(C.Structure):
+    _fields_ = [("rows", u32), ("columns", u32), ("trellis", vp), ("su", vp), ("sv", vp),
+                ("weight_scale", f32), ("codebook", vp)]
+
+
+class HeadChunk(C.Structure):
+    _fields_ = [("rows", u32), ("columns", u32), ("packed", vp), ("group_scale_f16", vp),
+                ("protected_rows", vp), ("protected_bf16", vp), ("protected_count", u32)]
+
+
+class Bf16Matrix(C.Structure):
+    _fields_ = [("rows", u32), ("columns", u32), ("values", vp)]
+
+
+class ExpertStack(C.Structure):
+    _fields_ = [("trellis", vp), ("su_f16", vp), ("sv_f16", vp), ("wave_gamma_f16", vp)]
+
+
+class MoeLayer(C.Structure):
+    _fields_ = [("hidden", u32), ("expert_hidden", u32), ("experts", u32),
+                ("router", Bf16Matrix), ("shared_expert_gate", Bf16Matrix),
+                ("gate", ExpertStack), ("up", ExpertStack), ("down", ExpertStack),
+                ("expert_codebook", vp),
+                ("shared_gate", NeMatrix), ("shared_up", NeMatrix), ("shared_down", NeMatrix)]
+
+
+class KernelProfile(C.Structure):
+    _fields_ = [("name", C.c_char * 48), ("launches", C.c_uint64), ("total_ms", C.c_double)]
+
+
+# (name, restype, argtypes) of every exported entry point.
+SIGNATURES = [
+    ("adi_hip_context_create", C.c_int, [C.c_int, C.POINTER(vp)]),
+    ("adi_hip_context_destroy", None, [vp]),
+    ("adi_hip_last_error", C.c_char_p, [vp]),
+    ("adi_hip_set_stream", C.c_int, [vp, vp]),
+    ("adi_hip_synchronize", C.c_int, [vp]),
+    ("adi_hip_set_reduction_isa", C.c_int, [vp, u32]),
+    ("adi_hip_codebook_create_expert", C.c_int, [vp, vp, C.POINTER(vp)]),
+    ("adi_hip_codebook_create_ne", C.c_int, [vp, vp, C.POINTER(vp)]),
+    ("adi_hip_codebook_destroy", None, [vp]),
+    ("adi_hip_expert_matmul", C.c_int, [vp, C.POINTER(ExpertMatrix), vp, u32, vp]),
+    ("adi_hip_expert_matvec", C.c_int, [vp, C.POINTER(ExpertMatrix), vp, vp]),
+    ("adi_hip_ne_matmul", C.c_int, [vp, C.POINTER(NeMatrix), vp, u32, vp]),
+    ("adi_hip_ne_matvec", C.c_int, [vp, C.POINTER(NeMatrix), vp, vp]),
+    ("adi_hip_expert_decode", C.c_int, [vp, C.POINTER(ExpertMatrix), vp]),
+    ("adi_hip_ne_decode", C.c_int, [vp, C.POINTER(NeMatrix), vp]),
+    ("adi_hip_head_matmul", C.c_int, [vp, C.POINTER(HeadChunk), vp, u32, vp]),
+    ("adi_hip_head_matvec", C.c_int, [vp, C.POINTER(HeadChunk), vp, vp]),
+    ("adi_hip_head_argmax", C.c_int, [vp, C.POINTER(HeadChunk), vp, u32, vp, vp]),
+    ("adi_hip_bf16_matmul", C.c_int, [vp, C.POINTER(Bf16Matrix), vp, u32, vp]),
+    ("adi_hip_bf16_matvec", C.c_int, [vp, C.POINTER(Bf16Matrix), vp, vp]),
+    ("adi_hip_rms_norm", C.c_int, [vp, vp, vp, u32, u32, f32, f32, vp]),
+    ("adi_hip_top_experts", C.c_int, [vp, vp, u32, u32, vp, vp]),
+    ("adi_hip_moe_route", C.c_int, [vp, vp, vp, u32, u32, vp, vp, vp, vp, vp, vp]),
+    ("adi_hip_moe_forward", C.c_int, [vp, C.POINTER(MoeLayer), vp, u32, vp, vp, vp, vp]),
+    ("adi_hip_profiling_enable", C.c_int, [vp, C.c_int]),
+    ("adi_hip_profiling_read", C.c_int, [vp, C.POINTER(KernelProfile), u32, C.POINTER(u32)]),
+]
+
+_lib: Optional[C.CDLL] = None
+
+
+def load() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIBRARY):
+            raise RuntimeError(
+                f"{LIBRARY} is not built: run `python -m adi_amd.build` (the HIP path has no fallback)")
+        lib = C.CDLL(LIBRARY)
+        for name, restype, argtypes in SIGNATURES:
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+    return _lib
+
+
+class HipError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"status {status}: {message}")
+        self.status = status
+
+
+def _addr(t) -> Optional[int]:
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+class Context:
+    """One adi_hip_context bound to torch's current stream on `device`."""
+
+    def __init__(self, device: int = 0, isa_lanes: int = 16):
+        import torch
+        self.torch = torch
+        self.lib = load()
+        handle = vp()
+        status = self.lib.adi_hip_context_create(device, C.byref(handle))
+        if status != OK:
+            raise HipError(status, self.lib.adi_hip_last_error(None).decode())
+        self.handle = handle
+        self.device = device
+        self._books = []
+        self.check(self.lib.adi_hip_set_stream(self.handle, vp(torch.cuda.current_stream(device).cuda_stream)))
+        self.set_isa(isa_lanes)
+
+    # -- plumbing --
+    def check(self, status: int) -> None:
+        if status != OK:
+            raise HipError(status, self.lib.adi_hip_last_error(self.handle).decode())
+
+    def set_isa(self, lanes: int) -> None:
+        self.check(self.lib.adi_hip_set_reduction_isa(self.handle, lanes))
+        self.isa_lanes = lanes
+
+    def synchronize(self) -> None:
+        self.check(self.lib.adi_hip_synchronize(self.handle))
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            for book in self._books:
+                self.lib.adi_hip_codebook_destroy(book)
+            self._books = []
+            self.lib.adi_hip_context_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- codebooks --
+    def expert_codebook(self, tlut: np.ndarray) -> int:
+        tlut = np.ascontiguousarray(tlut, np.float32)
+        out = vp()
+        self.check(self.lib.adi_hip_codebook_create_expert(self.handle, tlut.ctypes.data, C.byref(out)))
+        self._books.append(out)
+        return out.value
+
+    def ne_codebook(self, tlut: np.ndarray) -> int:
+        tlut = np.ascontiguousarray(tlut, np.float32)
+        out = vp()
+        self.check(self.lib.adi_hip_codebook_create_ne(self.handle, tlut.ctypes.data, C.byref(out)))
+        self._books.append(out)
+        return out.value
+
+    # -- device upload helpers --
+    def to_device(self, array: np.ndarray):
+        torch = self.torch
+        array = np.ascontiguousarray(array)
+        dtype = {np.dtype(np.uint16): torch.int16, np.dtype(np.int8): torch.int8,
+                 np.dtype(np.uint8): torch.uint8, np.dtype(np.uint32): torch.int32,
+                 np.dtype(np.float32): torch.float32}[array.dtype]
+        view = array.view({torch.int16: np.int16, torch.int8: np.int8, torch.uint8: np.uint8,
+                           torch.int32: np.int32, torch.float32: np.float32}[dtype])
+        return torch.from_numpy(view).to(f"cuda:{self.device}")
+
+    # -- profiling --
+    def profiling(self, enabled: bool) -> None:
+        self.check(self.lib.adi_hip_profiling_enable(self.handle, 1 if enabled else 0))
+
+    def profile(self) -> dict:
+        count = u32()
+        buf = (KernelProfile * 64)()
+        self.check(self.lib.adi_hip_profiling_read(self.handle, buf, 64, C.byref(count)))
+        return {buf[i].name.decode(): (buf[i].launches, buf[i].total_ms)
+                for i in range(min(count.value, 64))}
+
+
+@dataclass
+class DeviceExpert:
+    struct: ExpertMatrix
+    tensors: tuple
+
+
+@dataclass
+class DeviceNe:
+    struct: NeMatrix
+    tensors: tuple
+
+
+@dataclass
+class DeviceHead:
+    struct: HeadChunk
+    tensors: tuple
+
+
+def upload_expert(ctx: Context, m, codebook: int) -> DeviceExpert:
+    t = tuple(ctx.to_device(a) for a in (m.trellis, m.su_f16, m.sv_f16, m.wave_gamma_f16))
+    s = ExpertMatrix(m.rows, m.columns, *(x.data_ptr() for x in t), codebook)
+    return DeviceExpert(s, t)
+
+
+def upload_ne(ctx: Context, m, codebook: int) -> DeviceNe:
+    t = tuple(ctx.to_device(a) for a in (m.trellis, m.su, m.sv))
+    s = NeMatrix(m.rows, m.columns, t[0].data_ptr(), t[1].data_ptr(), t[2].data_ptr(),
+                 float(m.weight_scale), codebook)
+    return DeviceNe(s, t)
+
+
+def upload_head(ctx: Context, h) -> DeviceHead:
+    packed = ctx.to_device(h.packed)
+    scales = ctx.to_device(h.group_scale_f16)
+    tensors = [packed, scales]
+    prot_rows = prot_vals = None
+    count = 0
+    if h.protected_rows is not None and h.protected_rows.size:
+        prot_rows = ctx.to_device(h.protected_rows)
+        prot_vals = ctx.to_device(h.protected_bf16)
+        tensors += [prot_rows, prot_vals]
+        count = int(h.protected_rows.size)
+    s = HeadChunk(h.rows, h.columns, packed.data_ptr(), scales.data_ptr(),
+                  _addr(prot_rows), _addr(prot_vals), count)
+    return DeviceHead(s, tuple(tensors))
+
+
+@dataclass
+class DeviceMoeLayer:
+    struct: MoeLayer
+    tensors: tuple
+    experts: int
+    hidden: int
+
+
+def stack_experts(mats):
+    return (np.concatenate([m.trellis for m in mats]), np.concatenate([m.su_f16 for m in mats]),
+            np.concatenate([m.sv_f16 for m in mats]), np.concatenate([m.wave_gamma_f16 for m in mats]))
+
+
+def upload_moe_layer(ctx: Context, layer, expert_book: int, ne_book: int) -> DeviceMoeLayer:
+    keep = []
+
+    def dev(a):
+        t = ctx.to_device(a)
+        keep.append(t)
+        return t.data_ptr()
+
+    stacks = []
+    for mats in (layer.gate, layer.up, layer.down):
+        stacks.append(ExpertStack(*(dev(a) for a in stack_experts(mats))))
+    shared = []
+    for m in (layer.shared_gate, layer.shared_up, layer.shared_down):
+        d = upload_ne(ctx, m, ne_book)
+        keep.extend(d.tensors)
+        shared.append(d.struct)
+    router = Bf16Matrix(layer.experts, layer.hidden, dev(layer.router_bf16))
+    gate = Bf16Matrix(1, layer.hidden, dev(layer.shared_expert_gate_bf16))
+    s = MoeLayer(layer.hidden, layer.expert_hidden, layer.experts, router, gate,
+                 stacks[0], stacks[1], stacks[2], expert_book, shared[0], shared[1], shared[2])
+    return DeviceMoeLayer(s, tuple(keep), layer.experts, layer.hidden)
+
+
+# ---- calls on device tensors ------------------------------------------------
+
+def expert_matmul(ctx: Context, m: DeviceExpert, x, batch: int, out) -> None:
+    ctx.check(ctx.lib.adi_hip_expert_matmul(ctx.handle, C.byref(m.struct), x.data_ptr(), batch,
+                                            out.data_ptr()))
+
+
+def expert_decode(ctx: Context, m: DeviceExpert, out) -> None:
+    ctx.check(ctx.lib.adi_hip_expert_decode(ctx.handle, C.byref(m.struct), out.data_ptr()))
+
+
+def ne_decode(ctx: Context, m: DeviceNe, out) -> None:
+    ctx.check(ctx.lib.adi_hip_ne_decode(ctx.handle, C.byref(m.struct), out.data_ptr()))
+
+
+def ne_matmul(ctx: Context, m: DeviceNe, x, batch: int, out) -> None:
+    ctx.check(ctx.lib.adi_hip_ne_matmul(ctx.handle, C.byref(m.struct), x.data_ptr(), batch,
+                                        out.data_ptr()))
+
+
+def head_matmul(ctx: Context, h: DeviceHead, x, batch: int, out) -> None:
+    ctx.check(ctx.lib.adi_hip_head_matmul(ctx.handle, C.byref(h.struct), x.data_ptr(), batch,
+                                          out.data_ptr()))
+
+
+def head_argmax(ctx: Context, h: DeviceHead, x, batch: int, logits, argmax) -> None:
+    ctx.check(ctx.lib.adi_hip_head_argmax(ctx.handle, C.byref(h.struct), x.data_ptr(), batch,
+                                          _addr(logits), argmax.data_ptr()))
+
+
+def bf16_matmul(ctx: Context, values, rows: int, columns: int, x, batch: int, out) -> None:
+    s = Bf16Matrix(rows, columns, values.data_ptr())
+    ctx.check(ctx.lib.adi_hip_bf16_matmul(ctx.handle, C.byref(s), x.data_ptr(), batch,
+                                          out.data_ptr()))
+
+
+def rms_norm(ctx: Context, x, weight, count: int, rows: int, offset: float, eps: float, out) -> None:
+    ctx.check(ctx.lib.adi_hip_rms_norm(ctx.handle, x.data_ptr(), weight.data_ptr(), count, rows,
+                                       offset, eps, out.data_ptr()))
+
+
+def top_experts(ctx: Context, logits, batch: int, experts: int, route_expert, route_weight) -> None:
+    ctx.check(ctx.lib.adi_hip_top_experts(ctx.handle, logits.data_ptr(), batch, experts,
+                                          route_expert.data_ptr(), route_weight.data_ptr()))
+
+
+def moe_route(ctx: Context, logits, bias, batch: int, experts: int, out: dict) -> None:
+    ctx.check(ctx.lib.adi_hip_moe_route(
+        ctx.handle, logits.data_ptr(), _addr(bias), batch, experts,
+        out["route_expert"].data_ptr(), out["route_weight"].data_ptr(), out["counts"].data_ptr(),
+        out["offsets"].data_ptr(), out["grouped_batch"].data_ptr(),
+        out["route_to_grouped"].data_ptr()))
+
+
+def moe_forward(ctx: Context, layer: DeviceMoeLayer, x, batch: int, bias, out,
+                route_expert=None, route_weight=None) -> None:
+    ctx.check(ctx.lib.adi_hip_moe_forward(ctx.handle, C.byref(layer.struct), x.data_ptr(), batch,
+                                          _addr(bias), out.data_ptr(), _addr(route_expert),
+                                          _addr(route_weight)))

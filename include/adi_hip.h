@@ -1,0 +1,272 @@
+/*
+ * adi_hip.h -- C ABI of the MI355X (gfx950) packed-weight hot path of ADI.
+ *
+ * This is the drop-in boundary for ADI's backend op table. The reference
+ * evaluates every packed projection through `struct adi::Backend`
+ * (include/adi/backend.hpp:10-23), a table of C++ function pointers over
+ * std::span host views, and its MoE glue lives in the executor
+ * (src/executor.cpp:188-330, 1181-1453). Each entry point below replaces one of
+ * those, taking plain pointers and sizes:
+ *
+ *   * matrix descriptors hold DEVICE pointers to the packed data, which stays
+ *     packed in HBM and is decoded inside the kernels;
+ *   * activations are DEVICE pointers owned by the caller;
+ *   * every call is asynchronous on the context's HIP stream;
+ *   * no call throws: each returns an ADI_HIP_* status, and
+ *     adi_hip_last_error() gives the message. The reference throws
+ *     std::invalid_argument for the same shape violations
+ *     (src/kernels.cpp:393-408, 504-521, 606-620, 719-735, 855-862,
+ *     988-1016); the C++ backend shim maps statuses back to exceptions.
+ *
+ * Calls on one context are serialised by the caller (one context per host
+ * thread, or external locking); contexts are independent.
+ */
+#ifndef ADI_HIP_H
+#define ADI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define ADI_HIP_OK 0
+#define ADI_HIP_INVALID_ARGUMENT (-1) /* reference: std::invalid_argument */
+#define ADI_HIP_OUT_OF_MEMORY (-2)
+#define ADI_HIP_DEVICE_ERROR (-3)     /* a HIP runtime call failed */
+
+typedef struct adi_hip_context adi_hip_context;
+typedef struct adi_hip_codebook adi_hip_codebook;
+
+/* ---- context ------------------------------------------------------------ */
+
+/* Creates a context on `device` (HIP ordinal). Replaces cpu_backend()
+ * (src/backend.cpp:11-26): one context is one backend instance. */
+int adi_hip_context_create(int device, adi_hip_context **out);
+void adi_hip_context_destroy(adi_hip_context *ctx);
+
+/* Message of the last failed call on this context ("" if none). A NULL
+ * context gives the message of the last failed adi_hip_context_create. */
+const char *adi_hip_last_error(const adi_hip_context *ctx);
+
+/* Stream the context launches on (a hipStream_t; NULL = the null stream). */
+int adi_hip_set_stream(adi_hip_context *ctx, void *stream);
+int adi_hip_synchronize(adi_hip_context *ctx);
+
+/* CPU reduction order the ISA-ordered bf16 dot reproduces, so that router
+ * logits, and therefore routes, are bit-identical with the CPU build:
+ * 1 = scalar, 8 = AVX2 lanes, 16 = AVX-512 lanes with fused multiply-add
+ * (src/simd.cpp:88-96, src/simd_x86_avx2.cpp:172-193,
+ * src/simd_x86_avx512.cpp:109-130; ADI_CPU_ISA selects it there,
+ * src/simd.cpp:298-342). Default 16. */
+int adi_hip_set_reduction_isa(adi_hip_context *ctx, uint32_t lanes);
+
+/* ---- codebooks ------------------------------------------------------------ */
+
+/* Model-wide decoded-state tables, built once from the host TLUT and kept in
+ * HBM as f16 (exact: the reference rounds every lattice value through f16,
+ * src/codec_cache.cpp:27-29, 33-115). Replace the ExpertScratch caches and
+ * MachModel::cache_descriptors (src/kernels.cpp:33-94, src/model.cpp:549-551).
+ *   expert: tlut 32768x8 f32 -> the 16384 reachable rows x 8 f16 (256 KiB;
+ *           state s selects row (s*(s+1) mod 2^15)/2, always even);
+ *   ne:     tlut 512x2 f32 -> the 1024x2 signed table (4 KiB). */
+int adi_hip_codebook_create_expert(adi_hip_context *ctx, const float *tlut_host,
+                                   adi_hip_codebook **out);
+int adi_hip_codebook_create_ne(adi_hip_context *ctx, const float *tlut_host,
+                               adi_hip_codebook **out);
+void adi_hip_codebook_destroy(adi_hip_codebook *codebook);
+
+/* ---- matrix descriptors (all pointers are device pointers) --------------- */
+
+/* adi::MachExpertMatrix (include/adi/kernels.hpp:9-20). */
+typedef struct {
+    uint32_t rows;
+    uint32_t columns;
+    const uint16_t *trellis;        /* (rows/16)*(columns/16)*24 u16 words */
+    const uint16_t *su_f16;         /* columns */
+    const uint16_t *sv_f16;         /* rows */
+    const uint16_t *wave_gamma_f16; /* rows/16 + columns/16 */
+    const adi_hip_codebook *codebook; /* expert codebook */
+} adi_hip_expert_matrix;
+
+/* adi::MachNeMatrix (include/adi/kernels.hpp:42-52). */
+typedef struct {
+    uint32_t rows;
+    uint32_t columns;
+    const uint16_t *trellis; /* (rows/16)*(columns/16)*64 u16 words */
+    const int8_t *su;        /* columns, +-1 */
+    const int8_t *sv;        /* rows, +-1 */
+    float weight_scale;
+    const adi_hip_codebook *codebook; /* NE codebook */
+} adi_hip_ne_matrix;
+
+/* adi::MachHeadChunk (include/adi/kernels.hpp:64-71). */
+typedef struct {
+    uint32_t rows;
+    uint32_t columns;
+    const uint8_t *packed;           /* rows*columns/8*5 bytes */
+    const uint16_t *group_scale_f16; /* rows*columns/64 */
+    const uint32_t *protected_rows;  /* protected_count, may be NULL if 0 */
+    const uint16_t *protected_bf16;  /* protected_count*columns */
+    uint32_t protected_count;
+} adi_hip_head_chunk;
+
+/* adi::Bf16Matrix (include/adi/kernels.hpp:73-77). */
+typedef struct {
+    uint32_t rows;
+    uint32_t columns;
+    const uint16_t *values; /* rows*columns bf16 bits, row-major */
+} adi_hip_bf16_matrix;
+
+/* ---- Backend op table entries -------------------------------------------- */
+/* Inputs [batch, columns] and outputs [batch, rows], batch-major, device. */
+
+/* Backend::expert_matvec / expert_matmul -> mach_expert_matvec/matmul
+ * (src/kernels.cpp:385-593): y = sv * H_R(Z), Z[r] = sum over tile columns of
+ * gamma(tile) * (decoded tile row . x_hat), x_hat = H_C(su * x). */
+int adi_hip_expert_matmul(adi_hip_context *ctx, const adi_hip_expert_matrix *m,
+                          const float *inputs, uint32_t batch, float *outputs);
+int adi_hip_expert_matvec(adi_hip_context *ctx, const adi_hip_expert_matrix *m,
+                          const float *input, float *output);
+
+/* Backend::ne_matvec / ne_matmul -> mach_ne_matvec/matmul
+ * (src/kernels.cpp:595-800). */
+int adi_hip_ne_matmul(adi_hip_context *ctx, const adi_hip_ne_matrix *m,
+                      const float *inputs, uint32_t batch, float *outputs);
+int adi_hip_ne_matvec(adi_hip_context *ctx, const adi_hip_ne_matrix *m,
+                      const float *input, float *output);
+
+/* The decoded weights of a packed matrix as a dense fp32 [rows, columns]
+ * array, through the same loads and decode the GEMV kernels use: expert
+ * lattice values V (before the tile gamma and the su/sv/Hadamard rotations),
+ * NE values V * Wscale. Bit-identical with the reference's state tables
+ * (src/codec_cache.cpp:33-115) walked tile by tile
+ * (src/expert_trellis.hpp:44-105, src/ne_trellis.hpp:27-97); no reference
+ * function returns them as one array, they exist there only inside the
+ * projection loops (src/kernels.cpp:103-264). */
+int adi_hip_expert_decode(adi_hip_context *ctx, const adi_hip_expert_matrix *m,
+                          float *values);
+int adi_hip_ne_decode(adi_hip_context *ctx, const adi_hip_ne_matrix *m,
+                      float *values);
+
+/* Backend::head_matvec / head_matmul -> mach_head_matvec/matmul
+ * (src/kernels.cpp:847-979): int5_g64 logits, protected rows replaced by the
+ * ISA-ordered bf16 dot. Logits agree with the CPU path to fp32 rounding of a
+ * different summation order (the argmax is made exact by
+ * adi_hip_head_argmax). */
+int adi_hip_head_matmul(adi_hip_context *ctx, const adi_hip_head_chunk *h,
+                        const float *inputs, uint32_t batch, float *outputs);
+int adi_hip_head_matvec(adi_hip_context *ctx, const adi_hip_head_chunk *h,
+                        const float *input, float *output);
+
+/* Head logits plus the greedy token of each row: the first maximum, as
+ * sample_token at temperature 0 takes it (std::max_element,
+ * src/generation.cpp:177-180). Every row whose GPU logit lies within the
+ * summation-order error bound of the top GPU logit is re-evaluated in the CPU
+ * reduction order of adi_hip_set_reduction_isa, so the index is the one the
+ * CPU path returns. logits (nullable, device [batch, rows]) receives the
+ * logits of adi_hip_head_matmul; argmax [batch] u32, device. */
+int adi_hip_head_argmax(adi_hip_context *ctx, const adi_hip_head_chunk *h,
+                        const float *inputs, uint32_t batch, float *logits,
+                        uint32_t *argmax);
+
+/* Backend::dense_bf16_matvec / dense_bf16_matmul -> bf16_matvec/matmul
+ * (src/kernels.cpp:981-1050), in the CPU reduction order of
+ * adi_hip_set_reduction_isa: bit-identical with the CPU build. */
+int adi_hip_bf16_matmul(adi_hip_context *ctx, const adi_hip_bf16_matrix *m,
+                        const float *inputs, uint32_t batch, float *outputs);
+int adi_hip_bf16_matvec(adi_hip_context *ctx, const adi_hip_bf16_matrix *m,
+                        const float *input, float *output);
+
+/* Backend::normalize_rms -> rms_norm (src/kernels.cpp:1052-1073), applied to
+ * each of `rows` vectors of `count` values. */
+int adi_hip_rms_norm(adi_hip_context *ctx, const float *input,
+                     const uint16_t *weight_bf16, uint32_t count, uint32_t rows,
+                     float weight_offset, float epsilon, float *output);
+
+/* ---- executor-level MoE entries (new backend surface) --------------------- */
+
+/* top_experts for each of `batch` logit rows (src/executor.cpp:193-229):
+ * (logit desc, index asc), softmax over the eight. route_expert [batch*8] u32,
+ * route_weight [batch*8] f32, device. Indices are exact; weights agree to
+ * the last bits of expf. */
+int adi_hip_top_experts(adi_hip_context *ctx, const float *logits,
+                        uint32_t batch, uint32_t experts,
+                        uint32_t *route_expert, float *route_weight);
+
+/* Routing plus the stable counting sort of moe_forward_batch
+ * (src/executor.cpp:1221-1258). logit_bias (nullable) [experts] is added to
+ * each logit row first. Outputs (device): route_expert/route_weight
+ * [batch*8], counts [experts], offsets [experts+1], grouped_batch and
+ * route_to_grouped [batch*8]. The permutation is exact. */
+int adi_hip_moe_route(adi_hip_context *ctx, const float *logits,
+                      const float *logit_bias, uint32_t batch, uint32_t experts,
+                      uint32_t *route_expert, float *route_weight,
+                      uint32_t *counts, uint32_t *offsets,
+                      uint32_t *grouped_batch, uint32_t *route_to_grouped);
+
+/* Per-expert matrices stacked expert-major, as the checkpoint's 32-expert
+ * chunks are (src/model.cpp:483-532): expert e's trellis starts at
+ * e*(rows/16)*(columns/16)*24 words, su at e*columns, sv at e*rows, gamma at
+ * e*(rows/16 + columns/16). */
+typedef struct {
+    const uint16_t *trellis;
+    const uint16_t *su_f16;
+    const uint16_t *sv_f16;
+    const uint16_t *wave_gamma_f16;
+} adi_hip_expert_stack;
+
+/* The fields of one layer's MoE descriptor (include/adi/model.hpp:30-37,
+ * read by src/executor.cpp:254-324). */
+typedef struct {
+    uint32_t hidden;        /* 2048 */
+    uint32_t expert_hidden; /* 512 */
+    uint32_t experts;       /* 256 */
+    adi_hip_bf16_matrix router;             /* experts x hidden */
+    adi_hip_bf16_matrix shared_expert_gate; /* 1 x hidden */
+    adi_hip_expert_stack gate;  /* experts x (expert_hidden x hidden) */
+    adi_hip_expert_stack up;    /* experts x (expert_hidden x hidden) */
+    adi_hip_expert_stack down;  /* experts x (hidden x expert_hidden) */
+    const adi_hip_codebook *expert_codebook;
+    adi_hip_ne_matrix shared_gate; /* expert_hidden x hidden */
+    adi_hip_ne_matrix shared_up;   /* expert_hidden x hidden */
+    adi_hip_ne_matrix shared_down; /* hidden x expert_hidden */
+} adi_hip_moe_layer;
+
+/* One MoE block for `batch` rows: moe_forward (batch 1,
+ * src/executor.cpp:242-330) and moe_forward_batch (src/executor.cpp:
+ * 1181-1453). Routing uses the bit-exact router and sort; the eight expert
+ * outputs are combined in route order, then the sigmoid-gated shared expert
+ * is added. logit_bias (nullable, device [experts]) is added to the router
+ * logits before top_experts. route_expert/route_weight (nullable, device
+ * [batch*8]) receive the routes. Workspace is cached in the context and grows
+ * to the largest batch seen. */
+int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *layer,
+                        const float *inputs, uint32_t batch,
+                        const float *logit_bias, float *outputs,
+                        uint32_t *route_expert, float *route_weight);
+
+/* ---- kernel profiling ----------------------------------------------------- */
+
+/* Per-kernel timing with HIP events on the context stream, the counterpart
+ * of the reference's KernelTimer / kernel_profiles()
+ * (include/adi/profiling.hpp:9-40). Enabling resets the counters. */
+typedef struct {
+    char name[48];
+    uint64_t launches;
+    double total_ms;
+} adi_hip_kernel_profile;
+
+int adi_hip_profiling_enable(adi_hip_context *ctx, int enabled);
+/* Writes up to `capacity` entries; *count receives the number of kinds. The
+ * event timings are resolved here (this call synchronizes the stream). */
+int adi_hip_profiling_read(adi_hip_context *ctx, adi_hip_kernel_profile *out,
+                           uint32_t capacity, uint32_t *count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

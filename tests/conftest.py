@@ -25,3 +25,26 @@ def ref():
     if not pyoracle.ref_available():
         pytest.skip("reference CPU library (oracle/_ref) is not built here")
     return pyoracle.load_ref()
+
+
+@pytest.fixture(scope="session")
+def gpu():
+    """A context on cuda:0; fails loudly (no skip) when the library or the
+    GPU is missing, since GPU tests are selected only on a GPU box."""
+    import torch
+    from adi_amd import hip
+    assert torch.cuda.is_available(), "GPU tests need an MI355X"
+    ctx = hip.Context(0)
+    yield ctx
+    ctx.synchronize()
+    ctx.close()
+
+
+def max_rel_error(got, want):
+    """max_i |g_i - c_i| / max_i |c_i| over each output vector (last axis),
+    the worst vector returned."""
+    import numpy as np
+    got = np.asarray(got, np.float64).reshape(-1, np.shape(want)[-1])
+    want = np.asarray(want, np.float64).reshape(-1, np.shape(want)[-1])
+    scale = np.maximum(np.abs(want).max(axis=1), 1e-30)
+    return float((np.abs(got - want).max(axis=1) / scale).max())

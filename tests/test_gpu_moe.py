@@ -1,0 +1,79 @@
+"""One MoE block on the GPU against the oracle: routes bit-exact, outputs
+within max relative error 1e-3."""
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as po
+from adi_amd import hip
+from adi_amd import synthetic as syn
+from conftest import max_rel_error
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def small_layer(gpu):
+    rng = syn.rng_for(2, 5)
+    layer = syn.moe_layer(rng, hidden=256, expert_hidden=64, experts=16)
+    dl = hip.upload_moe_layer(gpu, layer, gpu.expert_codebook(layer.expert_tlut),
+                              gpu.ne_codebook(layer.ne_tlut))
+    return layer, dl
+
+
+@pytest.fixture(scope="module")
+def full_layer(gpu):
+    rng = syn.rng_for(2, 0)
+    layer = syn.moe_layer(rng)  # hidden 2048, expert 512, 256 experts
+    dl = hip.upload_moe_layer(gpu, layer, gpu.expert_codebook(layer.expert_tlut),
+                              gpu.ne_codebook(layer.ne_tlut))
+    return layer, dl
+
+
+def run_moe(gpu, dl, x, bias):
+    batch = x.shape[0]
+    out = torch.empty((batch, dl.hidden), dtype=torch.float32, device="cuda")
+    re = torch.empty(batch * 8, dtype=torch.int32, device="cuda")
+    rw = torch.empty(batch * 8, dtype=torch.float32, device="cuda")
+    hip.moe_forward(gpu, dl, gpu.to_device(x), batch, None if bias is None else gpu.to_device(bias),
+                    out, re, rw)
+    return (out.cpu().numpy(), re.cpu().numpy().astype(np.uint32).reshape(batch, 8),
+            rw.cpu().numpy().reshape(batch, 8))
+
+
+def check(oracle, layer, got, x, bias):
+    want, we, ww = po.moe_forward(oracle, layer, x, isa=16, logit_bias=bias)
+    out, ge, gw = got
+    assert np.array_equal(ge, we), "routes differ"
+    np.testing.assert_allclose(gw, ww, rtol=4e-7)
+    assert max_rel_error(out, want) <= 1e-3
+
+
+@pytest.mark.parametrize("batch", [1, 2, 4, 16, 33])
+@pytest.mark.parametrize("bias", [False, True])
+def test_moe_small(gpu, oracle, small_layer, batch, bias):
+    layer, dl = small_layer
+    rng = syn.rng_for(2, 100 + batch)
+    x = syn.hidden_states(rng, batch, layer.hidden)
+    b = syn.zipf_bias(rng, layer.experts) if bias else None
+    check(oracle, layer, run_moe(gpu, dl, x, b), x, b)
+
+
+@pytest.mark.parametrize("batch,bias", [(1, False), (4, False), (16, False), (128, True)])
+def test_moe_full(gpu, oracle, full_layer, batch, bias):
+    layer, dl = full_layer
+    rng = syn.rng_for(3 if bias else 2, 200 + batch)
+    x = syn.hidden_states(rng, batch, layer.hidden)
+    b = syn.zipf_bias(rng, layer.experts) if bias else None
+    check(oracle, layer, run_moe(gpu, dl, x, b), x, b)
+
+
+def test_moe_repeated_calls_are_deterministic(gpu, full_layer):
+    layer, dl = full_layer
+    rng = syn.rng_for(2, 77)
+    x = syn.hidden_states(rng, 16, layer.hidden)
+    first = run_moe(gpu, dl, x, None)
+    for _ in range(3):
+        again = run_moe(gpu, dl, x, None)
+        assert np.array_equal(first[0].view(np.uint32), again[0].view(np.uint32))
+        assert np.array_equal(first[1], again[1])

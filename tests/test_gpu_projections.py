@@ -1,0 +1,118 @@
+"""Packed projections on the GPU against the oracle (C restatement of the
+reference CPU path): decoded weights bit-exact, outputs within max relative
+error 1e-3 (max |g - c| / max |c| per output vector, fp32 accumulation)."""
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as po
+from adi_amd import hip
+from adi_amd import synthetic as syn
+from conftest import max_rel_error
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+EXPERT_SHAPES = [(16, 16), (64, 32), (32, 128), (512, 2048), (2048, 512), (16, 4096)]
+NE_SHAPES = [(16, 16), (64, 32), (128, 2048), (2048, 2048), (512, 2048), (2048, 512)]
+
+
+@pytest.fixture(scope="module")
+def books(gpu):
+    rng = syn.rng_for(0, 7)
+    et, nt = syn.expert_tlut(rng), syn.ne_tlut(rng)
+    return et, nt, gpu.expert_codebook(et), gpu.ne_codebook(nt)
+
+
+@pytest.mark.parametrize("rows,columns", EXPERT_SHAPES)
+def test_expert_decode_bit_exact(gpu, books, oracle, rows, columns):
+    et, _, eb, _ = books
+    m = syn.expert_matrix(syn.rng_for(0, rows * 7 + columns), rows, columns, et)
+    want = np.zeros((rows, columns), np.float32)
+    s = po.expert_struct(m)
+    po.check(oracle.ao_expert_decode_tiles(po.C.byref(s), po.ptr(want, po.C.c_float)), "decode")
+    dm = hip.upload_expert(gpu, m, eb)
+    out = torch.empty((rows, columns), dtype=torch.float32, device="cuda")
+    hip.expert_decode(gpu, dm, out)
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,columns", NE_SHAPES)
+def test_ne_decode_bit_exact(gpu, books, oracle, rows, columns):
+    _, nt, _, nb = books
+    m = syn.ne_matrix(syn.rng_for(0, rows * 11 + columns), rows, columns, nt)
+    want = np.zeros((rows, columns), np.float32)
+    s = po.ne_struct(m)
+    po.check(oracle.ao_ne_decode_tiles(po.C.byref(s), po.ptr(want, po.C.c_float)), "decode")
+    dm = hip.upload_ne(gpu, m, nb)
+    out = torch.empty((rows, columns), dtype=torch.float32, device="cuda")
+    hip.ne_decode(gpu, dm, out)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,columns", EXPERT_SHAPES)
+@pytest.mark.parametrize("batch", [1, 2, 4, 5, 16, 33])
+def test_expert_matmul(gpu, books, oracle, rows, columns, batch):
+    et, _, eb, _ = books
+    rng = syn.rng_for(0, rows + columns + batch)
+    m = syn.expert_matrix(rng, rows, columns, et)
+    x = syn.hidden_states(rng, batch, columns)
+    want = po.expert_matmul(oracle, m, x)
+    dm = hip.upload_expert(gpu, m, eb)
+    out = torch.empty((batch, rows), dtype=torch.float32, device="cuda")
+    hip.expert_matmul(gpu, dm, gpu.to_device(x), batch, out)
+    assert max_rel_error(out.cpu().numpy(), want) <= TOL
+
+
+@pytest.mark.parametrize("rows,columns", NE_SHAPES)
+@pytest.mark.parametrize("batch", [1, 3, 4, 16])
+def test_ne_matmul(gpu, books, oracle, rows, columns, batch):
+    _, nt, _, nb = books
+    rng = syn.rng_for(0, rows * 3 + columns + batch)
+    m = syn.ne_matrix(rng, rows, columns, nt)
+    x = syn.hidden_states(rng, batch, columns)
+    want = po.ne_matmul(oracle, m, x)
+    dm = hip.upload_ne(gpu, m, nb)
+    out = torch.empty((batch, rows), dtype=torch.float32, device="cuda")
+    hip.ne_matmul(gpu, dm, gpu.to_device(x), batch, out)
+    assert max_rel_error(out.cpu().numpy(), want) <= TOL
+
+
+def test_known_answers(gpu):
+    """tests/kernels_test.cpp:32-137: a zero expert tile with TLUT rows
+    1..8 and gamma slot 1 = 2 gives out[0] = 32; the NE tile with TLUT (1, 2)
+    and Wscale 0.5 gives out[0] = 8; every other output is 0."""
+    tlut = np.tile(np.arange(1, 9, dtype=np.float32), 32768)
+    one = syn.f16_bits(np.ones(16, np.float32))
+    m = syn.ExpertMatrix(16, 16, np.zeros(24, np.uint16), one, one,
+                         syn.f16_bits(np.array([1.0, 2.0], np.float32)), tlut)
+    dm = hip.upload_expert(gpu, m, gpu.expert_codebook(tlut))
+    out = torch.empty((1, 16), dtype=torch.float32, device="cuda")
+    hip.expert_matmul(gpu, dm, torch.ones((1, 16), device="cuda"), 1, out)
+    got = out.cpu().numpy()[0]
+    assert abs(got[0] - 32.0) < 1e-5 and np.all(np.abs(got[1:]) < 1e-5)
+
+    ntlut = np.tile(np.array([1.0, 2.0], np.float32), 512)
+    signs = np.ones(16, np.int8)
+    n = syn.NeMatrix(16, 16, np.zeros(64, np.uint16), signs, signs, 0.5, ntlut)
+    dn = hip.upload_ne(gpu, n, gpu.ne_codebook(ntlut))
+    hip.ne_matmul(gpu, dn, torch.ones((1, 16), device="cuda"), 1, out)
+    got = out.cpu().numpy()[0]
+    assert abs(got[0] - 8.0) < 1e-5 and np.all(np.abs(got[1:]) < 1e-5)
+
+
+def test_shape_errors_leave_outputs_untouched(gpu, books):
+    et, _, eb, _ = books
+    m = syn.expert_matrix(syn.rng_for(0, 99), 48, 16, et)  # 48 rows: not a power of two
+    dm = hip.upload_expert(gpu, m, eb)
+    out = torch.full((1, 48), 7.0, device="cuda")
+    with pytest.raises(hip.HipError) as err:
+        hip.expert_matmul(gpu, dm, torch.ones((1, 16), device="cuda"), 1, out)
+    assert err.value.status == hip.INVALID_ARGUMENT
+    assert "powers of two" in str(err.value)
+    assert torch.all(out == 7.0)
+    m2 = syn.expert_matrix(syn.rng_for(0, 98), 16, 16, et)
+    dm2 = hip.upload_expert(gpu, m2, eb)
+    with pytest.raises(hip.HipError):
+        hip.expert_matmul(gpu, dm2, torch.ones((1, 16), device="cuda"), 0, out)
