@@ -344,3 +344,55 @@ def moe_forward(ctx: Context, layer: DeviceMoeLayer, x, batch: int, bias, out,
     ctx.check(ctx.lib.adi_hip_moe_forward(ctx.handle, C.byref(layer.struct), x.data_ptr(), batch,
                                           _addr(bias), out.data_ptr(), _addr(route_expert),
                                           _addr(route_weight)))
+
+
+# ---- layers generated directly in device memory (benchmark rotation) --------
+
+def random_device_moe_layer(ctx: Context, seed: int, hidden: int, expert_hidden: int,
+                            experts: int, expert_book: int, ne_book: int) -> DeviceMoeLayer:
+    """A layer with the synthetic distributions of adi_amd.synthetic, drawn
+    with torch's device generator (no host round trip)."""
+    torch = ctx.torch
+    dev = f"cuda:{ctx.device}"
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    keep = []
+
+    def words(n):
+        t = torch.randint(-32768, 32768, (n,), dtype=torch.int16, device=dev, generator=g)
+        keep.append(t)
+        return t.data_ptr()
+
+    def lognormal_f16(n):
+        t = torch.empty(n, device=dev).log_normal_(0.0, 0.5, generator=g).half().view(torch.int16)
+        keep.append(t)
+        return t.data_ptr()
+
+    def bf16(shape):
+        t = (torch.randn(shape, device=dev, generator=g) * 0.02).to(torch.bfloat16).view(torch.int16)
+        keep.append(t)
+        return t.data_ptr()
+
+    def signs(n):
+        t = (torch.randint(0, 2, (n,), device=dev, generator=g) * 2 - 1).to(torch.int8)
+        keep.append(t)
+        return t.data_ptr()
+
+    def stack(rows, columns):
+        tiles = (rows // 16) * (columns // 16)
+        return ExpertStack(words(experts * tiles * 24), lognormal_f16(experts * columns),
+                           lognormal_f16(experts * rows),
+                           lognormal_f16(experts * (rows // 16 + columns // 16)))
+
+    def ne(rows, columns):
+        tiles = (rows // 16) * (columns // 16)
+        scale = float(torch.empty(1).log_normal_(0.0, 0.5, generator=torch.Generator().manual_seed(seed)).item())
+        return NeMatrix(rows, columns, words(tiles * 64), signs(columns), signs(rows), scale, ne_book)
+
+    s = MoeLayer(hidden, expert_hidden, experts,
+                 Bf16Matrix(experts, hidden, bf16((experts, hidden))),
+                 Bf16Matrix(1, hidden, bf16((1, hidden))),
+                 stack(expert_hidden, hidden), stack(expert_hidden, hidden),
+                 stack(hidden, expert_hidden), expert_book,
+                 ne(expert_hidden, hidden), ne(expert_hidden, hidden), ne(hidden, expert_hidden))
+    return DeviceMoeLayer(s, tuple(keep), experts, hidden)
