@@ -129,4 +129,73 @@ __device__ __forceinline__ void block_hadamard(float *v, uint32_t n, float scale
     __syncthreads();
 }
 
+// Value of lane (lane ^ MASK) for MASK < 32, without the LDS crossbar for
+// masks 1, 2, 4 and 8 (DPP: quad permutes, half-row mirror, row rotate by 8;
+// every pattern used is its own inverse, so the DPP shift direction does not
+// matter) and with a swizzle for 16.
+template <int MASK>
+__device__ __forceinline__ float lane_xor(float v) {
+    const int bits = __float_as_int(v);
+    if constexpr (MASK == 1) {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(bits, 0xB1, 0xF, 0xF, true));
+    } else if constexpr (MASK == 2) {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(bits, 0x4E, 0xF, 0xF, true));
+    } else if constexpr (MASK == 4) {
+        // lane i of a half-row takes lane 7-i after a [3,2,1,0] quad permute
+        const int q = __builtin_amdgcn_mov_dpp(bits, 0x1B, 0xF, 0xF, true);
+        return __int_as_float(__builtin_amdgcn_mov_dpp(q, 0x141, 0xF, 0xF, true));
+    } else if constexpr (MASK == 8) {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(bits, 0x128, 0xF, 0xF, true));
+    } else if constexpr (MASK == 16) {
+        // bitmask swizzle: and 0x1F, or 0, xor 0x10 within 32 lanes
+        return __int_as_float(__builtin_amdgcn_ds_swizzle(bits, 0x401F));
+    } else {
+        return __shfl_xor(v, MASK);
+    }
+}
+
+// Normalised FWHT of n = 64*VPL values held by one wave, element e in lane
+// e % 64, register e / 64 (consecutive lanes hold consecutive elements, so
+// loads and stores coalesce and LDS staging is conflict-free). Strides 1..32
+// pair lanes l and l ^ stride; strides 64, 128, ... pair registers. Strides
+// run 1, 2, 4, ... and each pair becomes (lo + hi, lo - hi): the reference's
+// exact sequence (src/simd.cpp:48-63), so the result is bit-identical to it.
+// Every lane of the wave must call this.
+template <int VPL>
+__device__ __forceinline__ void wave_hadamard(float (&v)[VPL], float scale, uint32_t lane) {
+#pragma clang fp contract(off)
+    // All exchanges of a stage are issued before any is consumed so the
+    // LDS-routed ones (masks 16 and 32) pipeline instead of waiting in turn.
+#define ADI_XOR_STAGE(MASK)                                              \
+    {                                                                    \
+        const bool upper = (lane & static_cast<uint32_t>(MASK)) != 0;    \
+        float other[VPL];                                                \
+        _Pragma("unroll") for (int i = 0; i < VPL; ++i) {                \
+            other[i] = lane_xor<MASK>(v[i]);                             \
+        }                                                                \
+        _Pragma("unroll") for (int i = 0; i < VPL; ++i) {                \
+            v[i] = upper ? other[i] - v[i] : v[i] + other[i];            \
+        }                                                                \
+    }
+    ADI_XOR_STAGE(1) ADI_XOR_STAGE(2) ADI_XOR_STAGE(4) ADI_XOR_STAGE(8)
+    ADI_XOR_STAGE(16) ADI_XOR_STAGE(32)
+#undef ADI_XOR_STAGE
+#pragma unroll
+    for (int stride = 1; stride < VPL; stride <<= 1) {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            if ((i & stride) == 0) {
+                const float a = v[i];
+                const float b = v[i + stride];
+                v[i] = a + b;
+                v[i + stride] = a - b;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        v[i] = v[i] * scale;
+    }
+}
+
 }  // namespace adi_hip

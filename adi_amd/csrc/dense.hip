@@ -87,6 +87,123 @@ __global__ __launch_bounds__(256) void k_bf16_ordered(
     out[static_cast<size_t>(t0 + t) * rows + row] = sum;
 }
 
+// Faster form of the same order for widths up to 4096: one wave per block
+// holding 64/LANES rows x LANES lanes; the block's weight rows and its
+// kTokensPerThread tokens are first staged in LDS with wide coalesced loads,
+// so the lanes' strictly sequential multiply-add chains read only LDS. An
+// optional extra row (the shared-expert gate) is appended after `rows` and
+// written to `out_extra`.
+template <int LANES, bool FUSED>
+__global__ __launch_bounds__(64) void k_bf16_lds(
+    const uint16_t *__restrict__ w, uint32_t rows, const uint16_t *__restrict__ w_extra,
+    uint32_t columns, const float *__restrict__ x, uint32_t batch, float *__restrict__ out,
+    float *__restrict__ out_extra) {
+#pragma clang fp contract(off)
+    constexpr uint32_t rows_per_block = 64 / LANES;
+    extern __shared__ float xs[];  // [tokens][columns] then [rows_per_block][columns] bf16
+    const uint32_t t0 = blockIdx.y * kTokensPerThread;
+    const uint32_t tokens = batch - t0 < kTokensPerThread ? batch - t0 : kTokensPerThread;
+    uint16_t *ws = reinterpret_cast<uint16_t *>(xs + static_cast<size_t>(kTokensPerThread) * columns);
+    for (uint32_t t = tokens; t < kTokensPerThread; ++t) {
+        for (uint32_t k = threadIdx.x; k < columns; k += 64u) {
+            xs[t * columns + k] = 0.0f;
+        }
+    }
+    const uint32_t total_rows = rows + (w_extra != nullptr ? 1u : 0u);
+    const uint32_t row0 = blockIdx.x * rows_per_block;
+    const bool wide = (columns % 8u) == 0;  // 16-byte staging when rows stay aligned
+    for (uint32_t t = 0; t < tokens; ++t) {
+        const float *src = x + static_cast<size_t>(t0 + t) * columns;
+        if (wide) {
+            for (uint32_t k = threadIdx.x; k < columns / 4u; k += 64u) {
+                reinterpret_cast<float4 *>(xs + t * columns)[k] = reinterpret_cast<const float4 *>(src)[k];
+            }
+        } else {
+            for (uint32_t k = threadIdx.x; k < columns; k += 64u) {
+                xs[t * columns + k] = src[k];
+            }
+        }
+    }
+    for (uint32_t r = 0; r < rows_per_block; ++r) {
+        const uint32_t row = row0 + r;
+        if (row >= total_rows) {
+            break;
+        }
+        const uint16_t *src = row < rows ? w + static_cast<size_t>(row) * columns : w_extra;
+        if (wide) {
+            for (uint32_t k = threadIdx.x; k < columns / 8u; k += 64u) {
+                reinterpret_cast<uint4 *>(ws + r * columns)[k] = reinterpret_cast<const uint4 *>(src)[k];
+            }
+        } else {
+            for (uint32_t k = threadIdx.x; k < columns; k += 64u) {
+                ws[r * columns + k] = src[k];
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t lane = threadIdx.x % LANES;
+    const uint32_t local_row = threadIdx.x / LANES;
+    const uint32_t row = row0 + local_row;
+    const bool row_ok = row < total_rows;
+    const uint16_t *wr = ws + local_row * columns;
+    const uint32_t full = columns / LANES * LANES;
+    float acc[kTokensPerThread] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (row_ok) {
+        constexpr uint32_t kUnroll = 8;
+        uint32_t base = 0;
+        // operands of kUnroll steps are read first, then the chain advances
+        for (; base + kUnroll * LANES <= full; base += kUnroll * LANES) {
+            float wk[kUnroll], xk[kTokensPerThread][kUnroll];
+#pragma unroll
+            for (uint32_t u = 0; u < kUnroll; ++u) {
+                const uint32_t k = base + u * LANES + lane;
+                wk[u] = bf16_bits_to_float(wr[k]);
+#pragma unroll
+                for (uint32_t t = 0; t < kTokensPerThread; ++t) {
+                    xk[t][u] = xs[t * columns + k];
+                }
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < kUnroll; ++u) {
+#pragma unroll
+                for (uint32_t t = 0; t < kTokensPerThread; ++t) {
+                    acc[t] = lane_step<LANES, FUSED>(acc[t], wk[u], xk[t][u]);
+                }
+            }
+        }
+        for (; base < full; base += LANES) {
+            const uint32_t k = base + lane;
+            const float wk = bf16_bits_to_float(wr[k]);
+#pragma unroll
+            for (uint32_t t = 0; t < kTokensPerThread; ++t) {
+                acc[t] = lane_step<LANES, FUSED>(acc[t], wk, xs[t * columns + k]);
+            }
+        }
+    }
+    // ordered lane sums through LDS: lane t of each row finishes token t
+    __shared__ float lane_sums[kTokensPerThread][64];
+#pragma unroll
+    for (uint32_t t = 0; t < kTokensPerThread; ++t) {
+        lane_sums[t][threadIdx.x] = acc[t];
+    }
+    __syncthreads();
+    if (!row_ok || lane >= tokens) {
+        return;
+    }
+    float sum = 0.0f;
+    for (uint32_t j = 0; j < LANES; ++j) {
+        sum = sum + lane_sums[lane][local_row * LANES + j];
+    }
+    for (uint32_t k = full; k < columns; ++k) {
+        sum = lane_step<LANES, FUSED>(sum, bf16_bits_to_float(wr[k]), xs[lane * columns + k]);
+    }
+    if (row < rows) {
+        out[static_cast<size_t>(t0 + lane) * rows + row] = sum;
+    } else {
+        out_extra[t0 + lane] = sum;
+    }
+}
+
 // The scalar order has one lane per row; its "lane sum" is 0 + the row sum,
 // so the generic kernel with LANES = 1 would need four lanes to finish four
 // tokens. This variant gives each thread one (row, token).
@@ -142,13 +259,13 @@ __device__ __forceinline__ bool route_before(float a, uint32_t ia, float b, uint
 // a wave-wide arg-max by the comparator pick the routes in order. The softmax
 // over the eight then runs on lane 0 in the reference's order
 // (src/executor.cpp:213-227).
-__global__ __launch_bounds__(64) void k_top_experts(
-    const float *__restrict__ logits, const float *__restrict__ bias, uint32_t experts,
-    uint32_t *__restrict__ route_expert, float *__restrict__ route_weight) {
+template <int SLOTS>
+__device__ __forceinline__ void top8_wave(const float *__restrict__ row,
+                                          const float *__restrict__ bias, uint32_t experts,
+                                          uint32_t lane, uint32_t *__restrict__ route_expert,
+                                          float *__restrict__ route_weight) {
 #pragma clang fp contract(off)
-    constexpr uint32_t per_lane = kMaxExperts / 64;
-    const uint32_t lane = threadIdx.x;
-    const float *row = logits + static_cast<size_t>(blockIdx.x) * experts;
+    constexpr uint32_t per_lane = SLOTS;
     float value[per_lane];
     uint32_t used = 0;
 #pragma unroll
@@ -178,16 +295,20 @@ __global__ __launch_bounds__(64) void k_top_experts(
                 best_index = e;
             }
         }
-        for (int offset = 32; offset >= 1; offset >>= 1) {
-            const float other = __shfl_xor(best, offset);
-            const uint32_t other_index = static_cast<uint32_t>(
-                __shfl_xor(static_cast<int>(best_index), offset));
-            if (other_index != 0xFFFFFFFFu &&
-                (best_index == 0xFFFFFFFFu || route_before(other, other_index, best, best_index))) {
-                best = other;
-                best_index = other_index;
-            }
-        }
+#define ADI_ARGMAX_STAGE(MASK)                                                          \
+    {                                                                                   \
+        const float other = lane_xor<MASK>(best);                                       \
+        const uint32_t other_index =                                                    \
+            __float_as_uint(lane_xor<MASK>(__uint_as_float(best_index)));               \
+        if (other_index != 0xFFFFFFFFu &&                                               \
+            (best_index == 0xFFFFFFFFu || route_before(other, other_index, best, best_index))) { \
+            best = other;                                                               \
+            best_index = other_index;                                                   \
+        }                                                                               \
+    }
+        ADI_ARGMAX_STAGE(1) ADI_ARGMAX_STAGE(2) ADI_ARGMAX_STAGE(4) ADI_ARGMAX_STAGE(8)
+        ADI_ARGMAX_STAGE(16) ADI_ARGMAX_STAGE(32)
+#undef ADI_ARGMAX_STAGE
         chosen_value[round] = best;
         chosen_index[round] = best_index;
         if (best_index % 64u == lane) {
@@ -204,10 +325,23 @@ __global__ __launch_bounds__(64) void k_top_experts(
         }
         sum = fmaxf(sum, 6.103515625e-5f);
         for (int i = 0; i < 8; ++i) {
-            route_expert[blockIdx.x * 8u + i] = chosen_index[i];
-            route_weight[blockIdx.x * 8u + i] = selected[i] / sum;
+            route_expert[i] = chosen_index[i];
+            route_weight[i] = selected[i] / sum;
         }
     }
+}
+
+// One wave per row, four rows per block.
+template <int SLOTS>
+__global__ __launch_bounds__(256) void k_top_experts(
+    const float *__restrict__ logits, const float *__restrict__ bias, uint32_t batch,
+    uint32_t experts, uint32_t *__restrict__ route_expert, float *__restrict__ route_weight) {
+    const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (row >= batch) {
+        return;
+    }
+    top8_wave<SLOTS>(logits + static_cast<size_t>(row) * experts, bias, experts,
+                     threadIdx.x & 63u, route_expert + row * 8u, route_weight + row * 8u);
 }
 
 // Counting sort of moe_forward_batch (src/executor.cpp:1235-1258) in one
@@ -215,18 +349,20 @@ __global__ __launch_bounds__(64) void k_top_experts(
 // (token, route) slots are placed 64 at a time in order; lanes that share an
 // expert in a chunk find their rank among earlier lanes with ballots, so each
 // expert's cursor advances exactly as the sequential loop's does.
-__global__ __launch_bounds__(64) void k_route_sort(RouteSort a) {
-    __shared__ uint32_t counts[kMaxExperts];
-    __shared__ uint32_t cursor[kMaxExperts];
-    const uint32_t lane = threadIdx.x;
-    for (uint32_t e = lane; e < a.experts; e += 64u) {
+__device__ __forceinline__ void route_sort_block(const RouteSort &a, uint32_t *counts,
+                                                 uint32_t *cursor) {
+    for (uint32_t e = threadIdx.x; e < a.experts; e += blockDim.x) {
         counts[e] = 0u;
     }
     __syncthreads();
-    for (uint32_t i = lane; i < a.positions; i += 64u) {
+    for (uint32_t i = threadIdx.x; i < a.positions; i += blockDim.x) {
         atomicAdd(&counts[a.route_expert[i]], 1u);
     }
     __syncthreads();
+    if (threadIdx.x >= 64) {
+        return;  // the scan and the ordered scatter run on wave 0
+    }
+    const uint32_t lane = threadIdx.x;
     // exclusive scan over experts: each lane owns a contiguous run
     const uint32_t per_lane = (a.experts + 63u) / 64u;
     const uint32_t first = lane * per_lane;
@@ -272,7 +408,8 @@ __global__ __launch_bounds__(64) void k_route_sort(RouteSort a) {
             *a.active_count = base;
         }
     }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
     const uint64_t below = (1ull << lane) - 1ull;
     for (uint32_t c = 0; c < a.positions; c += 64u) {
         const uint32_t i = c + lane;
@@ -293,7 +430,8 @@ __global__ __launch_bounds__(64) void k_route_sort(RouteSort a) {
         if (valid) {
             position = cursor[e] + rank;
         }
-        __syncthreads();
+        // every lane has read its cursor before any lane advances one
+        __builtin_amdgcn_wave_barrier();
         if (valid) {
             a.grouped_batch[position] = i / 8u;
             a.route_to_grouped[i] = position;
@@ -301,8 +439,34 @@ __global__ __launch_bounds__(64) void k_route_sort(RouteSort a) {
                 cursor[e] += total;
             }
         }
-        __syncthreads();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
     }
+}
+
+__global__ __launch_bounds__(64) void k_route_sort(RouteSort a) {
+    __shared__ uint32_t counts[kMaxExperts];
+    __shared__ uint32_t cursor[kMaxExperts];
+    route_sort_block(a, counts, cursor);
+}
+
+// Routing of a whole batch in one block: top_experts for every row (one wave
+// per row, rows spread over 16 waves), then the stable counting sort.
+template <int SLOTS>
+__global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
+                                               const float *__restrict__ bias, uint32_t batch,
+                                               uint32_t *__restrict__ route_expert,
+                                               float *__restrict__ route_weight, RouteSort a) {
+    __shared__ uint32_t counts[kMaxExperts];
+    __shared__ uint32_t cursor[kMaxExperts];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    for (uint32_t t = wave; t < batch; t += blockDim.x / 64u) {
+        top8_wave<SLOTS>(logits + static_cast<size_t>(t) * a.experts, bias, a.experts, lane,
+                         route_expert + t * 8u, route_weight + t * 8u);
+    }
+    __threadfence_block();
+    __syncthreads();
+    route_sort_block(a, counts, cursor);
 }
 
 }  // namespace
@@ -310,6 +474,37 @@ __global__ __launch_bounds__(64) void k_route_sort(RouteSort a) {
 void launch_bf16_ordered(adi_hip_context *ctx, const uint16_t *w, uint32_t rows,
                          uint32_t columns, const float *x, uint32_t batch,
                          float *out, uint32_t lanes) {
+    launch_bf16_ordered_extra(ctx, w, rows, nullptr, columns, x, batch, out, nullptr, lanes);
+}
+
+void launch_bf16_ordered_extra(adi_hip_context *ctx, const uint16_t *w, uint32_t rows,
+                               const uint16_t *w_extra, uint32_t columns, const float *x,
+                               uint32_t batch, float *out, float *out_extra, uint32_t lanes) {
+    const uint32_t total = rows + (w_extra != nullptr ? 1u : 0u);
+    const dim3 tokens(ceil_div(batch, kTokensPerThread));
+    const uint32_t rpb = lanes == 1 ? 1 : 64 / lanes;
+    const size_t lds = size_t(kTokensPerThread) * columns * sizeof(float) +
+                       size_t(rpb) * columns * sizeof(uint16_t);
+    // dynamic plus the kernel's static 1 KiB must fit the 64 KiB default
+    if (lanes != 1 && lds + 1024 <= 65536) {
+        if (lanes == 8) {
+            launch(ctx, "router", k_bf16_lds<8, false>, dim3(ceil_div(total, rpb), tokens.x),
+                   dim3(64), lds, w, rows, w_extra, columns, x, batch, out, out_extra);
+        } else {
+            launch(ctx, "router", k_bf16_lds<16, true>, dim3(ceil_div(total, rpb), tokens.x),
+                   dim3(64), lds, w, rows, w_extra, columns, x, batch, out, out_extra);
+        }
+        return;
+    }
+    if (w_extra != nullptr) {
+        launch_bf16_ordered_plain(ctx, w_extra, 1, columns, x, batch, out_extra, lanes);
+    }
+    launch_bf16_ordered_plain(ctx, w, rows, columns, x, batch, out, lanes);
+}
+
+void launch_bf16_ordered_plain(adi_hip_context *ctx, const uint16_t *w, uint32_t rows,
+                               uint32_t columns, const float *x, uint32_t batch, float *out,
+                               uint32_t lanes) {
     switch (lanes) {
     case 1:
         launch(ctx, "bf16_ordered", k_bf16_scalar, dim3(ceil_div(rows, 256), batch), dim3(256), 0,
@@ -331,12 +526,45 @@ void launch_bf16_ordered(adi_hip_context *ctx, const uint16_t *w, uint32_t rows,
 void launch_top_experts(adi_hip_context *ctx, const float *logits, const float *bias,
                         uint32_t batch, uint32_t experts, uint32_t *route_expert,
                         float *route_weight) {
-    launch(ctx, "top_experts", k_top_experts, dim3(batch), dim3(64), 0, logits, bias, experts,
-           route_expert, route_weight);
+    const dim3 grid(ceil_div(batch, 4));
+    const uint32_t slots = ceil_div(experts, 64);
+    if (slots <= 1) {
+        launch(ctx, "top_experts", k_top_experts<1>, grid, dim3(256), 0, logits, bias, batch, experts, route_expert, route_weight);
+    } else if (slots <= 2) {
+        launch(ctx, "top_experts", k_top_experts<2>, grid, dim3(256), 0, logits, bias, batch, experts, route_expert, route_weight);
+    } else if (slots <= 4) {
+        launch(ctx, "top_experts", k_top_experts<4>, grid, dim3(256), 0, logits, bias, batch, experts, route_expert, route_weight);
+    } else if (slots <= 8) {
+        launch(ctx, "top_experts", k_top_experts<8>, grid, dim3(256), 0, logits, bias, batch, experts, route_expert, route_weight);
+    } else {
+        launch(ctx, "top_experts", k_top_experts<16>, grid, dim3(256), 0, logits, bias, batch, experts, route_expert, route_weight);
+    }
 }
 
 void launch_route_sort(adi_hip_context *ctx, const RouteSort &args) {
     launch(ctx, "route_sort", k_route_sort, dim3(1), dim3(64), 0, args);
+}
+
+void launch_route(adi_hip_context *ctx, const float *logits, const float *bias, uint32_t batch,
+                  uint32_t *route_expert, float *route_weight, const RouteSort &args) {
+    const uint32_t slots = ceil_div(args.experts, 64);
+    if (batch > 16) {
+        // many rows: top_experts over a grid, then the one-block sort
+        launch_top_experts(ctx, logits, bias, batch, args.experts, route_expert, route_weight);
+        launch_route_sort(ctx, args);
+        return;
+    }
+    if (slots <= 1) {
+        launch(ctx, "route", k_route<1>, dim3(1), dim3(256), 0, logits, bias, batch, route_expert, route_weight, args);
+    } else if (slots <= 2) {
+        launch(ctx, "route", k_route<2>, dim3(1), dim3(256), 0, logits, bias, batch, route_expert, route_weight, args);
+    } else if (slots <= 4) {
+        launch(ctx, "route", k_route<4>, dim3(1), dim3(256), 0, logits, bias, batch, route_expert, route_weight, args);
+    } else if (slots <= 8) {
+        launch(ctx, "route", k_route<8>, dim3(1), dim3(256), 0, logits, bias, batch, route_expert, route_weight, args);
+    } else {
+        launch(ctx, "route", k_route<16>, dim3(1), dim3(256), 0, logits, bias, batch, route_expert, route_weight, args);
+    }
 }
 
 }  // namespace adi_hip

@@ -11,6 +11,14 @@ void launch_bf16_ordered(adi_hip_context *ctx, const uint16_t *w, uint32_t rows,
                          uint32_t columns, const float *x, uint32_t batch,
                          float *out, uint32_t lanes);
 
+// The same with an optional extra row appended (written to out_extra [batch]).
+void launch_bf16_ordered_extra(adi_hip_context *ctx, const uint16_t *w, uint32_t rows,
+                               const uint16_t *w_extra, uint32_t columns, const float *x,
+                               uint32_t batch, float *out, float *out_extra, uint32_t lanes);
+void launch_bf16_ordered_plain(adi_hip_context *ctx, const uint16_t *w, uint32_t rows,
+                               uint32_t columns, const float *x, uint32_t batch, float *out,
+                               uint32_t lanes);
+
 // Top-8 routes per logit row (bias nullable, [experts]).
 void launch_top_experts(adi_hip_context *ctx, const float *logits,
                         const float *bias, uint32_t batch, uint32_t experts,
@@ -30,6 +38,11 @@ struct RouteSort {
     uint32_t *route_to_grouped;   // [positions]
 };
 void launch_route_sort(adi_hip_context *ctx, const RouteSort &args);
+
+// top_experts for every row plus the counting sort, in one launch.
+// route_expert must be args.route_expert.
+void launch_route(adi_hip_context *ctx, const float *logits, const float *bias, uint32_t batch,
+                  uint32_t *route_expert, float *route_weight, const RouteSort &args);
 
 constexpr uint32_t kMaxExperts = 1024;
 

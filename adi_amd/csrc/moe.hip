@@ -2,18 +2,20 @@
 // (src/executor.cpp:242-330, 1181-1453).
 //
 // Launch sequence for a batch of B rows (P = 8B route positions):
-//   1  router logits, ISA-ordered bf16 (bit-exact)       [B, E]
-//      shared-expert gate logit, same kernel              [B]
-//   2  top_experts (+ optional fp32 logit bias)           routes [P]
-//   3  stable counting sort                               offsets, grouped_batch,
-//                                                         route_to_grouped, active list
-//   4  prologues x_hat = H(su_e * x[grouped_batch[p]]) for gate and up, and
-//      H(SU * x) for the shared expert
-//   5  decode-GEMV gate/up over the active experts, NE GEMV shared gate/up
-//   6  SwiGLU: g = sv*H(Zg), u = sv*H(Zu), a = silu(g)*u, x_hat = H(su_d * a)
-//   7  decode-GEMV down over the active experts, NE GEMV shared down
-//   8  combine per row: sum_r w_r * sv_d*H(Zd[p_r]) in route order, then
-//      + sigmoid(gate) * SV*H(Zshared)
+//   1 router   router logits and the shared-expert gate logit, ISA-ordered
+//              bf16 (bit-exact)
+//   2 route    top_experts for every row (+ optional fp32 logit bias) and the
+//              stable counting sort: offsets, grouped_batch, route_to_grouped,
+//              the ascending list of active experts
+//   3 prologue x_hat = H(su_e * x[grouped_batch[p]]) for gate and up of every
+//              route position, H(SU * x) for the shared expert (one wave per
+//              vector)
+//   4 gemv     decode-GEMV gate and up over the active experts and the NE
+//              GEMV of the shared gate and up, one launch
+//   5 swiglu   g = sv*H(Zg), u = sv*H(Zu), a = silu(g)*u, x_hat = H(su_d * a)
+//   6 gemv     down over the active experts and the shared down, one launch
+//   7 combine  per row: sum_r w_r * sv_d*H(Zd[p_r]) in route order, then
+//              + sigmoid(gate) * SV*H(Zshared)
 // Expert work is sized for the worst case (min(P, E) active experts); blocks
 // past the device-side active count return at once, so the host never waits
 // for the routing.
@@ -32,6 +34,162 @@ template <>
 __device__ __forceinline__ float to_float<uint16_t>(uint16_t s) { return half_bits_to_float(s); }
 template <>
 __device__ __forceinline__ float to_float<int8_t>(int8_t s) { return static_cast<float>(s); }
+
+struct SwigluSegment {
+    const float *z_gate;
+    const float *z_up;
+    size_t split_stride;
+    const uint16_t *sv_gate_f16;  // f16 per matrix (routed) ...
+    const uint16_t *sv_up_f16;
+    const uint16_t *su_down_f16;
+    const int8_t *sv_gate_sign;   // ... or +-1 (shared expert)
+    const int8_t *sv_up_sign;
+    const int8_t *su_down_sign;
+    const uint32_t *matrix_index;
+    float *x_hat;
+    uint32_t count;
+};
+
+struct SwigluJobs {
+    SwigluSegment seg[2];
+    uint32_t segments;
+    uint32_t splits;
+    float scale;
+};
+
+// One wave per vector of the intermediate width n = 64*VPL.
+template <int VPL>
+__global__ __launch_bounds__(256) void k_swiglu_wave(SwigluJobs j) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t v = blockIdx.x * 4u + (threadIdx.x >> 6);
+    uint32_t s = 0;
+    while (s < j.segments && v >= j.seg[s].count) {
+        v -= j.seg[s].count;
+        ++s;
+    }
+    if (s >= j.segments) {
+        return;
+    }
+    const SwigluSegment &g = j.seg[s];
+    const uint32_t n = 64u * VPL;
+    const size_t base = static_cast<size_t>(v) * n + lane;
+    float gv[VPL], uv[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        gv[i] = g.z_gate[base + i * 64];
+        uv[i] = g.z_up[base + i * 64];
+    }
+    for (uint32_t sp = 1; sp < j.splits; ++sp) {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            gv[i] += g.z_gate[sp * g.split_stride + base + i * 64];
+            uv[i] += g.z_up[sp * g.split_stride + base + i * 64];
+        }
+    }
+    wave_hadamard<VPL>(gv, j.scale, lane);
+    wave_hadamard<VPL>(uv, j.scale, lane);
+    const size_t mat = g.matrix_index != nullptr ? g.matrix_index[v] : 0u;
+    const size_t off = mat * n + lane;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        float a, b, c;
+        if (g.sv_gate_f16 != nullptr) {
+            a = half_bits_to_float(g.sv_gate_f16[off + i * 64]);
+            b = half_bits_to_float(g.sv_up_f16[off + i * 64]);
+            c = half_bits_to_float(g.su_down_f16[off + i * 64]);
+        } else {
+            a = static_cast<float>(g.sv_gate_sign[i * 64u + lane]);
+            b = static_cast<float>(g.sv_up_sign[i * 64u + lane]);
+            c = static_cast<float>(g.su_down_sign[i * 64u + lane]);
+        }
+        gv[i] = silu(gv[i] * a) * (uv[i] * b) * c;
+    }
+    wave_hadamard<VPL>(gv, j.scale, lane);
+    float *out = g.x_hat + static_cast<size_t>(v) * n + lane;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        out[i * 64] = gv[i];
+    }
+}
+
+struct CombineArgs {
+    const float *z_down;
+    uint32_t splits;
+    size_t split_stride;
+    const uint16_t *sv_down;  // f16 per expert, stride n
+    const uint32_t *route_expert;
+    const float *route_weight;
+    const uint32_t *route_to_grouped;
+    const float *z_shared;
+    uint32_t shared_splits;
+    size_t shared_split_stride;
+    const int8_t *sv_shared;
+    const float *shared_logit;
+    float scale;
+    float *out;
+};
+
+// One block of nine waves per row: wave r < 8 transforms route r's output,
+// wave 8 the shared expert's; the nine are then added into the row in route
+// order through LDS (src/executor.cpp:1373-1399, 1437-1452).
+template <int VPL>
+__global__ __launch_bounds__(576) void k_combine_wave(CombineArgs a) {
+    __shared__ float acc[64 * VPL];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t n = 64u * VPL;
+    const uint32_t b = blockIdx.x;
+    float val[VPL];
+    const float *src;
+    uint32_t splits;
+    size_t stride;
+    if (wave < 8) {
+        src = a.z_down + static_cast<size_t>(a.route_to_grouped[b * 8u + wave]) * n;
+        splits = a.splits;
+        stride = a.split_stride;
+    } else {
+        src = a.z_shared + static_cast<size_t>(b) * n;
+        splits = a.shared_splits;
+        stride = a.shared_split_stride;
+    }
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        val[i] = src[i * 64u + lane];
+    }
+    for (uint32_t sp = 1; sp < splits; ++sp) {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            val[i] += src[sp * stride + i * 64u + lane];
+        }
+    }
+    wave_hadamard<VPL>(val, a.scale, lane);
+    if (wave < 8) {
+        const float w = a.route_weight[b * 8u + wave];
+        const uint16_t *sv = a.sv_down + static_cast<size_t>(a.route_expert[b * 8u + wave]) * n;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            val[i] = w * (val[i] * half_bits_to_float(sv[i * 64u + lane]));
+        }
+    } else {
+        const float gate = sigmoid(a.shared_logit[b]);
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            val[i] = gate * (val[i] * static_cast<float>(a.sv_shared[i * 64u + lane]));
+        }
+    }
+    for (uint32_t r = 0; r < 9; ++r) {
+        if (wave == r) {
+#pragma unroll
+            for (int i = 0; i < VPL; ++i) {
+                acc[i * 64u + lane] = r == 0 ? val[i] : acc[i * 64u + lane] + val[i];
+            }
+        }
+        __syncthreads();
+    }
+    float *dst = a.out + static_cast<size_t>(b) * n;
+    for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
+        dst[k] = acc[k];
+    }
+}
 
 // One block per vector v of the intermediate width I.
 template <typename Scale>
@@ -216,11 +374,11 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         float *sxh_down = ws.take<float>(B * I);
         float *sz_down = ws.take<float>(sd * B * H);
 
-        // 1-3: routing
-        launch_bf16_ordered(ctx, L->router.values, E, H, inputs, batch, logits, ctx->isa_lanes);
-        launch_bf16_ordered(ctx, L->shared_expert_gate.values, 1, H, inputs, batch, shared_logit,
-                            ctx->isa_lanes);
-        launch_top_experts(ctx, logits, logit_bias, batch, E, route_expert, route_weight);
+        const bool wave_path = wave_width(H) && wave_width(I);
+
+        // 1-2: router logits (+ the shared gate row) and routing
+        launch_bf16_ordered_extra(ctx, L->router.values, E, L->shared_expert_gate.values, H, inputs,
+                                  batch, logits, shared_logit, ctx->isa_lanes);
         RouteSort sort{};
         sort.route_expert = route_expert;
         sort.positions = static_cast<uint32_t>(P);
@@ -232,100 +390,136 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         sort.position_expert = position_expert;
         sort.grouped_batch = grouped_batch;
         sort.route_to_grouped = route_to_grouped;
-        launch_route_sort(ctx, sort);
+        launch_route(ctx, logits, logit_bias, batch, route_expert, route_weight, sort);
 
-        // 4: prologues
-        launch_prologue_f16(ctx, inputs, H, L->gate.su_f16, H, grouped_batch, position_expert,
-                            static_cast<uint32_t>(P), xh_gate);
-        launch_prologue_f16(ctx, inputs, H, L->up.su_f16, H, grouped_batch, position_expert,
-                            static_cast<uint32_t>(P), xh_up);
-        launch_prologue_sign(ctx, inputs, H, L->shared_gate.su, batch, sxh_gate);
-        launch_prologue_sign(ctx, inputs, H, L->shared_up.su, batch, sxh_up);
+        // 3: prologues, routed gate/up and shared gate/up
+        PrologueJobs pro{};
+        pro.segments = 4;
+        pro.n = H;
+        pro.seg[0] = PrologueSegment{inputs, grouped_batch, position_expert, L->gate.su_f16, nullptr,
+                                     H, xh_gate, static_cast<uint32_t>(P)};
+        pro.seg[1] = PrologueSegment{inputs, grouped_batch, position_expert, L->up.su_f16, nullptr,
+                                     H, xh_up, static_cast<uint32_t>(P)};
+        pro.seg[2] = PrologueSegment{inputs, nullptr, nullptr, nullptr, L->shared_gate.su, 0,
+                                     sxh_gate, batch};
+        pro.seg[3] = PrologueSegment{inputs, nullptr, nullptr, nullptr, L->shared_up.su, 0,
+                                     sxh_up, batch};
+        launch_prologues(ctx, pro);
 
-        // 5: gate / up
+        // 4: gate / up GEMVs
         const size_t gu_words = size_t(I / kTile) * (H / kTile) * kExpertWords;
         const size_t d_words = size_t(H / kTile) * (I / kTile) * kExpertWords;
         const uint32_t gamma_stride = H / kTile + I / kTile;
-        ExpertGemv g{};
-        g.codebook = L->expert_codebook->data;
-        g.active = active;
-        g.active_count = active_count;
-        g.offsets = offsets;
-        g.max_active = max_active;
-        g.tokens_per_pass = batch == 1 ? 1 : 4;
-        g.gamma_stride = gamma_stride;
-        g.rows = I;
-        g.columns = H;
-        g.trellis_stride = gu_words;
-        g.z_split_stride = P * I;
-        g.trellis = L->gate.trellis;
-        g.gamma = L->gate.wave_gamma_f16;
-        g.x_hat = xh_gate;
-        g.z = z_gate;
-        launch_expert_gemv(ctx, g);
-        g.trellis = L->up.trellis;
-        g.gamma = L->up.wave_gamma_f16;
-        g.x_hat = xh_up;
-        g.z = z_up;
-        launch_expert_gemv(ctx, g);
-        NeGemv n{};
-        n.batch = batch;
-        n.rows = I;
-        n.columns = H;
-        n.z_split_stride = B * I;
-        n.trellis = L->shared_gate.trellis;
-        n.codebook = L->shared_gate.codebook->data;
-        n.weight_scale = L->shared_gate.weight_scale;
-        n.x_hat = sxh_gate;
-        n.z = sz_gate;
-        launch_ne_gemv(ctx, n);
-        n.trellis = L->shared_up.trellis;
-        n.codebook = L->shared_up.codebook->data;
-        n.weight_scale = L->shared_up.weight_scale;
-        n.x_hat = sxh_up;
-        n.z = sz_up;
-        launch_ne_gemv(ctx, n);
+        auto expert_job = [&](const adi_hip_expert_stack &st, uint32_t rows, uint32_t columns,
+                              size_t words, const float *x_hat, float *z) {
+            ExpertGemv g{};
+            g.codebook = L->expert_codebook->data;
+            g.active = active;
+            g.active_count = active_count;
+            g.offsets = offsets;
+            g.max_active = max_active;
+            g.tokens_per_pass = batch == 1 ? 1 : 4;
+            g.gamma_stride = gamma_stride;
+            g.rows = rows;
+            g.columns = columns;
+            g.trellis_stride = words;
+            g.z_split_stride = P * rows;
+            g.trellis = st.trellis;
+            g.gamma = st.wave_gamma_f16;
+            g.x_hat = x_hat;
+            g.z = z;
+            return g;
+        };
+        auto ne_job = [&](const adi_hip_ne_matrix &m, const float *x_hat, float *z) {
+            NeGemv n{};
+            n.batch = batch;
+            n.rows = m.rows;
+            n.columns = m.columns;
+            n.z_split_stride = B * m.rows;
+            n.trellis = m.trellis;
+            n.codebook = m.codebook->data;
+            n.weight_scale = m.weight_scale;
+            n.x_hat = x_hat;
+            n.z = z;
+            return n;
+        };
+        MoeGemv gu{};
+        gu.expert[0] = expert_job(L->gate, I, H, gu_words, xh_gate, z_gate);
+        gu.expert[1] = expert_job(L->up, I, H, gu_words, xh_up, z_up);
+        gu.expert_count = 2;
+        gu.ne[0] = ne_job(L->shared_gate, sxh_gate, sz_gate);
+        gu.ne[1] = ne_job(L->shared_up, sxh_up, sz_up);
+        gu.ne_count = 2;
+        gu.max_active = max_active;
+        launch_moe_gemv(ctx, gu, batch == 1);
 
-        // 6: SwiGLU and the down prologue
+        // 5: SwiGLU and the down prologue
         const float scale_i = hadamard_scale(I);
-        launch(ctx, "swiglu", k_swiglu<uint16_t>, dim3(static_cast<uint32_t>(P)), dim3(256),
-               2 * I * sizeof(float), static_cast<const float *>(z_gate),
-               static_cast<const float *>(z_up), sg, P * I, I, L->gate.sv_f16, L->up.sv_f16,
-               L->down.su_f16, I, static_cast<const uint32_t *>(position_expert), scale_i,
-               xh_down);
-        launch(ctx, "swiglu", k_swiglu<int8_t>, dim3(batch), dim3(256), 2 * I * sizeof(float),
-               static_cast<const float *>(sz_gate), static_cast<const float *>(sz_up), sg, B * I, I,
-               L->shared_gate.sv, L->shared_up.sv, L->shared_down.su, 0u,
-               static_cast<const uint32_t *>(nullptr), scale_i, sxh_down);
+        if (wave_path) {
+            SwigluJobs sj{};
+            sj.segments = 2;
+            sj.splits = sg;
+            sj.scale = scale_i;
+            sj.seg[0] = SwigluSegment{z_gate, z_up, P * I, L->gate.sv_f16, L->up.sv_f16,
+                                      L->down.su_f16, nullptr, nullptr, nullptr, position_expert,
+                                      xh_down, static_cast<uint32_t>(P)};
+            sj.seg[1] = SwigluSegment{sz_gate, sz_up, B * I, nullptr, nullptr, nullptr,
+                                      L->shared_gate.sv, L->shared_up.sv, L->shared_down.su,
+                                      nullptr, sxh_down, batch};
+            const dim3 grid(ceil_div(P + B, 4));
+            switch (I) {
+            case 64: launch(ctx, "swiglu", k_swiglu_wave<1>, grid, dim3(256), 0, sj); break;
+            case 128: launch(ctx, "swiglu", k_swiglu_wave<2>, grid, dim3(256), 0, sj); break;
+            case 256: launch(ctx, "swiglu", k_swiglu_wave<4>, grid, dim3(256), 0, sj); break;
+            case 512: launch(ctx, "swiglu", k_swiglu_wave<8>, grid, dim3(256), 0, sj); break;
+            case 1024: launch(ctx, "swiglu", k_swiglu_wave<16>, grid, dim3(256), 0, sj); break;
+            case 2048: launch(ctx, "swiglu", k_swiglu_wave<32>, grid, dim3(256), 0, sj); break;
+            default: launch(ctx, "swiglu", k_swiglu_wave<64>, grid, dim3(256), 0, sj); break;
+            }
+        } else {
+            launch(ctx, "swiglu", k_swiglu<uint16_t>, dim3(static_cast<uint32_t>(P)), dim3(256),
+                   2 * I * sizeof(float), static_cast<const float *>(z_gate),
+                   static_cast<const float *>(z_up), sg, P * I, I, L->gate.sv_f16, L->up.sv_f16,
+                   L->down.su_f16, I, static_cast<const uint32_t *>(position_expert), scale_i,
+                   xh_down);
+            launch(ctx, "swiglu", k_swiglu<int8_t>, dim3(batch), dim3(256), 2 * I * sizeof(float),
+                   static_cast<const float *>(sz_gate), static_cast<const float *>(sz_up), sg, B * I,
+                   I, L->shared_gate.sv, L->shared_up.sv, L->shared_down.su, 0u,
+                   static_cast<const uint32_t *>(nullptr), scale_i, sxh_down);
+        }
 
-        // 7: down
-        g.rows = H;
-        g.columns = I;
-        g.trellis_stride = d_words;
-        g.z_split_stride = P * H;
-        g.trellis = L->down.trellis;
-        g.gamma = L->down.wave_gamma_f16;
-        g.x_hat = xh_down;
-        g.z = z_down;
-        launch_expert_gemv(ctx, g);
-        n.rows = H;
-        n.columns = I;
-        n.z_split_stride = B * H;
-        n.trellis = L->shared_down.trellis;
-        n.codebook = L->shared_down.codebook->data;
-        n.weight_scale = L->shared_down.weight_scale;
-        n.x_hat = sxh_down;
-        n.z = sz_down;
-        launch_ne_gemv(ctx, n);
+        // 6: down GEMVs
+        MoeGemv dn{};
+        dn.expert[0] = expert_job(L->down, H, I, d_words, xh_down, z_down);
+        dn.expert_count = 1;
+        dn.ne[0] = ne_job(L->shared_down, sxh_down, sz_down);
+        dn.ne_count = 1;
+        dn.max_active = max_active;
+        launch_moe_gemv(ctx, dn, batch == 1);
 
-        // 8: combine
-        launch(ctx, "combine", k_combine, dim3(batch), dim3(256), H * sizeof(float),
-               static_cast<const float *>(z_down), sd, P * H, H, L->down.sv_f16,
-               static_cast<const uint32_t *>(route_expert),
-               static_cast<const float *>(route_weight),
-               static_cast<const uint32_t *>(route_to_grouped),
-               static_cast<const float *>(sz_down), sd, B * H, L->shared_down.sv,
-               static_cast<const float *>(shared_logit), hadamard_scale(H), outputs);
+        // 7: combine
+        if (wave_path) {
+            CombineArgs c{z_down, sd, P * H, L->down.sv_f16, route_expert, route_weight,
+                          route_to_grouped, sz_down, sd, B * H, L->shared_down.sv, shared_logit,
+                          hadamard_scale(H), outputs};
+            switch (H) {
+            case 64: launch(ctx, "combine", k_combine_wave<1>, dim3(batch), dim3(576), 0, c); break;
+            case 128: launch(ctx, "combine", k_combine_wave<2>, dim3(batch), dim3(576), 0, c); break;
+            case 256: launch(ctx, "combine", k_combine_wave<4>, dim3(batch), dim3(576), 0, c); break;
+            case 512: launch(ctx, "combine", k_combine_wave<8>, dim3(batch), dim3(576), 0, c); break;
+            case 1024: launch(ctx, "combine", k_combine_wave<16>, dim3(batch), dim3(576), 0, c); break;
+            case 2048: launch(ctx, "combine", k_combine_wave<32>, dim3(batch), dim3(576), 0, c); break;
+            default: launch(ctx, "combine", k_combine_wave<64>, dim3(batch), dim3(576), 0, c); break;
+            }
+        } else {
+            launch(ctx, "combine", k_combine, dim3(batch), dim3(256), H * sizeof(float),
+                   static_cast<const float *>(z_down), sd, P * H, H, L->down.sv_f16,
+                   static_cast<const uint32_t *>(route_expert),
+                   static_cast<const float *>(route_weight),
+                   static_cast<const uint32_t *>(route_to_grouped),
+                   static_cast<const float *>(sz_down), sd, B * H, L->shared_down.sv,
+                   static_cast<const float *>(shared_logit), hadamard_scale(H), outputs);
+        }
 
         if (route_expert_out != nullptr) {
             check_hip(hipMemcpyAsync(route_expert_out, route_expert, P * 4,

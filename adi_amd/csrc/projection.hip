@@ -212,6 +212,120 @@ __global__ __launch_bounds__(256) void k_epilogue(
     }
 }
 
+// ---- wave-per-vector prologue / epilogue ---------------------------------
+
+template <typename Scale>
+__device__ __forceinline__ float scale_at(const Scale *s, uint32_t k) {
+    return scale_value<Scale>(s[k]);
+}
+
+// Up to four segments of vectors, one wave each: x_hat = H_n(x[src] * su).
+template <int VPL>
+__global__ __launch_bounds__(256) void k_prologue_wave(PrologueJobs j) {
+#pragma clang fp contract(off)
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t v = blockIdx.x * 4u + (threadIdx.x >> 6);
+    uint32_t s = 0;
+    while (s < j.segments && v >= j.seg[s].count) {
+        v -= j.seg[s].count;
+        ++s;
+    }
+    if (s >= j.segments) {
+        return;
+    }
+    const PrologueSegment &g = j.seg[s];
+    const uint32_t n = 64u * VPL;
+    const uint32_t src = g.source_row != nullptr ? g.source_row[v] : v;
+    const uint32_t mat = g.matrix_index != nullptr ? g.matrix_index[v] : 0u;
+    const float *x = g.x + static_cast<size_t>(src) * n + lane;
+    float val[VPL];
+    if (g.su_f16 != nullptr) {
+        const uint16_t *su = g.su_f16 + static_cast<size_t>(mat) * g.su_stride + lane;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            val[i] = x[i * 64] * half_bits_to_float(su[i * 64]);
+        }
+    } else {
+        const int8_t *su = g.su_sign + lane;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            val[i] = x[i * 64] * static_cast<float>(su[i * 64]);
+        }
+    }
+    wave_hadamard<VPL>(val, j.scale, lane);
+    float *out = g.out + static_cast<size_t>(v) * n + lane;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        out[i * 64] = val[i];
+    }
+}
+
+// y = sv * H_n(sum over splits of z), one wave per vector.
+template <int VPL, typename Scale>
+__global__ __launch_bounds__(256) void k_epilogue_wave(
+    const float *__restrict__ z, uint32_t splits, size_t split_stride, const Scale *__restrict__ sv,
+    uint32_t vectors, float scale, float *__restrict__ out) {
+#pragma clang fp contract(off)
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t v = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (v >= vectors) {
+        return;
+    }
+    const uint32_t n = 64u * VPL;
+    const float *src = z + static_cast<size_t>(v) * n + lane;
+    float val[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        val[i] = src[i * 64];
+    }
+    for (uint32_t sp = 1; sp < splits; ++sp) {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            val[i] += src[sp * split_stride + i * 64];
+        }
+    }
+    wave_hadamard<VPL>(val, scale, lane);
+    float *dst = out + static_cast<size_t>(v) * n + lane;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        dst[i * 64] = val[i] * scale_value<Scale>(sv[i * 64u + lane]);
+    }
+}
+
+// In-place normalised FWHT of `count` vectors, one wave each (64 <= n <= 4096)
+// or one block each.
+template <int VPL>
+__global__ __launch_bounds__(256) void k_hadamard_wave(float *values, uint32_t count, float scale) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t v = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (v >= count) {
+        return;
+    }
+    float *p = values + static_cast<size_t>(v) * 64u * VPL + lane;
+    float val[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        val[i] = p[i * 64];
+    }
+    wave_hadamard<VPL>(val, scale, lane);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        p[i * 64] = val[i];
+    }
+}
+
+__global__ __launch_bounds__(256) void k_hadamard_block(float *values, uint32_t n, float scale) {
+    extern __shared__ float v[];
+    float *p = values + static_cast<size_t>(blockIdx.x) * n;
+    for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
+        v[k] = p[k];
+    }
+    block_hadamard(v, n, scale);
+    for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
+        p[k] = v[k];
+    }
+}
+
 // ---- cross-tile row reduction shared by both GEMVs -----------------------
 
 // Sums a lane's four row values (per token) over the tiles of its tile row
@@ -222,7 +336,7 @@ template <int NT>
 __device__ __forceinline__ void reduce_rows_and_store(
     float (&acc)[4][NT], uint32_t lane, uint32_t wave, uint32_t tile,
     uint32_t tile_columns, uint32_t tiles, uint32_t rows, uint32_t tok0,
-    uint32_t tok_count, float *z, size_t z_split_stride, float *lds) {
+    uint32_t tok_count, float *z, size_t z_split_stride, float *lds, uint32_t bx) {
     const uint32_t slot = lane >> 2;
     const uint32_t quad = lane & 3u;
     const uint32_t g = tile_columns < 16 ? tile_columns : 16u;
@@ -279,7 +393,7 @@ __device__ __forceinline__ void reduce_rows_and_store(
         for (uint32_t w = 0; w < wpr; ++w) {
             sum += lds[((group * wpr + w) * 16u + r) * NT + j];
         }
-        const uint32_t first_tile = blockIdx.x * 64u + group * wpr * 16u;
+        const uint32_t first_tile = bx * 64u + group * wpr * 16u;
         if (first_tile < tiles && j < tok_count) {
             const uint32_t tr = first_tile / tile_columns;
             const uint32_t split = (first_tile % tile_columns) / 64u;
@@ -293,24 +407,24 @@ __device__ __forceinline__ void reduce_rows_and_store(
 // Four rows of one expert tile = 8 states = bits [96q, 96q + 112) of the
 // 384-bit stream: words 6q..6q+5 of the lane plus word 0 of the next quad.
 template <int NT>
-__global__ __launch_bounds__(256) void k_expert_gemv(ExpertGemv a) {
+__device__ __forceinline__ void expert_gemv_block(const ExpertGemv &a, uint32_t bx, uint32_t by,
+                                                  float *lds) {
     uint32_t mat = 0, tok_begin = 0, tok_end = a.batch;
     if (a.active != nullptr) {
-        if (blockIdx.y >= *a.active_count) {
+        if (by >= *a.active_count) {
             return;
         }
-        mat = a.active[blockIdx.y];
+        mat = a.active[by];
         tok_begin = a.offsets[mat];
         tok_end = a.offsets[mat + 1];
     }
-    __shared__ float lds[4 * 16 * NT];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t quad = lane & 3u;
     const uint32_t tile_columns = a.columns / kTile;
     const uint32_t tile_rows = a.rows / kTile;
     const uint32_t tiles = tile_rows * tile_columns;
-    const uint32_t tile = blockIdx.x * 64u + wave * 16u + (lane >> 2);
+    const uint32_t tile = bx * 64u + wave * 16u + (lane >> 2);
     const bool valid = tile < tiles;
     const uint32_t tr = valid ? tile / tile_columns : 0u;
     const uint32_t tc = valid ? tile % tile_columns : 0u;
@@ -365,8 +479,14 @@ __global__ __launch_bounds__(256) void k_expert_gemv(ExpertGemv a) {
             }
         }
         reduce_rows_and_store<NT>(acc, lane, wave, tile, tile_columns, tiles, a.rows, t0, count,
-                                  a.z, a.z_split_stride, lds);
+                                  a.z, a.z_split_stride, lds, bx);
     }
+}
+
+template <int NT>
+__global__ __launch_bounds__(256) void k_expert_gemv(ExpertGemv a) {
+    __shared__ float lds[4 * 16 * NT];
+    expert_gemv_block<NT>(a, blockIdx.x, blockIdx.y, lds);
 }
 
 // ---- NE decode-GEMV --------------------------------------------------------
@@ -376,9 +496,8 @@ __global__ __launch_bounds__(256) void k_expert_gemv(ExpertGemv a) {
 // quad. The 1024-entry signed table, scaled by Wscale in fp32 as the
 // reference does per state (src/kernels.cpp:673-683), sits in LDS.
 template <int NT>
-__global__ __launch_bounds__(256) void k_ne_gemv(NeGemv a) {
-    __shared__ float2 table[1024];
-    __shared__ float lds[4 * 16 * NT];
+__device__ __forceinline__ void ne_gemv_block(const NeGemv &a, uint32_t bx, float2 *table,
+                                              float *lds) {
     const uint32_t *book = static_cast<const uint32_t *>(a.codebook);
     for (uint32_t i = threadIdx.x; i < 1024u; i += blockDim.x) {
         const float2 v = half2_bits_to_float2(book[i]);
@@ -389,7 +508,7 @@ __global__ __launch_bounds__(256) void k_ne_gemv(NeGemv a) {
     const uint32_t quad = lane & 3u;
     const uint32_t tile_columns = a.columns / kTile;
     const uint32_t tiles = (a.rows / kTile) * tile_columns;
-    const uint32_t tile = blockIdx.x * 64u + wave * 16u + (lane >> 2);
+    const uint32_t tile = bx * 64u + wave * 16u + (lane >> 2);
     const bool valid = tile < tiles;
     const uint32_t tc = valid ? tile % tile_columns : 0u;
 
@@ -435,13 +554,93 @@ __global__ __launch_bounds__(256) void k_ne_gemv(NeGemv a) {
             }
         }
         reduce_rows_and_store<NT>(acc, lane, wave, tile, tile_columns, tiles, a.rows, t0, count,
-                                  a.z, a.z_split_stride, lds);
+                                  a.z, a.z_split_stride, lds, bx);
     }
+}
+
+template <int NT>
+__global__ __launch_bounds__(256) void k_ne_gemv(NeGemv a) {
+    __shared__ float2 table[1024];
+    __shared__ float lds[4 * 16 * NT];
+    ne_gemv_block<NT>(a, blockIdx.x, table, lds);
+}
+
+// Several expert and NE GEMVs in one launch (the MoE gate/up pair plus the
+// shared expert's, or the down projections): blocks are numbered expert
+// matrices first (max_active slots each), then NE matrices.
+template <int NT>
+__global__ __launch_bounds__(256) void k_moe_gemv(MoeGemv m) {
+    __shared__ float2 table[1024];
+    __shared__ float lds[4 * 16 * NT];
+    uint32_t b = blockIdx.x;
+    const uint32_t per_expert = m.expert_blocks * m.max_active;
+    if (b < m.expert_count * per_expert) {
+        const uint32_t which = b / per_expert;
+        const uint32_t rest = b % per_expert;
+        expert_gemv_block<NT>(m.expert[which], rest % m.expert_blocks, rest / m.expert_blocks, lds);
+        return;
+    }
+    b -= m.expert_count * per_expert;
+    ne_gemv_block<NT>(m.ne[b / m.ne_blocks], b % m.ne_blocks, table, lds);
 }
 
 }  // namespace
 
 // ---- launchers -------------------------------------------------------------
+
+bool wave_width(uint32_t n) { return n >= 64 && n <= 4096 && is_power_of_two(n); }
+
+void launch_prologues(adi_hip_context *ctx, PrologueJobs &jobs) {
+    uint32_t vectors = 0;
+    for (uint32_t s = 0; s < jobs.segments; ++s) {
+        vectors += jobs.seg[s].count;
+    }
+    jobs.scale = hadamard_scale(jobs.n);
+    const dim3 grid(ceil_div(vectors, 4));
+    switch (jobs.n) {
+    case 64: launch(ctx, "hadamard_prologue", k_prologue_wave<1>, grid, dim3(256), 0, jobs); break;
+    case 128: launch(ctx, "hadamard_prologue", k_prologue_wave<2>, grid, dim3(256), 0, jobs); break;
+    case 256: launch(ctx, "hadamard_prologue", k_prologue_wave<4>, grid, dim3(256), 0, jobs); break;
+    case 512: launch(ctx, "hadamard_prologue", k_prologue_wave<8>, grid, dim3(256), 0, jobs); break;
+    case 1024: launch(ctx, "hadamard_prologue", k_prologue_wave<16>, grid, dim3(256), 0, jobs); break;
+    case 2048: launch(ctx, "hadamard_prologue", k_prologue_wave<32>, grid, dim3(256), 0, jobs); break;
+    case 4096: launch(ctx, "hadamard_prologue", k_prologue_wave<64>, grid, dim3(256), 0, jobs); break;
+    default:
+        for (uint32_t s = 0; s < jobs.segments; ++s) {
+            const PrologueSegment &g = jobs.seg[s];
+            if (g.su_f16 != nullptr) {
+                launch(ctx, "hadamard_prologue", k_prologue<uint16_t>, dim3(g.count), dim3(256),
+                       jobs.n * sizeof(float), g.x, jobs.n, g.su_f16, g.su_stride, g.source_row,
+                       g.matrix_index, jobs.scale, g.out);
+            } else {
+                launch(ctx, "hadamard_prologue", k_prologue<int8_t>, dim3(g.count), dim3(256),
+                       jobs.n * sizeof(float), g.x, jobs.n, g.su_sign, 0u, g.source_row,
+                       static_cast<const uint32_t *>(nullptr), jobs.scale, g.out);
+            }
+        }
+    }
+}
+
+template <typename Scale>
+void launch_epilogue_any(adi_hip_context *ctx, const float *z, uint32_t splits,
+                         size_t split_stride, uint32_t n, const Scale *sv, uint32_t vectors,
+                         float *out) {
+    const float scale = hadamard_scale(n);
+    const dim3 grid(ceil_div(vectors, 4));
+    switch (n) {
+    case 64: launch(ctx, "hadamard_epilogue", k_epilogue_wave<1, Scale>, grid, dim3(256), 0, z, splits, split_stride, sv, vectors, scale, out); break;
+    case 128: launch(ctx, "hadamard_epilogue", k_epilogue_wave<2, Scale>, grid, dim3(256), 0, z, splits, split_stride, sv, vectors, scale, out); break;
+    case 256: launch(ctx, "hadamard_epilogue", k_epilogue_wave<4, Scale>, grid, dim3(256), 0, z, splits, split_stride, sv, vectors, scale, out); break;
+    case 512: launch(ctx, "hadamard_epilogue", k_epilogue_wave<8, Scale>, grid, dim3(256), 0, z, splits, split_stride, sv, vectors, scale, out); break;
+    case 1024: launch(ctx, "hadamard_epilogue", k_epilogue_wave<16, Scale>, grid, dim3(256), 0, z, splits, split_stride, sv, vectors, scale, out); break;
+    case 2048: launch(ctx, "hadamard_epilogue", k_epilogue_wave<32, Scale>, grid, dim3(256), 0, z, splits, split_stride, sv, vectors, scale, out); break;
+    case 4096: launch(ctx, "hadamard_epilogue", k_epilogue_wave<64, Scale>, grid, dim3(256), 0, z, splits, split_stride, sv, vectors, scale, out); break;
+    default:
+        launch(ctx, "hadamard_epilogue", k_epilogue<Scale>, dim3(vectors), dim3(256),
+               n * sizeof(float), z, splits, split_stride, n, sv, 0u,
+               static_cast<const uint32_t *>(nullptr), scale, out);
+    }
+}
 
 void launch_prologue_f16(adi_hip_context *ctx, const float *x, uint32_t n,
                          const uint16_t *su, uint32_t su_stride,
@@ -485,6 +684,17 @@ void launch_expert_gemv(adi_hip_context *ctx, const ExpertGemv &args) {
     }
 }
 
+void launch_moe_gemv(adi_hip_context *ctx, MoeGemv &m, bool single_token) {
+    m.expert_blocks = ceil_div((m.expert[0].rows / kTile) * (m.expert[0].columns / kTile), 64);
+    m.ne_blocks = ceil_div((m.ne[0].rows / kTile) * (m.ne[0].columns / kTile), 64);
+    const uint32_t blocks = m.expert_count * m.expert_blocks * m.max_active + m.ne_count * m.ne_blocks;
+    if (single_token) {
+        launch(ctx, "moe_gemv", k_moe_gemv<1>, dim3(blocks), dim3(256), 0, m);
+    } else {
+        launch(ctx, "moe_gemv", k_moe_gemv<4>, dim3(blocks), dim3(256), 0, m);
+    }
+}
+
 void launch_ne_gemv(adi_hip_context *ctx, const NeGemv &args) {
     const uint32_t tiles = (args.rows / kTile) * (args.columns / kTile);
     if (args.batch == 1) {
@@ -493,6 +703,11 @@ void launch_ne_gemv(adi_hip_context *ctx, const NeGemv &args) {
         launch(ctx, "ne_gemv", k_ne_gemv<4>, dim3(ceil_div(tiles, 64)), dim3(256), 0, args);
     }
 }
+
+template void launch_epilogue_any<uint16_t>(adi_hip_context *, const float *, uint32_t, size_t,
+                                            uint32_t, const uint16_t *, uint32_t, float *);
+template void launch_epilogue_any<int8_t>(adi_hip_context *, const float *, uint32_t, size_t,
+                                          uint32_t, const int8_t *, uint32_t, float *);
 
 void validate_expert(const adi_hip_expert_matrix *m) {
     require(m != nullptr, "Mach expert matrix is null");
@@ -540,7 +755,11 @@ int adi_hip_expert_matmul(adi_hip_context *ctx, const adi_hip_expert_matrix *m,
                   Workspace::round(size_t(splits) * batch * m->rows * 4));
         float *x_hat = ws.take<float>(size_t(batch) * m->columns);
         float *z = ws.take<float>(size_t(splits) * batch * m->rows);
-        launch_prologue_f16(ctx, inputs, m->columns, m->su_f16, 0, nullptr, nullptr, batch, x_hat);
+        PrologueJobs jobs{};
+        jobs.segments = 1;
+        jobs.n = m->columns;
+        jobs.seg[0] = PrologueSegment{inputs, nullptr, nullptr, m->su_f16, nullptr, 0, x_hat, batch};
+        launch_prologues(ctx, jobs);
         ExpertGemv g{};
         g.trellis = m->trellis;
         g.gamma = m->wave_gamma_f16;
@@ -553,8 +772,8 @@ int adi_hip_expert_matmul(adi_hip_context *ctx, const adi_hip_expert_matrix *m,
         g.batch = batch;
         g.tokens_per_pass = batch == 1 ? 1 : 4;
         launch_expert_gemv(ctx, g);
-        launch_epilogue_f16(ctx, z, splits, size_t(batch) * m->rows, m->rows, m->sv_f16, 0,
-                            nullptr, batch, outputs);
+        launch_epilogue_any<uint16_t>(ctx, z, splits, size_t(batch) * m->rows, m->rows, m->sv_f16,
+                                      batch, outputs);
     });
 }
 
@@ -576,7 +795,11 @@ int adi_hip_ne_matmul(adi_hip_context *ctx, const adi_hip_ne_matrix *m,
                   Workspace::round(size_t(splits) * batch * m->rows * 4));
         float *x_hat = ws.take<float>(size_t(batch) * m->columns);
         float *z = ws.take<float>(size_t(splits) * batch * m->rows);
-        launch_prologue_sign(ctx, inputs, m->columns, m->su, batch, x_hat);
+        PrologueJobs jobs{};
+        jobs.segments = 1;
+        jobs.n = m->columns;
+        jobs.seg[0] = PrologueSegment{inputs, nullptr, nullptr, nullptr, m->su, 0, x_hat, batch};
+        launch_prologues(ctx, jobs);
         NeGemv g{};
         g.trellis = m->trellis;
         g.codebook = m->codebook->data;
@@ -588,14 +811,35 @@ int adi_hip_ne_matmul(adi_hip_context *ctx, const adi_hip_ne_matrix *m,
         g.z_split_stride = size_t(batch) * m->rows;
         g.batch = batch;
         launch_ne_gemv(ctx, g);
-        launch_epilogue_sign(ctx, z, splits, size_t(batch) * m->rows, m->rows, m->sv, batch,
-                             outputs);
+        launch_epilogue_any<int8_t>(ctx, z, splits, size_t(batch) * m->rows, m->rows, m->sv, batch,
+                                    outputs);
     });
 }
 
 int adi_hip_ne_matvec(adi_hip_context *ctx, const adi_hip_ne_matrix *m,
                       const float *input, float *output) {
     return adi_hip_ne_matmul(ctx, m, input, 1, output);
+}
+
+int adi_hip_hadamard(adi_hip_context *ctx, float *values, uint32_t n, uint32_t count) {
+    return guarded(ctx, [&] {
+        require(values != nullptr && count > 0, "Hadamard vectors are null or empty");
+        require(is_power_of_two(n) && n <= kMaxHadamard, "Hadamard width must be a power of two up to 8192");
+        const float scale = hadamard_scale(n);
+        const dim3 grid(ceil_div(count, 4));
+        switch (n) {
+        case 64: launch(ctx, "hadamard", k_hadamard_wave<1>, grid, dim3(256), 0, values, count, scale); break;
+        case 128: launch(ctx, "hadamard", k_hadamard_wave<2>, grid, dim3(256), 0, values, count, scale); break;
+        case 256: launch(ctx, "hadamard", k_hadamard_wave<4>, grid, dim3(256), 0, values, count, scale); break;
+        case 512: launch(ctx, "hadamard", k_hadamard_wave<8>, grid, dim3(256), 0, values, count, scale); break;
+        case 1024: launch(ctx, "hadamard", k_hadamard_wave<16>, grid, dim3(256), 0, values, count, scale); break;
+        case 2048: launch(ctx, "hadamard", k_hadamard_wave<32>, grid, dim3(256), 0, values, count, scale); break;
+        case 4096: launch(ctx, "hadamard", k_hadamard_wave<64>, grid, dim3(256), 0, values, count, scale); break;
+        default:
+            launch(ctx, "hadamard", k_hadamard_block, dim3(count), dim3(256), n * sizeof(float),
+                   values, n, scale);
+        }
+    });
 }
 
 int adi_hip_expert_decode(adi_hip_context *ctx, const adi_hip_expert_matrix *m, float *values) {

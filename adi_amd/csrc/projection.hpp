@@ -9,6 +9,31 @@ namespace adi_hip {
 // Largest vector a Hadamard prologue/epilogue block holds in LDS.
 constexpr uint32_t kMaxHadamard = 8192;
 
+// Vectors to transform in one launch: x_hat = H_n(x[src] * su). su is either
+// f16 (per matrix, stride su_stride, matrix from matrix_index) or +-1 int8.
+struct PrologueSegment {
+    const float *x;
+    const uint32_t *source_row;    // nullable: identity
+    const uint32_t *matrix_index;  // nullable: matrix 0
+    const uint16_t *su_f16;        // one of su_f16 / su_sign
+    const int8_t *su_sign;
+    uint32_t su_stride;
+    float *out;
+    uint32_t count;
+};
+struct PrologueJobs {
+    PrologueSegment seg[4];
+    uint32_t segments;
+    uint32_t n;
+    float scale;  // set by the launcher
+};
+bool wave_width(uint32_t n);
+void launch_prologues(adi_hip_context *ctx, PrologueJobs &jobs);
+template <typename Scale>
+void launch_epilogue_any(adi_hip_context *ctx, const float *z, uint32_t splits,
+                         size_t split_stride, uint32_t n, const Scale *sv, uint32_t vectors,
+                         float *out);
+
 // x_hat[v] = H_n(x[src(v)] * su[mat(v)]) for v < vectors.
 // source_row / matrix_index may be null (identity / matrix 0).
 void launch_prologue_f16(adi_hip_context *ctx, const float *x, uint32_t n,
@@ -67,6 +92,20 @@ struct NeGemv {
     uint32_t batch;
 };
 void launch_ne_gemv(adi_hip_context *ctx, const NeGemv &args);
+
+// Up to two expert GEMVs (routed over the same active list) and two NE GEMVs
+// in one launch. The expert entries must share shape and routing; so must
+// the NE entries.
+struct MoeGemv {
+    ExpertGemv expert[2];
+    uint32_t expert_count;
+    NeGemv ne[2];
+    uint32_t ne_count;
+    uint32_t max_active;
+    uint32_t expert_blocks;  // set by the launcher
+    uint32_t ne_blocks;      // set by the launcher
+};
+void launch_moe_gemv(adi_hip_context *ctx, MoeGemv &m, bool single_token);
 
 void validate_expert(const adi_hip_expert_matrix *m);
 void validate_ne(const adi_hip_ne_matrix *m);

@@ -76,6 +76,7 @@ SIGNATURES = [
     ("adi_hip_expert_matvec", C.c_int, [vp, C.POINTER(ExpertMatrix), vp, vp]),
     ("adi_hip_ne_matmul", C.c_int, [vp, C.POINTER(NeMatrix), vp, u32, vp]),
     ("adi_hip_ne_matvec", C.c_int, [vp, C.POINTER(NeMatrix), vp, vp]),
+    ("adi_hip_hadamard", C.c_int, [vp, vp, u32, u32]),
     ("adi_hip_expert_decode", C.c_int, [vp, C.POINTER(ExpertMatrix), vp]),
     ("adi_hip_ne_decode", C.c_int, [vp, C.POINTER(NeMatrix), vp]),
     ("adi_hip_head_matmul", C.c_int, [vp, C.POINTER(HeadChunk), vp, u32, vp]),
@@ -290,6 +291,10 @@ def upload_moe_layer(ctx: Context, layer, expert_book: int, ne_book: int) -> Dev
 def expert_matmul(ctx: Context, m: DeviceExpert, x, batch: int, out) -> None:
     ctx.check(ctx.lib.adi_hip_expert_matmul(ctx.handle, C.byref(m.struct), x.data_ptr(), batch,
                                             out.data_ptr()))
+
+
+def hadamard(ctx: Context, values, n: int, count: int) -> None:
+    ctx.check(ctx.lib.adi_hip_hadamard(ctx.handle, values.data_ptr(), n, count))
 
 
 def expert_decode(ctx: Context, m: DeviceExpert, out) -> None:

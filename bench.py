@@ -63,6 +63,10 @@ def log(msg):
 
 def kernel_bytes(name, active):
     """Algorithmic packed bytes one launch of `name` reads, or None."""
+    if name == "moe_gemv":
+        # two launches per step: gate+up (2 expert + 2 shared matrices), down
+        # (1 + 1); the mean launch reads half the step's GEMV packed bytes
+        return (3 * active * (EXPERT_TRELLIS_BYTES + EXPERT_GAMMA_BYTES) + 3 * NE_TRELLIS_BYTES) / 2
     if name == "expert_gemv":
         return active * (EXPERT_TRELLIS_BYTES + EXPERT_GAMMA_BYTES)
     if name == "ne_gemv":

@@ -138,6 +138,14 @@ int adi_hip_ne_matmul(adi_hip_context *ctx, const adi_hip_ne_matrix *m,
 int adi_hip_ne_matvec(adi_hip_context *ctx, const adi_hip_ne_matrix *m,
                       const float *input, float *output);
 
+/* In place, on `count` contiguous device vectors of n floats (n a power of
+ * two up to 8192): the normalised fast Walsh-Hadamard transform every packed
+ * projection applies to its input and output, hadamard_transform
+ * (src/simd.cpp:48-63, 395-397). Butterflies run with strides 1, 2, 4, ...
+ * as in the reference, so the result is bit-identical to it. */
+int adi_hip_hadamard(adi_hip_context *ctx, float *values, uint32_t n,
+                     uint32_t count);
+
 /* The decoded weights of a packed matrix as a dense fp32 [rows, columns]
  * array, through the same loads and decode the GEMV kernels use: expert
  * lattice values V (before the tile gamma and the su/sv/Hadamard rotations),

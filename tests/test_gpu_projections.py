@@ -116,3 +116,15 @@ def test_shape_errors_leave_outputs_untouched(gpu, books):
     dm2 = hip.upload_expert(gpu, m2, eb)
     with pytest.raises(hip.HipError):
         hip.expert_matmul(gpu, dm2, torch.ones((1, 16), device="cuda"), 0, out)
+
+
+@pytest.mark.parametrize("n", [16, 64, 128, 512, 2048, 4096, 8192])
+def test_hadamard_bit_exact(gpu, oracle, n):
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal((5, n)).astype(np.float32)
+    want = x.copy()
+    for row in want:
+        assert oracle.ao_hadamard(po.ptr(row, po.C.c_float), n) == 0
+    dev = gpu.to_device(x)
+    hip.hadamard(gpu, dev, n, 5)
+    assert np.array_equal(dev.cpu().numpy().view(np.uint32), want.view(np.uint32))
