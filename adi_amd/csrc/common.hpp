@@ -44,6 +44,15 @@ inline void check_hip(hipError_t error, const char *what) {
 
 inline bool is_power_of_two(uint32_t v) { return v != 0 && (v & (v - 1)) == 0; }
 
+// log2 of a power of two.
+inline uint32_t log2_of(uint32_t v) {
+    uint32_t s = 0;
+    while ((1u << s) < v) {
+        ++s;
+    }
+    return s;
+}
+
 // 1/sqrt(n) exactly as the reference computes it on the host
 // (src/simd.cpp:59): a correctly rounded sqrt and a correctly rounded divide.
 inline float hadamard_scale(uint32_t n) {
@@ -129,29 +138,64 @@ __device__ __forceinline__ void block_hadamard(float *v, uint32_t n, float scale
     __syncthreads();
 }
 
-// Value of lane (lane ^ MASK) for MASK < 32, without the LDS crossbar for
-// masks 1, 2, 4 and 8 (DPP: quad permutes, half-row mirror, row rotate by 8;
-// every pattern used is its own inverse, so the DPP shift direction does not
-// matter) and with a swizzle for 16.
+// Value of lane (lane ^ MASK) for MASK in {1, 2, 4, 8, 16, 32}, without the
+// LDS crossbar: DPP quad permutes, half-row mirror and row rotate by 8 for
+// masks up to 8 (every pattern used is its own inverse, so the DPP shift
+// direction does not matter), and gfx950's row swaps for 16 and 32.
 template <int MASK>
-__device__ __forceinline__ float lane_xor(float v) {
-    const int bits = __float_as_int(v);
+__device__ __forceinline__ uint32_t lane_xor_bits(uint32_t v) {
+    const int bits = static_cast<int>(v);
     if constexpr (MASK == 1) {
-        return __int_as_float(__builtin_amdgcn_mov_dpp(bits, 0xB1, 0xF, 0xF, true));
+        return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(bits, 0xB1, 0xF, 0xF, true));
     } else if constexpr (MASK == 2) {
-        return __int_as_float(__builtin_amdgcn_mov_dpp(bits, 0x4E, 0xF, 0xF, true));
+        return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(bits, 0x4E, 0xF, 0xF, true));
     } else if constexpr (MASK == 4) {
         // lane i of a half-row takes lane 7-i after a [3,2,1,0] quad permute
         const int q = __builtin_amdgcn_mov_dpp(bits, 0x1B, 0xF, 0xF, true);
-        return __int_as_float(__builtin_amdgcn_mov_dpp(q, 0x141, 0xF, 0xF, true));
+        return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(q, 0x141, 0xF, 0xF, true));
     } else if constexpr (MASK == 8) {
-        return __int_as_float(__builtin_amdgcn_mov_dpp(bits, 0x128, 0xF, 0xF, true));
+        return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(bits, 0x128, 0xF, 0xF, true));
     } else if constexpr (MASK == 16) {
-        // bitmask swizzle: and 0x1F, or 0, xor 0x10 within 32 lanes
-        return __int_as_float(__builtin_amdgcn_ds_swizzle(bits, 0x401F));
+        // v_permlane16_swap(v, v): the first result holds each even 16-lane
+        // row twice, the second each odd row twice
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (__lane_id() & 16u) ? r[0] : r[1];
     } else {
-        return __shfl_xor(v, MASK);
+        static_assert(MASK == 32, "lane_xor: unsupported mask");
+        // v_permlane32_swap(v, v): the first result holds lanes 0-31 twice,
+        // the second lanes 32-63 twice
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (__lane_id() & 32u) ? r[0] : r[1];
     }
+}
+
+template <int MASK>
+__device__ __forceinline__ float lane_xor(float v) {
+    return __uint_as_float(lane_xor_bits<MASK>(__float_as_uint(v)));
+}
+
+// Value of the next lane of the lane's quad (lane 3 of a quad reads lane 0):
+// a DPP quad permute [1, 2, 3, 0].
+__device__ __forceinline__ uint32_t quad_next(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x39, 0xF, 0xF, true));
+}
+
+// Sums v over the lanes that differ only in lane bits 2.. of `span` (a power
+// of two up to 16): the four lanes of a quad position across `span` quads.
+__device__ __forceinline__ float sum_over_quads(float v, uint32_t span) {
+    if (span > 1) {
+        v += lane_xor<4>(v);
+    }
+    if (span > 2) {
+        v += lane_xor<8>(v);
+    }
+    if (span > 4) {
+        v += lane_xor<16>(v);
+    }
+    if (span > 8) {
+        v += lane_xor<32>(v);
+    }
+    return v;
 }
 
 // Normalised FWHT of n = 64*VPL values held by one wave, element e in lane
@@ -195,6 +239,35 @@ __device__ __forceinline__ void wave_hadamard(float (&v)[VPL], float scale, uint
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
         v[i] = v[i] * scale;
+    }
+}
+
+// v[i] = sum over slices s < splits of src[s * stride + i * 64 + lane], added
+// in slice order; two slices are loaded per round so the loads overlap (one
+// for the widest vectors, whose registers would not hold two).
+template <int VPL>
+__device__ __forceinline__ void sum_slices(const float *src, size_t stride, uint32_t splits,
+                                           uint32_t lane, float (&v)[VPL]) {
+#pragma clang fp contract(off)
+    src += lane;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        v[i] = 0.0f;
+    }
+    constexpr uint32_t kRound = VPL > 32 ? 1u : 2u;
+    for (uint32_t s = 0; s < splits; s += kRound) {
+        const bool second = kRound == 2 && s + 1 < splits;
+        float a[VPL], b[VPL];
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            a[i] = src[s * stride + i * 64];
+            b[i] = second ? src[(s + 1) * stride + i * 64] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            v[i] = v[i] + a[i];
+            v[i] = v[i] + b[i];
+        }
     }
 }
 

@@ -178,11 +178,14 @@ int adi_hip_codebook_create_expert(adi_hip_context *ctx, const float *tlut,
         require(all_finite(tlut, 32768 * 8), "expert TLUT holds a non-finite value");
         // Row r of the reachable table is TLUT row 2r, every value rounded
         // through f16 (src/codec_cache.cpp:33-58); the per-state sign of
-        // component 0 is applied in the kernels.
+        // component 0 is applied in the kernels. Stored as two planes of
+        // 16384 x 4 f16 (components 0-3, then 4-7) so that one plane, 128 KiB,
+        // fits in a CU's LDS.
         std::vector<uint16_t> table(size_t(kExpertRows) * 8);
         for (uint32_t r = 0; r < kExpertRows; ++r) {
             for (uint32_t c = 0; c < 8; ++c) {
-                table[size_t(r) * 8 + c] = f16_bits(tlut[size_t(2 * r) * 8 + c]);
+                table[size_t(c / 4) * kExpertRows * 4 + size_t(r) * 4 + c % 4] =
+                    f16_bits(tlut[size_t(2 * r) * 8 + c]);
             }
         }
         *out = upload(ctx, adi_hip_codebook::expert, table);

@@ -14,7 +14,7 @@
 struct adi_hip_codebook {
     enum Kind { expert, ne } kind;
     int device;
-    void *data;    // expert: u16[16384][8]; ne: u16[1024][2]
+    void *data;    // expert: u16[2][16384][4] (component planes); ne: u16[1024][2]
     size_t bytes;
 };
 
@@ -144,6 +144,15 @@ void launch(adi_hip_context *ctx, const char *name, Kernel kernel, dim3 grid,
         check_hip(hipEventRecord(stop, ctx->stream), "hipEventRecord");
         stat_for(ctx, name).pending.emplace_back(start, stop);
     }
+}
+
+// Raises a kernel's dynamic LDS limit above the 64 KiB default (once per
+// kernel; the result is cached by the caller in a function-local static).
+inline bool set_lds_limit(const void *kernel, size_t bytes) {
+    check_hip(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(bytes)),
+              "hipFuncSetAttribute");
+    return true;
 }
 
 inline uint32_t ceil_div(uint64_t a, uint64_t b) {

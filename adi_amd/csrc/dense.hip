@@ -111,30 +111,61 @@ __global__ __launch_bounds__(64) void k_bf16_lds(
     }
     const uint32_t total_rows = rows + (w_extra != nullptr ? 1u : 0u);
     const uint32_t row0 = blockIdx.x * rows_per_block;
-    const bool wide = (columns % 8u) == 0;  // 16-byte staging when rows stay aligned
-    for (uint32_t t = 0; t < tokens; ++t) {
-        const float *src = x + static_cast<size_t>(t0 + t) * columns;
-        if (wide) {
-            for (uint32_t k = threadIdx.x; k < columns / 4u; k += 64u) {
-                reinterpret_cast<float4 *>(xs + t * columns)[k] = reinterpret_cast<const float4 *>(src)[k];
+    const uint32_t rows_here =
+        total_rows - row0 < rows_per_block ? total_rows - row0 : rows_per_block;
+    const uintptr_t addresses = reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x) |
+                                reinterpret_cast<uintptr_t>(w_extra);
+    if ((columns % 8u) == 0 && (addresses & 15u) == 0) {
+        // 16-byte staging; every load of a batch is issued before the first
+        // LDS store so the block waits for memory once per batch, not per load
+        constexpr uint32_t kBatch = 8;
+        const uint32_t w_per_row = columns / 8u;
+        const uint32_t w_total = rows_here * w_per_row;
+        // Indexes past the end are clamped to the last element: those lanes
+        // load it and store the same value again, so nothing is guarded and
+        // every load of a batch issues before the first store waits.
+        for (uint32_t f0 = 0; f0 < w_total; f0 += 64u * kBatch) {
+            uint4 v[kBatch];
+            uint32_t at[kBatch];
+#pragma unroll
+            for (uint32_t u = 0; u < kBatch; ++u) {
+                at[u] = min(f0 + u * 64u + threadIdx.x, w_total - 1u);
+                const uint32_t r = at[u] / w_per_row, k = at[u] - r * w_per_row;
+                const uint32_t row = row0 + r;
+                const uint16_t *src = row < rows ? w + static_cast<size_t>(row) * columns : w_extra;
+                v[u] = reinterpret_cast<const uint4 *>(src)[k];
             }
-        } else {
+#pragma unroll
+            for (uint32_t u = 0; u < kBatch; ++u) {
+                reinterpret_cast<uint4 *>(ws)[at[u]] = v[u];
+            }
+        }
+        const uint32_t x_per_row = columns / 4u;
+        const uint32_t x_total = tokens * x_per_row;
+        const float4 *xsrc = reinterpret_cast<const float4 *>(x + static_cast<size_t>(t0) * columns);
+        for (uint32_t f0 = 0; f0 < x_total; f0 += 64u * kBatch) {
+            float4 v[kBatch];
+            uint32_t at[kBatch];
+#pragma unroll
+            for (uint32_t u = 0; u < kBatch; ++u) {
+                at[u] = min(f0 + u * 64u + threadIdx.x, x_total - 1u);
+                v[u] = xsrc[at[u]];
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < kBatch; ++u) {
+                reinterpret_cast<float4 *>(xs)[at[u]] = v[u];
+            }
+        }
+    } else {
+        for (uint32_t t = 0; t < tokens; ++t) {
+            const float *src = x + static_cast<size_t>(t0 + t) * columns;
             for (uint32_t k = threadIdx.x; k < columns; k += 64u) {
                 xs[t * columns + k] = src[k];
             }
         }
-    }
-    for (uint32_t r = 0; r < rows_per_block; ++r) {
-        const uint32_t row = row0 + r;
-        if (row >= total_rows) {
-            break;
-        }
-        const uint16_t *src = row < rows ? w + static_cast<size_t>(row) * columns : w_extra;
-        if (wide) {
-            for (uint32_t k = threadIdx.x; k < columns / 8u; k += 64u) {
-                reinterpret_cast<uint4 *>(ws + r * columns)[k] = reinterpret_cast<const uint4 *>(src)[k];
-            }
-        } else {
+        for (uint32_t r = 0; r < rows_here; ++r) {
+            const uint32_t row = row0 + r;
+            const uint16_t *src = row < rows ? w + static_cast<size_t>(row) * columns : w_extra;
             for (uint32_t k = threadIdx.x; k < columns; k += 64u) {
                 ws[r * columns + k] = src[k];
             }
@@ -249,70 +280,87 @@ __global__ __launch_bounds__(64) void k_rms_norm(
     }
 }
 
-// Larger logit first, lower index on ties: the comparator of top_experts
-// (src/executor.cpp:202-211).
-__device__ __forceinline__ bool route_before(float a, uint32_t ia, float b, uint32_t ib) {
-    return a == b ? ia < ib : a > b;
+// Order-preserving key of (logit, expert) for "larger logit first, lower
+// index on ties": the float's bits mapped to an unsigned order (with -0
+// folded into +0, which compares equal to it) above the complemented index.
+// Key 0 is below every real key and marks an empty slot.
+__device__ __forceinline__ uint64_t route_key(float value, uint32_t expert) {
+    const uint32_t bits = __float_as_uint(value + 0.0f);
+    const uint32_t ordered = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+    return (static_cast<uint64_t>(ordered) << 32) | static_cast<uint32_t>(~expert);
+}
+
+__device__ __forceinline__ float route_key_value(uint64_t key) {
+    const uint32_t ordered = static_cast<uint32_t>(key >> 32);
+    return __uint_as_float((ordered & 0x80000000u) ? (ordered & 0x7FFFFFFFu) : ~ordered);
+}
+
+template <int MASK>
+__device__ __forceinline__ uint64_t key_max_step(uint64_t key) {
+    const uint64_t other =
+        (static_cast<uint64_t>(lane_xor_bits<MASK>(static_cast<uint32_t>(key >> 32))) << 32) |
+        lane_xor_bits<MASK>(static_cast<uint32_t>(key));
+    return other > key ? other : key;
 }
 
 // One wave per logit row. Lane l holds experts l, l+64, ...; eight rounds of
-// a wave-wide arg-max by the comparator pick the routes in order. The softmax
-// over the eight then runs on lane 0 in the reference's order
+// a wave-wide maximum over route keys (registers only) pick the routes in the
+// order of the comparator of top_experts (src/executor.cpp:202-211). The
+// softmax over the eight then runs on lane 0 in the reference's order
 // (src/executor.cpp:213-227).
 template <int SLOTS>
 __device__ __forceinline__ void top8_wave(const float *__restrict__ row,
                                           const float *__restrict__ bias, uint32_t experts,
                                           uint32_t lane, uint32_t *__restrict__ route_expert,
-                                          float *__restrict__ route_weight) {
+                                          float *__restrict__ route_weight,
+                                          uint32_t *local_expert = nullptr) {
 #pragma clang fp contract(off)
     constexpr uint32_t per_lane = SLOTS;
-    float value[per_lane];
-    uint32_t used = 0;
+    float value[per_lane], offset[per_lane];
+    // unguarded loads of clamped indexes, so all of them are in flight at once
+#pragma unroll
+    for (uint32_t i = 0; i < per_lane; ++i) {
+        const uint32_t e = min(lane + 64u * i, experts - 1u);
+        value[i] = row[e];
+        offset[i] = bias != nullptr ? bias[e] : 0.0f;
+    }
+    uint64_t key[per_lane];
 #pragma unroll
     for (uint32_t i = 0; i < per_lane; ++i) {
         const uint32_t e = lane + 64u * i;
-        value[i] = 0.0f;
-        if (e < experts) {
-            value[i] = row[e];
-            if (bias != nullptr) {
-                value[i] = value[i] + bias[e];
-            }
-        } else {
-            used |= 1u << i;
-        }
+        const float v = bias != nullptr ? value[i] + offset[i] : value[i];
+        key[i] = e < experts ? route_key(v, e) : 0ull;
     }
     float chosen_value[8];
     uint32_t chosen_index[8];
     for (int round = 0; round < 8; ++round) {
-        float best = 0.0f;
-        uint32_t best_index = 0xFFFFFFFFu;
+        uint64_t best = 0;
 #pragma unroll
         for (uint32_t i = 0; i < per_lane; ++i) {
-            const uint32_t e = lane + 64u * i;
-            if (!(used & (1u << i)) &&
-                (best_index == 0xFFFFFFFFu || route_before(value[i], e, best, best_index))) {
-                best = value[i];
-                best_index = e;
-            }
+            best = key[i] > best ? key[i] : best;
         }
-#define ADI_ARGMAX_STAGE(MASK)                                                          \
-    {                                                                                   \
-        const float other = lane_xor<MASK>(best);                                       \
-        const uint32_t other_index =                                                    \
-            __float_as_uint(lane_xor<MASK>(__uint_as_float(best_index)));               \
-        if (other_index != 0xFFFFFFFFu &&                                               \
-            (best_index == 0xFFFFFFFFu || route_before(other, other_index, best, best_index))) { \
-            best = other;                                                               \
-            best_index = other_index;                                                   \
-        }                                                                               \
-    }
-        ADI_ARGMAX_STAGE(1) ADI_ARGMAX_STAGE(2) ADI_ARGMAX_STAGE(4) ADI_ARGMAX_STAGE(8)
-        ADI_ARGMAX_STAGE(16) ADI_ARGMAX_STAGE(32)
-#undef ADI_ARGMAX_STAGE
-        chosen_value[round] = best;
-        chosen_index[round] = best_index;
-        if (best_index % 64u == lane) {
-            used |= 1u << (best_index / 64u);
+        best = key_max_step<1>(best);
+        best = key_max_step<2>(best);
+        best = key_max_step<4>(best);
+        best = key_max_step<8>(best);
+        best = key_max_step<16>(best);
+        best = key_max_step<32>(best);
+        // identical in every lane: keep it in scalar registers
+        const uint32_t win_hi =
+            static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(best >> 32)));
+        const uint32_t win_lo =
+            static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(best)));
+        const uint64_t win = (static_cast<uint64_t>(win_hi) << 32) | win_lo;
+        const uint32_t index = ~static_cast<uint32_t>(win);
+        chosen_value[round] = route_key_value(win);
+        chosen_index[round] = index;
+        if (index % 64u == lane) {
+#pragma unroll
+            for (uint32_t i = 0; i < per_lane; ++i) {
+                if (i == index / 64u) {
+                    key[i] = 0ull;
+                }
+            }
         }
     }
     if (lane == 0) {
@@ -327,6 +375,9 @@ __device__ __forceinline__ void top8_wave(const float *__restrict__ row,
         for (int i = 0; i < 8; ++i) {
             route_expert[i] = chosen_index[i];
             route_weight[i] = selected[i] / sum;
+            if (local_expert != nullptr) {
+                local_expert[i] = chosen_index[i];
+            }
         }
     }
 }
@@ -349,14 +400,16 @@ __global__ __launch_bounds__(256) void k_top_experts(
 // (token, route) slots are placed 64 at a time in order; lanes that share an
 // expert in a chunk find their rank among earlier lanes with ballots, so each
 // expert's cursor advances exactly as the sequential loop's does.
-__device__ __forceinline__ void route_sort_block(const RouteSort &a, uint32_t *counts,
-                                                 uint32_t *cursor) {
+// `route_expert` is a.route_expert or a copy of it in LDS.
+__device__ __forceinline__ void route_sort_block(const RouteSort &a,
+                                                 const uint32_t *route_expert,
+                                                 uint32_t *counts, uint32_t *cursor) {
     for (uint32_t e = threadIdx.x; e < a.experts; e += blockDim.x) {
         counts[e] = 0u;
     }
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < a.positions; i += blockDim.x) {
-        atomicAdd(&counts[a.route_expert[i]], 1u);
+        atomicAdd(&counts[route_expert[i]], 1u);
     }
     __syncthreads();
     if (threadIdx.x >= 64) {
@@ -400,9 +453,18 @@ __device__ __forceinline__ void route_sort_block(const RouteSort &a, uint32_t *c
             const bool on = e < a.experts && counts[e] != 0u;
             const uint64_t mask = __ballot(on);
             if (on) {
-                a.active[base + __popcll(mask & ((1ull << lane) - 1ull))] = e;
+                const uint32_t s = base + __popcll(mask & ((1ull << lane) - 1ull));
+                a.active[s] = e;
+                if (a.slot_info != nullptr) {
+                    a.slot_info[s] = make_uint4(e, cursor[e], cursor[e] + counts[e], 0u);
+                }
             }
             base += __popcll(mask);
+        }
+        if (a.slot_info != nullptr) {
+            for (uint32_t s = base + lane; s < a.experts; s += 64u) {
+                a.slot_info[s] = make_uint4(0u, 0u, 0u, 0u);
+            }
         }
         if (lane == 0 && a.active_count != nullptr) {
             *a.active_count = base;
@@ -414,7 +476,7 @@ __device__ __forceinline__ void route_sort_block(const RouteSort &a, uint32_t *c
     for (uint32_t c = 0; c < a.positions; c += 64u) {
         const uint32_t i = c + lane;
         const bool valid = i < a.positions;
-        const uint32_t e = valid ? a.route_expert[i] : 0u;
+        const uint32_t e = valid ? route_expert[i] : 0u;
         uint64_t peers = __ballot(valid);
         if (!valid) {
             peers = ~peers;
@@ -447,26 +509,27 @@ __device__ __forceinline__ void route_sort_block(const RouteSort &a, uint32_t *c
 __global__ __launch_bounds__(64) void k_route_sort(RouteSort a) {
     __shared__ uint32_t counts[kMaxExperts];
     __shared__ uint32_t cursor[kMaxExperts];
-    route_sort_block(a, counts, cursor);
+    route_sort_block(a, a.route_expert, counts, cursor);
 }
 
-// Routing of a whole batch in one block: top_experts for every row (one wave
-// per row, rows spread over 16 waves), then the stable counting sort.
+// Routing of a whole batch of at most kRouteBatch rows in one block:
+// top_experts for every row (one wave per row), then the stable counting sort
+// reading the routes back from LDS.
 template <int SLOTS>
-__global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
+__global__ __launch_bounds__(1024) void k_route(const float *__restrict__ logits,
                                                const float *__restrict__ bias, uint32_t batch,
                                                uint32_t *__restrict__ route_expert,
                                                float *__restrict__ route_weight, RouteSort a) {
     __shared__ uint32_t counts[kMaxExperts];
     __shared__ uint32_t cursor[kMaxExperts];
+    __shared__ uint32_t local_expert[kRouteBatch * 8];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     for (uint32_t t = wave; t < batch; t += blockDim.x / 64u) {
         top8_wave<SLOTS>(logits + static_cast<size_t>(t) * a.experts, bias, a.experts, lane,
-                         route_expert + t * 8u, route_weight + t * 8u);
+                         route_expert + t * 8u, route_weight + t * 8u, local_expert + t * 8u);
     }
-    __threadfence_block();
     __syncthreads();
-    route_sort_block(a, counts, cursor);
+    route_sort_block(a, local_expert, counts, cursor);
 }
 
 }  // namespace
@@ -548,22 +611,22 @@ void launch_route_sort(adi_hip_context *ctx, const RouteSort &args) {
 void launch_route(adi_hip_context *ctx, const float *logits, const float *bias, uint32_t batch,
                   uint32_t *route_expert, float *route_weight, const RouteSort &args) {
     const uint32_t slots = ceil_div(args.experts, 64);
-    if (batch > 16) {
+    if (batch > kRouteBatch) {
         // many rows: top_experts over a grid, then the one-block sort
         launch_top_experts(ctx, logits, bias, batch, args.experts, route_expert, route_weight);
         launch_route_sort(ctx, args);
         return;
     }
     if (slots <= 1) {
-        launch(ctx, "route", k_route<1>, dim3(1), dim3(256), 0, logits, bias, batch, route_expert, route_weight, args);
+        launch(ctx, "route", k_route<1>, dim3(1), dim3(64 * batch), 0, logits, bias, batch, route_expert, route_weight, args);
     } else if (slots <= 2) {
-        launch(ctx, "route", k_route<2>, dim3(1), dim3(256), 0, logits, bias, batch, route_expert, route_weight, args);
+        launch(ctx, "route", k_route<2>, dim3(1), dim3(64 * batch), 0, logits, bias, batch, route_expert, route_weight, args);
     } else if (slots <= 4) {
-        launch(ctx, "route", k_route<4>, dim3(1), dim3(256), 0, logits, bias, batch, route_expert, route_weight, args);
+        launch(ctx, "route", k_route<4>, dim3(1), dim3(64 * batch), 0, logits, bias, batch, route_expert, route_weight, args);
     } else if (slots <= 8) {
-        launch(ctx, "route", k_route<8>, dim3(1), dim3(256), 0, logits, bias, batch, route_expert, route_weight, args);
+        launch(ctx, "route", k_route<8>, dim3(1), dim3(64 * batch), 0, logits, bias, batch, route_expert, route_weight, args);
     } else {
-        launch(ctx, "route", k_route<16>, dim3(1), dim3(256), 0, logits, bias, batch, route_expert, route_weight, args);
+        launch(ctx, "route", k_route<16>, dim3(1), dim3(64 * batch), 0, logits, bias, batch, route_expert, route_weight, args);
     }
 }
 

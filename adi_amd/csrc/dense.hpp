@@ -33,6 +33,8 @@ struct RouteSort {
     uint32_t *offsets;            // [experts + 1]
     uint32_t *active;             // [experts] active experts ascending (nullable)
     uint32_t *active_count;       // [1] (nullable)
+    uint4 *slot_info;             // [experts] {expert, first, end, 0} per active slot,
+                                  // zero past the active count (nullable)
     uint32_t *position_expert;    // [positions] (nullable)
     uint32_t *grouped_batch;      // [positions]
     uint32_t *route_to_grouped;   // [positions]
@@ -45,5 +47,6 @@ void launch_route(adi_hip_context *ctx, const float *logits, const float *bias, 
                   uint32_t *route_expert, float *route_weight, const RouteSort &args);
 
 constexpr uint32_t kMaxExperts = 1024;
+constexpr uint32_t kRouteBatch = 16;  // largest batch launch_route handles in one block
 
 }  // namespace adi_hip

@@ -48,12 +48,12 @@ struct SwigluSegment {
     const uint32_t *matrix_index;
     float *x_hat;
     uint32_t count;
+    uint32_t splits;              // slices of z_gate / z_up
 };
 
 struct SwigluJobs {
     SwigluSegment seg[2];
     uint32_t segments;
-    uint32_t splits;
     float scale;
 };
 
@@ -72,20 +72,10 @@ __global__ __launch_bounds__(256) void k_swiglu_wave(SwigluJobs j) {
     }
     const SwigluSegment &g = j.seg[s];
     const uint32_t n = 64u * VPL;
-    const size_t base = static_cast<size_t>(v) * n + lane;
+    const size_t base = static_cast<size_t>(v) * n;
     float gv[VPL], uv[VPL];
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-        gv[i] = g.z_gate[base + i * 64];
-        uv[i] = g.z_up[base + i * 64];
-    }
-    for (uint32_t sp = 1; sp < j.splits; ++sp) {
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            gv[i] += g.z_gate[sp * g.split_stride + base + i * 64];
-            uv[i] += g.z_up[sp * g.split_stride + base + i * 64];
-        }
-    }
+    sum_slices<VPL>(g.z_gate + base, g.split_stride, g.splits, lane, gv);
+    sum_slices<VPL>(g.z_up + base, g.split_stride, g.splits, lane, uv);
     wave_hadamard<VPL>(gv, j.scale, lane);
     wave_hadamard<VPL>(uv, j.scale, lane);
     const size_t mat = g.matrix_index != nullptr ? g.matrix_index[v] : 0u;
@@ -151,16 +141,7 @@ __global__ __launch_bounds__(576) void k_combine_wave(CombineArgs a) {
         splits = a.shared_splits;
         stride = a.shared_split_stride;
     }
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-        val[i] = src[i * 64u + lane];
-    }
-    for (uint32_t sp = 1; sp < splits; ++sp) {
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            val[i] += src[sp * stride + i * 64u + lane];
-        }
-    }
+    sum_slices<VPL>(src, stride, splits, lane, val);
     wave_hadamard<VPL>(val, a.scale, lane);
     if (wave < 8) {
         const float w = a.route_weight[b * 8u + wave];
@@ -334,8 +315,8 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         require(inputs != nullptr && outputs != nullptr, "MoE vector is null");
         const uint32_t H = L->hidden, I = L->expert_hidden, E = L->experts;
         const size_t B = batch, P = B * 8;
-        const uint32_t sg = gemv_splits(H);  // gate/up: H inputs
-        const uint32_t sd = gemv_splits(I);  // down: I inputs
+        const uint32_t sg = expert_splits(H), ssg = ne_splits(H);  // gate/up: H inputs
+        const uint32_t sd = expert_splits(I), ssd = ne_splits(I);  // down: I inputs
         const uint32_t max_active = static_cast<uint32_t>(P < E ? P : E);
 
         auto &ws = ctx->workspace;
@@ -343,11 +324,11 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         const size_t bytes =
             Workspace::round(B * E * 4) + Workspace::round(B * 4) +
             Workspace::round(P * 4) * 5 + Workspace::round(E * 4) * 3 +
-            Workspace::round((E + 1) * 4) + Workspace::round(4) +
+            Workspace::round((E + 1) * 4) + Workspace::round(4) + Workspace::round(E * 16) +
             Workspace::round(P * H * 4) * 2 + Workspace::round(sg * P * I * 4) * 2 +
             Workspace::round(P * I * 4) + Workspace::round(sd * P * H * 4) +
-            Workspace::round(B * H * 4) * 2 + Workspace::round(sg * B * I * 4) * 2 +
-            Workspace::round(B * I * 4) + Workspace::round(sd * B * H * 4);
+            Workspace::round(B * H * 4) * 2 + Workspace::round(ssg * B * I * 4) * 2 +
+            Workspace::round(B * I * 4) + Workspace::round(ssd * B * H * 4);
         ws.ensure(bytes);
         float *logits = ws.take<float>(B * E);
         float *shared_logit = ws.take<float>(B);
@@ -361,6 +342,7 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         (void)ws.take<uint32_t>(E);
         uint32_t *offsets = ws.take<uint32_t>(E + 1);
         uint32_t *active_count = ws.take<uint32_t>(1);
+        uint4 *slot_info = ws.take<uint4>(E);
         float *xh_gate = ws.take<float>(P * H);
         float *xh_up = ws.take<float>(P * H);
         float *z_gate = ws.take<float>(sg * P * I);
@@ -369,10 +351,10 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         float *z_down = ws.take<float>(sd * P * H);
         float *sxh_gate = ws.take<float>(B * H);
         float *sxh_up = ws.take<float>(B * H);
-        float *sz_gate = ws.take<float>(sg * B * I);
-        float *sz_up = ws.take<float>(sg * B * I);
+        float *sz_gate = ws.take<float>(ssg * B * I);
+        float *sz_up = ws.take<float>(ssg * B * I);
         float *sxh_down = ws.take<float>(B * I);
-        float *sz_down = ws.take<float>(sd * B * H);
+        float *sz_down = ws.take<float>(ssd * B * H);
 
         const bool wave_path = wave_width(H) && wave_width(I);
 
@@ -390,6 +372,7 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         sort.position_expert = position_expert;
         sort.grouped_batch = grouped_batch;
         sort.route_to_grouped = route_to_grouped;
+        sort.slot_info = slot_info;
         launch_route(ctx, logits, logit_bias, batch, route_expert, route_weight, sort);
 
         // 3: prologues, routed gate/up and shared gate/up
@@ -413,12 +396,6 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         auto expert_job = [&](const adi_hip_expert_stack &st, uint32_t rows, uint32_t columns,
                               size_t words, const float *x_hat, float *z) {
             ExpertGemv g{};
-            g.codebook = L->expert_codebook->data;
-            g.active = active;
-            g.active_count = active_count;
-            g.offsets = offsets;
-            g.max_active = max_active;
-            g.tokens_per_pass = batch == 1 ? 1 : 4;
             g.gamma_stride = gamma_stride;
             g.rows = rows;
             g.columns = columns;
@@ -437,7 +414,6 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
             n.columns = m.columns;
             n.z_split_stride = B * m.rows;
             n.trellis = m.trellis;
-            n.codebook = m.codebook->data;
             n.weight_scale = m.weight_scale;
             n.x_hat = x_hat;
             n.z = z;
@@ -448,24 +424,36 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         gu.expert[1] = expert_job(L->up, I, H, gu_words, xh_up, z_up);
         gu.expert_count = 2;
         gu.ne[0] = ne_job(L->shared_gate, sxh_gate, sz_gate);
-        gu.ne[1] = ne_job(L->shared_up, sxh_up, sz_up);
-        gu.ne_count = 2;
+        gu.ne_count = 1;
+        gu.expert_book = L->expert_codebook->data;
+        gu.slot_info = slot_info;
+        gu.ne_book = L->shared_gate.codebook->data;
         gu.max_active = max_active;
-        launch_moe_gemv(ctx, gu, batch == 1);
+        if (L->shared_up.codebook->data == L->shared_gate.codebook->data) {
+            gu.ne[1] = ne_job(L->shared_up, sxh_up, sz_up);
+            gu.ne_count = 2;
+            launch_trellis_gemv(ctx, gu);
+        } else {
+            launch_trellis_gemv(ctx, gu);
+            MoeGemv su{};
+            su.ne[0] = ne_job(L->shared_up, sxh_up, sz_up);
+            su.ne_count = 1;
+            su.ne_book = L->shared_up.codebook->data;
+            launch_trellis_gemv(ctx, su);
+        }
 
         // 5: SwiGLU and the down prologue
         const float scale_i = hadamard_scale(I);
         if (wave_path) {
             SwigluJobs sj{};
             sj.segments = 2;
-            sj.splits = sg;
             sj.scale = scale_i;
             sj.seg[0] = SwigluSegment{z_gate, z_up, P * I, L->gate.sv_f16, L->up.sv_f16,
                                       L->down.su_f16, nullptr, nullptr, nullptr, position_expert,
-                                      xh_down, static_cast<uint32_t>(P)};
+                                      xh_down, static_cast<uint32_t>(P), sg};
             sj.seg[1] = SwigluSegment{sz_gate, sz_up, B * I, nullptr, nullptr, nullptr,
                                       L->shared_gate.sv, L->shared_up.sv, L->shared_down.su,
-                                      nullptr, sxh_down, batch};
+                                      nullptr, sxh_down, batch, ssg};
             const dim3 grid(ceil_div(P + B, 4));
             switch (I) {
             case 64: launch(ctx, "swiglu", k_swiglu_wave<1>, grid, dim3(256), 0, sj); break;
@@ -483,7 +471,7 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
                    L->down.su_f16, I, static_cast<const uint32_t *>(position_expert), scale_i,
                    xh_down);
             launch(ctx, "swiglu", k_swiglu<int8_t>, dim3(batch), dim3(256), 2 * I * sizeof(float),
-                   static_cast<const float *>(sz_gate), static_cast<const float *>(sz_up), sg, B * I,
+                   static_cast<const float *>(sz_gate), static_cast<const float *>(sz_up), ssg, B * I,
                    I, L->shared_gate.sv, L->shared_up.sv, L->shared_down.su, 0u,
                    static_cast<const uint32_t *>(nullptr), scale_i, sxh_down);
         }
@@ -494,13 +482,16 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         dn.expert_count = 1;
         dn.ne[0] = ne_job(L->shared_down, sxh_down, sz_down);
         dn.ne_count = 1;
+        dn.expert_book = L->expert_codebook->data;
+        dn.slot_info = slot_info;
+        dn.ne_book = L->shared_down.codebook->data;
         dn.max_active = max_active;
-        launch_moe_gemv(ctx, dn, batch == 1);
+        launch_trellis_gemv(ctx, dn);
 
         // 7: combine
         if (wave_path) {
             CombineArgs c{z_down, sd, P * H, L->down.sv_f16, route_expert, route_weight,
-                          route_to_grouped, sz_down, sd, B * H, L->shared_down.sv, shared_logit,
+                          route_to_grouped, sz_down, ssd, B * H, L->shared_down.sv, shared_logit,
                           hadamard_scale(H), outputs};
             switch (H) {
             case 64: launch(ctx, "combine", k_combine_wave<1>, dim3(batch), dim3(576), 0, c); break;
@@ -517,7 +508,7 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
                    static_cast<const uint32_t *>(route_expert),
                    static_cast<const float *>(route_weight),
                    static_cast<const uint32_t *>(route_to_grouped),
-                   static_cast<const float *>(sz_down), sd, B * H, L->shared_down.sv,
+                   static_cast<const float *>(sz_down), ssd, B * H, L->shared_down.sv,
                    static_cast<const float *>(shared_logit), hadamard_scale(H), outputs);
         }
 

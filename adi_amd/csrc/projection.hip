@@ -4,19 +4,23 @@
 // ne_matvec/matmul.
 //
 // Data flow of one projection y = W x (src/kernels.cpp:385-800):
-//   prologue  x_hat = H_C(su * x)                 one block per vector, LDS
+//   prologue  x_hat = H_C(su * x)                 one wave per vector
 //   gemv      Z[r] = sum_tiles decoded(tile) . x_hat   codes read once, decoded
 //                                                  in registers
-//   epilogue  y = sv * H_R(sum_splits Z)           one block per vector, LDS
+//   epilogue  y = sv * H_R(sum_slices Z)           one wave per vector
 //
-// GEMV work split: a 256-thread block owns 64 consecutive tiles of a matrix
-// (tile-row-major order), a wave 16 of them, and each tile is shared by four
-// lanes that own four of its sixteen rows ("quads"). A lane loads its quad's
-// slice of the packed stream with one coalesced vector load, decodes the
-// states of its four rows in registers, and multiplies them with the x_hat
-// values of the tile column. Rows are summed over the tiles of a tile row
-// with wave shuffles and, across waves, through LDS. With more than 64 tile
-// columns each block writes its own partial (split); the epilogue adds them.
+// The decode-GEMV is persistent: one 512-thread block per CU. Random gathers
+// from a 256 KiB expert codebook in global memory run at under half a gather
+// per clock per CU, from LDS at seven, so each block holds one component
+// plane of the codebook (components 0-3 or 4-7 of every row, 128 KiB) in LDS
+// and computes that half of every tile column; half-0 and half-1 blocks walk
+// the same tiles. A wave item is up to 64 consecutive tiles of one tile row
+// (four groups of 16); four lanes share a tile and own four of its sixteen
+// rows ("quads"). A lane loads its quad's slice of the packed stream, decodes
+// the states of its rows against the LDS plane, multiplies them with x_hat,
+// and the wave sums its tiles with shuffles, so no block barrier follows the
+// codebook fill. Each (item column range, half) writes its own slice of Z;
+// the consumer adds the slices in a fixed order.
 #include "projection.hpp"
 
 namespace adi_hip {
@@ -43,15 +47,18 @@ __device__ __forceinline__ void load_expert_quad(const uint16_t *trellis, uint32
     d[3] = static_cast<uint32_t>(__shfl(static_cast<int>(d[0]), partner)) & 0xFFFFu;
 }
 
-// The eight decoded states of a quad, each as 8 f16 lattice values (one
-// reachable codebook row, component 0 negated by bit 15 of the state hash).
-__device__ __forceinline__ void decode_expert_quad(const uint32_t (&d)[4], const uint4 *book,
-                                                   uint4 (&e)[8]) {
+// The eight states of a quad against one component plane of the expert
+// codebook: 4 f16 lattice values per state (components 4h..4h+3 of one
+// reachable row; bit 15 of the state hash negates component 0, which lives in
+// plane 0).
+__device__ __forceinline__ void decode_expert_half(const uint32_t (&d)[4], const uint2 *plane,
+                                                   uint32_t half, uint2 (&e)[8]) {
+    const uint32_t sign_mask = half == 0 ? 0x8000u : 0u;
 #define ADI_EXPERT_STATE(K)                                            \
     {                                                                  \
         const uint32_t p = state_product(stream_window<12 * K>(d));    \
-        e[K] = book[(p >> 1) & 0x3FFFu];                               \
-        e[K].x ^= p & 0x8000u;                                         \
+        e[K] = plane[(p >> 1) & 0x3FFFu];                              \
+        e[K].x ^= p & sign_mask;                                       \
     }
     ADI_EXPERT_STATE(0) ADI_EXPERT_STATE(1) ADI_EXPERT_STATE(2) ADI_EXPERT_STATE(3)
     ADI_EXPERT_STATE(4) ADI_EXPERT_STATE(5) ADI_EXPERT_STATE(6) ADI_EXPERT_STATE(7)
@@ -105,8 +112,10 @@ __global__ __launch_bounds__(256) void k_expert_decode(const uint16_t *trellis, 
     const bool valid = tile < tiles;
     uint32_t d[4];
     load_expert_quad(trellis, tile, quad, valid, lane, d);
-    uint4 e[8];
-    decode_expert_quad(d, static_cast<const uint4 *>(codebook), e);
+    const uint2 *plane = static_cast<const uint2 *>(codebook);
+    uint2 lo[8], hi[8];
+    decode_expert_half(d, plane, 0, lo);
+    decode_expert_half(d, plane + kExpertRows, 1, hi);
     if (!valid) {
         return;
     }
@@ -114,7 +123,7 @@ __global__ __launch_bounds__(256) void k_expert_decode(const uint16_t *trellis, 
     for (int k = 0; k < 8; ++k) {
         const uint32_t row = tr * kTile + quad * 4u + k / 2;
         float *dst = out + static_cast<size_t>(row) * columns + tc * kTile + (k & 1) * 8;
-        const uint32_t w[4] = {e[k].x, e[k].y, e[k].z, e[k].w};
+        const uint32_t w[4] = {lo[k].x, lo[k].y, hi[k].x, hi[k].y};
         for (int c = 0; c < 4; ++c) {
             const float2 v = half2_bits_to_float2(w[c]);
             dst[2 * c] = v.x;
@@ -272,18 +281,8 @@ __global__ __launch_bounds__(256) void k_epilogue_wave(
         return;
     }
     const uint32_t n = 64u * VPL;
-    const float *src = z + static_cast<size_t>(v) * n + lane;
     float val[VPL];
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-        val[i] = src[i * 64];
-    }
-    for (uint32_t sp = 1; sp < splits; ++sp) {
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            val[i] += src[sp * split_stride + i * 64];
-        }
-    }
+    sum_slices<VPL>(z + static_cast<size_t>(v) * n, split_stride, splits, lane, val);
     wave_hadamard<VPL>(val, scale, lane);
     float *dst = out + static_cast<size_t>(v) * n + lane;
 #pragma unroll
@@ -328,260 +327,376 @@ __global__ __launch_bounds__(256) void k_hadamard_block(float *values, uint32_t 
 
 // ---- cross-tile row reduction shared by both GEMVs -----------------------
 
-// Sums a lane's four row values (per token) over the tiles of its tile row
-// and stores them to z. `g` = tiles of one tile row inside a wave
-// (min(C_t, 16)), `wpr` = waves covering one tile row (C_t / 16 clamped to
-// 1..4).
-template <int NT>
-__device__ __forceinline__ void reduce_rows_and_store(
-    float (&acc)[4][NT], uint32_t lane, uint32_t wave, uint32_t tile,
-    uint32_t tile_columns, uint32_t tiles, uint32_t rows, uint32_t tok0,
-    uint32_t tok_count, float *z, size_t z_split_stride, float *lds, uint32_t bx) {
-    const uint32_t slot = lane >> 2;
-    const uint32_t quad = lane & 3u;
-    const uint32_t g = tile_columns < 16 ? tile_columns : 16u;
+// ---- persistent decode-GEMV ------------------------------------------------
+
+constexpr uint32_t kGemvThreads = 512;
+constexpr uint32_t kGemvWaves = kGemvThreads / kWave;
+constexpr size_t kPlaneBytes = size_t(kExpertRows) * 8;  // one component plane
+constexpr uint32_t kMaxSlots = 1024;                     // routed slots staged in LDS
+
+// The loads of one expert wave item, issued one item ahead of its arithmetic
+// so that a wave's next item is in flight while the current one computes.
+struct ExpertStage {
+    uint4 info;         // {matrix, first position, end position, -}; empty when end == first
+    uint32_t d[4][3];   // the lane's three stream dwords in each group of 16 tiles
+    float gamma[4];
+    float4 x[4][2];     // x_hat of the first position: columns c0..c0+3, c0+8..c0+11
+};
+
+struct ExpertItem {
+    uint32_t which, slot, item;
+};
+
+// Item i of the expert phase: matrix entry, routed slot, item within the slot
+// (items per slot is a power of two, so no division).
+__device__ __forceinline__ ExpertItem expert_item_of(const MoeGemv &m, uint32_t i) {
+    const uint32_t per_matrix = m.max_active << m.item_shift;
+    const uint32_t which = i >= per_matrix ? 1u : 0u;
+    const uint32_t rest = i - which * per_matrix;
+    return {which, rest >> m.item_shift, rest & ((1u << m.item_shift) - 1u)};
+}
+
+__device__ __forceinline__ void load_x_pair(const float *x_hat, uint32_t columns, uint32_t position,
+                                            const uint32_t (&column)[4], uint32_t groups,
+                                            const bool (&valid)[4], float4 (&x)[4][2]) {
 #pragma unroll
-    for (uint32_t off = 1; off < 16; off <<= 1) {
-        if (off < g) {
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-#pragma unroll
-                for (int j = 0; j < NT; ++j) {
-                    acc[m][j] += __shfl_xor(acc[m][j], static_cast<int>(off * 4u));
-                }
-            }
-        }
-    }
-    const uint32_t wpr = tile_columns >= 64 ? 4u : (tile_columns >= 16 ? tile_columns / 16u : 1u);
-    if (wpr == 1) {
-        if ((slot % g) == 0 && tile < tiles) {
-            const uint32_t tr = tile / tile_columns;
-            const uint32_t split = (tile % tile_columns) / 64u;
-#pragma unroll
-            for (int j = 0; j < NT; ++j) {
-                if (static_cast<uint32_t>(j) < tok_count) {
-                    float *dst = z + split * z_split_stride +
-                                 static_cast<size_t>(tok0 + j) * rows + tr * kTile + quad * 4u;
-#pragma unroll
-                    for (int m = 0; m < 4; ++m) {
-                        dst[m] = acc[m][j];
-                    }
-                }
-            }
-        }
-        return;
-    }
-    // Several waves share a tile row: stage the per-wave sums in LDS.
-    __syncthreads();
-    if (slot == 0) {
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-#pragma unroll
-            for (int j = 0; j < NT; ++j) {
-                lds[(wave * 16u + quad * 4u + m) * NT + j] = acc[m][j];
-            }
-        }
-    }
-    __syncthreads();
-    const uint32_t tid = threadIdx.x;
-    const uint32_t groups = 4u / wpr;  // tile rows in this block
-    if (tid < groups * 16u * NT) {
-        const uint32_t j = tid % NT;
-        const uint32_t r = (tid / NT) % 16u;
-        const uint32_t group = tid / (16u * NT);
-        float sum = 0.0f;
-        for (uint32_t w = 0; w < wpr; ++w) {
-            sum += lds[((group * wpr + w) * 16u + r) * NT + j];
-        }
-        const uint32_t first_tile = bx * 64u + group * wpr * 16u;
-        if (first_tile < tiles && j < tok_count) {
-            const uint32_t tr = first_tile / tile_columns;
-            const uint32_t split = (first_tile % tile_columns) / 64u;
-            z[split * z_split_stride + static_cast<size_t>(tok0 + j) * rows + tr * kTile + r] = sum;
+    for (int g = 0; g < 4; ++g) {
+        x[g][0] = x[g][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (static_cast<uint32_t>(g) < groups && valid[g]) {
+            const float *src = x_hat + static_cast<size_t>(position) * columns + column[g];
+            x[g][0] = *reinterpret_cast<const float4 *>(src);
+            x[g][1] = *reinterpret_cast<const float4 *>(src + 8);
         }
     }
 }
 
-// ---- expert decode-GEMV ----------------------------------------------------
-
-// Four rows of one expert tile = 8 states = bits [96q, 96q + 112) of the
-// 384-bit stream: words 6q..6q+5 of the lane plus word 0 of the next quad.
-template <int NT>
-__device__ __forceinline__ void expert_gemv_block(const ExpertGemv &a, uint32_t bx, uint32_t by,
-                                                  float *lds) {
-    uint32_t mat = 0, tok_begin = 0, tok_end = a.batch;
-    if (a.active != nullptr) {
-        if (by >= *a.active_count) {
-            return;
-        }
-        mat = a.active[by];
-        tok_begin = a.offsets[mat];
-        tok_end = a.offsets[mat + 1];
-    }
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t quad = lane & 3u;
-    const uint32_t tile_columns = a.columns / kTile;
-    const uint32_t tile_rows = a.rows / kTile;
-    const uint32_t tiles = tile_rows * tile_columns;
-    const uint32_t tile = bx * 64u + wave * 16u + (lane >> 2);
-    const bool valid = tile < tiles;
-    const uint32_t tr = valid ? tile / tile_columns : 0u;
-    const uint32_t tc = valid ? tile % tile_columns : 0u;
-
-    uint32_t d[4];
-    load_expert_quad(a.trellis + mat * a.trellis_stride, tile, quad, valid, lane, d);
-
-    const float gamma = valid ? half_bits_to_float(a.gamma[mat * a.gamma_stride +
-                                                           wave_slot(tr, tc, tile_rows, tile_columns)])
-                              : 0.0f;
-    uint4 e[8];
-    decode_expert_quad(d, static_cast<const uint4 *>(a.codebook), e);
-
-    for (uint32_t t0 = tok_begin; t0 < tok_end; t0 += NT) {
-        const uint32_t count = tok_end - t0 < NT ? tok_end - t0 : NT;
-        float acc[4][NT];
+// Tiles [item*16S, item*16S + 16S) of the item's matrix, S = item_groups.
+__device__ __forceinline__ void expert_tiles(const ExpertGemv &a, uint32_t item, uint32_t half,
+                                             uint32_t lane, uint32_t (&column)[4],
+                                             bool (&valid)[4], uint32_t (&tile)[4]) {
+    const uint32_t tiles = a.tile_rows << a.tc_shift;
+    const uint32_t tc_mask = (1u << a.tc_shift) - 1u;
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            float x[16];
-            if (valid && static_cast<uint32_t>(j) < count) {
-                const float4 *src = reinterpret_cast<const float4 *>(
-                    a.x_hat + static_cast<size_t>(t0 + j) * a.columns + tc * kTile);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float4 v = src[q];
-                    x[4 * q] = v.x;
-                    x[4 * q + 1] = v.y;
-                    x[4 * q + 2] = v.z;
-                    x[4 * q + 3] = v.w;
-                }
-            } else {
-#pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    x[q] = 0.0f;
-                }
-            }
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                float partial = 0.0f;
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const uint4 v = e[2 * m + h];
-                    const uint32_t words[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        const float2 w = half2_bits_to_float2(words[c]);
-                        partial = fmaf(w.x, x[8 * h + 2 * c], partial);
-                        partial = fmaf(w.y, x[8 * h + 2 * c + 1], partial);
-                    }
-                }
-                acc[m][j] = partial * gamma;
-            }
-        }
-        reduce_rows_and_store<NT>(acc, lane, wave, tile, tile_columns, tiles, a.rows, t0, count,
-                                  a.z, a.z_split_stride, lds, bx);
+    for (int g = 0; g < 4; ++g) {
+        tile[g] = (item << (4u + a.group_shift)) + g * 16u + (lane >> 2);
+        valid[g] = (static_cast<uint32_t>(g) >> a.group_shift) == 0 && tile[g] < tiles;
+        column[g] = valid[g] ? ((tile[g] & tc_mask) << 4) + 4u * half : 0u;
     }
 }
 
-template <int NT>
-__global__ __launch_bounds__(256) void k_expert_gemv(ExpertGemv a) {
-    __shared__ float lds[4 * 16 * NT];
-    expert_gemv_block<NT>(a, blockIdx.x, blockIdx.y, lds);
+__device__ __forceinline__ void expert_prefetch(const MoeGemv &m, const uint4 *slots, uint32_t i,
+                                                uint32_t half, uint32_t lane, ExpertStage &st) {
+    const ExpertItem it = expert_item_of(m, i);
+    const ExpertGemv &a = m.expert[it.which];
+    const uint4 info = slots[it.slot];
+    st.info = make_uint4(__builtin_amdgcn_readfirstlane(info.x), __builtin_amdgcn_readfirstlane(info.y),
+                         __builtin_amdgcn_readfirstlane(info.z), 0u);
+    const uint32_t quad = lane & 3u;
+    const uint32_t tile_columns = 1u << a.tc_shift;
+    const uint32_t groups = 1u << a.group_shift;
+    const bool live = st.info.z > st.info.y;
+    uint32_t column[4], tile[4];
+    bool valid[4];
+    expert_tiles(a, it.item, half, lane, column, valid, tile);
+    const uint32_t *words = reinterpret_cast<const uint32_t *>(a.trellis + st.info.x * a.trellis_stride);
+    const uint16_t *gamma_row = a.gamma + st.info.x * a.gamma_stride;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        valid[g] = valid[g] && live;
+        st.d[g][0] = st.d[g][1] = st.d[g][2] = 0u;
+        st.gamma[g] = 0.0f;
+        if (valid[g]) {
+            const uint32_t *src = words + static_cast<size_t>(tile[g]) * 12u + quad * 3u;
+            st.d[g][0] = __builtin_nontemporal_load(src);
+            st.d[g][1] = __builtin_nontemporal_load(src + 1);
+            st.d[g][2] = __builtin_nontemporal_load(src + 2);
+            const uint32_t tr = tile[g] >> a.tc_shift, tc = tile[g] & (tile_columns - 1u);
+            st.gamma[g] = half_bits_to_float(gamma_row[wave_slot(tr, tc, a.tile_rows, tile_columns)]);
+        }
+    }
+    load_x_pair(a.x_hat, a.columns, st.info.y, column, groups, valid, st.x);
 }
 
-// ---- NE decode-GEMV --------------------------------------------------------
-
-// Four rows of one NE tile = 32 states = bytes [32q, 32q + 34) of the
-// 1024-bit stream: words 16q..16q+15 of the lane plus word 0 of the next
-// quad. The 1024-entry signed table, scaled by Wscale in fp32 as the
-// reference does per state (src/kernels.cpp:673-683), sits in LDS.
-template <int NT>
-__device__ __forceinline__ void ne_gemv_block(const NeGemv &a, uint32_t bx, float2 *table,
-                                              float *lds) {
-    const uint32_t *book = static_cast<const uint32_t *>(a.codebook);
-    for (uint32_t i = threadIdx.x; i < 1024u; i += blockDim.x) {
-        const float2 v = half2_bits_to_float2(book[i]);
-        table[i] = make_float2(v.x * a.weight_scale, v.y * a.weight_scale);
+__device__ __forceinline__ void expert_compute(const MoeGemv &m, uint32_t i, uint32_t half,
+                                               const uint2 *plane, uint32_t lane,
+                                               ExpertStage &st) {
+    if (st.info.z <= st.info.y) {
+        return;  // slot past the active count (wave-uniform)
     }
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t quad = lane & 3u;
-    const uint32_t tile_columns = a.columns / kTile;
-    const uint32_t tiles = (a.rows / kTile) * tile_columns;
-    const uint32_t tile = bx * 64u + wave * 16u + (lane >> 2);
-    const bool valid = tile < tiles;
-    const uint32_t tc = valid ? tile % tile_columns : 0u;
+    const ExpertItem it = expert_item_of(m, i);
+    const ExpertGemv &a = m.expert[it.which];
+    const uint32_t quad = lane & 3u, tslot = lane >> 2;
+    const uint32_t tile_columns = 1u << a.tc_shift;
+    const uint32_t groups = 1u << a.group_shift;
+    uint32_t column[4], tile[4];
+    bool valid[4];
+    expert_tiles(a, it.item, half, lane, column, valid, tile);
+    // the states of the lane's rows: its 3 dwords plus word 0 of the next quad
+    // (quad 3 wraps to word 0 of the tile, src/expert_trellis.hpp:79-80)
+    uint32_t next_word[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        next_word[g] = quad_next(st.d[g][0]) & 0xFFFFu;
+    }
+    const uint32_t span = tile_columns < 16u ? tile_columns : 16u;  // tiles of one row in a group
+    const uint32_t tile0 = tile[0];
+    const uint32_t split = ((tile0 & (tile_columns - 1u)) >> (4u + a.group_shift)) * 2u + half;
+    const uint32_t tr = tile0 >> a.tc_shift;
+    const bool writer = (tslot % span) == 0 && valid[0];
+    float4 (&x)[4][2] = st.x;  // the first position's, then reloaded per position
+    for (uint32_t position = st.info.y; position < st.info.z; ++position) {
+        // keeps the codebook gathers of every group inside the loop (hoisted,
+        // the decoded states of all groups would stay live at once)
+        asm volatile("" ::: "memory");
+        if (position != st.info.y) {
+            load_x_pair(a.x_hat, a.columns, position, column, groups, valid, x);
+        }
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            if (static_cast<uint32_t>(g) >= groups) {
+                continue;
+            }
+            // decoded per group (and per position) to bound register use
+            const uint32_t d[4] = {st.d[g][0], st.d[g][1], st.d[g][2], next_word[g]};
+            uint2 e[8];
+            decode_expert_half(d, plane, half, e);
+            // row r: state 2r covers columns c0..c0+3, state 2r+1 c0+8..c0+11;
+            // the four rows' chains are interleaved so they hide each other's latency
+            const float xs[8] = {x[g][0].x, x[g][0].y, x[g][0].z, x[g][0].w,
+                                 x[g][1].x, x[g][1].y, x[g][1].z, x[g][1].w};
+            float partial[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint2 v = e[2 * r + (c >> 2)];
+                    const float2 w = half2_bits_to_float2((c & 2) ? v.y : v.x);
+                    partial[r] = fmaf((c & 1) ? w.y : w.x, xs[c], partial[r]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                acc[r] = fmaf(partial[r], st.gamma[g], acc[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            acc[r] = sum_over_quads(acc[r], span);
+        }
+        if (writer) {
+            float *dst = a.z + split * a.z_split_stride + static_cast<size_t>(position) * a.rows +
+                         tr * kTile + quad * 4u;
+            *reinterpret_cast<float4 *>(dst) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        }
+    }
+}
 
-    uint32_t d[9];
-    load_ne_quad(a.trellis, tile, quad, valid, lane, d);
-    __syncthreads();
+// The loads of one NE wave item (16 consecutive tiles of one matrix, all 16
+// columns of each tile), issued one item ahead.
+struct NeStage {
+    uint32_t d[8];   // the lane's 8 stream dwords
+    float x[16];     // x_hat of position 0 over the tile's columns
+};
+
+__device__ __forceinline__ void ne_tile(const NeGemv &a, uint32_t item, uint32_t lane,
+                                        uint32_t &tile, bool &valid, uint32_t &column) {
+    tile = item * 16u + (lane >> 2);
+    valid = tile < (a.tile_rows << a.tc_shift);
+    column = valid ? (tile & ((1u << a.tc_shift) - 1u)) << 4 : 0u;
+}
+
+// NE item k of a launch: matrix entry and item within it.
+__device__ __forceinline__ uint2 ne_item_of(const MoeGemv &m, uint32_t k) {
+    const uint32_t which = k >= m.ne_items_per_matrix ? 1u : 0u;
+    return make_uint2(which, k - which * m.ne_items_per_matrix);
+}
+
+__device__ __forceinline__ void load_x16(const float *x_hat, uint32_t columns, uint32_t position,
+                                         uint32_t column, bool valid, float (&x)[16]) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        x[q] = 0.0f;
+    }
+    if (valid) {
+        const float4 *src =
+            reinterpret_cast<const float4 *>(x_hat + static_cast<size_t>(position) * columns + column);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 v = src[q];
+            x[4 * q] = v.x;
+            x[4 * q + 1] = v.y;
+            x[4 * q + 2] = v.z;
+            x[4 * q + 3] = v.w;
+        }
+    }
+}
+
+__device__ __forceinline__ void ne_prefetch(const MoeGemv &m, uint32_t k, uint32_t lane,
+                                            NeStage &st) {
+    const uint2 it = ne_item_of(m, k);
+    const NeGemv &a = m.ne[it.x];
+    uint32_t tile, column;
+    bool valid;
+    ne_tile(a, it.y, lane, tile, valid, column);
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
+    if (valid) {
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(a.trellis) +
+                           static_cast<size_t>(tile) * 8u + (lane & 3u) * 2u;
+        lo = __builtin_nontemporal_load(src);
+        hi = __builtin_nontemporal_load(src + 1);
+    }
+    st.d[0] = lo.x; st.d[1] = lo.y; st.d[2] = lo.z; st.d[3] = lo.w;
+    st.d[4] = hi.x; st.d[5] = hi.y; st.d[6] = hi.z; st.d[7] = hi.w;
+    load_x16(a.x_hat, a.columns, 0, column, valid && a.batch > 0, st.x);
+}
+
+// Row sums over all 16 columns of each tile with the signed table in LDS,
+// scaled by Wscale once after the tile sums.
+__device__ __forceinline__ void ne_compute(const MoeGemv &m, uint32_t k, const uint32_t *table,
+                                           uint32_t lane, NeStage &st) {
+    const uint2 it = ne_item_of(m, k);
+    const NeGemv &a = m.ne[it.x];
+    const uint32_t quad = lane & 3u, tslot = lane >> 2;
+    const uint32_t tile_columns = 1u << a.tc_shift;
+    uint32_t tile, column;
+    bool valid;
+    ne_tile(a, it.y, lane, tile, valid, column);
+    // word 0 of the next quad (quad 3 wraps, src/ne_trellis.hpp:196-200)
+    const uint32_t d[9] = {st.d[0], st.d[1], st.d[2], st.d[3], st.d[4], st.d[5], st.d[6], st.d[7],
+                           quad_next(st.d[0]) & 0xFFFFu};
     uint32_t idx[32];
     decode_ne_quad(d, idx);
-
-    for (uint32_t t0 = 0; t0 < a.batch; t0 += NT) {
-        const uint32_t count = a.batch - t0 < NT ? a.batch - t0 : NT;
-        float acc[4][NT];
+    const uint32_t span = tile_columns < 16u ? tile_columns : 16u;
+    const uint32_t split = (tile & (tile_columns - 1u)) >> 4;
+    const uint32_t tr = tile >> a.tc_shift;
+    const bool writer = (tslot % span) == 0 && valid;
+    float (&x)[16] = st.x;  // position 0's, then reloaded per position
+    for (uint32_t position = 0; position < a.batch; ++position) {
+        if (position != 0) {
+            load_x16(a.x_hat, a.columns, position, column, valid, x);
+        }
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            float x[16];
-            if (valid && static_cast<uint32_t>(j) < count) {
-                const float4 *src = reinterpret_cast<const float4 *>(
-                    a.x_hat + static_cast<size_t>(t0 + j) * a.columns + tc * kTile);
+        for (int s = 0; s < 8; ++s) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float4 v = src[q];
-                    x[4 * q] = v.x;
-                    x[4 * q + 1] = v.y;
-                    x[4 * q + 2] = v.z;
-                    x[4 * q + 3] = v.w;
-                }
-            } else {
-#pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    x[q] = 0.0f;
-                }
-            }
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                float sum = 0.0f;
-#pragma unroll
-                for (int st = 0; st < 8; ++st) {
-                    const float2 w = table[idx[8 * m + st]];
-                    sum = fmaf(w.x, x[2 * st], sum);
-                    sum = fmaf(w.y, x[2 * st + 1], sum);
-                }
-                acc[m][j] = sum;
+            for (int r = 0; r < 4; ++r) {
+                const float2 w = half2_bits_to_float2(table[idx[8 * r + s]]);
+                acc[r] = fmaf(w.x, x[2 * s], acc[r]);
+                acc[r] = fmaf(w.y, x[2 * s + 1], acc[r]);
             }
         }
-        reduce_rows_and_store<NT>(acc, lane, wave, tile, tile_columns, tiles, a.rows, t0, count,
-                                  a.z, a.z_split_stride, lds, bx);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            acc[r] = sum_over_quads(acc[r], span);
+        }
+        if (writer) {
+            float *dst = a.z + split * a.z_split_stride + static_cast<size_t>(position) * a.rows +
+                         tr * kTile + quad * 4u;
+            *reinterpret_cast<float4 *>(dst) =
+                make_float4(acc[0] * a.weight_scale, acc[1] * a.weight_scale,
+                            acc[2] * a.weight_scale, acc[3] * a.weight_scale);
+        }
     }
 }
 
-template <int NT>
-__global__ __launch_bounds__(256) void k_ne_gemv(NeGemv a) {
-    __shared__ float2 table[1024];
-    __shared__ float lds[4 * 16 * NT];
-    ne_gemv_block<NT>(a, blockIdx.x, table, lds);
-}
-
-// Several expert and NE GEMVs in one launch (the MoE gate/up pair plus the
-// shared expert's, or the down projections): blocks are numbered expert
-// matrices first (max_active slots each), then NE matrices.
-template <int NT>
-__global__ __launch_bounds__(256) void k_moe_gemv(MoeGemv m) {
-    __shared__ float2 table[1024];
-    __shared__ float lds[4 * 16 * NT];
-    uint32_t b = blockIdx.x;
-    const uint32_t per_expert = m.expert_blocks * m.max_active;
-    if (b < m.expert_count * per_expert) {
-        const uint32_t which = b / per_expert;
-        const uint32_t rest = b % per_expert;
-        expert_gemv_block<NT>(m.expert[which], rest % m.expert_blocks, rest / m.expert_blocks, lds);
-        return;
+// Block b serves component plane (b / 8) % 2 as worker ((b / 16) * 8 + b % 8),
+// so the two blocks that walk the same tiles sit on the same XCD (blocks are
+// dealt to the eight XCDs round robin) and share its L2. Each wave walks its
+// expert items, then its share of the NE items, with the loads of item k+1
+// issued before the arithmetic of item k.
+__global__ __launch_bounds__(kGemvThreads) void k_trellis_gemv(MoeGemv m) {
+    extern __shared__ uint4 lds_dynamic[];  // [slot_capacity] slots, then the plane
+    __shared__ uint32_t ne_table[1024];
+    uint4 *slots = lds_dynamic;
+    uint4 *plane_lds = lds_dynamic + m.slot_capacity;
+    const uint32_t b = blockIdx.x;
+    const uint32_t half = (b >> 3) & 1u;
+    const uint32_t worker = ((b >> 4) << 3) | (b & 7u);
+    const uint32_t workers = gridDim.x >> 1;
+    if (m.expert_count > 0) {
+        // 8192 16-byte rows per plane, 16 per thread, all loads issued first
+        constexpr uint32_t kPer = static_cast<uint32_t>(kPlaneBytes / 16) / kGemvThreads;
+        const uint4 *src = static_cast<const uint4 *>(m.expert_book) + half * (kPlaneBytes / 16);
+        uint4 v[kPer];
+#pragma unroll
+        for (uint32_t u = 0; u < kPer; ++u) {
+            v[u] = src[u * kGemvThreads + threadIdx.x];
+        }
+        for (uint32_t s = threadIdx.x; s < m.max_active; s += kGemvThreads) {
+            slots[s] = m.slot_info != nullptr
+                           ? m.slot_info[s]
+                           : make_uint4(0u, 0u, s == 0 ? m.expert[0].batch : 0u, 0u);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kPer; ++u) {
+            plane_lds[u * kGemvThreads + threadIdx.x] = v[u];
+        }
     }
-    b -= m.expert_count * per_expert;
-    ne_gemv_block<NT>(m.ne[b / m.ne_blocks], b % m.ne_blocks, table, lds);
+    if (m.ne_count > 0) {
+        const uint32_t *src = static_cast<const uint32_t *>(m.ne_book);
+        for (uint32_t i = threadIdx.x; i < 1024u; i += kGemvThreads) {
+            ne_table[i] = src[i];
+        }
+    }
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t stride = workers * kGemvWaves;
+    const uint2 *plane = reinterpret_cast<const uint2 *>(plane_lds);
+    // the wave index is uniform: in scalar registers, the item bookkeeping and
+    // every branch on it stay scalar
+    uint32_t i = worker * kGemvWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (i < m.expert_items) {
+        ExpertStage s0, s1;
+        expert_prefetch(m, slots, i, half, lane, s0);
+        while (true) {
+            uint32_t j = i + stride;
+            if (j < m.expert_items) {
+                expert_prefetch(m, slots, j, half, lane, s1);
+            }
+            expert_compute(m, i, half, plane, lane, s0);
+            i = j;
+            if (i >= m.expert_items) {
+                break;
+            }
+            j = i + stride;
+            if (j < m.expert_items) {
+                expert_prefetch(m, slots, j, half, lane, s0);
+            }
+            expert_compute(m, i, half, plane, lane, s1);
+            i = j;
+            if (i >= m.expert_items) {
+                break;
+            }
+        }
+    }
+    // NE items: index k = (i - expert_items) * 2 + half
+    const uint32_t end = m.half_items[half];
+    if (i < end) {
+        NeStage s0, s1;
+        ne_prefetch(m, (i - m.expert_items) * 2u + half, lane, s0);
+        while (true) {
+            uint32_t j = i + stride;
+            if (j < end) {
+                ne_prefetch(m, (j - m.expert_items) * 2u + half, lane, s1);
+            }
+            ne_compute(m, (i - m.expert_items) * 2u + half, ne_table, lane, s0);
+            i = j;
+            if (i >= end) {
+                break;
+            }
+            j = i + stride;
+            if (j < end) {
+                ne_prefetch(m, (j - m.expert_items) * 2u + half, lane, s0);
+            }
+            ne_compute(m, (i - m.expert_items) * 2u + half, ne_table, lane, s1);
+            i = j;
+            if (i >= end) {
+                break;
+            }
+        }
+    }
 }
 
 }  // namespace
@@ -674,34 +789,61 @@ void launch_epilogue_sign(adi_hip_context *ctx, const float *z, uint32_t splits,
            static_cast<const uint32_t *>(nullptr), hadamard_scale(n), out);
 }
 
-void launch_expert_gemv(adi_hip_context *ctx, const ExpertGemv &args) {
-    const uint32_t tiles = (args.rows / kTile) * (args.columns / kTile);
-    const dim3 grid(ceil_div(tiles, 64), args.active != nullptr ? args.max_active : 1u);
-    if (args.tokens_per_pass == 1) {
-        launch(ctx, "expert_gemv", k_expert_gemv<1>, grid, dim3(256), 0, args);
+void launch_trellis_gemv(adi_hip_context *ctx, MoeGemv &m) {
+    require(m.expert_count <= 2 && m.ne_count <= 2, "trellis GEMV: too many matrices");
+    require(m.expert_count == 0 || m.expert_book != nullptr, "trellis GEMV: expert codebook missing");
+    require(m.ne_count == 0 || m.ne_book != nullptr, "trellis GEMV: NE codebook missing");
+    if (m.expert_count > 0) {
+        const ExpertGemv &e = m.expert[0];
+        require(m.max_active >= 1 && m.max_active <= kMaxSlots, "trellis GEMV: routed slots out of range");
+        require(m.slot_info != nullptr || m.max_active == 1, "trellis GEMV: routed slots need a slot table");
+        const uint32_t tiles = (e.rows / kTile) * (e.columns / kTile);
+        m.expert_items_per_slot = ceil_div(tiles, 16u * item_groups(e.columns / kTile));
+        m.item_shift = log2_of(m.expert_items_per_slot);
+        for (uint32_t i = 0; i < m.expert_count; ++i) {
+            ExpertGemv &x = m.expert[i];
+            require(x.rows == e.rows && x.columns == e.columns,
+                    "trellis GEMV: expert entries differ in shape");
+            x.tile_rows = x.rows / kTile;
+            x.tc_shift = log2_of(x.columns / kTile);
+            x.group_shift = log2_of(item_groups(x.columns / kTile));
+        }
+        m.slot_capacity = m.max_active;
     } else {
-        launch(ctx, "expert_gemv", k_expert_gemv<4>, grid, dim3(256), 0, args);
+        m.expert_items_per_slot = 0;
+        m.slot_capacity = 0;
     }
-}
-
-void launch_moe_gemv(adi_hip_context *ctx, MoeGemv &m, bool single_token) {
-    m.expert_blocks = ceil_div((m.expert[0].rows / kTile) * (m.expert[0].columns / kTile), 64);
-    m.ne_blocks = ceil_div((m.ne[0].rows / kTile) * (m.ne[0].columns / kTile), 64);
-    const uint32_t blocks = m.expert_count * m.expert_blocks * m.max_active + m.ne_count * m.ne_blocks;
-    if (single_token) {
-        launch(ctx, "moe_gemv", k_moe_gemv<1>, dim3(blocks), dim3(256), 0, m);
+    m.expert_items = m.expert_count * m.max_active * m.expert_items_per_slot;
+    if (m.ne_count > 0) {
+        const NeGemv &n = m.ne[0];
+        const uint32_t tiles = (n.rows / kTile) * (n.columns / kTile);
+        m.ne_items_per_matrix = ceil_div(tiles, 16u);
+        for (uint32_t i = 0; i < m.ne_count; ++i) {
+            NeGemv &x = m.ne[i];
+            require(x.rows == n.rows && x.columns == n.columns,
+                    "trellis GEMV: NE entries differ in shape");
+            x.tile_rows = x.rows / kTile;
+            x.tc_shift = log2_of(x.columns / kTile);
+        }
     } else {
-        launch(ctx, "moe_gemv", k_moe_gemv<4>, dim3(blocks), dim3(256), 0, m);
+        m.ne_items_per_matrix = 0;
     }
-}
-
-void launch_ne_gemv(adi_hip_context *ctx, const NeGemv &args) {
-    const uint32_t tiles = (args.rows / kTile) * (args.columns / kTile);
-    if (args.batch == 1) {
-        launch(ctx, "ne_gemv", k_ne_gemv<1>, dim3(ceil_div(tiles, 64)), dim3(256), 0, args);
-    } else {
-        launch(ctx, "ne_gemv", k_ne_gemv<4>, dim3(ceil_div(tiles, 64)), dim3(256), 0, args);
+    m.ne_items = m.ne_count * m.ne_items_per_matrix;
+    m.half_items[0] = m.expert_items + (m.ne_items + 1) / 2;
+    m.half_items[1] = m.expert_items + m.ne_items / 2;
+    if (m.half_items[0] == 0) {
+        return;
     }
+    // persistent grid: at most one block per CU, a multiple of 16 blocks
+    const uint32_t needed_workers = ceil_div(m.half_items[0], kGemvWaves);
+    uint32_t blocks = 16u * ceil_div(needed_workers, 8);
+    const uint32_t cap = ctx->cu_count >= 16 ? ctx->cu_count / 16 * 16 : 16u;
+    blocks = blocks < cap ? blocks : cap;
+    const size_t lds = size_t(m.slot_capacity) * 16 + (m.expert_count > 0 ? kPlaneBytes : 0);
+    static const bool ready = set_lds_limit(reinterpret_cast<const void *>(&k_trellis_gemv),
+                                            kPlaneBytes + size_t(kMaxSlots) * 16);
+    (void)ready;
+    launch(ctx, "moe_gemv", k_trellis_gemv, dim3(blocks), dim3(kGemvThreads), lds, m);
 }
 
 template void launch_epilogue_any<uint16_t>(adi_hip_context *, const float *, uint32_t, size_t,
@@ -748,7 +890,7 @@ int adi_hip_expert_matmul(adi_hip_context *ctx, const adi_hip_expert_matrix *m,
         validate_expert(m);
         require(batch > 0, "Mach expert batch shape mismatch");
         require(inputs != nullptr && outputs != nullptr, "Mach expert vector is null");
-        const uint32_t splits = gemv_splits(m->columns);
+        const uint32_t splits = expert_splits(m->columns);
         auto &ws = ctx->workspace;
         ws.used = 0;
         ws.ensure(Workspace::round(size_t(batch) * m->columns * 4) +
@@ -760,18 +902,20 @@ int adi_hip_expert_matmul(adi_hip_context *ctx, const adi_hip_expert_matrix *m,
         jobs.n = m->columns;
         jobs.seg[0] = PrologueSegment{inputs, nullptr, nullptr, m->su_f16, nullptr, 0, x_hat, batch};
         launch_prologues(ctx, jobs);
-        ExpertGemv g{};
-        g.trellis = m->trellis;
-        g.gamma = m->wave_gamma_f16;
-        g.codebook = m->codebook->data;
-        g.rows = m->rows;
-        g.columns = m->columns;
-        g.x_hat = x_hat;
-        g.z = z;
-        g.z_split_stride = size_t(batch) * m->rows;
-        g.batch = batch;
-        g.tokens_per_pass = batch == 1 ? 1 : 4;
-        launch_expert_gemv(ctx, g);
+        MoeGemv g{};
+        ExpertGemv &e = g.expert[0];
+        e.trellis = m->trellis;
+        e.gamma = m->wave_gamma_f16;
+        e.rows = m->rows;
+        e.columns = m->columns;
+        e.x_hat = x_hat;
+        e.z = z;
+        e.z_split_stride = size_t(batch) * m->rows;
+        e.batch = batch;
+        g.expert_count = 1;
+        g.expert_book = m->codebook->data;
+        g.max_active = 1;
+        launch_trellis_gemv(ctx, g);
         launch_epilogue_any<uint16_t>(ctx, z, splits, size_t(batch) * m->rows, m->rows, m->sv_f16,
                                       batch, outputs);
     });
@@ -788,7 +932,7 @@ int adi_hip_ne_matmul(adi_hip_context *ctx, const adi_hip_ne_matrix *m,
         validate_ne(m);
         require(batch > 0, "Mach NE batch shape mismatch");
         require(inputs != nullptr && outputs != nullptr, "Mach NE vector is null");
-        const uint32_t splits = gemv_splits(m->columns);
+        const uint32_t splits = ne_splits(m->columns);
         auto &ws = ctx->workspace;
         ws.used = 0;
         ws.ensure(Workspace::round(size_t(batch) * m->columns * 4) +
@@ -800,17 +944,19 @@ int adi_hip_ne_matmul(adi_hip_context *ctx, const adi_hip_ne_matrix *m,
         jobs.n = m->columns;
         jobs.seg[0] = PrologueSegment{inputs, nullptr, nullptr, nullptr, m->su, 0, x_hat, batch};
         launch_prologues(ctx, jobs);
-        NeGemv g{};
-        g.trellis = m->trellis;
-        g.codebook = m->codebook->data;
-        g.weight_scale = m->weight_scale;
-        g.rows = m->rows;
-        g.columns = m->columns;
-        g.x_hat = x_hat;
-        g.z = z;
-        g.z_split_stride = size_t(batch) * m->rows;
-        g.batch = batch;
-        launch_ne_gemv(ctx, g);
+        MoeGemv g{};
+        NeGemv &n = g.ne[0];
+        n.trellis = m->trellis;
+        n.weight_scale = m->weight_scale;
+        n.rows = m->rows;
+        n.columns = m->columns;
+        n.x_hat = x_hat;
+        n.z = z;
+        n.z_split_stride = size_t(batch) * m->rows;
+        n.batch = batch;
+        g.ne_count = 1;
+        g.ne_book = m->codebook->data;
+        launch_trellis_gemv(ctx, g);
         launch_epilogue_any<int8_t>(ctx, z, splits, size_t(batch) * m->rows, m->rows, m->sv, batch,
                                     outputs);
     });

@@ -52,60 +52,80 @@ void launch_epilogue_sign(adi_hip_context *ctx, const float *z, uint32_t splits,
                           size_t split_stride, uint32_t n, const int8_t *sv,
                           uint32_t vectors, float *out);
 
-// Number of partial-sum splits the GEMV kernels write for `columns` inputs.
-inline uint32_t gemv_splits(uint32_t columns) {
-    const uint32_t tile_columns = columns / kTile;
-    return tile_columns > 64 ? tile_columns / 64 : 1;
+// Groups of 16 tiles in one GEMV wave item (all in one tile row when the
+// matrix has at least 16 tile columns).
+__host__ __device__ inline uint32_t item_groups(uint32_t tile_columns) {
+    return tile_columns >= 64 ? 4u : (tile_columns >= 32 ? 2u : 1u);
+}
+// Column ranges a tile row is cut into by the wave items.
+__host__ __device__ inline uint32_t item_segments(uint32_t tile_columns) {
+    const uint32_t span = 16u * item_groups(tile_columns);
+    return tile_columns >= span ? tile_columns / span : 1u;
+}
+// Partial-sum slices of Z the GEMV writes for a matrix with `columns` inputs:
+// one per (column range, codebook plane) for the expert codec, one per range
+// of 16 tile columns for the NE codec. Slice s of position p, row r is at
+// z[s * split_stride + p * rows + r].
+inline uint32_t expert_splits(uint32_t columns) { return 2u * item_segments(columns / kTile); }
+inline uint32_t ne_splits(uint32_t columns) {
+    return columns / kTile > 16u ? columns / kTile / 16u : 1u;  // NE items are 16 tiles
 }
 
-// Expert decode-GEMV over one matrix or over the active experts of a routed
-// batch. Writes pre-Hadamard row sums z[split][position][rows].
+// An expert matrix for the GEMV: one matrix (positions [0, batch)), or the
+// routed experts of a batch, whose slots come from the MoeGemv slot table
+// (matrix e at e * trellis_stride words / e * gamma_stride).
 struct ExpertGemv {
-    const uint16_t *trellis;   // matrix 0; matrix e at e * trellis_stride words
+    const uint16_t *trellis;
     size_t trellis_stride;
-    const uint16_t *gamma;     // f16; matrix e at e * gamma_stride
+    const uint16_t *gamma;         // f16 wave gammas
     uint32_t gamma_stride;
-    const void *codebook;      // expert codebook (u16[16384][8])
     uint32_t rows;
     uint32_t columns;
-    const float *x_hat;        // [positions][columns]
-    float *z;                  // [splits][positions][rows]
-    size_t z_split_stride;     // positions * rows
-    const uint32_t *active;        // null: one matrix, tokens [0, batch)
-    const uint32_t *active_count;  // device scalar
-    const uint32_t *offsets;       // token range of matrix e: [offsets[e], offsets[e+1])
-    uint32_t batch;
-    uint32_t max_active;           // grid.y when routed
-    uint32_t tokens_per_pass;      // 1 or 4
+    const float *x_hat;            // [positions][columns]
+    float *z;                      // [expert_splits][positions][rows]
+    size_t z_split_stride;         // positions * rows
+    uint32_t batch;                // positions of a single matrix
+    // geometry, set by the launcher
+    uint32_t tile_rows;
+    uint32_t tc_shift;             // log2(tile columns)
+    uint32_t group_shift;          // log2(groups of 16 tiles per item)
 };
-void launch_expert_gemv(adi_hip_context *ctx, const ExpertGemv &args);
 
 struct NeGemv {
     const uint16_t *trellis;
-    const void *codebook;   // NE signed table (u16[1024][2])
     float weight_scale;
     uint32_t rows;
     uint32_t columns;
     const float *x_hat;     // [batch][columns]
-    float *z;               // [splits][batch][rows]
+    float *z;               // [ne_splits][batch][rows]
     size_t z_split_stride;  // batch * rows
     uint32_t batch;
+    // geometry, set by the launcher
+    uint32_t tile_rows;
+    uint32_t tc_shift;      // log2(tile columns)
 };
-void launch_ne_gemv(adi_hip_context *ctx, const NeGemv &args);
 
-// Up to two expert GEMVs (routed over the same active list) and two NE GEMVs
-// in one launch. The expert entries must share shape and routing; so must
-// the NE entries.
+// Up to two expert GEMVs (same shape and routing, one codebook) and two NE
+// GEMVs (same shape, one codebook) in one persistent launch.
 struct MoeGemv {
     ExpertGemv expert[2];
     uint32_t expert_count;
     NeGemv ne[2];
     uint32_t ne_count;
-    uint32_t max_active;
-    uint32_t expert_blocks;  // set by the launcher
-    uint32_t ne_blocks;      // set by the launcher
+    const void *expert_book;  // expert codebook planes
+    const void *ne_book;      // NE signed table
+    const uint4 *slot_info;   // [max_active] {expert, first, end, 0}; null: one matrix
+    uint32_t max_active;      // routed slots per expert entry (1 for a single matrix)
+    // set by the launcher
+    uint32_t slot_capacity;
+    uint32_t expert_items_per_slot;  // a power of two
+    uint32_t item_shift;             // its log2
+    uint32_t expert_items;
+    uint32_t ne_items_per_matrix;
+    uint32_t ne_items;
+    uint32_t half_items[2];
 };
-void launch_moe_gemv(adi_hip_context *ctx, MoeGemv &m, bool single_token);
+void launch_trellis_gemv(adi_hip_context *ctx, MoeGemv &m);
 
 void validate_expert(const adi_hip_expert_matrix *m);
 void validate_ne(const adi_hip_ne_matrix *m);
