@@ -1,0 +1,423 @@
+// hip_backend.cpp -- adi::Backend over the adi_hip C ABI.
+//
+// Each entry checks its arguments exactly as the reference entry it replaces
+// (same conditions, same std::invalid_argument messages: src/kernels.cpp:385-
+// 1073), finds or creates the device copy of the weights, copies the host
+// span in, launches, and copies the result out. Weights are views into the
+// model file (include/adi/kernels.hpp:9-77) and never change while mapped, so
+// their device copies are cached by host address, as ExpertScratch caches the
+// derived tables (src/kernels.cpp:33-94); a sampled fingerprint of the
+// contents is part of the key, so a buffer freed and reused at the same
+// address is uploaded again. Calls are serialised on one context:
+// moe_forward calls the projections from worker threads
+// (src/executor.cpp:261, 1321-1371), and the GPU runs them in turn anyway.
+#include "hip_backend.hpp"
+
+#include "adi_hip.h"
+
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <tuple>
+#include <utility>
+
+namespace adi {
+namespace {
+
+bool is_power_of_two(std::uint32_t v) { return v != 0 && (v & (v - 1)) == 0; }
+constexpr std::uint32_t kTile = 16;
+
+// FNV-1a over the size and 64 evenly spaced 8-byte samples of a buffer.
+template <typename T>
+std::uint64_t fingerprint(std::span<const T> values) {
+    const auto *bytes = reinterpret_cast<const unsigned char *>(values.data());
+    const std::size_t size = values.size_bytes();
+    std::uint64_t h = 1469598103934665603ull ^ size;
+    if (size == 0) {
+        return h;
+    }
+    for (std::size_t i = 0; i < 64; ++i) {
+        const std::size_t at = size <= 8 ? 0 : (size - 8) * i / 63;
+        for (std::size_t b = 0; b < 8 && at + b < size; ++b) {
+            h = (h ^ bytes[at + b]) * 1099511628211ull;
+        }
+    }
+    return h;
+}
+
+class Runtime {
+  public:
+    static Runtime &get() {
+        // never destroyed: device memory stays valid until the process ends
+        static Runtime *runtime = new Runtime();
+        return *runtime;
+    }
+
+    std::mutex mutex;
+    adi_hip_context *ctx = nullptr;
+
+    void check(int status) const {
+        if (status == ADI_HIP_OK) {
+            return;
+        }
+        const std::string message = adi_hip_last_error(ctx);
+        if (status == ADI_HIP_INVALID_ARGUMENT) {
+            throw std::invalid_argument(message);
+        }
+        throw std::runtime_error("adi_hip: " + message);
+    }
+
+    template <typename T>
+    const T *upload(std::span<const T> host) {
+        void *device = nullptr;
+        check(adi_hip_device_alloc(ctx, host.size_bytes(), &device));
+        check(adi_hip_copy_to_device(ctx, device, host.data(), host.size_bytes()));
+        return static_cast<const T *>(device);
+    }
+
+    // Grow-only staging buffers for the activations of one call.
+    float *staging(int which, std::size_t count) {
+        Buffer &b = buffers_[which];
+        if (b.bytes < count * sizeof(float)) {
+            adi_hip_device_free(ctx, b.pointer);
+            b.pointer = nullptr;
+            b.bytes = 0;
+            check(adi_hip_device_alloc(ctx, count * sizeof(float), &b.pointer));
+            b.bytes = count * sizeof(float);
+        }
+        return static_cast<float *>(b.pointer);
+    }
+
+    void to_device(float *device, std::span<const float> host) {
+        check(adi_hip_copy_to_device(ctx, device, host.data(), host.size_bytes()));
+    }
+    void to_host(std::span<float> host, const float *device) {
+        check(adi_hip_copy_to_host(ctx, host.data(), device, host.size_bytes()));
+    }
+
+    const adi_hip_codebook *expert_book(std::span<const float> tlut) {
+        auto &slot = expert_books_[{tlut.data(), fingerprint(tlut)}];
+        if (slot == nullptr) {
+            check(adi_hip_codebook_create_expert(ctx, tlut.data(), &slot));
+        }
+        return slot;
+    }
+    const adi_hip_codebook *ne_book(std::span<const float> tlut) {
+        auto &slot = ne_books_[{tlut.data(), fingerprint(tlut)}];
+        if (slot == nullptr) {
+            check(adi_hip_codebook_create_ne(ctx, tlut.data(), &slot));
+        }
+        return slot;
+    }
+
+    const adi_hip_expert_matrix &expert(const MachExpertMatrix &m) {
+        const Key key{m.trellis.data(), m.rows, m.columns,
+                      fingerprint(m.trellis) ^ fingerprint(m.su_f16) * 3 ^ fingerprint(m.sv_f16) * 5 ^
+                          fingerprint(m.wave_gamma_f16) * 7 ^ fingerprint(m.tlut) * 11};
+        auto found = experts_.find(key);
+        if (found == experts_.end()) {
+            adi_hip_expert_matrix d{};
+            d.rows = m.rows;
+            d.columns = m.columns;
+            d.trellis = upload(m.trellis);
+            d.su_f16 = upload(m.su_f16);
+            d.sv_f16 = upload(m.sv_f16);
+            d.wave_gamma_f16 = upload(m.wave_gamma_f16);
+            d.codebook = expert_book(m.tlut);
+            found = experts_.emplace(key, d).first;
+        }
+        return found->second;
+    }
+
+    const adi_hip_ne_matrix &ne(const MachNeMatrix &m) {
+        const Key key{m.trellis.data(), m.rows, m.columns,
+                      fingerprint(m.trellis) ^ fingerprint(m.su) * 3 ^ fingerprint(m.sv) * 5 ^
+                          fingerprint(m.tlut) * 7 ^ static_cast<std::uint64_t>(m.weight_scale * 1e6f)};
+        auto found = nes_.find(key);
+        if (found == nes_.end()) {
+            adi_hip_ne_matrix d{};
+            d.rows = m.rows;
+            d.columns = m.columns;
+            d.trellis = upload(m.trellis);
+            d.su = upload(m.su);
+            d.sv = upload(m.sv);
+            d.weight_scale = m.weight_scale;
+            d.codebook = ne_book(m.tlut);
+            found = nes_.emplace(key, d).first;
+        }
+        return found->second;
+    }
+
+    const adi_hip_head_chunk &head(const MachHeadChunk &h) {
+        const Key key{h.packed.data(), h.rows, h.columns,
+                      fingerprint(h.packed) ^ fingerprint(h.group_scale_f16) * 3 ^
+                          fingerprint(h.protected_rows) * 5 ^ fingerprint(h.protected_bf16) * 7};
+        auto found = heads_.find(key);
+        if (found == heads_.end()) {
+            adi_hip_head_chunk d{};
+            d.rows = h.rows;
+            d.columns = h.columns;
+            d.packed = upload(h.packed);
+            d.group_scale_f16 = upload(h.group_scale_f16);
+            d.protected_count = static_cast<std::uint32_t>(h.protected_rows.size());
+            if (d.protected_count != 0) {
+                d.protected_rows = upload(h.protected_rows);
+                d.protected_bf16 = upload(h.protected_bf16);
+            }
+            found = heads_.emplace(key, d).first;
+        }
+        return found->second;
+    }
+
+    const adi_hip_bf16_matrix &bf16(const Bf16Matrix &m) {
+        const Key key{m.values.data(), m.rows, m.columns, fingerprint(m.values)};
+        auto found = bf16s_.find(key);
+        if (found == bf16s_.end()) {
+            adi_hip_bf16_matrix d{};
+            d.rows = m.rows;
+            d.columns = m.columns;
+            d.values = upload(m.values);
+            found = bf16s_.emplace(key, d).first;
+        }
+        return found->second;
+    }
+
+    const std::uint16_t *weights(std::span<const std::uint16_t> w) {
+        auto &slot = weights_[{w.data(), fingerprint(w)}];
+        if (slot == nullptr) {
+            slot = upload(w);
+        }
+        return slot;
+    }
+
+    std::string name;
+
+  private:
+    Runtime() {
+        int device = 0;
+        if (const char *value = std::getenv("ADI_HIP_DEVICE")) {
+            device = std::atoi(value);
+        }
+        if (adi_hip_context_create(device, &ctx) != ADI_HIP_OK) {
+            throw std::runtime_error(std::string("adi_hip: ") + adi_hip_last_error(nullptr));
+        }
+        // follow the host CPU's reduction order (cpu_backend().name)
+        const std::string_view isa = cpu_backend().name;
+        const std::uint32_t lanes = isa == "avx512" ? 16u : (isa == "avx2" ? 8u : 1u);
+        check(adi_hip_set_reduction_isa(ctx, lanes));
+        name = "hip:" + std::string(isa);
+    }
+
+    struct Buffer {
+        void *pointer = nullptr;
+        std::size_t bytes = 0;
+    };
+    using Key = std::tuple<const void *, std::uint32_t, std::uint32_t, std::uint64_t>;
+    using TableKey = std::pair<const void *, std::uint64_t>;
+    Buffer buffers_[2];
+    std::map<TableKey, adi_hip_codebook *> expert_books_;
+    std::map<TableKey, adi_hip_codebook *> ne_books_;
+    std::map<Key, adi_hip_expert_matrix> experts_;
+    std::map<Key, adi_hip_ne_matrix> nes_;
+    std::map<Key, adi_hip_head_chunk> heads_;
+    std::map<Key, adi_hip_bf16_matrix> bf16s_;
+    std::map<TableKey, const std::uint16_t *> weights_;
+};
+
+// ---- argument checks: the reference's conditions and messages -------------
+
+void check_expert_codec(const MachExpertMatrix &m) {
+    const std::size_t tiles = static_cast<std::size_t>(m.rows / kTile) * (m.columns / kTile);
+    if (m.trellis.size() != tiles * 24 || m.wave_gamma_f16.size() != m.rows / kTile + m.columns / kTile ||
+        m.tlut.size() != 32768u * 8u) {
+        throw std::invalid_argument("Mach expert codec tensor shape mismatch");
+    }
+}
+
+void check_ne_codec(const MachNeMatrix &m) {
+    const std::size_t tiles = static_cast<std::size_t>(m.rows / kTile) * (m.columns / kTile);
+    if (m.trellis.size() != tiles * 64 || m.tlut.size() != 512u * 2u) {
+        throw std::invalid_argument("Mach NE codec tensor shape mismatch");
+    }
+}
+
+bool tiled_powers(std::uint32_t rows, std::uint32_t columns) {
+    return is_power_of_two(rows) && is_power_of_two(columns) && rows % kTile == 0 &&
+           columns % kTile == 0;
+}
+
+void check_head(const MachHeadChunk &h, std::size_t inputs, std::size_t outputs, std::uint32_t batch) {
+    constexpr std::uint32_t group = 64;
+    const bool shape_ok = h.columns % group == 0 && inputs == std::size_t(batch) * h.columns &&
+                          outputs == std::size_t(batch) * h.rows &&
+                          h.packed.size() == std::size_t(h.rows) * h.columns / 8 * 5 &&
+                          h.group_scale_f16.size() == std::size_t(h.rows) * h.columns / group;
+    if (batch == 1 && !shape_ok) {
+        throw std::invalid_argument("Mach output head shape mismatch");
+    }
+    if (batch != 1 && (batch == 0 || !shape_ok)) {
+        throw std::invalid_argument("Mach output head batch shape mismatch");
+    }
+    if (!h.protected_rows.empty()) {
+        if (h.protected_bf16.size() != h.protected_rows.size() * h.columns) {
+            throw std::invalid_argument("Mach protected output row shape mismatch");
+        }
+        for (const auto row : h.protected_rows) {
+            if (row >= h.rows) {
+                throw std::invalid_argument("Mach protected output row is out of range");
+            }
+        }
+    }
+}
+
+// ---- the entries ---------------------------------------------------------------
+
+void hip_expert_matmul(const MachExpertMatrix &m, std::span<const float> inputs, std::uint32_t batch,
+                       std::span<float> outputs, ExpertScratch &) {
+    if (batch == 1) {
+        if (!tiled_powers(m.rows, m.columns)) {
+            throw std::invalid_argument("Mach expert dimensions must be tiled powers of two");
+        }
+        if (inputs.size() != m.columns || outputs.size() != m.rows || m.su_f16.size() != m.columns ||
+            m.sv_f16.size() != m.rows) {
+            throw std::invalid_argument("Mach expert vector or scale shape mismatch");
+        }
+    } else if (batch == 0 || !tiled_powers(m.rows, m.columns) ||
+               inputs.size() != std::size_t(batch) * m.columns ||
+               outputs.size() != std::size_t(batch) * m.rows || m.su_f16.size() != m.columns ||
+               m.sv_f16.size() != m.rows) {
+        throw std::invalid_argument("Mach expert batch shape mismatch");
+    }
+    check_expert_codec(m);
+    Runtime &rt = Runtime::get();
+    std::lock_guard<std::mutex> lock(rt.mutex);
+    const adi_hip_expert_matrix &d = rt.expert(m);
+    float *in = rt.staging(0, inputs.size());
+    float *out = rt.staging(1, outputs.size());
+    rt.to_device(in, inputs);
+    rt.check(adi_hip_expert_matmul(rt.ctx, &d, in, batch, out));
+    rt.to_host(outputs, out);
+}
+
+void hip_expert_matvec(const MachExpertMatrix &m, std::span<const float> input, std::span<float> output,
+                       ExpertScratch &scratch) {
+    hip_expert_matmul(m, input, 1, output, scratch);
+}
+
+void hip_ne_matmul(const MachNeMatrix &m, std::span<const float> inputs, std::uint32_t batch,
+                   std::span<float> outputs, ExpertScratch &) {
+    if (batch == 1) {
+        if (!tiled_powers(m.rows, m.columns)) {
+            throw std::invalid_argument("Mach NE dimensions must be tiled powers of two");
+        }
+        if (inputs.size() != m.columns || outputs.size() != m.rows || m.su.size() != m.columns ||
+            m.sv.size() != m.rows) {
+            throw std::invalid_argument("Mach NE vector or sign shape mismatch");
+        }
+    } else if (batch == 0 || !tiled_powers(m.rows, m.columns) ||
+               inputs.size() != std::size_t(batch) * m.columns ||
+               outputs.size() != std::size_t(batch) * m.rows || m.su.size() != m.columns ||
+               m.sv.size() != m.rows) {
+        throw std::invalid_argument("Mach NE batch shape mismatch");
+    }
+    check_ne_codec(m);
+    Runtime &rt = Runtime::get();
+    std::lock_guard<std::mutex> lock(rt.mutex);
+    const adi_hip_ne_matrix &d = rt.ne(m);
+    float *in = rt.staging(0, inputs.size());
+    float *out = rt.staging(1, outputs.size());
+    rt.to_device(in, inputs);
+    rt.check(adi_hip_ne_matmul(rt.ctx, &d, in, batch, out));
+    rt.to_host(outputs, out);
+}
+
+void hip_ne_matvec(const MachNeMatrix &m, std::span<const float> input, std::span<float> output,
+                   ExpertScratch &scratch) {
+    hip_ne_matmul(m, input, 1, output, scratch);
+}
+
+void hip_head_matmul(const MachHeadChunk &h, std::span<const float> inputs, std::uint32_t batch,
+                     std::span<float> outputs) {
+    check_head(h, inputs.size(), outputs.size(), batch);
+    Runtime &rt = Runtime::get();
+    std::lock_guard<std::mutex> lock(rt.mutex);
+    const adi_hip_head_chunk &d = rt.head(h);
+    float *in = rt.staging(0, inputs.size());
+    float *out = rt.staging(1, outputs.size());
+    rt.to_device(in, inputs);
+    rt.check(adi_hip_head_matmul(rt.ctx, &d, in, batch, out));
+    rt.to_host(outputs, out);
+}
+
+void hip_head_matvec(const MachHeadChunk &h, std::span<const float> input, std::span<float> output) {
+    hip_head_matmul(h, input, 1, output);
+}
+
+void hip_bf16_matmul(const Bf16Matrix &m, std::span<const float> inputs, std::uint32_t batch,
+                     std::span<float> outputs) {
+    const bool values_ok = m.values.size() == std::size_t(m.rows) * m.columns;
+    if (batch == 1 && (inputs.size() != m.columns || outputs.size() != m.rows || !values_ok)) {
+        throw std::invalid_argument("BF16 matrix-vector shape mismatch");
+    }
+    if (batch != 1 && (batch == 0 || inputs.size() != std::size_t(batch) * m.columns ||
+                       outputs.size() != std::size_t(batch) * m.rows || !values_ok)) {
+        throw std::invalid_argument("BF16 matrix batch shape mismatch");
+    }
+    Runtime &rt = Runtime::get();
+    std::lock_guard<std::mutex> lock(rt.mutex);
+    const adi_hip_bf16_matrix &d = rt.bf16(m);
+    float *in = rt.staging(0, inputs.size());
+    float *out = rt.staging(1, outputs.size());
+    rt.to_device(in, inputs);
+    rt.check(adi_hip_bf16_matmul(rt.ctx, &d, in, batch, out));
+    rt.to_host(outputs, out);
+}
+
+void hip_bf16_matvec(const Bf16Matrix &m, std::span<const float> input, std::span<float> output) {
+    hip_bf16_matmul(m, input, 1, output);
+}
+
+void hip_rms_norm(std::span<const float> input, std::span<const std::uint16_t> weight_bf16,
+                  float weight_offset, float epsilon, std::span<float> output) {
+    if (input.size() != weight_bf16.size() || output.size() != input.size() || input.empty()) {
+        throw std::invalid_argument("RMS norm shape mismatch");
+    }
+    Runtime &rt = Runtime::get();
+    std::lock_guard<std::mutex> lock(rt.mutex);
+    const std::uint16_t *w = rt.weights(weight_bf16);
+    float *in = rt.staging(0, input.size());
+    float *out = rt.staging(1, output.size());
+    rt.to_device(in, input);
+    rt.check(adi_hip_rms_norm(rt.ctx, in, w, static_cast<std::uint32_t>(input.size()), 1,
+                              weight_offset, epsilon, out));
+    rt.to_host(output, out);
+}
+
+}  // namespace
+
+const Backend &hip_backend() {
+    static const Backend backend = [] {
+        Runtime &rt = Runtime::get();
+        return Backend{
+            rt.name,
+            hip_expert_matvec,
+            hip_expert_matmul,
+            hip_ne_matvec,
+            hip_ne_matmul,
+            // embedding rows are not on the packed-weight path this library
+            // accelerates: the CPU entry serves them (src/kernels.cpp:802-845)
+            mach_embedding_row,
+            hip_head_matvec,
+            hip_head_matmul,
+            hip_bf16_matvec,
+            hip_bf16_matmul,
+            hip_rms_norm,
+        };
+    }();
+    return backend;
+}
+
+}  // namespace adi

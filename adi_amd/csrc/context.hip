@@ -163,6 +163,50 @@ int adi_hip_synchronize(adi_hip_context *ctx) {
     return guarded(ctx, [&] { check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize"); });
 }
 
+int adi_hip_device_alloc(adi_hip_context *ctx, size_t bytes, void **out) {
+    return guarded(ctx, [&] {
+        require(out != nullptr, "device_alloc: null output");
+        *out = nullptr;
+        check_hip(hipMalloc(out, bytes == 0 ? 1 : bytes), "hipMalloc");
+    });
+}
+
+void adi_hip_device_free(adi_hip_context *ctx, void *pointer) {
+    if (ctx == nullptr || pointer == nullptr) {
+        return;
+    }
+    int previous = 0;
+    if (hipGetDevice(&previous) == hipSuccess) {
+        (void)hipSetDevice(ctx->device);
+        (void)hipFree(pointer);
+        (void)hipSetDevice(previous);
+    }
+}
+
+int adi_hip_copy_to_device(adi_hip_context *ctx, void *device, const void *host, size_t bytes) {
+    return guarded(ctx, [&] {
+        require(bytes == 0 || (device != nullptr && host != nullptr), "copy_to_device: null pointer");
+        if (bytes == 0) {
+            return;
+        }
+        check_hip(hipMemcpyAsync(device, host, bytes, hipMemcpyHostToDevice, ctx->stream),
+                  "hipMemcpyAsync");
+        check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    });
+}
+
+int adi_hip_copy_to_host(adi_hip_context *ctx, void *host, const void *device, size_t bytes) {
+    return guarded(ctx, [&] {
+        require(bytes == 0 || (device != nullptr && host != nullptr), "copy_to_host: null pointer");
+        if (bytes == 0) {
+            return;
+        }
+        check_hip(hipMemcpyAsync(host, device, bytes, hipMemcpyDeviceToHost, ctx->stream),
+                  "hipMemcpyAsync");
+        check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    });
+}
+
 int adi_hip_set_reduction_isa(adi_hip_context *ctx, uint32_t lanes) {
     return guarded(ctx, [&] {
         require(lanes == 1 || lanes == 8 || lanes == 16,

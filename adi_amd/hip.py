@@ -69,6 +69,10 @@ SIGNATURES = [
     ("adi_hip_set_stream", C.c_int, [vp, vp]),
     ("adi_hip_synchronize", C.c_int, [vp]),
     ("adi_hip_set_reduction_isa", C.c_int, [vp, u32]),
+    ("adi_hip_device_alloc", C.c_int, [vp, C.c_size_t, C.POINTER(vp)]),
+    ("adi_hip_device_free", None, [vp, vp]),
+    ("adi_hip_copy_to_device", C.c_int, [vp, vp, vp, C.c_size_t]),
+    ("adi_hip_copy_to_host", C.c_int, [vp, vp, vp, C.c_size_t]),
     ("adi_hip_codebook_create_expert", C.c_int, [vp, vp, C.POINTER(vp)]),
     ("adi_hip_codebook_create_ne", C.c_int, [vp, vp, C.POINTER(vp)]),
     ("adi_hip_codebook_destroy", None, [vp]),

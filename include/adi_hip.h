@@ -63,14 +63,27 @@ int adi_hip_synchronize(adi_hip_context *ctx);
  * src/simd.cpp:298-342). Default 16. */
 int adi_hip_set_reduction_isa(adi_hip_context *ctx, uint32_t lanes);
 
+/* ---- device memory -------------------------------------------------------- */
+
+/* Device buffers for callers that build descriptors without the HIP runtime
+ * (a host-compiled Backend shim). No reference counterpart: the reference's
+ * matrices are views into the mmap (include/adi/kernels.hpp:9-77), which
+ * this build copies to HBM once. Copies are synchronous on the context's
+ * stream. */
+int adi_hip_device_alloc(adi_hip_context *ctx, size_t bytes, void **out);
+void adi_hip_device_free(adi_hip_context *ctx, void *pointer);
+int adi_hip_copy_to_device(adi_hip_context *ctx, void *device, const void *host, size_t bytes);
+int adi_hip_copy_to_host(adi_hip_context *ctx, void *host, const void *device, size_t bytes);
+
 /* ---- codebooks ------------------------------------------------------------ */
 
 /* Model-wide decoded-state tables, built once from the host TLUT and kept in
  * HBM as f16 (exact: the reference rounds every lattice value through f16,
  * src/codec_cache.cpp:27-29, 33-115). Replace the ExpertScratch caches and
  * MachModel::cache_descriptors (src/kernels.cpp:33-94, src/model.cpp:549-551).
- *   expert: tlut 32768x8 f32 -> the 16384 reachable rows x 8 f16 (256 KiB;
- *           state s selects row (s*(s+1) mod 2^15)/2, always even);
+ *   expert: tlut 32768x8 f32 -> the 16384 reachable rows x 8 f16 (256 KiB,
+ *           two planes of components 0-3 and 4-7; state s selects row
+ *           (s*(s+1) mod 2^15)/2, always even);
  *   ne:     tlut 512x2 f32 -> the 1024x2 signed table (4 KiB). */
 int adi_hip_codebook_create_expert(adi_hip_context *ctx, const float *tlut_host,
                                    adi_hip_codebook **out);

@@ -88,3 +88,16 @@ def test_no_device_is_an_error_not_a_crash():
     # every entry point rejects a null context without touching a device
     assert lib.adi_hip_set_reduction_isa(None, 16) == hip.INVALID_ARGUMENT
     assert lib.adi_hip_expert_matmul(None, None, None, 1, None) == hip.INVALID_ARGUMENT
+
+
+def test_backend_library_exports_the_driver():
+    """Where the reference is present, its runtime linked with hip_backend()
+    loads on a host without a GPU (the table is created on first use)."""
+    import backend_binding as bb
+    if not bb.available():
+        pytest.skip("oracle/_ref/libadi_backend.so is not built here")
+    lib = bb.load()
+    for name in ("bd_backend_name", "bd_expert_matmul", "bd_ne_matmul", "bd_head_matmul",
+                 "bd_bf16_matmul", "bd_rms_norm"):
+        assert hasattr(lib, name)
+    assert bb.name(bb.CPU) in ("scalar", "avx2", "avx512")
