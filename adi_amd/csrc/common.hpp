@@ -271,4 +271,56 @@ __device__ __forceinline__ void sum_slices(const float *src, size_t stride, uint
     }
 }
 
+// Destination of a Hadamard-transformed input vector x_hat:
+//   planes 0: fp32 [vectors][n] (decode-GEMV);
+//   planes 1: f16 hi/lo pairs [vectors][n] (MFMA GEMM of an NE matrix);
+//   planes 2: f16 hi/lo pairs split by expert codebook plane,
+//             [2][vectors][n/2] (MFMA GEMM of an expert matrix).
+// hi = f16(x_hat), lo = f16(x_hat - hi), so hi + lo carries x_hat to about
+// 2^-22 relative. In the plane order, column c of tile column t = c/16 with
+// in-tile column q = c%16 goes to plane (q/4)%2 at position t*8 + (q/8)*4 +
+// q%4: the eight columns a codebook plane covers in each tile, contiguous.
+struct XhatOut {
+    float *f32;
+    uint16_t *hi;
+    uint16_t *lo;
+    uint32_t planes;
+    uint32_t vectors;  // vectors in the destination (plane stride)
+};
+
+__device__ __forceinline__ uint32_t f16_bits_rne(float v) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+
+template <int VPL>
+__device__ __forceinline__ void store_xhat(const XhatOut &out, uint32_t vector, uint32_t lane,
+                                           const float (&v)[VPL]) {
+#pragma clang fp contract(off)
+    constexpr uint32_t n = 64u * VPL;
+    if (out.planes == 0) {
+        float *dst = out.f32 + static_cast<size_t>(vector) * n + lane;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            dst[i * 64] = v[i];
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const uint32_t hi = f16_bits_rne(v[i]);
+        const uint32_t lo = f16_bits_rne(v[i] - half_bits_to_float(hi));
+        const uint32_t c = static_cast<uint32_t>(i) * 64u + lane;
+        size_t at;
+        if (out.planes == 1) {
+            at = static_cast<size_t>(vector) * n + c;
+        } else {
+            const uint32_t q = c & 15u;
+            at = static_cast<size_t>((q >> 2) & 1u) * out.vectors * (n / 2) +
+                 static_cast<size_t>(vector) * (n / 2) + (c >> 4) * 8u + (q >> 3) * 4u + (q & 3u);
+        }
+        out.hi[at] = static_cast<uint16_t>(hi);
+        out.lo[at] = static_cast<uint16_t>(lo);
+    }
+}
+
 }  // namespace adi_hip

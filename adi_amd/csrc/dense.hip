@@ -506,6 +506,140 @@ __device__ __forceinline__ void route_sort_block(const RouteSort &a,
     }
 }
 
+// ---- multi-block sort ---------------------------------------------------------
+
+constexpr uint32_t kChunk = 64;             // route positions per histogram chunk
+constexpr uint32_t kFinalizeBases = 16384;  // chunk x expert bases held in LDS
+
+// Exclusive scan of one value per thread over a block of up to 1024 threads
+// (16 waves); `sums` holds 16 words. Ends with a barrier.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t value, uint32_t *sums,
+                                                         uint32_t &block_total) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    uint32_t inclusive = value;
+#pragma unroll
+    for (int offset = 1; offset < 64; offset <<= 1) {
+        const uint32_t other = static_cast<uint32_t>(__shfl_up(static_cast<int>(inclusive), offset));
+        if (lane >= static_cast<uint32_t>(offset)) {
+            inclusive += other;
+        }
+    }
+    if (lane == 63u) {
+        sums[wave] = inclusive;
+    }
+    __syncthreads();
+    uint32_t before = 0, total = 0;
+    const uint32_t waves = blockDim.x >> 6;
+    for (uint32_t w = 0; w < waves; ++w) {
+        before += w < wave ? sums[w] : 0u;
+        total += sums[w];
+    }
+    __syncthreads();
+    block_total = total;
+    return before + inclusive - value;
+}
+
+// One wave per chunk of 64 route positions: the rank of each position among
+// the chunk's earlier positions with the same expert (ballot match on the
+// expert bits) and the chunk's per-expert counts.
+__global__ __launch_bounds__(256) void k_route_hist(RouteSort a, uint32_t chunks) {
+    extern __shared__ uint32_t hist[];  // [4][experts]
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t c = blockIdx.x * 4u + wave;
+    if (c >= chunks) {
+        return;  // wave-uniform; no block barrier follows
+    }
+    uint32_t *h = hist + wave * a.experts;
+    for (uint32_t e = lane; e < a.experts; e += 64u) {
+        h[e] = 0u;
+    }
+    const uint32_t i = c * kChunk + lane;
+    const bool valid = i < a.positions;
+    const uint32_t e = valid ? a.route_expert[i] : 0u;
+    uint64_t peers = __ballot(valid);
+    if (!valid) {
+        peers = ~peers;
+    }
+    for (uint32_t bit = 0; bit < 10u; ++bit) {
+        const bool set = (e >> bit) & 1u;
+        const uint64_t vote = __ballot(set);
+        peers &= set ? vote : ~vote;
+    }
+    const uint32_t rank = __popcll(peers & ((1ull << lane) - 1ull));
+    // LDS operations of one wave complete in order: the zeroing lands first
+    if (valid) {
+        a.position_rank[i] = rank;
+        if (rank == 0) {
+            h[e] = __popcll(peers);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    for (uint32_t x = lane; x < a.experts; x += 64u) {
+        a.chunk_hist[static_cast<size_t>(c) * a.experts + x] = h[x];
+    }
+}
+
+// One block: per-expert totals and offsets, the ascending active list and
+// slot table, each chunk's base within its expert, position_expert, and the
+// grouped index of every position (stable in (token, route) order: chunk
+// order, then rank within the chunk).
+__global__ __launch_bounds__(1024) void k_route_finalize(RouteSort a, uint32_t chunks) {
+    extern __shared__ uint32_t base[];  // [chunks][experts]
+    __shared__ uint32_t start[kMaxExperts];
+    __shared__ uint32_t sums[16];
+    const uint32_t t = threadIdx.x;
+    const bool mine = t < a.experts;
+    uint32_t total = 0;
+    if (mine) {
+        for (uint32_t c = 0; c < chunks; ++c) {
+            const uint32_t v = a.chunk_hist[static_cast<size_t>(c) * a.experts + t];
+            base[c * a.experts + t] = total;
+            total += v;
+        }
+    }
+    uint32_t all = 0;
+    const uint32_t offset = block_exclusive_scan(mine ? total : 0u, sums, all);
+    uint32_t active_total = 0;
+    const uint32_t slot = block_exclusive_scan(mine && total != 0u ? 1u : 0u, sums, active_total);
+    if (mine) {
+        start[t] = offset;
+        a.counts[t] = total;
+        a.offsets[t] = offset;
+        if (total != 0u) {
+            if (a.active != nullptr) {
+                a.active[slot] = t;
+            }
+            if (a.slot_info != nullptr) {
+                a.slot_info[slot] = make_uint4(t, offset, offset + total, 0u);
+            }
+        }
+        if (a.position_expert != nullptr) {
+            for (uint32_t p = offset; p < offset + total; ++p) {
+                a.position_expert[p] = t;
+            }
+        }
+    }
+    if (t == 0) {
+        a.offsets[a.experts] = all;
+        if (a.active_count != nullptr) {
+            *a.active_count = active_total;
+        }
+    }
+    if (a.slot_info != nullptr) {
+        for (uint32_t s = active_total + t; s < a.experts; s += blockDim.x) {
+            a.slot_info[s] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = t; i < a.positions; i += blockDim.x) {
+        const uint32_t e = a.route_expert[i];
+        const uint32_t g = start[e] + base[(i / kChunk) * a.experts + e] + a.position_rank[i];
+        a.grouped_batch[g] = i / 8u;
+        a.route_to_grouped[i] = g;
+    }
+}
+
 __global__ __launch_bounds__(64) void k_route_sort(RouteSort a) {
     __shared__ uint32_t counts[kMaxExperts];
     __shared__ uint32_t cursor[kMaxExperts];
@@ -605,6 +739,18 @@ void launch_top_experts(adi_hip_context *ctx, const float *logits, const float *
 }
 
 void launch_route_sort(adi_hip_context *ctx, const RouteSort &args) {
+    const uint32_t chunks = ceil_div(args.positions, kChunk);
+    if (args.position_rank != nullptr && args.chunk_hist != nullptr &&
+        size_t(chunks) * args.experts <= kFinalizeBases) {
+        launch(ctx, "route_hist", k_route_hist, dim3(ceil_div(chunks, 4)), dim3(256),
+               size_t(4) * args.experts * sizeof(uint32_t), args, chunks);
+        const size_t lds = size_t(chunks) * args.experts * sizeof(uint32_t);
+        static const bool ready = set_lds_limit(reinterpret_cast<const void *>(&k_route_finalize),
+                                                size_t(kFinalizeBases) * sizeof(uint32_t));
+        (void)ready;
+        launch(ctx, "route_sort", k_route_finalize, dim3(1), dim3(1024), lds, args, chunks);
+        return;
+    }
     launch(ctx, "route_sort", k_route_sort, dim3(1), dim3(64), 0, args);
 }
 
@@ -696,6 +842,11 @@ int adi_hip_moe_route(adi_hip_context *ctx, const float *logits, const float *lo
         s.offsets = offsets;
         s.grouped_batch = grouped_batch;
         s.route_to_grouped = route_to_grouped;
+        auto &ws = ctx->workspace;
+        ws.used = 0;
+        ws.ensure(Workspace::round(route_sort_scratch(s.positions, experts) * 4) + 256);
+        s.position_rank = ws.take<uint32_t>(s.positions);
+        s.chunk_hist = ws.take<uint32_t>(route_sort_scratch(s.positions, experts) - s.positions);
         launch_route_sort(ctx, s);
     });
 }

@@ -38,7 +38,15 @@ struct RouteSort {
     uint32_t *position_expert;    // [positions] (nullable)
     uint32_t *grouped_batch;      // [positions]
     uint32_t *route_to_grouped;   // [positions]
+    // scratch for the multi-block sort (both nullable: one block sorts)
+    uint32_t *position_rank;      // [positions]
+    uint32_t *chunk_hist;         // [ceil(positions / 64)][experts]
 };
+
+// Scratch words the multi-block sort needs for `positions` and `experts`.
+inline size_t route_sort_scratch(size_t positions, size_t experts) {
+    return positions + (positions + 63) / 64 * experts;
+}
 void launch_route_sort(adi_hip_context *ctx, const RouteSort &args);
 
 // top_experts for every row plus the counting sort, in one launch.

@@ -20,6 +20,7 @@
 // past the device-side active count return at once, so the host never waits
 // for the routing.
 #include "dense.hpp"
+#include "grouped.hpp"
 #include "projection.hpp"
 
 namespace adi_hip {
@@ -46,7 +47,7 @@ struct SwigluSegment {
     const int8_t *sv_up_sign;
     const int8_t *su_down_sign;
     const uint32_t *matrix_index;
-    float *x_hat;
+    XhatOut x_hat;
     uint32_t count;
     uint32_t splits;              // slices of z_gate / z_up
 };
@@ -95,11 +96,7 @@ __global__ __launch_bounds__(256) void k_swiglu_wave(SwigluJobs j) {
         gv[i] = silu(gv[i] * a) * (uv[i] * b) * c;
     }
     wave_hadamard<VPL>(gv, j.scale, lane);
-    float *out = g.x_hat + static_cast<size_t>(v) * n + lane;
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-        out[i * 64] = gv[i];
-    }
+    store_xhat<VPL>(g.x_hat, v, lane, gv);
 }
 
 struct CombineArgs {
@@ -315,9 +312,15 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         require(inputs != nullptr && outputs != nullptr, "MoE vector is null");
         const uint32_t H = L->hidden, I = L->expert_hidden, E = L->experts;
         const size_t B = batch, P = B * 8;
-        const uint32_t sg = expert_splits(H), ssg = ne_splits(H);  // gate/up: H inputs
-        const uint32_t sd = expert_splits(I), ssd = ne_splits(I);  // down: I inputs
         const uint32_t max_active = static_cast<uint32_t>(P < E ? P : E);
+        const bool wave_path = wave_width(H) && wave_width(I);
+        // prefill microbatches: MFMA grouped GEMMs over the expert-sorted
+        // positions; decode batches: the persistent decode-GEMV
+        const bool mfma = wave_path && batch >= kMfmaBatch && H >= 64 && I >= 64;
+        const uint32_t sg = mfma ? 2u : expert_splits(H);
+        const uint32_t sd = mfma ? 2u : expert_splits(I);
+        const uint32_t ssg = mfma ? ne_mfma_slices(I, H, batch) : ne_splits(H);
+        const uint32_t ssd = mfma ? ne_mfma_slices(H, I, batch) : ne_splits(I);
 
         auto &ws = ctx->workspace;
         ws.used = 0;
@@ -325,6 +328,7 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
             Workspace::round(B * E * 4) + Workspace::round(B * 4) +
             Workspace::round(P * 4) * 5 + Workspace::round(E * 4) * 3 +
             Workspace::round((E + 1) * 4) + Workspace::round(4) + Workspace::round(E * 16) +
+            Workspace::round(P * 4) + Workspace::round((route_sort_scratch(P, E) - P) * 4) +
             Workspace::round(P * H * 4) * 2 + Workspace::round(sg * P * I * 4) * 2 +
             Workspace::round(P * I * 4) + Workspace::round(sd * P * H * 4) +
             Workspace::round(B * H * 4) * 2 + Workspace::round(ssg * B * I * 4) * 2 +
@@ -343,6 +347,9 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         uint32_t *offsets = ws.take<uint32_t>(E + 1);
         uint32_t *active_count = ws.take<uint32_t>(1);
         uint4 *slot_info = ws.take<uint4>(E);
+        uint32_t *position_rank = ws.take<uint32_t>(P);
+        uint32_t *chunk_hist = ws.take<uint32_t>(route_sort_scratch(P, E) - P);
+        // x_hat buffers: fp32 for the GEMV, or f16 hi then lo (same bytes) for MFMA
         float *xh_gate = ws.take<float>(P * H);
         float *xh_up = ws.take<float>(P * H);
         float *z_gate = ws.take<float>(sg * P * I);
@@ -356,7 +363,18 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         float *sxh_down = ws.take<float>(B * I);
         float *sz_down = ws.take<float>(ssd * B * H);
 
-        const bool wave_path = wave_width(H) && wave_width(I);
+        // where x_hat goes: fp32, or f16 pairs (planes 2: expert, 1: NE)
+        auto xhat = [&](float *buffer, size_t vectors, size_t n, uint32_t planes) {
+            if (!mfma) {
+                return XhatOut{buffer, nullptr, nullptr, 0u, static_cast<uint32_t>(vectors)};
+            }
+            uint16_t *hi = reinterpret_cast<uint16_t *>(buffer);
+            return XhatOut{nullptr, hi, hi + vectors * n, planes, static_cast<uint32_t>(vectors)};
+        };
+        auto hi_of = [&](float *buffer) { return reinterpret_cast<const uint16_t *>(buffer); };
+        auto lo_of = [&](float *buffer, size_t count) {
+            return reinterpret_cast<const uint16_t *>(buffer) + count;
+        };
 
         // 1-2: router logits (+ the shared gate row) and routing
         launch_bf16_ordered_extra(ctx, L->router.values, E, L->shared_expert_gate.values, H, inputs,
@@ -373,6 +391,8 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         sort.grouped_batch = grouped_batch;
         sort.route_to_grouped = route_to_grouped;
         sort.slot_info = slot_info;
+        sort.position_rank = position_rank;
+        sort.chunk_hist = chunk_hist;
         launch_route(ctx, logits, logit_bias, batch, route_expert, route_weight, sort);
 
         // 3: prologues, routed gate/up and shared gate/up
@@ -380,66 +400,123 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         pro.segments = 4;
         pro.n = H;
         pro.seg[0] = PrologueSegment{inputs, grouped_batch, position_expert, L->gate.su_f16, nullptr,
-                                     H, xh_gate, static_cast<uint32_t>(P)};
+                                     H, xhat(xh_gate, P, H, 2), static_cast<uint32_t>(P)};
         pro.seg[1] = PrologueSegment{inputs, grouped_batch, position_expert, L->up.su_f16, nullptr,
-                                     H, xh_up, static_cast<uint32_t>(P)};
+                                     H, xhat(xh_up, P, H, 2), static_cast<uint32_t>(P)};
         pro.seg[2] = PrologueSegment{inputs, nullptr, nullptr, nullptr, L->shared_gate.su, 0,
-                                     sxh_gate, batch};
+                                     xhat(sxh_gate, B, H, 1), batch};
         pro.seg[3] = PrologueSegment{inputs, nullptr, nullptr, nullptr, L->shared_up.su, 0,
-                                     sxh_up, batch};
+                                     xhat(sxh_up, B, H, 1), batch};
         launch_prologues(ctx, pro);
 
-        // 4: gate / up GEMVs
         const size_t gu_words = size_t(I / kTile) * (H / kTile) * kExpertWords;
         const size_t d_words = size_t(H / kTile) * (I / kTile) * kExpertWords;
         const uint32_t gamma_stride = H / kTile + I / kTile;
-        auto expert_job = [&](const adi_hip_expert_stack &st, uint32_t rows, uint32_t columns,
-                              size_t words, const float *x_hat, float *z) {
-            ExpertGemv g{};
-            g.gamma_stride = gamma_stride;
-            g.rows = rows;
-            g.columns = columns;
-            g.trellis_stride = words;
-            g.z_split_stride = P * rows;
-            g.trellis = st.trellis;
-            g.gamma = st.wave_gamma_f16;
-            g.x_hat = x_hat;
-            g.z = z;
-            return g;
-        };
-        auto ne_job = [&](const adi_hip_ne_matrix &m, const float *x_hat, float *z) {
-            NeGemv n{};
-            n.batch = batch;
-            n.rows = m.rows;
-            n.columns = m.columns;
-            n.z_split_stride = B * m.rows;
-            n.trellis = m.trellis;
-            n.weight_scale = m.weight_scale;
-            n.x_hat = x_hat;
-            n.z = z;
-            return n;
-        };
-        MoeGemv gu{};
-        gu.expert[0] = expert_job(L->gate, I, H, gu_words, xh_gate, z_gate);
-        gu.expert[1] = expert_job(L->up, I, H, gu_words, xh_up, z_up);
-        gu.expert_count = 2;
-        gu.ne[0] = ne_job(L->shared_gate, sxh_gate, sz_gate);
-        gu.ne_count = 1;
-        gu.expert_book = L->expert_codebook->data;
-        gu.slot_info = slot_info;
-        gu.ne_book = L->shared_gate.codebook->data;
-        gu.max_active = max_active;
-        if (L->shared_up.codebook->data == L->shared_gate.codebook->data) {
-            gu.ne[1] = ne_job(L->shared_up, sxh_up, sz_up);
-            gu.ne_count = 2;
-            launch_trellis_gemv(ctx, gu);
+
+        // 4: gate / up projections
+        if (mfma) {
+            auto expert_mfma = [&](const adi_hip_expert_stack &st, uint32_t rows, uint32_t columns,
+                                   size_t words, float *x, float *z) {
+                ExpertMfma g{};
+                g.trellis = st.trellis;
+                g.trellis_stride = words;
+                g.gamma = st.wave_gamma_f16;
+                g.gamma_stride = gamma_stride;
+                g.rows = rows;
+                g.columns = columns;
+                g.x_hi = hi_of(x);
+                g.x_lo = lo_of(x, P * columns);
+                g.positions = static_cast<uint32_t>(P);
+                g.z = z;
+                g.z_split_stride = P * rows;
+                return g;
+            };
+            auto ne_mfma = [&](const adi_hip_ne_matrix &m, float *x, float *z) {
+                NeMfma n{};
+                n.trellis = m.trellis;
+                n.weight_scale = m.weight_scale;
+                n.rows = m.rows;
+                n.columns = m.columns;
+                n.x_hi = hi_of(x);
+                n.x_lo = lo_of(x, B * m.columns);
+                n.batch = batch;
+                n.z = z;
+                return n;
+            };
+            ExpertMfmaJobs gu{};
+            gu.expert[0] = expert_mfma(L->gate, I, H, gu_words, xh_gate, z_gate);
+            gu.expert[1] = expert_mfma(L->up, I, H, gu_words, xh_up, z_up);
+            gu.expert_count = 2;
+            gu.expert_book = L->expert_codebook->data;
+            gu.slot_info = slot_info;
+            gu.max_active = max_active;
+            gu.max_positions = batch;
+            launch_expert_mfma(ctx, gu);
+            NeMfmaJobs sgu{};
+            sgu.ne[0] = ne_mfma(L->shared_gate, sxh_gate, sz_gate);
+            sgu.ne_count = 1;
+            sgu.ne_book = L->shared_gate.codebook->data;
+            if (L->shared_up.codebook->data == L->shared_gate.codebook->data) {
+                sgu.ne[1] = ne_mfma(L->shared_up, sxh_up, sz_up);
+                sgu.ne_count = 2;
+                launch_ne_mfma(ctx, sgu);
+            } else {
+                launch_ne_mfma(ctx, sgu);
+                NeMfmaJobs su{};
+                su.ne[0] = ne_mfma(L->shared_up, sxh_up, sz_up);
+                su.ne_count = 1;
+                su.ne_book = L->shared_up.codebook->data;
+                launch_ne_mfma(ctx, su);
+            }
         } else {
-            launch_trellis_gemv(ctx, gu);
-            MoeGemv su{};
-            su.ne[0] = ne_job(L->shared_up, sxh_up, sz_up);
-            su.ne_count = 1;
-            su.ne_book = L->shared_up.codebook->data;
-            launch_trellis_gemv(ctx, su);
+            auto expert_job = [&](const adi_hip_expert_stack &st, uint32_t rows, uint32_t columns,
+                                  size_t words, const float *x_hat, float *z) {
+                ExpertGemv g{};
+                g.gamma_stride = gamma_stride;
+                g.rows = rows;
+                g.columns = columns;
+                g.trellis_stride = words;
+                g.z_split_stride = P * rows;
+                g.trellis = st.trellis;
+                g.gamma = st.wave_gamma_f16;
+                g.x_hat = x_hat;
+                g.z = z;
+                return g;
+            };
+            auto ne_job = [&](const adi_hip_ne_matrix &m, const float *x_hat, float *z) {
+                NeGemv n{};
+                n.batch = batch;
+                n.rows = m.rows;
+                n.columns = m.columns;
+                n.z_split_stride = B * m.rows;
+                n.trellis = m.trellis;
+                n.weight_scale = m.weight_scale;
+                n.x_hat = x_hat;
+                n.z = z;
+                return n;
+            };
+            MoeGemv gu{};
+            gu.expert[0] = expert_job(L->gate, I, H, gu_words, xh_gate, z_gate);
+            gu.expert[1] = expert_job(L->up, I, H, gu_words, xh_up, z_up);
+            gu.expert_count = 2;
+            gu.ne[0] = ne_job(L->shared_gate, sxh_gate, sz_gate);
+            gu.ne_count = 1;
+            gu.expert_book = L->expert_codebook->data;
+            gu.slot_info = slot_info;
+            gu.ne_book = L->shared_gate.codebook->data;
+            gu.max_active = max_active;
+            if (L->shared_up.codebook->data == L->shared_gate.codebook->data) {
+                gu.ne[1] = ne_job(L->shared_up, sxh_up, sz_up);
+                gu.ne_count = 2;
+                launch_trellis_gemv(ctx, gu);
+            } else {
+                launch_trellis_gemv(ctx, gu);
+                MoeGemv su{};
+                su.ne[0] = ne_job(L->shared_up, sxh_up, sz_up);
+                su.ne_count = 1;
+                su.ne_book = L->shared_up.codebook->data;
+                launch_trellis_gemv(ctx, su);
+            }
         }
 
         // 5: SwiGLU and the down prologue
@@ -450,10 +527,10 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
             sj.scale = scale_i;
             sj.seg[0] = SwigluSegment{z_gate, z_up, P * I, L->gate.sv_f16, L->up.sv_f16,
                                       L->down.su_f16, nullptr, nullptr, nullptr, position_expert,
-                                      xh_down, static_cast<uint32_t>(P), sg};
+                                      xhat(xh_down, P, I, 2), static_cast<uint32_t>(P), sg};
             sj.seg[1] = SwigluSegment{sz_gate, sz_up, B * I, nullptr, nullptr, nullptr,
                                       L->shared_gate.sv, L->shared_up.sv, L->shared_down.su,
-                                      nullptr, sxh_down, batch, ssg};
+                                      nullptr, xhat(sxh_down, B, I, 1), batch, ssg};
             const dim3 grid(ceil_div(P + B, 4));
             switch (I) {
             case 64: launch(ctx, "swiglu", k_swiglu_wave<1>, grid, dim3(256), 0, sj); break;
@@ -476,17 +553,69 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
                    static_cast<const uint32_t *>(nullptr), scale_i, sxh_down);
         }
 
-        // 6: down GEMVs
-        MoeGemv dn{};
-        dn.expert[0] = expert_job(L->down, H, I, d_words, xh_down, z_down);
-        dn.expert_count = 1;
-        dn.ne[0] = ne_job(L->shared_down, sxh_down, sz_down);
-        dn.ne_count = 1;
-        dn.expert_book = L->expert_codebook->data;
-        dn.slot_info = slot_info;
-        dn.ne_book = L->shared_down.codebook->data;
-        dn.max_active = max_active;
-        launch_trellis_gemv(ctx, dn);
+        // 6: down projections
+        if (mfma) {
+            ExpertMfmaJobs dn{};
+            ExpertMfma &g = dn.expert[0];
+            g.trellis = L->down.trellis;
+            g.trellis_stride = d_words;
+            g.gamma = L->down.wave_gamma_f16;
+            g.gamma_stride = gamma_stride;
+            g.rows = H;
+            g.columns = I;
+            g.x_hi = hi_of(xh_down);
+            g.x_lo = lo_of(xh_down, P * I);
+            g.positions = static_cast<uint32_t>(P);
+            g.z = z_down;
+            g.z_split_stride = P * H;
+            dn.expert_count = 1;
+            dn.expert_book = L->expert_codebook->data;
+            dn.slot_info = slot_info;
+            dn.max_active = max_active;
+            dn.max_positions = batch;
+            launch_expert_mfma(ctx, dn);
+            NeMfmaJobs sdn{};
+            NeMfma &n = sdn.ne[0];
+            n.trellis = L->shared_down.trellis;
+            n.weight_scale = L->shared_down.weight_scale;
+            n.rows = H;
+            n.columns = I;
+            n.x_hi = hi_of(sxh_down);
+            n.x_lo = lo_of(sxh_down, B * I);
+            n.batch = batch;
+            n.z = sz_down;
+            sdn.ne_count = 1;
+            sdn.ne_book = L->shared_down.codebook->data;
+            launch_ne_mfma(ctx, sdn);
+        } else {
+            MoeGemv dn{};
+            ExpertGemv &g = dn.expert[0];
+            g.gamma_stride = gamma_stride;
+            g.rows = H;
+            g.columns = I;
+            g.trellis_stride = d_words;
+            g.z_split_stride = P * H;
+            g.trellis = L->down.trellis;
+            g.gamma = L->down.wave_gamma_f16;
+            g.x_hat = xh_down;
+            g.z = z_down;
+            dn.expert_count = 1;
+            NeGemv &n = dn.ne[0];
+            n.batch = batch;
+            n.rows = H;
+            n.columns = I;
+            n.z_split_stride = B * H;
+            n.trellis = L->shared_down.trellis;
+            n.weight_scale = L->shared_down.weight_scale;
+            n.x_hat = sxh_down;
+            n.z = sz_down;
+            dn.ne_count = 1;
+            dn.expert_book = L->expert_codebook->data;
+            dn.slot_info = slot_info;
+            dn.ne_book = L->shared_down.codebook->data;
+            dn.max_active = max_active;
+            launch_trellis_gemv(ctx, dn);
+        }
 
         // 7: combine
         if (wave_path) {

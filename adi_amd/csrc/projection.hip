@@ -22,6 +22,7 @@
 // codebook fill. Each (item column range, half) writes its own slice of Z;
 // the consumer adds the slices in a fixed order.
 #include "projection.hpp"
+#include "grouped.hpp"
 
 namespace adi_hip {
 namespace {
@@ -262,11 +263,7 @@ __global__ __launch_bounds__(256) void k_prologue_wave(PrologueJobs j) {
         }
     }
     wave_hadamard<VPL>(val, j.scale, lane);
-    float *out = g.out + static_cast<size_t>(v) * n + lane;
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-        out[i * 64] = val[i];
-    }
+    store_xhat<VPL>(g.out, v, lane, val);
 }
 
 // y = sv * H_n(sum over splits of z), one wave per vector.
@@ -723,14 +720,15 @@ void launch_prologues(adi_hip_context *ctx, PrologueJobs &jobs) {
     default:
         for (uint32_t s = 0; s < jobs.segments; ++s) {
             const PrologueSegment &g = jobs.seg[s];
+            require(g.out.planes == 0, "f16 x_hat output needs a width of 64..4096");
             if (g.su_f16 != nullptr) {
                 launch(ctx, "hadamard_prologue", k_prologue<uint16_t>, dim3(g.count), dim3(256),
                        jobs.n * sizeof(float), g.x, jobs.n, g.su_f16, g.su_stride, g.source_row,
-                       g.matrix_index, jobs.scale, g.out);
+                       g.matrix_index, jobs.scale, g.out.f32);
             } else {
                 launch(ctx, "hadamard_prologue", k_prologue<int8_t>, dim3(g.count), dim3(256),
                        jobs.n * sizeof(float), g.x, jobs.n, g.su_sign, 0u, g.source_row,
-                       static_cast<const uint32_t *>(nullptr), jobs.scale, g.out);
+                       static_cast<const uint32_t *>(nullptr), jobs.scale, g.out.f32);
             }
         }
     }
@@ -890,7 +888,8 @@ int adi_hip_expert_matmul(adi_hip_context *ctx, const adi_hip_expert_matrix *m,
         validate_expert(m);
         require(batch > 0, "Mach expert batch shape mismatch");
         require(inputs != nullptr && outputs != nullptr, "Mach expert vector is null");
-        const uint32_t splits = expert_splits(m->columns);
+        const bool mfma = batch >= kMfmaBatch && m->columns >= 64 && wave_width(m->columns);
+        const uint32_t splits = mfma ? 2u : expert_splits(m->columns);
         auto &ws = ctx->workspace;
         ws.used = 0;
         ws.ensure(Workspace::round(size_t(batch) * m->columns * 4) +
@@ -900,8 +899,34 @@ int adi_hip_expert_matmul(adi_hip_context *ctx, const adi_hip_expert_matrix *m,
         PrologueJobs jobs{};
         jobs.segments = 1;
         jobs.n = m->columns;
-        jobs.seg[0] = PrologueSegment{inputs, nullptr, nullptr, m->su_f16, nullptr, 0, x_hat, batch};
+        uint16_t *hi = reinterpret_cast<uint16_t *>(x_hat);
+        uint16_t *lo = hi + size_t(batch) * m->columns;
+        jobs.seg[0] = PrologueSegment{inputs, nullptr, nullptr, m->su_f16, nullptr, 0,
+                                      mfma ? XhatOut{nullptr, hi, lo, 2, batch}
+                                           : XhatOut{x_hat, nullptr, nullptr, 0, batch},
+                                      batch};
         launch_prologues(ctx, jobs);
+        if (mfma) {
+            ExpertMfmaJobs J{};
+            ExpertMfma &e = J.expert[0];
+            e.trellis = m->trellis;
+            e.gamma = m->wave_gamma_f16;
+            e.rows = m->rows;
+            e.columns = m->columns;
+            e.x_hi = hi;
+            e.x_lo = lo;
+            e.positions = batch;
+            e.z = z;
+            e.z_split_stride = size_t(batch) * m->rows;
+            J.expert_count = 1;
+            J.expert_book = m->codebook->data;
+            J.max_active = 1;
+            J.max_positions = batch;
+            launch_expert_mfma(ctx, J);
+            launch_epilogue_any<uint16_t>(ctx, z, splits, size_t(batch) * m->rows, m->rows,
+                                          m->sv_f16, batch, outputs);
+            return;
+        }
         MoeGemv g{};
         ExpertGemv &e = g.expert[0];
         e.trellis = m->trellis;
@@ -932,7 +957,8 @@ int adi_hip_ne_matmul(adi_hip_context *ctx, const adi_hip_ne_matrix *m,
         validate_ne(m);
         require(batch > 0, "Mach NE batch shape mismatch");
         require(inputs != nullptr && outputs != nullptr, "Mach NE vector is null");
-        const uint32_t splits = ne_splits(m->columns);
+        const bool mfma = batch >= kMfmaBatch && m->columns >= 32 && wave_width(m->columns);
+        const uint32_t splits = mfma ? ne_mfma_slices(m->rows, m->columns, batch) : ne_splits(m->columns);
         auto &ws = ctx->workspace;
         ws.used = 0;
         ws.ensure(Workspace::round(size_t(batch) * m->columns * 4) +
@@ -942,8 +968,31 @@ int adi_hip_ne_matmul(adi_hip_context *ctx, const adi_hip_ne_matrix *m,
         PrologueJobs jobs{};
         jobs.segments = 1;
         jobs.n = m->columns;
-        jobs.seg[0] = PrologueSegment{inputs, nullptr, nullptr, nullptr, m->su, 0, x_hat, batch};
+        uint16_t *hi = reinterpret_cast<uint16_t *>(x_hat);
+        uint16_t *lo = hi + size_t(batch) * m->columns;
+        jobs.seg[0] = PrologueSegment{inputs, nullptr, nullptr, nullptr, m->su, 0,
+                                      mfma ? XhatOut{nullptr, hi, lo, 1, batch}
+                                           : XhatOut{x_hat, nullptr, nullptr, 0, batch},
+                                      batch};
         launch_prologues(ctx, jobs);
+        if (mfma) {
+            NeMfmaJobs J{};
+            NeMfma &n = J.ne[0];
+            n.trellis = m->trellis;
+            n.weight_scale = m->weight_scale;
+            n.rows = m->rows;
+            n.columns = m->columns;
+            n.x_hi = hi;
+            n.x_lo = lo;
+            n.batch = batch;
+            n.z = z;
+            J.ne_count = 1;
+            J.ne_book = m->codebook->data;
+            launch_ne_mfma(ctx, J);
+            launch_epilogue_any<int8_t>(ctx, z, splits, size_t(batch) * m->rows, m->rows, m->sv,
+                                        batch, outputs);
+            return;
+        }
         MoeGemv g{};
         NeGemv &n = g.ne[0];
         n.trellis = m->trellis;

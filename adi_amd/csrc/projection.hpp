@@ -18,7 +18,7 @@ struct PrologueSegment {
     const uint16_t *su_f16;        // one of su_f16 / su_sign
     const int8_t *su_sign;
     uint32_t su_stride;
-    float *out;
+    XhatOut out;
     uint32_t count;
 };
 struct PrologueJobs {

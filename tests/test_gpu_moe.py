@@ -49,7 +49,7 @@ def check(oracle, layer, got, x, bias):
     assert max_rel_error(out, want) <= 1e-3
 
 
-@pytest.mark.parametrize("batch", [1, 2, 4, 16, 33])
+@pytest.mark.parametrize("batch", [1, 2, 4, 16, 33, 64, 97])
 @pytest.mark.parametrize("bias", [False, True])
 def test_moe_small(gpu, oracle, small_layer, batch, bias):
     layer, dl = small_layer
@@ -59,7 +59,8 @@ def test_moe_small(gpu, oracle, small_layer, batch, bias):
     check(oracle, layer, run_moe(gpu, dl, x, b), x, b)
 
 
-@pytest.mark.parametrize("batch,bias", [(1, False), (4, False), (16, False), (128, True)])
+@pytest.mark.parametrize("batch,bias", [(1, False), (4, False), (16, False), (128, True),
+                                        (512, True)])
 def test_moe_full(gpu, oracle, full_layer, batch, bias):
     layer, dl = full_layer
     rng = syn.rng_for(3 if bias else 2, 200 + batch)

@@ -65,6 +65,39 @@ def test_expert_matmul(gpu, books, oracle, rows, columns, batch):
     assert max_rel_error(out.cpu().numpy(), want) <= TOL
 
 
+# from 64 rows the projections run as MFMA GEMMs (f16 hi/lo operands, fp32
+# accumulation): the error stays near fp32 rounding, well inside 1e-3
+MFMA_TOL = 1e-4
+
+
+@pytest.mark.parametrize("rows,columns", [(16, 64), (64, 128), (512, 2048), (2048, 512)])
+@pytest.mark.parametrize("batch", [64, 100, 300])
+def test_expert_matmul_mfma(gpu, books, oracle, rows, columns, batch):
+    et, _, eb, _ = books
+    rng = syn.rng_for(0, 5 * rows + columns + batch)
+    m = syn.expert_matrix(rng, rows, columns, et)
+    x = syn.hidden_states(rng, batch, columns)
+    want = po.expert_matmul(oracle, m, x)
+    dm = hip.upload_expert(gpu, m, eb)
+    out = torch.empty((batch, rows), dtype=torch.float32, device="cuda")
+    hip.expert_matmul(gpu, dm, gpu.to_device(x), batch, out)
+    assert max_rel_error(out.cpu().numpy(), want) <= MFMA_TOL
+
+
+@pytest.mark.parametrize("rows,columns", [(16, 32), (128, 2048), (512, 2048), (2048, 512)])
+@pytest.mark.parametrize("batch", [64, 100, 300])
+def test_ne_matmul_mfma(gpu, books, oracle, rows, columns, batch):
+    _, nt, _, nb = books
+    rng = syn.rng_for(0, 11 * rows + columns + batch)
+    m = syn.ne_matrix(rng, rows, columns, nt)
+    x = syn.hidden_states(rng, batch, columns)
+    want = po.ne_matmul(oracle, m, x)
+    dm = hip.upload_ne(gpu, m, nb)
+    out = torch.empty((batch, rows), dtype=torch.float32, device="cuda")
+    hip.ne_matmul(gpu, dm, gpu.to_device(x), batch, out)
+    assert max_rel_error(out.cpu().numpy(), want) <= MFMA_TOL
+
+
 @pytest.mark.parametrize("rows,columns", NE_SHAPES)
 @pytest.mark.parametrize("batch", [1, 3, 4, 16])
 def test_ne_matmul(gpu, books, oracle, rows, columns, batch):
