@@ -31,9 +31,12 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kMfmaThreads = 256;                   // NE GEMM blocks
 constexpr uint32_t kMfmaWaves = kMfmaThreads / kWave;
-constexpr uint32_t kExpertThreads = 512;                 // expert GEMM: 2 waves per SIMD
-constexpr uint32_t kExpertWaves = kExpertThreads / kWave;
-constexpr uint32_t kRowTiles = 4;                         // tile rows per item
+constexpr uint32_t kRowTiles = 4;                         // NE GEMM: tile rows per item
+// expert GEMM shape: positions 16 * kExpertNT, tile rows kExpertRT per item,
+// kExpertThreads per block (one block per CU)
+constexpr int kExpertNT = 2;
+constexpr int kExpertRT = 4;
+constexpr int kExpertThreads = 512;
 constexpr uint32_t kPlaneRows16 = kExpertRows * 8 / 16;   // 16-byte rows of a plane
 constexpr uint32_t kSlotCapacity = 1024;
 
@@ -61,72 +64,70 @@ __device__ __forceinline__ f32x4 mfma(half8 a, half8 b, f32x4 c) {
 
 // ---- expert ---------------------------------------------------------------
 
-template <int NT>
+template <int NT, int RT>
 struct ExpertStep {
     half8 bh[NT], bl[NT];
-    uint32_t d0[kRowTiles], d1[kRowTiles];
-    uint32_t gamma[kRowTiles];  // f16 bits
+    uint32_t d0[RT], d1[RT];
+    uint32_t gamma[RT];  // f16 bits
 };
 
+// A buffer resource over `bytes` bytes at `base`: loads past the end return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_over(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
+}
+
+// Everything about an item that does not change along K: buffer resources,
+// per-lane byte offsets (the K step advances the scalar offset only) and the
+// lane's window shifts.
+template <int NT, int RT>
 struct ExpertItem {
-    const ExpertMfma *a;
-    const uint32_t *words;      // the matrix's trellis as dwords
-    const uint16_t *gamma_row;
-    const uint16_t *xh, *xl;    // this plane's x_hat pairs
-    uint32_t first, end, p0;    // slot positions and this item's first
-    uint32_t tr0;
+    __amdgpu_buffer_rsrc_t xh, xl, words, gamma;
+    uint32_t xoff[NT];     // B fragment of position tile j at K step 0
+    uint32_t woff[RT];     // the lane's first stream dword of tile row t at K step 0
+    uint32_t wnext[RT];    // and its second (row 15 wraps to word 0)
+    uint32_t dgamma[RT];   // tr + tile column at K step 0
+    uint32_t gamma_top;    // R_t + C_t - 1
+    uint32_t tile_columns;
+    uint32_t sh0, sh1;     // shifts of the lane's two windows in the 64-bit string
+    uint32_t end, p0, tr0;
 };
 
-template <int NT>
-__device__ __forceinline__ void expert_load(const ExpertItem &it, uint32_t kc, uint32_t lane,
-                                            ExpertStep<NT> &s) {
-    const ExpertMfma &a = *it.a;
-    const uint32_t m = lane & 15u, kq = lane >> 4;
-    const uint32_t half_columns = a.columns >> 1;
+template <int NT, int RT>
+__device__ __forceinline__ void expert_load(const ExpertItem<NT, RT> &it, uint32_t kc,
+                                            ExpertStep<NT, RT> &s) {
+    const uint32_t kx = kc * 64u;   // 32 f16 of B per K step
+    const uint32_t kw = kc * 192u;  // 4 tiles of 48 bytes per K step
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-        const uint32_t p = it.p0 + 16u * j + m;
-        const uint32_t pc = p < it.end ? p : it.p0;
-        const size_t at = static_cast<size_t>(pc) * half_columns + kc * 32u + kq * 8u;
-        s.bh[j] = load_half8(it.xh + at);
-        s.bl[j] = load_half8(it.xl + at);
+        s.bh[j] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(it.xh, it.xoff[j], kx, 0));
+        s.bl[j] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(it.xl, it.xoff[j], kx, 0));
     }
-    const uint32_t tile_columns = 1u << a.tc_shift;
-    const uint32_t tc = kc * 4u + kq;
-    const uint32_t dw = (24u * m) >> 5;
-    const uint32_t dn = dw == 11u ? 0u : dw + 1u;  // row 15 wraps to word 0 (src/expert_trellis.hpp:79-80)
 #pragma unroll
-    for (uint32_t t = 0; t < kRowTiles; ++t) {
-        const uint32_t tr = min(it.tr0 + t, a.tile_rows - 1u);
-        const size_t tile = (static_cast<size_t>(tr) << a.tc_shift) + tc;
-        s.d0[t] = __builtin_nontemporal_load(it.words + tile * 12u + dw);
-        s.d1[t] = __builtin_nontemporal_load(it.words + tile * 12u + dn);
-        s.gamma[t] = it.gamma_row[wave_slot(tr, tc, a.tile_rows, tile_columns)];
+    for (int t = 0; t < RT; ++t) {
+        s.d0[t] = __builtin_amdgcn_raw_buffer_load_b32(it.words, it.woff[t], kw, 0);
+        s.d1[t] = __builtin_amdgcn_raw_buffer_load_b32(it.words, it.wnext[t], kw, 0);
+        // wave slot of (tr, tc): R_t + C_t - 1 - d, one less past the main
+        // anti-diagonal (src/codec_cache.cpp:117-147)
+        const uint32_t d = it.dgamma[t] + 4u * kc;
+        const uint32_t slot = it.gamma_top - d - (d >= it.tile_columns ? 1u : 0u);
+        s.gamma[t] = __builtin_amdgcn_raw_buffer_load_b16(it.gamma, slot * 2u, 0, 0);
     }
 }
 
-template <int NT>
-__device__ __forceinline__ void expert_compute(const ExpertItem &it, uint32_t half,
-                                               const uint2 *plane, uint32_t lane,
-                                               const ExpertStep<NT> &s, f32x4 (&acc)[kRowTiles][NT]) {
+template <int NT, int RT>
+__device__ __forceinline__ void expert_compute(const ExpertItem<NT, RT> &it, uint32_t sign_mask,
+                                               const uint2 *plane, const ExpertStep<NT, RT> &s,
+                                               f32x4 (&acc)[RT][NT]) {
 #pragma clang fp contract(off)
-    const uint32_t m = lane & 15u, kq = lane >> 4;
-    const uint32_t pos = ((24u * m) & 31u);  // bit of state 2m in the loaded words
-    const uint32_t sign_mask = half == 0 ? 0x8000u : 0u;
-    // zero the decoded values of masked lanes' invalid positions: B is clamped,
-    // so only positions past the slot need zeroing
-    half8 bh[NT], bl[NT];
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-        const bool ok = it.p0 + 16u * j + m < it.end;
-        bh[j] = ok ? s.bh[j] : zero_half8();
-        bl[j] = ok ? s.bl[j] : zero_half8();
-    }
-    (void)kq;
-#pragma unroll
-    for (uint32_t t = 0; t < kRowTiles; ++t) {
-        const uint32_t p0 = state_product(window64(s.d0[t], s.d1[t], pos));
-        const uint32_t p1 = state_product(window64(s.d0[t], s.d1[t], pos + 12u));
+    for (int t = 0; t < RT; ++t) {
+        // the lane's four stream words, most significant bit first
+        const uint64_t bits = (static_cast<uint64_t>(__builtin_amdgcn_alignbit(s.d0[t], s.d0[t], 16)) << 32) |
+                              __builtin_amdgcn_alignbit(s.d1[t], s.d1[t], 16);
+        const uint32_t w0 = static_cast<uint32_t>(bits >> it.sh0) & 0xFFFFu;
+        const uint32_t w1 = static_cast<uint32_t>(bits >> it.sh1) & 0xFFFFu;
+        const uint32_t p0 = state_product(w0);
+        const uint32_t p1 = state_product(w1);
         uint2 e0 = plane[(p0 >> 1) & 0x3FFFu];
         uint2 e1 = plane[(p1 >> 1) & 0x3FFFu];
         e0.x ^= p0 & sign_mask;
@@ -136,17 +137,19 @@ __device__ __forceinline__ void expert_compute(const ExpertItem &it, uint32_t ha
         const half8 gv = {g, g, g, g, g, g, g, g};
         const half8 hi = gv * v;
         const half8 lo = __builtin_elementwise_fma(gv, v, -hi);
+        // positions past the slot carry another slot's x_hat: their output
+        // columns are computed and never stored
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            acc[t][j] = mfma(hi, bh[j], acc[t][j]);
+            acc[t][j] = mfma(hi, s.bh[j], acc[t][j]);
         }
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            acc[t][j] = mfma(hi, bl[j], acc[t][j]);
+            acc[t][j] = mfma(hi, s.bl[j], acc[t][j]);
         }
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            acc[t][j] = mfma(lo, bh[j], acc[t][j]);
+            acc[t][j] = mfma(lo, s.bh[j], acc[t][j]);
         }
     }
 }
@@ -157,8 +160,10 @@ __device__ __forceinline__ void expert_compute(const ExpertItem &it, uint32_t ha
 // counts in LDS, so the waves walk only real items, evenly. Items are numbered
 // (entry, slot, position group, row group), row group fastest, so the waves of
 // a block share B fragments in L1.
-template <int NT>
-__global__ __launch_bounds__(kExpertThreads) void k_expert_mfma(ExpertMfmaJobs J) {
+template <int NT, int RT, int THREADS>
+__global__ __launch_bounds__(THREADS) void k_expert_mfma(ExpertMfmaJobs J) {
+    constexpr uint32_t kExpertThreads = THREADS;
+    constexpr uint32_t kExpertWaves = THREADS / kWave;
     extern __shared__ uint4 lds_dynamic[];  // [kSlotCapacity] slots, item starts, plane
     uint4 *slots = lds_dynamic;
     uint32_t *starts = reinterpret_cast<uint32_t *>(lds_dynamic + kSlotCapacity);  // [kSlotCapacity + 1]
@@ -170,11 +175,13 @@ __global__ __launch_bounds__(kExpertThreads) void k_expert_mfma(ExpertMfmaJobs J
     const uint32_t workers = gridDim.x >> 1;
     {
         const uint4 *src = static_cast<const uint4 *>(J.expert_book) + half * kPlaneRows16;
-        constexpr uint32_t kPer = kPlaneRows16 / kExpertThreads;  // 16
+        // indexes past the plane are clamped: those threads reload and rewrite
+        // its last row, so no load is guarded
+        constexpr uint32_t kPer = (kPlaneRows16 + kExpertThreads - 1) / kExpertThreads;
         uint4 v[kPer];
 #pragma unroll
         for (uint32_t u = 0; u < kPer; ++u) {
-            v[u] = src[u * kExpertThreads + threadIdx.x];
+            v[u] = src[min(u * kExpertThreads + threadIdx.x, kPlaneRows16 - 1u)];
         }
         // item counts per slot: each thread owns two consecutive slots
         const uint32_t group = 16u * NT;
@@ -206,7 +213,7 @@ __global__ __launch_bounds__(kExpertThreads) void k_expert_mfma(ExpertMfmaJobs J
         }
 #pragma unroll
         for (uint32_t u = 0; u < kPer; ++u) {
-            plane_lds[u * kExpertThreads + threadIdx.x] = v[u];
+            plane_lds[min(u * kExpertThreads + threadIdx.x, kPlaneRows16 - 1u)] = v[u];
         }
         __syncthreads();
         uint32_t before = 0;
@@ -247,47 +254,72 @@ __global__ __launch_bounds__(kExpertThreads) void k_expert_mfma(ExpertMfmaJobs J
         const uint32_t rg = within % J.row_groups;
         const uint32_t pg = within / J.row_groups;
         const uint4 info = slots[slot];
-        ExpertItem it;
-        it.first = __builtin_amdgcn_readfirstlane(info.y);
-        it.end = __builtin_amdgcn_readfirstlane(info.z);
-        it.p0 = it.first + pg * 16u * NT;
+        const uint32_t first = __builtin_amdgcn_readfirstlane(info.y);
         const uint32_t mat = __builtin_amdgcn_readfirstlane(info.x);
-        it.a = &J.expert[which];
-        const ExpertMfma &a = *it.a;
-        it.words = reinterpret_cast<const uint32_t *>(a.trellis + mat * a.trellis_stride);
-        it.gamma_row = a.gamma + mat * a.gamma_stride;
-        const size_t plane_stride = static_cast<size_t>(a.positions) * (a.columns >> 1);
-        it.xh = a.x_hi + half * plane_stride;
-        it.xl = a.x_lo + half * plane_stride;
-        it.tr0 = rg * kRowTiles;
-        f32x4 acc[kRowTiles][NT];
+        const ExpertMfma &a = J.expert[which];
+        ExpertItem<NT, RT> it;
+        it.end = __builtin_amdgcn_readfirstlane(info.z);
+        it.p0 = first + pg * 16u * NT;
+        it.tr0 = rg * RT;
+        const uint32_t m = lane & 15u, kq = lane >> 4;
+        const uint32_t half_columns = a.columns >> 1;
+        const uint32_t tile_columns = 1u << a.tc_shift;
+        const size_t plane_elems = static_cast<size_t>(a.positions) * half_columns;
+        const uint32_t x_bytes = static_cast<uint32_t>(plane_elems * 2u);
+        it.xh = buffer_over(a.x_hi + half * plane_elems, x_bytes);
+        it.xl = buffer_over(a.x_lo + half * plane_elems, x_bytes);
+        const uint32_t tiles = a.tile_rows << a.tc_shift;
+        it.words = buffer_over(a.trellis + mat * a.trellis_stride, tiles * 48u);
+        it.gamma = buffer_over(a.gamma + mat * a.gamma_stride, (a.tile_rows + tile_columns) * 2u);
 #pragma unroll
-        for (uint32_t t = 0; t < kRowTiles; ++t) {
+        for (int j = 0; j < NT; ++j) {
+            const uint32_t p = it.p0 + 16u * j + m;
+            const uint32_t pc = p < it.end ? p : it.p0;  // clamped: a real, finite row
+            it.xoff[j] = (pc * half_columns + kq * 8u) * 2u;
+        }
+        const uint32_t dw = (24u * m) >> 5;
+        const uint32_t dn = dw == 11u ? 0u : dw + 1u;  // row 15 wraps to word 0 (src/expert_trellis.hpp:79-80)
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const uint32_t tr = min(it.tr0 + t, a.tile_rows - 1u);
+            const uint32_t tile = (tr << a.tc_shift) + kq;
+            it.woff[t] = (tile * 12u + dw) * 4u;
+            it.wnext[t] = (tile * 12u + dn) * 4u;
+            it.dgamma[t] = tr + kq;
+        }
+        it.gamma_top = a.tile_rows + tile_columns - 1u;
+        it.tile_columns = tile_columns;
+        const uint32_t pos = (24u * m) & 31u;  // bit of state 2m in the loaded words
+        it.sh0 = 48u - pos;
+        it.sh1 = 36u - pos;
+        f32x4 acc[RT][NT];
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
 #pragma unroll
             for (int j = 0; j < NT; ++j) {
                 acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
         }
-        const uint32_t steps = (1u << a.tc_shift) / 4u;  // a power of two
-        ExpertStep<NT> s0, s1;
-        expert_load<NT>(it, 0, lane, s0);
+        const uint32_t steps = tile_columns / 4u;  // a power of two
+        const uint32_t sign_mask = half == 0 ? 0x8000u : 0u;
+        ExpertStep<NT, RT> s0, s1;
+        expert_load<NT, RT>(it, 0, s0);
         if (steps == 1) {
-            expert_compute<NT>(it, half, plane, lane, s0, acc);
+            expert_compute<NT, RT>(it, sign_mask, plane, s0, acc);
         } else {
             // no branch inside the body, so the compiler's wait counts see
             // that only the other stage's loads are outstanding; the last
             // iteration reloads the final step (in bounds, unused)
             for (uint32_t kc = 0; kc < steps; kc += 2) {
-                expert_load<NT>(it, kc + 1, lane, s1);
-                expert_compute<NT>(it, half, plane, lane, s0, acc);
-                expert_load<NT>(it, min(kc + 2, steps - 1), lane, s0);
-                expert_compute<NT>(it, half, plane, lane, s1, acc);
+                expert_load<NT, RT>(it, kc + 1, s1);
+                expert_compute<NT, RT>(it, sign_mask, plane, s0, acc);
+                expert_load<NT, RT>(it, min(kc + 2, steps - 1), s0);
+                expert_compute<NT, RT>(it, sign_mask, plane, s1, acc);
             }
         }
-        const uint32_t m = lane & 15u, kq = lane >> 4;
         float *z = a.z + half * a.z_split_stride;
 #pragma unroll
-        for (uint32_t t = 0; t < kRowTiles; ++t) {
+        for (uint32_t t = 0; t < RT; ++t) {
             const uint32_t tr = it.tr0 + t;
             if (tr >= a.tile_rows) {
                 continue;
@@ -464,18 +496,18 @@ void launch_expert_mfma(adi_hip_context *ctx, ExpertMfmaJobs &J) {
         x.tile_rows = x.rows / kTile;
         x.tc_shift = log2_of(x.columns / kTile);
     }
-    // 32 positions per item: two waves per SIMD fit in the registers
-    J.row_groups = ceil_div(e.rows / kTile, kRowTiles);
-    J.position_groups = ceil_div(J.max_positions, 32u);
+    J.row_groups = ceil_div(e.rows / kTile, kExpertRT);
+    J.position_groups = ceil_div(J.max_positions, 16u * kExpertNT);
     J.items = J.expert_count * J.max_active * J.position_groups * J.row_groups;  // upper bound
     const uint32_t cap = ctx->cu_count >= 16 ? ctx->cu_count / 16 * 16 : 16u;
-    const uint32_t needed = 16u * ceil_div(ceil_div(J.items, kExpertWaves), 8);
+    const uint32_t needed = 16u * ceil_div(ceil_div(J.items, kExpertThreads / kWave), 8);
     const uint32_t blocks = needed < cap ? needed : cap;
     const size_t lds = size_t(kSlotCapacity) * 16 + size_t(kSlotCapacity + 16) * 4 +
                        size_t(kPlaneRows16) * 16;
-    static const bool ready = set_lds_limit(reinterpret_cast<const void *>(&k_expert_mfma<2>), lds);
+    auto kernel = k_expert_mfma<kExpertNT, kExpertRT, kExpertThreads>;
+    static const bool ready = set_lds_limit(reinterpret_cast<const void *>(kernel), lds);
     (void)ready;
-    launch(ctx, "expert_mfma", k_expert_mfma<2>, dim3(blocks), dim3(kExpertThreads), lds, J);
+    launch(ctx, "expert_mfma", kernel, dim3(blocks), dim3(kExpertThreads), lds, J);
 }
 
 void launch_ne_mfma(adi_hip_context *ctx, NeMfmaJobs &J) {

@@ -74,26 +74,30 @@ __global__ __launch_bounds__(256) void k_swiglu_wave(SwigluJobs j) {
     const SwigluSegment &g = j.seg[s];
     const uint32_t n = 64u * VPL;
     const size_t base = static_cast<size_t>(v) * n;
+    // the scales are loaded with the slices, before the transforms
+    const size_t mat = g.matrix_index != nullptr ? g.matrix_index[v] : 0u;
+    const size_t off = mat * n + lane;
+    float sa[VPL], sb[VPL], sc[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        if (g.sv_gate_f16 != nullptr) {
+            sa[i] = half_bits_to_float(g.sv_gate_f16[off + i * 64]);
+            sb[i] = half_bits_to_float(g.sv_up_f16[off + i * 64]);
+            sc[i] = half_bits_to_float(g.su_down_f16[off + i * 64]);
+        } else {
+            sa[i] = static_cast<float>(g.sv_gate_sign[i * 64u + lane]);
+            sb[i] = static_cast<float>(g.sv_up_sign[i * 64u + lane]);
+            sc[i] = static_cast<float>(g.su_down_sign[i * 64u + lane]);
+        }
+    }
     float gv[VPL], uv[VPL];
     sum_slices<VPL>(g.z_gate + base, g.split_stride, g.splits, lane, gv);
     sum_slices<VPL>(g.z_up + base, g.split_stride, g.splits, lane, uv);
     wave_hadamard<VPL>(gv, j.scale, lane);
     wave_hadamard<VPL>(uv, j.scale, lane);
-    const size_t mat = g.matrix_index != nullptr ? g.matrix_index[v] : 0u;
-    const size_t off = mat * n + lane;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-        float a, b, c;
-        if (g.sv_gate_f16 != nullptr) {
-            a = half_bits_to_float(g.sv_gate_f16[off + i * 64]);
-            b = half_bits_to_float(g.sv_up_f16[off + i * 64]);
-            c = half_bits_to_float(g.su_down_f16[off + i * 64]);
-        } else {
-            a = static_cast<float>(g.sv_gate_sign[i * 64u + lane]);
-            b = static_cast<float>(g.sv_up_sign[i * 64u + lane]);
-            c = static_cast<float>(g.su_down_sign[i * 64u + lane]);
-        }
-        gv[i] = silu(gv[i] * a) * (uv[i] * b) * c;
+        gv[i] = silu(gv[i] * sa[i]) * (uv[i] * sb[i]) * sc[i];
     }
     wave_hadamard<VPL>(gv, j.scale, lane);
     store_xhat<VPL>(g.x_hat, v, lane, gv);
@@ -125,34 +129,39 @@ __global__ __launch_bounds__(576) void k_combine_wave(CombineArgs a) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t n = 64u * VPL;
     const uint32_t b = blockIdx.x;
-    float val[VPL];
+    float val[VPL], scale[VPL];
     const float *src;
     uint32_t splits;
     size_t stride;
+    float weight;
+    // the route's indexes first, then its slices and scales together
     if (wave < 8) {
-        src = a.z_down + static_cast<size_t>(a.route_to_grouped[b * 8u + wave]) * n;
+        const uint32_t grouped = a.route_to_grouped[b * 8u + wave];
+        const uint32_t expert = a.route_expert[b * 8u + wave];
+        weight = a.route_weight[b * 8u + wave];
+        src = a.z_down + static_cast<size_t>(grouped) * n;
         splits = a.splits;
         stride = a.split_stride;
+        const uint16_t *sv = a.sv_down + static_cast<size_t>(expert) * n;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            scale[i] = half_bits_to_float(sv[i * 64u + lane]);
+        }
     } else {
+        weight = sigmoid(a.shared_logit[b]);
         src = a.z_shared + static_cast<size_t>(b) * n;
         splits = a.shared_splits;
         stride = a.shared_split_stride;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            scale[i] = static_cast<float>(a.sv_shared[i * 64u + lane]);
+        }
     }
     sum_slices<VPL>(src, stride, splits, lane, val);
     wave_hadamard<VPL>(val, a.scale, lane);
-    if (wave < 8) {
-        const float w = a.route_weight[b * 8u + wave];
-        const uint16_t *sv = a.sv_down + static_cast<size_t>(a.route_expert[b * 8u + wave]) * n;
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            val[i] = w * (val[i] * half_bits_to_float(sv[i * 64u + lane]));
-        }
-    } else {
-        const float gate = sigmoid(a.shared_logit[b]);
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            val[i] = gate * (val[i] * static_cast<float>(a.sv_shared[i * 64u + lane]));
-        }
+    for (int i = 0; i < VPL; ++i) {
+        val[i] = weight * (val[i] * scale[i]);
     }
     for (uint32_t r = 0; r < 9; ++r) {
         if (wave == r) {
@@ -336,8 +345,11 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         ws.ensure(bytes);
         float *logits = ws.take<float>(B * E);
         float *shared_logit = ws.take<float>(B);
-        uint32_t *route_expert = ws.take<uint32_t>(P);
-        float *route_weight = ws.take<float>(P);
+        // routes go straight to the caller's buffers when it asks for them
+        uint32_t *route_expert_ws = ws.take<uint32_t>(P);
+        float *route_weight_ws = ws.take<float>(P);
+        uint32_t *route_expert = route_expert_out != nullptr ? route_expert_out : route_expert_ws;
+        float *route_weight = route_weight_out != nullptr ? route_weight_out : route_weight_ws;
         uint32_t *position_expert = ws.take<uint32_t>(P);
         uint32_t *grouped_batch = ws.take<uint32_t>(P);
         uint32_t *route_to_grouped = ws.take<uint32_t>(P);
@@ -641,16 +653,6 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
                    static_cast<const float *>(shared_logit), hadamard_scale(H), outputs);
         }
 
-        if (route_expert_out != nullptr) {
-            check_hip(hipMemcpyAsync(route_expert_out, route_expert, P * 4,
-                                     hipMemcpyDeviceToDevice, ctx->stream),
-                      "route copy");
-        }
-        if (route_weight_out != nullptr) {
-            check_hip(hipMemcpyAsync(route_weight_out, route_weight, P * 4,
-                                     hipMemcpyDeviceToDevice, ctx->stream),
-                      "route copy");
-        }
     });
 }
 
