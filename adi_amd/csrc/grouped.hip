@@ -32,11 +32,13 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr uint32_t kMfmaThreads = 256;                   // NE GEMM blocks
 constexpr uint32_t kMfmaWaves = kMfmaThreads / kWave;
 constexpr uint32_t kRowTiles = 4;                         // NE GEMM: tile rows per item
-// expert GEMM shape: positions 16 * kExpertNT, tile rows kExpertRT per item,
-// kExpertThreads per block (one block per CU)
+// expert GEMM shape: positions 16 * kExpertNT per block item, tile rows
+// kExpertRT per wave, kExpertThreads per block (one block per CU), MFMA
+// passes per product (hi*hi + hi*lo + lo*hi)
 constexpr int kExpertNT = 2;
 constexpr int kExpertRT = 4;
 constexpr int kExpertThreads = 512;
+constexpr int kExpertPasses = 3;
 constexpr uint32_t kPlaneRows16 = kExpertRows * 8 / 16;   // 16-byte rows of a plane
 constexpr uint32_t kSlotCapacity = 1024;
 
@@ -58,121 +60,141 @@ __device__ __forceinline__ uint32_t window64(uint32_t d0, uint32_t d1, uint32_t 
     return static_cast<uint32_t>(bits >> (48u - r)) & 0xFFFFu;
 }
 
+// w (w + 1) mod 2^16 in bits 0..15 for any 32-bit w whose low 16 bits are
+// the state: v_mad_u32_u24 reads 24 bits of each factor, and the bits above
+// bit 15 only add multiples of 2^16 (the compiler would otherwise pick the
+// quarter-rate v_mad_u64_u32 for the unmasked product).
+__device__ __forceinline__ uint32_t state_hash_low16(uint32_t w) {
+    uint32_t p;
+    asm("v_mad_u32_u24 %0, %1, %1, %1" : "=v"(p) : "v"(w));
+    return p;
+}
+
 __device__ __forceinline__ f32x4 mfma(half8 a, half8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 // ---- expert ---------------------------------------------------------------
+//
+// A block item is one routed slot's position group (16 * NT positions) times
+// 32 tile rows; wave w of the block takes tile rows 4w .. 4w + 3 of it. The
+// block loads each K step's B fragments (x_hat hi and lo of its positions)
+// once into an LDS ring that all eight waves read, with one barrier per K
+// step; each wave loads its own trellis words, four K steps ahead.
 
-template <int NT, int RT>
-struct ExpertStep {
-    half8 bh[NT], bl[NT];
-    uint32_t d0[RT], d1[RT];
-    uint32_t gamma[RT];  // f16 bits
-};
+constexpr uint32_t kBlockTileRows = kExpertRT * (kExpertThreads / kWave);  // 32
+constexpr uint32_t kBRowPitch = 80;  // bytes per B row in LDS: 64 of data, 16 of pad (no bank conflicts)
+constexpr uint32_t kGammaRow = kMaxTileColumns + kBlockTileRows;  // halves per gamma row
 
 // A buffer resource over `bytes` bytes at `base`: loads past the end return 0.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_over(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
 }
 
-// Everything about an item that does not change along K: buffer resources,
-// per-lane byte offsets (the K step advances the scalar offset only) and the
-// lane's window shifts.
-template <int NT, int RT>
-struct ExpertItem {
-    __amdgpu_buffer_rsrc_t xh, xl, words, gamma;
-    uint32_t xoff[NT];     // B fragment of position tile j at K step 0
-    uint32_t woff[RT];     // the lane's first stream dword of tile row t at K step 0
-    uint32_t wnext[RT];    // and its second (row 15 wraps to word 0)
-    uint32_t dgamma[RT];   // tr + tile column at K step 0
-    uint32_t gamma_top;    // R_t + C_t - 1
-    uint32_t tile_columns;
-    uint32_t sh0, sh1;     // shifts of the lane's two windows in the 64-bit string
-    uint32_t end, p0, tr0;
+// The trellis words of the wave's four tile rows at one K step.
+struct ExpertWords {
+    uint2 w[kExpertRT];  // the lane's two stream dwords of tile row t (row 15: dwords 10 and 11)
 };
 
-template <int NT, int RT>
-__device__ __forceinline__ void expert_load(const ExpertItem<NT, RT> &it, uint32_t kc,
-                                            ExpertStep<NT, RT> &s) {
-    const uint32_t kx = kc * 64u;   // 32 f16 of B per K step
+// Everything about a wave's share of a block item that does not change
+// along K: per-lane byte offsets (a K step advances the scalar offset only),
+// the lane's window shifts and its gamma row in LDS.
+struct ExpertWave {
+    __amdgpu_buffer_rsrc_t words;
+    uint32_t woff[kExpertRT];  // the lane's stream dword pair of tile row t at K step 0
+    const uint2 *gammas;       // gamma row kq of the block item, at the wave's first tile row
+    uint32_t sh0, sh1;         // shifts of the lane's two windows in the 64-bit string
+    bool row15;                // the lane holds tile row 15, whose last window wraps
+};
+
+__device__ __forceinline__ void expert_words(const ExpertWave &wv, uint32_t kc, ExpertWords &s) {
     const uint32_t kw = kc * 192u;  // 4 tiles of 48 bytes per K step
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-        s.bh[j] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(it.xh, it.xoff[j], kx, 0));
-        s.bl[j] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(it.xl, it.xoff[j], kx, 0));
-    }
-#pragma unroll
-    for (int t = 0; t < RT; ++t) {
-        s.d0[t] = __builtin_amdgcn_raw_buffer_load_b32(it.words, it.woff[t], kw, 0);
-        s.d1[t] = __builtin_amdgcn_raw_buffer_load_b32(it.words, it.wnext[t], kw, 0);
-        // wave slot of (tr, tc): R_t + C_t - 1 - d, one less past the main
-        // anti-diagonal (src/codec_cache.cpp:117-147)
-        const uint32_t d = it.dgamma[t] + 4u * kc;
-        const uint32_t slot = it.gamma_top - d - (d >= it.tile_columns ? 1u : 0u);
-        s.gamma[t] = __builtin_amdgcn_raw_buffer_load_b16(it.gamma, slot * 2u, 0, 0);
+    for (int t = 0; t < kExpertRT; ++t) {
+        s.w[t] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wv.words, wv.woff[t], kw, 0));
     }
 }
 
-template <int NT, int RT>
-__device__ __forceinline__ void expert_compute(const ExpertItem<NT, RT> &it, uint32_t sign_mask,
-                                               const uint2 *plane, const ExpertStep<NT, RT> &s,
-                                               f32x4 (&acc)[RT][NT]) {
+// Decodes the lane's A fragments of the wave's four tile rows at K step kc
+// and accumulates hi * bh + hi * bl + lo * bh (lo only when PASSES is 3).
+template <int NT, int PASSES>
+__device__ __forceinline__ void expert_compute(const ExpertWave &wv, uint32_t kc, uint32_t sign_mask,
+                                               const uint2 *plane, const ExpertWords &s,
+                                               const half8 (&bh)[NT], const half8 (&bl)[NT],
+                                               f32x4 (&acc)[kExpertRT][NT]) {
 #pragma clang fp contract(off)
+    // f16 gammas of the lane's tile in rows t = 0..3 at this K step
+    const uint2 graw = wv.gammas[kc];
 #pragma unroll
-    for (int t = 0; t < RT; ++t) {
+    for (int t = 0; t < kExpertRT; ++t) {
+        // row 15's second dword is dword 0 of its tile, which lane 0 of the
+        // same 16-lane row (the same tile) loaded first (row_ror:15 reads
+        // lane (i + 1) mod 16)
+        const uint32_t wrap = __builtin_amdgcn_update_dpp(0u, s.w[t].x, 0x12F, 0xF, 0xF, false);
+        const uint32_t d0 = wv.row15 ? s.w[t].y : s.w[t].x;
+        const uint32_t d1 = wv.row15 ? wrap : s.w[t].y;
         // the lane's four stream words, most significant bit first
-        const uint64_t bits = (static_cast<uint64_t>(__builtin_amdgcn_alignbit(s.d0[t], s.d0[t], 16)) << 32) |
-                              __builtin_amdgcn_alignbit(s.d1[t], s.d1[t], 16);
-        const uint32_t w0 = static_cast<uint32_t>(bits >> it.sh0) & 0xFFFFu;
-        const uint32_t w1 = static_cast<uint32_t>(bits >> it.sh1) & 0xFFFFu;
-        const uint32_t p0 = state_product(w0);
-        const uint32_t p1 = state_product(w1);
+        const uint64_t bits = (static_cast<uint64_t>(__builtin_amdgcn_alignbit(d0, d0, 16)) << 32) |
+                              __builtin_amdgcn_alignbit(d1, d1, 16);
+        const uint32_t p0 = state_hash_low16(static_cast<uint32_t>(bits >> wv.sh0));
+        const uint32_t p1 = state_hash_low16(static_cast<uint32_t>(bits >> wv.sh1));
         uint2 e0 = plane[(p0 >> 1) & 0x3FFFu];
         uint2 e1 = plane[(p1 >> 1) & 0x3FFFu];
         e0.x ^= p0 & sign_mask;
         e1.x ^= p1 & sign_mask;
         const half8 v = __builtin_bit_cast(half8, u32x4{e0.x, e0.y, e1.x, e1.y});
-        const _Float16 g = __builtin_bit_cast(_Float16, static_cast<uint16_t>(s.gamma[t]));
+        const uint32_t gpair = (t & 2) ? graw.y : graw.x;
+        const _Float16 g = __builtin_bit_cast(_Float16, static_cast<uint16_t>((t & 1) ? gpair >> 16 : gpair));
         const half8 gv = {g, g, g, g, g, g, g, g};
         const half8 hi = gv * v;
-        const half8 lo = __builtin_elementwise_fma(gv, v, -hi);
         // positions past the slot carry another slot's x_hat: their output
         // columns are computed and never stored
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            acc[t][j] = mfma(hi, s.bh[j], acc[t][j]);
+            acc[t][j] = mfma(hi, bh[j], acc[t][j]);
         }
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            acc[t][j] = mfma(hi, s.bl[j], acc[t][j]);
+            acc[t][j] = mfma(hi, bl[j], acc[t][j]);
         }
+        if constexpr (PASSES == 3) {
+            const half8 lo = __builtin_elementwise_fma(gv, v, -hi);
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            acc[t][j] = mfma(lo, s.bh[j], acc[t][j]);
+            for (int j = 0; j < NT; ++j) {
+                acc[t][j] = mfma(lo, bh[j], acc[t][j]);
+            }
         }
     }
 }
 
 // Block b serves codebook plane (b / 8) % 2 as worker ((b / 16) * 8 + b % 8)
 // (the two blocks that walk the same tiles share an XCD). Each block counts
-// the items of every routed slot (position groups x row groups) and scans the
-// counts in LDS, so the waves walk only real items, evenly. Items are numbered
-// (entry, slot, position group, row group), row group fastest, so the waves of
-// a block share B fragments in L1.
-template <int NT, int RT, int THREADS>
-__global__ __launch_bounds__(THREADS) void k_expert_mfma(ExpertMfmaJobs J) {
-    constexpr uint32_t kExpertThreads = THREADS;
-    constexpr uint32_t kExpertWaves = THREADS / kWave;
-    extern __shared__ uint4 lds_dynamic[];  // [kSlotCapacity] slots, item starts, plane
-    uint4 *slots = lds_dynamic;
-    uint32_t *starts = reinterpret_cast<uint32_t *>(lds_dynamic + kSlotCapacity);  // [kSlotCapacity + 1]
-    uint4 *plane_lds = lds_dynamic + kSlotCapacity + (kSlotCapacity + 16) / 4;
-    __shared__ uint32_t wave_sums[kExpertWaves];
+// the block items of every routed slot (position groups x row quarters) and
+// scans the counts in LDS, so the blocks walk only real items, evenly. Items
+// are numbered (entry, slot, position group, row quarter).
+template <int NT, int PASSES>
+__global__ __launch_bounds__(kExpertThreads) void k_expert_mfma(ExpertMfmaJobs J) {
+    static_assert(NT == 2, "the B ring is laid out for 32 positions");
+    constexpr uint32_t kWaves = kExpertThreads / kWave;
+    constexpr uint32_t kBRows = NT * 2u * 16u;            // (tile j, hi/lo, position) rows of B
+    constexpr uint32_t kBSlot = kBRows * kBRowPitch;      // bytes per K step in the ring
+    constexpr int kDepth = 4;                             // K steps of loads in flight
+    // static LDS with the plane first: its address is a compile-time
+    // constant, so a gather's address is the masked row offset alone
+    __shared__ uint4 plane_lds[kPlaneRows16];
+    __shared__ uint32_t starts[kSlotCapacity + 1];
+    __shared__ uint32_t wave_sums[kWaves];
+    // gamma rows of the block item: row q entry i = gamma of the tile at
+    // anti-diagonal tr_block + i + q, so lane (w, kq) reads the gammas of its
+    // four tile rows at K step kc as one 8-byte word at entry 4w + 4kc of row kq
+    __shared__ uint2 gamma_rows[4][kGammaRow / 4];
+    __shared__ uint4 b_ring[2][kBSlot / 16];
     const uint32_t b = blockIdx.x;
     const uint32_t half = (b >> 3) & 1u;
     const uint32_t worker = ((b >> 4) << 3) | (b & 7u);
     const uint32_t workers = gridDim.x >> 1;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     {
         const uint4 *src = static_cast<const uint4 *>(J.expert_book) + half * kPlaneRows16;
         // indexes past the plane are clamped: those threads reload and rewrite
@@ -185,6 +207,7 @@ __global__ __launch_bounds__(THREADS) void k_expert_mfma(ExpertMfmaJobs J) {
         }
         // item counts per slot: each thread owns two consecutive slots
         const uint32_t group = 16u * NT;
+        const uint32_t quarters = J.row_groups;
         uint32_t count[2];
 #pragma unroll
         for (uint32_t k = 0; k < 2; ++k) {
@@ -193,12 +216,10 @@ __global__ __launch_bounds__(THREADS) void k_expert_mfma(ExpertMfmaJobs J) {
             if (s < J.max_active) {
                 info = J.slot_info != nullptr ? J.slot_info[s]
                                               : make_uint4(0u, 0u, s == 0 ? J.max_positions : 0u, 0u);
-                slots[s] = info;
             }
-            count[k] = info.z > info.y ? (info.z - info.y + group - 1u) / group * J.row_groups : 0u;
+            count[k] = info.z > info.y ? (info.z - info.y + group - 1u) / group * quarters : 0u;
         }
         // block-wide exclusive scan of the counts (slot order)
-        const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
         const uint32_t own = count[0] + count[1];
         uint32_t inclusive = own;
 #pragma unroll
@@ -230,15 +251,21 @@ __global__ __launch_bounds__(THREADS) void k_expert_mfma(ExpertMfmaJobs J) {
         }
     }
     __syncthreads();
-    const uint32_t lane = threadIdx.x & 63u;
     const uint2 *plane = reinterpret_cast<const uint2 *>(plane_lds);
     const uint32_t per_entry = starts[kSlotCapacity];
     const uint32_t total = per_entry * J.expert_count;
-    const uint32_t stride = workers * kExpertWaves;
-    for (uint32_t i = worker * kExpertWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-         i < total; i += stride) {
-        const uint32_t which = i / per_entry;
-        const uint32_t local = i - which * per_entry;
+    const uint32_t m = lane & 15u, kq = lane >> 4;
+    const uint32_t sign_mask = half == 0 ? 0x8000u : 0u;
+    // the thread's share of the block's B loads: 8 bytes of one B row
+    // (rows 8w .. 8w + 7 for wave w, so the tile and the hi/lo plane are
+    // wave-uniform: derived from `wave`, the buffer resource stays scalar)
+    const uint32_t b_row = threadIdx.x >> 3, b_chunk = threadIdx.x & 7u;
+    const uint32_t b_j = wave >> 2, b_lo = (wave >> 1) & 1u, b_n = b_row & 15u;
+    char *ring = reinterpret_cast<char *>(b_ring);
+    const uint32_t b_store = b_row * kBRowPitch + b_chunk * 8u;
+    for (uint32_t item = worker; item < total; item += workers) {
+        const uint32_t which = item / per_entry;
+        const uint32_t local = item - which * per_entry;
         // the slot whose item range holds `local`: last s with starts[s] <= local
         uint32_t lo = 0, hi = J.max_active;
         while (hi - lo > 1u) {
@@ -251,83 +278,153 @@ __global__ __launch_bounds__(THREADS) void k_expert_mfma(ExpertMfmaJobs J) {
         }
         const uint32_t slot = __builtin_amdgcn_readfirstlane(lo);
         const uint32_t within = local - starts[slot];
-        const uint32_t rg = within % J.row_groups;
+        const uint32_t rq = within % J.row_groups;
         const uint32_t pg = within / J.row_groups;
-        const uint4 info = slots[slot];
+        // the slot is uniform: its entry comes through the scalar cache
+        const uint4 info = J.slot_info != nullptr ? J.slot_info[slot]
+                                                  : make_uint4(0u, 0u, J.max_positions, 0u);
         const uint32_t first = __builtin_amdgcn_readfirstlane(info.y);
         const uint32_t mat = __builtin_amdgcn_readfirstlane(info.x);
+        const uint32_t end = __builtin_amdgcn_readfirstlane(info.z);
         const ExpertMfma &a = J.expert[which];
-        ExpertItem<NT, RT> it;
-        it.end = __builtin_amdgcn_readfirstlane(info.z);
-        it.p0 = first + pg * 16u * NT;
-        it.tr0 = rg * RT;
-        const uint32_t m = lane & 15u, kq = lane >> 4;
+        const uint32_t p0 = first + pg * 16u * NT;
+        const uint32_t tr_block = rq * kBlockTileRows;
+        const uint32_t tr0 = tr_block + wave * kExpertRT;
         const uint32_t half_columns = a.columns >> 1;
         const uint32_t tile_columns = 1u << a.tc_shift;
+        const uint32_t steps = tile_columns / 4u;  // a power of two
+        const uint32_t last = steps - 1u;
+        // this thread's B row: position p0 + 16 b_j + b_n (clamped to a real
+        // row past the slot), hi or lo plane
         const size_t plane_elems = static_cast<size_t>(a.positions) * half_columns;
         const uint32_t x_bytes = static_cast<uint32_t>(plane_elems * 2u);
-        it.xh = buffer_over(a.x_hi + half * plane_elems, x_bytes);
-        it.xl = buffer_over(a.x_lo + half * plane_elems, x_bytes);
+        const __amdgpu_buffer_rsrc_t xsrc =
+            buffer_over((b_lo ? a.x_lo : a.x_hi) + half * plane_elems, x_bytes);
+        const uint32_t bp = p0 + 16u * b_j + b_n;
+        const uint32_t b_off = ((bp < end ? bp : p0) * half_columns + b_chunk * 4u) * 2u;
+        ExpertWave wv;
         const uint32_t tiles = a.tile_rows << a.tc_shift;
-        it.words = buffer_over(a.trellis + mat * a.trellis_stride, tiles * 48u);
-        it.gamma = buffer_over(a.gamma + mat * a.gamma_stride, (a.tile_rows + tile_columns) * 2u);
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            const uint32_t p = it.p0 + 16u * j + m;
-            const uint32_t pc = p < it.end ? p : it.p0;  // clamped: a real, finite row
-            it.xoff[j] = (pc * half_columns + kq * 8u) * 2u;
-        }
+        wv.words = buffer_over(a.trellis + mat * a.trellis_stride, tiles * 48u);
+        // the lane's states 2m, 2m + 1 start in dword dw = 24m / 32; row 15's
+        // second window wraps to dword 0 of its tile (src/expert_trellis.hpp:79-80),
+        // so that lane loads dwords 10 and 11 and takes dword 0 from lane 0
         const uint32_t dw = (24u * m) >> 5;
-        const uint32_t dn = dw == 11u ? 0u : dw + 1u;  // row 15 wraps to word 0 (src/expert_trellis.hpp:79-80)
+        wv.row15 = m == 15u;
+        const uint32_t dpair = wv.row15 ? 10u : dw;
 #pragma unroll
-        for (int t = 0; t < RT; ++t) {
-            const uint32_t tr = min(it.tr0 + t, a.tile_rows - 1u);
+        for (int t = 0; t < kExpertRT; ++t) {
+            const uint32_t tr = min(tr0 + t, a.tile_rows - 1u);
             const uint32_t tile = (tr << a.tc_shift) + kq;
-            it.woff[t] = (tile * 12u + dw) * 4u;
-            it.wnext[t] = (tile * 12u + dn) * 4u;
-            it.dgamma[t] = tr + kq;
+            wv.woff[t] = (tile * 12u + dpair) * 4u;
         }
-        it.gamma_top = a.tile_rows + tile_columns - 1u;
-        it.tile_columns = tile_columns;
-        const uint32_t pos = (24u * m) & 31u;  // bit of state 2m in the loaded words
-        it.sh0 = 48u - pos;
-        it.sh1 = 36u - pos;
-        f32x4 acc[RT][NT];
+        wv.gammas = gamma_rows[kq] + wave;  // entry 4 * wave
+        const uint32_t pos = (24u * m) & 31u;  // bit of state 2m in dword dw
+        wv.sh0 = 48u - pos;
+        wv.sh1 = 36u - pos;
+
+        // the previous item's readers of the gamma rows and the ring are done
+        __syncthreads();
+        {
+            // gamma of the tile at anti-diagonal d = tr_block + e sits in wave
+            // slot R_t + C_t - 1 - d, one less past the main anti-diagonal
+            // (src/codec_cache.cpp:117-147); slots past the matrix read 0 and
+            // belong to rows that are never stored
+            const __amdgpu_buffer_rsrc_t gbuf =
+                buffer_over(a.gamma + mat * a.gamma_stride, (a.tile_rows + tile_columns) * 2u);
+            const uint32_t top = a.tile_rows + tile_columns - 1u;
+            uint16_t *rows = reinterpret_cast<uint16_t *>(gamma_rows);
+            const uint32_t e = threadIdx.x;  // tile_columns + 31 <= kExpertThreads
+            const uint32_t d = tr_block + e;
+            const uint32_t gslot = top - d - (d >= tile_columns ? 1u : 0u);
+            const uint16_t g = __builtin_amdgcn_raw_buffer_load_b16(gbuf, gslot * 2u, 0, 0);
+            if (e < tile_columns + kBlockTileRows - 1u) {
 #pragma unroll
-        for (int t = 0; t < RT; ++t) {
+                for (uint32_t q = 0; q < 4u; ++q) {
+                    const uint32_t i = e - q;  // wraps past zero: then out of range
+                    if (i < kGammaRow) {
+                        rows[q * kGammaRow + i] = g;
+                    }
+                }
+            }
+        }
+        f32x4 acc[kExpertRT][NT];
+#pragma unroll
+        for (int t = 0; t < kExpertRT; ++t) {
 #pragma unroll
             for (int j = 0; j < NT; ++j) {
                 acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
         }
-        const uint32_t steps = tile_columns / 4u;  // a power of two
-        const uint32_t sign_mask = half == 0 ? 0x8000u : 0u;
-        ExpertStep<NT, RT> s0, s1;
-        expert_load<NT, RT>(it, 0, s0);
-        if (steps == 1) {
-            expert_compute<NT, RT>(it, sign_mask, plane, s0, acc);
+        // B of K step kc, as the MFMA operands of position tile j
+        auto read_b = [&](uint32_t ring_slot, half8 (&bh)[NT], half8 (&bl)[NT]) {
+            const char *base = ring + ring_slot * kBSlot + kq * 16u;
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                bh[j] = *reinterpret_cast<const half8 *>(base + (j * 32u + m) * kBRowPitch);
+                bl[j] = *reinterpret_cast<const half8 *>(base + (j * 32u + 16u + m) * kBRowPitch);
+            }
+        };
+        if (steps % kDepth != 0) {
+            // short K (under 4 steps): one step at a time
+            for (uint32_t kc = 0; kc < steps; ++kc) {
+                const uint2 bv = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(xsrc, b_off, kc * 64u, 0));
+                ExpertWords ws;
+                expert_words(wv, kc, ws);
+                *reinterpret_cast<uint2 *>(ring + b_store) = bv;
+                __syncthreads();
+                half8 bh[NT], bl[NT];
+                read_b(0, bh, bl);
+                expert_compute<NT, PASSES>(wv, kc, sign_mask, plane, ws, bh, bl, acc);
+                __syncthreads();
+            }
         } else {
-            // no branch inside the body, so the compiler's wait counts see
-            // that only the other stage's loads are outstanding; the last
-            // iteration reloads the final step (in bounds, unused)
-            for (uint32_t kc = 0; kc < steps; kc += 2) {
-                expert_load<NT, RT>(it, kc + 1, s1);
-                expert_compute<NT, RT>(it, sign_mask, plane, s0, acc);
-                expert_load<NT, RT>(it, min(kc + 2, steps - 1), s0);
-                expert_compute<NT, RT>(it, sign_mask, plane, s1, acc);
+            // B of step s waits in bv[s % 4] (registers) until step s - 1
+            // writes it to ring slot s % 2; the words of step s wait in
+            // ws[s % 4]. Loads past the last step reload it (in bounds,
+            // unused), so the loop body has no branch.
+            uint2 bv[kDepth];
+            ExpertWords ws[kDepth];
+#pragma unroll
+            for (int u = 0; u < kDepth; ++u) {
+                __builtin_amdgcn_sched_barrier(0);
+                bv[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(xsrc, b_off, u * 64u, 0));
+                if (u < kDepth - 1) {
+                    expert_words(wv, u, ws[u]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            *reinterpret_cast<uint2 *>(ring + b_store) = bv[0];
+            bv[0] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(xsrc, b_off, min(static_cast<uint32_t>(kDepth), last) * 64u, 0));
+            __syncthreads();
+            for (uint32_t kc = 0; kc < steps; kc += kDepth) {
+#pragma unroll
+                for (int u = 0; u < kDepth; ++u) {
+                    const uint32_t step = kc + u;
+                    __builtin_amdgcn_sched_barrier(0);
+                    // hand B of the next step to the ring and refill its registers
+                    *reinterpret_cast<uint2 *>(ring + ((u + 1) & 1) * kBSlot + b_store) = bv[(u + 1) % kDepth];
+                    bv[(u + 1) % kDepth] = __builtin_bit_cast(
+                        uint2, __builtin_amdgcn_raw_buffer_load_b64(xsrc, b_off, min(step + 1u + kDepth, last) * 64u, 0));
+                    expert_words(wv, min(step + kDepth - 1u, last), ws[(u + kDepth - 1) % kDepth]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    half8 bh[NT], bl[NT];
+                    read_b(u & 1, bh, bl);
+                    expert_compute<NT, PASSES>(wv, step, sign_mask, plane, ws[u], bh, bl, acc);
+                    __syncthreads();
+                }
             }
         }
         float *z = a.z + half * a.z_split_stride;
 #pragma unroll
-        for (uint32_t t = 0; t < RT; ++t) {
-            const uint32_t tr = it.tr0 + t;
+        for (uint32_t t = 0; t < kExpertRT; ++t) {
+            const uint32_t tr = tr0 + t;
             if (tr >= a.tile_rows) {
                 continue;
             }
 #pragma unroll
             for (int j = 0; j < NT; ++j) {
-                const uint32_t p = it.p0 + 16u * j + m;
-                if (p < it.end) {
+                const uint32_t p = p0 + 16u * j + m;
+                if (p < end) {
                     *reinterpret_cast<f32x4 *>(z + static_cast<size_t>(p) * a.rows + tr * kTile +
                                                kq * 4u) = acc[t][j];
                 }
@@ -489,25 +586,21 @@ void launch_expert_mfma(adi_hip_context *ctx, ExpertMfmaJobs &J) {
     require(J.max_active >= 1 && J.max_active <= kSlotCapacity, "MFMA GEMM: routed slots out of range");
     require(J.slot_info != nullptr || J.max_active == 1, "MFMA GEMM: routed slots need a slot table");
     const ExpertMfma &e = J.expert[0];
-    require(e.columns >= 64 && e.rows >= 16, "MFMA GEMM: expert matrix below 16 x 64");
+    require(expert_mfma_supports(e.rows, e.columns), "MFMA GEMM: expert matrix shape out of range");
     for (uint32_t i = 0; i < J.expert_count; ++i) {
         ExpertMfma &x = J.expert[i];
         require(x.rows == e.rows && x.columns == e.columns, "MFMA GEMM: expert entries differ in shape");
         x.tile_rows = x.rows / kTile;
         x.tc_shift = log2_of(x.columns / kTile);
     }
-    J.row_groups = ceil_div(e.rows / kTile, kExpertRT);
+    J.row_groups = ceil_div(e.rows / kTile, kBlockTileRows);  // row quarters of a block item
     J.position_groups = ceil_div(J.max_positions, 16u * kExpertNT);
     J.items = J.expert_count * J.max_active * J.position_groups * J.row_groups;  // upper bound
     const uint32_t cap = ctx->cu_count >= 16 ? ctx->cu_count / 16 * 16 : 16u;
-    const uint32_t needed = 16u * ceil_div(ceil_div(J.items, kExpertThreads / kWave), 8);
+    const uint32_t needed = 16u * ceil_div(J.items, 8u);
     const uint32_t blocks = needed < cap ? needed : cap;
-    const size_t lds = size_t(kSlotCapacity) * 16 + size_t(kSlotCapacity + 16) * 4 +
-                       size_t(kPlaneRows16) * 16;
-    auto kernel = k_expert_mfma<kExpertNT, kExpertRT, kExpertThreads>;
-    static const bool ready = set_lds_limit(reinterpret_cast<const void *>(kernel), lds);
-    (void)ready;
-    launch(ctx, "expert_mfma", kernel, dim3(blocks), dim3(kExpertThreads), lds, J);
+    auto kernel = k_expert_mfma<kExpertNT, kExpertPasses>;
+    launch(ctx, "expert_mfma", kernel, dim3(blocks), dim3(kExpertThreads), 0, J);
 }
 
 void launch_ne_mfma(adi_hip_context *ctx, NeMfmaJobs &J) {

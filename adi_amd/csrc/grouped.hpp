@@ -11,6 +11,14 @@ namespace adi_hip {
 // decode-GEMV.
 constexpr uint32_t kMfmaBatch = 64;
 
+// Widest expert matrix the MFMA GEMM takes, in 16-column tiles (its per-wave
+// gamma rows live in LDS).
+constexpr uint32_t kMaxTileColumns = 256;
+
+inline bool expert_mfma_supports(uint32_t rows, uint32_t columns) {
+    return rows >= 16 && columns >= 64 && columns / 16 <= kMaxTileColumns;
+}
+
 // One expert projection over the routed slots: Z[plane][p][r] for the
 // positions p of each active slot (x_hat in the codebook-plane order of
 // XhatOut, planes 2).

@@ -325,7 +325,8 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         const bool wave_path = wave_width(H) && wave_width(I);
         // prefill microbatches: MFMA grouped GEMMs over the expert-sorted
         // positions; decode batches: the persistent decode-GEMV
-        const bool mfma = wave_path && batch >= kMfmaBatch && H >= 64 && I >= 64;
+        const bool mfma = wave_path && batch >= kMfmaBatch && expert_mfma_supports(I, H) &&
+                          expert_mfma_supports(H, I);
         const uint32_t sg = mfma ? 2u : expert_splits(H);
         const uint32_t sd = mfma ? 2u : expert_splits(I);
         const uint32_t ssg = mfma ? ne_mfma_slices(I, H, batch) : ne_splits(H);

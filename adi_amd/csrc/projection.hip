@@ -888,7 +888,8 @@ int adi_hip_expert_matmul(adi_hip_context *ctx, const adi_hip_expert_matrix *m,
         validate_expert(m);
         require(batch > 0, "Mach expert batch shape mismatch");
         require(inputs != nullptr && outputs != nullptr, "Mach expert vector is null");
-        const bool mfma = batch >= kMfmaBatch && m->columns >= 64 && wave_width(m->columns);
+        const bool mfma = batch >= kMfmaBatch && expert_mfma_supports(m->rows, m->columns) &&
+                          wave_width(m->columns);
         const uint32_t splits = mfma ? 2u : expert_splits(m->columns);
         auto &ws = ctx->workspace;
         ws.used = 0;
