@@ -235,6 +235,164 @@ __global__ __launch_bounds__(64) void k_bf16_lds(
     }
 }
 
+// Register-tiled form of the same order for batches of many tokens: a block
+// of 128 threads holds 16 tokens x 16 rows; thread (lane l, tile group)
+// carries the chains of lane l for T tokens x R rows, so each operand read
+// from LDS feeds T or R multiply-adds. K is staged 256 columns at a time,
+// transposed to [token or row][lane][step] with a padded pitch, so a thread
+// reads four consecutive steps of its lane with one 16-byte read and the 16
+// (or 8) lanes of a read hit distinct banks. The lane sums are then added in
+// lane order from 0.0f, exactly as above. Needs columns % 256 == 0 and
+// 16-byte aligned operands.
+constexpr uint32_t kTiledChunk = 256;
+constexpr uint32_t kTiledBlock = 16;  // tokens and rows per block
+
+template <int LANES>
+struct TiledShape {
+    static constexpr uint32_t groups = 128 / LANES;                    // tile groups per lane
+    static constexpr uint32_t token_groups = LANES == 16 ? 2 : 4;
+    static constexpr uint32_t row_groups = groups / token_groups;      // 4
+    static constexpr uint32_t T = kTiledBlock / token_groups;          // tokens per thread
+    static constexpr uint32_t R = kTiledBlock / row_groups;            // rows per thread
+    static constexpr uint32_t steps = kTiledChunk / LANES;             // chunk steps per lane
+    static constexpr uint32_t pitch = steps + 4;                       // floats per [.][lane] row
+};
+
+template <int LANES, bool FUSED>
+__global__ __launch_bounds__(128) void k_bf16_tiled(
+    const uint16_t *__restrict__ w, uint32_t rows, const uint16_t *__restrict__ w_extra,
+    uint32_t columns, const float *__restrict__ x, uint32_t batch, float *__restrict__ out,
+    float *__restrict__ out_extra) {
+#pragma clang fp contract(off)
+    using S = TiledShape<LANES>;
+    __shared__ float xs[kTiledBlock][LANES][S::pitch];
+    __shared__ float ws[kTiledBlock][LANES][S::pitch];
+    const uint32_t total_rows = rows + (w_extra != nullptr ? 1u : 0u);
+    const uint32_t row0 = blockIdx.x * kTiledBlock;
+    const uint32_t t0 = blockIdx.y * kTiledBlock;
+    const uint32_t lane = threadIdx.x % LANES;
+    const uint32_t group = threadIdx.x / LANES;
+    const uint32_t tg = group / S::row_groups, rg = group % S::row_groups;
+    // staging: thread tid copies float4 number u * 128 + tid of the chunk's
+    // 16 x 256 x-block and uint4 (8 bf16) number u * 128 + tid of the
+    // w-block; rows and tokens past the ends are clamped to real ones (never
+    // stored)
+    float acc[S::T][S::R];
+#pragma unroll
+    for (uint32_t t = 0; t < S::T; ++t) {
+#pragma unroll
+        for (uint32_t r = 0; r < S::R; ++r) {
+            acc[t][r] = 0.0f;
+        }
+    }
+    // chunk c + 1 is loaded into registers while chunk c is multiplied
+    float4 xv[8];
+    uint4 wv[4];
+    auto load_chunk = [&](uint32_t c0) {
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) {
+            const uint32_t idx = u * 128u + threadIdx.x;  // 16 tokens x 64 float4
+            const uint32_t t = idx >> 6, k = (idx & 63u) * 4u;
+            const uint32_t tok = min(t0 + t, batch - 1u);
+            xv[u] = *reinterpret_cast<const float4 *>(x + static_cast<size_t>(tok) * columns + c0 + k);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const uint32_t idx = u * 128u + threadIdx.x;  // 16 rows x 32 uint4
+            const uint32_t r = idx >> 5, k = (idx & 31u) * 8u;
+            const uint32_t row = min(row0 + r, total_rows - 1u);
+            const uint16_t *src = row < rows ? w + static_cast<size_t>(row) * columns : w_extra;
+            wv[u] = *reinterpret_cast<const uint4 *>(src + c0 + k);
+        }
+    };
+    auto store_chunk = [&]() {
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) {
+            const uint32_t idx = u * 128u + threadIdx.x;
+            const uint32_t t = idx >> 6, k = (idx & 63u) * 4u;
+            const float e[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q) {
+                xs[t][(k + q) % LANES][(k + q) / LANES] = e[q];
+            }
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const uint32_t idx = u * 128u + threadIdx.x;
+            const uint32_t r = idx >> 5, k = (idx & 31u) * 8u;
+            const uint32_t e[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+#pragma unroll
+            for (uint32_t q = 0; q < 8; ++q) {
+                const uint32_t bits = q & 1u ? e[q / 2] >> 16 : e[q / 2] & 0xFFFFu;
+                ws[r][(k + q) % LANES][(k + q) / LANES] = bf16_bits_to_float(static_cast<uint16_t>(bits));
+            }
+        }
+    };
+    load_chunk(0);
+    store_chunk();
+    __syncthreads();
+    for (uint32_t c0 = 0; c0 < columns; c0 += kTiledChunk) {
+        // the last chunk reloads itself (in bounds, never staged)
+        load_chunk(c0 + kTiledChunk < columns ? c0 + kTiledChunk : c0);
+#pragma unroll 2
+        for (uint32_t i = 0; i < S::steps; i += 4) {
+            float4 xk[S::T], wk[S::R];
+#pragma unroll
+            for (uint32_t t = 0; t < S::T; ++t) {
+                xk[t] = *reinterpret_cast<const float4 *>(&xs[tg * S::T + t][lane][i]);
+            }
+#pragma unroll
+            for (uint32_t r = 0; r < S::R; ++r) {
+                wk[r] = *reinterpret_cast<const float4 *>(&ws[rg * S::R + r][lane][i]);
+            }
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q) {
+#pragma unroll
+                for (uint32_t t = 0; t < S::T; ++t) {
+#pragma unroll
+                    for (uint32_t r = 0; r < S::R; ++r) {
+                        acc[t][r] = lane_step<LANES, FUSED>(acc[t][r], wk[r][q], xk[t][q]);
+                    }
+                }
+            }
+        }
+        if (c0 + kTiledChunk < columns) {
+            __syncthreads();  // every reader of this chunk is done
+            store_chunk();
+            __syncthreads();
+        }
+    }
+    // ordered lane sums: the chains go to LDS (reusing xs), then each of the
+    // block's 256 outputs is finished by one thread
+    __syncthreads();
+    float *sums = &xs[0][0][0];  // [LANES][256] (16 * LANES * pitch >= 256 * LANES floats)
+#pragma unroll
+    for (uint32_t t = 0; t < S::T; ++t) {
+#pragma unroll
+        for (uint32_t r = 0; r < S::R; ++r) {
+            sums[lane * 256u + (tg * S::T + t) * kTiledBlock + rg * S::R + r] = acc[t][r];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t h = 0; h < 2; ++h) {
+        const uint32_t o = h * 128u + threadIdx.x;
+        const uint32_t t = o / kTiledBlock, r = o % kTiledBlock;
+        const uint32_t tok = t0 + t, row = row0 + r;
+        if (tok < batch && row < total_rows) {
+            float sum = 0.0f;
+            for (uint32_t j = 0; j < LANES; ++j) {
+                sum = sum + sums[j * 256u + o];
+            }
+            if (row < rows) {
+                out[static_cast<size_t>(tok) * rows + row] = sum;
+            } else {
+                out_extra[tok] = sum;
+            }
+        }
+    }
+}
+
 // The scalar order has one lane per row; its "lane sum" is 0 + the row sum,
 // so the generic kernel with LANES = 1 would need four lanes to finish four
 // tokens. This variant gives each thread one (row, token).
@@ -678,6 +836,20 @@ void launch_bf16_ordered_extra(adi_hip_context *ctx, const uint16_t *w, uint32_t
                                const uint16_t *w_extra, uint32_t columns, const float *x,
                                uint32_t batch, float *out, float *out_extra, uint32_t lanes) {
     const uint32_t total = rows + (w_extra != nullptr ? 1u : 0u);
+    const uintptr_t addresses = reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x) |
+                                reinterpret_cast<uintptr_t>(w_extra);
+    if ((lanes == 8 || lanes == 16) && batch >= kTiledBatch && columns % kTiledChunk == 0 &&
+        (addresses & 15u) == 0) {
+        const dim3 grid(ceil_div(total, kTiledBlock), ceil_div(batch, kTiledBlock));
+        if (lanes == 8) {
+            launch(ctx, "router", k_bf16_tiled<8, false>, grid, dim3(128), 0, w, rows, w_extra,
+                   columns, x, batch, out, out_extra);
+        } else {
+            launch(ctx, "router", k_bf16_tiled<16, true>, grid, dim3(128), 0, w, rows, w_extra,
+                   columns, x, batch, out, out_extra);
+        }
+        return;
+    }
     const dim3 tokens(ceil_div(batch, kTokensPerThread));
     const uint32_t rpb = lanes == 1 ? 1 : 64 / lanes;
     const size_t lds = size_t(kTokensPerThread) * columns * sizeof(float) +

@@ -55,6 +55,7 @@ void launch_route(adi_hip_context *ctx, const float *logits, const float *bias, 
                   uint32_t *route_expert, float *route_weight, const RouteSort &args);
 
 constexpr uint32_t kMaxExperts = 1024;
+constexpr uint32_t kTiledBatch = 32;  // batches from which the bf16 products run register-tiled
 constexpr uint32_t kRouteBatch = 16;  // largest batch launch_route handles in one block
 
 }  // namespace adi_hip

@@ -17,7 +17,10 @@ def bits(a):
 
 @pytest.mark.parametrize("isa", [1, 8, 16])
 @pytest.mark.parametrize("rows,columns,batch", [(256, 2048, 1), (256, 2048, 5), (1, 2048, 3),
-                                                (4, 67, 2), (37, 13, 9), (256, 2048, 128)])
+                                                (4, 67, 2), (37, 13, 9), (256, 2048, 128),
+                                                # register-tiled path: partial row and token
+                                                # blocks, several K chunks
+                                                (37, 512, 45), (256, 4096, 33), (20, 256, 64)])
 def test_bf16_matmul_bit_exact(gpu, oracle, isa, rows, columns, batch):
     rng = syn.rng_for(2, rows * 31 + columns + batch)
     w = syn.bf16_bits_rne(rng.normal(0, 0.02, (rows, columns)).astype(np.float32))
