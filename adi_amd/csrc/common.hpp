@@ -44,6 +44,13 @@ inline void check_hip(hipError_t error, const char *what) {
 
 inline bool is_power_of_two(uint32_t v) { return v != 0 && (v & (v - 1)) == 0; }
 
+// The wave-per-vector kernels move vectors of 512 or more elements with
+// 16-byte accesses (f32 vectors, 16-byte aligned), f16 scale rows with 8-byte
+// and +-1 sign rows with 4-byte accesses.
+inline bool aligned_to(const void *p, uintptr_t bytes) {
+    return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0;
+}
+
 // log2 of a power of two.
 inline uint32_t log2_of(uint32_t v) {
     uint32_t s = 0;
@@ -198,70 +205,202 @@ __device__ __forceinline__ float sum_over_quads(float v, uint32_t span) {
     return v;
 }
 
-// Normalised FWHT of n = 64*VPL values held by one wave, element e in lane
-// e % 64, register e / 64 (consecutive lanes hold consecutive elements, so
-// loads and stores coalesce and LDS staging is conflict-free). Strides 1..32
-// pair lanes l and l ^ stride; strides 64, 128, ... pair registers. Strides
-// run 1, 2, 4, ... and each pair becomes (lo + hi, lo - hi): the reference's
-// exact sequence (src/simd.cpp:48-63), so the result is bit-identical to it.
-// Every lane of the wave must call this.
+// Normalised FWHT of n = 64*VPL values held by one wave in the wave layout
+// (tiled_group_base: the tiled layout from VPL 8, element e in lane e % 64,
+// register e / 64 below). Each index bit's stride pairs either two registers
+// of a lane or lanes l and l ^ mask. Strides run 1, 2, 4, ... and each pair
+// becomes (lo + hi, lo - hi): the reference's exact sequence
+// (src/simd.cpp:48-63), so the result is bit-identical to it. Every lane of
+// the wave must call this.
 template <int VPL>
 __device__ __forceinline__ void wave_hadamard(float (&v)[VPL], float scale, uint32_t lane) {
 #pragma clang fp contract(off)
-    // All exchanges of a stage are issued before any is consumed so the
+    // One butterfly stage per index bit b, lower element of each pair a + b,
+    // upper a - b. The stages run in index-bit order (strides 1, 2, 4, ...),
+    // so the rounding is that of the in-place transform in that order. All
+    // exchanges of a lane stage are issued before any is consumed so the
     // LDS-routed ones (masks 16 and 32) pipeline instead of waiting in turn.
-#define ADI_XOR_STAGE(MASK)                                              \
+    // A lane stage gives the lower lane v + other and the upper other - v,
+    // both as fma(+-1, v, other): the product is exact, so the fma rounds
+    // the same sum once (x - x and -0 + -0 give the same zeros).
+#define ADI_LANE_STAGE(MASK)                                             \
     {                                                                    \
-        const bool upper = (lane & static_cast<uint32_t>(MASK)) != 0;    \
+        const float sign = (lane & static_cast<uint32_t>(MASK)) != 0 ? -1.0f : 1.0f; \
         float other[VPL];                                                \
         _Pragma("unroll") for (int i = 0; i < VPL; ++i) {                \
             other[i] = lane_xor<MASK>(v[i]);                             \
         }                                                                \
         _Pragma("unroll") for (int i = 0; i < VPL; ++i) {                \
-            v[i] = upper ? other[i] - v[i] : v[i] + other[i];            \
+            v[i] = __builtin_fmaf(sign, v[i], other[i]);                 \
         }                                                                \
     }
-    ADI_XOR_STAGE(1) ADI_XOR_STAGE(2) ADI_XOR_STAGE(4) ADI_XOR_STAGE(8)
-    ADI_XOR_STAGE(16) ADI_XOR_STAGE(32)
-#undef ADI_XOR_STAGE
+#define ADI_REG_STAGE(STRIDE)                                            \
+    {                                                                    \
+        _Pragma("unroll") for (int i = 0; i < VPL; ++i) {                \
+            if ((i & (STRIDE)) == 0) {                                   \
+                const float a = v[i];                                    \
+                const float b = v[i + (STRIDE)];                         \
+                v[i] = a + b;                                            \
+                v[i + (STRIDE)] = a - b;                                 \
+            }                                                            \
+        }                                                                \
+    }
+    if constexpr (VPL >= 8) {
+        // tiled layout: index bits 0, 1, 3 = register bits 0, 1, 2; bit 2 =
+        // register bit 3 (VPL >= 16) or lane bit 5; bits 4.. = lane bits, then
+        // register bits 4..
+        ADI_REG_STAGE(1) ADI_REG_STAGE(2)
+        if constexpr (VPL >= 16) {
+            ADI_REG_STAGE(8)
+        } else {
+            ADI_LANE_STAGE(32)
+        }
+        ADI_REG_STAGE(4)
+        ADI_LANE_STAGE(1) ADI_LANE_STAGE(2) ADI_LANE_STAGE(4) ADI_LANE_STAGE(8) ADI_LANE_STAGE(16)
+        if constexpr (VPL >= 16) {
+            ADI_LANE_STAGE(32)
+        }
 #pragma unroll
-    for (int stride = 1; stride < VPL; stride <<= 1) {
+        for (int stride = 16; stride < VPL; stride <<= 1) {
+            ADI_REG_STAGE(stride)
+        }
+    } else {
+        // c = 64 i + lane: the lane bits first, then the register bits
+        ADI_LANE_STAGE(1) ADI_LANE_STAGE(2) ADI_LANE_STAGE(4) ADI_LANE_STAGE(8)
+        ADI_LANE_STAGE(16) ADI_LANE_STAGE(32)
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            if ((i & stride) == 0) {
-                const float a = v[i];
-                const float b = v[i + stride];
-                v[i] = a + b;
-                v[i + stride] = a - b;
-            }
+        for (int stride = 1; stride < VPL; stride <<= 1) {
+            ADI_REG_STAGE(stride)
         }
     }
+#undef ADI_LANE_STAGE
+#undef ADI_REG_STAGE
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
         v[i] = v[i] * scale;
     }
 }
 
-// v[i] = sum over slices s < splits of src[s * stride + i * 64 + lane], added
-// in slice order; two slices are loaded per round so the loads overlap (one
-// for the widest vectors, whose registers would not hold two).
+
+// Tiled wave layout of an n = 64 * VPL vector (VPL >= 8) for the
+// wave-per-vector kernels. Register i of lane l holds element c(i, l) with
+//   c bits 0, 1 = i bits 0, 1;  c bit 3 = i bit 2;
+//   c bit 2     = i bit 3 (VPL >= 16) or l bit 5 (VPL == 8);
+//   c bits 4..  = the remaining lane bits, then the remaining register bits.
+// Registers 4g .. 4g + 3 are then four consecutive elements (one 16-byte
+// load or store) and registers 8k .. 8k + 7 are the eight columns that one
+// codebook plane covers in one 16-column tile, in plane order (one 16-byte
+// f16 store). Below VPL 8 the layout is c = 64 i + l.
+template <int VPL>
+__device__ __forceinline__ uint32_t tiled_group_base(uint32_t g, uint32_t lane) {
+    static_assert(VPL >= 8, "tiled layout needs 512 or more elements");
+    if constexpr (VPL >= 16) {
+        return ((g & 1u) << 3) | (((g >> 1) & 1u) << 2) | (lane << 4) | ((g >> 2) << 10);
+    } else {
+        return ((g & 1u) << 3) | ((lane >> 5) << 2) | ((lane & 31u) << 4);
+    }
+}
+
+// v = src in the wave layout (src 16-byte aligned when tiled).
+template <int VPL>
+__device__ __forceinline__ void load_wave(const float *src, uint32_t lane, float (&v)[VPL]) {
+    if constexpr (VPL >= 8) {
+#pragma unroll
+        for (int g = 0; g < VPL / 4; ++g) {
+            const float4 q = *reinterpret_cast<const float4 *>(src + tiled_group_base<VPL>(g, lane));
+            v[4 * g] = q.x;
+            v[4 * g + 1] = q.y;
+            v[4 * g + 2] = q.z;
+            v[4 * g + 3] = q.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            v[i] = src[i * 64 + lane];
+        }
+    }
+}
+
+// v = f16 src in the wave layout, widened (src 8-byte aligned when tiled).
+template <int VPL>
+__device__ __forceinline__ void load_wave_f16(const uint16_t *src, uint32_t lane, float (&v)[VPL]) {
+    if constexpr (VPL >= 8) {
+#pragma unroll
+        for (int g = 0; g < VPL / 4; ++g) {
+            const uint2 q = *reinterpret_cast<const uint2 *>(src + tiled_group_base<VPL>(g, lane));
+            v[4 * g] = half_bits_to_float(static_cast<uint16_t>(q.x));
+            v[4 * g + 1] = half_bits_to_float(static_cast<uint16_t>(q.x >> 16));
+            v[4 * g + 2] = half_bits_to_float(static_cast<uint16_t>(q.y));
+            v[4 * g + 3] = half_bits_to_float(static_cast<uint16_t>(q.y >> 16));
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            v[i] = half_bits_to_float(src[i * 64 + lane]);
+        }
+    }
+}
+
+// v = +-1 signs src in the wave layout (src 4-byte aligned when tiled).
+template <int VPL>
+__device__ __forceinline__ void load_wave_sign(const int8_t *src, uint32_t lane, float (&v)[VPL]) {
+    if constexpr (VPL >= 8) {
+#pragma unroll
+        for (int g = 0; g < VPL / 4; ++g) {
+            const uint32_t q = *reinterpret_cast<const uint32_t *>(src + tiled_group_base<VPL>(g, lane));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[4 * g + e] = static_cast<float>(static_cast<int8_t>(q >> (8 * e)));
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            v[i] = static_cast<float>(src[i * 64 + lane]);
+        }
+    }
+}
+
+// dst = v from the wave layout.
+template <int VPL>
+__device__ __forceinline__ void store_wave(float *dst, uint32_t lane, const float (&v)[VPL]) {
+    if constexpr (VPL >= 8) {
+#pragma unroll
+        for (int g = 0; g < VPL / 4; ++g) {
+            *reinterpret_cast<float4 *>(dst + tiled_group_base<VPL>(g, lane)) =
+                make_float4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            dst[i * 64 + lane] = v[i];
+        }
+    }
+}
+
+// v = sum over slices s < splits of src[s * stride ..] in the wave layout,
+// added in slice order; two slices are loaded per round so the loads overlap
+// (one for the widest vectors, whose registers would not hold two).
 template <int VPL>
 __device__ __forceinline__ void sum_slices(const float *src, size_t stride, uint32_t splits,
                                            uint32_t lane, float (&v)[VPL]) {
 #pragma clang fp contract(off)
-    src += lane;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
         v[i] = 0.0f;
     }
     constexpr uint32_t kRound = VPL > 32 ? 1u : 2u;
     for (uint32_t s = 0; s < splits; s += kRound) {
+        // a missing second slice reloads the first and adds zero
         const bool second = kRound == 2 && s + 1 < splits;
         float a[VPL], b[VPL];
+        load_wave<VPL>(src + s * stride, lane, a);
+        if constexpr (kRound == 2) {
+            load_wave<VPL>(src + (second ? s + 1 : s) * stride, lane, b);
+        }
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
-            a[i] = src[s * stride + i * 64];
-            b[i] = second ? src[(s + 1) * stride + i * 64] : 0.0f;
+            b[i] = second ? b[i] : 0.0f;
         }
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
@@ -298,28 +437,61 @@ __device__ __forceinline__ void store_xhat(const XhatOut &out, uint32_t vector, 
 #pragma clang fp contract(off)
     constexpr uint32_t n = 64u * VPL;
     if (out.planes == 0) {
-        float *dst = out.f32 + static_cast<size_t>(vector) * n + lane;
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            dst[i * 64] = v[i];
-        }
+        store_wave<VPL>(out.f32 + static_cast<size_t>(vector) * n, lane, v);
         return;
     }
+    if constexpr (VPL >= 8) {
+        uint32_t hi[VPL], lo[VPL];
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-        const uint32_t hi = f16_bits_rne(v[i]);
-        const uint32_t lo = f16_bits_rne(v[i] - half_bits_to_float(hi));
-        const uint32_t c = static_cast<uint32_t>(i) * 64u + lane;
-        size_t at;
-        if (out.planes == 1) {
-            at = static_cast<size_t>(vector) * n + c;
-        } else {
-            const uint32_t q = c & 15u;
-            at = static_cast<size_t>((q >> 2) & 1u) * out.vectors * (n / 2) +
-                 static_cast<size_t>(vector) * (n / 2) + (c >> 4) * 8u + (q >> 3) * 4u + (q & 3u);
+        for (int i = 0; i < VPL; ++i) {
+            hi[i] = f16_bits_rne(v[i]);
+            lo[i] = f16_bits_rne(v[i] - half_bits_to_float(hi[i]));
         }
-        out.hi[at] = static_cast<uint16_t>(hi);
-        out.lo[at] = static_cast<uint16_t>(lo);
+        if (out.planes == 1) {
+            // four consecutive columns per register group: 8-byte stores
+            uint16_t *dh = out.hi + static_cast<size_t>(vector) * n;
+            uint16_t *dl = out.lo + static_cast<size_t>(vector) * n;
+#pragma unroll
+            for (int g = 0; g < VPL / 4; ++g) {
+                const uint32_t c = tiled_group_base<VPL>(g, lane);
+                *reinterpret_cast<uint2 *>(dh + c) =
+                    make_uint2(hi[4 * g] | hi[4 * g + 1] << 16, hi[4 * g + 2] | hi[4 * g + 3] << 16);
+                *reinterpret_cast<uint2 *>(dl + c) =
+                    make_uint2(lo[4 * g] | lo[4 * g + 1] << 16, lo[4 * g + 2] | lo[4 * g + 3] << 16);
+            }
+        } else {
+            // registers 8k .. 8k + 7: one plane's columns of one tile, in
+            // plane order: 16-byte stores
+#pragma unroll
+            for (int k = 0; k < VPL / 8; ++k) {
+                const uint32_t c = tiled_group_base<VPL>(2 * k, lane);  // first column of the eight
+                const uint32_t plane = (c >> 2) & 1u, tile = c >> 4;
+                const size_t at = static_cast<size_t>(plane) * out.vectors * (n / 2) +
+                                  static_cast<size_t>(vector) * (n / 2) + tile * 8u;
+                const uint32_t *h = hi + 8 * k, *l = lo + 8 * k;
+                *reinterpret_cast<uint4 *>(out.hi + at) =
+                    make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
+                *reinterpret_cast<uint4 *>(out.lo + at) =
+                    make_uint4(l[0] | l[1] << 16, l[2] | l[3] << 16, l[4] | l[5] << 16, l[6] | l[7] << 16);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            const uint32_t hi = f16_bits_rne(v[i]);
+            const uint32_t lo = f16_bits_rne(v[i] - half_bits_to_float(hi));
+            const uint32_t c = static_cast<uint32_t>(i) * 64u + lane;
+            size_t at;
+            if (out.planes == 1) {
+                at = static_cast<size_t>(vector) * n + c;
+            } else {
+                const uint32_t q = c & 15u;
+                at = static_cast<size_t>((q >> 2) & 1u) * out.vectors * (n / 2) +
+                     static_cast<size_t>(vector) * (n / 2) + (c >> 4) * 8u + (q >> 3) * 4u + (q & 3u);
+            }
+            out.hi[at] = static_cast<uint16_t>(hi);
+            out.lo[at] = static_cast<uint16_t>(lo);
+        }
     }
 }
 

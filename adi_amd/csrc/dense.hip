@@ -739,21 +739,53 @@ __global__ __launch_bounds__(256) void k_route_hist(RouteSort a, uint32_t chunks
 }
 
 // One block: per-expert totals and offsets, the ascending active list and
-// slot table, each chunk's base within its expert, position_expert, and the
-// grouped index of every position (stable in (token, route) order: chunk
-// order, then rank within the chunk).
+// slot table, and each chunk's first grouped index per expert, written back
+// over chunk_hist (k_route_scatter then places the positions). The chunk
+// counts are staged in LDS with coalesced loads and each expert's scan over
+// the chunks is split into up to four ranges scanned by separate threads.
 __global__ __launch_bounds__(1024) void k_route_finalize(RouteSort a, uint32_t chunks) {
     extern __shared__ uint32_t base[];  // [chunks][experts]
     __shared__ uint32_t start[kMaxExperts];
+    __shared__ uint32_t part[4][kMaxExperts];
     __shared__ uint32_t sums[16];
     const uint32_t t = threadIdx.x;
-    const bool mine = t < a.experts;
+    const uint32_t E = a.experts;
+    const uint32_t cells = chunks * E;
+    for (uint32_t i = t; i < cells; i += blockDim.x) {
+        base[i] = a.chunk_hist[i];
+    }
+    __syncthreads();
+    // thread (q, e) = (t / E, t % E) scans chunks [q * per, (q + 1) * per)
+    const uint32_t ranges = E <= blockDim.x / 4u ? 4u : (E <= blockDim.x / 2u ? 2u : 1u);
+    const uint32_t per = (chunks + ranges - 1u) / ranges;
+    const uint32_t q = t / E, e_scan = t - q * E;
+    const bool scanner = q < ranges;
+    const uint32_t c_begin = scanner ? min(q * per, chunks) : 0u;
+    const uint32_t c_end = scanner ? min(c_begin + per, chunks) : 0u;
+    if (scanner) {
+        uint32_t running = 0;
+        for (uint32_t c = c_begin; c < c_end; ++c) {
+            const uint32_t v = base[c * E + e_scan];
+            base[c * E + e_scan] = running;
+            running += v;
+        }
+        part[q][e_scan] = running;
+    }
+    __syncthreads();
+    if (scanner && q > 0) {
+        uint32_t offset = 0;
+        for (uint32_t r = 0; r < q; ++r) {
+            offset += part[r][e_scan];
+        }
+        for (uint32_t c = c_begin; c < c_end; ++c) {
+            base[c * E + e_scan] += offset;
+        }
+    }
+    const bool mine = t < E;
     uint32_t total = 0;
     if (mine) {
-        for (uint32_t c = 0; c < chunks; ++c) {
-            const uint32_t v = a.chunk_hist[static_cast<size_t>(c) * a.experts + t];
-            base[c * a.experts + t] = total;
-            total += v;
+        for (uint32_t r = 0; r < ranges; ++r) {
+            total += part[r][t];
         }
     }
     uint32_t all = 0;
@@ -772,29 +804,37 @@ __global__ __launch_bounds__(1024) void k_route_finalize(RouteSort a, uint32_t c
                 a.slot_info[slot] = make_uint4(t, offset, offset + total, 0u);
             }
         }
-        if (a.position_expert != nullptr) {
-            for (uint32_t p = offset; p < offset + total; ++p) {
-                a.position_expert[p] = t;
-            }
-        }
     }
     if (t == 0) {
-        a.offsets[a.experts] = all;
+        a.offsets[E] = all;
         if (a.active_count != nullptr) {
             *a.active_count = active_total;
         }
     }
     if (a.slot_info != nullptr) {
-        for (uint32_t s = active_total + t; s < a.experts; s += blockDim.x) {
+        for (uint32_t s = active_total + t; s < E; s += blockDim.x) {
             a.slot_info[s] = make_uint4(0u, 0u, 0u, 0u);
         }
     }
     __syncthreads();
-    for (uint32_t i = t; i < a.positions; i += blockDim.x) {
-        const uint32_t e = a.route_expert[i];
-        const uint32_t g = start[e] + base[(i / kChunk) * a.experts + e] + a.position_rank[i];
-        a.grouped_batch[g] = i / 8u;
-        a.route_to_grouped[i] = g;
+    for (uint32_t i = t; i < cells; i += blockDim.x) {
+        a.chunk_hist[i] = start[i % E] + base[i];
+    }
+}
+
+// The grouped index of every position, stable in (token, route) order: its
+// chunk's first index for its expert plus its rank within the chunk.
+__global__ __launch_bounds__(256) void k_route_scatter(RouteSort a) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= a.positions) {
+        return;
+    }
+    const uint32_t e = a.route_expert[i];
+    const uint32_t g = a.chunk_hist[static_cast<size_t>(i / kChunk) * a.experts + e] + a.position_rank[i];
+    a.grouped_batch[g] = i / 8u;
+    a.route_to_grouped[i] = g;
+    if (a.position_expert != nullptr) {
+        a.position_expert[g] = e;
     }
 }
 
@@ -921,6 +961,8 @@ void launch_route_sort(adi_hip_context *ctx, const RouteSort &args) {
                                                 size_t(kFinalizeBases) * sizeof(uint32_t));
         (void)ready;
         launch(ctx, "route_sort", k_route_finalize, dim3(1), dim3(1024), lds, args, chunks);
+        launch(ctx, "route_scatter", k_route_scatter, dim3(ceil_div(args.positions, 256)), dim3(256), 0,
+               args);
         return;
     }
     launch(ctx, "route_sort", k_route_sort, dim3(1), dim3(64), 0, args);

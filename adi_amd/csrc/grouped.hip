@@ -22,6 +22,8 @@
 // MFMAs.
 #include "grouped.hpp"
 
+#include <type_traits>
+
 namespace adi_hip {
 namespace {
 
@@ -32,12 +34,12 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr uint32_t kMfmaThreads = 256;                   // NE GEMM blocks
 constexpr uint32_t kMfmaWaves = kMfmaThreads / kWave;
 constexpr uint32_t kRowTiles = 4;                         // NE GEMM: tile rows per item
-// expert GEMM shape: positions 16 * kExpertNT per block item, tile rows
-// kExpertRT per wave, kExpertThreads per block (one block per CU), MFMA
+// expert GEMM shape: positions 16 * kExpertNT per item, tile rows kExpertRT
+// per wave, 512 * kExpertGroups threads per block (one block per CU), MFMA
 // passes per product (hi*hi + hi*lo + lo*hi)
 constexpr int kExpertNT = 2;
 constexpr int kExpertRT = 4;
-constexpr int kExpertThreads = 512;
+constexpr int kExpertGroups = 1;  // wave groups of eight per block, each on its own item
 constexpr int kExpertPasses = 3;
 constexpr uint32_t kPlaneRows16 = kExpertRows * 8 / 16;   // 16-byte rows of a plane
 constexpr uint32_t kSlotCapacity = 1024;
@@ -76,13 +78,15 @@ __device__ __forceinline__ f32x4 mfma(half8 a, half8 b, f32x4 c) {
 
 // ---- expert ---------------------------------------------------------------
 //
-// A block item is one routed slot's position group (16 * NT positions) times
-// 32 tile rows; wave w of the block takes tile rows 4w .. 4w + 3 of it. The
-// block loads each K step's B fragments (x_hat hi and lo of its positions)
-// once into an LDS ring that all eight waves read, with one barrier per K
-// step; each wave loads its own trellis words, four K steps ahead.
+// An item is one routed slot's position group (16 * NT positions) times 32
+// tile rows of one entry. A block runs kExpertGroups wave groups of eight,
+// each on its own item; wave w of a group takes tile rows 4w .. 4w + 3 of it.
+// A group loads each K step's B fragments (x_hat hi and lo of its positions)
+// once into its LDS ring that its eight waves read; the block takes one
+// barrier per K step (all items of a launch have the same K). Each wave loads
+// its own trellis words, four K steps ahead.
 
-constexpr uint32_t kBlockTileRows = kExpertRT * (kExpertThreads / kWave);  // 32
+constexpr uint32_t kBlockTileRows = kExpertRT * 8;  // tile rows of an item (a wave group's share)
 constexpr uint32_t kBRowPitch = 80;  // bytes per B row in LDS: 64 of data, 16 of pad (no bank conflicts)
 constexpr uint32_t kGammaRow = kMaxTileColumns + kBlockTileRows;  // halves per gamma row
 
@@ -115,13 +119,17 @@ __device__ __forceinline__ void expert_words(const ExpertWave &wv, uint32_t kc, 
     }
 }
 
+// The lane's A fragments of the wave's four tile rows at one K step:
+// hi = f16(gamma * V) and lo = f16(gamma * V - hi).
+struct ExpertA {
+    half8 hi[kExpertRT], lo[kExpertRT];
+};
+
 // Decodes the lane's A fragments of the wave's four tile rows at K step kc
-// and accumulates hi * bh + hi * bl + lo * bh (lo only when PASSES is 3).
-template <int NT, int PASSES>
-__device__ __forceinline__ void expert_compute(const ExpertWave &wv, uint32_t kc, uint32_t sign_mask,
-                                               const uint2 *plane, const ExpertWords &s,
-                                               const half8 (&bh)[NT], const half8 (&bl)[NT],
-                                               f32x4 (&acc)[kExpertRT][NT]) {
+// (lo only when PASSES is 3).
+template <int PASSES>
+__device__ __forceinline__ void expert_decode(const ExpertWave &wv, uint32_t kc, uint32_t sign_mask,
+                                              const uint2 *plane, const ExpertWords &s, ExpertA &a) {
 #pragma clang fp contract(off)
     // f16 gammas of the lane's tile in rows t = 0..3 at this K step
     const uint2 graw = wv.gammas[kc];
@@ -146,22 +154,33 @@ __device__ __forceinline__ void expert_compute(const ExpertWave &wv, uint32_t kc
         const uint32_t gpair = (t & 2) ? graw.y : graw.x;
         const _Float16 g = __builtin_bit_cast(_Float16, static_cast<uint16_t>((t & 1) ? gpair >> 16 : gpair));
         const half8 gv = {g, g, g, g, g, g, g, g};
-        const half8 hi = gv * v;
-        // positions past the slot carry another slot's x_hat: their output
-        // columns are computed and never stored
+        a.hi[t] = gv * v;
+        if constexpr (PASSES == 3) {
+            a.lo[t] = __builtin_elementwise_fma(gv, v, -a.hi[t]);
+        }
+    }
+}
+
+// acc += hi * bh + hi * bl + lo * bh (lo only when PASSES is 3). Positions
+// past the slot carry another slot's x_hat: their output columns are
+// computed and never stored.
+template <int NT, int PASSES>
+__device__ __forceinline__ void expert_multiply(const ExpertA &a, const half8 (&bh)[NT],
+                                                const half8 (&bl)[NT], f32x4 (&acc)[kExpertRT][NT]) {
+#pragma unroll
+    for (int t = 0; t < kExpertRT; ++t) {
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            acc[t][j] = mfma(hi, bh[j], acc[t][j]);
+            acc[t][j] = mfma(a.hi[t], bh[j], acc[t][j]);
         }
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            acc[t][j] = mfma(hi, bl[j], acc[t][j]);
+            acc[t][j] = mfma(a.hi[t], bl[j], acc[t][j]);
         }
         if constexpr (PASSES == 3) {
-            const half8 lo = __builtin_elementwise_fma(gv, v, -hi);
 #pragma unroll
             for (int j = 0; j < NT; ++j) {
-                acc[t][j] = mfma(lo, bh[j], acc[t][j]);
+                acc[t][j] = mfma(a.lo[t], bh[j], acc[t][j]);
             }
         }
     }
@@ -169,13 +188,22 @@ __device__ __forceinline__ void expert_compute(const ExpertWave &wv, uint32_t kc
 
 // Block b serves codebook plane (b / 8) % 2 as worker ((b / 16) * 8 + b % 8)
 // (the two blocks that walk the same tiles share an XCD). Each block counts
-// the block items of every routed slot (position groups x row quarters) and
-// scans the counts in LDS, so the blocks walk only real items, evenly. Items
-// are numbered (entry, slot, position group, row quarter).
-template <int NT, int PASSES>
-__global__ __launch_bounds__(kExpertThreads) void k_expert_mfma(ExpertMfmaJobs J) {
-    static_assert(NT == 2, "the B ring is laid out for 32 positions");
+// the items of every routed slot (position groups x row quarters) and scans
+// the counts in LDS, so the blocks walk only real items, evenly. Items are
+// numbered (entry, slot, position group, row quarter); a block takes them
+// kExpertGroups at a time, and a group past the last item runs a copy of the
+// last one without storing it.
+template <int NT, int GROUPS, int PASSES>
+__global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) {
+    constexpr uint32_t kExpertThreads = 512 * GROUPS;
+    constexpr uint32_t kExpertGroups = GROUPS;
+    static_assert(NT == 2 || NT == 4, "items of 32 or 64 positions");
+    // a thread's share of a B row: 8 bytes (32 positions) or 16 (64)
+    using BChunk = std::conditional_t<NT == 2, uint2, uint4>;
+    constexpr uint32_t kThreadsPerRow = NT == 2 ? 8u : 4u;
+    constexpr uint32_t kChunkBytes = 64u / kThreadsPerRow;
     constexpr uint32_t kWaves = kExpertThreads / kWave;
+    constexpr uint32_t kGroupThreads = 512;
     constexpr uint32_t kBRows = NT * 2u * 16u;            // (tile j, hi/lo, position) rows of B
     constexpr uint32_t kBSlot = kBRows * kBRowPitch;      // bytes per K step in the ring
     constexpr int kDepth = 4;                             // K steps of loads in flight
@@ -187,14 +215,16 @@ __global__ __launch_bounds__(kExpertThreads) void k_expert_mfma(ExpertMfmaJobs J
     // gamma rows of the block item: row q entry i = gamma of the tile at
     // anti-diagonal tr_block + i + q, so lane (w, kq) reads the gammas of its
     // four tile rows at K step kc as one 8-byte word at entry 4w + 4kc of row kq
-    __shared__ uint2 gamma_rows[4][kGammaRow / 4];
-    __shared__ uint4 b_ring[2][kBSlot / 16];
+    __shared__ uint2 gamma_rows[kExpertGroups][4][kGammaRow / 4];
+    __shared__ uint4 b_ring[kExpertGroups][2][kBSlot / 16];
     const uint32_t b = blockIdx.x;
     const uint32_t half = (b >> 3) & 1u;
     const uint32_t worker = ((b >> 4) << 3) | (b & 7u);
     const uint32_t workers = gridDim.x >> 1;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t group = wave >> 3, gwave = wave & 7u;
+    const uint32_t gthread = threadIdx.x & (kGroupThreads - 1u);
     {
         const uint4 *src = static_cast<const uint4 *>(J.expert_book) + half * kPlaneRows16;
         // indexes past the plane are clamped: those threads reload and rewrite
@@ -256,14 +286,28 @@ __global__ __launch_bounds__(kExpertThreads) void k_expert_mfma(ExpertMfmaJobs J
     const uint32_t total = per_entry * J.expert_count;
     const uint32_t m = lane & 15u, kq = lane >> 4;
     const uint32_t sign_mask = half == 0 ? 0x8000u : 0u;
-    // the thread's share of the block's B loads: 8 bytes of one B row
-    // (rows 8w .. 8w + 7 for wave w, so the tile and the hi/lo plane are
-    // wave-uniform: derived from `wave`, the buffer resource stays scalar)
-    const uint32_t b_row = threadIdx.x >> 3, b_chunk = threadIdx.x & 7u;
-    const uint32_t b_j = wave >> 2, b_lo = (wave >> 1) & 1u, b_n = b_row & 15u;
-    char *ring = reinterpret_cast<char *>(b_ring);
-    const uint32_t b_store = b_row * kBRowPitch + b_chunk * 8u;
-    for (uint32_t item = worker; item < total; item += workers) {
+    // the thread's share of its group's B loads: one chunk of one B row
+    // (rows (64 / kThreadsPerRow) w .. for wave w of the group, so the tile
+    // and the hi/lo plane are wave-uniform: derived from `gwave`, the buffer
+    // resource stays scalar)
+    const uint32_t b_row = gthread / kThreadsPerRow, b_chunk = gthread % kThreadsPerRow;
+    const uint32_t b_j = NT == 2 ? gwave >> 2 : gwave >> 1;
+    const uint32_t b_lo = NT == 2 ? (gwave >> 1) & 1u : gwave & 1u;
+    const uint32_t b_n = b_row & 15u;
+    char *ring = reinterpret_cast<char *>(b_ring[group]);
+    const uint32_t b_store = b_row * kBRowPitch + b_chunk * kChunkBytes;
+    auto load_b = [](__amdgpu_buffer_rsrc_t src, uint32_t off, uint32_t soff) {
+        if constexpr (NT == 2) {
+            return __builtin_bit_cast(BChunk, __builtin_amdgcn_raw_buffer_load_b64(src, off, soff, 0));
+        } else {
+            return __builtin_bit_cast(BChunk, __builtin_amdgcn_raw_buffer_load_b128(src, off, soff, 0));
+        }
+    };
+    const uint32_t rounds = (total + kExpertGroups - 1u) / kExpertGroups;
+    for (uint32_t round = worker; round < rounds; round += workers) {
+        const uint32_t item_any = round * kExpertGroups + group;
+        const bool live = item_any < total;
+        const uint32_t item = live ? item_any : total - 1u;
         const uint32_t which = item / per_entry;
         const uint32_t local = item - which * per_entry;
         // the slot whose item range holds `local`: last s with starts[s] <= local
@@ -289,7 +333,7 @@ __global__ __launch_bounds__(kExpertThreads) void k_expert_mfma(ExpertMfmaJobs J
         const ExpertMfma &a = J.expert[which];
         const uint32_t p0 = first + pg * 16u * NT;
         const uint32_t tr_block = rq * kBlockTileRows;
-        const uint32_t tr0 = tr_block + wave * kExpertRT;
+        const uint32_t tr0 = tr_block + gwave * kExpertRT;
         const uint32_t half_columns = a.columns >> 1;
         const uint32_t tile_columns = 1u << a.tc_shift;
         const uint32_t steps = tile_columns / 4u;  // a power of two
@@ -301,7 +345,7 @@ __global__ __launch_bounds__(kExpertThreads) void k_expert_mfma(ExpertMfmaJobs J
         const __amdgpu_buffer_rsrc_t xsrc =
             buffer_over((b_lo ? a.x_lo : a.x_hi) + half * plane_elems, x_bytes);
         const uint32_t bp = p0 + 16u * b_j + b_n;
-        const uint32_t b_off = ((bp < end ? bp : p0) * half_columns + b_chunk * 4u) * 2u;
+        const uint32_t b_off = ((bp < end ? bp : p0) * half_columns + b_chunk * (kChunkBytes / 2u)) * 2u;
         ExpertWave wv;
         const uint32_t tiles = a.tile_rows << a.tc_shift;
         wv.words = buffer_over(a.trellis + mat * a.trellis_stride, tiles * 48u);
@@ -317,7 +361,7 @@ __global__ __launch_bounds__(kExpertThreads) void k_expert_mfma(ExpertMfmaJobs J
             const uint32_t tile = (tr << a.tc_shift) + kq;
             wv.woff[t] = (tile * 12u + dpair) * 4u;
         }
-        wv.gammas = gamma_rows[kq] + wave;  // entry 4 * wave
+        wv.gammas = gamma_rows[group][kq] + gwave;  // entry 4 * gwave
         const uint32_t pos = (24u * m) & 31u;  // bit of state 2m in dword dw
         wv.sh0 = 48u - pos;
         wv.sh1 = 36u - pos;
@@ -332,8 +376,8 @@ __global__ __launch_bounds__(kExpertThreads) void k_expert_mfma(ExpertMfmaJobs J
             const __amdgpu_buffer_rsrc_t gbuf =
                 buffer_over(a.gamma + mat * a.gamma_stride, (a.tile_rows + tile_columns) * 2u);
             const uint32_t top = a.tile_rows + tile_columns - 1u;
-            uint16_t *rows = reinterpret_cast<uint16_t *>(gamma_rows);
-            const uint32_t e = threadIdx.x;  // tile_columns + 31 <= kExpertThreads
+            uint16_t *rows = reinterpret_cast<uint16_t *>(gamma_rows[group]);
+            const uint32_t e = gthread;  // tile_columns + 31 <= 512
             const uint32_t d = tr_block + e;
             const uint32_t gslot = top - d - (d >= tile_columns ? 1u : 0u);
             const uint16_t g = __builtin_amdgcn_raw_buffer_load_b16(gbuf, gslot * 2u, 0, 0);
@@ -367,14 +411,16 @@ __global__ __launch_bounds__(kExpertThreads) void k_expert_mfma(ExpertMfmaJobs J
         if (steps % kDepth != 0) {
             // short K (under 4 steps): one step at a time
             for (uint32_t kc = 0; kc < steps; ++kc) {
-                const uint2 bv = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(xsrc, b_off, kc * 64u, 0));
+                const BChunk bv = load_b(xsrc, b_off, kc * 64u);
                 ExpertWords ws;
                 expert_words(wv, kc, ws);
-                *reinterpret_cast<uint2 *>(ring + b_store) = bv;
+                *reinterpret_cast<BChunk *>(ring + b_store) = bv;
                 __syncthreads();
                 half8 bh[NT], bl[NT];
                 read_b(0, bh, bl);
-                expert_compute<NT, PASSES>(wv, kc, sign_mask, plane, ws, bh, bl, acc);
+                ExpertA fa;
+                expert_decode<PASSES>(wv, kc, sign_mask, plane, ws, fa);
+                expert_multiply<NT, PASSES>(fa, bh, bl, acc);
                 __syncthreads();
             }
         } else {
@@ -382,19 +428,19 @@ __global__ __launch_bounds__(kExpertThreads) void k_expert_mfma(ExpertMfmaJobs J
             // writes it to ring slot s % 2; the words of step s wait in
             // ws[s % 4]. Loads past the last step reload it (in bounds,
             // unused), so the loop body has no branch.
-            uint2 bv[kDepth];
+            BChunk bv[kDepth];
             ExpertWords ws[kDepth];
 #pragma unroll
             for (int u = 0; u < kDepth; ++u) {
                 __builtin_amdgcn_sched_barrier(0);
-                bv[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(xsrc, b_off, u * 64u, 0));
+                bv[u] = load_b(xsrc, b_off, u * 64u);
                 if (u < kDepth - 1) {
                     expert_words(wv, u, ws[u]);
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
-            *reinterpret_cast<uint2 *>(ring + b_store) = bv[0];
-            bv[0] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(xsrc, b_off, min(static_cast<uint32_t>(kDepth), last) * 64u, 0));
+            *reinterpret_cast<BChunk *>(ring + b_store) = bv[0];
+            bv[0] = load_b(xsrc, b_off, min(static_cast<uint32_t>(kDepth), last) * 64u);
             __syncthreads();
             for (uint32_t kc = 0; kc < steps; kc += kDepth) {
 #pragma unroll
@@ -402,14 +448,15 @@ __global__ __launch_bounds__(kExpertThreads) void k_expert_mfma(ExpertMfmaJobs J
                     const uint32_t step = kc + u;
                     __builtin_amdgcn_sched_barrier(0);
                     // hand B of the next step to the ring and refill its registers
-                    *reinterpret_cast<uint2 *>(ring + ((u + 1) & 1) * kBSlot + b_store) = bv[(u + 1) % kDepth];
-                    bv[(u + 1) % kDepth] = __builtin_bit_cast(
-                        uint2, __builtin_amdgcn_raw_buffer_load_b64(xsrc, b_off, min(step + 1u + kDepth, last) * 64u, 0));
+                    *reinterpret_cast<BChunk *>(ring + ((u + 1) & 1) * kBSlot + b_store) = bv[(u + 1) % kDepth];
+                    bv[(u + 1) % kDepth] = load_b(xsrc, b_off, min(step + 1u + kDepth, last) * 64u);
                     expert_words(wv, min(step + kDepth - 1u, last), ws[(u + kDepth - 1) % kDepth]);
                     __builtin_amdgcn_sched_barrier(0);
                     half8 bh[NT], bl[NT];
                     read_b(u & 1, bh, bl);
-                    expert_compute<NT, PASSES>(wv, step, sign_mask, plane, ws[u], bh, bl, acc);
+                    ExpertA fa;
+                    expert_decode<PASSES>(wv, step, sign_mask, plane, ws[u], fa);
+                    expert_multiply<NT, PASSES>(fa, bh, bl, acc);
                     __syncthreads();
                 }
             }
@@ -418,7 +465,7 @@ __global__ __launch_bounds__(kExpertThreads) void k_expert_mfma(ExpertMfmaJobs J
 #pragma unroll
         for (uint32_t t = 0; t < kExpertRT; ++t) {
             const uint32_t tr = tr0 + t;
-            if (tr >= a.tile_rows) {
+            if (!live || tr >= a.tile_rows) {
                 continue;
             }
 #pragma unroll
@@ -597,10 +644,10 @@ void launch_expert_mfma(adi_hip_context *ctx, ExpertMfmaJobs &J) {
     J.position_groups = ceil_div(J.max_positions, 16u * kExpertNT);
     J.items = J.expert_count * J.max_active * J.position_groups * J.row_groups;  // upper bound
     const uint32_t cap = ctx->cu_count >= 16 ? ctx->cu_count / 16 * 16 : 16u;
-    const uint32_t needed = 16u * ceil_div(J.items, 8u);
+    const uint32_t needed = 16u * ceil_div(ceil_div(J.items, kExpertGroups), 8u);
     const uint32_t blocks = needed < cap ? needed : cap;
-    auto kernel = k_expert_mfma<kExpertNT, kExpertPasses>;
-    launch(ctx, "expert_mfma", kernel, dim3(blocks), dim3(kExpertThreads), 0, J);
+    auto kernel = k_expert_mfma<kExpertNT, kExpertGroups, kExpertPasses>;
+    launch(ctx, "expert_mfma", kernel, dim3(blocks), dim3(512 * kExpertGroups), 0, J);
 }
 
 void launch_ne_mfma(adi_hip_context *ctx, NeMfmaJobs &J) {

@@ -76,19 +76,15 @@ __global__ __launch_bounds__(256) void k_swiglu_wave(SwigluJobs j) {
     const size_t base = static_cast<size_t>(v) * n;
     // the scales are loaded with the slices, before the transforms
     const size_t mat = g.matrix_index != nullptr ? g.matrix_index[v] : 0u;
-    const size_t off = mat * n + lane;
     float sa[VPL], sb[VPL], sc[VPL];
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-        if (g.sv_gate_f16 != nullptr) {
-            sa[i] = half_bits_to_float(g.sv_gate_f16[off + i * 64]);
-            sb[i] = half_bits_to_float(g.sv_up_f16[off + i * 64]);
-            sc[i] = half_bits_to_float(g.su_down_f16[off + i * 64]);
-        } else {
-            sa[i] = static_cast<float>(g.sv_gate_sign[i * 64u + lane]);
-            sb[i] = static_cast<float>(g.sv_up_sign[i * 64u + lane]);
-            sc[i] = static_cast<float>(g.su_down_sign[i * 64u + lane]);
-        }
+    if (g.sv_gate_f16 != nullptr) {
+        load_wave_f16<VPL>(g.sv_gate_f16 + mat * n, lane, sa);
+        load_wave_f16<VPL>(g.sv_up_f16 + mat * n, lane, sb);
+        load_wave_f16<VPL>(g.su_down_f16 + mat * n, lane, sc);
+    } else {
+        load_wave_sign<VPL>(g.sv_gate_sign, lane, sa);
+        load_wave_sign<VPL>(g.sv_up_sign, lane, sb);
+        load_wave_sign<VPL>(g.su_down_sign, lane, sc);
     }
     float gv[VPL], uv[VPL];
     sum_slices<VPL>(g.z_gate + base, g.split_stride, g.splits, lane, gv);
@@ -142,20 +138,13 @@ __global__ __launch_bounds__(576) void k_combine_wave(CombineArgs a) {
         src = a.z_down + static_cast<size_t>(grouped) * n;
         splits = a.splits;
         stride = a.split_stride;
-        const uint16_t *sv = a.sv_down + static_cast<size_t>(expert) * n;
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            scale[i] = half_bits_to_float(sv[i * 64u + lane]);
-        }
+        load_wave_f16<VPL>(a.sv_down + static_cast<size_t>(expert) * n, lane, scale);
     } else {
         weight = sigmoid(a.shared_logit[b]);
         src = a.z_shared + static_cast<size_t>(b) * n;
         splits = a.shared_splits;
         stride = a.shared_split_stride;
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            scale[i] = static_cast<float>(a.sv_shared[i * 64u + lane]);
-        }
+        load_wave_sign<VPL>(a.sv_shared, lane, scale);
     }
     sum_slices<VPL>(src, stride, splits, lane, val);
     wave_hadamard<VPL>(val, a.scale, lane);
@@ -163,7 +152,9 @@ __global__ __launch_bounds__(576) void k_combine_wave(CombineArgs a) {
     for (int i = 0; i < VPL; ++i) {
         val[i] = weight * (val[i] * scale[i]);
     }
-    for (uint32_t r = 0; r < 9; ++r) {
+    // route order: acc = v0, acc += v1, ..., the last wave adds the shared
+    // expert's and stores the row
+    for (uint32_t r = 0; r < 8; ++r) {
         if (wave == r) {
 #pragma unroll
             for (int i = 0; i < VPL; ++i) {
@@ -172,9 +163,12 @@ __global__ __launch_bounds__(576) void k_combine_wave(CombineArgs a) {
         }
         __syncthreads();
     }
-    float *dst = a.out + static_cast<size_t>(b) * n;
-    for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
-        dst[k] = acc[k];
+    if (wave == 8) {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            val[i] = acc[i * 64u + lane] + val[i];
+        }
+        store_wave<VPL>(a.out + static_cast<size_t>(b) * n, lane, val);
     }
 }
 
@@ -293,6 +287,8 @@ void validate_layer(const adi_hip_moe_layer *L) {
         require(s->trellis != nullptr && s->su_f16 != nullptr && s->sv_f16 != nullptr &&
                     s->wave_gamma_f16 != nullptr,
                 "MoE expert stack tensor is null");
+        require(aligned_to(s->su_f16, 8) && aligned_to(s->sv_f16, 8),
+                "MoE expert scale rows must be 8-byte aligned");
     }
     require(L->expert_codebook != nullptr && L->expert_codebook->kind == adi_hip_codebook::expert,
             "MoE layer needs an expert codebook");
@@ -319,6 +315,7 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         validate_layer(L);
         require(batch > 0, "MoE batch shape mismatch");
         require(inputs != nullptr && outputs != nullptr, "MoE vector is null");
+        require(aligned_to(inputs, 16) && aligned_to(outputs, 16), "MoE vectors must be 16-byte aligned");
         const uint32_t H = L->hidden, I = L->expert_hidden, E = L->experts;
         const size_t B = batch, P = B * 8;
         const uint32_t max_active = static_cast<uint32_t>(P < E ? P : E);

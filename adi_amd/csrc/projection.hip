@@ -247,20 +247,16 @@ __global__ __launch_bounds__(256) void k_prologue_wave(PrologueJobs j) {
     const uint32_t n = 64u * VPL;
     const uint32_t src = g.source_row != nullptr ? g.source_row[v] : v;
     const uint32_t mat = g.matrix_index != nullptr ? g.matrix_index[v] : 0u;
-    const float *x = g.x + static_cast<size_t>(src) * n + lane;
-    float val[VPL];
+    float val[VPL], su[VPL];
+    load_wave<VPL>(g.x + static_cast<size_t>(src) * n, lane, val);
     if (g.su_f16 != nullptr) {
-        const uint16_t *su = g.su_f16 + static_cast<size_t>(mat) * g.su_stride + lane;
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            val[i] = x[i * 64] * half_bits_to_float(su[i * 64]);
-        }
+        load_wave_f16<VPL>(g.su_f16 + static_cast<size_t>(mat) * g.su_stride, lane, su);
     } else {
-        const int8_t *su = g.su_sign + lane;
+        load_wave_sign<VPL>(g.su_sign, lane, su);
+    }
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            val[i] = x[i * 64] * static_cast<float>(su[i * 64]);
-        }
+    for (int i = 0; i < VPL; ++i) {
+        val[i] = val[i] * su[i];
     }
     wave_hadamard<VPL>(val, j.scale, lane);
     store_xhat<VPL>(g.out, v, lane, val);
@@ -279,13 +275,19 @@ __global__ __launch_bounds__(256) void k_epilogue_wave(
     }
     const uint32_t n = 64u * VPL;
     float val[VPL];
+    float s[VPL];
+    if constexpr (sizeof(Scale) == 2) {
+        load_wave_f16<VPL>(reinterpret_cast<const uint16_t *>(sv), lane, s);
+    } else {
+        load_wave_sign<VPL>(reinterpret_cast<const int8_t *>(sv), lane, s);
+    }
     sum_slices<VPL>(z + static_cast<size_t>(v) * n, split_stride, splits, lane, val);
     wave_hadamard<VPL>(val, scale, lane);
-    float *dst = out + static_cast<size_t>(v) * n + lane;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-        dst[i * 64] = val[i] * scale_value<Scale>(sv[i * 64u + lane]);
+        val[i] = val[i] * s[i];
     }
+    store_wave<VPL>(out + static_cast<size_t>(v) * n, lane, val);
 }
 
 // In-place normalised FWHT of `count` vectors, one wave each (64 <= n <= 4096)
@@ -297,17 +299,11 @@ __global__ __launch_bounds__(256) void k_hadamard_wave(float *values, uint32_t c
     if (v >= count) {
         return;
     }
-    float *p = values + static_cast<size_t>(v) * 64u * VPL + lane;
+    float *p = values + static_cast<size_t>(v) * 64u * VPL;
     float val[VPL];
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-        val[i] = p[i * 64];
-    }
+    load_wave<VPL>(p, lane, val);
     wave_hadamard<VPL>(val, scale, lane);
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-        p[i * 64] = val[i];
-    }
+    store_wave<VPL>(p, lane, val);
 }
 
 __global__ __launch_bounds__(256) void k_hadamard_block(float *values, uint32_t n, float scale) {
@@ -708,6 +704,12 @@ void launch_prologues(adi_hip_context *ctx, PrologueJobs &jobs) {
         vectors += jobs.seg[s].count;
     }
     jobs.scale = hadamard_scale(jobs.n);
+    for (uint32_t s = 0; s < jobs.segments; ++s) {
+        const PrologueSegment &g = jobs.seg[s];
+        require(aligned_to(g.x, 16) && aligned_to(g.su_f16, 8) && aligned_to(g.su_sign, 4) &&
+                    aligned_to(g.out.f32, 16) && aligned_to(g.out.hi, 16) && aligned_to(g.out.lo, 16),
+                "vectors must be 16-byte aligned, f16 scale rows 8-byte and sign rows 4-byte");
+    }
     const dim3 grid(ceil_div(vectors, 4));
     switch (jobs.n) {
     case 64: launch(ctx, "hadamard_prologue", k_prologue_wave<1>, grid, dim3(256), 0, jobs); break;
@@ -739,6 +741,8 @@ void launch_epilogue_any(adi_hip_context *ctx, const float *z, uint32_t splits,
                          size_t split_stride, uint32_t n, const Scale *sv, uint32_t vectors,
                          float *out) {
     const float scale = hadamard_scale(n);
+    require(aligned_to(z, 16) && aligned_to(out, 16) && aligned_to(sv, sizeof(Scale) == 2 ? 8 : 4),
+            "vectors must be 16-byte aligned, f16 scale rows 8-byte and sign rows 4-byte");
     const dim3 grid(ceil_div(vectors, 4));
     switch (n) {
     case 64: launch(ctx, "hadamard_epilogue", k_epilogue_wave<1, Scale>, grid, dim3(256), 0, z, splits, split_stride, sv, vectors, scale, out); break;
@@ -874,6 +878,7 @@ void validate_ne(const adi_hip_ne_matrix *m) {
             "Mach NE codec tensor is null");
     require(m->codebook != nullptr && m->codebook->kind == adi_hip_codebook::ne,
             "Mach NE matrix needs an NE codebook");
+    require(aligned_to(m->su, 4) && aligned_to(m->sv, 4), "Mach NE sign rows must be 4-byte aligned");
 }
 
 }  // namespace adi_hip
@@ -1021,6 +1026,7 @@ int adi_hip_hadamard(adi_hip_context *ctx, float *values, uint32_t n, uint32_t c
     return guarded(ctx, [&] {
         require(values != nullptr && count > 0, "Hadamard vectors are null or empty");
         require(is_power_of_two(n) && n <= kMaxHadamard, "Hadamard width must be a power of two up to 8192");
+        require(n < 512 || aligned_to(values, 16), "Hadamard vectors must be 16-byte aligned");
         const float scale = hadamard_scale(n);
         const dim3 grid(ceil_div(count, 4));
         switch (n) {

@@ -103,10 +103,31 @@ def moe_bench(torch, hip, ctx, layers, x, bias, steps, warmup):
     return wall, float(np.mean(active)), prof
 
 
-def roofline_for(prof, steps, active):
+def kernel_flops(name, ubatch):
+    """Algorithmic flops of the mean launch of `name` (2 x rows x columns per
+    routed position), or None. expert_mfma runs twice per step: gate+up
+    (2 x 512 x 2048 per position) and down (2048 x 512); the mean launch is
+    1.5 projections of 8 * ubatch routed positions."""
+    if name == "expert_mfma":
+        return 1.5 * 2.0 * 8 * ubatch * EXPERT_HIDDEN * HIDDEN
+    return None
+
+
+def roofline_for(prof, steps, active, ubatch):
     total = sum(ms for _, ms in prof.values())
     ranked = sorted(prof.items(), key=lambda kv: -kv[1][1])
     for name, (launches, ms) in ranked:
+        flops = kernel_flops(name, ubatch)
+        if flops is not None:
+            avg_ms = ms / launches
+            achieved = flops / (avg_ms * 1e-3) / 1e12
+            return {
+                "kernel": name, "bound": "mfma", "achieved": round(achieved, 2),
+                "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                "avg_launch_us": round(avg_ms * 1e3, 2), "flops_per_launch": int(flops),
+                "share_of_step": round(ms / total, 3),
+            }
         nbytes = kernel_bytes(name, active)
         if nbytes is None:
             continue
@@ -244,7 +265,7 @@ def main():
             "layer_packed_bytes": int(layer_bytes),
             "layer_hbm_frac": round(layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "mfma_frac_equiv": round(FLOP_PER_TOKEN * u / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 5),
-            "roofline": roofline_for(prof, args.steps, active),
+            "roofline": roofline_for(prof, args.steps, active, u),
             "kernels_us_per_step": {k: round(v[1] * 1e3 / args.steps, 2) for k, v in
                                     sorted(prof.items(), key=lambda kv: -kv[1][1])},
         }
