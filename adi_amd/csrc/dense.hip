@@ -116,44 +116,46 @@ __global__ __launch_bounds__(64) void k_bf16_lds(
     const uintptr_t addresses = reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x) |
                                 reinterpret_cast<uintptr_t>(w_extra);
     if ((columns % 8u) == 0 && (addresses & 15u) == 0) {
-        // 16-byte staging; every load of a batch is issued before the first
-        // LDS store so the block waits for memory once per batch, not per load
-        constexpr uint32_t kBatch = 8;
+        // 16-byte staging in rounds: every load of a round (16 of the
+        // weight rows, 8 of the tokens; one round for a 4 x 2048 block and one
+        // token) is issued before the first LDS store, so the block waits for
+        // memory once per round. Indexes past the end are clamped to the last
+        // element: those lanes load it and store the same value again, so
+        // nothing is guarded.
+        constexpr uint32_t kWBatch = 16, kXBatch = 8;
         const uint32_t w_per_row = columns / 8u;
         const uint32_t w_total = rows_here * w_per_row;
-        // Indexes past the end are clamped to the last element: those lanes
-        // load it and store the same value again, so nothing is guarded and
-        // every load of a batch issues before the first store waits.
-        for (uint32_t f0 = 0; f0 < w_total; f0 += 64u * kBatch) {
-            uint4 v[kBatch];
-            uint32_t at[kBatch];
-#pragma unroll
-            for (uint32_t u = 0; u < kBatch; ++u) {
-                at[u] = min(f0 + u * 64u + threadIdx.x, w_total - 1u);
-                const uint32_t r = at[u] / w_per_row, k = at[u] - r * w_per_row;
-                const uint32_t row = row0 + r;
-                const uint16_t *src = row < rows ? w + static_cast<size_t>(row) * columns : w_extra;
-                v[u] = reinterpret_cast<const uint4 *>(src)[k];
-            }
-#pragma unroll
-            for (uint32_t u = 0; u < kBatch; ++u) {
-                reinterpret_cast<uint4 *>(ws)[at[u]] = v[u];
-            }
-        }
         const uint32_t x_per_row = columns / 4u;
         const uint32_t x_total = tokens * x_per_row;
         const float4 *xsrc = reinterpret_cast<const float4 *>(x + static_cast<size_t>(t0) * columns);
-        for (uint32_t f0 = 0; f0 < x_total; f0 += 64u * kBatch) {
-            float4 v[kBatch];
-            uint32_t at[kBatch];
+        for (uint32_t round = 0;; ++round) {
+            const uint32_t wf0 = round * 64u * kWBatch, xf0 = round * 64u * kXBatch;
+            if (wf0 >= w_total && xf0 >= x_total) {
+                break;
+            }
+            uint4 wv[kWBatch];
+            float4 xv[kXBatch];
+            uint32_t wat[kWBatch], xat[kXBatch];
 #pragma unroll
-            for (uint32_t u = 0; u < kBatch; ++u) {
-                at[u] = min(f0 + u * 64u + threadIdx.x, x_total - 1u);
-                v[u] = xsrc[at[u]];
+            for (uint32_t u = 0; u < kWBatch; ++u) {
+                wat[u] = min(wf0 + u * 64u + threadIdx.x, w_total - 1u);
+                const uint32_t r = wat[u] / w_per_row, k = wat[u] - r * w_per_row;
+                const uint32_t row = row0 + r;
+                const uint16_t *src = row < rows ? w + static_cast<size_t>(row) * columns : w_extra;
+                wv[u] = reinterpret_cast<const uint4 *>(src)[k];
             }
 #pragma unroll
-            for (uint32_t u = 0; u < kBatch; ++u) {
-                reinterpret_cast<float4 *>(xs)[at[u]] = v[u];
+            for (uint32_t u = 0; u < kXBatch; ++u) {
+                xat[u] = min(xf0 + u * 64u + threadIdx.x, x_total - 1u);
+                xv[u] = xsrc[xat[u]];
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < kWBatch; ++u) {
+                reinterpret_cast<uint4 *>(ws)[wat[u]] = wv[u];
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < kXBatch; ++u) {
+                reinterpret_cast<float4 *>(xs)[xat[u]] = xv[u];
             }
         }
     } else {

@@ -232,34 +232,7 @@ __device__ __forceinline__ float scale_at(const Scale *s, uint32_t k) {
 // Up to four segments of vectors, one wave each: x_hat = H_n(x[src] * su).
 template <int VPL>
 __global__ __launch_bounds__(256) void k_prologue_wave(PrologueJobs j) {
-#pragma clang fp contract(off)
-    const uint32_t lane = threadIdx.x & 63u;
-    uint32_t v = blockIdx.x * 4u + (threadIdx.x >> 6);
-    uint32_t s = 0;
-    while (s < j.segments && v >= j.seg[s].count) {
-        v -= j.seg[s].count;
-        ++s;
-    }
-    if (s >= j.segments) {
-        return;
-    }
-    const PrologueSegment &g = j.seg[s];
-    const uint32_t n = 64u * VPL;
-    const uint32_t src = g.source_row != nullptr ? g.source_row[v] : v;
-    const uint32_t mat = g.matrix_index != nullptr ? g.matrix_index[v] : 0u;
-    float val[VPL], su[VPL];
-    load_wave<VPL>(g.x + static_cast<size_t>(src) * n, lane, val);
-    if (g.su_f16 != nullptr) {
-        load_wave_f16<VPL>(g.su_f16 + static_cast<size_t>(mat) * g.su_stride, lane, su);
-    } else {
-        load_wave_sign<VPL>(g.su_sign, lane, su);
-    }
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-        val[i] = val[i] * su[i];
-    }
-    wave_hadamard<VPL>(val, j.scale, lane);
-    store_xhat<VPL>(g.out, v, lane, val);
+    prologue_vector<VPL>(j, blockIdx.x * 4u + (threadIdx.x >> 6), threadIdx.x & 63u);
 }
 
 // y = sv * H_n(sum over splits of z), one wave per vector.
@@ -698,11 +671,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_trellis_gemv(MoeGemv m) {
 
 bool wave_width(uint32_t n) { return n >= 64 && n <= 4096 && is_power_of_two(n); }
 
-void launch_prologues(adi_hip_context *ctx, PrologueJobs &jobs) {
-    uint32_t vectors = 0;
-    for (uint32_t s = 0; s < jobs.segments; ++s) {
-        vectors += jobs.seg[s].count;
-    }
+void prepare_prologues(PrologueJobs &jobs) {
     jobs.scale = hadamard_scale(jobs.n);
     for (uint32_t s = 0; s < jobs.segments; ++s) {
         const PrologueSegment &g = jobs.seg[s];
@@ -710,6 +679,14 @@ void launch_prologues(adi_hip_context *ctx, PrologueJobs &jobs) {
                     aligned_to(g.out.f32, 16) && aligned_to(g.out.hi, 16) && aligned_to(g.out.lo, 16),
                 "vectors must be 16-byte aligned, f16 scale rows 8-byte and sign rows 4-byte");
     }
+}
+
+void launch_prologues(adi_hip_context *ctx, PrologueJobs &jobs) {
+    uint32_t vectors = 0;
+    for (uint32_t s = 0; s < jobs.segments; ++s) {
+        vectors += jobs.seg[s].count;
+    }
+    prepare_prologues(jobs);
     const dim3 grid(ceil_div(vectors, 4));
     switch (jobs.n) {
     case 64: launch(ctx, "hadamard_prologue", k_prologue_wave<1>, grid, dim3(256), 0, jobs); break;

@@ -29,6 +29,41 @@ struct PrologueJobs {
 };
 bool wave_width(uint32_t n);
 void launch_prologues(adi_hip_context *ctx, PrologueJobs &jobs);
+// Checks the segments' alignment and sets jobs.scale (launch_prologues does
+// this itself; a fused launcher calls it before its own launch).
+void prepare_prologues(PrologueJobs &jobs);
+
+// x_hat = H_n(x[src] * su) of vector v of the jobs (segments in order), by
+// one wave; nothing past the last segment's vectors.
+template <int VPL>
+__device__ __forceinline__ void prologue_vector(const PrologueJobs &j, uint32_t v, uint32_t lane) {
+#pragma clang fp contract(off)
+    uint32_t s = 0;
+    while (s < j.segments && v >= j.seg[s].count) {
+        v -= j.seg[s].count;
+        ++s;
+    }
+    if (s >= j.segments) {
+        return;
+    }
+    const PrologueSegment &g = j.seg[s];
+    const uint32_t n = 64u * VPL;
+    const uint32_t src = g.source_row != nullptr ? g.source_row[v] : v;
+    const uint32_t mat = g.matrix_index != nullptr ? g.matrix_index[v] : 0u;
+    float val[VPL], su[VPL];
+    load_wave<VPL>(g.x + static_cast<size_t>(src) * n, lane, val);
+    if (g.su_f16 != nullptr) {
+        load_wave_f16<VPL>(g.su_f16 + static_cast<size_t>(mat) * g.su_stride, lane, su);
+    } else {
+        load_wave_sign<VPL>(g.su_sign, lane, su);
+    }
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        val[i] = val[i] * su[i];
+    }
+    wave_hadamard<VPL>(val, j.scale, lane);
+    store_xhat<VPL>(g.out, v, lane, val);
+}
 template <typename Scale>
 void launch_epilogue_any(adi_hip_context *ctx, const float *z, uint32_t splits,
                          size_t split_stride, uint32_t n, const Scale *sv, uint32_t vectors,
