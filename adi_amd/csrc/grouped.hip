@@ -34,11 +34,11 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr uint32_t kMfmaThreads = 256;                   // NE GEMM blocks
 constexpr uint32_t kMfmaWaves = kMfmaThreads / kWave;
 constexpr uint32_t kRowTiles = 4;                         // NE GEMM: tile rows per item
-// expert GEMM shape: positions 16 * kExpertNT per item, tile rows kExpertRT
-// per wave, 512 * kExpertGroups threads per block (one block per CU), MFMA
-// passes per product (hi*hi + hi*lo + lo*hi)
-constexpr int kExpertNT = 2;
+// expert GEMM shape: 32 positions per item, tile rows kExpertRT per wave,
+// 512 * kExpertGroups threads per block (one block per CU), MFMA passes per
+// product (hi*hi + hi*lo + lo*hi)
 constexpr int kExpertRT = 4;
+constexpr int kExpertCB = 1;      // blocks of 32 positions per item
 constexpr int kExpertGroups = 1;  // wave groups of eight per block, each on its own item
 constexpr int kExpertPasses = 3;
 constexpr uint32_t kPlaneRows16 = kExpertRows * 8 / 16;   // 16-byte rows of a plane
@@ -78,69 +78,87 @@ __device__ __forceinline__ f32x4 mfma(half8 a, half8 b, f32x4 c) {
 
 // ---- expert ---------------------------------------------------------------
 //
-// An item is one routed slot's position group (16 * NT positions) times 32
-// tile rows of one entry. A block runs kExpertGroups wave groups of eight,
-// each on its own item; wave w of a group takes tile rows 4w .. 4w + 3 of it.
-// A group loads each K step's B fragments (x_hat hi and lo of its positions)
-// once into its LDS ring that its eight waves read; the block takes one
-// barrier per K step (all items of a launch have the same K). Each wave loads
-// its own trellis words, four K steps ahead.
+// v_mfma_f32_32x32x16_f16 (on the box 1.6x the f16 rate of 16x16x32): lane l
+// holds A[l % 32][8 (l / 32) .. + 7], B[8 (l / 32) .. + 7][l % 32], and D
+// column l % 32, rows (r % 4) + 8 (r / 4) + 4 (l / 32) of register r.
+//
+// An item is one routed slot's 32 positions times 32 tile rows of one entry.
+// A block runs kExpertGroups wave groups of eight, each on its own item; wave
+// w of a group takes tile rows 4w .. 4w + 3 of it as two 32-row blocks. Lane
+// l holds row l % 16 of tile row 2 rb + (l % 32) / 16 of its block rb, and of
+// K pair c at K step kc the tile column 4 kc + 2 c + l / 32: its eight K
+// values (in the codebook-plane order of XhatOut planes 2) are the two
+// half-states of that row, two gathers from the LDS plane. A group loads each
+// K step's x_hat hi and lo of its positions once into its LDS ring that its
+// eight waves read; the block takes one barrier per K step (all items of a
+// launch have the same K). Each wave loads its own trellis words, four K
+// steps ahead.
 
 constexpr uint32_t kBlockTileRows = kExpertRT * 8;  // tile rows of an item (a wave group's share)
 constexpr uint32_t kBRowPitch = 80;  // bytes per B row in LDS: 64 of data, 16 of pad (no bank conflicts)
 constexpr uint32_t kGammaRow = kMaxTileColumns + kBlockTileRows;  // halves per gamma row
+constexpr int kFragments = 4;  // A fragments per K step: (row block, K pair)
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32(half8 a, half8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
 
 // A buffer resource over `bytes` bytes at `base`: loads past the end return 0.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_over(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
 }
 
-// The trellis words of the wave's four tile rows at one K step.
+// The trellis words of the lane's four tiles (fragment f = 2 rb + c) at one K
+// step: its two stream dwords (row 15: dwords 10 and 11).
 struct ExpertWords {
-    uint2 w[kExpertRT];  // the lane's two stream dwords of tile row t (row 15: dwords 10 and 11)
+    uint2 w[kFragments];
 };
 
-// Everything about a wave's share of a block item that does not change
-// along K: per-lane byte offsets (a K step advances the scalar offset only),
-// the lane's window shifts and its gamma row in LDS.
+// Everything about a wave's share of an item that does not change along K:
+// per-lane byte offsets (a K step advances the scalar offset only), the
+// lane's window shifts and its gamma row in LDS.
 struct ExpertWave {
     __amdgpu_buffer_rsrc_t words;
-    uint32_t woff[kExpertRT];  // the lane's stream dword pair of tile row t at K step 0
-    const uint2 *gammas;       // gamma row kq of the block item, at the wave's first tile row
-    uint32_t sh0, sh1;         // shifts of the lane's two windows in the 64-bit string
-    bool row15;                // the lane holds tile row 15, whose last window wraps
+    uint32_t woff[kFragments];  // the lane's stream dword pair of fragment f at K step 0
+    const uint2 *gammas;        // gamma row tsub + kh of the item, at the wave's first tile row
+    uint32_t sh0, sh1;          // shifts of the lane's two windows in the 64-bit string
+    bool row15;                 // the lane holds tile row 15, whose last window wraps
 };
 
 __device__ __forceinline__ void expert_words(const ExpertWave &wv, uint32_t kc, ExpertWords &s) {
     const uint32_t kw = kc * 192u;  // 4 tiles of 48 bytes per K step
 #pragma unroll
-    for (int t = 0; t < kExpertRT; ++t) {
-        s.w[t] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wv.words, wv.woff[t], kw, 0));
+    for (int f = 0; f < kFragments; ++f) {
+        s.w[f] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wv.words, wv.woff[f], kw, 0));
     }
 }
 
-// The lane's A fragments of the wave's four tile rows at one K step:
-// hi = f16(gamma * V) and lo = f16(gamma * V - hi).
+// The lane's A fragments at one K step: hi = f16(gamma * V) and
+// lo = f16(gamma * V - hi).
 struct ExpertA {
-    half8 hi[kExpertRT], lo[kExpertRT];
+    half8 hi[kFragments], lo[kFragments];
 };
 
-// Decodes the lane's A fragments of the wave's four tile rows at K step kc
-// (lo only when PASSES is 3).
+// Decodes the lane's A fragments at K step kc (lo only when PASSES is 3).
 template <int PASSES>
 __device__ __forceinline__ void expert_decode(const ExpertWave &wv, uint32_t kc, uint32_t sign_mask,
                                               const uint2 *plane, const ExpertWords &s, ExpertA &a) {
 #pragma clang fp contract(off)
-    // f16 gammas of the lane's tile in rows t = 0..3 at this K step
-    const uint2 graw = wv.gammas[kc];
+    // gammas of the lane's tiles: fragment (rb, c) sits 2 rb + 2 c anti-diagonals
+    // past the lane's first, so offsets 0, 2, 2, 4 of the lane's gamma row
+    const uint2 g03 = wv.gammas[kc];
+    const uint2 g47 = wv.gammas[kc + 1];
+    const uint32_t gbits[kFragments] = {g03.x & 0xFFFFu, g03.y & 0xFFFFu, g03.y & 0xFFFFu, g47.x & 0xFFFFu};
 #pragma unroll
-    for (int t = 0; t < kExpertRT; ++t) {
+    for (int f = 0; f < kFragments; ++f) {
         // row 15's second dword is dword 0 of its tile, which lane 0 of the
         // same 16-lane row (the same tile) loaded first (row_ror:15 reads
         // lane (i + 1) mod 16)
-        const uint32_t wrap = __builtin_amdgcn_update_dpp(0u, s.w[t].x, 0x12F, 0xF, 0xF, false);
-        const uint32_t d0 = wv.row15 ? s.w[t].y : s.w[t].x;
-        const uint32_t d1 = wv.row15 ? wrap : s.w[t].y;
+        const uint32_t wrap = __builtin_amdgcn_update_dpp(0u, s.w[f].x, 0x12F, 0xF, 0xF, false);
+        const uint32_t d0 = wv.row15 ? s.w[f].y : s.w[f].x;
+        const uint32_t d1 = wv.row15 ? wrap : s.w[f].y;
         // the lane's four stream words, most significant bit first
         const uint64_t bits = (static_cast<uint64_t>(__builtin_amdgcn_alignbit(d0, d0, 16)) << 32) |
                               __builtin_amdgcn_alignbit(d1, d1, 16);
@@ -151,36 +169,51 @@ __device__ __forceinline__ void expert_decode(const ExpertWave &wv, uint32_t kc,
         e0.x ^= p0 & sign_mask;
         e1.x ^= p1 & sign_mask;
         const half8 v = __builtin_bit_cast(half8, u32x4{e0.x, e0.y, e1.x, e1.y});
-        const uint32_t gpair = (t & 2) ? graw.y : graw.x;
-        const _Float16 g = __builtin_bit_cast(_Float16, static_cast<uint16_t>((t & 1) ? gpair >> 16 : gpair));
+        const _Float16 g = __builtin_bit_cast(_Float16, static_cast<uint16_t>(gbits[f]));
         const half8 gv = {g, g, g, g, g, g, g, g};
-        a.hi[t] = gv * v;
+        a.hi[f] = gv * v;
         if constexpr (PASSES == 3) {
-            a.lo[t] = __builtin_elementwise_fma(gv, v, -a.hi[t]);
+            a.lo[f] = __builtin_elementwise_fma(gv, v, -a.hi[f]);
         }
     }
 }
 
-// acc += hi * bh + hi * bl + lo * bh (lo only when PASSES is 3). Positions
-// past the slot carry another slot's x_hat: their output columns are
-// computed and never stored.
-template <int NT, int PASSES>
-__device__ __forceinline__ void expert_multiply(const ExpertA &a, const half8 (&bh)[NT],
-                                                const half8 (&bl)[NT], f32x4 (&acc)[kExpertRT][NT]) {
+// acc[rb][cb] += hi * bh + hi * bl + lo * bh over the two K pairs, for the
+// item's CB blocks of 32 positions (lo only when PASSES is 3). Positions past
+// the slot carry another slot's x_hat: their output columns are computed and
+// never stored.
+template <int CB, int PASSES>
+__device__ __forceinline__ void expert_multiply(const ExpertA &a, const half8 (&bh)[CB][2],
+                                                const half8 (&bl)[CB][2], f32x16 (&acc)[2][CB]) {
 #pragma unroll
-    for (int t = 0; t < kExpertRT; ++t) {
+    for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            acc[t][j] = mfma(a.hi[t], bh[j], acc[t][j]);
+        for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                acc[rb][cb] = mfma32(a.hi[2 * rb + c], bh[cb][c], acc[rb][cb]);
+            }
         }
+    }
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            acc[t][j] = mfma(a.hi[t], bl[j], acc[t][j]);
+    for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                acc[rb][cb] = mfma32(a.hi[2 * rb + c], bl[cb][c], acc[rb][cb]);
+            }
         }
-        if constexpr (PASSES == 3) {
+    }
+    if constexpr (PASSES == 3) {
 #pragma unroll
-            for (int j = 0; j < NT; ++j) {
-                acc[t][j] = mfma(a.lo[t], bh[j], acc[t][j]);
+        for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    acc[rb][cb] = mfma32(a.lo[2 * rb + c], bh[cb][c], acc[rb][cb]);
+                }
             }
         }
     }
@@ -193,18 +226,19 @@ __device__ __forceinline__ void expert_multiply(const ExpertA &a, const half8 (&
 // numbered (entry, slot, position group, row quarter); a block takes them
 // kExpertGroups at a time, and a group past the last item runs a copy of the
 // last one without storing it.
-template <int NT, int GROUPS, int PASSES>
+template <int CB, int GROUPS, int PASSES>
 __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) {
+    static_assert(CB == 1 || CB == 2, "items of 32 or 64 positions");
     constexpr uint32_t kExpertThreads = 512 * GROUPS;
     constexpr uint32_t kExpertGroups = GROUPS;
-    static_assert(NT == 2 || NT == 4, "items of 32 or 64 positions");
-    // a thread's share of a B row: 8 bytes (32 positions) or 16 (64)
-    using BChunk = std::conditional_t<NT == 2, uint2, uint4>;
-    constexpr uint32_t kThreadsPerRow = NT == 2 ? 8u : 4u;
+    constexpr uint32_t kPositions = 32 * CB;              // per item
+    // a thread's share of a K step's B rows: 8 bytes (32 positions) or 16 (64)
+    using BChunk = std::conditional_t<CB == 1, uint2, uint4>;
+    constexpr uint32_t kThreadsPerRow = CB == 1 ? 8u : 4u;
     constexpr uint32_t kChunkBytes = 64u / kThreadsPerRow;
     constexpr uint32_t kWaves = kExpertThreads / kWave;
     constexpr uint32_t kGroupThreads = 512;
-    constexpr uint32_t kBRows = NT * 2u * 16u;            // (tile j, hi/lo, position) rows of B
+    constexpr uint32_t kBRows = 2u * kPositions;          // (hi/lo, position) rows of B
     constexpr uint32_t kBSlot = kBRows * kBRowPitch;      // bytes per K step in the ring
     constexpr int kDepth = 4;                             // K steps of loads in flight
     // static LDS with the plane first: its address is a compile-time
@@ -212,9 +246,9 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
     __shared__ uint4 plane_lds[kPlaneRows16];
     __shared__ uint32_t starts[kSlotCapacity + 1];
     __shared__ uint32_t wave_sums[kWaves];
-    // gamma rows of the block item: row q entry i = gamma of the tile at
-    // anti-diagonal tr_block + i + q, so lane (w, kq) reads the gammas of its
-    // four tile rows at K step kc as one 8-byte word at entry 4w + 4kc of row kq
+    // gamma rows of an item: row q entry i = gamma of the tile at
+    // anti-diagonal tr_block + i + q; lane (w, tsub, kh) reads its tiles'
+    // gammas at K step kc from row tsub + kh at entries 4w + 4kc .. + 7
     __shared__ uint2 gamma_rows[kExpertGroups][4][kGammaRow / 4];
     __shared__ uint4 b_ring[kExpertGroups][2][kBSlot / 16];
     const uint32_t b = blockIdx.x;
@@ -236,7 +270,6 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
             v[u] = src[min(u * kExpertThreads + threadIdx.x, kPlaneRows16 - 1u)];
         }
         // item counts per slot: each thread owns two consecutive slots
-        const uint32_t group = 16u * NT;
         const uint32_t quarters = J.row_groups;
         uint32_t count[2];
 #pragma unroll
@@ -247,7 +280,7 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
                 info = J.slot_info != nullptr ? J.slot_info[s]
                                               : make_uint4(0u, 0u, s == 0 ? J.max_positions : 0u, 0u);
             }
-            count[k] = info.z > info.y ? (info.z - info.y + group - 1u) / group * quarters : 0u;
+            count[k] = info.z > info.y ? (info.z - info.y + kPositions - 1u) / kPositions * quarters : 0u;
         }
         // block-wide exclusive scan of the counts (slot order)
         const uint32_t own = count[0] + count[1];
@@ -284,20 +317,19 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
     const uint2 *plane = reinterpret_cast<const uint2 *>(plane_lds);
     const uint32_t per_entry = starts[kSlotCapacity];
     const uint32_t total = per_entry * J.expert_count;
-    const uint32_t m = lane & 15u, kq = lane >> 4;
+    const uint32_t m = lane & 31u, kh = lane >> 5;   // MFMA row / column and K half
+    const uint32_t trow = m & 15u, tsub = m >> 4;    // row within the tile, tile row within the block
     const uint32_t sign_mask = half == 0 ? 0x8000u : 0u;
-    // the thread's share of its group's B loads: one chunk of one B row
-    // (rows (64 / kThreadsPerRow) w .. for wave w of the group, so the tile
-    // and the hi/lo plane are wave-uniform: derived from `gwave`, the buffer
-    // resource stays scalar)
+    // the thread's share of its group's B loads: one chunk of one B row (B
+    // rows are (hi/lo, position); wave w of the group loads rows
+    // (64 / kThreadsPerRow) w .., so the hi/lo plane is wave-uniform: derived
+    // from `gwave`, the buffer resource stays scalar)
     const uint32_t b_row = gthread / kThreadsPerRow, b_chunk = gthread % kThreadsPerRow;
-    const uint32_t b_j = NT == 2 ? gwave >> 2 : gwave >> 1;
-    const uint32_t b_lo = NT == 2 ? (gwave >> 1) & 1u : gwave & 1u;
-    const uint32_t b_n = b_row & 15u;
+    const uint32_t b_lo = gwave >> 2, b_n = b_row & (kPositions - 1u);
     char *ring = reinterpret_cast<char *>(b_ring[group]);
     const uint32_t b_store = b_row * kBRowPitch + b_chunk * kChunkBytes;
     auto load_b = [](__amdgpu_buffer_rsrc_t src, uint32_t off, uint32_t soff) {
-        if constexpr (NT == 2) {
+        if constexpr (CB == 1) {
             return __builtin_bit_cast(BChunk, __builtin_amdgcn_raw_buffer_load_b64(src, off, soff, 0));
         } else {
             return __builtin_bit_cast(BChunk, __builtin_amdgcn_raw_buffer_load_b128(src, off, soff, 0));
@@ -331,38 +363,40 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
         const uint32_t mat = __builtin_amdgcn_readfirstlane(info.x);
         const uint32_t end = __builtin_amdgcn_readfirstlane(info.z);
         const ExpertMfma &a = J.expert[which];
-        const uint32_t p0 = first + pg * 16u * NT;
+        const uint32_t p0 = first + pg * kPositions;
         const uint32_t tr_block = rq * kBlockTileRows;
         const uint32_t tr0 = tr_block + gwave * kExpertRT;
         const uint32_t half_columns = a.columns >> 1;
         const uint32_t tile_columns = 1u << a.tc_shift;
         const uint32_t steps = tile_columns / 4u;  // a power of two
         const uint32_t last = steps - 1u;
-        // this thread's B row: position p0 + 16 b_j + b_n (clamped to a real
-        // row past the slot), hi or lo plane
+        // this thread's B row: position p0 + b_n (clamped to a real row past
+        // the slot), hi or lo plane
         const size_t plane_elems = static_cast<size_t>(a.positions) * half_columns;
         const uint32_t x_bytes = static_cast<uint32_t>(plane_elems * 2u);
         const __amdgpu_buffer_rsrc_t xsrc =
             buffer_over((b_lo ? a.x_lo : a.x_hi) + half * plane_elems, x_bytes);
-        const uint32_t bp = p0 + 16u * b_j + b_n;
+        const uint32_t bp = p0 + b_n;
         const uint32_t b_off = ((bp < end ? bp : p0) * half_columns + b_chunk * (kChunkBytes / 2u)) * 2u;
         ExpertWave wv;
         const uint32_t tiles = a.tile_rows << a.tc_shift;
         wv.words = buffer_over(a.trellis + mat * a.trellis_stride, tiles * 48u);
-        // the lane's states 2m, 2m + 1 start in dword dw = 24m / 32; row 15's
-        // second window wraps to dword 0 of its tile (src/expert_trellis.hpp:79-80),
-        // so that lane loads dwords 10 and 11 and takes dword 0 from lane 0
-        const uint32_t dw = (24u * m) >> 5;
-        wv.row15 = m == 15u;
+        // the lane's states 2 trow, 2 trow + 1 start in dword dw = 24 trow / 32;
+        // row 15's second window wraps to dword 0 of its tile
+        // (src/expert_trellis.hpp:79-80), so that lane loads dwords 10 and 11
+        // and takes dword 0 from lane 0 of its 16-lane row
+        const uint32_t dw = (24u * trow) >> 5;
+        wv.row15 = trow == 15u;
         const uint32_t dpair = wv.row15 ? 10u : dw;
 #pragma unroll
-        for (int t = 0; t < kExpertRT; ++t) {
-            const uint32_t tr = min(tr0 + t, a.tile_rows - 1u);
-            const uint32_t tile = (tr << a.tc_shift) + kq;
-            wv.woff[t] = (tile * 12u + dpair) * 4u;
+        for (int f = 0; f < kFragments; ++f) {
+            const uint32_t rb = f >> 1, c = f & 1;
+            const uint32_t tr = min(tr0 + 2u * rb + tsub, a.tile_rows - 1u);
+            const uint32_t tile = (tr << a.tc_shift) + 2u * c + kh;
+            wv.woff[f] = (tile * 12u + dpair) * 4u;
         }
-        wv.gammas = gamma_rows[group][kq] + gwave;  // entry 4 * gwave
-        const uint32_t pos = (24u * m) & 31u;  // bit of state 2m in dword dw
+        wv.gammas = gamma_rows[group][tsub + kh] + gwave;  // entry 4 * gwave
+        const uint32_t pos = (24u * trow) & 31u;  // bit of state 2 trow in dword dw
         wv.sh0 = 48u - pos;
         wv.sh1 = 36u - pos;
 
@@ -372,16 +406,16 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
             // gamma of the tile at anti-diagonal d = tr_block + e sits in wave
             // slot R_t + C_t - 1 - d, one less past the main anti-diagonal
             // (src/codec_cache.cpp:117-147); slots past the matrix read 0 and
-            // belong to rows that are never stored
+            // belong to tiles that are never stored
             const __amdgpu_buffer_rsrc_t gbuf =
                 buffer_over(a.gamma + mat * a.gamma_stride, (a.tile_rows + tile_columns) * 2u);
             const uint32_t top = a.tile_rows + tile_columns - 1u;
             uint16_t *rows = reinterpret_cast<uint16_t *>(gamma_rows[group]);
-            const uint32_t e = gthread;  // tile_columns + 31 <= 512
+            const uint32_t e = gthread;  // tile_columns + 35 <= 512
             const uint32_t d = tr_block + e;
             const uint32_t gslot = top - d - (d >= tile_columns ? 1u : 0u);
             const uint16_t g = __builtin_amdgcn_raw_buffer_load_b16(gbuf, gslot * 2u, 0, 0);
-            if (e < tile_columns + kBlockTileRows - 1u) {
+            if (e < tile_columns + kBlockTileRows + 3u) {
 #pragma unroll
                 for (uint32_t q = 0; q < 4u; ++q) {
                     const uint32_t i = e - q;  // wraps past zero: then out of range
@@ -391,21 +425,27 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
                 }
             }
         }
-        f32x4 acc[kExpertRT][NT];
+        f32x16 acc[2][CB];
 #pragma unroll
-        for (int t = 0; t < kExpertRT; ++t) {
+        for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
-            for (int j = 0; j < NT; ++j) {
-                acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    acc[rb][cb][r] = 0.0f;
+                }
             }
         }
-        // B of K step kc, as the MFMA operands of position tile j
-        auto read_b = [&](uint32_t ring_slot, half8 (&bh)[NT], half8 (&bl)[NT]) {
-            const char *base = ring + ring_slot * kBSlot + kq * 16u;
+        // B of K step kc, as the MFMA operands of position block cb, K pair c
+        auto read_b = [&](uint32_t ring_slot, half8 (&bh)[CB][2], half8 (&bl)[CB][2]) {
+            const char *base = ring + ring_slot * kBSlot + m * kBRowPitch + kh * 16u;
 #pragma unroll
-            for (int j = 0; j < NT; ++j) {
-                bh[j] = *reinterpret_cast<const half8 *>(base + (j * 32u + m) * kBRowPitch);
-                bl[j] = *reinterpret_cast<const half8 *>(base + (j * 32u + 16u + m) * kBRowPitch);
+            for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    bh[cb][c] = *reinterpret_cast<const half8 *>(base + cb * 32u * kBRowPitch + c * 32u);
+                    bl[cb][c] = *reinterpret_cast<const half8 *>(base + (kPositions + cb * 32u) * kBRowPitch + c * 32u);
+                }
             }
         };
         if (steps % kDepth != 0) {
@@ -416,11 +456,11 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
                 expert_words(wv, kc, ws);
                 *reinterpret_cast<BChunk *>(ring + b_store) = bv;
                 __syncthreads();
-                half8 bh[NT], bl[NT];
+                half8 bh[CB][2], bl[CB][2];
                 read_b(0, bh, bl);
                 ExpertA fa;
                 expert_decode<PASSES>(wv, kc, sign_mask, plane, ws, fa);
-                expert_multiply<NT, PASSES>(fa, bh, bl, acc);
+                expert_multiply<CB, PASSES>(fa, bh, bl, acc);
                 __syncthreads();
             }
         } else {
@@ -452,28 +492,33 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
                     bv[(u + 1) % kDepth] = load_b(xsrc, b_off, min(step + 1u + kDepth, last) * 64u);
                     expert_words(wv, min(step + kDepth - 1u, last), ws[(u + kDepth - 1) % kDepth]);
                     __builtin_amdgcn_sched_barrier(0);
-                    half8 bh[NT], bl[NT];
+                    half8 bh[CB][2], bl[CB][2];
                     read_b(u & 1, bh, bl);
                     ExpertA fa;
                     expert_decode<PASSES>(wv, step, sign_mask, plane, ws[u], fa);
-                    expert_multiply<NT, PASSES>(fa, bh, bl, acc);
+                    expert_multiply<CB, PASSES>(fa, bh, bl, acc);
                     __syncthreads();
                 }
             }
         }
+        // D register r of lane l: position 32 cb + l % 32, block row
+        // (r % 4) + 8 (r / 4) + 4 kh
         float *z = a.z + half * a.z_split_stride;
 #pragma unroll
-        for (uint32_t t = 0; t < kExpertRT; ++t) {
-            const uint32_t tr = tr0 + t;
-            if (!live || tr >= a.tile_rows) {
-                continue;
-            }
+        for (int cb = 0; cb < CB; ++cb) {
+            const uint32_t p = p0 + 32u * cb + m;
+            if (live && p < end) {
 #pragma unroll
-            for (int j = 0; j < NT; ++j) {
-                const uint32_t p = p0 + 16u * j + m;
-                if (p < end) {
-                    *reinterpret_cast<f32x4 *>(z + static_cast<size_t>(p) * a.rows + tr * kTile +
-                                               kq * 4u) = acc[t][j];
+                for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const uint32_t row = (tr0 + 2u * rb) * kTile + 8u * g + 4u * kh;
+                        if (row < a.rows) {
+                            *reinterpret_cast<f32x4 *>(z + static_cast<size_t>(p) * a.rows + row) =
+                                f32x4{acc[rb][cb][4 * g], acc[rb][cb][4 * g + 1], acc[rb][cb][4 * g + 2],
+                                      acc[rb][cb][4 * g + 3]};
+                        }
+                    }
                 }
             }
         }
@@ -640,13 +685,13 @@ void launch_expert_mfma(adi_hip_context *ctx, ExpertMfmaJobs &J) {
         x.tile_rows = x.rows / kTile;
         x.tc_shift = log2_of(x.columns / kTile);
     }
-    J.row_groups = ceil_div(e.rows / kTile, kBlockTileRows);  // row quarters of a block item
-    J.position_groups = ceil_div(J.max_positions, 16u * kExpertNT);
+    J.row_groups = ceil_div(e.rows / kTile, kBlockTileRows);  // row quarters of an item
+    J.position_groups = ceil_div(J.max_positions, 32u * kExpertCB);
     J.items = J.expert_count * J.max_active * J.position_groups * J.row_groups;  // upper bound
     const uint32_t cap = ctx->cu_count >= 16 ? ctx->cu_count / 16 * 16 : 16u;
     const uint32_t needed = 16u * ceil_div(ceil_div(J.items, kExpertGroups), 8u);
     const uint32_t blocks = needed < cap ? needed : cap;
-    auto kernel = k_expert_mfma<kExpertNT, kExpertGroups, kExpertPasses>;
+    auto kernel = k_expert_mfma<kExpertCB, kExpertGroups, kExpertPasses>;
     launch(ctx, "expert_mfma", kernel, dim3(blocks), dim3(512 * kExpertGroups), 0, J);
 }
 
