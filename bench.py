@@ -7,11 +7,14 @@ packed projections (2048x2048 non-expert, 151936x2048 int5 output head).
 
 Prints one JSON line. `value` is MoE-layer tokens/s at ubatch 1 (decode);
 the other ubatches and the projections are reported under `per_ubatch` and
-`projections`. Weights are synthetic (seeded, reference codec formats) and
-rotate through enough distinct layers that the 256 MB Infinity Cache cannot
-hold them; inputs are resident in HBM before the timed region. The roofline
-object is for the kernel with the largest share of the headline step time,
-timed with HIP events on the stream the library launches on.
+`projections`. Weights are synthetic (seeded, reference codec formats); the
+steps cycle through 8 layers and a pool of input batches, so each step routes
+to experts the recent steps did not touch and the 256 MB Infinity Cache does
+not hold the working set. Inputs are resident in HBM before the timed region.
+The roofline object is for the kernel with the largest share of the headline
+step time, timed with HIP events on the stream the library launches on; its
+`traffic` is the measured HBM bytes per launch from the committed counter
+summary (profiles/moe_layer_hbm_traffic.md), or null without one.
 """
 from __future__ import annotations
 
@@ -54,6 +57,9 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU baseline budget per ubatch")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-projections", action="store_true")
+    p.add_argument("--copy-bytes", type=int, default=0,
+                   help="first run a plain device-to-device copy of this many bytes three times "
+                        "(the calibration launch for the HBM byte counters)")
     return p.parse_args()
 
 
@@ -76,31 +82,77 @@ def kernel_bytes(name, active):
     return None
 
 
-def moe_bench(torch, hip, ctx, layers, x, bias, steps, warmup):
-    batch = x.shape[0]
+def input_pool_size(ubatch):
+    """Distinct input batches a run cycles through. Step s runs layer s % L on
+    batch (s // L) % X, so consecutive visits of a layer route different
+    tokens and touch different experts: at ubatch 1 a step reads about 7.5 MB
+    of weights that the previous ~30 steps did not, so the 256 MB Infinity
+    Cache does not hold the working set."""
+    return 64 if ubatch < 16 else (4 if ubatch < 256 else 2)
+
+
+def moe_bench(torch, hip, ctx, layers, xs, biases, steps, warmup):
+    batch = xs[0].shape[0]
     out = torch.empty((batch, HIDDEN), dtype=torch.float32, device="cuda")
     routes = torch.empty(batch * 8, dtype=torch.int32, device="cuda")
+    nl, nx = len(layers), len(xs)
+
+    def step(s):
+        j = (s // nl) % nx
+        hip.moe_forward(ctx, layers[s % nl], xs[j], batch, biases[j], out, routes, None)
+
     for s in range(warmup):
-        hip.moe_forward(ctx, layers[s % len(layers)], x, batch, bias, out, routes, None)
+        step(s)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for s in range(steps):
-        hip.moe_forward(ctx, layers[s % len(layers)], x, batch, bias, out, routes, None)
+    for s in range(warmup, warmup + steps):
+        step(s)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    # distinct experts per layer for the byte count
+    # distinct experts per step for the byte count
     active = []
-    for layer in layers:
-        hip.moe_forward(ctx, layer, x, batch, bias, out, routes, None)
+    for s in range(warmup, warmup + steps):
+        step(s)
         torch.cuda.synchronize()
         active.append(len(np.unique(routes.cpu().numpy())))
-    # per-kernel event timing in a separate pass
+    # per-kernel event timing in a separate pass over the same steps
     ctx.profiling(True)
-    for s in range(steps):
-        hip.moe_forward(ctx, layers[s % len(layers)], x, batch, bias, out, routes, None)
+    for s in range(warmup, warmup + steps):
+        step(s)
     prof = ctx.profile()
     ctx.profiling(False)
     return wall, float(np.mean(active)), prof
+
+
+def copy_calibration(torch, nbytes):
+    """Three plain device-to-device copies of `nbytes` (hipMemcpyAsync's blit
+    kernel): the known-size launch the FETCH_SIZE / WRITE_SIZE counters of the
+    hot-path kernels are scaled by."""
+    n = nbytes // 4
+    src = torch.arange(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy calibration: 3 copies of {nbytes} bytes")
+    del src, dst
+
+
+def traffic_from_profile(kernel, ubatch):
+    """Measured HBM bytes per launch of `kernel` at `ubatch`, from the
+    committed counter summary (FETCH_SIZE + WRITE_SIZE per dispatch, each
+    scaled by the same counter's reading for a copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "moe_layer_hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for row in open(path):
+        cells = [c.strip() for c in row.strip().strip("|").split("|")]
+        if len(cells) >= 6 and cells[0].isdigit() and int(cells[0]) == ubatch and cells[1] == kernel:
+            try:
+                return int(float(cells[5]))
+            except ValueError:
+                return None
+    return None
 
 
 def kernel_flops(name, ubatch):
@@ -114,6 +166,13 @@ def kernel_flops(name, ubatch):
 
 
 def roofline_for(prof, steps, active, ubatch):
+    r = roofline_kernel(prof, active, ubatch)
+    if r is not None:
+        r["traffic"] = traffic_from_profile(r["kernel"], ubatch)
+    return r
+
+
+def roofline_kernel(prof, active, ubatch):
     total = sum(ms for _, ms in prof.values())
     ranked = sorted(prof.items(), key=lambda kv: -kv[1][1])
     for name, (launches, ms) in ranked:
@@ -234,6 +293,8 @@ def main():
 
     ubatches = [int(u) for u in args.ubatch.split(",")]
     ctx = hip.Context(0)
+    if args.copy_bytes > 0:
+        copy_calibration(torch, args.copy_bytes)
     log("generating weights")
     rng = syn.rng_for(2, 0)
     layer_host = syn.moe_layer(rng)
@@ -247,16 +308,17 @@ def main():
     xs_host, biases_host = {}, {}
     for u in ubatches:
         r = syn.rng_for(3 if u >= 64 else 2, u)
-        xs_host[u] = syn.hidden_states(r, u, HIDDEN)
+        xs_host[u] = [syn.hidden_states(r, u, HIDDEN) for _ in range(input_pool_size(u))]
         biases_host[u] = syn.zipf_bias(r, EXPERTS) if u >= 64 else None
 
     per = {}
     headline = None
     for u in ubatches:
         log(f"moe layer ubatch {u}")
-        x = ctx.to_device(xs_host[u])
+        xs = [ctx.to_device(x) for x in xs_host[u]]
         bias = None if biases_host[u] is None else ctx.to_device(biases_host[u])
-        wall, active, prof = moe_bench(torch, hip, ctx, layers, x, bias, args.steps, args.warmup)
+        wall, active, prof = moe_bench(torch, hip, ctx, layers, xs, [bias] * len(xs), args.steps,
+                                       args.warmup)
         ms = wall / args.steps * 1e3
         layer_bytes = FIXED_LAYER_BYTES + PER_EXPERT_BYTES * active
         entry = {
@@ -278,7 +340,8 @@ def main():
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")
-        kind, cores, isa, results = cpu_baseline(layer_host, xs_host, biases_host, args.cpu_seconds)
+        kind, cores, isa, results = cpu_baseline(layer_host, {u: v[0] for u, v in xs_host.items()},
+                                                 biases_host, args.cpu_seconds)
         u0 = headline[0]
         cpu = {"value": results[u0]["tokens_per_s"], "unit": "tokens/s", "cores": cores,
                "kind": kind, "isa": isa,
