@@ -699,23 +699,13 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t value, uint32_
     return before + inclusive - value;
 }
 
-// One wave per chunk of 64 route positions: the rank of each position among
-// the chunk's earlier positions with the same expert (ballot match on the
-// expert bits) and the chunk's per-expert counts.
-__global__ __launch_bounds__(256) void k_route_hist(RouteSort a, uint32_t chunks) {
-    extern __shared__ uint32_t hist[];  // [4][experts]
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t c = blockIdx.x * 4u + wave;
-    if (c >= chunks) {
-        return;  // wave-uniform; no block barrier follows
-    }
-    uint32_t *h = hist + wave * a.experts;
-    for (uint32_t e = lane; e < a.experts; e += 64u) {
-        h[e] = 0u;
-    }
+// One wave over chunk c of 64 route positions (expert of position c * 64 +
+// lane in `e`): the rank of each position among the chunk's earlier positions
+// with the same expert (ballot match on the expert bits) and the chunk's
+// per-expert counts, built in `h` (zeroed by the caller, visible to this wave).
+__device__ __forceinline__ void chunk_hist_wave(const RouteSort &a, uint32_t c, uint32_t lane,
+                                                bool valid, uint32_t e, uint32_t *h) {
     const uint32_t i = c * kChunk + lane;
-    const bool valid = i < a.positions;
-    const uint32_t e = valid ? a.route_expert[i] : 0u;
     uint64_t peers = __ballot(valid);
     if (!valid) {
         peers = ~peers;
@@ -726,7 +716,6 @@ __global__ __launch_bounds__(256) void k_route_hist(RouteSort a, uint32_t chunks
         peers &= set ? vote : ~vote;
     }
     const uint32_t rank = __popcll(peers & ((1ull << lane) - 1ull));
-    // LDS operations of one wave complete in order: the zeroing lands first
     if (valid) {
         a.position_rank[i] = rank;
         if (rank == 0) {
@@ -740,9 +729,54 @@ __global__ __launch_bounds__(256) void k_route_hist(RouteSort a, uint32_t chunks
     }
 }
 
+// One wave per chunk of 64 route positions (routes from a.route_expert).
+__global__ __launch_bounds__(256) void k_route_hist(RouteSort a, uint32_t chunks) {
+    extern __shared__ uint32_t hist[];  // [4][experts]
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t c = blockIdx.x * 4u + wave;
+    if (c >= chunks) {
+        return;  // wave-uniform; no block barrier follows
+    }
+    uint32_t *h = hist + wave * a.experts;
+    for (uint32_t e = lane; e < a.experts; e += 64u) {
+        h[e] = 0u;
+    }
+    const uint32_t i = c * kChunk + lane;
+    const bool valid = i < a.positions;
+    // LDS operations of one wave complete in order: the zeroing lands first
+    chunk_hist_wave(a, c, lane, valid, valid ? a.route_expert[i] : 0u, h);
+}
+
+// top_experts for the 8 rows of one chunk (one wave per row), then the
+// chunk's ranks and counts from the routes kept in LDS: block b is chunk b.
+template <int SLOTS>
+__global__ __launch_bounds__(512) void k_top_experts_hist(
+    const float *__restrict__ logits, const float *__restrict__ bias, uint32_t batch,
+    uint32_t *__restrict__ route_expert, float *__restrict__ route_weight, RouteSort a) {
+    static_assert(kChunk == 64, "a chunk is the 8 routes of 8 rows");
+    __shared__ uint32_t local[kChunk];
+    __shared__ uint32_t hist[kMaxExperts];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t row = blockIdx.x * 8u + wave;
+    for (uint32_t e = threadIdx.x; e < a.experts; e += blockDim.x) {
+        hist[e] = 0u;
+    }
+    if (row < batch) {
+        top8_wave<SLOTS>(logits + static_cast<size_t>(row) * a.experts, bias, a.experts, lane,
+                         route_expert + row * 8u, route_weight + row * 8u, local + wave * 8u);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const uint32_t i = blockIdx.x * kChunk + lane;
+        const bool valid = i < a.positions;
+        chunk_hist_wave(a, blockIdx.x, lane, valid, valid ? local[lane] : 0u, hist);
+    }
+}
+
 // One block: per-expert totals and offsets, the ascending active list and
-// slot table, and each chunk's first grouped index per expert, written back
-// over chunk_hist (k_route_scatter then places the positions). The chunk
+// slot table, each chunk's first grouped index per expert (in LDS), and then
+// the grouped index of every position, stable in (token, route) order: its
+// chunk's first index for its expert plus its rank within the chunk. The chunk
 // counts are staged in LDS with coalesced loads and each expert's scan over
 // the chunks is split into up to four ranges scanned by separate threads.
 __global__ __launch_bounds__(1024) void k_route_finalize(RouteSort a, uint32_t chunks) {
@@ -819,24 +853,14 @@ __global__ __launch_bounds__(1024) void k_route_finalize(RouteSort a, uint32_t c
         }
     }
     __syncthreads();
-    for (uint32_t i = t; i < cells; i += blockDim.x) {
-        a.chunk_hist[i] = start[i % E] + base[i];
-    }
-}
-
-// The grouped index of every position, stable in (token, route) order: its
-// chunk's first index for its expert plus its rank within the chunk.
-__global__ __launch_bounds__(256) void k_route_scatter(RouteSort a) {
-    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-    if (i >= a.positions) {
-        return;
-    }
-    const uint32_t e = a.route_expert[i];
-    const uint32_t g = a.chunk_hist[static_cast<size_t>(i / kChunk) * a.experts + e] + a.position_rank[i];
-    a.grouped_batch[g] = i / 8u;
-    a.route_to_grouped[i] = g;
-    if (a.position_expert != nullptr) {
-        a.position_expert[g] = e;
+    for (uint32_t i = t; i < a.positions; i += blockDim.x) {
+        const uint32_t e = a.route_expert[i];
+        const uint32_t g = start[e] + base[(i / kChunk) * E + e] + a.position_rank[i];
+        a.grouped_batch[g] = i / 8u;
+        a.route_to_grouped[i] = g;
+        if (a.position_expert != nullptr) {
+            a.position_expert[g] = e;
+        }
     }
 }
 
@@ -963,11 +987,40 @@ void launch_route_sort(adi_hip_context *ctx, const RouteSort &args) {
                                                 size_t(kFinalizeBases) * sizeof(uint32_t));
         (void)ready;
         launch(ctx, "route_sort", k_route_finalize, dim3(1), dim3(1024), lds, args, chunks);
-        launch(ctx, "route_scatter", k_route_scatter, dim3(ceil_div(args.positions, 256)), dim3(256), 0,
-               args);
         return;
     }
     launch(ctx, "route_sort", k_route_sort, dim3(1), dim3(64), 0, args);
+}
+
+// top_experts with the chunk histograms in the same launch, then the one-block
+// finalize: two launches for batches whose chunk bases fit the finalize's LDS.
+bool launch_route_fused(adi_hip_context *ctx, const float *logits, const float *bias,
+                        uint32_t batch, uint32_t *route_expert, float *route_weight,
+                        const RouteSort &args) {
+    const uint32_t chunks = ceil_div(args.positions, kChunk);
+    if (args.position_rank == nullptr || args.chunk_hist == nullptr ||
+        args.positions != batch * 8u || size_t(chunks) * args.experts > kFinalizeBases) {
+        return false;
+    }
+    const uint32_t slots = ceil_div(args.experts, 64);
+    const dim3 grid(chunks);
+    if (slots <= 1) {
+        launch(ctx, "top_experts", k_top_experts_hist<1>, grid, dim3(512), 0, logits, bias, batch, route_expert, route_weight, args);
+    } else if (slots <= 2) {
+        launch(ctx, "top_experts", k_top_experts_hist<2>, grid, dim3(512), 0, logits, bias, batch, route_expert, route_weight, args);
+    } else if (slots <= 4) {
+        launch(ctx, "top_experts", k_top_experts_hist<4>, grid, dim3(512), 0, logits, bias, batch, route_expert, route_weight, args);
+    } else if (slots <= 8) {
+        launch(ctx, "top_experts", k_top_experts_hist<8>, grid, dim3(512), 0, logits, bias, batch, route_expert, route_weight, args);
+    } else {
+        launch(ctx, "top_experts", k_top_experts_hist<16>, grid, dim3(512), 0, logits, bias, batch, route_expert, route_weight, args);
+    }
+    const size_t lds = size_t(chunks) * args.experts * sizeof(uint32_t);
+    static const bool ready = set_lds_limit(reinterpret_cast<const void *>(&k_route_finalize),
+                                            size_t(kFinalizeBases) * sizeof(uint32_t));
+    (void)ready;
+    launch(ctx, "route_sort", k_route_finalize, dim3(1), dim3(1024), lds, args, chunks);
+    return true;
 }
 
 void launch_route(adi_hip_context *ctx, const float *logits, const float *bias, uint32_t batch,
@@ -975,6 +1028,9 @@ void launch_route(adi_hip_context *ctx, const float *logits, const float *bias, 
     const uint32_t slots = ceil_div(args.experts, 64);
     if (batch > kRouteBatch) {
         // many rows: top_experts over a grid, then the one-block sort
+        if (launch_route_fused(ctx, logits, bias, batch, route_expert, route_weight, args)) {
+            return;
+        }
         launch_top_experts(ctx, logits, bias, batch, args.experts, route_expert, route_weight);
         launch_route_sort(ctx, args);
         return;

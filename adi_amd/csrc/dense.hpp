@@ -49,8 +49,10 @@ inline size_t route_sort_scratch(size_t positions, size_t experts) {
 }
 void launch_route_sort(adi_hip_context *ctx, const RouteSort &args);
 
-// top_experts for every row plus the counting sort, in one launch.
-// route_expert must be args.route_expert.
+// top_experts for every row plus the counting sort: one launch up to
+// kRouteBatch rows, else top_experts with the chunk histograms and a one-block
+// finalize that also places the positions. route_expert must be
+// args.route_expert.
 void launch_route(adi_hip_context *ctx, const float *logits, const float *bias, uint32_t batch,
                   uint32_t *route_expert, float *route_weight, const RouteSort &args);
 
