@@ -1,25 +1,21 @@
 // grouped.hip -- MFMA grouped GEMMs for prefill microbatches
 // (src/kernels.cpp:491-593, 703-800 with the batch kernels of
 // src/expert_batch_impl.hpp and src/ne_batch_impl.hpp): the codes are decoded
-// straight into the A operand of v_mfma_f32_16x16x32_f16, x_hat is the B
-// operand as f16 hi/lo pairs, accumulation is fp32.
+// straight into the A operand of v_mfma_f32_32x32x16_f16, x_hat is the B
+// operand as f16 hi/lo pairs staged once per block in LDS, accumulation is
+// fp32.
 //
-// Expert codec. In 16x16x32 the lane l holds A[l % 16][8 * (l / 16) + 0..7]:
-// eight consecutive K values of one row. With the K axis laid out as the
-// eight columns a codebook plane covers in each tile (XhatOut planes 2), those
-// eight values are the two half-states of row l % 16 of one tile: exactly two
-// gathers from the block's LDS plane. The wave gamma of a tile is folded into
-// A in f16: hi = f16(gamma * V), lo = f16(gamma * V - hi) (one packed f16
-// multiply and one packed f16 fma; gamma and V are f16, so the product has at
-// most 22 significant bits and hi + lo holds it). Three MFMA passes,
-// hi*hi + hi*lo + lo*hi, keep the error near fp32 rounding.
+// Expert codec. The K axis is laid out as the eight columns a codebook plane
+// covers in each tile (XhatOut planes 2), so a lane's eight K values are the
+// two half-states of one tile row: two gathers from the block's LDS plane.
+// The wave gamma of a tile is folded into A in f16: hi = f16(gamma * V),
+// lo = f16(gamma * V - hi) (one packed f16 multiply and one packed f16 fma;
+// gamma and V are f16, so the product has at most 22 significant bits and
+// hi + lo holds it). Three MFMA passes, hi*hi + hi*lo + lo*hi, keep the error
+// near fp32 rounding.
 //
 // NE codec. The 4 KiB signed table gives V exactly in f16 (Wscale is applied
 // to the fp32 row sums); two passes, V*hi + V*lo.
-//
-// A wave item is 4 tile rows x 16*NT positions x the full K. Its next K step's
-// trellis words, gammas and B fragments are loaded before the current step's
-// MFMAs.
 #include "grouped.hpp"
 
 #include <type_traits>
@@ -31,9 +27,6 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t kMfmaThreads = 256;                   // NE GEMM blocks
-constexpr uint32_t kMfmaWaves = kMfmaThreads / kWave;
-constexpr uint32_t kRowTiles = 4;                         // NE GEMM: tile rows per item
 // expert GEMM shape: 32 positions per item, tile rows kExpertRT per wave,
 // 512 * kExpertGroups threads per block (one block per CU), MFMA passes per
 // product (hi*hi + hi*lo + lo*hi)
@@ -43,14 +36,6 @@ constexpr int kExpertGroups = 1;  // wave groups of eight per block, each on its
 constexpr int kExpertPasses = 3;
 constexpr uint32_t kPlaneRows16 = kExpertRows * 8 / 16;   // 16-byte rows of a plane
 constexpr uint32_t kSlotCapacity = 1024;
-
-__device__ __forceinline__ half8 load_half8(const uint16_t *p) {
-    return __builtin_bit_cast(half8, *reinterpret_cast<const u32x4 *>(p));
-}
-
-__device__ __forceinline__ half8 zero_half8() {
-    return __builtin_bit_cast(half8, u32x4{0u, 0u, 0u, 0u});
-}
 
 // The 16-bit window at bit r (r <= 48) of the 64-bit string of u16 words
 // w0 w1 w2 w3, each read most-significant bit first, where d0 = w0 | w1 << 16
@@ -70,10 +55,6 @@ __device__ __forceinline__ uint32_t state_hash_low16(uint32_t w) {
     uint32_t p;
     asm("v_mad_u32_u24 %0, %1, %1, %1" : "=v"(p) : "v"(w));
     return p;
-}
-
-__device__ __forceinline__ f32x4 mfma(half8 a, half8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 // ---- expert ---------------------------------------------------------------
@@ -526,130 +507,157 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
 }
 
 // ---- NE -------------------------------------------------------------------
+//
+// Also on v_mfma_f32_32x32x16_f16. A block of eight waves takes one item: 32
+// positions x 16 tile rows (256 rows) of one NE entry over one K slice; wave w
+// takes tile rows 2w, 2w + 1 as one 32-row block. Lane l holds row l % 16 of
+// tile row 2w + (l % 32) / 16 and, of K pair c at K step kc, columns
+// 8 (l / 32) .. + 7 of tile column 2 kc + c: NE states 8 (l % 16) +
+// 4 (l / 32) + 0..3, four lookups of the signed table (two f16 each). The
+// block loads each K step's x_hat hi and lo of its 32 positions once into an
+// LDS ring (one barrier per K step); each wave loads its trellis words four K
+// steps ahead.
 
-template <int NT>
-struct NeStep {
-    half8 bh[NT], bl[NT];
-    uint32_t d0[kRowTiles], d1[kRowTiles];
+constexpr uint32_t kNeThreads = 512;
+constexpr uint32_t kNeWaves = kNeThreads / kWave;
+constexpr uint32_t kNeItemTileRows = 2 * kNeWaves;   // 256 rows per item
+constexpr uint32_t kNeBSlot = 64 * kBRowPitch;      // (hi/lo, position) rows of one K step
+
+// The lane's trellis dwords of its two fragments (K pair c) at one K step.
+struct NeWords {
+    uint32_t d0[2], d1[2];
 };
 
-template <int NT>
-__device__ __forceinline__ void ne_load(const NeMfma &a, uint32_t tr0, uint32_t p0, uint32_t kc,
-                                        uint32_t lane, NeStep<NT> &s) {
-    const uint32_t m = lane & 15u, kq = lane >> 4;
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-        const uint32_t p = p0 + 16u * j + m;
-        const uint32_t pc = p < a.batch ? p : p0;
-        const size_t at = static_cast<size_t>(pc) * a.columns + kc * 32u + kq * 8u;
-        s.bh[j] = load_half8(a.x_hi + at);
-        s.bl[j] = load_half8(a.x_lo + at);
-    }
-    // lane: tile column 2kc + kq/2, columns 8*(kq%2)..+7 of row m = NE states
-    // 8m + 4(kq%2) + 0..3, the windows at bits 32*(2m + kq%2) + 8i
-    const uint32_t tc = kc * 2u + (kq >> 1);
-    const uint32_t dw = 2u * m + (kq & 1u);
-    const uint32_t dn = dw == 31u ? 0u : dw + 1u;  // row 15 wraps (src/ne_trellis.hpp:196-200)
-    const uint32_t *words = reinterpret_cast<const uint32_t *>(a.trellis);
-#pragma unroll
-    for (uint32_t t = 0; t < kRowTiles; ++t) {
-        const uint32_t tr = min(tr0 + t, a.tile_rows - 1u);
-        const size_t tile = (static_cast<size_t>(tr) << a.tc_shift) + tc;
-        s.d0[t] = __builtin_nontemporal_load(words + tile * 32u + dw);
-        s.d1[t] = __builtin_nontemporal_load(words + tile * 32u + dn);
-    }
-}
-
-template <int NT>
-__device__ __forceinline__ void ne_compute(const NeMfma &a, uint32_t p0, const uint32_t *table,
-                                           uint32_t lane, const NeStep<NT> &s,
-                                           f32x4 (&acc)[kRowTiles][NT]) {
-    const uint32_t m = lane & 15u;
-    half8 bh[NT], bl[NT];
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-        const bool ok = p0 + 16u * j + m < a.batch;
-        bh[j] = ok ? s.bh[j] : zero_half8();
-        bl[j] = ok ? s.bl[j] : zero_half8();
-    }
-#pragma unroll
-    for (uint32_t t = 0; t < kRowTiles; ++t) {
-        uint32_t v[4];
-#pragma unroll
-        for (uint32_t q = 0; q < 4; ++q) {
-            v[q] = table[(state_product(window64(s.d0[t], s.d1[t], 8u * q)) >> 6) & 0x3FFu];
-        }
-        const half8 w = __builtin_bit_cast(half8, u32x4{v[0], v[1], v[2], v[3]});
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            acc[t][j] = mfma(w, bh[j], acc[t][j]);
-        }
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            acc[t][j] = mfma(w, bl[j], acc[t][j]);
-        }
-    }
-}
-
-template <int NT>
-__global__ __launch_bounds__(kMfmaThreads) void k_ne_mfma(NeMfmaJobs J) {
+__global__ __launch_bounds__(kNeThreads) void k_ne_mfma(NeMfmaJobs J) {
     __shared__ uint32_t table[1024];
-    const uint32_t *src = static_cast<const uint32_t *>(J.ne_book);
-    for (uint32_t i = threadIdx.x; i < 1024u; i += kMfmaThreads) {
-        table[i] = src[i];
-    }
-    __syncthreads();
-    const uint32_t i = blockIdx.x * kMfmaWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (i >= J.items) {
-        return;
-    }
+    __shared__ uint4 b_ring[2][kNeBSlot / 16];
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t rg = i % J.row_groups;
-    uint32_t rest = i / J.row_groups;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // item (row group, K slice, position group, entry), fastest first
+    uint32_t rest = blockIdx.x;
+    const uint32_t rg = rest % J.row_groups;
+    rest /= J.row_groups;
     const uint32_t ks = rest % J.k_slices;
     rest /= J.k_slices;
     const uint32_t pg = rest % J.position_groups;
     const uint32_t which = rest / J.position_groups;
     const NeMfma &a = J.ne[which];
-    const uint32_t p0 = pg * 16u * NT;
-    const uint32_t tr0 = rg * kRowTiles;
-    f32x4 acc[kRowTiles][NT];
-#pragma unroll
-    for (uint32_t t = 0; t < kRowTiles; ++t) {
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-    }
-    const uint32_t steps = a.columns / 32u / J.k_slices;  // a power of two
+    const uint32_t steps = (a.columns >> 5) / J.k_slices;  // K steps of 32 columns, a power of two
     const uint32_t k0 = ks * steps;
-    NeStep<NT> s0, s1;
-    ne_load<NT>(a, tr0, p0, k0, lane, s0);
-    if (steps == 1) {
-        ne_compute<NT>(a, p0, table, lane, s0, acc);
+    const uint32_t last = steps - 1u;
+    const uint32_t p0 = pg * 32u;
+    // the table: eight bytes per thread, stored once the first loads are out
+    const uint2 tv = reinterpret_cast<const uint2 *>(J.ne_book)[threadIdx.x];
+    // B staging: thread t copies 8 bytes of B row t / 8 (rows 0..31 hi, 32..63
+    // lo, so the plane is wave-uniform); positions past the batch repeat p0
+    const uint32_t b_row = threadIdx.x >> 3, b_chunk = threadIdx.x & 7u;
+    const uint32_t bp = p0 + (b_row & 31u);
+    const uint32_t b_pos = bp < a.batch ? bp : p0;
+    const __amdgpu_buffer_rsrc_t xsrc =
+        buffer_over(wave >= 4u ? a.x_lo : a.x_hi, a.batch * a.columns * 2u);
+    const uint32_t b_off = (b_pos * a.columns + b_chunk * 4u) * 2u + k0 * 64u;
+    char *ring = reinterpret_cast<char *>(b_ring);
+    const uint32_t b_store = b_row * kBRowPitch + b_chunk * 8u;
+    auto load_b = [&](uint32_t kc) {
+        return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(xsrc, b_off, kc * 64u, 0));
+    };
+    // the lane's trellis words: row trow of tile row tr, dwords dw and dw + 1
+    // (row 15's second wraps to dword 0, src/ne_trellis.hpp:196-200)
+    const uint32_t m = lane & 31u, kh = lane >> 5;
+    const uint32_t trow = m & 15u;
+    const uint32_t tr_block = rg * kNeItemTileRows + 2u * wave;
+    const uint32_t tr = min(tr_block + (m >> 4), a.tile_rows - 1u);
+    const uint32_t dw = 2u * trow + kh, dn = dw == 31u ? 0u : dw + 1u;
+    const __amdgpu_buffer_rsrc_t wsrc = buffer_over(a.trellis, (a.tile_rows << a.tc_shift) * 128u);
+    const uint32_t w0 = ((tr << a.tc_shift) * 32u + dw) * 4u;
+    const uint32_t w1 = ((tr << a.tc_shift) * 32u + dn) * 4u;
+    auto load_words = [&](uint32_t kc, NeWords &w) {
+#pragma unroll
+        for (uint32_t c = 0; c < 2; ++c) {
+            const uint32_t soff = (2u * (k0 + kc) + c) * 128u;  // tile column 2 kc + c
+            w.d0[c] = __builtin_amdgcn_raw_buffer_load_b32(wsrc, w0, soff, 0);
+            w.d1[c] = __builtin_amdgcn_raw_buffer_load_b32(wsrc, w1, soff, 0);
+        }
+    };
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        acc[r] = 0.0f;
+    }
+    // one K step: the two A fragments from the table, B from ring slot `slot`
+    auto multiply = [&](uint32_t slot, const NeWords &w) {
+        const char *base = ring + slot * kNeBSlot + m * kBRowPitch + kh * 16u;
+#pragma unroll
+        for (uint32_t c = 0; c < 2; ++c) {
+            const half8 bh = *reinterpret_cast<const half8 *>(base + c * 32u);
+            const half8 bl = *reinterpret_cast<const half8 *>(base + 32u * kBRowPitch + c * 32u);
+            uint32_t v[4];
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q) {
+                v[q] = table[(state_product(window64(w.d0[c], w.d1[c], 8u * q)) >> 6) & 0x3FFu];
+            }
+            const half8 av = __builtin_bit_cast(half8, u32x4{v[0], v[1], v[2], v[3]});
+            acc = mfma32(av, bh, acc);
+            acc = mfma32(av, bl, acc);
+        }
+    };
+    constexpr uint32_t kDepth = 4;
+    if (steps % kDepth != 0) {
+        // short K (under 4 steps): one step at a time
+        table[threadIdx.x * 2u] = tv.x;
+        table[threadIdx.x * 2u + 1u] = tv.y;
+        for (uint32_t kc = 0; kc < steps; ++kc) {
+            const uint2 bv = load_b(kc);
+            NeWords w;
+            load_words(kc, w);
+            *reinterpret_cast<uint2 *>(ring + b_store) = bv;
+            __syncthreads();
+            multiply(0, w);
+            __syncthreads();
+        }
     } else {
-        for (uint32_t kc = 0; kc < steps; kc += 2) {
-            ne_load<NT>(a, tr0, p0, k0 + kc + 1, lane, s1);
-            ne_compute<NT>(a, p0, table, lane, s0, acc);
-            ne_load<NT>(a, tr0, p0, k0 + min(kc + 2, steps - 1), lane, s0);
-            ne_compute<NT>(a, p0, table, lane, s1, acc);
+        // B of step s waits in bv[s % 4] until step s - 1 writes it to ring
+        // slot s % 2; the words of step s wait in ws[s % 4]. Loads past the
+        // last step reload it (in bounds, unused).
+        uint2 bv[kDepth];
+        NeWords ws[kDepth];
+#pragma unroll
+        for (uint32_t u = 0; u < kDepth; ++u) {
+            bv[u] = load_b(u);
+            if (u < kDepth - 1) {
+                load_words(u, ws[u]);
+            }
+        }
+        table[threadIdx.x * 2u] = tv.x;
+        table[threadIdx.x * 2u + 1u] = tv.y;
+        *reinterpret_cast<uint2 *>(ring + b_store) = bv[0];
+        bv[0] = load_b(min(kDepth, last));
+        __syncthreads();
+        for (uint32_t kc = 0; kc < steps; kc += kDepth) {
+#pragma unroll
+            for (uint32_t u = 0; u < kDepth; ++u) {
+                const uint32_t step = kc + u;
+                __builtin_amdgcn_sched_barrier(0);
+                *reinterpret_cast<uint2 *>(ring + ((u + 1) & 1) * kNeBSlot + b_store) = bv[(u + 1) % kDepth];
+                bv[(u + 1) % kDepth] = load_b(min(step + 1u + kDepth, last));
+                load_words(min(step + kDepth - 1u, last), ws[(u + kDepth - 1) % kDepth]);
+                __builtin_amdgcn_sched_barrier(0);
+                multiply(u & 1, ws[u]);
+                __syncthreads();
+            }
         }
     }
-    float *z = a.z + static_cast<size_t>(ks) * a.batch * a.rows;
-    const uint32_t m = lane & 15u, kq = lane >> 4;
+    // D register r of lane l: position l % 32, row (r % 4) + 8 (r / 4) + 4 kh
+    // of the wave's 32-row block
+    const uint32_t p = p0 + m;
+    if (p < a.batch) {
+        float *z = a.z + static_cast<size_t>(ks) * a.batch * a.rows + static_cast<size_t>(p) * a.rows;
 #pragma unroll
-    for (uint32_t t = 0; t < kRowTiles; ++t) {
-        const uint32_t tr = tr0 + t;
-        if (tr >= a.tile_rows) {
-            continue;
-        }
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            const uint32_t p = p0 + 16u * j + m;
-            if (p < a.batch) {
-                const f32x4 r = acc[t][j] * a.weight_scale;
-                *reinterpret_cast<f32x4 *>(z + static_cast<size_t>(p) * a.rows + tr * kTile +
-                                           kq * 4u) = r;
+        for (uint32_t g = 0; g < 4; ++g) {
+            const uint32_t row = tr_block * kTile + 8u * g + 4u * kh;
+            if (row < a.rows) {
+                *reinterpret_cast<f32x4 *>(z + row) =
+                    f32x4{acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]} * a.weight_scale;
             }
         }
     }
@@ -657,16 +665,11 @@ __global__ __launch_bounds__(kMfmaThreads) void k_ne_mfma(NeMfmaJobs J) {
 
 }  // namespace
 
-uint32_t mfma_position_tiles(uint32_t batch) {
-    return batch >= 256u ? 4u : (batch >= 64u ? 2u : 1u);
-}
-
 uint32_t ne_mfma_slices(uint32_t rows, uint32_t columns, uint32_t batch) {
-    const uint32_t nt = mfma_position_tiles(batch);
-    const uint32_t items = ceil_div(rows / kTile, kRowTiles) * ceil_div(batch, 16u * nt);
+    const uint32_t items = ceil_div(rows, kNeItemTileRows * kTile) * ceil_div(batch, 32u);
     uint32_t slices = 1;
-    // at least about 2048 wave items, each with at least four K steps
-    while (items * slices < 2048u && columns / 32u / (slices * 2u) >= 4u) {
+    // about one block per CU, each with at least four K steps of 32 columns
+    while (items * slices < 256u && columns / 32u / (slices * 2u) >= 4u) {
         slices *= 2u;
     }
     return slices;
@@ -700,24 +703,25 @@ void launch_ne_mfma(adi_hip_context *ctx, NeMfmaJobs &J) {
     require(J.ne_book != nullptr, "MFMA GEMM: NE codebook missing");
     const NeMfma &n = J.ne[0];
     require(n.columns >= 32 && n.rows >= 16, "MFMA GEMM: NE matrix below 16 x 32");
+    require(is_power_of_two(n.columns) && n.rows % kTile == 0,
+            "MFMA GEMM: NE columns must be a power of two and rows whole tiles");
+    require(size_t(n.batch) * n.columns * 2u < (size_t(1) << 32) &&
+                size_t(n.rows / kTile) * (n.columns / kTile) * 128u < (size_t(1) << 32),
+            "MFMA GEMM: NE operands beyond 4 GiB");
     for (uint32_t i = 0; i < J.ne_count; ++i) {
         NeMfma &x = J.ne[i];
         require(x.rows == n.rows && x.columns == n.columns && x.batch == n.batch,
                 "MFMA GEMM: NE entries differ in shape");
+        require(aligned_to(x.x_hi, 16) && aligned_to(x.x_lo, 16) && aligned_to(x.z, 16),
+                "MFMA GEMM: NE x_hat and Z must be 16-byte aligned");
         x.tile_rows = x.rows / kTile;
         x.tc_shift = log2_of(x.columns / kTile);
     }
-    const uint32_t nt = mfma_position_tiles(n.batch);
-    J.row_groups = ceil_div(n.rows / kTile, kRowTiles);
-    J.position_groups = ceil_div(n.batch, 16u * nt);
+    J.row_groups = ceil_div(n.rows / kTile, kNeItemTileRows);
+    J.position_groups = ceil_div(n.batch, 32u);
     J.k_slices = ne_mfma_slices(n.rows, n.columns, n.batch);
     J.items = J.ne_count * J.position_groups * J.row_groups * J.k_slices;
-    const dim3 grid(ceil_div(J.items, kMfmaWaves));
-    switch (nt) {
-    case 1: launch(ctx, "ne_mfma", k_ne_mfma<1>, grid, dim3(kMfmaThreads), 0, J); break;
-    case 2: launch(ctx, "ne_mfma", k_ne_mfma<2>, grid, dim3(kMfmaThreads), 0, J); break;
-    default: launch(ctx, "ne_mfma", k_ne_mfma<4>, grid, dim3(kMfmaThreads), 0, J);
-    }
+    launch(ctx, "ne_mfma", k_ne_mfma, dim3(J.items), dim3(kNeThreads), 0, J);
 }
 
 }  // namespace adi_hip

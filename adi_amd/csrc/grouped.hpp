@@ -84,8 +84,6 @@ struct NeMfmaJobs {
 // `batch` positions (enough items to fill the GPU; the consumer adds them).
 uint32_t ne_mfma_slices(uint32_t rows, uint32_t columns, uint32_t batch);
 
-// Positions per MFMA item: 16 * tiles_n.
-uint32_t mfma_position_tiles(uint32_t batch);
 void launch_expert_mfma(adi_hip_context *ctx, ExpertMfmaJobs &jobs);
 void launch_ne_mfma(adi_hip_context *ctx, NeMfmaJobs &jobs);
 
