@@ -594,7 +594,9 @@ __global__ __launch_bounds__(kNeThreads) void k_ne_mfma(NeMfmaJobs J) {
             uint32_t v[4];
 #pragma unroll
             for (uint32_t q = 0; q < 4; ++q) {
-                v[q] = table[(state_product(window64(w.d0[c], w.d1[c], 8u * q)) >> 6) & 0x3FFu];
+                // state hash in v_mad_u32_u24: the window's bits above bit 15
+                // only add multiples of 2^16
+                v[q] = table[(state_hash_low16(window64(w.d0[c], w.d1[c], 8u * q)) >> 6) & 0x3FFu];
             }
             const half8 av = __builtin_bit_cast(half8, u32x4{v[0], v[1], v[2], v[3]});
             acc = mfma32(av, bh, acc);
