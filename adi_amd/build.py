@@ -1,6 +1,7 @@
-"""Builds libadi_hip.so in-tree: every HIP source under adi_amd/csrc compiled
-for gfx950 with hipcc and linked into one shared library exporting the C ABI
-declared in include/adi_hip.h.
+"""Builds libadi_hip.so in-tree: every HIP source under adi_amd/csrc (and the
+host-only .cpp sources, compiled as HIP for the shared headers) built for
+gfx950 with hipcc and linked into one shared library exporting the C ABI
+declared in include/adi_hip.h and include/adi_hip_gguf.h.
 
     python -m adi_amd.build          # or adi_amd.build.build()
 """
@@ -37,12 +38,15 @@ def hipcc() -> str:
 
 
 def sources():
-    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
 
 def _compile(source: str) -> str:
-    obj = os.path.join(BUILD_DIR, os.path.basename(source)[:-4] + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, "-c", source, "-o", obj]
+    stem, ext = os.path.splitext(os.path.basename(source))
+    obj = os.path.join(BUILD_DIR, stem + ".o")
+    # host-only .cpp sources share the HIP headers of the library
+    lang = ["-x", "hip"] if ext == ".cpp" else []
+    cmd = [hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, *lang, "-c", source, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {source}:\n{proc.stdout}\n{proc.stderr}")

@@ -1,4 +1,5 @@
-"""ctypes binding of libadi_hip.so, the C ABI in include/adi_hip.h.
+"""ctypes binding of libadi_hip.so, the C ABI in include/adi_hip.h and
+include/adi_hip_gguf.h.
 
 torch is used only to own device memory and to hand its current stream to the
 library; every computation runs in the library's HIP kernels. Loading fails
@@ -20,6 +21,9 @@ OK = 0
 INVALID_ARGUMENT = -1
 OUT_OF_MEMORY = -2
 DEVICE_ERROR = -3
+NOT_FOUND = -4
+
+GGML_F32, GGML_F16, GGML_I8, GGML_I16, GGML_I32, GGML_I64, GGML_F64, GGML_BF16 = 0, 1, 24, 25, 26, 27, 28, 30
 
 vp = C.c_void_p
 u32 = C.c_uint32
@@ -61,6 +65,20 @@ class KernelProfile(C.Structure):
     _fields_ = [("name", C.c_char * 48), ("launches", C.c_uint64), ("total_ms", C.c_double)]
 
 
+class GgufTensor(C.Structure):
+    _fields_ = [("type", u32), ("dimension_count", u32), ("dimensions", C.c_uint64 * 4),
+                ("elements", C.c_uint64), ("bytes", C.c_uint64), ("data", vp)]
+
+
+class MoeGeometry(C.Structure):
+    _fields_ = [("layers", u32), ("hidden", u32), ("experts", u32), ("active_experts", u32),
+                ("expert_hidden", u32), ("shared_hidden", u32)]
+
+
+u64 = C.c_uint64
+cs = C.c_char_p
+
+
 # (name, restype, argtypes) of every exported entry point.
 SIGNATURES = [
     ("adi_hip_context_create", C.c_int, [C.c_int, C.POINTER(vp)]),
@@ -94,6 +112,26 @@ SIGNATURES = [
     ("adi_hip_moe_forward", C.c_int, [vp, C.POINTER(MoeLayer), vp, u32, vp, vp, vp, vp]),
     ("adi_hip_profiling_enable", C.c_int, [vp, C.c_int]),
     ("adi_hip_profiling_read", C.c_int, [vp, C.POINTER(KernelProfile), u32, C.POINTER(u32)]),
+    # include/adi_hip_gguf.h
+    ("adi_hip_gguf_open", C.c_int, [cs, C.POINTER(vp)]),
+    ("adi_hip_gguf_close", None, [vp]),
+    ("adi_hip_gguf_error", C.c_char_p, []),
+    ("adi_hip_gguf_version", u32, [vp]),
+    ("adi_hip_gguf_alignment", u64, [vp]),
+    ("adi_hip_gguf_metadata_count", u64, [vp]),
+    ("adi_hip_gguf_tensor_count", u64, [vp]),
+    ("adi_hip_gguf_find_tensor", C.c_int, [vp, cs, C.POINTER(GgufTensor)]),
+    ("adi_hip_gguf_integer", C.c_int, [vp, cs, C.POINTER(u64)]),
+    ("adi_hip_gguf_number", C.c_int, [vp, cs, C.POINTER(C.c_double)]),
+    ("adi_hip_gguf_boolean", C.c_int, [vp, cs, C.POINTER(C.c_int)]),
+    ("adi_hip_gguf_string", C.c_int, [vp, cs, C.POINTER(vp), C.POINTER(u64)]),
+    ("adi_hip_gguf_string_array", C.c_int, [vp, cs, u64, C.POINTER(u64), C.POINTER(vp), C.POINTER(u64)]),
+    ("adi_hip_gguf_integer_array", C.c_int, [vp, cs, u64, C.POINTER(u64), C.POINTER(u64)]),
+    ("adi_hip_gguf_moe_geometry", C.c_int, [vp, C.POINTER(MoeGeometry)]),
+    ("adi_hip_gguf_check_moe_layer", C.c_int, [vp, u32]),
+    ("adi_hip_gguf_upload_codebooks", C.c_int, [vp, vp, C.POINTER(vp), C.POINTER(vp)]),
+    ("adi_hip_gguf_upload_moe_layer", C.c_int, [vp, vp, u32, vp, vp, C.POINTER(vp), C.POINTER(MoeLayer)]),
+    ("adi_hip_moe_weights_destroy", None, [vp]),
 ]
 
 _lib: Optional[C.CDLL] = None
@@ -288,6 +326,176 @@ def upload_moe_layer(ctx: Context, layer, expert_book: int, ne_book: int) -> Dev
     s = MoeLayer(layer.hidden, layer.expert_hidden, layer.experts, router, gate,
                  stacks[0], stacks[1], stacks[2], expert_book, shared[0], shared[1], shared[2])
     return DeviceMoeLayer(s, tuple(keep), layer.experts, layer.hidden)
+
+
+# ---- checkpoints (GGUF v3) ---------------------------------------------------
+
+_GGML_NUMPY = {GGML_F32: np.float32, GGML_F16: np.uint16, GGML_I8: np.int8, GGML_I16: np.uint16,
+               GGML_I32: np.int32, GGML_I64: np.int64, GGML_F64: np.float64, GGML_BF16: np.uint16}
+
+
+class Gguf:
+    """An open GGUF v3 file (adi_hip_gguf); host-side, needs no GPU."""
+
+    def __init__(self, path: str):
+        self.lib = load()
+        handle = vp()
+        status = self.lib.adi_hip_gguf_open(os.fsencode(path), C.byref(handle))
+        if status != OK:
+            raise HipError(status, self.lib.adi_hip_gguf_error().decode())
+        self.handle = handle
+
+    def _fail(self, status: int):
+        raise HipError(status, self.lib.adi_hip_gguf_error().decode())
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.adi_hip_gguf_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def version(self) -> int:
+        return self.lib.adi_hip_gguf_version(self.handle)
+
+    @property
+    def alignment(self) -> int:
+        return self.lib.adi_hip_gguf_alignment(self.handle)
+
+    @property
+    def metadata_count(self) -> int:
+        return self.lib.adi_hip_gguf_metadata_count(self.handle)
+
+    @property
+    def tensor_count(self) -> int:
+        return self.lib.adi_hip_gguf_tensor_count(self.handle)
+
+    def tensor(self, name: str):
+        """(GgufTensor, numpy view of its data) or None when absent."""
+        t = GgufTensor()
+        status = self.lib.adi_hip_gguf_find_tensor(self.handle, name.encode(), C.byref(t))
+        if status == NOT_FOUND:
+            return None
+        if status != OK:
+            self._fail(status)
+        dtype = _GGML_NUMPY[t.type]
+        buf = (C.c_uint8 * t.bytes).from_address(t.data)
+        return t, np.frombuffer(buf, dtype=dtype, count=t.elements)
+
+    def _scalar(self, fn, key, ctype):
+        out = ctype()
+        status = fn(self.handle, key.encode(), C.byref(out))
+        if status == NOT_FOUND:
+            return None
+        if status != OK:
+            self._fail(status)
+        return out.value
+
+    def integer(self, key: str):
+        return self._scalar(self.lib.adi_hip_gguf_integer, key, u64)
+
+    def number(self, key: str):
+        return self._scalar(self.lib.adi_hip_gguf_number, key, C.c_double)
+
+    def boolean(self, key: str):
+        v = self._scalar(self.lib.adi_hip_gguf_boolean, key, C.c_int)
+        return None if v is None else bool(v)
+
+    def string(self, key: str):
+        data, length = vp(), u64()
+        status = self.lib.adi_hip_gguf_string(self.handle, key.encode(), C.byref(data), C.byref(length))
+        if status == NOT_FOUND:
+            return None
+        if status != OK:
+            self._fail(status)
+        return C.string_at(data.value, length.value).decode()
+
+    def string_array(self, key: str):
+        count, data, length = u64(), vp(), u64()
+        status = self.lib.adi_hip_gguf_string_array(self.handle, key.encode(), 0, C.byref(count), None, None)
+        if status == NOT_FOUND:
+            return []
+        if status != OK:
+            self._fail(status)
+        out = []
+        for i in range(count.value):
+            self.lib.adi_hip_gguf_string_array(self.handle, key.encode(), i, C.byref(count),
+                                               C.byref(data), C.byref(length))
+            out.append(C.string_at(data.value, length.value).decode())
+        return out
+
+    def integer_array(self, key: str):
+        count, value = u64(), u64()
+        status = self.lib.adi_hip_gguf_integer_array(self.handle, key.encode(), 0, C.byref(count), None)
+        if status == NOT_FOUND:
+            return []
+        if status != OK:
+            self._fail(status)
+        out = []
+        for i in range(count.value):
+            self.lib.adi_hip_gguf_integer_array(self.handle, key.encode(), i, C.byref(count), C.byref(value))
+            out.append(value.value)
+        return out
+
+    def moe_geometry(self) -> MoeGeometry:
+        g = MoeGeometry()
+        status = self.lib.adi_hip_gguf_moe_geometry(self.handle, C.byref(g))
+        if status != OK:
+            self._fail(status)
+        return g
+
+    def check_moe_layer(self, layer: int) -> None:
+        status = self.lib.adi_hip_gguf_check_moe_layer(self.handle, layer)
+        if status != OK:
+            self._fail(status)
+
+
+@dataclass
+class GgufMoeLayer:
+    """A layer uploaded from a checkpoint; owns its adi_hip_moe_weights."""
+    struct: MoeLayer
+    weights: int
+    experts: int
+    hidden: int
+    lib: object = None
+
+    def close(self) -> None:
+        if self.weights:
+            self.lib.adi_hip_moe_weights_destroy(vp(self.weights))
+            self.weights = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def upload_codebooks_gguf(ctx: Context, file: Gguf):
+    expert, ne = vp(), vp()
+    ctx.check(ctx.lib.adi_hip_gguf_upload_codebooks(ctx.handle, file.handle, C.byref(expert), C.byref(ne)))
+    ctx._books.extend([expert, ne])
+    return expert.value, ne.value
+
+
+def upload_moe_layer_gguf(ctx: Context, file: Gguf, layer: int, expert_book: int,
+                          ne_book: int) -> GgufMoeLayer:
+    weights = vp()
+    s = MoeLayer()
+    ctx.check(ctx.lib.adi_hip_gguf_upload_moe_layer(ctx.handle, file.handle, layer, vp(expert_book),
+                                                    vp(ne_book), C.byref(weights), C.byref(s)))
+    return GgufMoeLayer(s, weights.value, s.experts, s.hidden, ctx.lib)
 
 
 # ---- calls on device tensors ------------------------------------------------

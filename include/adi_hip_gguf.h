@@ -1,0 +1,152 @@
+/*
+ * adi_hip_gguf.h -- the checkpoint side of the packed path: a GGUF v3 reader
+ * and the upload of one layer's packed MoE tensors into the device
+ * descriptors of adi_hip.h.
+ *
+ * The reference maps the checkpoint with adi::GgufFile (include/adi/gguf.hpp,
+ * src/gguf.cpp) and reads the packed tensors as non-owning host views in
+ * adi::MachModel (src/model.cpp:267-314 non_expert, 431-533 bf16_matrix and
+ * expert, 808-880 validate_manifest). Here the same tensors, under the same
+ * names and with the same shape rules, are copied once into HBM, where they
+ * stay packed; the kernels decode them in place.
+ *
+ * Tensor names (docs/gguf.md of the reference):
+ *   mach.expert.{layer}.e{chunk}.{gate|up|down}.{trellis|su|sv|wave_gamma}
+ *       32-expert chunks, chunk = 0, 32, 64, ...; GGUF dims {24, tiles, 32},
+ *       {columns, 32}, {rows, 32}, {rows/16 + columns/16, 32}; i16, f16 x 3
+ *   mach.ne.{layer}.{source}|{trellis|SU|SV|Wscale}
+ *       source = model.language_model.layers.{layer}.mlp.shared_expert.
+ *       {gate|up|down}_proj.weight; dims {64, tiles}, {columns}, {rows}, {1};
+ *       i16, i8, i8, f32
+ *   hf.model.language_model.layers.{layer}.mlp.gate.weight          bf16 {hidden, experts}
+ *   hf.model.language_model.layers.{layer}.mlp.shared_expert_gate.weight  bf16 {hidden, 1}
+ *   mach.tlut.expert.tlut  f32 {8, 32768};  mach.tlut.ne.tlut  f32 {2, 512}
+ *
+ * File-level calls take no context: their failures leave a message for
+ * adi_hip_gguf_error() (per calling thread). Upload calls take a context and
+ * report through adi_hip_last_error().
+ */
+#ifndef ADI_HIP_GGUF_H
+#define ADI_HIP_GGUF_H
+
+#include "adi_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ADI_HIP_NOT_FOUND (-4) /* tensor or metadata key absent (or of another type) */
+
+/* GGML storage types the reader accepts (adi::GgmlType,
+ * include/adi/gguf.hpp:30-39). */
+#define ADI_HIP_GGML_F32 0
+#define ADI_HIP_GGML_F16 1
+#define ADI_HIP_GGML_I8 24
+#define ADI_HIP_GGML_I16 25
+#define ADI_HIP_GGML_I32 26
+#define ADI_HIP_GGML_I64 27
+#define ADI_HIP_GGML_F64 28
+#define ADI_HIP_GGML_BF16 30
+
+typedef struct adi_hip_gguf adi_hip_gguf;
+
+/* adi::GgufTensor (include/adi/gguf.hpp:47-54) with its data. */
+typedef struct {
+    uint32_t type;            /* ADI_HIP_GGML_* */
+    uint32_t dimension_count; /* 1..4 */
+    uint64_t dimensions[4];   /* GGUF order: dimensions[0] is contiguous */
+    uint64_t elements;
+    uint64_t bytes;
+    const void *data;         /* host pointer into the file mapping */
+} adi_hip_gguf_tensor;
+
+/* GgufFile::GgufFile (src/gguf.cpp:232-330): maps the file read-only and
+ * validates it: magic "GGUF", version 3, known metadata value types (arrays
+ * nested at most 8 deep), no duplicate metadata key or tensor name, 1 to 4
+ * nonzero dimensions, a supported tensor type, general.alignment a nonzero
+ * power of two (default 32), and every tensor's bytes inside the file.
+ * On failure *out is NULL. */
+int adi_hip_gguf_open(const char *path, adi_hip_gguf **out);
+void adi_hip_gguf_close(adi_hip_gguf *file);
+/* Message of the calling thread's last failed file-level call. */
+const char *adi_hip_gguf_error(void);
+
+uint32_t adi_hip_gguf_version(const adi_hip_gguf *file);
+uint64_t adi_hip_gguf_alignment(const adi_hip_gguf *file);
+uint64_t adi_hip_gguf_metadata_count(const adi_hip_gguf *file);
+uint64_t adi_hip_gguf_tensor_count(const adi_hip_gguf *file);
+
+/* GgufFile::find_tensor + tensor_data (src/gguf.cpp:417-425, 570-572). */
+int adi_hip_gguf_find_tensor(const adi_hip_gguf *file, const char *name,
+                             adi_hip_gguf_tensor *out);
+
+/* GgufFile::integer / number / boolean / string (src/gguf.cpp:427-503):
+ * integer accepts unsigned types and non-negative signed ones; number also
+ * f32/f64; boolean only bool; string only string. */
+int adi_hip_gguf_integer(const adi_hip_gguf *file, const char *key, uint64_t *out);
+int adi_hip_gguf_number(const adi_hip_gguf *file, const char *key, double *out);
+int adi_hip_gguf_boolean(const adi_hip_gguf *file, const char *key, int *out);
+int adi_hip_gguf_string(const adi_hip_gguf *file, const char *key, const char **data,
+                        uint64_t *length);
+/* GgufFile::string_array / integer_array (src/gguf.cpp:505-568): *count
+ * receives the element count of an array of strings (string_array) or of
+ * unsigned integers (integer_array); item `index` when index < count. */
+int adi_hip_gguf_string_array(const adi_hip_gguf *file, const char *key, uint64_t index,
+                              uint64_t *count, const char **data, uint64_t *length);
+int adi_hip_gguf_integer_array(const adi_hip_gguf *file, const char *key, uint64_t index,
+                               uint64_t *count, uint64_t *value);
+
+/* The MoE geometry of the checkpoint (adi::MachConfig, src/model.cpp:216-223,
+ * qwen35moe.* keys). */
+typedef struct {
+    uint32_t layers;         /* qwen35moe.block_count */
+    uint32_t hidden;         /* qwen35moe.embedding_length */
+    uint32_t experts;        /* qwen35moe.expert_count */
+    uint32_t active_experts; /* qwen35moe.expert_used_count */
+    uint32_t expert_hidden;  /* qwen35moe.expert_feed_forward_length */
+    uint32_t shared_hidden;  /* qwen35moe.expert_shared_feed_forward_length */
+} adi_hip_moe_geometry;
+
+/* Reads the geometry and checks the codec metadata the packed path depends
+ * on (src/model.cpp:180-213): general.architecture qwen35moe, adi.additive,
+ * adi.format_version 1, the expert and NE codec names, adi.expert.k_num 3,
+ * k_den 2, l 16, v 8, tlut_bits 15, tile_x and tile_y 16; the geometry the
+ * kernels need (top-8 routing, a shared expert as wide as the routed ones,
+ * whole 32-expert chunks, power-of-two widths of at least 64); and the two
+ * TLUT tensors (shape, type, finite values, src/model.cpp:808-833). */
+int adi_hip_gguf_moe_geometry(const adi_hip_gguf *file, adi_hip_moe_geometry *out);
+
+/* Validates layer `layer`'s MoE tensors on the host as
+ * MachModel::validate_manifest does (src/model.cpp:834-880 with the checks of
+ * expert, non_expert and bf16_matrix): presence, type and shape of every
+ * tensor, finite f16 su/sv/wave_gamma and bf16 router rows, +-1 SU/SV and a
+ * positive finite Wscale. */
+int adi_hip_gguf_check_moe_layer(const adi_hip_gguf *file, uint32_t layer);
+
+/* The model's codebooks from mach.tlut.expert.tlut and mach.tlut.ne.tlut (the
+ * tables MachModel::cache_descriptors derives, src/model.cpp:546-551). */
+int adi_hip_gguf_upload_codebooks(adi_hip_context *ctx, const adi_hip_gguf *file,
+                                  adi_hip_codebook **expert_codebook,
+                                  adi_hip_codebook **ne_codebook);
+
+/* One layer's packed MoE tensors in one device allocation. */
+typedef struct adi_hip_moe_weights adi_hip_moe_weights;
+
+/* Validates layer `layer` (as adi_hip_gguf_check_moe_layer), copies its
+ * packed tensors into HBM once, still packed, and fills *descriptor with
+ * device pointers into that copy: the 32-expert chunks are laid end to end,
+ * so expert e's trellis, su, sv and gamma sit where adi_hip_expert_stack
+ * expects them. The weights stay valid until adi_hip_moe_weights_destroy;
+ * the file may be closed after the call. */
+int adi_hip_gguf_upload_moe_layer(adi_hip_context *ctx, const adi_hip_gguf *file, uint32_t layer,
+                                  const adi_hip_codebook *expert_codebook,
+                                  const adi_hip_codebook *ne_codebook,
+                                  adi_hip_moe_weights **weights,
+                                  adi_hip_moe_layer *descriptor);
+void adi_hip_moe_weights_destroy(adi_hip_moe_weights *weights);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

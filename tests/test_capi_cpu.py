@@ -13,6 +13,7 @@ from adi_amd import hip
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "adi_hip.h")
+HEADERS = [HEADER, os.path.join(ROOT, "include", "adi_hip_gguf.h")]
 
 STRUCTS = {
     "adi_hip_expert_matrix": hip.ExpertMatrix,
@@ -22,12 +23,15 @@ STRUCTS = {
     "adi_hip_expert_stack": hip.ExpertStack,
     "adi_hip_moe_layer": hip.MoeLayer,
     "adi_hip_kernel_profile": hip.KernelProfile,
+    "adi_hip_gguf_tensor": hip.GgufTensor,
+    "adi_hip_moe_geometry": hip.MoeGeometry,
 }
 
 
 def declared_functions():
-    text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|void|const char \*)\s*(adi_hip_\w+)\s*\(", text, re.M)))
+    text = "".join(open(h).read() for h in HEADERS)
+    return sorted(set(re.findall(r"^\s*(?:int|void|uint32_t|uint64_t|const char \*)\s*(adi_hip_\w+)\s*\(",
+                                 text, re.M)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -45,7 +49,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_struct_layouts_match_header(tmp_path):
-    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "adi_hip.h"', "int main(void) {"]
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "adi_hip_gguf.h"', "int main(void) {"]
     for cname, ctype in STRUCTS.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
         for field, _ in ctype._fields_:
@@ -69,7 +73,7 @@ def test_struct_layouts_match_header(tmp_path):
 
 def test_header_compiles_as_cpp(tmp_path):
     src = tmp_path / "use.cpp"
-    src.write_text('#include "adi_hip.h"\nint main() { adi_hip_context *c = nullptr; '
+    src.write_text('#include "adi_hip_gguf.h"\nint main() { adi_hip_context *c = nullptr; '
                    'return adi_hip_set_reduction_isa(c, 16) == ADI_HIP_INVALID_ARGUMENT ? 0 : 1; }\n')
     subprocess.run(["g++", "-std=c++17", "-fsyntax-only", "-Wall", "-Werror", "-I",
                     os.path.dirname(HEADER), str(src)], check=True)
