@@ -410,6 +410,21 @@ const adi_hip_gguf_tensor &required_tensor(const adi_hip_gguf &f, const std::str
 }
 
 bool finite_f16(uint16_t bits) { return (bits & 0x7C00u) != 0x7C00u; }
+
+// f16 bits to float on the host (finite values: normals and subnormals).
+float f16_bits_to_float_host(uint16_t bits) {
+    const uint32_t sign = (bits & 0x8000u) << 16;
+    const uint32_t exponent = (bits >> 10) & 0x1Fu;
+    const uint32_t mantissa = bits & 0x3FFu;
+    if (exponent == 0) {
+        const float v = std::ldexp(static_cast<float>(mantissa), -24);
+        return sign ? -v : v;
+    }
+    const uint32_t word = sign | ((exponent + 112u) << 23) | (mantissa << 13);
+    float v;
+    std::memcpy(&v, &word, sizeof(v));
+    return v;
+}
 bool finite_bf16(uint16_t bits) { return (bits & 0x7F80u) != 0x7F80u; }
 
 void require_finite(const adi_hip_gguf_tensor &t, bool (*finite)(uint16_t), const std::string &name) {
@@ -538,10 +553,62 @@ LayerTensors check_layer(const adi_hip_gguf &f, const adi_hip_moe_geometry &g, u
     return L;
 }
 
+// The embedding tensors, checked (src/model.cpp:316-363, 836-849).
+struct EmbeddingTensors {
+    const adi_hip_gguf_tensor *packed, *minimum, *maximum, *indexes, *bits;
+    uint32_t rows, columns;
+};
+
+EmbeddingTensors check_embedding(const adi_hip_gguf &f) {
+    const uint32_t hidden = required_u32(f, "qwen35moe.embedding_length");
+    const adi_hip_gguf_tensor *q = f.tensor("mach.embedding.q_packed");
+    if (q == nullptr || q->type != ADI_HIP_GGML_I8) {
+        model_fail("missing or invalid tensor 'mach.embedding.q_packed'");
+    }
+    if (q->dimension_count != 2 || q->dimensions[0] * 2 != hidden || hidden % 64 != 0 ||
+        q->dimensions[1] > 0xFFFFFFFFull ||
+        static_cast<uint64_t>(hidden) * q->dimensions[1] > 0xFFFFFFFFull) {
+        model_fail("malformed embedding geometry");
+    }
+    EmbeddingTensors t{};
+    t.rows = static_cast<uint32_t>(q->dimensions[1]);
+    t.columns = hidden;
+    t.packed = &required_tensor(f, "mach.embedding.q_packed", ADI_HIP_GGML_I8, {hidden / 2u, t.rows});
+    t.minimum = &required_tensor(f, "mach.embedding.mn", ADI_HIP_GGML_F16, {hidden / 64u, t.rows});
+    t.maximum = &required_tensor(f, "mach.embedding.mx", ADI_HIP_GGML_F16, {hidden / 64u, t.rows});
+    const adi_hip_gguf_tensor *ix = f.tensor("mach.embedding.exc_idx");
+    const adi_hip_gguf_tensor *bx = f.tensor("mach.embedding.exc_bits");
+    if (ix == nullptr || ix->type != ADI_HIP_GGML_I32 || bx == nullptr ||
+        bx->type != ADI_HIP_GGML_I16 || ix->dimension_count != 1 || bx->dimension_count != 1 ||
+        ix->dimensions[0] != bx->dimensions[0]) {
+        model_fail("malformed embedding tensors");
+    }
+    t.indexes = &required_tensor(f, "mach.embedding.exc_idx", ADI_HIP_GGML_I32, {ix->dimensions[0]});
+    t.bits = &required_tensor(f, "mach.embedding.exc_bits", ADI_HIP_GGML_I16, {bx->dimensions[0]});
+    const uint32_t *idx = static_cast<const uint32_t *>(t.indexes->data);
+    const uint64_t total = static_cast<uint64_t>(t.rows) * t.columns;
+    for (uint64_t i = 0; i < t.indexes->elements; ++i) {
+        if ((i > 0 && idx[i] <= idx[i - 1]) || idx[i] >= total) {
+            model_fail("malformed embedding tensors");
+        }
+    }
+    require_finite(*t.minimum, finite_f16, "mach.embedding.mn");
+    require_finite(*t.maximum, finite_f16, "mach.embedding.mx");
+    require_finite(*t.bits, finite_bf16, "mach.embedding.exc_bits");
+    const uint16_t *mn = static_cast<const uint16_t *>(t.minimum->data);
+    const uint16_t *mx = static_cast<const uint16_t *>(t.maximum->data);
+    for (uint64_t i = 0; i < t.minimum->elements; ++i) {
+        if (f16_bits_to_float_host(mn[i]) > f16_bits_to_float_host(mx[i])) {
+            model_fail("embedding minimum exceeds maximum");
+        }
+    }
+    return t;
+}
+
 }  // namespace
 }  // namespace adi_hip
 
-struct adi_hip_moe_weights {
+struct adi_hip_weights {
     int device = 0;
     void *base = nullptr;
 };
@@ -750,7 +817,7 @@ int adi_hip_gguf_upload_codebooks(adi_hip_context *ctx, const adi_hip_gguf *file
 int adi_hip_gguf_upload_moe_layer(adi_hip_context *ctx, const adi_hip_gguf *file, uint32_t layer,
                                   const adi_hip_codebook *expert_codebook,
                                   const adi_hip_codebook *ne_codebook,
-                                  adi_hip_moe_weights **weights,
+                                  adi_hip_weights **weights,
                                   adi_hip_moe_layer *descriptor) {
     return guarded(ctx, [&] {
         require(file != nullptr && weights != nullptr && descriptor != nullptr,
@@ -799,7 +866,7 @@ int adi_hip_gguf_upload_moe_layer(adi_hip_context *ctx, const adi_hip_gguf *file
                 shared_at[pr][fi] = place({L.shared[pr][fi]});
             }
         }
-        auto *w = new adi_hip_moe_weights;
+        auto *w = new adi_hip_weights;
         w->device = ctx->device;
         if (hipMalloc(&w->base, total) != hipSuccess) {
             delete w;
@@ -845,7 +912,62 @@ int adi_hip_gguf_upload_moe_layer(adi_hip_context *ctx, const adi_hip_gguf *file
     });
 }
 
-void adi_hip_moe_weights_destroy(adi_hip_moe_weights *weights) {
+int adi_hip_gguf_check_embedding(const adi_hip_gguf *file) {
+    return file_call([&] {
+        if (file == nullptr) {
+            fail(ADI_HIP_INVALID_ARGUMENT, "model: null file");
+        }
+        (void)check_embedding(*file);
+        return ADI_HIP_OK;
+    });
+}
+
+int adi_hip_gguf_upload_embedding(adi_hip_context *ctx, const adi_hip_gguf *file,
+                                  adi_hip_weights **weights, adi_hip_embedding *descriptor) {
+    return guarded(ctx, [&] {
+        require(file != nullptr && weights != nullptr && descriptor != nullptr,
+                "GGUF embedding upload: null argument");
+        *weights = nullptr;
+        const EmbeddingTensors t = check_embedding(*file);
+        const adi_hip_gguf_tensor *parts[5] = {t.packed, t.minimum, t.maximum, t.indexes, t.bits};
+        size_t at[5], total = 0;
+        for (int i = 0; i < 5; ++i) {
+            at[i] = total;
+            total = (total + static_cast<size_t>(parts[i]->bytes) + 255) & ~size_t(255);
+        }
+        auto *w = new adi_hip_weights;
+        w->device = ctx->device;
+        if (hipMalloc(&w->base, total) != hipSuccess) {
+            delete w;
+            fail(ADI_HIP_OUT_OF_MEMORY, "GGUF embedding upload: device allocation failed");
+        }
+        try {
+            for (int i = 0; i < 5; ++i) {
+                check_hip(hipMemcpy(static_cast<char *>(w->base) + at[i], parts[i]->data,
+                                    static_cast<size_t>(parts[i]->bytes), hipMemcpyHostToDevice),
+                          "GGUF embedding upload copy");
+            }
+        } catch (...) {
+            (void)hipFree(w->base);
+            delete w;
+            throw;
+        }
+        const char *base = static_cast<const char *>(w->base);
+        adi_hip_embedding d{};
+        d.rows = t.rows;
+        d.columns = t.columns;
+        d.packed = reinterpret_cast<const uint8_t *>(base + at[0]);
+        d.minimum_f16 = reinterpret_cast<const uint16_t *>(base + at[1]);
+        d.maximum_f16 = reinterpret_cast<const uint16_t *>(base + at[2]);
+        d.exception_indexes = reinterpret_cast<const uint32_t *>(base + at[3]);
+        d.exception_bf16 = reinterpret_cast<const uint16_t *>(base + at[4]);
+        d.exception_count = static_cast<uint32_t>(t.indexes->elements);
+        *descriptor = d;
+        *weights = w;
+    });
+}
+
+void adi_hip_weights_destroy(adi_hip_weights *weights) {
     if (weights == nullptr) {
         return;
     }

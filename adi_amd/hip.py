@@ -49,6 +49,12 @@ class Bf16Matrix(C.Structure):
     _fields_ = [("rows", u32), ("columns", u32), ("values", vp)]
 
 
+class Embedding(C.Structure):
+    _fields_ = [("rows", u32), ("columns", u32), ("packed", vp), ("minimum_f16", vp),
+                ("maximum_f16", vp), ("exception_indexes", vp), ("exception_bf16", vp),
+                ("exception_count", u32)]
+
+
 class ExpertStack(C.Structure):
     _fields_ = [("trellis", vp), ("su_f16", vp), ("sv_f16", vp), ("wave_gamma_f16", vp)]
 
@@ -110,6 +116,8 @@ SIGNATURES = [
     ("adi_hip_top_experts", C.c_int, [vp, vp, u32, u32, vp, vp]),
     ("adi_hip_moe_route", C.c_int, [vp, vp, vp, u32, u32, vp, vp, vp, vp, vp, vp]),
     ("adi_hip_moe_forward", C.c_int, [vp, C.POINTER(MoeLayer), vp, u32, vp, vp, vp, vp]),
+    ("adi_hip_embedding_rows", C.c_int, [vp, C.POINTER(Embedding), vp, u32, vp]),
+    ("adi_hip_argmax_rows", C.c_int, [vp, vp, u32, u32, vp]),
     ("adi_hip_profiling_enable", C.c_int, [vp, C.c_int]),
     ("adi_hip_profiling_read", C.c_int, [vp, C.POINTER(KernelProfile), u32, C.POINTER(u32)]),
     # include/adi_hip_gguf.h
@@ -131,7 +139,9 @@ SIGNATURES = [
     ("adi_hip_gguf_check_moe_layer", C.c_int, [vp, u32]),
     ("adi_hip_gguf_upload_codebooks", C.c_int, [vp, vp, C.POINTER(vp), C.POINTER(vp)]),
     ("adi_hip_gguf_upload_moe_layer", C.c_int, [vp, vp, u32, vp, vp, C.POINTER(vp), C.POINTER(MoeLayer)]),
-    ("adi_hip_moe_weights_destroy", None, [vp]),
+    ("adi_hip_weights_destroy", None, [vp]),
+    ("adi_hip_gguf_upload_embedding", C.c_int, [vp, vp, C.POINTER(vp), C.POINTER(Embedding)]),
+    ("adi_hip_gguf_check_embedding", C.c_int, [vp]),
 ]
 
 _lib: Optional[C.CDLL] = None
@@ -460,10 +470,15 @@ class Gguf:
         if status != OK:
             self._fail(status)
 
+    def check_embedding(self) -> None:
+        status = self.lib.adi_hip_gguf_check_embedding(self.handle)
+        if status != OK:
+            self._fail(status)
+
 
 @dataclass
 class GgufMoeLayer:
-    """A layer uploaded from a checkpoint; owns its adi_hip_moe_weights."""
+    """A layer uploaded from a checkpoint; owns its adi_hip_weights."""
     struct: MoeLayer
     weights: int
     experts: int
@@ -472,7 +487,7 @@ class GgufMoeLayer:
 
     def close(self) -> None:
         if self.weights:
-            self.lib.adi_hip_moe_weights_destroy(vp(self.weights))
+            self.lib.adi_hip_weights_destroy(vp(self.weights))
             self.weights = 0
 
     def __del__(self):
@@ -496,6 +511,60 @@ def upload_moe_layer_gguf(ctx: Context, file: Gguf, layer: int, expert_book: int
     ctx.check(ctx.lib.adi_hip_gguf_upload_moe_layer(ctx.handle, file.handle, layer, vp(expert_book),
                                                     vp(ne_book), C.byref(weights), C.byref(s)))
     return GgufMoeLayer(s, weights.value, s.experts, s.hidden, ctx.lib)
+
+
+@dataclass
+class GgufEmbedding:
+    """An embedding table uploaded from a checkpoint; owns its adi_hip_weights."""
+    struct: Embedding
+    weights: int
+    lib: object = None
+
+    def close(self) -> None:
+        if self.weights:
+            self.lib.adi_hip_weights_destroy(vp(self.weights))
+            self.weights = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def upload_embedding_gguf(ctx: Context, file: Gguf) -> GgufEmbedding:
+    weights = vp()
+    s = Embedding()
+    ctx.check(ctx.lib.adi_hip_gguf_upload_embedding(ctx.handle, file.handle, C.byref(weights),
+                                                    C.byref(s)))
+    return GgufEmbedding(s, weights.value, ctx.lib)
+
+
+@dataclass
+class DeviceEmbedding:
+    struct: Embedding
+    tensors: tuple
+
+
+def upload_embedding(ctx: Context, e) -> DeviceEmbedding:
+    """e: adi_amd.synthetic.Embedding."""
+    keep = [ctx.to_device(a) for a in (e.packed, e.minimum_f16, e.maximum_f16)]
+    count = int(e.exception_indexes.size)
+    if count:
+        keep += [ctx.to_device(e.exception_indexes), ctx.to_device(e.exception_bf16)]
+    ptrs = [t.data_ptr() for t in keep] + [None, None][:5 - len(keep)]
+    s = Embedding(e.rows, e.columns, *ptrs, count)
+    return DeviceEmbedding(s, tuple(keep))
+
+
+def embedding_rows(ctx: Context, emb, tokens, count: int, out) -> None:
+    ctx.check(ctx.lib.adi_hip_embedding_rows(ctx.handle, C.byref(emb.struct), tokens.data_ptr(),
+                                             count, out.data_ptr()))
+
+
+def argmax_rows(ctx: Context, logits, rows: int, count: int, tokens) -> None:
+    ctx.check(ctx.lib.adi_hip_argmax_rows(ctx.handle, logits.data_ptr(), rows, count,
+                                          tokens.data_ptr()))
 
 
 # ---- calls on device tensors ------------------------------------------------

@@ -82,6 +82,17 @@ class HeadChunk:
 
 
 @dataclass
+class Embedding:
+    rows: int
+    columns: int
+    packed: np.ndarray             # u8 [rows*columns/2], high nibble first
+    minimum_f16: np.ndarray        # u16 [rows*columns/64]
+    maximum_f16: np.ndarray        # u16 [rows*columns/64]
+    exception_indexes: np.ndarray  # u32 ascending flat indexes
+    exception_bf16: np.ndarray     # u16
+
+
+@dataclass
 class MoeLayer:
     hidden: int
     expert_hidden: int
@@ -150,6 +161,30 @@ def head_chunk(rng, rows: int, columns: int, protected: int = 0) -> HeadChunk:
         head.protected_rows = np.sort(rng.choice(rows, protected, replace=False)).astype(np.uint32)
         head.protected_bf16 = bf16_bits_rne(rng.normal(0.0, 0.02, protected * columns).astype(np.float32))
     return head
+
+
+def embedding(rng, rows: int, columns: int, exceptions: int = 0) -> Embedding:
+    """An affine_int4_g64 table with bf16 exceptions: per 64-column group a
+    minimum and maximum (every 17th group with maximum == minimum, so the step
+    takes its 1e-8 floor); the exceptions include the first and last column
+    of row 0 and of the last row."""
+    groups = rows * columns // 64
+    packed = rng.integers(0, 256, rows * columns // 2, dtype=np.uint8)
+    minimum = rng.normal(-0.06, 0.02, groups).astype(np.float32)
+    width = np.abs(rng.normal(0.1, 0.03, groups)).astype(np.float32)
+    width[::17] = 0.0
+    mn = f16_bits(minimum)
+    mx = f16_bits(f16_to_f32(mn) + width)
+    mx = np.where(f16_to_f32(mx) < f16_to_f32(mn), mn, mx).astype(np.uint16)
+    idx = set()
+    if exceptions:
+        total = rows * columns
+        idx.update([0, columns - 1, total - columns, total - 1])
+        while len(idx) < exceptions:
+            idx.add(int(rng.integers(0, total)))
+    ex = np.array(sorted(idx), dtype=np.uint32)
+    values = bf16_bits_rne(rng.normal(0.0, 0.5, ex.size).astype(np.float32))
+    return Embedding(rows, columns, packed, mn, mx, ex, values.astype(np.uint16))
 
 
 def hidden_states(rng, batch: int, hidden: int) -> np.ndarray:

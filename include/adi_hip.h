@@ -133,6 +133,18 @@ typedef struct {
     const uint16_t *values; /* rows*columns bf16 bits, row-major */
 } adi_hip_bf16_matrix;
 
+/* adi::MachEmbedding (include/adi/kernels.hpp:54-62). */
+typedef struct {
+    uint32_t rows;                     /* vocabulary */
+    uint32_t columns;                  /* hidden, a multiple of 64 */
+    const uint8_t *packed;             /* rows*columns/2 bytes, high nibble first */
+    const uint16_t *minimum_f16;       /* rows*columns/64 */
+    const uint16_t *maximum_f16;       /* rows*columns/64 */
+    const uint32_t *exception_indexes; /* exception_count, ascending flat indexes */
+    const uint16_t *exception_bf16;    /* exception_count */
+    uint32_t exception_count;
+} adi_hip_embedding;
+
 /* ---- Backend op table entries -------------------------------------------- */
 /* Inputs [batch, columns] and outputs [batch, rows], batch-major, device. */
 
@@ -268,6 +280,26 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *layer,
                         const float *inputs, uint32_t batch,
                         const float *logit_bias, float *outputs,
                         uint32_t *route_expert, float *route_weight);
+
+/* ---- token side of decoding ----------------------------------------------- */
+
+/* Backend::embedding_row -> mach_embedding_row (src/kernels.cpp:802-845) for
+ * `count` tokens at once: per 64-column group value = min + code * step with
+ * step = max(max - min, 1e-8) / 15 (f16 min/max, separate multiply and add),
+ * then the row's bf16 exceptions overwrite their columns; bit-exact.
+ * tokens: DEVICE [count] (a sampled token never leaves HBM); outputs: DEVICE
+ * [count, columns]. A token >= rows yields a row of NaN (the reference throws
+ * std::invalid_argument; the token is device data here). */
+int adi_hip_embedding_rows(adi_hip_context *ctx, const adi_hip_embedding *e,
+                           const uint32_t *tokens, uint32_t count, float *outputs);
+
+/* sample_token at temperature 0 (src/generation.cpp:180-183) for `rows` rows
+ * of `count` logits: the first index of the largest logit (std::max_element).
+ * A row holding a non-finite logit yields 0xFFFFFFFF (the reference rejects
+ * such logits with std::invalid_argument). logits: DEVICE [rows, count];
+ * tokens: DEVICE [rows]. */
+int adi_hip_argmax_rows(adi_hip_context *ctx, const float *logits, uint32_t rows,
+                        uint32_t count, uint32_t *tokens);
 
 /* ---- kernel profiling ----------------------------------------------------- */
 

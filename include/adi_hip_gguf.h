@@ -1,7 +1,7 @@
 /*
  * adi_hip_gguf.h -- the checkpoint side of the packed path: a GGUF v3 reader
- * and the upload of one layer's packed MoE tensors into the device
- * descriptors of adi_hip.h.
+ * and the upload of a layer's packed MoE tensors and of the embedding table
+ * into the device descriptors of adi_hip.h.
  *
  * The reference maps the checkpoint with adi::GgufFile (include/adi/gguf.hpp,
  * src/gguf.cpp) and reads the packed tensors as non-owning host views in
@@ -21,6 +21,7 @@
  *   hf.model.language_model.layers.{layer}.mlp.gate.weight          bf16 {hidden, experts}
  *   hf.model.language_model.layers.{layer}.mlp.shared_expert_gate.weight  bf16 {hidden, 1}
  *   mach.tlut.expert.tlut  f32 {8, 32768};  mach.tlut.ne.tlut  f32 {2, 512}
+ *   mach.embedding.{q_packed|mn|mx|exc_idx|exc_bits}
  *
  * File-level calls take no context: their failures leave a message for
  * adi_hip_gguf_error() (per calling thread). Upload calls take a context and
@@ -129,21 +130,33 @@ int adi_hip_gguf_upload_codebooks(adi_hip_context *ctx, const adi_hip_gguf *file
                                   adi_hip_codebook **expert_codebook,
                                   adi_hip_codebook **ne_codebook);
 
-/* One layer's packed MoE tensors in one device allocation. */
-typedef struct adi_hip_moe_weights adi_hip_moe_weights;
+/* Device copies of checkpoint tensors, in one allocation. */
+typedef struct adi_hip_weights adi_hip_weights;
 
 /* Validates layer `layer` (as adi_hip_gguf_check_moe_layer), copies its
  * packed tensors into HBM once, still packed, and fills *descriptor with
  * device pointers into that copy: the 32-expert chunks are laid end to end,
  * so expert e's trellis, su, sv and gamma sit where adi_hip_expert_stack
- * expects them. The weights stay valid until adi_hip_moe_weights_destroy;
+ * expects them. The weights stay valid until adi_hip_weights_destroy;
  * the file may be closed after the call. */
 int adi_hip_gguf_upload_moe_layer(adi_hip_context *ctx, const adi_hip_gguf *file, uint32_t layer,
                                   const adi_hip_codebook *expert_codebook,
                                   const adi_hip_codebook *ne_codebook,
-                                  adi_hip_moe_weights **weights,
+                                  adi_hip_weights **weights,
                                   adi_hip_moe_layer *descriptor);
-void adi_hip_moe_weights_destroy(adi_hip_moe_weights *weights);
+void adi_hip_weights_destroy(adi_hip_weights *weights);
+
+/* The embedding table (MachModel::embedding, src/model.cpp:316-363, and its
+ * checks in validate_manifest, src/model.cpp:836-849): mach.embedding.q_packed
+ * i8 {hidden/2, vocabulary}, .mn and .mx f16 {hidden/64, vocabulary},
+ * .exc_idx i32 {n} strictly ascending below vocabulary*hidden, .exc_bits i16
+ * {n} (bf16 bits); finite f16 and bf16 values and min <= max per group. The
+ * hidden width is qwen35moe.embedding_length. Copies the tensors into HBM
+ * once and fills *descriptor with device pointers. */
+int adi_hip_gguf_upload_embedding(adi_hip_context *ctx, const adi_hip_gguf *file,
+                                  adi_hip_weights **weights, adi_hip_embedding *descriptor);
+/* The same checks on the host, without uploading. */
+int adi_hip_gguf_check_embedding(const adi_hip_gguf *file);
 
 #ifdef __cplusplus
 }

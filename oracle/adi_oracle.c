@@ -713,6 +713,57 @@ int ao_rms_norm(const float *input, const uint16_t *weight_bf16, uint32_t count,
     return AO_OK;
 }
 
+/* ---- embedding rows and the greedy choice ---------------------------------- */
+
+/* src/kernels.cpp:802-845: per 64-column group, step = max(max - min, 1e-8)
+ * / 15 and value = min + code * step (separate multiply and add), codes high
+ * nibble first; then the row's bf16 exceptions, found by lower_bound over the
+ * ascending flat indexes, overwrite their columns. */
+int ao_embedding_row(const ao_embedding *e, uint32_t token, float *output) {
+    if (!e || !output || token >= e->rows || e->columns % 64 != 0 || !e->packed ||
+        !e->minimum_f16 || !e->maximum_f16 ||
+        (e->exception_count && (!e->exception_indexes || !e->exception_bf16))) {
+        return AO_INVALID_ARGUMENT;
+    }
+    const uint32_t groups = e->columns / 64;
+    const uint8_t *row = e->packed + (size_t)token * e->columns / 2;
+    const size_t scale_offset = (size_t)token * groups;
+    for (uint32_t c = 0; c < e->columns; ++c) {
+        const uint8_t byte = row[c / 2];
+        const uint32_t code = c % 2 == 0 ? (uint32_t)(byte >> 4) : (uint32_t)(byte & 0x0F);
+        const float minimum = ao_f16_to_f32(e->minimum_f16[scale_offset + c / 64]);
+        const float maximum = ao_f16_to_f32(e->maximum_f16[scale_offset + c / 64]);
+        const float span = maximum - minimum;
+        const float step = (span < 1.0e-8f ? 1.0e-8f : span) / 15.0f;
+        output[c] = minimum + (float)code * step;
+    }
+    const uint64_t first = (uint64_t)token * e->columns;
+    const uint64_t last = first + e->columns;
+    uint32_t lo = 0, hi = e->exception_count;
+    while (lo < hi) { /* lower_bound */
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (e->exception_indexes[mid] < first) {
+            lo = mid + 1;
+        } else {
+            hi = mid;
+        }
+    }
+    for (uint32_t i = lo; i < e->exception_count && e->exception_indexes[i] < last; ++i) {
+        output[e->exception_indexes[i] - first] = ao_bf16_to_f32(e->exception_bf16[i]);
+    }
+    return AO_OK;
+}
+
+uint32_t ao_argmax(const float *logits, uint32_t count) {
+    uint32_t best = 0;
+    for (uint32_t i = 1; i < count; ++i) {
+        if (logits[best] < logits[i]) {
+            best = i;
+        }
+    }
+    return best;
+}
+
 float ao_silu(float value) {
     return value / (1.0f + expf(-value));
 }

@@ -71,6 +71,18 @@ typedef struct {
     const uint16_t *values;
 } ao_bf16_matrix;
 
+/* Mirrors adi::MachEmbedding (include/adi/kernels.hpp:54-62). */
+typedef struct {
+    uint32_t rows;
+    uint32_t columns;
+    const uint8_t *packed;             /* rows*columns/2, high nibble first */
+    const uint16_t *minimum_f16;       /* rows*columns/64 */
+    const uint16_t *maximum_f16;       /* rows*columns/64 */
+    const uint32_t *exception_indexes; /* ascending flat indexes */
+    const uint16_t *exception_bf16;
+    uint32_t exception_count;
+} ao_embedding;
+
 /* One MoE block: the fields moe_forward reads from the model's layer
  * descriptor (src/executor.cpp:254, 270-288, 300-324). */
 typedef struct {
@@ -164,6 +176,13 @@ int ao_moe_forward(const ao_moe_layer *layer, const float *inputs,
                    uint32_t batch, const float *logit_bias, uint32_t lanes,
                    float *outputs, uint32_t *route_expert, float *route_weight,
                    int threads);
+
+/* Embedding row decode (mach_embedding_row, src/kernels.cpp:802-845). */
+int ao_embedding_row(const ao_embedding *embedding, uint32_t token, float *output);
+
+/* Greedy choice of sample_token at temperature 0: the first index of the
+ * largest logit (std::max_element, src/generation.cpp:180-183). */
+uint32_t ao_argmax(const float *logits, uint32_t count);
 
 #ifdef __cplusplus
 }

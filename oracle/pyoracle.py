@@ -53,6 +53,14 @@ class Bf16Matrix(C.Structure):
     _fields_ = [("rows", C.c_uint32), ("columns", C.c_uint32), ("values", u16p)]
 
 
+class Embedding(C.Structure):
+    _fields_ = [
+        ("rows", C.c_uint32), ("columns", C.c_uint32), ("packed", u8p),
+        ("minimum_f16", u16p), ("maximum_f16", u16p), ("exception_indexes", u32p),
+        ("exception_bf16", u16p), ("exception_count", C.c_uint32),
+    ]
+
+
 class MoeLayer(C.Structure):
     _fields_ = [
         ("hidden", C.c_uint32), ("expert_hidden", C.c_uint32), ("experts", C.c_uint32),
@@ -111,6 +119,8 @@ def load_oracle() -> C.CDLL:
              u32p, u32p, u32p, u32p)
     _declare(lib, "ao_moe_forward", C.c_int, C.POINTER(MoeLayer), f32p, C.c_uint32, f32p,
              C.c_uint32, f32p, u32p, f32p, C.c_int)
+    _declare(lib, "ao_embedding_row", C.c_int, C.POINTER(Embedding), C.c_uint32, f32p)
+    _declare(lib, "ao_argmax", C.c_uint32, f32p, C.c_uint32)
     return lib
 
 
@@ -148,6 +158,11 @@ def load_ref() -> C.CDLL:
     _declare(lib, "ref_moe_layer_create", C.c_void_p, C.POINTER(MoeLayer))
     _declare(lib, "ref_moe_layer_destroy", None, C.c_void_p)
     _declare(lib, "ref_moe_forward", C.c_int, C.c_void_p, f32p, C.c_uint32, f32p, f32p, u32p, f32p)
+    _declare(lib, "ref_embedding_row", C.c_int, C.POINTER(Embedding), C.c_uint32, f32p)
+    _declare(lib, "ref_sample_token", C.c_int, f32p, C.c_uint32, C.c_float, C.c_float, C.c_uint64,
+             C.POINTER(C.c_uint64), u32p)
+    _declare(lib, "ref_gguf_summary", C.c_int, C.c_char_p, C.POINTER(C.c_uint64),
+             C.POINTER(C.c_uint64), C.POINTER(C.c_uint64))
     return lib
 
 
@@ -251,6 +266,43 @@ def bf16_matmul(lib, values: np.ndarray, inputs: np.ndarray, isa: int = 16,
                                      ptr(out, C.c_float))
     check(status, "bf16_matmul")
     return out
+
+
+def embedding_struct(e) -> Embedding:
+    """e: adi_amd.synthetic.Embedding (arrays kept alive by the caller)."""
+    return Embedding(e.rows, e.columns, ptr(e.packed, C.c_uint8), ptr(e.minimum_f16, C.c_uint16),
+                     ptr(e.maximum_f16, C.c_uint16), ptr(e.exception_indexes, C.c_uint32),
+                     ptr(e.exception_bf16, C.c_uint16), int(e.exception_indexes.size))
+
+
+def embedding_rows(lib, e, tokens, prefix="ao") -> np.ndarray:
+    out = np.zeros((len(tokens), e.columns), np.float32)
+    s = embedding_struct(e)
+    fn = getattr(lib, f"{prefix}_embedding_row")
+    for i, t in enumerate(tokens):
+        row = np.zeros(e.columns, np.float32)
+        check(fn(C.byref(s), int(t), ptr(row, C.c_float)), "embedding_row")
+        out[i] = row
+    return out
+
+
+def ref_sample_token(lib, logits: np.ndarray, temperature: float, top_p: float, seed: int):
+    """(token, the engine's first 64-bit word) of the compiled sample_token."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    word = C.c_uint64()
+    token = np.zeros(1, np.uint32)
+    check(lib.ref_sample_token(ptr(logits, C.c_float), logits.size, temperature, top_p, seed,
+                               C.byref(word), ptr(token, C.c_uint32)), "sample_token")
+    return int(token[0]), word.value
+
+
+def ref_gguf_summary(lib, path: str):
+    """(tensors, metadata, alignment) as the reference's GgufFile reads the
+    file, or None when it rejects it."""
+    t, m, a = C.c_uint64(), C.c_uint64(), C.c_uint64()
+    if lib.ref_gguf_summary(os.fsencode(path), C.byref(t), C.byref(m), C.byref(a)) != 0:
+        return None
+    return t.value, m.value, a.value
 
 
 def top_experts(lib, logits: np.ndarray, prefix="ao"):

@@ -15,6 +15,8 @@
 // the way MachModel::cache_descriptors does (src/model.cpp:542-691).
 #include "adi/backend.hpp"
 #include "adi/executor.hpp"
+#include "adi/generation.hpp"
+#include "adi/gguf.hpp"
 #include "adi/kernels.hpp"
 #include "codec_cache.hpp"
 #include "expert_trellis.hpp"
@@ -269,6 +271,47 @@ int ref_rms_norm(const float *input, const std::uint16_t *weight_bf16,
     return guarded([&] {
         adi::rms_norm({input, count}, {weight_bf16, count}, weight_offset,
                       epsilon, {output, count});
+    });
+}
+
+int ref_embedding_row(const ao_embedding *e, std::uint32_t token, float *output) {
+    return guarded([&] {
+        const std::size_t groups = e->columns / 64;
+        const adi::MachEmbedding view{
+            e->rows,
+            e->columns,
+            {e->packed, static_cast<std::size_t>(e->rows) * e->columns / 2},
+            u16(e->minimum_f16, e->rows * groups),
+            u16(e->maximum_f16, e->rows * groups),
+            {e->exception_indexes, e->exception_count},
+            u16(e->exception_bf16, e->exception_count),
+        };
+        adi::mach_embedding_row(view, token, {output, e->columns});
+    });
+}
+
+/* sample_token (src/generation.cpp:161-225) with a std::mt19937_64 seeded
+ * with `seed`; *first_word receives the engine's first output, the one word a
+ * draw at temperature > 0 consumes. */
+int ref_sample_token(const float *logits, std::uint32_t count, float temperature, float top_p,
+                     std::uint64_t seed, std::uint64_t *first_word, std::uint32_t *token) {
+    return guarded([&] {
+        std::mt19937_64 random(seed);
+        std::mt19937_64 copy = random;
+        *first_word = copy();
+        *token = adi::sample_token({logits, count}, temperature, top_p, random);
+    });
+}
+
+/* GgufFile (src/gguf.cpp:232-330) on `path`: AO_OK with the counts, or
+ * AO_INVALID_ARGUMENT when the reader rejects the file. */
+int ref_gguf_summary(const char *path, std::uint64_t *tensors, std::uint64_t *metadata,
+                     std::uint64_t *alignment) {
+    return guarded([&] {
+        const adi::GgufFile file(path);
+        *tensors = file.tensors().size();
+        *metadata = file.metadata().size();
+        *alignment = file.alignment();
     });
 }
 

@@ -151,6 +151,19 @@ def moe_tensors(layers) -> List[Tuple[str, int, List[int], bytes]]:
     return out
 
 
+def embedding_tensors(e) -> List[Tuple[str, int, List[int], bytes]]:
+    """mach.embedding.* of a synthetic table (adi_amd.synthetic.Embedding),
+    as MachModel::embedding reads them (src/model.cpp:316-363)."""
+    n = int(e.exception_indexes.size)
+    return [
+        ("mach.embedding.q_packed", T_I8, [e.columns // 2, e.rows], np.asarray(e.packed, np.uint8).tobytes()),
+        ("mach.embedding.mn", T_F16, [e.columns // 64, e.rows], np.asarray(e.minimum_f16, np.uint16).tobytes()),
+        ("mach.embedding.mx", T_F16, [e.columns // 64, e.rows], np.asarray(e.maximum_f16, np.uint16).tobytes()),
+        ("mach.embedding.exc_idx", T_I32, [n], np.asarray(e.exception_indexes, np.uint32).tobytes()),
+        ("mach.embedding.exc_bits", T_I16, [n], np.asarray(e.exception_bf16, np.uint16).tobytes()),
+    ]
+
+
 def write_moe_checkpoint(path, layers, metadata=None, tensors=None) -> None:
     first = layers[0]
     md = metadata if metadata is not None else moe_metadata(len(layers), first.hidden,

@@ -23,6 +23,7 @@ STRUCTS = {
     "adi_hip_expert_stack": hip.ExpertStack,
     "adi_hip_moe_layer": hip.MoeLayer,
     "adi_hip_kernel_profile": hip.KernelProfile,
+    "adi_hip_embedding": hip.Embedding,
     "adi_hip_gguf_tensor": hip.GgufTensor,
     "adi_hip_moe_geometry": hip.MoeGeometry,
 }

@@ -1,0 +1,75 @@
+"""The oracle's token-side functions pinned without a GPU: embedding rows
+(mach_embedding_row, src/kernels.cpp:802-845) by a closed form and by the
+compiled reference, and the greedy choice of sample_token
+(src/generation.cpp:180-183) by the compiled reference with ties and signed
+zeros."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import pyoracle as po
+from adi_amd import synthetic as syn
+
+
+@pytest.fixture(scope="module")
+def oracle():
+    return po.load_oracle()
+
+
+@pytest.fixture(scope="module")
+def ref():
+    if not po.ref_available():
+        pytest.skip("oracle/_ref is not built here")
+    return po.load_ref()
+
+
+def test_embedding_closed_form(oracle):
+    # group 0: min 0, max 15 -> step 1, value = code; group 1: min == max = 1
+    # -> step 1e-8/15, value rounds back to 1.0; then exceptions overwrite
+    rows, columns = 3, 128
+    codes = np.arange(rows * columns, dtype=np.uint32) % 16
+    packed = ((codes[0::2] << 4) | codes[1::2]).astype(np.uint8)
+    f16 = lambda v: syn.f16_bits(np.array([v], np.float32))[0]
+    mn = np.array([f16(0.0), f16(1.0)] * rows, np.uint16)
+    mx = np.array([f16(15.0), f16(1.0)] * rows, np.uint16)
+    ex = np.array([columns + 5, 2 * columns + 127], np.uint32)
+    bits = syn.bf16_bits_rne(np.array([-2.5, 7.0], np.float32)).astype(np.uint16)
+    e = syn.Embedding(rows, columns, packed, mn, mx, ex, bits)
+    got = po.embedding_rows(oracle, e, [0, 1, 2])
+    want = np.where(np.arange(columns) < 64, codes[:columns] % 16, 1.0).astype(np.float32)
+    want = np.tile(want, (3, 1))
+    want[1, 5] = -2.5
+    want[2, 127] = 7.0
+    assert np.array_equal(got, want)
+    s = po.embedding_struct(e)
+    row = np.zeros(columns, np.float32)
+    assert oracle.ao_embedding_row(C.byref(s), 3, po.ptr(row, C.c_float)) == -1  # token >= rows
+
+
+@pytest.mark.parametrize("rows,columns,exceptions", [(50, 64, 0), (300, 256, 200), (17, 2048, 600)])
+def test_embedding_matches_reference(oracle, ref, rows, columns, exceptions):
+    e = syn.embedding(syn.rng_for(21, rows), rows, columns, exceptions=exceptions)
+    tokens = sorted({0, 1, rows // 2, rows - 1})
+    a = po.embedding_rows(oracle, e, tokens)
+    b = po.embedding_rows(ref, e, tokens, prefix="ref")
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def argmax(oracle, logits):
+    logits = np.ascontiguousarray(logits, np.float32)
+    return oracle.ao_argmax(po.ptr(logits, C.c_float), logits.size)
+
+
+def test_argmax_matches_reference_greedy(oracle, ref):
+    rng = np.random.default_rng(5)
+    cases = [rng.normal(0, 3, 1000).astype(np.float32) for _ in range(5)]
+    tie = rng.normal(0, 1, 500).astype(np.float32)
+    tie[[17, 300, 499]] = 9.0  # equal maxima: the first wins
+    zeros = np.full(64, -1.0, np.float32)
+    zeros[[10, 20]] = [-0.0, 0.0]  # -0 == +0: the first wins
+    cases += [tie, zeros, np.array([1.0], np.float32)]
+    for logits in cases:
+        want, _ = po.ref_sample_token(ref, logits, 0.0, 1.0, 0)
+        assert argmax(oracle, logits) == want
+    assert argmax(oracle, tie) == 17 and argmax(oracle, zeros) == 10

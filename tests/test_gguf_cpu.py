@@ -256,3 +256,81 @@ def test_malformed_layers_are_rejected(tmp_path, layers, change, match):
             f.check_moe_layer(0)
         assert info.value.status == hip.INVALID_ARGUMENT
         assert match in str(info.value), str(info.value)
+
+
+# ---- the embedding table --------------------------------------------------------
+
+def embedding_checkpoint(tmp_path, layers, e, change=None):
+    ts = gf.moe_tensors(layers) + gf.embedding_tensors(e)
+    if change:
+        name, data = change
+        ts = [(t[0], t[1], t[2], data) if t[0] == name else t for t in ts]
+    md = gf.moe_metadata(len(layers), layers[0].hidden, layers[0].expert_hidden, layers[0].experts)
+    path = str(tmp_path / "emb.gguf")
+    gf.write_moe_checkpoint(path, layers, md, ts)
+    return path
+
+
+def test_embedding_tensors_round_trip(tmp_path, layers):
+    e = syn.embedding(syn.rng_for(9, 7), 300, 256, exceptions=50)
+    with hip.Gguf(embedding_checkpoint(tmp_path, layers, e)) as f:
+        info, packed = f.tensor("mach.embedding.q_packed")
+        assert list(info.dimensions[:2]) == [128, 300]
+        assert np.array_equal(packed.view(np.uint8), e.packed)
+        info, idx = f.tensor("mach.embedding.exc_idx")
+        assert np.array_equal(idx.view(np.uint32), e.exception_indexes)
+
+
+def test_reference_reader_agrees(tmp_path, layers):
+    """The compiled GgufFile accepts and rejects the same files as this
+    reader (where the reference is built here)."""
+    import pyoracle as po
+    if not po.ref_available():
+        pytest.skip("oracle/_ref is not built here")
+    ref = po.load_ref()
+    good = embedding_checkpoint(tmp_path, layers, syn.embedding(syn.rng_for(9, 8), 64, 256, 8))
+    with hip.Gguf(good) as f:
+        assert po.ref_gguf_summary(ref, good) == (f.tensor_count, f.metadata_count, f.alignment)
+    data = gf.reference_fixture()
+    for i, bad in enumerate([data[:-1], data[:20], data[:40], b"GGUX" + data[4:],
+                             data[:4] + struct.pack("<I", 2) + data[8:]]):
+        path = write(tmp_path / f"bad{i}.gguf", bad)
+        assert po.ref_gguf_summary(ref, path) is None
+        with pytest.raises(hip.HipError):
+            hip.Gguf(path)
+
+
+def bad_exception_order(e):
+    v = e.exception_indexes.copy()
+    v[3], v[4] = v[4], v[3]
+    return v.astype(np.uint32).tobytes()
+
+
+def bad_minimum(e):
+    v = e.minimum_f16.copy()
+    v[10] = syn.f16_bits(np.array([1.0], np.float32))[0]  # above its maximum
+    return v.astype(np.uint16).tobytes()
+
+
+def bad_exception_value(e):
+    v = e.exception_bf16.copy()
+    v[2] = 0x7F80  # +inf
+    return v.astype(np.uint16).tobytes()
+
+
+@pytest.mark.parametrize("name, make, match", [
+    ("mach.embedding.exc_idx", bad_exception_order, "malformed embedding tensors"),
+    ("mach.embedding.mn", bad_minimum, "minimum exceeds maximum"),
+    ("mach.embedding.exc_bits", bad_exception_value, "nonfinite tensor 'mach.embedding.exc_bits'"),
+])
+def test_malformed_embedding_is_rejected(tmp_path, layers, name, make, match):
+    # src/model.cpp:342-363, 836-849
+    e = syn.embedding(syn.rng_for(9, 9), 64, 256, exceptions=20)
+    with hip.Gguf(embedding_checkpoint(tmp_path, layers, e)) as f:
+        f.check_embedding()
+    path = embedding_checkpoint(tmp_path, layers, e, (name, make(e)))
+    with hip.Gguf(path) as f:
+        with pytest.raises(hip.HipError) as info:
+            f.check_embedding()
+        assert info.value.status == hip.INVALID_ARGUMENT
+        assert match in str(info.value), str(info.value)
