@@ -185,6 +185,29 @@ class Runtime {
         return found->second;
     }
 
+    const adi_hip_embedding &embedding(const MachEmbedding &e) {
+        const Key key{e.packed.data(), e.rows, e.columns,
+                      fingerprint(e.packed) ^ fingerprint(e.minimum_f16) * 3 ^
+                          fingerprint(e.maximum_f16) * 5 ^ fingerprint(e.exception_indexes) * 7 ^
+                          fingerprint(e.exception_bf16) * 11};
+        auto found = embeddings_.find(key);
+        if (found == embeddings_.end()) {
+            adi_hip_embedding d{};
+            d.rows = e.rows;
+            d.columns = e.columns;
+            d.packed = upload(e.packed);
+            d.minimum_f16 = upload(e.minimum_f16);
+            d.maximum_f16 = upload(e.maximum_f16);
+            d.exception_count = static_cast<std::uint32_t>(e.exception_indexes.size());
+            if (d.exception_count != 0) {
+                d.exception_indexes = upload(e.exception_indexes);
+                d.exception_bf16 = upload(e.exception_bf16);
+            }
+            found = embeddings_.emplace(key, d).first;
+        }
+        return found->second;
+    }
+
     const std::uint16_t *weights(std::span<const std::uint16_t> w) {
         auto &slot = weights_[{w.data(), fingerprint(w)}];
         if (slot == nullptr) {
@@ -224,6 +247,7 @@ class Runtime {
     std::map<Key, adi_hip_ne_matrix> nes_;
     std::map<Key, adi_hip_head_chunk> heads_;
     std::map<Key, adi_hip_bf16_matrix> bf16s_;
+    std::map<Key, adi_hip_embedding> embeddings_;
     std::map<TableKey, const std::uint16_t *> weights_;
 };
 
@@ -396,6 +420,31 @@ void hip_rms_norm(std::span<const float> input, std::span<const std::uint16_t> w
     rt.to_host(output, out);
 }
 
+// mach_embedding_row's checks and messages (src/kernels.cpp:806-818); the
+// token goes to the device, the row comes back.
+void hip_embedding_row(const MachEmbedding &e, std::uint32_t token, std::span<float> output) {
+    constexpr std::uint32_t group = 64;
+    if (token >= e.rows || output.size() != e.columns || e.columns % group != 0 ||
+        e.packed.size() != static_cast<std::size_t>(e.rows) * e.columns / 2) {
+        throw std::invalid_argument("Mach embedding shape mismatch");
+    }
+    const std::size_t groups = e.columns / group;
+    if (e.minimum_f16.size() != static_cast<std::size_t>(e.rows) * groups ||
+        e.maximum_f16.size() != static_cast<std::size_t>(e.rows) * groups ||
+        e.exception_indexes.size() != e.exception_bf16.size()) {
+        throw std::invalid_argument("Mach embedding scale or exception shape mismatch");
+    }
+    Runtime &rt = Runtime::get();
+    std::lock_guard<std::mutex> lock(rt.mutex);
+    const adi_hip_embedding &d = rt.embedding(e);
+    float *staged = rt.staging(0, 1);
+    float *out = rt.staging(1, output.size());
+    rt.check(adi_hip_copy_to_device(rt.ctx, staged, &token, sizeof(token)));
+    rt.check(adi_hip_embedding_rows(rt.ctx, &d, reinterpret_cast<const std::uint32_t *>(staged), 1,
+                                    out));
+    rt.to_host(output, out);
+}
+
 }  // namespace
 
 const Backend &hip_backend() {
@@ -407,9 +456,7 @@ const Backend &hip_backend() {
             hip_expert_matmul,
             hip_ne_matvec,
             hip_ne_matmul,
-            // embedding rows are not on the packed-weight path this library
-            // accelerates: the CPU entry serves them (src/kernels.cpp:802-845)
-            mach_embedding_row,
+            hip_embedding_row,
             hip_head_matvec,
             hip_head_matmul,
             hip_bf16_matvec,

@@ -110,6 +110,24 @@ int bd_bf16_matmul(int hip, std::uint32_t rows, std::uint32_t columns, const std
     });
 }
 
+int bd_embedding_row(int hip, std::uint32_t rows, std::uint32_t columns, const std::uint8_t *packed,
+                     const std::uint16_t *minimum, const std::uint16_t *maximum,
+                     const std::uint32_t *indexes, const std::uint16_t *bits,
+                     std::size_t exceptions, std::uint32_t token, float *output,
+                     std::size_t output_size, char *error, std::size_t error_size) {
+    return run(error, error_size, [&] {
+        const std::size_t groups = columns / 64;
+        const adi::MachEmbedding e{rows,
+                                   columns,
+                                   {packed, std::size_t(rows) * columns / 2},
+                                   {minimum, std::size_t(rows) * groups},
+                                   {maximum, std::size_t(rows) * groups},
+                                   {indexes, exceptions},
+                                   {bits, exceptions}};
+        table(hip).embedding_row(e, token, {output, output_size});
+    });
+}
+
 int bd_rms_norm(int hip, const float *input, const std::uint16_t *weight, std::size_t count,
                 float offset, float epsilon, float *output, char *error, std::size_t error_size) {
     return run(error, error_size, [&] {

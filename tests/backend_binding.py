@@ -96,6 +96,15 @@ def bf16_matmul(which, values, rows, columns, x, batch):
     return out.reshape(batch, rows)
 
 
+def embedding_row(which, e, token, out_size=None):
+    out = np.zeros(e.columns if out_size is None else out_size, np.float32)
+    _call(load().bd_embedding_row, C.c_int(which), C.c_uint32(e.rows), C.c_uint32(e.columns),
+          _p(e.packed), _p(e.minimum_f16), _p(e.maximum_f16), _p(e.exception_indexes),
+          _p(e.exception_bf16), C.c_size_t(e.exception_indexes.size), C.c_uint32(token), _p(out),
+          C.c_size_t(out.size))
+    return out
+
+
 def rms_norm(which, x, weight, offset, epsilon):
     x = np.ascontiguousarray(x, np.float32)
     weight = np.ascontiguousarray(weight, np.uint16)

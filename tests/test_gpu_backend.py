@@ -81,6 +81,22 @@ def test_backend_rms_norm():
     assert max_rel_error(got, want) <= 1e-6
 
 
+def test_backend_embedding_row_bit_exact():
+    e = syn.embedding(syn.rng_for(1, 321), 400, 2048, exceptions=500)
+    for token in (0, 17, 399):
+        want = bb.embedding_row(bb.CPU, e, token)
+        got = bb.embedding_row(bb.HIP, e, token)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    errors = []
+    for which in (bb.CPU, bb.HIP):
+        for token, size in ((400, 2048), (3, 2047)):
+            with pytest.raises(bb.BackendError) as info:
+                bb.embedding_row(which, e, token, out_size=size)
+            errors.append((which, info.value.status, info.value.message))
+    assert [x[1:] for x in errors[:2]] == [x[1:] for x in errors[2:]]
+    assert errors[0][1:] == (1, "Mach embedding shape mismatch")
+
+
 def test_backend_repeated_calls_reuse_device_weights():
     rng = syn.rng_for(1, 1234)
     m = syn.expert_matrix(rng, 512, 2048, syn.expert_tlut(rng))
