@@ -123,6 +123,315 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_argmax_rows(const float *log
     }
 }
 
+// ---- top-p sampling ----------------------------------------------------------
+
+constexpr uint32_t kSampleThreads = 1024;
+constexpr uint32_t kSampleWaves = kSampleThreads / kWave;
+constexpr uint32_t kWindow = 4096;  // candidates sorted and walked at a time
+
+// Ascending order of this key is descending logit order, with -0 folded into
+// +0 (src/generation.cpp:36-47); ties keep ascending token order.
+__device__ __forceinline__ uint32_t descending_key(float v) {
+    const uint32_t bits = v == 0.0f ? 0u : __float_as_uint(v);
+    const uint32_t ascending = (bits & 0x80000000u) != 0u ? ~bits : bits ^ 0x80000000u;
+    return ~ascending;
+}
+
+// The block's state between the phases of a row (in LDS).
+struct SampleState {
+    uint64_t floor;     // (key << 32 | index) of the last walked candidate
+    uint32_t has_floor;
+    uint32_t count;     // candidates in the window
+    uint32_t select;    // radix select: chosen prefix
+    uint32_t want;      // rank still wanted within the prefix
+    uint32_t all;       // fewer than kWindow eligible: take them all
+    uint32_t ties;      // eligible candidates with the selected key
+    uint32_t done;
+    uint32_t token;
+    double walk[2];     // running sums carried across windows
+};
+
+__device__ __forceinline__ bool eligible(const SampleState &s, uint32_t key, uint32_t index) {
+    const uint64_t packed = (static_cast<uint64_t>(key) << 32) | index;
+    return s.has_floor == 0u || packed > s.floor;
+}
+
+// Radix select over 32-bit values v(i) of the eligible tokens passing
+// `filter`: the value of the s.want-th smallest (MSB first, 8 bits a pass),
+// with s.want left as the rank within it; s.all when fewer are eligible.
+template <typename Value, typename Filter>
+__device__ void radix_select(const float *row, uint32_t count, SampleState &s, uint32_t *hist,
+                             Value value, Filter filter) {
+    uint32_t prefix = 0, mask = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (uint32_t b = threadIdx.x; b < 256u; b += blockDim.x) {
+            hist[b] = 0u;
+        }
+        __syncthreads();
+        for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
+            const uint32_t key = descending_key(row[i]);
+            const uint32_t v = value(key, i);
+            if (eligible(s, key, i) && filter(key, i) && (v & mask) == prefix) {
+                atomicAdd(&hist[(v >> shift) & 0xFFu], 1u);
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint32_t b = 0, w = s.want;
+            while (b < 256u && w > hist[b]) {
+                w -= hist[b];
+                ++b;
+            }
+            if (b == 256u) {
+                s.all = 1u;
+            } else {
+                s.select = prefix | (b << shift);
+                s.want = w;
+                s.ties = hist[b];
+            }
+        }
+        __syncthreads();
+        if (s.all != 0u) {
+            return;
+        }
+        prefix = s.select;
+        mask |= 0xFFu << shift;
+    }
+}
+
+// The next kWindow tokens after s.floor in (key, index) order, sorted into
+// cand, with their p in prob.
+__device__ void gather_window(const float *row, uint32_t count, double maximum, double temperature,
+                              SampleState &s, uint64_t *cand, double *prob, uint32_t *hist) {
+    if (threadIdx.x == 0) {
+        s.want = kWindow;
+        s.all = 0u;
+        s.count = 0u;
+    }
+    __syncthreads();
+    radix_select(row, count, s, hist, [](uint32_t key, uint32_t) { return key; },
+                 [](uint32_t, uint32_t) { return true; });
+    const uint32_t take_all = s.all;
+    const uint32_t key_th = s.select;
+    uint32_t index_th = 0xFFFFFFFFu;
+    if (take_all == 0u && s.ties != s.want) {
+        // only the first `want` of the tokens tied at key_th, by index
+        radix_select(row, count, s, hist, [](uint32_t, uint32_t i) { return i; },
+                     [key_th](uint32_t key, uint32_t) { return key == key_th; });
+        index_th = s.select;
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
+        const uint32_t key = descending_key(row[i]);
+        if (eligible(s, key, i) &&
+            (take_all != 0u || key < key_th || (key == key_th && i <= index_th))) {
+            const uint32_t at = atomicAdd(&s.count, 1u);
+            if (at < kWindow) {  // the select admits exactly min(kWindow, eligible)
+                cand[at] = (static_cast<uint64_t>(key) << 32) | i;
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t n = s.count < kWindow ? s.count : kWindow;
+    for (uint32_t k = n + threadIdx.x; k < kWindow; k += blockDim.x) {
+        cand[k] = ~0ull;
+    }
+    // bitonic sort, ascending
+    for (uint32_t size = 2; size <= kWindow; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            for (uint32_t i = threadIdx.x; i < kWindow; i += blockDim.x) {
+                const uint32_t j = i ^ stride;
+                if (j > i) {
+                    const uint64_t a = cand[i], b = cand[j];
+                    const bool up = (i & size) == 0u;
+                    if ((a > b) == up) {
+                        cand[i] = b;
+                        cand[j] = a;
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        s.count = n;
+    }
+    for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
+        const float logit = row[static_cast<uint32_t>(cand[k])];
+        prob[k] = exp((static_cast<double>(logit) - maximum) / temperature);
+    }
+    __syncthreads();
+}
+
+// One block per row (src/generation.cpp:161-225): the maximum, the sum of p
+// over all tokens (a fixed tree order), then windows of the sorted order
+// walked on one thread exactly as the reference walks its sorted vector:
+// first the cumulative p / sum up to top_p (summing the kept p on the way),
+// then the running p up to the target.
+__global__ __launch_bounds__(kSampleThreads) void k_sample_rows(const float *logits, uint32_t count,
+                                                                float temperature, float top_p,
+                                                                const uint64_t *words,
+                                                                uint32_t *tokens) {
+    __shared__ uint64_t cand[kWindow];
+    __shared__ double prob[kWindow];
+    __shared__ uint32_t hist[256];
+    __shared__ double wave_sum[kSampleWaves];
+    __shared__ float wave_max[kSampleWaves];
+    __shared__ uint32_t wave_bad[kSampleWaves];
+    __shared__ SampleState s;
+    const float *row = logits + static_cast<size_t>(blockIdx.x) * count;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    // the maximum; any non-finite logit rejects the row
+    float m = -__builtin_huge_valf();
+    uint32_t bad = 0;
+    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
+        const float v = row[i];
+        bad |= __builtin_isfinite(v) ? 0u : 1u;
+        m = v > m ? v : m;
+    }
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        const float o = __shfl_xor(m, offset);
+        m = o > m ? o : m;
+        bad |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(bad), offset));
+    }
+    if (lane == 0) {
+        wave_max[wave] = m;
+        wave_bad[wave] = bad;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t w = 1; w < kSampleWaves; ++w) {
+            m = wave_max[w] > m ? wave_max[w] : m;
+            bad |= wave_bad[w];
+        }
+        wave_max[0] = m;
+        s.done = bad;
+        s.has_floor = 0u;
+        s.walk[0] = 0.0;
+        s.walk[1] = 0.0;
+    }
+    __syncthreads();
+    if (s.done != 0u) {
+        if (threadIdx.x == 0) {
+            tokens[blockIdx.x] = 0xFFFFFFFFu;
+        }
+        return;
+    }
+    const double maximum = static_cast<double>(wave_max[0]);
+    const double t = static_cast<double>(temperature);
+    // sum of p over the row: each thread in index order, then a fixed tree
+    double part = 0.0;
+    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
+        part += exp((static_cast<double>(row[i]) - maximum) / t);
+    }
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        part += __shfl_xor(part, offset);
+    }
+    if (lane == 0) {
+        wave_sum[wave] = part;
+    }
+    __syncthreads();
+    double denominator = 0.0;
+    for (uint32_t w = 0; w < kSampleWaves; ++w) {
+        denominator += wave_sum[w];
+    }
+    // phase 1: the kept prefix and the sum of its p
+    uint64_t last = 0;
+    uint32_t window = 0;
+    while (true) {
+        gather_window(row, count, maximum, t, s, cand, prob, hist);
+        if (threadIdx.x == 0) {
+            double cumulative = s.walk[0], kept = s.walk[1];
+            const uint32_t n = s.count;
+            uint32_t k = 0;
+            for (; k < n; ++k) {
+                cumulative += prob[k] / denominator;
+                kept += prob[k];
+                if (cumulative >= static_cast<double>(top_p)) {
+                    break;
+                }
+            }
+            s.walk[0] = cumulative;
+            s.walk[1] = kept;
+            if (k < n || n < kWindow) {
+                // crossed, or every token is walked: the kept set ends here
+                // (an empty window leaves the previous window's last token)
+                s.done = 1u;
+                if (n > 0) {
+                    s.floor = cand[k < n ? k : n - 1];
+                }
+            } else {
+                s.floor = cand[n - 1];
+                s.has_floor = 1u;
+            }
+        }
+        __syncthreads();
+        if (s.done != 0u) {
+            break;
+        }
+        ++window;
+    }
+    last = s.floor;  // the last kept token
+    // the draw (std::uniform_real_distribution<double>(0, kept) over
+    // generate_canonical<double, 53> of a 64-bit engine)
+    double u = static_cast<double>(words[blockIdx.x]) * 0x1p-64;
+    if (u >= 1.0) {
+        u = 0x1.fffffffffffffp-1;
+    }
+    const double target = u * s.walk[1];
+    // phase 2: the running p from the first token until it reaches target
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        s.done = 0u;
+        s.walk[0] = 0.0;
+        s.token = static_cast<uint32_t>(last);
+    }
+    __syncthreads();
+    uint32_t current = window;  // the window in LDS
+    if (current != 0u) {
+        if (threadIdx.x == 0) {
+            s.has_floor = 0u;
+        }
+        __syncthreads();
+    }
+    while (true) {
+        if (current != 0u) {
+            gather_window(row, count, maximum, t, s, cand, prob, hist);
+        }
+        current = 1u;  // later windows are gathered after the floor
+        if (threadIdx.x == 0) {
+            double running = s.walk[0];
+            const uint32_t n = s.count;
+            for (uint32_t k = 0; k < n && s.done == 0u; ++k) {
+                running += prob[k];
+                if (target <= running) {
+                    s.done = 1u;
+                    s.token = static_cast<uint32_t>(cand[k]);
+                } else if (cand[k] == last) {
+                    s.done = 1u;  // past the kept set: the last kept token
+                }
+            }
+            s.walk[0] = running;
+            if (s.done == 0u && n == 0u) {
+                s.done = 1u;  // not reached: the last kept token stands
+            } else if (s.done == 0u) {
+                s.floor = cand[n - 1];
+                s.has_floor = 1u;
+            }
+        }
+        __syncthreads();
+        if (s.done != 0u) {
+            break;
+        }
+    }
+    if (threadIdx.x == 0) {
+        tokens[blockIdx.x] = s.token;
+    }
+}
+
 }  // namespace
 }  // namespace adi_hip
 
@@ -163,6 +472,31 @@ int adi_hip_argmax_rows(adi_hip_context *ctx, const float *logits, uint32_t rows
         }
         launch(ctx, "argmax", k_argmax_rows, dim3(rows), dim3(kArgmaxThreads), 0, logits, count,
                tokens);
+    });
+}
+
+int adi_hip_sample_rows(adi_hip_context *ctx, const float *logits, uint32_t rows,
+                        uint32_t count, float temperature, float top_p,
+                        const uint64_t *words, uint32_t *tokens) {
+    return guarded(ctx, [&] {
+        // the reference's parameter checks (src/generation.cpp:167-176)
+        require(count > 0 && std::isfinite(temperature) && std::isfinite(top_p) &&
+                    temperature >= 0.0f && !(temperature > 0.0f && temperature < 1.0e-4f) &&
+                    temperature <= 2.0f && top_p > 0.0f && top_p <= 1.0f,
+                "invalid sampling parameters");
+        require(rows == 0 || (logits != nullptr && tokens != nullptr), "sampling vector is null");
+        require(temperature == 0.0f || rows == 0 || words != nullptr,
+                "sampling needs one random word per row");
+        if (rows == 0) {
+            return;
+        }
+        if (temperature == 0.0f) {
+            launch(ctx, "argmax", k_argmax_rows, dim3(rows), dim3(kArgmaxThreads), 0, logits,
+                   count, tokens);
+            return;
+        }
+        launch(ctx, "sample", k_sample_rows, dim3(rows), dim3(kSampleThreads), 0, logits, count,
+               temperature, top_p, words, tokens);
     });
 }
 

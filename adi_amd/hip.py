@@ -118,6 +118,7 @@ SIGNATURES = [
     ("adi_hip_moe_forward", C.c_int, [vp, C.POINTER(MoeLayer), vp, u32, vp, vp, vp, vp]),
     ("adi_hip_embedding_rows", C.c_int, [vp, C.POINTER(Embedding), vp, u32, vp]),
     ("adi_hip_argmax_rows", C.c_int, [vp, vp, u32, u32, vp]),
+    ("adi_hip_sample_rows", C.c_int, [vp, vp, u32, u32, f32, f32, vp, vp]),
     ("adi_hip_profiling_enable", C.c_int, [vp, C.c_int]),
     ("adi_hip_profiling_read", C.c_int, [vp, C.POINTER(KernelProfile), u32, C.POINTER(u32)]),
     # include/adi_hip_gguf.h
@@ -565,6 +566,12 @@ def embedding_rows(ctx: Context, emb, tokens, count: int, out) -> None:
 def argmax_rows(ctx: Context, logits, rows: int, count: int, tokens) -> None:
     ctx.check(ctx.lib.adi_hip_argmax_rows(ctx.handle, logits.data_ptr(), rows, count,
                                           tokens.data_ptr()))
+
+
+def sample_rows(ctx: Context, logits, rows: int, count: int, temperature: float, top_p: float,
+                words, tokens) -> None:
+    ctx.check(ctx.lib.adi_hip_sample_rows(ctx.handle, logits.data_ptr(), rows, count, temperature,
+                                          top_p, _addr(words), tokens.data_ptr()))
 
 
 # ---- calls on device tensors ------------------------------------------------

@@ -301,6 +301,26 @@ int adi_hip_embedding_rows(adi_hip_context *ctx, const adi_hip_embedding *e,
 int adi_hip_argmax_rows(adi_hip_context *ctx, const float *logits, uint32_t rows,
                         uint32_t count, uint32_t *tokens);
 
+/* sample_token (src/generation.cpp:161-225) for `rows` rows of `count`
+ * logits. temperature 0 is the greedy choice (as adi_hip_argmax_rows); above
+ * 0 the tokens are ordered by logit (ties by index), p_i = exp((l_i - max) /
+ * temperature) in double, the smallest prefix whose sum of p_i / sum(p)
+ * reaches top_p is kept, and the token is where the running sum of p first
+ * reaches target = kept_sum * u, u = min(word * 2^-64, 1 - 2^-53) for the row's
+ * 64-bit word: the draw of std::uniform_real_distribution<double>(0,
+ * kept_sum) from a std::mt19937_64 whose next output is the word (one word
+ * per sampled row, as the reference draws). The orderings, prefix and draw
+ * follow the reference exactly; sum(p) is added in a fixed tree order rather
+ * than in sorted order, so a token can differ only where a threshold lies
+ * within the double rounding of a running sum. Rejected like the reference:
+ * temperature outside {0} and [1e-4, 2], top_p outside (0, 1], count 0
+ * (ADI_HIP_INVALID_ARGUMENT); a row holding a non-finite logit yields
+ * 0xFFFFFFFF. logits: DEVICE [rows, count]; words: DEVICE [rows] (unused at
+ * temperature 0, may be NULL); tokens: DEVICE [rows]. */
+int adi_hip_sample_rows(adi_hip_context *ctx, const float *logits, uint32_t rows,
+                        uint32_t count, float temperature, float top_p,
+                        const uint64_t *words, uint32_t *tokens);
+
 /* ---- kernel profiling ----------------------------------------------------- */
 
 /* Per-kernel timing with HIP events on the context stream, the counterpart

@@ -764,6 +764,94 @@ uint32_t ao_argmax(const float *logits, uint32_t count) {
     return best;
 }
 
+/* src/generation.cpp:36-47: ascending order of this key is descending logit
+ * order, with -0 folded into +0. */
+static uint32_t descending_key(float value) {
+    uint32_t bits = 0;
+    if (value != 0.0f) {
+        memcpy(&bits, &value, sizeof(bits));
+    }
+    const uint32_t ascending = (bits & 0x80000000u) ? ~bits : bits ^ 0x80000000u;
+    return ~ascending;
+}
+
+static int by_key_then_index(const void *a, const void *b) {
+    const uint64_t x = *(const uint64_t *)a, y = *(const uint64_t *)b;
+    return x < y ? -1 : (x > y ? 1 : 0);
+}
+
+int ao_sample_token(const float *logits, uint32_t count, float temperature, float top_p,
+                    uint64_t word, uint32_t *token) {
+    if (!logits || !token || count == 0 || !isfinite(temperature) || !isfinite(top_p) ||
+        temperature < 0.0f || (temperature > 0.0f && temperature < 1.0e-4f) ||
+        temperature > 2.0f || top_p <= 0.0f || top_p > 1.0f) {
+        return AO_INVALID_ARGUMENT;
+    }
+    for (uint32_t i = 0; i < count; ++i) {
+        if (!isfinite(logits[i])) {
+            return AO_INVALID_ARGUMENT;
+        }
+    }
+    if (temperature == 0.0f) {
+        *token = ao_argmax(logits, count);
+        return AO_OK;
+    }
+    /* the reference's stable LSD radix sort over the key from ascending
+     * indexes is the order of (key, index) */
+    uint64_t *order = malloc(sizeof(uint64_t) * count);
+    double *p = malloc(sizeof(double) * count);
+    if (!order || !p) {
+        free(order);
+        free(p);
+        return AO_OUT_OF_MEMORY;
+    }
+    for (uint32_t i = 0; i < count; ++i) {
+        order[i] = ((uint64_t)descending_key(logits[i]) << 32) | i;
+    }
+    qsort(order, count, sizeof(uint64_t), by_key_then_index);
+    const double maximum = (double)logits[(uint32_t)order[0]];
+    double denominator = 0.0;
+    for (uint32_t k = 0; k < count; ++k) {
+        p[k] = exp(((double)logits[(uint32_t)order[k]] - maximum) / (double)temperature);
+        denominator += p[k];
+    }
+    double cumulative = 0.0;
+    uint32_t retained = 0;
+    for (; retained < count; ++retained) {
+        cumulative += p[retained] / denominator;
+        if (cumulative >= top_p) {
+            ++retained;
+            break;
+        }
+    }
+    if (retained == 0) {
+        retained = 1;
+    }
+    double retained_sum = 0.0;
+    for (uint32_t k = 0; k < retained; ++k) {
+        retained_sum += p[k];
+    }
+    /* uniform_real_distribution<double>(0, retained_sum) over
+     * generate_canonical<double, 53> of a 64-bit engine: one word */
+    double u = (double)word * 0x1p-64;
+    if (u >= 1.0) {
+        u = nextafter(1.0, 0.0);
+    }
+    const double target = u * retained_sum + 0.0;
+    double running = 0.0;
+    *token = (uint32_t)order[retained - 1];
+    for (uint32_t k = 0; k < retained; ++k) {
+        running += p[k];
+        if (target <= running) {
+            *token = (uint32_t)order[k];
+            break;
+        }
+    }
+    free(order);
+    free(p);
+    return AO_OK;
+}
+
 float ao_silu(float value) {
     return value / (1.0f + expf(-value));
 }

@@ -184,6 +184,16 @@ int ao_embedding_row(const ao_embedding *embedding, uint32_t token, float *outpu
  * largest logit (std::max_element, src/generation.cpp:180-183). */
 uint32_t ao_argmax(const float *logits, uint32_t count);
 
+/* sample_token (src/generation.cpp:161-225) with the engine's draw given as
+ * its 64-bit word: tokens sorted by logit descending (ties by index, -0 ==
+ * +0), p = exp((l - max) / temperature) in double, the prefix whose running
+ * p / sum(p) reaches top_p, target = kept_sum * (word * 2^-64, capped below
+ * 1), and the first token where the running p reaches target. The sums run
+ * in sorted order as the reference's. AO_INVALID_ARGUMENT for the
+ * reference's rejected parameters or a non-finite logit. */
+int ao_sample_token(const float *logits, uint32_t count, float temperature, float top_p,
+                    uint64_t word, uint32_t *token);
+
 #ifdef __cplusplus
 }
 #endif

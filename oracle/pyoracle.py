@@ -121,6 +121,7 @@ def load_oracle() -> C.CDLL:
              C.c_uint32, f32p, u32p, f32p, C.c_int)
     _declare(lib, "ao_embedding_row", C.c_int, C.POINTER(Embedding), C.c_uint32, f32p)
     _declare(lib, "ao_argmax", C.c_uint32, f32p, C.c_uint32)
+    _declare(lib, "ao_sample_token", C.c_int, f32p, C.c_uint32, C.c_float, C.c_float, C.c_uint64, u32p)
     return lib
 
 
@@ -294,6 +295,14 @@ def ref_sample_token(lib, logits: np.ndarray, temperature: float, top_p: float, 
     check(lib.ref_sample_token(ptr(logits, C.c_float), logits.size, temperature, top_p, seed,
                                C.byref(word), ptr(token, C.c_uint32)), "sample_token")
     return int(token[0]), word.value
+
+
+def sample_token(lib, logits: np.ndarray, temperature: float, top_p: float, word: int) -> int:
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    token = np.zeros(1, np.uint32)
+    check(lib.ao_sample_token(ptr(logits, C.c_float), logits.size, temperature, top_p, word,
+                              ptr(token, C.c_uint32)), "sample_token")
+    return int(token[0])
 
 
 def ref_gguf_summary(lib, path: str):

@@ -73,3 +73,43 @@ def test_argmax_matches_reference_greedy(oracle, ref):
         want, _ = po.ref_sample_token(ref, logits, 0.0, 1.0, 0)
         assert argmax(oracle, logits) == want
     assert argmax(oracle, tie) == 17 and argmax(oracle, zeros) == 10
+
+
+@pytest.mark.parametrize("count", [1, 7, 1000, 151936])
+def test_sample_token_matches_reference(oracle, ref, count):
+    """The oracle's sample_token given the engine's first word draws the
+    same token as the compiled sample_token with its std::mt19937_64."""
+    rng = np.random.default_rng(count)
+    for trial in range(40 if count < 100000 else 6):
+        kind = trial % 4
+        if kind == 0:
+            logits = rng.normal(0, 3, count).astype(np.float32)
+        elif kind == 1:
+            logits = rng.integers(-3, 3, count).astype(np.float32)   # ties
+        elif kind == 2:
+            logits = rng.normal(0, 0.01, count).astype(np.float32)  # flat
+        else:
+            logits = rng.normal(0, 1, count).astype(np.float32)
+            logits[0] = -0.0
+        temperature = float(rng.choice([0.0, 1e-4, 0.1, 0.7, 2.0]))
+        top_p = float(rng.choice([0.05, 0.5, 0.9, 1.0]))
+        want, word = po.ref_sample_token(ref, logits, temperature, top_p, int(rng.integers(0, 2**63)))
+        assert po.sample_token(oracle, logits, temperature, top_p, word) == want
+
+
+def test_sample_token_closed_form(oracle):
+    # two tokens, logits 0 and ln 3 at temperature 1: p = 1/3 and 1 in sorted
+    # order (token 1 first); kept sum 4/3 at top_p 1; target = u * 4/3
+    logits = np.array([0.0, np.log(3.0)], np.float32)
+    t1 = po.sample_token(oracle, logits, 1.0, 1.0, 0)              # u = 0 -> first sorted
+    t2 = po.sample_token(oracle, logits, 1.0, 1.0, (1 << 64) - 1)  # u -> 1 -> last
+    t3 = po.sample_token(oracle, logits, 1.0, 0.5, (1 << 64) - 1)  # top_p 0.5 keeps one
+    assert (t1, t2, t3) == (1, 0, 1)
+
+
+@pytest.mark.parametrize("temperature,top_p", [(-1.0, 0.9), (5e-5, 0.9), (2.5, 0.9), (1.0, 0.0),
+                                               (1.0, 1.5), (float("nan"), 0.9)])
+def test_sample_token_rejects_parameters(oracle, temperature, top_p):
+    logits = np.zeros(4, np.float32)
+    with pytest.raises(ValueError):
+        po.sample_token(oracle, logits, temperature, top_p, 1)

@@ -87,3 +87,68 @@ def test_embedding_from_checkpoint(gpu, oracle, tmp_path):
     want = po.embedding_rows(oracle, e, tokens)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     emb.close()
+
+
+def sample_device(gpu, logits, temperature, top_p, words):
+    rows, count = logits.shape
+    t = torch.empty(rows, dtype=torch.int32, device="cuda")
+    w = torch.tensor(np.asarray(words, np.uint64).view(np.int64), device="cuda")
+    hip.sample_rows(gpu, torch.from_numpy(np.ascontiguousarray(logits)).cuda(), rows, count,
+                    temperature, top_p, w, t)
+    return t.cpu().numpy().view(np.uint32)
+
+
+def logit_rows(rng, rows, count):
+    out = np.empty((rows, count), np.float32)
+    for r in range(rows):
+        kind = r % 4
+        if kind == 0:
+            out[r] = rng.normal(0, 3, count)
+        elif kind == 1:
+            out[r] = rng.integers(-4, 4, count)            # many ties
+        elif kind == 2:
+            out[r] = rng.normal(0, 0.05, count)            # flat: top-p keeps many
+        else:
+            out[r] = rng.normal(0, 1.5, count)
+            out[r, rng.integers(0, count, 5)] = 0.0
+            out[r, min(1, count - 1)] = -0.0
+    return out
+
+
+@pytest.mark.parametrize("temperature,top_p", [(0.0, 0.9), (1e-4, 0.9), (0.7, 0.9), (1.0, 1.0),
+                                               (2.0, 0.5), (0.3, 0.05)])
+def test_sample_rows_match_oracle(gpu, oracle, temperature, top_p):
+    rng = np.random.default_rng(int(temperature * 1000 + top_p * 100))
+    rows, count = 12, 151936
+    logits = logit_rows(rng, rows, count)
+    words = rng.integers(0, 2**63, rows, dtype=np.uint64) * 2 + rng.integers(0, 2, rows, dtype=np.uint64)
+    got = sample_device(gpu, logits, temperature, top_p, words)
+    want = [po.sample_token(oracle, logits[r], temperature, top_p, int(words[r])) for r in range(rows)]
+    assert got.tolist() == want
+
+
+def test_sample_rows_small_vocabularies_and_edges(gpu, oracle):
+    rng = np.random.default_rng(77)
+    for count in (1, 2, 63, 4096, 4097, 12289):
+        logits = logit_rows(rng, 8, count)
+        words = np.array([0, (1 << 64) - 1] + rng.integers(0, 2**63, 6).tolist(), np.uint64)
+        for temperature, top_p in ((0.8, 0.95), (1.5, 1.0)):
+            got = sample_device(gpu, logits, temperature, top_p, words)
+            want = [po.sample_token(oracle, logits[r], temperature, top_p, int(words[r]))
+                    for r in range(8)]
+            assert got.tolist() == want, (count, temperature, top_p)
+
+
+def test_sample_rows_non_finite_and_parameters(gpu):
+    logits = np.random.default_rng(5).normal(0, 1, (3, 1000)).astype(np.float32)
+    logits[1, 10] = np.nan
+    logits[2, 999] = -np.inf
+    got = sample_device(gpu, logits, 0.7, 0.9, [1, 2, 3])
+    assert got[1] == 0xFFFFFFFF and got[2] == 0xFFFFFFFF and got[0] < 1000
+    t = torch.empty(3, dtype=torch.int32, device="cuda")
+    x = torch.from_numpy(logits).cuda()
+    for temperature, top_p in ((5e-5, 0.9), (2.5, 0.9), (0.7, 0.0), (0.7, 1.01)):
+        with pytest.raises(hip.HipError, match="invalid sampling parameters"):
+            hip.sample_rows(gpu, x, 3, 1000, temperature, top_p, None, t)
+    with pytest.raises(hip.HipError, match="one random word per row"):
+        hip.sample_rows(gpu, x, 3, 1000, 0.7, 0.9, None, t)
