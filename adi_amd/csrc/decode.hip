@@ -10,7 +10,50 @@ namespace adi_hip {
 namespace {
 
 constexpr uint32_t kEmbeddingThreads = 256;
-constexpr uint32_t kArgmaxThreads = 256;
+constexpr uint32_t kArgmaxThreads = 1024;
+
+// Calls f(i, v) for every logit of a row, each index once, from this thread's
+// share of the block: 16-byte loads with four in flight when the row is
+// 16-byte aligned, one float at a time otherwise. The order is fixed by the
+// row length and the block size.
+template <typename F>
+__device__ __forceinline__ void for_each_logit(const float *row, uint32_t count, F &&f) {
+    const uint32_t step = blockDim.x;
+    if ((reinterpret_cast<uintptr_t>(row) & 15u) == 0u) {
+        const uint32_t vectors = count / 4u;
+        const float4 *r4 = reinterpret_cast<const float4 *>(row);
+        uint32_t j = threadIdx.x;
+        for (; j + 3u * step < vectors; j += 4u * step) {
+            float4 a[4];
+#pragma unroll
+            for (uint32_t u = 0; u < 4; ++u) {
+                a[u] = r4[j + u * step];
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 4; ++u) {
+                const uint32_t i = 4u * (j + u * step);
+                f(i, a[u].x);
+                f(i + 1u, a[u].y);
+                f(i + 2u, a[u].z);
+                f(i + 3u, a[u].w);
+            }
+        }
+        for (; j < vectors; j += step) {
+            const float4 a = r4[j];
+            f(4u * j, a.x);
+            f(4u * j + 1u, a.y);
+            f(4u * j + 2u, a.z);
+            f(4u * j + 3u, a.w);
+        }
+        for (uint32_t i = 4u * vectors + threadIdx.x; i < count; i += step) {
+            f(i, row[i]);
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < count; i += step) {
+            f(i, row[i]);
+        }
+    }
+}
 
 // First index of `key` in the ascending list, or `count` (lower_bound).
 __device__ __forceinline__ uint32_t lower_bound_u32(const uint32_t *list, uint32_t count,
@@ -95,11 +138,10 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_argmax_rows(const float *log
     float value = -__builtin_huge_valf();
     uint32_t index = 0xFFFFFFFFu;
     uint32_t bad = 0;
-    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
-        const float v = row[i];
+    for_each_logit(row, count, [&](uint32_t i, float v) {
         bad |= __builtin_isfinite(v) ? 0u : 1u;
         better(value, index, v, i);
-    }
+    });
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1) {
         const float v = __shfl_xor(value, offset);
@@ -168,13 +210,13 @@ __device__ void radix_select(const float *row, uint32_t count, SampleState &s, u
             hist[b] = 0u;
         }
         __syncthreads();
-        for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
-            const uint32_t key = descending_key(row[i]);
+        for_each_logit(row, count, [&](uint32_t i, float logit) {
+            const uint32_t key = descending_key(logit);
             const uint32_t v = value(key, i);
             if (eligible(s, key, i) && filter(key, i) && (v & mask) == prefix) {
                 atomicAdd(&hist[(v >> shift) & 0xFFu], 1u);
             }
-        }
+        });
         __syncthreads();
         if (threadIdx.x == 0) {
             uint32_t b = 0, w = s.want;
@@ -221,8 +263,8 @@ __device__ void gather_window(const float *row, uint32_t count, double maximum, 
         index_th = s.select;
     }
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
-        const uint32_t key = descending_key(row[i]);
+    for_each_logit(row, count, [&](uint32_t i, float logit) {
+        const uint32_t key = descending_key(logit);
         if (eligible(s, key, i) &&
             (take_all != 0u || key < key_th || (key == key_th && i <= index_th))) {
             const uint32_t at = atomicAdd(&s.count, 1u);
@@ -230,7 +272,7 @@ __device__ void gather_window(const float *row, uint32_t count, double maximum, 
                 cand[at] = (static_cast<uint64_t>(key) << 32) | i;
             }
         }
-    }
+    });
     __syncthreads();
     const uint32_t n = s.count < kWindow ? s.count : kWindow;
     for (uint32_t k = n + threadIdx.x; k < kWindow; k += blockDim.x) {
@@ -285,11 +327,10 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_rows(const float *log
     // the maximum; any non-finite logit rejects the row
     float m = -__builtin_huge_valf();
     uint32_t bad = 0;
-    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
-        const float v = row[i];
+    for_each_logit(row, count, [&](uint32_t, float v) {
         bad |= __builtin_isfinite(v) ? 0u : 1u;
         m = v > m ? v : m;
-    }
+    });
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1) {
         const float o = __shfl_xor(m, offset);
@@ -323,9 +364,9 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_rows(const float *log
     const double t = static_cast<double>(temperature);
     // sum of p over the row: each thread in index order, then a fixed tree
     double part = 0.0;
-    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
-        part += exp((static_cast<double>(row[i]) - maximum) / t);
-    }
+    for_each_logit(row, count, [&](uint32_t, float v) {
+        part += exp((static_cast<double>(v) - maximum) / t);
+    });
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1) {
         part += __shfl_xor(part, offset);

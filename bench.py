@@ -278,6 +278,47 @@ def projections(torch, hip, ctx, steps):
             "ms_per_call": round(dt * 1e3, 4), "vectors_per_s": round(batch / dt, 1),
             "packed_gbs": round(nbytes / dt / 1e9, 1),
             "hbm_frac": round(nbytes / dt / 1e9 / HBM_PEAK_GBS, 4)}
+    res.update(decode_side(torch, hip, ctx, steps))
+    return res
+
+
+def decode_side(torch, hip, ctx, steps):
+    """The token side of a decode step at the checkpoint's vocabulary
+    (248,320 x 2048): the embedding row of a device-resident token, the greedy
+    choice, and top-p sampling (temperature 0.7, top_p 0.9) over logits shaped
+    like an LM's (a few dominant tokens over a normal tail)."""
+    from adi_amd import synthetic as syn
+    res = {}
+    vocab, hidden = 248320, 2048
+    rng = syn.rng_for(4, 0)
+    e = syn.embedding(rng, vocab, hidden, exceptions=20000)
+    emb = hip.upload_embedding(ctx, e)
+    tokens = torch.tensor(rng.integers(0, vocab, 64).astype(np.int32), device="cuda")
+    out = torch.empty((64, hidden), dtype=torch.float32, device="cuda")
+    logits_host = rng.normal(0.0, 2.0, (4, vocab)).astype(np.float32)
+    logits_host[:, rng.integers(0, vocab, 16)] += 12.0
+    logits = torch.from_numpy(logits_host).cuda()
+    words = torch.tensor(rng.integers(0, 2**62, 4).astype(np.int64), device="cuda")
+    picked = torch.empty(4, dtype=torch.int32, device="cuda")
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps * 1e6
+
+    for batch in (1, 64):
+        us = timed(lambda: hip.embedding_rows(ctx, emb, tokens, batch, out))
+        res[f"embedding_{vocab}x{hidden}_b{batch}"] = {"us_per_call": round(us, 2)}
+    for rows in (1, 4):
+        us = timed(lambda: hip.argmax_rows(ctx, logits, rows, vocab, picked))
+        res[f"greedy_{vocab}_rows{rows}"] = {"us_per_call": round(us, 2)}
+        us = timed(lambda: hip.sample_rows(ctx, logits, rows, vocab, 0.7, 0.9, words, picked))
+        res[f"top_p_{vocab}_rows{rows}"] = {"us_per_call": round(us, 2)}
     return res
 
 
