@@ -378,6 +378,41 @@ __device__ __forceinline__ void store_wave(float *dst, uint32_t lane, const floa
     }
 }
 
+// Up to four slices of a vector of at most 512 elements, loaded at once
+// (slices past `splits` reload the last one and are not added).
+template <int VPL>
+struct SliceLoads {
+    float a[4][VPL];
+};
+
+template <int VPL>
+__device__ __forceinline__ void load_slices(const float *src, size_t stride, uint32_t splits,
+                                            uint32_t lane, SliceLoads<VPL> &l) {
+    static_assert(VPL <= 8, "load_slices: vectors of at most 512 elements");
+#pragma unroll
+    for (uint32_t s = 0; s < 4; ++s) {
+        load_wave<VPL>(src + (s < splits ? s : splits - 1u) * stride, lane, l.a[s]);
+    }
+}
+
+// v = ((0 + slice 0) + slice 1) + ..., the order of sum_slices.
+template <int VPL>
+__device__ __forceinline__ void add_slices(const SliceLoads<VPL> &l, uint32_t splits,
+                                           float (&v)[VPL]) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        v[i] = 0.0f + l.a[0][i];
+    }
+#pragma unroll
+    for (uint32_t s = 1; s < 4; ++s) {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            v[i] = s < splits ? v[i] + l.a[s][i] : v[i];
+        }
+    }
+}
+
 // v = sum over slices s < splits of src[s * stride ..] in the wave layout,
 // added in slice order; two slices are loaded per round so the loads overlap
 // (one for the widest vectors, whose registers would not hold two).
@@ -385,6 +420,14 @@ template <int VPL>
 __device__ __forceinline__ void sum_slices(const float *src, size_t stride, uint32_t splits,
                                            uint32_t lane, float (&v)[VPL]) {
 #pragma clang fp contract(off)
+    if constexpr (VPL <= 8) {
+        if (splits >= 1 && splits <= 4) {
+            SliceLoads<VPL> l;
+            load_slices<VPL>(src, stride, splits, lane, l);
+            add_slices<VPL>(l, splits, v);
+            return;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
         v[i] = 0.0f;

@@ -11,6 +11,7 @@
 // builds do not. Contraction is switched off in this file and the fused form
 // is written as fmaf.
 #include "dense.hpp"
+#include "route.hpp"
 
 namespace adi_hip {
 namespace {
@@ -93,8 +94,49 @@ __global__ __launch_bounds__(256) void k_bf16_ordered(
 // so the lanes' strictly sequential multiply-add chains read only LDS. An
 // optional extra row (the shared-expert gate) is appended after `rows` and
 // written to `out_extra`.
+// The chains of one thread for the first NT tokens: lane `lane` of a row
+// accumulates columns lane, lane + LANES, ... in order (operands of kUnroll
+// steps are read from LDS first, then the chains advance).
+template <int LANES, bool FUSED, int NT>
+__device__ __forceinline__ void bf16_chains(const uint16_t *wr, const float *xs, uint32_t columns,
+                                            uint32_t full, uint32_t lane,
+                                            float (&acc)[kTokensPerThread]) {
+#pragma clang fp contract(off)
+    constexpr uint32_t kUnroll = 8;
+    uint32_t base = 0;
+    for (; base + kUnroll * LANES <= full; base += kUnroll * LANES) {
+        float wk[kUnroll], xk[NT][kUnroll];
+#pragma unroll
+        for (uint32_t u = 0; u < kUnroll; ++u) {
+            const uint32_t k = base + u * LANES + lane;
+            wk[u] = bf16_bits_to_float(wr[k]);
+#pragma unroll
+            for (uint32_t t = 0; t < NT; ++t) {
+                xk[t][u] = xs[t * columns + k];
+            }
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kUnroll; ++u) {
+#pragma unroll
+            for (uint32_t t = 0; t < NT; ++t) {
+                acc[t] = lane_step<LANES, FUSED>(acc[t], wk[u], xk[t][u]);
+            }
+        }
+    }
+    for (; base < full; base += LANES) {
+        const uint32_t k = base + lane;
+        const float wk = bf16_bits_to_float(wr[k]);
+#pragma unroll
+        for (uint32_t t = 0; t < NT; ++t) {
+            acc[t] = lane_step<LANES, FUSED>(acc[t], wk, xs[t * columns + k]);
+        }
+    }
+}
+
+// One wave per block: registers for a whole staging round (24 16-byte loads
+// in flight) matter more than occupancy.
 template <int LANES, bool FUSED>
-__global__ __launch_bounds__(64) void k_bf16_lds(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_bf16_lds(
     const uint16_t *__restrict__ w, uint32_t rows, const uint16_t *__restrict__ w_extra,
     uint32_t columns, const float *__restrict__ x, uint32_t batch, float *__restrict__ out,
     float *__restrict__ out_extra) {
@@ -104,11 +146,6 @@ __global__ __launch_bounds__(64) void k_bf16_lds(
     const uint32_t t0 = blockIdx.y * kTokensPerThread;
     const uint32_t tokens = batch - t0 < kTokensPerThread ? batch - t0 : kTokensPerThread;
     uint16_t *ws = reinterpret_cast<uint16_t *>(xs + static_cast<size_t>(kTokensPerThread) * columns);
-    for (uint32_t t = tokens; t < kTokensPerThread; ++t) {
-        for (uint32_t k = threadIdx.x; k < columns; k += 64u) {
-            xs[t * columns + k] = 0.0f;
-        }
-    }
     const uint32_t total_rows = rows + (w_extra != nullptr ? 1u : 0u);
     const uint32_t row0 = blockIdx.x * rows_per_block;
     const uint32_t rows_here =
@@ -180,37 +217,16 @@ __global__ __launch_bounds__(64) void k_bf16_lds(
     const bool row_ok = row < total_rows;
     const uint16_t *wr = ws + local_row * columns;
     const uint32_t full = columns / LANES * LANES;
+    // chains of the block's tokens only (rows of xs past `tokens` are not
+    // staged; the sums of those chains are never read)
     float acc[kTokensPerThread] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (row_ok) {
-        constexpr uint32_t kUnroll = 8;
-        uint32_t base = 0;
-        // operands of kUnroll steps are read first, then the chain advances
-        for (; base + kUnroll * LANES <= full; base += kUnroll * LANES) {
-            float wk[kUnroll], xk[kTokensPerThread][kUnroll];
-#pragma unroll
-            for (uint32_t u = 0; u < kUnroll; ++u) {
-                const uint32_t k = base + u * LANES + lane;
-                wk[u] = bf16_bits_to_float(wr[k]);
-#pragma unroll
-                for (uint32_t t = 0; t < kTokensPerThread; ++t) {
-                    xk[t][u] = xs[t * columns + k];
-                }
-            }
-#pragma unroll
-            for (uint32_t u = 0; u < kUnroll; ++u) {
-#pragma unroll
-                for (uint32_t t = 0; t < kTokensPerThread; ++t) {
-                    acc[t] = lane_step<LANES, FUSED>(acc[t], wk[u], xk[t][u]);
-                }
-            }
-        }
-        for (; base < full; base += LANES) {
-            const uint32_t k = base + lane;
-            const float wk = bf16_bits_to_float(wr[k]);
-#pragma unroll
-            for (uint32_t t = 0; t < kTokensPerThread; ++t) {
-                acc[t] = lane_step<LANES, FUSED>(acc[t], wk, xs[t * columns + k]);
-            }
+        static_assert(kTokensPerThread == 4, "one case per token count");
+        switch (tokens) {
+        case 1: bf16_chains<LANES, FUSED, 1>(wr, xs, columns, full, lane, acc); break;
+        case 2: bf16_chains<LANES, FUSED, 2>(wr, xs, columns, full, lane, acc); break;
+        case 3: bf16_chains<LANES, FUSED, 3>(wr, xs, columns, full, lane, acc); break;
+        default: bf16_chains<LANES, FUSED, 4>(wr, xs, columns, full, lane, acc); break;
         }
     }
     // ordered lane sums through LDS: lane t of each row finishes token t
@@ -440,108 +456,6 @@ __global__ __launch_bounds__(64) void k_rms_norm(
     }
 }
 
-// Order-preserving key of (logit, expert) for "larger logit first, lower
-// index on ties": the float's bits mapped to an unsigned order (with -0
-// folded into +0, which compares equal to it) above the complemented index.
-// Key 0 is below every real key and marks an empty slot.
-__device__ __forceinline__ uint64_t route_key(float value, uint32_t expert) {
-    const uint32_t bits = __float_as_uint(value + 0.0f);
-    const uint32_t ordered = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
-    return (static_cast<uint64_t>(ordered) << 32) | static_cast<uint32_t>(~expert);
-}
-
-__device__ __forceinline__ float route_key_value(uint64_t key) {
-    const uint32_t ordered = static_cast<uint32_t>(key >> 32);
-    return __uint_as_float((ordered & 0x80000000u) ? (ordered & 0x7FFFFFFFu) : ~ordered);
-}
-
-template <int MASK>
-__device__ __forceinline__ uint64_t key_max_step(uint64_t key) {
-    const uint64_t other =
-        (static_cast<uint64_t>(lane_xor_bits<MASK>(static_cast<uint32_t>(key >> 32))) << 32) |
-        lane_xor_bits<MASK>(static_cast<uint32_t>(key));
-    return other > key ? other : key;
-}
-
-// One wave per logit row. Lane l holds experts l, l+64, ...; eight rounds of
-// a wave-wide maximum over route keys (registers only) pick the routes in the
-// order of the comparator of top_experts (src/executor.cpp:202-211). The
-// softmax over the eight then runs on lane 0 in the reference's order
-// (src/executor.cpp:213-227).
-template <int SLOTS>
-__device__ __forceinline__ void top8_wave(const float *__restrict__ row,
-                                          const float *__restrict__ bias, uint32_t experts,
-                                          uint32_t lane, uint32_t *__restrict__ route_expert,
-                                          float *__restrict__ route_weight,
-                                          uint32_t *local_expert = nullptr) {
-#pragma clang fp contract(off)
-    constexpr uint32_t per_lane = SLOTS;
-    float value[per_lane], offset[per_lane];
-    // unguarded loads of clamped indexes, so all of them are in flight at once
-#pragma unroll
-    for (uint32_t i = 0; i < per_lane; ++i) {
-        const uint32_t e = min(lane + 64u * i, experts - 1u);
-        value[i] = row[e];
-        offset[i] = bias != nullptr ? bias[e] : 0.0f;
-    }
-    uint64_t key[per_lane];
-#pragma unroll
-    for (uint32_t i = 0; i < per_lane; ++i) {
-        const uint32_t e = lane + 64u * i;
-        const float v = bias != nullptr ? value[i] + offset[i] : value[i];
-        key[i] = e < experts ? route_key(v, e) : 0ull;
-    }
-    float chosen_value[8];
-    uint32_t chosen_index[8];
-    for (int round = 0; round < 8; ++round) {
-        uint64_t best = 0;
-#pragma unroll
-        for (uint32_t i = 0; i < per_lane; ++i) {
-            best = key[i] > best ? key[i] : best;
-        }
-        best = key_max_step<1>(best);
-        best = key_max_step<2>(best);
-        best = key_max_step<4>(best);
-        best = key_max_step<8>(best);
-        best = key_max_step<16>(best);
-        best = key_max_step<32>(best);
-        // identical in every lane: keep it in scalar registers
-        const uint32_t win_hi =
-            static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(best >> 32)));
-        const uint32_t win_lo =
-            static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(best)));
-        const uint64_t win = (static_cast<uint64_t>(win_hi) << 32) | win_lo;
-        const uint32_t index = ~static_cast<uint32_t>(win);
-        chosen_value[round] = route_key_value(win);
-        chosen_index[round] = index;
-        if (index % 64u == lane) {
-#pragma unroll
-            for (uint32_t i = 0; i < per_lane; ++i) {
-                if (i == index / 64u) {
-                    key[i] = 0ull;
-                }
-            }
-        }
-    }
-    if (lane == 0) {
-        const float maximum = chosen_value[0];
-        float selected[8];
-        float sum = 0.0f;
-        for (int i = 0; i < 8; ++i) {
-            selected[i] = expf(chosen_value[i] - maximum);
-            sum = sum + selected[i];
-        }
-        sum = fmaxf(sum, 6.103515625e-5f);
-        for (int i = 0; i < 8; ++i) {
-            route_expert[i] = chosen_index[i];
-            route_weight[i] = selected[i] / sum;
-            if (local_expert != nullptr) {
-                local_expert[i] = chosen_index[i];
-            }
-        }
-    }
-}
-
 // One wave per row, four rows per block.
 template <int SLOTS>
 __global__ __launch_bounds__(256) void k_top_experts(
@@ -553,117 +467,6 @@ __global__ __launch_bounds__(256) void k_top_experts(
     }
     top8_wave<SLOTS>(logits + static_cast<size_t>(row) * experts, bias, experts,
                      threadIdx.x & 63u, route_expert + row * 8u, route_weight + row * 8u);
-}
-
-// Counting sort of moe_forward_batch (src/executor.cpp:1235-1258) in one
-// wave: counts by LDS integer atomics, an exclusive scan for offsets, then the
-// (token, route) slots are placed 64 at a time in order; lanes that share an
-// expert in a chunk find their rank among earlier lanes with ballots, so each
-// expert's cursor advances exactly as the sequential loop's does.
-// `route_expert` is a.route_expert or a copy of it in LDS.
-__device__ __forceinline__ void route_sort_block(const RouteSort &a,
-                                                 const uint32_t *route_expert,
-                                                 uint32_t *counts, uint32_t *cursor) {
-    for (uint32_t e = threadIdx.x; e < a.experts; e += blockDim.x) {
-        counts[e] = 0u;
-    }
-    __syncthreads();
-    for (uint32_t i = threadIdx.x; i < a.positions; i += blockDim.x) {
-        atomicAdd(&counts[route_expert[i]], 1u);
-    }
-    __syncthreads();
-    if (threadIdx.x >= 64) {
-        return;  // the scan and the ordered scatter run on wave 0
-    }
-    const uint32_t lane = threadIdx.x;
-    // exclusive scan over experts: each lane owns a contiguous run
-    const uint32_t per_lane = (a.experts + 63u) / 64u;
-    const uint32_t first = lane * per_lane;
-    uint32_t local = 0;
-    for (uint32_t e = first; e < first + per_lane && e < a.experts; ++e) {
-        local += counts[e];
-    }
-    uint32_t inclusive = local;
-    for (int offset = 1; offset < 64; offset <<= 1) {
-        const uint32_t other = static_cast<uint32_t>(__shfl_up(static_cast<int>(inclusive), offset));
-        if (lane >= static_cast<uint32_t>(offset)) {
-            inclusive += other;
-        }
-    }
-    uint32_t running = inclusive - local;
-    for (uint32_t e = first; e < first + per_lane && e < a.experts; ++e) {
-        cursor[e] = running;
-        a.offsets[e] = running;
-        a.counts[e] = counts[e];
-        if (a.position_expert != nullptr) {
-            for (uint32_t p = running; p < running + counts[e]; ++p) {
-                a.position_expert[p] = e;
-            }
-        }
-        running += counts[e];
-    }
-    if (lane == 63) {
-        a.offsets[a.experts] = inclusive;
-    }
-    // ascending list of active experts
-    if (a.active != nullptr) {
-        uint32_t base = 0;
-        for (uint32_t e0 = 0; e0 < a.experts; e0 += 64u) {
-            const uint32_t e = e0 + lane;
-            const bool on = e < a.experts && counts[e] != 0u;
-            const uint64_t mask = __ballot(on);
-            if (on) {
-                const uint32_t s = base + __popcll(mask & ((1ull << lane) - 1ull));
-                a.active[s] = e;
-                if (a.slot_info != nullptr) {
-                    a.slot_info[s] = make_uint4(e, cursor[e], cursor[e] + counts[e], 0u);
-                }
-            }
-            base += __popcll(mask);
-        }
-        if (a.slot_info != nullptr) {
-            for (uint32_t s = base + lane; s < a.experts; s += 64u) {
-                a.slot_info[s] = make_uint4(0u, 0u, 0u, 0u);
-            }
-        }
-        if (lane == 0 && a.active_count != nullptr) {
-            *a.active_count = base;
-        }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    const uint64_t below = (1ull << lane) - 1ull;
-    for (uint32_t c = 0; c < a.positions; c += 64u) {
-        const uint32_t i = c + lane;
-        const bool valid = i < a.positions;
-        const uint32_t e = valid ? route_expert[i] : 0u;
-        uint64_t peers = __ballot(valid);
-        if (!valid) {
-            peers = ~peers;
-        }
-        for (uint32_t bit = 0; bit < 10u; ++bit) {
-            const bool set = (e >> bit) & 1u;
-            const uint64_t vote = __ballot(set);
-            peers &= set ? vote : ~vote;
-        }
-        const uint32_t rank = __popcll(peers & below);
-        const uint32_t total = __popcll(peers);
-        uint32_t position = 0;
-        if (valid) {
-            position = cursor[e] + rank;
-        }
-        // every lane has read its cursor before any lane advances one
-        __builtin_amdgcn_wave_barrier();
-        if (valid) {
-            a.grouped_batch[position] = i / 8u;
-            a.route_to_grouped[i] = position;
-            if (rank == 0) {
-                cursor[e] += total;
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-    }
 }
 
 // ---- multi-block sort ---------------------------------------------------------

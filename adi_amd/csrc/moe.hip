@@ -22,6 +22,7 @@
 #include "dense.hpp"
 #include "grouped.hpp"
 #include "projection.hpp"
+#include "route.hpp"
 
 namespace adi_hip {
 namespace {
@@ -74,8 +75,18 @@ __global__ __launch_bounds__(256) void k_swiglu_wave(SwigluJobs j) {
     const SwigluSegment &g = j.seg[s];
     const uint32_t n = 64u * VPL;
     const size_t base = static_cast<size_t>(v) * n;
-    // the scales are loaded with the slices, before the transforms
+    // the matrix index, then the slices (up to four at once), then the scales
+    // that depend on the index: the slices are in flight during its wait
     const size_t mat = g.matrix_index != nullptr ? g.matrix_index[v] : 0u;
+    float gv[VPL], uv[VPL];
+    const bool at_once = VPL <= 8 && g.splits >= 1 && g.splits <= 4;
+    SliceLoads<VPL <= 8 ? VPL : 1> lg, lu;
+    if constexpr (VPL <= 8) {
+        if (at_once) {
+            load_slices<VPL>(g.z_gate + base, g.split_stride, g.splits, lane, lg);
+            load_slices<VPL>(g.z_up + base, g.split_stride, g.splits, lane, lu);
+        }
+    }
     float sa[VPL], sb[VPL], sc[VPL];
     if (g.sv_gate_f16 != nullptr) {
         load_wave_f16<VPL>(g.sv_gate_f16 + mat * n, lane, sa);
@@ -86,9 +97,16 @@ __global__ __launch_bounds__(256) void k_swiglu_wave(SwigluJobs j) {
         load_wave_sign<VPL>(g.sv_up_sign, lane, sb);
         load_wave_sign<VPL>(g.su_down_sign, lane, sc);
     }
-    float gv[VPL], uv[VPL];
-    sum_slices<VPL>(g.z_gate + base, g.split_stride, g.splits, lane, gv);
-    sum_slices<VPL>(g.z_up + base, g.split_stride, g.splits, lane, uv);
+    if constexpr (VPL <= 8) {
+        if (at_once) {
+            add_slices<VPL>(lg, g.splits, gv);
+            add_slices<VPL>(lu, g.splits, uv);
+        }
+    }
+    if (!at_once) {
+        sum_slices<VPL>(g.z_gate + base, g.split_stride, g.splits, lane, gv);
+        sum_slices<VPL>(g.z_up + base, g.split_stride, g.splits, lane, uv);
+    }
     wave_hadamard<VPL>(gv, j.scale, lane);
     wave_hadamard<VPL>(uv, j.scale, lane);
 #pragma unroll
@@ -117,11 +135,12 @@ struct CombineArgs {
 };
 
 // One block of nine waves per row: wave r < 8 transforms route r's output,
-// wave 8 the shared expert's; the nine are then added into the row in route
-// order through LDS (src/executor.cpp:1373-1399, 1437-1452).
+// wave 8 the shared expert's, each into its own LDS row; after one barrier
+// every thread adds four columns over the nine rows, in route order and then
+// the shared expert (src/executor.cpp:1373-1399, 1437-1452).
 template <int VPL>
 __global__ __launch_bounds__(576) void k_combine_wave(CombineArgs a) {
-    __shared__ float acc[64 * VPL];
+    extern __shared__ float parts[];  // [9][64 * VPL]
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t n = 64u * VPL;
     const uint32_t b = blockIdx.x;
@@ -152,24 +171,134 @@ __global__ __launch_bounds__(576) void k_combine_wave(CombineArgs a) {
     for (int i = 0; i < VPL; ++i) {
         val[i] = weight * (val[i] * scale[i]);
     }
-    // route order: acc = v0, acc += v1, ..., the last wave adds the shared
-    // expert's and stores the row
-    for (uint32_t r = 0; r < 8; ++r) {
-        if (wave == r) {
+    store_wave<VPL>(parts + wave * n, lane, val);
+    __syncthreads();
+    // acc = v0, acc += v1, ..., acc += v7, then + the shared expert's
+    const float4 *rows = reinterpret_cast<const float4 *>(parts);
+    float4 *row_out = reinterpret_cast<float4 *>(a.out + static_cast<size_t>(b) * n);
+    for (uint32_t c = threadIdx.x; c < n / 4u; c += blockDim.x) {
+        float4 acc = rows[c];
 #pragma unroll
-            for (int i = 0; i < VPL; ++i) {
-                acc[i * 64u + lane] = r == 0 ? val[i] : acc[i * 64u + lane] + val[i];
-            }
+        for (uint32_t r = 1; r < 9; ++r) {
+            const float4 v = rows[r * (n / 4u) + c];
+            acc.x = acc.x + v.x;
+            acc.y = acc.y + v.y;
+            acc.z = acc.z + v.z;
+            acc.w = acc.w + v.w;
+        }
+        row_out[c] = acc;
+    }
+}
+
+template <int VPL>
+void launch_combine(adi_hip_context *ctx, const CombineArgs &c, uint32_t batch) {
+    const size_t lds = size_t(9) * 64u * VPL * sizeof(float);
+    static const bool ready =
+        lds <= 65536 || set_lds_limit(reinterpret_cast<const void *>(&k_combine_wave<VPL>), lds);
+    (void)ready;
+    launch(ctx, "combine", k_combine_wave<VPL>, dim3(batch), dim3(576), lds, c);
+}
+
+// Batch 1: routing and the Hadamard prologues in one launch. Block 0 routes
+// the row as the routing launch does (top_experts, the counting sort and all
+// of its outputs). Every other wave holds one prologue vector. A routed
+// vector's expert is the one at its grouped position, and for one row the
+// grouped order is the ascending order of the eight chosen experts, so the
+// wave recomputes the row's top-8 in registers (the computation of block 0,
+// deterministic) and takes the v-th smallest. The input row is loaded before
+// the top-8, which hides its load.
+template <int SLOTS, int VPL>
+__global__ __launch_bounds__(256) void k_route_prologue(const float *__restrict__ logits,
+                                                        const float *__restrict__ bias,
+                                                        uint32_t *__restrict__ route_expert,
+                                                        float *__restrict__ route_weight,
+                                                        RouteSort a, PrologueJobs j) {
+#pragma clang fp contract(off)
+    __shared__ uint32_t counts[kMaxExperts];
+    __shared__ uint32_t cursor[kMaxExperts];
+    __shared__ uint32_t local_expert[8];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    if (blockIdx.x == 0) {
+        if (wave == 0) {
+            top8_wave<SLOTS>(logits, bias, a.experts, lane, route_expert, route_weight, local_expert);
         }
         __syncthreads();
+        route_sort_block(a, local_expert, counts, cursor);
+        return;
     }
-    if (wave == 8) {
+    uint32_t v = (blockIdx.x - 1u) * 4u + wave;
+    uint32_t s = 0;
+    while (s < j.segments && v >= j.seg[s].count) {
+        v -= j.seg[s].count;
+        ++s;
+    }
+    if (s >= j.segments) {
+        return;
+    }
+    const PrologueSegment &g = j.seg[s];
+    float val[VPL], su[VPL];
+    load_wave<VPL>(g.x, lane, val);  // one row: every vector's source row is 0
+    if (g.matrix_index != nullptr) {
+        uint32_t chosen[8];
+        top8_wave<SLOTS>(logits, bias, a.experts, lane, nullptr, nullptr, nullptr, chosen);
+        uint32_t expert = 0;
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            val[i] = acc[i * 64u + lane] + val[i];
+        for (int k = 0; k < 8; ++k) {
+            uint32_t rank = 0;
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                rank += chosen[m] < chosen[k] ? 1u : 0u;
+            }
+            expert = rank == v ? chosen[k] : expert;
         }
-        store_wave<VPL>(a.out + static_cast<size_t>(b) * n, lane, val);
+        load_wave_f16<VPL>(g.su_f16 + static_cast<size_t>(expert) * g.su_stride, lane, su);
+    } else if (g.su_f16 != nullptr) {
+        load_wave_f16<VPL>(g.su_f16, lane, su);
+    } else {
+        load_wave_sign<VPL>(g.su_sign, lane, su);
     }
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        val[i] = val[i] * su[i];
+    }
+    wave_hadamard<VPL>(val, j.scale, lane);
+    store_xhat<VPL>(g.out, v, lane, val);
+}
+
+// The fused batch-1 launch for widths of 256..2048 and up to 256 experts;
+// false when the shape is outside that range.
+template <int SLOTS>
+bool launch_route_prologue_slots(adi_hip_context *ctx, const float *logits, const float *bias,
+                                 uint32_t *route_expert, float *route_weight, const RouteSort &a,
+                                 PrologueJobs &j, dim3 grid) {
+    switch (j.n) {
+    case 256: launch(ctx, "route_prologue", k_route_prologue<SLOTS, 4>, grid, dim3(256), 0, logits, bias, route_expert, route_weight, a, j); return true;
+    case 512: launch(ctx, "route_prologue", k_route_prologue<SLOTS, 8>, grid, dim3(256), 0, logits, bias, route_expert, route_weight, a, j); return true;
+    case 1024: launch(ctx, "route_prologue", k_route_prologue<SLOTS, 16>, grid, dim3(256), 0, logits, bias, route_expert, route_weight, a, j); return true;
+    case 2048: launch(ctx, "route_prologue", k_route_prologue<SLOTS, 32>, grid, dim3(256), 0, logits, bias, route_expert, route_weight, a, j); return true;
+    default: return false;
+    }
+}
+
+bool launch_route_prologue(adi_hip_context *ctx, const float *logits, const float *bias,
+                           uint32_t *route_expert, float *route_weight, const RouteSort &a,
+                           PrologueJobs &j) {
+    if (j.n < 256 || j.n > 2048 || a.experts > 256 || a.positions != 8) {
+        return false;
+    }
+    uint32_t vectors = 0;
+    for (uint32_t s = 0; s < j.segments; ++s) {
+        vectors += j.seg[s].count;
+    }
+    prepare_prologues(j);
+    const dim3 grid(1u + ceil_div(vectors, 4u));
+    if (a.experts <= 64) {
+        return launch_route_prologue_slots<1>(ctx, logits, bias, route_expert, route_weight, a, j, grid);
+    }
+    if (a.experts <= 128) {
+        return launch_route_prologue_slots<2>(ctx, logits, bias, route_expert, route_weight, a, j, grid);
+    }
+    return launch_route_prologue_slots<4>(ctx, logits, bias, route_expert, route_weight, a, j, grid);
 }
 
 // One block per vector v of the intermediate width I.
@@ -403,7 +532,6 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         sort.slot_info = slot_info;
         sort.position_rank = position_rank;
         sort.chunk_hist = chunk_hist;
-        launch_route(ctx, logits, logit_bias, batch, route_expert, route_weight, sort);
 
         // 3: prologues, routed gate/up and shared gate/up
         PrologueJobs pro{};
@@ -417,7 +545,12 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
                                      xhat(sxh_gate, B, H, 1), batch};
         pro.seg[3] = PrologueSegment{inputs, nullptr, nullptr, nullptr, L->shared_up.su, 0,
                                      xhat(sxh_up, B, H, 1), batch};
-        launch_prologues(ctx, pro);
+        // one row on the decode-GEMV path: routing and prologues in one launch
+        if (!(batch == 1 && !mfma && wave_path &&
+              launch_route_prologue(ctx, logits, logit_bias, route_expert, route_weight, sort, pro))) {
+            launch_route(ctx, logits, logit_bias, batch, route_expert, route_weight, sort);
+            launch_prologues(ctx, pro);
+        }
 
         const size_t gu_words = size_t(I / kTile) * (H / kTile) * kExpertWords;
         const size_t d_words = size_t(H / kTile) * (I / kTile) * kExpertWords;
@@ -633,13 +766,13 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
                           route_to_grouped, sz_down, ssd, B * H, L->shared_down.sv, shared_logit,
                           hadamard_scale(H), outputs};
             switch (H) {
-            case 64: launch(ctx, "combine", k_combine_wave<1>, dim3(batch), dim3(576), 0, c); break;
-            case 128: launch(ctx, "combine", k_combine_wave<2>, dim3(batch), dim3(576), 0, c); break;
-            case 256: launch(ctx, "combine", k_combine_wave<4>, dim3(batch), dim3(576), 0, c); break;
-            case 512: launch(ctx, "combine", k_combine_wave<8>, dim3(batch), dim3(576), 0, c); break;
-            case 1024: launch(ctx, "combine", k_combine_wave<16>, dim3(batch), dim3(576), 0, c); break;
-            case 2048: launch(ctx, "combine", k_combine_wave<32>, dim3(batch), dim3(576), 0, c); break;
-            default: launch(ctx, "combine", k_combine_wave<64>, dim3(batch), dim3(576), 0, c); break;
+            case 64: launch_combine<1>(ctx, c, batch); break;
+            case 128: launch_combine<2>(ctx, c, batch); break;
+            case 256: launch_combine<4>(ctx, c, batch); break;
+            case 512: launch_combine<8>(ctx, c, batch); break;
+            case 1024: launch_combine<16>(ctx, c, batch); break;
+            case 2048: launch_combine<32>(ctx, c, batch); break;
+            default: launch_combine<64>(ctx, c, batch); break;
             }
         } else {
             launch(ctx, "combine", k_combine, dim3(batch), dim3(256), H * sizeof(float),
