@@ -19,10 +19,11 @@ __device__ __forceinline__ float route_order_value(uint32_t ordered) {
 }
 
 // One wave per logit row. Lane l holds experts l, l+64, ...; eight rounds of
-// a wave-wide maximum of the ordered values, each followed by a ballot for the
+// a wave-wide maximum of the ordered values, each followed by ballots for the
 // lowest expert holding it, pick the routes in the order of the comparator of
 // top_experts: larger logit first, lower index on ties (src/executor.cpp:
-// 202-211). The softmax over the eight then runs on lane 0 in the reference's
+// 202-211). Order 0 marks an empty or chosen slot; a live value's order is at
+// least 1 (only the negative NaNs 0xFFFFFFFF and 0xFFFFFFFE share order 1). The softmax over the eight then runs on lane 0 in the reference's
 // order (src/executor.cpp:213-227) when route_expert is set. `chosen` (when
 // set) receives the eight experts in every lane.
 template <int SLOTS>
@@ -42,20 +43,18 @@ __device__ __forceinline__ void top8_wave(const float *__restrict__ row,
         offset[i] = bias != nullptr ? bias[e] : 0.0f;
     }
     uint32_t order[SLOTS];
-    bool alive[SLOTS];
 #pragma unroll
     for (uint32_t i = 0; i < SLOTS; ++i) {
         const float v = bias != nullptr ? value[i] + offset[i] : value[i];
-        alive[i] = lane + 64u * i < experts;
-        order[i] = alive[i] ? route_order(v) : 0u;
+        order[i] = lane + 64u * i < experts ? max(route_order(v), 1u) : 0u;
     }
     float chosen_value[8];
     uint32_t chosen_index[8];
     for (int round = 0; round < 8; ++round) {
-        uint32_t best = 0;
+        uint32_t best = order[0];
 #pragma unroll
-        for (uint32_t i = 0; i < SLOTS; ++i) {
-            best = alive[i] && order[i] > best ? order[i] : best;
+        for (uint32_t i = 1; i < SLOTS; ++i) {
+            best = max(best, order[i]);
         }
         best = max(best, lane_xor_bits<1>(best));
         best = max(best, lane_xor_bits<2>(best));
@@ -64,25 +63,23 @@ __device__ __forceinline__ void top8_wave(const float *__restrict__ row,
         best = max(best, lane_xor_bits<16>(best));
         best = max(best, lane_xor_bits<32>(best));
         best = __builtin_amdgcn_readfirstlane(best);
-        // the lowest live expert holding the maximum: slot i covers experts
-        // 64i .. 64i + 63, so the first slot with a vote decides
-        uint32_t index = 0xFFFFFFFFu;
+        // the lowest expert holding the maximum: slot i covers experts
+        // 64i .. 64i + 63, so the last slot with a vote, counting down, decides
+        uint64_t votes[SLOTS];
 #pragma unroll
         for (uint32_t i = 0; i < SLOTS; ++i) {
-            const uint64_t votes = __ballot(alive[i] && order[i] == best);
-            if (index == 0xFFFFFFFFu && votes != 0ull) {
-                index = 64u * i + static_cast<uint32_t>(__builtin_ctzll(votes));
-            }
+            votes[i] = __ballot(order[i] == best);
+        }
+        uint32_t index = 0u;
+#pragma unroll
+        for (int i = SLOTS - 1; i >= 0; --i) {
+            index = votes[i] != 0ull ? 64u * i + static_cast<uint32_t>(__builtin_ctzll(votes[i])) : index;
         }
         chosen_value[round] = route_order_value(best);
         chosen_index[round] = index;
-        if (index % 64u == lane) {
 #pragma unroll
-            for (uint32_t i = 0; i < SLOTS; ++i) {
-                if (i == index / 64u) {
-                    alive[i] = false;
-                }
-            }
+        for (uint32_t i = 0; i < SLOTS; ++i) {
+            order[i] = lane + 64u * i == index ? 0u : order[i];
         }
     }
     if (chosen != nullptr) {
