@@ -71,6 +71,9 @@ struct adi_hip_context {
     int cu_count = 256;
     std::string last_error;
     adi_hip::Workspace workspace;
+    // scratch of the layer-level entries (attention), kept apart from
+    // `workspace`, which every projection entry they call resets
+    adi_hip::Workspace layer_workspace;
     bool profiling = false;
     std::vector<adi_hip::KernelStat> stats;
 };

@@ -67,6 +67,17 @@ class MoeLayer(C.Structure):
                 ("shared_gate", NeMatrix), ("shared_up", NeMatrix), ("shared_down", NeMatrix)]
 
 
+class FullAttentionStruct(C.Structure):
+    _fields_ = [("query", NeMatrix), ("key", NeMatrix), ("value", NeMatrix), ("output", NeMatrix),
+                ("query_norm", C.c_void_p), ("key_norm", C.c_void_p)]
+
+
+class LinearAttentionStruct(C.Structure):
+    _fields_ = [("qkv", NeMatrix), ("gate", NeMatrix), ("output", NeMatrix),
+                ("alpha", Bf16Matrix), ("beta", Bf16Matrix), ("convolution", C.c_void_p),
+                ("alpha_bias", C.c_void_p), ("a_log", C.c_void_p), ("norm", C.c_void_p)]
+
+
 class KernelProfile(C.Structure):
     _fields_ = [("name", C.c_char * 48), ("launches", C.c_uint64), ("total_ms", C.c_double)]
 
@@ -119,6 +130,10 @@ SIGNATURES = [
     ("adi_hip_embedding_rows", C.c_int, [vp, C.POINTER(Embedding), vp, u32, vp]),
     ("adi_hip_argmax_rows", C.c_int, [vp, vp, u32, u32, vp]),
     ("adi_hip_sample_rows", C.c_int, [vp, vp, u32, u32, f32, f32, vp, vp]),
+    ("adi_hip_full_attention_forward", C.c_int,
+     [vp, C.POINTER(FullAttentionStruct), u32, vp, vp, vp, vp, u32]),
+    ("adi_hip_linear_attention_forward", C.c_int,
+     [vp, C.POINTER(LinearAttentionStruct), vp, vp, vp, vp]),
     ("adi_hip_profiling_enable", C.c_int, [vp, C.c_int]),
     ("adi_hip_profiling_read", C.c_int, [vp, C.POINTER(KernelProfile), u32, C.POINTER(u32)]),
     # include/adi_hip_gguf.h
@@ -689,3 +704,50 @@ def random_device_moe_layer(ctx: Context, seed: int, hidden: int, expert_hidden:
                  stack(hidden, expert_hidden), expert_book,
                  ne(expert_hidden, hidden), ne(expert_hidden, hidden), ne(hidden, expert_hidden))
     return DeviceMoeLayer(s, tuple(keep), experts, hidden)
+
+
+@dataclass
+class DeviceFullAttention:
+    struct: FullAttentionStruct
+    tensors: tuple
+
+
+@dataclass
+class DeviceLinearAttention:
+    struct: LinearAttentionStruct
+    tensors: tuple
+
+
+def upload_full_attention(ctx: Context, layer, ne_book: int) -> DeviceFullAttention:
+    """layer: adi_amd.synthetic.FullAttention."""
+    mats = [upload_ne(ctx, m, ne_book) for m in (layer.query, layer.key, layer.value, layer.output)]
+    norms = [ctx.to_device(a) for a in (layer.query_norm, layer.key_norm)]
+    s = FullAttentionStruct(*(m.struct for m in mats), *(t.data_ptr() for t in norms))
+    return DeviceFullAttention(s, (mats, norms))
+
+
+def upload_linear_attention(ctx: Context, layer, ne_book: int) -> DeviceLinearAttention:
+    """layer: adi_amd.synthetic.LinearAttention."""
+    mats = [upload_ne(ctx, m, ne_book) for m in (layer.qkv, layer.gate, layer.output)]
+    alpha = ctx.to_device(layer.alpha)
+    beta = ctx.to_device(layer.beta)
+    rest = [ctx.to_device(a) for a in (layer.convolution, layer.alpha_bias, layer.a_log, layer.norm)]
+    s = LinearAttentionStruct(
+        *(m.struct for m in mats),
+        Bf16Matrix(32, layer.hidden, alpha.data_ptr()), Bf16Matrix(32, layer.hidden, beta.data_ptr()),
+        *(t.data_ptr() for t in rest))
+    return DeviceLinearAttention(s, (mats, alpha, beta, rest))
+
+
+def full_attention_forward(ctx: Context, layer: DeviceFullAttention, position: int, x, out,
+                           keys, values, capacity: int) -> None:
+    ctx.check(load().adi_hip_full_attention_forward(
+        ctx.handle, C.byref(layer.struct), position, _addr(x), _addr(out), _addr(keys),
+        _addr(values), capacity))
+
+
+def linear_attention_forward(ctx: Context, layer: DeviceLinearAttention, x, out, convolution,
+                             recurrent) -> None:
+    ctx.check(load().adi_hip_linear_attention_forward(
+        ctx.handle, C.byref(layer.struct), _addr(x), _addr(out), _addr(convolution),
+        _addr(recurrent)))

@@ -230,3 +230,54 @@ def moe_layer(rng, hidden: int = 2048, expert_hidden: int = 512, experts: int = 
     layer.shared_up = ne_matrix(rng, expert_hidden, hidden, ntlut)
     layer.shared_down = ne_matrix(rng, hidden, expert_hidden, ntlut)
     return layer
+
+
+@dataclass
+class FullAttention:
+    """One full-attention layer (adi::FullAttentionDescriptor): 16 query
+    heads and 2 KV heads of 256; query rows hold per head 256 query then 256
+    gate values."""
+    hidden: int
+    query: NeMatrix   # 8192 x hidden
+    key: NeMatrix     # 512 x hidden
+    value: NeMatrix   # 512 x hidden
+    output: NeMatrix  # hidden x 4096
+    query_norm: np.ndarray  # 256 bf16 bits
+    key_norm: np.ndarray
+
+
+@dataclass
+class LinearAttention:
+    """One Gated DeltaNet layer (adi::LinearAttentionDescriptor): 16 key
+    heads and 32 value heads of 128, 8192 qkv channels."""
+    hidden: int
+    qkv: NeMatrix     # 8192 x hidden
+    gate: NeMatrix    # 4096 x hidden
+    output: NeMatrix  # hidden x 4096
+    alpha: np.ndarray        # [32, hidden] bf16 bits
+    beta: np.ndarray         # [32, hidden] bf16 bits
+    convolution: np.ndarray  # [8192 * 4] bf16 bits
+    alpha_bias: np.ndarray   # [32] bf16 bits
+    a_log: np.ndarray        # [32] bf16 bits
+    norm: np.ndarray         # [128] bf16 bits
+
+
+def full_attention(rng, hidden: int, tlut: np.ndarray) -> FullAttention:
+    ne = lambda rows, columns: ne_matrix(rng, rows, columns, tlut)
+    norm = lambda: bf16_bits_rne(rng.normal(0.0, 0.2, 256).astype(np.float32))
+    return FullAttention(hidden, ne(8192, hidden), ne(512, hidden), ne(512, hidden),
+                         ne(hidden, 4096), norm(), norm())
+
+
+def linear_attention(rng, hidden: int, tlut: np.ndarray) -> LinearAttention:
+    """Decay inputs keep exp(-exp(a_log) * softplus(alpha + bias)) inside
+    (0, 1) with both softplus branches reachable (alpha_bias up to ~25)."""
+    ne = lambda rows, columns: ne_matrix(rng, rows, columns, tlut)
+    bf = lambda loc, scale, n: bf16_bits_rne(rng.normal(loc, scale, n).astype(np.float32))
+    alpha_bias = bf(0.0, 1.0, 32)
+    alpha_bias[:2] = bf16_bits_rne(np.array([22.0, 25.0], np.float32))
+    return LinearAttention(
+        hidden, ne(8192, hidden), ne(4096, hidden), ne(hidden, 4096),
+        bf(0.0, 0.02, 32 * hidden).reshape(32, hidden),
+        bf(0.0, 0.02, 32 * hidden).reshape(32, hidden),
+        bf(0.0, 0.5, 8192 * 4), alpha_bias, bf(-1.0, 0.5, 32), bf(1.0, 0.1, 128))

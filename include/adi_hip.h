@@ -321,6 +321,62 @@ int adi_hip_sample_rows(adi_hip_context *ctx, const float *logits, uint32_t rows
                         uint32_t count, float temperature, float top_p,
                         const uint64_t *words, uint32_t *tokens);
 
+/* ---- attention of one decode token (the hybrid model's head geometry) --- */
+
+/* adi::FullAttentionDescriptor (include/adi/model.hpp:39-46): 16 query heads
+ * and 2 KV heads of 256. query rows hold per head 256 query then 256 gate
+ * values (8192 rows); key and value have 512 rows; output has 4096 columns.
+ * The norms are 256 bf16 values in device memory. */
+typedef struct {
+    adi_hip_ne_matrix query;
+    adi_hip_ne_matrix key;
+    adi_hip_ne_matrix value;
+    adi_hip_ne_matrix output;
+    const uint16_t *query_norm;
+    const uint16_t *key_norm;
+} adi_hip_full_attention;
+
+/* full_attention_forward (src/executor.cpp:332-418) for the token at
+ * `position` of one sequence: q/k/v projections, per-head RMS norm with
+ * (1 + w) and partial RoPE on the first 64 dimensions (theta base 1e7,
+ * src/model.cpp:606-615), the new key and value appended to the cache, grouped
+ * online-softmax attention over positions 0..position, the sigmoid output
+ * gate, and the output projection. keys and values are device caches of
+ * `capacity` entries of [2][256] floats; entries below `position` hold the
+ * sequence's history and entry `position` receives this token's. Input and
+ * output have `hidden` (= the projections' columns) floats. */
+int adi_hip_full_attention_forward(adi_hip_context *ctx, const adi_hip_full_attention *layer,
+                                   uint32_t position, const float *input, float *output,
+                                   float *keys, float *values, uint32_t capacity);
+
+/* adi::LinearAttentionDescriptor (include/adi/model.hpp:48-58): Gated
+ * DeltaNet with 16 key heads and 32 value heads of 128. qkv has 8192 rows
+ * (2048 query, 2048 key, 4096 value channels), gate 4096, output 4096
+ * columns; alpha and beta are 32 x hidden bf16; convolution is 8192 x 4 bf16;
+ * alpha_bias and a_log 32 bf16; norm 128 bf16. */
+typedef struct {
+    adi_hip_ne_matrix qkv;
+    adi_hip_ne_matrix gate;
+    adi_hip_ne_matrix output;
+    adi_hip_bf16_matrix alpha;
+    adi_hip_bf16_matrix beta;
+    const uint16_t *convolution;
+    const uint16_t *alpha_bias;
+    const uint16_t *a_log;
+    const uint16_t *norm;
+} adi_hip_linear_attention;
+
+/* linear_attention_forward (src/executor.cpp:420-557) for one token:
+ * projections, the width-4 causal convolution with SiLU, L2-normalised query
+ * and key heads, the gated delta recurrence (src/executor.cpp:121-184,
+ * src/simd.cpp:108-127), per-head RMS norm times SiLU(gate), and the output
+ * projection. convolution_state [8192][3] and recurrent_state [32][128][128]
+ * are the sequence's device state, updated in place (all zero for a new
+ * sequence). alpha and beta use the context's bf16 reduction order. */
+int adi_hip_linear_attention_forward(adi_hip_context *ctx, const adi_hip_linear_attention *layer,
+                                     const float *input, float *output, float *convolution_state,
+                                     float *recurrent_state);
+
 /* ---- kernel profiling ----------------------------------------------------- */
 
 /* Per-kernel timing with HIP events on the context stream, the counterpart

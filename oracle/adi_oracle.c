@@ -1106,3 +1106,268 @@ done:
     free(table);
     return status;
 }
+
+/* ---- attention of one decode token ----------------------------------------- */
+
+/* src/executor.cpp:25-41 */
+int ao_normalize_head(float *values, const uint16_t *weights, uint32_t count, float epsilon) {
+    if (!values || !weights || count == 0) {
+        return AO_INVALID_ARGUMENT;
+    }
+    float squares = 0.0f;
+    for (uint32_t i = 0; i < count; ++i) {
+        squares += values[i] * values[i];
+    }
+    const float scale = 1.0f / sqrtf(squares / (float)count + epsilon);
+    for (uint32_t i = 0; i < count; ++i) {
+        values[i] *= scale * (1.0f + ao_bf16_to_f32(weights[i]));
+    }
+    return AO_OK;
+}
+
+/* src/executor.cpp:43-58, src/model.cpp:606-615 */
+void ao_rope_table(uint32_t position, float *cosine, float *sine) {
+    for (uint32_t i = 0; i < 32; ++i) {
+        const float divisor = powf(10000000.0f, 2.0f * (float)i / 64.0f);
+        const float theta = (float)position / divisor;
+        cosine[i] = cosf(theta);
+        sine[i] = sinf(theta);
+    }
+}
+
+/* src/executor.cpp:60-72 */
+void ao_apply_rope(float *values, const float *cosine, const float *sine) {
+    for (uint32_t i = 0; i < 32; ++i) {
+        const float first = values[i];
+        const float second = values[i + 32];
+        values[i] = first * cosine[i] - second * sine[i];
+        values[i + 32] = second * cosine[i] + first * sine[i];
+    }
+}
+
+/* update_online_softmax (src/attention.cpp:15-35) */
+static void online_softmax_step(float score, const float *value, uint32_t count,
+                                float *maximum, float *denominator, float *attended) {
+    if (score <= *maximum) {
+        const float weight = expf(score - *maximum);
+        *denominator += weight;
+        for (uint32_t i = 0; i < count; ++i) {
+            attended[i] += value[i] * weight;
+        }
+        return;
+    }
+    const float previous_scale = expf(*maximum - score);
+    *denominator = *denominator * previous_scale + 1.0f;
+    for (uint32_t i = 0; i < count; ++i) {
+        attended[i] = attended[i] * previous_scale + value[i];
+    }
+    *maximum = score;
+}
+
+/* src/attention.cpp:38-229: per query head, tokens in order, then * 1/den */
+int ao_grouped_attention(const float *queries, const float *keys, const float *values,
+                         uint32_t tokens, uint32_t query_heads, uint32_t kv_heads,
+                         uint32_t head_size, uint32_t query_stride, float *output) {
+    if (!queries || !keys || !values || !output || tokens == 0 || kv_heads == 0 ||
+        head_size == 0 || query_heads % kv_heads != 0 || query_stride < head_size) {
+        return AO_INVALID_ARGUMENT;
+    }
+    const uint32_t group = query_heads / kv_heads;
+    const float score_scale = 1.0f / sqrtf((float)head_size);
+    for (uint32_t h = 0; h < query_heads; ++h) {
+        const uint32_t kv = h / group;
+        const float *q = queries + (size_t)h * query_stride;
+        float *attended = output + (size_t)h * head_size;
+        memset(attended, 0, head_size * sizeof(float));
+        float maximum = -INFINITY, denominator = 0.0f;
+        for (uint32_t t = 0; t < tokens; ++t) {
+            const size_t at = ((size_t)t * kv_heads + kv) * head_size;
+            float dot = 0.0f;
+            for (uint32_t i = 0; i < head_size; ++i) {
+                dot += q[i] * keys[at + i];
+            }
+            online_softmax_step(dot * score_scale, values + at, head_size, &maximum, &denominator,
+                                attended);
+        }
+        const float inverse = 1.0f / denominator;
+        for (uint32_t i = 0; i < head_size; ++i) {
+            attended[i] *= inverse;
+        }
+    }
+    return AO_OK;
+}
+
+/* src/kernels.cpp:1075-1087 */
+int ao_l2_normalize(float *values, uint32_t count, float epsilon) {
+    if (!values || count == 0 || epsilon < 0.0f) {
+        return AO_INVALID_ARGUMENT;
+    }
+    float squares = 0.0f;
+    for (uint32_t i = 0; i < count; ++i) {
+        squares += values[i] * values[i];
+    }
+    const float scale = 1.0f / sqrtf(squares + epsilon);
+    for (uint32_t i = 0; i < count; ++i) {
+        values[i] *= scale;
+    }
+    return AO_OK;
+}
+
+/* src/simd.cpp:108-127 */
+float ao_gated_delta_update(float *state, const float *query, const float *key, float value,
+                            float beta, float decay, uint32_t count) {
+    float prediction = 0.0f;
+    for (uint32_t i = 0; i < count; ++i) {
+        state[i] *= decay;
+        prediction += state[i] * key[i];
+    }
+    const float delta = (value - prediction) * beta;
+    float attended = 0.0f;
+    for (uint32_t i = 0; i < count; ++i) {
+        state[i] += key[i] * delta;
+        attended += state[i] * query[i];
+    }
+    return attended;
+}
+
+/* src/executor.cpp:332-418 */
+int ao_full_attention_forward(const ao_full_attention *L, uint32_t position,
+                              const float *input, float *output, float *keys, float *values) {
+    enum { query_heads = 16, kv_heads = 2, head_size = 256, stride = 512 };
+    const float epsilon = 1.0e-6f;
+    if (!L || !input || !output || !keys || !values || L->query.rows != query_heads * stride ||
+        L->key.rows != kv_heads * head_size || L->value.rows != kv_heads * head_size ||
+        L->output.columns != query_heads * head_size || !L->query_norm || !L->key_norm) {
+        return AO_INVALID_ARGUMENT;
+    }
+    float *query_gate = malloc(sizeof(float) * query_heads * stride);
+    float *attended = malloc(sizeof(float) * query_heads * head_size);
+    float *key = keys + (size_t)position * kv_heads * head_size;
+    float *value = values + (size_t)position * kv_heads * head_size;
+    int rc = query_gate && attended ? AO_OK : AO_INVALID_ARGUMENT;
+    if (rc == AO_OK) {
+        rc = ao_ne_matmul(&L->query, input, 1, query_gate);
+    }
+    if (rc == AO_OK) {
+        rc = ao_ne_matmul(&L->key, input, 1, key);
+    }
+    if (rc == AO_OK) {
+        rc = ao_ne_matmul(&L->value, input, 1, value);
+    }
+    if (rc == AO_OK) {
+        float cosine[32], sine[32];
+        ao_rope_table(position, cosine, sine);
+        for (uint32_t h = 0; h < query_heads; ++h) {
+            ao_normalize_head(query_gate + (size_t)h * stride, L->query_norm, head_size, epsilon);
+            ao_apply_rope(query_gate + (size_t)h * stride, cosine, sine);
+        }
+        for (uint32_t h = 0; h < kv_heads; ++h) {
+            ao_normalize_head(key + (size_t)h * head_size, L->key_norm, head_size, epsilon);
+            ao_apply_rope(key + (size_t)h * head_size, cosine, sine);
+        }
+        rc = ao_grouped_attention(query_gate, keys, values, position + 1, query_heads, kv_heads,
+                                  head_size, stride, attended);
+    }
+    if (rc == AO_OK) {
+        for (uint32_t h = 0; h < query_heads; ++h) {
+            for (uint32_t i = 0; i < head_size; ++i) {
+                attended[h * head_size + i] *=
+                    ao_sigmoid(query_gate[(size_t)h * stride + head_size + i]);
+            }
+        }
+        rc = ao_ne_matmul(&L->output, attended, 1, output);
+    }
+    free(query_gate);
+    free(attended);
+    return rc;
+}
+
+/* src/executor.cpp:420-557, with gated_delta_recurrent (157-184) and
+ * gated_delta_head (121-155) */
+int ao_linear_attention_forward(const ao_linear_attention *L, const float *input,
+                                float *output, float *convolution, float *recurrent,
+                                uint32_t lanes) {
+    enum { key_heads = 16, value_heads = 32, head_size = 128, qk_size = key_heads * head_size,
+           value_size = value_heads * head_size, channels = 2 * qk_size + value_size };
+    const float epsilon = 1.0e-6f;
+    if (!L || !input || !output || !convolution || !recurrent || L->qkv.rows != channels ||
+        L->gate.rows != value_size || L->output.columns != value_size ||
+        L->alpha.rows != value_heads || L->beta.rows != value_heads || !L->convolution ||
+        !L->alpha_bias || !L->a_log || !L->norm) {
+        return AO_INVALID_ARGUMENT;
+    }
+    float *qkv = malloc(sizeof(float) * channels);
+    float *gate = malloc(sizeof(float) * value_size);
+    float *convolved = malloc(sizeof(float) * channels);
+    float *recurrent_output = malloc(sizeof(float) * value_size);
+    float *normalized = malloc(sizeof(float) * value_size);
+    float alpha[value_heads], beta[value_heads];
+    int rc = qkv && gate && convolved && recurrent_output && normalized ? AO_OK
+                                                                       : AO_INVALID_ARGUMENT;
+    if (rc == AO_OK) {
+        rc = ao_ne_matmul(&L->qkv, input, 1, qkv);
+    }
+    if (rc == AO_OK) {
+        rc = ao_ne_matmul(&L->gate, input, 1, gate);
+    }
+    if (rc == AO_OK) {
+        rc = ao_bf16_matmul(&L->alpha, input, 1, alpha, lanes);
+    }
+    if (rc == AO_OK) {
+        rc = ao_bf16_matmul(&L->beta, input, 1, beta, lanes);
+    }
+    if (rc == AO_OK) {
+        for (uint32_t c = 0; c < channels; ++c) {
+            float *history = convolution + (size_t)c * 3;
+            const uint16_t *w = L->convolution + (size_t)c * 4;
+            float v = 0.0f;
+            for (uint32_t i = 0; i < 3; ++i) {
+                v += history[i] * ao_bf16_to_f32(w[i]);
+            }
+            v += qkv[c] * ao_bf16_to_f32(w[3]);
+            convolved[c] = ao_silu(v);
+            history[0] = history[1];
+            history[1] = history[2];
+            history[2] = qkv[c];
+        }
+        for (uint32_t h = 0; h < key_heads; ++h) {
+            ao_l2_normalize(convolved + (size_t)h * head_size, head_size, epsilon);
+            ao_l2_normalize(convolved + qk_size + (size_t)h * head_size, head_size, epsilon);
+        }
+        const float output_scale = 1.0f / sqrtf((float)head_size);
+        const float *query = convolved, *key = convolved + qk_size, *value = convolved + 2 * qk_size;
+        for (uint32_t h = 0; h < value_heads; ++h) {
+            const uint32_t kh = h / (value_heads / key_heads);
+            const float *q = query + (size_t)kh * head_size;
+            const float *k = key + (size_t)kh * head_size;
+            const float *v = value + (size_t)h * head_size;
+            const float beta_value = ao_sigmoid(beta[h]);
+            const float biased = alpha[h] + ao_bf16_to_f32(L->alpha_bias[h]);
+            const float softplus = biased > 20.0f ? biased : log1pf(expf(biased));
+            const float decay = expf(-expf(ao_bf16_to_f32(L->a_log[h])) * softplus);
+            for (uint32_t r = 0; r < head_size; ++r) {
+                float *row = recurrent + ((size_t)h * head_size + r) * head_size;
+                recurrent_output[(size_t)h * head_size + r] =
+                    ao_gated_delta_update(row, q, k, v[r], beta_value, decay, head_size) *
+                    output_scale;
+            }
+        }
+        for (uint32_t h = 0; h < value_heads && rc == AO_OK; ++h) {
+            float *dst = normalized + (size_t)h * head_size;
+            rc = ao_rms_norm(recurrent_output + (size_t)h * head_size, L->norm, head_size, 0.0f,
+                             epsilon, dst);
+            for (uint32_t i = 0; i < head_size; ++i) {
+                dst[i] *= ao_silu(gate[(size_t)h * head_size + i]);
+            }
+        }
+    }
+    if (rc == AO_OK) {
+        rc = ao_ne_matmul(&L->output, normalized, 1, output);
+    }
+    free(qkv);
+    free(gate);
+    free(convolved);
+    free(recurrent_output);
+    free(normalized);
+    return rc;
+}

@@ -194,6 +194,74 @@ uint32_t ao_argmax(const float *logits, uint32_t count);
 int ao_sample_token(const float *logits, uint32_t count, float temperature, float top_p,
                     uint64_t word, uint32_t *token);
 
+/* ---- attention of one decode token (src/executor.cpp:25-186, 332-557,
+ * src/attention.cpp) -------------------------------------------------------- */
+
+/* normalize_head (src/executor.cpp:25-41): values[i] *= scale * (1 + w[i]),
+ * scale = 1 / sqrt(sum(v^2) / count + epsilon). */
+int ao_normalize_head(float *values, const uint16_t *weights, uint32_t count, float epsilon);
+
+/* prepare_rope (src/executor.cpp:43-58) with MachModel's divisors
+ * (src/model.cpp:606-615): divisor_i = powf(1e7, 2i / 64), theta = position /
+ * divisor_i, for i < 32. */
+void ao_rope_table(uint32_t position, float *cosine /*32*/, float *sine /*32*/);
+/* apply_rope (src/executor.cpp:60-72): pairs (i, i + 32), i < 32. */
+void ao_apply_rope(float *values, const float *cosine, const float *sine);
+
+/* grouped_query_online_attention (src/attention.cpp:38-229) with a
+ * sequential dot: queries [query_heads][query_stride] (the first head_size
+ * values of each row), keys/values [tokens][kv_heads][head_size], output
+ * [query_heads][head_size]. */
+int ao_grouped_attention(const float *queries, const float *keys, const float *values,
+                         uint32_t tokens, uint32_t query_heads, uint32_t kv_heads,
+                         uint32_t head_size, uint32_t query_stride, float *output);
+
+/* l2_normalize (src/kernels.cpp:1075-1087). */
+int ao_l2_normalize(float *values, uint32_t count, float epsilon);
+
+/* The scalar gated_delta_update (src/simd.cpp:108-127): one state row. */
+float ao_gated_delta_update(float *state, const float *query, const float *key, float value,
+                            float beta, float decay, uint32_t count);
+
+/* Full attention layer weights (adi::FullAttentionDescriptor,
+ * include/adi/model.hpp:39-46): 16 query heads and 2 KV heads of 256. */
+typedef struct {
+    ao_ne_matrix query;         /* 8192 x hidden: per head 256 query, 256 gate */
+    ao_ne_matrix key;           /* 512 x hidden */
+    ao_ne_matrix value;         /* 512 x hidden */
+    ao_ne_matrix output;        /* hidden x 4096 */
+    const uint16_t *query_norm; /* 256 bf16 */
+    const uint16_t *key_norm;   /* 256 bf16 */
+} ao_full_attention;
+
+/* full_attention_forward (src/executor.cpp:332-418) for the token at
+ * `position`: keys and values hold `position` earlier entries of [2][256]
+ * and receive this token's at index `position`. */
+int ao_full_attention_forward(const ao_full_attention *layer, uint32_t position,
+                              const float *input, float *output, float *keys, float *values);
+
+/* Linear attention layer weights (adi::LinearAttentionDescriptor,
+ * include/adi/model.hpp:48-58): Gated DeltaNet, 16 key heads and 32 value
+ * heads of 128, a width-4 causal convolution over the 8192 qkv channels. */
+typedef struct {
+    ao_ne_matrix qkv;            /* 8192 x hidden */
+    ao_ne_matrix gate;           /* 4096 x hidden */
+    ao_ne_matrix output;         /* hidden x 4096 */
+    ao_bf16_matrix alpha;        /* 32 x hidden */
+    ao_bf16_matrix beta;         /* 32 x hidden */
+    const uint16_t *convolution; /* 8192 x 4 bf16 */
+    const uint16_t *alpha_bias;  /* 32 bf16 */
+    const uint16_t *a_log;       /* 32 bf16 */
+    const uint16_t *norm;        /* 128 bf16 */
+} ao_linear_attention;
+
+/* linear_attention_forward (src/executor.cpp:420-557): convolution [8192][3]
+ * and recurrent [32][128][128] are the layer's state, updated in place (zero
+ * for a new sequence). `lanes` is the bf16 dot order of alpha and beta. */
+int ao_linear_attention_forward(const ao_linear_attention *layer, const float *input,
+                                float *output, float *convolution, float *recurrent,
+                                uint32_t lanes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,6 +70,18 @@ class MoeLayer(C.Structure):
     ]
 
 
+class FullAttention(C.Structure):
+    _fields_ = [("query", NeMatrix), ("key", NeMatrix), ("value", NeMatrix), ("output", NeMatrix),
+                ("query_norm", C.POINTER(C.c_uint16)), ("key_norm", C.POINTER(C.c_uint16))]
+
+
+class LinearAttention(C.Structure):
+    _fields_ = [("qkv", NeMatrix), ("gate", NeMatrix), ("output", NeMatrix),
+                ("alpha", Bf16Matrix), ("beta", Bf16Matrix),
+                ("convolution", C.POINTER(C.c_uint16)), ("alpha_bias", C.POINTER(C.c_uint16)),
+                ("a_log", C.POINTER(C.c_uint16)), ("norm", C.POINTER(C.c_uint16))]
+
+
 def ptr(array: Optional[np.ndarray], ctype):
     if array is None:
         return C.cast(None, C.POINTER(ctype))
@@ -122,6 +134,18 @@ def load_oracle() -> C.CDLL:
     _declare(lib, "ao_embedding_row", C.c_int, C.POINTER(Embedding), C.c_uint32, f32p)
     _declare(lib, "ao_argmax", C.c_uint32, f32p, C.c_uint32)
     _declare(lib, "ao_sample_token", C.c_int, f32p, C.c_uint32, C.c_float, C.c_float, C.c_uint64, u32p)
+    _declare(lib, "ao_normalize_head", C.c_int, f32p, u16p, C.c_uint32, C.c_float)
+    _declare(lib, "ao_rope_table", None, C.c_uint32, f32p, f32p)
+    _declare(lib, "ao_apply_rope", None, f32p, f32p, f32p)
+    _declare(lib, "ao_grouped_attention", C.c_int, f32p, f32p, f32p, C.c_uint32, C.c_uint32,
+             C.c_uint32, C.c_uint32, C.c_uint32, f32p)
+    _declare(lib, "ao_l2_normalize", C.c_int, f32p, C.c_uint32, C.c_float)
+    _declare(lib, "ao_gated_delta_update", C.c_float, f32p, f32p, f32p, C.c_float, C.c_float,
+             C.c_float, C.c_uint32)
+    _declare(lib, "ao_full_attention_forward", C.c_int, C.POINTER(FullAttention), C.c_uint32,
+             f32p, f32p, f32p, f32p)
+    _declare(lib, "ao_linear_attention_forward", C.c_int, C.POINTER(LinearAttention), f32p, f32p,
+             f32p, f32p, C.c_uint32)
     return lib
 
 
@@ -164,6 +188,11 @@ def load_ref() -> C.CDLL:
              C.POINTER(C.c_uint64), u32p)
     _declare(lib, "ref_gguf_summary", C.c_int, C.c_char_p, C.POINTER(C.c_uint64),
              C.POINTER(C.c_uint64), C.POINTER(C.c_uint64))
+    _declare(lib, "ref_grouped_attention", C.c_int, f32p, f32p, f32p, C.c_uint32, C.c_uint32,
+             C.c_uint32, C.c_uint32, C.c_uint32, f32p)
+    _declare(lib, "ref_gated_delta_update", C.c_float, f32p, f32p, f32p, C.c_float, C.c_float,
+             C.c_float, C.c_uint32)
+    _declare(lib, "ref_l2_normalize", C.c_int, f32p, C.c_uint32, C.c_float)
     return lib
 
 
@@ -393,3 +422,62 @@ class RefMoeLayer:
 
     def __del__(self):
         self.close()
+
+
+# ---- attention of one decode token -----------------------------------------
+
+class FullAttentionStruct:
+    """Holds an ao_full_attention over a synthetic.FullAttention."""
+
+    def __init__(self, layer):
+        self.layer = layer
+        self.struct = FullAttention(ne_struct(layer.query), ne_struct(layer.key),
+                                    ne_struct(layer.value), ne_struct(layer.output),
+                                    ptr(layer.query_norm, C.c_uint16), ptr(layer.key_norm, C.c_uint16))
+
+
+class LinearAttentionStruct:
+    """Holds an ao_linear_attention over a synthetic.LinearAttention."""
+
+    def __init__(self, layer):
+        self.layer = layer
+        self.struct = LinearAttention(
+            ne_struct(layer.qkv), ne_struct(layer.gate), ne_struct(layer.output),
+            bf16_struct(layer.alpha), bf16_struct(layer.beta),
+            ptr(layer.convolution, C.c_uint16), ptr(layer.alpha_bias, C.c_uint16),
+            ptr(layer.a_log, C.c_uint16), ptr(layer.norm, C.c_uint16))
+
+
+def full_attention_forward(lib, held: FullAttentionStruct, position: int, x: np.ndarray,
+                           keys: np.ndarray, values: np.ndarray) -> np.ndarray:
+    """keys/values: float32 [capacity, 2, 256], entry `position` is written."""
+    out = np.zeros(held.layer.hidden, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    check(lib.ao_full_attention_forward(C.byref(held.struct), position, ptr(x, C.c_float),
+                                        ptr(out, C.c_float), ptr(keys, C.c_float),
+                                        ptr(values, C.c_float)), "ao_full_attention_forward")
+    return out
+
+
+def linear_attention_forward(lib, held: LinearAttentionStruct, x: np.ndarray,
+                             convolution: np.ndarray, recurrent: np.ndarray,
+                             isa: int = 16) -> np.ndarray:
+    """convolution float32 [8192 * 3], recurrent float32 [32 * 128 * 128],
+    updated in place."""
+    out = np.zeros(held.layer.hidden, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    check(lib.ao_linear_attention_forward(C.byref(held.struct), ptr(x, C.c_float),
+                                          ptr(out, C.c_float), ptr(convolution, C.c_float),
+                                          ptr(recurrent, C.c_float), isa),
+          "ao_linear_attention_forward")
+    return out
+
+
+def grouped_attention(lib, queries, keys, values, tokens, query_heads, kv_heads, head_size,
+                      query_stride, prefix="ao") -> np.ndarray:
+    out = np.zeros(query_heads * head_size, np.float32)
+    q, k, v = (np.ascontiguousarray(a, np.float32) for a in (queries, keys, values))
+    check(getattr(lib, f"{prefix}_grouped_attention")(
+        ptr(q, C.c_float), ptr(k, C.c_float), ptr(v, C.c_float), tokens, query_heads, kv_heads,
+        head_size, query_stride, ptr(out, C.c_float)), f"{prefix}_grouped_attention")
+    return out

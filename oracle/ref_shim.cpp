@@ -18,6 +18,7 @@
 #include "adi/generation.hpp"
 #include "adi/gguf.hpp"
 #include "adi/kernels.hpp"
+#include "attention.hpp"
 #include "codec_cache.hpp"
 #include "expert_trellis.hpp"
 #include "ne_trellis.hpp"
@@ -580,6 +581,32 @@ int ref_moe_forward(void *handle, const float *inputs, std::uint32_t batch,
             }
         }
     });
+}
+
+// detail::grouped_query_online_attention (src/attention.cpp:38-229), heads
+// in one pass (its sequential form).
+int ref_grouped_attention(const float *queries, const float *keys, const float *values,
+                          std::uint32_t tokens, std::uint32_t query_heads,
+                          std::uint32_t kv_heads, std::uint32_t head_size,
+                          std::uint32_t query_stride, float *output) {
+    return guarded([&] {
+        const std::size_t kv = static_cast<std::size_t>(tokens) * kv_heads * head_size;
+        adi::detail::grouped_query_online_attention(
+            {queries, static_cast<std::size_t>(query_heads) * query_stride}, {keys, kv},
+            {values, kv}, query_heads, kv_heads, head_size, query_stride, false,
+            {output, static_cast<std::size_t>(query_heads) * head_size});
+    });
+}
+
+// detail::gated_delta_update (src/simd.cpp) of the selected ISA.
+float ref_gated_delta_update(float *state, const float *query, const float *key, float value,
+                             float beta, float decay, std::uint32_t count) {
+    return adi::detail::gated_delta_update({state, count}, {query, count}, {key, count}, value,
+                                           beta, decay);
+}
+
+int ref_l2_normalize(float *values, std::uint32_t count, float epsilon) {
+    return guarded([&] { adi::l2_normalize({values, count}, epsilon); });
 }
 
 } // extern "C"

@@ -1,0 +1,252 @@
+"""The oracle's attention of one decode token (full GQA attention and Gated
+DeltaNet), pinned before it judges the GPU:
+
+- its pieces against the compiled reference: grouped_query_online_attention
+  (src/attention.cpp) and gated_delta_update (src/simd.cpp) bit-exact at the
+  scalar ISA, within float rounding at the others; l2_normalize bit-exact;
+- closed forms: one history token attends to its own value, equal keys give
+  the mean of the values, RoPE at position 0 is the identity and preserves
+  pair norms, the rope table matches float64 trigonometry, normalize_head
+  matches its float64 formula;
+- the two layer compositions (src/executor.cpp:332-557) against float64
+  numpy restatements that share only the packed projection (itself pinned
+  against the reference elsewhere), over several tokens of state.
+MachModel cannot be built here (it needs the full checkpoint), so the layer
+functions themselves have no compiled counterpart."""
+import numpy as np
+import pytest
+
+import pyoracle as po
+from adi_amd import synthetic as syn
+
+HIDDEN = 256
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def rand(rng, *shape):
+    return rng.normal(0.0, 1.0, shape).astype(np.float32)
+
+
+@pytest.mark.parametrize("tokens", [1, 7, 70])
+def test_grouped_attention_against_reference(oracle, ref, tokens):
+    rng = syn.rng_for(30, tokens)
+    q = rand(rng, 16 * 512)
+    k = rand(rng, tokens * 2 * 256)
+    v = rand(rng, tokens * 2 * 256)
+    args = (q, k, v, tokens, 16, 2, 256, 512)
+    mine = po.grouped_attention(oracle, *args)
+    try:
+        ref.ref_force_isa_lanes(1)
+        assert np.array_equal(bits(mine), bits(po.grouped_attention(ref, *args, prefix="ref")))
+    finally:
+        ref.ref_force_isa_lanes(0)
+    native = po.grouped_attention(ref, *args, prefix="ref")
+    assert np.max(np.abs(native - mine)) <= 1e-5 * np.max(np.abs(mine))
+
+
+def test_gated_delta_update_against_reference(oracle, ref):
+    rng = syn.rng_for(31, 0)
+    for trial in range(20):
+        state = rand(rng, 128)
+        q, k = rand(rng, 128), rand(rng, 128)
+        value, beta, decay = (float(x) for x in rng.uniform(0.0, 1.0, 3))
+        want_state = state.copy()
+        got_state = state.copy()
+        got = oracle.ao_gated_delta_update(po.ptr(got_state, po.C.c_float), po.ptr(q, po.C.c_float),
+                                           po.ptr(k, po.C.c_float), value, beta, decay, 128)
+        try:
+            ref.ref_force_isa_lanes(1)
+            want = ref.ref_gated_delta_update(po.ptr(want_state, po.C.c_float),
+                                              po.ptr(q, po.C.c_float), po.ptr(k, po.C.c_float),
+                                              value, beta, decay, 128)
+        finally:
+            ref.ref_force_isa_lanes(0)
+        assert np.float32(got).view(np.uint32) == np.float32(want).view(np.uint32)
+        assert np.array_equal(bits(got_state), bits(want_state))
+
+
+def test_l2_normalize_against_reference(oracle, ref):
+    rng = syn.rng_for(32, 0)
+    for count in (1, 128, 333):
+        x = rand(rng, count)
+        a, b = x.copy(), x.copy()
+        assert oracle.ao_l2_normalize(po.ptr(a, po.C.c_float), count, 1e-6) == 0
+        assert ref.ref_l2_normalize(po.ptr(b, po.C.c_float), count, 1e-6) == 0
+        assert np.array_equal(bits(a), bits(b))
+
+
+def test_attention_closed_forms(oracle):
+    rng = syn.rng_for(33, 0)
+    q = rand(rng, 16 * 512)
+    # one token: every head attends to its KV head's value, exactly
+    v1 = rand(rng, 2 * 256)
+    out = po.grouped_attention(oracle, q, rand(rng, 2 * 256), v1, 1, 16, 2, 256, 512)
+    for h in range(16):
+        assert np.array_equal(out[h * 256:(h + 1) * 256], v1[(h // 8) * 256:(h // 8 + 1) * 256])
+    # equal keys: the mean of the values
+    tokens = 9
+    k = np.tile(rand(rng, 2 * 256), tokens)
+    v = rand(rng, tokens * 2 * 256)
+    out = po.grouped_attention(oracle, q, k, v, tokens, 16, 2, 256, 512)
+    mean = v.reshape(tokens, 2, 256).astype(np.float64).mean(axis=0)
+    for h in range(16):
+        np.testing.assert_allclose(out[h * 256:(h + 1) * 256], mean[h // 8], rtol=0, atol=1e-5)
+
+
+def rope_table(oracle, position):
+    cos = np.zeros(32, np.float32)
+    sin = np.zeros(32, np.float32)
+    oracle.ao_rope_table(position, po.ptr(cos, po.C.c_float), po.ptr(sin, po.C.c_float))
+    return cos, sin
+
+
+def test_rope(oracle):
+    rng = syn.rng_for(34, 0)
+    cos, sin = rope_table(oracle, 0)
+    x = rand(rng, 256)
+    y = x.copy()
+    oracle.ao_apply_rope(po.ptr(y, po.C.c_float), po.ptr(cos, po.C.c_float), po.ptr(sin, po.C.c_float))
+    assert np.array_equal(y, x)
+    for position in (1, 37, 4095):
+        cos, sin = rope_table(oracle, position)
+        theta = position / (1e7 ** (2.0 * np.arange(32) / 64.0))
+        np.testing.assert_allclose(cos, np.cos(theta), rtol=0, atol=2e-6 * max(1.0, theta.max()))
+        np.testing.assert_allclose(sin, np.sin(theta), rtol=0, atol=2e-6 * max(1.0, theta.max()))
+        y = x.copy()
+        oracle.ao_apply_rope(po.ptr(y, po.C.c_float), po.ptr(cos, po.C.c_float),
+                             po.ptr(sin, po.C.c_float))
+        np.testing.assert_allclose(np.hypot(y[:32], y[32:64]), np.hypot(x[:32], x[32:64]), rtol=1e-6)
+        assert np.array_equal(y[64:], x[64:])
+
+
+def test_normalize_head_formula(oracle):
+    rng = syn.rng_for(35, 0)
+    x = rand(rng, 256)
+    w = syn.bf16_bits_rne(rng.normal(0.0, 0.3, 256).astype(np.float32))
+    y = x.copy()
+    assert oracle.ao_normalize_head(po.ptr(y, po.C.c_float), po.ptr(w, po.C.c_uint16), 256, 1e-6) == 0
+    want = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-6) * \
+        (1.0 + syn.bf16_to_f32(w).astype(np.float64))
+    np.testing.assert_allclose(y, want, rtol=2e-6, atol=1e-7)
+
+
+# ---- the two layers against float64 restatements ---------------------------
+
+def ne(oracle, m, x):
+    return po.ne_matmul(oracle, m, np.asarray(x, np.float32)[None, :])[0].astype(np.float64)
+
+
+def rope64(x, position):
+    theta = position / (1e7 ** (2.0 * np.arange(32) / 64.0))
+    y = x.copy()
+    y[:32] = x[:32] * np.cos(theta) - x[32:64] * np.sin(theta)
+    y[32:64] = x[32:64] * np.cos(theta) + x[:32] * np.sin(theta)
+    return y
+
+
+def full_attention64(oracle, L, x, history):
+    """history: list of (k [2,256], v [2,256]) float64 of earlier tokens;
+    returns the output and this token's (k, v)."""
+    position = len(history)
+    qg = ne(oracle, L.query, x).reshape(16, 512)
+    k = ne(oracle, L.key, x).reshape(2, 256)
+    v = ne(oracle, L.value, x).reshape(2, 256)
+    qn = 1.0 + syn.bf16_to_f32(L.query_norm).astype(np.float64)
+    kn = 1.0 + syn.bf16_to_f32(L.key_norm).astype(np.float64)
+    norm = lambda a, w: a / np.sqrt(np.mean(a * a) + 1e-6) * w
+    q = np.stack([rope64(norm(qg[h, :256], qn), position) for h in range(16)])
+    k = np.stack([rope64(norm(k[h], kn), position) for h in range(2)])
+    keys = np.stack([hk for hk, _ in history] + [k])
+    values = np.stack([hv for _, hv in history] + [v])
+    attended = np.zeros((16, 256))
+    for h in range(16):
+        scores = keys[:, h // 8] @ q[h] / 16.0
+        p = np.exp(scores - scores.max())
+        attended[h] = (p / p.sum()) @ values[:, h // 8]
+        attended[h] *= 1.0 / (1.0 + np.exp(-qg[h, 256:]))
+    return ne(oracle, L.output, attended.reshape(-1)), (k, v)
+
+
+def test_full_attention_composition(oracle):
+    rng = syn.rng_for(36, 0)
+    L = syn.full_attention(rng, HIDDEN, syn.ne_tlut(rng))
+    held = po.FullAttentionStruct(L)
+    capacity = 5
+    keys = np.zeros((capacity, 2, 256), np.float32)
+    values = np.zeros((capacity, 2, 256), np.float32)
+    history = []
+    for position in range(capacity):
+        x = syn.rms_normalized(syn.hidden_states(rng, 1, HIDDEN))[0]
+        got = po.full_attention_forward(oracle, held, position, x, keys, values)
+        want, kv = full_attention64(oracle, L, x, history)
+        history.append(kv)
+        assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want)), position
+        np.testing.assert_allclose(keys[position], kv[0], rtol=0, atol=1e-4 * np.abs(kv[0]).max())
+        np.testing.assert_allclose(values[position], kv[1], rtol=0, atol=1e-6 * np.abs(kv[1]).max())
+
+
+def linear_attention64(oracle, L, x, conv, rec):
+    """conv [8192, 3], rec [32, 128, 128] float64 state, updated in place."""
+    qkv = ne(oracle, L.qkv, x)
+    gate = ne(oracle, L.gate, x)
+    xs = np.asarray(x, np.float64)
+    alpha = syn.bf16_to_f32(L.alpha).astype(np.float64) @ xs
+    beta = syn.bf16_to_f32(L.beta).astype(np.float64) @ xs
+    w = syn.bf16_to_f32(L.convolution).astype(np.float64).reshape(8192, 4)
+    pre = (conv * w[:, :3]).sum(axis=1) + qkv * w[:, 3]
+    y = pre / (1.0 + np.exp(-pre))
+    conv[:, 0], conv[:, 1], conv[:, 2] = conv[:, 1].copy(), conv[:, 2].copy(), qkv
+    q = y[:2048].reshape(16, 128)
+    k = y[2048:4096].reshape(16, 128)
+    v = y[4096:].reshape(32, 128)
+    q = q / np.sqrt((q * q).sum(axis=1, keepdims=True) + 1e-6)
+    k = k / np.sqrt((k * k).sum(axis=1, keepdims=True) + 1e-6)
+    bias = syn.bf16_to_f32(L.alpha_bias).astype(np.float64)
+    a_log = syn.bf16_to_f32(L.a_log).astype(np.float64)
+    out = np.zeros((32, 128))
+    for h in range(32):
+        b = 1.0 / (1.0 + np.exp(-beta[h]))
+        biased = alpha[h] + bias[h]
+        softplus = biased if biased > 20.0 else np.log1p(np.exp(biased))
+        decay = np.exp(-np.exp(a_log[h]) * softplus)
+        kh, qh = k[h // 2], q[h // 2]
+        rec[h] *= decay
+        delta = (v[h] - rec[h] @ kh) * b
+        rec[h] += delta[:, None] * kh[None, :]
+        out[h] = rec[h] @ qh / np.sqrt(128.0)
+    norm = syn.bf16_to_f32(L.norm).astype(np.float64)
+    normalized = out / np.sqrt(np.mean(out * out, axis=1, keepdims=True) + 1e-6) * norm
+    normalized *= (gate / (1.0 + np.exp(-gate))).reshape(32, 128)
+    return ne(oracle, L.output, normalized.reshape(-1))
+
+
+def test_linear_attention_composition(oracle):
+    rng = syn.rng_for(37, 0)
+    L = syn.linear_attention(rng, HIDDEN, syn.ne_tlut(rng))
+    held = po.LinearAttentionStruct(L)
+    conv = np.zeros(8192 * 3, np.float32)
+    rec = np.zeros(32 * 128 * 128, np.float32)
+    conv64 = np.zeros((8192, 3))
+    rec64 = np.zeros((32, 128, 128))
+    for step in range(4):
+        x = syn.rms_normalized(syn.hidden_states(rng, 1, HIDDEN))[0]
+        got = po.linear_attention_forward(oracle, held, x, conv, rec, isa=1)
+        want = linear_attention64(oracle, L, x, conv64, rec64)
+        assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want)), step
+        np.testing.assert_allclose(conv.reshape(8192, 3), conv64, rtol=0,
+                                   atol=1e-6 * np.abs(conv64).max())
+        np.testing.assert_allclose(rec.reshape(32, 128, 128), rec64, rtol=0,
+                                   atol=1e-4 * np.abs(rec64).max())
+
+
+def test_layer_rejections(oracle):
+    rng = syn.rng_for(38, 0)
+    L = syn.full_attention(rng, HIDDEN, syn.ne_tlut(rng))
+    L.key = syn.ne_matrix(rng, 256, HIDDEN, L.query.tlut)  # one KV head short
+    held = po.FullAttentionStruct(L)
+    keys = np.zeros((2, 2, 256), np.float32)
+    with pytest.raises(ValueError):
+        po.full_attention_forward(oracle, held, 0, np.zeros(HIDDEN, np.float32), keys, keys.copy())

@@ -26,6 +26,8 @@ STRUCTS = {
     "adi_hip_embedding": hip.Embedding,
     "adi_hip_gguf_tensor": hip.GgufTensor,
     "adi_hip_moe_geometry": hip.MoeGeometry,
+    "adi_hip_full_attention": hip.FullAttentionStruct,
+    "adi_hip_linear_attention": hip.LinearAttentionStruct,
 }
 
 
