@@ -286,6 +286,15 @@ __global__ __launch_bounds__(kLinearHead) void k_linear_norm_gate(const float *r
     normalized[i] = x * scale * (0.0f + bf16_bits_to_float(norm[threadIdx.x])) * silu_of(gate[i]);
 }
 
+// hidden += branch (the residual adds of decode_layer).
+__global__ __launch_bounds__(256) void k_residual_add(float *hidden, const float *branch,
+                                                      uint32_t count) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) {
+        hidden[i] = hidden[i] + branch[i];
+    }
+}
+
 // prepare_rope (src/executor.cpp:43-58) with MachModel's divisors
 // (src/model.cpp:606-615), on the host with the reference's float libm calls.
 RopeTable rope_table(uint32_t position) {
@@ -409,6 +418,40 @@ int adi_hip_linear_attention_forward(adi_hip_context *ctx, const adi_hip_linear_
                static_cast<const float *>(recurrent_output), L->norm,
                static_cast<const float *>(gate), normalized);
         forward(ctx, adi_hip_ne_matvec(ctx, &L->output, normalized, output));
+    });
+}
+
+int adi_hip_decode_layer(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_t position,
+                         float *hidden, const adi_hip_layer_state *state) {
+    return guarded(ctx, [&] {
+        require(L != nullptr && hidden != nullptr && state != nullptr && L->input_norm != nullptr &&
+                    L->post_attention_norm != nullptr,
+                "decoder layer input is null");
+        const uint32_t n = L->moe.hidden;
+        require(n > 0 && aligned_to(hidden, 16), "decoder hidden row must be 16-byte aligned");
+        auto &ws = ctx->decoder_workspace;
+        ws.used = 0;
+        ws.ensure(Workspace::round(size_t(n) * 4) * 2);
+        float *normalized = ws.take<float>(n);
+        float *branch = ws.take<float>(n);
+        const dim3 grid(ceil_div(n, 256));
+        forward(ctx, adi_hip_rms_norm(ctx, hidden, L->input_norm, n, 1, 1.0f, 1.0e-6f, normalized));
+        if (L->full_attention != 0) {
+            forward(ctx, adi_hip_full_attention_forward(ctx, &L->full, position, normalized, branch,
+                                                        state->keys, state->values,
+                                                        state->capacity));
+        } else {
+            forward(ctx, adi_hip_linear_attention_forward(ctx, &L->linear, normalized, branch,
+                                                          state->convolution, state->recurrent));
+        }
+        launch(ctx, "residual_add", k_residual_add, grid, dim3(256), 0, hidden,
+               static_cast<const float *>(branch), n);
+        forward(ctx, adi_hip_rms_norm(ctx, hidden, L->post_attention_norm, n, 1, 1.0f, 1.0e-6f,
+                                      normalized));
+        forward(ctx, adi_hip_moe_forward(ctx, &L->moe, normalized, 1, nullptr, branch, nullptr,
+                                         nullptr));
+        launch(ctx, "residual_add", k_residual_add, grid, dim3(256), 0, hidden,
+               static_cast<const float *>(branch), n);
     });
 }
 

@@ -140,6 +140,9 @@ void adi_hip_context_destroy(adi_hip_context *ctx) {
             (void)hipEventDestroy(pair.second);
         }
     }
+    if (ctx->decoder_workspace.base != nullptr) {
+        (void)hipFree(ctx->decoder_workspace.base);
+    }
     if (ctx->layer_workspace.base != nullptr) {
         (void)hipFree(ctx->layer_workspace.base);
     }

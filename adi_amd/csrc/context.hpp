@@ -74,6 +74,8 @@ struct adi_hip_context {
     // scratch of the layer-level entries (attention), kept apart from
     // `workspace`, which every projection entry they call resets
     adi_hip::Workspace layer_workspace;
+    // scratch of the decoder-layer entry, which calls the attention entries
+    adi_hip::Workspace decoder_workspace;
     bool profiling = false;
     std::vector<adi_hip::KernelStat> stats;
 };

@@ -78,6 +78,17 @@ class LinearAttentionStruct(C.Structure):
                 ("alpha_bias", C.c_void_p), ("a_log", C.c_void_p), ("norm", C.c_void_p)]
 
 
+class DecoderLayerStruct(C.Structure):
+    _fields_ = [("input_norm", C.c_void_p), ("post_attention_norm", C.c_void_p),
+                ("full_attention", C.c_int), ("full", FullAttentionStruct),
+                ("linear", LinearAttentionStruct), ("moe", MoeLayer)]
+
+
+class LayerState(C.Structure):
+    _fields_ = [("keys", C.c_void_p), ("values", C.c_void_p), ("capacity", C.c_uint32),
+                ("convolution", C.c_void_p), ("recurrent", C.c_void_p)]
+
+
 class KernelProfile(C.Structure):
     _fields_ = [("name", C.c_char * 48), ("launches", C.c_uint64), ("total_ms", C.c_double)]
 
@@ -134,6 +145,8 @@ SIGNATURES = [
      [vp, C.POINTER(FullAttentionStruct), u32, vp, vp, vp, vp, u32]),
     ("adi_hip_linear_attention_forward", C.c_int,
      [vp, C.POINTER(LinearAttentionStruct), vp, vp, vp, vp]),
+    ("adi_hip_decode_layer", C.c_int,
+     [vp, C.POINTER(DecoderLayerStruct), u32, vp, C.POINTER(LayerState)]),
     ("adi_hip_profiling_enable", C.c_int, [vp, C.c_int]),
     ("adi_hip_profiling_read", C.c_int, [vp, C.POINTER(KernelProfile), u32, C.POINTER(u32)]),
     # include/adi_hip_gguf.h
@@ -751,3 +764,40 @@ def linear_attention_forward(ctx: Context, layer: DeviceLinearAttention, x, out,
     ctx.check(load().adi_hip_linear_attention_forward(
         ctx.handle, C.byref(layer.struct), _addr(x), _addr(out), _addr(convolution),
         _addr(recurrent)))
+
+
+@dataclass
+class DeviceDecoderLayer:
+    struct: DecoderLayerStruct
+    tensors: tuple
+
+
+def upload_decoder_layer(ctx: Context, layer, expert_book: int, ne_book: int) -> DeviceDecoderLayer:
+    """layer: adi_amd.synthetic.DecoderLayer."""
+    norms = [ctx.to_device(a) for a in (layer.input_norm, layer.post_attention_norm)]
+    moe = upload_moe_layer(ctx, layer.moe, expert_book, ne_book)
+    full = upload_full_attention(ctx, layer.full, ne_book) if layer.full is not None else None
+    linear = (upload_linear_attention(ctx, layer.linear, ne_book)
+              if layer.linear is not None else None)
+    s = DecoderLayerStruct(norms[0].data_ptr(), norms[1].data_ptr(), int(full is not None),
+                           full.struct if full else FullAttentionStruct(),
+                           linear.struct if linear else LinearAttentionStruct(), moe.struct)
+    return DeviceDecoderLayer(s, (norms, moe, full, linear))
+
+
+def layer_state(full: bool, capacity: int = 0):
+    """Zeroed device state of one layer for a new sequence: the KV cache of
+    a full-attention layer, else the convolution and recurrent state."""
+    import torch
+    if full:
+        keys = torch.zeros((capacity, 2, 256), dtype=torch.float32, device="cuda")
+        values = torch.zeros_like(keys)
+        return LayerState(keys.data_ptr(), values.data_ptr(), capacity, None, None), (keys, values)
+    conv = torch.zeros(8192 * 3, dtype=torch.float32, device="cuda")
+    rec = torch.zeros(32 * 128 * 128, dtype=torch.float32, device="cuda")
+    return LayerState(None, None, 0, conv.data_ptr(), rec.data_ptr()), (conv, rec)
+
+
+def decode_layer(ctx: Context, layer: DeviceDecoderLayer, position: int, hidden, state) -> None:
+    ctx.check(load().adi_hip_decode_layer(ctx.handle, C.byref(layer.struct), position,
+                                          _addr(hidden), C.byref(state)))

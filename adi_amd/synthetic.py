@@ -281,3 +281,24 @@ def linear_attention(rng, hidden: int, tlut: np.ndarray) -> LinearAttention:
         bf(0.0, 0.02, 32 * hidden).reshape(32, hidden),
         bf(0.0, 0.02, 32 * hidden).reshape(32, hidden),
         bf(0.0, 0.5, 8192 * 4), alpha_bias, bf(-1.0, 0.5, 32), bf(1.0, 0.1, 128))
+
+
+@dataclass
+class DecoderLayer:
+    """One decoder layer (adi::LayerDescriptor): two RMS norms, full or
+    linear attention, and the MoE block."""
+    input_norm: np.ndarray           # hidden bf16 bits
+    post_attention_norm: np.ndarray  # hidden bf16 bits
+    full: Optional[FullAttention]
+    linear: Optional[LinearAttention]
+    moe: MoeLayer
+
+
+def decoder_layer(rng, full: bool, hidden: int, expert_hidden: int, experts: int,
+                  etlut: np.ndarray, ntlut: np.ndarray) -> DecoderLayer:
+    norm = lambda: bf16_bits_rne(rng.normal(0.0, 0.1, hidden).astype(np.float32))
+    return DecoderLayer(
+        norm(), norm(),
+        full_attention(rng, hidden, ntlut) if full else None,
+        None if full else linear_attention(rng, hidden, ntlut),
+        moe_layer(rng, hidden, expert_hidden, experts, etlut=etlut, ntlut=ntlut))

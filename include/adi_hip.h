@@ -377,6 +377,40 @@ int adi_hip_linear_attention_forward(adi_hip_context *ctx, const adi_hip_linear_
                                      const float *input, float *output, float *convolution_state,
                                      float *recurrent_state);
 
+/* ---- one decoder layer of a decode step ---------------------------------- */
+
+/* adi::LayerDescriptor (include/adi/model.hpp:60-66): the two RMS norms,
+ * the layer's attention (full or linear) and its MoE block, all in device
+ * memory. */
+typedef struct {
+    const uint16_t *input_norm;          /* hidden bf16 */
+    const uint16_t *post_attention_norm; /* hidden bf16 */
+    int full_attention;                  /* nonzero: `full` is used, else `linear` */
+    adi_hip_full_attention full;
+    adi_hip_linear_attention linear;
+    adi_hip_moe_layer moe;
+} adi_hip_decoder_layer;
+
+/* The layer's share of a sequence's decoder state (adi::DecoderState,
+ * include/adi/executor.hpp:86-90): the KV cache of a full-attention layer
+ * (capacity entries of [2][256] keys and values) or the convolution
+ * [8192][3] and recurrent [32][128][128] state of a linear one. */
+typedef struct {
+    float *keys;
+    float *values;
+    uint32_t capacity;
+    float *convolution;
+    float *recurrent;
+} adi_hip_layer_state;
+
+/* decode_layer (src/executor.cpp:1473-1529) for the token at `position`, in
+ * place on the device row `hidden` (moe.hidden floats): hidden +=
+ * attention(rms_norm(hidden, input_norm)), then hidden +=
+ * moe_forward(rms_norm(hidden, post_attention_norm)), both norms with weight
+ * offset 1 and epsilon 1e-6. */
+int adi_hip_decode_layer(adi_hip_context *ctx, const adi_hip_decoder_layer *layer,
+                         uint32_t position, float *hidden, const adi_hip_layer_state *state);
+
 /* ---- kernel profiling ----------------------------------------------------- */
 
 /* Per-kernel timing with HIP events on the context stream, the counterpart

@@ -1371,3 +1371,42 @@ int ao_linear_attention_forward(const ao_linear_attention *L, const float *input
     free(normalized);
     return rc;
 }
+
+/* src/executor.cpp:1473-1529 */
+int ao_decode_layer(const ao_decoder_layer *L, uint32_t position, float *hidden,
+                    float *keys, float *values, float *convolution, float *recurrent,
+                    uint32_t lanes) {
+    if (!L || !hidden || !L->input_norm || !L->post_attention_norm) {
+        return AO_INVALID_ARGUMENT;
+    }
+    const uint32_t n = L->moe.hidden;
+    float *normalized = malloc(sizeof(float) * n);
+    float *branch = malloc(sizeof(float) * n);
+    int rc = normalized && branch ? AO_OK : AO_INVALID_ARGUMENT;
+    if (rc == AO_OK) {
+        rc = ao_rms_norm(hidden, L->input_norm, n, 1.0f, 1.0e-6f, normalized);
+    }
+    if (rc == AO_OK) {
+        rc = L->full_attention
+                 ? ao_full_attention_forward(&L->full, position, normalized, branch, keys, values)
+                 : ao_linear_attention_forward(&L->linear, normalized, branch, convolution,
+                                               recurrent, lanes);
+    }
+    if (rc == AO_OK) {
+        for (uint32_t i = 0; i < n; ++i) {
+            hidden[i] += branch[i];
+        }
+        rc = ao_rms_norm(hidden, L->post_attention_norm, n, 1.0f, 1.0e-6f, normalized);
+    }
+    if (rc == AO_OK) {
+        rc = ao_moe_forward(&L->moe, normalized, 1, NULL, lanes, branch, NULL, NULL, 1);
+    }
+    if (rc == AO_OK) {
+        for (uint32_t i = 0; i < n; ++i) {
+            hidden[i] += branch[i];
+        }
+    }
+    free(normalized);
+    free(branch);
+    return rc;
+}

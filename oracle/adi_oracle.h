@@ -262,6 +262,24 @@ int ao_linear_attention_forward(const ao_linear_attention *layer, const float *i
                                 float *output, float *convolution, float *recurrent,
                                 uint32_t lanes);
 
+/* One decoder layer (adi::LayerDescriptor, include/adi/model.hpp:60-66). */
+typedef struct {
+    const uint16_t *input_norm;          /* hidden bf16 */
+    const uint16_t *post_attention_norm; /* hidden bf16 */
+    int full_attention;                  /* nonzero: full, else linear */
+    ao_full_attention full;
+    ao_linear_attention linear;
+    ao_moe_layer moe;
+} ao_decoder_layer;
+
+/* decode_layer (src/executor.cpp:1473-1529) for the token at `position`:
+ * hidden += attention(rms_norm(hidden, input_norm, 1, 1e-6)), then hidden +=
+ * moe_forward(rms_norm(hidden, post_attention_norm, 1, 1e-6)). keys/values
+ * (full) or convolution/recurrent (linear) are the layer's state. */
+int ao_decode_layer(const ao_decoder_layer *layer, uint32_t position, float *hidden,
+                    float *keys, float *values, float *convolution, float *recurrent,
+                    uint32_t lanes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -82,6 +82,12 @@ class LinearAttention(C.Structure):
                 ("a_log", C.POINTER(C.c_uint16)), ("norm", C.POINTER(C.c_uint16))]
 
 
+class DecoderLayer(C.Structure):
+    _fields_ = [("input_norm", C.POINTER(C.c_uint16)), ("post_attention_norm", C.POINTER(C.c_uint16)),
+                ("full_attention", C.c_int), ("full", FullAttention), ("linear", LinearAttention),
+                ("moe", MoeLayer)]
+
+
 def ptr(array: Optional[np.ndarray], ctype):
     if array is None:
         return C.cast(None, C.POINTER(ctype))
@@ -146,6 +152,8 @@ def load_oracle() -> C.CDLL:
              f32p, f32p, f32p, f32p)
     _declare(lib, "ao_linear_attention_forward", C.c_int, C.POINTER(LinearAttention), f32p, f32p,
              f32p, f32p, C.c_uint32)
+    _declare(lib, "ao_decode_layer", C.c_int, C.POINTER(DecoderLayer), C.c_uint32, f32p, f32p,
+             f32p, f32p, f32p, C.c_uint32)
     return lib
 
 
@@ -481,3 +489,29 @@ def grouped_attention(lib, queries, keys, values, tokens, query_heads, kv_heads,
         ptr(q, C.c_float), ptr(k, C.c_float), ptr(v, C.c_float), tokens, query_heads, kv_heads,
         head_size, query_stride, ptr(out, C.c_float)), f"{prefix}_grouped_attention")
     return out
+
+
+class DecoderLayerStruct:
+    """Holds an ao_decoder_layer over a synthetic.DecoderLayer and its state
+    (keys/values for full attention, convolution/recurrent for linear)."""
+
+    def __init__(self, layer, capacity: int = 0):
+        self.layer = layer
+        self.moe = MoeLayerStruct(layer.moe)
+        self.full = FullAttentionStruct(layer.full) if layer.full is not None else None
+        self.linear = LinearAttentionStruct(layer.linear) if layer.linear is not None else None
+        self.struct = DecoderLayer(
+            ptr(layer.input_norm, C.c_uint16), ptr(layer.post_attention_norm, C.c_uint16),
+            int(self.full is not None), self.full.struct if self.full else FullAttention(),
+            self.linear.struct if self.linear else LinearAttention(), self.moe.struct)
+        self.keys = np.zeros((max(capacity, 1), 2, 256), np.float32)
+        self.values = np.zeros_like(self.keys)
+        self.convolution = np.zeros(8192 * 3, np.float32)
+        self.recurrent = np.zeros(32 * 128 * 128, np.float32)
+
+    def decode(self, lib, position: int, hidden: np.ndarray, isa: int = 16) -> None:
+        """hidden: float32 row, updated in place."""
+        check(lib.ao_decode_layer(C.byref(self.struct), position, ptr(hidden, C.c_float),
+                                  ptr(self.keys, C.c_float), ptr(self.values, C.c_float),
+                                  ptr(self.convolution, C.c_float),
+                                  ptr(self.recurrent, C.c_float), isa), "ao_decode_layer")

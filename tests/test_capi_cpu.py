@@ -28,6 +28,8 @@ STRUCTS = {
     "adi_hip_moe_geometry": hip.MoeGeometry,
     "adi_hip_full_attention": hip.FullAttentionStruct,
     "adi_hip_linear_attention": hip.LinearAttentionStruct,
+    "adi_hip_decoder_layer": hip.DecoderLayerStruct,
+    "adi_hip_layer_state": hip.LayerState,
 }
 
 
