@@ -453,6 +453,36 @@ __device__ __forceinline__ void sum_slices(const float *src, size_t stride, uint
     }
 }
 
+// sum_slices with up to `G` slices of loads in flight per round, G * VPL
+// at most 256 registers (for kernels that may hold that many): the same
+// slice-order sum, fewer dependent rounds of memory latency.
+template <int VPL>
+__device__ __forceinline__ void sum_slices_deep(const float *src, size_t stride, uint32_t splits,
+                                                uint32_t lane, float (&v)[VPL]) {
+#pragma clang fp contract(off)
+    constexpr uint32_t G = VPL >= 64 ? 4u : 8u;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        v[i] = 0.0f;
+    }
+    for (uint32_t s0 = 0; s0 < splits; s0 += G) {
+        float a[G][VPL];
+#pragma unroll
+        for (uint32_t g = 0; g < G; ++g) {
+            // a slice past the end reloads the last one and is not added
+            const uint32_t s = s0 + g < splits ? s0 + g : splits - 1u;
+            load_wave<VPL>(src + s * stride, lane, a[g]);
+        }
+#pragma unroll
+        for (uint32_t g = 0; g < G; ++g) {
+#pragma unroll
+            for (int i = 0; i < VPL; ++i) {
+                v[i] = s0 + g < splits ? v[i] + a[g][i] : v[i];
+            }
+        }
+    }
+}
+
 // Destination of a Hadamard-transformed input vector x_hat:
 //   planes 0: fp32 [vectors][n] (decode-GEMV);
 //   planes 1: f16 hi/lo pairs [vectors][n] (MFMA GEMM of an NE matrix);

@@ -235,9 +235,10 @@ __global__ __launch_bounds__(256) void k_prologue_wave(PrologueJobs j) {
     prologue_vector<VPL>(j, blockIdx.x * 4u + (threadIdx.x >> 6), threadIdx.x & 63u);
 }
 
-// y = sv * H_n(sum over splits of z), one wave per vector.
+// y = sv * H_n(sum over splits of z), one wave per vector (the slices' loads
+// go out up to eight at a time, so the kernel may hold up to 256 registers).
 template <int VPL, typename Scale>
-__global__ __launch_bounds__(256) void k_epilogue_wave(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_epilogue_wave(
     const float *__restrict__ z, uint32_t splits, size_t split_stride, const Scale *__restrict__ sv,
     uint32_t vectors, float scale, float *__restrict__ out) {
 #pragma clang fp contract(off)
@@ -254,13 +255,96 @@ __global__ __launch_bounds__(256) void k_epilogue_wave(
     } else {
         load_wave_sign<VPL>(reinterpret_cast<const int8_t *>(sv), lane, s);
     }
-    sum_slices<VPL>(z + static_cast<size_t>(v) * n, split_stride, splits, lane, val);
+    sum_slices_deep<VPL>(z + static_cast<size_t>(v) * n, split_stride, splits, lane, val);
     wave_hadamard<VPL>(val, scale, lane);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
         val[i] = val[i] * s[i];
     }
     store_wave<VPL>(out + static_cast<size_t>(v) * n, lane, val);
+}
+
+// z[i] = ((0 + z[i]) + z[stride + i]) + ... over the slices, in place in
+// slice 0: the slice-order sum of sum_slices, spread over many CUs. A
+// single-vector epilogue would otherwise pull every slice through one CU.
+__global__ __launch_bounds__(64) void k_reduce_slices(float *z, uint32_t splits, size_t stride,
+                                                      uint32_t count4) {
+#pragma clang fp contract(off)
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count4) {
+        return;
+    }
+    float4 *z4 = reinterpret_cast<float4 *>(z);
+    const size_t stride4 = stride / 4;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t s0 = 0; s0 < splits; s0 += 8) {
+        float4 a[8];
+#pragma unroll
+        for (uint32_t g = 0; g < 8; ++g) {
+            a[g] = z4[(s0 + g < splits ? s0 + g : splits - 1u) * stride4 + i];
+        }
+#pragma unroll
+        for (uint32_t g = 0; g < 8; ++g) {
+            if (s0 + g < splits) {
+                acc.x = acc.x + a[g].x;
+                acc.y = acc.y + a[g].y;
+                acc.z = acc.z + a[g].z;
+                acc.w = acc.w + a[g].w;
+            }
+        }
+    }
+    z4[i] = acc;
+}
+
+// y = sv * H_8192(sum over splits of z): four waves per vector, wave w
+// holding values [2048 w, 2048 w + 2048) in the wave layout. Each quarter's
+// transform runs the strides 1 .. 1024; strides 2048 and 4096 then pair
+// values across quarters in LDS. The butterflies run in the reference's
+// stride order, so the result is the reference's transform.
+template <typename Scale>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_epilogue_8192(
+    const float *__restrict__ z, uint32_t splits, size_t split_stride, const Scale *__restrict__ sv,
+    float scale, float *__restrict__ out) {
+#pragma clang fp contract(off)
+    constexpr uint32_t n = 8192, quarter = 2048;
+    __shared__ __align__(16) float v[n];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    float val[32];
+    sum_slices_deep<32>(z + static_cast<size_t>(blockIdx.x) * n + wave * quarter, split_stride,
+                        splits, lane, val);
+    wave_hadamard<32>(val, 1.0f, lane);  // x * 1 is exact: the scale comes last
+    store_wave<32>(v + wave * quarter, lane, val);
+    for (uint32_t stride = quarter; stride < n; stride <<= 1) {
+        __syncthreads();
+        for (uint32_t k = threadIdx.x; k < n / 2; k += blockDim.x) {
+            const uint32_t lo = ((k & ~(stride - 1)) << 1) | (k & (stride - 1));
+            const float a = v[lo];
+            const float b = v[lo + stride];
+            v[lo] = a + b;
+            v[lo + stride] = a - b;
+        }
+    }
+    __syncthreads();
+    // four consecutive values per thread and pass, every scale load issued
+    // before the first store
+    float4 *dst = reinterpret_cast<float4 *>(out + static_cast<size_t>(blockIdx.x) * n);
+    const float4 *v4 = reinterpret_cast<const float4 *>(v);
+    constexpr uint32_t kPasses = n / 4 / 256;
+    float s[kPasses][4];
+#pragma unroll
+    for (uint32_t p = 0; p < kPasses; ++p) {
+        const uint32_t k = (p * 256 + threadIdx.x) * 4;
+#pragma unroll
+        for (uint32_t e = 0; e < 4; ++e) {
+            s[p][e] = scale_value<Scale>(sv[k + e]);
+        }
+    }
+#pragma unroll
+    for (uint32_t p = 0; p < kPasses; ++p) {
+        const float4 a = v4[p * 256 + threadIdx.x];
+        dst[p * 256 + threadIdx.x] = make_float4(a.x * scale * s[p][0], a.y * scale * s[p][1],
+                                                 a.z * scale * s[p][2], a.w * scale * s[p][3]);
+    }
 }
 
 // In-place normalised FWHT of `count` vectors, one wave each (64 <= n <= 4096)
@@ -720,6 +804,15 @@ void launch_epilogue_any(adi_hip_context *ctx, const float *z, uint32_t splits,
     const float scale = hadamard_scale(n);
     require(aligned_to(z, 16) && aligned_to(out, 16) && aligned_to(sv, sizeof(Scale) == 2 ? 8 : 4),
             "vectors must be 16-byte aligned, f16 scale rows 8-byte and sign rows 4-byte");
+    // few vectors over many slice bytes (128 KiB and up): add the slices
+    // across the GPU first
+    if (splits > 1 && vectors <= 8 && size_t(splits) * vectors * n >= 32768 && n % 4 == 0 &&
+        split_stride % 4 == 0) {
+        const uint32_t count4 = vectors * n / 4;
+        launch(ctx, "reduce_slices", k_reduce_slices, dim3(ceil_div(count4, 64)), dim3(64), 0,
+               const_cast<float *>(z), splits, split_stride, count4);
+        splits = 1;
+    }
     const dim3 grid(ceil_div(vectors, 4));
     switch (n) {
     case 64: launch(ctx, "hadamard_epilogue", k_epilogue_wave<1, Scale>, grid, dim3(256), 0, z, splits, split_stride, sv, vectors, scale, out); break;
@@ -729,6 +822,7 @@ void launch_epilogue_any(adi_hip_context *ctx, const float *z, uint32_t splits,
     case 1024: launch(ctx, "hadamard_epilogue", k_epilogue_wave<16, Scale>, grid, dim3(256), 0, z, splits, split_stride, sv, vectors, scale, out); break;
     case 2048: launch(ctx, "hadamard_epilogue", k_epilogue_wave<32, Scale>, grid, dim3(256), 0, z, splits, split_stride, sv, vectors, scale, out); break;
     case 4096: launch(ctx, "hadamard_epilogue", k_epilogue_wave<64, Scale>, grid, dim3(256), 0, z, splits, split_stride, sv, vectors, scale, out); break;
+    case 8192: launch(ctx, "hadamard_epilogue", k_epilogue_8192<Scale>, dim3(vectors), dim3(256), 0, z, splits, split_stride, sv, scale, out); break;
     default:
         launch(ctx, "hadamard_epilogue", k_epilogue<Scale>, dim3(vectors), dim3(256),
                n * sizeof(float), z, splits, split_stride, n, sv, 0u,

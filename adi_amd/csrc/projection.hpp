@@ -64,6 +64,8 @@ __device__ __forceinline__ void prologue_vector(const PrologueJobs &j, uint32_t 
     wave_hadamard<VPL>(val, j.scale, lane);
     store_xhat<VPL>(g.out, v, lane, val);
 }
+// y = sv * H_n(sum over splits of z). z is scratch: for a few vectors over
+// several slices the launch first adds the slices into slice 0, in place.
 template <typename Scale>
 void launch_epilogue_any(adi_hip_context *ctx, const float *z, uint32_t splits,
                          size_t split_stride, uint32_t n, const Scale *sv, uint32_t vectors,

@@ -1,7 +1,10 @@
 """Benchmark of the MI355X packed-weight hot path: one MoE block (router,
 top-8 routing, stable dispatch, trellis-packed SwiGLU experts, route-order
 combine, gated shared expert) at ubatch 1, 128 and 512 tokens, plus the
-packed projections (2048x2048 non-expert, 151936x2048 int5 output head).
+packed projections (2048x2048 non-expert, 151936x2048 int5 output head), the
+token side of decoding (embedding rows, greedy and top-p choice) and the
+attention half of a decode step (full GQA attention, Gated DeltaNet, a whole
+decoder layer).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
@@ -279,6 +282,7 @@ def projections(torch, hip, ctx, steps):
             "packed_gbs": round(nbytes / dt / 1e9, 1),
             "hbm_frac": round(nbytes / dt / 1e9 / HBM_PEAK_GBS, 4)}
     res.update(decode_side(torch, hip, ctx, steps))
+    res.update(attention_side(torch, hip, ctx, steps))
     return res
 
 
@@ -319,6 +323,49 @@ def decode_side(torch, hip, ctx, steps):
         res[f"greedy_{vocab}_rows{rows}"] = {"us_per_call": round(us, 2)}
         us = timed(lambda: hip.sample_rows(ctx, logits, rows, vocab, 0.7, 0.9, words, picked))
         res[f"top_p_{vocab}_rows{rows}"] = {"us_per_call": round(us, 2)}
+    return res
+
+
+def attention_side(torch, hip, ctx, steps):
+    """The attention half of a decode step at hidden 2048: full GQA attention
+    at history positions 255 and 4095 (KV cache resident), one Gated DeltaNet
+    token, and a whole decoder layer (linear attention + the 256-expert MoE
+    block)."""
+    from adi_amd import synthetic as syn
+    res = {}
+    rng = syn.rng_for(5, 0)
+    etlut, ntlut = syn.expert_tlut(rng), syn.ne_tlut(rng)
+    nbook, ebook = ctx.ne_codebook(ntlut), ctx.expert_codebook(etlut)
+    full = hip.upload_full_attention(ctx, syn.full_attention(rng, 2048, ntlut), nbook)
+    x = torch.from_numpy(syn.rms_normalized(syn.hidden_states(rng, 1, 2048))[0]).cuda()
+    out = torch.empty(2048, dtype=torch.float32, device="cuda")
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return round((time.perf_counter() - t0) / steps * 1e6, 2)
+
+    for position in (255, 4095):
+        keys = torch.randn((position + 1, 2, 256), dtype=torch.float32, device="cuda")
+        values = torch.randn_like(keys)
+        res[f"full_attention_2048_pos{position}"] = {"us_per_call": timed(
+            lambda: hip.full_attention_forward(ctx, full, position, x, out, keys, values, position + 1))}
+    linear = hip.upload_linear_attention(ctx, syn.linear_attention(rng, 2048, ntlut), nbook)
+    conv = torch.zeros(8192 * 3, dtype=torch.float32, device="cuda")
+    rec = torch.zeros(32 * 128 * 128, dtype=torch.float32, device="cuda")
+    res["linear_attention_2048"] = {"us_per_call": timed(
+        lambda: hip.linear_attention_forward(ctx, linear, x, out, conv, rec))}
+    layer = hip.upload_decoder_layer(
+        ctx, syn.decoder_layer(rng, False, 2048, 512, 256, etlut, ntlut), ebook, nbook)
+    state, keep = hip.layer_state(False)
+    hidden = x.clone().reshape(1, 2048)
+    res["decoder_layer_linear_2048"] = {"us_per_call": timed(
+        lambda: hip.decode_layer(ctx, layer, 0, hidden, state))}
     return res
 
 
