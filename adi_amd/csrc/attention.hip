@@ -1,7 +1,10 @@
-// attention.hip -- the attention half of a decode step on the device, for one
-// token of one sequence:
+// attention.hip -- the attention half of a decoder layer on the device, for a
+// chunk of consecutive tokens of one sequence (one token when decoding):
 //   full_attention_forward   (src/executor.cpp:332-418, src/attention.cpp)
 //   linear_attention_forward (src/executor.cpp:420-557, Gated DeltaNet)
+// A chunk gives what decoding its tokens one after another gives (token b sees
+// the cache up to its own position; the recurrence runs over the chunk in
+// order); its projections and MoE run batched.
 //
 // Full attention, after the q/k/v projections:
 //   norm_rope   one block per head: RMS norm with (1 + w), then RoPE on the
@@ -50,6 +53,11 @@ struct RopeTable {
     float sine[kRopeHalf];
 };
 
+// MachModel's RoPE divisors (src/model.cpp:606-615), computed on the host.
+struct RopeDivisors {
+    float divisor[kRopeHalf];
+};
+
 __device__ __forceinline__ float wave_sum(float v) {
     v += lane_xor<1>(v);
     v += lane_xor<2>(v);
@@ -81,14 +89,19 @@ __device__ __forceinline__ float silu_of(float v) { return v / (1.0f + expf(-v))
 __device__ __forceinline__ float sigmoid_of(float v) { return 1.0f / (1.0f + expf(-v)); }
 
 // normalize_head then apply_rope (src/executor.cpp:25-41, 60-72, 376-390):
-// blocks 0-15 the query heads (stride 512), 16-17 the new key heads.
+// block (h, b) of token b: h 0-15 the query heads (stride 512), 16-17 the new
+// key heads. One token takes the host's table `rope`; in a chunk, token b's
+// table is computed here for position + b from the host's divisors.
 __global__ __launch_bounds__(kHeadSize) void k_norm_rope(float *query_gate, float *key,
                                                          const uint16_t *query_norm,
-                                                         const uint16_t *key_norm, RopeTable rope) {
+                                                         const uint16_t *key_norm, RopeTable rope,
+                                                         RopeDivisors divisors, uint32_t position) {
 #pragma clang fp contract(off)
     __shared__ float partial[16];
     __shared__ float head[kHeadSize];
-    const uint32_t h = blockIdx.x, t = threadIdx.x;
+    const uint32_t h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+    query_gate += static_cast<size_t>(b) * kQueryHeads * kQueryStride;
+    key += static_cast<size_t>(b) * kKvHeads * kHeadSize;
     float *v = h < kQueryHeads ? query_gate + static_cast<size_t>(h) * kQueryStride
                                : key + static_cast<size_t>(h - kQueryHeads) * kHeadSize;
     const uint16_t *w = h < kQueryHeads ? query_norm : key_norm;
@@ -99,9 +112,15 @@ __global__ __launch_bounds__(kHeadSize) void k_norm_rope(float *query_gate, floa
     head[t] = x;
     __syncthreads();
     if (t < kRopeHalf) {
+        float cosine = rope.cosine[t], sine = rope.sine[t];
+        if (gridDim.y > 1) {
+            const float theta = static_cast<float>(position + b) / divisors.divisor[t];
+            cosine = cosf(theta);
+            sine = sinf(theta);
+        }
         const float first = head[t], second = head[t + kRopeHalf];
-        v[t] = first * rope.cosine[t] - second * rope.sine[t];
-        v[t + kRopeHalf] = second * rope.cosine[t] + first * rope.sine[t];
+        v[t] = first * cosine - second * sine;
+        v[t + kRopeHalf] = second * cosine + first * sine;
     } else if (t >= 2 * kRopeHalf) {
         v[t] = x;
     }
@@ -129,19 +148,24 @@ __device__ __forceinline__ void online_step(float score, float4 value, float &ma
     maximum = score;
 }
 
-// Block (query head, split): tokens [split * chunk, min(tokens, ...)) of the
-// head's KV stream, wave w taking every fourth. Lane l holds dimensions
-// 4l..4l+3. Writes the split's accumulator, maximum and denominator.
+// Block (query head, split, token b): cache entries [split * chunk, ...) up
+// to token b's own position of the head's KV stream, wave w taking every
+// fourth. Lane l holds dimensions 4l..4l+3. Writes the split's accumulator,
+// maximum and denominator (maximum -inf and denominator 0 when the split
+// lies past the token).
 __global__ __launch_bounds__(256) void k_attention_partial(const float *query_gate,
                                                            const float *keys, const float *values,
-                                                           uint32_t tokens, uint32_t chunk,
+                                                           uint32_t position, uint32_t chunk,
                                                            float *partial) {
 #pragma clang fp contract(off)
     __shared__ __align__(16) float wave_acc[4][kHeadSize];
     __shared__ float wave_max[4], wave_den[4];
-    const uint32_t h = blockIdx.x, split = blockIdx.y, splits = gridDim.y;
+    const uint32_t h = blockIdx.x, split = blockIdx.y, splits = gridDim.y, b = blockIdx.z;
     const uint32_t kv = h / (kQueryHeads / kKvHeads);
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t tokens = position + b + 1;
+    query_gate += static_cast<size_t>(b) * kQueryHeads * kQueryStride;
+    partial += static_cast<size_t>(b) * kQueryHeads * splits * kPartialStride;
     const float4 q = reinterpret_cast<const float4 *>(query_gate + static_cast<size_t>(h) * kQueryStride)[lane];
     const float score_scale = 1.0f / 16.0f;  // 1 / sqrt(256)
     const uint32_t begin = split * chunk;
@@ -161,16 +185,17 @@ __global__ __launch_bounds__(256) void k_attention_partial(const float *query_ga
         wave_den[wave] = denominator;
     }
     __syncthreads();
-    // every split holds at least one token, so the block maximum is finite
     float m = wave_max[0];
     for (uint32_t w = 1; w < 4; ++w) {
         m = fmaxf(m, wave_max[w]);
     }
     float a = 0.0f, d = 0.0f;
-    for (uint32_t w = 0; w < 4; ++w) {
-        const float f = expf(wave_max[w] - m);  // 0 for a wave without tokens
-        a += wave_acc[w][threadIdx.x] * f;
-        d += wave_den[w] * f;
+    if (m != -__builtin_huge_valf()) {  // else no token in this split
+        for (uint32_t w = 0; w < 4; ++w) {
+            const float f = expf(wave_max[w] - m);  // 0 for a wave without tokens
+            a += wave_acc[w][threadIdx.x] * f;
+            d += wave_den[w] * f;
+        }
     }
     float *out = partial + (static_cast<size_t>(h) * splits + split) * kPartialStride;
     out[threadIdx.x] = a;
@@ -187,14 +212,20 @@ __global__ __launch_bounds__(kHeadSize) void k_attention_combine(const float *pa
                                                                  const float *query_gate,
                                                                  float *attended) {
 #pragma clang fp contract(off)
-    const uint32_t h = blockIdx.x, t = threadIdx.x;
-    const float *p = partial + static_cast<size_t>(h) * splits * kPartialStride;
+    const uint32_t h = blockIdx.x, t = threadIdx.x, b = blockIdx.y;
+    query_gate += static_cast<size_t>(b) * kQueryHeads * kQueryStride;
+    attended += static_cast<size_t>(b) * kQueryHeads * kHeadSize;
+    const float *p = partial + (static_cast<size_t>(b) * kQueryHeads + h) * splits * kPartialStride;
+    // split 0 always holds token 0, so the maximum is finite
     float m = p[kHeadSize];
     for (uint32_t s = 1; s < splits; ++s) {
         m = fmaxf(m, p[s * kPartialStride + kHeadSize]);
     }
     float a = 0.0f, d = 0.0f;
     for (uint32_t s = 0; s < splits; ++s) {
+        if (p[s * kPartialStride + kHeadSize + 1] == 0.0f) {
+            continue;  // a split past the token
+        }
         const float f = expf(p[s * kPartialStride + kHeadSize] - m);
         a += p[s * kPartialStride + t] * f;
         d += p[s * kPartialStride + kHeadSize + 1] * f;
@@ -203,71 +234,121 @@ __global__ __launch_bounds__(kHeadSize) void k_attention_combine(const float *pa
     attended[static_cast<size_t>(h) * kHeadSize + t] = a * (1.0f / d) * sigmoid_of(gate);
 }
 
-// The causal convolution of 128 channels (src/executor.cpp:480-496) and, for
-// the query and key groups (blocks 0-31), their L2 norm (497-505).
+// The causal convolution of 128 channels for token b (src/executor.cpp:
+// 480-496) and, for the query and key groups (blocks 0-31), their L2 norm
+// (497-505). The three inputs before token b are the chunk's earlier qkv rows
+// or, before the chunk, the state. With one token the state shifts here;
+// for a chunk k_conv_history does it after every token has read it.
 __global__ __launch_bounds__(kLinearHead) void k_linear_conv(const float *qkv,
                                                              const uint16_t *weights,
                                                              float *state, float *convolved) {
 #pragma clang fp contract(off)
     __shared__ float partial[16];
-    const uint32_t c = blockIdx.x * kLinearHead + threadIdx.x;
+    const uint32_t c = blockIdx.x * kLinearHead + threadIdx.x, b = blockIdx.y;
     float *history = state + static_cast<size_t>(c) * 3u;
     const uint2 packed = *reinterpret_cast<const uint2 *>(weights + static_cast<size_t>(c) * 4u);
     const float w0 = bf16_bits_to_float(packed.x & 0xFFFFu), w1 = bf16_bits_to_float(packed.x >> 16);
     const float w2 = bf16_bits_to_float(packed.y & 0xFFFFu), w3 = bf16_bits_to_float(packed.y >> 16);
-    const float h0 = history[0], h1 = history[1], h2 = history[2];
-    const float x = qkv[c];
+    // input at relative time b - 3 + i: row b - 3 + i, or state slot b + i
+    float earlier[3];
+#pragma unroll
+    for (uint32_t i = 0; i < 3; ++i) {
+        earlier[i] = b + i >= 3 ? qkv[static_cast<size_t>(b + i - 3) * kChannels + c] : history[b + i];
+    }
+    const float h0 = earlier[0], h1 = earlier[1], h2 = earlier[2];
+    const float x = qkv[static_cast<size_t>(b) * kChannels + c];
     float v = 0.0f;
     v += h0 * w0;
     v += h1 * w1;
     v += h2 * w2;
     v += x * w3;
     float y = silu_of(v);
-    history[0] = h1;
-    history[1] = h2;
-    history[2] = x;
+    if (gridDim.y == 1) {
+        history[0] = h1;
+        history[1] = h2;
+        history[2] = x;
+    }
     if (blockIdx.x < 2u * kKeyHeads) {  // uniform over the block
         const float squares = block_sum(y * y, partial);
         y *= 1.0f / sqrtf(squares + kEpsilon);
     }
-    convolved[c] = y;
+    convolved[static_cast<size_t>(b) * kChannels + c] = y;
 }
 
-// gated_delta_head (src/executor.cpp:121-155) for rows [16 y, 16 y + 16) of
-// value head x: each wave updates four state rows in turn, a lane holding two
-// of a row's 128 values (src/simd.cpp:108-127).
+// The convolution state after a chunk of `count` tokens: the last three of
+// (state, qkv rows) per channel.
+__global__ __launch_bounds__(256) void k_conv_history(const float *qkv, uint32_t count,
+                                                      float *state) {
+    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= kChannels) {
+        return;
+    }
+    float *history = state + static_cast<size_t>(c) * 3u;
+    float next[3];
+#pragma unroll
+    for (uint32_t i = 0; i < 3; ++i) {
+        // slot i holds relative time count - 3 + i
+        next[i] = count + i >= 3 ? qkv[static_cast<size_t>(count + i - 3) * kChannels + c]
+                                 : history[count + i];
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < 3; ++i) {
+        history[i] = next[i];
+    }
+}
+
+// gated_delta_head (src/executor.cpp:121-155) for state rows [16 y, 16 y +
+// 16) of value head x over the chunk's `count` tokens in order: each wave
+// keeps four rows in registers through the chunk, a lane holding two of a
+// row's 128 values (src/simd.cpp:108-127); the state is read and written once
+// per chunk.
 __global__ __launch_bounds__(256) void k_gated_delta(const float *convolved, const float *alpha,
                                                      const float *beta, const uint16_t *alpha_bias,
-                                                     const uint16_t *a_log, float *recurrent,
-                                                     float *output) {
+                                                     const uint16_t *a_log, uint32_t count,
+                                                     float *recurrent, float *output) {
 #pragma clang fp contract(off)
+    constexpr uint32_t kRows = kDeltaRows / 4u;
     const uint32_t h = blockIdx.x;
     const uint32_t kh = h / (kValueHeads / kKeyHeads);
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const float2 q = reinterpret_cast<const float2 *>(convolved + static_cast<size_t>(kh) * kLinearHead)[lane];
-    const float2 k = reinterpret_cast<const float2 *>(convolved + kQkSize + static_cast<size_t>(kh) * kLinearHead)[lane];
-    const float *v = convolved + 2u * kQkSize + static_cast<size_t>(h) * kLinearHead;
-    const float beta_value = sigmoid_of(beta[h]);
-    const float biased = alpha[h] + bf16_bits_to_float(alpha_bias[h]);
-    const float softplus = biased > 20.0f ? biased : log1pf(expf(biased));
-    const float decay = expf(-expf(bf16_bits_to_float(a_log[h])) * softplus);
+    const uint32_t row0 = blockIdx.y * kDeltaRows + wave * kRows;
+    const float bias = bf16_bits_to_float(alpha_bias[h]);
+    const float rate = expf(bf16_bits_to_float(a_log[h]));
     const float output_scale = 1.0f / sqrtf(static_cast<float>(kLinearHead));
-    for (uint32_t j = 0; j < kDeltaRows / 4u; ++j) {
-        const uint32_t row = blockIdx.y * kDeltaRows + wave * (kDeltaRows / 4u) + j;
-        float2 *state = reinterpret_cast<float2 *>(
-            recurrent + (static_cast<size_t>(h) * kLinearHead + row) * kLinearHead);
-        float2 s = state[lane];
-        s.x *= decay;
-        s.y *= decay;
-        const float prediction = wave_sum(s.x * k.x + s.y * k.y);
-        const float delta = (v[row] - prediction) * beta_value;
-        s.x += k.x * delta;
-        s.y += k.y * delta;
-        const float attended = wave_sum(s.x * q.x + s.y * q.y);
-        state[lane] = s;
-        if (lane == 0) {
-            output[static_cast<size_t>(h) * kLinearHead + row] = attended * output_scale;
+    float2 *state = reinterpret_cast<float2 *>(
+        recurrent + (static_cast<size_t>(h) * kLinearHead + row0) * kLinearHead);
+    float2 s[kRows];
+#pragma unroll
+    for (uint32_t j = 0; j < kRows; ++j) {
+        s[j] = state[j * (kLinearHead / 2u) + lane];
+    }
+    for (uint32_t b = 0; b < count; ++b) {
+        const float *token = convolved + static_cast<size_t>(b) * kChannels;
+        const float2 q = reinterpret_cast<const float2 *>(token + static_cast<size_t>(kh) * kLinearHead)[lane];
+        const float2 k = reinterpret_cast<const float2 *>(token + kQkSize + static_cast<size_t>(kh) * kLinearHead)[lane];
+        const float *v = token + 2u * kQkSize + static_cast<size_t>(h) * kLinearHead;
+        const float beta_value = sigmoid_of(beta[static_cast<size_t>(b) * kValueHeads + h]);
+        const float biased = alpha[static_cast<size_t>(b) * kValueHeads + h] + bias;
+        const float softplus = biased > 20.0f ? biased : log1pf(expf(biased));
+        const float decay = expf(-rate * softplus);
+#pragma unroll
+        for (uint32_t j = 0; j < kRows; ++j) {
+            s[j].x *= decay;
+            s[j].y *= decay;
+            const float prediction = wave_sum(s[j].x * k.x + s[j].y * k.y);
+            const float delta = (v[row0 + j] - prediction) * beta_value;
+            s[j].x += k.x * delta;
+            s[j].y += k.y * delta;
+            const float attended = wave_sum(s[j].x * q.x + s[j].y * q.y);
+            if (lane == 0) {
+                output[static_cast<size_t>(b) * kValueSize + static_cast<size_t>(h) * kLinearHead +
+                       row0 + j] = attended * output_scale;
+            }
         }
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kRows; ++j) {
+        state[j * (kLinearHead / 2u) + lane] = s[j];
     }
 }
 
@@ -279,7 +360,8 @@ __global__ __launch_bounds__(kLinearHead) void k_linear_norm_gate(const float *r
                                                                   float *normalized) {
 #pragma clang fp contract(off)
     __shared__ float partial[16];
-    const size_t i = static_cast<size_t>(blockIdx.x) * kLinearHead + threadIdx.x;
+    const size_t i = static_cast<size_t>(blockIdx.y) * kValueSize +
+                     static_cast<size_t>(blockIdx.x) * kLinearHead + threadIdx.x;
     const float x = recurrent_output[i];
     const float squares = block_sum(x * x, partial);
     const float scale = 1.0f / sqrtf(squares / static_cast<float>(kLinearHead) + kEpsilon);
@@ -297,11 +379,19 @@ __global__ __launch_bounds__(256) void k_residual_add(float *hidden, const float
 
 // prepare_rope (src/executor.cpp:43-58) with MachModel's divisors
 // (src/model.cpp:606-615), on the host with the reference's float libm calls.
+RopeDivisors rope_divisors() {
+    RopeDivisors d{};
+    for (uint32_t i = 0; i < kRopeHalf; ++i) {
+        d.divisor[i] = std::pow(10000000.0F, 2.0F * static_cast<float>(i) / 64.0F);
+    }
+    return d;
+}
+
 RopeTable rope_table(uint32_t position) {
+    const RopeDivisors d = rope_divisors();
     RopeTable t{};
     for (uint32_t i = 0; i < kRopeHalf; ++i) {
-        const float divisor = std::pow(10000000.0F, 2.0F * static_cast<float>(i) / 64.0F);
-        const float theta = static_cast<float>(position) / divisor;
+        const float theta = static_cast<float>(position) / d.divisor[i];
         t.cosine[i] = std::cos(theta);
         t.sine[i] = std::sin(theta);
     }
@@ -319,6 +409,142 @@ bool ne_shaped(const adi_hip_ne_matrix &m, uint32_t rows, uint32_t columns) {
     return m.rows == rows && m.columns == columns && m.trellis != nullptr;
 }
 
+// full_attention_forward for tokens position .. position + count - 1.
+void full_attention_chunk(adi_hip_context *ctx, const adi_hip_full_attention *L,
+                          uint32_t position, uint32_t count, const float *inputs, float *outputs,
+                          float *keys, float *values, uint32_t capacity) {
+    require(L != nullptr && inputs != nullptr && outputs != nullptr && keys != nullptr &&
+                values != nullptr && count > 0,
+            "full attention state or input shape mismatch");
+    const uint32_t hidden = L->query.columns;
+    require(ne_shaped(L->query, kQueryHeads * kQueryStride, hidden) &&
+                ne_shaped(L->key, kKvHeads * kHeadSize, hidden) &&
+                ne_shaped(L->value, kKvHeads * kHeadSize, hidden) &&
+                ne_shaped(L->output, hidden, kQueryHeads * kHeadSize) &&
+                L->query_norm != nullptr && L->key_norm != nullptr && position < capacity &&
+                count <= capacity - position,
+            "full attention state or input shape mismatch");
+    require(aligned_to(keys, 16) && aligned_to(values, 16),
+            "attention caches must be 16-byte aligned");
+    auto &ws = ctx->layer_workspace;
+    ws.used = 0;
+    // splits of the history for the chunk's last token; a chunk's many tokens
+    // already give blocks enough, so they split less
+    const uint32_t last = position + count;
+    const uint32_t cap = kMaxSplits / count > 0 ? kMaxSplits / count : 1u;
+    uint32_t splits = ceil_div(last, 32);
+    splits = splits < 1 ? 1 : (splits > cap ? cap : splits);
+    const uint32_t chunk = ceil_div(last, splits);
+    splits = ceil_div(last, chunk);
+    ws.ensure(Workspace::round(size_t(count) * kQueryHeads * kQueryStride * 4) +
+              Workspace::round(size_t(count) * kQueryHeads * kHeadSize * 4) +
+              Workspace::round(size_t(count) * kQueryHeads * splits * kPartialStride * 4));
+    float *query_gate = ws.take<float>(size_t(count) * kQueryHeads * kQueryStride);
+    float *attended = ws.take<float>(size_t(count) * kQueryHeads * kHeadSize);
+    float *partial = ws.take<float>(size_t(count) * kQueryHeads * splits * kPartialStride);
+    float *key = keys + static_cast<size_t>(position) * kKvHeads * kHeadSize;
+    float *value = values + static_cast<size_t>(position) * kKvHeads * kHeadSize;
+    forward(ctx, adi_hip_ne_matmul(ctx, &L->query, inputs, count, query_gate));
+    forward(ctx, adi_hip_ne_matmul(ctx, &L->key, inputs, count, key));
+    forward(ctx, adi_hip_ne_matmul(ctx, &L->value, inputs, count, value));
+    launch(ctx, "attention_norm_rope", k_norm_rope, dim3(kQueryHeads + kKvHeads, count),
+           dim3(kHeadSize), 0, query_gate, key, L->query_norm, L->key_norm,
+           count == 1 ? rope_table(position) : RopeTable{}, rope_divisors(), position);
+    launch(ctx, "attention_partial", k_attention_partial, dim3(kQueryHeads, splits, count),
+           dim3(256), 0, static_cast<const float *>(query_gate), static_cast<const float *>(keys),
+           static_cast<const float *>(values), position, chunk, partial);
+    launch(ctx, "attention_combine", k_attention_combine, dim3(kQueryHeads, count),
+           dim3(kHeadSize), 0, static_cast<const float *>(partial), splits,
+           static_cast<const float *>(query_gate), attended);
+    forward(ctx, adi_hip_ne_matmul(ctx, &L->output, attended, count, outputs));
+}
+
+// linear_attention_forward for `count` consecutive tokens.
+void linear_attention_chunk(adi_hip_context *ctx, const adi_hip_linear_attention *L,
+                            uint32_t count, const float *inputs, float *outputs,
+                            float *convolution_state, float *recurrent_state) {
+    require(L != nullptr && inputs != nullptr && outputs != nullptr &&
+                convolution_state != nullptr && recurrent_state != nullptr && count > 0,
+            "linear attention input shape mismatch");
+    const uint32_t hidden = L->qkv.columns;
+    require(ne_shaped(L->qkv, kChannels, hidden) && ne_shaped(L->gate, kValueSize, hidden) &&
+                ne_shaped(L->output, hidden, kValueSize),
+            "linear attention input shape mismatch");
+    require(L->alpha.rows == kValueHeads && L->alpha.columns == hidden &&
+                L->beta.rows == kValueHeads && L->beta.columns == hidden &&
+                L->alpha.values != nullptr && L->beta.values != nullptr &&
+                L->alpha_bias != nullptr && L->a_log != nullptr,
+            "linear attention decay shape mismatch");
+    require(L->convolution != nullptr && aligned_to(L->convolution, 8),
+            "linear attention convolution shape mismatch");
+    require(L->norm != nullptr, "linear attention input shape mismatch");
+    require(aligned_to(recurrent_state, 8), "linear attention state must be 8-byte aligned");
+    auto &ws = ctx->layer_workspace;
+    ws.used = 0;
+    const size_t n = count;
+    ws.ensure(Workspace::round(n * kChannels * 4) * 2 + Workspace::round(n * kValueSize * 4) * 3 +
+              Workspace::round(n * kValueHeads * 4) * 2);
+    float *qkv = ws.take<float>(n * kChannels);
+    float *convolved = ws.take<float>(n * kChannels);
+    float *gate = ws.take<float>(n * kValueSize);
+    float *recurrent_output = ws.take<float>(n * kValueSize);
+    float *normalized = ws.take<float>(n * kValueSize);
+    float *alpha = ws.take<float>(n * kValueHeads);
+    float *beta = ws.take<float>(n * kValueHeads);
+    forward(ctx, adi_hip_ne_matmul(ctx, &L->qkv, inputs, count, qkv));
+    forward(ctx, adi_hip_ne_matmul(ctx, &L->gate, inputs, count, gate));
+    forward(ctx, adi_hip_bf16_matmul(ctx, &L->alpha, inputs, count, alpha));
+    forward(ctx, adi_hip_bf16_matmul(ctx, &L->beta, inputs, count, beta));
+    launch(ctx, "linear_conv", k_linear_conv, dim3(kChannels / kLinearHead, count),
+           dim3(kLinearHead), 0, static_cast<const float *>(qkv), L->convolution,
+           convolution_state, convolved);
+    if (count > 1) {
+        launch(ctx, "linear_conv_history", k_conv_history, dim3(kChannels / 256), dim3(256), 0,
+               static_cast<const float *>(qkv), count, convolution_state);
+    }
+    launch(ctx, "gated_delta", k_gated_delta, dim3(kValueHeads, kLinearHead / kDeltaRows),
+           dim3(256), 0, static_cast<const float *>(convolved), static_cast<const float *>(alpha),
+           static_cast<const float *>(beta), L->alpha_bias, L->a_log, count, recurrent_state,
+           recurrent_output);
+    launch(ctx, "linear_norm_gate", k_linear_norm_gate, dim3(kValueHeads, count),
+           dim3(kLinearHead), 0, static_cast<const float *>(recurrent_output), L->norm,
+           static_cast<const float *>(gate), normalized);
+    forward(ctx, adi_hip_ne_matmul(ctx, &L->output, normalized, count, outputs));
+}
+
+// decode_layer for `count` consecutive tokens of rows `hidden`.
+void decoder_chunk(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_t position,
+                   uint32_t count, float *hidden, const adi_hip_layer_state *state) {
+    require(L != nullptr && hidden != nullptr && state != nullptr && L->input_norm != nullptr &&
+                L->post_attention_norm != nullptr && count > 0,
+            "decoder layer input is null");
+    const uint32_t n = L->moe.hidden;
+    require(n > 0 && aligned_to(hidden, 16), "decoder hidden row must be 16-byte aligned");
+    auto &ws = ctx->decoder_workspace;
+    ws.used = 0;
+    const size_t rows = size_t(count) * n;
+    ws.ensure(Workspace::round(rows * 4) * 2);
+    float *normalized = ws.take<float>(rows);
+    float *branch = ws.take<float>(rows);
+    const dim3 grid(ceil_div(rows, 256));
+    forward(ctx, adi_hip_rms_norm(ctx, hidden, L->input_norm, n, count, 1.0f, 1.0e-6f, normalized));
+    if (L->full_attention != 0) {
+        full_attention_chunk(ctx, &L->full, position, count, normalized, branch, state->keys,
+                             state->values, state->capacity);
+    } else {
+        linear_attention_chunk(ctx, &L->linear, count, normalized, branch, state->convolution,
+                               state->recurrent);
+    }
+    launch(ctx, "residual_add", k_residual_add, grid, dim3(256), 0, hidden,
+           static_cast<const float *>(branch), static_cast<uint32_t>(rows));
+    forward(ctx, adi_hip_rms_norm(ctx, hidden, L->post_attention_norm, n, count, 1.0f, 1.0e-6f,
+                                  normalized));
+    forward(ctx, adi_hip_moe_forward(ctx, &L->moe, normalized, count, nullptr, branch, nullptr,
+                                     nullptr));
+    launch(ctx, "residual_add", k_residual_add, grid, dim3(256), 0, hidden,
+           static_cast<const float *>(branch), static_cast<uint32_t>(rows));
+}
+
 }  // namespace
 }  // namespace adi_hip
 
@@ -330,46 +556,15 @@ int adi_hip_full_attention_forward(adi_hip_context *ctx, const adi_hip_full_atte
                                    uint32_t position, const float *input, float *output,
                                    float *keys, float *values, uint32_t capacity) {
     return guarded(ctx, [&] {
-        require(L != nullptr && input != nullptr && output != nullptr && keys != nullptr &&
-                    values != nullptr,
-                "full attention state or input shape mismatch");
-        const uint32_t hidden = L->query.columns;
-        require(ne_shaped(L->query, kQueryHeads * kQueryStride, hidden) &&
-                    ne_shaped(L->key, kKvHeads * kHeadSize, hidden) &&
-                    ne_shaped(L->value, kKvHeads * kHeadSize, hidden) &&
-                    ne_shaped(L->output, hidden, kQueryHeads * kHeadSize) &&
-                    L->query_norm != nullptr && L->key_norm != nullptr && position < capacity,
-                "full attention state or input shape mismatch");
-        require(aligned_to(keys, 16) && aligned_to(values, 16),
-                "attention caches must be 16-byte aligned");
-        auto &ws = ctx->layer_workspace;
-        ws.used = 0;
-        const uint32_t tokens = position + 1;
-        uint32_t splits = ceil_div(tokens, 32);
-        splits = splits < 1 ? 1 : (splits > kMaxSplits ? kMaxSplits : splits);
-        const uint32_t chunk = ceil_div(tokens, splits);
-        splits = ceil_div(tokens, chunk);  // every split holds a token
-        ws.ensure(Workspace::round(kQueryHeads * kQueryStride * 4) +
-                  Workspace::round(kQueryHeads * kHeadSize * 4) +
-                  Workspace::round(size_t(kQueryHeads) * kMaxSplits * kPartialStride * 4));
-        float *query_gate = ws.take<float>(kQueryHeads * kQueryStride);
-        float *attended = ws.take<float>(kQueryHeads * kHeadSize);
-        float *partial = ws.take<float>(size_t(kQueryHeads) * splits * kPartialStride);
-        float *key = keys + static_cast<size_t>(position) * kKvHeads * kHeadSize;
-        float *value = values + static_cast<size_t>(position) * kKvHeads * kHeadSize;
-        forward(ctx, adi_hip_ne_matvec(ctx, &L->query, input, query_gate));
-        forward(ctx, adi_hip_ne_matvec(ctx, &L->key, input, key));
-        forward(ctx, adi_hip_ne_matvec(ctx, &L->value, input, value));
-        launch(ctx, "attention_norm_rope", k_norm_rope, dim3(kQueryHeads + kKvHeads),
-               dim3(kHeadSize), 0, query_gate, key, L->query_norm, L->key_norm,
-               rope_table(position));
-        launch(ctx, "attention_partial", k_attention_partial, dim3(kQueryHeads, splits), dim3(256),
-               0, static_cast<const float *>(query_gate), static_cast<const float *>(keys),
-               static_cast<const float *>(values), tokens, chunk, partial);
-        launch(ctx, "attention_combine", k_attention_combine, dim3(kQueryHeads), dim3(kHeadSize), 0,
-               static_cast<const float *>(partial), splits,
-               static_cast<const float *>(query_gate), attended);
-        forward(ctx, adi_hip_ne_matvec(ctx, &L->output, attended, output));
+        full_attention_chunk(ctx, L, position, 1, input, output, keys, values, capacity);
+    });
+}
+
+int adi_hip_full_attention_prefill(adi_hip_context *ctx, const adi_hip_full_attention *L,
+                                   uint32_t position, uint32_t count, const float *inputs,
+                                   float *outputs, float *keys, float *values, uint32_t capacity) {
+    return guarded(ctx, [&] {
+        full_attention_chunk(ctx, L, position, count, inputs, outputs, keys, values, capacity);
     });
 }
 
@@ -377,82 +572,26 @@ int adi_hip_linear_attention_forward(adi_hip_context *ctx, const adi_hip_linear_
                                      const float *input, float *output, float *convolution_state,
                                      float *recurrent_state) {
     return guarded(ctx, [&] {
-        require(L != nullptr && input != nullptr && output != nullptr &&
-                    convolution_state != nullptr && recurrent_state != nullptr,
-                "linear attention input shape mismatch");
-        const uint32_t hidden = L->qkv.columns;
-        require(ne_shaped(L->qkv, kChannels, hidden) && ne_shaped(L->gate, kValueSize, hidden) &&
-                    ne_shaped(L->output, hidden, kValueSize),
-                "linear attention input shape mismatch");
-        require(L->alpha.rows == kValueHeads && L->alpha.columns == hidden &&
-                    L->beta.rows == kValueHeads && L->beta.columns == hidden &&
-                    L->alpha.values != nullptr && L->beta.values != nullptr &&
-                    L->alpha_bias != nullptr && L->a_log != nullptr,
-                "linear attention decay shape mismatch");
-        require(L->convolution != nullptr && aligned_to(L->convolution, 8),
-                "linear attention convolution shape mismatch");
-        require(L->norm != nullptr, "linear attention input shape mismatch");
-        require(aligned_to(recurrent_state, 8), "linear attention state must be 8-byte aligned");
-        auto &ws = ctx->layer_workspace;
-        ws.used = 0;
-        ws.ensure(Workspace::round(kChannels * 4) * 2 + Workspace::round(kValueSize * 4) * 3 +
-                  Workspace::round(kValueHeads * 4) * 2);
-        float *qkv = ws.take<float>(kChannels);
-        float *convolved = ws.take<float>(kChannels);
-        float *gate = ws.take<float>(kValueSize);
-        float *recurrent_output = ws.take<float>(kValueSize);
-        float *normalized = ws.take<float>(kValueSize);
-        float *alpha = ws.take<float>(kValueHeads);
-        float *beta = ws.take<float>(kValueHeads);
-        forward(ctx, adi_hip_ne_matvec(ctx, &L->qkv, input, qkv));
-        forward(ctx, adi_hip_ne_matvec(ctx, &L->gate, input, gate));
-        forward(ctx, adi_hip_bf16_matvec(ctx, &L->alpha, input, alpha));
-        forward(ctx, adi_hip_bf16_matvec(ctx, &L->beta, input, beta));
-        launch(ctx, "linear_conv", k_linear_conv, dim3(kChannels / kLinearHead), dim3(kLinearHead),
-               0, static_cast<const float *>(qkv), L->convolution, convolution_state, convolved);
-        launch(ctx, "gated_delta", k_gated_delta, dim3(kValueHeads, kLinearHead / kDeltaRows),
-               dim3(256), 0, static_cast<const float *>(convolved),
-               static_cast<const float *>(alpha), static_cast<const float *>(beta), L->alpha_bias,
-               L->a_log, recurrent_state, recurrent_output);
-        launch(ctx, "linear_norm_gate", k_linear_norm_gate, dim3(kValueHeads), dim3(kLinearHead), 0,
-               static_cast<const float *>(recurrent_output), L->norm,
-               static_cast<const float *>(gate), normalized);
-        forward(ctx, adi_hip_ne_matvec(ctx, &L->output, normalized, output));
+        linear_attention_chunk(ctx, L, 1, input, output, convolution_state, recurrent_state);
+    });
+}
+
+int adi_hip_linear_attention_prefill(adi_hip_context *ctx, const adi_hip_linear_attention *L,
+                                     uint32_t count, const float *inputs, float *outputs,
+                                     float *convolution_state, float *recurrent_state) {
+    return guarded(ctx, [&] {
+        linear_attention_chunk(ctx, L, count, inputs, outputs, convolution_state, recurrent_state);
     });
 }
 
 int adi_hip_decode_layer(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_t position,
                          float *hidden, const adi_hip_layer_state *state) {
-    return guarded(ctx, [&] {
-        require(L != nullptr && hidden != nullptr && state != nullptr && L->input_norm != nullptr &&
-                    L->post_attention_norm != nullptr,
-                "decoder layer input is null");
-        const uint32_t n = L->moe.hidden;
-        require(n > 0 && aligned_to(hidden, 16), "decoder hidden row must be 16-byte aligned");
-        auto &ws = ctx->decoder_workspace;
-        ws.used = 0;
-        ws.ensure(Workspace::round(size_t(n) * 4) * 2);
-        float *normalized = ws.take<float>(n);
-        float *branch = ws.take<float>(n);
-        const dim3 grid(ceil_div(n, 256));
-        forward(ctx, adi_hip_rms_norm(ctx, hidden, L->input_norm, n, 1, 1.0f, 1.0e-6f, normalized));
-        if (L->full_attention != 0) {
-            forward(ctx, adi_hip_full_attention_forward(ctx, &L->full, position, normalized, branch,
-                                                        state->keys, state->values,
-                                                        state->capacity));
-        } else {
-            forward(ctx, adi_hip_linear_attention_forward(ctx, &L->linear, normalized, branch,
-                                                          state->convolution, state->recurrent));
-        }
-        launch(ctx, "residual_add", k_residual_add, grid, dim3(256), 0, hidden,
-               static_cast<const float *>(branch), n);
-        forward(ctx, adi_hip_rms_norm(ctx, hidden, L->post_attention_norm, n, 1, 1.0f, 1.0e-6f,
-                                      normalized));
-        forward(ctx, adi_hip_moe_forward(ctx, &L->moe, normalized, 1, nullptr, branch, nullptr,
-                                         nullptr));
-        launch(ctx, "residual_add", k_residual_add, grid, dim3(256), 0, hidden,
-               static_cast<const float *>(branch), n);
-    });
+    return guarded(ctx, [&] { decoder_chunk(ctx, L, position, 1, hidden, state); });
+}
+
+int adi_hip_prefill_layer(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_t position,
+                          uint32_t count, float *hidden, const adi_hip_layer_state *state) {
+    return guarded(ctx, [&] { decoder_chunk(ctx, L, position, count, hidden, state); });
 }
 
 }  // extern "C"

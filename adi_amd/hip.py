@@ -147,6 +147,12 @@ SIGNATURES = [
      [vp, C.POINTER(LinearAttentionStruct), vp, vp, vp, vp]),
     ("adi_hip_decode_layer", C.c_int,
      [vp, C.POINTER(DecoderLayerStruct), u32, vp, C.POINTER(LayerState)]),
+    ("adi_hip_full_attention_prefill", C.c_int,
+     [vp, C.POINTER(FullAttentionStruct), u32, u32, vp, vp, vp, vp, u32]),
+    ("adi_hip_linear_attention_prefill", C.c_int,
+     [vp, C.POINTER(LinearAttentionStruct), u32, vp, vp, vp, vp]),
+    ("adi_hip_prefill_layer", C.c_int,
+     [vp, C.POINTER(DecoderLayerStruct), u32, u32, vp, C.POINTER(LayerState)]),
     ("adi_hip_profiling_enable", C.c_int, [vp, C.c_int]),
     ("adi_hip_profiling_read", C.c_int, [vp, C.POINTER(KernelProfile), u32, C.POINTER(u32)]),
     # include/adi_hip_gguf.h
@@ -801,3 +807,23 @@ def layer_state(full: bool, capacity: int = 0):
 def decode_layer(ctx: Context, layer: DeviceDecoderLayer, position: int, hidden, state) -> None:
     ctx.check(load().adi_hip_decode_layer(ctx.handle, C.byref(layer.struct), position,
                                           _addr(hidden), C.byref(state)))
+
+
+def full_attention_prefill(ctx: Context, layer: DeviceFullAttention, position: int, count: int, x,
+                           out, keys, values, capacity: int) -> None:
+    ctx.check(load().adi_hip_full_attention_prefill(
+        ctx.handle, C.byref(layer.struct), position, count, _addr(x), _addr(out), _addr(keys),
+        _addr(values), capacity))
+
+
+def linear_attention_prefill(ctx: Context, layer: DeviceLinearAttention, count: int, x, out,
+                             convolution, recurrent) -> None:
+    ctx.check(load().adi_hip_linear_attention_prefill(
+        ctx.handle, C.byref(layer.struct), count, _addr(x), _addr(out), _addr(convolution),
+        _addr(recurrent)))
+
+
+def prefill_layer(ctx: Context, layer: DeviceDecoderLayer, position: int, count: int, hidden,
+                  state) -> None:
+    ctx.check(load().adi_hip_prefill_layer(ctx.handle, C.byref(layer.struct), position, count,
+                                           _addr(hidden), C.byref(state)))

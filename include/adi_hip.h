@@ -348,6 +348,14 @@ typedef struct {
 int adi_hip_full_attention_forward(adi_hip_context *ctx, const adi_hip_full_attention *layer,
                                    uint32_t position, const float *input, float *output,
                                    float *keys, float *values, uint32_t capacity);
+/* The same for `count` consecutive tokens at positions position ..
+ * position + count - 1 (inputs and outputs [count][hidden]): the result of
+ * calling the one-token form for each in turn, with the projections batched
+ * (the attention half of prefill, src/executor.cpp:561-731). position + count
+ * must not exceed capacity. */
+int adi_hip_full_attention_prefill(adi_hip_context *ctx, const adi_hip_full_attention *layer,
+                                   uint32_t position, uint32_t count, const float *inputs,
+                                   float *outputs, float *keys, float *values, uint32_t capacity);
 
 /* adi::LinearAttentionDescriptor (include/adi/model.hpp:48-58): Gated
  * DeltaNet with 16 key heads and 32 value heads of 128. qkv has 8192 rows
@@ -376,6 +384,12 @@ typedef struct {
 int adi_hip_linear_attention_forward(adi_hip_context *ctx, const adi_hip_linear_attention *layer,
                                      const float *input, float *output, float *convolution_state,
                                      float *recurrent_state);
+/* The same for `count` consecutive tokens (inputs and outputs
+ * [count][hidden]): the recurrence runs over them in order, the projections
+ * batched (src/executor.cpp:733-1179). */
+int adi_hip_linear_attention_prefill(adi_hip_context *ctx, const adi_hip_linear_attention *layer,
+                                     uint32_t count, const float *inputs, float *outputs,
+                                     float *convolution_state, float *recurrent_state);
 
 /* ---- one decoder layer of a decode step ---------------------------------- */
 
@@ -410,6 +424,13 @@ typedef struct {
  * offset 1 and epsilon 1e-6. */
 int adi_hip_decode_layer(adi_hip_context *ctx, const adi_hip_decoder_layer *layer,
                          uint32_t position, float *hidden, const adi_hip_layer_state *state);
+/* The layer for `count` consecutive tokens at positions position ..
+ * position + count - 1, rows hidden[count][moe.hidden] in place: the prefill
+ * step of a chunk (src/executor.cpp:1827-2101), with batched norms,
+ * projections and MoE (adi_hip_moe_forward at batch `count`). */
+int adi_hip_prefill_layer(adi_hip_context *ctx, const adi_hip_decoder_layer *layer,
+                          uint32_t position, uint32_t count, float *hidden,
+                          const adi_hip_layer_state *state);
 
 /* ---- kernel profiling ----------------------------------------------------- */
 
