@@ -283,6 +283,7 @@ def projections(torch, hip, ctx, steps):
             "hbm_frac": round(nbytes / dt / 1e9 / HBM_PEAK_GBS, 4)}
     res.update(decode_side(torch, hip, ctx, steps))
     res.update(attention_side(torch, hip, ctx, steps))
+    res.update(stack_side(torch, hip, ctx))
     return res
 
 
@@ -367,6 +368,65 @@ def attention_side(torch, hip, ctx, steps):
     res["decoder_layer_linear_2048"] = {"us_per_call": timed(
         lambda: hip.decode_layer(ctx, layer, 0, hidden, state))}
     return res
+
+
+def stack_side(torch, hip, ctx):
+    """A 3:1 hybrid stack of four decoder layers at hidden 2048 (three Gated
+    DeltaNet layers then full attention, each with the 256-expert MoE block),
+    a 248,320-token embedding and int5 head: a 256-token prompt prefilled in
+    chunks of 128, then 64 greedy steps with every token chosen and embedded
+    on the device. Each full-model figure would scale with its 40 layers."""
+    from adi_amd import synthetic as syn
+    rng = syn.rng_for(6, 0)
+    etlut, ntlut = syn.expert_tlut(rng), syn.ne_tlut(rng)
+    ebook, nbook = ctx.expert_codebook(etlut), ctx.ne_codebook(ntlut)
+    vocab, prompt, chunk, steps = 248320, 256, 128, 64
+    layers = [hip.upload_decoder_layer(ctx, syn.decoder_layer(rng, i % 4 == 3, HIDDEN, EXPERT_HIDDEN,
+                                                              EXPERTS, etlut, ntlut), ebook, nbook)
+              for i in range(4)]
+    emb = hip.upload_embedding(ctx, syn.embedding(rng, vocab, HIDDEN))
+    head = hip.upload_head(ctx, syn.head_chunk(rng, vocab, HIDDEN))
+    final_norm = ctx.to_device(syn.bf16_bits_rne(rng.normal(0.0, 0.1, HIDDEN).astype(np.float32)))
+    capacity = prompt + steps
+    lib = hip.load()
+
+    def run():
+        states = [hip.layer_state(i % 4 == 3, capacity) for i in range(4)]
+        tokens = torch.tensor(rng.integers(0, vocab, prompt).astype(np.int32), device="cuda")
+        hidden = torch.empty((chunk, HIDDEN), dtype=torch.float32, device="cuda")
+        normed = torch.empty((1, HIDDEN), dtype=torch.float32, device="cuda")
+        logits = torch.empty((1, vocab), dtype=torch.float32, device="cuda")
+        token = torch.empty(1, dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for c in range(0, prompt, chunk):
+            hip.embedding_rows(ctx, emb, tokens[c:c + chunk], chunk, hidden)
+            for layer, (state, _) in zip(layers, states):
+                hip.prefill_layer(ctx, layer, c, chunk, hidden, state)
+        last = hidden[chunk - 1:chunk]
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for step in range(steps):
+            ctx.check(lib.adi_hip_rms_norm(ctx.handle, last.data_ptr(), final_norm.data_ptr(), HIDDEN,
+                                           1, 1.0, 1e-6, normed.data_ptr()))
+            hip.head_matmul(ctx, head, normed, 1, logits)
+            hip.argmax_rows(ctx, logits, 1, vocab, token)
+            hip.embedding_rows(ctx, emb, token, 1, hidden)
+            last = hidden[0:1]
+            for layer, (state, _) in zip(layers, states):
+                hip.decode_layer(ctx, layer, prompt + step, last, state)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        return t1 - t0, t2 - t1
+
+    run()  # warm-up: workspaces, kernels
+    prefill_s, decode_s = run()
+    return {"hybrid4_2048": {
+        "prefill_tokens_per_s": round(prompt / prefill_s, 1),
+        "prefill_ms": round(prefill_s * 1e3, 2),
+        "decode_ms_per_token": round(decode_s / steps * 1e3, 3),
+        "decode_tokens_per_s": round(steps / decode_s, 1),
+        "layers": 4, "prompt": prompt, "ubatch": chunk, "greedy_steps": steps}}
 
 
 def main():
