@@ -662,9 +662,49 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
             }
         }
 
+        // the down-projection GEMV (decode path); for one row it builds its
+        // x_hat from the gate/up slices itself, so step 5 launches nothing
+        MoeGemv dn{};
+        if (!mfma) {
+            ExpertGemv &g = dn.expert[0];
+            g.gamma_stride = gamma_stride;
+            g.rows = H;
+            g.columns = I;
+            g.trellis_stride = d_words;
+            g.z_split_stride = P * H;
+            g.trellis = L->down.trellis;
+            g.gamma = L->down.wave_gamma_f16;
+            g.x_hat = xh_down;
+            g.z = z_down;
+            dn.expert_count = 1;
+            NeGemv &n = dn.ne[0];
+            n.batch = batch;
+            n.rows = H;
+            n.columns = I;
+            n.z_split_stride = B * H;
+            n.trellis = L->shared_down.trellis;
+            n.weight_scale = L->shared_down.weight_scale;
+            n.x_hat = sxh_down;
+            n.z = sz_down;
+            dn.ne_count = 1;
+            dn.expert_book = L->expert_codebook->data;
+            dn.slot_info = slot_info;
+            dn.ne_book = L->shared_down.codebook->data;
+            dn.max_active = max_active;
+            if (batch == 1 && wave_path && trellis_gemv_can_fuse_swiglu(ctx, dn)) {
+                dn.fused_swiglu = 1;
+                dn.swiglu = GemvSwiglu{z_gate, z_up, P * I, sg, L->gate.sv_f16, L->up.sv_f16,
+                                       L->down.su_f16, sz_gate, sz_up, B * I, ssg,
+                                       L->shared_gate.sv, L->shared_up.sv, L->shared_down.su,
+                                       hadamard_scale(I)};
+            }
+        }
+
         // 5: SwiGLU and the down prologue
         const float scale_i = hadamard_scale(I);
-        if (wave_path) {
+        if (dn.fused_swiglu != 0) {
+            // built inside the down GEMV
+        } else if (wave_path) {
             SwigluJobs sj{};
             sj.segments = 2;
             sj.scale = scale_i;
@@ -731,32 +771,6 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
             sdn.ne_book = L->shared_down.codebook->data;
             launch_ne_mfma(ctx, sdn);
         } else {
-            MoeGemv dn{};
-            ExpertGemv &g = dn.expert[0];
-            g.gamma_stride = gamma_stride;
-            g.rows = H;
-            g.columns = I;
-            g.trellis_stride = d_words;
-            g.z_split_stride = P * H;
-            g.trellis = L->down.trellis;
-            g.gamma = L->down.wave_gamma_f16;
-            g.x_hat = xh_down;
-            g.z = z_down;
-            dn.expert_count = 1;
-            NeGemv &n = dn.ne[0];
-            n.batch = batch;
-            n.rows = H;
-            n.columns = I;
-            n.z_split_stride = B * H;
-            n.trellis = L->shared_down.trellis;
-            n.weight_scale = L->shared_down.weight_scale;
-            n.x_hat = sxh_down;
-            n.z = sz_down;
-            dn.ne_count = 1;
-            dn.expert_book = L->expert_codebook->data;
-            dn.slot_info = slot_info;
-            dn.ne_book = L->shared_down.codebook->data;
-            dn.max_active = max_active;
             launch_trellis_gemv(ctx, dn);
         }
 

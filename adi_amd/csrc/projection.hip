@@ -435,7 +435,8 @@ __device__ __forceinline__ void expert_tiles(const ExpertGemv &a, uint32_t item,
 }
 
 __device__ __forceinline__ void expert_prefetch(const MoeGemv &m, const uint4 *slots, uint32_t i,
-                                                uint32_t half, uint32_t lane, ExpertStage &st) {
+                                                uint32_t half, uint32_t lane, ExpertStage &st,
+                                                const float *x_lds = nullptr) {
     const ExpertItem it = expert_item_of(m, i);
     const ExpertGemv &a = m.expert[it.which];
     const uint4 info = slots[it.slot];
@@ -464,7 +465,9 @@ __device__ __forceinline__ void expert_prefetch(const MoeGemv &m, const uint4 *s
             st.gamma[g] = half_bits_to_float(gamma_row[wave_slot(tr, tc, a.tile_rows, tile_columns)]);
         }
     }
-    load_x_pair(a.x_hat, a.columns, st.info.y, column, groups, valid, st.x);
+    // a fused SwiGLU's x_hat sits in LDS for the item's single position
+    load_x_pair(x_lds != nullptr ? x_lds : a.x_hat, a.columns, x_lds != nullptr ? 0u : st.info.y,
+                column, groups, valid, st.x);
 }
 
 __device__ __forceinline__ void expert_compute(const MoeGemv &m, uint32_t i, uint32_t half,
@@ -583,7 +586,7 @@ __device__ __forceinline__ void load_x16(const float *x_hat, uint32_t columns, u
 }
 
 __device__ __forceinline__ void ne_prefetch(const MoeGemv &m, uint32_t k, uint32_t lane,
-                                            NeStage &st) {
+                                            NeStage &st, const float *x_lds = nullptr) {
     const uint2 it = ne_item_of(m, k);
     const NeGemv &a = m.ne[it.x];
     uint32_t tile, column;
@@ -599,7 +602,7 @@ __device__ __forceinline__ void ne_prefetch(const MoeGemv &m, uint32_t k, uint32
     }
     st.d[0] = lo.x; st.d[1] = lo.y; st.d[2] = lo.z; st.d[3] = lo.w;
     st.d[4] = hi.x; st.d[5] = hi.y; st.d[6] = hi.z; st.d[7] = hi.w;
-    load_x16(a.x_hat, a.columns, 0, column, valid && a.batch > 0, st.x);
+    load_x16(x_lds != nullptr ? x_lds : a.x_hat, a.columns, 0, column, valid && a.batch > 0, st.x);
 }
 
 // Row sums over all 16 columns of each tile with the signed table in LDS,
@@ -651,20 +654,148 @@ __device__ __forceinline__ void ne_compute(const MoeGemv &m, uint32_t k, const u
     }
 }
 
+// One row's SwiGLU into x_hat (width 512, the wave layout), as the MoE's
+// swiglu launch computes it (src/executor.cpp:300-312): the routed row of
+// grouped position `row` with expert `expert`'s f16 scales, or the shared
+// expert's with its signs. Split in two so that the scale and first four
+// slice loads go out before the codebook plane's (loads return in order).
+struct SwigluInputs {
+    float sa[kFusedSwigluWidth / 64], sb[kFusedSwigluWidth / 64], sc[kFusedSwigluWidth / 64];
+    float g[4][kFusedSwigluWidth / 64], u[4][kFusedSwigluWidth / 64];
+};
+
+__device__ __forceinline__ void swiglu_issue(const GemvSwiglu &f, bool shared, uint32_t row,
+                                             uint32_t expert, uint32_t lane, SwigluInputs &in) {
+    constexpr int VPL = kFusedSwigluWidth / 64;
+    constexpr uint32_t n = kFusedSwigluWidth;
+    const float *zg = shared ? f.shared_z_gate : f.z_gate + static_cast<size_t>(row) * n;
+    const float *zu = shared ? f.shared_z_up : f.z_up + static_cast<size_t>(row) * n;
+    const size_t stride = shared ? f.shared_split_stride : f.split_stride;
+    const uint32_t splits = shared ? f.shared_splits : f.splits;
+    if (shared) {
+        load_wave_sign<VPL>(f.shared_sv_gate, lane, in.sa);
+        load_wave_sign<VPL>(f.shared_sv_up, lane, in.sb);
+        load_wave_sign<VPL>(f.shared_su_down, lane, in.sc);
+    } else {
+        const size_t mat = static_cast<size_t>(expert) * n;
+        load_wave_f16<VPL>(f.sv_gate + mat, lane, in.sa);
+        load_wave_f16<VPL>(f.sv_up + mat, lane, in.sb);
+        load_wave_f16<VPL>(f.su_down + mat, lane, in.sc);
+    }
+#pragma unroll
+    for (uint32_t s = 0; s < 4; ++s) {
+        const uint32_t at = s < splits ? s : splits - 1u;  // a missing slice reloads the last
+        load_wave<VPL>(zg + at * stride, lane, in.g[s]);
+        load_wave<VPL>(zu + at * stride, lane, in.u[s]);
+    }
+}
+
+__device__ __forceinline__ void swiglu_finish(const GemvSwiglu &f, bool shared, uint32_t row,
+                                              uint32_t lane, SwigluInputs &in,
+                                              float (&out)[kFusedSwigluWidth / 64]) {
+#pragma clang fp contract(off)
+    constexpr int VPL = kFusedSwigluWidth / 64;
+    constexpr uint32_t n = kFusedSwigluWidth;
+    const float *zg = shared ? f.shared_z_gate : f.z_gate + static_cast<size_t>(row) * n;
+    const float *zu = shared ? f.shared_z_up : f.z_up + static_cast<size_t>(row) * n;
+    const size_t stride = shared ? f.shared_split_stride : f.split_stride;
+    const uint32_t splits = shared ? f.shared_splits : f.splits;
+    float gv[VPL], uv[VPL];
+    // the slice-order sums of sum_slices: 0 + slice 0 + slice 1 + ...
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        gv[i] = 0.0f + in.g[0][i];
+        uv[i] = 0.0f + in.u[0][i];
+    }
+#pragma unroll
+    for (uint32_t s = 1; s < 4; ++s) {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            gv[i] = s < splits ? gv[i] + in.g[s][i] : gv[i];
+            uv[i] = s < splits ? uv[i] + in.u[s][i] : uv[i];
+        }
+    }
+    for (uint32_t s = 4; s < splits; ++s) {
+        float a[VPL], c[VPL];
+        load_wave<VPL>(zg + s * stride, lane, a);
+        load_wave<VPL>(zu + s * stride, lane, c);
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            gv[i] = gv[i] + a[i];
+            uv[i] = uv[i] + c[i];
+        }
+    }
+    wave_hadamard<VPL>(gv, f.scale, lane);
+    wave_hadamard<VPL>(uv, f.scale, lane);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const float g = gv[i] * in.sa[i];
+        gv[i] = g / (1.0f + expf(-g)) * (uv[i] * in.sb[i]) * in.sc[i];
+    }
+    wave_hadamard<VPL>(gv, f.scale, lane);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        out[i] = gv[i];
+    }
+}
+
+// Slot of expert item i (one expert entry).
+__device__ __forceinline__ uint32_t item_slot(const MoeGemv &m, uint32_t i) {
+    return expert_item_of(m, i).slot;
+}
+
 // Block b serves component plane (b / 8) % 2 as worker ((b / 16) * 8 + b % 8),
 // so the two blocks that walk the same tiles sit on the same XCD (blocks are
 // dealt to the eight XCDs round robin) and share its L2. Each wave walks its
 // expert items, then its share of the NE items, with the loads of item k+1
 // issued before the arithmetic of item k.
 __global__ __launch_bounds__(kGemvThreads) void k_trellis_gemv(MoeGemv m) {
-    extern __shared__ uint4 lds_dynamic[];  // [slot_capacity] slots, then the plane
+    // [slot_capacity] slots, then the plane; with a fused SwiGLU then the
+    // shared expert's x_hat and one routed x_hat per wave
+    extern __shared__ uint4 lds_dynamic[];
     __shared__ uint32_t ne_table[1024];
     uint4 *slots = lds_dynamic;
     uint4 *plane_lds = lds_dynamic + m.slot_capacity;
+    float *shared_x_lds = reinterpret_cast<float *>(plane_lds + (m.expert_count > 0 ? kPlaneBytes / 16 : 0));
     const uint32_t b = blockIdx.x;
     const uint32_t half = (b >> 3) & 1u;
     const uint32_t worker = ((b >> 4) << 3) | (b & 7u);
     const uint32_t workers = gridDim.x >> 1;
+    const uint32_t my_wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // A fused SwiGLU: the first wave of each run of items with the same slot
+    // in this block builds that slot's x_hat (the block's items are
+    // consecutive, so usually wave 0 alone), the last wave the shared
+    // expert's; their loads go out before the plane's.
+    const uint32_t item0 = worker * kGemvWaves;
+    uint32_t owner = my_wave;  // the wave whose LDS x_hat this wave's expert item reads
+    bool routed_owner = false, shared_owner = false;
+    uint4 owner_info = make_uint4(0u, 0u, 0u, 0u);
+    SwigluInputs routed_in, shared_in;
+    if (m.fused_swiglu != 0) {
+        const uint32_t lane = threadIdx.x & 63u;
+        const uint32_t item = item0 + my_wave;
+        if (item < m.expert_items) {
+            while (owner > 0 && item_slot(m, item0 + owner - 1u) == item_slot(m, item0 + owner)) {
+                --owner;
+            }
+            routed_owner = owner == my_wave;
+            if (routed_owner) {
+                const uint4 info = m.slot_info[item_slot(m, item)];
+                owner_info = make_uint4(__builtin_amdgcn_readfirstlane(info.x),
+                                        __builtin_amdgcn_readfirstlane(info.y),
+                                        __builtin_amdgcn_readfirstlane(info.z), 0u);
+                routed_owner = owner_info.z > owner_info.y;
+                if (routed_owner) {
+                    swiglu_issue(m.swiglu, false, owner_info.y, owner_info.x, lane, routed_in);
+                }
+            }
+        }
+        shared_owner = my_wave == kGemvWaves - 1u && m.ne_count > 0;
+        if (shared_owner) {
+            swiglu_issue(m.swiglu, true, 0u, 0u, lane, shared_in);
+        }
+    }
+    float *wave_x_lds = shared_x_lds + kFusedSwigluWidth * (1u + owner);
     if (m.expert_count > 0) {
         // 8192 16-byte rows per plane, 16 per thread, all loads issued first
         constexpr uint32_t kPer = static_cast<uint32_t>(kPlaneBytes / 16) / kGemvThreads;
@@ -678,6 +809,19 @@ __global__ __launch_bounds__(kGemvThreads) void k_trellis_gemv(MoeGemv m) {
             slots[s] = m.slot_info != nullptr
                            ? m.slot_info[s]
                            : make_uint4(0u, 0u, s == 0 ? m.expert[0].batch : 0u, 0u);
+        }
+        // while the plane is in flight: the owners' x_hat into LDS
+        if (routed_owner || shared_owner) {
+            const uint32_t lane = threadIdx.x & 63u;
+            float x[kFusedSwigluWidth / 64];
+            if (routed_owner) {
+                swiglu_finish(m.swiglu, false, owner_info.y, lane, routed_in, x);
+                store_wave<kFusedSwigluWidth / 64>(wave_x_lds, lane, x);
+            }
+            if (shared_owner) {
+                swiglu_finish(m.swiglu, true, 0u, lane, shared_in, x);
+                store_wave<kFusedSwigluWidth / 64>(shared_x_lds, lane, x);
+            }
         }
 #pragma unroll
         for (uint32_t u = 0; u < kPer; ++u) {
@@ -699,7 +843,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_trellis_gemv(MoeGemv m) {
     uint32_t i = worker * kGemvWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (i < m.expert_items) {
         ExpertStage s0, s1;
-        expert_prefetch(m, slots, i, half, lane, s0);
+        expert_prefetch(m, slots, i, half, lane, s0, m.fused_swiglu != 0 ? wave_x_lds : nullptr);
         while (true) {
             uint32_t j = i + stride;
             if (j < m.expert_items) {
@@ -725,11 +869,13 @@ __global__ __launch_bounds__(kGemvThreads) void k_trellis_gemv(MoeGemv m) {
     const uint32_t end = m.half_items[half];
     if (i < end) {
         NeStage s0, s1;
-        ne_prefetch(m, (i - m.expert_items) * 2u + half, lane, s0);
+        ne_prefetch(m, (i - m.expert_items) * 2u + half, lane, s0,
+                    m.fused_swiglu != 0 ? shared_x_lds : nullptr);
         while (true) {
             uint32_t j = i + stride;
             if (j < end) {
-                ne_prefetch(m, (j - m.expert_items) * 2u + half, lane, s1);
+                ne_prefetch(m, (j - m.expert_items) * 2u + half, lane, s1,
+                            m.fused_swiglu != 0 ? shared_x_lds : nullptr);
             }
             ne_compute(m, (i - m.expert_items) * 2u + half, ne_table, lane, s0);
             i = j;
@@ -738,7 +884,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_trellis_gemv(MoeGemv m) {
             }
             j = i + stride;
             if (j < end) {
-                ne_prefetch(m, (j - m.expert_items) * 2u + half, lane, s0);
+                ne_prefetch(m, (j - m.expert_items) * 2u + half, lane, s0,
+                            m.fused_swiglu != 0 ? shared_x_lds : nullptr);
             }
             ne_compute(m, (i - m.expert_items) * 2u + half, ne_table, lane, s1);
             i = j;
@@ -862,7 +1009,8 @@ void launch_epilogue_sign(adi_hip_context *ctx, const float *z, uint32_t splits,
            static_cast<const uint32_t *>(nullptr), hadamard_scale(n), out);
 }
 
-void launch_trellis_gemv(adi_hip_context *ctx, MoeGemv &m) {
+// Fills the launch geometry of `m`; returns the grid (0: nothing to do).
+uint32_t plan_trellis_gemv(adi_hip_context *ctx, MoeGemv &m) {
     require(m.expert_count <= 2 && m.ne_count <= 2, "trellis GEMV: too many matrices");
     require(m.expert_count == 0 || m.expert_book != nullptr, "trellis GEMV: expert codebook missing");
     require(m.ne_count == 0 || m.ne_book != nullptr, "trellis GEMV: NE codebook missing");
@@ -905,16 +1053,37 @@ void launch_trellis_gemv(adi_hip_context *ctx, MoeGemv &m) {
     m.half_items[0] = m.expert_items + (m.ne_items + 1) / 2;
     m.half_items[1] = m.expert_items + m.ne_items / 2;
     if (m.half_items[0] == 0) {
-        return;
+        return 0;
     }
     // persistent grid: at most one block per CU, a multiple of 16 blocks
     const uint32_t needed_workers = ceil_div(m.half_items[0], kGemvWaves);
     uint32_t blocks = 16u * ceil_div(needed_workers, 8);
     const uint32_t cap = ctx->cu_count >= 16 ? ctx->cu_count / 16 * 16 : 16u;
-    blocks = blocks < cap ? blocks : cap;
-    const size_t lds = size_t(m.slot_capacity) * 16 + (m.expert_count > 0 ? kPlaneBytes : 0);
-    static const bool ready = set_lds_limit(reinterpret_cast<const void *>(&k_trellis_gemv),
-                                            kPlaneBytes + size_t(kMaxSlots) * 16);
+    return blocks < cap ? blocks : cap;
+}
+
+bool trellis_gemv_can_fuse_swiglu(adi_hip_context *ctx, MoeGemv m) {
+    const uint32_t blocks = plan_trellis_gemv(ctx, m);
+    return blocks > 0 && m.expert_count == 1 && m.slot_info != nullptr &&
+           m.expert[0].columns == kFusedSwigluWidth &&
+           (m.ne_count == 0 || m.ne[0].columns == kFusedSwigluWidth) &&
+           m.expert_items <= (blocks / 2) * kGemvWaves;
+}
+
+void launch_trellis_gemv(adi_hip_context *ctx, MoeGemv &m) {
+    require(m.fused_swiglu == 0 || trellis_gemv_can_fuse_swiglu(ctx, m),
+            "trellis GEMV: the fused SwiGLU needs one row and one expert item per wave");
+    const uint32_t blocks = plan_trellis_gemv(ctx, m);
+    if (blocks == 0) {
+        return;
+    }
+    const size_t lds = size_t(m.slot_capacity) * 16 + (m.expert_count > 0 ? kPlaneBytes : 0) +
+                       (m.fused_swiglu != 0 ? size_t(1 + kGemvWaves) * kFusedSwigluWidth * 4 : 0);
+    // LDS is 160 KiB; the kernel's static NE table takes 4 KiB
+    constexpr size_t kMaxDynamic = 160 * 1024 - 4096;
+    require(lds <= kMaxDynamic, "trellis GEMV: LDS plan exceeds 156 KiB");
+    static const bool ready =
+        set_lds_limit(reinterpret_cast<const void *>(&k_trellis_gemv), kMaxDynamic);
     (void)ready;
     launch(ctx, "moe_gemv", k_trellis_gemv, dim3(blocks), dim3(kGemvThreads), lds, m);
 }

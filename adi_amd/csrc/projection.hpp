@@ -142,6 +142,29 @@ struct NeGemv {
     uint32_t tc_shift;      // log2(tile columns)
 };
 
+// One row's SwiGLU, for a down-projection GEMV that builds its own x_hat:
+// x_hat = H(su_down * silu(sv_gate * H(sum z_gate)) * (sv_up * H(sum z_up)))
+// of the routed slot's grouped row (f16 scales of its expert) and of the
+// shared expert (+-1 scales), width 512.
+struct GemvSwiglu {
+    const float *z_gate;        // [splits][rows][512] by grouped row
+    const float *z_up;
+    size_t split_stride;
+    uint32_t splits;
+    const uint16_t *sv_gate;    // [experts][512] f16
+    const uint16_t *sv_up;
+    const uint16_t *su_down;
+    const float *shared_z_gate; // [shared_splits][1][512]
+    const float *shared_z_up;
+    size_t shared_split_stride;
+    uint32_t shared_splits;
+    const int8_t *shared_sv_gate;
+    const int8_t *shared_sv_up;
+    const int8_t *shared_su_down;
+    float scale;                // 1 / sqrt(512)
+};
+constexpr uint32_t kFusedSwigluWidth = 512;
+
 // Up to two expert GEMVs (same shape and routing, one codebook) and two NE
 // GEMVs (same shape, one codebook) in one persistent launch.
 struct MoeGemv {
@@ -153,6 +176,10 @@ struct MoeGemv {
     const void *ne_book;      // NE signed table
     const uint4 *slot_info;   // [max_active] {expert, first, end, 0}; null: one matrix
     uint32_t max_active;      // routed slots per expert entry (1 for a single matrix)
+    // nonzero: one row, one expert item per wave at most; x_hat of the expert
+    // and NE entries comes from `swiglu` (their x_hat pointers are unused)
+    uint32_t fused_swiglu;
+    GemvSwiglu swiglu;
     // set by the launcher
     uint32_t slot_capacity;
     uint32_t expert_items_per_slot;  // a power of two
@@ -163,6 +190,10 @@ struct MoeGemv {
     uint32_t half_items[2];
 };
 void launch_trellis_gemv(adi_hip_context *ctx, MoeGemv &m);
+// Whether `m` (a down projection of one row) can build its x_hat from
+// m.swiglu in the launch: one expert entry of width 512 and at most one
+// expert item per wave.
+bool trellis_gemv_can_fuse_swiglu(adi_hip_context *ctx, MoeGemv m);
 
 void validate_expert(const adi_hip_expert_matrix *m);
 void validate_ne(const adi_hip_ne_matrix *m);
