@@ -4,6 +4,7 @@
 // head's logits to the next step's hidden state without leaving HBM.
 #include "context.hpp"
 
+#include <algorithm>
 #include <cmath>
 
 namespace adi_hip {
@@ -126,22 +127,12 @@ __device__ __forceinline__ void better(float &value, uint32_t &index, float v, u
     }
 }
 
-// One block per row: each thread scans a strided share, then wave and block
-// reductions of (value, index); any non-finite logit marks the row.
-__global__ __launch_bounds__(kArgmaxThreads) void k_argmax_rows(const float *logits,
-                                                                uint32_t count,
-                                                                uint32_t *tokens) {
+// Wave and block reductions of a thread's (value, index, bad); thread 0 of
+// the block returns the block's answer.
+__device__ __forceinline__ void argmax_block(float &value, uint32_t &index, uint32_t &bad) {
     __shared__ float wave_value[kArgmaxThreads / kWave];
     __shared__ uint32_t wave_index[kArgmaxThreads / kWave];
     __shared__ uint32_t wave_bad[kArgmaxThreads / kWave];
-    const float *row = logits + static_cast<size_t>(blockIdx.x) * count;
-    float value = -__builtin_huge_valf();
-    uint32_t index = 0xFFFFFFFFu;
-    uint32_t bad = 0;
-    for_each_logit(row, count, [&](uint32_t i, float v) {
-        bad |= __builtin_isfinite(v) ? 0u : 1u;
-        better(value, index, v, i);
-    });
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1) {
         const float v = __shfl_xor(value, offset);
@@ -161,8 +152,107 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_argmax_rows(const float *log
             better(value, index, wave_value[w], wave_index[w]);
             bad |= wave_bad[w];
         }
+    }
+}
+
+// One block per row: each thread scans a strided share, then wave and block
+// reductions of (value, index); any non-finite logit marks the row.
+__global__ __launch_bounds__(kArgmaxThreads) void k_argmax_rows(const float *logits,
+                                                                uint32_t count,
+                                                                uint32_t *tokens) {
+    const float *row = logits + static_cast<size_t>(blockIdx.x) * count;
+    float value = -__builtin_huge_valf();
+    uint32_t index = 0xFFFFFFFFu;
+    uint32_t bad = 0;
+    for_each_logit(row, count, [&](uint32_t i, float v) {
+        bad |= __builtin_isfinite(v) ? 0u : 1u;
+        better(value, index, v, i);
+    });
+    argmax_block(value, index, bad);
+    if (threadIdx.x == 0) {
         tokens[blockIdx.x] = bad != 0u ? 0xFFFFFFFFu : index;
     }
+}
+
+// A long row splits into `gridDim.x` spans of `span` logits (a multiple of 4,
+// so an aligned row keeps its spans aligned); block (p, r) reduces span p of
+// row r into partial p of that row. The answer does not depend on the split:
+// better() keeps the larger value and, among equal values, the lower index.
+constexpr uint32_t kArgmaxPartThreads = 256;
+constexpr uint32_t kArgmaxMaxParts = 64;
+constexpr uint32_t kArgmaxSplitCount = 32768;  // shorter rows take one block
+
+__global__ __launch_bounds__(kArgmaxPartThreads) void k_argmax_parts(
+    const float *logits, uint32_t count, uint32_t span, float *part_value,
+    uint32_t *part_index) {
+    const uint32_t begin = blockIdx.x * span;
+    const uint32_t end = begin + span < count ? begin + span : count;
+    const float *row = logits + static_cast<size_t>(blockIdx.y) * count + begin;
+    float value = -__builtin_huge_valf();
+    uint32_t index = 0xFFFFFFFFu;
+    uint32_t bad = 0;
+    for_each_logit(row, end - begin, [&](uint32_t i, float v) {
+        bad |= __builtin_isfinite(v) ? 0u : 1u;
+        better(value, index, v, begin + i);
+    });
+    argmax_block(value, index, bad);
+    if (threadIdx.x == 0) {
+        const size_t slot = static_cast<size_t>(blockIdx.y) * gridDim.x + blockIdx.x;
+        part_value[slot] = value;
+        part_index[slot] = bad != 0u ? 0xFFFFFFFFu : index;
+    }
+}
+
+// One wave per row folds that row's `parts` partials; a partial index of
+// 0xFFFFFFFF marks a span that held a non-finite logit (every span holds at
+// least one logit, so no finite span reports that index).
+__global__ __launch_bounds__(kWave) void k_argmax_finish(const float *part_value,
+                                                         const uint32_t *part_index,
+                                                         uint32_t parts, uint32_t *tokens) {
+    const size_t base = static_cast<size_t>(blockIdx.x) * parts;
+    float value = -__builtin_huge_valf();
+    uint32_t index = 0xFFFFFFFFu;
+    uint32_t bad = 0;
+    for (uint32_t p = threadIdx.x; p < parts; p += kWave) {
+        const uint32_t i = part_index[base + p];
+        bad |= i == 0xFFFFFFFFu ? 1u : 0u;
+        better(value, index, part_value[base + p], i);
+    }
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        const float v = __shfl_xor(value, offset);
+        const uint32_t i = static_cast<uint32_t>(__shfl_xor(static_cast<int>(index), offset));
+        better(value, index, v, i);
+        bad |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(bad), offset));
+    }
+    if (threadIdx.x == 0) {
+        tokens[blockIdx.x] = bad != 0u ? 0xFFFFFFFFu : index;
+    }
+}
+
+// Greedy choice of every row: rows of at least kArgmaxSplitCount logits split
+// over up to kArgmaxMaxParts blocks each (a 248,320-logit row is one block's
+// worth of latency otherwise), shorter rows take one block.
+void launch_argmax(adi_hip_context *ctx, const float *logits, uint32_t rows, uint32_t count,
+                   uint32_t *tokens) {
+    if (count < kArgmaxSplitCount || rows > 65535u) {
+        launch(ctx, "argmax", k_argmax_rows, dim3(rows), dim3(kArgmaxThreads), 0, logits, count,
+               tokens);
+        return;
+    }
+    const uint32_t wanted = std::min<uint32_t>(kArgmaxMaxParts, ceil_div(count, 4096));
+    const uint32_t span = (ceil_div(count, wanted) + 3u) & ~3u;
+    const uint32_t parts = ceil_div(count, span);
+    auto &ws = ctx->workspace;
+    ws.used = 0;
+    ws.ensure(Workspace::round(size_t(rows) * parts * 4) * 2);
+    float *part_value = ws.take<float>(size_t(rows) * parts);
+    uint32_t *part_index = ws.take<uint32_t>(size_t(rows) * parts);
+    launch(ctx, "argmax_parts", k_argmax_parts, dim3(parts, rows), dim3(kArgmaxPartThreads), 0,
+           logits, count, span, part_value, part_index);
+    launch(ctx, "argmax_finish", k_argmax_finish, dim3(rows), dim3(kWave), 0,
+           static_cast<const float *>(part_value), static_cast<const uint32_t *>(part_index),
+           parts, tokens);
 }
 
 // ---- top-p sampling ----------------------------------------------------------
@@ -511,8 +601,7 @@ int adi_hip_argmax_rows(adi_hip_context *ctx, const float *logits, uint32_t rows
         if (rows == 0) {
             return;
         }
-        launch(ctx, "argmax", k_argmax_rows, dim3(rows), dim3(kArgmaxThreads), 0, logits, count,
-               tokens);
+        launch_argmax(ctx, logits, rows, count, tokens);
     });
 }
 
@@ -532,8 +621,7 @@ int adi_hip_sample_rows(adi_hip_context *ctx, const float *logits, uint32_t rows
             return;
         }
         if (temperature == 0.0f) {
-            launch(ctx, "argmax", k_argmax_rows, dim3(rows), dim3(kArgmaxThreads), 0, logits,
-                   count, tokens);
+            launch_argmax(ctx, logits, rows, count, tokens);
             return;
         }
         launch(ctx, "sample", k_sample_rows, dim3(rows), dim3(kSampleThreads), 0, logits, count,

@@ -73,6 +73,29 @@ def test_argmax_rows(gpu, oracle):
     assert got[1] == 5 and got[2] == 100 and got[5] == count - 1
 
 
+@pytest.mark.parametrize("count", [1, 5, 4097, 32767, 32768, 32771, 248320, 262147])
+def test_argmax_rows_split_and_unaligned(gpu, oracle, count):
+    """Rows of 32,768 logits and more split over up to 64 blocks; odd counts
+    leave every other row unaligned. Ties across spans keep the first index
+    and a non-finite logit in any span marks its row."""
+    rng = np.random.default_rng(count)
+    rows = 5
+    logits = rng.normal(0, 3, (rows, count)).astype(np.float32)
+    logits[1, [count - 1, count // 2, 0]] = 30.0                 # first of three ties
+    logits[2, count - 1] = 31.0
+    logits[3, count // 3] = np.nan
+    logits[4, count - 1] = -np.inf
+    t = torch.empty(rows, dtype=torch.int32, device="cuda")
+    hip.argmax_rows(gpu, torch.from_numpy(logits).cuda(), rows, count, t)
+    got = t.cpu().numpy().view(np.uint32)
+    for r in range(rows):
+        row = np.ascontiguousarray(logits[r])
+        finite = np.isfinite(row).all()
+        want = oracle.ao_argmax(po.ptr(row, po.C.c_float), count) if finite else 0xFFFFFFFF
+        assert got[r] == want, (count, r)
+    assert got[1] == 0 and got[2] == count - 1
+
+
 def test_embedding_from_checkpoint(gpu, oracle, tmp_path):
     layer = syn.moe_layer(syn.rng_for(22, 3), hidden=256, expert_hidden=64, experts=32)
     e = syn.embedding(syn.rng_for(22, 4), 500, 256, exceptions=300)
