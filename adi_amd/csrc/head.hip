@@ -153,6 +153,175 @@ __global__ __launch_bounds__(256) void k_head_gemv(
     }
 }
 
+// Sums V per-lane values over the 64 lanes of a wave by halving exchanges:
+// at offset 1 a lane keeps one half of its values and sends the other, then
+// at offset 2 half of the rest, until one value is left, which the remaining
+// offsets sum over all lanes. `which` says which value the lane ends with;
+// lanes 0..V-1 hold all V. Every value is summed over the same pair tree as
+// a full xor butterfly with offsets 1, 2, ..., 32, so the sums are
+// bit-identical to it.
+__device__ __forceinline__ bool first_max_before(float a, uint32_t ia, float b, uint32_t ib) {
+    return a == b ? ia < ib : a > b;
+}
+
+// Per-wave summaries the 2048-column GEMV leaves for the certified arg-max,
+// [batch][waves] each: the wave's first maximum logit and its row
+// (0xFFFFFFFF for a wave with no rows), and the largest
+// fmaf(factor, bound, logit) over the wave's rows.
+struct HeadWaveBest {
+    float factor;
+    float *value;
+    uint32_t *index;
+    float *upper;
+};
+
+template <int V>
+__device__ __forceinline__ float reduce_scatter64(float (&v)[V], uint32_t lane,
+                                                  uint32_t &which) {
+#pragma clang fp contract(off)
+    uint32_t off = 1;
+    which = 0;
+#pragma unroll
+    for (int h = V / 2; h >= 1; h /= 2) {
+        const bool hi = (lane & off) != 0u;
+#pragma unroll
+        for (int i = 0; i < h; ++i) {
+            const float send = hi ? v[i] : v[i + h];
+            const float keep = hi ? v[i + h] : v[i];
+            v[i] = keep + __shfl_xor(send, static_cast<int>(off));
+        }
+        which += hi ? static_cast<uint32_t>(h) : 0u;
+        off <<= 1;
+    }
+    for (; off < 64u; off <<= 1) {
+        v[0] += __shfl_xor(v[0], static_cast<int>(off));
+    }
+    return v[0];
+}
+
+// k_head_gemv for 2048 columns (64 quads: one row per wave per pass), with
+// the next row's codes loaded while this row is summed, the lane sums
+// reduce-scattered, and the bound sums only when they are wanted.
+template <int NT, bool BOUNDS>
+__global__ __launch_bounds__(256) void k_head_gemv_2048(
+    const uint8_t *__restrict__ packed, const uint16_t *__restrict__ scales, uint32_t rows,
+    const float *__restrict__ x, const float *__restrict__ sums,
+    const float *__restrict__ abs_sums, uint32_t batch, float *__restrict__ logits,
+    float *__restrict__ bounds, HeadWaveBest best) {
+    // no contraction: a lane's logit stays a rounded product in every variant
+    // (with the bounds or without), so both variants give the same bits
+#pragma clang fp contract(off)
+    constexpr uint32_t columns = 2048u, quads = 64u, groups = 32u;
+    constexpr int V = BOUNDS ? 2 * NT : NT;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave_global = blockIdx.x * (blockDim.x / 64u) + (threadIdx.x >> 6);
+    const uint32_t wave_count = gridDim.x * (blockDim.x / 64u);
+    const uint32_t *codes = reinterpret_cast<const uint32_t *>(packed);
+
+    for (uint32_t t0 = 0; t0 < batch; t0 += NT) {
+        float xv[NT][kQuadColumns];
+        float sx[NT], sa[NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const uint32_t t = t0 + j < batch ? t0 + j : t0;
+            const float4 *src = reinterpret_cast<const float4 *>(
+                x + static_cast<size_t>(t) * columns + lane * kQuadColumns);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float4 v = src[q];
+                xv[j][4 * q] = v.x;
+                xv[j][4 * q + 1] = v.y;
+                xv[j][4 * q + 2] = v.z;
+                xv[j][4 * q + 3] = v.w;
+            }
+            sx[j] = sums[static_cast<size_t>(t) * quads + lane];
+            sa[j] = abs_sums[static_cast<size_t>(t) * quads + lane];
+        }
+        // with the bounds, even lanes end a row with a logit and their odd
+        // partners with its bound (the first halving exchange is at offset 1)
+        float best_v = -INFINITY, upper = -INFINITY;
+        uint32_t best_i = 0xFFFFFFFFu;
+        uint32_t row = wave_global;
+        uint32_t dn[5] = {0u, 0u, 0u, 0u, 0u};
+        uint16_t sn = 0;
+        if (row < rows) {
+            const uint32_t *src = codes + (static_cast<size_t>(row) * quads + lane) * 5u;
+#pragma unroll
+            for (int i = 0; i < 5; ++i) {
+                dn[i] = __builtin_nontemporal_load(src + i);
+            }
+            sn = scales[static_cast<size_t>(row) * groups + lane / 2u];
+        }
+        for (; row < rows; row += wave_count) {
+            uint32_t d[6] = {dn[0], dn[1], dn[2], dn[3], dn[4], 0u};
+            const float scale = half_bits_to_float(sn);
+            const uint32_t next = row + wave_count;
+            if (next < rows) {
+                const uint32_t *src = codes + (static_cast<size_t>(next) * quads + lane) * 5u;
+#pragma unroll
+                for (int i = 0; i < 5; ++i) {
+                    dn[i] = __builtin_nontemporal_load(src + i);
+                }
+                sn = scales[static_cast<size_t>(next) * groups + lane / 2u];
+            }
+            float u[kQuadColumns];
+#define ADI_CODE(K) u[K] = code_at<K>(d);
+            ADI_CODE(0) ADI_CODE(1) ADI_CODE(2) ADI_CODE(3) ADI_CODE(4) ADI_CODE(5) ADI_CODE(6)
+            ADI_CODE(7) ADI_CODE(8) ADI_CODE(9) ADI_CODE(10) ADI_CODE(11) ADI_CODE(12)
+            ADI_CODE(13) ADI_CODE(14) ADI_CODE(15) ADI_CODE(16) ADI_CODE(17) ADI_CODE(18)
+            ADI_CODE(19) ADI_CODE(20) ADI_CODE(21) ADI_CODE(22) ADI_CODE(23) ADI_CODE(24)
+            ADI_CODE(25) ADI_CODE(26) ADI_CODE(27) ADI_CODE(28) ADI_CODE(29) ADI_CODE(30)
+            ADI_CODE(31)
+#undef ADI_CODE
+            float v[V];
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 32; k += 2) {
+                    acc0 = fmaf(u[k], xv[j][k], acc0);
+                    acc1 = fmaf(u[k + 1], xv[j][k + 1], acc1);
+                }
+                v[j] = scale * ((acc0 + acc1) - 16.0f * sx[j]);
+                if constexpr (BOUNDS) {
+                    v[NT + j] = 16.0f * scale * sa[j];
+                }
+            }
+            uint32_t k;
+            const float total = reduce_scatter64<V>(v, lane, k);
+            if (lane < static_cast<uint32_t>(V)) {
+                const uint32_t j = k % NT;
+                if (t0 + j < batch) {
+                    float *dst = BOUNDS && k >= NT ? bounds : logits;
+                    dst[static_cast<size_t>(t0 + j) * rows + row] = total;
+                }
+            }
+            if constexpr (BOUNDS) {
+                const float bound = __shfl_xor(total, 1);
+                const float up = fmaf(best.factor, bound, total);
+                upper = up > upper ? up : upper;
+                if (best_i == 0xFFFFFFFFu || first_max_before(total, row, best_v, best_i)) {
+                    best_v = total;
+                    best_i = row;
+                }
+            }
+        }
+        if constexpr (BOUNDS) {
+            uint32_t j = 0;  // the token of an even lane below V (as reduce_scatter64)
+            for (uint32_t off = 1, h = V / 2; h >= 1u; h /= 2u, off <<= 1) {
+                j += (lane & off) != 0u ? h : 0u;
+            }
+            if (best.value != nullptr && (lane & 1u) == 0u && lane < static_cast<uint32_t>(V) &&
+                t0 + j < batch) {
+                const size_t at = static_cast<size_t>(t0 + j) * wave_count + wave_global;
+                best.value[at] = best_v;
+                best.index[at] = best_i;
+                best.upper[at] = upper;
+            }
+        }
+    }
+}
+
 // A row's dot in the CPU order: weights of lane j are columns j, j+LANES,
 // ...; lane sums added 0..LANES-1 from 0; then the tail (columns % LANES).
 // `weight(k)` supplies w_k. Runs on one wave; the result is valid on lane 0.
@@ -254,19 +423,74 @@ __global__ __launch_bounds__(64) void k_head_exact_rows(HeadView h, const float 
     }
 }
 
-__device__ __forceinline__ bool first_max_before(float a, uint32_t ia, float b, uint32_t ib) {
-    return a == b ? ia < ib : a > b;
-}
-
 constexpr uint32_t kArgmaxThreads = 1024;
 constexpr uint32_t kCandidateCap = 2048;
 
+// Calls f(r, logit, bound) for every row r of this thread's share of the
+// block, each row once: 16-byte loads (four of the logits in flight, or two
+// of each array with the bounds) when the arrays are 16-byte aligned, one
+// float at a time otherwise. `bound` is 0 when BOUND is false.
+template <bool BOUND, typename F>
+__device__ __forceinline__ void for_each_head_row(const float *__restrict__ a,
+                                                  const float *__restrict__ b, uint32_t count,
+                                                  F &&f) {
+    constexpr uint32_t kUnroll = BOUND ? 2u : 4u;
+    const uint32_t step = blockDim.x;
+    const uintptr_t bits =
+        reinterpret_cast<uintptr_t>(a) | (BOUND ? reinterpret_cast<uintptr_t>(b) : uintptr_t(0));
+    if ((bits & 15u) == 0u) {
+        const uint32_t vectors = count / 4u;
+        const float4 *a4 = reinterpret_cast<const float4 *>(a);
+        const float4 *b4 = reinterpret_cast<const float4 *>(b);
+        uint32_t j = threadIdx.x;
+        for (; j + (kUnroll - 1u) * step < vectors; j += kUnroll * step) {
+            float4 va[kUnroll], vb[kUnroll];
+#pragma unroll
+            for (uint32_t u = 0; u < kUnroll; ++u) {
+                va[u] = a4[j + u * step];
+                vb[u] = BOUND ? b4[j + u * step] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < kUnroll; ++u) {
+                const uint32_t i = 4u * (j + u * step);
+                f(i, va[u].x, vb[u].x);
+                f(i + 1u, va[u].y, vb[u].y);
+                f(i + 2u, va[u].z, vb[u].z);
+                f(i + 3u, va[u].w, vb[u].w);
+            }
+        }
+        for (; j < vectors; j += step) {
+            const float4 va = a4[j];
+            const float4 vb = BOUND ? b4[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            f(4u * j, va.x, vb.x);
+            f(4u * j + 1u, va.y, vb.y);
+            f(4u * j + 2u, va.z, vb.z);
+            f(4u * j + 3u, va.w, vb.w);
+        }
+        for (uint32_t i = 4u * vectors + threadIdx.x; i < count; i += step) {
+            f(i, a[i], BOUND ? b[i] : 0.0f);
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < count; i += step) {
+            f(i, a[i], BOUND ? b[i] : 0.0f);
+        }
+    }
+}
+
 // One block per row of logits: top GPU logit, candidate rows, exact
 // re-evaluation, first maximum.
-template <int LANES, bool FUSED>
+//
+// With WAVES the GEMV's per-wave summaries stand in for the scans: the top
+// logit is the first maximum of the waves' maxima, and only the rows of
+// waves whose largest fmaf(factor, bound, logit) reaches the threshold are
+// tested (a wave of `wave_count` covers rows w, w + wave_count, ...). The
+// candidate set is the same as the full scan's.
+template <int LANES, bool FUSED, bool WAVES>
 __global__ __launch_bounds__(kArgmaxThreads) void k_head_argmax(
     HeadView h, const float *__restrict__ x, const float *__restrict__ logits,
-    const float *__restrict__ bounds, float factor, uint32_t *__restrict__ argmax) {
+    const float *__restrict__ bounds, float factor, const float *__restrict__ wave_value,
+    const uint32_t *__restrict__ wave_index, const float *__restrict__ wave_upper,
+    uint32_t wave_count, uint32_t *__restrict__ argmax) {
     __shared__ float best_value[kArgmaxThreads / 64];
     __shared__ uint32_t best_index[kArgmaxThreads / 64];
     __shared__ uint32_t candidates[kCandidateCap];
@@ -282,12 +506,23 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_head_argmax(
     // 1. first maximum of the GPU logits
     float v = -INFINITY;
     uint32_t vi = 0xFFFFFFFFu;
-    for (uint32_t r = threadIdx.x; r < h.rows; r += kArgmaxThreads) {
-        const float c = row_logits[r];
-        if (vi == 0xFFFFFFFFu || first_max_before(c, r, v, vi)) {
-            v = c;
-            vi = r;
+    if constexpr (WAVES) {
+        const size_t base = static_cast<size_t>(b) * wave_count;
+        for (uint32_t w = threadIdx.x; w < wave_count; w += kArgmaxThreads) {
+            const uint32_t r = wave_index[base + w];
+            const float c = wave_value[base + w];
+            if (r != 0xFFFFFFFFu && (vi == 0xFFFFFFFFu || first_max_before(c, r, v, vi))) {
+                v = c;
+                vi = r;
+            }
         }
+    } else {
+        for_each_head_row<false>(row_logits, nullptr, h.rows, [&](uint32_t r, float c, float) {
+            if (vi == 0xFFFFFFFFu || first_max_before(c, r, v, vi)) {
+                v = c;
+                vi = r;
+            }
+        });
     }
     for (int off = 32; off >= 1; off >>= 1) {
         const float ov = __shfl_xor(v, off);
@@ -319,13 +554,25 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_head_argmax(
     __syncthreads();
     // 2. candidates: rows whose bound interval reaches the threshold
     const float t = threshold;
-    for (uint32_t r = threadIdx.x; r < h.rows; r += kArgmaxThreads) {
-        if (row_logits[r] + factor * row_bounds[r] >= t) {
+    const auto consider = [&](uint32_t r, float c, float bd) {
+        if (fmaf(factor, bd, c) >= t) {
             const uint32_t slot = atomicAdd(&candidate_count, 1u);
             if (slot < kCandidateCap) {
                 candidates[slot] = r;
             }
         }
+    };
+    if constexpr (WAVES) {
+        const size_t base = static_cast<size_t>(b) * wave_count;
+        for (uint32_t w = threadIdx.x; w < wave_count; w += kArgmaxThreads) {
+            if (wave_upper[base + w] >= t) {
+                for (uint32_t r = w; r < h.rows; r += wave_count) {
+                    consider(r, row_logits[r], row_bounds[r]);
+                }
+            }
+        }
+    } else {
+        for_each_head_row<true>(row_logits, row_bounds, h.rows, consider);
     }
     __syncthreads();
     const uint32_t count = candidate_count;
@@ -396,8 +643,21 @@ void launch_exact_parts(adi_hip_context *ctx, const HeadView &v, const float *x,
     }
 }
 
+// Blocks of the 2048-column GEMV: one row per wave per pass, enough waves
+// for four passes each.
+uint32_t head_wide_blocks(const adi_hip_context *ctx, uint32_t rows) {
+    return std::min<uint32_t>(ceil_div(rows, 4u * 4u), static_cast<uint32_t>(ctx->cu_count) * 8u);
+}
+
+// Whether head_logits can leave per-wave summaries (2048 columns, no
+// protected rows: those are rewritten after the GEMV).
+bool head_wave_best(const adi_hip_head_chunk *h) {
+    return h->columns == 2048u && h->protected_count == 0;
+}
+
 void head_logits(adi_hip_context *ctx, const adi_hip_head_chunk *h, const float *x,
-                 uint32_t batch, float *logits, float *bounds) {
+                 uint32_t batch, float *logits, float *bounds,
+                 HeadWaveBest best = HeadWaveBest{0.0f, nullptr, nullptr, nullptr}) {
     const HeadView v = view_of(h);
     const bool fast = fast_width(h->columns);
     if (fast) {
@@ -410,7 +670,17 @@ void head_logits(adi_hip_context *ctx, const adi_hip_head_chunk *h, const float 
         const uint32_t rows_per_block = 4u * (64u / quads);
         const uint32_t blocks = std::min<uint32_t>(ceil_div(h->rows, rows_per_block),
                                                    static_cast<uint32_t>(ctx->cu_count) * 8u);
-        if (batch == 1) {
+        if (quads == 64u) {
+            const uint32_t wide = head_wide_blocks(ctx, h->rows);
+            const bool with = bounds != nullptr;
+            const auto kernel = batch == 1 ? (with ? k_head_gemv_2048<1, true>
+                                                   : k_head_gemv_2048<1, false>)
+                                           : (with ? k_head_gemv_2048<4, true>
+                                                   : k_head_gemv_2048<4, false>);
+            launch(ctx, "head_gemv", kernel, dim3(wide), dim3(256), 0, h->packed,
+                   h->group_scale_f16, h->rows, x, static_cast<const float *>(sums),
+                   static_cast<const float *>(abs_sums), batch, logits, bounds, best);
+        } else if (batch == 1) {
             launch(ctx, "head_gemv", k_head_gemv<1>, dim3(blocks), dim3(256), 0, h->packed,
                    h->group_scale_f16, h->rows, h->columns, x, static_cast<const float *>(sums),
                    static_cast<const float *>(abs_sums), batch, logits, bounds);
@@ -433,10 +703,12 @@ void head_logits(adi_hip_context *ctx, const adi_hip_head_chunk *h, const float 
     }
 }
 
-size_t head_workspace(const adi_hip_head_chunk *h, uint32_t batch, bool with_logits,
-                      bool with_bounds) {
+size_t head_workspace(const adi_hip_context *ctx, const adi_hip_head_chunk *h, uint32_t batch,
+                      bool with_logits, bool with_bounds) {
     const size_t quads = h->columns / kQuadColumns;
+    const size_t waves = static_cast<size_t>(head_wide_blocks(ctx, h->rows)) * 4u;
     return Workspace::round(batch * quads * 4) * 2 +
+           (with_bounds && head_wave_best(h) ? Workspace::round(batch * waves * 4) * 3 : 0) +
            (with_logits ? Workspace::round(size_t(batch) * h->rows * 4) : 0) +
            (with_bounds ? Workspace::round(size_t(batch) * h->rows * 4) : 0);
 }
@@ -456,7 +728,7 @@ int adi_hip_head_matmul(adi_hip_context *ctx, const adi_hip_head_chunk *h, const
                 "Mach output head batch shape mismatch");
         auto &ws = ctx->workspace;
         ws.used = 0;
-        ws.ensure(head_workspace(h, batch, false, false));
+        ws.ensure(head_workspace(ctx, h, batch, false, false));
         head_logits(ctx, h, inputs, batch, outputs, nullptr);
     });
 }
@@ -474,29 +746,38 @@ int adi_hip_head_argmax(adi_hip_context *ctx, const adi_hip_head_chunk *h, const
                 "Mach output head batch shape mismatch");
         auto &ws = ctx->workspace;
         ws.used = 0;
-        ws.ensure(head_workspace(h, batch, logits == nullptr, true));
+        ws.ensure(head_workspace(ctx, h, batch, logits == nullptr, true));
         float *out = logits != nullptr ? logits : ws.take<float>(size_t(batch) * h->rows);
         float *bounds = ws.take<float>(size_t(batch) * h->rows);
-        head_logits(ctx, h, inputs, batch, out, bounds);
         // Both orders are within (n + 80) * 2^-24 * A of the exact sum; the
         // 1.25 margin also covers the rounding of A itself.
         const float factor = 2.5f * static_cast<float>(h->columns + 80u) * 5.9604645e-8f;
+        HeadWaveBest best{factor, nullptr, nullptr, nullptr};
+        const bool waves = head_wave_best(h);
+        const uint32_t wave_count = head_wide_blocks(ctx, h->rows) * 4u;
+        if (waves) {
+            best.value = ws.take<float>(size_t(batch) * wave_count);
+            best.index = ws.take<uint32_t>(size_t(batch) * wave_count);
+            best.upper = ws.take<float>(size_t(batch) * wave_count);
+        }
+        head_logits(ctx, h, inputs, batch, out, bounds, best);
         const HeadView v = view_of(h);
+        const auto run = [&](auto kernel) {
+            launch(ctx, "head_argmax", kernel, dim3(batch), dim3(kArgmaxThreads), 0, v, inputs,
+                   static_cast<const float *>(out), static_cast<const float *>(bounds), factor,
+                   static_cast<const float *>(best.value),
+                   static_cast<const uint32_t *>(best.index),
+                   static_cast<const float *>(best.upper), wave_count, argmax);
+        };
         switch (ctx->isa_lanes) {
         case 1:
-            launch(ctx, "head_argmax", k_head_argmax<1, false>, dim3(batch), dim3(kArgmaxThreads),
-                   0, v, inputs, static_cast<const float *>(out),
-                   static_cast<const float *>(bounds), factor, argmax);
+            waves ? run(k_head_argmax<1, false, true>) : run(k_head_argmax<1, false, false>);
             break;
         case 8:
-            launch(ctx, "head_argmax", k_head_argmax<8, false>, dim3(batch), dim3(kArgmaxThreads),
-                   0, v, inputs, static_cast<const float *>(out),
-                   static_cast<const float *>(bounds), factor, argmax);
+            waves ? run(k_head_argmax<8, false, true>) : run(k_head_argmax<8, false, false>);
             break;
         default:
-            launch(ctx, "head_argmax", k_head_argmax<16, true>, dim3(batch), dim3(kArgmaxThreads),
-                   0, v, inputs, static_cast<const float *>(out),
-                   static_cast<const float *>(bounds), factor, argmax);
+            waves ? run(k_head_argmax<16, true, true>) : run(k_head_argmax<16, true, false>);
             break;
         }
     });
