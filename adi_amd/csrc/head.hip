@@ -200,13 +200,13 @@ __device__ __forceinline__ float reduce_scatter64(float (&v)[V], uint32_t lane,
 }
 
 // k_head_gemv for 2048 columns (64 quads: one row per wave per pass), with
-// the next row's codes loaded while this row is summed, the lane sums
+// the x sums of a lane's quad computed in place, the next row's codes loaded
+// while this row is summed, the lane sums
 // reduce-scattered, and the bound sums only when they are wanted.
 template <int NT, bool BOUNDS>
 __global__ __launch_bounds__(256) void k_head_gemv_2048(
     const uint8_t *__restrict__ packed, const uint16_t *__restrict__ scales, uint32_t rows,
-    const float *__restrict__ x, const float *__restrict__ sums,
-    const float *__restrict__ abs_sums, uint32_t batch, float *__restrict__ logits,
+    const float *__restrict__ x, uint32_t batch, float *__restrict__ logits,
     float *__restrict__ bounds, HeadWaveBest best) {
     // no contraction: a lane's logit stays a rounded product in every variant
     // (with the bounds or without), so both variants give the same bits
@@ -234,8 +234,15 @@ __global__ __launch_bounds__(256) void k_head_gemv_2048(
                 xv[j][4 * q + 2] = v.z;
                 xv[j][4 * q + 3] = v.w;
             }
-            sx[j] = sums[static_cast<size_t>(t) * quads + lane];
-            sa[j] = abs_sums[static_cast<size_t>(t) * quads + lane];
+            // the quad's sums of x and |x|, in k_head_sums' order
+            float s = 0.0f, a = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 32; ++k) {
+                s += xv[j][k];
+                a += fabsf(xv[j][k]);
+            }
+            sx[j] = s;
+            sa[j] = a;
         }
         // with the bounds, even lanes end a row with a logit and their odd
         // partners with its bound (the first halving exchange is at offset 1)
@@ -332,6 +339,9 @@ __device__ float ordered_row_dot(uint32_t columns, const float *__restrict__ x, 
     const uint32_t full = columns / LANES * LANES;
     float acc = 0.0f;
     if (lane < LANES) {
+        // unrolled so that the loads of many steps are in flight at once;
+        // the sum still runs in k order
+#pragma unroll 16
         for (uint32_t base = 0; base < full; base += LANES) {
             const uint32_t k = base + lane;
             if constexpr (FUSED) {
@@ -425,6 +435,11 @@ __global__ __launch_bounds__(64) void k_head_exact_rows(HeadView h, const float 
 
 constexpr uint32_t kArgmaxThreads = 1024;
 constexpr uint32_t kCandidateCap = 2048;
+constexpr uint32_t kWaveListCap = 1024;
+
+__device__ __forceinline__ uint32_t ceil_div_device(uint32_t a, uint32_t b) {
+    return (a + b - 1u) / b;
+}
 
 // Calls f(r, logit, bound) for every row r of this thread's share of the
 // block, each row once: 16-byte loads (four of the logits in flight, or two
@@ -496,6 +511,8 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_head_argmax(
     __shared__ uint32_t candidates[kCandidateCap];
     __shared__ uint32_t candidate_count;
     __shared__ float threshold;
+    __shared__ uint32_t wave_list[WAVES ? kWaveListCap : 1];
+    __shared__ uint32_t wave_list_count;
     const uint32_t b = blockIdx.x;
     const float *row_logits = logits + static_cast<size_t>(b) * h.rows;
     const float *row_bounds = bounds + static_cast<size_t>(b) * h.rows;
@@ -538,6 +555,7 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_head_argmax(
     }
     if (threadIdx.x == 0) {
         candidate_count = 0;
+        wave_list_count = 0;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -563,13 +581,29 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_head_argmax(
         }
     };
     if constexpr (WAVES) {
+        // the waves that reach the threshold, then their rows over the block
+        // (every row of a wave once); too many such waves: the full scan
         const size_t base = static_cast<size_t>(b) * wave_count;
         for (uint32_t w = threadIdx.x; w < wave_count; w += kArgmaxThreads) {
             if (wave_upper[base + w] >= t) {
-                for (uint32_t r = w; r < h.rows; r += wave_count) {
+                const uint32_t slot = atomicAdd(&wave_list_count, 1u);
+                if (slot < kWaveListCap) {
+                    wave_list[slot] = w;
+                }
+            }
+        }
+        __syncthreads();
+        const uint32_t listed = wave_list_count;
+        if (listed <= kWaveListCap) {
+            const uint32_t passes = ceil_div_device(h.rows, wave_count);
+            for (uint32_t k = threadIdx.x; k < listed * passes; k += kArgmaxThreads) {
+                const uint32_t r = wave_list[k / passes] + (k % passes) * wave_count;
+                if (r < h.rows) {
                     consider(r, row_logits[r], row_bounds[r]);
                 }
             }
+        } else {
+            for_each_head_row<true>(row_logits, row_bounds, h.rows, consider);
         }
     } else {
         for_each_head_row<true>(row_logits, row_bounds, h.rows, consider);
@@ -665,8 +699,10 @@ void head_logits(adi_hip_context *ctx, const adi_hip_head_chunk *h, const float 
         auto &ws = ctx->workspace;
         float *sums = ws.take<float>(size_t(batch) * quads);
         float *abs_sums = ws.take<float>(size_t(batch) * quads);
-        launch(ctx, "head_sums", k_head_sums, dim3(batch), dim3(256), 0, x, h->columns, sums,
-               abs_sums);
+        if (quads != 64u) {
+            launch(ctx, "head_sums", k_head_sums, dim3(batch), dim3(256), 0, x, h->columns, sums,
+                   abs_sums);
+        }
         const uint32_t rows_per_block = 4u * (64u / quads);
         const uint32_t blocks = std::min<uint32_t>(ceil_div(h->rows, rows_per_block),
                                                    static_cast<uint32_t>(ctx->cu_count) * 8u);
@@ -678,8 +714,7 @@ void head_logits(adi_hip_context *ctx, const adi_hip_head_chunk *h, const float 
                                            : (with ? k_head_gemv_2048<4, true>
                                                    : k_head_gemv_2048<4, false>);
             launch(ctx, "head_gemv", kernel, dim3(wide), dim3(256), 0, h->packed,
-                   h->group_scale_f16, h->rows, x, static_cast<const float *>(sums),
-                   static_cast<const float *>(abs_sums), batch, logits, bounds, best);
+                   h->group_scale_f16, h->rows, x, batch, logits, bounds, best);
         } else if (batch == 1) {
             launch(ctx, "head_gemv", k_head_gemv<1>, dim3(blocks), dim3(256), 0, h->packed,
                    h->group_scale_f16, h->rows, h->columns, x, static_cast<const float *>(sums),
