@@ -512,6 +512,7 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_head_argmax(
     __shared__ uint32_t candidate_count;
     __shared__ float threshold;
     __shared__ uint32_t wave_list[WAVES ? kWaveListCap : 1];
+    __shared__ __align__(16) float weights[WAVES ? kArgmaxThreads / 64 : 1][WAVES ? 2048 : 4];
     __shared__ uint32_t wave_list_count;
     const uint32_t b = blockIdx.x;
     const float *row_logits = logits + static_cast<size_t>(b) * h.rows;
@@ -617,7 +618,45 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_head_argmax(
     uint32_t wi = 0xFFFFFFFFu;
     for (uint32_t c = wave; c < work; c += waves) {
         const uint32_t r = overflow ? c : candidates[c];
-        const float e = exact_logit<LANES, FUSED>(h, r, xb);
+        float e;
+        if constexpr (WAVES) {
+            // 2048 columns, no protected rows: the wave decodes the row into
+            // LDS with the GEMV's coalesced loads (lane l: columns 32l..32l+31,
+            // the same float (u - 16) * scale as exact_logit), then runs the
+            // CPU-order dot over it
+            float *w = weights[wave];
+            const uint32_t *src = reinterpret_cast<const uint32_t *>(h.packed) +
+                                  (static_cast<size_t>(r) * 64u + lane) * 5u;
+            uint32_t d[6] = {src[0], src[1], src[2], src[3], src[4], 0u};
+            const float scale = half_bits_to_float(h.scales[static_cast<size_t>(r) * 32u + lane / 2u]);
+            float u[kQuadColumns];
+#define ADI_CODE(K) u[K] = code_at<K>(d);
+            ADI_CODE(0) ADI_CODE(1) ADI_CODE(2) ADI_CODE(3) ADI_CODE(4) ADI_CODE(5) ADI_CODE(6)
+            ADI_CODE(7) ADI_CODE(8) ADI_CODE(9) ADI_CODE(10) ADI_CODE(11) ADI_CODE(12)
+            ADI_CODE(13) ADI_CODE(14) ADI_CODE(15) ADI_CODE(16) ADI_CODE(17) ADI_CODE(18)
+            ADI_CODE(19) ADI_CODE(20) ADI_CODE(21) ADI_CODE(22) ADI_CODE(23) ADI_CODE(24)
+            ADI_CODE(25) ADI_CODE(26) ADI_CODE(27) ADI_CODE(28) ADI_CODE(29) ADI_CODE(30)
+            ADI_CODE(31)
+#undef ADI_CODE
+            float4 *w4 = reinterpret_cast<float4 *>(w + lane * kQuadColumns);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                w4[q] = make_float4(static_cast<float>(static_cast<int>(u[4 * q]) - 16) * scale,
+                                    static_cast<float>(static_cast<int>(u[4 * q + 1]) - 16) * scale,
+                                    static_cast<float>(static_cast<int>(u[4 * q + 2]) - 16) * scale,
+                                    static_cast<float>(static_cast<int>(u[4 * q + 3]) - 16) * scale);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            e = ordered_row_dot<LANES, FUSED>(2048u, xb, [&](uint32_t k) { return w[k]; });
+            // every lane's reads of w end before the next row is written
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        } else {
+            e = exact_logit<LANES, FUSED>(h, r, xb);
+        }
         if (wi == 0xFFFFFFFFu || first_max_before(e, r, wv, wi)) {
             wv = e;
             wi = r;
