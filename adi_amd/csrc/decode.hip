@@ -269,6 +269,57 @@ __device__ __forceinline__ uint32_t descending_key(float v) {
     return ~ascending;
 }
 
+// The split denominator of a long row: block (p, r) folds row r's span maxima
+// (k_argmax_parts: the maximum is the same in any order) and sums
+// exp((v - max) / t) in double over span p, each thread in index order, then
+// a fixed tree; k_sample_rows adds the spans' sums in span order. A row with
+// a non-finite logit (a span index of 0xFFFFFFFF) gets sums of 0: the
+// sampler rejects it.
+__global__ __launch_bounds__(kArgmaxPartThreads) void k_expsum_parts(
+    const float *logits, uint32_t count, uint32_t span, const float *part_value,
+    const uint32_t *part_index, float temperature, double *part_sum) {
+    __shared__ double wave_sum[kArgmaxPartThreads / kWave];
+    const size_t base = static_cast<size_t>(blockIdx.y) * gridDim.x;
+    float m = -__builtin_huge_valf();
+    uint32_t bad = 0;
+    for (uint32_t p = 0; p < gridDim.x; ++p) {
+        const float v = part_value[base + p];
+        m = v > m ? v : m;
+        bad |= part_index[base + p] == 0xFFFFFFFFu ? 1u : 0u;
+    }
+    if (bad != 0u) {
+        if (threadIdx.x == 0) {
+            part_sum[base + blockIdx.x] = 0.0;
+        }
+        return;
+    }
+    const double maximum = static_cast<double>(m);
+    const double t = static_cast<double>(temperature);
+    const uint32_t begin = blockIdx.x * span;
+    const uint32_t end = begin + span < count ? begin + span : count;
+    const float *row = logits + static_cast<size_t>(blockIdx.y) * count + begin;
+    double part = 0.0;
+    for_each_logit(row, end - begin, [&](uint32_t, float v) {
+        part += exp((static_cast<double>(v) - maximum) / t);
+    });
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        part += __shfl_xor(part, offset);
+    }
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        wave_sum[wave] = part;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double sum = 0.0;
+        for (uint32_t w = 0; w < kArgmaxPartThreads / kWave; ++w) {
+            sum += wave_sum[w];
+        }
+        part_sum[base + blockIdx.x] = sum;
+    }
+}
+
 // The block's state between the phases of a row (in LDS).
 struct SampleState {
     uint64_t floor;     // (key << 32 | index) of the last walked candidate
@@ -404,7 +455,10 @@ __device__ void gather_window(const float *row, uint32_t count, double maximum, 
 __global__ __launch_bounds__(kSampleThreads) void k_sample_rows(const float *logits, uint32_t count,
                                                                 float temperature, float top_p,
                                                                 const uint64_t *words,
-                                                                uint32_t *tokens) {
+                                                                uint32_t *tokens, uint32_t parts,
+                                                                const float *part_value,
+                                                                const uint32_t *part_index,
+                                                                const double *part_sum) {
     __shared__ uint64_t cand[kWindow];
     __shared__ double prob[kWindow];
     __shared__ uint32_t hist[256];
@@ -417,10 +471,20 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_rows(const float *log
     // the maximum; any non-finite logit rejects the row
     float m = -__builtin_huge_valf();
     uint32_t bad = 0;
-    for_each_logit(row, count, [&](uint32_t, float v) {
-        bad |= __builtin_isfinite(v) ? 0u : 1u;
-        m = v > m ? v : m;
-    });
+    if (parts != 0u) {
+        // split rows: the spans' maxima and flags, read by every thread
+        const size_t base = static_cast<size_t>(blockIdx.x) * parts;
+        for (uint32_t p = 0; p < parts; ++p) {
+            const float v = part_value[base + p];
+            m = v > m ? v : m;
+            bad |= part_index[base + p] == 0xFFFFFFFFu ? 1u : 0u;
+        }
+    } else {
+        for_each_logit(row, count, [&](uint32_t, float v) {
+            bad |= __builtin_isfinite(v) ? 0u : 1u;
+            m = v > m ? v : m;
+        });
+    }
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1) {
         const float o = __shfl_xor(m, offset);
@@ -453,21 +517,29 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_rows(const float *log
     const double maximum = static_cast<double>(wave_max[0]);
     const double t = static_cast<double>(temperature);
     // sum of p over the row: each thread in index order, then a fixed tree
-    double part = 0.0;
-    for_each_logit(row, count, [&](uint32_t, float v) {
-        part += exp((static_cast<double>(v) - maximum) / t);
-    });
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) {
-        part += __shfl_xor(part, offset);
-    }
-    if (lane == 0) {
-        wave_sum[wave] = part;
-    }
-    __syncthreads();
+    // (split rows: the spans' sums in span order)
     double denominator = 0.0;
-    for (uint32_t w = 0; w < kSampleWaves; ++w) {
-        denominator += wave_sum[w];
+    if (parts != 0u) {
+        const size_t base = static_cast<size_t>(blockIdx.x) * parts;
+        for (uint32_t p = 0; p < parts; ++p) {
+            denominator += part_sum[base + p];
+        }
+    } else {
+        double part = 0.0;
+        for_each_logit(row, count, [&](uint32_t, float v) {
+            part += exp((static_cast<double>(v) - maximum) / t);
+        });
+#pragma unroll
+        for (int offset = 32; offset > 0; offset >>= 1) {
+            part += __shfl_xor(part, offset);
+        }
+        if (lane == 0) {
+            wave_sum[wave] = part;
+        }
+        __syncthreads();
+        for (uint32_t w = 0; w < kSampleWaves; ++w) {
+            denominator += wave_sum[w];
+        }
     }
     // phase 1: the kept prefix and the sum of its p
     uint64_t last = 0;
@@ -624,8 +696,32 @@ int adi_hip_sample_rows(adi_hip_context *ctx, const float *logits, uint32_t rows
             launch_argmax(ctx, logits, rows, count, tokens);
             return;
         }
+        if (count < kArgmaxSplitCount || rows > 65535u) {
+            launch(ctx, "sample", k_sample_rows, dim3(rows), dim3(kSampleThreads), 0, logits,
+                   count, temperature, top_p, words, tokens, 0u,
+                   static_cast<const float *>(nullptr), static_cast<const uint32_t *>(nullptr),
+                   static_cast<const double *>(nullptr));
+            return;
+        }
+        // long rows: the maximum and the denominator over up to 64 blocks a row
+        const uint32_t wanted = std::min<uint32_t>(kArgmaxMaxParts, ceil_div(count, 4096));
+        const uint32_t span = (ceil_div(count, wanted) + 3u) & ~3u;
+        const uint32_t parts = ceil_div(count, span);
+        auto &ws = ctx->workspace;
+        ws.used = 0;
+        ws.ensure(Workspace::round(size_t(rows) * parts * 4) * 2 +
+                  Workspace::round(size_t(rows) * parts * 8));
+        float *part_value = ws.take<float>(size_t(rows) * parts);
+        uint32_t *part_index = ws.take<uint32_t>(size_t(rows) * parts);
+        double *part_sum = ws.take<double>(size_t(rows) * parts);
+        launch(ctx, "argmax_parts", k_argmax_parts, dim3(parts, rows), dim3(kArgmaxPartThreads), 0,
+               logits, count, span, part_value, part_index);
+        launch(ctx, "expsum_parts", k_expsum_parts, dim3(parts, rows), dim3(kArgmaxPartThreads), 0,
+               logits, count, span, static_cast<const float *>(part_value),
+               static_cast<const uint32_t *>(part_index), temperature, part_sum);
         launch(ctx, "sample", k_sample_rows, dim3(rows), dim3(kSampleThreads), 0, logits, count,
-               temperature, top_p, words, tokens);
+               temperature, top_p, words, tokens, parts, static_cast<const float *>(part_value),
+               static_cast<const uint32_t *>(part_index), static_cast<const double *>(part_sum));
     });
 }
 

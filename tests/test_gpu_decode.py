@@ -168,6 +168,12 @@ def test_sample_rows_non_finite_and_parameters(gpu):
     logits[2, 999] = -np.inf
     got = sample_device(gpu, logits, 0.7, 0.9, [1, 2, 3])
     assert got[1] == 0xFFFFFFFF and got[2] == 0xFFFFFFFF and got[0] < 1000
+    # rows long enough to split over blocks: the flag of any span marks the row
+    long_rows = np.random.default_rng(6).normal(0, 1, (3, 40000)).astype(np.float32)
+    long_rows[1, 39999] = np.nan
+    long_rows[2, 20000] = np.inf
+    got = sample_device(gpu, long_rows, 0.7, 0.9, [4, 5, 6])
+    assert got[1] == 0xFFFFFFFF and got[2] == 0xFFFFFFFF and got[0] < 40000
     t = torch.empty(3, dtype=torch.int32, device="cuda")
     x = torch.from_numpy(logits).cuda()
     for temperature, top_p in ((5e-5, 0.9), (2.5, 0.9), (0.7, 0.0), (0.7, 1.01)):
