@@ -215,20 +215,34 @@ __global__ __launch_bounds__(kHeadSize) void k_attention_combine(const float *pa
     const uint32_t h = blockIdx.x, t = threadIdx.x, b = blockIdx.y;
     query_gate += static_cast<size_t>(b) * kQueryHeads * kQueryStride;
     attended += static_cast<size_t>(b) * kQueryHeads * kHeadSize;
+    __shared__ float split_max[kMaxSplits], split_den[kMaxSplits], split_factor[kMaxSplits];
     const float *p = partial + (static_cast<size_t>(b) * kQueryHeads + h) * splits * kPartialStride;
-    // split 0 always holds token 0, so the maximum is finite
-    float m = p[kHeadSize];
-    for (uint32_t s = 1; s < splits; ++s) {
-        m = fmaxf(m, p[s * kPartialStride + kHeadSize]);
+    // the splits' maxima and denominators through LDS, so the loop below
+    // loads only the accumulators (splits <= kMaxSplits)
+    for (uint32_t s = t; s < splits; s += kHeadSize) {
+        split_max[s] = p[s * kPartialStride + kHeadSize];
+        split_den[s] = p[s * kPartialStride + kHeadSize + 1];
     }
+    __syncthreads();
+    // split 0 always holds token 0, so the maximum is finite
+    float m = split_max[0];
+    for (uint32_t s = 1; s < splits; ++s) {
+        m = fmaxf(m, split_max[s]);
+    }
+    for (uint32_t s = t; s < splits; s += kHeadSize) {
+        split_factor[s] = expf(split_max[s] - m);
+    }
+    __syncthreads();
     float a = 0.0f, d = 0.0f;
+#pragma unroll 8
     for (uint32_t s = 0; s < splits; ++s) {
-        if (p[s * kPartialStride + kHeadSize + 1] == 0.0f) {
+        const float den = split_den[s];
+        if (den == 0.0f) {
             continue;  // a split past the token
         }
-        const float f = expf(p[s * kPartialStride + kHeadSize] - m);
+        const float f = split_factor[s];
         a += p[s * kPartialStride + t] * f;
-        d += p[s * kPartialStride + kHeadSize + 1] * f;
+        d += den * f;
     }
     const float gate = query_gate[static_cast<size_t>(h) * kQueryStride + kHeadSize + t];
     attended[static_cast<size_t>(h) * kHeadSize + t] = a * (1.0f / d) * sigmoid_of(gate);
