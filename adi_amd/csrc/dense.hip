@@ -445,10 +445,31 @@ __global__ __launch_bounds__(256) void k_rms_norm(
     __shared__ float scale_shared;
     __shared__ float wave_sums[4];
     const float *row = x + static_cast<size_t>(blockIdx.x) * count;
+    float *dst = out + static_cast<size_t>(blockIdx.x) * count;
+    // up to 8 values a thread: the row and the weights are loaded at once
+    // and kept in registers for the output (same sums, same products)
+    constexpr uint32_t kHeld = 8;
+    const bool held = count <= kHeld * blockDim.x;
+    float v[kHeld], w[kHeld];
     float squares = 0.0f;
-    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
-        const float v = row[i];
-        squares += v * v;
+    if (held) {
+#pragma unroll
+        for (uint32_t k = 0; k < kHeld; ++k) {
+            const uint32_t i = threadIdx.x + k * blockDim.x;
+            v[k] = i < count ? row[i] : 0.0f;
+            w[k] = i < count ? bf16_bits_to_float(weight[i]) : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kHeld; ++k) {
+            if (threadIdx.x + k * blockDim.x < count) {
+                squares += v[k] * v[k];
+            }
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
+            const float value = row[i];
+            squares += value * value;
+        }
     }
     squares += lane_xor<1>(squares);
     squares += lane_xor<2>(squares);
@@ -466,7 +487,16 @@ __global__ __launch_bounds__(256) void k_rms_norm(
     }
     __syncthreads();
     const float scale = scale_shared;
-    float *dst = out + static_cast<size_t>(blockIdx.x) * count;
+    if (held) {
+#pragma unroll
+        for (uint32_t k = 0; k < kHeld; ++k) {
+            const uint32_t i = threadIdx.x + k * blockDim.x;
+            if (i < count) {
+                dst[i] = v[k] * scale * (offset + w[k]);
+            }
+        }
+        return;
+    }
     for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
         dst[i] = row[i] * scale * (offset + bf16_bits_to_float(weight[i]));
     }
