@@ -5,10 +5,14 @@
 // 1073), finds or creates the device copy of the weights, copies the host
 // span in, launches, and copies the result out. Weights are views into the
 // model file (include/adi/kernels.hpp:9-77) and never change while mapped, so
-// their device copies are cached by host address, as ExpertScratch caches the
-// derived tables (src/kernels.cpp:33-94); a sampled fingerprint of the
-// contents is part of the key, so a buffer freed and reused at the same
-// address is uploaded again. Calls are serialised on one context:
+// their device copies are cached by host address and shape, as ExpertScratch
+// caches the derived tables by source pointer (src/kernels.cpp:33-94). Each
+// entry also keeps a fingerprint of sampled contents: a different buffer met
+// at the same address replaces the entry (its device copies are freed and
+// the new contents uploaded), so the cache holds one copy per live address.
+// hip_backend_release_weights() frees every copy; a caller that unmaps a
+// model calls it, since a new mapping at the old address whose samples all
+// match would otherwise reuse the old copy. Calls are serialised on one context:
 // moe_forward calls the projections from worker threads
 // (src/executor.cpp:261, 1321-1371), and the GPU runs them in turn anyway.
 #include "hip_backend.hpp"
@@ -23,6 +27,7 @@
 #include <string>
 #include <tuple>
 #include <utility>
+#include <vector>
 
 namespace adi {
 namespace {
@@ -58,6 +63,10 @@ class Runtime {
 
     std::mutex mutex;
     adi_hip_context *ctx = nullptr;
+
+    // cache keys: host address and shape (matrices) or address and length
+    using Key = std::tuple<const void *, std::uint32_t, std::uint32_t>;
+    using TableKey = std::pair<const void *, std::size_t>;
 
     void check(int status) const {
         if (status == ADI_HIP_OK) {
@@ -98,122 +107,190 @@ class Runtime {
         check(adi_hip_copy_to_host(ctx, host.data(), device, host.size_bytes()));
     }
 
-    const adi_hip_codebook *expert_book(std::span<const float> tlut) {
-        auto &slot = expert_books_[{tlut.data(), fingerprint(tlut)}];
-        if (slot == nullptr) {
-            check(adi_hip_codebook_create_expert(ctx, tlut.data(), &slot));
+    // An entry of a cache: the descriptor, the contents' fingerprint and the
+    // device buffers it owns.
+    template <typename T>
+    struct Entry {
+        std::uint64_t fingerprint = 0;
+        T value{};
+        std::vector<void *> owned;
+    };
+
+    // The entry of `key`, (re)built by make(entry) when it is missing or its
+    // fingerprint differs from `fp` (the old copies are freed first).
+    template <typename K, typename T, typename Make>
+    const T &cached(std::map<K, Entry<T>> &cache, const K &key, std::uint64_t fp, Make &&make) {
+        auto found = cache.find(key);
+        if (found != cache.end() && found->second.fingerprint == fp) {
+            return found->second.value;
         }
-        return slot;
+        if (found != cache.end()) {
+            release(found->second);
+            cache.erase(found);
+        }
+        Entry<T> entry;
+        entry.fingerprint = fp;
+        make(entry);
+        return cache.emplace(key, std::move(entry)).first->second.value;
+    }
+
+    template <typename U, typename T>
+    const U *upload_into(Entry<T> &entry, std::span<const U> host) {
+        const U *device = upload(host);
+        entry.owned.push_back(const_cast<U *>(device));
+        return device;
+    }
+
+    template <typename T>
+    void release(Entry<T> &entry) {
+        check(adi_hip_synchronize(ctx));
+        for (void *p : entry.owned) {
+            adi_hip_device_free(ctx, p);
+        }
+        entry.owned.clear();
+    }
+
+    template <typename K, typename T>
+    void release_all(std::map<K, Entry<T>> &cache) {
+        for (auto &kv : cache) {
+            release(kv.second);
+        }
+        cache.clear();
+    }
+
+    void release_books(std::map<TableKey, Entry<adi_hip_codebook *>> &books) {
+        check(adi_hip_synchronize(ctx));
+        for (auto &kv : books) {
+            adi_hip_codebook_destroy(kv.second.value);
+        }
+        books.clear();
+    }
+
+    void release_weights() {
+        release_all(experts_);
+        release_all(nes_);
+        release_all(heads_);
+        release_all(bf16s_);
+        release_all(embeddings_);
+        release_all(weights_);
+        release_books(expert_books_);
+        release_books(ne_books_);
+    }
+
+    const adi_hip_codebook *book(std::map<TableKey, Entry<adi_hip_codebook *>> &books,
+                                 std::span<const float> tlut, bool expert) {
+        const TableKey key{tlut.data(), tlut.size()};
+        auto found = books.find(key);
+        const std::uint64_t fp = fingerprint(tlut);
+        if (found != books.end() && found->second.fingerprint == fp) {
+            return found->second.value;
+        }
+        if (found != books.end()) {
+            check(adi_hip_synchronize(ctx));
+            adi_hip_codebook_destroy(found->second.value);
+            books.erase(found);
+        }
+        Entry<adi_hip_codebook *> entry;
+        entry.fingerprint = fp;
+        check(expert ? adi_hip_codebook_create_expert(ctx, tlut.data(), &entry.value)
+                     : adi_hip_codebook_create_ne(ctx, tlut.data(), &entry.value));
+        return books.emplace(key, std::move(entry)).first->second.value;
+    }
+    const adi_hip_codebook *expert_book(std::span<const float> tlut) {
+        return book(expert_books_, tlut, true);
     }
     const adi_hip_codebook *ne_book(std::span<const float> tlut) {
-        auto &slot = ne_books_[{tlut.data(), fingerprint(tlut)}];
-        if (slot == nullptr) {
-            check(adi_hip_codebook_create_ne(ctx, tlut.data(), &slot));
-        }
-        return slot;
+        return book(ne_books_, tlut, false);
     }
 
     const adi_hip_expert_matrix &expert(const MachExpertMatrix &m) {
-        const Key key{m.trellis.data(), m.rows, m.columns,
-                      fingerprint(m.trellis) ^ fingerprint(m.su_f16) * 3 ^ fingerprint(m.sv_f16) * 5 ^
-                          fingerprint(m.wave_gamma_f16) * 7 ^ fingerprint(m.tlut) * 11};
-        auto found = experts_.find(key);
-        if (found == experts_.end()) {
-            adi_hip_expert_matrix d{};
-            d.rows = m.rows;
-            d.columns = m.columns;
-            d.trellis = upload(m.trellis);
-            d.su_f16 = upload(m.su_f16);
-            d.sv_f16 = upload(m.sv_f16);
-            d.wave_gamma_f16 = upload(m.wave_gamma_f16);
-            d.codebook = expert_book(m.tlut);
-            found = experts_.emplace(key, d).first;
-        }
-        return found->second;
+        const std::uint64_t fp = fingerprint(m.trellis) ^ fingerprint(m.su_f16) * 3 ^
+                                 fingerprint(m.sv_f16) * 5 ^ fingerprint(m.wave_gamma_f16) * 7 ^
+                                 fingerprint(m.tlut) * 11;
+        return cached(experts_, Key{m.trellis.data(), m.rows, m.columns}, fp,
+                      [&](Entry<adi_hip_expert_matrix> &e) {
+                          adi_hip_expert_matrix &d = e.value;
+                          d.rows = m.rows;
+                          d.columns = m.columns;
+                          d.trellis = upload_into(e, m.trellis);
+                          d.su_f16 = upload_into(e, m.su_f16);
+                          d.sv_f16 = upload_into(e, m.sv_f16);
+                          d.wave_gamma_f16 = upload_into(e, m.wave_gamma_f16);
+                          d.codebook = expert_book(m.tlut);
+                      });
     }
 
     const adi_hip_ne_matrix &ne(const MachNeMatrix &m) {
-        const Key key{m.trellis.data(), m.rows, m.columns,
-                      fingerprint(m.trellis) ^ fingerprint(m.su) * 3 ^ fingerprint(m.sv) * 5 ^
-                          fingerprint(m.tlut) * 7 ^ static_cast<std::uint64_t>(m.weight_scale * 1e6f)};
-        auto found = nes_.find(key);
-        if (found == nes_.end()) {
-            adi_hip_ne_matrix d{};
-            d.rows = m.rows;
-            d.columns = m.columns;
-            d.trellis = upload(m.trellis);
-            d.su = upload(m.su);
-            d.sv = upload(m.sv);
-            d.weight_scale = m.weight_scale;
-            d.codebook = ne_book(m.tlut);
-            found = nes_.emplace(key, d).first;
-        }
-        return found->second;
+        std::uint32_t scale_bits = 0;
+        std::memcpy(&scale_bits, &m.weight_scale, sizeof(scale_bits));
+        const std::uint64_t fp = fingerprint(m.trellis) ^ fingerprint(m.su) * 3 ^
+                                 fingerprint(m.sv) * 5 ^ fingerprint(m.tlut) * 7 ^
+                                 static_cast<std::uint64_t>(scale_bits) * 13;
+        return cached(nes_, Key{m.trellis.data(), m.rows, m.columns}, fp,
+                      [&](Entry<adi_hip_ne_matrix> &e) {
+                          adi_hip_ne_matrix &d = e.value;
+                          d.rows = m.rows;
+                          d.columns = m.columns;
+                          d.trellis = upload_into(e, m.trellis);
+                          d.su = upload_into(e, m.su);
+                          d.sv = upload_into(e, m.sv);
+                          d.weight_scale = m.weight_scale;
+                          d.codebook = ne_book(m.tlut);
+                      });
     }
 
     const adi_hip_head_chunk &head(const MachHeadChunk &h) {
-        const Key key{h.packed.data(), h.rows, h.columns,
-                      fingerprint(h.packed) ^ fingerprint(h.group_scale_f16) * 3 ^
-                          fingerprint(h.protected_rows) * 5 ^ fingerprint(h.protected_bf16) * 7};
-        auto found = heads_.find(key);
-        if (found == heads_.end()) {
-            adi_hip_head_chunk d{};
-            d.rows = h.rows;
-            d.columns = h.columns;
-            d.packed = upload(h.packed);
-            d.group_scale_f16 = upload(h.group_scale_f16);
-            d.protected_count = static_cast<std::uint32_t>(h.protected_rows.size());
-            if (d.protected_count != 0) {
-                d.protected_rows = upload(h.protected_rows);
-                d.protected_bf16 = upload(h.protected_bf16);
-            }
-            found = heads_.emplace(key, d).first;
-        }
-        return found->second;
+        const std::uint64_t fp = fingerprint(h.packed) ^ fingerprint(h.group_scale_f16) * 3 ^
+                                 fingerprint(h.protected_rows) * 5 ^
+                                 fingerprint(h.protected_bf16) * 7;
+        return cached(heads_, Key{h.packed.data(), h.rows, h.columns}, fp,
+                      [&](Entry<adi_hip_head_chunk> &e) {
+                          adi_hip_head_chunk &d = e.value;
+                          d.rows = h.rows;
+                          d.columns = h.columns;
+                          d.packed = upload_into(e, h.packed);
+                          d.group_scale_f16 = upload_into(e, h.group_scale_f16);
+                          d.protected_count = static_cast<std::uint32_t>(h.protected_rows.size());
+                          if (d.protected_count != 0) {
+                              d.protected_rows = upload_into(e, h.protected_rows);
+                              d.protected_bf16 = upload_into(e, h.protected_bf16);
+                          }
+                      });
     }
 
     const adi_hip_bf16_matrix &bf16(const Bf16Matrix &m) {
-        const Key key{m.values.data(), m.rows, m.columns, fingerprint(m.values)};
-        auto found = bf16s_.find(key);
-        if (found == bf16s_.end()) {
-            adi_hip_bf16_matrix d{};
-            d.rows = m.rows;
-            d.columns = m.columns;
-            d.values = upload(m.values);
-            found = bf16s_.emplace(key, d).first;
-        }
-        return found->second;
+        return cached(bf16s_, Key{m.values.data(), m.rows, m.columns}, fingerprint(m.values),
+                      [&](Entry<adi_hip_bf16_matrix> &e) {
+                          e.value.rows = m.rows;
+                          e.value.columns = m.columns;
+                          e.value.values = upload_into(e, m.values);
+                      });
     }
 
     const adi_hip_embedding &embedding(const MachEmbedding &e) {
-        const Key key{e.packed.data(), e.rows, e.columns,
-                      fingerprint(e.packed) ^ fingerprint(e.minimum_f16) * 3 ^
-                          fingerprint(e.maximum_f16) * 5 ^ fingerprint(e.exception_indexes) * 7 ^
-                          fingerprint(e.exception_bf16) * 11};
-        auto found = embeddings_.find(key);
-        if (found == embeddings_.end()) {
-            adi_hip_embedding d{};
-            d.rows = e.rows;
-            d.columns = e.columns;
-            d.packed = upload(e.packed);
-            d.minimum_f16 = upload(e.minimum_f16);
-            d.maximum_f16 = upload(e.maximum_f16);
-            d.exception_count = static_cast<std::uint32_t>(e.exception_indexes.size());
-            if (d.exception_count != 0) {
-                d.exception_indexes = upload(e.exception_indexes);
-                d.exception_bf16 = upload(e.exception_bf16);
-            }
-            found = embeddings_.emplace(key, d).first;
-        }
-        return found->second;
+        const std::uint64_t fp = fingerprint(e.packed) ^ fingerprint(e.minimum_f16) * 3 ^
+                                 fingerprint(e.maximum_f16) * 5 ^
+                                 fingerprint(e.exception_indexes) * 7 ^
+                                 fingerprint(e.exception_bf16) * 11;
+        return cached(embeddings_, Key{e.packed.data(), e.rows, e.columns}, fp,
+                      [&](Entry<adi_hip_embedding> &entry) {
+                          adi_hip_embedding &d = entry.value;
+                          d.rows = e.rows;
+                          d.columns = e.columns;
+                          d.packed = upload_into(entry, e.packed);
+                          d.minimum_f16 = upload_into(entry, e.minimum_f16);
+                          d.maximum_f16 = upload_into(entry, e.maximum_f16);
+                          d.exception_count = static_cast<std::uint32_t>(e.exception_indexes.size());
+                          if (d.exception_count != 0) {
+                              d.exception_indexes = upload_into(entry, e.exception_indexes);
+                              d.exception_bf16 = upload_into(entry, e.exception_bf16);
+                          }
+                      });
     }
 
     const std::uint16_t *weights(std::span<const std::uint16_t> w) {
-        auto &slot = weights_[{w.data(), fingerprint(w)}];
-        if (slot == nullptr) {
-            slot = upload(w);
-        }
-        return slot;
+        return cached(weights_, TableKey{w.data(), w.size()}, fingerprint(w),
+                      [&](Entry<const std::uint16_t *> &e) { e.value = upload_into(e, w); });
     }
 
     std::string name;
@@ -238,17 +315,15 @@ class Runtime {
         void *pointer = nullptr;
         std::size_t bytes = 0;
     };
-    using Key = std::tuple<const void *, std::uint32_t, std::uint32_t, std::uint64_t>;
-    using TableKey = std::pair<const void *, std::uint64_t>;
     Buffer buffers_[2];
-    std::map<TableKey, adi_hip_codebook *> expert_books_;
-    std::map<TableKey, adi_hip_codebook *> ne_books_;
-    std::map<Key, adi_hip_expert_matrix> experts_;
-    std::map<Key, adi_hip_ne_matrix> nes_;
-    std::map<Key, adi_hip_head_chunk> heads_;
-    std::map<Key, adi_hip_bf16_matrix> bf16s_;
-    std::map<Key, adi_hip_embedding> embeddings_;
-    std::map<TableKey, const std::uint16_t *> weights_;
+    std::map<TableKey, Entry<adi_hip_codebook *>> expert_books_;
+    std::map<TableKey, Entry<adi_hip_codebook *>> ne_books_;
+    std::map<Key, Entry<adi_hip_expert_matrix>> experts_;
+    std::map<Key, Entry<adi_hip_ne_matrix>> nes_;
+    std::map<Key, Entry<adi_hip_head_chunk>> heads_;
+    std::map<Key, Entry<adi_hip_bf16_matrix>> bf16s_;
+    std::map<Key, Entry<adi_hip_embedding>> embeddings_;
+    std::map<TableKey, Entry<const std::uint16_t *>> weights_;
 };
 
 // ---- argument checks: the reference's conditions and messages -------------
@@ -465,6 +540,12 @@ const Backend &hip_backend() {
         };
     }();
     return backend;
+}
+
+void hip_backend_release_weights() {
+    Runtime &rt = Runtime::get();
+    const std::lock_guard<std::mutex> lock(rt.mutex);
+    rt.release_weights();
 }
 
 }  // namespace adi

@@ -19,4 +19,11 @@ namespace adi {
 // std::runtime_error rather than falling back to the CPU.
 [[nodiscard]] const Backend &hip_backend();
 
+// Frees every device copy of weights the table has made. The table caches
+// copies by host address (the reference's ExpertScratch caches its derived
+// tables by source pointer, src/kernels.cpp:33-94), so a caller that unmaps a
+// model calls this before mapping another. No counterpart in the reference,
+// whose weights are used in place.
+void hip_backend_release_weights();
+
 }  // namespace adi

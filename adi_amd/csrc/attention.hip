@@ -9,8 +9,10 @@
 // Full attention, after the q/k/v projections:
 //   norm_rope   one block per head: RMS norm with (1 + w), then RoPE on the
 //               first 64 dimensions from a cos/sin table the host computes
-//               with the same libm calls as the reference (prepare_rope);
-//               the key lands in its cache slot, the value is projected there
+//               with the same libm calls as the reference (prepare_rope):
+//               a kernel argument for one token, a cached device table of
+//               every position for a chunk; the key lands in its cache slot,
+//               the value is projected there
 //   partial     flash-decoding: block (head, split) runs the online softmax
 //               over its share of the history, one wave per token stream,
 //               and merges its four waves
@@ -25,6 +27,7 @@
 // reductions); results agree to float rounding.
 #include "dense.hpp"
 
+#include <algorithm>
 #include <cmath>
 
 namespace adi_hip {
@@ -90,12 +93,15 @@ __device__ __forceinline__ float sigmoid_of(float v) { return 1.0f / (1.0f + exp
 
 // normalize_head then apply_rope (src/executor.cpp:25-41, 60-72, 376-390):
 // block (h, b) of token b: h 0-15 the query heads (stride 512), 16-17 the new
-// key heads. One token takes the host's table `rope`; in a chunk, token b's
-// table is computed here for position + b from the host's divisors.
+// key heads. One token takes the host's table `rope`; in a chunk, token b
+// reads the host-computed table of position + b from `rope_rows`
+// ([position][32 cosines, 32 sines]), so every token of a chunk rotates
+// exactly as it would alone (the reference builds its prefill table on the
+// host too, src/executor.cpp:1853-1866).
 __global__ __launch_bounds__(kHeadSize) void k_norm_rope(float *query_gate, float *key,
                                                          const uint16_t *query_norm,
                                                          const uint16_t *key_norm, RopeTable rope,
-                                                         RopeDivisors divisors, uint32_t position) {
+                                                         const float *rope_rows, uint32_t position) {
 #pragma clang fp contract(off)
     __shared__ float partial[16];
     __shared__ float head[kHeadSize];
@@ -113,10 +119,10 @@ __global__ __launch_bounds__(kHeadSize) void k_norm_rope(float *query_gate, floa
     __syncthreads();
     if (t < kRopeHalf) {
         float cosine = rope.cosine[t], sine = rope.sine[t];
-        if (gridDim.y > 1) {
-            const float theta = static_cast<float>(position + b) / divisors.divisor[t];
-            cosine = cosf(theta);
-            sine = sinf(theta);
+        if (rope_rows != nullptr) {
+            const float *row = rope_rows + static_cast<size_t>(position + b) * (2 * kRopeHalf);
+            cosine = row[t];
+            sine = row[kRopeHalf + t];
         }
         const float first = head[t], second = head[t + kRopeHalf];
         v[t] = first * cosine - second * sine;
@@ -412,6 +418,30 @@ RopeTable rope_table(uint32_t position) {
     return t;
 }
 
+// The context's device table of rope_table(p) for p < end, grown on demand
+// (the whole table is rebuilt on the host and copied when it grows).
+const float *rope_rows(adi_hip_context *ctx, uint32_t end) {
+    if (end > ctx->rope_positions) {
+        uint32_t positions = ctx->rope_positions * 2 > 1024 ? ctx->rope_positions * 2 : 1024u;
+        positions = positions > end ? positions : end;
+        std::vector<float> host(size_t(positions) * 2 * kRopeHalf);
+        for (uint32_t p = 0; p < positions; ++p) {
+            const RopeTable t = rope_table(p);
+            std::copy(t.cosine, t.cosine + kRopeHalf, host.begin() + size_t(p) * 2 * kRopeHalf);
+            std::copy(t.sine, t.sine + kRopeHalf,
+                      host.begin() + size_t(p) * 2 * kRopeHalf + kRopeHalf);
+        }
+        ctx->rope_positions = 0;
+        ctx->rope_cache.ensure(host.size() * sizeof(float));  // waits for the device before a free
+        check_hip(hipStreamSynchronize(ctx->stream), "rope table synchronize");
+        check_hip(hipMemcpy(ctx->rope_cache.base, host.data(), host.size() * sizeof(float),
+                            hipMemcpyHostToDevice),
+                  "rope table upload");
+        ctx->rope_positions = positions;
+    }
+    return static_cast<const float *>(ctx->rope_cache.base);
+}
+
 // A nested entry's status becomes this call's failure.
 void forward(adi_hip_context *ctx, int status) {
     if (status != ADI_HIP_OK) {
@@ -463,7 +493,8 @@ void full_attention_chunk(adi_hip_context *ctx, const adi_hip_full_attention *L,
     forward(ctx, adi_hip_ne_matmul(ctx, &L->value, inputs, count, value));
     launch(ctx, "attention_norm_rope", k_norm_rope, dim3(kQueryHeads + kKvHeads, count),
            dim3(kHeadSize), 0, query_gate, key, L->query_norm, L->key_norm,
-           count == 1 ? rope_table(position) : RopeTable{}, rope_divisors(), position);
+           count == 1 ? rope_table(position) : RopeTable{},
+           count == 1 ? nullptr : rope_rows(ctx, position + count), position);
     launch(ctx, "attention_partial", k_attention_partial, dim3(kQueryHeads, splits, count),
            dim3(256), 0, static_cast<const float *>(query_gate), static_cast<const float *>(keys),
            static_cast<const float *>(values), position, chunk, partial);

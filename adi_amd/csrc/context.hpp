@@ -76,6 +76,10 @@ struct adi_hip_context {
     adi_hip::Workspace layer_workspace;
     // scratch of the decoder-layer entry, which calls the attention entries
     adi_hip::Workspace decoder_workspace;
+    // RoPE cos/sin of positions 0 .. rope_positions - 1 ([position][cos 32,
+    // sin 32] floats), computed on the host and grown on demand
+    adi_hip::Workspace rope_cache;
+    uint32_t rope_positions = 0;
     bool profiling = false;
     std::vector<adi_hip::KernelStat> stats;
 };
@@ -129,26 +133,28 @@ int guarded(adi_hip_context *ctx, F &&function) {
 
 KernelStat &stat_for(adi_hip_context *ctx, const char *name);
 
-// Launches `kernel` on the context stream, timing it with events when
-// profiling is on.
+// Launches `kernel` on the context stream. With profiling on, the launch
+// carries a start and a stop event that the runtime stamps from the kernel's
+// own dispatch (hipExtLaunchKernel), so the time is the kernel's execution,
+// as a kernel trace reports it, not the gap between two event packets.
 template <typename Kernel, typename... Args>
 void launch(adi_hip_context *ctx, const char *name, Kernel kernel, dim3 grid,
             dim3 block, size_t lds_bytes, Args... args) {
     if (grid.x == 0 || grid.y == 0 || grid.z == 0) {
         return;
     }
+    if (!ctx->profiling) {
+        hipLaunchKernelGGL(kernel, grid, block, lds_bytes, ctx->stream, args...);
+        check_hip(hipGetLastError(), name);
+        return;
+    }
     hipEvent_t start = nullptr, stop = nullptr;
-    if (ctx->profiling) {
-        check_hip(hipEventCreate(&start), "hipEventCreate");
-        check_hip(hipEventCreate(&stop), "hipEventCreate");
-        check_hip(hipEventRecord(start, ctx->stream), "hipEventRecord");
-    }
-    hipLaunchKernelGGL(kernel, grid, block, lds_bytes, ctx->stream, args...);
+    check_hip(hipEventCreate(&start), "hipEventCreate");
+    check_hip(hipEventCreate(&stop), "hipEventCreate");
+    hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds_bytes), ctx->stream,
+                          start, stop, 0, args...);
     check_hip(hipGetLastError(), name);
-    if (ctx->profiling) {
-        check_hip(hipEventRecord(stop, ctx->stream), "hipEventRecord");
-        stat_for(ctx, name).pending.emplace_back(start, stop);
-    }
+    stat_for(ctx, name).pending.emplace_back(start, stop);
 }
 
 // Raises a kernel's dynamic LDS limit above the 64 KiB default (once per

@@ -359,8 +359,10 @@ def upload_moe_layer(ctx: Context, layer, expert_book: int, ne_book: int) -> Dev
         return t.data_ptr()
 
     stacks = []
-    for mats in (layer.gate, layer.up, layer.down):
-        stacks.append(ExpertStack(*(dev(a) for a in stack_experts(mats))))
+    for kind in ("gate", "up", "down"):
+        held = getattr(layer, "stacks", None)
+        arrays = held[kind] if held else stack_experts(getattr(layer, kind))
+        stacks.append(ExpertStack(*(dev(a) for a in arrays)))
     shared = []
     for m in (layer.shared_gate, layer.shared_up, layer.shared_down):
         d = upload_ne(ctx, m, ne_book)

@@ -107,6 +107,9 @@ class MoeLayer:
     shared_down: Optional[NeMatrix] = None
     expert_tlut: Optional[np.ndarray] = None
     ne_tlut: Optional[np.ndarray] = None
+    # expert-major stacks {"gate"|"up"|"down": (trellis, su, sv, gamma)} when
+    # the per-expert matrices are views into them (stacked_moe_layer)
+    stacks: Optional[dict] = None
 
 
 def rng_for(config_index: int, salt: int = 0) -> np.random.Generator:
@@ -232,6 +235,40 @@ def moe_layer(rng, hidden: int = 2048, expert_hidden: int = 512, experts: int = 
     return layer
 
 
+def stacked_moe_layer(rng, hidden: int = 2048, expert_hidden: int = 512, experts: int = 256,
+                      etlut: Optional[np.ndarray] = None,
+                      ntlut: Optional[np.ndarray] = None) -> MoeLayer:
+    """The layer of moe_layer with each projection kind drawn for all experts
+    at once, expert-major as the checkpoint's 32-expert chunks store them
+    (src/model.cpp:483-532). The per-expert matrices are views into the
+    stacks, so a 256-expert layer costs one draw per tensor kind."""
+    etlut = expert_tlut(rng) if etlut is None else etlut
+    ntlut = ne_tlut(rng) if ntlut is None else ntlut
+    layer = MoeLayer(
+        hidden, expert_hidden, experts,
+        bf16_bits_rne(rng.normal(0.0, 0.02, (experts, hidden)).astype(np.float32)),
+        bf16_bits_rne(rng.normal(0.0, 0.02, (1, hidden)).astype(np.float32)),
+        expert_tlut=etlut, ne_tlut=ntlut, stacks={},
+    )
+    for kind, rows, columns in (("gate", expert_hidden, hidden), ("up", expert_hidden, hidden),
+                                ("down", hidden, expert_hidden)):
+        words = (rows // 16) * (columns // 16) * EXPERT_WORDS_PER_TILE
+        waves = rows // 16 + columns // 16
+        stack = (uniform_words(rng, experts * words), lognormal_f16(rng, experts * columns),
+                 lognormal_f16(rng, experts * rows), lognormal_f16(rng, experts * waves))
+        layer.stacks[kind] = stack
+        mats = getattr(layer, kind)
+        for e in range(experts):
+            mats.append(ExpertMatrix(rows, columns, stack[0][e * words:(e + 1) * words],
+                                     stack[1][e * columns:(e + 1) * columns],
+                                     stack[2][e * rows:(e + 1) * rows],
+                                     stack[3][e * waves:(e + 1) * waves], etlut))
+    layer.shared_gate = ne_matrix(rng, expert_hidden, hidden, ntlut)
+    layer.shared_up = ne_matrix(rng, expert_hidden, hidden, ntlut)
+    layer.shared_down = ne_matrix(rng, hidden, expert_hidden, ntlut)
+    return layer
+
+
 @dataclass
 class FullAttention:
     """One full-attention layer (adi::FullAttentionDescriptor): 16 query
@@ -295,10 +332,63 @@ class DecoderLayer:
 
 
 def decoder_layer(rng, full: bool, hidden: int, expert_hidden: int, experts: int,
-                  etlut: np.ndarray, ntlut: np.ndarray) -> DecoderLayer:
+                  etlut: np.ndarray, ntlut: np.ndarray, stacked: bool = False) -> DecoderLayer:
     norm = lambda: bf16_bits_rne(rng.normal(0.0, 0.1, hidden).astype(np.float32))
+    make_moe = stacked_moe_layer if stacked else moe_layer
     return DecoderLayer(
         norm(), norm(),
         full_attention(rng, hidden, ntlut) if full else None,
         None if full else linear_attention(rng, hidden, ntlut),
-        moe_layer(rng, hidden, expert_hidden, experts, etlut=etlut, ntlut=ntlut))
+        make_moe(rng, hidden, expert_hidden, experts, etlut=etlut, ntlut=ntlut))
+
+
+# ---- the hybrid decoder stack ------------------------------------------------
+
+@dataclass
+class StackGeometry:
+    """A Qwen3.5-MoE-style hybrid stack: every fourth layer full GQA
+    attention (16 query / 2 KV heads of 256), the others Gated DeltaNet, each
+    with the 256-expert top-8 MoE block and a shared expert
+    (src/model.cpp:228-262 fixes the same pattern at 40 layers)."""
+    layers: int = 40
+    hidden: int = 2048
+    expert_hidden: int = 512
+    experts: int = 256
+    vocab: int = 151936
+    prompt: int = 256
+    ubatch: int = 128
+    greedy_steps: int = 64
+    embedding_exceptions: int = 64
+
+    @staticmethod
+    def full_attention(layer: int) -> bool:
+        return layer % 4 == 3
+
+
+STACK_CONFIG = 5  # seed stream of the full-stack workload
+
+
+def stack_codebooks(config: int = STACK_CONFIG):
+    rng = rng_for(config, 0)
+    return expert_tlut(rng), ne_tlut(rng)
+
+
+def stack_layer(geometry: StackGeometry, index: int, etlut: np.ndarray, ntlut: np.ndarray,
+                config: int = STACK_CONFIG) -> DecoderLayer:
+    """Layer `index` of the stack, from a seed stream of its own, so layers
+    can be drawn (and released) one at a time."""
+    g = geometry
+    return decoder_layer(rng_for(config, 100 + index), g.full_attention(index), g.hidden,
+                         g.expert_hidden, g.experts, etlut, ntlut, stacked=True)
+
+
+def stack_token_side(geometry: StackGeometry, config: int = STACK_CONFIG):
+    """Embedding table, int5 head, final norm weights (bf16) and the prompt's
+    token ids of the stack."""
+    g = geometry
+    emb = embedding(rng_for(config, 1), g.vocab, g.hidden, exceptions=g.embedding_exceptions)
+    head = head_chunk(rng_for(config, 2), g.vocab, g.hidden)
+    rng = rng_for(config, 3)
+    final_norm = bf16_bits_rne(rng.normal(0.0, 0.1, g.hidden).astype(np.float32))
+    prompt = rng.integers(0, g.vocab, g.prompt).astype(np.uint32)
+    return emb, head, final_norm, prompt

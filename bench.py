@@ -1,23 +1,30 @@
 """Benchmark of the MI355X packed-weight hot path: one MoE block (router,
 top-8 routing, stable dispatch, trellis-packed SwiGLU experts, route-order
-combine, gated shared expert) at ubatch 1, 128 and 512 tokens, plus the
+combine, gated shared expert) at ubatch 1, 4, 16, 128 and 512 tokens, plus the
 packed projections (2048x2048 non-expert, 151936x2048 int5 output head), the
-token side of decoding (embedding rows, greedy and top-p choice) and the
+token side of decoding (embedding rows, greedy and top-p choice), the
 attention half of a decode step (full GQA attention, Gated DeltaNet, a whole
-decoder layer).
+decoder layer) and the full 40-layer hybrid stack (256-token prefill at
+ubatch 128, 64 greedy decode steps).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
 Prints one JSON line. `value` is MoE-layer tokens/s at ubatch 1 (decode);
 the other ubatches and the projections are reported under `per_ubatch` and
-`projections`. Weights are synthetic (seeded, reference codec formats); the
-steps cycle through 8 layers and a pool of input batches, so each step routes
-to experts the recent steps did not touch and the 256 MB Infinity Cache does
-not hold the working set. Inputs are resident in HBM before the timed region.
+`projections`. Each figure is the median of 7 runs of K timed steps after W
+warm-up steps (the reference reports medians of 7, docs/benchmarks.md:262-265).
+Weights are synthetic (seeded, reference codec formats); the steps cycle
+through 8 layers and a pool of input batches, so each step routes to experts
+the recent steps did not touch and the 256 MB Infinity Cache does not hold
+the working set. Inputs are resident in HBM before the timed region.
 The roofline object is for the kernel with the largest share of the headline
-step time, timed with HIP events on the stream the library launches on; its
-`traffic` is the measured HBM bytes per launch from the committed counter
-summary (profiles/moe_layer_hbm_traffic.md), or null without one.
+step time; its launch times come from start/stop events the runtime stamps
+from each launch's own dispatch (the kernel's execution, as a kernel trace
+reports it) over a separate pass of the same steps, and its `traffic` is the
+measured HBM bytes per launch from the committed counter summary
+(profiles/moe_layer_hbm_traffic.md), or null without one. `checksum` holds
+the FNV-1a digests of the output bits of one layer call on each side
+(src/main.cpp:90-103) and their largest relative difference.
 """
 from __future__ import annotations
 
@@ -56,9 +63,12 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--layers", type=int, default=8, help="distinct layers in the weight rotation")
-    p.add_argument("--ubatch", type=str, default="1,128,512")
+    p.add_argument("--ubatch", type=str, default="1,4,16,128,512")
+    p.add_argument("--runs", type=int, default=7, help="timed runs per figure (median reported)")
+    p.add_argument("--no-stack", action="store_true", help="skip the 40-layer stack")
     p.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU baseline budget per ubatch")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--cpu-child", action="store_true", help=argparse.SUPPRESS)
     p.add_argument("--no-projections", action="store_true")
     p.add_argument("--copy-bytes", type=int, default=0,
                    help="first run a plain device-to-device copy of this many bytes three times "
@@ -94,7 +104,9 @@ def input_pool_size(ubatch):
     return 64 if ubatch < 16 else (4 if ubatch < 256 else 2)
 
 
-def moe_bench(torch, hip, ctx, layers, xs, biases, steps, warmup):
+def moe_bench(torch, hip, ctx, layers, xs, biases, steps, warmup, runs):
+    """Median wall time of `runs` runs of `steps` timed steps, the distinct
+    experts per step, and a per-kernel timing pass over the same steps."""
     batch = xs[0].shape[0]
     out = torch.empty((batch, HIDDEN), dtype=torch.float32, device="cuda")
     routes = torch.empty(batch * 8, dtype=torch.int32, device="cuda")
@@ -106,25 +118,34 @@ def moe_bench(torch, hip, ctx, layers, xs, biases, steps, warmup):
 
     for s in range(warmup):
         step(s)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for s in range(warmup, warmup + steps):
-        step(s)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    walls = []
+    for r in range(runs):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(warmup + r * steps, warmup + (r + 1) * steps):
+            step(s)
+        torch.cuda.synchronize()
+        walls.append(time.perf_counter() - t0)
     # distinct experts per step for the byte count
     active = []
     for s in range(warmup, warmup + steps):
         step(s)
         torch.cuda.synchronize()
         active.append(len(np.unique(routes.cpu().numpy())))
-    # per-kernel event timing in a separate pass over the same steps
+    # per-kernel timing in a separate pass over the same steps
     ctx.profiling(True)
     for s in range(warmup, warmup + steps):
         step(s)
     prof = ctx.profile()
     ctx.profiling(False)
-    return wall, float(np.mean(active)), prof
+    return walls, float(np.mean(active)), prof
+
+
+def fnv1a64(data: bytes, h: int = 0xCBF29CE484222325) -> int:
+    """FNV-1a over raw bytes (hash_bytes, src/main.cpp:90-103)."""
+    for b in data:
+        h = ((h ^ b) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    return h
 
 
 def copy_calibration(torch, nbytes):
@@ -204,7 +225,21 @@ def roofline_kernel(prof, active, ubatch):
     return None
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(layer_host, xs, biases, seconds):
+    """The reference's own CPU layer (compiled from its sources, its worker
+    pool at ADI_THREADS threads) on the bench's first layer and inputs: one
+    warm call, then timed calls for about `seconds` per ubatch. Returns the
+    warm call's outputs too, for the checksum."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle
     if pyoracle.ref_available():
@@ -217,9 +252,9 @@ def cpu_baseline(layer_host, xs, biases, seconds):
         lib = pyoracle.load_oracle()
         kind, cores, isa = "port", os.cpu_count() or 1, "scalar-order C"
         run = lambda x, b: pyoracle.moe_forward(lib, layer_host, x, isa=16, logit_bias=b)
-    results = {}
+    results, outputs = {}, {}
     for u, x in xs.items():
-        run(x, biases[u])  # warm call
+        outputs[u] = run(x, biases[u])[0]  # warm call
         n, t0 = 0, time.perf_counter()
         while True:
             run(x, biases[u])
@@ -229,10 +264,52 @@ def cpu_baseline(layer_host, xs, biases, seconds):
         dt = (time.perf_counter() - t0) / n
         results[u] = {"tokens_per_s": round(u / dt, 1), "ms_per_step": round(dt * 1e3, 3),
                       "calls": n}
-    return kind, cores, isa, results
+    return kind, cores, isa, results, outputs
 
 
-def projections(torch, hip, ctx, steps):
+def cpu_child(args):
+    """--cpu-child: the CPU baseline alone, in a process of its own (started
+    with ADI_THREADS=1 for the single-thread figure; it never touches the GPU)."""
+    from adi_amd import synthetic as syn
+    layer_host = syn.moe_layer(syn.rng_for(2, 0))
+    xs, biases = {}, {}
+    for u in [int(v) for v in args.ubatch.split(",")]:
+        r = syn.rng_for(3 if u >= 64 else 2, u)
+        xs[u] = syn.hidden_states(r, u, HIDDEN)
+        biases[u] = syn.zipf_bias(r, EXPERTS) if u >= 64 else None
+    kind, cores, isa, results, _ = cpu_baseline(layer_host, xs, biases, args.cpu_seconds)
+    print(json.dumps({"kind": kind, "cores": cores, "isa": isa,
+                      "per_ubatch": {str(k): v for k, v in results.items()}}))
+
+
+def cpu_single_thread(args):
+    import subprocess
+    env = dict(os.environ, ADI_THREADS="1", OMP_NUM_THREADS="1")
+    cmd = [sys.executable, os.path.abspath(__file__), "--cpu-child", "--ubatch", args.ubatch,
+           "--cpu-seconds", str(args.cpu_seconds / 2)]
+    proc = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=600)
+    if proc.returncode != 0:
+        log(f"single-thread CPU baseline failed: {proc.stderr[-400:]}")
+        return None
+    return json.loads(proc.stdout.strip().splitlines()[-1])
+
+
+def median_seconds(torch, fn, steps, runs, warm=3):
+    """Median over `runs` runs of the mean time of `steps` calls of fn."""
+    for _ in range(warm):
+        fn(0)
+    times = []
+    for r in range(runs):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            fn(r * steps + i)
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) / steps)
+    return float(np.median(times))
+
+
+def projections(torch, hip, ctx, steps, runs):
     from adi_amd import synthetic as syn
     res = {}
     rng = syn.rng_for(1, 0)
@@ -241,14 +318,8 @@ def projections(torch, hip, ctx, steps):
     for batch in (1, 4):
         x = ctx.to_device(syn.rms_normalized(syn.hidden_states(rng, batch, HEAD_COLUMNS)))
         out = torch.empty((batch, HEAD_ROWS), dtype=torch.float32, device="cuda")
-        for i in range(3):
-            hip.head_matmul(ctx, heads[i % copies], x, batch, out)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for i in range(steps):
-            hip.head_matmul(ctx, heads[i % copies], x, batch, out)
-        torch.cuda.synchronize()
-        dt = (time.perf_counter() - t0) / steps
+        dt = median_seconds(torch, lambda i: hip.head_matmul(ctx, heads[i % copies], x, batch, out),
+                            steps, runs)
         res[f"head_151936x2048_b{batch}"] = {
             "ms_per_call": round(dt * 1e3, 4), "vectors_per_s": round(batch / dt, 1),
             "packed_gbs": round(HEAD_BYTES / dt / 1e9, 1),
@@ -266,24 +337,15 @@ def projections(torch, hip, ctx, steps):
     for batch in (1, 4):
         x = ctx.to_device(syn.hidden_states(rng, batch, 2048))
         out = torch.empty((batch, 2048), dtype=torch.float32, device="cuda")
-        n = max(steps, count)
-        for i in range(count):
-            ctx.check(ctx.lib.adi_hip_ne_matmul(ctx.handle, hip.C.byref(mats[i]), x.data_ptr(),
-                                                batch, out.data_ptr()))
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for i in range(n):
-            ctx.check(ctx.lib.adi_hip_ne_matmul(ctx.handle, hip.C.byref(mats[i % count]),
-                                                x.data_ptr(), batch, out.data_ptr()))
-        torch.cuda.synchronize()
-        dt = (time.perf_counter() - t0) / n
+        call = lambda i: ctx.check(ctx.lib.adi_hip_ne_matmul(
+            ctx.handle, hip.C.byref(mats[i % count]), x.data_ptr(), batch, out.data_ptr()))
+        dt = median_seconds(torch, call, max(steps, count), runs)
         res[f"ne_2048x2048_b{batch}"] = {
             "ms_per_call": round(dt * 1e3, 4), "vectors_per_s": round(batch / dt, 1),
             "packed_gbs": round(nbytes / dt / 1e9, 1),
             "hbm_frac": round(nbytes / dt / 1e9 / HBM_PEAK_GBS, 4)}
     res.update(decode_side(torch, hip, ctx, steps))
     res.update(attention_side(torch, hip, ctx, steps))
-    res.update(stack_side(torch, hip, ctx))
     return res
 
 
@@ -370,67 +432,79 @@ def attention_side(torch, hip, ctx, steps):
     return res
 
 
-def stack_side(torch, hip, ctx):
-    """A 3:1 hybrid stack of four decoder layers at hidden 2048 (three Gated
-    DeltaNet layers then full attention, each with the 256-expert MoE block),
-    a 248,320-token embedding and int5 head: a 256-token prompt prefilled in
-    chunks of 128, then 64 greedy steps with every token chosen and embedded
-    on the device. Each full-model figure would scale with its 40 layers."""
+def stack40(torch, hip, ctx, runs):
+    """The full hybrid stack of synthetic.StackGeometry: 40 layers at hidden
+    2048 (every fourth full GQA attention, the others Gated DeltaNet, each
+    with the 256-expert MoE block), the 151,936-token embedding and int5 head.
+    A 256-token prompt is prefilled in chunks of 128 (every layer per chunk),
+    then 64 greedy steps run with every token chosen and embedded on the
+    device. The weights are drawn layer by layer and uploaded (about 7 GB)."""
     from adi_amd import synthetic as syn
-    rng = syn.rng_for(6, 0)
-    etlut, ntlut = syn.expert_tlut(rng), syn.ne_tlut(rng)
+    g = syn.StackGeometry()
+    etlut, ntlut = syn.stack_codebooks()
     ebook, nbook = ctx.expert_codebook(etlut), ctx.ne_codebook(ntlut)
-    vocab, prompt, chunk, steps = 248320, 256, 128, 64
-    layers = [hip.upload_decoder_layer(ctx, syn.decoder_layer(rng, i % 4 == 3, HIDDEN, EXPERT_HIDDEN,
-                                                              EXPERTS, etlut, ntlut), ebook, nbook)
-              for i in range(4)]
-    emb = hip.upload_embedding(ctx, syn.embedding(rng, vocab, HIDDEN))
-    head = hip.upload_head(ctx, syn.head_chunk(rng, vocab, HIDDEN))
-    final_norm = ctx.to_device(syn.bf16_bits_rne(rng.normal(0.0, 0.1, HIDDEN).astype(np.float32)))
-    capacity = prompt + steps
+    layers = []
+    for i in range(g.layers):
+        layers.append(hip.upload_decoder_layer(ctx, syn.stack_layer(g, i, etlut, ntlut), ebook, nbook))
+    emb_host, head_host, norm_host, prompt_host = syn.stack_token_side(g)
+    emb, head = hip.upload_embedding(ctx, emb_host), hip.upload_head(ctx, head_host)
+    final_norm = ctx.to_device(norm_host)
+    del emb_host, head_host
+    capacity = g.prompt + g.greedy_steps
     lib = hip.load()
+    tokens = torch.tensor(prompt_host.astype(np.int32), device="cuda")
+    hidden = torch.empty((g.ubatch, g.hidden), dtype=torch.float32, device="cuda")
+    normed = torch.empty((1, g.hidden), dtype=torch.float32, device="cuda")
+    logits = torch.empty((1, g.vocab), dtype=torch.float32, device="cuda")
+    token = torch.empty(1, dtype=torch.int32, device="cuda")
+    states = [hip.layer_state(g.full_attention(i), capacity) for i in range(g.layers)]
 
     def run():
-        states = [hip.layer_state(i % 4 == 3, capacity) for i in range(4)]
-        tokens = torch.tensor(rng.integers(0, vocab, prompt).astype(np.int32), device="cuda")
-        hidden = torch.empty((chunk, HIDDEN), dtype=torch.float32, device="cuda")
-        normed = torch.empty((1, HIDDEN), dtype=torch.float32, device="cuda")
-        logits = torch.empty((1, vocab), dtype=torch.float32, device="cuda")
-        token = torch.empty(1, dtype=torch.int32, device="cuda")
+        for state, keep in states:
+            for t in keep:
+                t.zero_()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for c in range(0, prompt, chunk):
-            hip.embedding_rows(ctx, emb, tokens[c:c + chunk], chunk, hidden)
+        for c in range(0, g.prompt, g.ubatch):
+            hip.embedding_rows(ctx, emb, tokens[c:c + g.ubatch], g.ubatch, hidden)
             for layer, (state, _) in zip(layers, states):
-                hip.prefill_layer(ctx, layer, c, chunk, hidden, state)
-        last = hidden[chunk - 1:chunk]
+                hip.prefill_layer(ctx, layer, c, g.ubatch, hidden, state)
+        last = hidden[g.ubatch - 1:g.ubatch]
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-        for step in range(steps):
-            ctx.check(lib.adi_hip_rms_norm(ctx.handle, last.data_ptr(), final_norm.data_ptr(), HIDDEN,
-                                           1, 1.0, 1e-6, normed.data_ptr()))
+        for step in range(g.greedy_steps):
+            ctx.check(lib.adi_hip_rms_norm(ctx.handle, last.data_ptr(), final_norm.data_ptr(),
+                                           g.hidden, 1, 1.0, 1e-6, normed.data_ptr()))
             hip.head_matmul(ctx, head, normed, 1, logits)
-            hip.argmax_rows(ctx, logits, 1, vocab, token)
+            hip.argmax_rows(ctx, logits, 1, g.vocab, token)
             hip.embedding_rows(ctx, emb, token, 1, hidden)
             last = hidden[0:1]
             for layer, (state, _) in zip(layers, states):
-                hip.decode_layer(ctx, layer, prompt + step, last, state)
+                hip.decode_layer(ctx, layer, g.prompt + step, last, state)
         torch.cuda.synchronize()
         t2 = time.perf_counter()
         return t1 - t0, t2 - t1
 
     run()  # warm-up: workspaces, kernels
-    prefill_s, decode_s = run()
-    return {"hybrid4_2048": {
-        "prefill_tokens_per_s": round(prompt / prefill_s, 1),
+    times = [run() for _ in range(runs)]
+    prefill_s = float(np.median([t[0] for t in times]))
+    decode_s = float(np.median([t[1] for t in times]))
+    del layers, states
+    torch.cuda.empty_cache()
+    return {"stack40": {
+        "prefill_tokens_per_s": round(g.prompt / prefill_s, 1),
         "prefill_ms": round(prefill_s * 1e3, 2),
-        "decode_ms_per_token": round(decode_s / steps * 1e3, 3),
-        "decode_tokens_per_s": round(steps / decode_s, 1),
-        "layers": 4, "prompt": prompt, "ubatch": chunk, "greedy_steps": steps}}
+        "decode_ms_per_token": round(decode_s / g.greedy_steps * 1e3, 3),
+        "decode_tokens_per_s": round(g.greedy_steps / decode_s, 1),
+        "layers": g.layers, "hidden": g.hidden, "vocab": g.vocab, "prompt": g.prompt,
+        "ubatch": g.ubatch, "greedy_steps": g.greedy_steps}}
 
 
 def main():
     args = parse()
+    if args.cpu_child:
+        cpu_child(args)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is "
                           "described in DESIGN.md but not built", "n_gpus": args.gpus}))
@@ -460,17 +534,20 @@ def main():
         biases_host[u] = syn.zipf_bias(r, EXPERTS) if u >= 64 else None
 
     per = {}
+    gpu_out = {}
     headline = None
     for u in ubatches:
         log(f"moe layer ubatch {u}")
         xs = [ctx.to_device(x) for x in xs_host[u]]
         bias = None if biases_host[u] is None else ctx.to_device(biases_host[u])
-        wall, active, prof = moe_bench(torch, hip, ctx, layers, xs, [bias] * len(xs), args.steps,
-                                       args.warmup)
+        walls, active, prof = moe_bench(torch, hip, ctx, layers, xs, [bias] * len(xs), args.steps,
+                                        args.warmup, args.runs)
+        wall = float(np.median(walls))
         ms = wall / args.steps * 1e3
         layer_bytes = FIXED_LAYER_BYTES + PER_EXPERT_BYTES * active
         entry = {
             "tokens_per_s": round(u / (wall / args.steps), 1), "ms_per_step": round(ms, 4),
+            "runs_ms_per_step": [round(w / args.steps * 1e3, 4) for w in walls],
             "active_experts": round(active, 1),
             "layer_packed_bytes": int(layer_bytes),
             "layer_hbm_frac": round(layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -479,31 +556,53 @@ def main():
             "kernels_us_per_step": {k: round(v[1] * 1e3 / args.steps, 2) for k, v in
                                     sorted(prof.items(), key=lambda kv: -kv[1][1])},
         }
+        # one call of layer 0 on the first input: the checksum's GPU side
+        out = torch.empty((u, HIDDEN), dtype=torch.float32, device="cuda")
+        hip.moe_forward(ctx, layers[0], xs[0], u, bias, out, None, None)
+        gpu_out[u] = out.cpu().numpy()
         per[str(u)] = entry
         if headline is None:
             headline = (u, entry)
+        del xs
 
-    proj = {} if args.no_projections else projections(torch, hip, ctx, args.steps)
+    proj = {} if args.no_projections else projections(torch, hip, ctx, args.steps, args.runs)
+    if not args.no_stack:
+        log("40-layer stack")
+        del layers
+        torch.cuda.empty_cache()
+        proj.update(stack40(torch, hip, ctx, min(args.runs, 3)))
 
     cpu = None
+    checksum = None
     if not args.no_cpu:
         log("cpu baseline")
-        kind, cores, isa, results = cpu_baseline(layer_host, {u: v[0] for u, v in xs_host.items()},
-                                                 biases_host, args.cpu_seconds)
+        kind, cores, isa, results, cpu_out = cpu_baseline(
+            layer_host, {u: v[0] for u, v in xs_host.items()}, biases_host, args.cpu_seconds)
+        single = cpu_single_thread(args)
         u0 = headline[0]
         cpu = {"value": results[u0]["tokens_per_s"], "unit": "tokens/s", "cores": cores,
-               "kind": kind, "isa": isa,
+               "kind": kind, "isa": isa, "cpu_model": cpu_model(),
                "sample": f"one MoE layer (2048 hidden, 256 experts, top-8 + shared) at ubatch "
-                         f"{u0}, {results[u0]['calls']} calls; other ubatches in per_ubatch",
-               "per_ubatch": {str(k): v for k, v in results.items()}}
+                         f"{u0}, {results[u0]['calls']} calls after one warm call; other "
+                         f"ubatches in per_ubatch",
+               "per_ubatch": {str(k): v for k, v in results.items()},
+               "single_thread": None if single is None else single["per_ubatch"]}
         for k, v in results.items():
             per[str(k)]["cpu_tokens_per_s"] = v["tokens_per_s"]
+        checksum = {}
+        for u in ubatches:
+            g, c = gpu_out[u], cpu_out[u]
+            err = float(np.max(np.abs(g - c).max(axis=1) / np.abs(c).max(axis=1)))
+            checksum[str(u)] = {"gpu_fnv1a": f"{fnv1a64(g.tobytes()):#018x}",
+                                "cpu_fnv1a": f"{fnv1a64(c.tobytes()):#018x}",
+                                "max_rel_error": float(f"{err:.3g}")}
 
     u0, e0 = headline
     line = {
         "metric": "MoE-layer + projection tokens/s at ubatch 1/128/512; % of HBM/MFMA peak",
         "value": e0["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": e0["ms_per_step"],
+        "steps": args.steps, "warmup": args.warmup, "runs": args.runs,
+        "ms_per_step": e0["ms_per_step"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
         "data": "synthetic (seeded reference codecs: 1.5 bpw expert trellis, 4 bpw NE trellis, "
                 "int5_g64 head; random-init)",
@@ -513,6 +612,7 @@ def main():
                    "zipf_bias_at_ubatch_ge": 64},
         "roofline": e0["roofline"],
         "cpu_baseline": cpu,
+        "checksum": checksum,
         "per_ubatch": per,
         "projections": proj,
     }

@@ -754,6 +754,15 @@ int ao_embedding_row(const ao_embedding *e, uint32_t token, float *output) {
     return AO_OK;
 }
 
+uint64_t ao_fnv1a64(uint64_t hash, const void *data, size_t bytes) {
+    const unsigned char *p = (const unsigned char *)data;
+    for (size_t i = 0; i < bytes; ++i) {
+        hash ^= p[i];
+        hash *= 0x00000100000001B3ULL;
+    }
+    return hash;
+}
+
 uint32_t ao_argmax(const float *logits, uint32_t count) {
     uint32_t best = 0;
     for (uint32_t i = 1; i < count; ++i) {

@@ -17,6 +17,7 @@
 #ifndef ADI_ORACLE_H
 #define ADI_ORACLE_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -179,6 +180,11 @@ int ao_moe_forward(const ao_moe_layer *layer, const float *inputs,
 
 /* Embedding row decode (mach_embedding_row, src/kernels.cpp:802-845). */
 int ao_embedding_row(const ao_embedding *embedding, uint32_t token, float *output);
+
+/* FNV-1a (64-bit) over raw bytes, continuing from `hash` (the benchmark's
+ * hash_bytes, src/main.cpp:90-103; start from 0xCBF29CE484222325 as
+ * decoder_state_checksum does, src/main.cpp:105-117). */
+uint64_t ao_fnv1a64(uint64_t hash, const void *data, size_t bytes);
 
 /* Greedy choice of sample_token at temperature 0: the first index of the
  * largest logit (std::max_element, src/generation.cpp:180-183). */

@@ -135,4 +135,8 @@ int bd_rms_norm(int hip, const float *input, const std::uint16_t *weight, std::s
     });
 }
 
+int bd_release_weights(char *error, std::size_t error_size) {
+    return run(error, error_size, [&] { adi::hip_backend_release_weights(); });
+}
+
 }  // extern "C"

@@ -139,6 +139,7 @@ def load_oracle() -> C.CDLL:
              C.c_uint32, f32p, u32p, f32p, C.c_int)
     _declare(lib, "ao_embedding_row", C.c_int, C.POINTER(Embedding), C.c_uint32, f32p)
     _declare(lib, "ao_argmax", C.c_uint32, f32p, C.c_uint32)
+    _declare(lib, "ao_fnv1a64", C.c_uint64, C.c_uint64, C.c_void_p, C.c_size_t)
     _declare(lib, "ao_sample_token", C.c_int, f32p, C.c_uint32, C.c_float, C.c_float, C.c_uint64, u32p)
     _declare(lib, "ao_normalize_head", C.c_int, f32p, u16p, C.c_uint32, C.c_float)
     _declare(lib, "ao_rope_table", None, C.c_uint32, f32p, f32p)

@@ -52,6 +52,10 @@ def name(which: int) -> str:
     return out.value.decode()
 
 
+def release_weights():
+    _call(load().bd_release_weights)
+
+
 def expert_matmul(which, m, x, batch, out_size=None, x_size=None):
     x = np.ascontiguousarray(x, np.float32)
     out = np.zeros(batch * m.rows if out_size is None else out_size, np.float32)

@@ -48,3 +48,20 @@ def max_rel_error(got, want):
     want = np.asarray(want, np.float64).reshape(-1, np.shape(want)[-1])
     scale = np.maximum(np.abs(want).max(axis=1), 1e-30)
     return float((np.abs(got - want).max(axis=1) / scale).max())
+
+
+def error_report(got, want):
+    """The three output-error figures of the measurement contract, over the
+    whole array: the max-normalised error (as max_rel_error), the normwise
+    relative L2 error ||g - c|| / ||c||, and the largest elementwise relative
+    error |g_i - c_i| / |c_i| over the elements with |c_i| >= 1% of max |c|."""
+    import numpy as np
+    g = np.asarray(got, np.float64).ravel()
+    c = np.asarray(want, np.float64).ravel()
+    scale = max(float(np.abs(c).max()), 1e-30)
+    big = np.abs(c) >= 0.01 * scale
+    return {
+        "max_rel": float(np.abs(g - c).max() / scale),
+        "l2_rel": float(np.linalg.norm(g - c) / max(float(np.linalg.norm(c)), 1e-30)),
+        "elem_rel_1pct": float((np.abs(g - c)[big] / np.abs(c)[big]).max()) if big.any() else 0.0,
+    }

@@ -113,3 +113,63 @@ def test_sample_token_rejects_parameters(oracle, temperature, top_p):
     logits = np.zeros(4, np.float32)
     with pytest.raises(ValueError):
         po.sample_token(oracle, logits, temperature, top_p, 1)
+
+
+def _device_order_sum(p: np.ndarray, threads: int) -> float:
+    """sum(p) in the order one block of `threads` threads adds a span on the
+    device: thread t adds the float4 groups t, t + threads, ... in index
+    order, each lane pair of a wave is then added in a butterfly (offsets 32
+    down to 1), and the waves' sums are added in wave order from 0."""
+    assert p.size % 4 == 0
+    groups = p.reshape(-1, 4)
+    acc = np.zeros(threads, np.float64)
+    for start in range(0, groups.shape[0], threads):
+        block = groups[start:start + threads]
+        for c in range(4):
+            acc[:block.shape[0]] = acc[:block.shape[0]] + block[:, c]
+    lanes = acc.reshape(-1, 64)
+    for offset in (32, 16, 8, 4, 2, 1):
+        lanes = lanes + lanes[:, np.arange(64) ^ offset]
+    total = 0.0
+    for w in range(lanes.shape[0]):
+        total = total + lanes[w, 0]
+    return total
+
+
+def _device_denominator(p: np.ndarray) -> float:
+    """adi_hip_sample_rows' sum of p: one 1024-thread block below 32,768
+    logits; above, spans of up to 64 blocks of 256 threads, added in span
+    order (k_expsum_parts, k_sample_rows)."""
+    n = p.size
+    if n < 32768:
+        return _device_order_sum(p, 1024)
+    wanted = min(64, -(-n // 4096))
+    span = (-(-n // wanted) + 3) & ~3
+    total = 0.0
+    for begin in range(0, n, span):
+        total = total + _device_order_sum(p[begin:begin + span], 256)
+    return total
+
+
+@pytest.mark.parametrize("count", [4096, 151936, 248320])
+def test_top_p_denominator_order_bound(count):
+    """The sampler's one known departure from sample_token: the reference adds
+    sum(p) in descending-logit order (src/generation.cpp:185-194), the device
+    in its thread/tree order. Both are double sums of positive terms, so they
+    differ by less than the recursive-summation bound (count - 1) * 2^-53
+    relative (measured: 3.5e-15 at 4,096 logits, 2.5e-14 at 151,936, 4.4e-14 at
+    248,320). A draw picks another token only if its threshold lies within that
+    relative distance of a running sum."""
+    rng = np.random.default_rng([syn.SEED_BASE, 91, count])
+    worst = 0.0
+    for _ in range(4):
+        logits = rng.normal(0.0, 2.0, count).astype(np.float32)
+        logits[rng.integers(0, count, 16)] += 12.0
+        m = np.float64(logits.max())
+        p = np.exp((logits.astype(np.float64) - m) / np.float64(np.float32(0.7)))
+        order = np.lexsort((np.arange(count), -logits.astype(np.float64)))
+        reference = np.cumsum(p[order])[-1]  # sequential adds in sorted order
+        device = _device_denominator(p)
+        worst = max(worst, abs(device - reference) / reference)
+    print(f"count {count}: largest relative denominator difference {worst:.3g}")
+    assert worst <= (count - 1) * 2.0 ** -53

@@ -124,3 +124,22 @@ def test_backend_shape_errors_match_the_reference(batch, x_extra, out_extra):
         errors.append((info.value.status, info.value.message))
     assert errors[0] == errors[1]
     assert errors[0][0] == 1
+
+
+def test_backend_weight_cache_follows_contents():
+    """The HIP table caches device copies of weights by host address. New
+    contents at the same address replace the copy (results follow the new
+    weights, as the CPU table's do), and hip_backend_release_weights() drops
+    every copy; calls after it upload again."""
+    rng = syn.rng_for(1, 977)
+    m = syn.ne_matrix(rng, 512, 2048, syn.ne_tlut(rng))
+    x = syn.hidden_states(rng, 1, 2048)
+    first = bb.ne_matmul(bb.HIP, m, x, 1)
+    assert max_rel_error(first, bb.ne_matmul(bb.CPU, m, x, 1)) <= 1e-3
+    m.trellis[:] = syn.uniform_words(rng, m.trellis.size)  # same buffer, new weights
+    second = bb.ne_matmul(bb.HIP, m, x, 1)
+    assert max_rel_error(second, bb.ne_matmul(bb.CPU, m, x, 1)) <= 1e-3
+    assert not np.array_equal(first, second)
+    bb.release_weights()
+    third = bb.ne_matmul(bb.HIP, m, x, 1)
+    assert np.array_equal(third.view(np.uint32), second.view(np.uint32))

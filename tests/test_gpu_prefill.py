@@ -107,3 +107,31 @@ def test_prefill_rejections(gpu, oracle, tluts):
     with pytest.raises(hip.HipError, match="full attention state or input shape mismatch"):
         hip.full_attention_prefill(gpu, d, 0, 0, x, out, cache, cache.clone(), 5)
     torch.cuda.synchronize()
+
+
+def test_chunk_rope_equals_single_tokens(gpu, tluts):
+    """A chunk's keys are bit-identical with the keys of its tokens projected
+    one at a time: the key projection runs each row in the same order at any
+    batch below the MFMA path, so the only difference could be the RoPE table,
+    and the chunk's must be rope_table(position + b) itself (the reference
+    builds its prefill table on the host, src/executor.cpp:1853-1866)."""
+    rng = syn.rng_for(64, 0)
+    layer = syn.full_attention(rng, HIDDEN, tluts[1])
+    d = hip.upload_full_attention(gpu, layer, gpu.ne_codebook(tluts[1]))
+    for position, count in ((0, 5), (1000, 9), (5000, 3)):
+        capacity = position + count
+        x = dev(syn.rms_normalized(syn.hidden_states(rng, count, HIDDEN)))
+        chunk_keys = torch.zeros((capacity, 2, 256), dtype=torch.float32, device="cuda")
+        chunk_values = torch.zeros_like(chunk_keys)
+        out = torch.empty((count, HIDDEN), dtype=torch.float32, device="cuda")
+        hip.full_attention_prefill(gpu, d, position, count, x, out, chunk_keys, chunk_values,
+                                   capacity)
+        one_keys = torch.zeros_like(chunk_keys)
+        one_values = torch.zeros_like(chunk_keys)
+        row = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+        for b in range(count):
+            hip.full_attention_forward(gpu, d, position + b, x[b].contiguous(), row, one_keys,
+                                       one_values, capacity)
+        got = chunk_keys.cpu().numpy()[position:].view(np.uint32)
+        want = one_keys.cpu().numpy()[position:].view(np.uint32)
+        assert np.array_equal(got, want), (position, count)
