@@ -122,6 +122,23 @@ int adi_hip_context_create(int device, adi_hip_context **out) {
     }
     ctx->device = device;
     ctx->cu_count = props.multiProcessorCount;
+    // each device holds its own copy of the static scratch array: take this
+    // device's address with the device current
+    int previous = 0;
+    hipError_t status = hipGetDevice(&previous);
+    if (status == hipSuccess) {
+        status = hipSetDevice(device);
+    }
+    if (status == hipSuccess) {
+        status = adi_hip::static_scratch_address(&ctx->static_scratch);
+        (void)hipSetDevice(previous);
+    }
+    if (status != hipSuccess || ctx->static_scratch == nullptr) {
+        record(std::string("adi_hip_context_create: hipGetSymbolAddress failed: ") +
+               hipGetErrorString(status));
+        delete ctx;
+        return ADI_HIP_DEVICE_ERROR;
+    }
     *out = ctx;
     return ADI_HIP_OK;
 }

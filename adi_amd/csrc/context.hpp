@@ -80,6 +80,9 @@ struct adi_hip_context {
     // sin 32] floats), computed on the host and grown on demand
     adi_hip::Workspace rope_cache;
     uint32_t rope_positions = 0;
+    // device address of moe.hip's fixed scratch array on this context's
+    // device (adi_hip_moe_forward_static), taken once at creation
+    void *static_scratch = nullptr;
     bool profiling = false;
     std::vector<adi_hip::KernelStat> stats;
 };
@@ -165,6 +168,10 @@ inline bool set_lds_limit(const void *kernel, size_t bytes) {
               "hipFuncSetAttribute");
     return true;
 }
+
+// The device address of the no-allocation MoE entry's fixed scratch array
+// on the current device (defined beside the array in moe.hip).
+hipError_t static_scratch_address(void **out);
 
 inline uint32_t ceil_div(uint64_t a, uint64_t b) {
     return static_cast<uint32_t>((a + b - 1) / b);

@@ -430,17 +430,22 @@ void validate_layer(const adi_hip_moe_layer *L) {
             "MoE shared expert shape mismatch");
 }
 
-}  // namespace
-}  // namespace adi_hip
+// The fixed scratch of adi_hip_moe_forward_static: every intermediate of a
+// decode batch (batch <= kStaticBatch) of the model's layer geometry fits in
+// it (about 6.5 MiB at batch 16, hidden 2048, 256 experts). Each device
+// holds its own copy until the process ends; host code uses the address
+// static_scratch_address() returns for its device, never this name. Nothing
+// in it needs to start at zero: every kernel writes what it later reads.
+constexpr size_t kStaticScratchBytes = size_t(8) << 20;
+constexpr uint32_t kStaticBatch = 16;
+__device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 
-using namespace adi_hip;
-
-extern "C" {
-
-int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const float *inputs,
-                        uint32_t batch, const float *logit_bias, float *outputs,
-                        uint32_t *route_expert_out, float *route_weight_out) {
-    return guarded(ctx, [&] {
+// One MoE block; `arena` (non-null) is a fixed scratch the call must fit in,
+// otherwise the context workspace grows to the call's plan.
+void moe_forward_body(adi_hip_context *ctx, const adi_hip_moe_layer *L, const float *inputs,
+                      uint32_t batch, const float *logit_bias, float *outputs,
+                      uint32_t *route_expert_out, float *route_weight_out, Workspace *arena) {
+    {
         validate_layer(L);
         require(batch > 0, "MoE batch shape mismatch");
         require(inputs != nullptr && outputs != nullptr, "MoE vector is null");
@@ -458,7 +463,7 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
         const uint32_t ssg = mfma ? ne_mfma_slices(I, H, batch) : ne_splits(H);
         const uint32_t ssd = mfma ? ne_mfma_slices(H, I, batch) : ne_splits(I);
 
-        auto &ws = ctx->workspace;
+        auto &ws = arena != nullptr ? *arena : ctx->workspace;
         ws.used = 0;
         const size_t bytes =
             Workspace::round(B * E * 4) + Workspace::round(B * 4) +
@@ -469,7 +474,12 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
             Workspace::round(P * I * 4) + Workspace::round(sd * P * H * 4) +
             Workspace::round(B * H * 4) * 2 + Workspace::round(ssg * B * I * 4) * 2 +
             Workspace::round(B * I * 4) + Workspace::round(ssd * B * H * 4);
-        ws.ensure(bytes);
+        if (arena != nullptr) {
+            require(bytes <= arena->capacity,
+                    "MoE batch needs more scratch than the fixed no-allocation buffer holds");
+        } else {
+            ws.ensure(bytes);
+        }
         float *logits = ws.take<float>(B * E);
         float *shared_logit = ws.take<float>(B);
         // routes go straight to the caller's buffers when it asks for them
@@ -797,7 +807,43 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const 
                    static_cast<const float *>(sz_down), ssd, B * H, L->shared_down.sv,
                    static_cast<const float *>(shared_logit), hadamard_scale(H), outputs);
         }
+    }
+}
 
+}  // namespace
+
+hipError_t static_scratch_address(void **out) {
+    return hipGetSymbolAddress(out, HIP_SYMBOL(scratch));
+}
+
+}  // namespace adi_hip
+
+using namespace adi_hip;
+
+extern "C" {
+
+int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *L, const float *inputs,
+                        uint32_t batch, const float *logit_bias, float *outputs,
+                        uint32_t *route_expert_out, float *route_weight_out) {
+    return guarded(ctx, [&] {
+        moe_forward_body(ctx, L, inputs, batch, logit_bias, outputs, route_expert_out,
+                         route_weight_out, nullptr);
+    });
+}
+
+int adi_hip_moe_forward_static(adi_hip_context *ctx, const adi_hip_moe_layer *L,
+                               const float *inputs, uint32_t batch, const float *logit_bias,
+                               float *outputs, uint32_t *route_expert_out,
+                               float *route_weight_out) {
+    return guarded(ctx, [&] {
+        require(batch > 0 && batch <= kStaticBatch,
+                "MoE batch for the no-allocation entry must be 1..16");
+        require(ctx->static_scratch != nullptr, "no-allocation scratch address missing");
+        Workspace arena;
+        arena.base = ctx->static_scratch;
+        arena.capacity = kStaticScratchBytes;
+        moe_forward_body(ctx, L, inputs, batch, logit_bias, outputs, route_expert_out,
+                         route_weight_out, &arena);
     });
 }
 

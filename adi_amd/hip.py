@@ -138,6 +138,7 @@ SIGNATURES = [
     ("adi_hip_top_experts", C.c_int, [vp, vp, u32, u32, vp, vp]),
     ("adi_hip_moe_route", C.c_int, [vp, vp, vp, u32, u32, vp, vp, vp, vp, vp, vp]),
     ("adi_hip_moe_forward", C.c_int, [vp, C.POINTER(MoeLayer), vp, u32, vp, vp, vp, vp]),
+    ("adi_hip_moe_forward_static", C.c_int, [vp, C.POINTER(MoeLayer), vp, u32, vp, vp, vp, vp]),
     ("adi_hip_embedding_rows", C.c_int, [vp, C.POINTER(Embedding), vp, u32, vp]),
     ("adi_hip_argmax_rows", C.c_int, [vp, vp, u32, u32, vp]),
     ("adi_hip_sample_rows", C.c_int, [vp, vp, u32, u32, f32, f32, vp, vp]),

@@ -281,6 +281,20 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *layer,
                         const float *logit_bias, float *outputs,
                         uint32_t *route_expert, float *route_weight);
 
+/* adi_hip_moe_forward for a decode batch (1..16 rows) without allocating:
+ * no hipMalloc, hipFree or allocating library call on any path. No
+ * counterpart in the reference; it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * it). The intermediates live in a fixed 8 MiB device array of the library,
+ * one per GPU, held until the process ends; a batch or layer geometry whose
+ * plan exceeds it is rejected (ADI_HIP_INVALID_ARGUMENT, outputs untouched).
+ * Every call on one GPU shares that array: calls that overlap on one GPU (from
+ * several contexts or streams) race. Results equal adi_hip_moe_forward's. */
+int adi_hip_moe_forward_static(adi_hip_context *ctx, const adi_hip_moe_layer *layer,
+                               const float *inputs, uint32_t batch,
+                               const float *logit_bias, float *outputs,
+                               uint32_t *route_expert, float *route_weight);
+
 /* ---- token side of decoding ----------------------------------------------- */
 
 /* Backend::embedding_row -> mach_embedding_row (src/kernels.cpp:802-845) for
