@@ -302,13 +302,85 @@ __device__ __forceinline__ uint32_t tiled_group_base(uint32_t g, uint32_t lane) 
     }
 }
 
-// v = src in the wave layout (src 16-byte aligned when tiled).
+// ---- data handed between blocks of one launch ------------------------------
+//
+// The L2 of each XCD is not coherent with the others', and the device-scope
+// release and acquire fences (an L2 writeback and an L2 invalidate) cost about
+// 0.3 us per block on this part, serialised. Data a block passes to another
+// block of the same launch therefore moves through device-coherent accesses:
+// relaxed device-scope atomics, which compile to sc1 stores (written through
+// to memory) and sc1 loads (not served from a line another XCD may hold
+// stale). The producer waits for its own stores (wait_stores: vmcnt(0)) before
+// the relaxed atomic that signals them; the consumer polls the signal with
+// coherent loads. Bulk data it then reads for the first time in the launch
+// may come through ordinary loads (no cache can hold an older copy of lines
+// the launch has not touched before), which are several times faster than
+// 4-byte coherent loads.
+__device__ __forceinline__ float coherent_load(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t coherent_load(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coherent_store(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coherent_store(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t coherent_add(uint32_t *p, uint32_t v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Waits until every memory access the wave issued has completed.
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
+
+// float4 at p (16-byte aligned), through coherent loads when COHERENT.
+template <bool COHERENT>
+__device__ __forceinline__ float4 load4(const float *p) {
+    if constexpr (COHERENT) {
+        return make_float4(coherent_load(p), coherent_load(p + 1), coherent_load(p + 2),
+                           coherent_load(p + 3));
+    } else {
+        return *reinterpret_cast<const float4 *>(p);
+    }
+}
+
+template <bool COHERENT>
+__device__ __forceinline__ void store4(float *p, float4 v) {
+    if constexpr (COHERENT) {
+        coherent_store(p, v.x);
+        coherent_store(p + 1, v.y);
+        coherent_store(p + 2, v.z);
+        coherent_store(p + 3, v.w);
+    } else {
+        *reinterpret_cast<float4 *>(p) = v;
+    }
+}
+
+// dst = v from the wave layout (VPL >= 8, dst wave-uniform and 16-byte
+// aligned) through 16-byte stores written through to memory (buffer stores
+// with the sc1 bit): the coherent form of store_wave for hand-over data.
 template <int VPL>
+__device__ __forceinline__ void store_wave_through(float *dst, uint32_t lane, const float (&v)[VPL]) {
+    static_assert(VPL >= 8, "16-byte groups need the tiled layout");
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(dst, 0, static_cast<int>(64u * VPL * sizeof(float)), 0x00020000);
+#pragma unroll
+    for (int g = 0; g < VPL / 4; ++g) {
+        const u32x4_t q = {__float_as_uint(v[4 * g]), __float_as_uint(v[4 * g + 1]),
+                           __float_as_uint(v[4 * g + 2]), __float_as_uint(v[4 * g + 3])};
+        __builtin_amdgcn_raw_buffer_store_b128(q, rs, tiled_group_base<VPL>(g, lane) * 4u, 0, 16 /* sc1 */);
+    }
+}
+
+// v = src in the wave layout (src 16-byte aligned when tiled).
+template <int VPL, bool COHERENT = false>
 __device__ __forceinline__ void load_wave(const float *src, uint32_t lane, float (&v)[VPL]) {
     if constexpr (VPL >= 8) {
 #pragma unroll
         for (int g = 0; g < VPL / 4; ++g) {
-            const float4 q = *reinterpret_cast<const float4 *>(src + tiled_group_base<VPL>(g, lane));
+            const float4 q = load4<COHERENT>(src + tiled_group_base<VPL>(g, lane));
             v[4 * g] = q.x;
             v[4 * g + 1] = q.y;
             v[4 * g + 2] = q.z;
@@ -317,7 +389,7 @@ __device__ __forceinline__ void load_wave(const float *src, uint32_t lane, float
     } else {
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
-            v[i] = src[i * 64 + lane];
+            v[i] = COHERENT ? coherent_load(src + i * 64 + lane) : src[i * 64 + lane];
         }
     }
 }
@@ -363,18 +435,22 @@ __device__ __forceinline__ void load_wave_sign(const int8_t *src, uint32_t lane,
 }
 
 // dst = v from the wave layout.
-template <int VPL>
+template <int VPL, bool COHERENT = false>
 __device__ __forceinline__ void store_wave(float *dst, uint32_t lane, const float (&v)[VPL]) {
     if constexpr (VPL >= 8) {
 #pragma unroll
         for (int g = 0; g < VPL / 4; ++g) {
-            *reinterpret_cast<float4 *>(dst + tiled_group_base<VPL>(g, lane)) =
-                make_float4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
+            store4<COHERENT>(dst + tiled_group_base<VPL>(g, lane),
+                             make_float4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]));
         }
     } else {
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
-            dst[i * 64 + lane] = v[i];
+            if constexpr (COHERENT) {
+                coherent_store(dst + i * 64 + lane, v[i]);
+            } else {
+                dst[i * 64 + lane] = v[i];
+            }
         }
     }
 }
@@ -386,13 +462,13 @@ struct SliceLoads {
     float a[4][VPL];
 };
 
-template <int VPL>
+template <int VPL, bool COHERENT = false>
 __device__ __forceinline__ void load_slices(const float *src, size_t stride, uint32_t splits,
                                             uint32_t lane, SliceLoads<VPL> &l) {
     static_assert(VPL <= 8, "load_slices: vectors of at most 512 elements");
 #pragma unroll
     for (uint32_t s = 0; s < 4; ++s) {
-        load_wave<VPL>(src + (s < splits ? s : splits - 1u) * stride, lane, l.a[s]);
+        load_wave<VPL, COHERENT>(src + (s < splits ? s : splits - 1u) * stride, lane, l.a[s]);
     }
 }
 
@@ -417,14 +493,14 @@ __device__ __forceinline__ void add_slices(const SliceLoads<VPL> &l, uint32_t sp
 // v = sum over slices s < splits of src[s * stride ..] in the wave layout,
 // added in slice order; two slices are loaded per round so the loads overlap
 // (one for the widest vectors, whose registers would not hold two).
-template <int VPL>
+template <int VPL, bool COHERENT = false>
 __device__ __forceinline__ void sum_slices(const float *src, size_t stride, uint32_t splits,
                                            uint32_t lane, float (&v)[VPL]) {
 #pragma clang fp contract(off)
     if constexpr (VPL <= 8) {
         if (splits >= 1 && splits <= 4) {
             SliceLoads<VPL> l;
-            load_slices<VPL>(src, stride, splits, lane, l);
+            load_slices<VPL, COHERENT>(src, stride, splits, lane, l);
             add_slices<VPL>(l, splits, v);
             return;
         }
@@ -438,9 +514,9 @@ __device__ __forceinline__ void sum_slices(const float *src, size_t stride, uint
         // a missing second slice reloads the first and adds zero
         const bool second = kRound == 2 && s + 1 < splits;
         float a[VPL], b[VPL];
-        load_wave<VPL>(src + s * stride, lane, a);
+        load_wave<VPL, COHERENT>(src + s * stride, lane, a);
         if constexpr (kRound == 2) {
-            load_wave<VPL>(src + (second ? s + 1 : s) * stride, lane, b);
+            load_wave<VPL, COHERENT>(src + (second ? s + 1 : s) * stride, lane, b);
         }
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {

@@ -139,6 +139,27 @@ int adi_hip_context_create(int device, adi_hip_context **out) {
         delete ctx;
         return ADI_HIP_DEVICE_ERROR;
     }
+    // the one-launch MoE block's counters, zero before the first call
+    status = hipSetDevice(device);
+    if (status == hipSuccess) {
+        status = hipMalloc(reinterpret_cast<void **>(&ctx->moe_sync),
+                           adi_hip::kMoeSyncWords * sizeof(uint32_t));
+    }
+    if (status == hipSuccess) {
+        status = hipMemset(ctx->moe_sync, 0, adi_hip::kMoeSyncWords * sizeof(uint32_t));
+    }
+    if (status == hipSuccess) {
+        status = hipDeviceSynchronize();
+    }
+    (void)hipSetDevice(previous);
+    if (status != hipSuccess) {
+        record(std::string("adi_hip_context_create: MoE counters: ") + hipGetErrorString(status));
+        if (ctx->moe_sync != nullptr) {
+            (void)hipFree(ctx->moe_sync);
+        }
+        delete ctx;
+        return ADI_HIP_DEVICE_ERROR;
+    }
     *out = ctx;
     return ADI_HIP_OK;
 }
@@ -156,6 +177,9 @@ void adi_hip_context_destroy(adi_hip_context *ctx) {
             (void)hipEventDestroy(pair.first);
             (void)hipEventDestroy(pair.second);
         }
+    }
+    if (ctx->moe_sync != nullptr) {
+        (void)hipFree(ctx->moe_sync);
     }
     if (ctx->decoder_workspace.base != nullptr) {
         (void)hipFree(ctx->decoder_workspace.base);
@@ -183,7 +207,30 @@ int adi_hip_set_stream(adi_hip_context *ctx, void *stream) {
 }
 
 int adi_hip_synchronize(adi_hip_context *ctx) {
-    return guarded(ctx, [&] { check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize"); });
+    return guarded(ctx, [&] {
+        check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        if (ctx->moe_sync_pending) {
+            // a wait of the one-launch MoE block that ran out leaves its bit
+            // here (its outputs are then wrong): report it, reset the words
+            ctx->moe_sync_pending = false;
+            uint32_t error = 0;
+            check_hip(hipMemcpy(&error, ctx->moe_sync + adi_hip::kMoeSyncError, sizeof(error),
+                                hipMemcpyDeviceToHost),
+                      "MoE counters read");
+            if (error != 0) {
+                check_hip(hipMemset(ctx->moe_sync, 0, adi_hip::kMoeSyncWords * sizeof(uint32_t)),
+                          "MoE counters reset");
+                check_hip(hipDeviceSynchronize(), "MoE counters reset");
+                fail(ADI_HIP_DEVICE_ERROR,
+                     "one-launch MoE block: a cross-block wait ran out (error bits " +
+                         std::to_string(error) + "); its outputs are invalid");
+            }
+        }
+    });
+}
+
+int adi_hip_set_fused_decode(adi_hip_context *ctx, int enabled) {
+    return guarded(ctx, [&] { ctx->fused_moe = enabled != 0; });
 }
 
 int adi_hip_device_alloc(adi_hip_context *ctx, size_t bytes, void **out) {

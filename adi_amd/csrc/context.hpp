@@ -83,11 +83,25 @@ struct adi_hip_context {
     // device address of moe.hip's fixed scratch array on this context's
     // device (adi_hip_moe_forward_static), taken once at creation
     void *static_scratch = nullptr;
+    // counters and hand-over words of the one-launch batch-1 MoE block
+    // (kMoeSyncWords, zero between calls but for the error word), whether a
+    // launch since the last synchronize may have set that word, and whether
+    // the one-launch path is enabled
+    uint32_t *moe_sync = nullptr;
+    bool moe_sync_pending = false;
+    bool fused_moe = true;
     bool profiling = false;
     std::vector<adi_hip::KernelStat> stats;
 };
 
 namespace adi_hip {
+
+// adi_hip_context::moe_sync: 91 lines of kMoeSyncLine words (counters and
+// flags, the error word, the route record, the logits and the combine's nine
+// rows) and the index of its error word.
+constexpr uint32_t kMoeSyncLine = 1024;
+constexpr uint32_t kMoeSyncWords = 91 * kMoeSyncLine;
+constexpr uint32_t kMoeSyncError = 70 * kMoeSyncLine;
 
 // Selects the context's device for the duration of a call.
 class DeviceScope {

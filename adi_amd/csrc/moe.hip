@@ -525,6 +525,100 @@ void moe_forward_body(adi_hip_context *ctx, const adi_hip_moe_layer *L, const fl
             return reinterpret_cast<const uint16_t *>(buffer) + count;
         };
 
+        const size_t gu_words = size_t(I / kTile) * (H / kTile) * kExpertWords;
+        const size_t d_words = size_t(H / kTile) * (I / kTile) * kExpertWords;
+        const uint32_t gamma_stride = H / kTile + I / kTile;
+        // the decode-GEMV plans of the gate/up and down launches
+        auto expert_job = [&](const adi_hip_expert_stack &st, uint32_t rows, uint32_t columns,
+                              size_t words, const float *x_hat, float *z) {
+            ExpertGemv g{};
+            g.gamma_stride = gamma_stride;
+            g.rows = rows;
+            g.columns = columns;
+            g.trellis_stride = words;
+            g.z_split_stride = P * rows;
+            g.trellis = st.trellis;
+            g.gamma = st.wave_gamma_f16;
+            g.x_hat = x_hat;
+            g.z = z;
+            return g;
+        };
+        auto ne_job = [&](const adi_hip_ne_matrix &m, const float *x_hat, float *z) {
+            NeGemv n{};
+            n.batch = batch;
+            n.rows = m.rows;
+            n.columns = m.columns;
+            n.z_split_stride = B * m.rows;
+            n.trellis = m.trellis;
+            n.weight_scale = m.weight_scale;
+            n.x_hat = x_hat;
+            n.z = z;
+            return n;
+        };
+        auto gate_up_plan = [&]() {
+            MoeGemv gu{};
+            gu.expert[0] = expert_job(L->gate, I, H, gu_words, xh_gate, z_gate);
+            gu.expert[1] = expert_job(L->up, I, H, gu_words, xh_up, z_up);
+            gu.expert_count = 2;
+            gu.ne[0] = ne_job(L->shared_gate, sxh_gate, sz_gate);
+            gu.ne_count = 1;
+            gu.expert_book = L->expert_codebook->data;
+            gu.slot_info = slot_info;
+            gu.ne_book = L->shared_gate.codebook->data;
+            gu.max_active = max_active;
+            return gu;
+        };
+        auto down_plan = [&]() {
+            MoeGemv dn{};
+            dn.expert[0] = expert_job(L->down, H, I, d_words, xh_down, z_down);
+            dn.expert_count = 1;
+            dn.ne[0] = ne_job(L->shared_down, sxh_down, sz_down);
+            dn.ne_count = 1;
+            dn.expert_book = L->expert_codebook->data;
+            dn.slot_info = slot_info;
+            dn.ne_book = L->shared_down.codebook->data;
+            dn.max_active = max_active;
+            return dn;
+        };
+        auto swiglu_plan = [&]() {
+            return GemvSwiglu{z_gate, z_up, P * I, sg, L->gate.sv_f16, L->up.sv_f16,
+                              L->down.su_f16, sz_gate, sz_up, B * I, ssg,
+                              L->shared_gate.sv, L->shared_up.sv, L->shared_down.su,
+                              hadamard_scale(I)};
+        };
+
+        // one row: the whole block in one persistent launch when it fits
+        if (batch == 1 && !mfma && wave_path &&
+            L->shared_up.codebook->data == L->shared_gate.codebook->data) {
+            MoeDecodeOne f{};
+            f.gu = gate_up_plan();
+            f.gu.ne[1] = ne_job(L->shared_up, sxh_up, sz_up);
+            f.gu.ne_count = 2;
+            f.dn = down_plan();
+            f.dn.swiglu = swiglu_plan();
+            f.router = L->router.values;
+            f.shared_gate_row = L->shared_expert_gate.values;
+            f.logit_bias = logit_bias;
+            f.x = inputs;
+            f.su_gate = L->gate.su_f16;
+            f.su_up = L->up.su_f16;
+            f.shared_su_gate = L->shared_gate.su;
+            f.shared_su_up = L->shared_up.su;
+            f.sv_down = L->down.sv_f16;
+            f.shared_sv_down = L->shared_down.sv;
+            f.scale_hidden = hadamard_scale(H);
+            f.out = outputs;
+            f.route_expert_out = route_expert_out;
+            f.route_weight_out = route_weight_out;
+            f.sync = ctx->moe_sync;
+            f.experts = E;
+            if (ctx->fused_moe && plan_moe_decode_one(ctx, f)) {
+                launch_moe_decode_one(ctx, f);
+                ctx->moe_sync_pending = true;
+                return;
+            }
+        }
+
         // 1-2: router logits (+ the shared gate row) and routing
         launch_bf16_ordered_extra(ctx, L->router.values, E, L->shared_expert_gate.values, H, inputs,
                                   batch, logits, shared_logit, ctx->isa_lanes);
@@ -561,10 +655,6 @@ void moe_forward_body(adi_hip_context *ctx, const adi_hip_moe_layer *L, const fl
             launch_route(ctx, logits, logit_bias, batch, route_expert, route_weight, sort);
             launch_prologues(ctx, pro);
         }
-
-        const size_t gu_words = size_t(I / kTile) * (H / kTile) * kExpertWords;
-        const size_t d_words = size_t(H / kTile) * (I / kTile) * kExpertWords;
-        const uint32_t gamma_stride = H / kTile + I / kTile;
 
         // 4: gate / up projections
         if (mfma) {
@@ -622,42 +712,7 @@ void moe_forward_body(adi_hip_context *ctx, const adi_hip_moe_layer *L, const fl
                 launch_ne_mfma(ctx, su);
             }
         } else {
-            auto expert_job = [&](const adi_hip_expert_stack &st, uint32_t rows, uint32_t columns,
-                                  size_t words, const float *x_hat, float *z) {
-                ExpertGemv g{};
-                g.gamma_stride = gamma_stride;
-                g.rows = rows;
-                g.columns = columns;
-                g.trellis_stride = words;
-                g.z_split_stride = P * rows;
-                g.trellis = st.trellis;
-                g.gamma = st.wave_gamma_f16;
-                g.x_hat = x_hat;
-                g.z = z;
-                return g;
-            };
-            auto ne_job = [&](const adi_hip_ne_matrix &m, const float *x_hat, float *z) {
-                NeGemv n{};
-                n.batch = batch;
-                n.rows = m.rows;
-                n.columns = m.columns;
-                n.z_split_stride = B * m.rows;
-                n.trellis = m.trellis;
-                n.weight_scale = m.weight_scale;
-                n.x_hat = x_hat;
-                n.z = z;
-                return n;
-            };
-            MoeGemv gu{};
-            gu.expert[0] = expert_job(L->gate, I, H, gu_words, xh_gate, z_gate);
-            gu.expert[1] = expert_job(L->up, I, H, gu_words, xh_up, z_up);
-            gu.expert_count = 2;
-            gu.ne[0] = ne_job(L->shared_gate, sxh_gate, sz_gate);
-            gu.ne_count = 1;
-            gu.expert_book = L->expert_codebook->data;
-            gu.slot_info = slot_info;
-            gu.ne_book = L->shared_gate.codebook->data;
-            gu.max_active = max_active;
+            MoeGemv gu = gate_up_plan();
             if (L->shared_up.codebook->data == L->shared_gate.codebook->data) {
                 gu.ne[1] = ne_job(L->shared_up, sxh_up, sz_up);
                 gu.ne_count = 2;
@@ -676,37 +731,10 @@ void moe_forward_body(adi_hip_context *ctx, const adi_hip_moe_layer *L, const fl
         // x_hat from the gate/up slices itself, so step 5 launches nothing
         MoeGemv dn{};
         if (!mfma) {
-            ExpertGemv &g = dn.expert[0];
-            g.gamma_stride = gamma_stride;
-            g.rows = H;
-            g.columns = I;
-            g.trellis_stride = d_words;
-            g.z_split_stride = P * H;
-            g.trellis = L->down.trellis;
-            g.gamma = L->down.wave_gamma_f16;
-            g.x_hat = xh_down;
-            g.z = z_down;
-            dn.expert_count = 1;
-            NeGemv &n = dn.ne[0];
-            n.batch = batch;
-            n.rows = H;
-            n.columns = I;
-            n.z_split_stride = B * H;
-            n.trellis = L->shared_down.trellis;
-            n.weight_scale = L->shared_down.weight_scale;
-            n.x_hat = sxh_down;
-            n.z = sz_down;
-            dn.ne_count = 1;
-            dn.expert_book = L->expert_codebook->data;
-            dn.slot_info = slot_info;
-            dn.ne_book = L->shared_down.codebook->data;
-            dn.max_active = max_active;
+            dn = down_plan();
             if (batch == 1 && wave_path && trellis_gemv_can_fuse_swiglu(ctx, dn)) {
                 dn.fused_swiglu = 1;
-                dn.swiglu = GemvSwiglu{z_gate, z_up, P * I, sg, L->gate.sv_f16, L->up.sv_f16,
-                                       L->down.su_f16, sz_gate, sz_up, B * I, ssg,
-                                       L->shared_gate.sv, L->shared_up.sv, L->shared_down.su,
-                                       hadamard_scale(I)};
+                dn.swiglu = swiglu_plan();
             }
         }
 

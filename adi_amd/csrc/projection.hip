@@ -23,6 +23,7 @@
 // the consumer adds the slices in a fixed order.
 #include "projection.hpp"
 #include "grouped.hpp"
+#include "route.hpp"
 
 namespace adi_hip {
 namespace {
@@ -436,7 +437,7 @@ __device__ __forceinline__ void expert_tiles(const ExpertGemv &a, uint32_t item,
 
 __device__ __forceinline__ void expert_prefetch(const MoeGemv &m, const uint4 *slots, uint32_t i,
                                                 uint32_t half, uint32_t lane, ExpertStage &st,
-                                                const float *x_lds = nullptr) {
+                                                const float *x_lds = nullptr, bool with_x = true) {
     const ExpertItem it = expert_item_of(m, i);
     const ExpertGemv &a = m.expert[it.which];
     const uint4 info = slots[it.slot];
@@ -466,10 +467,30 @@ __device__ __forceinline__ void expert_prefetch(const MoeGemv &m, const uint4 *s
         }
     }
     // a fused SwiGLU's x_hat sits in LDS for the item's single position
-    load_x_pair(x_lds != nullptr ? x_lds : a.x_hat, a.columns, x_lds != nullptr ? 0u : st.info.y,
-                column, groups, valid, st.x);
+    if (with_x) {
+        load_x_pair(x_lds != nullptr ? x_lds : a.x_hat, a.columns, x_lds != nullptr ? 0u : st.info.y,
+                    column, groups, valid, st.x);
+    }
 }
 
+// The x_hat loads of expert_prefetch for a stage whose words were loaded
+// without them (with_x false): the item's single position from x_lds.
+__device__ __forceinline__ void expert_prefetch_x(const MoeGemv &m, uint32_t i, uint32_t half,
+                                                  uint32_t lane, ExpertStage &st, const float *x_lds) {
+    const ExpertItem it = expert_item_of(m, i);
+    const ExpertGemv &a = m.expert[it.which];
+    uint32_t column[4], tile[4];
+    bool valid[4];
+    expert_tiles(a, it.item, half, lane, column, valid, tile);
+    const bool live = st.info.z > st.info.y;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        valid[g] = valid[g] && live;
+    }
+    load_x_pair(x_lds, a.columns, 0u, column, 1u << a.group_shift, valid, st.x);
+}
+
+template <bool COHERENT = false>
 __device__ __forceinline__ void expert_compute(const MoeGemv &m, uint32_t i, uint32_t half,
                                                const uint2 *plane, uint32_t lane,
                                                ExpertStage &st) {
@@ -540,7 +561,7 @@ __device__ __forceinline__ void expert_compute(const MoeGemv &m, uint32_t i, uin
         if (writer) {
             float *dst = a.z + split * a.z_split_stride + static_cast<size_t>(position) * a.rows +
                          tr * kTile + quad * 4u;
-            *reinterpret_cast<float4 *>(dst) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            store4<COHERENT>(dst, make_float4(acc[0], acc[1], acc[2], acc[3]));
         }
     }
 }
@@ -565,6 +586,7 @@ __device__ __forceinline__ uint2 ne_item_of(const MoeGemv &m, uint32_t k) {
     return make_uint2(which, k - which * m.ne_items_per_matrix);
 }
 
+template <bool COHERENT = false>
 __device__ __forceinline__ void load_x16(const float *x_hat, uint32_t columns, uint32_t position,
                                          uint32_t column, bool valid, float (&x)[16]) {
 #pragma unroll
@@ -572,11 +594,10 @@ __device__ __forceinline__ void load_x16(const float *x_hat, uint32_t columns, u
         x[q] = 0.0f;
     }
     if (valid) {
-        const float4 *src =
-            reinterpret_cast<const float4 *>(x_hat + static_cast<size_t>(position) * columns + column);
+        const float *src = x_hat + static_cast<size_t>(position) * columns + column;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float4 v = src[q];
+            const float4 v = load4<COHERENT>(src + 4 * q);
             x[4 * q] = v.x;
             x[4 * q + 1] = v.y;
             x[4 * q + 2] = v.z;
@@ -585,6 +606,7 @@ __device__ __forceinline__ void load_x16(const float *x_hat, uint32_t columns, u
     }
 }
 
+template <bool COHERENT = false>
 __device__ __forceinline__ void ne_prefetch(const MoeGemv &m, uint32_t k, uint32_t lane,
                                             NeStage &st, const float *x_lds = nullptr) {
     const uint2 it = ne_item_of(m, k);
@@ -602,11 +624,16 @@ __device__ __forceinline__ void ne_prefetch(const MoeGemv &m, uint32_t k, uint32
     }
     st.d[0] = lo.x; st.d[1] = lo.y; st.d[2] = lo.z; st.d[3] = lo.w;
     st.d[4] = hi.x; st.d[5] = hi.y; st.d[6] = hi.z; st.d[7] = hi.w;
-    load_x16(x_lds != nullptr ? x_lds : a.x_hat, a.columns, 0, column, valid && a.batch > 0, st.x);
+    if (x_lds != nullptr) {
+        load_x16(x_lds, a.columns, 0, column, valid && a.batch > 0, st.x);
+    } else {
+        load_x16<COHERENT>(a.x_hat, a.columns, 0, column, valid && a.batch > 0, st.x);
+    }
 }
 
 // Row sums over all 16 columns of each tile with the signed table in LDS,
 // scaled by Wscale once after the tile sums.
+template <bool COHERENT = false>
 __device__ __forceinline__ void ne_compute(const MoeGemv &m, uint32_t k, const uint32_t *table,
                                            uint32_t lane, NeStage &st) {
     const uint2 it = ne_item_of(m, k);
@@ -647,9 +674,8 @@ __device__ __forceinline__ void ne_compute(const MoeGemv &m, uint32_t k, const u
         if (writer) {
             float *dst = a.z + split * a.z_split_stride + static_cast<size_t>(position) * a.rows +
                          tr * kTile + quad * 4u;
-            *reinterpret_cast<float4 *>(dst) =
-                make_float4(acc[0] * a.weight_scale, acc[1] * a.weight_scale,
-                            acc[2] * a.weight_scale, acc[3] * a.weight_scale);
+            store4<COHERENT>(dst, make_float4(acc[0] * a.weight_scale, acc[1] * a.weight_scale,
+                                              acc[2] * a.weight_scale, acc[3] * a.weight_scale));
         }
     }
 }
@@ -664,14 +690,10 @@ struct SwigluInputs {
     float g[4][kFusedSwigluWidth / 64], u[4][kFusedSwigluWidth / 64];
 };
 
-__device__ __forceinline__ void swiglu_issue(const GemvSwiglu &f, bool shared, uint32_t row,
-                                             uint32_t expert, uint32_t lane, SwigluInputs &in) {
+__device__ __forceinline__ void swiglu_issue_scales(const GemvSwiglu &f, bool shared, uint32_t expert,
+                                                    uint32_t lane, SwigluInputs &in) {
     constexpr int VPL = kFusedSwigluWidth / 64;
     constexpr uint32_t n = kFusedSwigluWidth;
-    const float *zg = shared ? f.shared_z_gate : f.z_gate + static_cast<size_t>(row) * n;
-    const float *zu = shared ? f.shared_z_up : f.z_up + static_cast<size_t>(row) * n;
-    const size_t stride = shared ? f.shared_split_stride : f.split_stride;
-    const uint32_t splits = shared ? f.shared_splits : f.splits;
     if (shared) {
         load_wave_sign<VPL>(f.shared_sv_gate, lane, in.sa);
         load_wave_sign<VPL>(f.shared_sv_up, lane, in.sb);
@@ -682,14 +704,33 @@ __device__ __forceinline__ void swiglu_issue(const GemvSwiglu &f, bool shared, u
         load_wave_f16<VPL>(f.sv_up + mat, lane, in.sb);
         load_wave_f16<VPL>(f.su_down + mat, lane, in.sc);
     }
+}
+
+template <bool COHERENT = false>
+__device__ __forceinline__ void swiglu_issue_slices(const GemvSwiglu &f, bool shared, uint32_t row,
+                                                    uint32_t lane, SwigluInputs &in) {
+    constexpr int VPL = kFusedSwigluWidth / 64;
+    constexpr uint32_t n = kFusedSwigluWidth;
+    const float *zg = shared ? f.shared_z_gate : f.z_gate + static_cast<size_t>(row) * n;
+    const float *zu = shared ? f.shared_z_up : f.z_up + static_cast<size_t>(row) * n;
+    const size_t stride = shared ? f.shared_split_stride : f.split_stride;
+    const uint32_t splits = shared ? f.shared_splits : f.splits;
 #pragma unroll
     for (uint32_t s = 0; s < 4; ++s) {
         const uint32_t at = s < splits ? s : splits - 1u;  // a missing slice reloads the last
-        load_wave<VPL>(zg + at * stride, lane, in.g[s]);
-        load_wave<VPL>(zu + at * stride, lane, in.u[s]);
+        load_wave<VPL, COHERENT>(zg + at * stride, lane, in.g[s]);
+        load_wave<VPL, COHERENT>(zu + at * stride, lane, in.u[s]);
     }
 }
 
+template <bool COHERENT = false>
+__device__ __forceinline__ void swiglu_issue(const GemvSwiglu &f, bool shared, uint32_t row,
+                                             uint32_t expert, uint32_t lane, SwigluInputs &in) {
+    swiglu_issue_scales(f, shared, expert, lane, in);
+    swiglu_issue_slices<COHERENT>(f, shared, row, lane, in);
+}
+
+template <bool COHERENT = false>
 __device__ __forceinline__ void swiglu_finish(const GemvSwiglu &f, bool shared, uint32_t row,
                                               uint32_t lane, SwigluInputs &in,
                                               float (&out)[kFusedSwigluWidth / 64]) {
@@ -715,10 +756,29 @@ __device__ __forceinline__ void swiglu_finish(const GemvSwiglu &f, bool shared, 
             uv[i] = s < splits ? uv[i] + in.u[s][i] : uv[i];
         }
     }
-    for (uint32_t s = 4; s < splits; ++s) {
+    if (splits > 4) {
+        // slices 4 .. 7 in one round of loads (a missing one reloads the
+        // last and is not added), the rest one at a time
+        float a[4][VPL], c[4][VPL];
+#pragma unroll
+        for (uint32_t t = 0; t < 4; ++t) {
+            const uint32_t at = 4 + t < splits ? 4 + t : splits - 1u;
+            load_wave<VPL, COHERENT>(zg + at * stride, lane, a[t]);
+            load_wave<VPL, COHERENT>(zu + at * stride, lane, c[t]);
+        }
+#pragma unroll
+        for (uint32_t t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int i = 0; i < VPL; ++i) {
+                gv[i] = 4 + t < splits ? gv[i] + a[t][i] : gv[i];
+                uv[i] = 4 + t < splits ? uv[i] + c[t][i] : uv[i];
+            }
+        }
+    }
+    for (uint32_t s = 8; s < splits; ++s) {
         float a[VPL], c[VPL];
-        load_wave<VPL>(zg + s * stride, lane, a);
-        load_wave<VPL>(zu + s * stride, lane, c);
+        load_wave<VPL, COHERENT>(zg + s * stride, lane, a);
+        load_wave<VPL, COHERENT>(zu + s * stride, lane, c);
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
             gv[i] = gv[i] + a[i];
@@ -895,6 +955,826 @@ __global__ __launch_bounds__(kGemvThreads) void k_trellis_gemv(MoeGemv m) {
         }
     }
 }
+
+// ---- the MoE block of one row in one launch ----------------------------------
+//
+// Phases (B = 1; items and slices as in the separate launches):
+//   P0  every block: codebook plane and NE table into LDS; wave 7 computes one
+//       or two router logits (rows b and b + blocks; row `experts` is the
+//       shared-expert gate) in the CPU's ISA order and takes a ticket; the
+//       last block to do so runs top_experts and publishes the routes. Wave 0
+//       of blocks 0 and 1 publishes the shared expert's gate and up x_hat.
+//   P1  wave 7 copies the routes into the block's slot table and builds the
+//       x_hat of the block's (entry, slot); each wave runs its routed gate/up
+//       item (its codes in flight meanwhile). The last wave of the block to
+//       finish adds the block's items to its slot's counter. Waves 4 and 5 then
+//       run the shared gate/up NE items.
+//   P2  wave 0 waits for the slot of the block's down items, builds its
+//       SwiGLU x_hat; each wave runs its down item; wave 1 builds the shared
+//       SwiGLU x_hat and runs a shared down NE item.
+//   P3  the last block to finish combines the eight routes and the shared
+//       expert in route order (the combine launch's arithmetic) and clears the
+//       counters for the next call.
+// The grid is one block per CU and every block is resident (LDS admits one
+// per CU); waits are bounded and a wait that runs out sets a bit of the error
+// word (the host reports it), so no call can hang.
+// Hand-over data (logits, routes, x_hat, Z slices) is written with coherent
+// (write-through) stores and waited for before the counter that publishes
+// it; consumers read it after the counter with ordinary loads, which are
+// their first touch of those lines in the launch (the launch starts with
+// clean caches, every line holds one producer's data), so no cache can hold
+// a stale copy. Counters and flags themselves are read with coherent loads.
+
+// The sync buffer is cut into lines of kMoeSyncLine words (4 KiB), one per
+// counter or flag, so that pollers and atomics of different words meet in
+// different memory channels. A flag that every block polls is written to
+// eight replica lines; block b polls replica b % 8 (its XCD's, as blocks are
+// dealt to the XCDs round robin). The route lines carry data: word s of each
+// replica is 1 + the expert of routed slot s, so a block's poll returns its
+// slot's expert. Grid-wide tickets count in two levels: eight group lines of
+// up to 32 blocks each, then a top line.
+namespace moe_sync {
+constexpr uint32_t kRouterGroup = 0, kRouterTop = 8, kRoutes = 9, kSharedXhatCount = 17,
+                   kSharedXhatReady = 18, kSharedCount = 26, kSharedReady = 27, kSlotCount = 35,
+                   kDownCount = 43, kSharedDownGroup = 51, kSharedDownTop = 59, kCombineTicket = 60,
+                   kRecordReady = 69, kCounterLines = 70,
+                   kError = kMoeSyncError / kMoeSyncLine, kRecord = 71, kLogits = 72, kParts = 73;
+// words of the route record line
+constexpr uint32_t kToGrouped = 0, kRouteWeight = 8, kSharedLogit = 16;
+// kParts: the combine's nine rows (routes 0-7, then the shared expert), two
+// lines each
+}  // namespace moe_sync
+
+__device__ __forceinline__ uint32_t *sync_line(uint32_t *sync, uint32_t line) {
+    return sync + static_cast<size_t>(line) * kMoeSyncLine;
+}
+
+constexpr uint32_t kFusedHidden = 2048;
+constexpr uint32_t kFusedThreads = kGemvThreads + kWave;  // eight GEMV waves and a helper
+constexpr uint32_t kFusedSlots = 8;
+constexpr uint32_t kSpinLimit = 1u << 20;  // about a second of polling
+constexpr size_t kFusedRegion = 16384;     // LDS after the plane: staging and x_hat rows
+
+// Polls (the whole wave) until *word is nonzero and returns it; bounded (0
+// after a timeout, which sets `bit` of the error word).
+__device__ __forceinline__ uint32_t wait_nonzero(uint32_t *word, uint32_t *error, uint32_t bit) {
+    uint32_t older = coherent_load(word);
+    for (uint32_t spins = 0;; ++spins) {
+        __builtin_amdgcn_s_sleep(1);
+        const uint32_t newer = coherent_load(word);
+        const uint32_t v = __builtin_amdgcn_readfirstlane(older);
+        if (v != 0u) {
+            return v;
+        }
+        if (spins >= kSpinLimit) {
+            if ((threadIdx.x & 63u) == 0) {
+                __hip_atomic_fetch_or(error, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return 0u;
+        }
+        older = newer;
+    }
+}
+
+// Polls the eight route words of a replica line (two 16-byte coherent
+// loads per poll, two polls in flight) until words s1 and s2 are both
+// nonzero; returns them (0 after a timeout, which sets error bit 1).
+__device__ __forceinline__ uint2 wait_route_words(uint32_t *line, uint32_t s1, uint32_t s2,
+                                                  uint32_t *error) {
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(line, 0, 32, 0x00020000);
+    auto poll = [&](u32x4_t &lo, u32x4_t &hi) {
+        lo = __builtin_amdgcn_raw_buffer_load_b128(rs, 0, 0, 16 /* sc1 */);
+        hi = __builtin_amdgcn_raw_buffer_load_b128(rs, 16, 0, 16);
+    };
+    auto word = [](const u32x4_t &lo, const u32x4_t &hi, uint32_t s) {
+        uint32_t v = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+            v = s == q ? lo[q] : v;
+            v = s == q + 4 ? hi[q] : v;
+        }
+        return __builtin_amdgcn_readfirstlane(v);
+    };
+    u32x4_t lo0, hi0, lo1, hi1;
+    poll(lo0, hi0);
+    for (uint32_t spins = 0;; ++spins) {
+        __builtin_amdgcn_s_sleep(1);
+        poll(lo1, hi1);
+        const uint32_t a = word(lo0, hi0, s1), b = word(lo0, hi0, s2);
+        if (a != 0u && b != 0u) {
+            return make_uint2(a, b);
+        }
+        if (spins >= kSpinLimit) {
+            if ((threadIdx.x & 63u) == 0) {
+                __hip_atomic_fetch_or(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return make_uint2(0u, 0u);
+        }
+        lo0 = lo1;
+        hi0 = hi1;
+    }
+}
+
+// Polls (the whole wave, uniformly) until *word >= target; bounded. Two
+// loads are in flight at a time, so a change is seen about half a load
+// latency after it lands rather than up to a whole one.
+__device__ __forceinline__ void wait_count(uint32_t *word, uint32_t target, uint32_t *error,
+                                           uint32_t bit) {
+    uint32_t older = coherent_load(word);
+    for (uint32_t spins = 0;; ++spins) {
+        __builtin_amdgcn_s_sleep(1);
+        const uint32_t newer = coherent_load(word);
+        if (__builtin_amdgcn_readfirstlane(older) >= target) {
+            return;
+        }
+        if (spins >= kSpinLimit) {
+            if ((threadIdx.x & 63u) == 0) {
+                __hip_atomic_fetch_or(error, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return;
+        }
+        older = newer;
+    }
+}
+
+// An LDS flag of the block: set (release) by one wave, awaited (acquire;
+// bounded like wait_count, error bit 16).
+__device__ __forceinline__ void set_flag(uint32_t *flag) {
+    __hip_atomic_store(flag, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void wait_flag(uint32_t *flag, uint32_t *error) {
+    for (uint32_t spins = 0; __builtin_amdgcn_readfirstlane(__hip_atomic_load(
+                                 flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) == 0u;
+         ++spins) {
+        if (spins >= 16u * kSpinLimit) {
+            if ((threadIdx.x & 63u) == 0) {
+                __hip_atomic_fetch_or(error, 16u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// count_block without a result: the device add is fire-and-forget.
+__device__ __forceinline__ void count_block_quiet(uint32_t *lds_count, uint32_t waves, uint32_t *word) {
+    wait_stores();
+    if ((threadIdx.x & 63u) == 0 && atomicAdd(lds_count, 1u) + 1u == waves) {
+        (void)__hip_atomic_fetch_add(word, waves, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Waits (bounded) until an LDS word reaches at least `at_least`, returns it.
+__device__ __forceinline__ uint32_t wait_lds_value(uint32_t *word, uint32_t at_least, uint32_t *error) {
+    for (uint32_t spins = 0;; ++spins) {
+        const uint32_t v = __builtin_amdgcn_readfirstlane(
+            __hip_atomic_load(word, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP));
+        if (v >= at_least) {
+            return v;
+        }
+        if (spins >= 16u * kSpinLimit) {
+            if ((threadIdx.x & 63u) == 0) {
+                __hip_atomic_fetch_or(error, 16u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return at_least;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// An LDS arrival counter of the block: count the wave in (release), then
+// wait (acquire, bounded) until `target` waves have arrived.
+__device__ __forceinline__ void arrive_and_wait(uint32_t *count, uint32_t target, uint32_t *error) {
+    if ((threadIdx.x & 63u) == 0) {
+        __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    for (uint32_t spins = 0; __builtin_amdgcn_readfirstlane(__hip_atomic_load(
+                                 count, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) < target;
+         ++spins) {
+        if (spins >= 16u * kSpinLimit) {
+            if ((threadIdx.x & 63u) == 0) {
+                __hip_atomic_fetch_or(error, 16u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Counts the wave into the block's LDS counter; the wave that completes
+// `waves` adds them to the device counter (its own stores and those of the
+// counted waves are complete: each waits for them before counting). True in
+// the wave whose add brings the device counter to `total`.
+__device__ __forceinline__ bool count_block(uint32_t *lds_count, uint32_t waves, uint32_t *word,
+                                           uint32_t total = 0xFFFFFFFFu) {
+    wait_stores();
+    uint32_t completes = 0;
+    if ((threadIdx.x & 63u) == 0) {
+        if (atomicAdd(lds_count, 1u) + 1u == waves) {
+            completes = coherent_add(word, waves) + waves == total ? 1u : 0u;
+        }
+    }
+    return __builtin_amdgcn_readfirstlane(completes) != 0u;
+}
+
+// One row of the combine (k_combine_wave): weight * (sv * H(sum of the Z
+// slices)), written through to `dst`. sv is f16 (a routed expert's, in LDS)
+// or +-1 (the shared expert's).
+template <int VPL>
+__device__ __forceinline__ void combine_row(const float *z, size_t stride, uint32_t splits,
+                                            const uint16_t *sv_f16, const int8_t *sv_sign,
+                                            float weight, float scale_h, uint32_t lane, float *dst) {
+#pragma clang fp contract(off)
+    float val[VPL], sv[VPL];
+    sum_slices<VPL>(z, stride, splits, lane, val);
+    if (sv_f16 != nullptr) {
+        load_wave_f16<VPL>(sv_f16, lane, sv);
+    } else {
+        load_wave_sign<VPL>(sv_sign, lane, sv);
+    }
+    wave_hadamard<VPL>(val, scale_h, lane);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        val[i] = weight * (val[i] * sv[i]);
+    }
+    store_wave_through<VPL>(dst, lane, val);
+}
+
+// Two-level ticket over the grid, taken by one thread per block once the
+// block's stores are complete: true in the one block that completes it.
+__device__ __forceinline__ bool grid_ticket(uint32_t *sync, uint32_t group_line, uint32_t top_line,
+                                            uint32_t b, uint32_t blocks) {
+    const uint32_t group = b & 7u;
+    const uint32_t members = (blocks - group + 7u) >> 3;
+    if (coherent_add(sync_line(sync, group_line + group), 1u) + 1u != members) {
+        return false;
+    }
+    const uint32_t groups = blocks < 8u ? blocks : 8u;
+    return coherent_add(sync_line(sync, top_line), 1u) + 1u == groups;
+}
+
+// Sets the eight replicas of a flag every block polls.
+__device__ __forceinline__ void publish_flag(uint32_t *sync, uint32_t line) {
+#pragma unroll
+    for (uint32_t x = 0; x < 8; ++x) {
+        coherent_store(sync_line(sync, line + x), 1u);
+    }
+}
+
+// One router logit per LANES-lane group in the CPU's order (dense.hip): lane
+// j of the group adds columns j, j + LANES, ... of its row (fused multiply-add
+// for the 16-lane order, multiply then add for the 8-lane order), then the
+// group's lane sums are added in lane order from 0. w (bf16) and x in LDS.
+template <int LANES>
+__device__ __forceinline__ float router_chain(const uint16_t *w, const float *x, uint32_t columns,
+                                              uint32_t j) {
+#pragma clang fp contract(off)
+    constexpr uint32_t kBatch = 16;  // LDS reads of 16 steps issued before their adds
+    float acc = 0.0f;
+    for (uint32_t base = 0; base < columns; base += kBatch * LANES) {
+        float wk[kBatch], xk[kBatch];
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch; ++u) {
+            const uint32_t k = base + u * LANES + j;
+            wk[u] = bf16_bits_to_float(w[k]);
+            xk[u] = x[k];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch; ++u) {
+            if constexpr (LANES == 16) {
+                acc = fmaf(wk[u], xk[u], acc);
+            } else {
+                acc = acc + wk[u] * xk[u];
+            }
+        }
+    }
+    return acc;
+}
+
+// The lane sums of lanes group * LANES .. + LANES - 1, added in lane order
+// from 0 (every lane gets the sum).
+template <int LANES>
+__device__ __forceinline__ float router_lane_sum(float acc, uint32_t group) {
+#pragma clang fp contract(off)
+    float sum = 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < LANES; ++j) {
+        sum = sum + __uint_as_float(static_cast<uint32_t>(
+                        __builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(acc)),
+                                                  static_cast<int>(group * LANES + j))));
+    }
+    return sum;
+}
+
+// The thread's share of a codebook plane into LDS: all loads, then the stores.
+__device__ __forceinline__ void fill_plane_share(const uint4 *src, uint4 *dst) {
+    constexpr uint32_t kPer = static_cast<uint32_t>(kPlaneBytes / 16) / kGemvThreads;
+    uint4 v[kPer];
+#pragma unroll
+    for (uint32_t u = 0; u < kPer; ++u) {
+        v[u] = src[u * kGemvThreads + threadIdx.x];
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kPer; ++u) {
+        dst[u * kGemvThreads + threadIdx.x] = v[u];
+    }
+}
+
+// A combine row is in (the calling wave's stores and those it waited for
+// are complete): true for the ninth of the eight route rows and the shared
+// row to arrive, whose block then adds them. Every other wait of the launch
+// has ended by then: each row needs all its slot's down items (whose waves
+// have polled everything) and the shared row every helper's down item.
+__device__ __forceinline__ bool combine_ticket(uint32_t *sync, uint32_t lane) {
+    wait_stores();
+    uint32_t ticket = 0;
+    if (lane == 0) {
+        ticket = coherent_add(sync_line(sync, moe_sync::kCombineTicket), 1u);
+    }
+    return __builtin_amdgcn_readfirstlane(ticket) == 8u;
+}
+
+// The last combine ticket's block (`threads` threads from `first`): clears
+// the counters and route words for the next call, then adds the nine rows
+// in route order, then the shared expert (the combine launch's order).
+__device__ __forceinline__ void finish_combine(const MoeDecodeOne &a, uint32_t *sync, uint32_t t0,
+                                               uint32_t threads) {
+    for (uint32_t t = t0; t < moe_sync::kCounterLines; t += threads) {
+        coherent_store(sync_line(sync, t), 0u);
+    }
+    for (uint32_t t = t0; t < 64u; t += threads) {
+        coherent_store(sync_line(sync, moe_sync::kRoutes + (t >> 3)) + (t & 7u), 0u);
+    }
+    constexpr uint32_t H = kFusedHidden;
+    float4 *row_out = reinterpret_cast<float4 *>(a.out);
+    for (uint32_t c = t0; c < H / 4u; c += threads) {
+        float4 v[9];
+#pragma unroll
+        for (uint32_t r = 0; r < 9; ++r) {
+            v[r] = reinterpret_cast<const float4 *>(sync_line(sync, moe_sync::kParts + 2u * r))[c];
+        }
+        float4 acc = v[0];
+#pragma unroll
+        for (uint32_t r = 1; r < 9; ++r) {
+            acc.x = acc.x + v[r].x;
+            acc.y = acc.y + v[r].y;
+            acc.z = acc.z + v[r].z;
+            acc.w = acc.w + v[r].w;
+        }
+        row_out[c] = acc;
+    }
+}
+
+template <int LANES>
+__global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a) {
+#pragma clang fp contract(off)
+    extern __shared__ uint4 lds_dynamic[];  // the codebook plane, then kFusedRegion bytes
+    __shared__ uint32_t ne_table[1024];
+    __shared__ uint4 slots[kFusedSlots];
+    // top-8 block: expert and weight bits of each route; then, in every
+    // block, the route record: grouped position and weight bits of each
+    // route, the shared gate logit
+    __shared__ uint32_t routes[24];
+    __shared__ uint32_t record_lds[17];
+    // 0: waves that filled their plane share and table part; 1: slot table;
+    // 2, 8: waves through the two halves of the routed x_hat (2 again for the
+    // combine row); 3: gate/up items counted; 4: down x_hat; 5: shared
+    // gate/up items counted; 6: down items counted; 7: route record in LDS;
+    // 9: the block's slot-completion state; 10: combine row stores counted
+    __shared__ uint32_t flags[12];
+    constexpr uint32_t H = kFusedHidden;
+    constexpr int VPL = kFusedHidden / 64;
+    constexpr int VPLI = kFusedSwigluWidth / 64;
+    uint4 *plane_lds = lds_dynamic;
+    float *region = reinterpret_cast<float *>(lds_dynamic + kPlaneBytes / 16);
+    float *x_routed = region;       // P1: x_hat of the block's (entry, slot)
+    float *x_staged = region + H;   // P0-P1: x as the router staged it
+    float *x_down = region + H;     // P2: the slot's SwiGLU x_hat (x no longer needed)
+    float *x_shared_down = region + H + kFusedSwigluWidth;  // P1: the shared SwiGLU x_hat
+    uint16_t *sv_slot = reinterpret_cast<uint16_t *>(region + H + 2 * kFusedSwigluWidth);  // P2: f16 sv
+    const uint32_t b = blockIdx.x, blocks = gridDim.x;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63u;
+    const bool helper = wave == kGemvWaves;
+    const uint32_t half = (b >> 3) & 1u;
+    const uint32_t worker = ((b >> 4) << 3) | (b & 7u);
+    uint32_t *sync = a.sync;
+    uint32_t *error = sync_line(sync, moe_sync::kError);
+    uint32_t *record = sync_line(sync, moe_sync::kRecord);
+    float *record_f = reinterpret_cast<float *>(record);
+    float *logits_g = reinterpret_cast<float *>(sync_line(sync, moe_sync::kLogits));
+    auto part = [&](uint32_t r) { return reinterpret_cast<float *>(sync_line(sync, moe_sync::kParts + 2u * r)); };
+    const uint32_t replica = b & 7u;
+    // the block's routed slots: gate/up items (P1) and down items (P2)
+    const uint32_t slot1 = expert_item_of(a.gu, worker * kGemvWaves).slot;
+    const uint32_t slot2 = expert_item_of(a.dn, worker * kGemvWaves).slot;
+    if (threadIdx.x < 12) {
+        flags[threadIdx.x] = 0u;
+    }
+    __syncthreads();
+    // waits (bounded) until the eight GEMV waves have counted into an LDS
+    // counter: flags[0] says the plane and the NE table are complete,
+    // flags[2] that the staged x has been read for the routed x_hat
+    auto wait_waves = [&](uint32_t *count) {
+        for (uint32_t spins = 0; __builtin_amdgcn_readfirstlane(__hip_atomic_load(
+                                     count, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) < kGemvWaves;
+             ++spins) {
+            if (spins >= 16u * kSpinLimit) {
+                if (lane == 0) {
+                    __hip_atomic_fetch_or(error, 16u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                return;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    };
+    auto wait_plane = [&]() { wait_waves(&flags[0]); };
+
+    // ---- P0 ----
+    if (!helper) {
+        fill_plane_share(static_cast<const uint4 *>(a.gu.expert_book) + half * (kPlaneBytes / 16),
+                         plane_lds);
+        const uint32_t *src = static_cast<const uint32_t *>(a.gu.ne_book);
+        for (uint32_t i = threadIdx.x; i < 1024u; i += kGemvThreads) {
+            ne_table[i] = src[i];
+        }
+        if (lane == 0) {
+            __hip_atomic_fetch_add(&flags[0], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    } else {
+        // router rows b and 2 blocks - 1 - b (the second rows, the shared
+        // gate's among them, on the last blocks), staged with x in the region
+        const uint32_t rows_total = a.experts + 1u;
+        uint16_t *wl = reinterpret_cast<uint16_t *>(region);
+        // the two shared-prologue blocks carry no row: theirs go to the two
+        // blocks after them as second rows (those have none of their own)
+        const uint32_t p0 = blocks / 2u;
+        const uint32_t r0 = b - p0 < 2u ? rows_total : b;
+        const uint32_t r1 = b - (p0 + 2u) < 2u ? b - 2u : 2u * blocks - 1u - b;
+        auto row = [&](uint32_t r) {
+            return reinterpret_cast<const uint4 *>(r < a.experts ? a.router + static_cast<size_t>(r) * H
+                                                                 : a.shared_gate_row);
+        };
+        uint4 w0[4], w1[4];
+        float4 xv[8];
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            w0[u] = r0 < rows_total ? row(r0)[u * 64u + lane] : make_uint4(0u, 0u, 0u, 0u);
+            w1[u] = r1 < rows_total ? row(r1)[u * 64u + lane] : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) {
+            xv[u] = reinterpret_cast<const float4 *>(a.x)[u * 64u + lane];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            reinterpret_cast<uint4 *>(wl)[u * 64u + lane] = w0[u];
+            reinterpret_cast<uint4 *>(wl + H)[u * 64u + lane] = w1[u];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) {
+            reinterpret_cast<float4 *>(x_staged)[u * 64u + lane] = xv[u];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        const uint32_t group = lane / LANES;  // 0: row r0, 1: row r1, others unused
+        const float acc = router_chain<LANES>(wl + (group == 1u ? H : 0u), x_staged, H, lane % LANES);
+        const float s0 = router_lane_sum<LANES>(acc, 0u);
+        const float s1 = router_lane_sum<LANES>(acc, 1u);
+        if (lane == 0) {
+            if (r0 < rows_total) {
+                coherent_store(r0 < a.experts ? logits_g + r0 : record_f + moe_sync::kSharedLogit, s0);
+            }
+            if (r1 < rows_total) {
+                coherent_store(r1 < a.experts ? logits_g + r1 : record_f + moe_sync::kSharedLogit, s1);
+            }
+        }
+        wait_stores();
+        uint32_t last = 0;
+        if (lane == 0) {
+            last = grid_ticket(sync, moe_sync::kRouterGroup, moe_sync::kRouterTop, b, blocks) ? 1u : 0u;
+        }
+        if (__builtin_amdgcn_readfirstlane(last) != 0u) {
+            // the last router block: top_experts over the published logits
+            float *logits = region;  // the staged rows are no longer needed
+            for (uint32_t e = lane; e < a.experts; e += 64u) {
+                logits[e] = logits_g[e];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            uint32_t chosen[8];
+            top8_wave<4>(logits, a.logit_bias, a.experts, lane, routes,
+                         reinterpret_cast<float *>(routes + 8), nullptr, chosen);
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            // lane l < 64: word l % 8 of replica l / 8 is 1 + the expert of
+            // slot l % 8 (slots in ascending expert order: the counting sort's
+            // grouped order for one row)
+            const uint32_t sl = lane & 7u;
+            uint32_t sorted = 0;
+#pragma unroll
+            for (uint32_t q = 0; q < 8; ++q) {
+                uint32_t rank = 0;
+#pragma unroll
+                for (uint32_t t = 0; t < 8; ++t) {
+                    rank += chosen[t] < chosen[q] ? 1u : 0u;
+                }
+                sorted = rank == sl ? chosen[q] : sorted;
+            }
+            coherent_store(sync_line(sync, moe_sync::kRoutes + (lane >> 3)) + sl, sorted + 1u);
+            if (lane < 8) {
+                uint32_t e = chosen[0];
+#pragma unroll
+                for (uint32_t q = 1; q < 8; ++q) {
+                    e = lane == q ? chosen[q] : e;
+                }
+                uint32_t rank = 0;
+#pragma unroll
+                for (uint32_t q = 0; q < 8; ++q) {
+                    rank += chosen[q] < e ? 1u : 0u;
+                }
+                const float w = reinterpret_cast<const float *>(routes)[8 + lane];
+                coherent_store(record + moe_sync::kToGrouped + lane, rank);
+                coherent_store(record_f + moe_sync::kRouteWeight + lane, w);
+                if (a.route_expert_out != nullptr) {
+                    a.route_expert_out[lane] = e;
+                }
+                if (a.route_weight_out != nullptr) {
+                    a.route_weight_out[lane] = w;
+                }
+            }
+            wait_stores();
+            if (lane == 0) {
+                coherent_store(sync_line(sync, moe_sync::kRecordReady), 1u);
+            }
+        }
+    }
+    const uint32_t prologue_block = blocks / 2u;  // carries no router row
+    if (wave == 6 && b - prologue_block < 2u) {
+        // the shared expert's gate (first block) or up (second) x_hat, for
+        // every block, by a wave of two mid-grid blocks
+        const uint32_t which = b - prologue_block;
+        float v[VPL], su[VPL];
+        load_wave<VPL>(a.x, lane, v);
+        load_wave_sign<VPL>(which == 0 ? a.shared_su_gate : a.shared_su_up, lane, su);
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            v[i] = v[i] * su[i];
+        }
+        wave_hadamard<VPL>(v, a.scale_hidden, lane);
+        store_wave_through<VPL>(const_cast<float *>(a.gu.ne[which].x_hat), lane, v);
+        wait_stores();
+        if (lane == 0 && coherent_add(sync_line(sync, moe_sync::kSharedXhatCount), 1u) == 1u) {
+            publish_flag(sync, moe_sync::kSharedXhatReady);  // the second of the two
+        }
+    }
+    // the shared expert while the router finishes: gate/up NE items on waves
+    // 6 and 7 (item (w - 6) * blocks + b; off the helper's SIMD); the wave
+    // that completes them publishes the shared flag
+    if (wave == 6u || wave == 7u) {
+        const uint32_t k = (wave - 6u) * blocks + b;
+        if (k < a.gu.ne_items) {
+            wait_plane();
+            wait_count(sync_line(sync, moe_sync::kSharedXhatReady + replica), 1u, error, 2u);
+            NeStage st;
+            ne_prefetch(a.gu, k, lane, st);
+            ne_compute<true>(a.gu, k, ne_table, lane, st);
+            wait_stores();
+            uint32_t finisher = 0;
+            if (lane == 0) {
+                const uint32_t mine = (b < a.gu.ne_items ? 1u : 0u) + (blocks + b < a.gu.ne_items ? 1u : 0u);
+                finisher = atomicAdd(&flags[5], 1u) + 1u == mine &&
+                                   coherent_add(sync_line(sync, moe_sync::kSharedCount), mine) + mine ==
+                                       a.gu.ne_items
+                               ? 1u
+                               : 0u;
+            }
+            if (__builtin_amdgcn_readfirstlane(finisher) != 0u && lane == 0) {
+                publish_flag(sync, moe_sync::kSharedReady);
+            }
+        }
+    }
+
+    // ---- P1 ----
+    const uint32_t item = worker * kGemvWaves + wave;  // gate/up and down items alike (GEMV waves)
+    const uint2 *plane = reinterpret_cast<const uint2 *>(plane_lds);
+    if (helper) {
+        uint32_t *route_line = sync_line(sync, moe_sync::kRoutes + replica);
+        // (a wait that runs out gives 0: expert 0 keeps every access in
+        // bounds, and the error word already marks the outputs invalid)
+        const uint2 vv = wait_route_words(route_line, slot1, slot2, error);
+        const uint32_t v1 = vv.x, v2 = vv.y;
+        const uint32_t e1 = v1 != 0u ? v1 - 1u : 0u;
+        const uint32_t e2 = v2 != 0u ? v2 - 1u : 0u;
+        if (lane == 0) {
+            slots[slot1] = make_uint4(e1, slot1, slot1 + 1u, 0u);
+            slots[slot2] = make_uint4(e2, slot2, slot2 + 1u, 0u);
+        }
+        set_flag(&flags[1]);
+        // the route record for the combine rows this block may build
+        wait_count(sync_line(sync, moe_sync::kRecordReady), 1u, error, 1u);
+        if (lane < 17) {
+            record_lds[lane] = coherent_load(record + lane);
+        }
+        set_flag(&flags[7]);
+        // the shared expert's SwiGLU x_hat (every block's helper builds it
+        // from the published gate/up slices), then its down NE item b; the
+        // block that completes those builds the shared combine row
+        wait_plane();
+        wait_count(sync_line(sync, moe_sync::kSharedReady + replica), 1u, error, 8u);
+        SwigluInputs in;
+        float xd[VPLI];
+        swiglu_issue(a.dn.swiglu, true, 0u, 0u, lane, in);
+        swiglu_finish(a.dn.swiglu, true, 0u, lane, in, xd);
+        wait_waves(&flags[2]);  // x_shared_down overlays the staged x
+        store_wave<VPLI>(x_shared_down, lane, xd);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        NeStage st;
+        ne_prefetch(a.dn, b, lane, st, x_shared_down);
+        ne_compute<true>(a.dn, b, ne_table, lane, st);
+        wait_stores();
+        uint32_t finisher = 0;
+        if (lane == 0) {
+            finisher = grid_ticket(sync, moe_sync::kSharedDownGroup, moe_sync::kSharedDownTop, b, blocks) ? 1u : 0u;
+        }
+        if (__builtin_amdgcn_readfirstlane(finisher) != 0u) {
+            const float g = __uint_as_float(record_lds[moe_sync::kSharedLogit]);
+            combine_row<VPL>(a.dn.ne[0].z, a.dn.ne[0].z_split_stride, a.shared_down_splits, nullptr,
+                             a.shared_sv_down, 1.0f / (1.0f + expf(-g)), a.scale_hidden, lane, part(8));
+            if (combine_ticket(sync, lane)) {
+                finish_combine(a, sync, lane, 64u);
+            }
+        }
+    } else {
+        ExpertStage st;
+        wait_flag(&flags[1], error);
+        // x_hat = H(su[expert] * x) of the block's (entry, slot), by the eight
+        // waves: wave w transforms elements 256 w .. 256 w + 255 (index bits
+        // 0-7, element 64 i + lane of its chunk in register i), then each
+        // wave takes 32 of the 256 columns across the chunks for bits 8-10,
+        // so every butterfly is the one-wave transform's, in the same order.
+        // Its su loads go out before the item's codes, which return later.
+        const ExpertItem it = expert_item_of(a.gu, worker * kGemvWaves);
+        const uint16_t *su = (it.which == 0 ? a.su_gate : a.su_up) +
+                             static_cast<size_t>(slots[slot1].x) * H + 256u * wave;
+        float v[4], sv4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sv4[i] = half_bits_to_float(su[64 * i + lane]);
+        }
+        expert_prefetch(a.gu, slots, item, half, lane, st, nullptr, false);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = x_staged[256u * wave + 64u * i + lane] * sv4[i];
+        }
+        wave_hadamard<4>(v, 1.0f, lane);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x_routed[256u * wave + 64u * i + lane] = v[i];
+        }
+        arrive_and_wait(&flags[2], kGemvWaves, error);
+        if (lane < 32) {
+            const uint32_t j = 32u * wave + lane;
+            float u[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                u[k] = x_routed[256u * k + j];
+            }
+#pragma unroll
+            for (int stride = 1; stride < 8; stride <<= 1) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    if ((k & stride) == 0) {
+                        const float p = u[k], q = u[k + stride];
+                        u[k] = p + q;
+                        u[k + stride] = p - q;
+                    }
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                x_routed[256u * k + j] = u[k] * a.scale_hidden;
+            }
+        }
+        wait_plane();
+        arrive_and_wait(&flags[8], kGemvWaves, error);
+        expert_prefetch_x(a.gu, item, half, lane, st, x_routed);
+        expert_compute<true>(a.gu, item, half, plane, lane, st);
+        count_block_quiet(&flags[3], kGemvWaves, sync_line(sync, moe_sync::kSlotCount + slot1));
+    }
+
+    // ---- P2 ----
+    if (!helper) {
+        ExpertStage st;
+        expert_prefetch(a.dn, slots, item, half, lane, st, nullptr, false);
+        const uint4 info = slots[slot2];
+        if (wave == 1) {  // off the helper's SIMD
+            SwigluInputs in;
+            swiglu_issue_scales(a.dn.swiglu, false, info.x, lane, in);
+            wait_count(sync_line(sync, moe_sync::kSlotCount + slot2), a.expect_slot, error, 4u);
+            float xd[VPLI];
+            swiglu_issue_slices(a.dn.swiglu, false, info.y, lane, in);
+            swiglu_finish(a.dn.swiglu, false, info.y, lane, in, xd);
+            store_wave<VPLI>(x_down, lane, xd);
+            set_flag(&flags[4]);
+        } else {
+            if (wave == 2) {
+                // the slot's sv row (f16) for the combine row, should this
+                // block complete the slot's down items
+                const uint4 *src = reinterpret_cast<const uint4 *>(a.sv_down + static_cast<size_t>(info.x) * H);
+                uint4 q[4];
+#pragma unroll
+                for (uint32_t u = 0; u < 4; ++u) {
+                    q[u] = src[u * 64u + lane];
+                }
+#pragma unroll
+                for (uint32_t u = 0; u < 4; ++u) {
+                    reinterpret_cast<uint4 *>(sv_slot)[u * 64u + lane] = q[u];
+                }
+            }
+            wait_flag(&flags[4], error);
+        }
+        expert_prefetch_x(a.dn, item, half, lane, st, x_down);
+        expert_compute<true>(a.dn, item, half, plane, lane, st);
+        // the block's count; flags[9]: 1 = another block completes the slot,
+        // 2 = this block does, 3 = its row is in, 4 = and it was the last
+        wait_stores();
+        if (lane == 0 && atomicAdd(&flags[6], 1u) + 1u == kGemvWaves) {
+            const bool completes =
+                coherent_add(sync_line(sync, moe_sync::kDownCount + slot2), kGemvWaves) + kGemvWaves ==
+                a.expect_down;
+            __hip_atomic_store(&flags[9], completes ? 2u : 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        if (wait_lds_value(&flags[9], 1u, error) == 1u) {
+            return;
+        }
+        // the slot's last down items are in: its route's combine row, by the
+        // eight waves (chunks of 256, then the top three butterfly stages
+        // across chunks, as for the routed x_hat)
+        wait_flag(&flags[7], error);
+        uint32_t r = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) {
+            r = record_lds[moe_sync::kToGrouped + q] == slot2 ? q : r;
+        }
+        const float weight = __uint_as_float(record_lds[moe_sync::kRouteWeight + r]);
+        const float *z = a.dn.expert[0].z + static_cast<size_t>(slot2) * H + 256u * wave;
+        const size_t zs = a.dn.expert[0].z_split_stride;
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = 0.0f;
+        }
+        for (uint32_t sl = 0; sl < a.down_splits; ++sl) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = v[i] + z[sl * zs + 64u * i + lane];
+            }
+        }
+        wave_hadamard<4>(v, 1.0f, lane);
+        float *row = x_routed;  // free in P2
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            row[256u * wave + 64u * i + lane] = v[i];
+        }
+        arrive_and_wait(&flags[2], 2u * kGemvWaves, error);
+        float *out_row = part(r);
+        if (lane < 32) {
+            const uint32_t j = 32u * wave + lane;
+            float u[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                u[k] = row[256u * k + j];
+            }
+#pragma unroll
+            for (int stride = 1; stride < 8; stride <<= 1) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    if ((k & stride) == 0) {
+                        const float p = u[k], q = u[k + stride];
+                        u[k] = p + q;
+                        u[k + stride] = p - q;
+                    }
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float h = u[k] * a.scale_hidden;
+                coherent_store(out_row + 256u * k + j,
+                               weight * (h * half_bits_to_float(sv_slot[256u * k + j])));
+            }
+        }
+        // the row is complete once every wave's stores are: the last to
+        // arrive takes the combine ticket
+        wait_stores();
+        if (lane == 0 && atomicAdd(&flags[10], 1u) + 1u == kGemvWaves) {
+            uint32_t t = coherent_add(sync_line(sync, moe_sync::kCombineTicket), 1u);
+            __hip_atomic_store(&flags[9], t == 8u ? 4u : 3u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        if (wait_lds_value(&flags[9], 3u, error) == 4u) {
+            finish_combine(a, sync, threadIdx.x, kGemvThreads);
+        }
+    }
+}
+
 
 }  // namespace
 
@@ -1086,6 +1966,57 @@ void launch_trellis_gemv(adi_hip_context *ctx, MoeGemv &m) {
         set_lds_limit(reinterpret_cast<const void *>(&k_trellis_gemv), kMaxDynamic);
     (void)ready;
     launch(ctx, "moe_gemv", k_trellis_gemv, dim3(blocks), dim3(kGemvThreads), lds, m);
+}
+
+bool plan_moe_decode_one(adi_hip_context *ctx, MoeDecodeOne &a) {
+    if (ctx->cu_count < 16 || (ctx->isa_lanes != 8 && ctx->isa_lanes != 16) || a.sync == nullptr ||
+        a.experts < 8 || a.experts > 256 || a.gu.expert_count != 2 || a.gu.ne_count != 2 ||
+        a.dn.expert_count != 1 || a.dn.ne_count != 1 || a.gu.max_active != kFusedSlots ||
+        a.dn.max_active != kFusedSlots || a.gu.ne_book != a.dn.ne_book) {
+        return false;
+    }
+    const ExpertGemv &g = a.gu.expert[0], &d = a.dn.expert[0];
+    if (g.rows != kFusedSwigluWidth || g.columns != kFusedHidden || d.rows != kFusedHidden ||
+        d.columns != kFusedSwigluWidth || a.gu.ne[0].rows != kFusedSwigluWidth ||
+        a.gu.ne[0].columns != kFusedHidden || a.dn.ne[0].rows != kFusedHidden ||
+        a.dn.ne[0].columns != kFusedSwigluWidth) {
+        return false;
+    }
+    const uint32_t blocks = ctx->cu_count / 16 * 16;
+    if (plan_trellis_gemv(ctx, a.gu) != blocks || plan_trellis_gemv(ctx, a.dn) != blocks) {
+        return false;
+    }
+    // one item per wave, a block's eight items in one slot, every router row
+    // on some block, every NE item on a wave
+    const uint32_t wave_items = (blocks / 2) * kGemvWaves;
+    if (a.gu.expert_items != wave_items || a.dn.expert_items != wave_items ||
+        a.gu.expert_items_per_slot % kGemvWaves != 0 || a.dn.expert_items_per_slot % kGemvWaves != 0 ||
+        a.experts + 1 > 2 * blocks || a.gu.ne_items > 2 * blocks || a.dn.ne_items != blocks ||
+        2 * blocks - 1 - (blocks / 2 + 3) < a.experts + 1) {
+        return false;
+    }
+    // each half of the grid runs every item once
+    a.expect_slot = 2u * a.gu.expert_count * a.gu.expert_items_per_slot;
+    a.expect_down = 2u * a.dn.expert_items_per_slot;
+    a.down_splits = expert_splits(kFusedSwigluWidth);
+    a.shared_down_splits = ne_splits(kFusedSwigluWidth);
+    return true;
+}
+
+void launch_moe_decode_one(adi_hip_context *ctx, const MoeDecodeOne &a) {
+    const uint32_t blocks = ctx->cu_count / 16 * 16;
+    const size_t lds = kPlaneBytes + kFusedRegion;
+    if (ctx->isa_lanes == 16) {
+        static const bool ready =
+            set_lds_limit(reinterpret_cast<const void *>(&k_moe_decode_one<16>), lds);
+        (void)ready;
+        launch(ctx, "moe_decode_one", k_moe_decode_one<16>, dim3(blocks), dim3(kFusedThreads), lds, a);
+    } else {
+        static const bool ready =
+            set_lds_limit(reinterpret_cast<const void *>(&k_moe_decode_one<8>), lds);
+        (void)ready;
+        launch(ctx, "moe_decode_one", k_moe_decode_one<8>, dim3(blocks), dim3(kFusedThreads), lds, a);
+    }
 }
 
 template void launch_epilogue_any<uint16_t>(adi_hip_context *, const float *, uint32_t, size_t,

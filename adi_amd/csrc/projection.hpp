@@ -190,6 +190,45 @@ struct MoeGemv {
     uint32_t half_items[2];
 };
 void launch_trellis_gemv(adi_hip_context *ctx, MoeGemv &m);
+
+// The MoE block of one row in one persistent launch, for decode
+// (src/executor.cpp:242-330): router and top-8, the shared expert's
+// prologues, the routed and shared gate/up, the SwiGLUs, the down projections
+// and the route-order combine, one block per CU. Data passes between blocks
+// through device-coherent accesses and counters in `sync` (bounded waits; a
+// wait that runs out sets the error word). gu and dn are the plans of the
+// separate gate/up and down launches (same buffers, same slices), so the
+// arithmetic is the separate launches' exactly.
+struct MoeDecodeOne {
+    MoeGemv gu;                       // routed gate/up (entries 0, 1), shared gate/up (NE 0, 1)
+    MoeGemv dn;                       // routed down (entry 0), shared down (NE 0); dn.swiglu set
+    const uint16_t *router;           // [experts][hidden] bf16
+    const uint16_t *shared_gate_row;  // [hidden] bf16
+    const float *logit_bias;          // [experts] or null
+    const float *x;                   // [hidden]
+    const uint16_t *su_gate;          // [experts][hidden] f16
+    const uint16_t *su_up;
+    const int8_t *shared_su_gate;     // [hidden] +-1
+    const int8_t *shared_su_up;
+    const uint16_t *sv_down;          // [experts][hidden] f16
+    const int8_t *shared_sv_down;     // [hidden] +-1
+    float scale_hidden;               // 1 / sqrt(hidden)
+    float *out;                       // [hidden]
+    uint32_t *route_expert_out;       // [8] or null
+    float *route_weight_out;          // [8] or null
+    uint32_t *sync;                   // kMoeSyncWords words, zero between calls (but the error word)
+    uint32_t experts;
+    // set by plan_moe_decode_one
+    uint32_t expect_slot;             // gate/up wave items per routed slot
+    uint32_t expect_down;             // down wave items per routed slot
+    uint32_t down_splits;             // Z slices of the routed and shared down projections
+    uint32_t shared_down_splits;
+};
+// Fills the plans; false when the shapes or the device do not fit the launch
+// (hidden 2048, expert hidden 512, at most 256 experts, 256 CUs, the ISA
+// order of 8 or 16 lanes). The caller then runs the separate launches.
+bool plan_moe_decode_one(adi_hip_context *ctx, MoeDecodeOne &a);
+void launch_moe_decode_one(adi_hip_context *ctx, const MoeDecodeOne &a);
 // Whether `m` (a down projection of one row) can build its x_hat from
 // m.swiglu in the launch: one expert entry of width 512 and at most one
 // expert item per wave.

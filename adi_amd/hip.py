@@ -114,6 +114,7 @@ SIGNATURES = [
     ("adi_hip_last_error", C.c_char_p, [vp]),
     ("adi_hip_set_stream", C.c_int, [vp, vp]),
     ("adi_hip_synchronize", C.c_int, [vp]),
+    ("adi_hip_set_fused_decode", C.c_int, [vp, C.c_int]),
     ("adi_hip_set_reduction_isa", C.c_int, [vp, u32]),
     ("adi_hip_device_alloc", C.c_int, [vp, C.c_size_t, C.POINTER(vp)]),
     ("adi_hip_device_free", None, [vp, vp]),
@@ -238,6 +239,11 @@ class Context:
 
     def synchronize(self) -> None:
         self.check(self.lib.adi_hip_synchronize(self.handle))
+
+    def set_fused_decode(self, enabled: bool) -> None:
+        """One persistent launch for a one-row MoE block (default) or the
+        separate launches."""
+        self.check(self.lib.adi_hip_set_fused_decode(self.handle, 1 if enabled else 0))
 
     def close(self) -> None:
         if getattr(self, "handle", None):

@@ -78,3 +78,51 @@ def test_moe_repeated_calls_are_deterministic(gpu, full_layer):
         again = run_moe(gpu, dl, x, None)
         assert np.array_equal(first[0].view(np.uint32), again[0].view(np.uint32))
         assert np.array_equal(first[1], again[1])
+
+
+def run_both(gpu, dl, x, bias):
+    """The layer with the one-launch batch-1 path and with the separate
+    launches (the same arithmetic); adi_hip_synchronize reports a cross-block
+    wait of the one launch that ran out."""
+    try:
+        gpu.set_fused_decode(True)
+        fused = run_moe(gpu, dl, x, bias)
+        gpu.synchronize()
+        gpu.set_fused_decode(False)
+        separate = run_moe(gpu, dl, x, bias)
+    finally:
+        gpu.set_fused_decode(True)
+    return fused, separate
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+@pytest.mark.parametrize("bias", [False, True])
+def test_moe_one_launch_equals_separate_launches(gpu, oracle, full_layer, seed, bias):
+    layer, dl = full_layer
+    rng = syn.rng_for(2, 300 + seed)
+    x = syn.hidden_states(rng, 1, layer.hidden)
+    b = syn.zipf_bias(rng, layer.experts) if bias else None
+    fused, separate = run_both(gpu, dl, x, b)
+    assert np.array_equal(fused[1], separate[1]), "routes differ"
+    assert np.array_equal(fused[2].view(np.uint32), separate[2].view(np.uint32)), "weights differ"
+    assert np.array_equal(fused[0].view(np.uint32), separate[0].view(np.uint32)), "outputs differ"
+    check(oracle, layer, fused, x, b)
+
+
+def test_moe_one_launch_repeated_calls(gpu, full_layer):
+    """Back-to-back one-row calls on new inputs: each call's counters start
+    from zero (the last block of a call clears them), so every call equals the
+    separate launches on its own input."""
+    layer, dl = full_layer
+    rng = syn.rng_for(2, 400)
+    xs = [syn.hidden_states(rng, 1, layer.hidden) for _ in range(6)]
+    outs = [run_moe(gpu, dl, x, None) for x in xs]
+    gpu.synchronize()
+    gpu.set_fused_decode(False)
+    try:
+        for x, got in zip(xs, outs):
+            want = run_moe(gpu, dl, x, None)
+            assert np.array_equal(got[0].view(np.uint32), want[0].view(np.uint32))
+            assert np.array_equal(got[1], want[1])
+    finally:
+        gpu.set_fused_decode(True)
