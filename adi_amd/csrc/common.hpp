@@ -333,6 +333,10 @@ __device__ __forceinline__ uint32_t coherent_add(uint32_t *p, uint32_t v) {
 }
 // Waits until every memory access the wave issued has completed.
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
+// s_waitcnt operand that waits for the wave's LDS (and scalar) accesses only:
+// lgkmcnt 0 (bits 11:8) with vmcnt (bits 15:14, 3:0) and expcnt (bits 6:4)
+// at their maxima, so outstanding global loads stay in flight.
+constexpr uint16_t kWaitLds = 0xC07F;
 
 // float4 at p (16-byte aligned), through coherent loads when COHERENT.
 template <bool COHERENT>

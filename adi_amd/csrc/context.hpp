@@ -96,12 +96,12 @@ struct adi_hip_context {
 
 namespace adi_hip {
 
-// adi_hip_context::moe_sync: 91 lines of kMoeSyncLine words (counters and
-// flags, the error word, the route record, the logits and the combine's nine
-// rows) and the index of its error word.
+// adi_hip_context::moe_sync: 64 lines of kMoeSyncLine words (counters and
+// flags, the logits, the error word and the combine's nine rows) and the
+// index of its error word.
 constexpr uint32_t kMoeSyncLine = 1024;
-constexpr uint32_t kMoeSyncWords = 91 * kMoeSyncLine;
-constexpr uint32_t kMoeSyncError = 70 * kMoeSyncLine;
+constexpr uint32_t kMoeSyncWords = 64 * kMoeSyncLine;
+constexpr uint32_t kMoeSyncError = 45 * kMoeSyncLine;
 
 // Selects the context's device for the duration of a call.
 class DeviceScope {

@@ -390,7 +390,8 @@ constexpr uint32_t kMaxSlots = 1024;                     // routed slots staged 
 struct ExpertStage {
     uint4 info;         // {matrix, first position, end position, -}; empty when end == first
     uint32_t d[4][3];   // the lane's three stream dwords in each group of 16 tiles
-    float gamma[4];
+    uint32_t gamma[4];  // f16 bits of each group's wave gamma, converted at use so
+                        // that nothing waits on these loads when they are issued
     float4 x[4][2];     // x_hat of the first position: columns c0..c0+3, c0+8..c0+11
 };
 
@@ -450,20 +451,25 @@ __device__ __forceinline__ void expert_prefetch(const MoeGemv &m, const uint4 *s
     uint32_t column[4], tile[4];
     bool valid[4];
     expert_tiles(a, it.item, half, lane, column, valid, tile);
-    const uint32_t *words = reinterpret_cast<const uint32_t *>(a.trellis + st.info.x * a.trellis_stride);
-    const uint16_t *gamma_row = a.gamma + st.info.x * a.gamma_stride;
+    // a slot past the active count may name any expert: its stage reads
+    // expert 0 and is never computed
+    const uint32_t expert = live ? st.info.x : 0u;
+    const uint32_t *words = reinterpret_cast<const uint32_t *>(a.trellis + expert * a.trellis_stride);
+    const uint16_t *gamma_row = a.gamma + expert * a.gamma_stride;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         valid[g] = valid[g] && live;
-        st.d[g][0] = st.d[g][1] = st.d[g][2] = 0u;
-        st.gamma[g] = 0.0f;
-        if (valid[g]) {
-            const uint32_t *src = words + static_cast<size_t>(tile[g]) * 12u + quad * 3u;
+        if (static_cast<uint32_t>(g) < groups) {
+            // no lane branches here: a lane past the matrix reads tile 0 and
+            // expert_compute zeroes its gamma, so the loads go straight to
+            // their registers and nothing waits on them until the compute
+            const uint32_t t = valid[g] ? tile[g] : 0u;
+            const uint32_t *src = words + static_cast<size_t>(t) * 12u + quad * 3u;
             st.d[g][0] = __builtin_nontemporal_load(src);
             st.d[g][1] = __builtin_nontemporal_load(src + 1);
             st.d[g][2] = __builtin_nontemporal_load(src + 2);
-            const uint32_t tr = tile[g] >> a.tc_shift, tc = tile[g] & (tile_columns - 1u);
-            st.gamma[g] = half_bits_to_float(gamma_row[wave_slot(tr, tc, a.tile_rows, tile_columns)]);
+            const uint32_t tr = t >> a.tc_shift, tc = t & (tile_columns - 1u);
+            st.gamma[g] = gamma_row[wave_slot(tr, tc, a.tile_rows, tile_columns)];
         }
     }
     // a fused SwiGLU's x_hat sits in LDS for the item's single position
@@ -549,9 +555,14 @@ __device__ __forceinline__ void expert_compute(const MoeGemv &m, uint32_t i, uin
                     partial[r] = fmaf((c & 1) ? w.y : w.x, xs[c], partial[r]);
                 }
             }
+            // the opaque copy keeps the conversion (and the wait for the
+            // load) here rather than where the load was issued
+            uint32_t gamma_bits = st.gamma[g];
+            asm volatile("" : "+v"(gamma_bits));
+            const float gamma = valid[g] ? half_bits_to_float(gamma_bits) : 0.0f;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                acc[r] = fmaf(partial[r], st.gamma[g], acc[r]);
+                acc[r] = fmaf(partial[r], gamma, acc[r]);
             }
         }
 #pragma unroll
@@ -989,20 +1000,22 @@ __global__ __launch_bounds__(kGemvThreads) void k_trellis_gemv(MoeGemv m) {
 // counter or flag, so that pollers and atomics of different words meet in
 // different memory channels. A flag that every block polls is written to
 // eight replica lines; block b polls replica b % 8 (its XCD's, as blocks are
-// dealt to the XCDs round robin). The route lines carry data: word s of each
-// replica is 1 + the expert of routed slot s, so a block's poll returns its
-// slot's expert. Grid-wide tickets count in two levels: eight group lines of
-// up to 32 blocks each, then a top line.
+// dealt to the XCDs round robin), and the counters behind it are polled by
+// one wave only (the publisher), so they take their atomics undisturbed.
+// Grid-wide tickets count in two levels: eight group lines of up to 32
+// blocks each, then a top line. The logits
+// line holds the router logits as complemented bits, so its cleared state
+// (zero) reads as "not written yet" (a logit whose bits are all ones, one
+// particular NaN, would never read as written: its wait runs out).
 namespace moe_sync {
-constexpr uint32_t kRouterGroup = 0, kRouterTop = 8, kRoutes = 9, kSharedXhatCount = 17,
-                   kSharedXhatReady = 18, kSharedCount = 26, kSharedReady = 27, kSlotCount = 35,
-                   kDownCount = 43, kSharedDownGroup = 51, kSharedDownTop = 59, kCombineTicket = 60,
-                   kRecordReady = 69, kCounterLines = 70,
-                   kError = kMoeSyncError / kMoeSyncLine, kRecord = 71, kLogits = 72, kParts = 73;
-// words of the route record line
-constexpr uint32_t kToGrouped = 0, kRouteWeight = 8, kSharedLogit = 16;
+constexpr uint32_t kSharedGroup = 0, kSharedReady = 8, kSlotCount = 16, kDownCount = 24,
+                   kSharedDownGroup = 32, kSharedDownTop = 40, kCombineTicket = 41, kCounterLines = 42,
+                   kLogits = 42,
+                   kError = kMoeSyncError / kMoeSyncLine, kParts = 46;
 // kParts: the combine's nine rows (routes 0-7, then the shared expert), two
 // lines each
+// words of a block's route record in LDS
+constexpr uint32_t kToGrouped = 0, kRouteWeight = 8;
 }  // namespace moe_sync
 
 __device__ __forceinline__ uint32_t *sync_line(uint32_t *sync, uint32_t line) {
@@ -1014,6 +1027,7 @@ constexpr uint32_t kFusedThreads = kGemvThreads + kWave;  // eight GEMV waves an
 constexpr uint32_t kFusedSlots = 8;
 constexpr uint32_t kSpinLimit = 1u << 20;  // about a second of polling
 constexpr size_t kFusedRegion = 16384;     // LDS after the plane: staging and x_hat rows
+constexpr uint32_t kFusedMaxExperts = 256;  // routed experts the one-launch block handles
 
 // Polls (the whole wave) until *word is nonzero and returns it; bounded (0
 // after a timeout, which sets `bit` of the error word).
@@ -1036,43 +1050,38 @@ __device__ __forceinline__ uint32_t wait_nonzero(uint32_t *word, uint32_t *error
     }
 }
 
-// Polls the eight route words of a replica line (two 16-byte coherent
-// loads per poll, two polls in flight) until words s1 and s2 are both
-// nonzero; returns them (0 after a timeout, which sets error bit 1).
-__device__ __forceinline__ uint2 wait_route_words(uint32_t *line, uint32_t s1, uint32_t s2,
-                                                  uint32_t *error) {
+// Polls the logits line (16-byte coherent loads, lane l words 4l .. 4l + 3)
+// until the first `count` words are all written (nonzero), then stores the
+// logits (the words complemented back) into `out` in LDS; bounded (a timeout
+// sets error bit 1 and leaves zeros, which still route).
+__device__ __forceinline__ void wait_logits(uint32_t *words, uint32_t count, uint32_t lane, float *out,
+                                            uint32_t *error) {
     typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(line, 0, 32, 0x00020000);
-    auto poll = [&](u32x4_t &lo, u32x4_t &hi) {
-        lo = __builtin_amdgcn_raw_buffer_load_b128(rs, 0, 0, 16 /* sc1 */);
-        hi = __builtin_amdgcn_raw_buffer_load_b128(rs, 16, 0, 16);
-    };
-    auto word = [](const u32x4_t &lo, const u32x4_t &hi, uint32_t s) {
-        uint32_t v = 0;
-#pragma unroll
-        for (uint32_t q = 0; q < 4; ++q) {
-            v = s == q ? lo[q] : v;
-            v = s == q + 4 ? hi[q] : v;
-        }
-        return __builtin_amdgcn_readfirstlane(v);
-    };
-    u32x4_t lo0, hi0, lo1, hi1;
-    poll(lo0, hi0);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(words, 0, 1024, 0x00020000);
+    u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16u, 0, 16 /* sc1 */);
     for (uint32_t spins = 0;; ++spins) {
-        __builtin_amdgcn_s_sleep(1);
-        poll(lo1, hi1);
-        const uint32_t a = word(lo0, hi0, s1), b = word(lo0, hi0, s2);
-        if (a != 0u && b != 0u) {
-            return make_uint2(a, b);
+        bool in = true;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            in = in && (4u * lane + i >= count || q[i] != 0u);
+        }
+        if (__all(in ? 1 : 0)) {
+            break;
         }
         if (spins >= kSpinLimit) {
-            if ((threadIdx.x & 63u) == 0) {
+            if (lane == 0) {
                 __hip_atomic_fetch_or(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            return make_uint2(0u, 0u);
+            break;
         }
-        lo0 = lo1;
-        hi0 = hi1;
+        __builtin_amdgcn_s_sleep(1);
+        q = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16u, 0, 16);
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+        if (4u * lane + i < count) {
+            out[4u * lane + i] = __uint_as_float(~q[i]);
+        }
     }
 }
 
@@ -1214,6 +1223,30 @@ __device__ __forceinline__ bool grid_ticket(uint32_t *sync, uint32_t group_line,
     return coherent_add(sync_line(sync, top_line), 1u) + 1u == groups;
 }
 
+// Polls (the whole wave) the eight group lines from `first` until group g
+// (the blocks b with b % 8 == g) has counted `per_block` for each of its
+// blocks; lane g loads group g's line, so each round is one load latency.
+// Bounded: a timeout sets `bit` of the error word.
+__device__ __forceinline__ void wait_groups(uint32_t *sync, uint32_t first, uint32_t per_block,
+                                            uint32_t blocks, uint32_t lane, uint32_t *error,
+                                            uint32_t bit) {
+    const uint32_t g = lane & 7u;
+    const uint32_t target = g < blocks ? per_block * ((blocks - g + 7u) >> 3) : 0u;
+    uint32_t *word = sync_line(sync, first + g);
+    for (uint32_t spins = 0;; ++spins) {
+        if (__all(coherent_load(word) >= target ? 1 : 0)) {
+            return;
+        }
+        if (spins >= kSpinLimit) {
+            if (lane == 0) {
+                __hip_atomic_fetch_or(error, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 // Sets the eight replicas of a flag every block polls.
 __device__ __forceinline__ void publish_flag(uint32_t *sync, uint32_t line) {
 #pragma unroll
@@ -1267,6 +1300,52 @@ __device__ __forceinline__ float router_lane_sum(float acc, uint32_t group) {
     return sum;
 }
 
+// The 2048-point transform of x * m by the eight GEMV waves of a block, in
+// two steps with a block barrier between them. Step one: wave w transforms
+// elements 256 w .. 256 w + 255 (index bits 0-7; element 64 i + lane of its
+// chunk in register i) into `dst`. Step two: each wave takes 32 of the 256
+// columns across the eight chunks (index bits 8-10) and scales. Every
+// butterfly is the one-wave transform's (wave_hadamard over 2048), in the
+// same order, so the result is bit-identical to it.
+__device__ __forceinline__ void hadamard_chunk(const float *x, const float (&m)[4], uint32_t wave,
+                                               uint32_t lane, float *dst) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[i] = x[256u * wave + 64u * i + lane] * m[i];
+    }
+    wave_hadamard<4>(v, 1.0f, lane);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        dst[256u * wave + 64u * i + lane] = v[i];
+    }
+}
+__device__ __forceinline__ void hadamard_cross(float *dst, float scale, uint32_t wave, uint32_t lane) {
+    if (lane < 32) {
+        const uint32_t j = 32u * wave + lane;
+        float u[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            u[k] = dst[256u * k + j];
+        }
+#pragma unroll
+        for (int stride = 1; stride < 8; stride <<= 1) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if ((k & stride) == 0) {
+                    const float p = u[k], q = u[k + stride];
+                    u[k] = p + q;
+                    u[k + stride] = p - q;
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            dst[256u * k + j] = u[k] * scale;
+        }
+    }
+}
+
 // The thread's share of a codebook plane into LDS: all loads, then the stores.
 __device__ __forceinline__ void fill_plane_share(const uint4 *src, uint4 *dst) {
     constexpr uint32_t kPer = static_cast<uint32_t>(kPlaneBytes / 16) / kGemvThreads;
@@ -1303,8 +1382,8 @@ __device__ __forceinline__ void finish_combine(const MoeDecodeOne &a, uint32_t *
     for (uint32_t t = t0; t < moe_sync::kCounterLines; t += threads) {
         coherent_store(sync_line(sync, t), 0u);
     }
-    for (uint32_t t = t0; t < 64u; t += threads) {
-        coherent_store(sync_line(sync, moe_sync::kRoutes + (t >> 3)) + (t & 7u), 0u);
+    for (uint32_t t = t0; t < 257u; t += threads) {
+        coherent_store(sync_line(sync, moe_sync::kLogits) + t, 0u);
     }
     constexpr uint32_t H = kFusedHidden;
     float4 *row_out = reinterpret_cast<float4 *>(a.out);
@@ -1332,16 +1411,22 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
     extern __shared__ uint4 lds_dynamic[];  // the codebook plane, then kFusedRegion bytes
     __shared__ uint32_t ne_table[1024];
     __shared__ uint4 slots[kFusedSlots];
-    // top-8 block: expert and weight bits of each route; then, in every
-    // block, the route record: grouped position and weight bits of each
-    // route, the shared gate logit
-    __shared__ uint32_t routes[24];
-    __shared__ uint32_t record_lds[17];
+    // the block's routing: expert and weight bits of each route (top8_wave's
+    // output), then the route record: grouped position and weight bits of
+    // each route, the shared gate logit
+    __shared__ uint32_t routes[16];
+    __shared__ uint32_t record_lds[16];
+    __shared__ uint16_t su_lds[kFusedHidden];  // su (f16) of the block's gate/up entry and slot
+    __shared__ float bias_lds[kFusedMaxExperts];  // the routing bias, staged before the logits arrive
+    // the logits as the helper collects them (the region is busy with the
+    // shared x_hat meanwhile)
+    __shared__ float logits_lds[kFusedMaxExperts];
     // 0: waves that filled their plane share and table part; 1: slot table;
     // 2, 8: waves through the two halves of the routed x_hat (2 again for the
     // combine row); 3: gate/up items counted; 4: down x_hat; 5: shared
-    // gate/up items counted; 6: down items counted; 7: route record in LDS;
-    // 9: the block's slot-completion state; 10: combine row stores counted
+    // gate/up items counted; 6: down items counted; 7: the router's staged
+    // rows read (their space free); 9: the block's slot-completion state;
+    // 10: combine row stores counted; 11: P0 barrier arrivals
     __shared__ uint32_t flags[12];
     constexpr uint32_t H = kFusedHidden;
     constexpr int VPL = kFusedHidden / 64;
@@ -1361,11 +1446,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
     const uint32_t worker = ((b >> 4) << 3) | (b & 7u);
     uint32_t *sync = a.sync;
     uint32_t *error = sync_line(sync, moe_sync::kError);
-    uint32_t *record = sync_line(sync, moe_sync::kRecord);
-    float *record_f = reinterpret_cast<float *>(record);
-    float *logits_g = reinterpret_cast<float *>(sync_line(sync, moe_sync::kLogits));
+    uint32_t *logit_words = sync_line(sync, moe_sync::kLogits);  // complemented bits
     auto part = [&](uint32_t r) { return reinterpret_cast<float *>(sync_line(sync, moe_sync::kParts + 2u * r)); };
-    const uint32_t replica = b & 7u;
     // the block's routed slots: gate/up items (P1) and down items (P2)
     const uint32_t slot1 = expert_item_of(a.gu, worker * kGemvWaves).slot;
     const uint32_t slot2 = expert_item_of(a.dn, worker * kGemvWaves).slot;
@@ -1407,11 +1489,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
         // gate's among them, on the last blocks), staged with x in the region
         const uint32_t rows_total = a.experts + 1u;
         uint16_t *wl = reinterpret_cast<uint16_t *>(region);
-        // the two shared-prologue blocks carry no row: theirs go to the two
-        // blocks after them as second rows (those have none of their own)
-        const uint32_t p0 = blocks / 2u;
-        const uint32_t r0 = b - p0 < 2u ? rows_total : b;
-        const uint32_t r1 = b - (p0 + 2u) < 2u ? b - 2u : 2u * blocks - 1u - b;
+        const uint32_t r0 = b;
+        const uint32_t r1 = 2u * blocks - 1u - b;
         auto row = [&](uint32_t r) {
             return reinterpret_cast<const uint4 *>(r < a.experts ? a.router + static_cast<size_t>(r) * H
                                                                  : a.shared_gate_row);
@@ -1441,115 +1520,67 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
         const float acc = router_chain<LANES>(wl + (group == 1u ? H : 0u), x_staged, H, lane % LANES);
         const float s0 = router_lane_sum<LANES>(acc, 0u);
         const float s1 = router_lane_sum<LANES>(acc, 1u);
+        set_flag(&flags[7]);  // the staged rows are read
+        // rows 0 .. experts - 1 are the router's, row `experts` the shared
+        // gate's; every block's helper polls them (no ticket)
         if (lane == 0) {
             if (r0 < rows_total) {
-                coherent_store(r0 < a.experts ? logits_g + r0 : record_f + moe_sync::kSharedLogit, s0);
+                coherent_store(logit_words + r0, ~__float_as_uint(s0));
             }
             if (r1 < rows_total) {
-                coherent_store(r1 < a.experts ? logits_g + r1 : record_f + moe_sync::kSharedLogit, s1);
+                coherent_store(logit_words + r1, ~__float_as_uint(s1));
             }
         }
-        wait_stores();
-        uint32_t last = 0;
-        if (lane == 0) {
-            last = grid_ticket(sync, moe_sync::kRouterGroup, moe_sync::kRouterTop, b, blocks) ? 1u : 0u;
+    }
+    // the shared expert's gate/up NE items while the router finishes: the
+    // first half of the blocks takes the gate's items, the second the up's,
+    // two consecutive ones per block on waves 6 and 7, so that a block needs
+    // the x_hat of one matrix only. The eight waves build it in x_routed's
+    // space (free until the routes) as in P1; waves 6 and 7 take their x
+    // from it, run the items and count them, all before the routed codes
+    // load the memory system. Each block counts into its group line (b % 8)
+    // without waiting for the count; block 0's helper publishes the shared
+    // flag once every group line is full.
+    const uint32_t shared_which = b < blocks / 2u ? 0u : 1u;
+    const uint32_t shared_first = 2u * (b - shared_which * (blocks / 2u));  // within the matrix
+    const uint32_t shared_mine = (shared_first < a.gu.ne_items_per_matrix ? 1u : 0u) +
+                                 (shared_first + 1u < a.gu.ne_items_per_matrix ? 1u : 0u);
+    const bool shared_item = !helper && wave >= 6u && wave - 6u < shared_mine;
+    const uint32_t shared_k = shared_which * a.gu.ne_items_per_matrix + shared_first + (wave - 6u);
+    if (!helper) {
+        float sign[4];
+        const int8_t *su_shared = shared_which == 0u ? a.shared_su_gate : a.shared_su_up;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sign[i] = static_cast<float>(su_shared[256u * wave + 64u * i + lane]);
         }
-        if (__builtin_amdgcn_readfirstlane(last) != 0u) {
-            // the last router block: top_experts over the published logits
-            float *logits = region;  // the staged rows are no longer needed
-            for (uint32_t e = lane; e < a.experts; e += 64u) {
-                logits[e] = logits_g[e];
-            }
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            uint32_t chosen[8];
-            top8_wave<4>(logits, a.logit_bias, a.experts, lane, routes,
-                         reinterpret_cast<float *>(routes + 8), nullptr, chosen);
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            // lane l < 64: word l % 8 of replica l / 8 is 1 + the expert of
-            // slot l % 8 (slots in ascending expert order: the counting sort's
-            // grouped order for one row)
-            const uint32_t sl = lane & 7u;
-            uint32_t sorted = 0;
-#pragma unroll
-            for (uint32_t q = 0; q < 8; ++q) {
-                uint32_t rank = 0;
-#pragma unroll
-                for (uint32_t t = 0; t < 8; ++t) {
-                    rank += chosen[t] < chosen[q] ? 1u : 0u;
-                }
-                sorted = rank == sl ? chosen[q] : sorted;
-            }
-            coherent_store(sync_line(sync, moe_sync::kRoutes + (lane >> 3)) + sl, sorted + 1u);
-            if (lane < 8) {
-                uint32_t e = chosen[0];
-#pragma unroll
-                for (uint32_t q = 1; q < 8; ++q) {
-                    e = lane == q ? chosen[q] : e;
-                }
-                uint32_t rank = 0;
-#pragma unroll
-                for (uint32_t q = 0; q < 8; ++q) {
-                    rank += chosen[q] < e ? 1u : 0u;
-                }
-                const float w = reinterpret_cast<const float *>(routes)[8 + lane];
-                coherent_store(record + moe_sync::kToGrouped + lane, rank);
-                coherent_store(record_f + moe_sync::kRouteWeight + lane, w);
-                if (a.route_expert_out != nullptr) {
-                    a.route_expert_out[lane] = e;
-                }
-                if (a.route_weight_out != nullptr) {
-                    a.route_weight_out[lane] = w;
-                }
-            }
-            wait_stores();
+        // arrivals of the eight waves at the n-th P0 barrier: flags[11] >= 8 n
+        // (each wave's LDS reads and writes complete before it arrives)
+        uint32_t barriers = 0;
+        auto p0_barrier = [&]() {
+            __builtin_amdgcn_s_waitcnt(kWaitLds);
             if (lane == 0) {
-                coherent_store(sync_line(sync, moe_sync::kRecordReady), 1u);
+                __hip_atomic_fetch_add(&flags[11], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
+            wait_lds_value(&flags[11], kGemvWaves * ++barriers, error);
+        };
+        wait_lds_value(&flags[7], 1u, error);
+        NeStage st;
+        hadamard_chunk(x_staged, sign, wave, lane, x_routed);
+        p0_barrier();
+        hadamard_cross(x_routed, a.scale_hidden, wave, lane);
+        p0_barrier();
+        if (shared_item) {
+            ne_prefetch(a.gu, shared_k, lane, st, x_routed);
         }
-    }
-    const uint32_t prologue_block = blocks / 2u;  // carries no router row
-    if (wave == 6 && b - prologue_block < 2u) {
-        // the shared expert's gate (first block) or up (second) x_hat, for
-        // every block, by a wave of two mid-grid blocks
-        const uint32_t which = b - prologue_block;
-        float v[VPL], su[VPL];
-        load_wave<VPL>(a.x, lane, v);
-        load_wave_sign<VPL>(which == 0 ? a.shared_su_gate : a.shared_su_up, lane, su);
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            v[i] = v[i] * su[i];
-        }
-        wave_hadamard<VPL>(v, a.scale_hidden, lane);
-        store_wave_through<VPL>(const_cast<float *>(a.gu.ne[which].x_hat), lane, v);
-        wait_stores();
-        if (lane == 0 && coherent_add(sync_line(sync, moe_sync::kSharedXhatCount), 1u) == 1u) {
-            publish_flag(sync, moe_sync::kSharedXhatReady);  // the second of the two
-        }
-    }
-    // the shared expert while the router finishes: gate/up NE items on waves
-    // 6 and 7 (item (w - 6) * blocks + b; off the helper's SIMD); the wave
-    // that completes them publishes the shared flag
-    if (wave == 6u || wave == 7u) {
-        const uint32_t k = (wave - 6u) * blocks + b;
-        if (k < a.gu.ne_items) {
+        p0_barrier();  // x_routed is free again
+        if (shared_item) {
             wait_plane();
-            wait_count(sync_line(sync, moe_sync::kSharedXhatReady + replica), 1u, error, 2u);
-            NeStage st;
-            ne_prefetch(a.gu, k, lane, st);
-            ne_compute<true>(a.gu, k, ne_table, lane, st);
-            wait_stores();
-            uint32_t finisher = 0;
-            if (lane == 0) {
-                const uint32_t mine = (b < a.gu.ne_items ? 1u : 0u) + (blocks + b < a.gu.ne_items ? 1u : 0u);
-                finisher = atomicAdd(&flags[5], 1u) + 1u == mine &&
-                                   coherent_add(sync_line(sync, moe_sync::kSharedCount), mine) + mine ==
-                                       a.gu.ne_items
-                               ? 1u
-                               : 0u;
-            }
-            if (__builtin_amdgcn_readfirstlane(finisher) != 0u && lane == 0) {
-                publish_flag(sync, moe_sync::kSharedReady);
-            }
+            ne_compute<true>(a.gu, shared_k, ne_table, lane, st);
+        }
+        if (wave >= 6u) {
+            // both waves count (also one without an item): 2 per block
+            count_block_quiet(&flags[5], 2u, sync_line(sync, moe_sync::kSharedGroup + (b & 7u)));
         }
     }
 
@@ -1557,29 +1588,73 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
     const uint32_t item = worker * kGemvWaves + wave;  // gate/up and down items alike (GEMV waves)
     const uint2 *plane = reinterpret_cast<const uint2 *>(plane_lds);
     if (helper) {
-        uint32_t *route_line = sync_line(sync, moe_sync::kRoutes + replica);
-        // (a wait that runs out gives 0: expert 0 keeps every access in
-        // bounds, and the error word already marks the outputs invalid)
-        const uint2 vv = wait_route_words(route_line, slot1, slot2, error);
-        const uint32_t v1 = vv.x, v2 = vv.y;
-        const uint32_t e1 = v1 != 0u ? v1 - 1u : 0u;
-        const uint32_t e2 = v2 != 0u ? v2 - 1u : 0u;
-        if (lane == 0) {
-            slots[slot1] = make_uint4(e1, slot1, slot1 + 1u, 0u);
-            slots[slot2] = make_uint4(e2, slot2, slot2 + 1u, 0u);
+        // every block routes the row itself once all logits are in: the
+        // same top_experts over the same logits in every block
+        float *logits = logits_lds;
+        if (a.logit_bias != nullptr) {
+            for (uint32_t e = lane; e < a.experts; e += 64u) {
+                bias_lds[e] = a.logit_bias[e];
+            }
+        }
+        wait_logits(logit_words, a.experts, lane, logits, error);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        uint32_t chosen[8];
+        top8_wave<4>(logits, a.logit_bias != nullptr ? bias_lds : nullptr, a.experts, lane, routes,
+                     reinterpret_cast<float *>(routes + 8), nullptr, chosen);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        // slot s: the s-th smallest chosen expert (the counting sort's
+        // grouped order for one row); route r sits at grouped position rank(r)
+        if (lane < 8) {
+            uint32_t e = chosen[0];
+#pragma unroll
+            for (uint32_t q = 1; q < 8; ++q) {
+                e = lane == q ? chosen[q] : e;
+            }
+            uint32_t rank = 0;
+#pragma unroll
+            for (uint32_t q = 0; q < 8; ++q) {
+                rank += chosen[q] < e ? 1u : 0u;
+            }
+            slots[rank] = make_uint4(e, rank, rank + 1u, 0u);
+            record_lds[moe_sync::kToGrouped + lane] = rank;
+            record_lds[moe_sync::kRouteWeight + lane] = routes[8 + lane];
+            if (b == 0 && a.route_expert_out != nullptr) {
+                a.route_expert_out[lane] = e;
+            }
+            if (b == 0 && a.route_weight_out != nullptr) {
+                a.route_weight_out[lane] = __uint_as_float(routes[8 + lane]);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        {
+            // su of the block's (entry, slot) into LDS, loaded before the
+            // GEMV waves' codes flood the memory queues
+            const ExpertItem it = expert_item_of(a.gu, worker * kGemvWaves);
+            const uint4 *src = reinterpret_cast<const uint4 *>(
+                (it.which == 0 ? a.su_gate : a.su_up) + static_cast<size_t>(slots[slot1].x) * H);
+            uint4 q[4];
+#pragma unroll
+            for (uint32_t u = 0; u < 4; ++u) {
+                q[u] = src[u * 64u + lane];
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 4; ++u) {
+                reinterpret_cast<uint4 *>(su_lds)[u * 64u + lane] = q[u];
+            }
         }
         set_flag(&flags[1]);
-        // the route record for the combine rows this block may build
-        wait_count(sync_line(sync, moe_sync::kRecordReady), 1u, error, 1u);
-        if (lane < 17) {
-            record_lds[lane] = coherent_load(record + lane);
-        }
-        set_flag(&flags[7]);
         // the shared expert's SwiGLU x_hat (every block's helper builds it
         // from the published gate/up slices), then its down NE item b; the
         // block that completes those builds the shared combine row
         wait_plane();
-        wait_count(sync_line(sync, moe_sync::kSharedReady + replica), 1u, error, 8u);
+        if (b == 0) {
+            wait_groups(sync, moe_sync::kSharedGroup, 2u, blocks, lane, error, 8u);
+            if (lane == 0) {
+                publish_flag(sync, moe_sync::kSharedReady);
+            }
+        } else {
+            wait_count(sync_line(sync, moe_sync::kSharedReady + (b & 7u)), 1u, error, 8u);
+        }
         SwigluInputs in;
         float xd[VPLI];
         swiglu_issue(a.dn.swiglu, true, 0u, 0u, lane, in);
@@ -1596,7 +1671,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
             finisher = grid_ticket(sync, moe_sync::kSharedDownGroup, moe_sync::kSharedDownTop, b, blocks) ? 1u : 0u;
         }
         if (__builtin_amdgcn_readfirstlane(finisher) != 0u) {
-            const float g = __uint_as_float(record_lds[moe_sync::kSharedLogit]);
+            const float g = __uint_as_float(~wait_nonzero(logit_words + a.experts, error, 1u));
             combine_row<VPL>(a.dn.ne[0].z, a.dn.ne[0].z_split_stride, a.shared_down_splits, nullptr,
                              a.shared_sv_down, 1.0f / (1.0f + expf(-g)), a.scale_hidden, lane, part(8));
             if (combine_ticket(sync, lane)) {
@@ -1606,54 +1681,20 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
     } else {
         ExpertStage st;
         wait_flag(&flags[1], error);
-        // x_hat = H(su[expert] * x) of the block's (entry, slot), by the eight
-        // waves: wave w transforms elements 256 w .. 256 w + 255 (index bits
-        // 0-7, element 64 i + lane of its chunk in register i), then each
-        // wave takes 32 of the 256 columns across the chunks for bits 8-10,
-        // so every butterfly is the one-wave transform's, in the same order.
-        // Its su loads go out before the item's codes, which return later.
-        const ExpertItem it = expert_item_of(a.gu, worker * kGemvWaves);
-        const uint16_t *su = (it.which == 0 ? a.su_gate : a.su_up) +
-                             static_cast<size_t>(slots[slot1].x) * H + 256u * wave;
-        float v[4], sv4[4];
+        // x_hat = H(su[expert] * x) of the block's (entry, slot) by the eight
+        // waves, su from the helper's LDS copy; the item's codes go out once
+        // the wave's chunk is stored, so the transform does not queue behind
+        // their issue
+        const uint16_t *su = su_lds + 256u * wave;
+        float sv4[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             sv4[i] = half_bits_to_float(su[64 * i + lane]);
         }
+        hadamard_chunk(x_staged, sv4, wave, lane, x_routed);
         expert_prefetch(a.gu, slots, item, half, lane, st, nullptr, false);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            v[i] = x_staged[256u * wave + 64u * i + lane] * sv4[i];
-        }
-        wave_hadamard<4>(v, 1.0f, lane);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            x_routed[256u * wave + 64u * i + lane] = v[i];
-        }
         arrive_and_wait(&flags[2], kGemvWaves, error);
-        if (lane < 32) {
-            const uint32_t j = 32u * wave + lane;
-            float u[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                u[k] = x_routed[256u * k + j];
-            }
-#pragma unroll
-            for (int stride = 1; stride < 8; stride <<= 1) {
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    if ((k & stride) == 0) {
-                        const float p = u[k], q = u[k + stride];
-                        u[k] = p + q;
-                        u[k + stride] = p - q;
-                    }
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                x_routed[256u * k + j] = u[k] * a.scale_hidden;
-            }
-        }
+        hadamard_cross(x_routed, a.scale_hidden, wave, lane);
         wait_plane();
         arrive_and_wait(&flags[8], kGemvWaves, error);
         expert_prefetch_x(a.gu, item, half, lane, st, x_routed);
@@ -1709,7 +1750,6 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
         // the slot's last down items are in: its route's combine row, by the
         // eight waves (chunks of 256, then the top three butterfly stages
         // across chunks, as for the routed x_hat)
-        wait_flag(&flags[7], error);
         uint32_t r = 0;
 #pragma unroll
         for (uint32_t q = 0; q < 8; ++q) {
@@ -1970,7 +2010,7 @@ void launch_trellis_gemv(adi_hip_context *ctx, MoeGemv &m) {
 
 bool plan_moe_decode_one(adi_hip_context *ctx, MoeDecodeOne &a) {
     if (ctx->cu_count < 16 || (ctx->isa_lanes != 8 && ctx->isa_lanes != 16) || a.sync == nullptr ||
-        a.experts < 8 || a.experts > 256 || a.gu.expert_count != 2 || a.gu.ne_count != 2 ||
+        a.experts < 8 || a.experts > kFusedMaxExperts || a.gu.expert_count != 2 || a.gu.ne_count != 2 ||
         a.dn.expert_count != 1 || a.dn.ne_count != 1 || a.gu.max_active != kFusedSlots ||
         a.dn.max_active != kFusedSlots || a.gu.ne_book != a.dn.ne_book) {
         return false;
@@ -1987,12 +2027,13 @@ bool plan_moe_decode_one(adi_hip_context *ctx, MoeDecodeOne &a) {
         return false;
     }
     // one item per wave, a block's eight items in one slot, every router row
-    // on some block, every NE item on a wave
+    // on some block (rows b and 2 blocks - 1 - b), every shared gate/up NE
+    // item on a wave (two per block), one shared down NE item per block
     const uint32_t wave_items = (blocks / 2) * kGemvWaves;
     if (a.gu.expert_items != wave_items || a.dn.expert_items != wave_items ||
         a.gu.expert_items_per_slot % kGemvWaves != 0 || a.dn.expert_items_per_slot % kGemvWaves != 0 ||
-        a.experts + 1 > 2 * blocks || a.gu.ne_items > 2 * blocks || a.dn.ne_items != blocks ||
-        2 * blocks - 1 - (blocks / 2 + 3) < a.experts + 1) {
+        a.experts + 1 > 2 * blocks || a.gu.ne_items != 2 * a.gu.ne_items_per_matrix ||
+        a.gu.ne_items_per_matrix > blocks || a.dn.ne_items != blocks) {
         return false;
     }
     // each half of the grid runs every item once
