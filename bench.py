@@ -82,6 +82,10 @@ def log(msg):
 
 def kernel_bytes(name, active):
     """Algorithmic packed bytes one launch of `name` reads, or None."""
+    if name == "moe_decode_one":
+        # the whole ubatch-1 layer in one launch: router, shared expert, and
+        # the active experts' gate, up and down with their scales
+        return FIXED_LAYER_BYTES + active * PER_EXPERT_BYTES
     if name == "moe_gemv":
         # two launches per step: gate+up (2 expert + 2 shared matrices), down
         # (1 + 1); the mean launch reads half the step's GEMV packed bytes
@@ -189,10 +193,48 @@ def kernel_flops(name, ubatch):
     return None
 
 
-def roofline_for(prof, steps, active, ubatch):
+ROCPROF_NAMES = {"moe_decode_one": "k_moe_decode_one", "moe_gemv": "k_trellis_gemv",
+                 "expert_mfma": "k_expert_mfma"}
+
+
+def rocprof_avg_us(kernel, ubatch):
+    """Average duration (us) of `kernel` at `ubatch` in the committed
+    rocprofv3 --kernel-trace --stats summary, or None."""
+    path = os.path.join(ROOT, "profiles", "moe_layer_kernel_stats.md")
+    want = ROCPROF_NAMES.get(kernel)
+    if want is None or not os.path.exists(path):
+        return None
+    section = None
+    for row in open(path):
+        if row.startswith("## ubatch "):
+            section = int(row.split()[2])
+            continue
+        cells = [c.strip().strip("`") for c in row.strip().strip("|").split("|")]
+        if section == ubatch and len(cells) >= 3 and cells[0].split("<")[0] == want:
+            return float(cells[2])
+    return None
+
+
+def roofline_for(prof, steps, active, ubatch, wall_ms_per_step):
     r = roofline_kernel(prof, active, ubatch)
-    if r is not None:
-        r["traffic"] = traffic_from_profile(r["kernel"], ubatch)
+    if r is None:
+        return None
+    name = r["kernel"]
+    launches, ms = prof[name]
+    r["event_avg_us"] = r["avg_launch_us"]
+    r["timing"] = "per-launch HIP events"
+    if launches == steps and r["share_of_step"] == 1.0:
+        # the step is this one launch: the timed region (bracketed by device
+        # synchronisation) per step bounds its duration from above without the
+        # per-launch event overhead
+        us = min(wall_ms_per_step * 1e3, r["avg_launch_us"])
+        scale = r["avg_launch_us"] / us
+        r["avg_launch_us"] = round(us, 2)
+        r["achieved"] = round(r["achieved"] * scale, 2)
+        r["frac"] = round(r["frac"] * scale, 4)
+        r["timing"] = "timed region / launches (one launch per step)"
+    r["rocprof_avg_us"] = rocprof_avg_us(name, ubatch)
+    r["traffic"] = traffic_from_profile(name, ubatch)
     return r
 
 
@@ -552,7 +594,7 @@ def main():
             "layer_packed_bytes": int(layer_bytes),
             "layer_hbm_frac": round(layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "mfma_frac_equiv": round(FLOP_PER_TOKEN * u / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 5),
-            "roofline": roofline_for(prof, args.steps, active, u),
+            "roofline": roofline_for(prof, args.steps, active, u, ms),
             "kernels_us_per_step": {k: round(v[1] * 1e3 / args.steps, 2) for k, v in
                                     sorted(prof.items(), key=lambda kv: -kv[1][1])},
         }
