@@ -31,7 +31,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // 512 * kExpertGroups threads per block (one block per CU), MFMA passes per
 // product (hi*hi + hi*lo + lo*hi)
 constexpr int kExpertRT = 4;
-constexpr int kExpertCB = 1;      // blocks of 32 positions per item
+constexpr int kExpertCB = 2;      // blocks of 32 positions per item (the later one may be empty)
 constexpr int kExpertGroups = 1;  // wave groups of eight per block, each on its own item
 constexpr int kExpertPasses = 3;
 constexpr uint32_t kPlaneRows16 = kExpertRows * 8 / 16;   // 16-byte rows of a plane
@@ -160,16 +160,17 @@ __device__ __forceinline__ void expert_decode(const ExpertWave &wv, uint32_t kc,
 }
 
 // acc[rb][cb] += hi * bh + hi * bl + lo * bh over the two K pairs, for the
-// item's CB blocks of 32 positions (lo only when PASSES is 3). Positions past
-// the slot carry another slot's x_hat: their output columns are computed and
-// never stored.
-template <int CB, int PASSES>
+// item's first LIVE of its CB blocks of 32 positions (lo only when PASSES is
+// 3). Positions past the slot in a live block carry another slot's x_hat:
+// their output columns are computed and never stored.
+template <int CB, int LIVE, int PASSES>
 __device__ __forceinline__ void expert_multiply(const ExpertA &a, const half8 (&bh)[CB][2],
                                                 const half8 (&bl)[CB][2], f32x16 (&acc)[2][CB]) {
+    static_assert(LIVE >= 1 && LIVE <= CB, "live blocks of an item");
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb) {
+        for (int cb = 0; cb < LIVE; ++cb) {
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
                 acc[rb][cb] = mfma32(a.hi[2 * rb + c], bh[cb][c], acc[rb][cb]);
@@ -179,7 +180,7 @@ __device__ __forceinline__ void expert_multiply(const ExpertA &a, const half8 (&
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb) {
+        for (int cb = 0; cb < LIVE; ++cb) {
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
                 acc[rb][cb] = mfma32(a.hi[2 * rb + c], bl[cb][c], acc[rb][cb]);
@@ -190,7 +191,7 @@ __device__ __forceinline__ void expert_multiply(const ExpertA &a, const half8 (&
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
-            for (int cb = 0; cb < CB; ++cb) {
+            for (int cb = 0; cb < LIVE; ++cb) {
 #pragma unroll
                 for (int c = 0; c < 2; ++c) {
                     acc[rb][cb] = mfma32(a.lo[2 * rb + c], bh[cb][c], acc[rb][cb]);
@@ -418,10 +419,11 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
             }
         }
         // B of K step kc, as the MFMA operands of position block cb, K pair c
-        auto read_b = [&](uint32_t ring_slot, half8 (&bh)[CB][2], half8 (&bl)[CB][2]) {
+        // (the item's first LIVE blocks)
+        auto read_b = [&]<int LIVE>(uint32_t ring_slot, half8 (&bh)[CB][2], half8 (&bl)[CB][2]) {
             const char *base = ring + ring_slot * kBSlot + m * kBRowPitch + kh * 16u;
 #pragma unroll
-            for (int cb = 0; cb < CB; ++cb) {
+            for (int cb = 0; cb < LIVE; ++cb) {
 #pragma unroll
                 for (int c = 0; c < 2; ++c) {
                     bh[cb][c] = *reinterpret_cast<const half8 *>(base + cb * 32u * kBRowPitch + c * 32u);
@@ -429,58 +431,73 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
                 }
             }
         };
-        if (steps % kDepth != 0) {
-            // short K (under 4 steps): one step at a time
-            for (uint32_t kc = 0; kc < steps; ++kc) {
-                const BChunk bv = load_b(xsrc, b_off, kc * 64u);
-                ExpertWords ws;
-                expert_words(wv, kc, ws);
-                *reinterpret_cast<BChunk *>(ring + b_store) = bv;
-                __syncthreads();
-                half8 bh[CB][2], bl[CB][2];
-                read_b(0, bh, bl);
-                ExpertA fa;
-                expert_decode<PASSES>(wv, kc, sign_mask, plane, ws, fa);
-                expert_multiply<CB, PASSES>(fa, bh, bl, acc);
-                __syncthreads();
-            }
-        } else {
-            // B of step s waits in bv[s % 4] (registers) until step s - 1
-            // writes it to ring slot s % 2; the words of step s wait in
-            // ws[s % 4]. Loads past the last step reload it (in bounds,
-            // unused), so the loop body has no branch.
-            BChunk bv[kDepth];
-            ExpertWords ws[kDepth];
-#pragma unroll
-            for (int u = 0; u < kDepth; ++u) {
-                __builtin_amdgcn_sched_barrier(0);
-                bv[u] = load_b(xsrc, b_off, u * 64u);
-                if (u < kDepth - 1) {
-                    expert_words(wv, u, ws[u]);
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            *reinterpret_cast<BChunk *>(ring + b_store) = bv[0];
-            bv[0] = load_b(xsrc, b_off, min(static_cast<uint32_t>(kDepth), last) * 64u);
-            __syncthreads();
-            for (uint32_t kc = 0; kc < steps; kc += kDepth) {
-#pragma unroll
-                for (int u = 0; u < kDepth; ++u) {
-                    const uint32_t step = kc + u;
-                    __builtin_amdgcn_sched_barrier(0);
-                    // hand B of the next step to the ring and refill its registers
-                    *reinterpret_cast<BChunk *>(ring + ((u + 1) & 1) * kBSlot + b_store) = bv[(u + 1) % kDepth];
-                    bv[(u + 1) % kDepth] = load_b(xsrc, b_off, min(step + 1u + kDepth, last) * 64u);
-                    expert_words(wv, min(step + kDepth - 1u, last), ws[(u + kDepth - 1) % kDepth]);
-                    __builtin_amdgcn_sched_barrier(0);
+        // the K loop for an item whose first LIVE blocks of 32 positions hold
+        // positions of its slot: each K step's A fragments are decoded once
+        // and multiplied with every live block (the slot's later blocks skip
+        // their MFMAs, not the decode)
+        auto k_loop = [&]<int LIVE>() {
+            if (steps % kDepth != 0) {
+                // short K (under 4 steps): one step at a time
+                for (uint32_t kc = 0; kc < steps; ++kc) {
+                    const BChunk bv = load_b(xsrc, b_off, kc * 64u);
+                    ExpertWords ws;
+                    expert_words(wv, kc, ws);
+                    *reinterpret_cast<BChunk *>(ring + b_store) = bv;
+                    __syncthreads();
                     half8 bh[CB][2], bl[CB][2];
-                    read_b(u & 1, bh, bl);
+                    read_b.template operator()<LIVE>(0, bh, bl);
                     ExpertA fa;
-                    expert_decode<PASSES>(wv, step, sign_mask, plane, ws[u], fa);
-                    expert_multiply<CB, PASSES>(fa, bh, bl, acc);
+                    expert_decode<PASSES>(wv, kc, sign_mask, plane, ws, fa);
+                    expert_multiply<CB, LIVE, PASSES>(fa, bh, bl, acc);
                     __syncthreads();
                 }
+            } else {
+                // B of step s waits in bv[s % 4] (registers) until step s - 1
+                // writes it to ring slot s % 2; the words of step s wait in
+                // ws[s % 4]. Loads past the last step reload it (in bounds,
+                // unused), so the loop body has no branch.
+                BChunk bv[kDepth];
+                ExpertWords ws[kDepth];
+#pragma unroll
+                for (int u = 0; u < kDepth; ++u) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    bv[u] = load_b(xsrc, b_off, u * 64u);
+                    if (u < kDepth - 1) {
+                        expert_words(wv, u, ws[u]);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                *reinterpret_cast<BChunk *>(ring + b_store) = bv[0];
+                bv[0] = load_b(xsrc, b_off, min(static_cast<uint32_t>(kDepth), last) * 64u);
+                __syncthreads();
+                for (uint32_t kc = 0; kc < steps; kc += kDepth) {
+#pragma unroll
+                    for (int u = 0; u < kDepth; ++u) {
+                        const uint32_t step = kc + u;
+                        __builtin_amdgcn_sched_barrier(0);
+                        // hand B of the next step to the ring and refill its registers
+                        *reinterpret_cast<BChunk *>(ring + ((u + 1) & 1) * kBSlot + b_store) = bv[(u + 1) % kDepth];
+                        bv[(u + 1) % kDepth] = load_b(xsrc, b_off, min(step + 1u + kDepth, last) * 64u);
+                        expert_words(wv, min(step + kDepth - 1u, last), ws[(u + kDepth - 1) % kDepth]);
+                        __builtin_amdgcn_sched_barrier(0);
+                        half8 bh[CB][2], bl[CB][2];
+                        read_b.template operator()<LIVE>(u & 1, bh, bl);
+                        ExpertA fa;
+                        expert_decode<PASSES>(wv, step, sign_mask, plane, ws[u], fa);
+                        expert_multiply<CB, LIVE, PASSES>(fa, bh, bl, acc);
+                        __syncthreads();
+                    }
+                }
             }
+        };
+        if constexpr (CB == 2) {
+            if (p0 + 32u < end) {
+                k_loop.template operator()<2>();
+            } else {
+                k_loop.template operator()<1>();
+            }
+        } else {
+            k_loop.template operator()<1>();
         }
         // D register r of lane l: position 32 cb + l % 32, block row
         // (r % 4) + 8 (r / 4) + 4 kh
