@@ -102,6 +102,7 @@ namespace adi_hip {
 constexpr uint32_t kMoeSyncLine = 1024;
 constexpr uint32_t kMoeSyncWords = 64 * kMoeSyncLine;
 constexpr uint32_t kMoeSyncError = 45 * kMoeSyncLine;
+constexpr uint32_t kMoeSyncNeTicket = 43 * kMoeSyncLine;  // the one-launch NE projection's ticket
 
 // Selects the context's device for the duration of a call.
 class DeviceScope {

@@ -1320,7 +1320,36 @@ __device__ __forceinline__ void hadamard_chunk(const float *x, const float (&m)[
         dst[256u * wave + 64u * i + lane] = v[i];
     }
 }
+// Step two for any chunk of SPAN elements (SPAN / 8 columns per wave).
+template <uint32_t SPAN>
+__device__ __forceinline__ void hadamard_cross_span(float *dst, float scale, uint32_t wave, uint32_t lane) {
+#pragma clang fp contract(off)
+    constexpr uint32_t per_wave = SPAN / 8u;
+    for (uint32_t j = per_wave * wave + lane; j < per_wave * (wave + 1u); j += 64u) {
+        float u[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            u[k] = dst[SPAN * k + j];
+        }
+#pragma unroll
+        for (int stride = 1; stride < 8; stride <<= 1) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if ((k & stride) == 0) {
+                    const float p = u[k], q = u[k + stride];
+                    u[k] = p + q;
+                    u[k + stride] = p - q;
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            dst[SPAN * k + j] = u[k] * scale;
+        }
+    }
+}
 __device__ __forceinline__ void hadamard_cross(float *dst, float scale, uint32_t wave, uint32_t lane) {
+#pragma clang fp contract(off)
     if (lane < 32) {
         const uint32_t j = 32u * wave + lane;
         float u[8];
@@ -1816,9 +1845,263 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
 }
 
 
+
+// ---- one-launch NE projection of a few rows -------------------------------
+//
+// y = sv * H_rows(W x_hat) * scale_rows with x_hat = H_columns(su * x) *
+// scale_columns (src/kernels.cpp:899-979), for up to kNeFusedRows input rows,
+// in one launch instead of prologue, GEMV and epilogue. Block b takes tile
+// rows b, b + blocks, ... whole: it builds every input row's x_hat itself
+// (eight waves' cooperative transform, bit-identical to the one-wave one),
+// runs the tile row's NE items (16 tiles each, the GEMV's arithmetic, the
+// table values gathered once per item), and adds the items' partial sums in
+// item (slice) order in LDS, so the sum is the one the separate epilogue
+// forms. With two or more input rows the grid is two halves: half g takes
+// input rows g, g + 2, ... of every tile row (each half decodes the codes
+// itself), so the VALU work of the input rows spreads over all CUs. The
+// block of a half that completes its last tile row (a ticket per half;
+// nobody waits) runs the row transform over that half's sums.
+template <int VC, int VR>
+__global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
+#pragma clang fp contract(off)
+    extern __shared__ float ne_lds[];  // x_hat [batch][C], then the outputs [batch][R]
+    __shared__ uint32_t table[1024];
+    __shared__ float part[kNeFusedMaxItems][16][kNeFusedRows];  // [item in tile row][row][input row]
+    __shared__ uint32_t last;
+    constexpr uint32_t C = 512u * VC, R = 512u * VR, CH = C / 8u, RH = R / 8u;
+    __shared__ int8_t sv_lds[R];  // the output signs, staged by every block for whichever ends last
+    constexpr uint32_t tile_columns = C / kTile, per_row = tile_columns / 16u;
+    constexpr uint32_t tile_rows = R / kTile;
+    constexpr uint32_t kMine = kNeFusedRows;  // input rows of a half, at most
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t w8 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t quad = lane & 3u, tslot = lane >> 2;
+    const uint32_t halves = a.halves;
+    const uint32_t group = blockIdx.x % halves;      // the half: input rows group, group + halves, ...
+    const uint32_t b = blockIdx.x / halves, blocks = gridDim.x / halves;  // within the half
+    uint32_t *ticket = a.ticket + 32u * group;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    // the codes of the block's first tile row go out first
+    constexpr uint32_t kWaveItems = per_row > 8u ? per_row / 8u : 1u;
+    u32x4 code[kWaveItems][2];
+    auto load_codes = [&](uint32_t tr) {
+#pragma unroll
+        for (uint32_t q = 0; q < kWaveItems; ++q) {
+            const uint32_t j = w8 + 8u * q;
+            const uint32_t tile = (tr * per_row + (j < per_row ? j : 0u)) * 16u + tslot;
+            const u32x4 *src = reinterpret_cast<const u32x4 *>(a.trellis) + static_cast<size_t>(tile) * 8u + quad * 2u;
+            code[q][0] = __builtin_nontemporal_load(src);
+            code[q][1] = __builtin_nontemporal_load(src + 1);
+        }
+    };
+    load_codes(b);
+    for (uint32_t i = threadIdx.x; i < 1024u; i += kNeFusedThreads) {
+        table[i] = a.table[i];
+    }
+    for (uint32_t i = threadIdx.x; i < R / 4u; i += kNeFusedThreads) {
+        reinterpret_cast<uint32_t *>(sv_lds)[i] = reinterpret_cast<const uint32_t *>(a.sv)[i];
+    }
+    // x_hat of the half's input rows (their loads first)
+    {
+        float v[kMine][VC], s[VC];
+        load_wave_sign<VC>(a.su + w8 * CH, lane, s);
+#pragma unroll
+        for (uint32_t i = 0; i < kMine; ++i) {
+            const uint32_t p = group + halves * i;
+            if (p < a.batch) {
+                load_wave<VC>(a.x + static_cast<size_t>(p) * C + w8 * CH, lane, v[i]);
+            }
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < kMine; ++i) {
+            const uint32_t p = group + halves * i;
+            if (p < a.batch) {
+#pragma unroll
+                for (int e = 0; e < VC; ++e) {
+                    v[i][e] = v[i][e] * s[e];
+                }
+                wave_hadamard<VC>(v[i], 1.0f, lane);
+                store_wave<VC>(ne_lds + p * C + w8 * CH, lane, v[i]);
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t p = group; p < a.batch; p += halves) {
+        hadamard_cross_span<CH>(ne_lds + p * C, a.scale_columns, w8, lane);
+    }
+    __syncthreads();
+    for (uint32_t tr = b; tr < tile_rows; tr += blocks) {
+#pragma unroll
+        for (uint32_t q = 0; q < kWaveItems; ++q) {
+            const uint32_t j = w8 + 8u * q;
+            if (j < per_row) {
+                const uint32_t d[9] = {code[q][0].x, code[q][0].y, code[q][0].z, code[q][0].w,
+                                       code[q][1].x, code[q][1].y, code[q][1].z, code[q][1].w,
+                                       quad_next(code[q][0].x) & 0xFFFFu};
+                uint32_t idx[32];
+                decode_ne_quad(d, idx);
+                uint32_t w[32];
+#pragma unroll
+                for (int k = 0; k < 32; ++k) {
+                    w[k] = table[idx[k]];
+                }
+                const uint32_t column = (j * 16u + tslot) << 4;
+#pragma unroll
+                for (uint32_t i = 0; i < kMine; ++i) {
+                    const uint32_t p = group + halves * i;
+                    if (p >= a.batch) {
+                        break;
+                    }
+                    float x[16];
+                    const float4 *src = reinterpret_cast<const float4 *>(ne_lds + p * C + column);
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const float4 t = src[g];
+                        x[4 * g] = t.x;
+                        x[4 * g + 1] = t.y;
+                        x[4 * g + 2] = t.z;
+                        x[4 * g + 3] = t.w;
+                    }
+                    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int s = 0; s < 8; ++s) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float2 wv = half2_bits_to_float2(w[8 * r + s]);
+                            acc[r] = fmaf(wv.x, x[2 * s], acc[r]);
+                            acc[r] = fmaf(wv.y, x[2 * s + 1], acc[r]);
+                        }
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        acc[r] = sum_over_quads(acc[r], 16u);
+                    }
+                    if (tslot == 0) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            part[j][quad * 4u + r][p] = acc[r] * a.weight_scale;
+                        }
+                    }
+                }
+            }
+        }
+        if (tr + blocks < tile_rows) {
+            load_codes(tr + blocks);
+        }
+        __syncthreads();
+        // the slice-order sum of the tile row's items: ((0 + item 0) + item 1) + ...
+        if (threadIdx.x < 16u * kMine && group + halves * (threadIdx.x >> 4) < a.batch) {
+            const uint32_t r = threadIdx.x & 15u, p = group + halves * (threadIdx.x >> 4);
+            float sum = 0.0f;
+            for (uint32_t j = 0; j < per_row; ++j) {
+                sum = sum + part[j][r][p];
+            }
+            coherent_store(reinterpret_cast<uint32_t *>(a.zsum) + static_cast<size_t>(p) * R + tr * kTile + r,
+                           __float_as_uint(sum));
+        }
+        __syncthreads();
+    }
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        last = coherent_add(ticket, 1u) + 1u == blocks ? 1u : 0u;
+    }
+    __syncthreads();
+    if (last == 0u) {
+        return;
+    }
+    // the half's last block: every sum of its input rows is in (first touch
+    // here, ordinary loads; all the loads first)
+    {
+        float v[kMine][VR];
+#pragma unroll
+        for (uint32_t i = 0; i < kMine; ++i) {
+            const uint32_t p = group + halves * i;
+            if (p < a.batch) {
+                load_wave<VR>(a.zsum + static_cast<size_t>(p) * R + w8 * RH, lane, v[i]);
+            }
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < kMine; ++i) {
+            const uint32_t p = group + halves * i;
+            if (p < a.batch) {
+                wave_hadamard<VR>(v[i], 1.0f, lane);
+                store_wave<VR>(ne_lds + p * R + w8 * RH, lane, v[i]);
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t p = group; p < a.batch; p += halves) {
+        hadamard_cross_span<RH>(ne_lds + p * R, a.scale_rows, w8, lane);
+    }
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < R; e += kNeFusedThreads) {
+        const float sign = static_cast<float>(sv_lds[e]);
+#pragma unroll
+        for (uint32_t i = 0; i < kMine; ++i) {
+            const uint32_t p = group + halves * i;
+            if (p < a.batch) {
+                a.out[p * R + e] = ne_lds[p * R + e] * sign;
+            }
+        }
+    }
+    if (threadIdx.x == 0) {
+        coherent_store(ticket, 0u);
+    }
+}
+
 }  // namespace
 
 // ---- launchers -------------------------------------------------------------
+
+bool launch_ne_fused(adi_hip_context *ctx, const adi_hip_ne_matrix *m, const float *inputs, uint32_t batch,
+                     float *outputs, float *zsum) {
+    if (batch == 0 || batch > kNeFusedRows || ctx->moe_sync == nullptr || !aligned_to(inputs, 16) ||
+        !aligned_to(zsum, 16)) {
+        return false;
+    }
+    using Kernel = void (*)(NeFused);
+    Kernel kernel = nullptr;
+    const uint32_t vc = m->columns / 512u, vr = m->rows / 512u;
+    auto pick = [&](auto vcs, auto vrs) {
+        constexpr int VC = decltype(vcs)::value, VR = decltype(vrs)::value;
+        if (vc == VC && vr == VR) {
+            kernel = k_ne_fused<VC, VR>;
+        }
+    };
+    using I4 = std::integral_constant<int, 4>;
+    using I8 = std::integral_constant<int, 8>;
+    using I1 = std::integral_constant<int, 1>;
+    using I16 = std::integral_constant<int, 16>;
+    pick(I4{}, I1{}); pick(I4{}, I4{}); pick(I4{}, I8{}); pick(I4{}, I16{});
+    pick(I8{}, I1{}); pick(I8{}, I4{}); pick(I8{}, I8{}); pick(I8{}, I16{});
+    if (kernel == nullptr || m->columns % 512u != 0 || m->rows % 512u != 0) {
+        return false;
+    }
+    NeFused a{};
+    a.trellis = m->trellis;
+    a.su = m->su;
+    a.sv = m->sv;
+    a.table = static_cast<const uint32_t *>(m->codebook->data);
+    a.x = inputs;
+    a.zsum = zsum;
+    a.out = outputs;
+    a.ticket = ctx->moe_sync + kMoeSyncNeTicket;
+    a.weight_scale = m->weight_scale;
+    a.scale_columns = hadamard_scale(m->columns);
+    a.scale_rows = hadamard_scale(m->rows);
+    a.batch = batch;
+    a.halves = batch >= 2 ? 2u : 1u;
+    const uint32_t tile_rows = m->rows / kTile;
+    const uint32_t per_half = ctx->cu_count / a.halves;
+    const uint32_t blocks = a.halves * (tile_rows < per_half ? tile_rows : per_half);
+    const size_t floats = size_t(batch) * std::max(m->columns, m->rows);
+    const size_t lds = floats * sizeof(float);
+    require(lds <= 65536 || set_lds_limit(reinterpret_cast<const void *>(kernel), lds),
+            "one-launch NE projection: LDS limit");
+    launch(ctx, "ne_fused", kernel, dim3(blocks), dim3(kNeFusedThreads), lds, a);
+    return true;
+}
 
 bool wave_width(uint32_t n) { return n >= 64 && n <= 4096 && is_power_of_two(n); }
 
@@ -2175,6 +2458,15 @@ int adi_hip_ne_matmul(adi_hip_context *ctx, const adi_hip_ne_matrix *m,
         validate_ne(m);
         require(batch > 0, "Mach NE batch shape mismatch");
         require(inputs != nullptr && outputs != nullptr, "Mach NE vector is null");
+        if (ctx->fused_moe && batch <= kNeFusedRows) {
+            auto &ws = ctx->workspace;
+            ws.used = 0;
+            ws.ensure(Workspace::round(size_t(batch) * m->rows * 4));
+            float *zsum = ws.take<float>(size_t(batch) * m->rows);
+            if (launch_ne_fused(ctx, m, inputs, batch, outputs, zsum)) {
+                return;
+            }
+        }
         const bool mfma = batch >= kMfmaBatch && m->columns >= 32 && wave_width(m->columns);
         const uint32_t splits = mfma ? ne_mfma_slices(m->rows, m->columns, batch) : ne_splits(m->columns);
         auto &ws = ctx->workspace;

@@ -229,6 +229,30 @@ struct MoeDecodeOne {
 // order of 8 or 16 lanes). The caller then runs the separate launches.
 bool plan_moe_decode_one(adi_hip_context *ctx, MoeDecodeOne &a);
 void launch_moe_decode_one(adi_hip_context *ctx, const MoeDecodeOne &a);
+// One-launch NE projection of up to kNeFusedRows input rows (k_ne_fused):
+// x_hat, the NE items of whole tile rows per block with the slice-order sum
+// in LDS, and the row transform by the block that takes the last ticket.
+constexpr uint32_t kNeFusedRows = 4;
+constexpr uint32_t kNeFusedThreads = 512;
+constexpr uint32_t kNeFusedMaxItems = 32;  // NE items of one tile row at 8192 columns
+struct NeFused {
+    const uint16_t *trellis;
+    const int8_t *su;
+    const int8_t *sv;
+    const uint32_t *table;  // the 4 KiB signed table
+    const float *x;         // [batch][columns]
+    float *zsum;            // [batch][rows]: the slice-order sums
+    float *out;             // [batch][rows]
+    uint32_t *ticket;       // two words (32 apart), zero between launches (each half's last block clears its own)
+    float weight_scale, scale_columns, scale_rows;
+    uint32_t batch;
+    uint32_t halves;        // 1, or 2 when the grid splits the input rows in two
+};
+// Runs `m` on `batch` rows in one launch; false (nothing launched) when the
+// shape is not one the kernel is built for (columns 2048 or 4096, rows 512,
+// 2048, 4096 or 8192, at most kNeFusedRows rows).
+bool launch_ne_fused(adi_hip_context *ctx, const adi_hip_ne_matrix *m, const float *inputs, uint32_t batch,
+                     float *outputs, float *zsum);
 // Whether `m` (a down projection of one row) can build its x_hat from
 // m.swiglu in the launch: one expert entry of width 512 and at most one
 // expert item per wave.

@@ -63,13 +63,15 @@ int adi_hip_synchronize(adi_hip_context *ctx);
  * src/simd.cpp:298-342). Default 16. */
 int adi_hip_set_reduction_isa(adi_hip_context *ctx, uint32_t lanes);
 
-/* Whether adi_hip_moe_forward runs a one-row call as one persistent launch
- * (router, routing, both projections of every route, shared expert and
- * combine; default on) or as the separate launches. Both give bit-identical
- * results. No counterpart in the reference (a tuning switch of this
- * backend). A cross-block wait of the one launch that runs out (only
- * possible when other work keeps some of its blocks off the GPU) is reported
- * by the next adi_hip_synchronize. */
+/* Whether decode-size calls run as one launch (default on) or as the
+ * separate launches: adi_hip_moe_forward on one row (router, routing, both
+ * projections of every route, shared expert and combine in one persistent
+ * launch) and adi_hip_ne_matmul on up to 4 rows of the shapes it is built
+ * for (x_hat, the NE items and the output transform in one launch). Both
+ * ways give bit-identical results. No counterpart in the reference (a tuning
+ * switch of this backend). A cross-block wait of the one-launch MoE block
+ * that runs out (only possible when other work keeps some of its blocks off
+ * the GPU) is reported by the next adi_hip_synchronize. */
 int adi_hip_set_fused_decode(adi_hip_context *ctx, int enabled);
 
 /* ---- device memory -------------------------------------------------------- */

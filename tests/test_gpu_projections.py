@@ -112,6 +112,37 @@ def test_ne_matmul(gpu, books, oracle, rows, columns, batch):
     assert max_rel_error(out.cpu().numpy(), want) <= TOL
 
 
+@pytest.mark.parametrize("rows,columns", [(2048, 2048), (512, 2048), (8192, 2048), (4096, 2048),
+                                          (2048, 4096), (512, 4096)])
+@pytest.mark.parametrize("batch", [1, 2, 4])
+def test_ne_one_launch_equals_separate_launches(gpu, books, oracle, rows, columns, batch):
+    """The one-launch NE projection (rows of up to four inputs) against the
+    prologue + GEMV + epilogue launches: bit-identical, and within the
+    tolerance of the oracle."""
+    _, nt, _, nb = books
+    rng = syn.rng_for(0, 7 * rows + columns + 13 * batch)
+    m = syn.ne_matrix(rng, rows, columns, nt)
+    x = syn.hidden_states(rng, batch, columns)
+    dm = hip.upload_ne(gpu, m, nb)
+    xd = gpu.to_device(x)
+    one = torch.full((batch, rows), float("nan"), dtype=torch.float32, device="cuda")
+    sep = torch.full((batch, rows), float("nan"), dtype=torch.float32, device="cuda")
+    hip.ne_matmul(gpu, dm, xd, batch, one)
+    gpu.set_fused_decode(False)
+    try:
+        hip.ne_matmul(gpu, dm, xd, batch, sep)
+    finally:
+        gpu.set_fused_decode(True)
+    gpu.synchronize()
+    a, b = one.cpu().numpy(), sep.cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), "one launch differs from separate launches"
+    assert max_rel_error(a, po.ne_matmul(oracle, m, x)) <= TOL
+    # a second call reuses the ticket the first one cleared
+    hip.ne_matmul(gpu, dm, xd, batch, one)
+    gpu.synchronize()
+    assert np.array_equal(one.cpu().numpy().view(np.uint32), b.view(np.uint32))
+
+
 def test_known_answers(gpu):
     """tests/kernels_test.cpp:32-137: a zero expert tile with TLUT rows
     1..8 and gamma slot 1 = 2 gives out[0] = 32; the NE tile with TLUT (1, 2)
