@@ -286,8 +286,19 @@ __global__ __launch_bounds__(128) void k_bf16_tiled(
     __shared__ float xs[kTiledBlock][LANES][S::pitch];
     __shared__ float ws[kTiledBlock][LANES][S::pitch];
     const uint32_t total_rows = rows + (w_extra != nullptr ? 1u : 0u);
-    const uint32_t row0 = blockIdx.x * kTiledBlock;
-    const uint32_t t0 = blockIdx.y * kTiledBlock;
+    // XCD-aware tiles: blocks are dealt to the eight XCDs round robin, so
+    // block id goes to XCD id % 8; XCD x takes token tiles x, x + 8, ... with
+    // every row tile, and its L2 holds only its own tokens (and the weights,
+    // which every XCD needs) instead of every token
+    const uint32_t row_tiles = (total_rows + kTiledBlock - 1u) / kTiledBlock;
+    const uint32_t token_tiles = (batch + kTiledBlock - 1u) / kTiledBlock;
+    const uint32_t xcd = blockIdx.x & 7u, k = blockIdx.x >> 3;
+    const uint32_t token_tile = xcd + 8u * (k / row_tiles);
+    if (token_tile >= token_tiles) {
+        return;  // the whole block, before any barrier
+    }
+    const uint32_t row0 = (k % row_tiles) * kTiledBlock;
+    const uint32_t t0 = token_tile * kTiledBlock;
     const uint32_t lane = threadIdx.x % LANES;
     const uint32_t group = threadIdx.x / LANES;
     const uint32_t tg = group / S::row_groups, rg = group % S::row_groups;
@@ -755,7 +766,9 @@ void launch_bf16_ordered_extra(adi_hip_context *ctx, const uint16_t *w, uint32_t
                                 reinterpret_cast<uintptr_t>(w_extra);
     if ((lanes == 8 || lanes == 16) && batch >= kTiledBatch && columns % kTiledChunk == 0 &&
         (addresses & 15u) == 0) {
-        const dim3 grid(ceil_div(total, kTiledBlock), ceil_div(batch, kTiledBlock));
+        // one dimension: the kernel maps block ids to (row tile, token tile)
+        // per XCD
+        const dim3 grid(8u * ceil_div(ceil_div(batch, kTiledBlock), 8u) * ceil_div(total, kTiledBlock));
         if (lanes == 8) {
             launch(ctx, "router", k_bf16_tiled<8, false>, grid, dim3(128), 0, w, rows, w_extra,
                    columns, x, batch, out, out_extra);
