@@ -605,6 +605,235 @@ EmbeddingTensors check_embedding(const adi_hip_gguf &f) {
     return t;
 }
 
+// ---- attention, norms and the output head ---------------------------------
+
+// A bf16 tensor by its source name, stored as "hf." + name
+// (MachModel::bf16_vector / bf16_matrix / bf16_data, src/model.cpp:440-470),
+// with the shape and finite values validate_manifest requires
+// (src/model.cpp:140-148, 808-900).
+const adi_hip_gguf_tensor &bf16_tensor(const adi_hip_gguf &f, const std::string &source,
+                                       std::initializer_list<uint64_t> dims) {
+    const std::string name = "hf." + source;
+    const adi_hip_gguf_tensor &t = required_tensor(f, name, ADI_HIP_GGML_BF16, dims);
+    require_finite(t, finite_bf16, name);
+    return t;
+}
+
+// One NE matrix (MachModel::non_expert, src/model.cpp:267-314, with
+// require_ne_shape, src/model.cpp:150-175): trellis i16 {64, tiles}, SU i8
+// {columns}, SV i8 {rows}, Wscale f32 {1}; +-1 signs, finite positive Wscale.
+struct NeTensors {
+    const adi_hip_gguf_tensor *trellis, *su, *sv;
+    float wscale;
+    uint32_t rows, columns;
+};
+
+NeTensors check_ne(const adi_hip_gguf &f, uint32_t layer, const std::string &source, uint32_t rows,
+                   uint32_t columns) {
+    const std::string p = "mach.ne." + std::to_string(layer) + "." + source + "|";
+    NeTensors n{};
+    n.rows = rows;
+    n.columns = columns;
+    n.trellis = &required_tensor(f, p + "trellis", ADI_HIP_GGML_I16,
+                                 {64, static_cast<uint64_t>(rows / 16) * (columns / 16)});
+    n.su = &required_tensor(f, p + "SU", ADI_HIP_GGML_I8, {columns});
+    n.sv = &required_tensor(f, p + "SV", ADI_HIP_GGML_I8, {rows});
+    n.wscale = *static_cast<const float *>(required_tensor(f, p + "Wscale", ADI_HIP_GGML_F32, {1}).data);
+    if (!std::isfinite(n.wscale) || n.wscale <= 0.0f) {
+        model_fail("unexpected non-expert shape '" + source + "'");
+    }
+    for (const adi_hip_gguf_tensor *t : {n.su, n.sv}) {
+        const int8_t *v = static_cast<const int8_t *>(t->data);
+        for (uint64_t i = 0; i < t->elements; ++i) {
+            if (v[i] != 1 && v[i] != -1) {
+                model_fail("invalid non-expert sign tensor '" + source + "'");
+            }
+        }
+    }
+    return n;
+}
+
+// The attention half of a decoder layer and its two norms
+// (MachModel::cache_descriptors, src/model.cpp:619-683, with the shapes of
+// validate_manifest, src/model.cpp:808-880): every fourth layer (layer + 1
+// divisible by 4) full attention, the others Gated DeltaNet.
+struct AttentionTensors {
+    bool full;
+    NeTensors ne[4];                    // full: q, k, v, o; linear: qkv, z, out
+    const adi_hip_gguf_tensor *bf[6];  // full: q_norm, k_norm; linear: a, b, conv1d, dt_bias, A_log, norm
+    const adi_hip_gguf_tensor *input_norm, *post_norm;
+};
+
+AttentionTensors check_attention(const adi_hip_gguf &f, const adi_hip_moe_geometry &g, uint32_t layer) {
+    if (layer >= g.layers) {
+        model_fail("layer index is out of range");
+    }
+    AttentionTensors A{};
+    const std::string prefix = layer_prefix(layer);
+    A.input_norm = &bf16_tensor(f, prefix + "input_layernorm.weight", {g.hidden});
+    A.post_norm = &bf16_tensor(f, prefix + "post_attention_layernorm.weight", {g.hidden});
+    A.full = (layer + 1) % 4 == 0;
+    if (A.full) {
+        const std::string a = prefix + "self_attn.";
+        A.ne[0] = check_ne(f, layer, a + "q_proj.weight", 8192, g.hidden);
+        A.ne[1] = check_ne(f, layer, a + "k_proj.weight", 512, g.hidden);
+        A.ne[2] = check_ne(f, layer, a + "v_proj.weight", 512, g.hidden);
+        A.ne[3] = check_ne(f, layer, a + "o_proj.weight", g.hidden, 4096);
+        A.bf[0] = &bf16_tensor(f, a + "q_norm.weight", {256});
+        A.bf[1] = &bf16_tensor(f, a + "k_norm.weight", {256});
+    } else {
+        const std::string a = prefix + "linear_attn.";
+        A.ne[0] = check_ne(f, layer, a + "in_proj_qkv.weight", 8192, g.hidden);
+        A.ne[1] = check_ne(f, layer, a + "in_proj_z.weight", 4096, g.hidden);
+        A.ne[2] = check_ne(f, layer, a + "out_proj.weight", g.hidden, 4096);
+        A.bf[0] = &bf16_tensor(f, a + "in_proj_a.weight", {g.hidden, 32});
+        A.bf[1] = &bf16_tensor(f, a + "in_proj_b.weight", {g.hidden, 32});
+        A.bf[2] = &bf16_tensor(f, a + "conv1d.weight", {4, 1, 8192});
+        A.bf[3] = &bf16_tensor(f, a + "dt_bias", {32});
+        A.bf[4] = &bf16_tensor(f, a + "A_log", {32});
+        A.bf[5] = &bf16_tensor(f, a + "norm.weight", {128});
+    }
+    return A;
+}
+
+// The output head: eight chunks of vocabulary / 8 rows (MachModel::head_chunk,
+// src/model.cpp:367-420): qp i8 {hidden/8*5, rows}, gscale f16 {hidden/64,
+// rows} finite, and optionally prot_rows i32 {n} with prot_dense bf16
+// {hidden, n} (both or neither; rows inside the chunk, finite values); then
+// the final norm (bf16 {hidden}, src/model.cpp:604, 884-887). The vocabulary
+// and hidden width are the embedding's.
+struct HeadTensors {
+    uint32_t vocabulary, hidden, chunk_rows;
+    const adi_hip_gguf_tensor *qp[8], *scale[8], *rows[8], *dense[8];
+    const adi_hip_gguf_tensor *final_norm;
+};
+
+HeadTensors check_head(const adi_hip_gguf &f) {
+    const EmbeddingTensors e = check_embedding(f);
+    HeadTensors h{};
+    h.vocabulary = e.rows;
+    h.hidden = e.columns;
+    if (h.vocabulary % 8 != 0 || h.hidden % 64 != 0) {
+        model_fail("output chunk index is out of range");
+    }
+    h.chunk_rows = h.vocabulary / 8;
+    for (uint32_t c = 0; c < 8; ++c) {
+        const uint32_t begin = c * h.chunk_rows, end = begin + h.chunk_rows;
+        const std::string p = "mach.output." + std::to_string(c) + ".LMHEADCHUNK:" + std::to_string(begin) +
+                              ":" + std::to_string(end) + "|";
+        h.qp[c] = &required_tensor(f, p + "qp", ADI_HIP_GGML_I8, {h.hidden / 8u * 5u, h.chunk_rows});
+        h.scale[c] = &required_tensor(f, p + "gscale", ADI_HIP_GGML_F16, {h.hidden / 64u, h.chunk_rows});
+        require_finite(*h.scale[c], finite_f16, "output head scale");
+        const adi_hip_gguf_tensor *r = f.tensor(p + "prot_rows");
+        const adi_hip_gguf_tensor *d = f.tensor(p + "prot_dense");
+        if ((r == nullptr) != (d == nullptr)) {
+            model_fail("incomplete protected output rows");
+        }
+        if (r != nullptr) {
+            if (r->type != ADI_HIP_GGML_I32 || r->dimension_count != 1) {
+                model_fail("invalid protected output row indexes");
+            }
+            h.rows[c] = &required_tensor(f, p + "prot_rows", ADI_HIP_GGML_I32, {r->dimensions[0]});
+            h.dense[c] = &required_tensor(f, p + "prot_dense", ADI_HIP_GGML_BF16, {h.hidden, r->dimensions[0]});
+            require_finite(*h.dense[c], finite_bf16, "protected output rows");
+            const uint32_t *v = static_cast<const uint32_t *>(h.rows[c]->data);
+            for (uint64_t i = 0; i < h.rows[c]->elements; ++i) {
+                if (v[i] >= h.chunk_rows) {
+                    model_fail("protected output row is out of range");
+                }
+            }
+        }
+    }
+    h.final_norm = &bf16_tensor(f, "model.language_model.norm.weight", {h.hidden});
+    return h;
+}
+
+// One device allocation for a set of host pieces, each 256-byte aligned (a
+// run of pieces can be laid end to end).
+struct Upload {
+    struct Piece {
+        const void *data;
+        size_t bytes;
+        size_t at;
+    };
+    std::vector<Piece> pieces;
+    size_t total = 0;
+    size_t add(const void *data, size_t bytes) {
+        const size_t at = total;
+        pieces.push_back({data, bytes, at});
+        total = (total + bytes + 255) & ~size_t(255);
+        return at;
+    }
+    size_t add(const adi_hip_gguf_tensor *t) { return add(t->data, static_cast<size_t>(t->bytes)); }
+    size_t add_run(const std::vector<const adi_hip_gguf_tensor *> &run) {
+        const size_t start = total;
+        for (const adi_hip_gguf_tensor *t : run) {
+            pieces.push_back({t->data, static_cast<size_t>(t->bytes), total});
+            total += static_cast<size_t>(t->bytes);
+        }
+        total = (total + 255) & ~size_t(255);
+        return start;
+    }
+    adi_hip_weights *commit(adi_hip_context *ctx, const char *what);
+};
+
+// Offsets of a layer's MoE tensors in an Upload.
+struct MoeAt {
+    size_t router, gate_row, stack[3][4], shared[3][3];
+};
+
+MoeAt place_moe(Upload &u, const LayerTensors &L) {
+    MoeAt at{};
+    at.router = u.add(L.router);
+    at.gate_row = u.add(L.gate_row);
+    for (int pr = 0; pr < 3; ++pr) {
+        for (int fi = 0; fi < 4; ++fi) {
+            at.stack[pr][fi] = u.add_run(L.expert[pr][fi]);
+        }
+        for (int fi = 0; fi < 3; ++fi) {
+            at.shared[pr][fi] = u.add(L.shared[pr][fi]);
+        }
+    }
+    return at;
+}
+
+adi_hip_ne_matrix ne_descriptor(const char *base, size_t trellis, size_t su, size_t sv, uint32_t rows,
+                                uint32_t columns, float wscale, const adi_hip_codebook *ne_codebook) {
+    adi_hip_ne_matrix n{};
+    n.rows = rows;
+    n.columns = columns;
+    n.trellis = reinterpret_cast<const uint16_t *>(base + trellis);
+    n.su = reinterpret_cast<const int8_t *>(base + su);
+    n.sv = reinterpret_cast<const int8_t *>(base + sv);
+    n.weight_scale = wscale;
+    n.codebook = ne_codebook;
+    return n;
+}
+
+adi_hip_moe_layer moe_descriptor(const char *base, const MoeAt &at, const adi_hip_moe_geometry &g,
+                                 const LayerTensors &L, const adi_hip_codebook *expert_codebook,
+                                 const adi_hip_codebook *ne_codebook) {
+    adi_hip_moe_layer d{};
+    d.hidden = g.hidden;
+    d.expert_hidden = g.expert_hidden;
+    d.experts = g.experts;
+    d.router = adi_hip_bf16_matrix{g.experts, g.hidden, reinterpret_cast<const uint16_t *>(base + at.router)};
+    d.shared_expert_gate = adi_hip_bf16_matrix{1, g.hidden, reinterpret_cast<const uint16_t *>(base + at.gate_row)};
+    adi_hip_expert_stack *stacks[3] = {&d.gate, &d.up, &d.down};
+    adi_hip_ne_matrix *shared[3] = {&d.shared_gate, &d.shared_up, &d.shared_down};
+    for (int pr = 0; pr < 3; ++pr) {
+        stacks[pr]->trellis = reinterpret_cast<const uint16_t *>(base + at.stack[pr][0]);
+        stacks[pr]->su_f16 = reinterpret_cast<const uint16_t *>(base + at.stack[pr][1]);
+        stacks[pr]->sv_f16 = reinterpret_cast<const uint16_t *>(base + at.stack[pr][2]);
+        stacks[pr]->wave_gamma_f16 = reinterpret_cast<const uint16_t *>(base + at.stack[pr][3]);
+        *shared[pr] = ne_descriptor(base, at.shared[pr][0], at.shared[pr][1], at.shared[pr][2],
+                                    pr == 2 ? g.hidden : g.shared_hidden, pr == 2 ? g.shared_hidden : g.hidden,
+                                    L.wscale[pr], ne_codebook);
+    }
+    d.expert_codebook = expert_codebook;
+    return d;
+}
+
 }  // namespace
 }  // namespace adi_hip
 
@@ -612,6 +841,26 @@ struct adi_hip_weights {
     int device = 0;
     void *base = nullptr;
 };
+
+adi_hip_weights *adi_hip::Upload::commit(adi_hip_context *ctx, const char *what) {
+    auto *w = new adi_hip_weights;
+    w->device = ctx->device;
+    if (hipMalloc(&w->base, total == 0 ? 256 : total) != hipSuccess) {
+        delete w;
+        fail(ADI_HIP_OUT_OF_MEMORY, std::string(what) + ": device allocation failed");
+    }
+    try {
+        for (const Piece &p : pieces) {
+            check_hip(hipMemcpy(static_cast<char *>(w->base) + p.at, p.data, p.bytes, hipMemcpyHostToDevice),
+                      (std::string(what) + " copy").c_str());
+        }
+    } catch (...) {
+        (void)hipFree(w->base);
+        delete w;
+        throw;
+    }
+    return w;
+}
 
 extern "C" {
 
@@ -828,86 +1077,12 @@ int adi_hip_gguf_upload_moe_layer(adi_hip_context *ctx, const adi_hip_gguf *file
         *weights = nullptr;
         const adi_hip_moe_geometry g = read_geometry(*file);
         const LayerTensors L = check_layer(*file, g, layer);
-
-        // one allocation, every piece 256-byte aligned; the chunks of a stack
-        // field are laid end to end (expert-major, as the stack expects)
-        struct Piece {
-            const adi_hip_gguf_tensor *tensor;
-            size_t at;
-        };
-        std::vector<Piece> pieces;
-        size_t total = 0;
-        auto place = [&](std::initializer_list<const adi_hip_gguf_tensor *> run) {
-            const size_t start = total;
-            for (const adi_hip_gguf_tensor *t : run) {
-                pieces.push_back({t, total});
-                total += static_cast<size_t>(t->bytes);
-            }
-            total = (total + 255) & ~size_t(255);
-            return start;
-        };
-        auto place_chunks = [&](const std::vector<const adi_hip_gguf_tensor *> &chunks) {
-            const size_t start = total;
-            for (const adi_hip_gguf_tensor *t : chunks) {
-                pieces.push_back({t, total});
-                total += static_cast<size_t>(t->bytes);
-            }
-            total = (total + 255) & ~size_t(255);
-            return start;
-        };
-        const size_t router_at = place({L.router});
-        const size_t gate_row_at = place({L.gate_row});
-        size_t stack_at[3][4], shared_at[3][3];
-        for (int pr = 0; pr < 3; ++pr) {
-            for (int fi = 0; fi < 4; ++fi) {
-                stack_at[pr][fi] = place_chunks(L.expert[pr][fi]);
-            }
-            for (int fi = 0; fi < 3; ++fi) {
-                shared_at[pr][fi] = place({L.shared[pr][fi]});
-            }
-        }
-        auto *w = new adi_hip_weights;
-        w->device = ctx->device;
-        if (hipMalloc(&w->base, total) != hipSuccess) {
-            delete w;
-            fail(ADI_HIP_OUT_OF_MEMORY, "GGUF layer upload: device allocation failed");
-        }
-        try {
-            for (const Piece &p : pieces) {
-                check_hip(hipMemcpy(static_cast<char *>(w->base) + p.at, p.tensor->data,
-                                    static_cast<size_t>(p.tensor->bytes), hipMemcpyHostToDevice),
-                          "GGUF layer upload copy");
-            }
-        } catch (...) {
-            (void)hipFree(w->base);
-            delete w;
-            throw;
-        }
-        char *base = static_cast<char *>(w->base);
-        adi_hip_moe_layer d{};
-        d.hidden = g.hidden;
-        d.expert_hidden = g.expert_hidden;
-        d.experts = g.experts;
-        d.router = adi_hip_bf16_matrix{g.experts, g.hidden, reinterpret_cast<const uint16_t *>(base + router_at)};
-        d.shared_expert_gate = adi_hip_bf16_matrix{1, g.hidden, reinterpret_cast<const uint16_t *>(base + gate_row_at)};
-        adi_hip_expert_stack *stacks[3] = {&d.gate, &d.up, &d.down};
-        adi_hip_ne_matrix *shared[3] = {&d.shared_gate, &d.shared_up, &d.shared_down};
-        for (int pr = 0; pr < 3; ++pr) {
-            stacks[pr]->trellis = reinterpret_cast<const uint16_t *>(base + stack_at[pr][0]);
-            stacks[pr]->su_f16 = reinterpret_cast<const uint16_t *>(base + stack_at[pr][1]);
-            stacks[pr]->sv_f16 = reinterpret_cast<const uint16_t *>(base + stack_at[pr][2]);
-            stacks[pr]->wave_gamma_f16 = reinterpret_cast<const uint16_t *>(base + stack_at[pr][3]);
-            adi_hip_ne_matrix &n = *shared[pr];
-            n.rows = pr == 2 ? g.hidden : g.shared_hidden;
-            n.columns = pr == 2 ? g.shared_hidden : g.hidden;
-            n.trellis = reinterpret_cast<const uint16_t *>(base + shared_at[pr][0]);
-            n.su = reinterpret_cast<const int8_t *>(base + shared_at[pr][1]);
-            n.sv = reinterpret_cast<const int8_t *>(base + shared_at[pr][2]);
-            n.weight_scale = L.wscale[pr];
-            n.codebook = ne_codebook;
-        }
-        d.expert_codebook = expert_codebook;
-        *descriptor = d;
+        // one allocation; the chunks of a stack field are laid end to end
+        // (expert-major, as the stack expects)
+        Upload u;
+        const MoeAt at = place_moe(u, L);
+        adi_hip_weights *w = u.commit(ctx, "GGUF layer upload");
+        *descriptor = moe_descriptor(static_cast<const char *>(w->base), at, g, L, expert_codebook, ne_codebook);
         *weights = w;
     });
 }
@@ -963,6 +1138,134 @@ int adi_hip_gguf_upload_embedding(adi_hip_context *ctx, const adi_hip_gguf *file
         d.exception_bf16 = reinterpret_cast<const uint16_t *>(base + at[4]);
         d.exception_count = static_cast<uint32_t>(t.indexes->elements);
         *descriptor = d;
+        *weights = w;
+    });
+}
+
+int adi_hip_gguf_check_decoder_layer(const adi_hip_gguf *file, uint32_t layer) {
+    return file_call([&] {
+        if (file == nullptr) {
+            fail(ADI_HIP_INVALID_ARGUMENT, "model: null file");
+        }
+        const adi_hip_moe_geometry g = read_geometry(*file);
+        (void)check_layer(*file, g, layer);
+        (void)check_attention(*file, g, layer);
+        return ADI_HIP_OK;
+    });
+}
+
+int adi_hip_gguf_upload_decoder_layer(adi_hip_context *ctx, const adi_hip_gguf *file, uint32_t layer,
+                                      const adi_hip_codebook *expert_codebook,
+                                      const adi_hip_codebook *ne_codebook, adi_hip_weights **weights,
+                                      adi_hip_decoder_layer *descriptor) {
+    return guarded(ctx, [&] {
+        require(file != nullptr && weights != nullptr && descriptor != nullptr,
+                "GGUF decoder layer upload: null argument");
+        require(expert_codebook != nullptr && expert_codebook->kind == adi_hip_codebook::expert &&
+                    ne_codebook != nullptr && ne_codebook->kind == adi_hip_codebook::ne,
+                "GGUF decoder layer upload: expert and NE codebooks required");
+        *weights = nullptr;
+        const adi_hip_moe_geometry g = read_geometry(*file);
+        const LayerTensors L = check_layer(*file, g, layer);
+        const AttentionTensors A = check_attention(*file, g, layer);
+        Upload u;
+        const MoeAt moe = place_moe(u, L);
+        const size_t input_norm = u.add(A.input_norm), post_norm = u.add(A.post_norm);
+        size_t ne[4][3] = {};
+        const int ne_count = A.full ? 4 : 3;
+        for (int i = 0; i < ne_count; ++i) {
+            ne[i][0] = u.add(A.ne[i].trellis);
+            ne[i][1] = u.add(A.ne[i].su);
+            ne[i][2] = u.add(A.ne[i].sv);
+        }
+        size_t bf[6] = {};
+        const int bf_count = A.full ? 2 : 6;
+        for (int i = 0; i < bf_count; ++i) {
+            bf[i] = u.add(A.bf[i]);
+        }
+        adi_hip_weights *w = u.commit(ctx, "GGUF decoder layer upload");
+        const char *base = static_cast<const char *>(w->base);
+        auto ne_at = [&](int i) {
+            return ne_descriptor(base, ne[i][0], ne[i][1], ne[i][2], A.ne[i].rows, A.ne[i].columns, A.ne[i].wscale,
+                                 ne_codebook);
+        };
+        auto bf_at = [&](int i) { return reinterpret_cast<const uint16_t *>(base + bf[i]); };
+        adi_hip_decoder_layer d{};
+        d.input_norm = reinterpret_cast<const uint16_t *>(base + input_norm);
+        d.post_attention_norm = reinterpret_cast<const uint16_t *>(base + post_norm);
+        d.full_attention = A.full ? 1 : 0;
+        if (A.full) {
+            d.full.query = ne_at(0);
+            d.full.key = ne_at(1);
+            d.full.value = ne_at(2);
+            d.full.output = ne_at(3);
+            d.full.query_norm = bf_at(0);
+            d.full.key_norm = bf_at(1);
+        } else {
+            d.linear.qkv = ne_at(0);
+            d.linear.gate = ne_at(1);
+            d.linear.output = ne_at(2);
+            d.linear.alpha = adi_hip_bf16_matrix{32, g.hidden, bf_at(0)};
+            d.linear.beta = adi_hip_bf16_matrix{32, g.hidden, bf_at(1)};
+            d.linear.convolution = bf_at(2);
+            d.linear.alpha_bias = bf_at(3);
+            d.linear.a_log = bf_at(4);
+            d.linear.norm = bf_at(5);
+        }
+        d.moe = moe_descriptor(base, moe, g, L, expert_codebook, ne_codebook);
+        *descriptor = d;
+        *weights = w;
+    });
+}
+
+int adi_hip_gguf_check_head(const adi_hip_gguf *file) {
+    return file_call([&] {
+        if (file == nullptr) {
+            fail(ADI_HIP_INVALID_ARGUMENT, "model: null file");
+        }
+        (void)check_head(*file);
+        return ADI_HIP_OK;
+    });
+}
+
+int adi_hip_gguf_upload_head(adi_hip_context *ctx, const adi_hip_gguf *file, adi_hip_weights **weights,
+                             adi_hip_head_chunk *head, const uint16_t **final_norm) {
+    return guarded(ctx, [&] {
+        require(file != nullptr && weights != nullptr && head != nullptr && final_norm != nullptr,
+                "GGUF head upload: null argument");
+        *weights = nullptr;
+        const HeadTensors h = check_head(*file);
+        // the chunks end to end: packed rows, scales, then the protected rows
+        // renumbered to the whole head and their dense rows
+        std::vector<const adi_hip_gguf_tensor *> qp(h.qp, h.qp + 8), scale(h.scale, h.scale + 8), dense;
+        std::vector<uint32_t> protected_rows;
+        for (uint32_t c = 0; c < 8; ++c) {
+            if (h.rows[c] != nullptr) {
+                const uint32_t *v = static_cast<const uint32_t *>(h.rows[c]->data);
+                for (uint64_t i = 0; i < h.rows[c]->elements; ++i) {
+                    protected_rows.push_back(c * h.chunk_rows + v[i]);
+                }
+                dense.push_back(h.dense[c]);
+            }
+        }
+        Upload u;
+        const size_t packed = u.add_run(qp);
+        const size_t scales = u.add_run(scale);
+        const size_t rows = protected_rows.empty() ? 0 : u.add(protected_rows.data(), protected_rows.size() * 4);
+        const size_t bf = dense.empty() ? 0 : u.add_run(dense);
+        const size_t norm = u.add(h.final_norm);
+        adi_hip_weights *w = u.commit(ctx, "GGUF head upload");
+        const char *base = static_cast<const char *>(w->base);
+        adi_hip_head_chunk d{};
+        d.rows = h.vocabulary;
+        d.columns = h.hidden;
+        d.packed = reinterpret_cast<const uint8_t *>(base + packed);
+        d.group_scale_f16 = reinterpret_cast<const uint16_t *>(base + scales);
+        d.protected_count = static_cast<uint32_t>(protected_rows.size());
+        d.protected_rows = protected_rows.empty() ? nullptr : reinterpret_cast<const uint32_t *>(base + rows);
+        d.protected_bf16 = dense.empty() ? nullptr : reinterpret_cast<const uint16_t *>(base + bf);
+        *head = d;
+        *final_norm = reinterpret_cast<const uint16_t *>(base + norm);
         *weights = w;
     });
 }

@@ -178,6 +178,12 @@ SIGNATURES = [
     ("adi_hip_gguf_upload_moe_layer", C.c_int, [vp, vp, u32, vp, vp, C.POINTER(vp), C.POINTER(MoeLayer)]),
     ("adi_hip_weights_destroy", None, [vp]),
     ("adi_hip_gguf_upload_embedding", C.c_int, [vp, vp, C.POINTER(vp), C.POINTER(Embedding)]),
+    ("adi_hip_gguf_check_decoder_layer", C.c_int, [vp, u32]),
+    ("adi_hip_gguf_upload_decoder_layer", C.c_int, [vp, vp, u32, vp, vp, C.POINTER(vp),
+                                                    C.POINTER(DecoderLayerStruct)]),
+    ("adi_hip_gguf_check_head", C.c_int, [vp]),
+    ("adi_hip_gguf_upload_head", C.c_int, [vp, vp, C.POINTER(vp), C.POINTER(HeadChunk),
+                                           C.POINTER(vp)]),
     ("adi_hip_gguf_check_embedding", C.c_int, [vp]),
 ]
 
@@ -519,6 +525,16 @@ class Gguf:
         if status != OK:
             self._fail(status)
 
+    def check_decoder_layer(self, layer: int) -> None:
+        status = self.lib.adi_hip_gguf_check_decoder_layer(self.handle, layer)
+        if status != OK:
+            self._fail(status)
+
+    def check_head(self) -> None:
+        status = self.lib.adi_hip_gguf_check_head(self.handle)
+        if status != OK:
+            self._fail(status)
+
 
 @dataclass
 class GgufMoeLayer:
@@ -574,6 +590,64 @@ class GgufEmbedding:
             self.close()
         except Exception:
             pass
+
+
+@dataclass
+class GgufDecoderLayer:
+    """A whole decoder layer uploaded from a checkpoint (norms, attention,
+    MoE block); owns its adi_hip_weights."""
+    struct: DecoderLayerStruct
+    weights: int
+    lib: object = None
+
+    def close(self) -> None:
+        if self.weights:
+            self.lib.adi_hip_weights_destroy(vp(self.weights))
+            self.weights = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def upload_decoder_layer_gguf(ctx: Context, file: Gguf, layer: int, expert_book: int,
+                              ne_book: int) -> GgufDecoderLayer:
+    weights = vp()
+    s = DecoderLayerStruct()
+    ctx.check(ctx.lib.adi_hip_gguf_upload_decoder_layer(ctx.handle, file.handle, layer, vp(expert_book),
+                                                        vp(ne_book), C.byref(weights), C.byref(s)))
+    return GgufDecoderLayer(s, weights.value, ctx.lib)
+
+
+@dataclass
+class GgufHead:
+    """The output head (eight chunks end to end) and the final norm uploaded
+    from a checkpoint; owns its adi_hip_weights."""
+    struct: HeadChunk
+    final_norm: int
+    weights: int
+    lib: object = None
+
+    def close(self) -> None:
+        if self.weights:
+            self.lib.adi_hip_weights_destroy(vp(self.weights))
+            self.weights = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def upload_head_gguf(ctx: Context, file: Gguf) -> GgufHead:
+    weights, norm = vp(), vp()
+    s = HeadChunk()
+    ctx.check(ctx.lib.adi_hip_gguf_upload_head(ctx.handle, file.handle, C.byref(weights), C.byref(s),
+                                               C.byref(norm)))
+    return GgufHead(s, norm.value, weights.value, ctx.lib)
 
 
 def upload_embedding_gguf(ctx: Context, file: Gguf) -> GgufEmbedding:

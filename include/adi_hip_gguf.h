@@ -1,7 +1,8 @@
 /*
  * adi_hip_gguf.h -- the checkpoint side of the packed path: a GGUF v3 reader
- * and the upload of a layer's packed MoE tensors and of the embedding table
- * into the device descriptors of adi_hip.h.
+ * and the upload of a layer's packed MoE tensors, of whole decoder layers, of
+ * the output head and of the embedding table into the device descriptors of
+ * adi_hip.h.
  *
  * The reference maps the checkpoint with adi::GgufFile (include/adi/gguf.hpp,
  * src/gguf.cpp) and reads the packed tensors as non-owning host views in
@@ -22,6 +23,12 @@
  *   hf.model.language_model.layers.{layer}.mlp.shared_expert_gate.weight  bf16 {hidden, 1}
  *   mach.tlut.expert.tlut  f32 {8, 32768};  mach.tlut.ne.tlut  f32 {2, 512}
  *   mach.embedding.{q_packed|mn|mx|exc_idx|exc_bits}
+ *   hf.model.language_model.layers.{layer}.{input_layernorm|post_attention_layernorm}.weight,
+ *   .self_attn.{q|k|v|o}_proj.weight (NE), .self_attn.{q|k}_norm.weight,
+ *   .linear_attn.{in_proj_qkv|in_proj_z|out_proj}.weight (NE),
+ *   .linear_attn.{in_proj_a|in_proj_b|conv1d|norm}.weight, .linear_attn.{dt_bias|A_log}
+ *   mach.output.{chunk}.LMHEADCHUNK:{begin}:{end}|{qp|gscale|prot_rows|prot_dense},
+ *   hf.model.language_model.norm.weight
  *
  * File-level calls take no context: their failures leave a message for
  * adi_hip_gguf_error() (per calling thread). Upload calls take a context and
@@ -157,6 +164,41 @@ int adi_hip_gguf_upload_embedding(adi_hip_context *ctx, const adi_hip_gguf *file
                                   adi_hip_weights **weights, adi_hip_embedding *descriptor);
 /* The same checks on the host, without uploading. */
 int adi_hip_gguf_check_embedding(const adi_hip_gguf *file);
+
+/* The decoder layer around the MoE block (MachModel::cache_descriptors,
+ * src/model.cpp:619-683, with the shapes and values validate_manifest checks,
+ * src/model.cpp:808-880): hf.{prefix}input_layernorm.weight and
+ * post_attention_layernorm.weight bf16 {hidden}; every fourth layer ((layer +
+ * 1) % 4 == 0) self_attn.{q,k,v,o}_proj.weight as NE matrices of 8192, 512,
+ * 512 rows x hidden and hidden x 4096, with q_norm and k_norm bf16 {256};
+ * the others linear_attn.in_proj_qkv (8192 x hidden), in_proj_z (4096 x
+ * hidden), out_proj (hidden x 4096) as NE matrices, in_proj_a and in_proj_b
+ * bf16 {hidden, 32}, conv1d bf16 {4, 1, 8192}, dt_bias and A_log bf16 {32},
+ * norm bf16 {128}. NE matrices as mach.ne.{layer}.{prefix}{name}|{trellis|SU|
+ * SV|Wscale} (src/model.cpp:267-314). The check runs on the host; the upload
+ * also checks the MoE block (as adi_hip_gguf_upload_moe_layer), copies the
+ * whole layer into one allocation and fills every part of *descriptor. */
+int adi_hip_gguf_check_decoder_layer(const adi_hip_gguf *file, uint32_t layer);
+int adi_hip_gguf_upload_decoder_layer(adi_hip_context *ctx, const adi_hip_gguf *file, uint32_t layer,
+                                      const adi_hip_codebook *expert_codebook,
+                                      const adi_hip_codebook *ne_codebook, adi_hip_weights **weights,
+                                      adi_hip_decoder_layer *descriptor);
+
+/* The int5 output head and the final norm (MachModel::head_chunk,
+ * src/model.cpp:367-420, final_norm_, src/model.cpp:604): eight chunks of
+ * vocabulary / 8 rows, mach.output.{c}.LMHEADCHUNK:{begin}:{end}|qp i8
+ * {hidden/8*5, rows} and |gscale f16 {hidden/64, rows} (finite), optionally
+ * |prot_rows i32 {n} with |prot_dense bf16 {hidden, n} (both or neither; rows
+ * inside their chunk; finite); hf.model.language_model.norm.weight bf16
+ * {hidden}. The vocabulary and hidden width are the embedding's
+ * (mach.embedding.q_packed; this build takes any vocabulary divisible by 8,
+ * where the reference accepts 248,320 only). The upload lays the chunks end
+ * to end as one head of vocabulary rows, protected rows renumbered to it
+ * (the logits are the chunks' in order), and returns the final norm's device
+ * copy in *final_norm. */
+int adi_hip_gguf_check_head(const adi_hip_gguf *file);
+int adi_hip_gguf_upload_head(adi_hip_context *ctx, const adi_hip_gguf *file, adi_hip_weights **weights,
+                             adi_hip_head_chunk *head, const uint16_t **final_norm);
 
 #ifdef __cplusplus
 }

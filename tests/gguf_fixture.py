@@ -112,15 +112,28 @@ def moe_metadata(layers: int, hidden: int, expert_hidden: int, experts: int,
     return [(k, t, v) for k, (t, v) in entries.items()]
 
 
-def moe_tensors(layers) -> List[Tuple[str, int, List[int], bytes]]:
+def ne_tensors(layer_index: int, source: str, m) -> List[Tuple[str, int, List[int], bytes]]:
+    """One NE matrix (adi_amd.synthetic.NeMatrix) as
+    mach.ne.{layer}.{source}|{trellis|SU|SV|Wscale} (src/model.cpp:267-314)."""
+    base = f"mach.ne.{layer_index}.{source}|"
+    tiles = (m.rows // 16) * (m.columns // 16)
+    return [(base + "trellis", T_I16, [64, tiles], np.asarray(m.trellis, np.uint16).tobytes()),
+            (base + "SU", T_I8, [m.columns], np.asarray(m.su, np.int8).tobytes()),
+            (base + "SV", T_I8, [m.rows], np.asarray(m.sv, np.int8).tobytes()),
+            (base + "Wscale", T_F32, [1], np.array([m.weight_scale], np.float32).tobytes())]
+
+
+def moe_tensors(layers, indices=None) -> List[Tuple[str, int, List[int], bytes]]:
     """The mach.*, hf.* and TLUT tensors of synthetic MoE layers
-    (adi_amd.synthetic.MoeLayer), all sharing layer 0's TLUTs."""
+    (adi_amd.synthetic.MoeLayer), all sharing the first layer's TLUTs; layer
+    i is written as checkpoint layer indices[i] (default i)."""
     first = layers[0]
     out = [
         ("mach.tlut.expert.tlut", T_F32, [8, 32768], np.asarray(first.expert_tlut, np.float32).tobytes()),
         ("mach.tlut.ne.tlut", T_F32, [2, 512], np.asarray(first.ne_tlut, np.float32).tobytes()),
     ]
-    for li, layer in enumerate(layers):
+    indices = list(range(len(layers))) if indices is None else indices
+    for li, layer in zip(indices, layers):
         H, I, E = layer.hidden, layer.expert_hidden, layer.experts
         p = f"model.language_model.layers.{li}."
         out.append((f"hf.{p}mlp.gate.weight", T_BF16, [H, E], np.asarray(layer.router_bf16, np.uint16).tobytes()))
@@ -142,12 +155,54 @@ def moe_tensors(layers) -> List[Tuple[str, int, List[int], bytes]]:
                 out.append((base + "wave_gamma", T_F16, [gammas, 32],
                             np.concatenate([m.wave_gamma_f16 for m in part]).astype(np.uint16).tobytes()))
         for name, m in (("gate", layer.shared_gate), ("up", layer.shared_up), ("down", layer.shared_down)):
-            base = f"mach.ne.{li}.{p}mlp.shared_expert.{name}_proj.weight|"
-            tiles = (m.rows // 16) * (m.columns // 16)
-            out.append((base + "trellis", T_I16, [64, tiles], np.asarray(m.trellis, np.uint16).tobytes()))
-            out.append((base + "SU", T_I8, [m.columns], np.asarray(m.su, np.int8).tobytes()))
-            out.append((base + "SV", T_I8, [m.rows], np.asarray(m.sv, np.int8).tobytes()))
-            out.append((base + "Wscale", T_F32, [1], np.array([m.weight_scale], np.float32).tobytes()))
+            out += ne_tensors(li, f"{p}mlp.shared_expert.{name}_proj.weight", m)
+    return out
+
+
+def attention_tensors(layer_index: int, d) -> List[Tuple[str, int, List[int], bytes]]:
+    """The norms and attention tensors of a synthetic decoder layer
+    (adi_amd.synthetic.DecoderLayer) at checkpoint layer `layer_index`, named
+    as MachModel::cache_descriptors reads them (src/model.cpp:619-683)."""
+    p = f"model.language_model.layers.{layer_index}."
+    bf = lambda name, dims, a: ("hf." + name, T_BF16, dims, np.asarray(a, np.uint16).tobytes())
+    H = d.moe.hidden
+    out = [bf(p + "input_layernorm.weight", [H], d.input_norm),
+           bf(p + "post_attention_layernorm.weight", [H], d.post_attention_norm)]
+    if d.full is not None:
+        a = p + "self_attn."
+        for name, m in (("q_proj", d.full.query), ("k_proj", d.full.key), ("v_proj", d.full.value),
+                        ("o_proj", d.full.output)):
+            out += ne_tensors(layer_index, a + name + ".weight", m)
+        out += [bf(a + "q_norm.weight", [256], d.full.query_norm),
+                bf(a + "k_norm.weight", [256], d.full.key_norm)]
+    else:
+        a = p + "linear_attn."
+        L = d.linear
+        for name, m in (("in_proj_qkv", L.qkv), ("in_proj_z", L.gate), ("out_proj", L.output)):
+            out += ne_tensors(layer_index, a + name + ".weight", m)
+        out += [bf(a + "in_proj_a.weight", [H, 32], L.alpha), bf(a + "in_proj_b.weight", [H, 32], L.beta),
+                bf(a + "conv1d.weight", [4, 1, 8192], L.convolution), bf(a + "dt_bias", [32], L.alpha_bias),
+                bf(a + "A_log", [32], L.a_log), bf(a + "norm.weight", [128], L.norm)]
+    return out
+
+
+def head_tensors(chunks, final_norm) -> List[Tuple[str, int, List[int], bytes]]:
+    """Eight output-head chunks (adi_amd.synthetic.HeadChunk, chunk-local
+    protected rows) and the final norm, as MachModel::head_chunk and
+    final_norm_ read them (src/model.cpp:367-420, 604)."""
+    out = []
+    rows = chunks[0].rows
+    for c, h in enumerate(chunks):
+        p = f"mach.output.{c}.LMHEADCHUNK:{c * rows}:{(c + 1) * rows}|"
+        out.append((p + "qp", T_I8, [h.columns // 8 * 5, h.rows], np.asarray(h.packed, np.uint8).tobytes()))
+        out.append((p + "gscale", T_F16, [h.columns // 64, h.rows],
+                    np.asarray(h.group_scale_f16, np.uint16).tobytes()))
+        if h.protected_rows is not None and h.protected_rows.size:
+            n = int(h.protected_rows.size)
+            out.append((p + "prot_rows", T_I32, [n], np.asarray(h.protected_rows, np.uint32).tobytes()))
+            out.append((p + "prot_dense", T_BF16, [h.columns, n], np.asarray(h.protected_bf16, np.uint16).tobytes()))
+    out.append(("hf.model.language_model.norm.weight", T_BF16, [chunks[0].columns],
+                np.asarray(final_norm, np.uint16).tobytes()))
     return out
 
 

@@ -334,3 +334,104 @@ def test_malformed_embedding_is_rejected(tmp_path, layers, name, make, match):
             f.check_embedding()
         assert info.value.status == hip.INVALID_ARGUMENT
         assert match in str(info.value), str(info.value)
+
+
+# ---- decoder layers and the output head ----------------------------------------
+
+def decoder_checkpoint_tensors(hidden=256, vocabulary=1024):
+    """Checkpoint layers 0 (Gated DeltaNet) and 3 (full attention) of a
+    four-layer model, with the embedding, the eight head chunks (protected
+    rows in two of them) and the final norm."""
+    rng = syn.rng_for(9, 40)
+    etlut, ntlut = syn.expert_tlut(rng), syn.ne_tlut(rng)
+    layers = {i: syn.decoder_layer(syn.rng_for(9, 41 + i), (i + 1) % 4 == 0, hidden, 64, 32, etlut, ntlut)
+              for i in (0, 3)}
+    chunks = [syn.head_chunk(syn.rng_for(9, 50 + c), vocabulary // 8, hidden, protected=3 if c in (2, 7) else 0)
+              for c in range(8)]
+    norm = syn.bf16_bits_rne(rng.normal(0.0, 0.1, hidden).astype(np.float32))
+    md = gf.moe_metadata(4, hidden, 64, 32)
+    ts = gf.moe_tensors([layers[0].moe, layers[3].moe], indices=[0, 3])
+    for i in (0, 3):
+        ts += gf.attention_tensors(i, layers[i])
+    ts += gf.embedding_tensors(syn.embedding(syn.rng_for(9, 60), vocabulary, hidden, exceptions=4))
+    ts += gf.head_tensors(chunks, norm)
+    return md, ts, layers, chunks, norm
+
+
+@pytest.fixture(scope="module")
+def decoder_parts():
+    return decoder_checkpoint_tensors()[:2]
+
+
+def decoder_file(tmp_path, parts, drop=None, replace=None):
+    md, ts = parts
+    out = []
+    for t in ts:
+        if t[0] == drop:
+            continue
+        if replace is not None and t[0] in replace:
+            name, kind, dims, data = t
+            new = replace[t[0]]
+            out.append((name, new.get("type", kind), new.get("dims", dims), new.get("data", data)))
+            continue
+        out.append(t)
+    return write(tmp_path / "decoder.gguf", gf.gguf_bytes(md, out))
+
+
+def test_decoder_layer_and_head_checks(tmp_path, decoder_parts):
+    with hip.Gguf(decoder_file(tmp_path, decoder_parts)) as f:
+        f.check_decoder_layer(0)
+        f.check_decoder_layer(3)
+        with pytest.raises(hip.HipError, match="missing or invalid tensor"):
+            f.check_decoder_layer(1)  # not in this file
+        with pytest.raises(hip.HipError, match="layer index is out of range"):
+            f.check_decoder_layer(4)
+        f.check_head()
+
+
+def tensor_bytes(parts, name):
+    return next(t for t in parts[1] if t[0] == name)
+
+
+Q = "mach.ne.3.model.language_model.layers.3.self_attn.q_proj.weight|"
+QKV = "mach.ne.0.model.language_model.layers.0.linear_attn.in_proj_qkv.weight|"
+LIN = "hf.model.language_model.layers.0.linear_attn."
+
+
+@pytest.mark.parametrize("layer, change, match", [
+    (3, {"drop": Q + "SV"}, "missing or invalid tensor"),
+    (3, {"replace": {Q + "SV": {"dims": [4096], "data": b"\x01" * 4096}}}, "unexpected tensor shape"),
+    (0, {"replace": {QKV + "SU": {"data": b"\x01" * 255 + b"\x00"}}}, "invalid non-expert sign tensor"),
+    (0, {"replace": {QKV + "Wscale": {"data": np.array([-1.0], np.float32).tobytes()}}},
+     "unexpected non-expert shape"),
+    (0, {"drop": LIN + "conv1d.weight"}, "missing or invalid tensor"),
+    (0, {"replace": {LIN + "conv1d.weight": {"dims": [4, 8192]}}}, "unexpected tensor shape"),
+    (0, {"replace": {LIN + "A_log": {"data": np.full(32, 0x7F80, np.uint16).tobytes()}}}, "nonfinite tensor"),
+    (3, {"replace": {"hf.model.language_model.layers.3.self_attn.k_norm.weight":
+                     {"type": gf.T_F16}}}, "missing or invalid tensor"),
+    (3, {"drop": "hf.model.language_model.layers.3.post_attention_layernorm.weight"}, "missing or invalid tensor"),
+])
+def test_decoder_layer_rejections(tmp_path, decoder_parts, layer, change, match):
+    with hip.Gguf(decoder_file(tmp_path, decoder_parts, **change)) as f:
+        with pytest.raises(hip.HipError, match=match):
+            f.check_decoder_layer(layer)
+
+
+H2 = "mach.output.2.LMHEADCHUNK:256:384|"
+H5 = "mach.output.5.LMHEADCHUNK:640:768|"
+
+
+@pytest.mark.parametrize("change, match", [
+    ({"drop": H2 + "prot_dense"}, "incomplete protected output rows"),
+    ({"replace": {H2 + "prot_rows": {"data": np.array([0, 5, 128], np.uint32).tobytes()}}},
+     "protected output row is out of range"),
+    ({"replace": {H5 + "gscale": {"data": np.full(4 * 128, 0x7C00, np.uint16).tobytes()}}},
+     "nonfinite tensor 'output head scale'"),
+    ({"drop": H5 + "qp"}, "missing or invalid tensor"),
+    ({"drop": "hf.model.language_model.norm.weight"}, "missing or invalid tensor"),
+    ({"replace": {H5 + "qp": {"dims": [160, 64]}}}, "unexpected tensor shape"),
+])
+def test_head_rejections(tmp_path, decoder_parts, change, match):
+    with hip.Gguf(decoder_file(tmp_path, decoder_parts, **change)) as f:
+        with pytest.raises(hip.HipError, match=match):
+            f.check_head()
