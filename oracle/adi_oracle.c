@@ -1291,6 +1291,15 @@ int ao_full_attention_forward(const ao_full_attention *L, uint32_t position,
     return rc;
 }
 
+/* gated_delta_key_head (src/executor.cpp:231-240): the key head a value head
+ * reads; UINT32_MAX for an invalid geometry. */
+uint32_t ao_gated_delta_key_head(uint32_t value_head, uint32_t value_heads, uint32_t key_heads) {
+    if (key_heads == 0 || value_heads == 0 || value_heads % key_heads != 0 || value_head >= value_heads) {
+        return UINT32_MAX;
+    }
+    return value_head / (value_heads / key_heads);
+}
+
 /* src/executor.cpp:420-557, with gated_delta_recurrent (157-184) and
  * gated_delta_head (121-155) */
 int ao_linear_attention_forward(const ao_linear_attention *L, const float *input,
@@ -1346,7 +1355,7 @@ int ao_linear_attention_forward(const ao_linear_attention *L, const float *input
         const float output_scale = 1.0f / sqrtf((float)head_size);
         const float *query = convolved, *key = convolved + qk_size, *value = convolved + 2 * qk_size;
         for (uint32_t h = 0; h < value_heads; ++h) {
-            const uint32_t kh = h / (value_heads / key_heads);
+            const uint32_t kh = ao_gated_delta_key_head(h, value_heads, key_heads);
             const float *q = query + (size_t)kh * head_size;
             const float *k = key + (size_t)kh * head_size;
             const float *v = value + (size_t)h * head_size;

@@ -264,6 +264,7 @@ typedef struct {
 /* linear_attention_forward (src/executor.cpp:420-557): convolution [8192][3]
  * and recurrent [32][128][128] are the layer's state, updated in place (zero
  * for a new sequence). `lanes` is the bf16 dot order of alpha and beta. */
+uint32_t ao_gated_delta_key_head(uint32_t value_head, uint32_t value_heads, uint32_t key_heads);
 int ao_linear_attention_forward(const ao_linear_attention *layer, const float *input,
                                 float *output, float *convolution, float *recurrent,
                                 uint32_t lanes);

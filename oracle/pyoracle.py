@@ -151,6 +151,7 @@ def load_oracle() -> C.CDLL:
              C.c_float, C.c_uint32)
     _declare(lib, "ao_full_attention_forward", C.c_int, C.POINTER(FullAttention), C.c_uint32,
              f32p, f32p, f32p, f32p)
+    _declare(lib, "ao_gated_delta_key_head", C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32)
     _declare(lib, "ao_linear_attention_forward", C.c_int, C.POINTER(LinearAttention), f32p, f32p,
              f32p, f32p, C.c_uint32)
     _declare(lib, "ao_decode_layer", C.c_int, C.POINTER(DecoderLayer), C.c_uint32, f32p, f32p,

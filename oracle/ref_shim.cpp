@@ -609,4 +609,13 @@ int ref_l2_normalize(float *values, std::uint32_t count, float epsilon) {
     return guarded([&] { adi::l2_normalize({values, count}, epsilon); });
 }
 
+// gated_delta_key_head (src/executor.cpp:231-240); UINT32_MAX where it throws.
+uint32_t ref_gated_delta_key_head(uint32_t value_head, uint32_t value_heads, uint32_t key_heads) {
+    try {
+        return adi::gated_delta_key_head(value_head, value_heads, key_heads);
+    } catch (const std::exception &) {
+        return UINT32_MAX;
+    }
+}
+
 } // extern "C"

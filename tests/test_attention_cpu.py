@@ -250,3 +250,139 @@ def test_layer_rejections(oracle):
     keys = np.zeros((2, 2, 256), np.float32)
     with pytest.raises(ValueError):
         po.full_attention_forward(oracle, held, 0, np.zeros(HIDDEN, np.float32), keys, keys.copy())
+
+
+# ---- the layers' layout decisions, pinned by checks a misreading fails ------
+
+def test_value_head_to_key_head(oracle, ref):
+    """gated_delta_key_head, as the reference's own test states it
+    (tests/executor_test.cpp: value head / 2 for 32 value and 16 key heads),
+    against the compiled reference, and its rejections; the oracle's linear
+    layer calls this function for every value head."""
+    ref.ref_gated_delta_key_head.restype = po.C.c_uint32
+    ref.ref_gated_delta_key_head.argtypes = [po.C.c_uint32] * 3
+    for h in range(32):
+        assert oracle.ao_gated_delta_key_head(h, 32, 16) == h // 2
+        assert oracle.ao_gated_delta_key_head(h, 32, 16) == ref.ref_gated_delta_key_head(h, 32, 16)
+    for args in ((32, 32, 16), (0, 32, 0), (0, 0, 16), (0, 30, 16)):
+        assert oracle.ao_gated_delta_key_head(*args) == 0xFFFFFFFF == ref.ref_gated_delta_key_head(*args)
+
+
+def test_key_at_position_p_is_the_rotated_key_of_position_zero(oracle):
+    """The same input at positions 0 and p: the cached key of p is the key of
+    0 rotated pairwise (i, i + 32) for i < 32 by p / 1e7^(2i/64), the other
+    192 dimensions unchanged, the value unchanged. Rotating adjacent pairs
+    (2i, 2i + 1) instead would not match."""
+    rng = syn.rng_for(39, 0)
+    L = syn.full_attention(rng, HIDDEN, syn.ne_tlut(rng))
+    held = po.FullAttentionStruct(L)
+    x = syn.rms_normalized(syn.hidden_states(rng, 1, HIDDEN))[0]
+    for p in (1, 7, 3000):
+        keys = np.zeros((p + 1, 2, 256), np.float32)
+        values = np.zeros_like(keys)
+        po.full_attention_forward(oracle, held, 0, x, keys, values)
+        po.full_attention_forward(oracle, held, p, x, keys, values)
+        k0, kp = keys[0].astype(np.float64), keys[p].astype(np.float64)
+        theta = p / (1e7 ** (2.0 * np.arange(32) / 64.0))
+        want = k0.copy()
+        want[:, :32] = k0[:, :32] * np.cos(theta) - k0[:, 32:64] * np.sin(theta)
+        want[:, 32:64] = k0[:, 32:64] * np.cos(theta) + k0[:, :32] * np.sin(theta)
+        scale = np.abs(k0).max()
+        # the angles are float32 products p * inv_freq: ~1e-4 of slack at p = 3000
+        assert np.abs(kp - want).max() <= 2e-4 * scale, p
+        assert np.array_equal(kp[:, 64:], k0[:, 64:])
+        assert np.array_equal(values[p], values[0])
+        adjacent = k0.copy()
+        c, s = np.cos(theta), np.sin(theta)
+        adjacent[:, 0:64:2] = k0[:, 0:64:2] * c - k0[:, 1:64:2] * s
+        adjacent[:, 1:64:2] = k0[:, 1:64:2] * c + k0[:, 0:64:2] * s
+        assert np.abs(kp - adjacent).max() > 1e-2 * scale, p
+
+
+def test_gate_rows_of_one_head(oracle):
+    """Query rows hold per head 256 query then 256 gate values: negating the
+    output signs (SV) of head h's 256 gate rows at position 0 (one key, so the
+    queries do not matter) changes the output, and the change lies in the span
+    of the output projection's columns of head h; the caches are unchanged. A
+    layout that puts the gates elsewhere would change nothing (the rows would
+    be queries) or another head's columns."""
+    from dataclasses import replace
+    hidden = 2048
+    rng = syn.rng_for(39, 1)
+    L = syn.full_attention(rng, hidden, syn.ne_tlut(rng))
+    h = 5
+    sv = L.query.sv.copy()
+    sv[512 * h + 256:512 * h + 512] *= -1
+    flipped = replace(L, query=replace(L.query, sv=sv))
+    x = syn.rms_normalized(syn.hidden_states(rng, 1, hidden))[0]
+    out = []
+    caches = []
+    for layer in (L, flipped):
+        keys = np.zeros((1, 2, 256), np.float32)
+        values = np.zeros_like(keys)
+        out.append(po.full_attention_forward(oracle, po.FullAttentionStruct(layer), 0, x, keys, values)
+                   .astype(np.float64))
+        caches.append((keys, values))
+    assert np.array_equal(caches[0][0], caches[1][0]) and np.array_equal(caches[0][1], caches[1][1])
+    delta = out[1] - out[0]
+    assert np.abs(delta).max() > 1e-3 * np.abs(out[0]).max()
+
+    def head_columns(head):
+        unit = np.zeros((256, 4096), np.float32)
+        unit[np.arange(256), 256 * head + np.arange(256)] = 1.0
+        return po.ne_matmul(oracle, L.output, unit).astype(np.float64).T  # [hidden, 256]
+
+    def residual(head):
+        m = head_columns(head)
+        c, *_ = np.linalg.lstsq(m, delta, rcond=None)
+        return np.abs(m @ c - delta).max() / np.abs(delta).max()
+
+    assert residual(h) <= 1e-4
+    assert residual(h + 1) > 0.1 and residual(2 * h + 1) > 0.1
+
+
+@pytest.mark.parametrize("tap, same", [
+    (3, "current"),   # only the current input: any history gives the same step
+    (2, "previous"),  # only the previous input
+    (0, "oldest"),    # only the input three steps back
+])
+def test_single_tap_convolution(oracle, tap, same):
+    """The causal convolution's taps 0..3 weigh the inputs three, two and one
+    steps back and the current one: with one nonzero tap, two sequences that
+    agree only in the input that tap sees give the same step (recurrent state
+    cleared before it), whatever the other inputs were."""
+    rng = syn.rng_for(39, 2 + tap)
+    L = syn.linear_attention(rng, HIDDEN, syn.ne_tlut(rng))
+    conv = L.convolution.reshape(8192, 4).copy()
+    conv[:, [t for t in range(4) if t != tap]] = 0
+    L.convolution = conv.reshape(-1)
+    held = po.LinearAttentionStruct(L)
+    xs = [syn.rms_normalized(syn.hidden_states(rng, 1, HIDDEN))[0] for _ in range(8)]
+    a = [xs[0], xs[1], xs[2], xs[3]]
+    b = {"current": [xs[4], xs[5], xs[6], xs[3]],
+         "previous": [xs[4], xs[5], xs[2], xs[3]],
+         "oldest": [xs[0], xs[5], xs[6], xs[3]]}[same]
+    results = []
+    for seq in (a, b):
+        state = np.zeros(8192 * 3, np.float32)
+        rec = np.zeros(32 * 128 * 128, np.float32)
+        for x in seq[:3]:
+            po.linear_attention_forward(oracle, held, x, state, rec, isa=1)
+        rec[:] = 0.0
+        results.append(po.linear_attention_forward(oracle, held, seq[3], state, rec, isa=1))
+    assert np.array_equal(results[0].view(np.uint32), results[1].view(np.uint32))
+    # and the inputs the tap does not see do reach it when it is another tap
+    other = (tap + 2) % 4  # sees an input where the two sequences differ
+    conv2 = syn.linear_attention(syn.rng_for(39, 2 + tap), HIDDEN, L.qkv.tlut).convolution.reshape(8192, 4).copy()
+    conv2[:, [t for t in range(4) if t != other]] = 0
+    L.convolution = conv2.reshape(-1)
+    held2 = po.LinearAttentionStruct(L)
+    results = []
+    for seq in (a, b):
+        state = np.zeros(8192 * 3, np.float32)
+        rec = np.zeros(32 * 128 * 128, np.float32)
+        for x in seq[:3]:
+            po.linear_attention_forward(oracle, held2, x, state, rec, isa=1)
+        rec[:] = 0.0
+        results.append(po.linear_attention_forward(oracle, held2, seq[3], state, rec, isa=1))
+    assert not np.array_equal(results[0], results[1])
