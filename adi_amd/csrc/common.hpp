@@ -36,8 +36,12 @@ inline void require(bool condition, const char *message) {
     }
 }
 
+// A failed runtime call also leaves its error as the thread's last error,
+// which the launch checks read: consume it here, so that a failed call (an
+// allocation beyond the device's memory) does not fail the next launch.
 inline void check_hip(hipError_t error, const char *what) {
     if (error != hipSuccess) {
+        (void)hipGetLastError();
         fail(error == hipErrorOutOfMemory ? ADI_HIP_OUT_OF_MEMORY : ADI_HIP_DEVICE_ERROR,
              std::string(what) + ": " + hipGetErrorString(error));
     }

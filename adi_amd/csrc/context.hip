@@ -233,6 +233,15 @@ int adi_hip_set_fused_decode(adi_hip_context *ctx, int enabled) {
     return guarded(ctx, [&] { ctx->fused_moe = enabled != 0; });
 }
 
+int adi_hip_set_workspace_limit(adi_hip_context *ctx, size_t bytes) {
+    return guarded(ctx, [&] {
+        for (adi_hip::Workspace *w : {&ctx->workspace, &ctx->layer_workspace, &ctx->decoder_workspace,
+                                      &ctx->rope_cache}) {
+            w->limit = bytes;
+        }
+    });
+}
+
 int adi_hip_device_alloc(adi_hip_context *ctx, size_t bytes, void **out) {
     return guarded(ctx, [&] {
         require(out != nullptr, "device_alloc: null output");

@@ -28,15 +28,22 @@ struct KernelStat {
 };
 
 // Grow-only device arena; reserve() hands out 256-byte aligned slices of one
-// allocation, reset per call.
+// allocation, reset per call. `limit` caps its size (adi_hip_set_workspace_limit):
+// growth beyond it fails before anything is freed or launched.
 struct Workspace {
     void *base = nullptr;
     size_t capacity = 0;
     size_t used = 0;
+    size_t limit = SIZE_MAX;
 
     void ensure(size_t bytes) {
         if (bytes <= capacity) {
             return;
+        }
+        if (bytes > limit) {
+            fail(ADI_HIP_OUT_OF_MEMORY, "workspace of " + std::to_string(bytes) +
+                                            " bytes exceeds the context's workspace limit of " +
+                                            std::to_string(limit) + " bytes");
         }
         if (base != nullptr) {
             check_hip(hipDeviceSynchronize(), "workspace synchronize");

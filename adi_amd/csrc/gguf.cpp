@@ -846,6 +846,7 @@ adi_hip_weights *adi_hip::Upload::commit(adi_hip_context *ctx, const char *what)
     auto *w = new adi_hip_weights;
     w->device = ctx->device;
     if (hipMalloc(&w->base, total == 0 ? 256 : total) != hipSuccess) {
+        (void)hipGetLastError();
         delete w;
         fail(ADI_HIP_OUT_OF_MEMORY, std::string(what) + ": device allocation failed");
     }
@@ -1113,6 +1114,7 @@ int adi_hip_gguf_upload_embedding(adi_hip_context *ctx, const adi_hip_gguf *file
         auto *w = new adi_hip_weights;
         w->device = ctx->device;
         if (hipMalloc(&w->base, total) != hipSuccess) {
+            (void)hipGetLastError();
             delete w;
             fail(ADI_HIP_OUT_OF_MEMORY, "GGUF embedding upload: device allocation failed");
         }

@@ -115,6 +115,7 @@ SIGNATURES = [
     ("adi_hip_set_stream", C.c_int, [vp, vp]),
     ("adi_hip_synchronize", C.c_int, [vp]),
     ("adi_hip_set_fused_decode", C.c_int, [vp, C.c_int]),
+    ("adi_hip_set_workspace_limit", C.c_int, [vp, C.c_size_t]),
     ("adi_hip_set_reduction_isa", C.c_int, [vp, u32]),
     ("adi_hip_device_alloc", C.c_int, [vp, C.c_size_t, C.POINTER(vp)]),
     ("adi_hip_device_free", None, [vp, vp]),
@@ -250,6 +251,11 @@ class Context:
         """One persistent launch for a one-row MoE block (default) or the
         separate launches."""
         self.check(self.lib.adi_hip_set_fused_decode(self.handle, 1 if enabled else 0))
+
+    def set_workspace_limit(self, limit: int | None) -> None:
+        """Cap each scratch arena at `limit` bytes (None: no cap); a call that
+        would grow one beyond it fails with OUT_OF_MEMORY."""
+        self.check(self.lib.adi_hip_set_workspace_limit(self.handle, (1 << 64) - 1 if limit is None else limit))
 
     def close(self) -> None:
         if getattr(self, "handle", None):

@@ -74,6 +74,18 @@ int adi_hip_set_reduction_isa(adi_hip_context *ctx, uint32_t lanes);
  * the GPU) is reported by the next adi_hip_synchronize. */
 int adi_hip_set_fused_decode(adi_hip_context *ctx, int enabled);
 
+/* Caps each of the context's grow-on-demand scratch arenas at `bytes`
+ * (default SIZE_MAX); arenas already larger stay as they are. A call whose
+ * plan needs a larger arena fails with ADI_HIP_OUT_OF_MEMORY where the plan
+ * is made, before that arena is freed or regrown. The projection, router,
+ * routing, MoE and head entries plan before they launch anything, so their
+ * outputs are untouched; a layer entry may already have run some of its
+ * steps, as the reference's layer has when one of its steps throws. No
+ * counterpart in the reference, whose scratch is host vectors: it bounds
+ * device memory in a server and lets a caller force the allocation-failure
+ * path from the host. */
+int adi_hip_set_workspace_limit(adi_hip_context *ctx, size_t bytes);
+
 /* ---- device memory -------------------------------------------------------- */
 
 /* Device buffers for callers that build descriptors without the HIP runtime
