@@ -25,6 +25,7 @@
 //   norm_gate   per value head: RMS norm (weight offset 0) times SiLU(gate)
 // The sums run in a different order from the CPU's (wave and block
 // reductions); results agree to float rounding.
+#include "attention.hpp"
 #include "dense.hpp"
 
 #include <algorithm>
@@ -50,6 +51,22 @@ constexpr uint32_t kChannels = 2 * kQkSize + kValueSize;   // 8192
 constexpr uint32_t kDeltaRows = 16;                        // state rows per block
 
 constexpr float kEpsilon = 1.0e-6f;
+
+// Sequences per launch of the per-sequence kernels of a decode step over
+// many sequences; their state pointers and positions travel as kernel
+// arguments.
+constexpr uint32_t kRowGroup = 32;
+
+struct FullRows {
+    float *keys[kRowGroup];
+    float *values[kRowGroup];
+    uint32_t position[kRowGroup];
+};
+
+struct LinearRows {
+    float *convolution[kRowGroup];
+    float *recurrent[kRowGroup];
+};
 
 struct RopeTable {
     float cosine[kRopeHalf];
@@ -91,18 +108,40 @@ __device__ __forceinline__ float block_sum(float v, float *partial) {
 __device__ __forceinline__ float silu_of(float v) { return v / (1.0f + expf(-v)); }
 __device__ __forceinline__ float sigmoid_of(float v) { return 1.0f / (1.0f + expf(-v)); }
 
-// normalize_head then apply_rope (src/executor.cpp:25-41, 60-72, 376-390):
-// block (h, b) of token b: h 0-15 the query heads (stride 512), 16-17 the new
-// key heads. One token takes the host's table `rope`; in a chunk, token b
-// reads the host-computed table of position + b from `rope_rows`
-// ([position][32 cosines, 32 sines]), so every token of a chunk rotates
-// exactly as it would alone (the reference builds its prefill table on the
-// host too, src/executor.cpp:1853-1866).
+// normalize_head then apply_rope (src/executor.cpp:25-41, 60-72, 376-390)
+// of one 256-value head by a block of kHeadSize threads: RMS norm with
+// (1 + w), then thread t < 32 rotates the pair (t, t + 32) by its cosine and
+// sine. src and dst may be the same.
+__device__ __forceinline__ void norm_rope_head(const float *src, float *dst, const uint16_t *w,
+                                               float cosine, float sine, float *partial,
+                                               float *head) {
+#pragma clang fp contract(off)
+    const uint32_t t = threadIdx.x;
+    float x = src[t];
+    const float squares = block_sum(x * x, partial);
+    const float scale = 1.0f / sqrtf(squares / static_cast<float>(kHeadSize) + kEpsilon);
+    x *= scale * (1.0f + bf16_bits_to_float(w[t]));
+    head[t] = x;
+    __syncthreads();
+    if (t < kRopeHalf) {
+        const float first = head[t], second = head[t + kRopeHalf];
+        dst[t] = first * cosine - second * sine;
+        dst[t + kRopeHalf] = second * cosine + first * sine;
+    } else if (t >= 2 * kRopeHalf) {
+        dst[t] = x;
+    }
+}
+
+// Block (h, b) of token b of a chunk: h 0-15 the query heads (stride 512),
+// 16-17 the new key heads, in place. One token takes the host's table `rope`;
+// in a chunk, token b reads the host-computed table of position + b from
+// `rope_rows` ([position][32 cosines, 32 sines]), so every token of a chunk
+// rotates exactly as it would alone (the reference builds its prefill table
+// on the host too, src/executor.cpp:1853-1866).
 __global__ __launch_bounds__(kHeadSize) void k_norm_rope(float *query_gate, float *key,
                                                          const uint16_t *query_norm,
                                                          const uint16_t *key_norm, RopeTable rope,
                                                          const float *rope_rows, uint32_t position) {
-#pragma clang fp contract(off)
     __shared__ float partial[16];
     __shared__ float head[kHeadSize];
     const uint32_t h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
@@ -110,25 +149,55 @@ __global__ __launch_bounds__(kHeadSize) void k_norm_rope(float *query_gate, floa
     key += static_cast<size_t>(b) * kKvHeads * kHeadSize;
     float *v = h < kQueryHeads ? query_gate + static_cast<size_t>(h) * kQueryStride
                                : key + static_cast<size_t>(h - kQueryHeads) * kHeadSize;
-    const uint16_t *w = h < kQueryHeads ? query_norm : key_norm;
-    float x = v[t];
-    const float squares = block_sum(x * x, partial);
-    const float scale = 1.0f / sqrtf(squares / static_cast<float>(kHeadSize) + kEpsilon);
-    x *= scale * (1.0f + bf16_bits_to_float(w[t]));
-    head[t] = x;
-    __syncthreads();
+    float cosine = 0.0f, sine = 0.0f;
     if (t < kRopeHalf) {
-        float cosine = rope.cosine[t], sine = rope.sine[t];
+        cosine = rope.cosine[t];
+        sine = rope.sine[t];
         if (rope_rows != nullptr) {
             const float *row = rope_rows + static_cast<size_t>(position + b) * (2 * kRopeHalf);
             cosine = row[t];
             sine = row[kRopeHalf + t];
         }
-        const float first = head[t], second = head[t + kRopeHalf];
-        v[t] = first * cosine - second * sine;
-        v[t + kRopeHalf] = second * cosine + first * sine;
-    } else if (t >= 2 * kRopeHalf) {
-        v[t] = x;
+    }
+    norm_rope_head(v, v, h < kQueryHeads ? query_norm : key_norm, cosine, sine, partial, head);
+}
+
+// The same for one decode token of each of up to kRowGroup sequences: block
+// (h, r), h 0-15 the query heads of row r (in place), 16-17 its key heads,
+// normalized and rotated into the sequence's cache entry rows.position[r],
+// and 18-19 its value heads, copied into that entry. The RoPE table row is
+// the row's position.
+__global__ __launch_bounds__(kHeadSize) void k_norm_rope_rows(float *query_gate, const float *key,
+                                                              const float *value,
+                                                              const uint16_t *query_norm,
+                                                              const uint16_t *key_norm,
+                                                              const float *rope_rows, FullRows rows) {
+    __shared__ float partial[16];
+    __shared__ float head[kHeadSize];
+    const uint32_t h = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
+    const uint32_t position = rows.position[r];
+    const size_t entry = static_cast<size_t>(position) * kKvHeads * kHeadSize;
+    if (h >= kQueryHeads + kKvHeads) {  // uniform over the block
+        const uint32_t kv = h - kQueryHeads - kKvHeads;
+        rows.values[r][entry + kv * kHeadSize + t] =
+            value[(static_cast<size_t>(r) * kKvHeads + kv) * kHeadSize + t];
+        return;
+    }
+    float cosine = 0.0f, sine = 0.0f;
+    if (t < kRopeHalf) {
+        const float *row = rope_rows + static_cast<size_t>(position) * (2 * kRopeHalf);
+        cosine = row[t];
+        sine = row[kRopeHalf + t];
+    }
+    if (h < kQueryHeads) {
+        float *q = query_gate + static_cast<size_t>(r) * kQueryHeads * kQueryStride +
+                   static_cast<size_t>(h) * kQueryStride;
+        norm_rope_head(q, q, query_norm, cosine, sine, partial, head);
+    } else {
+        const uint32_t kv = h - kQueryHeads;
+        norm_rope_head(key + (static_cast<size_t>(r) * kKvHeads + kv) * kHeadSize,
+                       rows.keys[r] + entry + kv * kHeadSize, key_norm, cosine, sine, partial,
+                       head);
     }
 }
 
@@ -154,24 +223,20 @@ __device__ __forceinline__ void online_step(float score, float4 value, float &ma
     maximum = score;
 }
 
-// Block (query head, split, token b): cache entries [split * chunk, ...) up
-// to token b's own position of the head's KV stream, wave w taking every
-// fourth. Lane l holds dimensions 4l..4l+3. Writes the split's accumulator,
-// maximum and denominator (maximum -inf and denominator 0 when the split
-// lies past the token).
-__global__ __launch_bounds__(256) void k_attention_partial(const float *query_gate,
-                                                           const float *keys, const float *values,
-                                                           uint32_t position, uint32_t chunk,
-                                                           float *partial) {
+// Block (query head, split) of one token's query row: cache entries
+// [split * chunk, ...) below `tokens` of the head's KV stream, wave w taking
+// every fourth. Lane l holds dimensions 4l..4l+3. Writes the split's
+// accumulator, maximum and denominator to the token's partial rows
+// (maximum -inf and denominator 0 when the split lies past the token).
+__device__ __forceinline__ void attention_partial_span(const float *query_gate, const float *keys,
+                                                       const float *values, uint32_t tokens,
+                                                       uint32_t chunk, float *partial) {
 #pragma clang fp contract(off)
     __shared__ __align__(16) float wave_acc[4][kHeadSize];
     __shared__ float wave_max[4], wave_den[4];
-    const uint32_t h = blockIdx.x, split = blockIdx.y, splits = gridDim.y, b = blockIdx.z;
+    const uint32_t h = blockIdx.x, split = blockIdx.y, splits = gridDim.y;
     const uint32_t kv = h / (kQueryHeads / kKvHeads);
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t tokens = position + b + 1;
-    query_gate += static_cast<size_t>(b) * kQueryHeads * kQueryStride;
-    partial += static_cast<size_t>(b) * kQueryHeads * splits * kPartialStride;
     const float4 q = reinterpret_cast<const float4 *>(query_gate + static_cast<size_t>(h) * kQueryStride)[lane];
     const float score_scale = 1.0f / 16.0f;  // 1 / sqrt(256)
     const uint32_t begin = split * chunk;
@@ -209,6 +274,28 @@ __global__ __launch_bounds__(256) void k_attention_partial(const float *query_ga
         out[kHeadSize] = m;
         out[kHeadSize + 1] = d;
     }
+}
+
+// Token b of a chunk at `position` sees entries 0 .. position + b.
+__global__ __launch_bounds__(256) void k_attention_partial(const float *query_gate,
+                                                           const float *keys, const float *values,
+                                                           uint32_t position, uint32_t chunk,
+                                                           float *partial) {
+    const uint32_t b = blockIdx.z;
+    attention_partial_span(query_gate + static_cast<size_t>(b) * kQueryHeads * kQueryStride, keys,
+                           values, position + b + 1, chunk,
+                           partial + static_cast<size_t>(b) * kQueryHeads * gridDim.y * kPartialStride);
+}
+
+// Row r of a decode step over sequences sees its own cache's entries
+// 0 .. rows.position[r], split evenly over the grid's splits.
+__global__ __launch_bounds__(256) void k_attention_partial_rows(const float *query_gate,
+                                                                FullRows rows, float *partial) {
+    const uint32_t r = blockIdx.z;
+    const uint32_t tokens = rows.position[r] + 1;
+    attention_partial_span(query_gate + static_cast<size_t>(r) * kQueryHeads * kQueryStride,
+                           rows.keys[r], rows.values[r], tokens, (tokens + gridDim.y - 1u) / gridDim.y,
+                           partial + static_cast<size_t>(r) * kQueryHeads * gridDim.y * kPartialStride);
 }
 
 // Per query head: the splits merged, divided by the denominator, times the
@@ -254,17 +341,18 @@ __global__ __launch_bounds__(kHeadSize) void k_attention_combine(const float *pa
     attended[static_cast<size_t>(h) * kHeadSize + t] = a * (1.0f / d) * sigmoid_of(gate);
 }
 
-// The causal convolution of 128 channels for token b (src/executor.cpp:
-// 480-496) and, for the query and key groups (blocks 0-31), their L2 norm
-// (497-505). The three inputs before token b are the chunk's earlier qkv rows
-// or, before the chunk, the state. With one token the state shifts here;
-// for a chunk k_conv_history does it after every token has read it.
-__global__ __launch_bounds__(kLinearHead) void k_linear_conv(const float *qkv,
-                                                             const uint16_t *weights,
-                                                             float *state, float *convolved) {
+// The causal convolution of 128 channels for token b of a chunk
+// (src/executor.cpp:480-496) and, for the query and key groups (blocks
+// 0-31), their L2 norm (497-505). The three inputs before token b are the
+// chunk's earlier qkv rows or, before the chunk, the state. With `shift` (one
+// token) the state shifts here; for a chunk k_conv_history does it after
+// every token has read it.
+__device__ __forceinline__ void linear_conv_token(const float *qkv, const uint16_t *weights,
+                                                  float *state, float *convolved, uint32_t b,
+                                                  bool shift) {
 #pragma clang fp contract(off)
     __shared__ float partial[16];
-    const uint32_t c = blockIdx.x * kLinearHead + threadIdx.x, b = blockIdx.y;
+    const uint32_t c = blockIdx.x * kLinearHead + threadIdx.x;
     float *history = state + static_cast<size_t>(c) * 3u;
     const uint2 packed = *reinterpret_cast<const uint2 *>(weights + static_cast<size_t>(c) * 4u);
     const float w0 = bf16_bits_to_float(packed.x & 0xFFFFu), w1 = bf16_bits_to_float(packed.x >> 16);
@@ -283,7 +371,7 @@ __global__ __launch_bounds__(kLinearHead) void k_linear_conv(const float *qkv,
     v += h2 * w2;
     v += x * w3;
     float y = silu_of(v);
-    if (gridDim.y == 1) {
+    if (shift) {
         history[0] = h1;
         history[1] = h2;
         history[2] = x;
@@ -293,6 +381,23 @@ __global__ __launch_bounds__(kLinearHead) void k_linear_conv(const float *qkv,
         y *= 1.0f / sqrtf(squares + kEpsilon);
     }
     convolved[static_cast<size_t>(b) * kChannels + c] = y;
+}
+
+__global__ __launch_bounds__(kLinearHead) void k_linear_conv(const float *qkv,
+                                                             const uint16_t *weights,
+                                                             float *state, float *convolved) {
+    linear_conv_token(qkv, weights, state, convolved, blockIdx.y, gridDim.y == 1);
+}
+
+// One decode token of each of up to kRowGroup sequences: row r convolves
+// with its own state, which shifts.
+__global__ __launch_bounds__(kLinearHead) void k_linear_conv_rows(const float *qkv,
+                                                                  const uint16_t *weights,
+                                                                  LinearRows rows,
+                                                                  float *convolved) {
+    const uint32_t r = blockIdx.y;
+    linear_conv_token(qkv + static_cast<size_t>(r) * kChannels, weights, rows.convolution[r],
+                      convolved + static_cast<size_t>(r) * kChannels, 0, true);
 }
 
 // The convolution state after a chunk of `count` tokens: the last three of
@@ -318,14 +423,14 @@ __global__ __launch_bounds__(256) void k_conv_history(const float *qkv, uint32_t
 }
 
 // gated_delta_head (src/executor.cpp:121-155) for state rows [16 y, 16 y +
-// 16) of value head x over the chunk's `count` tokens in order: each wave
-// keeps four rows in registers through the chunk, a lane holding two of a
-// row's 128 values (src/simd.cpp:108-127); the state is read and written once
-// per chunk.
-__global__ __launch_bounds__(256) void k_gated_delta(const float *convolved, const float *alpha,
-                                                     const float *beta, const uint16_t *alpha_bias,
-                                                     const uint16_t *a_log, uint32_t count,
-                                                     float *recurrent, float *output) {
+// 16) of value head x over `count` tokens in order: each wave keeps four
+// rows in registers through them, a lane holding two of a row's 128 values
+// (src/simd.cpp:108-127); the state is read and written once.
+__device__ __forceinline__ void gated_delta_rows_of_head(const float *convolved, const float *alpha,
+                                                         const float *beta,
+                                                         const uint16_t *alpha_bias,
+                                                         const uint16_t *a_log, uint32_t count,
+                                                         float *recurrent, float *output) {
 #pragma clang fp contract(off)
     constexpr uint32_t kRows = kDeltaRows / 4u;
     const uint32_t h = blockIdx.x;
@@ -370,6 +475,28 @@ __global__ __launch_bounds__(256) void k_gated_delta(const float *convolved, con
     for (uint32_t j = 0; j < kRows; ++j) {
         state[j * (kLinearHead / 2u) + lane] = s[j];
     }
+}
+
+// Block (value head, row block) over the chunk's `count` tokens.
+__global__ __launch_bounds__(256) void k_gated_delta(const float *convolved, const float *alpha,
+                                                     const float *beta, const uint16_t *alpha_bias,
+                                                     const uint16_t *a_log, uint32_t count,
+                                                     float *recurrent, float *output) {
+    gated_delta_rows_of_head(convolved, alpha, beta, alpha_bias, a_log, count, recurrent, output);
+}
+
+// Block (value head, row block, r): one token of sequence r with its own
+// recurrent state.
+__global__ __launch_bounds__(256) void k_gated_delta_rows(const float *convolved,
+                                                          const float *alpha, const float *beta,
+                                                          const uint16_t *alpha_bias,
+                                                          const uint16_t *a_log, LinearRows rows,
+                                                          float *output) {
+    const uint32_t r = blockIdx.z;
+    gated_delta_rows_of_head(convolved + static_cast<size_t>(r) * kChannels,
+                             alpha + static_cast<size_t>(r) * kValueHeads,
+                             beta + static_cast<size_t>(r) * kValueHeads, alpha_bias, a_log, 1,
+                             rows.recurrent[r], output + static_cast<size_t>(r) * kValueSize);
 }
 
 // rms_norm (weight offset 0, src/kernels.cpp:1052-1073) of each value head,
@@ -590,7 +717,182 @@ void decoder_chunk(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_
            static_cast<const float *>(branch), static_cast<uint32_t>(rows));
 }
 
+// full_attention_forward_batch (src/executor.cpp:561-731) for one decode
+// token of each of `rows` sequences: row r is at positions[r] of the
+// sequence whose cache is states[r]. The projections run batched over the
+// rows; normalization, RoPE, the cache append and the attention run per
+// sequence, kRowGroup sequences per launch.
+void full_attention_rows(adi_hip_context *ctx, const adi_hip_full_attention *L, uint32_t rows,
+                         const float *inputs, float *outputs,
+                         const adi_hip_layer_state *const *states, const uint32_t *positions) {
+    require(L != nullptr && inputs != nullptr && outputs != nullptr && states != nullptr &&
+                positions != nullptr && rows > 0,
+            "full attention batch shape mismatch");
+    const uint32_t hidden = L->query.columns;
+    require(ne_shaped(L->query, kQueryHeads * kQueryStride, hidden) &&
+                ne_shaped(L->key, kKvHeads * kHeadSize, hidden) &&
+                ne_shaped(L->value, kKvHeads * kHeadSize, hidden) &&
+                ne_shaped(L->output, hidden, kQueryHeads * kHeadSize) &&
+                L->query_norm != nullptr && L->key_norm != nullptr,
+            "full attention batch shape mismatch");
+    uint32_t last = 0;
+    for (uint32_t r = 0; r < rows; ++r) {
+        const adi_hip_layer_state *st = states[r];
+        require(st != nullptr && st->keys != nullptr && st->values != nullptr &&
+                    positions[r] < st->capacity,
+                "full attention batch state mismatch");
+        require(aligned_to(st->keys, 16) && aligned_to(st->values, 16),
+                "attention caches must be 16-byte aligned");
+        last = positions[r] + 1 > last ? positions[r] + 1 : last;
+    }
+    auto &ws = ctx->layer_workspace;
+    ws.used = 0;
+    const uint32_t cap = kMaxSplits / rows > 0 ? kMaxSplits / rows : 1u;
+    uint32_t splits = ceil_div(last, 32);
+    splits = splits < 1 ? 1 : (splits > cap ? cap : splits);
+    const size_t n = rows;
+    ws.ensure(Workspace::round(n * kQueryHeads * kQueryStride * 4) +
+              Workspace::round(n * kKvHeads * kHeadSize * 4) * 2 +
+              Workspace::round(n * kQueryHeads * kHeadSize * 4) +
+              Workspace::round(n * kQueryHeads * splits * kPartialStride * 4));
+    float *query_gate = ws.take<float>(n * kQueryHeads * kQueryStride);
+    float *key = ws.take<float>(n * kKvHeads * kHeadSize);
+    float *value = ws.take<float>(n * kKvHeads * kHeadSize);
+    float *attended = ws.take<float>(n * kQueryHeads * kHeadSize);
+    float *partial = ws.take<float>(n * kQueryHeads * splits * kPartialStride);
+    forward(ctx, adi_hip_ne_matmul(ctx, &L->query, inputs, rows, query_gate));
+    forward(ctx, adi_hip_ne_matmul(ctx, &L->key, inputs, rows, key));
+    forward(ctx, adi_hip_ne_matmul(ctx, &L->value, inputs, rows, value));
+    const float *rope = rope_rows(ctx, last);
+    for (uint32_t first = 0; first < rows; first += kRowGroup) {
+        const uint32_t count = rows - first < kRowGroup ? rows - first : kRowGroup;
+        FullRows table{};
+        for (uint32_t i = 0; i < count; ++i) {
+            table.keys[i] = states[first + i]->keys;
+            table.values[i] = states[first + i]->values;
+            table.position[i] = positions[first + i];
+        }
+        float *qg = query_gate + static_cast<size_t>(first) * kQueryHeads * kQueryStride;
+        launch(ctx, "attention_norm_rope_rows", k_norm_rope_rows,
+               dim3(kQueryHeads + 2 * kKvHeads, count), dim3(kHeadSize), 0, qg,
+               static_cast<const float *>(key + static_cast<size_t>(first) * kKvHeads * kHeadSize),
+               static_cast<const float *>(value + static_cast<size_t>(first) * kKvHeads * kHeadSize),
+               L->query_norm, L->key_norm, rope, table);
+        launch(ctx, "attention_partial_rows", k_attention_partial_rows,
+               dim3(kQueryHeads, splits, count), dim3(256), 0, static_cast<const float *>(qg), table,
+               partial + static_cast<size_t>(first) * kQueryHeads * splits * kPartialStride);
+    }
+    launch(ctx, "attention_combine", k_attention_combine, dim3(kQueryHeads, rows), dim3(kHeadSize),
+           0, static_cast<const float *>(partial), splits, static_cast<const float *>(query_gate),
+           attended);
+    forward(ctx, adi_hip_ne_matmul(ctx, &L->output, attended, rows, outputs));
+}
+
+// linear_attention_forward_batch (src/executor.cpp:733-966) for one decode
+// token of each of `rows` sequences with the states states[r]: projections
+// batched, convolution and recurrence per sequence.
+void linear_attention_rows(adi_hip_context *ctx, const adi_hip_linear_attention *L, uint32_t rows,
+                           const float *inputs, float *outputs,
+                           const adi_hip_layer_state *const *states) {
+    require(L != nullptr && inputs != nullptr && outputs != nullptr && states != nullptr &&
+                rows > 0,
+            "linear attention batch shape mismatch");
+    const uint32_t hidden = L->qkv.columns;
+    require(ne_shaped(L->qkv, kChannels, hidden) && ne_shaped(L->gate, kValueSize, hidden) &&
+                ne_shaped(L->output, hidden, kValueSize),
+            "linear attention batch shape mismatch");
+    require(L->alpha.rows == kValueHeads && L->alpha.columns == hidden &&
+                L->beta.rows == kValueHeads && L->beta.columns == hidden &&
+                L->alpha.values != nullptr && L->beta.values != nullptr &&
+                L->alpha_bias != nullptr && L->a_log != nullptr,
+            "linear attention decay shape mismatch");
+    require(L->convolution != nullptr && aligned_to(L->convolution, 8),
+            "linear attention convolution shape mismatch");
+    require(L->norm != nullptr, "linear attention batch shape mismatch");
+    for (uint32_t r = 0; r < rows; ++r) {
+        const adi_hip_layer_state *st = states[r];
+        require(st != nullptr && st->convolution != nullptr && st->recurrent != nullptr,
+                "linear attention recurrent state mismatch");
+        require(aligned_to(st->recurrent, 8), "linear attention state must be 8-byte aligned");
+    }
+    auto &ws = ctx->layer_workspace;
+    ws.used = 0;
+    const size_t n = rows;
+    ws.ensure(Workspace::round(n * kChannels * 4) * 2 + Workspace::round(n * kValueSize * 4) * 3 +
+              Workspace::round(n * kValueHeads * 4) * 2);
+    float *qkv = ws.take<float>(n * kChannels);
+    float *convolved = ws.take<float>(n * kChannels);
+    float *gate = ws.take<float>(n * kValueSize);
+    float *recurrent_output = ws.take<float>(n * kValueSize);
+    float *normalized = ws.take<float>(n * kValueSize);
+    float *alpha = ws.take<float>(n * kValueHeads);
+    float *beta = ws.take<float>(n * kValueHeads);
+    forward(ctx, adi_hip_ne_matmul(ctx, &L->qkv, inputs, rows, qkv));
+    forward(ctx, adi_hip_ne_matmul(ctx, &L->gate, inputs, rows, gate));
+    forward(ctx, adi_hip_bf16_matmul(ctx, &L->alpha, inputs, rows, alpha));
+    forward(ctx, adi_hip_bf16_matmul(ctx, &L->beta, inputs, rows, beta));
+    for (uint32_t first = 0; first < rows; first += kRowGroup) {
+        const uint32_t count = rows - first < kRowGroup ? rows - first : kRowGroup;
+        LinearRows table{};
+        for (uint32_t i = 0; i < count; ++i) {
+            table.convolution[i] = states[first + i]->convolution;
+            table.recurrent[i] = states[first + i]->recurrent;
+        }
+        const size_t at = static_cast<size_t>(first);
+        launch(ctx, "linear_conv_rows", k_linear_conv_rows, dim3(kChannels / kLinearHead, count),
+               dim3(kLinearHead), 0, static_cast<const float *>(qkv + at * kChannels),
+               L->convolution, table, convolved + at * kChannels);
+        launch(ctx, "gated_delta_rows", k_gated_delta_rows,
+               dim3(kValueHeads, kLinearHead / kDeltaRows, count), dim3(256), 0,
+               static_cast<const float *>(convolved + at * kChannels),
+               static_cast<const float *>(alpha + at * kValueHeads),
+               static_cast<const float *>(beta + at * kValueHeads), L->alpha_bias, L->a_log, table,
+               recurrent_output + at * kValueSize);
+    }
+    launch(ctx, "linear_norm_gate", k_linear_norm_gate, dim3(kValueHeads, rows), dim3(kLinearHead),
+           0, static_cast<const float *>(recurrent_output), L->norm,
+           static_cast<const float *>(gate), normalized);
+    forward(ctx, adi_hip_ne_matmul(ctx, &L->output, normalized, rows, outputs));
+}
+
 }  // namespace
+
+void decoder_rows(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_t rows,
+                  float *hidden, const adi_hip_layer_state *const *states,
+                  const uint32_t *positions) {
+    require(L != nullptr && hidden != nullptr && states != nullptr && positions != nullptr &&
+                L->input_norm != nullptr && L->post_attention_norm != nullptr && rows > 0,
+            "decoder batch shape mismatch");
+    const uint32_t n = L->moe.hidden;
+    require(n > 0 && aligned_to(hidden, 16), "decoder hidden row must be 16-byte aligned");
+    auto &ws = ctx->decoder_workspace;
+    ws.used = 0;
+    const size_t all = size_t(rows) * n;
+    ws.ensure(Workspace::round(all * 4) * 2);
+    float *normalized = ws.take<float>(all);
+    float *branch = ws.take<float>(all);
+    const dim3 grid(ceil_div(all, 256));
+    forward(ctx, adi_hip_rms_norm(ctx, hidden, L->input_norm, n, rows, 1.0f, 1.0e-6f, normalized));
+    if (L->full_attention != 0) {
+        full_attention_rows(ctx, &L->full, rows, normalized, branch, states, positions);
+    } else {
+        linear_attention_rows(ctx, &L->linear, rows, normalized, branch, states);
+    }
+    launch(ctx, "residual_add", k_residual_add, grid, dim3(256), 0, hidden,
+           static_cast<const float *>(branch), static_cast<uint32_t>(all));
+    forward(ctx, adi_hip_rms_norm(ctx, hidden, L->post_attention_norm, n, rows, 1.0f, 1.0e-6f,
+                                  normalized));
+    forward(ctx, adi_hip_moe_forward(ctx, &L->moe, normalized, rows, nullptr, branch, nullptr,
+                                     nullptr));
+    launch(ctx, "residual_add", k_residual_add, grid, dim3(256), 0, hidden,
+           static_cast<const float *>(branch), static_cast<uint32_t>(all));
+}
+
+void prefill_chunk(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_t position,
+                   uint32_t count, float *hidden, const adi_hip_layer_state *state) {
+    decoder_chunk(ctx, L, position, count, hidden, state);
+}
+
 }  // namespace adi_hip
 
 using namespace adi_hip;

@@ -83,6 +83,9 @@ struct adi_hip_context {
     adi_hip::Workspace layer_workspace;
     // scratch of the decoder-layer entry, which calls the attention entries
     adi_hip::Workspace decoder_workspace;
+    // scratch of the model-level entries (decode steps, prefill), which call
+    // the decoder layers
+    adi_hip::Workspace sequence_workspace;
     // RoPE cos/sin of positions 0 .. rope_positions - 1 ([position][cos 32,
     // sin 32] floats), computed on the host and grown on demand
     adi_hip::Workspace rope_cache;

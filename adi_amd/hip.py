@@ -21,6 +21,7 @@ OK = 0
 INVALID_ARGUMENT = -1
 OUT_OF_MEMORY = -2
 DEVICE_ERROR = -3
+OUT_OF_RANGE = -4
 NOT_FOUND = -4
 
 GGML_F32, GGML_F16, GGML_I8, GGML_I16, GGML_I32, GGML_I64, GGML_F64, GGML_BF16 = 0, 1, 24, 25, 26, 27, 28, 30
@@ -87,6 +88,16 @@ class DecoderLayerStruct(C.Structure):
 class LayerState(C.Structure):
     _fields_ = [("keys", C.c_void_p), ("values", C.c_void_p), ("capacity", C.c_uint32),
                 ("convolution", C.c_void_p), ("recurrent", C.c_void_p)]
+
+
+class ModelStruct(C.Structure):
+    _fields_ = [("layers", u32), ("layer", C.POINTER(DecoderLayerStruct)),
+                ("embedding", C.POINTER(Embedding)), ("final_norm", vp), ("head_chunks", u32),
+                ("head", C.POINTER(HeadChunk)), ("context", u32)]
+
+
+class DecoderStateStruct(C.Structure):
+    _fields_ = [("position", u32), ("layers", C.POINTER(LayerState))]
 
 
 class KernelProfile(C.Structure):
@@ -156,6 +167,10 @@ SIGNATURES = [
      [vp, C.POINTER(LinearAttentionStruct), u32, vp, vp, vp, vp]),
     ("adi_hip_prefill_layer", C.c_int,
      [vp, C.POINTER(DecoderLayerStruct), u32, u32, vp, C.POINTER(LayerState)]),
+    ("adi_hip_decode_batch", C.c_int,
+     [vp, C.POINTER(ModelStruct), C.POINTER(u32), u32, C.POINTER(DecoderStateStruct), vp]),
+    ("adi_hip_prefill", C.c_int,
+     [vp, C.POINTER(ModelStruct), C.POINTER(u32), u32, u32, C.POINTER(DecoderStateStruct), vp]),
     ("adi_hip_profiling_enable", C.c_int, [vp, C.c_int]),
     ("adi_hip_profiling_read", C.c_int, [vp, C.POINTER(KernelProfile), u32, C.POINTER(u32)]),
     # include/adi_hip_gguf.h
@@ -916,3 +931,73 @@ def prefill_layer(ctx: Context, layer: DeviceDecoderLayer, position: int, count:
                   state) -> None:
     ctx.check(load().adi_hip_prefill_layer(ctx.handle, C.byref(layer.struct), position, count,
                                            _addr(hidden), C.byref(state)))
+
+
+# ---- the whole model: decode steps over sequences, prompt prefill -----------
+
+CONTEXT = 262144  # ModelConfig::context of the checkpoint
+
+
+class Model:
+    """adi_hip_model over uploaded parts: decoder layers (DeviceDecoderLayer or
+    GgufDecoderLayer), an embedding, the final norm (device bf16 tensor) and
+    head chunks (DeviceHead or GgufHead), whose rows in order cover the
+    vocabulary."""
+
+    def __init__(self, layers, embedding, final_norm, heads, context: int = CONTEXT):
+        self.layers = list(layers)
+        self.embedding, self.final_norm, self.heads = embedding, final_norm, list(heads)
+        self._layer_array = (DecoderLayerStruct * len(self.layers))(*(L.struct for L in self.layers))
+        self._head_array = (HeadChunk * len(self.heads))(*(h.struct for h in self.heads))
+        self.struct = ModelStruct(len(self.layers), self._layer_array, C.pointer(embedding.struct),
+                                  _addr(final_norm), len(self.heads), self._head_array, context)
+        self.vocabulary = int(embedding.struct.rows)
+        self.hidden = int(embedding.struct.columns)
+
+    def full_attention(self, layer: int) -> bool:
+        return bool(self.layers[layer].struct.full_attention)
+
+
+class Sequence:
+    """A sequence's decoder state on the device: position and one
+    LayerState per layer of `model`, zeroed (a new sequence); full-attention
+    caches hold `capacity` positions."""
+
+    def __init__(self, model: Model, capacity: int):
+        made = [layer_state(model.full_attention(i), capacity) for i in range(len(model.layers))]
+        self.tensors = [keep for _, keep in made]
+        self._layers = (LayerState * len(made))(*(state for state, _ in made))
+        self.struct = DecoderStateStruct(0, self._layers)
+        self.capacity = capacity
+
+    @property
+    def position(self) -> int:
+        return int(self.struct.position)
+
+    def reset(self) -> None:
+        for keep in self.tensors:
+            for t in keep:
+                t.zero_()
+        self.struct.position = 0
+
+
+def decode_batch(ctx: Context, model: Model, tokens, sequences, logits=None) -> None:
+    """One decode step of each sequence with its token (host ints): logits
+    [len(sequences), vocabulary] (device tensor or None); positions advance."""
+    n = len(sequences)
+    toks = (u32 * max(n, 1))(*[int(t) for t in tokens])
+    states = (DecoderStateStruct * max(n, 1))(*(s.struct for s in sequences))
+    status = ctx.lib.adi_hip_decode_batch(ctx.handle, C.byref(model.struct), toks, n, states,
+                                          _addr(logits))
+    for s, st in zip(sequences, states):
+        s.struct.position = st.position
+    ctx.check(status)
+
+
+def prefill(ctx: Context, model: Model, tokens, sequence: Sequence, logits=None,
+            ubatch: int = 0) -> None:
+    """prefill_prompt of `tokens` (host ints) into the sequence, chunks of
+    `ubatch` (0: 128); logits [vocabulary] of the last token (device) or None."""
+    toks = (u32 * max(len(tokens), 1))(*[int(t) for t in tokens])
+    ctx.check(ctx.lib.adi_hip_prefill(ctx.handle, C.byref(model.struct), toks, len(tokens), ubatch,
+                                      C.byref(sequence.struct), _addr(logits)))

@@ -351,6 +351,19 @@ def median_seconds(torch, fn, steps, runs, warm=3):
     return float(np.median(times))
 
 
+def kernel_us(ctx, fn, calls):
+    """Mean device time of one call of fn: the sum of its kernels' own
+    start/stop events (the context's profiling mode) over `calls` calls. A
+    Python loop issues about one small call per 15 us, so a call shorter than
+    that is host-bound in wall time; this figure is the GPU's part."""
+    ctx.profiling(True)
+    for i in range(calls):
+        fn(i)
+    prof = ctx.profile()
+    ctx.profiling(False)
+    return sum(ms for _, ms in prof.values()) / calls * 1e3
+
+
 def projections(torch, hip, ctx, steps, runs):
     from adi_amd import synthetic as syn
     res = {}
@@ -360,12 +373,15 @@ def projections(torch, hip, ctx, steps, runs):
     for batch in (1, 4):
         x = ctx.to_device(syn.rms_normalized(syn.hidden_states(rng, batch, HEAD_COLUMNS)))
         out = torch.empty((batch, HEAD_ROWS), dtype=torch.float32, device="cuda")
-        dt = median_seconds(torch, lambda i: hip.head_matmul(ctx, heads[i % copies], x, batch, out),
-                            steps, runs)
+        call = lambda i: hip.head_matmul(ctx, heads[i % copies], x, batch, out)
+        dt = median_seconds(torch, call, steps, runs)
+        us = kernel_us(ctx, call, steps)
         res[f"head_151936x2048_b{batch}"] = {
             "ms_per_call": round(dt * 1e3, 4), "vectors_per_s": round(batch / dt, 1),
             "packed_gbs": round(HEAD_BYTES / dt / 1e9, 1),
-            "hbm_frac": round(HEAD_BYTES / dt / 1e9 / HBM_PEAK_GBS, 4)}
+            "hbm_frac": round(HEAD_BYTES / dt / 1e9 / HBM_PEAK_GBS, 4),
+            "kernel_us_per_call": round(us, 2),
+            "kernel_hbm_frac": round(HEAD_BYTES / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     del heads
     tlut = syn.ne_tlut(rng)
     book = ctx.ne_codebook(tlut)
@@ -382,10 +398,13 @@ def projections(torch, hip, ctx, steps, runs):
         call = lambda i: ctx.check(ctx.lib.adi_hip_ne_matmul(
             ctx.handle, hip.C.byref(mats[i % count]), x.data_ptr(), batch, out.data_ptr()))
         dt = median_seconds(torch, call, max(steps, count), runs)
+        us = kernel_us(ctx, call, max(steps, count))
         res[f"ne_2048x2048_b{batch}"] = {
             "ms_per_call": round(dt * 1e3, 4), "vectors_per_s": round(batch / dt, 1),
             "packed_gbs": round(nbytes / dt / 1e9, 1),
-            "hbm_frac": round(nbytes / dt / 1e9 / HBM_PEAK_GBS, 4)}
+            "hbm_frac": round(nbytes / dt / 1e9 / HBM_PEAK_GBS, 4),
+            "kernel_us_per_call": round(us, 2),
+            "kernel_hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     res.update(decode_side(torch, hip, ctx, steps))
     res.update(attention_side(torch, hip, ctx, steps))
     return res

@@ -36,6 +36,7 @@ extern "C" {
 #define ADI_HIP_INVALID_ARGUMENT (-1) /* reference: std::invalid_argument */
 #define ADI_HIP_OUT_OF_MEMORY (-2)
 #define ADI_HIP_DEVICE_ERROR (-3)     /* a HIP runtime call failed */
+#define ADI_HIP_OUT_OF_RANGE (-4)     /* reference: std::out_of_range */
 
 typedef struct adi_hip_context adi_hip_context;
 typedef struct adi_hip_codebook adi_hip_codebook;
@@ -468,6 +469,63 @@ int adi_hip_decode_layer(adi_hip_context *ctx, const adi_hip_decoder_layer *laye
 int adi_hip_prefill_layer(adi_hip_context *ctx, const adi_hip_decoder_layer *layer,
                           uint32_t position, uint32_t count, float *hidden,
                           const adi_hip_layer_state *state);
+
+/* ---- the whole model: decode steps over sequences, prompt prefill -------- */
+
+/* The parts of adi::MachModel (include/adi/model.hpp) that decoding uses, in
+ * device memory: the decoder layers (host array of descriptors), the
+ * embedding (its rows are the vocabulary, its columns the hidden size), the
+ * final RMS norm (hidden bf16) and the head chunks (host array; their rows,
+ * in order, cover the vocabulary). `context` is the model's context length
+ * (ModelConfig::context, 262,144 for the checkpoint). */
+typedef struct {
+    uint32_t layers;
+    const adi_hip_decoder_layer *layer;
+    const adi_hip_embedding *embedding;
+    const uint16_t *final_norm;
+    uint32_t head_chunks;
+    const adi_hip_head_chunk *head;
+    uint32_t context;
+} adi_hip_model;
+
+/* adi::DecoderState (include/adi/executor.hpp:86-90): the sequence's
+ * position (tokens decoded so far) and its state for each layer (host array
+ * of `layers` entries). A full-attention layer's cache must hold every
+ * position the calls below reach (capacity > position); a new sequence has
+ * position 0 and zero linear-attention states. */
+typedef struct {
+    uint32_t position;
+    const adi_hip_layer_state *layers;
+} adi_hip_decoder_state;
+
+/* decode_batch (src/executor.cpp:1592-1825): one decode step of `batch`
+ * sequences, token tokens[b] (HOST) of sequence states[b] (HOST array):
+ * embedding rows, every layer with the norms, projections and MoE batched
+ * over the sequences and the attention per sequence at its own position,
+ * the final norm, and the head into logits[b][vocabulary] (DEVICE; NULL
+ * skips the norm and head, as decode_token with empty logits). Each
+ * position advances by one. Rejected before anything runs, states untouched:
+ * batch 0 or NULL arrays ("decoder batch shape mismatch"), a token >= the
+ * vocabulary ("decoder batch token is out of range") with
+ * ADI_HIP_INVALID_ARGUMENT; a position >= context ("decoder context is
+ * exhausted") with ADI_HIP_OUT_OF_RANGE; a missing layer state or a full
+ * cache with ADI_HIP_INVALID_ARGUMENT. decode_token (src/executor.cpp:
+ * 1565-1590) is this call with batch 1. */
+int adi_hip_decode_batch(adi_hip_context *ctx, const adi_hip_model *model, const uint32_t *tokens,
+                         uint32_t batch, adi_hip_decoder_state *states, float *logits);
+
+/* prefill_prompt (src/generation.cpp:131-159) over prefill (src/executor.cpp:
+ * 1827-2101): `count` prompt tokens (HOST) of one sequence in chunks of
+ * `ubatch` tokens (0: 128; ExecutionOptions::prefill_ubatch, 1..4096), each
+ * chunk through every layer with adi_hip_prefill_layer's arithmetic, then
+ * the last token's final norm and head into logits[vocabulary] (DEVICE;
+ * NULL skips them). The position advances by count. Rejected before
+ * anything runs: count 0 or a prompt past the context ("prefill shape or
+ * context is invalid"), a token >= the vocabulary ("prefill token is out of
+ * range"), ubatch > 4096, a missing layer state or a cache too small for the
+ * prompt, all ADI_HIP_INVALID_ARGUMENT. */
+int adi_hip_prefill(adi_hip_context *ctx, const adi_hip_model *model, const uint32_t *tokens,
+                    uint32_t count, uint32_t ubatch, adi_hip_decoder_state *state, float *logits);
 
 /* ---- kernel profiling ----------------------------------------------------- */
 

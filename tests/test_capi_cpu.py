@@ -30,6 +30,8 @@ STRUCTS = {
     "adi_hip_linear_attention": hip.LinearAttentionStruct,
     "adi_hip_decoder_layer": hip.DecoderLayerStruct,
     "adi_hip_layer_state": hip.LayerState,
+    "adi_hip_model": hip.ModelStruct,
+    "adi_hip_decoder_state": hip.DecoderStateStruct,
 }
 
 
