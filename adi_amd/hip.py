@@ -28,6 +28,7 @@ GGML_F32, GGML_F16, GGML_I8, GGML_I16, GGML_I32, GGML_I64, GGML_F64, GGML_BF16 =
 
 vp = C.c_void_p
 u32 = C.c_uint32
+u64 = C.c_uint64
 f32 = C.c_float
 
 
@@ -98,6 +99,21 @@ class ModelStruct(C.Structure):
 
 class DecoderStateStruct(C.Structure):
     _fields_ = [("position", u32), ("layers", C.POINTER(LayerState))]
+
+
+class BatcherOptions(C.Structure):
+    _fields_ = [("max_batch", u32), ("capacity", u32), ("prefill_ubatch", u32),
+                ("stop_tokens", C.POINTER(u32)), ("stop_count", u32),
+                ("masked_tokens", C.POINTER(u32)), ("masked_count", u32)]
+
+
+class GenerationOptions(C.Structure):
+    _fields_ = [("max_output_tokens", u32), ("temperature", f32), ("top_p", f32), ("seed", u64)]
+
+
+class RequestStatus(C.Structure):
+    _fields_ = [("state", u32), ("input_tokens", u32), ("output_tokens", u32),
+                ("prefill_seconds", C.c_double), ("decode_seconds", C.c_double)]
 
 
 class KernelProfile(C.Structure):
@@ -171,6 +187,16 @@ SIGNATURES = [
      [vp, C.POINTER(ModelStruct), C.POINTER(u32), u32, C.POINTER(DecoderStateStruct), vp]),
     ("adi_hip_prefill", C.c_int,
      [vp, C.POINTER(ModelStruct), C.POINTER(u32), u32, u32, C.POINTER(DecoderStateStruct), vp]),
+    ("adi_hip_batcher_create", C.c_int,
+     [vp, C.POINTER(ModelStruct), C.POINTER(BatcherOptions), C.POINTER(vp)]),
+    ("adi_hip_batcher_destroy", None, [vp]),
+    ("adi_hip_batcher_submit", C.c_int,
+     [vp, C.POINTER(u32), u32, C.POINTER(GenerationOptions), C.POINTER(u64)]),
+    ("adi_hip_batcher_cancel", C.c_int, [vp, u64]),
+    ("adi_hip_batcher_step", C.c_int, [vp, C.POINTER(u32)]),
+    ("adi_hip_batcher_status", C.c_int, [vp, u64, C.POINTER(RequestStatus), C.POINTER(u32), u32]),
+    ("adi_hip_batcher_request_error", C.c_char_p, [vp, u64]),
+    ("adi_hip_batcher_release", C.c_int, [vp, u64]),
     ("adi_hip_profiling_enable", C.c_int, [vp, C.c_int]),
     ("adi_hip_profiling_read", C.c_int, [vp, C.POINTER(KernelProfile), u32, C.POINTER(u32)]),
     # include/adi_hip_gguf.h

@@ -527,6 +527,92 @@ int adi_hip_decode_batch(adi_hip_context *ctx, const adi_hip_model *model, const
 int adi_hip_prefill(adi_hip_context *ctx, const adi_hip_model *model, const uint32_t *tokens,
                     uint32_t count, uint32_t ubatch, adi_hip_decoder_state *state, float *logits);
 
+/* ---- continuous batching (serving) --------------------------------------- */
+
+/* ContinuousBatcher (src/generation.cpp:343-660) without the tokenizer:
+ * requests are prompt token ids, outputs are token ids. One call of
+ * adi_hip_batcher_step is one iteration of the reference's worker loop
+ * (generation.cpp:540-646): admit the oldest pending request (prefill of its
+ * prompt into a free sequence slot, the logits row of its last token), then
+ * for every active sequence in order: fail it if cancelled, sample its next
+ * token from its logits row (temperature and top_p of the request, the draw
+ * from the request's std::mt19937_64 seeded with its seed; the device
+ * sampler of adi_hip_sample_rows, or the greedy choice at temperature 0),
+ * finish it on a stop token (not kept) or at its output limit, and decode
+ * the survivors' tokens in one adi_hip_decode_batch step. The caller drives
+ * the loop (a serving thread calls step while work remains); submit, cancel,
+ * status and release may come from other threads, while the context belongs
+ * to the stepping thread. Sequence state for max_batch slots of `capacity`
+ * positions is allocated at creation; a request waits while every slot is
+ * busy (the reference admits without a bound). */
+typedef struct adi_hip_batcher adi_hip_batcher;
+
+typedef struct {
+    uint32_t max_batch;             /* sequence slots (1..256) */
+    uint32_t capacity;              /* positions per sequence; the context a request may use */
+    uint32_t prefill_ubatch;        /* 0: 128 */
+    const uint32_t *stop_tokens;    /* HOST; the tokenizer's eos and <|im_end|> */
+    uint32_t stop_count;
+    const uint32_t *masked_tokens;  /* HOST; Tokenizer::mask_unused_logits: set to the lowest float */
+    uint32_t masked_count;
+} adi_hip_batcher_options;
+
+/* adi::GenerationOptions (include/adi/generation.hpp:17-22); 0 output
+ * tokens means "up to the context". */
+typedef struct {
+    uint32_t max_output_tokens;
+    float temperature;
+    float top_p;
+    uint64_t seed;
+} adi_hip_generation_options;
+
+#define ADI_HIP_REQUEST_PENDING 0
+#define ADI_HIP_REQUEST_RUNNING 1
+#define ADI_HIP_REQUEST_STOP_TOKEN 2 /* FinishReason::stop_token */
+#define ADI_HIP_REQUEST_LENGTH 3     /* FinishReason::length */
+#define ADI_HIP_REQUEST_FAILED 4     /* the request's exception; message in adi_hip_batcher_request_error */
+
+/* adi::GenerationResult (include/adi/generation.hpp:29-38) of a request so
+ * far: its state, prompt and output token counts, and the prefill and decode
+ * wall times in seconds. */
+typedef struct {
+    uint32_t state;
+    uint32_t input_tokens;
+    uint32_t output_tokens;
+    double prefill_seconds;
+    double decode_seconds;
+} adi_hip_request_status;
+
+/* Copies the model descriptor (its arrays too) and the options; the model's
+ * device memory must outlive the batcher. Rejects max_batch outside 1..256,
+ * capacity 0 or above the model's context, a stop or masked token outside
+ * the vocabulary. */
+int adi_hip_batcher_create(adi_hip_context *ctx, const adi_hip_model *model,
+                           const adi_hip_batcher_options *options, adi_hip_batcher **out);
+void adi_hip_batcher_destroy(adi_hip_batcher *batcher);
+/* Queues a request (validate_generation_options, generation.cpp:93-110:
+ * "max_output_tokens must be positive" is not possible here, 0 meaning
+ * unbounded; above the context "max_output_tokens exceeds model context";
+ * "invalid generation options"). `request` receives its id (from 1). */
+int adi_hip_batcher_submit(adi_hip_batcher *batcher, const uint32_t *prompt, uint32_t count,
+                           const adi_hip_generation_options *options, uint64_t *request);
+/* Marks a request cancelled: the next step fails it ("generation
+ * cancelled") whether pending or active. */
+int adi_hip_batcher_cancel(adi_hip_batcher *batcher, uint64_t request);
+/* One iteration of the loop; `remaining` (may be NULL) receives the number
+ * of requests pending or active afterwards. A failure of the decode step
+ * fails every active request and is returned. */
+int adi_hip_batcher_step(adi_hip_batcher *batcher, uint32_t *remaining);
+/* The request's status and up to `capacity` of its output tokens (HOST,
+ * may be NULL). */
+int adi_hip_batcher_status(adi_hip_batcher *batcher, uint64_t request,
+                           adi_hip_request_status *status, uint32_t *tokens, uint32_t capacity);
+/* The failure message of a failed request ("" otherwise); valid until the
+ * request is released. */
+const char *adi_hip_batcher_request_error(adi_hip_batcher *batcher, uint64_t request);
+/* Forgets a finished or failed request. */
+int adi_hip_batcher_release(adi_hip_batcher *batcher, uint64_t request);
+
 /* ---- kernel profiling ----------------------------------------------------- */
 
 /* Per-kernel timing with HIP events on the context stream, the counterpart

@@ -789,6 +789,33 @@ static int by_key_then_index(const void *a, const void *b) {
     return x < y ? -1 : (x > y ? 1 : 0);
 }
 
+void ao_mt19937_64(uint64_t seed, uint32_t count, uint64_t *out) {
+    enum { N = 312, M = 156 };
+    const uint64_t upper = 0xFFFFFFFF80000000ull, lower = 0x7FFFFFFFull;
+    uint64_t mt[N];
+    mt[0] = seed;
+    for (uint32_t i = 1; i < N; ++i) {
+        mt[i] = 6364136223846793005ull * (mt[i - 1] ^ (mt[i - 1] >> 62)) + i;
+    }
+    uint32_t index = N;
+    for (uint32_t k = 0; k < count; ++k) {
+        if (index == N) {
+            for (uint32_t i = 0; i < N; ++i) {
+                const uint64_t x = (mt[i] & upper) | (mt[(i + 1) % N] & lower);
+                const uint64_t shifted = (x >> 1) ^ ((x & 1u) ? 0xB5026F5AA96619E9ull : 0u);
+                mt[i] = mt[(i + M) % N] ^ shifted;
+            }
+            index = 0;
+        }
+        uint64_t y = mt[index++];
+        y ^= (y >> 29) & 0x5555555555555555ull;
+        y ^= (y << 17) & 0x71D67FFFEDA60000ull;
+        y ^= (y << 37) & 0xFFF7EEE000000000ull;
+        y ^= y >> 43;
+        out[k] = y;
+    }
+}
+
 int ao_sample_token(const float *logits, uint32_t count, float temperature, float top_p,
                     uint64_t word, uint32_t *token) {
     if (!logits || !token || count == 0 || !isfinite(temperature) || !isfinite(top_p) ||

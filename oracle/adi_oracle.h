@@ -200,6 +200,15 @@ uint32_t ao_argmax(const float *logits, uint32_t count);
 int ao_sample_token(const float *logits, uint32_t count, float temperature, float top_p,
                     uint64_t word, uint32_t *token);
 
+/* The first `count` outputs of std::mt19937_64 seeded with `seed` (the
+ * engine ContinuousBatcher and generate give each request,
+ * src/generation.cpp:270, 495): the 64-bit Mersenne Twister with the
+ * parameters of C++11 [rand.predef] (n 312, m 156, r 31, a
+ * 0xB5026F5AA96619E9, tempering u 29 d 0x5555555555555555, s 17 b
+ * 0x71D67FFFEDA60000, t 37 c 0xFFF7EEE000000000, l 43, initialisation
+ * multiplier 6364136223846793005). */
+void ao_mt19937_64(uint64_t seed, uint32_t count, uint64_t *out);
+
 /* ---- attention of one decode token (src/executor.cpp:25-186, 332-557,
  * src/attention.cpp) -------------------------------------------------------- */
 

@@ -141,6 +141,7 @@ def load_oracle() -> C.CDLL:
     _declare(lib, "ao_argmax", C.c_uint32, f32p, C.c_uint32)
     _declare(lib, "ao_fnv1a64", C.c_uint64, C.c_uint64, C.c_void_p, C.c_size_t)
     _declare(lib, "ao_sample_token", C.c_int, f32p, C.c_uint32, C.c_float, C.c_float, C.c_uint64, u32p)
+    _declare(lib, "ao_mt19937_64", None, C.c_uint64, C.c_uint32, C.POINTER(C.c_uint64))
     _declare(lib, "ao_normalize_head", C.c_int, f32p, u16p, C.c_uint32, C.c_float)
     _declare(lib, "ao_rope_table", None, C.c_uint32, f32p, f32p)
     _declare(lib, "ao_apply_rope", None, f32p, f32p, f32p)
@@ -342,6 +343,13 @@ def sample_token(lib, logits: np.ndarray, temperature: float, top_p: float, word
     check(lib.ao_sample_token(ptr(logits, C.c_float), logits.size, temperature, top_p, word,
                               ptr(token, C.c_uint32)), "sample_token")
     return int(token[0])
+
+
+def mt19937_64(lib, seed: int, count: int) -> list:
+    """The first `count` outputs of std::mt19937_64(seed)."""
+    out = (C.c_uint64 * max(count, 1))()
+    lib.ao_mt19937_64(seed, count, out)
+    return [int(v) for v in out[:count]]
 
 
 def ref_gguf_summary(lib, path: str):

@@ -173,3 +173,18 @@ def test_top_p_denominator_order_bound(count):
         worst = max(worst, abs(device - reference) / reference)
     print(f"count {count}: largest relative denominator difference {worst:.3g}")
     assert worst <= (count - 1) * 2.0 ** -53
+
+
+def test_mt19937_64_known_answer_and_reference(oracle, ref):
+    """The oracle's std::mt19937_64: C++11 [rand.predef] requires the 10000th
+    output of a default-constructed engine (seed 5489) to be
+    9981545732273789042; and the first word of each seeded engine is the one
+    the compiled sample_token's engine draws first."""
+    assert po.mt19937_64(oracle, 5489, 10000)[-1] == 9981545732273789042
+    logits = np.linspace(-1.0, 1.0, 64).astype(np.float32)
+    for seed in (0, 1, 1234, 2**63 + 5):
+        _, word = po.ref_sample_token(ref, logits, 0.7, 0.9, seed)
+        assert po.mt19937_64(oracle, seed, 1)[0] == word, seed
+    # and the stream continues past the first twist (312 words)
+    words = po.mt19937_64(oracle, 42, 700)
+    assert len(set(words)) == 700

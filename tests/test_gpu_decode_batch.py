@@ -14,56 +14,19 @@ import numpy as np
 import pytest
 import torch
 
-import pyoracle as po
 from adi_amd import hip
-from adi_amd import synthetic as syn
 from conftest import max_rel_error
+import small_model
+from small_model import VOCAB
 
 pytestmark = pytest.mark.gpu
 
-HIDDEN, EXPERT_HIDDEN, EXPERTS, VOCAB, CAPACITY = 256, 64, 16, 512, 16
-
-
-def head_rows(h, first, end):
-    per_row = h.columns // 8 * 5
-    groups = h.columns // 64
-    return syn.HeadChunk(end - first, h.columns,
-                         h.packed.reshape(h.rows, per_row)[first:end].reshape(-1).copy(),
-                         h.group_scale_f16.reshape(h.rows, groups)[first:end].reshape(-1).copy())
+CAPACITY = 16
 
 
 @pytest.fixture(scope="module")
 def parts(gpu):
-    rng = syn.rng_for(70, 0)
-    etlut, ntlut = syn.expert_tlut(rng), syn.ne_tlut(rng)
-    layers = [syn.decoder_layer(rng, i % 4 == 3, HIDDEN, EXPERT_HIDDEN, EXPERTS, etlut, ntlut)
-              for i in range(4)]
-    emb = syn.embedding(rng, VOCAB, HIDDEN, exceptions=20)
-    head = syn.head_chunk(rng, VOCAB, HIDDEN)
-    final_norm = syn.bf16_bits_rne(rng.normal(0.0, 0.1, HIDDEN).astype(np.float32))
-    ebook, nbook = gpu.expert_codebook(etlut), gpu.ne_codebook(ntlut)
-    dlayers = [hip.upload_decoder_layer(gpu, L, ebook, nbook) for L in layers]
-    demb, dnorm = hip.upload_embedding(gpu, emb), gpu.to_device(final_norm)
-    one = hip.Model(dlayers, demb, dnorm, [hip.upload_head(gpu, head)])
-    two = hip.Model(dlayers, demb, dnorm, [hip.upload_head(gpu, head_rows(head, 0, 200)),
-                                           hip.upload_head(gpu, head_rows(head, 200, VOCAB))])
-    return dict(layers=layers, emb=emb, head=head, final_norm=final_norm, one=one, two=two)
-
-
-class OracleSequence:
-    def __init__(self, layers):
-        self.held = [po.DecoderLayerStruct(L, capacity=CAPACITY) for L in layers]
-        self.position = 0
-
-    def step(self, oracle, parts, token):
-        h = po.embedding_rows(oracle, parts["emb"], [token])[0].copy()
-        for held in self.held:
-            held.decode(oracle, self.position, h, isa=16)
-        self.position += 1
-        n = np.zeros(HIDDEN, np.float32)
-        assert oracle.ao_rms_norm(po.ptr(h, po.C.c_float), po.ptr(parts["final_norm"], po.C.c_uint16),
-                                  HIDDEN, 1.0, 1e-6, po.ptr(n, po.C.c_float)) == 0
-        return po.head_matmul(oracle, parts["head"], n[None, :], isa=16)[0]
+    return small_model.build(gpu)
 
 
 def close(got, want, what):
@@ -75,7 +38,7 @@ def test_decode_batch_matches_each_sequence_alone(gpu, oracle, parts, chunks):
     model = parts[chunks]
     prompts = [[], [3, 9], [5, 1, 4, 1, 5]]
     seqs = [hip.Sequence(model, CAPACITY) for _ in prompts]
-    orc = [OracleSequence(parts["layers"]) for _ in prompts]
+    orc = [small_model.OracleSequence(parts, CAPACITY) for _ in prompts]
     tokens = []
     for prompt, s, o in zip(prompts, seqs, orc):
         if not prompt:
@@ -85,7 +48,7 @@ def test_decode_batch_matches_each_sequence_alone(gpu, oracle, parts, chunks):
         logits = torch.empty(VOCAB, dtype=torch.float32, device="cuda")
         hip.prefill(gpu, model, prompt, s, logits, ubatch=2)
         for t in prompt:
-            want = o.step(oracle, parts, t)
+            want = o.step(oracle, t)
         assert max_rel_error(logits.cpu().numpy(), want) <= 1e-3
         assert s.position == len(prompt)
         tokens.append(int(np.argmax(want)))
@@ -96,7 +59,7 @@ def test_decode_batch_matches_each_sequence_alone(gpu, oracle, parts, chunks):
         got = out.cpu().numpy()
         nxt = []
         for b, o in enumerate(orc):
-            want = o.step(oracle, parts, tokens[b])
+            want = o.step(oracle, tokens[b])
             assert max_rel_error(got[b], want) <= 1e-3, (step, b)
             nxt.append(int(np.argmax(want)))
         tokens = nxt
