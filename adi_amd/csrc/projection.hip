@@ -2388,7 +2388,7 @@ int adi_hip_expert_matmul(adi_hip_context *ctx, const adi_hip_expert_matrix *m,
         validate_expert(m);
         require(batch > 0, "Mach expert batch shape mismatch");
         require(inputs != nullptr && outputs != nullptr, "Mach expert vector is null");
-        const bool mfma = batch >= kMfmaBatch && expert_mfma_supports(m->rows, m->columns) &&
+        const bool mfma = batch >= kExpertMfmaBatch && expert_mfma_supports(m->rows, m->columns) &&
                           wave_width(m->columns);
         const uint32_t splits = mfma ? 2u : expert_splits(m->columns);
         auto &ws = ctx->workspace;
@@ -2467,7 +2467,7 @@ int adi_hip_ne_matmul(adi_hip_context *ctx, const adi_hip_ne_matrix *m,
                 return;
             }
         }
-        const bool mfma = batch >= kMfmaBatch && m->columns >= 32 && wave_width(m->columns);
+        const bool mfma = batch >= kNeMfmaBatch && m->columns >= 32 && wave_width(m->columns);
         const uint32_t splits = mfma ? ne_mfma_slices(m->rows, m->columns, batch) : ne_splits(m->columns);
         auto &ws = ctx->workspace;
         ws.used = 0;

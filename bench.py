@@ -493,13 +493,16 @@ def attention_side(torch, hip, ctx, steps):
     return res
 
 
-def stack40(torch, hip, ctx, runs):
+def stack40(torch, hip, ctx, runs, sequences=16):
     """The full hybrid stack of synthetic.StackGeometry: 40 layers at hidden
     2048 (every fourth full GQA attention, the others Gated DeltaNet, each
-    with the 256-expert MoE block), the 151,936-token embedding and int5 head.
-    A 256-token prompt is prefilled in chunks of 128 (every layer per chunk),
-    then 64 greedy steps run with every token chosen and embedded on the
-    device. The weights are drawn layer by layer and uploaded (about 7 GB)."""
+    with the 256-expert MoE block), the 151,936-token embedding and int5 head,
+    driven through the model-level entry points. One sequence: a 256-token
+    prompt prefilled in chunks of 128 (adi_hip_prefill), then 64 greedy steps
+    (the device's choice read back, adi_hip_decode_batch of one sequence).
+    Then `sequences` sequences, each prefilled with the prompt, take 64
+    greedy steps together as one decode_batch per step. The weights are drawn
+    layer by layer and uploaded (about 7 GB)."""
     from adi_amd import synthetic as syn
     g = syn.StackGeometry()
     etlut, ntlut = syn.stack_codebooks()
@@ -511,52 +514,54 @@ def stack40(torch, hip, ctx, runs):
     emb, head = hip.upload_embedding(ctx, emb_host), hip.upload_head(ctx, head_host)
     final_norm = ctx.to_device(norm_host)
     del emb_host, head_host
+    model = hip.Model(layers, emb, final_norm, [head])
     capacity = g.prompt + g.greedy_steps
-    lib = hip.load()
-    tokens = torch.tensor(prompt_host.astype(np.int32), device="cuda")
-    hidden = torch.empty((g.ubatch, g.hidden), dtype=torch.float32, device="cuda")
-    normed = torch.empty((1, g.hidden), dtype=torch.float32, device="cuda")
-    logits = torch.empty((1, g.vocab), dtype=torch.float32, device="cuda")
-    token = torch.empty(1, dtype=torch.int32, device="cuda")
-    states = [hip.layer_state(g.full_attention(i), capacity) for i in range(g.layers)]
+    prompt = [int(t) for t in prompt_host]
+    logits = torch.empty((sequences, g.vocab), dtype=torch.float32, device="cuda")
+    chosen = torch.empty(sequences, dtype=torch.int32, device="cuda")
+    seqs = [hip.Sequence(model, capacity) for _ in range(sequences)]
 
-    def run():
-        for state, keep in states:
-            for t in keep:
-                t.zero_()
+    def greedy(active):
+        n = len(active)
+        for step in range(g.greedy_steps):
+            hip.argmax_rows(ctx, logits, n, g.vocab, chosen)
+            hip.decode_batch(ctx, model, chosen[:n].tolist(), active, logits)
+        torch.cuda.synchronize()
+
+    def run_one():
+        seqs[0].reset()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for c in range(0, g.prompt, g.ubatch):
-            hip.embedding_rows(ctx, emb, tokens[c:c + g.ubatch], g.ubatch, hidden)
-            for layer, (state, _) in zip(layers, states):
-                hip.prefill_layer(ctx, layer, c, g.ubatch, hidden, state)
-        last = hidden[g.ubatch - 1:g.ubatch]
+        hip.prefill(ctx, model, prompt, seqs[0], logits[0], ubatch=g.ubatch)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-        for step in range(g.greedy_steps):
-            ctx.check(lib.adi_hip_rms_norm(ctx.handle, last.data_ptr(), final_norm.data_ptr(),
-                                           g.hidden, 1, 1.0, 1e-6, normed.data_ptr()))
-            hip.head_matmul(ctx, head, normed, 1, logits)
-            hip.argmax_rows(ctx, logits, 1, g.vocab, token)
-            hip.embedding_rows(ctx, emb, token, 1, hidden)
-            last = hidden[0:1]
-            for layer, (state, _) in zip(layers, states):
-                hip.decode_layer(ctx, layer, g.prompt + step, last, state)
-        torch.cuda.synchronize()
-        t2 = time.perf_counter()
-        return t1 - t0, t2 - t1
+        greedy(seqs[:1])
+        return t1 - t0, time.perf_counter() - t1
 
-    run()  # warm-up: workspaces, kernels
-    times = [run() for _ in range(runs)]
+    def run_batch():
+        for k, s in enumerate(seqs):
+            s.reset()
+            hip.prefill(ctx, model, prompt, s, logits[k], ubatch=g.ubatch)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        greedy(seqs)
+        return time.perf_counter() - t0
+
+    run_one()  # warm-up: workspaces, kernels
+    times = [run_one() for _ in range(runs)]
     prefill_s = float(np.median([t[0] for t in times]))
     decode_s = float(np.median([t[1] for t in times]))
-    del layers, states
+    run_batch()
+    batch_s = float(np.median([run_batch() for _ in range(runs)]))
+    del layers, seqs, model
     torch.cuda.empty_cache()
     return {"stack40": {
         "prefill_tokens_per_s": round(g.prompt / prefill_s, 1),
         "prefill_ms": round(prefill_s * 1e3, 2),
         "decode_ms_per_token": round(decode_s / g.greedy_steps * 1e3, 3),
         "decode_tokens_per_s": round(g.greedy_steps / decode_s, 1),
+        f"decode_batch{sequences}_ms_per_step": round(batch_s / g.greedy_steps * 1e3, 3),
+        f"decode_batch{sequences}_tokens_per_s": round(sequences * g.greedy_steps / batch_s, 1),
         "layers": g.layers, "hidden": g.hidden, "vocab": g.vocab, "prompt": g.prompt,
         "ubatch": g.ubatch, "greedy_steps": g.greedy_steps}}
 

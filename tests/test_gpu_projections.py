@@ -52,7 +52,7 @@ def test_ne_decode_bit_exact(gpu, books, oracle, rows, columns):
 
 
 @pytest.mark.parametrize("rows,columns", EXPERT_SHAPES)
-@pytest.mark.parametrize("batch", [1, 2, 4, 5, 16, 33])
+@pytest.mark.parametrize("batch", [1, 2, 4, 5, 15, 16, 33])
 def test_expert_matmul(gpu, books, oracle, rows, columns, batch):
     et, _, eb, _ = books
     rng = syn.rng_for(0, rows + columns + batch)
@@ -65,13 +65,14 @@ def test_expert_matmul(gpu, books, oracle, rows, columns, batch):
     assert max_rel_error(out.cpu().numpy(), want) <= TOL
 
 
-# from 64 rows the projections run as MFMA GEMMs (f16 hi/lo operands, fp32
-# accumulation): the error stays near fp32 rounding, well inside 1e-3
+# from 16 rows (expert) and 8 rows (NE) a single projection runs as an MFMA
+# GEMM (f16 hi/lo operands, fp32 accumulation): the error stays near fp32
+# rounding, well inside 1e-3
 MFMA_TOL = 1e-4
 
 
 @pytest.mark.parametrize("rows,columns", [(16, 64), (64, 128), (512, 2048), (2048, 512)])
-@pytest.mark.parametrize("batch", [64, 100, 300])
+@pytest.mark.parametrize("batch", [16, 33, 64, 100, 300])
 def test_expert_matmul_mfma(gpu, books, oracle, rows, columns, batch):
     et, _, eb, _ = books
     rng = syn.rng_for(0, 5 * rows + columns + batch)
@@ -85,7 +86,7 @@ def test_expert_matmul_mfma(gpu, books, oracle, rows, columns, batch):
 
 
 @pytest.mark.parametrize("rows,columns", [(16, 32), (128, 2048), (512, 2048), (2048, 512)])
-@pytest.mark.parametrize("batch", [64, 100, 300])
+@pytest.mark.parametrize("batch", [8, 9, 31, 64, 100, 300])
 def test_ne_matmul_mfma(gpu, books, oracle, rows, columns, batch):
     _, nt, _, nb = books
     rng = syn.rng_for(0, 11 * rows + columns + batch)
@@ -99,7 +100,7 @@ def test_ne_matmul_mfma(gpu, books, oracle, rows, columns, batch):
 
 
 @pytest.mark.parametrize("rows,columns", NE_SHAPES)
-@pytest.mark.parametrize("batch", [1, 3, 4, 16])
+@pytest.mark.parametrize("batch", [1, 3, 4, 7, 8, 16])
 def test_ne_matmul(gpu, books, oracle, rows, columns, batch):
     _, nt, _, nb = books
     rng = syn.rng_for(0, rows * 3 + columns + batch)
