@@ -153,18 +153,11 @@ __global__ __launch_bounds__(256) void k_head_gemv(
     }
 }
 
-// Sums V per-lane values over the 64 lanes of a wave by halving exchanges:
-// at offset 1 a lane keeps one half of its values and sends the other, then
-// at offset 2 half of the rest, until one value is left, which the remaining
-// offsets sum over all lanes. `which` says which value the lane ends with;
-// lanes 0..V-1 hold all V. Every value is summed over the same pair tree as
-// a full xor butterfly with offsets 1, 2, ..., 32, so the sums are
-// bit-identical to it.
 __device__ __forceinline__ bool first_max_before(float a, uint32_t ia, float b, uint32_t ib) {
     return a == b ? ia < ib : a > b;
 }
 
-// Per-wave summaries the 2048-column GEMV leaves for the certified arg-max,
+// Per-wave summaries the 2048-column MFMA head leaves for the certified arg-max,
 // [batch][waves] each: the wave's first maximum logit and its row
 // (0xFFFFFFFF for a wave with no rows), and the largest
 // fmaf(factor, bound, logit) over the wave's rows.
@@ -175,152 +168,340 @@ struct HeadWaveBest {
     float *upper;
 };
 
-template <int V>
-__device__ __forceinline__ float reduce_scatter64(float (&v)[V], uint32_t lane,
-                                                  uint32_t &which) {
-#pragma clang fp contract(off)
-    uint32_t off = 1;
-    which = 0;
-#pragma unroll
-    for (int h = V / 2; h >= 1; h /= 2) {
-        const bool hi = (lane & off) != 0u;
-#pragma unroll
-        for (int i = 0; i < h; ++i) {
-            const float send = hi ? v[i] : v[i + h];
-            const float keep = hi ? v[i + h] : v[i];
-            v[i] = keep + __shfl_xor(send, static_cast<int>(off));
-        }
-        which += hi ? static_cast<uint32_t>(h) : 0u;
-        off <<= 1;
-    }
-    for (; off < 64u; off <<= 1) {
-        v[0] += __shfl_xor(v[0], static_cast<int>(off));
-    }
-    return v[0];
+// ---- the 2048-column head on the bf16 MFMA ----------------------------------
+//
+// logit[t][r] = sum over the 32 groups g of 64 columns of scale[r][g] *
+// sum_{k in g} (u[r][k] - 16) x[t][k]. A wave takes 16-row tiles; per group a
+// tile is two v_mfma_f32_16x16x32_bf16 whose operands are exact:
+//   A[r][slot] = 1 + u * delta, bf16 0x3F80 | u << 2 (delta 1/32, the low
+//                half of a dword) or 0x3F80 | u << 1 (delta 1/64, the high half)
+//   B[slot][4t + p] = piece p of x[t][k] / delta, three bf16 pieces (p 0-2)
+//                that sum to it exactly (8 + 8 + 8 significant bits)
+// so column 4t + p accumulates sum_k a_k b_k = sum_k b_k + sum_k u_k x_k in
+// fp32 over exact products. The accumulator starts at -K[g][4t + p] with K =
+// sum_k b_k (1 + 16 delta_k), so the pieces' sum is sum_k (u_k - 16) x_k;
+// column 4t + 3 has B = 0 and K = -16 sum_k |x_k|, and accumulates the row's
+// bound sum 16 sum_g scale sum|x| of the certified arg-max. The group sums
+// are scaled and added per row in fp32; the pieces of a row add in the order
+// (0 + 1) + 2. Each rounding is relative to sums of |u x|, |x| / delta, well
+// inside the arg-max bound's (n + 80) 2^-24 16 scale sum|x| (x 2.5).
+//
+// A lane holds 16 codes of its row per group (columns 16q .. 16q + 15, q =
+// lane / 16): its three aligned dwords, shifted by 16 bits for odd q, hold
+// code c at bits 5c; pairs (c, c + 3) and (13, 14) each take one funnel shift
+// and one and-or into the two bf16 mantissas of an A dword. The B fragments,
+// K and each tile's scales live in LDS; the B fragments are built by every
+// block from x while its first tile's codes load.
+constexpr uint32_t kHmWaves = 8;
+constexpr uint32_t kHmThreads = 64 * kHmWaves;
+constexpr uint32_t kHmGroups = 32;
+constexpr uint32_t kHmTile = 16;    // rows per tile
+constexpr uint32_t kHmTokens = 4;   // tokens per pass: 4 columns each
+constexpr uint32_t kHmChunk = 8;    // groups per load chunk (a quarter tile)
+
+typedef __bf16 hm_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float hm_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t hm_u32x4 __attribute__((ext_vector_type(4)));
+
+struct HeadMfmaLds {
+    hm_u32x4 b[kHmGroups][2][4][16];  // B fragment of (group, MFMA, lane / 16, column)
+    hm_f32x4 c[kHmGroups][16];        // -K of (group, column), the accumulator's start
+    union {
+        float part[kHmGroups][16][8];            // K's partial sums while the tables build
+        float scale[kHmWaves][kHmGroups][kHmTile];  // each wave's tile scales
+    } u;
+};
+
+// The two codes of each A dword, by MFMA and dword: (low half, high half).
+__device__ __forceinline__ uint32_t hm_code(uint32_t i, uint32_t d, uint32_t h) {
+    // MFMA 0: (0,3) (1,4) (2,5) (6,9); MFMA 1: (7,10) (8,11) (12,15) (13,14)
+    constexpr uint8_t lo[8] = {0, 1, 2, 6, 7, 8, 12, 13};
+    constexpr uint8_t hi[8] = {3, 4, 5, 9, 10, 11, 15, 14};
+    return h == 0 ? lo[4 * i + d] : hi[4 * i + d];
 }
 
-// k_head_gemv for 2048 columns (64 quads: one row per wave per pass), with
-// the x sums of a lane's quad computed in place, the next row's codes loaded
-// while this row is summed, the lane sums
-// reduce-scattered, and the bound sums only when they are wanted.
-template <int NT, bool BOUNDS>
-__global__ __launch_bounds__(256) void k_head_gemv_2048(
+// bf16 bits of piece p of v (p < 3): v = hi + mid + lo exactly, each the
+// leading 8 significant bits of what is left.
+__device__ __forceinline__ uint32_t hm_piece(float v, uint32_t p) {
+    const uint32_t bits = __float_as_uint(v);
+    const float hi = __uint_as_float(bits & 0xFFFF0000u);
+    const float r1 = v - hi;
+    const float mid = __uint_as_float(__float_as_uint(r1) & 0xFFFF0000u);
+    const float r2 = r1 - mid;
+    const float pick = p == 0 ? hi : (p == 1 ? mid : r2);
+    return __float_as_uint(pick) >> 16;
+}
+
+// The 16 codes of (row, group g, quarter q) as the 8 A dwords of the
+// group's two MFMAs, from the lane's three dwords w (already shifted so
+// that code c sits at bits 5c).
+__device__ __forceinline__ void hm_decode(uint32_t w0, uint32_t w1, uint32_t w2, hm_u32x4 &a0,
+                                          hm_u32x4 &a1) {
+    constexpr uint32_t M = 0x003E007Cu, ONE = 0x3F803F80u;
+    const auto and_or = [](uint32_t v, uint32_t m, uint32_t o) { return (v & m) | o; };
+    a0.x = and_or(w0 << 2, M, ONE);
+    a0.y = and_or(w0 >> 3, M, ONE);
+    a0.z = and_or(w0 >> 8, M, ONE);
+    a0.w = and_or(__builtin_amdgcn_alignbit(w1, w0, 28), M, ONE);
+    a1.x = and_or(w1 >> 1, M, ONE);
+    a1.y = and_or(w1 >> 6, M, ONE);
+    a1.z = and_or(__builtin_amdgcn_alignbit(w2, w1, 26), M, ONE);
+    const uint32_t high = and_or(__builtin_amdgcn_alignbit(w2, w1, 21), 0x003E0000u, ONE);
+    a1.w = and_or(__builtin_amdgcn_alignbit(w2, w1, 31), 0x7Cu, high);
+}
+
+// LDS reads at a byte address the compiler keeps in one VGPR per array,
+// the per-group part an immediate offset (all under 64 KiB past the base).
+typedef __attribute__((address_space(3))) const hm_u32x4 *hm_lds_u32x4;
+typedef __attribute__((address_space(3))) const hm_f32x4 *hm_lds_f32x4;
+__device__ __forceinline__ hm_u32x4 hm_lds_u(uint32_t address) {
+    return *reinterpret_cast<hm_lds_u32x4>(static_cast<size_t>(address));
+}
+__device__ __forceinline__ hm_f32x4 hm_lds_f(uint32_t address) {
+    return *reinterpret_cast<hm_lds_f32x4>(static_cast<size_t>(address));
+}
+__device__ __forceinline__ uint32_t hm_opaque(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+__device__ __forceinline__ hm_f32x4 hm_mfma(hm_u32x4 a, hm_u32x4 b, hm_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(hm_bf16x8, a),
+                                                    __builtin_bit_cast(hm_bf16x8, b), c, 0, 0, 0);
+}
+
+// The B fragments and accumulator starts of tokens t0 .. t0 + 3 (zero past
+// `batch`) into LDS; ends with a block barrier.
+__device__ void hm_build_tables(HeadMfmaLds &L, const float *__restrict__ x, uint32_t t0,
+                                uint32_t batch) {
+#pragma clang fp contract(off)
+    // thread (group, quarter, token): per MFMA the fragments of its three
+    // pieces and the bound column, and their four partial sums of K
+    for (uint32_t e = threadIdx.x; e < kHmGroups * 4 * kHmTokens; e += kHmThreads) {
+        const uint32_t t = e % kHmTokens, q = (e / kHmTokens) % 4, g = e / 16;
+        const bool live = t0 + t < batch;
+        const float *xt = x + static_cast<size_t>(live ? t0 + t : 0) * 2048u + 64u * g + 16u * q;
+#pragma unroll
+        for (uint32_t i = 0; i < 2; ++i) {
+            hm_u32x4 frag[3];
+            float sum[3] = {0.0f, 0.0f, 0.0f}, bound = 0.0f;
+#pragma unroll
+            for (uint32_t d = 0; d < 4; ++d) {
+                uint32_t half[3][2];
+#pragma unroll
+                for (uint32_t h = 0; h < 2; ++h) {
+                    const float xv = live ? xt[hm_code(i, d, h)] : 0.0f;
+                    const float v = xv * (h == 0 ? 32.0f : 64.0f);  // exact
+                    const float f = h == 0 ? 1.5f : 1.25f;           // 1 + 16 delta
+#pragma unroll
+                    for (uint32_t p = 0; p < 3; ++p) {
+                        half[p][h] = hm_piece(v, p);
+                        sum[p] += __uint_as_float(half[p][h] << 16) * f;
+                    }
+                    bound += fabsf(xv);
+                }
+#pragma unroll
+                for (uint32_t p = 0; p < 3; ++p) {
+                    frag[p][d] = half[p][0] | (half[p][1] << 16);
+                }
+            }
+#pragma unroll
+            for (uint32_t p = 0; p < 3; ++p) {
+                L.b[g][i][q][4 * t + p] = frag[p];
+                L.u.part[g][4 * t + p][4 * i + q] = sum[p];
+            }
+            L.b[g][i][q][4 * t + 3] = hm_u32x4{0u, 0u, 0u, 0u};
+            L.u.part[g][4 * t + 3][4 * i + q] = -16.0f * bound;
+        }
+    }
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < kHmGroups * 16; e += kHmThreads) {
+        const uint32_t g = e / 16, n = e % 16;
+        float k = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j) {
+            k += L.u.part[g][n][j];
+        }
+        L.c[g][n] = hm_f32x4{-k, -k, -k, -k};
+    }
+    __syncthreads();
+}
+
+// The lane's three dwords of (row, group g) for its quarter q: aligned, from
+// the 10-byte stretch's start (even q) or two bytes before it (odd q).
+__device__ __forceinline__ void hm_load(const uint8_t *__restrict__ row_codes, uint32_t g,
+                                        uint32_t q, uint32_t (&w)[3]) {
+    const uint32_t *src = reinterpret_cast<const uint32_t *>(
+        row_codes + 40u * g + 10u * q - 2u * (q & 1u));
+    // plain loads: the four quarters of a row's 40 bytes and the next
+    // groups' share cache lines, which nontemporal loads would fetch again
+    // (2048-column head, loads alone: 75.6 us nontemporal, 47.0 us plain)
+#pragma unroll
+    for (uint32_t i = 0; i < 3; ++i) {
+        w[i] = src[i];
+    }
+}
+
+// Wave w takes tiles w, w + waves, ...; per pass of four tokens it leaves
+// the logits and, with BOUNDS, the bounds and its per-token summary
+// (HeadWaveBest) for the arg-max.
+template <bool BOUNDS>
+__global__ __launch_bounds__(kHmThreads) void k_head_mfma(
     const uint8_t *__restrict__ packed, const uint16_t *__restrict__ scales, uint32_t rows,
     const float *__restrict__ x, uint32_t batch, float *__restrict__ logits,
     float *__restrict__ bounds, HeadWaveBest best) {
-    // no contraction: a lane's logit stays a rounded product in every variant
-    // (with the bounds or without), so both variants give the same bits
 #pragma clang fp contract(off)
-    constexpr uint32_t columns = 2048u, quads = 64u, groups = 32u;
-    constexpr int V = BOUNDS ? 2 * NT : NT;
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave_global = blockIdx.x * (blockDim.x / 64u) + (threadIdx.x >> 6);
-    const uint32_t wave_count = gridDim.x * (blockDim.x / 64u);
-    const uint32_t *codes = reinterpret_cast<const uint32_t *>(packed);
+    extern __shared__ __align__(16) unsigned char hm_raw[];
+    HeadMfmaLds &L = *reinterpret_cast<HeadMfmaLds *>(hm_raw);
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t wave_global = blockIdx.x * kHmWaves + wave;
+    const uint32_t wave_count = gridDim.x * kHmWaves;
+    const uint32_t tiles = (rows + kHmTile - 1u) / kHmTile;
+    const uint32_t q = lane / 16u, i_row = lane % 16u;
+    const uint32_t n = lane % 16u, p = lane % 4u, t_lane = n / 4u;
+    const uint32_t shift = 16u * (q & 1u);
+    float *sc = &L.u.scale[wave][0][0];
+    // LDS byte addresses of this lane's B fragment, accumulator start and
+    // scales for group 0; group g adds g * 2048, g * 256, g * 64
+    const uint32_t lds0 = static_cast<uint32_t>(
+        (uintptr_t)(__attribute__((address_space(3))) unsigned char *)hm_raw);
+    const uint32_t b_at = hm_opaque(lds0 + static_cast<uint32_t>(offsetof(HeadMfmaLds, b)) +
+                                    q * 256u + n * 16u);
+    const uint32_t c_at = hm_opaque(lds0 + static_cast<uint32_t>(offsetof(HeadMfmaLds, c)) + n * 16u);
+    const uint32_t s_at = hm_opaque(lds0 + static_cast<uint32_t>(offsetof(HeadMfmaLds, u)) +
+                                    (wave * kHmGroups * kHmTile + 4u * q) * 4u);
 
-    for (uint32_t t0 = 0; t0 < batch; t0 += NT) {
-        float xv[NT][kQuadColumns];
-        float sx[NT], sa[NT];
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            const uint32_t t = t0 + j < batch ? t0 + j : t0;
-            const float4 *src = reinterpret_cast<const float4 *>(
-                x + static_cast<size_t>(t) * columns + lane * kQuadColumns);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const float4 v = src[q];
-                xv[j][4 * q] = v.x;
-                xv[j][4 * q + 1] = v.y;
-                xv[j][4 * q + 2] = v.z;
-                xv[j][4 * q + 3] = v.w;
-            }
-            // the quad's sums of x and |x|, in k_head_sums' order
-            float s = 0.0f, a = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 32; ++k) {
-                s += xv[j][k];
-                a += fabsf(xv[j][k]);
-            }
-            sx[j] = s;
-            sa[j] = a;
-        }
-        // with the bounds, even lanes end a row with a logit and their odd
-        // partners with its bound (the first halving exchange is at offset 1)
+    for (uint32_t t0 = 0; t0 < batch; t0 += kHmTokens) {
         float best_v = -INFINITY, upper = -INFINITY;
         uint32_t best_i = 0xFFFFFFFFu;
-        uint32_t row = wave_global;
-        uint32_t dn[5] = {0u, 0u, 0u, 0u, 0u};
-        uint16_t sn = 0;
-        if (row < rows) {
-            const uint32_t *src = codes + (static_cast<size_t>(row) * quads + lane) * 5u;
+        // a ring of the four quarter-tile chunks: after a chunk is summed its
+        // slot loads the same chunk of the wave's next tile, three chunks of
+        // codes (18 KiB a wave) in flight while one is summed
+        uint32_t w[4][kHmChunk][3];
+        hm_u32x4 sreg = hm_u32x4{0u, 0u, 0u, 0u};
+        uint32_t tile = wave_global;
+        // the first tile's codes and scales load while the tables build
+        const auto row_of = [&](uint32_t t, uint32_t r) {
+            const uint32_t row = t < tiles ? t * kHmTile + r : rows;
+            return row < rows ? row : rows - 1u;
+        };
+        const auto load_chunk = [&](uint32_t t, uint32_t part, uint32_t (&dst)[kHmChunk][3]) {
+            const uint8_t *rc = packed + static_cast<size_t>(row_of(t, i_row)) * 1280u;
 #pragma unroll
-            for (int i = 0; i < 5; ++i) {
-                dn[i] = __builtin_nontemporal_load(src + i);
+            for (uint32_t g = 0; g < kHmChunk; ++g) {
+                hm_load(rc, kHmChunk * part + g, q, dst[g]);
             }
-            sn = scales[static_cast<size_t>(row) * groups + lane / 2u];
+        };
+        const auto load_scales = [&](uint32_t t) {
+            // lane l: row l / 4, groups 8 (l % 4) .. + 7
+            const hm_u32x4 *src = reinterpret_cast<const hm_u32x4 *>(
+                scales + static_cast<size_t>(row_of(t, lane / 4u)) * kHmGroups + 8u * (lane % 4u));
+            sreg = *src;
+        };
+        if (tile < tiles) {
+            load_chunk(tile, 0, w[0]);
+            load_chunk(tile, 1, w[1]);
+            load_chunk(tile, 2, w[2]);
+            load_chunk(tile, 3, w[3]);
+            load_scales(tile);
         }
-        for (; row < rows; row += wave_count) {
-            uint32_t d[6] = {dn[0], dn[1], dn[2], dn[3], dn[4], 0u};
-            const float scale = half_bits_to_float(sn);
-            const uint32_t next = row + wave_count;
-            if (next < rows) {
-                const uint32_t *src = codes + (static_cast<size_t>(next) * quads + lane) * 5u;
+        if (t0 > 0) {
+            __syncthreads();  // the previous pass's readers are done with the tables
+        }
+        hm_build_tables(L, x, t0, batch);
+        for (; tile < tiles; tile += wave_count) {
+            // this tile's scales, transposed: sc[g][row] as floats
 #pragma unroll
-                for (int i = 0; i < 5; ++i) {
-                    dn[i] = __builtin_nontemporal_load(src + i);
-                }
-                sn = scales[static_cast<size_t>(next) * groups + lane / 2u];
+            for (uint32_t e = 0; e < 8; ++e) {
+                const uint32_t bits = sreg[e / 2] >> (16u * (e % 2u));
+                sc[(8u * (lane % 4u) + e) * kHmTile + lane / 4u] = half_bits_to_float(bits & 0xFFFFu);
             }
-            float u[kQuadColumns];
-#define ADI_CODE(K) u[K] = code_at<K>(d);
-            ADI_CODE(0) ADI_CODE(1) ADI_CODE(2) ADI_CODE(3) ADI_CODE(4) ADI_CODE(5) ADI_CODE(6)
-            ADI_CODE(7) ADI_CODE(8) ADI_CODE(9) ADI_CODE(10) ADI_CODE(11) ADI_CODE(12)
-            ADI_CODE(13) ADI_CODE(14) ADI_CODE(15) ADI_CODE(16) ADI_CODE(17) ADI_CODE(18)
-            ADI_CODE(19) ADI_CODE(20) ADI_CODE(21) ADI_CODE(22) ADI_CODE(23) ADI_CODE(24)
-            ADI_CODE(25) ADI_CODE(26) ADI_CODE(27) ADI_CODE(28) ADI_CODE(29) ADI_CODE(30)
-            ADI_CODE(31)
-#undef ADI_CODE
-            float v[V];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            hm_f32x4 out = hm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            const auto run_chunk = [&](uint32_t part, const uint32_t (&src)[kHmChunk][3]) {
 #pragma unroll
-            for (int j = 0; j < NT; ++j) {
-                float acc0 = 0.0f, acc1 = 0.0f;
-#pragma unroll
-                for (int k = 0; k < 32; k += 2) {
-                    acc0 = fmaf(u[k], xv[j][k], acc0);
-                    acc1 = fmaf(u[k + 1], xv[j][k + 1], acc1);
+                for (uint32_t j = 0; j < kHmChunk; ++j) {
+                    const uint32_t g = kHmChunk * part + j;
+                    const uint32_t w0 = __builtin_amdgcn_alignbit(src[j][1], src[j][0], shift);
+                    const uint32_t w1 = __builtin_amdgcn_alignbit(src[j][2], src[j][1], shift);
+                    const uint32_t w2 = src[j][2] >> shift;
+                    hm_u32x4 a0, a1;
+                    hm_decode(w0, w1, w2, a0, a1);
+                    hm_f32x4 acc = hm_mfma(a0, hm_lds_u(b_at + g * 2048u), hm_lds_f(c_at + g * 256u));
+                    acc = hm_mfma(a1, hm_lds_u(b_at + g * 2048u + 1024u), acc);
+                    const hm_f32x4 s = hm_lds_f(s_at + g * 64u);
+                    out.x = fmaf(s.x, acc.x, out.x);
+                    out.y = fmaf(s.y, acc.y, out.y);
+                    out.z = fmaf(s.z, acc.z, out.z);
+                    out.w = fmaf(s.w, acc.w, out.w);
+                    // the sums complete here, group by group: left to the
+                    // compiler, they sink past the next loads and every
+                    // group's accumulator and scales stay live (and spill)
+                    asm volatile("" : "+v"(out.x), "+v"(out.y), "+v"(out.z), "+v"(out.w));
                 }
-                v[j] = scale * ((acc0 + acc1) - 16.0f * sx[j]);
-                if constexpr (BOUNDS) {
-                    v[NT + j] = 16.0f * scale * sa[j];
-                }
-            }
-            uint32_t k;
-            const float total = reduce_scatter64<V>(v, lane, k);
-            if (lane < static_cast<uint32_t>(V)) {
-                const uint32_t j = k % NT;
-                if (t0 + j < batch) {
-                    float *dst = BOUNDS && k >= NT ? bounds : logits;
-                    dst[static_cast<size_t>(t0 + j) * rows + row] = total;
-                }
-            }
-            if constexpr (BOUNDS) {
-                const float bound = __shfl_xor(total, 1);
-                const float up = fmaf(best.factor, bound, total);
-                upper = up > upper ? up : upper;
-                if (best_i == 0xFFFFFFFFu || first_max_before(total, row, best_v, best_i)) {
-                    best_v = total;
-                    best_i = row;
+            };
+            // past the last tile the loads read the last row again (row_of
+            // clamps), unused: no branch breaks the in-order load counts
+            const uint32_t next = tile + wave_count;
+            run_chunk(0, w[0]);
+            load_chunk(next, 0, w[0]);
+            load_scales(next);
+            run_chunk(1, w[1]);
+            load_chunk(next, 1, w[1]);
+            run_chunk(2, w[2]);
+            load_chunk(next, 2, w[2]);
+            run_chunk(3, w[3]);
+            load_chunk(next, 3, w[3]);
+            // every lane's reads of this tile's scales end before the next
+            // tile's are written
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // lane p = 0 of a quad: logit (piece 0 + piece 1) + piece 2, bound piece 3
+            for (uint32_t j = 0; j < 4; ++j) {
+                const float v = out[j];
+                const float v1 = __uint_as_float(static_cast<uint32_t>(
+                    __builtin_amdgcn_mov_dpp(static_cast<int>(__float_as_uint(v)), 0x39, 0xF, 0xF, true)));
+                const float v2 = __uint_as_float(static_cast<uint32_t>(
+                    __builtin_amdgcn_mov_dpp(static_cast<int>(__float_as_uint(v)), 0x4E, 0xF, 0xF, true)));
+                const float v3 = __uint_as_float(static_cast<uint32_t>(
+                    __builtin_amdgcn_mov_dpp(static_cast<int>(__float_as_uint(v)), 0x93, 0xF, 0xF, true)));
+                const float total = (v + v1) + v2;
+                const uint32_t row = tile * kHmTile + 4u * q + j;
+                const uint32_t t = t0 + t_lane;
+                if (p == 0 && row < rows && t < batch) {
+                    logits[static_cast<size_t>(t) * rows + row] = total;
+                    if constexpr (BOUNDS) {
+                        bounds[static_cast<size_t>(t) * rows + row] = v3;
+                        const float up = fmaf(best.factor, v3, total);
+                        upper = up > upper ? up : upper;
+                        if (best_i == 0xFFFFFFFFu || first_max_before(total, row, best_v, best_i)) {
+                            best_v = total;
+                            best_i = row;
+                        }
+                    }
                 }
             }
         }
         if constexpr (BOUNDS) {
-            uint32_t j = 0;  // the token of an even lane below V (as reduce_scatter64)
-            for (uint32_t off = 1, h = V / 2; h >= 1u; h /= 2u, off <<= 1) {
-                j += (lane & off) != 0u ? h : 0u;
+            // the wave's summary per token: over the four quarters' lanes of
+            // column 4t (lanes 4t + 16 k)
+#pragma unroll
+            for (int off = 16; off <= 32; off <<= 1) {
+                const float ov = __shfl_xor(best_v, off);
+                const uint32_t oi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(best_i), off));
+                const float ou = __shfl_xor(upper, off);
+                upper = ou > upper ? ou : upper;
+                if (oi != 0xFFFFFFFFu && (best_i == 0xFFFFFFFFu || first_max_before(ov, oi, best_v, best_i))) {
+                    best_v = ov;
+                    best_i = oi;
+                }
             }
-            if (best.value != nullptr && (lane & 1u) == 0u && lane < static_cast<uint32_t>(V) &&
-                t0 + j < batch) {
-                const size_t at = static_cast<size_t>(t0 + j) * wave_count + wave_global;
+            const uint32_t t = t0 + t_lane;
+            if (best.value != nullptr && lane < 16u && p == 0 && t < batch) {
+                const size_t at = static_cast<size_t>(t) * wave_count + wave_global;
                 best.value[at] = best_v;
                 best.index[at] = best_i;
                 best.upper[at] = upper;
@@ -596,9 +777,12 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_head_argmax(
         __syncthreads();
         const uint32_t listed = wave_list_count;
         if (listed <= kWaveListCap) {
-            const uint32_t passes = ceil_div_device(h.rows, wave_count);
-            for (uint32_t k = threadIdx.x; k < listed * passes; k += kArgmaxThreads) {
-                const uint32_t r = wave_list[k / passes] + (k % passes) * wave_count;
+            // wave w's rows: 16-row tiles w, w + wave_count, ...
+            const uint32_t span = ceil_div_device(ceil_div_device(h.rows, kHmTile), wave_count) * kHmTile;
+            for (uint32_t k = threadIdx.x; k < listed * span; k += kArgmaxThreads) {
+                const uint32_t at = k % span;
+                const uint32_t r = (wave_list[k / span] + (at / kHmTile) * wave_count) * kHmTile +
+                                   at % kHmTile;
                 if (r < h.rows) {
                     consider(r, row_logits[r], row_bounds[r]);
                 }
@@ -716,10 +900,16 @@ void launch_exact_parts(adi_hip_context *ctx, const HeadView &v, const float *x,
     }
 }
 
-// Blocks of the 2048-column GEMV: one row per wave per pass, enough waves
-// for four passes each.
+// Blocks of the 2048-column MFMA head: one per CU (its LDS tables), fewer
+// when the tiles do not need them.
 uint32_t head_wide_blocks(const adi_hip_context *ctx, uint32_t rows) {
-    return std::min<uint32_t>(ceil_div(rows, 4u * 4u), static_cast<uint32_t>(ctx->cu_count) * 8u);
+    return std::min<uint32_t>(ceil_div(ceil_div(rows, kHmTile), kHmWaves),
+                              static_cast<uint32_t>(ctx->cu_count));
+}
+
+// Waves of that launch: the per-wave arg-max summaries are [batch][waves].
+uint32_t head_wave_count(const adi_hip_context *ctx, uint32_t rows) {
+    return head_wide_blocks(ctx, rows) * kHmWaves;
 }
 
 // Whether head_logits can leave per-wave summaries (2048 columns, no
@@ -747,13 +937,13 @@ void head_logits(adi_hip_context *ctx, const adi_hip_head_chunk *h, const float 
                                                    static_cast<uint32_t>(ctx->cu_count) * 8u);
         if (quads == 64u) {
             const uint32_t wide = head_wide_blocks(ctx, h->rows);
-            const bool with = bounds != nullptr;
-            const auto kernel = batch == 1 ? (with ? k_head_gemv_2048<1, true>
-                                                   : k_head_gemv_2048<1, false>)
-                                           : (with ? k_head_gemv_2048<4, true>
-                                                   : k_head_gemv_2048<4, false>);
-            launch(ctx, "head_gemv", kernel, dim3(wide), dim3(256), 0, h->packed,
-                   h->group_scale_f16, h->rows, x, batch, logits, bounds, best);
+            const auto kernel = bounds != nullptr ? k_head_mfma<true> : k_head_mfma<false>;
+            static const bool ready =
+                set_lds_limit(reinterpret_cast<const void *>(&k_head_mfma<true>), sizeof(HeadMfmaLds)) &&
+                set_lds_limit(reinterpret_cast<const void *>(&k_head_mfma<false>), sizeof(HeadMfmaLds));
+            (void)ready;
+            launch(ctx, "head_mfma", kernel, dim3(wide), dim3(kHmThreads), sizeof(HeadMfmaLds),
+                   h->packed, h->group_scale_f16, h->rows, x, batch, logits, bounds, best);
         } else if (batch == 1) {
             launch(ctx, "head_gemv", k_head_gemv<1>, dim3(blocks), dim3(256), 0, h->packed,
                    h->group_scale_f16, h->rows, h->columns, x, static_cast<const float *>(sums),
@@ -780,7 +970,7 @@ void head_logits(adi_hip_context *ctx, const adi_hip_head_chunk *h, const float 
 size_t head_workspace(const adi_hip_context *ctx, const adi_hip_head_chunk *h, uint32_t batch,
                       bool with_logits, bool with_bounds) {
     const size_t quads = h->columns / kQuadColumns;
-    const size_t waves = static_cast<size_t>(head_wide_blocks(ctx, h->rows)) * 4u;
+    const size_t waves = head_wave_count(ctx, h->rows);
     return Workspace::round(batch * quads * 4) * 2 +
            (with_bounds && head_wave_best(h) ? Workspace::round(batch * waves * 4) * 3 : 0) +
            (with_logits ? Workspace::round(size_t(batch) * h->rows * 4) : 0) +
@@ -828,7 +1018,7 @@ int adi_hip_head_argmax(adi_hip_context *ctx, const adi_hip_head_chunk *h, const
         const float factor = 2.5f * static_cast<float>(h->columns + 80u) * 5.9604645e-8f;
         HeadWaveBest best{factor, nullptr, nullptr, nullptr};
         const bool waves = head_wave_best(h);
-        const uint32_t wave_count = head_wide_blocks(ctx, h->rows) * 4u;
+        const uint32_t wave_count = head_wave_count(ctx, h->rows);
         if (waves) {
             best.value = ws.take<float>(size_t(batch) * wave_count);
             best.index = ws.take<uint32_t>(size_t(batch) * wave_count);

@@ -276,6 +276,10 @@ class Context:
         self.check(self.lib.adi_hip_set_stream(self.handle, vp(torch.cuda.current_stream(device).cuda_stream)))
         self.set_isa(isa_lanes)
 
+    def use_stream(self, stream) -> None:
+        """Launch on `stream` (a torch stream) from now on."""
+        self.check(self.lib.adi_hip_set_stream(self.handle, vp(stream.cuda_stream)))
+
     # -- plumbing --
     def check(self, status: int) -> None:
         if status != OK:

@@ -46,6 +46,20 @@ def test_head_logits_and_argmax(gpu, oracle, isa, rows, columns, protected, batc
         assert np.array_equal(logits[:, rows_p].view(np.uint32), want[:, rows_p].view(np.uint32))
 
 
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 9])
+def test_head_2048_columns_by_batch(gpu, oracle, batch):
+    """The 2048-column head (MFMA tiles of 16 rows, four tokens per pass) on
+    rows that do not fill the last tile, one to three passes."""
+    rng = syn.rng_for(1, 5000 + batch)
+    h = syn.head_chunk(rng, 1000, 2048, 0)
+    x = syn.rms_normalized(syn.hidden_states(rng, batch, 2048))
+    want = po.head_matmul(oracle, h, x, isa=16)
+    logits, arg, plain = run_head(gpu, h, x)
+    assert max_rel_error(logits, want) <= 1e-3
+    assert np.array_equal(logits.view(np.uint32), plain.view(np.uint32))
+    assert np.array_equal(arg, np.argmax(want, axis=1).astype(np.uint32))
+
+
 def test_head_argmax_near_ties(gpu, oracle):
     """Rows built to tie or nearly tie with the maximum: the certified
     arg-max must still return the CPU path's first maximum."""
