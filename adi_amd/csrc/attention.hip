@@ -685,9 +685,15 @@ void linear_attention_chunk(adi_hip_context *ctx, const adi_hip_linear_attention
 }
 
 // decode_layer for `count` consecutive tokens of rows `hidden`.
-void decoder_chunk(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_t position,
-                   uint32_t count, float *hidden, const adi_hip_layer_state *state) {
-    require(L != nullptr && hidden != nullptr && state != nullptr && L->input_norm != nullptr &&
+// The decoder layer on rows hidden[count][moe.hidden] (decode_layer,
+// src/executor.cpp:1473-1529) up to its MoE block: hidden (+= pending, the
+// previous layer's MoE rows, when given) is normalized, the attention's rows
+// are added to it and normalized again, each add fused into its norm; the MoE
+// rows go to moe_out (may be `pending`: that is read first), not yet added.
+template <typename Attention>
+void layer_body(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_t count,
+                float *hidden, const float *pending, float *moe_out, Attention &&attention) {
+    require(L != nullptr && hidden != nullptr && moe_out != nullptr && L->input_norm != nullptr &&
                 L->post_attention_norm != nullptr && count > 0,
             "decoder layer input is null");
     const uint32_t n = L->moe.hidden;
@@ -698,23 +704,43 @@ void decoder_chunk(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_
     ws.ensure(Workspace::round(rows * 4) * 2);
     float *normalized = ws.take<float>(rows);
     float *branch = ws.take<float>(rows);
-    const dim3 grid(ceil_div(rows, 256));
-    forward(ctx, adi_hip_rms_norm(ctx, hidden, L->input_norm, n, count, 1.0f, 1.0e-6f, normalized));
-    if (L->full_attention != 0) {
-        full_attention_chunk(ctx, &L->full, position, count, normalized, branch, state->keys,
-                             state->values, state->capacity);
-    } else {
-        linear_attention_chunk(ctx, &L->linear, count, normalized, branch, state->convolution,
-                               state->recurrent);
-    }
-    launch(ctx, "residual_add", k_residual_add, grid, dim3(256), 0, hidden,
-           static_cast<const float *>(branch), static_cast<uint32_t>(rows));
-    forward(ctx, adi_hip_rms_norm(ctx, hidden, L->post_attention_norm, n, count, 1.0f, 1.0e-6f,
-                                  normalized));
-    forward(ctx, adi_hip_moe_forward(ctx, &L->moe, normalized, count, nullptr, branch, nullptr,
+    launch_add_rms_norm(ctx, hidden, pending, L->input_norm, n, count, normalized);
+    attention(static_cast<const float *>(normalized), branch);
+    launch_add_rms_norm(ctx, hidden, branch, L->post_attention_norm, n, count, normalized);
+    forward(ctx, adi_hip_moe_forward(ctx, &L->moe, normalized, count, nullptr, moe_out, nullptr,
                                      nullptr));
-    launch(ctx, "residual_add", k_residual_add, grid, dim3(256), 0, hidden,
-           static_cast<const float *>(branch), static_cast<uint32_t>(rows));
+}
+
+// `count` consecutive tokens of one sequence at position .. position + count
+// - 1 (pending and moe_out as layer_body's).
+void decoder_chunk_body(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_t position,
+                        uint32_t count, float *hidden, const float *pending, float *moe_out,
+                        const adi_hip_layer_state *state) {
+    require(state != nullptr, "decoder layer input is null");
+    layer_body(ctx, L, count, hidden, pending, moe_out, [&](const float *in, float *out) {
+        if (L->full_attention != 0) {
+            full_attention_chunk(ctx, &L->full, position, count, in, out, state->keys,
+                                 state->values, state->capacity);
+        } else {
+            linear_attention_chunk(ctx, &L->linear, count, in, out, state->convolution,
+                                   state->recurrent);
+        }
+    });
+}
+
+// The whole layer in place (the public layer entries): the MoE rows are
+// added to hidden at the end.
+void decoder_chunk(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_t position,
+                   uint32_t count, float *hidden, const adi_hip_layer_state *state) {
+    require(L != nullptr && hidden != nullptr && count > 0, "decoder layer input is null");
+    auto &ws = ctx->layer_output;
+    ws.used = 0;
+    const size_t rows = size_t(count) * L->moe.hidden;
+    ws.ensure(Workspace::round(rows * 4));
+    float *moe_out = ws.take<float>(rows);
+    decoder_chunk_body(ctx, L, position, count, hidden, nullptr, moe_out, state);
+    launch(ctx, "residual_add", k_residual_add, dim3(ceil_div(rows, 256)), dim3(256), 0, hidden,
+           static_cast<const float *>(moe_out), static_cast<uint32_t>(rows));
 }
 
 // full_attention_forward_batch (src/executor.cpp:561-731) for one decode
@@ -858,39 +884,22 @@ void linear_attention_rows(adi_hip_context *ctx, const adi_hip_linear_attention 
 }  // namespace
 
 void decoder_rows(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_t rows,
-                  float *hidden, const adi_hip_layer_state *const *states,
-                  const uint32_t *positions) {
-    require(L != nullptr && hidden != nullptr && states != nullptr && positions != nullptr &&
-                L->input_norm != nullptr && L->post_attention_norm != nullptr && rows > 0,
-            "decoder batch shape mismatch");
-    const uint32_t n = L->moe.hidden;
-    require(n > 0 && aligned_to(hidden, 16), "decoder hidden row must be 16-byte aligned");
-    auto &ws = ctx->decoder_workspace;
-    ws.used = 0;
-    const size_t all = size_t(rows) * n;
-    ws.ensure(Workspace::round(all * 4) * 2);
-    float *normalized = ws.take<float>(all);
-    float *branch = ws.take<float>(all);
-    const dim3 grid(ceil_div(all, 256));
-    forward(ctx, adi_hip_rms_norm(ctx, hidden, L->input_norm, n, rows, 1.0f, 1.0e-6f, normalized));
-    if (L->full_attention != 0) {
-        full_attention_rows(ctx, &L->full, rows, normalized, branch, states, positions);
-    } else {
-        linear_attention_rows(ctx, &L->linear, rows, normalized, branch, states);
-    }
-    launch(ctx, "residual_add", k_residual_add, grid, dim3(256), 0, hidden,
-           static_cast<const float *>(branch), static_cast<uint32_t>(all));
-    forward(ctx, adi_hip_rms_norm(ctx, hidden, L->post_attention_norm, n, rows, 1.0f, 1.0e-6f,
-                                  normalized));
-    forward(ctx, adi_hip_moe_forward(ctx, &L->moe, normalized, rows, nullptr, branch, nullptr,
-                                     nullptr));
-    launch(ctx, "residual_add", k_residual_add, grid, dim3(256), 0, hidden,
-           static_cast<const float *>(branch), static_cast<uint32_t>(all));
+                  float *hidden, const float *pending, float *moe_out,
+                  const adi_hip_layer_state *const *states, const uint32_t *positions) {
+    require(states != nullptr && positions != nullptr, "decoder batch shape mismatch");
+    layer_body(ctx, L, rows, hidden, pending, moe_out, [&](const float *in, float *out) {
+        if (L->full_attention != 0) {
+            full_attention_rows(ctx, &L->full, rows, in, out, states, positions);
+        } else {
+            linear_attention_rows(ctx, &L->linear, rows, in, out, states);
+        }
+    });
 }
 
 void prefill_chunk(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_t position,
-                   uint32_t count, float *hidden, const adi_hip_layer_state *state) {
-    decoder_chunk(ctx, L, position, count, hidden, state);
+                   uint32_t count, float *hidden, const float *pending, float *moe_out,
+                   const adi_hip_layer_state *state) {
+    decoder_chunk_body(ctx, L, position, count, hidden, pending, moe_out, state);
 }
 
 }  // namespace adi_hip

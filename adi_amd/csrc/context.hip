@@ -181,7 +181,8 @@ void adi_hip_context_destroy(adi_hip_context *ctx) {
     if (ctx->moe_sync != nullptr) {
         (void)hipFree(ctx->moe_sync);
     }
-    for (adi_hip::Workspace *w : {&ctx->sequence_workspace, &ctx->decoder_workspace, &ctx->rope_cache}) {
+    for (adi_hip::Workspace *w : {&ctx->sequence_workspace, &ctx->layer_output, &ctx->decoder_workspace,
+                                  &ctx->rope_cache}) {
         if (w->base != nullptr) {
             (void)hipFree(w->base);
         }
@@ -238,7 +239,7 @@ int adi_hip_set_fused_decode(adi_hip_context *ctx, int enabled) {
 int adi_hip_set_workspace_limit(adi_hip_context *ctx, size_t bytes) {
     return guarded(ctx, [&] {
         for (adi_hip::Workspace *w : {&ctx->workspace, &ctx->layer_workspace, &ctx->decoder_workspace,
-                                      &ctx->sequence_workspace, &ctx->rope_cache}) {
+                                      &ctx->sequence_workspace, &ctx->layer_output, &ctx->rope_cache}) {
             w->limit = bytes;
         }
     });

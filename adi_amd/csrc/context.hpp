@@ -86,6 +86,8 @@ struct adi_hip_context {
     // scratch of the model-level entries (decode steps, prefill), which call
     // the decoder layers
     adi_hip::Workspace sequence_workspace;
+    // the MoE rows of the public decoder-layer entries, added at their end
+    adi_hip::Workspace layer_output;
     // RoPE cos/sin of positions 0 .. rope_positions - 1 ([position][cos 32,
     // sin 32] floats), computed on the host and grown on demand
     adi_hip::Workspace rope_cache;

@@ -449,13 +449,18 @@ __global__ __launch_bounds__(256) void k_bf16_scalar(
 // its strided share, then the wave and block sums) rather than the CPU's
 // left-to-right loop, so the scale agrees to float rounding (a sequential
 // sum on one lane costs ~20 us for 2048 values).
+// With ADD the row is first replaced by row + residual (the residual add of
+// a decoder layer), and the norm is taken of that sum: the same values as a
+// separate add and norm.
+template <bool ADD>
 __global__ __launch_bounds__(256) void k_rms_norm(
-    const float *__restrict__ x, const uint16_t *__restrict__ weight, uint32_t count,
-    float offset, float epsilon, float *__restrict__ out) {
+    float *__restrict__ x, const float *__restrict__ residual, const uint16_t *__restrict__ weight,
+    uint32_t count, float offset, float epsilon, float *__restrict__ out) {
 #pragma clang fp contract(off)
     __shared__ float scale_shared;
     __shared__ float wave_sums[4];
-    const float *row = x + static_cast<size_t>(blockIdx.x) * count;
+    float *row = x + static_cast<size_t>(blockIdx.x) * count;
+    const float *add = ADD ? residual + static_cast<size_t>(blockIdx.x) * count : nullptr;
     float *dst = out + static_cast<size_t>(blockIdx.x) * count;
     // up to 8 values a thread: the row and the weights are loaded at once
     // and kept in registers for the output (same sums, same products)
@@ -469,6 +474,12 @@ __global__ __launch_bounds__(256) void k_rms_norm(
             const uint32_t i = threadIdx.x + k * blockDim.x;
             v[k] = i < count ? row[i] : 0.0f;
             w[k] = i < count ? bf16_bits_to_float(weight[i]) : 0.0f;
+            if constexpr (ADD) {
+                if (i < count) {
+                    v[k] = v[k] + add[i];
+                    row[i] = v[k];
+                }
+            }
         }
 #pragma unroll
         for (uint32_t k = 0; k < kHeld; ++k) {
@@ -478,7 +489,11 @@ __global__ __launch_bounds__(256) void k_rms_norm(
         }
     } else {
         for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
-            const float value = row[i];
+            float value = row[i];
+            if constexpr (ADD) {
+                value = value + add[i];
+                row[i] = value;
+            }
             squares += value * value;
         }
     }
@@ -910,6 +925,19 @@ void launch_route(adi_hip_context *ctx, const float *logits, const float *bias, 
     }
 }
 
+void launch_add_rms_norm(adi_hip_context *ctx, float *rows_in_out, const float *residual,
+                         const uint16_t *weight, uint32_t count, uint32_t rows, float *out) {
+    require(count > 0 && rows > 0 && rows_in_out != nullptr && weight != nullptr && out != nullptr,
+            "RMS norm shape mismatch");
+    if (residual != nullptr) {
+        launch(ctx, "add_rms_norm", k_rms_norm<true>, dim3(rows), dim3(256), 0, rows_in_out,
+               residual, weight, count, 1.0f, 1.0e-6f, out);
+    } else {
+        launch(ctx, "rms_norm", k_rms_norm<false>, dim3(rows), dim3(256), 0, rows_in_out,
+               residual, weight, count, 1.0f, 1.0e-6f, out);
+    }
+}
+
 }  // namespace adi_hip
 
 using namespace adi_hip;
@@ -939,7 +967,8 @@ int adi_hip_rms_norm(adi_hip_context *ctx, const float *input, const uint16_t *w
         require(count > 0 && rows > 0, "RMS norm shape mismatch");
         require(input != nullptr && weight_bf16 != nullptr && output != nullptr,
                 "RMS norm vector is null");
-        launch(ctx, "rms_norm", k_rms_norm, dim3(rows), dim3(256), 0, input, weight_bf16, count,
+        launch(ctx, "rms_norm", k_rms_norm<false>, dim3(rows), dim3(256), 0,
+               const_cast<float *>(input), static_cast<const float *>(nullptr), weight_bf16, count,
                weight_offset, epsilon, output);
     });
 }

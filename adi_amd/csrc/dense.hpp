@@ -56,6 +56,12 @@ void launch_route_sort(adi_hip_context *ctx, const RouteSort &args);
 void launch_route(adi_hip_context *ctx, const float *logits, const float *bias, uint32_t batch,
                   uint32_t *route_expert, float *route_weight, const RouteSort &args);
 
+// The decoder layers' norm (weight offset 1, epsilon 1e-6) of `rows` rows of
+// `count`: with `residual` (nullable) each row first becomes row + residual
+// in place, the residual add before the norm in one launch.
+void launch_add_rms_norm(adi_hip_context *ctx, float *rows_in_out, const float *residual,
+                         const uint16_t *weight, uint32_t count, uint32_t rows, float *out);
+
 constexpr uint32_t kMaxExperts = 1024;
 constexpr uint32_t kTiledBatch = 32;  // batches from which the bf16 products run register-tiled
 constexpr uint32_t kRouteBatch = 16;  // largest batch launch_route handles in one block

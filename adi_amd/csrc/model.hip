@@ -5,6 +5,7 @@
 // src/executor.cpp:1827-2101). Every argument is checked before anything is
 // launched, so a rejected call leaves the states and outputs as they were.
 #include "attention.hpp"
+#include "dense.hpp"
 
 #include <vector>
 
@@ -89,13 +90,13 @@ void validate_state(const adi_hip_model *m, const adi_hip_decoder_state &s, uint
     }
 }
 
-// The final norm of rows[rows][hidden] and the head chunks into
+// The final norm of rows[rows][hidden] + pending (the last layer's MoE
+// rows, added in place first) and the head chunks into
 // logits[rows][vocabulary].
 void model_logits(adi_hip_context *ctx, const adi_hip_model *m, const ModelShape &shape,
-                  const float *hidden, uint32_t rows, float *normalized, float *staging,
-                  float *logits) {
-    forward_status(ctx, adi_hip_rms_norm(ctx, hidden, m->final_norm, shape.hidden, rows, 1.0f,
-                                         1.0e-6f, normalized));
+                  float *hidden, const float *pending, uint32_t rows, float *normalized,
+                  float *staging, float *logits) {
+    launch_add_rms_norm(ctx, hidden, pending, m->final_norm, shape.hidden, rows, normalized);
     size_t offset = 0;
     for (uint32_t c = 0; c < m->head_chunks; ++c) {
         const adi_hip_head_chunk &h = m->head[c];
@@ -119,11 +120,12 @@ void decode_rows(adi_hip_context *ctx, const adi_hip_model *m, const ModelShape 
     ws.used = 0;
     const size_t rows = batch;
     const bool staged = logits != nullptr && batch > 1 && m->head_chunks > 1;
-    ws.ensure(Workspace::round(rows * 4) + Workspace::round(rows * shape.hidden * 4) * 2 +
+    ws.ensure(Workspace::round(rows * 4) + Workspace::round(rows * shape.hidden * 4) * 3 +
               (staged ? Workspace::round(rows * shape.widest_chunk * 4) : 0));
     uint32_t *device_tokens = ws.take<uint32_t>(rows);
     float *hidden = ws.take<float>(rows * shape.hidden);
     float *normalized = ws.take<float>(rows * shape.hidden);
+    float *moe_rows = ws.take<float>(rows * shape.hidden);
     float *staging = staged ? ws.take<float>(rows * shape.widest_chunk) : nullptr;
     upload_tokens(ctx, device_tokens, tokens, batch);
     forward_status(ctx, adi_hip_embedding_rows(ctx, m->embedding, device_tokens, batch, hidden));
@@ -132,14 +134,18 @@ void decode_rows(adi_hip_context *ctx, const adi_hip_model *m, const ModelShape 
     for (uint32_t b = 0; b < batch; ++b) {
         positions[b] = states[b].position;
     }
+    // each layer's MoE rows are added by the next layer's first norm, the
+    // last layer's by the final norm (not at all without logits: nothing
+    // reads the hidden rows then)
     for (uint32_t l = 0; l < m->layers; ++l) {
         for (uint32_t b = 0; b < batch; ++b) {
             layer_states[b] = &states[b].layers[l];
         }
-        decoder_rows(ctx, &m->layer[l], batch, hidden, layer_states.data(), positions.data());
+        decoder_rows(ctx, &m->layer[l], batch, hidden, l > 0 ? moe_rows : nullptr, moe_rows,
+                     layer_states.data(), positions.data());
     }
     if (logits != nullptr) {
-        model_logits(ctx, m, shape, hidden, batch, normalized, staging, logits);
+        model_logits(ctx, m, shape, hidden, moe_rows, batch, normalized, staging, logits);
     }
 }
 
@@ -190,10 +196,11 @@ int adi_hip_prefill(adi_hip_context *ctx, const adi_hip_model *model, const uint
         ws.used = 0;
         const uint32_t rows = count < chunk ? count : chunk;
         ws.ensure(Workspace::round(size_t(count) * 4) +
-                  Workspace::round(size_t(rows) * shape.hidden * 4) +
+                  Workspace::round(size_t(rows) * shape.hidden * 4) * 2 +
                   Workspace::round(size_t(shape.hidden) * 4));
         uint32_t *device_tokens = ws.take<uint32_t>(count);
         float *hidden = ws.take<float>(size_t(rows) * shape.hidden);
+        float *moe_rows = ws.take<float>(size_t(rows) * shape.hidden);
         float *normalized = ws.take<float>(shape.hidden);
         const uint32_t start = state->position;
         upload_tokens(ctx, device_tokens, tokens, count);
@@ -203,12 +210,14 @@ int adi_hip_prefill(adi_hip_context *ctx, const adi_hip_model *model, const uint
             forward_status(ctx, adi_hip_embedding_rows(ctx, model->embedding, device_tokens + offset,
                                                        n, hidden));
             for (uint32_t l = 0; l < model->layers; ++l) {
-                prefill_chunk(ctx, &model->layer[l], start + offset, n, hidden, &state->layers[l]);
+                prefill_chunk(ctx, &model->layer[l], start + offset, n, hidden,
+                              l > 0 ? moe_rows : nullptr, moe_rows, &state->layers[l]);
             }
         }
         if (logits != nullptr) {
-            model_logits(ctx, model, shape, hidden + size_t(n - 1) * shape.hidden, 1, normalized,
-                         nullptr, logits);
+            const size_t last = size_t(n - 1) * shape.hidden;
+            model_logits(ctx, model, shape, hidden + last, moe_rows + last, 1, normalized, nullptr,
+                         logits);
         }
         state->position += count;
     });
