@@ -8,12 +8,13 @@
 namespace adi_hip {
 
 // Batches from which the MoE block runs its projections as MFMA GEMMs
-// instead of the decode-GEMV (its routed slots hold a few positions each
-// below this), and from which a single expert or NE projection does: an NE
-// matrix from 8 rows (MFMA 2048 x 2048: 22.8 us at 8 rows and 22.9 at 16,
-// against 30.3 and 31.4 for the GEMV, which decodes per row), an expert
-// matrix from 16 (512 x 2048: 35.8 against 39.8 us; 27.0 against 35.3 at 8).
-constexpr uint32_t kMfmaBatch = 64;
+// instead of the decode-GEMV (the 256-expert layer at 8 rows: 111 against
+// 122 us, at 16 rows 154 against 189, at 32 rows 203 against 308), and from
+// which a single expert or NE projection does: an NE matrix from 8 rows
+// (MFMA 2048 x 2048: 22.8 us at 8 rows and 22.9 at 16, against 30.3 and 31.4
+// for the GEMV, which decodes per row), an expert matrix from 16 (512 x
+// 2048: 35.8 against 39.8 us; 27.0 against 35.3 at 8).
+constexpr uint32_t kMfmaBatch = 8;
 constexpr uint32_t kNeMfmaBatch = 8;
 constexpr uint32_t kExpertMfmaBatch = 16;
 
