@@ -25,10 +25,9 @@ def run_head(gpu, h, x):
 
 @pytest.mark.parametrize("isa", [1, 8, 16])
 @pytest.mark.parametrize("rows,columns,protected,batch", [
-    (1, 64, 0, 1), (37, 128, 0, 3), (1000, 2048, 3, 4), (3000, 192, 2, 2), (151936, 2048, 0, 1)])
+    (1, 64, 0, 1), (37, 128, 0, 3), (1000, 2048, 3, 4), (3000, 192, 2, 2), (151936, 2048, 0, 1),
+    (151936, 2048, 0, 4)])
 def test_head_logits_and_argmax(gpu, oracle, isa, rows, columns, protected, batch):
-    if rows > 100000 and isa != 16:
-        pytest.skip("full-vocabulary head is checked in the AVX-512 order")
     rng = syn.rng_for(1, rows + columns + protected)
     h = syn.head_chunk(rng, rows, columns, protected)
     x = syn.rms_normalized(syn.hidden_states(rng, batch, columns))
