@@ -254,7 +254,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
 }
 
 // Register-tiled form of the same order for batches of many tokens: a block
-// of 128 threads holds 16 tokens x 16 rows; thread (lane l, tile group)
+// of 128 threads holds BLOCK tokens x BLOCK rows (16, or 8 where 16 would
+// leave most CUs idle); thread (lane l, tile group)
 // carries the chains of lane l for T tokens x R rows, so each operand read
 // from LDS feeds T or R multiply-adds. K is staged 256 columns at a time,
 // transposed to [token or row][lane][step] with a padded pitch, so a thread
@@ -263,42 +264,50 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
 // lane order from 0.0f, exactly as above. Needs columns % 256 == 0 and
 // 16-byte aligned operands.
 constexpr uint32_t kTiledChunk = 256;
-constexpr uint32_t kTiledBlock = 16;  // tokens and rows per block
 
-template <int LANES>
+template <int LANES, uint32_t BLOCK>
 struct TiledShape {
     static constexpr uint32_t groups = 128 / LANES;                    // tile groups per lane
     static constexpr uint32_t token_groups = LANES == 16 ? 2 : 4;
     static constexpr uint32_t row_groups = groups / token_groups;      // 4
-    static constexpr uint32_t T = kTiledBlock / token_groups;          // tokens per thread
-    static constexpr uint32_t R = kTiledBlock / row_groups;            // rows per thread
+    static constexpr uint32_t T = BLOCK / token_groups;                // tokens per thread
+    static constexpr uint32_t R = BLOCK / row_groups;                  // rows per thread
     static constexpr uint32_t steps = kTiledChunk / LANES;             // chunk steps per lane
     static constexpr uint32_t pitch = steps + 4;                       // floats per [.][lane] row
 };
 
-template <int LANES, bool FUSED>
+template <int LANES, bool FUSED, uint32_t BLOCK>
 __global__ __launch_bounds__(128) void k_bf16_tiled(
     const uint16_t *__restrict__ w, uint32_t rows, const uint16_t *__restrict__ w_extra,
     uint32_t columns, const float *__restrict__ x, uint32_t batch, float *__restrict__ out,
     float *__restrict__ out_extra) {
 #pragma clang fp contract(off)
-    using S = TiledShape<LANES>;
-    __shared__ float xs[kTiledBlock][LANES][S::pitch];
-    __shared__ float ws[kTiledBlock][LANES][S::pitch];
+    using S = TiledShape<LANES, BLOCK>;
+    __shared__ float xs[BLOCK][LANES][S::pitch];
+    __shared__ float ws[BLOCK][LANES][S::pitch];
     const uint32_t total_rows = rows + (w_extra != nullptr ? 1u : 0u);
     // XCD-aware tiles: blocks are dealt to the eight XCDs round robin, so
-    // block id goes to XCD id % 8; XCD x takes token tiles x, x + 8, ... with
-    // every row tile, and its L2 holds only its own tokens (and the weights,
-    // which every XCD needs) instead of every token
-    const uint32_t row_tiles = (total_rows + kTiledBlock - 1u) / kTiledBlock;
-    const uint32_t token_tiles = (batch + kTiledBlock - 1u) / kTiledBlock;
+    // block id goes to XCD id % 8. With at least eight token tiles XCD x
+    // takes token tiles x, x + 8, ... with every row tile, and its L2 holds
+    // only its own tokens (and the weights, which every XCD needs); with
+    // fewer it takes row tiles x, x + 8, ... with every token tile, so no
+    // XCD idles and each reads an eighth of the weights
+    const uint32_t row_tiles = (total_rows + BLOCK - 1u) / BLOCK;
+    const uint32_t token_tiles = (batch + BLOCK - 1u) / BLOCK;
     const uint32_t xcd = blockIdx.x & 7u, k = blockIdx.x >> 3;
-    const uint32_t token_tile = xcd + 8u * (k / row_tiles);
-    if (token_tile >= token_tiles) {
+    uint32_t token_tile, row_tile;
+    if (token_tiles >= 8u) {
+        token_tile = xcd + 8u * (k / row_tiles);
+        row_tile = k % row_tiles;
+    } else {
+        row_tile = xcd + 8u * (k / token_tiles);
+        token_tile = k % token_tiles;
+    }
+    if (token_tile >= token_tiles || row_tile >= row_tiles) {
         return;  // the whole block, before any barrier
     }
-    const uint32_t row0 = (k % row_tiles) * kTiledBlock;
-    const uint32_t t0 = token_tile * kTiledBlock;
+    const uint32_t row0 = row_tile * BLOCK;
+    const uint32_t t0 = token_tile * BLOCK;
     const uint32_t lane = threadIdx.x % LANES;
     const uint32_t group = threadIdx.x / LANES;
     const uint32_t tg = group / S::row_groups, rg = group % S::row_groups;
@@ -315,19 +324,20 @@ __global__ __launch_bounds__(128) void k_bf16_tiled(
         }
     }
     // chunk c + 1 is loaded into registers while chunk c is multiplied
-    float4 xv[8];
-    uint4 wv[4];
+    constexpr uint32_t kXU = BLOCK * 64u / 128u, kWU = BLOCK * 32u / 128u;
+    float4 xv[kXU];
+    uint4 wv[kWU];
     auto load_chunk = [&](uint32_t c0) {
 #pragma unroll
-        for (uint32_t u = 0; u < 8; ++u) {
-            const uint32_t idx = u * 128u + threadIdx.x;  // 16 tokens x 64 float4
+        for (uint32_t u = 0; u < kXU; ++u) {
+            const uint32_t idx = u * 128u + threadIdx.x;  // tokens x 64 float4
             const uint32_t t = idx >> 6, k = (idx & 63u) * 4u;
             const uint32_t tok = min(t0 + t, batch - 1u);
             xv[u] = *reinterpret_cast<const float4 *>(x + static_cast<size_t>(tok) * columns + c0 + k);
         }
 #pragma unroll
-        for (uint32_t u = 0; u < 4; ++u) {
-            const uint32_t idx = u * 128u + threadIdx.x;  // 16 rows x 32 uint4
+        for (uint32_t u = 0; u < kWU; ++u) {
+            const uint32_t idx = u * 128u + threadIdx.x;  // rows x 32 uint4
             const uint32_t r = idx >> 5, k = (idx & 31u) * 8u;
             const uint32_t row = min(row0 + r, total_rows - 1u);
             const uint16_t *src = row < rows ? w + static_cast<size_t>(row) * columns : w_extra;
@@ -336,7 +346,7 @@ __global__ __launch_bounds__(128) void k_bf16_tiled(
     };
     auto store_chunk = [&]() {
 #pragma unroll
-        for (uint32_t u = 0; u < 8; ++u) {
+        for (uint32_t u = 0; u < kXU; ++u) {
             const uint32_t idx = u * 128u + threadIdx.x;
             const uint32_t t = idx >> 6, k = (idx & 63u) * 4u;
             const float e[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
@@ -346,7 +356,7 @@ __global__ __launch_bounds__(128) void k_bf16_tiled(
             }
         }
 #pragma unroll
-        for (uint32_t u = 0; u < 4; ++u) {
+        for (uint32_t u = 0; u < kWU; ++u) {
             const uint32_t idx = u * 128u + threadIdx.x;
             const uint32_t r = idx >> 5, k = (idx & 31u) * 8u;
             const uint32_t e[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
@@ -392,26 +402,27 @@ __global__ __launch_bounds__(128) void k_bf16_tiled(
         }
     }
     // ordered lane sums: the chains go to LDS (reusing xs), then each of the
-    // block's 256 outputs is finished by one thread
+    // block's kOut outputs is finished by one thread
+    constexpr uint32_t kOut = BLOCK * BLOCK;
+    static_assert(kOut <= BLOCK * S::pitch, "lane sums must fit the x staging");
     __syncthreads();
-    float *sums = &xs[0][0][0];  // [LANES][256] (16 * LANES * pitch >= 256 * LANES floats)
+    float *sums = &xs[0][0][0];  // [LANES][kOut]
 #pragma unroll
     for (uint32_t t = 0; t < S::T; ++t) {
 #pragma unroll
         for (uint32_t r = 0; r < S::R; ++r) {
-            sums[lane * 256u + (tg * S::T + t) * kTiledBlock + rg * S::R + r] = acc[t][r];
+            sums[lane * kOut + (tg * S::T + t) * BLOCK + rg * S::R + r] = acc[t][r];
         }
     }
     __syncthreads();
 #pragma unroll
-    for (uint32_t h = 0; h < 2; ++h) {
-        const uint32_t o = h * 128u + threadIdx.x;
-        const uint32_t t = o / kTiledBlock, r = o % kTiledBlock;
+    for (uint32_t o = threadIdx.x; o < kOut; o += 128u) {
+        const uint32_t t = o / BLOCK, r = o % BLOCK;
         const uint32_t tok = t0 + t, row = row0 + r;
         if (tok < batch && row < total_rows) {
             float sum = 0.0f;
             for (uint32_t j = 0; j < LANES; ++j) {
-                sum = sum + sums[j * 256u + o];
+                sum = sum + sums[j * kOut + o];
             }
             if (row < rows) {
                 out[static_cast<size_t>(tok) * rows + row] = sum;
@@ -782,14 +793,20 @@ void launch_bf16_ordered_extra(adi_hip_context *ctx, const uint16_t *w, uint32_t
     if ((lanes == 8 || lanes == 16) && batch >= kTiledBatch && columns % kTiledChunk == 0 &&
         (addresses & 15u) == 0) {
         // one dimension: the kernel maps block ids to (row tile, token tile)
-        // per XCD
-        const dim3 grid(8u * ceil_div(ceil_div(batch, kTiledBlock), 8u) * ceil_div(total, kTiledBlock));
+        // per XCD. 8 x 8 tiles up to kTiledSmallBatch tokens (257 x 2048
+        // router: 16.2 -> 8.0 us at 32 and 64 tokens, 9.5 us at 128, 12.6 at
+        // 256), 16 x 16 above (both 20.6 us at 512)
+        const bool small = batch <= kTiledSmallBatch;
+        const uint32_t block = small ? 8u : 16u;
+        const uint32_t token_tiles = ceil_div(batch, block), row_tiles = ceil_div(total, block);
+        const dim3 grid(token_tiles >= 8u ? 8u * ceil_div(token_tiles, 8u) * row_tiles
+                                          : 8u * ceil_div(row_tiles, 8u) * token_tiles);
         if (lanes == 8) {
-            launch(ctx, "router", k_bf16_tiled<8, false>, grid, dim3(128), 0, w, rows, w_extra,
-                   columns, x, batch, out, out_extra);
+            launch(ctx, "router", small ? k_bf16_tiled<8, false, 8> : k_bf16_tiled<8, false, 16>,
+                   grid, dim3(128), 0, w, rows, w_extra, columns, x, batch, out, out_extra);
         } else {
-            launch(ctx, "router", k_bf16_tiled<16, true>, grid, dim3(128), 0, w, rows, w_extra,
-                   columns, x, batch, out, out_extra);
+            launch(ctx, "router", small ? k_bf16_tiled<16, true, 8> : k_bf16_tiled<16, true, 16>,
+                   grid, dim3(128), 0, w, rows, w_extra, columns, x, batch, out, out_extra);
         }
         return;
     }

@@ -64,6 +64,7 @@ void launch_add_rms_norm(adi_hip_context *ctx, float *rows_in_out, const float *
 
 constexpr uint32_t kMaxExperts = 1024;
 constexpr uint32_t kTiledBatch = 32;  // batches from which the bf16 products run register-tiled
+constexpr uint32_t kTiledSmallBatch = 256;  // and up to which with 8 x 8 tiles
 constexpr uint32_t kRouteBatch = 16;  // largest batch launch_route handles in one block
 
 }  // namespace adi_hip

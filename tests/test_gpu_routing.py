@@ -19,8 +19,11 @@ def bits(a):
 @pytest.mark.parametrize("rows,columns,batch", [(256, 2048, 1), (256, 2048, 5), (1, 2048, 3),
                                                 (4, 67, 2), (37, 13, 9), (256, 2048, 128),
                                                 # register-tiled path: partial row and token
-                                                # blocks, several K chunks
-                                                (37, 512, 45), (256, 4096, 33), (20, 256, 64)])
+                                                # blocks, several K chunks; 8 x 8 tiles dealt
+                                                # by row tiles (under 8 token tiles) and by
+                                                # token tiles, then 16 x 16 tiles past 256
+                                                (37, 512, 45), (256, 4096, 33), (20, 256, 64),
+                                                (37, 512, 70), (37, 512, 300)])
 def test_bf16_matmul_bit_exact(gpu, oracle, isa, rows, columns, batch):
     rng = syn.rng_for(2, rows * 31 + columns + batch)
     w = syn.bf16_bits_rne(rng.normal(0, 0.02, (rows, columns)).astype(np.float32))
