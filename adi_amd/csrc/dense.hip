@@ -673,8 +673,22 @@ __global__ __launch_bounds__(1024) void k_route_finalize(RouteSort a, uint32_t c
     const uint32_t t = threadIdx.x;
     const uint32_t E = a.experts;
     const uint32_t cells = chunks * E;
-    for (uint32_t i = t; i < cells; i += blockDim.x) {
-        base[i] = a.chunk_hist[i];
+    // kStage loads in flight per thread before their LDS stores
+    constexpr uint32_t kStage = 8;
+    for (uint32_t i0 = t; i0 < cells; i0 += kStage * blockDim.x) {
+        uint32_t v[kStage];
+#pragma unroll
+        for (uint32_t u = 0; u < kStage; ++u) {
+            const uint32_t i = i0 + u * blockDim.x;
+            v[u] = i < cells ? a.chunk_hist[i] : 0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kStage; ++u) {
+            const uint32_t i = i0 + u * blockDim.x;
+            if (i < cells) {
+                base[i] = v[u];
+            }
+        }
     }
     __syncthreads();
     // thread (q, e) = (t / E, t % E) scans chunks [q * per, (q + 1) * per)
@@ -686,10 +700,20 @@ __global__ __launch_bounds__(1024) void k_route_finalize(RouteSort a, uint32_t c
     const uint32_t c_end = scanner ? min(c_begin + per, chunks) : 0u;
     if (scanner) {
         uint32_t running = 0;
-        for (uint32_t c = c_begin; c < c_end; ++c) {
-            const uint32_t v = base[c * E + e_scan];
-            base[c * E + e_scan] = running;
-            running += v;
+        // eight chunks' counts are read before any is overwritten
+        for (uint32_t c0 = c_begin; c0 < c_end; c0 += 8u) {
+            uint32_t v[8];
+#pragma unroll
+            for (uint32_t u = 0; u < 8u; ++u) {
+                v[u] = c0 + u < c_end ? base[(c0 + u) * E + e_scan] : 0u;
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 8u; ++u) {
+                if (c0 + u < c_end) {
+                    base[(c0 + u) * E + e_scan] = running;
+                }
+                running += v[u];
+            }
         }
         part[q][e_scan] = running;
     }
@@ -739,13 +763,30 @@ __global__ __launch_bounds__(1024) void k_route_finalize(RouteSort a, uint32_t c
         }
     }
     __syncthreads();
-    for (uint32_t i = t; i < a.positions; i += blockDim.x) {
-        const uint32_t e = a.route_expert[i];
-        const uint32_t g = start[e] + base[(i / kChunk) * E + e] + a.position_rank[i];
-        a.grouped_batch[g] = i / 8u;
-        a.route_to_grouped[i] = g;
-        if (a.position_expert != nullptr) {
-            a.position_expert[g] = e;
+    // kPlace positions per thread at a time: every load of a batch is issued
+    // before its stores (the outputs may alias the inputs as far as the
+    // compiler knows, so it would not move later loads above them)
+    constexpr uint32_t kPlace = 4;
+    for (uint32_t i0 = t; i0 < a.positions; i0 += kPlace * blockDim.x) {
+        uint32_t e[kPlace], rank[kPlace];
+#pragma unroll
+        for (uint32_t u = 0; u < kPlace; ++u) {
+            const uint32_t i = i0 + u * blockDim.x;
+            const bool valid = i < a.positions;
+            e[u] = valid ? a.route_expert[i] : 0u;
+            rank[u] = valid ? a.position_rank[i] : 0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kPlace; ++u) {
+            const uint32_t i = i0 + u * blockDim.x;
+            if (i < a.positions) {
+                const uint32_t g = start[e[u]] + base[(i / kChunk) * E + e[u]] + rank[u];
+                a.grouped_batch[g] = i / 8u;
+                a.route_to_grouped[i] = g;
+                if (a.position_expert != nullptr) {
+                    a.position_expert[g] = e[u];
+                }
+            }
         }
     }
 }
