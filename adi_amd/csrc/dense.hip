@@ -264,25 +264,27 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
 // lane order from 0.0f, exactly as above. Needs columns % 256 == 0 and
 // 16-byte aligned operands.
 constexpr uint32_t kTiledChunk = 256;
+constexpr uint32_t kTiledLargeThreads = 256;  // threads of a 16 x 16 tile block
 
-template <int LANES, uint32_t BLOCK>
+template <int LANES, uint32_t BLOCK, uint32_t THREADS>
 struct TiledShape {
-    static constexpr uint32_t groups = 128 / LANES;                    // tile groups per lane
-    static constexpr uint32_t token_groups = LANES == 16 ? 2 : 4;
-    static constexpr uint32_t row_groups = groups / token_groups;      // 4
+    static constexpr uint32_t groups = THREADS / LANES;                // tile groups per lane
+    static constexpr uint32_t row_groups = 4;
+    static constexpr uint32_t token_groups = groups / row_groups;
     static constexpr uint32_t T = BLOCK / token_groups;                // tokens per thread
     static constexpr uint32_t R = BLOCK / row_groups;                  // rows per thread
     static constexpr uint32_t steps = kTiledChunk / LANES;             // chunk steps per lane
     static constexpr uint32_t pitch = steps + 4;                       // floats per [.][lane] row
 };
 
-template <int LANES, bool FUSED, uint32_t BLOCK>
-__global__ __launch_bounds__(128) void k_bf16_tiled(
+template <int LANES, bool FUSED, uint32_t BLOCK, uint32_t THREADS>
+__global__ __launch_bounds__(THREADS) void k_bf16_tiled(
     const uint16_t *__restrict__ w, uint32_t rows, const uint16_t *__restrict__ w_extra,
     uint32_t columns, const float *__restrict__ x, uint32_t batch, float *__restrict__ out,
     float *__restrict__ out_extra) {
 #pragma clang fp contract(off)
-    using S = TiledShape<LANES, BLOCK>;
+    using S = TiledShape<LANES, BLOCK, THREADS>;
+    static_assert(S::T >= 1 && S::R >= 1 && S::T * S::token_groups == BLOCK, "tile shape");
     __shared__ float xs[BLOCK][LANES][S::pitch];
     __shared__ float ws[BLOCK][LANES][S::pitch];
     const uint32_t total_rows = rows + (w_extra != nullptr ? 1u : 0u);
@@ -324,20 +326,21 @@ __global__ __launch_bounds__(128) void k_bf16_tiled(
         }
     }
     // chunk c + 1 is loaded into registers while chunk c is multiplied
-    constexpr uint32_t kXU = BLOCK * 64u / 128u, kWU = BLOCK * 32u / 128u;
+    constexpr uint32_t kXU = BLOCK * 64u / THREADS, kWU = BLOCK * 32u / THREADS;
+    static_assert(kXU >= 1 && kWU >= 1, "staging shares");
     float4 xv[kXU];
     uint4 wv[kWU];
     auto load_chunk = [&](uint32_t c0) {
 #pragma unroll
         for (uint32_t u = 0; u < kXU; ++u) {
-            const uint32_t idx = u * 128u + threadIdx.x;  // tokens x 64 float4
+            const uint32_t idx = u * THREADS + threadIdx.x;  // tokens x 64 float4
             const uint32_t t = idx >> 6, k = (idx & 63u) * 4u;
             const uint32_t tok = min(t0 + t, batch - 1u);
             xv[u] = *reinterpret_cast<const float4 *>(x + static_cast<size_t>(tok) * columns + c0 + k);
         }
 #pragma unroll
         for (uint32_t u = 0; u < kWU; ++u) {
-            const uint32_t idx = u * 128u + threadIdx.x;  // rows x 32 uint4
+            const uint32_t idx = u * THREADS + threadIdx.x;  // rows x 32 uint4
             const uint32_t r = idx >> 5, k = (idx & 31u) * 8u;
             const uint32_t row = min(row0 + r, total_rows - 1u);
             const uint16_t *src = row < rows ? w + static_cast<size_t>(row) * columns : w_extra;
@@ -347,7 +350,7 @@ __global__ __launch_bounds__(128) void k_bf16_tiled(
     auto store_chunk = [&]() {
 #pragma unroll
         for (uint32_t u = 0; u < kXU; ++u) {
-            const uint32_t idx = u * 128u + threadIdx.x;
+            const uint32_t idx = u * THREADS + threadIdx.x;
             const uint32_t t = idx >> 6, k = (idx & 63u) * 4u;
             const float e[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
 #pragma unroll
@@ -357,7 +360,7 @@ __global__ __launch_bounds__(128) void k_bf16_tiled(
         }
 #pragma unroll
         for (uint32_t u = 0; u < kWU; ++u) {
-            const uint32_t idx = u * 128u + threadIdx.x;
+            const uint32_t idx = u * THREADS + threadIdx.x;
             const uint32_t r = idx >> 5, k = (idx & 31u) * 8u;
             const uint32_t e[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
 #pragma unroll
@@ -416,7 +419,7 @@ __global__ __launch_bounds__(128) void k_bf16_tiled(
     }
     __syncthreads();
 #pragma unroll
-    for (uint32_t o = threadIdx.x; o < kOut; o += 128u) {
+    for (uint32_t o = threadIdx.x; o < kOut; o += THREADS) {
         const uint32_t t = o / BLOCK, r = o % BLOCK;
         const uint32_t tok = t0 + t, row = row0 + r;
         if (tok < batch && row < total_rows) {
@@ -834,20 +837,22 @@ void launch_bf16_ordered_extra(adi_hip_context *ctx, const uint16_t *w, uint32_t
     if ((lanes == 8 || lanes == 16) && batch >= kTiledBatch && columns % kTiledChunk == 0 &&
         (addresses & 15u) == 0) {
         // one dimension: the kernel maps block ids to (row tile, token tile)
-        // per XCD. 8 x 8 tiles up to kTiledSmallBatch tokens (257 x 2048
-        // router: 16.2 -> 8.0 us at 32 and 64 tokens, 9.5 us at 128, 12.6 at
-        // 256), 16 x 16 above (both 20.6 us at 512)
+        // per XCD. 8 x 8 tiles of 128 threads up to kTiledSmallBatch tokens
+        // (257 x 2048 router: 16.2 -> 8.0 us at 32 and 64 tokens, 9.5 us at
+        // 128, 12.6 at 256), 16 x 16 tiles of 256 threads above (21.3 us at
+        // 512 tokens with 128 threads, 17.4 with 256; 8 x 8: 20.7)
         const bool small = batch <= kTiledSmallBatch;
         const uint32_t block = small ? 8u : 16u;
         const uint32_t token_tiles = ceil_div(batch, block), row_tiles = ceil_div(total, block);
         const dim3 grid(token_tiles >= 8u ? 8u * ceil_div(token_tiles, 8u) * row_tiles
                                           : 8u * ceil_div(row_tiles, 8u) * token_tiles);
+        const uint32_t threads = small ? 128u : kTiledLargeThreads;
         if (lanes == 8) {
-            launch(ctx, "router", small ? k_bf16_tiled<8, false, 8> : k_bf16_tiled<8, false, 16>,
-                   grid, dim3(128), 0, w, rows, w_extra, columns, x, batch, out, out_extra);
+            launch(ctx, "router", small ? k_bf16_tiled<8, false, 8, 128> : k_bf16_tiled<8, false, 16, kTiledLargeThreads>,
+                   grid, dim3(threads), 0, w, rows, w_extra, columns, x, batch, out, out_extra);
         } else {
-            launch(ctx, "router", small ? k_bf16_tiled<16, true, 8> : k_bf16_tiled<16, true, 16>,
-                   grid, dim3(128), 0, w, rows, w_extra, columns, x, batch, out, out_extra);
+            launch(ctx, "router", small ? k_bf16_tiled<16, true, 8, 128> : k_bf16_tiled<16, true, 16, kTiledLargeThreads>,
+                   grid, dim3(threads), 0, w, rows, w_extra, columns, x, batch, out, out_extra);
         }
         return;
     }
