@@ -133,9 +133,9 @@ __device__ __forceinline__ void bf16_chains(const uint16_t *wr, const float *xs,
     }
 }
 
-// One wave per block: registers for a whole staging round (24 16-byte loads
-// in flight) matter more than occupancy.
-template <int LANES, bool FUSED>
+// One wave per block: registers for a whole staging round (16 + XB 16-byte
+// loads in flight) matter more than occupancy.
+template <int LANES, bool FUSED, uint32_t XB>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_bf16_lds(
     const uint16_t *__restrict__ w, uint32_t rows, const uint16_t *__restrict__ w_extra,
     uint32_t columns, const float *__restrict__ x, uint32_t batch, float *__restrict__ out,
@@ -154,12 +154,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
                                 reinterpret_cast<uintptr_t>(w_extra);
     if ((columns % 8u) == 0 && (addresses & 15u) == 0) {
         // 16-byte staging in rounds: every load of a round (16 of the
-        // weight rows, 8 of the tokens; one round for a 4 x 2048 block and one
-        // token) is issued before the first LDS store, so the block waits for
-        // memory once per round. Indexes past the end are clamped to the last
+        // weight rows, XB of the tokens: 8 for one token, 32 for four; one
+        // round for a 4 x 2048 block) is issued before the first LDS store,
+        // so the block waits for memory once per round (with 8 token loads a
+        // round, four tokens took four rounds: 257 x 2048 at 4 tokens
+        // 10.6 -> 6.8 us, at 16 tokens 10.7 -> 7.0). Indexes past the end are clamped to the last
         // element: those lanes load it and store the same value again, so
         // nothing is guarded.
-        constexpr uint32_t kWBatch = 16, kXBatch = 8;
+        constexpr uint32_t kWBatch = 16, kXBatch = XB;
         const uint32_t w_per_row = columns / 8u;
         const uint32_t w_total = rows_here * w_per_row;
         const uint32_t x_per_row = columns / 4u;
@@ -863,10 +865,12 @@ void launch_bf16_ordered_extra(adi_hip_context *ctx, const uint16_t *w, uint32_t
     // dynamic plus the kernel's static 1 KiB must fit the 64 KiB default
     if (lanes != 1 && lds + 1024 <= 65536) {
         if (lanes == 8) {
-            launch(ctx, "router", k_bf16_lds<8, false>, dim3(ceil_div(total, rpb), tokens.x),
+            launch(ctx, "router", batch == 1 ? k_bf16_lds<8, false, 8> : k_bf16_lds<8, false, 32>,
+                   dim3(ceil_div(total, rpb), tokens.x),
                    dim3(64), lds, w, rows, w_extra, columns, x, batch, out, out_extra);
         } else {
-            launch(ctx, "router", k_bf16_lds<16, true>, dim3(ceil_div(total, rpb), tokens.x),
+            launch(ctx, "router", batch == 1 ? k_bf16_lds<16, true, 8> : k_bf16_lds<16, true, 32>,
+                   dim3(ceil_div(total, rpb), tokens.x),
                    dim3(64), lds, w, rows, w_extra, columns, x, batch, out, out_extra);
         }
         return;
