@@ -517,23 +517,22 @@ __device__ __forceinline__ void sum_slices(const float *src, size_t stride, uint
     for (int i = 0; i < VPL; ++i) {
         v[i] = 0.0f;
     }
-    constexpr uint32_t kRound = VPL > 32 ? 1u : 2u;
+    // slices loaded per round: four for short vectors (the registers of the
+    // at-once path above), two up to 2048 elements, one beyond
+    constexpr uint32_t kRound = VPL > 32 ? 1u : (VPL <= 8 ? 4u : 2u);
     for (uint32_t s = 0; s < splits; s += kRound) {
-        // a missing second slice reloads the first and adds zero
-        const bool second = kRound == 2 && s + 1 < splits;
-        float a[VPL], b[VPL];
-        load_wave<VPL, COHERENT>(src + s * stride, lane, a);
-        if constexpr (kRound == 2) {
-            load_wave<VPL, COHERENT>(src + (second ? s + 1 : s) * stride, lane, b);
+        // a missing later slice reloads the round's first and adds nothing
+        float a[kRound][VPL];
+#pragma unroll
+        for (uint32_t q = 0; q < kRound; ++q) {
+            load_wave<VPL, COHERENT>(src + (s + q < splits ? s + q : s) * stride, lane, a[q]);
         }
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            b[i] = second ? b[i] : 0.0f;
-        }
+        for (uint32_t q = 0; q < kRound; ++q) {
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            v[i] = v[i] + a[i];
-            v[i] = v[i] + b[i];
+            for (int i = 0; i < VPL; ++i) {
+                v[i] = s + q < splits ? v[i] + a[q][i] : v[i];
+            }
         }
     }
 }
