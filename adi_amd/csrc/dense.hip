@@ -158,9 +158,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
         // round for a 4 x 2048 block) is issued before the first LDS store,
         // so the block waits for memory once per round (with 8 token loads a
         // round, four tokens took four rounds: 257 x 2048 at 4 tokens
-        // 10.6 -> 6.8 us, at 16 tokens 10.7 -> 7.0). Indexes past the end are clamped to the last
-        // element: those lanes load it and store the same value again, so
-        // nothing is guarded.
+        // 10.6 -> 6.8 us, at 16 tokens 10.7 -> 7.0). Indexes past the end
+        // are clamped to the last element: those lanes load it and store the
+        // same value again, so nothing is guarded.
         constexpr uint32_t kWBatch = 16, kXBatch = XB;
         const uint32_t w_per_row = columns / 8u;
         const uint32_t w_total = rows_here * w_per_row;
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
 }
 
 // Register-tiled form of the same order for batches of many tokens: a block
-// of 128 threads holds BLOCK tokens x BLOCK rows (16, or 8 where 16 would
+// of THREADS threads holds BLOCK tokens x BLOCK rows (16, or 8 where 16 would
 // leave most CUs idle); thread (lane l, tile group)
 // carries the chains of lane l for T tokens x R rows, so each operand read
 // from LDS feeds T or R multiply-adds. K is staged 256 columns at a time,
