@@ -23,7 +23,9 @@ def bits(a):
                                                 # by row tiles (under 8 token tiles) and by
                                                 # token tiles, then 16 x 16 tiles past 256
                                                 (37, 512, 45), (256, 4096, 33), (20, 256, 64),
-                                                (37, 512, 70), (37, 512, 300)])
+                                                (37, 512, 70), (37, 512, 300),
+                                                # either side of the tile-shape switch
+                                                (20, 256, 256), (20, 256, 257)])
 def test_bf16_matmul_bit_exact(gpu, oracle, isa, rows, columns, batch):
     rng = syn.rng_for(2, rows * 31 + columns + batch)
     w = syn.bf16_bits_rne(rng.normal(0, 0.02, (rows, columns)).astype(np.float32))
