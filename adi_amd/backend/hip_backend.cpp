@@ -7,12 +7,15 @@
 // model file (include/adi/kernels.hpp:9-77) and never change while mapped, so
 // their device copies are cached by host address and shape, as ExpertScratch
 // caches the derived tables by source pointer (src/kernels.cpp:33-94). Each
-// entry also keeps a fingerprint of sampled contents: a different buffer met
-// at the same address replaces the entry (its device copies are freed and
-// the new contents uploaded), so the cache holds one copy per live address.
-// hip_backend_release_weights() frees every copy; a caller that unmaps a
-// model calls it, since a new mapping at the old address whose samples all
-// match would otherwise reuse the old copy. Calls are serialised on one context:
+// entry also keeps a hash of the buffer's full contents, taken at upload and
+// compared on every call: a different buffer met at the same address (a
+// remapped model) replaces the entry (its device copies are freed and the new
+// contents uploaded), so the cache holds one copy per live address and never
+// serves stale weights. The hash reads every byte of the weights a call uses
+// (four independent 64-bit lanes, about 10-20 GB/s on one core): a parity
+// cost of this host-span path, which copies activations in and out per call
+// anyway. hip_backend_release_weights() frees every copy. Calls are serialised
+// on one context:
 // moe_forward calls the projections from worker threads
 // (src/executor.cpp:261, 1321-1371), and the GPU runs them in turn anyway.
 #include "hip_backend.hpp"
@@ -35,20 +38,40 @@ namespace {
 bool is_power_of_two(std::uint32_t v) { return v != 0 && (v & (v - 1)) == 0; }
 constexpr std::uint32_t kTile = 16;
 
-// FNV-1a over the size and 64 evenly spaced 8-byte samples of a buffer.
+// 64-bit hash of a buffer's full contents: four independent multiply-rotate
+// lanes over 8-byte words (so the loads pipeline), the tail bytes and the
+// size folded in at the end.
+inline std::uint64_t mix_lane(std::uint64_t lane, std::uint64_t word) {
+    lane ^= word * 0x9E3779B97F4A7C15ull;
+    lane = (lane << 31) | (lane >> 33);
+    return lane * 0xC2B2AE3D27D4EB4Full;
+}
+
 template <typename T>
 std::uint64_t fingerprint(std::span<const T> values) {
     const auto *bytes = reinterpret_cast<const unsigned char *>(values.data());
     const std::size_t size = values.size_bytes();
-    std::uint64_t h = 1469598103934665603ull ^ size;
-    if (size == 0) {
-        return h;
-    }
-    for (std::size_t i = 0; i < 64; ++i) {
-        const std::size_t at = size <= 8 ? 0 : (size - 8) * i / 63;
-        for (std::size_t b = 0; b < 8 && at + b < size; ++b) {
-            h = (h ^ bytes[at + b]) * 1099511628211ull;
+    std::uint64_t lane[4] = {0x243F6A8885A308D3ull, 0x13198A2E03707344ull, 0xA4093822299F31D0ull,
+                             0x082EFA98EC4E6C89ull};
+    std::size_t at = 0;
+    for (; at + 32 <= size; at += 32) {
+        std::uint64_t w[4];
+        std::memcpy(w, bytes + at, 32);
+        for (int i = 0; i < 4; ++i) {
+            lane[i] = mix_lane(lane[i], w[i]);
         }
+    }
+    std::uint64_t tail = 0;
+    for (std::size_t b = 0; at + b < size; ++b) {
+        tail |= static_cast<std::uint64_t>(bytes[at + b]) << (8 * (b & 7));
+        if ((b & 7) == 7 || at + b + 1 == size) {
+            lane[0] = mix_lane(lane[0], tail);
+            tail = 0;
+        }
+    }
+    std::uint64_t h = size * 0xFF51AFD7ED558CCDull;
+    for (int i = 0; i < 4; ++i) {
+        h = mix_lane(h ^ lane[i], static_cast<std::uint64_t>(i) + 1);
     }
     return h;
 }
@@ -107,7 +130,7 @@ class Runtime {
         check(adi_hip_copy_to_host(ctx, host.data(), device, host.size_bytes()));
     }
 
-    // An entry of a cache: the descriptor, the contents' fingerprint and the
+    // An entry of a cache: the descriptor, the contents' full hash and the
     // device buffers it owns.
     template <typename T>
     struct Entry {
@@ -117,7 +140,7 @@ class Runtime {
     };
 
     // The entry of `key`, (re)built by make(entry) when it is missing or its
-    // fingerprint differs from `fp` (the old copies are freed first).
+    // contents' hash differs from `fp` (the old copies are freed first).
     template <typename K, typename T, typename Make>
     const T &cached(std::map<K, Entry<T>> &cache, const K &key, std::uint64_t fp, Make &&make) {
         auto found = cache.find(key);

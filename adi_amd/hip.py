@@ -22,7 +22,7 @@ INVALID_ARGUMENT = -1
 OUT_OF_MEMORY = -2
 DEVICE_ERROR = -3
 OUT_OF_RANGE = -4
-NOT_FOUND = -4
+NOT_FOUND = -5
 
 GGML_F32, GGML_F16, GGML_I8, GGML_I16, GGML_I32, GGML_I64, GGML_F64, GGML_BF16 = 0, 1, 24, 25, 26, 27, 28, 30
 

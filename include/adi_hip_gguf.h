@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define ADI_HIP_NOT_FOUND (-4) /* tensor or metadata key absent (or of another type) */
+#define ADI_HIP_NOT_FOUND (-5) /* tensor or metadata key absent (or of another type) */
 
 /* GGML storage types the reader accepts (adi::GgmlType,
  * include/adi/gguf.hpp:30-39). */

@@ -112,3 +112,16 @@ def test_backend_library_exports_the_driver():
                  "bd_bf16_matmul", "bd_rms_norm"):
         assert hasattr(lib, name)
     assert bb.name(bb.CPU) in ("scalar", "avx2", "avx512")
+
+
+def test_status_codes_are_distinct_and_mirrored():
+    """Every ADI_HIP_* status a call can return has its own value, and the
+    ctypes mirror carries the same numbers, so a caller can tell them apart."""
+    text = "".join(open(h).read() for h in HEADERS)
+    codes = dict(re.findall(r"^#define ADI_HIP_(OK|[A-Z_]+_(?:ARGUMENT|MEMORY|ERROR|RANGE|FOUND))\s+\(?(-?\d+)\)?",
+                            text, re.M))
+    assert set(codes) == {"OK", "INVALID_ARGUMENT", "OUT_OF_MEMORY", "DEVICE_ERROR", "OUT_OF_RANGE", "NOT_FOUND"}
+    values = {int(v) for v in codes.values()}
+    assert len(values) == len(codes), f"status codes collide: {codes}"
+    for name, value in codes.items():
+        assert getattr(hip, name) == int(value), name

@@ -129,8 +129,9 @@ def test_backend_shape_errors_match_the_reference(batch, x_extra, out_extra):
 def test_backend_weight_cache_follows_contents():
     """The HIP table caches device copies of weights by host address. New
     contents at the same address replace the copy (results follow the new
-    weights, as the CPU table's do), and hip_backend_release_weights() drops
-    every copy; calls after it upload again."""
+    weights, as the CPU table's do), also when a single word changes, and
+    hip_backend_release_weights() drops every copy; calls after it upload
+    again."""
     rng = syn.rng_for(1, 977)
     m = syn.ne_matrix(rng, 512, 2048, syn.ne_tlut(rng))
     x = syn.hidden_states(rng, 1, 2048)
@@ -140,6 +141,16 @@ def test_backend_weight_cache_follows_contents():
     second = bb.ne_matmul(bb.HIP, m, x, 1)
     assert max_rel_error(second, bb.ne_matmul(bb.CPU, m, x, 1)) <= 1e-3
     assert not np.array_equal(first, second)
+    # one word changed between the points a sampled fingerprint would read:
+    # the copy is keyed on the full contents, so the change is seen
+    spacing = (m.trellis.nbytes - 8) // 63
+    word = (spacing + spacing // 2) // 2
+    m.trellis[word] ^= 0x5A5A
+    changed = bb.ne_matmul(bb.HIP, m, x, 1)
+    assert max_rel_error(changed, bb.ne_matmul(bb.CPU, m, x, 1)) <= 1e-3
+    assert not np.array_equal(changed, second)
+    m.trellis[word] ^= 0x5A5A
+    second = bb.ne_matmul(bb.HIP, m, x, 1)
     bb.release_weights()
     third = bb.ne_matmul(bb.HIP, m, x, 1)
     assert np.array_equal(third.view(np.uint32), second.view(np.uint32))
