@@ -572,7 +572,7 @@ const float *rope_rows(adi_hip_context *ctx, uint32_t end) {
 // A nested entry's status becomes this call's failure.
 void forward(adi_hip_context *ctx, int status) {
     if (status != ADI_HIP_OK) {
-        fail(status, ctx->last_error);
+        fail(status, ctx->last_error());
     }
 }
 

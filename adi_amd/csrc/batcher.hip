@@ -4,6 +4,7 @@
 // the thread that drives it.
 #include "context.hpp"
 
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <deque>
@@ -103,6 +104,10 @@ struct adi_hip_batcher {
     uint64_t *words = nullptr;   // device [max_batch]
     std::vector<Slot> slots;
     std::vector<Active> active;  // logits row i belongs to active[i]
+    // host-forced failures for the failure-handling tests: the next
+    // admission, or the next step's sampling, fails as a device error would
+    std::atomic<bool> fail_admission_for_testing{false};
+    std::atomic<bool> fail_step_for_testing{false};
 
     std::mutex mutex;  // guards the fields below
     std::deque<uint64_t> pending;
@@ -206,20 +211,37 @@ void admit_pending(adi_hip_batcher *b) {
     }
     Slot &s = b->slots[slot];
     const uint32_t row = static_cast<uint32_t>(b->active.size());
-    for (const auto &z : s.zeroed) {
-        check_hip(hipMemsetAsync(z.first, 0, z.second, b->ctx->stream), "sequence state clear");
-    }
-    s.state.position = 0;
+    // Any failure from here on fails this request alone (Impl::admit_pending,
+    // src/generation.cpp:520-540): the slot stays free and the loop goes on.
+    // The synchronize also reads the one-launch MoE block's error word, so a
+    // prompt whose layers ran on invalid MoE outputs is failed here instead
+    // of being sampled.
     const auto started = Clock::now();
-    const int status = adi_hip_prefill(b->ctx, &b->model, copy.prompt.data(),
-                                       static_cast<uint32_t>(copy.prompt.size()), b->ubatch,
-                                       &s.state, b->logits + static_cast<size_t>(row) * b->vocabulary);
-    if (status != ADI_HIP_OK) {
-        fail_request(b, id, b->ctx->last_error);
+    try {
+        for (const auto &z : s.zeroed) {
+            check_hip(hipMemsetAsync(z.first, 0, z.second, b->ctx->stream), "sequence state clear");
+        }
+        s.state.position = 0;
+        int status = adi_hip_prefill(b->ctx, &b->model, copy.prompt.data(),
+                                     static_cast<uint32_t>(copy.prompt.size()), b->ubatch, &s.state,
+                                     b->logits + static_cast<size_t>(row) * b->vocabulary);
+        if (status == ADI_HIP_OK) {
+            mask_rows(b, row, 1);
+            status = adi_hip_synchronize(b->ctx);
+        }
+        if (status != ADI_HIP_OK) {
+            fail(status, b->ctx->last_error());
+        }
+        if (b->fail_admission_for_testing.exchange(false)) {
+            fail(ADI_HIP_DEVICE_ERROR, "admission failure forced by the host");
+        }
+    } catch (const Failure &f) {
+        fail_request(b, id, f.message);
+        return;
+    } catch (const std::exception &e) {
+        fail_request(b, id, e.what());
         return;
     }
-    mask_rows(b, row, 1);
-    check_hip(hipStreamSynchronize(b->ctx->stream), "prefill synchronize");
     const auto finished = Clock::now();
     s.busy = true;
     b->active.push_back(Active{id, slot, limit, copy.options.temperature, copy.options.top_p,
@@ -229,6 +251,16 @@ void admit_pending(adi_hip_batcher *b) {
     r.state = ADI_HIP_REQUEST_RUNNING;
     r.max_output = limit;
     r.prefill_seconds = seconds_between(started, finished);
+}
+
+// Fails every active request with `message` and frees their slots (the
+// decode-failure branch of the worker loop, src/generation.cpp:640-652).
+void fail_active(adi_hip_batcher *b, const std::string &message) {
+    for (const Active &a : b->active) {
+        fail_request(b, a.id, message);
+        b->slots[a.slot].busy = false;
+    }
+    b->active.clear();
 }
 
 // sample_token for every active row: the greedy choice or the top-p draw,
@@ -263,17 +295,35 @@ void sample_active(adi_hip_batcher *b, std::vector<uint32_t> &chosen) {
                                       b->active[first].temperature, b->active[first].top_p,
                                       b->words + first, b->tokens + first);
         if (status != ADI_HIP_OK) {
-            fail(status, b->ctx->last_error);
+            const std::string message = b->ctx->last_error();
+            fail_active(b, message);
+            fail(status, message);
         }
         first = end;
     }
     chosen.assign(n, 0);
-    check_hip(hipMemcpyAsync(chosen.data(), b->tokens, size_t(n) * 4, hipMemcpyDeviceToHost,
-                             b->ctx->stream),
-              "token copy");
-    const int status = adi_hip_synchronize(b->ctx);
+    int status = ADI_HIP_OK;
+    if (hipMemcpyAsync(chosen.data(), b->tokens, size_t(n) * 4, hipMemcpyDeviceToHost,
+                       b->ctx->stream) != hipSuccess) {
+        status = ADI_HIP_DEVICE_ERROR;
+    }
+    // the synchronize reports a one-launch MoE wait that ran out in the last
+    // decode step: its logits are invalid, so every active request fails
+    // (their draws are spent) instead of sampling them
+    const int synced = adi_hip_synchronize(b->ctx);
+    if (status == ADI_HIP_OK && synced != ADI_HIP_OK) {
+        status = synced;
+    }
+    if (status == ADI_HIP_OK && b->fail_step_for_testing.exchange(false)) {
+        b->ctx->set_error("decode step failure forced by the host");
+        status = ADI_HIP_DEVICE_ERROR;
+    }
     if (status != ADI_HIP_OK) {
-        fail(status, b->ctx->last_error);
+        const std::string message =
+            synced != ADI_HIP_OK || b->ctx->last_error().size() > 0 ? b->ctx->last_error()
+                                                                    : std::string("token copy failed");
+        fail_active(b, message);
+        fail(status, message);
     }
 }
 
@@ -327,12 +377,8 @@ void step_active(adi_hip_batcher *b) {
     const int status = adi_hip_decode_batch(b->ctx, &b->model, next_tokens.data(), n,
                                             next_states.data(), b->logits);
     if (status != ADI_HIP_OK) {
-        const std::string message = b->ctx->last_error;
-        for (const Active &a : b->active) {
-            fail_request(b, a.id, message);
-            b->slots[a.slot].busy = false;
-        }
-        b->active.clear();
+        const std::string message = b->ctx->last_error();
+        fail_active(b, message);
         fail(status, message);
     }
     for (uint32_t i = 0; i < n; ++i) {
@@ -520,6 +566,19 @@ const char *adi_hip_batcher_request_error(adi_hip_batcher *b, uint64_t request) 
     std::lock_guard<std::mutex> lock(b->mutex);
     auto it = b->requests.find(request);
     return it == b->requests.end() ? "" : it->second.error.c_str();
+}
+
+int adi_hip_batcher_force_failure(adi_hip_batcher *b, int where) {
+    if (b == nullptr ||
+        (where != ADI_HIP_BATCHER_FAIL_ADMISSION && where != ADI_HIP_BATCHER_FAIL_STEP)) {
+        return ADI_HIP_INVALID_ARGUMENT;
+    }
+    if (where == ADI_HIP_BATCHER_FAIL_ADMISSION) {
+        b->fail_admission_for_testing = true;
+    } else {
+        b->fail_step_for_testing = true;
+    }
+    return ADI_HIP_OK;
 }
 
 int adi_hip_batcher_release(adi_hip_batcher *b, uint64_t request) {

@@ -202,7 +202,7 @@ const char *adi_hip_last_error(const adi_hip_context *ctx) {
         std::lock_guard<std::mutex> lock(g_create_error_mutex);
         return g_create_error.c_str();
     }
-    return ctx->last_error.c_str();
+    return const_cast<adi_hip_context *>(ctx)->last_error_cstr();
 }
 
 int adi_hip_set_stream(adi_hip_context *ctx, void *stream) {

@@ -6,8 +6,11 @@
 
 #include <cmath>
 #include <exception>
+#include <mutex>
 #include <new>
 #include <string>
+#include <thread>
+#include <unordered_map>
 #include <utility>
 #include <vector>
 
@@ -76,7 +79,27 @@ struct adi_hip_context {
     hipStream_t stream = nullptr;
     uint32_t isa_lanes = 16;
     int cu_count = 256;
-    std::string last_error;
+    // Message of the last failed call, kept per calling thread: a batcher's
+    // submit, cancel and status calls may run on other threads while one
+    // thread steps it, and each thread reads back only its own calls'
+    // messages. Map nodes are stable, so a returned c_str() stays valid until
+    // that thread's next call on the context.
+    std::mutex error_mutex;
+    std::unordered_map<std::thread::id, std::string> errors;
+
+    void set_error(std::string message) {
+        std::lock_guard<std::mutex> lock(error_mutex);
+        errors[std::this_thread::get_id()] = std::move(message);
+    }
+    std::string last_error() {
+        std::lock_guard<std::mutex> lock(error_mutex);
+        auto it = errors.find(std::this_thread::get_id());
+        return it == errors.end() ? std::string() : it->second;
+    }
+    const char *last_error_cstr() {
+        std::lock_guard<std::mutex> lock(error_mutex);
+        return errors[std::this_thread::get_id()].c_str();
+    }
     adi_hip::Workspace workspace;
     // scratch of the layer-level entries (attention), kept apart from
     // `workspace`, which every projection entry they call resets
@@ -147,16 +170,16 @@ int guarded(adi_hip_context *ctx, F &&function) {
     try {
         DeviceScope scope(ctx->device);
         function();
-        ctx->last_error.clear();
+        ctx->set_error(std::string());
         return ADI_HIP_OK;
     } catch (const Failure &failure) {
-        ctx->last_error = failure.message;
+        ctx->set_error(failure.message);
         return failure.status;
     } catch (const std::bad_alloc &) {
-        ctx->last_error = "host allocation failed";
+        ctx->set_error("host allocation failed");
         return ADI_HIP_OUT_OF_MEMORY;
     } catch (const std::exception &error) {
-        ctx->last_error = error.what();
+        ctx->set_error(error.what());
         return ADI_HIP_DEVICE_ERROR;
     }
 }

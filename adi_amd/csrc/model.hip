@@ -43,7 +43,7 @@ void upload_tokens(adi_hip_context *ctx, uint32_t *dst, const uint32_t *tokens, 
 
 void forward_status(adi_hip_context *ctx, int status) {
     if (status != ADI_HIP_OK) {
-        fail(status, ctx->last_error);
+        fail(status, ctx->last_error());
     }
 }
 

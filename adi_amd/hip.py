@@ -197,6 +197,7 @@ SIGNATURES = [
     ("adi_hip_batcher_status", C.c_int, [vp, u64, C.POINTER(RequestStatus), C.POINTER(u32), u32]),
     ("adi_hip_batcher_request_error", C.c_char_p, [vp, u64]),
     ("adi_hip_batcher_release", C.c_int, [vp, u64]),
+    ("adi_hip_batcher_force_failure", C.c_int, [vp, C.c_int]),
     ("adi_hip_profiling_enable", C.c_int, [vp, C.c_int]),
     ("adi_hip_profiling_read", C.c_int, [vp, C.POINTER(KernelProfile), u32, C.POINTER(u32)]),
     # include/adi_hip_gguf.h

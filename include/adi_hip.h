@@ -612,6 +612,17 @@ int adi_hip_batcher_status(adi_hip_batcher *batcher, uint64_t request,
 const char *adi_hip_batcher_request_error(adi_hip_batcher *batcher, uint64_t request);
 /* Forgets a finished or failed request. */
 int adi_hip_batcher_release(adi_hip_batcher *batcher, uint64_t request);
+/* Failure injection for tests of the loop's failure handling; no counterpart
+ * in the reference, whose tests throw from a stub model instead. `where` =
+ * ADI_HIP_BATCHER_FAIL_ADMISSION makes the next admission fail after its
+ * prefill, as a device error there would (that request alone fails and its
+ * slot stays free); ADI_HIP_BATCHER_FAIL_STEP makes the next step's sampling
+ * fail after its synchronize, as a one-launch MoE wait that ran out would
+ * (every active request fails, the step returns the error). Nothing faults:
+ * the device work runs normally and the host reports the failure. */
+#define ADI_HIP_BATCHER_FAIL_ADMISSION 1
+#define ADI_HIP_BATCHER_FAIL_STEP 2
+int adi_hip_batcher_force_failure(adi_hip_batcher *batcher, int where);
 
 /* ---- kernel profiling ----------------------------------------------------- */
 

@@ -141,6 +141,67 @@ def test_stop_token_cancel_and_failures(ctx, oracle, parts):
         b.close()
 
 
+def test_forced_failures_leave_the_loop_consistent(ctx, oracle, parts):
+    """Failures forced from the host (no kernel faults): a failed admission
+    fails that request alone and leaves its slot free; a failed step (as a
+    one-launch MoE wait that ran out would report at the step's synchronize)
+    fails every active request, returns the error, and frees every slot, so
+    the next request is admitted and decodes along the oracle's path."""
+    b = serving.ContinuousBatcher(ctx, parts["two"], max_batch=2, capacity=CAPACITY,
+                                  masked_tokens=MASKED, start=False)
+    try:
+        lib = ctx.lib
+        assert lib.adi_hip_batcher_force_failure(b.handle, 3) == hip.INVALID_ARGUMENT
+        ctx.check(lib.adi_hip_batcher_force_failure(b.handle, 1))
+        a = b.submit([5, 6], max_output_tokens=3, temperature=0.0)
+        assert b.step() == 0
+        with pytest.raises(serving.GenerationError, match="admission failure forced by the host"):
+            b.result(a)
+        first = b.submit([7], max_output_tokens=6, temperature=0.0)
+        second = b.submit([8, 9], max_output_tokens=6, temperature=0.0)
+        b.step()
+        b.step()  # both admitted, one token each so far
+        assert b.status(first)[0] == serving.RUNNING and b.status(second)[0] == serving.RUNNING
+        ctx.check(lib.adi_hip_batcher_force_failure(b.handle, 2))
+        with pytest.raises(hip.HipError, match="decode step failure forced by the host"):
+            b.step()
+        for r in (first, second):
+            assert b.status(r)[0] == serving.FAILED
+            with pytest.raises(serving.GenerationError, match="decode step failure forced"):
+                b.result(r)
+        after = b.submit([7], max_output_tokens=4, temperature=0.0)
+        while b.step() != 0:
+            pass
+        r = b.result(after)
+        assert r.output_tokens == 4
+        compared, _ = check_path(oracle, parts, [7], r.tokens, 0.0, 0.9, 0)
+        assert compared >= len(r.tokens) - 1
+    finally:
+        b.close()
+
+
+def test_error_messages_are_per_thread(ctx):
+    """A failed call on one thread leaves the context's message on other
+    threads alone: a batcher's submit may fail on a client thread while the
+    stepping thread's own calls succeed (adi_hip_last_error reads back the
+    calling thread's last call)."""
+    ctx.synchronize()
+    seen = {}
+
+    def failing():
+        status = ctx.lib.adi_hip_set_reduction_isa(ctx.handle, 3)
+        seen["status"] = status
+        seen["message"] = ctx.lib.adi_hip_last_error(ctx.handle).decode()
+
+    t = threading.Thread(target=failing)
+    t.start()
+    t.join()
+    assert seen["status"] == hip.INVALID_ARGUMENT and seen["message"] != ""
+    assert ctx.lib.adi_hip_last_error(ctx.handle).decode() == ""
+    ctx.check(ctx.lib.adi_hip_synchronize(ctx.handle))
+    assert ctx.lib.adi_hip_last_error(ctx.handle).decode() == ""
+
+
 def test_more_requests_than_slots_and_the_worker_thread(ctx, oracle, parts):
     """Five requests from five threads through two slots with the worker
     thread: each result is the one the same request gives when it runs

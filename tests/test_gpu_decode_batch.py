@@ -75,6 +75,44 @@ def test_decode_batch_matches_each_sequence_alone(gpu, oracle, parts, chunks):
                 close(keep[1].cpu().numpy(), held.recurrent, ("recurrent", i))
 
 
+@pytest.mark.parametrize("count", [9, 17, 40])
+def test_decode_batch_many_sequences_mixed_positions(gpu, oracle, parts, count):
+    """Batches on both sides of the kernels' row thresholds, through the model
+    entry: from 8 rows the NE projections run on the MFMA GEMM, from 16 the
+    expert projections too, and above 32 rows the per-sequence attention
+    kernels take a second group of row pointers. Each sequence starts at its
+    own position (prompts of 0-5 tokens) and every row is compared with the
+    oracle decoding that sequence alone, for two steps."""
+    model = parts["one"]
+    rng = np.random.default_rng(1000 + count)
+    prompts = [[int(t) for t in rng.integers(3, VOCAB, size=i % 6)] for i in range(count)]
+    seqs = [hip.Sequence(model, CAPACITY) for _ in prompts]
+    orc = [small_model.OracleSequence(parts, CAPACITY) for _ in prompts]
+    tokens = []
+    print("prefill", count, flush=True)
+    for prompt, s, o in zip(prompts, seqs, orc):
+        if not prompt:
+            tokens.append(int(rng.integers(3, VOCAB)))
+            continue
+        hip.prefill(gpu, model, prompt, s, None, ubatch=4)
+        for t in prompt:
+            want = o.step(oracle, t)
+        tokens.append(int(np.argmax(want)))
+    for step in range(2):
+        print("decode_batch", count, step, flush=True)
+        out = torch.empty((count, VOCAB), dtype=torch.float32, device="cuda")
+        hip.decode_batch(gpu, model, tokens, seqs, out)
+        got = out.cpu().numpy()
+        nxt = []
+        for b, o in enumerate(orc):
+            want = o.step(oracle, tokens[b])
+            assert max_rel_error(got[b], want) <= 1e-3, (count, step, b, len(prompts[b]))
+            nxt.append(int(np.argmax(want)))
+        tokens = nxt
+    for prompt, s in zip(prompts, seqs):
+        assert s.position == len(prompt) + 2
+
+
 def test_fresh_sequences_batched_equal_decoded_alone(gpu, parts):
     """tests/model_batch_test.cpp:24-51: two new sequences decoded as one
     batch give the logits of each decoded alone, and both reach position 1.

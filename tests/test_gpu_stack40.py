@@ -18,7 +18,15 @@ and the device's greedy token equals the oracle's at every step whose top-two
 logit margin exceeds twice that tolerance (there the 1e-3 agreement of the
 logits fixes the order). decoder_state_checksum (src/main.cpp:105-117) is
 printed for both runs; the two differ in the last bits of the floats, so the
-digests are reported, not compared."""
+digests are reported, not compared.
+
+A second run drives the same weights through the model-level entries that
+the benchmark times: adi_hip_prefill of the prompt at ubatch 128 (the final
+norm and head on its last token inside the call), then 64 adi_hip_decode_batch
+steps of the one sequence, teacher-forced, each writing its logits row
+(src/executor.cpp:1592-1825, 1827-2101; the residual adds fused into the next
+layer's norm). Its logits, greedy tokens and states are held to the same
+checks."""
 import os
 import sys
 
@@ -40,9 +48,10 @@ FIXTURE = os.path.join(HERE, "golden", "stack40.npz")
 TOL = 1e-3
 
 
-@pytest.mark.timeout(900)
-@pytest.mark.skipif(not os.path.exists(FIXTURE), reason="tests/golden/stack40.npz not generated")
-def test_stack40_matches_oracle(gpu, oracle):
+@pytest.fixture(scope="module")
+def stack(gpu):
+    if not os.path.exists(FIXTURE):
+        pytest.skip("tests/golden/stack40.npz not generated")
     want = np.load(FIXTURE)
     g = syn.StackGeometry()
     etlut, ntlut = syn.stack_codebooks()
@@ -58,6 +67,48 @@ def test_stack40_matches_oracle(gpu, oracle):
     emb, head = hip.upload_embedding(gpu, emb_host), hip.upload_head(gpu, head_host)
     final_norm = gpu.to_device(norm_host)
     del emb_host, head_host
+    model = hip.Model(layers, emb, final_norm, [head])
+    yield dict(want=want, g=g, layers=layers, emb=emb, head=head, final_norm=final_norm,
+               prompt=prompt, model=model)
+    del layers, model
+    torch.cuda.empty_cache()
+
+
+class Greedy:
+    """Counts the steps whose greedy token is checked (top-two margin above
+    twice the tolerance) and asserts the device's choice there."""
+
+    def __init__(self, want):
+        self.want, self.agreed, self.checked = want, 0, 0
+
+    def __call__(self, step, choice):
+        if self.want["margin"][step] > 2 * TOL * self.want["logit_max"][step]:
+            self.checked += 1
+            assert choice == int(self.want["tokens"][step]), ("greedy token", step)
+            self.agreed += 1
+
+
+def check_states(oracle, g, want, keeps, label):
+    """Every layer's two state tensors at the fixture's sampled indexes and
+    their largest value; returns decoder_state_checksum of the device's."""
+    end = g.prompt + g.greedy_steps
+    tensors = []
+    for i, keep in enumerate(keeps):
+        a, b = (t.cpu().numpy() for t in keep)
+        pair = (a[:end].ravel(), b[:end].ravel()) if g.full_attention(i) else (a.ravel(), b.ravel())
+        tensors.append(pair)
+        for j, t in enumerate(pair):
+            idx = fixture.state_sample_indexes(i, j, t.size)
+            err = np.abs(t[idx] - want["state_sample"][i, j]).max() / want["state_max"][i, j]
+            assert err <= TOL, (label, "state", i, j, float(err))
+            assert abs(np.abs(t).max() - want["state_max"][i, j]) <= TOL * want["state_max"][i, j]
+    return fixture.decoder_state_checksum(oracle, end, tensors)
+
+
+@pytest.mark.timeout(900)
+def test_stack40_matches_oracle(gpu, oracle, stack):
+    want, g, layers, emb, head = (stack[k] for k in ("want", "g", "layers", "emb", "head"))
+    final_norm, prompt = stack["final_norm"], stack["prompt"]
     capacity = g.prompt + g.greedy_steps
     states = [hip.layer_state(g.full_attention(i), capacity) for i in range(g.layers)]
     tokens = torch.tensor(prompt.astype(np.int32), device="cuda")
@@ -87,15 +138,7 @@ def test_stack40_matches_oracle(gpu, oracle):
     report = error_report(got, want["logits_prefill"])
     print(f"stack40 prefill logits: {report}", flush=True)
     assert report["max_rel"] <= TOL
-    agreed = checked = 0
-
-    def agree(step, choice):
-        nonlocal agreed, checked
-        if want["margin"][step] > 2 * TOL * want["logit_max"][step]:
-            checked += 1
-            assert choice == int(want["tokens"][step]), ("greedy token", step)
-            agreed += 1
-
+    agree = Greedy(want)
     agree(0, choice)
     # decode steps, fed the oracle's tokens
     token = torch.empty(1, dtype=torch.int32, device="cuda")
@@ -108,23 +151,46 @@ def test_stack40_matches_oracle(gpu, oracle):
         got, choice = head_logits(row)
         agree(step + 1, choice)
     report = error_report(got, want["logits_final"])
-    print(f"stack40 final logits: {report}; greedy tokens equal at {agreed} of {checked} "
-          f"clear steps (of {g.greedy_steps + 1})", flush=True)
+    print(f"stack40 final logits: {report}; greedy tokens equal at {agree.agreed} of "
+          f"{agree.checked} clear steps (of {g.greedy_steps + 1})", flush=True)
     assert report["max_rel"] <= TOL
-    assert checked >= (g.greedy_steps + 1) // 2
-
-    # states at the end
-    end = g.prompt + g.greedy_steps
-    tensors = []
-    for i, (state, keep) in enumerate(states):
-        a, b = (t.cpu().numpy() for t in keep)
-        pair = (a[:end].ravel(), b[:end].ravel()) if g.full_attention(i) else (a.ravel(), b.ravel())
-        tensors.append(pair)
-        for j, t in enumerate(pair):
-            idx = fixture.state_sample_indexes(i, j, t.size)
-            err = np.abs(t[idx] - want["state_sample"][i, j]).max() / want["state_max"][i, j]
-            assert err <= TOL, ("state", i, j, float(err))
-            assert abs(np.abs(t).max() - want["state_max"][i, j]) <= TOL * want["state_max"][i, j]
-    gpu_checksum = fixture.decoder_state_checksum(oracle, end, tensors)
+    assert agree.checked >= (g.greedy_steps + 1) // 2
+    gpu_checksum = check_states(oracle, g, want, [keep for _, keep in states], "layer entries")
     print(f"stack40 decoder_state_checksum: device {gpu_checksum:#018x}, oracle "
+          f"{int(want['checksum'][0]):#018x}", flush=True)
+
+
+@pytest.mark.timeout(900)
+def test_stack40_model_entries_match_oracle(gpu, oracle, stack):
+    """The benchmark's entries: adi_hip_prefill (two 128-token chunks, logits
+    of the last prompt token) and 64 teacher-forced adi_hip_decode_batch
+    steps of one sequence."""
+    want, g, model = stack["want"], stack["g"], stack["model"]
+    seq = hip.Sequence(model, g.prompt + g.greedy_steps)
+    logits = torch.empty((1, g.vocab), dtype=torch.float32, device="cuda")
+    picked = torch.empty(1, dtype=torch.int32, device="cuda")
+
+    def choice():
+        hip.argmax_rows(gpu, logits, 1, g.vocab, picked)
+        return int(picked.cpu().numpy()[0])
+
+    print("stack40 model entries: prefill", flush=True)
+    hip.prefill(gpu, model, [int(t) for t in stack["prompt"]], seq, logits[0], ubatch=g.ubatch)
+    assert seq.position == g.prompt
+    report = error_report(logits.cpu().numpy()[0], want["logits_prefill"])
+    print(f"stack40 model entries, prefill logits: {report}", flush=True)
+    assert report["max_rel"] <= TOL
+    agree = Greedy(want)
+    agree(0, choice())
+    for step in range(g.greedy_steps):
+        hip.decode_batch(gpu, model, [int(want["tokens"][step])], [seq], logits)
+        agree(step + 1, choice())
+    assert seq.position == g.prompt + g.greedy_steps
+    report = error_report(logits.cpu().numpy()[0], want["logits_final"])
+    print(f"stack40 model entries, final logits: {report}; greedy tokens equal at "
+          f"{agree.agreed} of {agree.checked} clear steps", flush=True)
+    assert report["max_rel"] <= TOL
+    assert agree.checked >= (g.greedy_steps + 1) // 2
+    gpu_checksum = check_states(oracle, g, want, seq.tensors, "model entries")
+    print(f"stack40 model entries decoder_state_checksum: device {gpu_checksum:#018x}, oracle "
           f"{int(want['checksum'][0]):#018x}", flush=True)
