@@ -53,15 +53,23 @@ constexpr uint32_t kDeltaRows = 16;                        // state rows per blo
 constexpr float kEpsilon = 1.0e-6f;
 
 // Sequences per launch of the per-sequence kernels of a decode step over
-// many sequences; their state pointers and positions travel as kernel
-// arguments.
+// many sequences; their state pointers travel as kernel arguments, their
+// positions in a device array (so a captured step replays at new positions).
 constexpr uint32_t kRowGroup = 32;
 
 struct FullRows {
     float *keys[kRowGroup];
     float *values[kRowGroup];
-    uint32_t position[kRowGroup];
 };
+
+// Splits of the history of a row at `tokens` entries: one per 32 entries, at
+// most `cap`. Each row's split count follows from its own position alone, so
+// its result does not depend on the launch's grid (any grid with at least
+// this many splits gives the same bits) or on the other rows.
+__host__ __device__ __forceinline__ uint32_t row_splits(uint32_t tokens, uint32_t cap) {
+    const uint32_t s = (tokens + 31u) / 32u;
+    return s < 1u ? 1u : (s > cap ? cap : s);
+}
 
 struct LinearRows {
     float *convolution[kRowGroup];
@@ -164,18 +172,19 @@ __global__ __launch_bounds__(kHeadSize) void k_norm_rope(float *query_gate, floa
 
 // The same for one decode token of each of up to kRowGroup sequences: block
 // (h, r), h 0-15 the query heads of row r (in place), 16-17 its key heads,
-// normalized and rotated into the sequence's cache entry rows.position[r],
-// and 18-19 its value heads, copied into that entry. The RoPE table row is
-// the row's position.
+// normalized and rotated into the sequence's cache entry positions[r], and
+// 18-19 its value heads, copied into that entry. The RoPE table row is the
+// row's position.
 __global__ __launch_bounds__(kHeadSize) void k_norm_rope_rows(float *query_gate, const float *key,
                                                               const float *value,
                                                               const uint16_t *query_norm,
                                                               const uint16_t *key_norm,
-                                                              const float *rope_rows, FullRows rows) {
+                                                              const float *rope_rows, FullRows rows,
+                                                              const uint32_t *positions) {
     __shared__ float partial[16];
     __shared__ float head[kHeadSize];
     const uint32_t h = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
-    const uint32_t position = rows.position[r];
+    const uint32_t position = positions[r];
     const size_t entry = static_cast<size_t>(position) * kKvHeads * kHeadSize;
     if (h >= kQueryHeads + kKvHeads) {  // uniform over the block
         const uint32_t kv = h - kQueryHeads - kKvHeads;
@@ -288,13 +297,18 @@ __global__ __launch_bounds__(256) void k_attention_partial(const float *query_ga
 }
 
 // Row r of a decode step over sequences sees its own cache's entries
-// 0 .. rows.position[r], split evenly over the grid's splits.
+// 0 .. positions[r], split evenly over row_splits(positions[r] + 1, cap)
+// splits; the grid's further splits lie past the row's tokens and come out
+// empty (skipped by the combine).
 __global__ __launch_bounds__(256) void k_attention_partial_rows(const float *query_gate,
-                                                                FullRows rows, float *partial) {
+                                                                FullRows rows,
+                                                                const uint32_t *positions,
+                                                                uint32_t cap, float *partial) {
     const uint32_t r = blockIdx.z;
-    const uint32_t tokens = rows.position[r] + 1;
+    const uint32_t tokens = positions[r] + 1;
+    const uint32_t splits = row_splits(tokens, cap);
     attention_partial_span(query_gate + static_cast<size_t>(r) * kQueryHeads * kQueryStride,
-                           rows.keys[r], rows.values[r], tokens, (tokens + gridDim.y - 1u) / gridDim.y,
+                           rows.keys[r], rows.values[r], tokens, (tokens + splits - 1u) / splits,
                            partial + static_cast<size_t>(r) * kQueryHeads * gridDim.y * kPartialStride);
 }
 
@@ -745,14 +759,17 @@ void decoder_chunk(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_
 
 // full_attention_forward_batch (src/executor.cpp:561-731) for one decode
 // token of each of `rows` sequences: row r is at positions[r] of the
-// sequence whose cache is states[r]. The projections run batched over the
-// rows; normalization, RoPE, the cache append and the attention run per
-// sequence, kRowGroup sequences per launch.
+// sequence whose cache is states[r]; the kernels read the positions from
+// device_positions. The launches cover positions below `span` (the RoPE
+// table and the grid's splits; at least every positions[r] + 1). The
+// projections run batched over the rows; normalization, RoPE, the cache
+// append and the attention run per sequence, kRowGroup sequences per launch.
 void full_attention_rows(adi_hip_context *ctx, const adi_hip_full_attention *L, uint32_t rows,
                          const float *inputs, float *outputs,
-                         const adi_hip_layer_state *const *states, const uint32_t *positions) {
+                         const adi_hip_layer_state *const *states, const uint32_t *positions,
+                         const uint32_t *device_positions, uint32_t span) {
     require(L != nullptr && inputs != nullptr && outputs != nullptr && states != nullptr &&
-                positions != nullptr && rows > 0,
+                positions != nullptr && device_positions != nullptr && rows > 0,
             "full attention batch shape mismatch");
     const uint32_t hidden = L->query.columns;
     require(ne_shaped(L->query, kQueryHeads * kQueryStride, hidden) &&
@@ -771,11 +788,11 @@ void full_attention_rows(adi_hip_context *ctx, const adi_hip_full_attention *L, 
                 "attention caches must be 16-byte aligned");
         last = positions[r] + 1 > last ? positions[r] + 1 : last;
     }
+    last = span > last ? span : last;
     auto &ws = ctx->layer_workspace;
     ws.used = 0;
     const uint32_t cap = kMaxSplits / rows > 0 ? kMaxSplits / rows : 1u;
-    uint32_t splits = ceil_div(last, 32);
-    splits = splits < 1 ? 1 : (splits > cap ? cap : splits);
+    const uint32_t splits = row_splits(last, cap);
     const size_t n = rows;
     ws.ensure(Workspace::round(n * kQueryHeads * kQueryStride * 4) +
               Workspace::round(n * kKvHeads * kHeadSize * 4) * 2 +
@@ -796,16 +813,17 @@ void full_attention_rows(adi_hip_context *ctx, const adi_hip_full_attention *L, 
         for (uint32_t i = 0; i < count; ++i) {
             table.keys[i] = states[first + i]->keys;
             table.values[i] = states[first + i]->values;
-            table.position[i] = positions[first + i];
         }
+        const uint32_t *row_positions = device_positions + first;
         float *qg = query_gate + static_cast<size_t>(first) * kQueryHeads * kQueryStride;
         launch(ctx, "attention_norm_rope_rows", k_norm_rope_rows,
                dim3(kQueryHeads + 2 * kKvHeads, count), dim3(kHeadSize), 0, qg,
                static_cast<const float *>(key + static_cast<size_t>(first) * kKvHeads * kHeadSize),
                static_cast<const float *>(value + static_cast<size_t>(first) * kKvHeads * kHeadSize),
-               L->query_norm, L->key_norm, rope, table);
+               L->query_norm, L->key_norm, rope, table, row_positions);
         launch(ctx, "attention_partial_rows", k_attention_partial_rows,
                dim3(kQueryHeads, splits, count), dim3(256), 0, static_cast<const float *>(qg), table,
+               row_positions, cap,
                partial + static_cast<size_t>(first) * kQueryHeads * splits * kPartialStride);
     }
     launch(ctx, "attention_combine", k_attention_combine, dim3(kQueryHeads, rows), dim3(kHeadSize),
@@ -885,11 +903,13 @@ void linear_attention_rows(adi_hip_context *ctx, const adi_hip_linear_attention 
 
 void decoder_rows(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_t rows,
                   float *hidden, const float *pending, float *moe_out,
-                  const adi_hip_layer_state *const *states, const uint32_t *positions) {
+                  const adi_hip_layer_state *const *states, const uint32_t *positions,
+                  const uint32_t *device_positions, uint32_t span) {
     require(states != nullptr && positions != nullptr, "decoder batch shape mismatch");
     layer_body(ctx, L, rows, hidden, pending, moe_out, [&](const float *in, float *out) {
         if (L->full_attention != 0) {
-            full_attention_rows(ctx, &L->full, rows, in, out, states, positions);
+            full_attention_rows(ctx, &L->full, rows, in, out, states, positions, device_positions,
+                                span);
         } else {
             linear_attention_rows(ctx, &L->linear, rows, in, out, states);
         }

@@ -106,6 +106,14 @@ struct adi_hip_batcher {
     std::vector<Active> active;  // logits row i belongs to active[i]
     // host-forced failures for the failure-handling tests: the next
     // admission, or the next step's sampling, fails as a device error would
+    // the decode step recorded as a HIP graph for the rows' slots
+    // graph_slots; last_slots and stable_steps track how long the same rows
+    // have run
+    adi_hip_decode_graph *graph = nullptr;
+    std::vector<uint32_t> graph_slots;
+    std::vector<uint32_t> last_slots;
+    uint32_t stable_steps = 0;
+    bool use_graphs = true;
     std::atomic<bool> fail_admission_for_testing{false};
     std::atomic<bool> fail_step_for_testing{false};
 
@@ -119,6 +127,10 @@ namespace adi_hip {
 namespace {
 
 void free_batcher(adi_hip_batcher *b) {
+    if (b->graph != nullptr) {
+        adi_hip_decode_graph_destroy(b->graph);
+        b->graph = nullptr;
+    }
     for (Slot &s : b->slots) {
         if (s.memory != nullptr) {
             (void)hipFree(s.memory);
@@ -253,9 +265,19 @@ void admit_pending(adi_hip_batcher *b) {
     r.prefill_seconds = seconds_between(started, finished);
 }
 
+// Destroys the recorded decode step (its rows changed).
+void drop_graph(adi_hip_batcher *b) {
+    if (b->graph != nullptr) {
+        adi_hip_decode_graph_destroy(b->graph);
+        b->graph = nullptr;
+        b->graph_slots.clear();
+    }
+}
+
 // Fails every active request with `message` and frees their slots (the
 // decode-failure branch of the worker loop, src/generation.cpp:640-652).
 void fail_active(adi_hip_batcher *b, const std::string &message) {
+    drop_graph(b);
     for (const Active &a : b->active) {
         fail_request(b, a.id, message);
         b->slots[a.slot].busy = false;
@@ -369,15 +391,45 @@ void step_active(adi_hip_batcher *b) {
             next.push_back(std::move(a));
         }
     }
+    // nobody left: row i is still active[i], so the sampled tokens already
+    // sit in b->tokens in the order of the rows
+    const bool same_rows = next.size() == b->active.size();
     b->active = std::move(next);
     if (b->active.empty()) {
+        drop_graph(b);
         return;
     }
     const uint32_t n = static_cast<uint32_t>(b->active.size());
-    const int status = adi_hip_decode_batch(b->ctx, &b->model, next_tokens.data(), n,
-                                            next_states.data(), b->logits);
+    std::vector<uint32_t> slots(n);
+    for (uint32_t i = 0; i < n; ++i) {
+        slots[i] = b->active[i].slot;
+    }
+    int status = ADI_HIP_OK;
+    if (same_rows && b->graph != nullptr && slots == b->graph_slots) {
+        // the same sequences as the recorded step: replay it
+        status = adi_hip_decode_graph_launch(b->graph, next_states.data());
+    } else {
+        drop_graph(b);
+        status = adi_hip_decode_batch(b->ctx, &b->model, next_tokens.data(), n, next_states.data(),
+                                      b->logits);
+        // record a step once the same rows have run twice in a row: a set
+        // of rows that changes every iteration (admissions, finishes) would
+        // not replay its recording
+        b->stable_steps = same_rows && slots == b->last_slots ? b->stable_steps + 1 : 0;
+        b->last_slots = slots;
+        if (status == ADI_HIP_OK && b->use_graphs && b->stable_steps >= 1) {
+            adi_hip_decoder_state *after = next_states.data();
+            if (adi_hip_decode_graph_create(b->ctx, &b->model, n, after, b->tokens, b->logits,
+                                            &b->graph) == ADI_HIP_OK) {
+                b->graph_slots = slots;
+            } else {
+                b->graph = nullptr;  // the direct launches serve instead
+            }
+        }
+    }
     if (status != ADI_HIP_OK) {
         const std::string message = b->ctx->last_error();
+        drop_graph(b);
         fail_active(b, message);
         fail(status, message);
     }
@@ -419,6 +471,7 @@ int adi_hip_batcher_create(adi_hip_context *ctx, const adi_hip_model *model,
             b->context = options->capacity;
             b->max_batch = options->max_batch;
             b->ubatch = options->prefill_ubatch;
+            b->use_graphs = options->direct_steps == 0;
             for (uint32_t i = 0; i < options->stop_count; ++i) {
                 require(options->stop_tokens[i] < b->vocabulary, "batcher stop token is out of range");
                 b->stop.insert(options->stop_tokens[i]);

@@ -38,10 +38,17 @@ struct Workspace {
     size_t capacity = 0;
     size_t used = 0;
     size_t limit = SIZE_MAX;
+    // set while a stream capture records launches into these slices: growing
+    // then would free memory the graph is recording pointers into
+    bool frozen = false;
 
     void ensure(size_t bytes) {
         if (bytes <= capacity) {
             return;
+        }
+        if (frozen) {
+            fail(ADI_HIP_DEVICE_ERROR,
+                 "a captured decode step needs more workspace than its planning pass reserved");
         }
         if (bytes > limit) {
             fail(ADI_HIP_OUT_OF_MEMORY, "workspace of " + std::to_string(bytes) +
@@ -126,6 +133,16 @@ struct adi_hip_context {
     bool moe_sync_pending = false;
     bool fused_moe = true;
     bool profiling = false;
+    // planning pass of a graph capture: every host step of a call runs
+    // (checks, workspace and RoPE table growth) but nothing is launched
+    bool dry_run = false;
+
+    // every grow-on-demand arena, for the capture's freeze and its check
+    // that none was reallocated since
+    std::vector<adi_hip::Workspace *> arenas() {
+        return {&workspace, &layer_workspace, &decoder_workspace, &sequence_workspace,
+                &layer_output, &rope_cache};
+    }
     std::vector<adi_hip::KernelStat> stats;
 };
 
@@ -193,7 +210,7 @@ KernelStat &stat_for(adi_hip_context *ctx, const char *name);
 template <typename Kernel, typename... Args>
 void launch(adi_hip_context *ctx, const char *name, Kernel kernel, dim3 grid,
             dim3 block, size_t lds_bytes, Args... args) {
-    if (grid.x == 0 || grid.y == 0 || grid.z == 0) {
+    if (grid.x == 0 || grid.y == 0 || grid.z == 0 || ctx->dry_run) {
         return;
     }
     if (!ctx->profiling) {

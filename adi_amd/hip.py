@@ -104,7 +104,7 @@ class DecoderStateStruct(C.Structure):
 class BatcherOptions(C.Structure):
     _fields_ = [("max_batch", u32), ("capacity", u32), ("prefill_ubatch", u32),
                 ("stop_tokens", C.POINTER(u32)), ("stop_count", u32),
-                ("masked_tokens", C.POINTER(u32)), ("masked_count", u32)]
+                ("masked_tokens", C.POINTER(u32)), ("masked_count", u32), ("direct_steps", u32)]
 
 
 class GenerationOptions(C.Structure):
@@ -187,6 +187,11 @@ SIGNATURES = [
      [vp, C.POINTER(ModelStruct), C.POINTER(u32), u32, C.POINTER(DecoderStateStruct), vp]),
     ("adi_hip_prefill", C.c_int,
      [vp, C.POINTER(ModelStruct), C.POINTER(u32), u32, u32, C.POINTER(DecoderStateStruct), vp]),
+    ("adi_hip_decode_graph_create", C.c_int,
+     [vp, C.POINTER(ModelStruct), u32, C.POINTER(DecoderStateStruct), vp, vp, C.POINTER(vp)]),
+    ("adi_hip_decode_graph_launch", C.c_int, [vp, C.POINTER(DecoderStateStruct)]),
+    ("adi_hip_decode_graph_captures", u32, [vp]),
+    ("adi_hip_decode_graph_destroy", None, [vp]),
     ("adi_hip_batcher_create", C.c_int,
      [vp, C.POINTER(ModelStruct), C.POINTER(BatcherOptions), C.POINTER(vp)]),
     ("adi_hip_batcher_destroy", None, [vp]),
@@ -1023,6 +1028,48 @@ def decode_batch(ctx: Context, model: Model, tokens, sequences, logits=None) -> 
     for s, st in zip(sequences, states):
         s.struct.position = st.position
     ctx.check(status)
+
+
+class DecodeGraph:
+    """adi_hip_decode_graph: one decode step of `sequences` captured as a HIP
+    graph. Each launch() replays it: the step's tokens are read from
+    `tokens` (device int32/uint32 [len(sequences)]), logits go to `logits`
+    (device [len(sequences)][vocabulary] or None), and every sequence's
+    position advances by one."""
+
+    def __init__(self, ctx: Context, model: Model, sequences, tokens, logits=None):
+        self.ctx, self.model, self.sequences = ctx, model, list(sequences)
+        self._keep = (tokens, logits)
+        n = len(self.sequences)
+        self._states = (DecoderStateStruct * max(n, 1))(*(s.struct for s in self.sequences))
+        handle = vp()
+        ctx.check(ctx.lib.adi_hip_decode_graph_create(ctx.handle, C.byref(model.struct), n,
+                                                      self._states, _addr(tokens), _addr(logits),
+                                                      C.byref(handle)))
+        self.handle = handle
+
+    def launch(self) -> None:
+        for st, s in zip(self._states, self.sequences):
+            st.position = s.struct.position
+        status = self.ctx.lib.adi_hip_decode_graph_launch(self.handle, self._states)
+        for st, s in zip(self._states, self.sequences):
+            s.struct.position = st.position
+        self.ctx.check(status)
+
+    @property
+    def captures(self) -> int:
+        return int(self.ctx.lib.adi_hip_decode_graph_captures(self.handle))
+
+    def close(self) -> None:
+        if self.handle:
+            self.ctx.lib.adi_hip_decode_graph_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def prefill(ctx: Context, model: Model, tokens, sequence: Sequence, logits=None,

@@ -7,7 +7,9 @@ A worker thread runs the loop: while requests are pending or active it calls
 adi_hip_batcher_step, one iteration of the reference's loop (admit the oldest
 pending request by prefilling its prompt, sample every active sequence,
 finish on a stop token or the output limit, decode the rest in one batched
-step). generate() submits a request and blocks until it finishes, passing
+step). While the same sequences keep stepping, their decode step is
+recorded once as a HIP graph and replayed (replay_steps=False launches every
+step directly; both give the same bits). generate() submits a request and blocks until it finishes, passing
 each new token to `token_callback` as it appears and cancelling the request
 when `cancelled()` turns true, as generate_from_prompt does. The worker owns
 the context while the batcher runs: other work must not use it meanwhile."""
@@ -44,12 +46,12 @@ class ContinuousBatcher:
     def __init__(self, ctx: hip.Context, model: hip.Model, max_batch: int = 16,
                  capacity: int = 4096, prefill_ubatch: int = 128,
                  stop_tokens: Sequence[int] = (), masked_tokens: Sequence[int] = (),
-                 start: bool = True):
+                 start: bool = True, replay_steps: bool = True):
         self.ctx, self.model = ctx, model
         stop = (hip.u32 * max(len(stop_tokens), 1))(*stop_tokens)
         masked = (hip.u32 * max(len(masked_tokens), 1))(*masked_tokens)
         options = hip.BatcherOptions(max_batch, capacity, prefill_ubatch, stop, len(stop_tokens),
-                                     masked, len(masked_tokens))
+                                     masked, len(masked_tokens), 0 if replay_steps else 1)
         handle = hip.vp()
         ctx.check(ctx.lib.adi_hip_batcher_create(ctx.handle, C.byref(model.struct),
                                                  C.byref(options), C.byref(handle)))

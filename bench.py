@@ -69,6 +69,9 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU baseline budget per ubatch")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-child", action="store_true", help=argparse.SUPPRESS)
+    p.add_argument("--cpu-projections", action="store_true", help=argparse.SUPPRESS)
+    p.add_argument("--projection-cpu-seconds", type=float, default=2.0,
+                   help="CPU baseline budget per projection figure")
     p.add_argument("--no-projections", action="store_true")
     p.add_argument("--copy-bytes", type=int, default=0,
                    help="first run a plain device-to-device copy of this many bytes three times "
@@ -90,6 +93,12 @@ def kernel_bytes(name, active):
         # two launches per step: gate+up (2 expert + 2 shared matrices), down
         # (1 + 1); the mean launch reads half the step's GEMV packed bytes
         return (3 * active * (EXPERT_TRELLIS_BYTES + EXPERT_GAMMA_BYTES) + 3 * NE_TRELLIS_BYTES) / 2
+    if name == "expert_mfma":
+        # gate+up (2 matrices of every active expert) and down (1): the mean
+        # launch decodes 1.5 matrices of each active expert
+        return 1.5 * active * (EXPERT_TRELLIS_BYTES + EXPERT_GAMMA_BYTES)
+    if name == "ne_mfma":
+        return 1.5 * NE_TRELLIS_BYTES
     if name == "expert_gemv":
         return active * (EXPERT_TRELLIS_BYTES + EXPERT_GAMMA_BYTES)
     if name == "ne_gemv":
@@ -122,6 +131,7 @@ def moe_bench(torch, hip, ctx, layers, xs, biases, steps, warmup, runs):
 
     for s in range(warmup):
         step(s)
+    ctx.synchronize()
     walls = []
     for r in range(runs):
         torch.cuda.synchronize()
@@ -130,11 +140,14 @@ def moe_bench(torch, hip, ctx, layers, xs, biases, steps, warmup, runs):
             step(s)
         torch.cuda.synchronize()
         walls.append(time.perf_counter() - t0)
+        # the library's own check after each run: a one-launch MoE wait that
+        # ran out (its outputs invalid) fails the benchmark here
+        ctx.synchronize()
     # distinct experts per step for the byte count
     active = []
     for s in range(warmup, warmup + steps):
         step(s)
-        torch.cuda.synchronize()
+        ctx.synchronize()
         active.append(len(np.unique(routes.cpu().numpy())))
     # per-kernel timing in a separate pass over the same steps
     ctx.profiling(True)
@@ -142,6 +155,7 @@ def moe_bench(torch, hip, ctx, layers, xs, biases, steps, warmup, runs):
         step(s)
     prof = ctx.profile()
     ctx.profiling(False)
+    ctx.synchronize()
     return walls, float(np.mean(active)), prof
 
 
@@ -166,16 +180,22 @@ def copy_calibration(torch, nbytes):
     del src, dst
 
 
-def traffic_from_profile(kernel, ubatch):
-    """Measured HBM bytes per launch of `kernel` at `ubatch`, from the
-    committed counter summary (FETCH_SIZE + WRITE_SIZE per dispatch, each
-    scaled by the same counter's reading for a copy of known size), or None."""
-    path = os.path.join(ROOT, "profiles", "moe_layer_hbm_traffic.md")
+MOE_STATS = os.path.join(ROOT, "profiles", "moe_layer_kernel_stats.md")
+MOE_TRAFFIC = os.path.join(ROOT, "profiles", "moe_layer_hbm_traffic.md")
+PROJ_STATS = os.path.join(ROOT, "profiles", "projections_kernel_stats.md")
+PROJ_TRAFFIC = os.path.join(ROOT, "profiles", "projections_hbm_traffic.md")
+
+
+def traffic_from_profile(kernel, key, path=MOE_TRAFFIC):
+    """Measured HBM bytes per launch of `kernel` in the workload `key` (an
+    ubatch, or a projection's name), from a committed counter summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the same counter's
+    reading for a copy of known size), or None."""
     if not os.path.exists(path):
         return None
     for row in open(path):
         cells = [c.strip() for c in row.strip().strip("|").split("|")]
-        if len(cells) >= 6 and cells[0].isdigit() and int(cells[0]) == ubatch and cells[1] == kernel:
+        if len(cells) >= 6 and cells[0] == str(key) and cells[1] == kernel:
             try:
                 return int(float(cells[5]))
             except ValueError:
@@ -187,30 +207,38 @@ def kernel_flops(name, ubatch):
     """Algorithmic flops of the mean launch of `name` (2 x rows x columns per
     routed position), or None. expert_mfma runs twice per step: gate+up
     (2 x 512 x 2048 per position) and down (2048 x 512); the mean launch is
-    1.5 projections of 8 * ubatch routed positions."""
-    if name == "expert_mfma":
+    1.5 projections of 8 * ubatch routed positions. ne_mfma likewise for the
+    shared expert's ubatch rows."""
+    if name in ("expert_mfma", "moe_gemv"):
         return 1.5 * 2.0 * 8 * ubatch * EXPERT_HIDDEN * HIDDEN
+    if name == "ne_mfma":
+        return 1.5 * 2.0 * ubatch * EXPERT_HIDDEN * HIDDEN
+    if name == "moe_decode_one":
+        return FLOP_PER_TOKEN * ubatch
     return None
 
 
+RIDGE_FLOP_PER_BYTE = MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)  # 312.5
+
+
 ROCPROF_NAMES = {"moe_decode_one": "k_moe_decode_one", "moe_gemv": "k_trellis_gemv",
-                 "expert_mfma": "k_expert_mfma"}
+                 "expert_mfma": "k_expert_mfma", "ne_fused": "k_ne_fused", "head": "k_head_mfma"}
 
 
-def rocprof_avg_us(kernel, ubatch):
-    """Average duration (us) of `kernel` at `ubatch` in the committed
-    rocprofv3 --kernel-trace --stats summary, or None."""
-    path = os.path.join(ROOT, "profiles", "moe_layer_kernel_stats.md")
+def rocprof_avg_us(kernel, key, path=MOE_STATS):
+    """Average duration (us) of `kernel` in the section `## <key>` of a
+    committed rocprofv3 --kernel-trace --stats summary ("ubatch 4", or a
+    projection's name), or None."""
     want = ROCPROF_NAMES.get(kernel)
     if want is None or not os.path.exists(path):
         return None
     section = None
     for row in open(path):
-        if row.startswith("## ubatch "):
-            section = int(row.split()[2])
+        if row.startswith("## "):
+            section = row[3:].strip()
             continue
         cells = [c.strip().strip("`") for c in row.strip().strip("|").split("|")]
-        if section == ubatch and len(cells) >= 3 and cells[0].split("<")[0] == want:
+        if section == str(key) and len(cells) >= 3 and cells[0].split("<")[0] == want:
             return float(cells[2])
     return None
 
@@ -233,38 +261,83 @@ def roofline_for(prof, steps, active, ubatch, wall_ms_per_step):
         r["achieved"] = round(r["achieved"] * scale, 2)
         r["frac"] = round(r["frac"] * scale, 4)
         r["timing"] = "timed region / launches (one launch per step)"
-    r["rocprof_avg_us"] = rocprof_avg_us(name, ubatch)
+    r["rocprof_avg_us"] = rocprof_avg_us(name, f"ubatch {ubatch}")
     r["traffic"] = traffic_from_profile(name, ubatch)
     return r
 
 
 def roofline_kernel(prof, active, ubatch):
+    """The roofline of the launch kind with the largest share of the step
+    that has an algorithmic count. Its bound follows its algorithmic
+    intensity: MFMA at or above the ridge (312.5 FLOP per packed byte on
+    MI355X), HBM below it."""
     total = sum(ms for _, ms in prof.values())
     ranked = sorted(prof.items(), key=lambda kv: -kv[1][1])
     for name, (launches, ms) in ranked:
-        flops = kernel_flops(name, ubatch)
-        if flops is not None:
-            avg_ms = ms / launches
-            achieved = flops / (avg_ms * 1e-3) / 1e12
-            return {
-                "kernel": name, "bound": "mfma", "achieved": round(achieved, 2),
-                "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / MFMA_PEAK_TFLOPS, 4), "traffic": None,
-                "avg_launch_us": round(avg_ms * 1e3, 2), "flops_per_launch": int(flops),
-                "share_of_step": round(ms / total, 3),
-            }
         nbytes = kernel_bytes(name, active)
-        if nbytes is None:
+        flops = kernel_flops(name, ubatch)
+        if nbytes is None and flops is None:
             continue
         avg_ms = ms / launches
-        achieved = nbytes / (avg_ms * 1e-3) / 1e9
-        return {
-            "kernel": name, "bound": "hbm", "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None, "avg_launch_us": round(avg_ms * 1e3, 2),
-            "bytes_per_launch": int(nbytes), "share_of_step": round(ms / total, 3),
-        }
+        intensity = None if nbytes is None or flops is None else flops / nbytes
+        r = {"kernel": name, "avg_launch_us": round(avg_ms * 1e3, 2),
+             "share_of_step": round(ms / total, 3),
+             "intensity_flop_per_byte": None if intensity is None else round(intensity, 1)}
+        if nbytes is None or (intensity is not None and intensity >= RIDGE_FLOP_PER_BYTE):
+            achieved = flops / (avg_ms * 1e-3) / 1e12
+            r.update({"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_PEAK_TFLOPS,
+                      "unit": "TFLOP/s", "frac": round(achieved / MFMA_PEAK_TFLOPS, 4),
+                      "traffic": None, "flops_per_launch": int(flops)})
+        else:
+            achieved = nbytes / (avg_ms * 1e-3) / 1e9
+            r.update({"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                      "bytes_per_launch": int(nbytes)})
+            if flops is not None:
+                r["flops_per_launch"] = int(flops)
+        return r
     return None
+
+
+# The reference's kernel kinds (include/adi/profiling.hpp:9-40) of this
+# library's MoE launches. The routing, Hadamard, SwiGLU and combine launches
+# are work the reference does inside moe_forward(_batch) outside any kernel
+# timer: they count under "moe" only. At one row the whole layer is one
+# launch, so its kinds are not separable on the device.
+KIND_OF_LAUNCH = {"router": "bf16_projection", "expert_mfma": "expert_batch",
+                  "ne_mfma": "non_expert_batch", "moe_gemv": "expert_batch+non_expert_batch"}
+
+
+def kind_report(prof, steps, ubatch, cpu_kinds, cpu_ms):
+    """The step by the reference's kernel kinds, device beside CPU: calls,
+    milliseconds and the reference's work items per step."""
+    gpu = {}
+    total_ms, total_launches = 0.0, 0
+    for name, (launches, ms) in prof.items():
+        total_ms += ms
+        total_launches += launches
+        kind = KIND_OF_LAUNCH.get(name)
+        if kind is not None:
+            k = gpu.setdefault(kind, [0, 0.0])
+            k[0] += launches
+            k[1] += ms
+    report = {"moe": {"gpu_launches_per_step": round(total_launches / steps, 2),
+                      "gpu_ms_per_step": round(total_ms / steps, 4),
+                      "cpu_ms_per_step": cpu_ms,
+                      "work_items_per_step": ubatch * HIDDEN}}
+    for kind, (launches, ms) in gpu.items():
+        report[kind] = {"gpu_launches_per_step": round(launches / steps, 2),
+                        "gpu_ms_per_step": round(ms / steps, 4)}
+    for kind, v in (cpu_kinds or {}).items():
+        entry = report.setdefault(kind, {})
+        entry["cpu_calls_per_step"] = v["calls_per_step"]
+        entry["cpu_ms_per_step"] = v["ms_per_step"]
+        entry["work_items_per_step"] = v["work_items_per_step"]
+        if "gpu_ms_per_step" not in entry:
+            entry["gpu_ms_per_step"] = None
+            entry["gpu_note"] = ("inside the one-launch layer" if "moe_decode_one" in prof else
+                                 "inside " + next((k for k in gpu if kind in k.split("+")), "moe"))
+    return report
 
 
 def cpu_model() -> str:
@@ -306,12 +379,26 @@ def cpu_baseline(layer_host, xs, biases, seconds):
         dt = (time.perf_counter() - t0) / n
         results[u] = {"tokens_per_s": round(u / dt, 1), "ms_per_step": round(dt * 1e3, 3),
                       "calls": n}
+        if kind == "reference":
+            # the reference's per-kind kernel profile over a few more calls
+            calls = max(1, min(n, 20))
+            lib.ref_kernel_profiling(1)
+            for _ in range(calls):
+                run(x, biases[u])
+            lib.ref_kernel_profiling(0)
+            results[u]["kinds"] = {k: {"calls_per_step": round(c / calls, 2),
+                                       "ms_per_step": round(ms / calls, 4),
+                                       "work_items_per_step": int(w // calls)}
+                                   for k, (c, ms, w) in pyoracle.ref_kernel_profiles(lib).items()}
     return kind, cores, isa, results, outputs
 
 
 def cpu_child(args):
     """--cpu-child: the CPU baseline alone, in a process of its own (started
     with ADI_THREADS=1 for the single-thread figure; it never touches the GPU)."""
+    if args.cpu_projections:
+        print(json.dumps(projection_cpu_baseline(args.cpu_seconds)))
+        return
     from adi_amd import synthetic as syn
     layer_host = syn.moe_layer(syn.rng_for(2, 0))
     xs, biases = {}, {}
@@ -322,6 +409,18 @@ def cpu_child(args):
     kind, cores, isa, results, _ = cpu_baseline(layer_host, xs, biases, args.cpu_seconds)
     print(json.dumps({"kind": kind, "cores": cores, "isa": isa,
                       "per_ubatch": {str(k): v for k, v in results.items()}}))
+
+
+def cpu_single_thread_projections(seconds):
+    import subprocess
+    env = dict(os.environ, ADI_THREADS="1", OMP_NUM_THREADS="1")
+    cmd = [sys.executable, os.path.abspath(__file__), "--cpu-child", "--cpu-projections",
+           "--cpu-seconds", str(seconds)]
+    proc = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=900)
+    if proc.returncode != 0:
+        log(f"single-thread projection baseline failed: {proc.stderr[-400:]}")
+        return None
+    return json.loads(proc.stdout.strip().splitlines()[-1])
 
 
 def cpu_single_thread(args):
@@ -384,7 +483,50 @@ def graph_us(torch, ctx, fn, calls, replays=7):
         ctx.use_stream(torch.cuda.current_stream())
 
 
-def projections(torch, hip, ctx, steps, runs):
+def projection_cpu_inputs():
+    """Host inputs of the CPU figures for the two packed projections: the
+    151,936 x 2048 int5 head and a 2048 x 2048 NE matrix (seeded, the same
+    shapes and generators as the device runs) and their input rows."""
+    from adi_amd import synthetic as syn
+    head = syn.head_chunk(syn.rng_for(1, 0), HEAD_ROWS, HEAD_COLUMNS)
+    r = syn.rng_for(1, 1)
+    ne = syn.ne_matrix(r, 2048, 2048, syn.ne_tlut(r))
+    xs = {b: syn.hidden_states(syn.rng_for(1, 100 + b), b, 2048) for b in (1, 4)}
+    heads_x = {b: syn.rms_normalized(x) for b, x in xs.items()}
+    return head, ne, xs, heads_x
+
+
+def projection_cpu_baseline(seconds):
+    """mach_ne_matmul and mach_head_matmul of the reference (compiled from
+    its sources, oracle/_ref; its worker pool at ADI_THREADS threads, the
+    bench-ne / bench-head commands of src/main.cpp:376-461): one warm call,
+    then timed calls for about `seconds` each. Returns {name: figures} or
+    None without the reference library."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+    if not pyoracle.ref_available():
+        return None
+    lib = pyoracle.load_ref()
+    head, ne, xs, heads_x = projection_cpu_inputs()
+    out = {}
+    for b in (1, 4):
+        for name, fn in ((f"ne_2048x2048_b{b}", lambda: pyoracle.ne_matmul(lib, ne, xs[b], prefix="ref")),
+                         (f"head_151936x2048_b{b}",
+                          lambda: pyoracle.head_matmul(lib, head, heads_x[b], prefix="ref"))):
+            fn()  # warm call
+            n, t0 = 0, time.perf_counter()
+            while n < 3 or time.perf_counter() - t0 < seconds:
+                fn()
+                n += 1
+            dt = (time.perf_counter() - t0) / n
+            out[name] = {"ms_per_call": round(dt * 1e3, 4), "vectors_per_s": round(b / dt, 1),
+                         "calls": n}
+    return {"threads": int(lib.ref_worker_threads()),
+            "isa": {1: "scalar", 8: "avx2", 16: "avx512"}[lib.ref_selected_isa_lanes()],
+            "per_call": out}
+
+
+def projections(torch, hip, ctx, steps, runs, cpu_seconds):
     from adi_amd import synthetic as syn
     res = {}
     rng = syn.rng_for(1, 0)
@@ -395,13 +537,19 @@ def projections(torch, hip, ctx, steps, runs):
         out = torch.empty((batch, HEAD_ROWS), dtype=torch.float32, device="cuda")
         call = lambda i: hip.head_matmul(ctx, heads[i % copies], x, batch, out)
         dt = median_seconds(torch, call, steps, runs)
+        ctx.synchronize()
         us = graph_us(torch, ctx, call, 30)
-        res[f"head_151936x2048_b{batch}"] = {
+        key = f"head_151936x2048_b{batch}"
+        res[key] = {
             "ms_per_call": round(dt * 1e3, 4), "vectors_per_s": round(batch / dt, 1),
             "packed_gbs": round(HEAD_BYTES / dt / 1e9, 1),
             "hbm_frac": round(HEAD_BYTES / dt / 1e9 / HBM_PEAK_GBS, 4),
             "graph_us_per_call": round(us, 2),
-            "graph_hbm_frac": round(HEAD_BYTES / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+            "graph_hbm_frac": round(HEAD_BYTES / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes_per_call": HEAD_BYTES,
+            "rocprof_kernel": ROCPROF_NAMES["head"],
+            "rocprof_avg_us": rocprof_avg_us("head", key, PROJ_STATS),
+            "traffic": traffic_from_profile("head", key, PROJ_TRAFFIC)}
     del heads
     tlut = syn.ne_tlut(rng)
     book = ctx.ne_codebook(tlut)
@@ -418,13 +566,30 @@ def projections(torch, hip, ctx, steps, runs):
         call = lambda i: ctx.check(ctx.lib.adi_hip_ne_matmul(
             ctx.handle, hip.C.byref(mats[i % count]), x.data_ptr(), batch, out.data_ptr()))
         dt = median_seconds(torch, call, max(steps, count), runs)
+        ctx.synchronize()
         us = graph_us(torch, ctx, call, count)
-        res[f"ne_2048x2048_b{batch}"] = {
+        key = f"ne_2048x2048_b{batch}"
+        res[key] = {
             "ms_per_call": round(dt * 1e3, 4), "vectors_per_s": round(batch / dt, 1),
             "packed_gbs": round(nbytes / dt / 1e9, 1),
             "hbm_frac": round(nbytes / dt / 1e9 / HBM_PEAK_GBS, 4),
             "graph_us_per_call": round(us, 2),
-            "graph_hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+            "graph_hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes_per_call": nbytes,
+            "rocprof_kernel": ROCPROF_NAMES["ne_fused"],
+            "rocprof_avg_us": rocprof_avg_us("ne_fused", key, PROJ_STATS),
+            "traffic": traffic_from_profile("ne_fused", key, PROJ_TRAFFIC)}
+    del trellis, mats
+    if cpu_seconds > 0:
+        log("projections: cpu baseline")
+        cpu = projection_cpu_baseline(cpu_seconds)
+        single = cpu_single_thread_projections(cpu_seconds)
+        for key, entry in res.items():
+            if cpu is not None and key in cpu["per_call"]:
+                entry["cpu_baseline"] = {
+                    "kind": "reference", "threads": cpu["threads"], "isa": cpu["isa"],
+                    **cpu["per_call"][key],
+                    "single_thread": None if single is None else single["per_call"].get(key)}
     res.update(decode_side(torch, hip, ctx, steps))
     res.update(attention_side(torch, hip, ctx, steps))
     return res
@@ -541,47 +706,69 @@ def stack40(torch, hip, ctx, runs, sequences=16):
     chosen = torch.empty(sequences, dtype=torch.int32, device="cuda")
     seqs = [hip.Sequence(model, capacity) for _ in range(sequences)]
 
-    def greedy(active):
+    def greedy(active, replay):
+        """64 greedy steps; with `replay` the step is recorded once (in the
+        timed region) and replayed, its tokens read from the device."""
         n = len(active)
+        graph = hip.DecodeGraph(ctx, model, active, chosen[:n], logits) if replay else None
         for step in range(g.greedy_steps):
             hip.argmax_rows(ctx, logits, n, g.vocab, chosen)
-            hip.decode_batch(ctx, model, chosen[:n].tolist(), active, logits)
+            if graph is not None:
+                graph.launch()
+            else:
+                hip.decode_batch(ctx, model, chosen[:n].tolist(), active, logits)
         torch.cuda.synchronize()
+        ctx.synchronize()
+        if graph is not None:
+            graph.close()
 
-    def run_one():
+    def run_one(replay=False):
         seqs[0].reset()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         hip.prefill(ctx, model, prompt, seqs[0], logits[0], ubatch=g.ubatch)
         torch.cuda.synchronize()
+        ctx.synchronize()
         t1 = time.perf_counter()
-        greedy(seqs[:1])
+        greedy(seqs[:1], replay)
         return t1 - t0, time.perf_counter() - t1
 
-    def run_batch():
+    def run_batch(replay=False):
         for k, s in enumerate(seqs):
             s.reset()
             hip.prefill(ctx, model, prompt, s, logits[k], ubatch=g.ubatch)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        greedy(seqs)
+        greedy(seqs, replay)
         return time.perf_counter() - t0
 
     run_one()  # warm-up: workspaces, kernels
     times = [run_one() for _ in range(runs)]
     prefill_s = float(np.median([t[0] for t in times]))
     decode_s = float(np.median([t[1] for t in times]))
+    run_one(True)
+    decode_graph_s = float(np.median([run_one(True)[1] for _ in range(runs)]))
     run_batch()
     batch_s = float(np.median([run_batch() for _ in range(runs)]))
+    run_batch(True)
+    batch_graph_s = float(np.median([run_batch(True) for _ in range(runs)]))
     del layers, seqs, model
     torch.cuda.empty_cache()
+    steps = g.greedy_steps
     return {"stack40": {
         "prefill_tokens_per_s": round(g.prompt / prefill_s, 1),
         "prefill_ms": round(prefill_s * 1e3, 2),
-        "decode_ms_per_token": round(decode_s / g.greedy_steps * 1e3, 3),
-        "decode_tokens_per_s": round(g.greedy_steps / decode_s, 1),
-        f"decode_batch{sequences}_ms_per_step": round(batch_s / g.greedy_steps * 1e3, 3),
-        f"decode_batch{sequences}_tokens_per_s": round(sequences * g.greedy_steps / batch_s, 1),
+        "decode_ms_per_token": round(decode_s / steps * 1e3, 3),
+        "decode_tokens_per_s": round(steps / decode_s, 1),
+        "decode_replayed_ms_per_token": round(decode_graph_s / steps * 1e3, 3),
+        "decode_replayed_tokens_per_s": round(steps / decode_graph_s, 1),
+        f"decode_batch{sequences}_ms_per_step": round(batch_s / steps * 1e3, 3),
+        f"decode_batch{sequences}_tokens_per_s": round(sequences * steps / batch_s, 1),
+        f"decode_batch{sequences}_replayed_ms_per_step": round(batch_graph_s / steps * 1e3, 3),
+        f"decode_batch{sequences}_replayed_tokens_per_s":
+            round(sequences * steps / batch_graph_s, 1),
+        "replay": "one decode step recorded as a HIP graph (adi_hip_decode_graph) per run, "
+                  "the recording inside the timed region; tokens chosen on the device",
         "layers": g.layers, "hidden": g.hidden, "vocab": g.vocab, "prompt": g.prompt,
         "ubatch": g.ubatch, "greedy_steps": g.greedy_steps}}
 
@@ -621,6 +808,7 @@ def main():
 
     per = {}
     gpu_out = {}
+    profiles = {}
     headline = None
     for u in ubatches:
         log(f"moe layer ubatch {u}")
@@ -631,6 +819,7 @@ def main():
         wall = float(np.median(walls))
         ms = wall / args.steps * 1e3
         layer_bytes = FIXED_LAYER_BYTES + PER_EXPERT_BYTES * active
+        profiles[u] = prof
         entry = {
             "tokens_per_s": round(u / (wall / args.steps), 1), "ms_per_step": round(ms, 4),
             "runs_ms_per_step": [round(w / args.steps * 1e3, 4) for w in walls],
@@ -651,7 +840,8 @@ def main():
             headline = (u, entry)
         del xs
 
-    proj = {} if args.no_projections else projections(torch, hip, ctx, args.steps, args.runs)
+    proj = {} if args.no_projections else projections(
+        torch, hip, ctx, args.steps, args.runs, 0.0 if args.no_cpu else args.projection_cpu_seconds)
     if not args.no_stack:
         log("40-layer stack")
         del layers
@@ -675,6 +865,8 @@ def main():
                "single_thread": None if single is None else single["per_ubatch"]}
         for k, v in results.items():
             per[str(k)]["cpu_tokens_per_s"] = v["tokens_per_s"]
+            per[str(k)]["kernel_profile"] = kind_report(profiles[k], args.steps, k, v.get("kinds"),
+                                                        v["ms_per_step"])
         checksum = {}
         for u in ubatches:
             g, c = gpu_out[u], cpu_out[u]

@@ -527,6 +527,37 @@ int adi_hip_decode_batch(adi_hip_context *ctx, const adi_hip_model *model, const
 int adi_hip_prefill(adi_hip_context *ctx, const adi_hip_model *model, const uint32_t *tokens,
                     uint32_t count, uint32_t ubatch, adi_hip_decoder_state *state, float *logits);
 
+/* A decode step captured as a HIP graph and replayed, for the serving loop
+ * that calls decode_batch once per iteration (src/generation.cpp:560-660)
+ * with the same sequences: one hipGraphLaunch in place of the step's
+ * several hundred kernel launches. The graph holds adi_hip_decode_batch's
+ * launches for `batch` sequences; each replay reads the step's tokens from
+ * `tokens` (DEVICE [batch], written by the caller before the launch, e.g. by
+ * adi_hip_argmax_rows or adi_hip_sample_rows; a token >= the vocabulary
+ * gives NaN rows, it is not checked) and writes logits[b][vocabulary]
+ * (DEVICE; NULL skips the norm and head). The positions live in a device
+ * array the graph advances itself; every replay gives the bits of
+ * adi_hip_decode_batch at the same positions.
+ *
+ * create copies the model descriptor and each sequence's layer states
+ * (same checks as adi_hip_decode_batch; ADI_HIP_INVALID_ARGUMENT with
+ * profiling on) and records the step without running it. launch replays
+ * it and advances every states[b].position by one; states must be the
+ * sequences the graph was created with (same layer state pointers), at any
+ * positions (positions the caller changed, e.g. a reset, are taken over).
+ * A launch re-records the step by itself when the positions outgrow what
+ * the recording covers (steps of 512) or a call since has grown one of the
+ * context's scratch arenas. captures returns how many recordings a graph
+ * has made. The model, the states, `tokens` and `logits` must outlive the
+ * graph. No counterpart in the reference (its CPU loop has no launches). */
+typedef struct adi_hip_decode_graph adi_hip_decode_graph;
+int adi_hip_decode_graph_create(adi_hip_context *ctx, const adi_hip_model *model, uint32_t batch,
+                                const adi_hip_decoder_state *states, const uint32_t *tokens,
+                                float *logits, adi_hip_decode_graph **out);
+int adi_hip_decode_graph_launch(adi_hip_decode_graph *graph, adi_hip_decoder_state *states);
+uint32_t adi_hip_decode_graph_captures(const adi_hip_decode_graph *graph);
+void adi_hip_decode_graph_destroy(adi_hip_decode_graph *graph);
+
 /* ---- continuous batching (serving) --------------------------------------- */
 
 /* ContinuousBatcher (src/generation.cpp:343-660) without the tokenizer:
@@ -555,6 +586,10 @@ typedef struct {
     uint32_t stop_count;
     const uint32_t *masked_tokens;  /* HOST; Tokenizer::mask_unused_logits: set to the lowest float */
     uint32_t masked_count;
+    uint32_t direct_steps;          /* 0: once the same sequences have stepped twice in a row,
+                                       their decode step is recorded (adi_hip_decode_graph) and
+                                       replayed while they stay; nonzero: every step launched
+                                       directly */
 } adi_hip_batcher_options;
 
 /* adi::GenerationOptions (include/adi/generation.hpp:17-22); 0 output

@@ -172,6 +172,9 @@ def load_ref() -> C.CDLL:
     _declare(lib, "ref_force_isa_lanes", None, C.c_int)
     _declare(lib, "ref_avx512_vbmi", C.c_int)
     _declare(lib, "ref_worker_threads", C.c_uint32)
+    _declare(lib, "ref_kernel_profiling", None, C.c_int)
+    _declare(lib, "ref_kernel_profile", C.c_uint32, C.c_uint32, C.c_char_p, C.c_uint32,
+             C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64))
     _declare(lib, "ref_f16_to_f32", C.c_float, C.c_uint16)
     _declare(lib, "ref_f32_to_f16", C.c_uint16, C.c_float)
     _declare(lib, "ref_silu", C.c_float, C.c_float)
@@ -205,6 +208,20 @@ def load_ref() -> C.CDLL:
              C.c_float, C.c_uint32)
     _declare(lib, "ref_l2_normalize", C.c_int, f32p, C.c_uint32, C.c_float)
     return lib
+
+
+def ref_kernel_profiles(lib) -> dict:
+    """The reference's per-kind profile since ref_kernel_profiling(1):
+    {kind name: (calls, milliseconds, work items)} for kinds that ran."""
+    out = {}
+    calls, ns, work = C.c_uint64(), C.c_uint64(), C.c_uint64()
+    name = C.create_string_buffer(32)
+    count = lib.ref_kernel_profile(0, name, 32, C.byref(calls), C.byref(ns), C.byref(work))
+    for kind in range(count):
+        lib.ref_kernel_profile(kind, name, 32, C.byref(calls), C.byref(ns), C.byref(work))
+        if calls.value:
+            out[name.value.decode()] = (int(calls.value), ns.value / 1e6, int(work.value))
+    return out
 
 
 # ---- struct builders over numpy arrays (the caller keeps the arrays alive) --

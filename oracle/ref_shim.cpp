@@ -18,6 +18,7 @@
 #include "adi/generation.hpp"
 #include "adi/gguf.hpp"
 #include "adi/kernels.hpp"
+#include "adi/profiling.hpp"
 #include "attention.hpp"
 #include "codec_cache.hpp"
 #include "expert_trellis.hpp"
@@ -150,6 +151,36 @@ int ref_avx512_vbmi(void) {
 
 std::uint32_t ref_worker_threads(void) {
     return adi::worker_threads();
+}
+
+// The reference's per-kind kernel profile (include/adi/profiling.hpp:9-40),
+// as its bench commands print it (src/main.cpp:199-227): enabling resets it.
+void ref_kernel_profiling(int enabled) {
+    if (enabled != 0) {
+        adi::reset_kernel_profiles();
+    }
+    adi::set_kernel_profiling_enabled(enabled != 0);
+}
+
+// Kind `kind`'s name (up to `capacity` bytes with the terminator), calls,
+// nanoseconds and work items; returns the number of kinds.
+std::uint32_t ref_kernel_profile(std::uint32_t kind, char *name, std::uint32_t capacity,
+                                 std::uint64_t *calls, std::uint64_t *nanoseconds,
+                                 std::uint64_t *work_items) {
+    const auto profiles = adi::kernel_profiles();
+    const auto count = static_cast<std::uint32_t>(profiles.size());
+    if (kind < count) {
+        const auto text = adi::kernel_name(static_cast<adi::KernelKind>(kind));
+        const std::size_t n = std::min<std::size_t>(text.size(), capacity > 0 ? capacity - 1 : 0);
+        if (capacity > 0) {
+            std::memcpy(name, text.data(), n);
+            name[n] = '\0';
+        }
+        *calls = profiles[kind].calls;
+        *nanoseconds = profiles[kind].nanoseconds;
+        *work_items = profiles[kind].work_items;
+    }
+    return count;
 }
 
 float ref_f16_to_f32(std::uint16_t bits) { return adi::f16_to_f32(bits); }

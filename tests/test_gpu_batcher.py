@@ -180,6 +180,30 @@ def test_forced_failures_leave_the_loop_consistent(ctx, oracle, parts):
         b.close()
 
 
+def test_replayed_steps_give_the_direct_tokens(ctx, oracle, parts):
+    """Three sampled and greedy requests with the recorded-step replay on and
+    off: the same tokens (the replayed step gives the direct step's bits), and
+    both along the oracle's path."""
+    results = []
+    for replay in (True, False):
+        b = serving.ContinuousBatcher(ctx, parts["two"], max_batch=3, capacity=CAPACITY,
+                                      masked_tokens=MASKED, start=False, replay_steps=replay)
+        try:
+            ids = [b.submit([9, 4], max_output_tokens=7, temperature=0.0),
+                   b.submit([6], max_output_tokens=8, temperature=0.8, top_p=0.9, seed=5),
+                   b.submit([3, 3, 8], max_output_tokens=6, temperature=0.0)]
+            while b.step() != 0:
+                pass
+            results.append([b.result(i).tokens for i in ids])
+        finally:
+            b.close()
+    assert results[0] == results[1]
+    for prompt, toks, (t, p, seed) in zip([[9, 4], [6], [3, 3, 8]], results[0],
+                                          [(0.0, 0.9, 0), (0.8, 0.9, 5), (0.0, 0.9, 0)]):
+        compared, _ = check_path(oracle, parts, prompt, toks, t, p, seed)
+        assert compared >= len(toks) - 1
+
+
 def test_error_messages_are_per_thread(ctx):
     """A failed call on one thread leaves the context's message on other
     threads alone: a batcher's submit may fail on a client thread while the

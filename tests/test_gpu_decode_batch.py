@@ -171,3 +171,93 @@ def test_rejections_leave_states_untouched(gpu, parts):
     with pytest.raises(hip.HipError, match="prefill state mismatch"):
         hip.prefill(gpu, model, [1, 2, 3, 4, 5], s)  # more than the caches hold
     assert s.position == 0
+
+
+def bits(t):
+    return t.cpu().numpy().view(np.uint32)
+
+
+def twin_sequences(gpu, model, prompts, capacity):
+    """Two identical sets of sequences, each prefilled with the prompts."""
+    sets = []
+    for _ in range(2):
+        seqs = [hip.Sequence(model, capacity) for _ in prompts]
+        for p, s in zip(prompts, seqs):
+            if p:
+                hip.prefill(gpu, model, p, s, None, ubatch=128)
+        sets.append(seqs)
+    return sets
+
+
+@pytest.mark.parametrize("count", [1, 3, 20])
+def test_decode_graph_replays_equal_direct_steps(gpu, parts, count):
+    """A captured decode step replayed 8 times gives, bit for bit, the logits
+    and states of 8 directly launched adi_hip_decode_batch steps at the same
+    positions, fed the same (greedy) tokens from a device array; then the
+    positions are reset by the caller (the graph takes them over) and the
+    replays still match."""
+    model = parts["two"]
+    prompts = [[3 + (7 * i) % 500] * (i % 4) for i in range(count)]
+    direct, replayed = twin_sequences(gpu, model, prompts, CAPACITY)
+    tokens = torch.tensor([11 + i for i in range(count)], dtype=torch.int32, device="cuda")
+    want = torch.empty((count, VOCAB), dtype=torch.float32, device="cuda")
+    got = torch.empty_like(want)
+    graph = hip.DecodeGraph(gpu, model, replayed, tokens, got)
+    try:
+        for round_ in range(2):
+            for step in range(8 if round_ == 0 else 3):
+                print("decode graph", count, round_, step, flush=True)
+                host = [int(t) for t in tokens.cpu().numpy()]
+                hip.decode_batch(gpu, model, host, direct, want)
+                graph.launch()
+                assert np.array_equal(bits(got), bits(want)), (count, round_, step)
+                assert [s.position for s in replayed] == [s.position for s in direct]
+                picked = torch.empty(count, dtype=torch.int32, device="cuda")
+                hip.argmax_rows(gpu, want, count, VOCAB, picked)
+                tokens.copy_(picked)
+            for a, b in zip(direct, replayed):
+                for ta, tb in zip(a.tensors, b.tensors):
+                    for x, y in zip(ta, tb):
+                        assert torch.equal(x, y)
+            for s in direct + replayed:  # the caller resets every sequence
+                s.reset()
+        assert graph.captures == 1
+    finally:
+        graph.close()
+
+
+def test_decode_graph_recaptures_when_needed(gpu, parts):
+    """The graph re-records itself when the positions pass the span it
+    covers (512) and when a call in between has grown a scratch arena; the
+    replays stay equal to direct steps. A launch with other sequences is
+    rejected."""
+    model = parts["one"]
+    capacity = 520
+    prompt = [5 + (i * 13) % 400 for i in range(509)]
+    direct, replayed = twin_sequences(gpu, model, [prompt, prompt[:3]], capacity)
+    tokens = torch.tensor([17, 29], dtype=torch.int32, device="cuda")
+    want = torch.empty((2, VOCAB), dtype=torch.float32, device="cuda")
+    got = torch.empty_like(want)
+    graph = hip.DecodeGraph(gpu, model, replayed, tokens, got)
+    try:
+        for step in range(6):  # positions 509..514 of the first sequence
+            print("decode graph span", step, flush=True)
+            hip.decode_batch(gpu, model, [17, 29], direct, want)
+            graph.launch()
+            assert np.array_equal(bits(got), bits(want)), step
+        assert graph.captures == 2  # at position 512
+        # a larger call grows the shared scratch arenas
+        big = hip.Sequence(model, 300)
+        hip.prefill(gpu, model, list(range(3, 259)), big, None, ubatch=256)
+        hip.decode_batch(gpu, model, [17, 29], direct, want)
+        graph.launch()
+        assert np.array_equal(bits(got), bits(want))
+        assert graph.captures == 3
+        other = [hip.Sequence(model, capacity) for _ in range(2)]
+        states = (hip.DecoderStateStruct * 2)(*(s.struct for s in other))
+        status = gpu.lib.adi_hip_decode_graph_launch(graph.handle, states)
+        assert status == hip.INVALID_ARGUMENT
+        assert "differ from the captured" in gpu.lib.adi_hip_last_error(gpu.handle).decode()
+        assert [s.position for s in other] == [0, 0]
+    finally:
+        graph.close()

@@ -194,3 +194,41 @@ def test_stack40_model_entries_match_oracle(gpu, oracle, stack):
     gpu_checksum = check_states(oracle, g, want, seq.tensors, "model entries")
     print(f"stack40 model entries decoder_state_checksum: device {gpu_checksum:#018x}, oracle "
           f"{int(want['checksum'][0]):#018x}", flush=True)
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("count", [1, 4, 16])
+def test_stack40_graph_replay_equals_direct(gpu, stack, count):
+    """The benchmark's replayed decode step at the full geometry: `count`
+    sequences prefilled with the prompt, then 8 greedy steps replayed from one
+    captured step (adi_hip_decode_graph) give the logits of 8 direct
+    adi_hip_decode_batch steps bit for bit (one sequence runs the one-launch
+    MoE block and the one-launch NE projections inside the graph)."""
+    g, model = stack["g"], stack["model"]
+    prompt = [int(t) for t in stack["prompt"]]
+    capacity = g.prompt + 16
+    sets = []
+    for _ in range(2):
+        seqs = [hip.Sequence(model, capacity) for _ in range(count)]
+        for s in seqs:
+            hip.prefill(gpu, model, prompt, s, None, ubatch=g.ubatch)
+        sets.append(seqs)
+    direct, replayed = sets
+    tokens = torch.tensor([int(stack["want"]["tokens"][0])] * count, dtype=torch.int32, device="cuda")
+    want = torch.empty((count, g.vocab), dtype=torch.float32, device="cuda")
+    got = torch.empty_like(want)
+    graph = hip.DecodeGraph(gpu, model, replayed, tokens, got)
+    try:
+        for step in range(8):
+            print(f"stack40 graph replay, {count} sequences, step {step}", flush=True)
+            hip.decode_batch(gpu, model, [int(t) for t in tokens.cpu().numpy()], direct, want)
+            graph.launch()
+            assert np.array_equal(got.cpu().numpy().view(np.uint32),
+                                  want.cpu().numpy().view(np.uint32)), step
+            hip.argmax_rows(gpu, want, count, g.vocab, tokens)
+        gpu.synchronize()  # also reports a one-launch MoE wait that ran out
+        assert graph.captures == 1
+    finally:
+        graph.close()
+    del sets, direct, replayed
+    torch.cuda.empty_cache()
