@@ -1472,14 +1472,25 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
     const uint32_t lane = threadIdx.x & 63u;
     const bool helper = wave == kGemvWaves;
     const uint32_t half = (b >> 3) & 1u;
-    const uint32_t worker = ((b >> 4) << 3) | (b & 7u);
+    // Routed slot s lives on XCD s (blocks are dealt to the eight XCDs round
+    // robin, XCD b % 8): its gate and up items, the down x_hat built from
+    // their Z slices, its down items and its combine row all run on one XCD,
+    // so the hand-over data is read from that XCD's L2. Block b, the m-th of
+    // its (XCD, half) pair, takes gate or up items (m below or above half the
+    // pair's blocks) and its share of the slot's down items.
+    const uint32_t xcd = b & 7u, m_block = b >> 4;
+    const uint32_t per_entry = a.gu.expert_items_per_slot / kGemvWaves;  // blocks per (entry, half)
+    const uint32_t gu_which = m_block >= per_entry ? 1u : 0u;
+    const uint32_t item_gu = ((gu_which * kFusedSlots + xcd) * per_entry + (m_block - gu_which * per_entry)) *
+                                 kGemvWaves + wave;
+    const uint32_t item_dn = (xcd * (a.dn.expert_items_per_slot / kGemvWaves) + m_block) * kGemvWaves + wave;
     uint32_t *sync = a.sync;
     uint32_t *error = sync_line(sync, moe_sync::kError);
     uint32_t *logit_words = sync_line(sync, moe_sync::kLogits);  // complemented bits
     auto part = [&](uint32_t r) { return reinterpret_cast<float *>(sync_line(sync, moe_sync::kParts + 2u * r)); };
     // the block's routed slots: gate/up items (P1) and down items (P2)
-    const uint32_t slot1 = expert_item_of(a.gu, worker * kGemvWaves).slot;
-    const uint32_t slot2 = expert_item_of(a.dn, worker * kGemvWaves).slot;
+    const uint32_t slot1 = expert_item_of(a.gu, item_gu - wave).slot;
+    const uint32_t slot2 = expert_item_of(a.dn, item_dn - wave).slot;
     if (threadIdx.x < 12) {
         flags[threadIdx.x] = 0u;
     }
@@ -1614,7 +1625,6 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
     }
 
     // ---- P1 ----
-    const uint32_t item = worker * kGemvWaves + wave;  // gate/up and down items alike (GEMV waves)
     const uint2 *plane = reinterpret_cast<const uint2 *>(plane_lds);
     if (helper) {
         // every block routes the row itself once all logits are in: the
@@ -1658,7 +1668,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
         {
             // su of the block's (entry, slot) into LDS, loaded before the
             // GEMV waves' codes flood the memory queues
-            const ExpertItem it = expert_item_of(a.gu, worker * kGemvWaves);
+            const ExpertItem it = expert_item_of(a.gu, item_gu - wave);
             const uint4 *src = reinterpret_cast<const uint4 *>(
                 (it.which == 0 ? a.su_gate : a.su_up) + static_cast<size_t>(slots[slot1].x) * H);
             uint4 q[4];
@@ -1721,20 +1731,20 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
             sv4[i] = half_bits_to_float(su[64 * i + lane]);
         }
         hadamard_chunk(x_staged, sv4, wave, lane, x_routed);
-        expert_prefetch(a.gu, slots, item, half, lane, st, nullptr, false);
+        expert_prefetch(a.gu, slots, item_gu, half, lane, st, nullptr, false);
         arrive_and_wait(&flags[2], kGemvWaves, error);
         hadamard_cross(x_routed, a.scale_hidden, wave, lane);
         wait_plane();
         arrive_and_wait(&flags[8], kGemvWaves, error);
-        expert_prefetch_x(a.gu, item, half, lane, st, x_routed);
-        expert_compute<true>(a.gu, item, half, plane, lane, st);
+        expert_prefetch_x(a.gu, item_gu, half, lane, st, x_routed);
+        expert_compute<true>(a.gu, item_gu, half, plane, lane, st);
         count_block_quiet(&flags[3], kGemvWaves, sync_line(sync, moe_sync::kSlotCount + slot1));
     }
 
     // ---- P2 ----
     if (!helper) {
         ExpertStage st;
-        expert_prefetch(a.dn, slots, item, half, lane, st, nullptr, false);
+        expert_prefetch(a.dn, slots, item_dn, half, lane, st, nullptr, false);
         const uint4 info = slots[slot2];
         if (wave == 1) {  // off the helper's SIMD
             SwigluInputs in;
@@ -1762,8 +1772,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
             }
             wait_flag(&flags[4], error);
         }
-        expert_prefetch_x(a.dn, item, half, lane, st, x_down);
-        expert_compute<true>(a.dn, item, half, plane, lane, st);
+        expert_prefetch_x(a.dn, item_dn, half, lane, st, x_down);
+        expert_compute<true>(a.dn, item_dn, half, plane, lane, st);
         // the block's count; flags[9]: 1 = another block completes the slot,
         // 2 = this block does, 3 = its row is in, 4 = and it was the last
         wait_stores();
@@ -2317,6 +2327,14 @@ bool plan_moe_decode_one(adi_hip_context *ctx, MoeDecodeOne &a) {
         a.gu.expert_items_per_slot % kGemvWaves != 0 || a.dn.expert_items_per_slot % kGemvWaves != 0 ||
         a.experts + 1 > 2 * blocks || a.gu.ne_items != 2 * a.gu.ne_items_per_matrix ||
         a.gu.ne_items_per_matrix > blocks || a.dn.ne_items != blocks) {
+        return false;
+    }
+    // the slot-per-XCD assignment: eight slots on eight XCDs, each (XCD,
+    // half) pair's blocks running one slot's gate and up items (half each)
+    // and all of its down items
+    static_assert(kFusedSlots == 8, "one routed slot per XCD");
+    if (blocks % 32u != 0 || a.gu.expert_items_per_slot * 32u != blocks * kGemvWaves ||
+        a.dn.expert_items_per_slot * 16u != blocks * kGemvWaves) {
         return false;
     }
     // each half of the grid runs every item once
