@@ -203,13 +203,22 @@ typedef __bf16 hm_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float hm_f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t hm_u32x4 __attribute__((ext_vector_type(4)));
 
+// A quarter tile (8 groups of 16 rows: 16 row pieces of 320 bytes) as the
+// wave stages it: rows kHmStagePitch bytes apart.
+constexpr uint32_t kHmPieceBytes = kHmChunk * 40u;          // 320
+constexpr uint32_t kHmStagePitch = kHmPieceBytes + 16u;      // 336: rows start on other banks
+constexpr uint32_t kHmRawLoads = kHmTile * kHmPieceBytes / (16u * 64u);  // 5 16-byte loads a lane
+
 struct HeadMfmaLds {
     hm_u32x4 b[kHmGroups][2][4][16];  // B fragment of (group, MFMA, lane / 16, column)
-    hm_f32x4 c[kHmGroups][16];        // -K of (group, column), the accumulator's start
+    float c[kHmGroups][16];           // -K of (group, column), the accumulator's start
     union {
-        float part[kHmGroups][16][8];            // K's partial sums while the tables build
-        float scale[kHmWaves][kHmGroups][kHmTile];  // each wave's tile scales
+        float part[kHmGroups][16][8];               // K's partial sums while the tables build
+        uint16_t scale[kHmWaves][kHmGroups][kHmTile];  // each wave's tile scales (f16 bits)
     } u;
+    // each wave's staging of the quarter tile it sums (the coalesced loads'
+    // bytes, read back in the A layout)
+    uint32_t stage[kHmWaves][kHmTile * kHmStagePitch / 4];
 };
 
 // The two codes of each A dword, by MFMA and dword: (low half, high half).
@@ -256,6 +265,13 @@ typedef __attribute__((address_space(3))) const hm_u32x4 *hm_lds_u32x4;
 typedef __attribute__((address_space(3))) const hm_f32x4 *hm_lds_f32x4;
 __device__ __forceinline__ hm_u32x4 hm_lds_u(uint32_t address) {
     return *reinterpret_cast<hm_lds_u32x4>(static_cast<size_t>(address));
+}
+__device__ __forceinline__ float hm_lds_f1(uint32_t address) {
+    return *reinterpret_cast<__attribute__((address_space(3))) const float *>(static_cast<size_t>(address));
+}
+typedef uint32_t hm_u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ hm_u32x2 hm_lds_u2(uint32_t address) {
+    return *reinterpret_cast<__attribute__((address_space(3))) const hm_u32x2 *>(static_cast<size_t>(address));
 }
 __device__ __forceinline__ hm_f32x4 hm_lds_f(uint32_t address) {
     return *reinterpret_cast<hm_lds_f32x4>(static_cast<size_t>(address));
@@ -322,7 +338,7 @@ __device__ void hm_build_tables(HeadMfmaLds &L, const float *__restrict__ x, uin
         for (uint32_t j = 0; j < 8; ++j) {
             k += L.u.part[g][n][j];
         }
-        L.c[g][n] = hm_f32x4{-k, -k, -k, -k};
+        L.c[g][n] = -k;
     }
     __syncthreads();
 }
@@ -344,8 +360,13 @@ __device__ __forceinline__ void hm_load(const uint8_t *__restrict__ row_codes, u
 
 // Wave w takes tiles w, w + waves, ...; per pass of four tokens it leaves
 // the logits and, with BOUNDS, the bounds and its per-token summary
-// (HeadWaveBest) for the arg-max.
-template <bool BOUNDS>
+// (HeadWaveBest) for the arg-max. With COALESCED (16-byte aligned codes) a
+// quarter tile is loaded as 16-byte pieces in row order, each load
+// instruction of the wave covering about 1 KiB of consecutive bytes, and
+// staged in the wave's LDS before its lanes read their three dwords of each
+// group; otherwise each lane loads its three dwords of every group itself
+// (16 rows' 40-byte groups a load instruction). Both give the same bits.
+template <bool BOUNDS, bool COALESCED>
 __global__ __launch_bounds__(kHmThreads) void k_head_mfma(
     const uint8_t *__restrict__ packed, const uint16_t *__restrict__ scales, uint32_t rows,
     const float *__restrict__ x, uint32_t batch, float *__restrict__ logits,
@@ -360,16 +381,16 @@ __global__ __launch_bounds__(kHmThreads) void k_head_mfma(
     const uint32_t q = lane / 16u, i_row = lane % 16u;
     const uint32_t n = lane % 16u, p = lane % 4u, t_lane = n / 4u;
     const uint32_t shift = 16u * (q & 1u);
-    float *sc = &L.u.scale[wave][0][0];
+    uint16_t *sc = &L.u.scale[wave][0][0];
     // LDS byte addresses of this lane's B fragment, accumulator start and
     // scales for group 0; group g adds g * 2048, g * 256, g * 64
     const uint32_t lds0 = static_cast<uint32_t>(
         (uintptr_t)(__attribute__((address_space(3))) unsigned char *)hm_raw);
     const uint32_t b_at = hm_opaque(lds0 + static_cast<uint32_t>(offsetof(HeadMfmaLds, b)) +
                                     q * 256u + n * 16u);
-    const uint32_t c_at = hm_opaque(lds0 + static_cast<uint32_t>(offsetof(HeadMfmaLds, c)) + n * 16u);
+    const uint32_t c_at = hm_opaque(lds0 + static_cast<uint32_t>(offsetof(HeadMfmaLds, c)) + n * 4u);
     const uint32_t s_at = hm_opaque(lds0 + static_cast<uint32_t>(offsetof(HeadMfmaLds, u)) +
-                                    (wave * kHmGroups * kHmTile + 4u * q) * 4u);
+                                    (wave * kHmGroups * kHmTile + 4u * q) * 2u);
 
     for (uint32_t t0 = 0; t0 < batch; t0 += kHmTokens) {
         float best_v = -INFINITY, upper = -INFINITY;
@@ -377,7 +398,8 @@ __global__ __launch_bounds__(kHmThreads) void k_head_mfma(
         // a ring of the four quarter-tile chunks: after a chunk is summed its
         // slot loads the same chunk of the wave's next tile, three chunks of
         // codes (18 KiB a wave) in flight while one is summed
-        uint32_t w[4][kHmChunk][3];
+        uint32_t w[COALESCED ? 1 : 4][kHmChunk][3];
+        hm_u32x4 raw[COALESCED ? 4 : 1][kHmRawLoads];
         hm_u32x4 sreg = hm_u32x4{0u, 0u, 0u, 0u};
         uint32_t tile = wave_global;
         // the first tile's codes and scales load while the tables build
@@ -392,6 +414,44 @@ __global__ __launch_bounds__(kHmThreads) void k_head_mfma(
                 hm_load(rc, kHmChunk * part + g, q, dst[g]);
             }
         };
+        // load k of a lane: piece e = 64 k + lane of the quarter tile, row
+        // e / 20, bytes 16 (e % 20) .. + 15 of that row's 320
+        const auto load_raw = [&](uint32_t t, uint32_t part, hm_u32x4 (&dst)[kHmRawLoads]) {
+#pragma unroll
+            for (uint32_t k = 0; k < kHmRawLoads; ++k) {
+                const uint32_t e = 64u * k + lane;
+                const uint32_t r = e / 20u, piece = e % 20u;
+                dst[k] = *reinterpret_cast<const hm_u32x4 *>(
+                    packed + static_cast<size_t>(row_of(t, r)) * 1280u + kHmPieceBytes * part + 16u * piece);
+            }
+        };
+        uint32_t *stage = &L.stage[wave][0];
+        // the staged quarter tile back as the lane's three dwords of each of
+        // its eight groups (the bytes hm_load reads from memory)
+        const auto unstage = [&](const hm_u32x4 (&src)[kHmRawLoads], uint32_t (&dst)[kHmChunk][3]) {
+#pragma unroll
+            for (uint32_t k = 0; k < kHmRawLoads; ++k) {
+                const uint32_t e = 64u * k + lane;
+                const uint32_t r = e / 20u, piece = e % 20u;
+                *reinterpret_cast<hm_u32x4 *>(stage + (r * kHmStagePitch + 16u * piece) / 4u) = src[k];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const uint32_t *row = stage + (i_row * kHmStagePitch) / 4u;
+#pragma unroll
+            for (uint32_t g = 0; g < kHmChunk; ++g) {
+                const uint32_t *at = row + (40u * g + 10u * q - 2u * (q & 1u)) / 4u;
+#pragma unroll
+                for (uint32_t i = 0; i < 3; ++i) {
+                    dst[g][i] = at[i];
+                }
+            }
+            // every lane's reads end before the next quarter is staged
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        };
         const auto load_scales = [&](uint32_t t) {
             // lane l: row l / 4, groups 8 (l % 4) .. + 7
             const hm_u32x4 *src = reinterpret_cast<const hm_u32x4 *>(
@@ -399,10 +459,17 @@ __global__ __launch_bounds__(kHmThreads) void k_head_mfma(
             sreg = *src;
         };
         if (tile < tiles) {
-            load_chunk(tile, 0, w[0]);
-            load_chunk(tile, 1, w[1]);
-            load_chunk(tile, 2, w[2]);
-            load_chunk(tile, 3, w[3]);
+            if constexpr (COALESCED) {
+                load_raw(tile, 0, raw[0]);
+                load_raw(tile, 1, raw[1]);
+                load_raw(tile, 2, raw[2]);
+                load_raw(tile, 3, raw[3]);
+            } else {
+                load_chunk(tile, 0, w[0]);
+                load_chunk(tile, 1, w[1]);
+                load_chunk(tile, 2, w[2]);
+                load_chunk(tile, 3, w[3]);
+            }
             load_scales(tile);
         }
         if (t0 > 0) {
@@ -410,11 +477,11 @@ __global__ __launch_bounds__(kHmThreads) void k_head_mfma(
         }
         hm_build_tables(L, x, t0, batch);
         for (; tile < tiles; tile += wave_count) {
-            // this tile's scales, transposed: sc[g][row] as floats
+            // this tile's scales, transposed: sc[g][row] as f16 bits
 #pragma unroll
             for (uint32_t e = 0; e < 8; ++e) {
                 const uint32_t bits = sreg[e / 2] >> (16u * (e % 2u));
-                sc[(8u * (lane % 4u) + e) * kHmTile + lane / 4u] = half_bits_to_float(bits & 0xFFFFu);
+                sc[(8u * (lane % 4u) + e) * kHmTile + lane / 4u] = static_cast<uint16_t>(bits & 0xFFFFu);
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
@@ -429,9 +496,14 @@ __global__ __launch_bounds__(kHmThreads) void k_head_mfma(
                     const uint32_t w2 = src[j][2] >> shift;
                     hm_u32x4 a0, a1;
                     hm_decode(w0, w1, w2, a0, a1);
-                    hm_f32x4 acc = hm_mfma(a0, hm_lds_u(b_at + g * 2048u), hm_lds_f(c_at + g * 256u));
+                    // the group's accumulator start is one float per column
+                    // (the same for the four rows a lane holds)
+                    const float c0 = hm_lds_f1(c_at + g * 64u);
+                    hm_f32x4 acc = hm_mfma(a0, hm_lds_u(b_at + g * 2048u), hm_f32x4{c0, c0, c0, c0});
                     acc = hm_mfma(a1, hm_lds_u(b_at + g * 2048u + 1024u), acc);
-                    const hm_f32x4 s = hm_lds_f(s_at + g * 64u);
+                    const hm_u32x2 sb = hm_lds_u2(s_at + g * 32u);
+                    const hm_f32x4 s = hm_f32x4{half_bits_to_float(sb.x & 0xFFFFu), half_bits_to_float(sb.x >> 16),
+                                                half_bits_to_float(sb.y & 0xFFFFu), half_bits_to_float(sb.y >> 16)};
                     out.x = fmaf(s.x, acc.x, out.x);
                     out.y = fmaf(s.y, acc.y, out.y);
                     out.z = fmaf(s.z, acc.z, out.z);
@@ -445,15 +517,33 @@ __global__ __launch_bounds__(kHmThreads) void k_head_mfma(
             // past the last tile the loads read the last row again (row_of
             // clamps), unused: no branch breaks the in-order load counts
             const uint32_t next = tile + wave_count;
-            run_chunk(0, w[0]);
-            load_chunk(next, 0, w[0]);
-            load_scales(next);
-            run_chunk(1, w[1]);
-            load_chunk(next, 1, w[1]);
-            run_chunk(2, w[2]);
-            load_chunk(next, 2, w[2]);
-            run_chunk(3, w[3]);
-            load_chunk(next, 3, w[3]);
+            if constexpr (COALESCED) {
+                // each quarter staged and read back, its registers then
+                // reloaded with the next tile's quarter
+                unstage(raw[0], w[0]);
+                load_raw(next, 0, raw[0]);
+                load_scales(next);
+                run_chunk(0, w[0]);
+                unstage(raw[1], w[0]);
+                load_raw(next, 1, raw[1]);
+                run_chunk(1, w[0]);
+                unstage(raw[2], w[0]);
+                load_raw(next, 2, raw[2]);
+                run_chunk(2, w[0]);
+                unstage(raw[3], w[0]);
+                load_raw(next, 3, raw[3]);
+                run_chunk(3, w[0]);
+            } else {
+                run_chunk(0, w[0]);
+                load_chunk(next, 0, w[0]);
+                load_scales(next);
+                run_chunk(1, w[1]);
+                load_chunk(next, 1, w[1]);
+                run_chunk(2, w[2]);
+                load_chunk(next, 2, w[2]);
+                run_chunk(3, w[3]);
+                load_chunk(next, 3, w[3]);
+            }
             // every lane's reads of this tile's scales end before the next
             // tile's are written
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -937,10 +1027,17 @@ void head_logits(adi_hip_context *ctx, const adi_hip_head_chunk *h, const float 
                                                    static_cast<uint32_t>(ctx->cu_count) * 8u);
         if (quads == 64u) {
             const uint32_t wide = head_wide_blocks(ctx, h->rows);
-            const auto kernel = bounds != nullptr ? k_head_mfma<true> : k_head_mfma<false>;
+            // 16-byte aligned codes (every row is 1280 bytes) take the
+            // coalesced loads
+            const bool coalesced = aligned_to(h->packed, 16);
+            const auto kernel = bounds != nullptr
+                                    ? (coalesced ? k_head_mfma<true, true> : k_head_mfma<true, false>)
+                                    : (coalesced ? k_head_mfma<false, true> : k_head_mfma<false, false>);
             static const bool ready =
-                set_lds_limit(reinterpret_cast<const void *>(&k_head_mfma<true>), sizeof(HeadMfmaLds)) &&
-                set_lds_limit(reinterpret_cast<const void *>(&k_head_mfma<false>), sizeof(HeadMfmaLds));
+                set_lds_limit(reinterpret_cast<const void *>(&k_head_mfma<true, true>), sizeof(HeadMfmaLds)) &&
+                set_lds_limit(reinterpret_cast<const void *>(&k_head_mfma<false, true>), sizeof(HeadMfmaLds)) &&
+                set_lds_limit(reinterpret_cast<const void *>(&k_head_mfma<true, false>), sizeof(HeadMfmaLds)) &&
+                set_lds_limit(reinterpret_cast<const void *>(&k_head_mfma<false, false>), sizeof(HeadMfmaLds));
             (void)ready;
             launch(ctx, "head_mfma", kernel, dim3(wide), dim3(kHmThreads), sizeof(HeadMfmaLds),
                    h->packed, h->group_scale_f16, h->rows, x, batch, logits, bounds, best);
