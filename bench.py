@@ -73,6 +73,11 @@ def parse():
     p.add_argument("--projection-cpu-seconds", type=float, default=2.0,
                    help="CPU baseline budget per projection figure")
     p.add_argument("--no-projections", action="store_true")
+    p.add_argument("--no-graph", action="store_true",
+                   help="skip the graph-replay timing of the projections (counter runs)")
+    p.add_argument("--projections-only", type=str, default="",
+                   help="run only these packed projections (comma list of head_b1, head_b4, ne_b1, "
+                        "ne_b4) and print their figures: one workload per profiler run")
     p.add_argument("--copy-bytes", type=int, default=0,
                    help="first run a plain device-to-device copy of this many bytes three times "
                         "(the calibration launch for the HBM byte counters)")
@@ -526,19 +531,23 @@ def projection_cpu_baseline(seconds):
             "per_call": out}
 
 
-def projections(torch, hip, ctx, steps, runs, cpu_seconds):
+def projections(torch, hip, ctx, steps, runs, cpu_seconds, only=None, graphs=True):
     from adi_amd import synthetic as syn
     res = {}
+    want = lambda name: only is None or name in only
     rng = syn.rng_for(1, 0)
     copies = 3  # 3 x 204 MB heads exceed the 256 MB Infinity Cache
     heads = [hip.upload_head(ctx, syn.head_chunk(rng, HEAD_ROWS, HEAD_COLUMNS)) for _ in range(copies)]
     for batch in (1, 4):
+        if not want(f"head_b{batch}"):
+            syn.hidden_states(rng, batch, HEAD_COLUMNS)  # the later draws stay those of a full run
+            continue
         x = ctx.to_device(syn.rms_normalized(syn.hidden_states(rng, batch, HEAD_COLUMNS)))
         out = torch.empty((batch, HEAD_ROWS), dtype=torch.float32, device="cuda")
         call = lambda i: hip.head_matmul(ctx, heads[i % copies], x, batch, out)
         dt = median_seconds(torch, call, steps, runs)
         ctx.synchronize()
-        us = graph_us(torch, ctx, call, 30)
+        us = graph_us(torch, ctx, call, 30) if graphs else float("nan")
         key = f"head_151936x2048_b{batch}"
         res[key] = {
             "ms_per_call": round(dt * 1e3, 4), "vectors_per_s": round(batch / dt, 1),
@@ -561,13 +570,15 @@ def projections(torch, hip, ctx, steps, runs, cpu_seconds):
                          base.weight_scale, book) for i in range(count)]
     nbytes = base.trellis.size * 2 + 4096
     for batch in (1, 4):
+        if not want(f"ne_b{batch}"):
+            continue
         x = ctx.to_device(syn.hidden_states(rng, batch, 2048))
         out = torch.empty((batch, 2048), dtype=torch.float32, device="cuda")
         call = lambda i: ctx.check(ctx.lib.adi_hip_ne_matmul(
             ctx.handle, hip.C.byref(mats[i % count]), x.data_ptr(), batch, out.data_ptr()))
         dt = median_seconds(torch, call, max(steps, count), runs)
         ctx.synchronize()
-        us = graph_us(torch, ctx, call, count)
+        us = graph_us(torch, ctx, call, count) if graphs else float("nan")
         key = f"ne_2048x2048_b{batch}"
         res[key] = {
             "ms_per_call": round(dt * 1e3, 4), "vectors_per_s": round(batch / dt, 1),
@@ -580,6 +591,8 @@ def projections(torch, hip, ctx, steps, runs, cpu_seconds):
             "rocprof_avg_us": rocprof_avg_us("ne_fused", key, PROJ_STATS),
             "traffic": traffic_from_profile("ne_fused", key, PROJ_TRAFFIC)}
     del trellis, mats
+    if only is not None:
+        return res
     if cpu_seconds > 0:
         log("projections: cpu baseline")
         cpu = projection_cpu_baseline(cpu_seconds)
@@ -790,6 +803,12 @@ def main():
     ctx = hip.Context(0)
     if args.copy_bytes > 0:
         copy_calibration(torch, args.copy_bytes)
+    if args.projections_only:
+        only = set(args.projections_only.split(","))
+        print(json.dumps({"projections": projections(torch, hip, ctx, args.steps, args.runs, 0.0, only,
+                                                     graphs=not args.no_graph)}))
+        ctx.close()
+        return
     log("generating weights")
     rng = syn.rng_for(2, 0)
     layer_host = syn.moe_layer(rng)
