@@ -15,7 +15,9 @@ from typing import Optional
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIBRARY = os.path.join(HERE, "libadi_hip.so")
+# ADI_HIP_LIBRARY names another build of the same library (the host-side
+# sanitizer build of tests/sanitize.sh); by default the in-tree one.
+LIBRARY = os.environ.get("ADI_HIP_LIBRARY") or os.path.join(HERE, "libadi_hip.so")
 
 OK = 0
 INVALID_ARGUMENT = -1

@@ -14,7 +14,9 @@ from typing import Optional
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-ORACLE_PATH = os.path.join(HERE, "liboracle.so")
+# ADI_ORACLE_LIBRARY names another build of the oracle (the sanitizer build
+# of tests/sanitize.sh); by default the in-tree one.
+ORACLE_PATH = os.environ.get("ADI_ORACLE_LIBRARY") or os.path.join(HERE, "liboracle.so")
 REF_PATH = os.path.join(HERE, "_ref", "libadi_ref.so")
 
 u16p = C.POINTER(C.c_uint16)
