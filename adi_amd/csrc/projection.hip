@@ -1737,7 +1737,10 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
         wait_plane();
         arrive_and_wait(&flags[8], kGemvWaves, error);
         expert_prefetch_x(a.gu, item_gu, half, lane, st, x_routed);
-        expert_compute<true>(a.gu, item_gu, half, plane, lane, st);
+        // plain stores: only the slot's down blocks read these Z slices, on
+        // this XCD, so they only have to reach its L2 (the block's count
+        // goes out once they have)
+        expert_compute<false>(a.gu, item_gu, half, plane, lane, st);
         count_block_quiet(&flags[3], kGemvWaves, sync_line(sync, moe_sync::kSlotCount + slot1));
     }
 
@@ -1773,7 +1776,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
             wait_flag(&flags[4], error);
         }
         expert_prefetch_x(a.dn, item_dn, half, lane, st, x_down);
-        expert_compute<true>(a.dn, item_dn, half, plane, lane, st);
+        expert_compute<false>(a.dn, item_dn, half, plane, lane, st);  // read on this XCD only, as above
         // the block's count; flags[9]: 1 = another block completes the slot,
         // 2 = this block does, 3 = its row is in, 4 = and it was the last
         wait_stores();
