@@ -27,6 +27,7 @@
 // reductions); results agree to float rounding.
 #include "attention.hpp"
 #include "dense.hpp"
+#include "projection.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -590,6 +591,26 @@ void forward(adi_hip_context *ctx, int status) {
     }
 }
 
+// The query (with its gate), key and value projections of the same rows
+// (three backend.ne_matmul calls, src/executor.cpp:596-613) in one NE launch
+// where it takes the shapes.
+void project_qkv(adi_hip_context *ctx, const adi_hip_full_attention *L, const float *inputs,
+                 uint32_t count, float *query_gate, float *key, float *value) {
+    const adi_hip_ne_matrix *m[3] = {&L->query, &L->key, &L->value};
+    float *out[3] = {query_gate, key, value};
+    ne_matmul_group(ctx, m, 3, inputs, count, out);
+}
+
+// The Gated DeltaNet's qkv and gate projections of the same rows (two
+// backend.ne_matmul calls, src/executor.cpp:764-775) in one NE launch where
+// it takes the shapes.
+void project_qkv_gate(adi_hip_context *ctx, const adi_hip_linear_attention *L, const float *inputs,
+                      uint32_t count, float *qkv, float *gate) {
+    const adi_hip_ne_matrix *m[2] = {&L->qkv, &L->gate};
+    float *out[2] = {qkv, gate};
+    ne_matmul_group(ctx, m, 2, inputs, count, out);
+}
+
 bool ne_shaped(const adi_hip_ne_matrix &m, uint32_t rows, uint32_t columns) {
     return m.rows == rows && m.columns == columns && m.trellis != nullptr;
 }
@@ -629,9 +650,7 @@ void full_attention_chunk(adi_hip_context *ctx, const adi_hip_full_attention *L,
     float *partial = ws.take<float>(size_t(count) * kQueryHeads * splits * kPartialStride);
     float *key = keys + static_cast<size_t>(position) * kKvHeads * kHeadSize;
     float *value = values + static_cast<size_t>(position) * kKvHeads * kHeadSize;
-    forward(ctx, adi_hip_ne_matmul(ctx, &L->query, inputs, count, query_gate));
-    forward(ctx, adi_hip_ne_matmul(ctx, &L->key, inputs, count, key));
-    forward(ctx, adi_hip_ne_matmul(ctx, &L->value, inputs, count, value));
+    project_qkv(ctx, L, inputs, count, query_gate, key, value);
     launch(ctx, "attention_norm_rope", k_norm_rope, dim3(kQueryHeads + kKvHeads, count),
            dim3(kHeadSize), 0, query_gate, key, L->query_norm, L->key_norm,
            count == 1 ? rope_table(position) : RopeTable{},
@@ -677,8 +696,7 @@ void linear_attention_chunk(adi_hip_context *ctx, const adi_hip_linear_attention
     float *normalized = ws.take<float>(n * kValueSize);
     float *alpha = ws.take<float>(n * kValueHeads);
     float *beta = ws.take<float>(n * kValueHeads);
-    forward(ctx, adi_hip_ne_matmul(ctx, &L->qkv, inputs, count, qkv));
-    forward(ctx, adi_hip_ne_matmul(ctx, &L->gate, inputs, count, gate));
+    project_qkv_gate(ctx, L, inputs, count, qkv, gate);
     forward(ctx, adi_hip_bf16_matmul(ctx, &L->alpha, inputs, count, alpha));
     forward(ctx, adi_hip_bf16_matmul(ctx, &L->beta, inputs, count, beta));
     launch(ctx, "linear_conv", k_linear_conv, dim3(kChannels / kLinearHead, count),
@@ -803,9 +821,7 @@ void full_attention_rows(adi_hip_context *ctx, const adi_hip_full_attention *L, 
     float *value = ws.take<float>(n * kKvHeads * kHeadSize);
     float *attended = ws.take<float>(n * kQueryHeads * kHeadSize);
     float *partial = ws.take<float>(n * kQueryHeads * splits * kPartialStride);
-    forward(ctx, adi_hip_ne_matmul(ctx, &L->query, inputs, rows, query_gate));
-    forward(ctx, adi_hip_ne_matmul(ctx, &L->key, inputs, rows, key));
-    forward(ctx, adi_hip_ne_matmul(ctx, &L->value, inputs, rows, value));
+    project_qkv(ctx, L, inputs, rows, query_gate, key, value);
     const float *rope = rope_rows(ctx, last);
     for (uint32_t first = 0; first < rows; first += kRowGroup) {
         const uint32_t count = rows - first < kRowGroup ? rows - first : kRowGroup;
@@ -871,8 +887,7 @@ void linear_attention_rows(adi_hip_context *ctx, const adi_hip_linear_attention 
     float *normalized = ws.take<float>(n * kValueSize);
     float *alpha = ws.take<float>(n * kValueHeads);
     float *beta = ws.take<float>(n * kValueHeads);
-    forward(ctx, adi_hip_ne_matmul(ctx, &L->qkv, inputs, rows, qkv));
-    forward(ctx, adi_hip_ne_matmul(ctx, &L->gate, inputs, rows, gate));
+    project_qkv_gate(ctx, L, inputs, rows, qkv, gate);
     forward(ctx, adi_hip_bf16_matmul(ctx, &L->alpha, inputs, rows, alpha));
     forward(ctx, adi_hip_bf16_matmul(ctx, &L->beta, inputs, rows, beta));
     for (uint32_t first = 0; first < rows; first += kRowGroup) {

@@ -1863,36 +1863,90 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
 //
 // y = sv * H_rows(W x_hat) * scale_rows with x_hat = H_columns(su * x) *
 // scale_columns (src/kernels.cpp:899-979), for up to kNeFusedRows input rows,
-// in one launch instead of prologue, GEMV and epilogue. Block b takes tile
-// rows b, b + blocks, ... whole: it builds every input row's x_hat itself
-// (eight waves' cooperative transform, bit-identical to the one-wave one),
-// runs the tile row's NE items (16 tiles each, the GEMV's arithmetic, the
-// table values gathered once per item), and adds the items' partial sums in
-// item (slice) order in LDS, so the sum is the one the separate epilogue
-// forms. With two or more input rows the grid is two halves: half g takes
-// input rows g, g + 2, ... of every tile row (each half decodes the codes
-// itself), so the VALU work of the input rows spreads over all CUs. The
-// block of a half that completes its last tile row (a ticket per half;
-// nobody waits) runs the row transform over that half's sums.
-template <int VC, int VR>
+// in one launch instead of prologue, GEMV and epilogue. A launch carries up to
+// kNeFusedJobs matrices of one column count over the same input rows, each on
+// a range of blocks of its own; block b of a matrix takes its tile rows b,
+// b + blocks, ... whole: it builds every input row's x_hat itself (eight
+// waves' cooperative transform, bit-identical to the one-wave one), runs the
+// tile row's NE items (16 tiles each, the GEMV's arithmetic, the table values
+// gathered once per item), and adds the items' partial sums in item (slice)
+// order in LDS, so the sum is the one the separate epilogue forms. With two or
+// more input rows the grid is two halves: half g takes input rows g, g + 2,
+// ... of every tile row (each half decodes the codes itself), so the VALU work
+// of the input rows spreads over all CUs. The block of a matrix and half that
+// completes its last tile row (a ticket each; nobody waits) runs the row
+// transform over that half's sums.
+template <int VR>
+__device__ void ne_fused_rows(const NeFusedJob &job, float *ne_lds, const int8_t *sv_lds, uint32_t group,
+                              uint32_t halves, uint32_t batch, uint32_t w8, uint32_t lane) {
+    constexpr uint32_t R = 512u * VR, RH = R / 8u;
+    // every sum of the half's input rows is in (first touch here, ordinary
+    // loads; all the loads first)
+    {
+        float v[kNeFusedRows][VR];
+#pragma unroll
+        for (uint32_t i = 0; i < kNeFusedRows; ++i) {
+            const uint32_t p = group + halves * i;
+            if (p < batch) {
+                load_wave<VR>(job.zsum + static_cast<size_t>(p) * R + w8 * RH, lane, v[i]);
+            }
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < kNeFusedRows; ++i) {
+            const uint32_t p = group + halves * i;
+            if (p < batch) {
+                wave_hadamard<VR>(v[i], 1.0f, lane);
+                store_wave<VR>(ne_lds + p * R + w8 * RH, lane, v[i]);
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t p = group; p < batch; p += halves) {
+        hadamard_cross_span<RH>(ne_lds + p * R, job.scale_rows, w8, lane);
+    }
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < R; e += kNeFusedThreads) {
+        const float sign = static_cast<float>(sv_lds[e]);
+#pragma unroll
+        for (uint32_t i = 0; i < kNeFusedRows; ++i) {
+            const uint32_t p = group + halves * i;
+            if (p < batch) {
+                job.out[p * R + e] = ne_lds[p * R + e] * sign;
+            }
+        }
+    }
+}
+
+template <int VC>
 __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
 #pragma clang fp contract(off)
-    extern __shared__ float ne_lds[];  // x_hat [batch][C], then the outputs [batch][R]
+    extern __shared__ float ne_lds[];  // x_hat [batch][C], then the outputs [batch][rows]
     __shared__ uint32_t table[1024];
     __shared__ float part[kNeFusedMaxItems][16][kNeFusedRows];  // [item in tile row][row][input row]
     __shared__ uint32_t last;
-    constexpr uint32_t C = 512u * VC, R = 512u * VR, CH = C / 8u, RH = R / 8u;
-    __shared__ int8_t sv_lds[R];  // the output signs, staged by every block for whichever ends last
+    __shared__ int8_t sv_lds[kNeFusedMaxRows];  // the output signs, staged by every block for whichever ends last
+    constexpr uint32_t C = 512u * VC, CH = C / 8u;
     constexpr uint32_t tile_columns = C / kTile, per_row = tile_columns / 16u;
-    constexpr uint32_t tile_rows = R / kTile;
     constexpr uint32_t kMine = kNeFusedRows;  // input rows of a half, at most
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t w8 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t quad = lane & 3u, tslot = lane >> 2;
     const uint32_t halves = a.halves;
-    const uint32_t group = blockIdx.x % halves;      // the half: input rows group, group + halves, ...
-    const uint32_t b = blockIdx.x / halves, blocks = gridDim.x / halves;  // within the half
-    uint32_t *ticket = a.ticket + 32u * group;
+    const uint32_t group = blockIdx.x % halves;  // the half: input rows group, group + halves, ...
+    const uint32_t g = blockIdx.x / halves;      // block within the half
+    // the block's matrix (constant indexes only, so the arguments stay in
+    // the kernel argument segment)
+    uint32_t j = 0;
+    if (a.jobs > 1u && g >= a.job[1].first_block) {
+        j = 1;
+    }
+    if (a.jobs > 2u && g >= a.job[2].first_block) {
+        j = 2;
+    }
+    const NeFusedJob job = j == 0 ? a.job[0] : (j == 1 ? a.job[1] : a.job[2]);
+    const uint32_t R = job.rows, tile_rows = R / kTile;
+    const uint32_t b = g - job.first_block, blocks = job.blocks;  // within the matrix and half
+    uint32_t *ticket = a.ticket + 32u * (2u * j + group);
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     // the codes of the block's first tile row go out first
     constexpr uint32_t kWaveItems = per_row > 8u ? per_row / 8u : 1u;
@@ -1900,24 +1954,24 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
     auto load_codes = [&](uint32_t tr) {
 #pragma unroll
         for (uint32_t q = 0; q < kWaveItems; ++q) {
-            const uint32_t j = w8 + 8u * q;
-            const uint32_t tile = (tr * per_row + (j < per_row ? j : 0u)) * 16u + tslot;
-            const u32x4 *src = reinterpret_cast<const u32x4 *>(a.trellis) + static_cast<size_t>(tile) * 8u + quad * 2u;
+            const uint32_t i = w8 + 8u * q;
+            const uint32_t tile = (tr * per_row + (i < per_row ? i : 0u)) * 16u + tslot;
+            const u32x4 *src = reinterpret_cast<const u32x4 *>(job.trellis) + static_cast<size_t>(tile) * 8u + quad * 2u;
             code[q][0] = __builtin_nontemporal_load(src);
             code[q][1] = __builtin_nontemporal_load(src + 1);
         }
     };
     load_codes(b);
     for (uint32_t i = threadIdx.x; i < 1024u; i += kNeFusedThreads) {
-        table[i] = a.table[i];
+        table[i] = job.table[i];
     }
     for (uint32_t i = threadIdx.x; i < R / 4u; i += kNeFusedThreads) {
-        reinterpret_cast<uint32_t *>(sv_lds)[i] = reinterpret_cast<const uint32_t *>(a.sv)[i];
+        reinterpret_cast<uint32_t *>(sv_lds)[i] = reinterpret_cast<const uint32_t *>(job.sv)[i];
     }
     // x_hat of the half's input rows (their loads first)
     {
         float v[kMine][VC], s[VC];
-        load_wave_sign<VC>(a.su + w8 * CH, lane, s);
+        load_wave_sign<VC>(job.su + w8 * CH, lane, s);
 #pragma unroll
         for (uint32_t i = 0; i < kMine; ++i) {
             const uint32_t p = group + halves * i;
@@ -1946,8 +2000,8 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
     for (uint32_t tr = b; tr < tile_rows; tr += blocks) {
 #pragma unroll
         for (uint32_t q = 0; q < kWaveItems; ++q) {
-            const uint32_t j = w8 + 8u * q;
-            if (j < per_row) {
+            const uint32_t i8 = w8 + 8u * q;
+            if (i8 < per_row) {
                 const uint32_t d[9] = {code[q][0].x, code[q][0].y, code[q][0].z, code[q][0].w,
                                        code[q][1].x, code[q][1].y, code[q][1].z, code[q][1].w,
                                        quad_next(code[q][0].x) & 0xFFFFu};
@@ -1958,7 +2012,7 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
                 for (int k = 0; k < 32; ++k) {
                     w[k] = table[idx[k]];
                 }
-                const uint32_t column = (j * 16u + tslot) << 4;
+                const uint32_t column = (i8 * 16u + tslot) << 4;
 #pragma unroll
                 for (uint32_t i = 0; i < kMine; ++i) {
                     const uint32_t p = group + halves * i;
@@ -1968,12 +2022,12 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
                     float x[16];
                     const float4 *src = reinterpret_cast<const float4 *>(ne_lds + p * C + column);
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const float4 t = src[g];
-                        x[4 * g] = t.x;
-                        x[4 * g + 1] = t.y;
-                        x[4 * g + 2] = t.z;
-                        x[4 * g + 3] = t.w;
+                    for (int e = 0; e < 4; ++e) {
+                        const float4 t = src[e];
+                        x[4 * e] = t.x;
+                        x[4 * e + 1] = t.y;
+                        x[4 * e + 2] = t.z;
+                        x[4 * e + 3] = t.w;
                     }
                     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -1992,7 +2046,7 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
                     if (tslot == 0) {
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            part[j][quad * 4u + r][p] = acc[r] * a.weight_scale;
+                            part[i8][quad * 4u + r][p] = acc[r] * job.weight_scale;
                         }
                     }
                 }
@@ -2006,10 +2060,10 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
         if (threadIdx.x < 16u * kMine && group + halves * (threadIdx.x >> 4) < a.batch) {
             const uint32_t r = threadIdx.x & 15u, p = group + halves * (threadIdx.x >> 4);
             float sum = 0.0f;
-            for (uint32_t j = 0; j < per_row; ++j) {
-                sum = sum + part[j][r][p];
+            for (uint32_t i = 0; i < per_row; ++i) {
+                sum = sum + part[i][r][p];
             }
-            coherent_store(reinterpret_cast<uint32_t *>(a.zsum) + static_cast<size_t>(p) * R + tr * kTile + r,
+            coherent_store(reinterpret_cast<uint32_t *>(job.zsum) + static_cast<size_t>(p) * R + tr * kTile + r,
                            __float_as_uint(sum));
         }
         __syncthreads();
@@ -2023,40 +2077,12 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
     if (last == 0u) {
         return;
     }
-    // the half's last block: every sum of its input rows is in (first touch
-    // here, ordinary loads; all the loads first)
-    {
-        float v[kMine][VR];
-#pragma unroll
-        for (uint32_t i = 0; i < kMine; ++i) {
-            const uint32_t p = group + halves * i;
-            if (p < a.batch) {
-                load_wave<VR>(a.zsum + static_cast<size_t>(p) * R + w8 * RH, lane, v[i]);
-            }
-        }
-#pragma unroll
-        for (uint32_t i = 0; i < kMine; ++i) {
-            const uint32_t p = group + halves * i;
-            if (p < a.batch) {
-                wave_hadamard<VR>(v[i], 1.0f, lane);
-                store_wave<VR>(ne_lds + p * R + w8 * RH, lane, v[i]);
-            }
-        }
-    }
-    __syncthreads();
-    for (uint32_t p = group; p < a.batch; p += halves) {
-        hadamard_cross_span<RH>(ne_lds + p * R, a.scale_rows, w8, lane);
-    }
-    __syncthreads();
-    for (uint32_t e = threadIdx.x; e < R; e += kNeFusedThreads) {
-        const float sign = static_cast<float>(sv_lds[e]);
-#pragma unroll
-        for (uint32_t i = 0; i < kMine; ++i) {
-            const uint32_t p = group + halves * i;
-            if (p < a.batch) {
-                a.out[p * R + e] = ne_lds[p * R + e] * sign;
-            }
-        }
+    // the last block of the matrix and half: the row transform
+    switch (R) {
+    case 512u: ne_fused_rows<1>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane); break;
+    case 2048u: ne_fused_rows<4>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane); break;
+    case 4096u: ne_fused_rows<8>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane); break;
+    default: ne_fused_rows<16>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane); break;
     }
     if (threadIdx.x == 0) {
         coherent_store(ticket, 0u);
@@ -2067,52 +2093,70 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
 
 // ---- launchers -------------------------------------------------------------
 
-bool launch_ne_fused(adi_hip_context *ctx, const adi_hip_ne_matrix *m, const float *inputs, uint32_t batch,
-                     float *outputs, float *zsum) {
-    if (batch == 0 || batch > kNeFusedRows || ctx->moe_sync == nullptr || !aligned_to(inputs, 16) ||
-        !aligned_to(zsum, 16)) {
+bool launch_ne_fused(adi_hip_context *ctx, const adi_hip_ne_matrix *const *m, uint32_t count,
+                     const float *inputs, uint32_t batch, float *const *outputs, float *zsum) {
+    if (batch == 0 || batch > kNeFusedRows || count == 0 || count > kNeFusedJobs || ctx->moe_sync == nullptr ||
+        !aligned_to(inputs, 16) || !aligned_to(zsum, 16)) {
         return false;
     }
-    using Kernel = void (*)(NeFused);
-    Kernel kernel = nullptr;
-    const uint32_t vc = m->columns / 512u, vr = m->rows / 512u;
-    auto pick = [&](auto vcs, auto vrs) {
-        constexpr int VC = decltype(vcs)::value, VR = decltype(vrs)::value;
-        if (vc == VC && vr == VR) {
-            kernel = k_ne_fused<VC, VR>;
+    const uint32_t columns = m[0]->columns;
+    uint32_t widest = columns, tile_rows = 0;
+    for (uint32_t j = 0; j < count; ++j) {
+        const uint32_t rows = m[j]->rows;
+        if (m[j]->columns != columns || (rows != 512u && rows != 2048u && rows != 4096u && rows != 8192u)) {
+            return false;
         }
-    };
-    using I4 = std::integral_constant<int, 4>;
-    using I8 = std::integral_constant<int, 8>;
-    using I1 = std::integral_constant<int, 1>;
-    using I16 = std::integral_constant<int, 16>;
-    pick(I4{}, I1{}); pick(I4{}, I4{}); pick(I4{}, I8{}); pick(I4{}, I16{});
-    pick(I8{}, I1{}); pick(I8{}, I4{}); pick(I8{}, I8{}); pick(I8{}, I16{});
-    if (kernel == nullptr || m->columns % 512u != 0 || m->rows % 512u != 0) {
+        widest = std::max(widest, rows);
+        tile_rows += rows / kTile;
+    }
+    using Kernel = void (*)(NeFused);
+    Kernel kernel = columns == 2048u ? k_ne_fused<4> : (columns == 4096u ? k_ne_fused<8> : nullptr);
+    if (kernel == nullptr) {
         return false;
     }
     NeFused a{};
-    a.trellis = m->trellis;
-    a.su = m->su;
-    a.sv = m->sv;
-    a.table = static_cast<const uint32_t *>(m->codebook->data);
+    a.jobs = count;
     a.x = inputs;
-    a.zsum = zsum;
-    a.out = outputs;
     a.ticket = ctx->moe_sync + kMoeSyncNeTicket;
-    a.weight_scale = m->weight_scale;
-    a.scale_columns = hadamard_scale(m->columns);
-    a.scale_rows = hadamard_scale(m->rows);
+    a.scale_columns = hadamard_scale(columns);
     a.batch = batch;
     a.halves = batch >= 2 ? 2u : 1u;
-    const uint32_t tile_rows = m->rows / kTile;
-    const uint32_t per_half = ctx->cu_count / a.halves;
-    const uint32_t blocks = a.halves * (tile_rows < per_half ? tile_rows : per_half);
-    const size_t floats = size_t(batch) * std::max(m->columns, m->rows);
-    const size_t lds = floats * sizeof(float);
+    // Each matrix gets ceil(tile rows / rounds) blocks, with the fewest rounds
+    // of tile rows per block whose blocks fit a half's share of the CUs (one
+    // matrix: min(tile rows, share) blocks).
+    const uint32_t share = std::max(ctx->cu_count / a.halves, count);
+    uint32_t rounds = ceil_div(tile_rows, share), blocks = 0;
+    for (;; ++rounds) {
+        blocks = 0;
+        for (uint32_t j = 0; j < count; ++j) {
+            blocks += ceil_div(m[j]->rows / kTile, rounds);
+        }
+        if (blocks <= share) {
+            break;
+        }
+    }
+    float *sums = zsum;
+    uint32_t first = 0;
+    for (uint32_t j = 0; j < count; ++j) {
+        NeFusedJob &job = a.job[j];
+        job.trellis = m[j]->trellis;
+        job.su = m[j]->su;
+        job.sv = m[j]->sv;
+        job.table = static_cast<const uint32_t *>(m[j]->codebook->data);
+        job.zsum = sums;
+        job.out = outputs[j];
+        job.weight_scale = m[j]->weight_scale;
+        job.scale_rows = hadamard_scale(m[j]->rows);
+        job.rows = m[j]->rows;
+        job.first_block = first;
+        job.blocks = ceil_div(m[j]->rows / kTile, rounds);
+        first += job.blocks;
+        sums += size_t(batch) * m[j]->rows;
+    }
+    const size_t lds = size_t(batch) * widest * sizeof(float);
     require(lds <= 65536 || set_lds_limit(reinterpret_cast<const void *>(kernel), lds),
             "one-launch NE projection: LDS limit");
-    launch(ctx, "ne_fused", kernel, dim3(blocks), dim3(kNeFusedThreads), lds, a);
+    launch(ctx, "ne_fused", kernel, dim3(a.halves * blocks), dim3(kNeFusedThreads), lds, a);
     return true;
 }
 
@@ -2397,6 +2441,33 @@ void validate_ne(const adi_hip_ne_matrix *m) {
     require(aligned_to(m->su, 4) && aligned_to(m->sv, 4), "Mach NE sign rows must be 4-byte aligned");
 }
 
+void ne_matmul_group(adi_hip_context *ctx, const adi_hip_ne_matrix *const *m, uint32_t count,
+                     const float *inputs, uint32_t batch, float *const *outputs) {
+    require(count > 0 && count <= kNeFusedJobs && batch > 0, "Mach NE batch shape mismatch");
+    require(inputs != nullptr, "Mach NE vector is null");
+    size_t floats = 0;
+    for (uint32_t j = 0; j < count; ++j) {
+        validate_ne(m[j]);
+        require(outputs[j] != nullptr, "Mach NE vector is null");
+        floats += size_t(batch) * m[j]->rows;
+    }
+    if (ctx->fused_moe && batch <= kNeFusedRows) {
+        auto &ws = ctx->workspace;
+        ws.used = 0;
+        ws.ensure(Workspace::round(floats * 4));
+        float *zsum = ws.take<float>(floats);
+        if (launch_ne_fused(ctx, m, count, inputs, batch, outputs, zsum)) {
+            return;
+        }
+    }
+    for (uint32_t j = 0; j < count; ++j) {
+        const int status = adi_hip_ne_matmul(ctx, m[j], inputs, batch, outputs[j]);
+        if (status != ADI_HIP_OK) {
+            fail(status, ctx->last_error());
+        }
+    }
+}
+
 }  // namespace adi_hip
 
 using namespace adi_hip;
@@ -2484,7 +2555,7 @@ int adi_hip_ne_matmul(adi_hip_context *ctx, const adi_hip_ne_matrix *m,
             ws.used = 0;
             ws.ensure(Workspace::round(size_t(batch) * m->rows * 4));
             float *zsum = ws.take<float>(size_t(batch) * m->rows);
-            if (launch_ne_fused(ctx, m, inputs, batch, outputs, zsum)) {
+            if (launch_ne_fused(ctx, &m, 1, inputs, batch, &outputs, zsum)) {
                 return;
             }
         }

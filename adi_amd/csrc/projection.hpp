@@ -231,28 +231,48 @@ bool plan_moe_decode_one(adi_hip_context *ctx, MoeDecodeOne &a);
 void launch_moe_decode_one(adi_hip_context *ctx, const MoeDecodeOne &a);
 // One-launch NE projection of up to kNeFusedRows input rows (k_ne_fused):
 // x_hat, the NE items of whole tile rows per block with the slice-order sum
-// in LDS, and the row transform by the block that takes the last ticket.
+// in LDS, and the row transform by the block that takes the last ticket. One
+// launch carries up to kNeFusedJobs matrices of the same column count over the
+// same input rows (a layer's query, key and value), each on blocks of its own.
 constexpr uint32_t kNeFusedRows = 4;
 constexpr uint32_t kNeFusedThreads = 512;
 constexpr uint32_t kNeFusedMaxItems = 32;  // NE items of one tile row at 8192 columns
-struct NeFused {
+constexpr uint32_t kNeFusedJobs = 3;
+constexpr uint32_t kNeFusedMaxRows = 8192;
+struct NeFusedJob {
     const uint16_t *trellis;
     const int8_t *su;
     const int8_t *sv;
     const uint32_t *table;  // the 4 KiB signed table
-    const float *x;         // [batch][columns]
     float *zsum;            // [batch][rows]: the slice-order sums
     float *out;             // [batch][rows]
-    uint32_t *ticket;       // two words (32 apart), zero between launches (each half's last block clears its own)
-    float weight_scale, scale_columns, scale_rows;
+    float weight_scale, scale_rows;
+    uint32_t rows;          // 512, 2048, 4096 or 8192
+    uint32_t first_block;   // the job's blocks within a half: first_block .. first_block + blocks - 1
+    uint32_t blocks;
+};
+struct NeFused {
+    NeFusedJob job[kNeFusedJobs];
+    uint32_t jobs;
+    const float *x;         // [batch][columns]
+    uint32_t *ticket;       // word 32 * (2 * job + half) per job and half, zero between launches
+                            // (the block that takes a ticket last clears it)
+    float scale_columns;
     uint32_t batch;
     uint32_t halves;        // 1, or 2 when the grid splits the input rows in two
 };
-// Runs `m` on `batch` rows in one launch; false (nothing launched) when the
-// shape is not one the kernel is built for (columns 2048 or 4096, rows 512,
-// 2048, 4096 or 8192, at most kNeFusedRows rows).
-bool launch_ne_fused(adi_hip_context *ctx, const adi_hip_ne_matrix *m, const float *inputs, uint32_t batch,
-                     float *outputs, float *zsum);
+// Runs m[0 .. count - 1] on the same `batch` input rows in one launch, output
+// j to outputs[j]; false (nothing launched) when a shape is not one the kernel
+// is built for (columns 2048 or 4096, the same for all; rows 512, 2048, 4096
+// or 8192; at most kNeFusedRows input rows and kNeFusedJobs matrices).
+// `zsum` holds batch x (the sum of the rows) floats.
+bool launch_ne_fused(adi_hip_context *ctx, const adi_hip_ne_matrix *const *m, uint32_t count,
+                     const float *inputs, uint32_t batch, float *const *outputs, float *zsum);
+// NE projections of the same input rows, outputs[j] = m[j] x inputs: one
+// launch for a few rows where launch_ne_fused takes the shapes, else one
+// adi_hip_ne_matmul each. Throws on a rejected call.
+void ne_matmul_group(adi_hip_context *ctx, const adi_hip_ne_matrix *const *m, uint32_t count,
+                     const float *inputs, uint32_t batch, float *const *outputs);
 // Whether `m` (a down projection of one row) can build its x_hat from
 // m.swiglu in the launch: one expert entry of width 512 and at most one
 // expert item per wave.

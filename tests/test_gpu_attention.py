@@ -139,3 +139,44 @@ def test_linear_attention_rejections(gpu, linear_layer):
     with pytest.raises(hip.HipError, match="linear attention decay shape mismatch"):
         hip.linear_attention_forward(gpu, hip.DeviceLinearAttention(bad, d.tensors), x, out, conv, rec)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("count", [1, 2, 4])
+def test_projection_group_equals_separate_launches(gpu, count):
+    """At hidden 2048 the query, key and value projections (Gated DeltaNet:
+    qkv and gate) of 1-4 tokens run as one NE launch; with the one-launch
+    paths switched off they run one projection at a time. Outputs, caches and
+    states are bit-identical, on two calls in a row (the tickets the first
+    call cleared are reused)."""
+    hidden = 2048
+    rng = syn.rng_for(45, count)
+    tlut = syn.ne_tlut(rng)
+    full = hip.upload_full_attention(gpu, syn.full_attention(rng, hidden, tlut), gpu.ne_codebook(tlut))
+    linear = hip.upload_linear_attention(gpu, syn.linear_attention(rng, hidden, tlut),
+                                         gpu.ne_codebook(tlut))
+    xs = [dev(syn.rms_normalized(syn.hidden_states(rng, count, hidden))) for _ in range(2)]
+    capacity = 2 * count
+
+    def run(fused):
+        gpu.set_fused_decode(fused)
+        try:
+            keys = torch.zeros((capacity, 2, 256), dtype=torch.float32, device="cuda")
+            values = torch.zeros_like(keys)
+            conv = torch.zeros(8192 * 3, dtype=torch.float32, device="cuda")
+            rec = torch.zeros(32 * 128 * 128, dtype=torch.float32, device="cuda")
+            outs = []
+            for step, x in enumerate(xs):
+                fo = torch.full((count, hidden), float("nan"), dtype=torch.float32, device="cuda")
+                lo = torch.full_like(fo, float("nan"))
+                hip.full_attention_prefill(gpu, full, step * count, count, x, fo, keys, values,
+                                           capacity)
+                hip.linear_attention_prefill(gpu, linear, count, x, lo, conv, rec)
+                outs += [fo, lo]
+            gpu.synchronize()
+            return [t.cpu().numpy() for t in outs + [keys, values, conv, rec]]
+        finally:
+            gpu.set_fused_decode(True)
+
+    one, separate = run(True), run(False)
+    for i, (a, b) in enumerate(zip(one, separate)):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), i
