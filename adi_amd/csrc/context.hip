@@ -233,7 +233,10 @@ int adi_hip_synchronize(adi_hip_context *ctx) {
 }
 
 int adi_hip_set_fused_decode(adi_hip_context *ctx, int enabled) {
-    return guarded(ctx, [&] { ctx->fused_moe = enabled != 0; });
+    return guarded(ctx, [&] {
+        ctx->fused_moe = enabled != 0 && enabled != 2;
+        ctx->gemv_up_to_16 = enabled == 2;
+    });
 }
 
 int adi_hip_set_workspace_limit(adi_hip_context *ctx, size_t bytes) {

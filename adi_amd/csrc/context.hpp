@@ -132,6 +132,9 @@ struct adi_hip_context {
     uint32_t *moe_sync = nullptr;
     bool moe_sync_pending = false;
     bool fused_moe = true;
+    // with fused_moe off: batches of up to 16 rows still take the decode-GEMV
+    // launches (the few-row one-launch block's arithmetic) instead of the MFMA
+    bool gemv_up_to_16 = false;
     bool profiling = false;
     // planning pass of a graph capture: every host step of a call runs
     // (checks, workspace and RoPE table growth) but nothing is launched
@@ -148,13 +151,16 @@ struct adi_hip_context {
 
 namespace adi_hip {
 
-// adi_hip_context::moe_sync: 64 lines of kMoeSyncLine words (counters and
-// flags, the logits, the error word and the combine's nine rows) and the
-// index of its error word.
+// adi_hip_context::moe_sync: 96 lines of kMoeSyncLine words. Lines 0-45
+// hold the one-row MoE block's counters and flags, its logits, the NE
+// projection's ticket (43) and the error word (45); lines 46-63 the one-row
+// block's nine combine rows (data it leaves behind); lines 64-95 the few-row
+// block's counters.
 constexpr uint32_t kMoeSyncLine = 1024;
-constexpr uint32_t kMoeSyncWords = 64 * kMoeSyncLine;
+constexpr uint32_t kMoeSyncWords = 96 * kMoeSyncLine;
 constexpr uint32_t kMoeSyncError = 45 * kMoeSyncLine;
 constexpr uint32_t kMoeSyncNeTicket = 43 * kMoeSyncLine;  // the one-launch NE projection's ticket
+constexpr uint32_t kMoeSyncFew = 64 * kMoeSyncLine;       // the few-row MoE block's counters
 
 // Selects the context's device for the duration of a call.
 class DeviceScope {

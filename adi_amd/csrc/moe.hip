@@ -436,7 +436,7 @@ void validate_layer(const adi_hip_moe_layer *L) {
 // holds its own copy until the process ends; host code uses the address
 // static_scratch_address() returns for its device, never this name. Nothing
 // in it needs to start at zero: every kernel writes what it later reads.
-constexpr size_t kStaticScratchBytes = size_t(8) << 20;
+constexpr size_t kStaticScratchBytes = size_t(12) << 20;
 constexpr uint32_t kStaticBatch = 16;
 __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 
@@ -454,9 +454,15 @@ void moe_forward_body(adi_hip_context *ctx, const adi_hip_moe_layer *L, const fl
         const size_t B = batch, P = B * 8;
         const uint32_t max_active = static_cast<uint32_t>(P < E ? P : E);
         const bool wave_path = wave_width(H) && wave_width(I);
+        // 2-12 rows of the one-launch block's geometry: the whole block in one
+        // persistent launch on the decode-GEMV arithmetic
+        const bool few = ctx->fused_moe && wave_path && batch >= 2 && batch <= kFewMaxRows &&
+                         H == kFusedHidden && I == kFusedSwigluWidth && E <= kFusedMaxExperts &&
+                         L->shared_up.codebook->data == L->shared_gate.codebook->data;
         // prefill microbatches: MFMA grouped GEMMs over the expert-sorted
         // positions; decode batches: the persistent decode-GEMV
-        const bool mfma = wave_path && batch >= kMfmaBatch && expert_mfma_supports(I, H) &&
+        const bool gemv_batch = few || (ctx->gemv_up_to_16 && batch <= 16u);
+        const bool mfma = !gemv_batch && wave_path && batch >= kMfmaBatch && expert_mfma_supports(I, H) &&
                           expert_mfma_supports(H, I);
         const uint32_t sg = mfma ? 2u : expert_splits(H);
         const uint32_t sd = mfma ? 2u : expert_splits(I);
@@ -473,7 +479,8 @@ void moe_forward_body(adi_hip_context *ctx, const adi_hip_moe_layer *L, const fl
             Workspace::round(P * H * 4) * 2 + Workspace::round(sg * P * I * 4) * 2 +
             Workspace::round(P * I * 4) + Workspace::round(sd * P * H * 4) +
             Workspace::round(B * H * 4) * 2 + Workspace::round(ssg * B * I * 4) * 2 +
-            Workspace::round(B * I * 4) + Workspace::round(ssd * B * H * 4);
+            Workspace::round(B * I * 4) + Workspace::round(ssd * B * H * 4) +
+            (few ? Workspace::round(B * (E + 1) * 4) + Workspace::round(B * 9 * H * 4) : 0);
         if (arena != nullptr) {
             require(bytes <= arena->capacity,
                     "MoE batch needs more scratch than the fixed no-allocation buffer holds");
@@ -511,6 +518,8 @@ void moe_forward_body(adi_hip_context *ctx, const adi_hip_moe_layer *L, const fl
         float *sz_up = ws.take<float>(ssg * B * I);
         float *sxh_down = ws.take<float>(B * I);
         float *sz_down = ws.take<float>(ssd * B * H);
+        float *few_logits = few ? ws.take<float>(B * (E + 1)) : nullptr;
+        float *few_parts = few ? ws.take<float>(B * 9 * H) : nullptr;
 
         // where x_hat goes: fp32, or f16 pairs (planes 2: expert, 1: NE)
         auto xhat = [&](float *buffer, size_t vectors, size_t n, uint32_t planes) {
@@ -614,6 +623,41 @@ void moe_forward_body(adi_hip_context *ctx, const adi_hip_moe_layer *L, const fl
             f.experts = E;
             if (ctx->fused_moe && plan_moe_decode_one(ctx, f)) {
                 launch_moe_decode_one(ctx, f);
+                ctx->moe_sync_pending = true;
+                return;
+            }
+        }
+
+        // 2-12 rows: the whole block in one persistent launch when it fits
+        if (few) {
+            MoeDecodeFew f{};
+            f.gu = gate_up_plan();
+            f.gu.ne[1] = ne_job(L->shared_up, sxh_up, sz_up);
+            f.gu.ne_count = 2;
+            f.dn = down_plan();
+            f.dn.swiglu = swiglu_plan();
+            f.router = L->router.values;
+            f.shared_gate_row = L->shared_expert_gate.values;
+            f.logit_bias = logit_bias;
+            f.x = inputs;
+            f.su_gate = L->gate.su_f16;
+            f.su_up = L->up.su_f16;
+            f.shared_su_gate = L->shared_gate.su;
+            f.shared_su_up = L->shared_up.su;
+            f.sv_down = L->down.sv_f16;
+            f.shared_sv_down = L->shared_down.sv;
+            f.scale_hidden = hadamard_scale(H);
+            f.out = outputs;
+            f.route_expert_out = route_expert_out;
+            f.route_weight_out = route_weight_out;
+            f.logits = few_logits;
+            f.parts = few_parts;
+            f.sync = ctx->moe_sync + kMoeSyncFew;
+            f.error = ctx->moe_sync + kMoeSyncError;
+            f.experts = E;
+            f.batch = batch;
+            if (plan_moe_decode_few(ctx, f)) {
+                launch_moe_decode_few(ctx, f);
                 ctx->moe_sync_pending = true;
                 return;
             }

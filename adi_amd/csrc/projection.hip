@@ -619,7 +619,7 @@ __device__ __forceinline__ void load_x16(const float *x_hat, uint32_t columns, u
 
 template <bool COHERENT = false>
 __device__ __forceinline__ void ne_prefetch(const MoeGemv &m, uint32_t k, uint32_t lane,
-                                            NeStage &st, const float *x_lds = nullptr) {
+                                            NeStage &st, const float *x_lds = nullptr, uint32_t first = 0) {
     const uint2 it = ne_item_of(m, k);
     const NeGemv &a = m.ne[it.x];
     uint32_t tile, column;
@@ -638,15 +638,44 @@ __device__ __forceinline__ void ne_prefetch(const MoeGemv &m, uint32_t k, uint32
     if (x_lds != nullptr) {
         load_x16(x_lds, a.columns, 0, column, valid && a.batch > 0, st.x);
     } else {
-        load_x16<COHERENT>(a.x_hat, a.columns, 0, column, valid && a.batch > 0, st.x);
+        load_x16<COHERENT>(a.x_hat, a.columns, first, column, valid && first < a.batch, st.x);
     }
+}
+
+// ne_prefetch in two parts: the codes (no dependence on the launch's data),
+// then the x_hat of position `first` once it is in.
+__device__ __forceinline__ void ne_prefetch_codes(const MoeGemv &m, uint32_t k, uint32_t lane, NeStage &st) {
+    const uint2 it = ne_item_of(m, k);
+    const NeGemv &a = m.ne[it.x];
+    uint32_t tile, column;
+    bool valid;
+    ne_tile(a, it.y, lane, tile, valid, column);
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
+    if (valid) {
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(a.trellis) + static_cast<size_t>(tile) * 8u + (lane & 3u) * 2u;
+        lo = __builtin_nontemporal_load(src);
+        hi = __builtin_nontemporal_load(src + 1);
+    }
+    st.d[0] = lo.x; st.d[1] = lo.y; st.d[2] = lo.z; st.d[3] = lo.w;
+    st.d[4] = hi.x; st.d[5] = hi.y; st.d[6] = hi.z; st.d[7] = hi.w;
+}
+__device__ __forceinline__ void ne_prefetch_x(const MoeGemv &m, uint32_t k, uint32_t lane, NeStage &st,
+                                              uint32_t first) {
+    const uint2 it = ne_item_of(m, k);
+    const NeGemv &a = m.ne[it.x];
+    uint32_t tile, column;
+    bool valid;
+    ne_tile(a, it.y, lane, tile, valid, column);
+    load_x16(a.x_hat, a.columns, first, column, valid && first < a.batch, st.x);
 }
 
 // Row sums over all 16 columns of each tile with the signed table in LDS,
 // scaled by Wscale once after the tile sums.
 template <bool COHERENT = false>
 __device__ __forceinline__ void ne_compute(const MoeGemv &m, uint32_t k, const uint32_t *table,
-                                           uint32_t lane, NeStage &st) {
+                                           uint32_t lane, NeStage &st, uint32_t first = 0,
+                                           uint32_t end = 0xFFFFFFFFu) {
     const uint2 it = ne_item_of(m, k);
     const NeGemv &a = m.ne[it.x];
     const uint32_t quad = lane & 3u, tslot = lane >> 2;
@@ -663,9 +692,10 @@ __device__ __forceinline__ void ne_compute(const MoeGemv &m, uint32_t k, const u
     const uint32_t split = (tile & (tile_columns - 1u)) >> 4;
     const uint32_t tr = tile >> a.tc_shift;
     const bool writer = (tslot % span) == 0 && valid;
-    float (&x)[16] = st.x;  // position 0's, then reloaded per position
-    for (uint32_t position = 0; position < a.batch; ++position) {
-        if (position != 0) {
+    float (&x)[16] = st.x;  // position first's, then reloaded per position
+    const uint32_t stop = end < a.batch ? end : a.batch;
+    for (uint32_t position = first; position < stop; ++position) {
+        if (position != first) {
             load_x16(a.x_hat, a.columns, position, column, valid, x);
         }
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -694,7 +724,7 @@ __device__ __forceinline__ void ne_compute(const MoeGemv &m, uint32_t k, const u
 // One row's SwiGLU into x_hat (width 512, the wave layout), as the MoE's
 // swiglu launch computes it (src/executor.cpp:300-312): the routed row of
 // grouped position `row` with expert `expert`'s f16 scales, or the shared
-// expert's with its signs. Split in two so that the scale and first four
+// expert's row `row` with its signs. Split in two so that the scale and first four
 // slice loads go out before the codebook plane's (loads return in order).
 struct SwigluInputs {
     float sa[kFusedSwigluWidth / 64], sb[kFusedSwigluWidth / 64], sc[kFusedSwigluWidth / 64];
@@ -722,8 +752,8 @@ __device__ __forceinline__ void swiglu_issue_slices(const GemvSwiglu &f, bool sh
                                                     uint32_t lane, SwigluInputs &in) {
     constexpr int VPL = kFusedSwigluWidth / 64;
     constexpr uint32_t n = kFusedSwigluWidth;
-    const float *zg = shared ? f.shared_z_gate : f.z_gate + static_cast<size_t>(row) * n;
-    const float *zu = shared ? f.shared_z_up : f.z_up + static_cast<size_t>(row) * n;
+    const float *zg = (shared ? f.shared_z_gate : f.z_gate) + static_cast<size_t>(row) * n;
+    const float *zu = (shared ? f.shared_z_up : f.z_up) + static_cast<size_t>(row) * n;
     const size_t stride = shared ? f.shared_split_stride : f.split_stride;
     const uint32_t splits = shared ? f.shared_splits : f.splits;
 #pragma unroll
@@ -748,8 +778,8 @@ __device__ __forceinline__ void swiglu_finish(const GemvSwiglu &f, bool shared, 
 #pragma clang fp contract(off)
     constexpr int VPL = kFusedSwigluWidth / 64;
     constexpr uint32_t n = kFusedSwigluWidth;
-    const float *zg = shared ? f.shared_z_gate : f.z_gate + static_cast<size_t>(row) * n;
-    const float *zu = shared ? f.shared_z_up : f.z_up + static_cast<size_t>(row) * n;
+    const float *zg = (shared ? f.shared_z_gate : f.z_gate) + static_cast<size_t>(row) * n;
+    const float *zu = (shared ? f.shared_z_up : f.z_up) + static_cast<size_t>(row) * n;
     const size_t stride = shared ? f.shared_split_stride : f.split_stride;
     const uint32_t splits = shared ? f.shared_splits : f.splits;
     float gv[VPL], uv[VPL];
@@ -1022,12 +1052,10 @@ __device__ __forceinline__ uint32_t *sync_line(uint32_t *sync, uint32_t line) {
     return sync + static_cast<size_t>(line) * kMoeSyncLine;
 }
 
-constexpr uint32_t kFusedHidden = 2048;
 constexpr uint32_t kFusedThreads = kGemvThreads + kWave;  // eight GEMV waves and a helper
 constexpr uint32_t kFusedSlots = 8;
 constexpr uint32_t kSpinLimit = 1u << 20;  // about a second of polling
 constexpr size_t kFusedRegion = 16384;     // LDS after the plane: staging and x_hat rows
-constexpr uint32_t kFusedMaxExperts = 256;  // routed experts the one-launch block handles
 
 // Polls (the whole wave) until *word is nonzero and returns it; bounded (0
 // after a timeout, which sets `bit` of the error word).
@@ -1859,6 +1887,718 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
 
 
 
+// ---- the MoE block of a few rows in one launch ---------------------------------
+//
+// B = 2 .. kFewMaxRows rows. Phases (items, slices and every sum as in the
+// separate launches, so results are bit-identical to theirs):
+//   P0  every block: codebook plane and NE table into LDS; router rows b and
+//       2 blocks - 1 - b (row `experts` is the shared gate) for every row of
+//       the batch, in the CPU's ISA order, counted in per XCD. Blocks
+//       0 .. 2B - 1 build the shared expert's gate and up x_hat of one row.
+//       The helper wave then runs two shared gate/up NE items (all B rows).
+//   P1  the GEMV waves route every row (top_experts, then the stable
+//       counting sort by expert: slot s is the s-th smallest chosen expert,
+//       its positions in route order) once all logits are in, and build
+//       their share of the gate and up x_hat rows of their XCD's slots (slot
+//       s runs on XCD s % 8, whose 32 blocks take the rows in turn).
+//   P2  each GEMV wave runs one gate/up item of every slot of its XCD, as
+//       soon as that slot's x_hat rows are in (the codes are in flight
+//       meanwhile); Z slices stay on the XCD.
+//   P3  the helper builds the SwiGLU x_hat rows of its share of the XCD's
+//       routes once their slot's gate/up items are in; the helpers of blocks
+//       0 .. B - 1 build the shared expert's, and every helper then runs one
+//       shared down NE item.
+//   P4  each GEMV wave runs one down item of every slot of its XCD; the wave
+//       that completes a slot's down items builds its combine rows (one wave
+//       each, the combine launch's arithmetic). The helpers of blocks
+//       0 .. B - 1 build the shared combine rows once every shared down item
+//       is in. Whoever adds a row's ninth combine row adds the nine in route
+//       order, then the shared expert's, into the output.
+// The last block through clears the counters for the next call. Every block
+// is resident (one per CU) and every wait is bounded: a wait that runs out
+// sets a bit of the error word.
+namespace few_sync {
+constexpr uint32_t kStride = 32;  // words between counters: a 128-byte line each
+constexpr uint32_t kLogits = 0,        // 8 group counters (block b adds to b % 8): blocks with their logits out
+                   kSharedX = 8,       // 8: shared gate/up x_hat rows written
+                   kSharedGu = 16,     // 8: shared gate/up NE items done
+                   kSharedDownX = 24,  // 8: shared SwiGLU x_hat rows written
+                   kSharedDown = 32,   // 8 and a top counter (40): shared down NE items done
+                   kSharedDone = 41,   // 8 replicas: every shared down item is in
+                   kExit = 49,         // 8 and a top counter (57): blocks that are through
+                   kXReady = 64,       // per (slot, entry): x_hat row chunks written (8 per row)
+                   kGuDone = kXReady + 2 * kFewMaxRoutes,  // per slot: gate/up wave items done
+                   kDownX = kGuDone + kFewMaxRoutes,       // per slot: SwiGLU x_hat rows written
+                   kDnDone = kDownX + kFewMaxRoutes,       // per slot: down wave items done
+                   kPosition = kDnDone + kFewMaxRoutes,    // per row: combine rows in
+                   kCounters = kPosition + kFewMaxRows;
+}  // namespace few_sync
+static_assert(kMoeSyncFew >= (moe_sync::kParts + 18u) * kMoeSyncLine &&
+                  kMoeSyncFew + few_sync::kCounters * few_sync::kStride <= kMoeSyncWords,
+              "the few-row counters sit after the one-row block's lines, inside the sync buffer");
+
+__device__ __forceinline__ uint32_t *few_word(uint32_t *sync, uint32_t i) {
+    return sync + static_cast<size_t>(i) * few_sync::kStride;
+}
+
+// Polls (the whole wave) until the eight group counters from `first` add up
+// to at least `total`; bounded (a timeout sets `bit` of the error word).
+__device__ __forceinline__ void few_wait_total(uint32_t *sync, uint32_t first, uint32_t total, uint32_t lane,
+                                               uint32_t *error, uint32_t bit) {
+    for (uint32_t spins = 0;; ++spins) {
+        const uint32_t v = lane < 8u ? coherent_load(few_word(sync, first + lane)) : 0u;
+        uint32_t sum = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            sum += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), j));
+        }
+        if (sum >= total) {
+            return;
+        }
+        if (spins >= kSpinLimit) {
+            if (lane == 0) {
+                __hip_atomic_fetch_or(error, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Two-level ticket over the grid from group counters `first` and top counter
+// `top`: true in the one caller that completes it.
+__device__ __forceinline__ bool few_ticket(uint32_t *sync, uint32_t first, uint32_t top, uint32_t b,
+                                           uint32_t blocks) {
+    const uint32_t group = b & 7u;
+    const uint32_t members = (blocks - group + 7u) >> 3;
+    if (coherent_add(few_word(sync, first + group), 1u) + 1u != members) {
+        return false;
+    }
+    const uint32_t groups = blocks < 8u ? blocks : 8u;
+    return coherent_add(few_word(sync, top), 1u) + 1u == groups;
+}
+
+// The x_hat loads of expert_prefetch for a stage whose words were loaded
+// without them: the item's first position, from the entry's x_hat rows.
+__device__ __forceinline__ void expert_load_x(const MoeGemv &m, uint32_t i, uint32_t half, uint32_t lane,
+                                              ExpertStage &st) {
+    const ExpertItem it = expert_item_of(m, i);
+    const ExpertGemv &a = m.expert[it.which];
+    uint32_t column[4], tile[4];
+    bool valid[4];
+    expert_tiles(a, it.item, half, lane, column, valid, tile);
+    const bool live = st.info.z > st.info.y;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        valid[g] = valid[g] && live;
+    }
+    load_x_pair(a.x_hat, a.columns, st.info.y, column, 1u << a.group_shift, valid, st.x);
+}
+
+// 256 consecutive floats (a wave's chunk, 4 a lane) written through to memory.
+__device__ __forceinline__ void store_chunk_through(float *dst, uint32_t lane, float4 v) {
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(dst, 0, 1024, 0x00020000);
+    const u32x4_t q = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
+    __builtin_amdgcn_raw_buffer_store_b128(q, rs, lane * 16u, 0, 16 /* sc1 */);
+}
+
+// Row p of the output: its eight routed combine rows in route order, then the
+// shared expert's (the combine launch's sum), by one wave.
+__device__ __forceinline__ void few_finish_row(const MoeDecodeFew &a, uint32_t p, uint32_t lane) {
+#pragma clang fp contract(off)
+    constexpr uint32_t n4 = kFusedHidden / 4u;
+    const float4 *rows = reinterpret_cast<const float4 *>(a.parts + static_cast<size_t>(p) * 9u * kFusedHidden);
+    float4 *row_out = reinterpret_cast<float4 *>(a.out + static_cast<size_t>(p) * kFusedHidden);
+    for (uint32_t c = lane; c < n4; c += 64u) {
+        float4 v[9];
+#pragma unroll
+        for (uint32_t r = 0; r < 9; ++r) {
+            v[r] = rows[r * n4 + c];
+        }
+        float4 acc = v[0];
+#pragma unroll
+        for (uint32_t r = 1; r < 9; ++r) {
+            acc.x = acc.x + v[r].x;
+            acc.y = acc.y + v[r].y;
+            acc.z = acc.z + v[r].z;
+            acc.w = acc.w + v[r].w;
+        }
+        row_out[c] = acc;
+    }
+}
+
+// Counts combine row (p, *) in (the wave's stores complete first); the wave
+// that adds the ninth writes output row p.
+__device__ __forceinline__ void few_row_in(const MoeDecodeFew &a, uint32_t p, uint32_t lane) {
+    wait_stores();
+    uint32_t old = 0;
+    if (lane == 0) {
+        old = coherent_add(few_word(a.sync, few_sync::kPosition + p), 1u);
+    }
+    if (__builtin_amdgcn_readfirstlane(old) == 8u) {
+        few_finish_row(a, p, lane);
+    }
+}
+
+template <int LANES>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_decode_few(MoeDecodeFew a) {
+#pragma clang fp contract(off)
+    extern __shared__ uint4 lds_dynamic[];  // the codebook plane (first the staged rows), then kFusedRegion bytes
+    __shared__ uint32_t ne_table[1024];
+    __shared__ uint4 slots[kFewMaxRoutes];          // {expert, first, end, 0} by slot
+    __shared__ uint32_t route_e[kFewMaxRoutes];     // route r = 8 p + k: expert
+    __shared__ float route_w[kFewMaxRoutes];        // and weight
+    __shared__ uint32_t grouped_route[kFewMaxRoutes];  // the route at each grouped position
+    __shared__ uint32_t hist[kFusedMaxExperts];     // routes per expert, then its first grouped position
+    __shared__ uint32_t posmask[kFusedMaxExperts];  // rows choosing each expert (bit p)
+    __shared__ uint32_t counts[40];                 // LDS arrival counters
+    __shared__ uint8_t xcd_slot[8][kFewMaxRoutes / 8];  // the slots each XCD runs, in order
+    __shared__ uint32_t slot_count, last;
+    constexpr uint32_t H = kFusedHidden;
+    constexpr int VPLI = kFusedSwigluWidth / 64;
+    // counts: 0 routing done, 1 slot table, 2 wave barrier,
+    // 3 .. 18 gate/up items per XCD slot, 19 .. 34 down items per XCD slot
+    constexpr uint32_t kRouted = 0, kTable = 1, kBar = 2, kGuCount = 3, kDnCount = 19;
+    uint4 *plane_lds = lds_dynamic;
+    float *x_lds = reinterpret_cast<float *>(lds_dynamic);  // P0: the batch's rows, before the plane
+    float *region = reinterpret_cast<float *>(lds_dynamic + kPlaneBytes / 16);
+    const uint32_t b = blockIdx.x, blocks = gridDim.x;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63u;
+    // block b is the k-th of XCD b % 8 (blocks are dealt round robin);
+    // plane half k % 2, and the m-th of its (XCD, half) pair
+    const uint32_t xcd = b & 7u, k = b >> 3, half = k & 1u, m_block = k >> 1;
+    const uint32_t xcd_blocks = blocks >> 3;
+    const uint32_t B = a.batch, routes_total = 8u * B, E = a.experts, row_words = E + 1u;
+    uint32_t *sync = a.sync;
+    uint32_t *error = a.error;
+    for (uint32_t i = threadIdx.x; i < kFusedMaxExperts; i += kGemvThreads) {
+        hist[i] = 0u;
+        posmask[i] = 0u;
+    }
+    if (threadIdx.x < 40) {
+        counts[threadIdx.x] = 0u;
+    }
+    // The shared expert's NE items in units of (item, group of rows), at most
+    // one a wave: unit u runs on wave u % 8 of block blocks - 1 - u / 8 (from
+    // the last block down, away from the blocks that build the routed SwiGLU
+    // and combine rows). The gate/up units take up to four groups of rows,
+    // the down units up to eight; their codes are loaded at the start.
+    const uint32_t from_top = (blocks - 1u - b) * kGemvWaves + wave;
+    const uint32_t gu_groups = B < 4u ? B : 4u, gu_per = (B + gu_groups - 1u) / gu_groups;
+    const uint32_t dn_groups = B < 8u ? (B < 4u ? B : 4u) : 8u, dn_per = (B + dn_groups - 1u) / dn_groups;
+    const bool gu_unit = from_top < a.gu.ne_items * gu_groups;
+    const bool dn_unit = from_top < a.dn.ne_items * dn_groups;
+    const uint32_t gu_k = from_top % a.gu.ne_items, gu_first = (from_top / a.gu.ne_items) * gu_per;
+    const uint32_t dn_k = from_top % a.dn.ne_items, dn_first = (from_top / a.dn.ne_items) * dn_per;
+    NeStage gu_st;
+    if (gu_unit) {
+        ne_prefetch_codes(a.gu, gu_k, lane, gu_st);
+    }
+    uint32_t barriers = 0;
+    auto block_barrier = [&]() {
+        __builtin_amdgcn_s_waitcnt(kWaitLds);
+        if (lane == 0) {
+            __hip_atomic_fetch_add(&counts[kBar], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        wait_lds_value(&counts[kBar], kGemvWaves * ++barriers, error);
+    };
+
+    // ---- P0: router rows b and 2 blocks - 1 - b (row `experts` is the
+    // shared gate) of every row of the batch, x staged in LDS ----
+    const uint32_t r0 = b, r1 = 2u * blocks - 1u - b;
+    const uint32_t nrows = (r0 < row_words ? 1u : 0u) + (r1 < row_words ? 1u : 0u);
+    uint16_t *wl = reinterpret_cast<uint16_t *>(region);  // the block's router rows
+    {
+        auto row = [&](uint32_t r) {
+            return reinterpret_cast<const uint4 *>(r < E ? a.router + static_cast<size_t>(r) * H : a.shared_gate_row);
+        };
+        // row 0 of the LDS copy is the block's first valid row, row 1 its second
+        const uint32_t first = r0 < row_words ? r0 : r1;
+        const uint32_t u = threadIdx.x;  // 512 uint4 = the two rows
+        uint4 w = make_uint4(0u, 0u, 0u, 0u);
+        if (u < 256u && nrows > 0) {
+            w = row(first)[u];
+        } else if (u >= 256u && nrows > 1) {
+            w = row(r1)[u - 256u];
+        }
+        reinterpret_cast<uint4 *>(wl)[u] = w;
+        // the rows in rounds of eight loads (a row past the batch reloads the last)
+#pragma unroll
+        for (uint32_t p0 = 0; p0 < kFewMaxRows; p0 += 8u) {
+            if (p0 < B) {
+                float4 xv[8];
+#pragma unroll
+                for (uint32_t j = 0; j < 8u; ++j) {
+                    const uint32_t p = p0 + j < B ? p0 + j : B - 1u;
+                    xv[j] = reinterpret_cast<const float4 *>(a.x + static_cast<size_t>(p) * H)[u];
+                }
+#pragma unroll
+                for (uint32_t j = 0; j < 8u; ++j) {
+                    if (p0 + j < B) {
+                        reinterpret_cast<float4 *>(x_lds + static_cast<size_t>(p0 + j) * H)[u] = xv[j];
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+    {
+        // chain c = (row sel, input row p) = (c / B, c % B), 64 / LANES chains a wave
+        constexpr uint32_t kChains = 64u / LANES;
+        const uint32_t chains = nrows * B;
+        if (wave * kChains < chains) {
+            const uint32_t c = wave * kChains + lane / LANES;
+            const uint32_t cc = c < chains ? c : chains - 1u;
+            const float acc = router_chain<LANES>(wl + (cc / B) * H, x_lds + static_cast<size_t>(cc % B) * H, H,
+                                                  lane % LANES);
+#pragma unroll
+            for (uint32_t g = 0; g < kChains; ++g) {
+                const float s = router_lane_sum<LANES>(acc, g);
+                const uint32_t cg = wave * kChains + g;
+                if (lane == 0 && cg < chains) {
+                    const uint32_t sel = cg / B, p = cg % B;
+                    const uint32_t r = sel == 0 && r0 < row_words ? r0 : r1;
+                    coherent_store(a.logits + static_cast<size_t>(p) * row_words + r, s);
+                }
+            }
+        }
+    }
+    wait_stores();
+    __syncthreads();  // every chain's logits out; the staged rows are free
+    if (threadIdx.x == 0) {
+        coherent_add(few_word(sync, few_sync::kLogits + xcd), 1u);
+    }
+    // the codebook plane and the NE table
+    fill_plane_share(static_cast<const uint4 *>(a.gu.expert_book) + half * (kPlaneBytes / 16), plane_lds);
+    {
+        const uint32_t *src = static_cast<const uint32_t *>(a.gu.ne_book);
+        for (uint32_t i = threadIdx.x; i < 1024u; i += kGemvThreads) {
+            ne_table[i] = src[i];
+        }
+    }
+    // the shared expert's gate (blocks 0 .. B - 1) and up (B .. 2B - 1) x_hat of one row
+    if (b < 2u * B) {
+        const uint32_t which = b / B, p = b % B;
+        float *xs = region;
+        const int8_t *su = which == 0 ? a.shared_su_gate : a.shared_su_up;
+        float sign[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sign[i] = static_cast<float>(su[256u * wave + 64u * i + lane]);
+        }
+        hadamard_chunk(a.x + static_cast<size_t>(p) * H, sign, wave, lane, xs);
+        block_barrier();
+        hadamard_cross(xs, a.scale_hidden, wave, lane);
+        block_barrier();
+        float *dst = const_cast<float *>(a.gu.ne[which].x_hat) + static_cast<size_t>(p) * H + 256u * wave;
+        store_chunk_through(dst, lane, reinterpret_cast<const float4 *>(xs + 256u * wave)[lane]);
+        wait_stores();
+        block_barrier();
+        if (threadIdx.x == 0) {
+            coherent_add(few_word(sync, few_sync::kSharedX + xcd), 1u);
+        }
+    }
+    __syncthreads();  // the plane and the table are complete
+    const uint2 *plane = reinterpret_cast<const uint2 *>(plane_lds);
+
+    // ---- P1: routing (top_experts of row p on wave p % 8, then the stable
+    // counting sort by expert: slot s is the s-th smallest chosen expert, its
+    // positions in route order) ----
+    if (wave < B) {
+        few_wait_total(sync, few_sync::kLogits, blocks, lane, error, 1u);
+        for (uint32_t p = wave; p < B; p += kGemvWaves) {
+            top8_wave<4>(a.logits + static_cast<size_t>(p) * row_words, a.logit_bias, E, lane, route_e + 8u * p,
+                         route_w + 8u * p);
+        }
+    }
+    arrive_and_wait(&counts[kRouted], kGemvWaves, error);
+    if (wave == 0) {
+        // the counting sort: routes per expert and the rows choosing it,
+        // then each expert's first grouped position and slot
+        for (uint32_t r = lane; r < routes_total; r += 64u) {
+            const uint32_t e = route_e[r];
+            atomicAdd(&hist[e], 1u);
+            atomicOr(&posmask[e], 1u << (r >> 3));
+        }
+        __builtin_amdgcn_s_waitcnt(kWaitLds);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        uint32_t cnt[4], run = 0, nz = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            const uint32_t e = 4u * lane + j;
+            cnt[j] = e < E ? hist[e] : 0u;
+            run += cnt[j];
+            nz += cnt[j] != 0u ? 1u : 0u;
+        }
+        // exclusive prefix sums over the lanes (lane order = expert order)
+        uint32_t run_ex = run, nz_ex = nz;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t a1 = static_cast<uint32_t>(__shfl_up(static_cast<int>(run_ex), d, 64));
+            const uint32_t a2 = static_cast<uint32_t>(__shfl_up(static_cast<int>(nz_ex), d, 64));
+            if (lane >= static_cast<uint32_t>(d)) {
+                run_ex += a1;
+                nz_ex += a2;
+            }
+        }
+        run_ex -= run;
+        nz_ex -= nz;
+        if (lane == 63u) {
+            slot_count = nz_ex + nz;
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            const uint32_t e = 4u * lane + j;
+            if (e < E) {
+                hist[e] = run_ex;
+                if (cnt[j] != 0u) {
+                    slots[nz_ex] = make_uint4(e, run_ex, run_ex + cnt[j], 0u);
+                    ++nz_ex;
+                }
+                run_ex += cnt[j];
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(kWaitLds);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        {
+            // slots to XCDs: by rows held, most first (ties by slot), dealt in
+            // snake order 0..7, 7..0, ... so the XCDs' rows stay even
+            const uint32_t total = __builtin_amdgcn_readfirstlane(slot_count);
+            uint32_t size[2], rank[2] = {0u, 0u};
+#pragma unroll
+            for (uint32_t h = 0; h < 2u; ++h) {
+                const uint32_t sl = 64u * h + lane;
+                size[h] = sl < total ? slots[sl].z - slots[sl].y : 0u;
+            }
+            const uint64_t below = (uint64_t(1) << lane) - 1u;
+            uint32_t base = 0;
+            for (uint32_t c = kFewMaxRows; c >= 1u; --c) {
+                const uint64_t m0 = __ballot(size[0] == c), m1 = __ballot(size[1] == c);
+                const uint32_t n0 = static_cast<uint32_t>(__builtin_popcountll(m0));
+                if (size[0] == c) {
+                    rank[0] = base + static_cast<uint32_t>(__builtin_popcountll(m0 & below));
+                }
+                if (size[1] == c) {
+                    rank[1] = base + n0 + static_cast<uint32_t>(__builtin_popcountll(m1 & below));
+                }
+                base += n0 + static_cast<uint32_t>(__builtin_popcountll(m1));
+            }
+#pragma unroll
+            for (uint32_t h = 0; h < 2u; ++h) {
+                const uint32_t sl = 64u * h + lane;
+                if (sl < total) {
+                    const uint32_t round = rank[h] >> 3, at = rank[h] & 7u;
+                    xcd_slot[(round & 1u) != 0u ? 7u - at : at][round] = static_cast<uint8_t>(sl);
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(kWaitLds);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        for (uint32_t r = lane; r < routes_total; r += 64u) {
+            const uint32_t e = route_e[r], p = r >> 3;
+            const uint32_t g = hist[e] + __builtin_popcount(posmask[e] & ((1u << p) - 1u));
+            grouped_route[g] = r;
+            if (b == 0 && a.route_expert_out != nullptr) {
+                a.route_expert_out[r] = e;
+            }
+            if (b == 0 && a.route_weight_out != nullptr) {
+                a.route_weight_out[r] = route_w[r];
+            }
+        }
+        set_flag(&counts[kTable]);
+    }
+    wait_flag(&counts[kTable], error);
+    const uint32_t slot_total = slot_count;
+    // the XCD's slots: one per full round of the deal, and one in the last
+    // round when the snake reaches it
+    const uint32_t rounds = slot_total >> 3, rest = slot_total & 7u;
+    const uint32_t at_last = (rounds & 1u) != 0u ? 7u - xcd : xcd;
+    const uint32_t n_slots = rounds + (at_last < rest ? 1u : 0u);
+    auto slot_of = [&](uint32_t t) { return static_cast<uint32_t>(xcd_slot[xcd][t]); };
+    // the XCD's routes (grouped positions of its slots, slot by slot) are
+    // shared out: route q to block q % 32 of the XCD, wave (q / 32) % 8
+    // (SwiGLU rows), and block q % 32 (combine rows)
+
+    if (gu_unit) {
+        few_wait_total(sync, few_sync::kSharedX, 2u * B, lane, error, 2u);
+        ne_prefetch_x(a.gu, gu_k, lane, gu_st, gu_first);
+    }
+    // ---- P1: the block's share of its XCD's gate and up x_hat rows ----
+    {
+        float *xs = region;
+        uint32_t j = 0;
+        for (uint32_t t = 0; t < n_slots; ++t) {
+            const uint32_t s = slot_of(t);
+            const uint4 info = slots[s];
+            for (uint32_t g = info.y; g < info.z; ++g) {
+                for (uint32_t which = 0; which < 2u; ++which, ++j) {
+                    if (j % xcd_blocks != k) {
+                        continue;
+                    }
+                    const uint32_t p = grouped_route[g] >> 3;
+                    const uint16_t *su = (which == 0 ? a.su_gate : a.su_up) + static_cast<size_t>(info.x) * H +
+                                         256u * wave;
+                    float m4[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        m4[i] = half_bits_to_float(su[64 * i + lane]);
+                    }
+                    hadamard_chunk(a.x + static_cast<size_t>(p) * H, m4, wave, lane, xs);
+                    block_barrier();
+                    hadamard_cross(xs, a.scale_hidden, wave, lane);
+                    block_barrier();
+                    float *dst = const_cast<float *>(a.gu.expert[which].x_hat) + static_cast<size_t>(g) * H;
+                    reinterpret_cast<float4 *>(dst)[64u * wave + lane] =
+                        reinterpret_cast<const float4 *>(xs)[64u * wave + lane];
+                    block_barrier();  // xs is free again
+                    wait_stores();
+                    if (lane == 0) {
+                        coherent_add(few_word(sync, few_sync::kXReady + 2u * s + which), 1u);
+                    }
+                }
+            }
+        }
+    }
+    // the shared gate/up unit, while the first slot's x_hat rows come in
+    if (gu_unit) {
+        ne_compute<true>(a.gu, gu_k, ne_table, lane, gu_st, gu_first, gu_first + gu_per);
+        wait_stores();
+        if (lane == 0) {
+            coherent_add(few_word(sync, few_sync::kSharedGu + xcd), 1u);
+        }
+    }
+    // ---- P2: item m_block * 8 + wave of every slot of the XCD, the next
+    // slot's codes and x_hat in flight during the arithmetic ----
+    const uint32_t il = m_block * kGemvWaves + wave;
+    {
+        const uint32_t which = il / a.gu.expert_items_per_slot;
+        const uint32_t item = il % a.gu.expert_items_per_slot;
+        auto index = [&](uint32_t t) { return ((which * a.gu.max_active + slot_of(t)) << a.gu.item_shift) + item; };
+        auto stage = [&](uint32_t t, ExpertStage &st) {
+            const uint32_t s = slot_of(t);
+            const uint4 info = slots[s];
+            expert_prefetch(a.gu, slots, index(t), half, lane, st, nullptr, false);
+            wait_count(few_word(sync, few_sync::kXReady + 2u * s + which), kGemvWaves * (info.z - info.y), error, 4u);
+            expert_load_x(a.gu, index(t), half, lane, st);
+        };
+        // plain stores: only this XCD's SwiGLU rows read these Z slices
+        auto run = [&](uint32_t t, ExpertStage &st) {
+            expert_compute<false>(a.gu, index(t), half, plane, lane, st);
+            count_block_quiet(&counts[kGuCount + t], kGemvWaves, few_word(sync, few_sync::kGuDone + slot_of(t)));
+        };
+        ExpertStage s0, s1;
+        if (n_slots > 0) {
+            stage(0, s0);
+        }
+        for (uint32_t t = 0; t < n_slots; t += 2u) {
+            if (t + 1u < n_slots) {
+                stage(t + 1u, s1);
+            }
+            run(t, s0);
+            if (t + 1u >= n_slots) {
+                break;
+            }
+            if (t + 2u < n_slots) {
+                stage(t + 2u, s0);
+            }
+            run(t + 1u, s1);
+        }
+    }
+    NeStage dn_st;
+    if (dn_unit) {
+        ne_prefetch_codes(a.dn, dn_k, lane, dn_st);
+    }
+    // ---- P3: the wave's SwiGLU rows of its XCD's routes (waves 0 .. 6 below
+    // 224 routes per XCD), and the shared expert's SwiGLU row p on wave 7 of
+    // block p ----
+    {
+        uint32_t q = 0;
+        for (uint32_t t = 0; t < n_slots; ++t) {
+            const uint32_t s = slot_of(t);
+            const uint4 info = slots[s];
+            for (uint32_t g = info.y; g < info.z; ++g, ++q) {
+                if (q % xcd_blocks != k || (q / xcd_blocks) % kGemvWaves != wave) {
+                    continue;
+                }
+                SwigluInputs in;
+                swiglu_issue_scales(a.dn.swiglu, false, info.x, lane, in);
+                wait_count(few_word(sync, few_sync::kGuDone + s), a.expect_gu, error, 4u);
+                float xd[VPLI];
+                swiglu_issue_slices(a.dn.swiglu, false, g, lane, in);
+                swiglu_finish(a.dn.swiglu, false, g, lane, in, xd);
+                store_wave<VPLI>(const_cast<float *>(a.dn.expert[0].x_hat) + static_cast<size_t>(g) * kFusedSwigluWidth,
+                                 lane, xd);
+                wait_stores();
+                if (lane == 0) {
+                    coherent_add(few_word(sync, few_sync::kDownX + s), 1u);
+                }
+            }
+        }
+    }
+    if (wave == kGemvWaves - 1u && b < B) {
+        const uint32_t p = b;
+        few_wait_total(sync, few_sync::kSharedGu, a.gu.ne_items * gu_groups, lane, error, 8u);
+        SwigluInputs in;
+        float xd[VPLI];
+        swiglu_issue(a.dn.swiglu, true, p, 0u, lane, in);
+        swiglu_finish(a.dn.swiglu, true, p, lane, in, xd);
+        store_wave_through<VPLI>(const_cast<float *>(a.dn.ne[0].x_hat) + static_cast<size_t>(p) * kFusedSwigluWidth,
+                                 lane, xd);
+        wait_stores();
+        if (lane == 0) {
+            coherent_add(few_word(sync, few_sync::kSharedDownX + xcd), 1u);
+        }
+    }
+    // ---- P4: down item m_block * 8 + wave of every slot of the XCD, the
+    // next slot's codes and x_hat in flight during the arithmetic ----
+    {
+        auto index = [&](uint32_t t) { return (slot_of(t) << a.dn.item_shift) + il; };
+        auto stage = [&](uint32_t t, ExpertStage &st) {
+            const uint4 info = slots[slot_of(t)];
+            expert_prefetch(a.dn, slots, index(t), half, lane, st, nullptr, false);
+            wait_count(few_word(sync, few_sync::kDownX + slot_of(t)), info.z - info.y, error, 4u);
+            expert_load_x(a.dn, index(t), half, lane, st);
+        };
+        auto run = [&](uint32_t t, ExpertStage &st) {
+            expert_compute<false>(a.dn, index(t), half, plane, lane, st);  // read on this XCD only
+            count_block_quiet(&counts[kDnCount + t], kGemvWaves, few_word(sync, few_sync::kDnDone + slot_of(t)));
+        };
+        ExpertStage s0, s1;
+        if (n_slots > 0) {
+            stage(0, s0);
+        }
+        for (uint32_t t = 0; t < n_slots; t += 2u) {
+            if (t + 1u < n_slots) {
+                stage(t + 1u, s1);
+            }
+            run(t, s0);
+            if (t + 1u >= n_slots) {
+                break;
+            }
+            if (t + 2u < n_slots) {
+                stage(t + 2u, s0);
+            }
+            run(t + 1u, s1);
+        }
+    }
+    // the shared down unit; the last one in (two-level count: each group
+    // line b % 8 takes an eighth of them) sets the shared flag
+    if (dn_unit) {
+        const uint32_t per_line = a.dn.ne_items * dn_groups / 8u;
+        few_wait_total(sync, few_sync::kSharedDownX, B, lane, error, 8u);
+        ne_prefetch_x(a.dn, dn_k, lane, dn_st, dn_first);
+        ne_compute<true>(a.dn, dn_k, ne_table, lane, dn_st, dn_first, dn_first + dn_per);
+        wait_stores();
+        uint32_t finisher = 0;
+        if (lane == 0 && coherent_add(few_word(sync, few_sync::kSharedDown + xcd), 1u) + 1u == per_line &&
+            coherent_add(few_word(sync, few_sync::kSharedDown + 8u), 1u) + 1u == 8u) {
+            finisher = 1u;
+        }
+        if (__builtin_amdgcn_readfirstlane(finisher) != 0u && lane < 8u) {
+            coherent_store(few_word(sync, few_sync::kSharedDone + lane), 1u);
+        }
+    }
+    // ---- P5: combine rows by the eight waves (chunks of 256, then the top
+    // three butterfly stages across chunks: combine_row's values); route q
+    // of the XCD on block q % 32, once its slot's down items are in ----
+    float *row = region;
+    auto block_combine_row = [&](const float *z, size_t zs, uint32_t splits, const uint16_t *sv_f16,
+                                 const int8_t *sv_sign, float weight, float *dst) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = 0.0f;
+        }
+        for (uint32_t sl = 0; sl < splits; ++sl) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = v[i] + z[sl * zs + 256u * wave + 64u * i + lane];
+            }
+        }
+        wave_hadamard<4>(v, 1.0f, lane);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            row[256u * wave + 64u * i + lane] = v[i];
+        }
+        block_barrier();
+        if (lane < 32) {
+            const uint32_t j = 32u * wave + lane;
+            float u[8];
+#pragma unroll
+            for (int qq = 0; qq < 8; ++qq) {
+                u[qq] = row[256u * qq + j];
+            }
+#pragma unroll
+            for (int stride = 1; stride < 8; stride <<= 1) {
+#pragma unroll
+                for (int qq = 0; qq < 8; ++qq) {
+                    if ((qq & stride) == 0) {
+                        const float x0 = u[qq], x1 = u[qq + stride];
+                        u[qq] = x0 + x1;
+                        u[qq + stride] = x0 - x1;
+                    }
+                }
+            }
+#pragma unroll
+            for (int qq = 0; qq < 8; ++qq) {
+                const float h = u[qq] * a.scale_hidden;
+                const float sv = sv_f16 != nullptr ? half_bits_to_float(sv_f16[256u * qq + j])
+                                                   : static_cast<float>(sv_sign[256u * qq + j]);
+                coherent_store(dst + 256u * qq + j, weight * (h * sv));
+            }
+        }
+        wait_stores();
+        block_barrier();  // every wave's stores are complete, the LDS row is free
+    };
+    {
+        uint32_t q = 0;
+        for (uint32_t t = 0; t < n_slots; ++t) {
+            const uint32_t s = slot_of(t);
+            const uint4 info = slots[s];
+            for (uint32_t g = info.y; g < info.z; ++g, ++q) {
+                if (q % xcd_blocks != k) {
+                    continue;
+                }
+                wait_count(few_word(sync, few_sync::kDnDone + s), a.expect_dn, error, 4u);
+                const uint32_t r = grouped_route[g];
+                const uint32_t p = r >> 3;
+                block_combine_row(a.dn.expert[0].z + static_cast<size_t>(g) * H, a.dn.expert[0].z_split_stride,
+                                  a.down_splits, a.sv_down + static_cast<size_t>(info.x) * H, nullptr, route_w[r],
+                                  a.parts + (static_cast<size_t>(p) * 9u + (r & 7u)) * H);
+                if (wave == 0) {
+                    few_row_in(a, p, lane);
+                }
+            }
+        }
+    }
+    // the shared expert's combine row p on block blocks / 2 + p
+    if (b >= blocks / 2u && b - blocks / 2u < B) {
+        const uint32_t p = b - blocks / 2u;
+        wait_count(few_word(sync, few_sync::kSharedDone + xcd), 1u, error, 8u);
+        const float gate = a.logits[static_cast<size_t>(p) * row_words + E];
+        block_combine_row(a.dn.ne[0].z + static_cast<size_t>(p) * H, a.dn.ne[0].z_split_stride, a.shared_down_splits,
+                          nullptr, a.shared_sv_down, 1.0f / (1.0f + expf(-gate)),
+                          a.parts + (static_cast<size_t>(p) * 9u + 8u) * H);
+        if (wave == 0) {
+            few_row_in(a, p, lane);
+        }
+    }
+    // ---- the last block through clears the counters ----
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        last = few_ticket(sync, few_sync::kExit, few_sync::kExit + 8u, b, blocks) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (last != 0u) {
+        for (uint32_t i = threadIdx.x; i < few_sync::kCounters; i += kGemvThreads) {
+            coherent_store(few_word(sync, i), 0u);
+        }
+    }
+}
+
 // ---- one-launch NE projection of a few rows -------------------------------
 //
 // y = sv * H_rows(W x_hat) * scale_rows with x_hat = H_columns(su * x) *
@@ -2405,6 +3145,56 @@ void launch_moe_decode_one(adi_hip_context *ctx, const MoeDecodeOne &a) {
             set_lds_limit(reinterpret_cast<const void *>(&k_moe_decode_one<8>), lds);
         (void)ready;
         launch(ctx, "moe_decode_one", k_moe_decode_one<8>, dim3(blocks), dim3(kFusedThreads), lds, a);
+    }
+}
+
+bool plan_moe_decode_few(adi_hip_context *ctx, MoeDecodeFew &a) {
+    if (ctx->cu_count < 32 || (ctx->isa_lanes != 8 && ctx->isa_lanes != 16) || a.sync == nullptr ||
+        a.error == nullptr || a.batch < 2 || a.batch > kFewMaxRows || a.experts < 8 ||
+        a.experts > kFusedMaxExperts || a.gu.expert_count != 2 || a.gu.ne_count != 2 || a.dn.expert_count != 1 ||
+        a.dn.ne_count != 1 || a.gu.max_active < 8 * a.batch || a.dn.max_active < 8 * a.batch ||
+        a.gu.max_active > kFewMaxRoutes || a.dn.max_active > kFewMaxRoutes || a.gu.ne_book != a.dn.ne_book ||
+        a.logits == nullptr || a.parts == nullptr) {
+        return false;
+    }
+    const ExpertGemv &g = a.gu.expert[0], &d = a.dn.expert[0];
+    if (g.rows != kFusedSwigluWidth || g.columns != kFusedHidden || d.rows != kFusedHidden ||
+        d.columns != kFusedSwigluWidth || a.gu.ne[0].rows != kFusedSwigluWidth ||
+        a.gu.ne[0].columns != kFusedHidden || a.dn.ne[0].rows != kFusedHidden ||
+        a.dn.ne[0].columns != kFusedSwigluWidth || a.gu.ne[0].batch != a.batch || a.dn.ne[0].batch != a.batch) {
+        return false;
+    }
+    const uint32_t blocks = ctx->cu_count / 32 * 32;
+    plan_trellis_gemv(ctx, a.gu);
+    plan_trellis_gemv(ctx, a.dn);
+    // an (XCD, half) pair of blocks runs one item of every slot of its XCD
+    // per wave: both gate/up entries' items, and the down entry's
+    const uint32_t pair_waves = blocks / 16u * kGemvWaves;
+    if (2u * a.gu.expert_items_per_slot != pair_waves || a.dn.expert_items_per_slot != pair_waves ||
+        a.experts + 1 > 2 * blocks || a.gu.ne_items != 2 * a.gu.ne_items_per_matrix ||
+        a.gu.ne_items_per_matrix > blocks || a.dn.ne_items != blocks || 2u * a.batch > blocks) {
+        return false;
+    }
+    a.expect_gu = 2u * a.gu.expert_count * a.gu.expert_items_per_slot;
+    a.expect_dn = 2u * a.dn.expert_items_per_slot;
+    a.down_splits = expert_splits(kFusedSwigluWidth);
+    a.shared_down_splits = ne_splits(kFusedSwigluWidth);
+    return true;
+}
+
+void launch_moe_decode_few(adi_hip_context *ctx, const MoeDecodeFew &a) {
+    const uint32_t blocks = ctx->cu_count / 32 * 32;
+    const size_t lds = kPlaneBytes + kFusedRegion;
+    if (ctx->isa_lanes == 16) {
+        static const bool ready =
+            set_lds_limit(reinterpret_cast<const void *>(&k_moe_decode_few<16>), lds);
+        (void)ready;
+        launch(ctx, "moe_decode_few", k_moe_decode_few<16>, dim3(blocks), dim3(kGemvThreads), lds, a);
+    } else {
+        static const bool ready =
+            set_lds_limit(reinterpret_cast<const void *>(&k_moe_decode_few<8>), lds);
+        (void)ready;
+        launch(ctx, "moe_decode_few", k_moe_decode_few<8>, dim3(blocks), dim3(kGemvThreads), lds, a);
     }
 }
 

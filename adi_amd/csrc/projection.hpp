@@ -229,6 +229,54 @@ struct MoeDecodeOne {
 // order of 8 or 16 lanes). The caller then runs the separate launches.
 bool plan_moe_decode_one(adi_hip_context *ctx, MoeDecodeOne &a);
 void launch_moe_decode_one(adi_hip_context *ctx, const MoeDecodeOne &a);
+// The MoE block of 2 to kFewMaxRows rows in one persistent launch
+// (src/executor.cpp:242-330 for each row): router and top-8 of every row,
+// the expert-sorted slots, the routed and shared gate/up, the SwiGLUs, the
+// down projections and the route-order combine, one block per CU, with the
+// separate launches' arithmetic (decode-GEMV items, one-wave combine rows),
+// so results are bit-identical to theirs. Routed slot s runs on XCD s % 8.
+// Data passes between blocks through device-coherent accesses and counters
+// from `sync` (bounded waits; a wait that runs out sets the error word).
+constexpr uint32_t kFusedHidden = 2048;     // hidden width of the one-launch MoE blocks
+constexpr uint32_t kFusedMaxExperts = 256;  // routed experts they handle
+// Up to 12 rows: from there the MFMA grouped GEMMs (16 rows: 148.7 against
+// 164.8 us a layer) overtake the decode-GEMV items this launch runs.
+constexpr uint32_t kFewMaxRows = 12;
+constexpr uint32_t kFewMaxRoutes = 8 * kFewMaxRows;
+struct MoeDecodeFew {
+    MoeGemv gu;                       // routed gate/up (entries 0, 1), shared gate/up (NE 0, 1)
+    MoeGemv dn;                       // routed down (entry 0), shared down (NE 0); dn.swiglu set
+    const uint16_t *router;           // [experts][hidden] bf16
+    const uint16_t *shared_gate_row;  // [hidden] bf16
+    const float *logit_bias;          // [experts] or null
+    const float *x;                   // [batch][hidden]
+    const uint16_t *su_gate;          // [experts][hidden] f16
+    const uint16_t *su_up;
+    const int8_t *shared_su_gate;     // [hidden] +-1
+    const int8_t *shared_su_up;
+    const uint16_t *sv_down;          // [experts][hidden] f16
+    const int8_t *shared_sv_down;     // [hidden] +-1
+    float scale_hidden;               // 1 / sqrt(hidden)
+    float *out;                       // [batch][hidden]
+    uint32_t *route_expert_out;       // [batch * 8] or null
+    float *route_weight_out;
+    float *logits;                    // [batch][experts + 1]: router logits, then the shared gate's
+    float *parts;                     // [batch][9][hidden]: the combine rows
+    uint32_t *sync;                   // the counters (zero between calls)
+    uint32_t *error;                  // the error word
+    uint32_t experts;
+    uint32_t batch;
+    // set by plan_moe_decode_few
+    uint32_t expect_gu;               // gate/up wave items per routed slot (both planes)
+    uint32_t expect_dn;               // down wave items per routed slot
+    uint32_t down_splits;             // Z slices of the routed and shared down projections
+    uint32_t shared_down_splits;
+};
+// Fills the plans; false when the shapes or the device do not fit the launch
+// (hidden 2048, expert hidden 512, at most 256 experts, 2 to kFewMaxRows rows,
+// 256 CUs, the ISA order of 8 or 16 lanes).
+bool plan_moe_decode_few(adi_hip_context *ctx, MoeDecodeFew &a);
+void launch_moe_decode_few(adi_hip_context *ctx, const MoeDecodeFew &a);
 // One-launch NE projection of up to kNeFusedRows input rows (k_ne_fused):
 // x_hat, the NE items of whole tile rows per block with the slice-order sum
 // in LDS, and the row transform by the block that takes the last ticket. One

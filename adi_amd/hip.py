@@ -300,10 +300,13 @@ class Context:
     def synchronize(self) -> None:
         self.check(self.lib.adi_hip_synchronize(self.handle))
 
-    def set_fused_decode(self, enabled: bool) -> None:
-        """One persistent launch for a one-row MoE block (default) or the
-        separate launches."""
-        self.check(self.lib.adi_hip_set_fused_decode(self.handle, 1 if enabled else 0))
+    def set_fused_decode(self, enabled) -> None:
+        """One persistent launch for a MoE block of 1-12 rows and for NE
+        projections of up to 4 rows (True, the default), or the separate
+        launches (False); "gemv" is the separate launches with the
+        decode-GEMV path up to 16 rows (the one-launch block's arithmetic)."""
+        mode = 2 if enabled == "gemv" else (1 if enabled else 0)
+        self.check(self.lib.adi_hip_set_fused_decode(self.handle, mode))
 
     def set_workspace_limit(self, limit: int | None) -> None:
         """Cap each scratch arena at `limit` bytes (None: no cap); a call that

@@ -90,9 +90,9 @@ def log(msg):
 
 def kernel_bytes(name, active):
     """Algorithmic packed bytes one launch of `name` reads, or None."""
-    if name == "moe_decode_one":
-        # the whole ubatch-1 layer in one launch: router, shared expert, and
-        # the active experts' gate, up and down with their scales
+    if name in ("moe_decode_one", "moe_decode_few"):
+        # the whole layer in one launch (1 row, or 2-12 rows): router, shared
+        # expert, and the active experts' gate, up and down with their scales
         return FIXED_LAYER_BYTES + active * PER_EXPERT_BYTES
     if name == "moe_gemv":
         # two launches per step: gate+up (2 expert + 2 shared matrices), down
@@ -218,7 +218,7 @@ def kernel_flops(name, ubatch):
         return 1.5 * 2.0 * 8 * ubatch * EXPERT_HIDDEN * HIDDEN
     if name == "ne_mfma":
         return 1.5 * 2.0 * ubatch * EXPERT_HIDDEN * HIDDEN
-    if name == "moe_decode_one":
+    if name in ("moe_decode_one", "moe_decode_few"):
         return FLOP_PER_TOKEN * ubatch
     return None
 
@@ -226,7 +226,8 @@ def kernel_flops(name, ubatch):
 RIDGE_FLOP_PER_BYTE = MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)  # 312.5
 
 
-ROCPROF_NAMES = {"moe_decode_one": "k_moe_decode_one", "moe_gemv": "k_trellis_gemv",
+ROCPROF_NAMES = {"moe_decode_one": "k_moe_decode_one", "moe_decode_few": "k_moe_decode_few",
+                 "moe_gemv": "k_trellis_gemv",
                  "expert_mfma": "k_expert_mfma", "ne_fused": "k_ne_fused", "head": "k_head_mfma"}
 
 
@@ -340,7 +341,8 @@ def kind_report(prof, steps, ubatch, cpu_kinds, cpu_ms):
         entry["work_items_per_step"] = v["work_items_per_step"]
         if "gpu_ms_per_step" not in entry:
             entry["gpu_ms_per_step"] = None
-            entry["gpu_note"] = ("inside the one-launch layer" if "moe_decode_one" in prof else
+            entry["gpu_note"] = ("inside the one-launch layer" if ("moe_decode_one" in prof or
+                                                                    "moe_decode_few" in prof) else
                                  "inside " + next((k for k in gpu if kind in k.split("+")), "moe"))
     return report
 

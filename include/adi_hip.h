@@ -64,13 +64,17 @@ int adi_hip_synchronize(adi_hip_context *ctx);
  * src/simd.cpp:298-342). Default 16. */
 int adi_hip_set_reduction_isa(adi_hip_context *ctx, uint32_t lanes);
 
-/* Whether decode-size calls run as one launch (default on) or as the
- * separate launches: adi_hip_moe_forward on one row (router, routing, both
- * projections of every route, shared expert and combine in one persistent
- * launch) and adi_hip_ne_matmul on up to 4 rows of the shapes it is built
- * for (x_hat, the NE items and the output transform in one launch). Both
- * ways give bit-identical results. No counterpart in the reference (a tuning
- * switch of this backend). A cross-block wait of the one-launch MoE block
+/* Whether decode-size calls run as one launch (enabled 1, the default) or
+ * as the separate launches (0): adi_hip_moe_forward on 1 to 12 rows (router,
+ * routing, both projections of every route, shared expert and combine in
+ * one persistent launch) and adi_hip_ne_matmul on up to 4 rows of the shapes
+ * it is built for (x_hat, the NE items and the output transform in one
+ * launch). The one-launch MoE block of 2 to 12 rows runs the decode-GEMV
+ * arithmetic; the separate launches take the MFMA GEMMs from 8 rows, except
+ * with enabled 2 (separate launches, decode-GEMV up to 16 rows), which gives
+ * results bit-identical to the one-launch block at every batch it runs; at
+ * 1 to 7 rows, 0 and 2 are the same. No counterpart in the reference (a tuning
+ * switch of this backend). A cross-block wait of a one-launch MoE block
  * that runs out (only possible when other work keeps some of its blocks off
  * the GPU) is reported by the next adi_hip_synchronize. */
 int adi_hip_set_fused_decode(adi_hip_context *ctx, int enabled);
@@ -309,7 +313,7 @@ int adi_hip_moe_forward(adi_hip_context *ctx, const adi_hip_moe_layer *layer,
  * no hipMalloc, hipFree or allocating library call on any path. No
  * counterpart in the reference; it is for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
- * it). The intermediates live in a fixed 8 MiB device array of the library,
+ * it). The intermediates live in a fixed 12 MiB device array of the library,
  * one per GPU, held until the process ends; a batch or layer geometry whose
  * plan exceeds it is rejected (ADI_HIP_INVALID_ARGUMENT, outputs untouched).
  * Every call on one GPU shares that array: calls that overlap on one GPU (from

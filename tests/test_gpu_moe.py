@@ -126,3 +126,68 @@ def test_moe_one_launch_repeated_calls(gpu, full_layer):
             assert np.array_equal(got[1], want[1])
     finally:
         gpu.set_fused_decode(True)
+
+
+def run_few_both(gpu, dl, x, bias):
+    """The layer as the one-launch block of 2-12 rows and as the separate
+    launches on the decode-GEMV path (the same arithmetic)."""
+    try:
+        gpu.set_fused_decode(True)
+        fused = run_moe(gpu, dl, x, bias)
+        gpu.synchronize()
+        gpu.set_fused_decode("gemv")
+        separate = run_moe(gpu, dl, x, bias)
+    finally:
+        gpu.set_fused_decode(True)
+    return fused, separate
+
+
+@pytest.mark.parametrize("batch", [2, 3, 4, 8, 12])
+@pytest.mark.parametrize("bias", [False, True])
+def test_moe_few_rows_one_launch_equals_separate_launches(gpu, oracle, full_layer, batch, bias):
+    """2-12 rows in one launch (k_moe_decode_few) against the separate
+    decode-GEMV launches: routes, weights and outputs bit-identical, and within
+    the tolerance of the oracle."""
+    layer, dl = full_layer
+    rng = syn.rng_for(2, 500 + 7 * batch + (1 if bias else 0))
+    x = syn.hidden_states(rng, batch, layer.hidden)
+    b = syn.zipf_bias(rng, layer.experts) if bias else None
+    print(f"moe few rows: batch {batch}, bias {bias}", flush=True)
+    fused, separate = run_few_both(gpu, dl, x, b)
+    assert np.array_equal(fused[1], separate[1]), "routes differ"
+    assert np.array_equal(fused[2].view(np.uint32), separate[2].view(np.uint32)), "weights differ"
+    assert np.array_equal(fused[0].view(np.uint32), separate[0].view(np.uint32)), "outputs differ"
+    check(oracle, layer, fused, x, b)
+
+
+def test_moe_few_rows_shared_slots(gpu, oracle, full_layer):
+    """Every row the same input: all rows choose the same eight experts, so
+    each slot holds all 12 rows (the widest slots)."""
+    layer, dl = full_layer
+    rng = syn.rng_for(2, 600)
+    x = np.repeat(syn.hidden_states(rng, 1, layer.hidden), 12, axis=0)
+    fused, separate = run_few_both(gpu, dl, x, None)
+    assert np.array_equal(fused[1], separate[1])
+    assert np.array_equal(fused[0].view(np.uint32), separate[0].view(np.uint32))
+    assert np.array_equal(fused[0][0].view(np.uint32), fused[0][11].view(np.uint32))
+    check(oracle, layer, fused, x, None)
+
+
+def test_moe_few_rows_repeated_calls(gpu, full_layer):
+    """Back-to-back calls of 12, 1, 5, 2, 1 and 12 rows on new inputs: every
+    call's counters start from zero (the last block through clears them), and
+    the one-row block's leftover combine rows sit outside the few-row block's
+    counters."""
+    layer, dl = full_layer
+    rng = syn.rng_for(2, 700)
+    xs = [syn.hidden_states(rng, n, layer.hidden) for n in (12, 1, 5, 2, 1, 12)]
+    outs = [run_moe(gpu, dl, x, None) for x in xs]
+    gpu.synchronize()
+    gpu.set_fused_decode("gemv")
+    try:
+        for x, got in zip(xs, outs):
+            want = run_moe(gpu, dl, x, None)
+            assert np.array_equal(got[0].view(np.uint32), want[0].view(np.uint32))
+            assert np.array_equal(got[1], want[1])
+    finally:
+        gpu.set_fused_decode(True)
