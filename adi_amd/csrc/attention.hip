@@ -595,20 +595,45 @@ void forward(adi_hip_context *ctx, int status) {
 // (three backend.ne_matmul calls, src/executor.cpp:596-613) in one NE launch
 // where it takes the shapes.
 void project_qkv(adi_hip_context *ctx, const adi_hip_full_attention *L, const float *inputs,
-                 uint32_t count, float *query_gate, float *key, float *value) {
+                 uint32_t count, float *query_gate, float *key, float *value, const NeNormIn *norm_in) {
     const adi_hip_ne_matrix *m[3] = {&L->query, &L->key, &L->value};
     float *out[3] = {query_gate, key, value};
-    ne_matmul_group(ctx, m, 3, inputs, count, out);
+    ne_matmul_group(ctx, m, 3, inputs, count, out, norm_in);
 }
 
 // The Gated DeltaNet's qkv and gate projections of the same rows (two
 // backend.ne_matmul calls, src/executor.cpp:764-775) in one NE launch where
 // it takes the shapes.
 void project_qkv_gate(adi_hip_context *ctx, const adi_hip_linear_attention *L, const float *inputs,
-                      uint32_t count, float *qkv, float *gate) {
+                      uint32_t count, float *qkv, float *gate, const NeNormIn *norm_in) {
     const adi_hip_ne_matrix *m[2] = {&L->qkv, &L->gate};
     float *out[2] = {qkv, gate};
-    ne_matmul_group(ctx, m, 2, inputs, count, out);
+    ne_matmul_group(ctx, m, 2, inputs, count, out, norm_in);
+}
+
+// The decay inputs alpha and beta of the same rows (two dense bf16 matmuls,
+// src/executor.cpp:776-787) in one launch where the small-batch kernel
+// takes them (with the one-launch decode paths on).
+void project_decay(adi_hip_context *ctx, const adi_hip_linear_attention *L, const float *x, uint32_t count,
+                   float *alpha, float *beta) {
+    if (!ctx->fused_moe) {
+        forward(ctx, adi_hip_bf16_matmul(ctx, &L->alpha, x, count, alpha));
+        forward(ctx, adi_hip_bf16_matmul(ctx, &L->beta, x, count, beta));
+        return;
+    }
+    launch_bf16_pair(ctx, L->alpha.values, L->alpha.rows, L->beta.values, L->beta.rows, L->alpha.columns, x,
+                     count, alpha, beta, ctx->isa_lanes);
+}
+
+// The output projection, then (with `tail`) the residual add and the next
+// RMS norm folded into it where the one-launch NE projection takes it.
+void project_output(adi_hip_context *ctx, const adi_hip_ne_matrix *m, const float *inputs, uint32_t count,
+                    float *outputs, const NeNormTail *tail) {
+    if (tail == nullptr) {
+        forward(ctx, adi_hip_ne_matmul(ctx, m, inputs, count, outputs));
+        return;
+    }
+    ne_matmul_group(ctx, &m, 1, inputs, count, &outputs, nullptr, tail);
 }
 
 bool ne_shaped(const adi_hip_ne_matrix &m, uint32_t rows, uint32_t columns) {
@@ -618,7 +643,8 @@ bool ne_shaped(const adi_hip_ne_matrix &m, uint32_t rows, uint32_t columns) {
 // full_attention_forward for tokens position .. position + count - 1.
 void full_attention_chunk(adi_hip_context *ctx, const adi_hip_full_attention *L,
                           uint32_t position, uint32_t count, const float *inputs, float *outputs,
-                          float *keys, float *values, uint32_t capacity) {
+                          float *keys, float *values, uint32_t capacity,
+                          const NeNormIn *norm_in = nullptr, const NeNormTail *norm_tail = nullptr) {
     require(L != nullptr && inputs != nullptr && outputs != nullptr && keys != nullptr &&
                 values != nullptr && count > 0,
             "full attention state or input shape mismatch");
@@ -650,7 +676,7 @@ void full_attention_chunk(adi_hip_context *ctx, const adi_hip_full_attention *L,
     float *partial = ws.take<float>(size_t(count) * kQueryHeads * splits * kPartialStride);
     float *key = keys + static_cast<size_t>(position) * kKvHeads * kHeadSize;
     float *value = values + static_cast<size_t>(position) * kKvHeads * kHeadSize;
-    project_qkv(ctx, L, inputs, count, query_gate, key, value);
+    project_qkv(ctx, L, inputs, count, query_gate, key, value, norm_in);
     launch(ctx, "attention_norm_rope", k_norm_rope, dim3(kQueryHeads + kKvHeads, count),
            dim3(kHeadSize), 0, query_gate, key, L->query_norm, L->key_norm,
            count == 1 ? rope_table(position) : RopeTable{},
@@ -661,13 +687,14 @@ void full_attention_chunk(adi_hip_context *ctx, const adi_hip_full_attention *L,
     launch(ctx, "attention_combine", k_attention_combine, dim3(kQueryHeads, count),
            dim3(kHeadSize), 0, static_cast<const float *>(partial), splits,
            static_cast<const float *>(query_gate), attended);
-    forward(ctx, adi_hip_ne_matmul(ctx, &L->output, attended, count, outputs));
+    project_output(ctx, &L->output, attended, count, outputs, norm_tail);
 }
 
 // linear_attention_forward for `count` consecutive tokens.
 void linear_attention_chunk(adi_hip_context *ctx, const adi_hip_linear_attention *L,
                             uint32_t count, const float *inputs, float *outputs,
-                            float *convolution_state, float *recurrent_state) {
+                            float *convolution_state, float *recurrent_state,
+                            const NeNormIn *norm_in = nullptr, const NeNormTail *norm_tail = nullptr) {
     require(L != nullptr && inputs != nullptr && outputs != nullptr &&
                 convolution_state != nullptr && recurrent_state != nullptr && count > 0,
             "linear attention input shape mismatch");
@@ -696,9 +723,9 @@ void linear_attention_chunk(adi_hip_context *ctx, const adi_hip_linear_attention
     float *normalized = ws.take<float>(n * kValueSize);
     float *alpha = ws.take<float>(n * kValueHeads);
     float *beta = ws.take<float>(n * kValueHeads);
-    project_qkv_gate(ctx, L, inputs, count, qkv, gate);
-    forward(ctx, adi_hip_bf16_matmul(ctx, &L->alpha, inputs, count, alpha));
-    forward(ctx, adi_hip_bf16_matmul(ctx, &L->beta, inputs, count, beta));
+    project_qkv_gate(ctx, L, inputs, count, qkv, gate, norm_in);
+    const float *x = norm_in != nullptr ? norm_in->out : inputs;  // the normalized rows
+    project_decay(ctx, L, x, count, alpha, beta);
     launch(ctx, "linear_conv", k_linear_conv, dim3(kChannels / kLinearHead, count),
            dim3(kLinearHead), 0, static_cast<const float *>(qkv), L->convolution,
            convolution_state, convolved);
@@ -713,7 +740,7 @@ void linear_attention_chunk(adi_hip_context *ctx, const adi_hip_linear_attention
     launch(ctx, "linear_norm_gate", k_linear_norm_gate, dim3(kValueHeads, count),
            dim3(kLinearHead), 0, static_cast<const float *>(recurrent_output), L->norm,
            static_cast<const float *>(gate), normalized);
-    forward(ctx, adi_hip_ne_matmul(ctx, &L->output, normalized, count, outputs));
+    project_output(ctx, &L->output, normalized, count, outputs, norm_tail);
 }
 
 // decode_layer for `count` consecutive tokens of rows `hidden`.
@@ -736,9 +763,12 @@ void layer_body(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_t c
     ws.ensure(Workspace::round(rows * 4) * 2);
     float *normalized = ws.take<float>(rows);
     float *branch = ws.take<float>(rows);
-    launch_add_rms_norm(ctx, hidden, pending, L->input_norm, n, count, normalized);
-    attention(static_cast<const float *>(normalized), branch);
-    launch_add_rms_norm(ctx, hidden, branch, L->post_attention_norm, n, count, normalized);
+    // the input norm (with the residual add of the previous layer's MoE rows)
+    // and the post-attention norm run inside the attention's first and last
+    // projections where they can, else as norm launches around them
+    const NeNormIn norm_in{hidden, pending, L->input_norm, normalized};
+    const NeNormTail norm_tail{hidden, L->post_attention_norm, normalized};
+    attention(static_cast<const float *>(normalized), branch, &norm_in, &norm_tail);
     forward(ctx, adi_hip_moe_forward(ctx, &L->moe, normalized, count, nullptr, moe_out, nullptr,
                                      nullptr));
 }
@@ -749,13 +779,14 @@ void decoder_chunk_body(adi_hip_context *ctx, const adi_hip_decoder_layer *L, ui
                         uint32_t count, float *hidden, const float *pending, float *moe_out,
                         const adi_hip_layer_state *state) {
     require(state != nullptr, "decoder layer input is null");
-    layer_body(ctx, L, count, hidden, pending, moe_out, [&](const float *in, float *out) {
+    layer_body(ctx, L, count, hidden, pending, moe_out,
+               [&](const float *in, float *out, const NeNormIn *norm_in, const NeNormTail *norm_tail) {
         if (L->full_attention != 0) {
             full_attention_chunk(ctx, &L->full, position, count, in, out, state->keys,
-                                 state->values, state->capacity);
+                                 state->values, state->capacity, norm_in, norm_tail);
         } else {
             linear_attention_chunk(ctx, &L->linear, count, in, out, state->convolution,
-                                   state->recurrent);
+                                   state->recurrent, norm_in, norm_tail);
         }
     });
 }
@@ -785,7 +816,8 @@ void decoder_chunk(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_
 void full_attention_rows(adi_hip_context *ctx, const adi_hip_full_attention *L, uint32_t rows,
                          const float *inputs, float *outputs,
                          const adi_hip_layer_state *const *states, const uint32_t *positions,
-                         const uint32_t *device_positions, uint32_t span) {
+                         const uint32_t *device_positions, uint32_t span,
+                         const NeNormIn *norm_in, const NeNormTail *norm_tail) {
     require(L != nullptr && inputs != nullptr && outputs != nullptr && states != nullptr &&
                 positions != nullptr && device_positions != nullptr && rows > 0,
             "full attention batch shape mismatch");
@@ -821,7 +853,7 @@ void full_attention_rows(adi_hip_context *ctx, const adi_hip_full_attention *L, 
     float *value = ws.take<float>(n * kKvHeads * kHeadSize);
     float *attended = ws.take<float>(n * kQueryHeads * kHeadSize);
     float *partial = ws.take<float>(n * kQueryHeads * splits * kPartialStride);
-    project_qkv(ctx, L, inputs, rows, query_gate, key, value);
+    project_qkv(ctx, L, inputs, rows, query_gate, key, value, norm_in);
     const float *rope = rope_rows(ctx, last);
     for (uint32_t first = 0; first < rows; first += kRowGroup) {
         const uint32_t count = rows - first < kRowGroup ? rows - first : kRowGroup;
@@ -845,7 +877,7 @@ void full_attention_rows(adi_hip_context *ctx, const adi_hip_full_attention *L, 
     launch(ctx, "attention_combine", k_attention_combine, dim3(kQueryHeads, rows), dim3(kHeadSize),
            0, static_cast<const float *>(partial), splits, static_cast<const float *>(query_gate),
            attended);
-    forward(ctx, adi_hip_ne_matmul(ctx, &L->output, attended, rows, outputs));
+    project_output(ctx, &L->output, attended, rows, outputs, norm_tail);
 }
 
 // linear_attention_forward_batch (src/executor.cpp:733-966) for one decode
@@ -853,7 +885,8 @@ void full_attention_rows(adi_hip_context *ctx, const adi_hip_full_attention *L, 
 // batched, convolution and recurrence per sequence.
 void linear_attention_rows(adi_hip_context *ctx, const adi_hip_linear_attention *L, uint32_t rows,
                            const float *inputs, float *outputs,
-                           const adi_hip_layer_state *const *states) {
+                           const adi_hip_layer_state *const *states,
+                           const NeNormIn *norm_in, const NeNormTail *norm_tail) {
     require(L != nullptr && inputs != nullptr && outputs != nullptr && states != nullptr &&
                 rows > 0,
             "linear attention batch shape mismatch");
@@ -887,9 +920,9 @@ void linear_attention_rows(adi_hip_context *ctx, const adi_hip_linear_attention 
     float *normalized = ws.take<float>(n * kValueSize);
     float *alpha = ws.take<float>(n * kValueHeads);
     float *beta = ws.take<float>(n * kValueHeads);
-    project_qkv_gate(ctx, L, inputs, rows, qkv, gate);
-    forward(ctx, adi_hip_bf16_matmul(ctx, &L->alpha, inputs, rows, alpha));
-    forward(ctx, adi_hip_bf16_matmul(ctx, &L->beta, inputs, rows, beta));
+    project_qkv_gate(ctx, L, inputs, rows, qkv, gate, norm_in);
+    const float *x = norm_in != nullptr ? norm_in->out : inputs;  // the normalized rows
+    project_decay(ctx, L, x, rows, alpha, beta);
     for (uint32_t first = 0; first < rows; first += kRowGroup) {
         const uint32_t count = rows - first < kRowGroup ? rows - first : kRowGroup;
         LinearRows table{};
@@ -911,7 +944,7 @@ void linear_attention_rows(adi_hip_context *ctx, const adi_hip_linear_attention 
     launch(ctx, "linear_norm_gate", k_linear_norm_gate, dim3(kValueHeads, rows), dim3(kLinearHead),
            0, static_cast<const float *>(recurrent_output), L->norm,
            static_cast<const float *>(gate), normalized);
-    forward(ctx, adi_hip_ne_matmul(ctx, &L->output, normalized, rows, outputs));
+    project_output(ctx, &L->output, normalized, rows, outputs, norm_tail);
 }
 
 }  // namespace
@@ -921,12 +954,13 @@ void decoder_rows(adi_hip_context *ctx, const adi_hip_decoder_layer *L, uint32_t
                   const adi_hip_layer_state *const *states, const uint32_t *positions,
                   const uint32_t *device_positions, uint32_t span) {
     require(states != nullptr && positions != nullptr, "decoder batch shape mismatch");
-    layer_body(ctx, L, rows, hidden, pending, moe_out, [&](const float *in, float *out) {
+    layer_body(ctx, L, rows, hidden, pending, moe_out,
+               [&](const float *in, float *out, const NeNormIn *norm_in, const NeNormTail *norm_tail) {
         if (L->full_attention != 0) {
             full_attention_rows(ctx, &L->full, rows, in, out, states, positions, device_positions,
-                                span);
+                                span, norm_in, norm_tail);
         } else {
-            linear_attention_rows(ctx, &L->linear, rows, in, out, states);
+            linear_attention_rows(ctx, &L->linear, rows, in, out, states, norm_in, norm_tail);
         }
     });
 }

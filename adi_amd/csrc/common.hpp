@@ -186,6 +186,66 @@ __device__ __forceinline__ float lane_xor(float v) {
     return __uint_as_float(lane_xor_bits<MASK>(__float_as_uint(v)));
 }
 
+// rms_norm of one row of up to 2048 values (src/kernels.cpp:1052-1073) by
+// threads tid 0..255 of a block; threads from 256 take part in the two block
+// barriers only. Thread t holds values t + 256 k (k < 8): value(i) gives them
+// (the row, or the row plus a residual), keep(i, v) sees each once (to write
+// the sum back), and the sum of squares runs in k order, then over the lanes
+// (xor 1 .. 32) and the four waves ((0 + 1) + (2 + 3)); dst[i] = v * scale *
+// (offset + w[i]). wave_sums (4 floats) and scale_shared are LDS. The same
+// values as the rms_norm launch.
+template <typename Value, typename Keep>
+__device__ __forceinline__ void block_rms_norm(Value &&value, Keep &&keep, const uint16_t *weight, uint32_t count,
+                                               float offset, float epsilon, float *dst, float *wave_sums,
+                                               float *scale_shared, uint32_t tid) {
+#pragma clang fp contract(off)
+    constexpr uint32_t kHeld = 8, kThreads = 256;
+    float v[kHeld], w[kHeld];
+    float squares = 0.0f;
+    if (tid < kThreads) {
+#pragma unroll
+        for (uint32_t k = 0; k < kHeld; ++k) {
+            const uint32_t i = tid + k * kThreads;
+            v[k] = i < count ? value(i) : 0.0f;
+            w[k] = i < count ? bf16_bits_to_float(weight[i]) : 0.0f;
+            if (i < count) {
+                keep(i, v[k]);
+            }
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kHeld; ++k) {
+            if (tid + k * kThreads < count) {
+                squares += v[k] * v[k];
+            }
+        }
+        squares += lane_xor<1>(squares);
+        squares += lane_xor<2>(squares);
+        squares += lane_xor<4>(squares);
+        squares += lane_xor<8>(squares);
+        squares += lane_xor<16>(squares);
+        squares += lane_xor<32>(squares);
+        if ((tid & 63u) == 0) {
+            wave_sums[tid >> 6] = squares;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const float total = (wave_sums[0] + wave_sums[1]) + (wave_sums[2] + wave_sums[3]);
+        *scale_shared = 1.0f / sqrtf(total / static_cast<float>(count) + epsilon);
+    }
+    __syncthreads();
+    if (tid < kThreads) {
+        const float scale = *scale_shared;
+#pragma unroll
+        for (uint32_t k = 0; k < kHeld; ++k) {
+            const uint32_t i = tid + k * kThreads;
+            if (i < count) {
+                dst[i] = v[k] * scale * (offset + w[k]);
+            }
+        }
+    }
+}
+
 // Value of the next lane of the lane's quad (lane 3 of a quad reads lane 0):
 // a DPP quad permute [1, 2, 3, 0].
 __device__ __forceinline__ uint32_t quad_next(uint32_t v) {

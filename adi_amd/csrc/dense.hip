@@ -137,7 +137,7 @@ __device__ __forceinline__ void bf16_chains(const uint16_t *wr, const float *xs,
 // loads in flight) matter more than occupancy.
 template <int LANES, bool FUSED, uint32_t XB>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_bf16_lds(
-    const uint16_t *__restrict__ w, uint32_t rows, const uint16_t *__restrict__ w_extra,
+    const uint16_t *__restrict__ w, uint32_t rows, const uint16_t *__restrict__ w_extra, uint32_t extra_rows,
     uint32_t columns, const float *__restrict__ x, uint32_t batch, float *__restrict__ out,
     float *__restrict__ out_extra) {
 #pragma clang fp contract(off)
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
     const uint32_t t0 = blockIdx.y * kTokensPerThread;
     const uint32_t tokens = batch - t0 < kTokensPerThread ? batch - t0 : kTokensPerThread;
     uint16_t *ws = reinterpret_cast<uint16_t *>(xs + static_cast<size_t>(kTokensPerThread) * columns);
-    const uint32_t total_rows = rows + (w_extra != nullptr ? 1u : 0u);
+    const uint32_t total_rows = rows + (w_extra != nullptr ? extra_rows : 0u);
     const uint32_t row0 = blockIdx.x * rows_per_block;
     const uint32_t rows_here =
         total_rows - row0 < rows_per_block ? total_rows - row0 : rows_per_block;
@@ -180,7 +180,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
                 wat[u] = min(wf0 + u * 64u + threadIdx.x, w_total - 1u);
                 const uint32_t r = wat[u] / w_per_row, k = wat[u] - r * w_per_row;
                 const uint32_t row = row0 + r;
-                const uint16_t *src = row < rows ? w + static_cast<size_t>(row) * columns : w_extra;
+                const uint16_t *src = row < rows ? w + static_cast<size_t>(row) * columns
+                                                 : w_extra + static_cast<size_t>(row - rows) * columns;
                 wv[u] = reinterpret_cast<const uint4 *>(src)[k];
             }
 #pragma unroll
@@ -206,7 +207,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
         }
         for (uint32_t r = 0; r < rows_here; ++r) {
             const uint32_t row = row0 + r;
-            const uint16_t *src = row < rows ? w + static_cast<size_t>(row) * columns : w_extra;
+            const uint16_t *src = row < rows ? w + static_cast<size_t>(row) * columns
+                                             : w_extra + static_cast<size_t>(row - rows) * columns;
             for (uint32_t k = threadIdx.x; k < columns; k += 64u) {
                 ws[r * columns + k] = src[k];
             }
@@ -251,7 +253,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
     if (row < rows) {
         out[static_cast<size_t>(t0 + lane) * rows + row] = sum;
     } else {
-        out_extra[t0 + lane] = sum;
+        out_extra[static_cast<size_t>(t0 + lane) * extra_rows + (row - rows)] = sum;
     }
 }
 
@@ -480,38 +482,31 @@ __global__ __launch_bounds__(256) void k_rms_norm(
     float *dst = out + static_cast<size_t>(blockIdx.x) * count;
     // up to 8 values a thread: the row and the weights are loaded at once
     // and kept in registers for the output (same sums, same products)
-    constexpr uint32_t kHeld = 8;
-    const bool held = count <= kHeld * blockDim.x;
-    float v[kHeld], w[kHeld];
-    float squares = 0.0f;
-    if (held) {
-#pragma unroll
-        for (uint32_t k = 0; k < kHeld; ++k) {
-            const uint32_t i = threadIdx.x + k * blockDim.x;
-            v[k] = i < count ? row[i] : 0.0f;
-            w[k] = i < count ? bf16_bits_to_float(weight[i]) : 0.0f;
-            if constexpr (ADD) {
-                if (i < count) {
-                    v[k] = v[k] + add[i];
-                    row[i] = v[k];
+    if (count <= 8u * blockDim.x) {
+        block_rms_norm(
+            [&](uint32_t i) {
+                if constexpr (ADD) {
+                    return row[i] + add[i];
+                } else {
+                    return row[i];
                 }
-            }
+            },
+            [&](uint32_t i, float v) {
+                if constexpr (ADD) {
+                    row[i] = v;
+                }
+            },
+            weight, count, offset, epsilon, dst, wave_sums, &scale_shared, threadIdx.x);
+        return;
+    }
+    float squares = 0.0f;
+    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
+        float value = row[i];
+        if constexpr (ADD) {
+            value = value + add[i];
+            row[i] = value;
         }
-#pragma unroll
-        for (uint32_t k = 0; k < kHeld; ++k) {
-            if (threadIdx.x + k * blockDim.x < count) {
-                squares += v[k] * v[k];
-            }
-        }
-    } else {
-        for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
-            float value = row[i];
-            if constexpr (ADD) {
-                value = value + add[i];
-                row[i] = value;
-            }
-            squares += value * value;
-        }
+        squares += value * value;
     }
     squares += lane_xor<1>(squares);
     squares += lane_xor<2>(squares);
@@ -529,16 +524,6 @@ __global__ __launch_bounds__(256) void k_rms_norm(
     }
     __syncthreads();
     const float scale = scale_shared;
-    if (held) {
-#pragma unroll
-        for (uint32_t k = 0; k < kHeld; ++k) {
-            const uint32_t i = threadIdx.x + k * blockDim.x;
-            if (i < count) {
-                dst[i] = v[k] * scale * (offset + w[k]);
-            }
-        }
-        return;
-    }
     for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
         dst[i] = row[i] * scale * (offset + bf16_bits_to_float(weight[i]));
     }
@@ -867,11 +852,11 @@ void launch_bf16_ordered_extra(adi_hip_context *ctx, const uint16_t *w, uint32_t
         if (lanes == 8) {
             launch(ctx, "router", batch == 1 ? k_bf16_lds<8, false, 8> : k_bf16_lds<8, false, 32>,
                    dim3(ceil_div(total, rpb), tokens.x),
-                   dim3(64), lds, w, rows, w_extra, columns, x, batch, out, out_extra);
+                   dim3(64), lds, w, rows, w_extra, 1u, columns, x, batch, out, out_extra);
         } else {
             launch(ctx, "router", batch == 1 ? k_bf16_lds<16, true, 8> : k_bf16_lds<16, true, 32>,
                    dim3(ceil_div(total, rpb), tokens.x),
-                   dim3(64), lds, w, rows, w_extra, columns, x, batch, out, out_extra);
+                   dim3(64), lds, w, rows, w_extra, 1u, columns, x, batch, out, out_extra);
         }
         return;
     }
@@ -879,6 +864,29 @@ void launch_bf16_ordered_extra(adi_hip_context *ctx, const uint16_t *w, uint32_t
         launch_bf16_ordered_plain(ctx, w_extra, 1, columns, x, batch, out_extra, lanes);
     }
     launch_bf16_ordered_plain(ctx, w, rows, columns, x, batch, out, lanes);
+}
+
+void launch_bf16_pair(adi_hip_context *ctx, const uint16_t *w0, uint32_t rows0, const uint16_t *w1,
+                      uint32_t rows1, uint32_t columns, const float *x, uint32_t batch, float *out0,
+                      float *out1, uint32_t lanes) {
+    const uintptr_t addresses = reinterpret_cast<uintptr_t>(w0) | reinterpret_cast<uintptr_t>(w1) |
+                                reinterpret_cast<uintptr_t>(x);
+    const uint32_t rpb = 64 / (lanes == 1 ? 64 : lanes);
+    const size_t lds = size_t(kTokensPerThread) * columns * sizeof(float) + size_t(rpb) * columns * sizeof(uint16_t);
+    if ((lanes == 8 || lanes == 16) && batch < kTiledBatch && lds + 1024 <= 65536 && (addresses & 15u) == 0) {
+        // both matrices' rows in one launch of the small-batch kernel
+        const dim3 grid(ceil_div(rows0 + rows1, rpb), ceil_div(batch, kTokensPerThread));
+        if (lanes == 8) {
+            launch(ctx, "bf16_pair", batch == 1 ? k_bf16_lds<8, false, 8> : k_bf16_lds<8, false, 32>, grid,
+                   dim3(64), lds, w0, rows0, w1, rows1, columns, x, batch, out0, out1);
+        } else {
+            launch(ctx, "bf16_pair", batch == 1 ? k_bf16_lds<16, true, 8> : k_bf16_lds<16, true, 32>, grid,
+                   dim3(64), lds, w0, rows0, w1, rows1, columns, x, batch, out0, out1);
+        }
+        return;
+    }
+    launch_bf16_ordered(ctx, w0, rows0, columns, x, batch, out0, lanes);
+    launch_bf16_ordered(ctx, w1, rows1, columns, x, batch, out1, lanes);
 }
 
 void launch_bf16_ordered_plain(adi_hip_context *ctx, const uint16_t *w, uint32_t rows,

@@ -15,6 +15,12 @@ void launch_bf16_ordered(adi_hip_context *ctx, const uint16_t *w, uint32_t rows,
 void launch_bf16_ordered_extra(adi_hip_context *ctx, const uint16_t *w, uint32_t rows,
                                const uint16_t *w_extra, uint32_t columns, const float *x,
                                uint32_t batch, float *out, float *out_extra, uint32_t lanes);
+// Two bf16 matrices of the same width over the same rows in one launch of the
+// small-batch kernel (each row's chain and sum as launch_bf16_ordered forms
+// them), else one launch each.
+void launch_bf16_pair(adi_hip_context *ctx, const uint16_t *w0, uint32_t rows0, const uint16_t *w1,
+                      uint32_t rows1, uint32_t columns, const float *x, uint32_t batch, float *out0,
+                      float *out1, uint32_t lanes);
 void launch_bf16_ordered_plain(adi_hip_context *ctx, const uint16_t *w, uint32_t rows,
                                uint32_t columns, const float *x, uint32_t batch, float *out,
                                uint32_t lanes);

@@ -24,6 +24,7 @@
 #include "projection.hpp"
 #include "grouped.hpp"
 #include "route.hpp"
+#include "dense.hpp"
 
 namespace adi_hip {
 namespace {
@@ -2618,7 +2619,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_decode_few(MoeDecodeFew a)
 // transform over that half's sums.
 template <int VR>
 __device__ void ne_fused_rows(const NeFusedJob &job, float *ne_lds, const int8_t *sv_lds, uint32_t group,
-                              uint32_t halves, uint32_t batch, uint32_t w8, uint32_t lane) {
+                              uint32_t halves, uint32_t batch, uint32_t w8, uint32_t lane, float *norm_sums,
+                              float *norm_scale) {
     constexpr uint32_t R = 512u * VR, RH = R / 8u;
     // every sum of the half's input rows is in (first touch here, ordinary
     // loads; all the loads first)
@@ -2655,6 +2657,18 @@ __device__ void ne_fused_rows(const NeFusedJob &job, float *ne_lds, const int8_t
             }
         }
     }
+    if constexpr (R <= 2048u) {
+        if (job.tail_row != nullptr) {
+            // the residual add and the next RMS norm of the half's rows
+            for (uint32_t p = group; p < batch; p += halves) {
+                float *row = job.tail_row + static_cast<size_t>(p) * R;
+                const float *y = ne_lds + p * R;
+                block_rms_norm([&](uint32_t e) { return row[e] + y[e] * static_cast<float>(sv_lds[e]); },
+                               [&](uint32_t e, float v) { row[e] = v; }, job.tail_weight, R, 1.0f, 1.0e-6f,
+                               job.tail_out + static_cast<size_t>(p) * R, norm_sums, norm_scale, threadIdx.x);
+            }
+        }
+    }
 }
 
 template <int VC>
@@ -2664,6 +2678,7 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
     __shared__ uint32_t table[1024];
     __shared__ float part[kNeFusedMaxItems][16][kNeFusedRows];  // [item in tile row][row][input row]
     __shared__ uint32_t last;
+    __shared__ float norm_sums[4], norm_scale;  // block_rms_norm's block sums
     __shared__ int8_t sv_lds[kNeFusedMaxRows];  // the output signs, staged by every block for whichever ends last
     constexpr uint32_t C = 512u * VC, CH = C / 8u;
     constexpr uint32_t tile_columns = C / kTile, per_row = tile_columns / 16u;
@@ -2708,6 +2723,32 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
     for (uint32_t i = threadIdx.x; i < R / 4u; i += kNeFusedThreads) {
         reinterpret_cast<uint32_t *>(sv_lds)[i] = reinterpret_cast<const uint32_t *>(job.sv)[i];
     }
+    // with a norm the half's input rows are computed here, into the x_hat
+    // rows' place; the first block of the half writes them out
+    const float *x = a.x;
+    size_t x_stride = C;
+    if constexpr (C == 2048u) {
+        if (a.norm_row != nullptr) {
+            for (uint32_t p = group; p < a.batch; p += halves) {
+                const float *row = a.norm_row + static_cast<size_t>(p) * C;
+                const float *add = a.norm_add != nullptr ? a.norm_add + static_cast<size_t>(p) * C : nullptr;
+                block_rms_norm([&](uint32_t e) { return add != nullptr ? row[e] + add[e] : row[e]; },
+                               [](uint32_t, float) {}, a.norm_weight, C, 1.0f, 1.0e-6f, ne_lds + p * C, norm_sums,
+                               &norm_scale, threadIdx.x);
+            }
+            __syncthreads();
+            if (g == 0) {
+                for (uint32_t p = group; p < a.batch; p += halves) {
+                    for (uint32_t e = threadIdx.x; e < C / 4u; e += kNeFusedThreads) {
+                        reinterpret_cast<float4 *>(a.x_out + static_cast<size_t>(p) * C)[e] =
+                            reinterpret_cast<const float4 *>(ne_lds + p * C)[e];
+                    }
+                }
+                __syncthreads();  // copied before the x_hat rows overwrite them
+            }
+            x = ne_lds;
+        }
+    }
     // x_hat of the half's input rows (their loads first)
     {
         float v[kMine][VC], s[VC];
@@ -2716,7 +2757,7 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
         for (uint32_t i = 0; i < kMine; ++i) {
             const uint32_t p = group + halves * i;
             if (p < a.batch) {
-                load_wave<VC>(a.x + static_cast<size_t>(p) * C + w8 * CH, lane, v[i]);
+                load_wave<VC>(x + static_cast<size_t>(p) * x_stride + w8 * CH, lane, v[i]);
             }
         }
 #pragma unroll
@@ -2814,18 +2855,39 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
         last = coherent_add(ticket, 1u) + 1u == blocks ? 1u : 0u;
     }
     __syncthreads();
-    if (last == 0u) {
-        return;
+    if (last != 0u) {
+        // the last block of the matrix and half: the row transform
+        switch (R) {
+        case 512u: ne_fused_rows<1>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane, norm_sums, &norm_scale); break;
+        case 2048u: ne_fused_rows<4>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane, norm_sums, &norm_scale); break;
+        case 4096u: ne_fused_rows<8>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane, norm_sums, &norm_scale); break;
+        default: ne_fused_rows<16>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane, norm_sums, &norm_scale); break;
+        }
+        if (threadIdx.x == 0) {
+            coherent_store(ticket, 0u);
+        }
     }
-    // the last block of the matrix and half: the row transform
-    switch (R) {
-    case 512u: ne_fused_rows<1>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane); break;
-    case 2048u: ne_fused_rows<4>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane); break;
-    case 4096u: ne_fused_rows<8>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane); break;
-    default: ne_fused_rows<16>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane); break;
-    }
-    if (threadIdx.x == 0) {
-        coherent_store(ticket, 0u);
+    if (a.norm_row != nullptr && a.norm_add != nullptr) {
+        // the residual sum back into the input rows, by the last block
+        // through (every block has read them by then)
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            last = coherent_add(a.ticket + 256u, 1u) + 1u == gridDim.x ? 1u : 0u;
+        }
+        __syncthreads();
+        if (last != 0u) {
+            for (uint32_t p = 0; p < a.batch; ++p) {
+                float4 *row = reinterpret_cast<float4 *>(a.norm_row + static_cast<size_t>(p) * C);
+                const float4 *add = reinterpret_cast<const float4 *>(a.norm_add + static_cast<size_t>(p) * C);
+                for (uint32_t e = threadIdx.x; e < C / 4u; e += kNeFusedThreads) {
+                    const float4 u = row[e], v = add[e];
+                    row[e] = make_float4(u.x + v.x, u.y + v.y, u.z + v.z, u.w + v.w);
+                }
+            }
+            if (threadIdx.x == 0) {
+                coherent_store(a.ticket + 256u, 0u);
+            }
+        }
     }
 }
 
@@ -2834,9 +2896,19 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
 // ---- launchers -------------------------------------------------------------
 
 bool launch_ne_fused(adi_hip_context *ctx, const adi_hip_ne_matrix *const *m, uint32_t count,
-                     const float *inputs, uint32_t batch, float *const *outputs, float *zsum) {
+                     const float *inputs, uint32_t batch, float *const *outputs, float *zsum,
+                     const NeNormIn *in, const NeNormTail *tail) {
     if (batch == 0 || batch > kNeFusedRows || count == 0 || count > kNeFusedJobs || ctx->moe_sync == nullptr ||
-        !aligned_to(inputs, 16) || !aligned_to(zsum, 16)) {
+        !aligned_to(zsum, 16) || (in == nullptr && !aligned_to(inputs, 16))) {
+        return false;
+    }
+    if (in != nullptr && (m[0]->columns != 2048u || in->row == nullptr || in->weight == nullptr ||
+                          in->out == nullptr || !aligned_to(in->row, 16) || !aligned_to(in->add, 16) ||
+                          !aligned_to(in->out, 16))) {
+        return false;
+    }
+    if (tail != nullptr && (m[0]->rows != 2048u || tail->row == nullptr || tail->weight == nullptr ||
+                            tail->out == nullptr)) {
         return false;
     }
     const uint32_t columns = m[0]->columns;
@@ -2857,6 +2929,13 @@ bool launch_ne_fused(adi_hip_context *ctx, const adi_hip_ne_matrix *const *m, ui
     NeFused a{};
     a.jobs = count;
     a.x = inputs;
+    if (in != nullptr) {
+        a.x = nullptr;
+        a.norm_row = in->row;
+        a.norm_add = in->add;
+        a.norm_weight = in->weight;
+        a.x_out = in->out;
+    }
     a.ticket = ctx->moe_sync + kMoeSyncNeTicket;
     a.scale_columns = hadamard_scale(columns);
     a.batch = batch;
@@ -2890,6 +2969,11 @@ bool launch_ne_fused(adi_hip_context *ctx, const adi_hip_ne_matrix *const *m, ui
         job.rows = m[j]->rows;
         job.first_block = first;
         job.blocks = ceil_div(m[j]->rows / kTile, rounds);
+        if (j == 0 && tail != nullptr) {
+            job.tail_row = tail->row;
+            job.tail_weight = tail->weight;
+            job.tail_out = tail->out;
+        }
         first += job.blocks;
         sums += size_t(batch) * m[j]->rows;
     }
@@ -3232,9 +3316,10 @@ void validate_ne(const adi_hip_ne_matrix *m) {
 }
 
 void ne_matmul_group(adi_hip_context *ctx, const adi_hip_ne_matrix *const *m, uint32_t count,
-                     const float *inputs, uint32_t batch, float *const *outputs) {
+                     const float *inputs, uint32_t batch, float *const *outputs, const NeNormIn *in,
+                     const NeNormTail *tail) {
     require(count > 0 && count <= kNeFusedJobs && batch > 0, "Mach NE batch shape mismatch");
-    require(inputs != nullptr, "Mach NE vector is null");
+    require(inputs != nullptr || in != nullptr, "Mach NE vector is null");
     size_t floats = 0;
     for (uint32_t j = 0; j < count; ++j) {
         validate_ne(m[j]);
@@ -3246,15 +3331,22 @@ void ne_matmul_group(adi_hip_context *ctx, const adi_hip_ne_matrix *const *m, ui
         ws.used = 0;
         ws.ensure(Workspace::round(floats * 4));
         float *zsum = ws.take<float>(floats);
-        if (launch_ne_fused(ctx, m, count, inputs, batch, outputs, zsum)) {
+        if (launch_ne_fused(ctx, m, count, inputs, batch, outputs, zsum, in, tail)) {
             return;
         }
+    }
+    if (in != nullptr) {
+        launch_add_rms_norm(ctx, in->row, in->add, in->weight, m[0]->columns, batch, in->out);
+        inputs = in->out;
     }
     for (uint32_t j = 0; j < count; ++j) {
         const int status = adi_hip_ne_matmul(ctx, m[j], inputs, batch, outputs[j]);
         if (status != ADI_HIP_OK) {
             fail(status, ctx->last_error());
         }
+    }
+    if (tail != nullptr) {
+        launch_add_rms_norm(ctx, tail->row, outputs[0], tail->weight, m[0]->rows, batch, tail->out);
     }
 }
 

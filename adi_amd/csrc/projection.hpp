@@ -298,29 +298,61 @@ struct NeFusedJob {
     uint32_t rows;          // 512, 2048, 4096 or 8192
     uint32_t first_block;   // the job's blocks within a half: first_block .. first_block + blocks - 1
     uint32_t blocks;
+    // optional, rows 2048: then tail_row += out and tail_out = rms_norm(tail_row)
+    float *tail_row;        // [batch][rows], or null
+    const uint16_t *tail_weight;
+    float *tail_out;
 };
 struct NeFused {
     NeFusedJob job[kNeFusedJobs];
     uint32_t jobs;
-    const float *x;         // [batch][columns]
-    uint32_t *ticket;       // word 32 * (2 * job + half) per job and half, zero between launches
-                            // (the block that takes a ticket last clears it)
+    const float *x;         // [batch][columns], unless norm_row is set
+    // optional, columns 2048: x = rms_norm(norm_row + norm_add), computed by
+    // every block for its rows; the first block of each half writes them to
+    // x_out, and the last block through writes norm_row + norm_add back
+    float *norm_row;        // [batch][columns], or null
+    const float *norm_add;  // or null (then norm_row is left as it is)
+    const uint16_t *norm_weight;
+    float *x_out;
+    uint32_t *ticket;       // word 32 * (2 * job + half) per job and half, and word 256 for the
+                            // whole grid; zero between launches (the block that takes one last clears it)
     float scale_columns;
     uint32_t batch;
     uint32_t halves;        // 1, or 2 when the grid splits the input rows in two
 };
+// A decoder layer's RMS norms (weight offset 1, epsilon 1e-6, src/kernels.cpp:
+// 1052-1073) folded into its projections. NeNormIn: the projections' input is
+// rms_norm(row + add), with row += add written back (add may be null) and
+// the normalized rows written to out. NeNormTail: after the projection,
+// row += y and out = rms_norm(row).
+struct NeNormIn {
+    float *row;
+    const float *add;
+    const uint16_t *weight;
+    float *out;
+};
+struct NeNormTail {
+    float *row;
+    const uint16_t *weight;
+    float *out;
+};
 // Runs m[0 .. count - 1] on the same `batch` input rows in one launch, output
 // j to outputs[j]; false (nothing launched) when a shape is not one the kernel
 // is built for (columns 2048 or 4096, the same for all; rows 512, 2048, 4096
-// or 8192; at most kNeFusedRows input rows and kNeFusedJobs matrices).
-// `zsum` holds batch x (the sum of the rows) floats.
+// or 8192; at most kNeFusedRows input rows and kNeFusedJobs matrices; 2048
+// columns with `in`, 2048 rows of matrix 0 with `tail`). With `in` the
+// inputs are its normalized rows (`inputs` unused); `tail` applies to
+// matrix 0. `zsum` holds batch x (the sum of the rows) floats.
 bool launch_ne_fused(adi_hip_context *ctx, const adi_hip_ne_matrix *const *m, uint32_t count,
-                     const float *inputs, uint32_t batch, float *const *outputs, float *zsum);
-// NE projections of the same input rows, outputs[j] = m[j] x inputs: one
-// launch for a few rows where launch_ne_fused takes the shapes, else one
-// adi_hip_ne_matmul each. Throws on a rejected call.
+                     const float *inputs, uint32_t batch, float *const *outputs, float *zsum,
+                     const NeNormIn *in = nullptr, const NeNormTail *tail = nullptr);
+// NE projections of the same input rows, outputs[j] = m[j] x inputs (or x
+// the normalized rows of `in`), then `tail` on matrix 0's outputs: one
+// launch for a few rows where launch_ne_fused takes the shapes, else the
+// norm launches and one adi_hip_ne_matmul each. Throws on a rejected call.
 void ne_matmul_group(adi_hip_context *ctx, const adi_hip_ne_matrix *const *m, uint32_t count,
-                     const float *inputs, uint32_t batch, float *const *outputs);
+                     const float *inputs, uint32_t batch, float *const *outputs,
+                     const NeNormIn *in = nullptr, const NeNormTail *tail = nullptr);
 // Whether `m` (a down projection of one row) can build its x_hat from
 // m.swiglu in the launch: one expert entry of width 512 and at most one
 // expert item per wave.

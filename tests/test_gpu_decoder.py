@@ -79,3 +79,46 @@ def test_decode_layer_rejections(gpu, stack):
     with pytest.raises(hip.HipError, match="full attention state or input shape mismatch"):
         hip.decode_layer(gpu, full, 2, hidden, state)  # position past the cache
     torch.cuda.synchronize()
+
+
+@pytest.fixture(scope="module")
+def wide_layers(gpu):
+    """A Gated DeltaNet and a full-attention layer of the 40-layer stack's
+    geometry (hidden 2048, 256 experts)."""
+    g = syn.StackGeometry()
+    etlut, ntlut = syn.stack_codebooks()
+    ebook, nbook = gpu.expert_codebook(etlut), gpu.ne_codebook(ntlut)
+    return [hip.upload_decoder_layer(gpu, syn.stack_layer(g, i, etlut, ntlut), ebook, nbook)
+            for i in (0, 3)]
+
+
+@pytest.mark.parametrize("count", [1, 2, 4])
+def test_layer_norms_folded_equal_separate_launches(gpu, wide_layers, count):
+    """At hidden 2048 a layer of 1-4 tokens runs its input RMS norm (with the
+    residual add) inside its first attention projection launch, the
+    post-attention norm inside its output projection launch, and the Gated
+    DeltaNet's alpha and beta matmuls as one launch; with the one-launch
+    paths off they are launches of their own. Hidden rows and every state
+    are bit-identical over three steps of both layers."""
+    rng = syn.rng_for(51, count)
+    x0 = syn.hidden_states(rng, count, 2048)
+
+    def run(fused):
+        gpu.set_fused_decode(fused)
+        try:
+            hidden = gpu.to_device(x0.copy())
+            states = [hip.layer_state(i == 1, 3 * count) for i in range(2)]
+            for step in range(3):
+                for layer, (state, _) in zip(wide_layers, states):
+                    if count == 1:
+                        hip.decode_layer(gpu, layer, step, hidden, state)
+                    else:
+                        hip.prefill_layer(gpu, layer, step * count, count, hidden, state)
+            gpu.synchronize()
+            return [hidden.cpu().numpy()] + [t.cpu().numpy() for _, keep in states for t in keep]
+        finally:
+            gpu.set_fused_decode(True)
+
+    one, separate = run(True), run(False)
+    for i, (a, b) in enumerate(zip(one, separate)):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), i
