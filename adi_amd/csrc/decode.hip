@@ -184,7 +184,17 @@ constexpr uint32_t kArgmaxSplitCount = 32768;  // shorter rows take one block
 
 __global__ __launch_bounds__(kArgmaxPartThreads) void k_argmax_parts(
     const float *logits, uint32_t count, uint32_t span, float *part_value,
-    uint32_t *part_index) {
+    uint32_t *part_index, uint32_t *zero, uint32_t zero_words, uint32_t zero_stride) {
+    if (zero != nullptr) {
+        // the sampler's per-row bins and state (the first zero_words of each
+        // row's zero_stride), cleared for the launches after
+        const uint32_t share = (zero_words + gridDim.x - 1u) / gridDim.x;
+        uint32_t *words = zero + static_cast<size_t>(blockIdx.y) * zero_stride;
+        const uint32_t w0 = blockIdx.x * share, w1 = w0 + share < zero_words ? w0 + share : zero_words;
+        for (uint32_t w = w0 + threadIdx.x; w < w1; w += blockDim.x) {
+            words[w] = 0u;
+        }
+    }
     const uint32_t begin = blockIdx.x * span;
     const uint32_t end = begin + span < count ? begin + span : count;
     const float *row = logits + static_cast<size_t>(blockIdx.y) * count + begin;
@@ -249,7 +259,7 @@ void launch_argmax(adi_hip_context *ctx, const float *logits, uint32_t rows, uin
     float *part_value = ws.take<float>(size_t(rows) * parts);
     uint32_t *part_index = ws.take<uint32_t>(size_t(rows) * parts);
     launch(ctx, "argmax_parts", k_argmax_parts, dim3(parts, rows), dim3(kArgmaxPartThreads), 0,
-           logits, count, span, part_value, part_index);
+           logits, count, span, part_value, part_index, static_cast<uint32_t *>(nullptr), 0u, 0u);
     launch(ctx, "argmax_finish", k_argmax_finish, dim3(rows), dim3(kWave), 0,
            static_cast<const float *>(part_value), static_cast<const uint32_t *>(part_index),
            parts, tokens);
@@ -260,6 +270,15 @@ void launch_argmax(adi_hip_context *ctx, const float *logits, uint32_t rows, uin
 constexpr uint32_t kSampleThreads = 1024;
 constexpr uint32_t kSampleWaves = kSampleThreads / kWave;
 constexpr uint32_t kWindow = 4096;  // candidates sorted and walked at a time
+
+// The sampler's words of a long row (after the span maxima and sums): token
+// counts and float masses p of 4096 bins of the descending key's top 12 bits,
+// the state of the short walk, then up to kWindow candidates (key, index).
+constexpr uint32_t kTopBins = 4096, kTopShift = 20;
+constexpr uint32_t kTopState = 2 * kTopBins;      // appended, expected, decided
+constexpr uint32_t kTopCand = kTopState + 8;      // 8-byte aligned
+constexpr uint32_t kTopRowWords = kTopCand + 2 * kWindow;
+constexpr uint32_t kTopZeroWords = kTopState + 4;  // cleared before a call
 
 // Ascending order of this key is descending logit order, with -0 folded into
 // +0 (src/generation.cpp:36-47); ties keep ascending token order.
@@ -277,8 +296,11 @@ __device__ __forceinline__ uint32_t descending_key(float v) {
 // sampler rejects it.
 __global__ __launch_bounds__(kArgmaxPartThreads) void k_expsum_parts(
     const float *logits, uint32_t count, uint32_t span, const float *part_value,
-    const uint32_t *part_index, float temperature, double *part_sum) {
+    const uint32_t *part_index, float temperature, double *part_sum, uint32_t *top) {
     __shared__ double wave_sum[kArgmaxPartThreads / kWave];
+    // with `top`: the span's bin counts and masses, added into the row's
+    __shared__ uint32_t bin_count[kTopBins];
+    __shared__ float bin_mass[kTopBins];
     const size_t base = static_cast<size_t>(blockIdx.y) * gridDim.x;
     float m = -__builtin_huge_valf();
     uint32_t bad = 0;
@@ -298,10 +320,34 @@ __global__ __launch_bounds__(kArgmaxPartThreads) void k_expsum_parts(
     const uint32_t begin = blockIdx.x * span;
     const uint32_t end = begin + span < count ? begin + span : count;
     const float *row = logits + static_cast<size_t>(blockIdx.y) * count + begin;
+    if (top != nullptr) {
+        for (uint32_t b = threadIdx.x; b < kTopBins; b += blockDim.x) {
+            bin_count[b] = 0u;
+            bin_mass[b] = 0.0f;
+        }
+        __syncthreads();
+    }
     double part = 0.0;
     for_each_logit(row, end - begin, [&](uint32_t, float v) {
-        part += exp((static_cast<double>(v) - maximum) / t);
+        const double p = exp((static_cast<double>(v) - maximum) / t);
+        part += p;
+        if (top != nullptr) {
+            const uint32_t bin = descending_key(v) >> kTopShift;
+            atomicAdd(&bin_count[bin], 1u);
+            atomicAdd(&bin_mass[bin], static_cast<float>(p));
+        }
     });
+    if (top != nullptr) {
+        __syncthreads();
+        uint32_t *counts = top + static_cast<size_t>(blockIdx.y) * kTopRowWords;
+        float *masses = reinterpret_cast<float *>(counts + kTopBins);
+        for (uint32_t b = threadIdx.x; b < kTopBins; b += blockDim.x) {
+            if (bin_count[b] != 0u) {
+                atomicAdd(&counts[b], bin_count[b]);
+                atomicAdd(&masses[b], bin_mass[b]);
+            }
+        }
+    }
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1) {
         part += __shfl_xor(part, offset);
@@ -458,7 +504,11 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_rows(const float *log
                                                                 uint32_t *tokens, uint32_t parts,
                                                                 const float *part_value,
                                                                 const uint32_t *part_index,
-                                                                const double *part_sum) {
+                                                                const double *part_sum,
+                                                                const uint32_t *top) {
+    if (top != nullptr && top[static_cast<size_t>(blockIdx.x) * kTopRowWords + kTopState + 2] != 0u) {
+        return;  // the short walk chose this row's token
+    }
     __shared__ uint64_t cand[kWindow];
     __shared__ double prob[kWindow];
     __shared__ uint32_t hist[256];
@@ -635,6 +685,195 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_rows(const float *log
     }
 }
 
+// The short walk of a long row, first step: the prefix of the sorted order
+// (ascending key: descending logit, then ascending index) up to the first
+// bin whose inclusive mass reaches top_p of the row's sum, by a 0.1% margin
+// over the bins' float masses, when it holds at most kWindow tokens. Every
+// block (p, r) finds the same cut from the row's bins and appends its span's
+// tokens before it; block (0, r) records how many the prefix holds. A row
+// with a non-finite logit, or whose cut is out of reach, is left to the
+// full sampler.
+__global__ __launch_bounds__(kArgmaxPartThreads) void k_top_collect(const float *logits, uint32_t count,
+                                                                    uint32_t span, const uint32_t *part_index,
+                                                                    const double *part_sum, float top_p,
+                                                                    uint32_t *top) {
+    constexpr uint32_t kPer = kTopBins / kArgmaxPartThreads;
+    __shared__ uint32_t scan_count[kArgmaxPartThreads];
+    __shared__ double scan_mass[kArgmaxPartThreads];
+    __shared__ uint32_t cut, cut_count;
+    const uint32_t t = threadIdx.x;
+    const size_t base = static_cast<size_t>(blockIdx.y) * gridDim.x;
+    uint32_t bad = 0;
+    double denominator = 0.0;
+    for (uint32_t p = 0; p < gridDim.x; ++p) {
+        bad |= part_index[base + p] == 0xFFFFFFFFu ? 1u : 0u;
+        denominator += part_sum[base + p];
+    }
+    if (bad != 0u) {
+        return;
+    }
+    uint32_t *words = top + static_cast<size_t>(blockIdx.y) * kTopRowWords;
+    const float *masses = reinterpret_cast<const float *>(words + kTopBins);
+    uint32_t c[kPer], own_count = 0;
+    double mass[kPer], own_mass = 0.0;
+#pragma unroll
+    for (uint32_t j = 0; j < kPer; ++j) {
+        c[j] = words[kPer * t + j];
+        mass[j] = static_cast<double>(masses[kPer * t + j]);
+        own_count += c[j];
+        own_mass += mass[j];
+    }
+    scan_count[t] = own_count;
+    scan_mass[t] = own_mass;
+    if (t == 0) {
+        cut = 0xFFFFFFFFu;
+    }
+    __syncthreads();
+    for (uint32_t d = 1; d < kArgmaxPartThreads; d <<= 1) {
+        const uint32_t a = t >= d ? scan_count[t - d] : 0u;
+        const double m = t >= d ? scan_mass[t - d] : 0.0;
+        __syncthreads();
+        scan_count[t] += a;
+        scan_mass[t] += m;
+        __syncthreads();
+    }
+    const double target = static_cast<double>(top_p) * denominator * 1.001;
+    double reached = scan_mass[t] - own_mass;
+    for (uint32_t j = 0; j < kPer; ++j) {
+        reached += mass[j];
+        if (reached >= target) {
+            atomicMin(&cut, kPer * t + j);
+            break;
+        }
+    }
+    __syncthreads();
+    const uint32_t b_cut = cut;
+    if (b_cut / kPer == t) {
+        uint32_t inclusive = scan_count[t] - own_count;
+        for (uint32_t j = 0; j <= b_cut % kPer; ++j) {
+            inclusive += c[j];
+        }
+        cut_count = inclusive;
+    }
+    __syncthreads();
+    if (b_cut == 0xFFFFFFFFu || cut_count > kWindow) {
+        return;
+    }
+    if (blockIdx.x == 0 && t == 0) {
+        words[kTopState + 1] = cut_count;
+    }
+    uint64_t *cand = reinterpret_cast<uint64_t *>(words + kTopCand);
+    const uint32_t begin = blockIdx.x * span;
+    const uint32_t end = begin + span < count ? begin + span : count;
+    const float *row = logits + static_cast<size_t>(blockIdx.y) * count + begin;
+    for_each_logit(row, end - begin, [&](uint32_t i, float v) {
+        const uint32_t key = descending_key(v);
+        if ((key >> kTopShift) <= b_cut) {
+            const uint32_t at = atomicAdd(&words[kTopState], 1u);
+            cand[at] = (static_cast<uint64_t>(key) << 32) | (begin + i);
+        }
+    });
+}
+
+// The short walk, second step (one block per row, src/generation.cpp:
+// 184-225): the prefix sorted, its p, and the reference's two walks over it
+// on one thread, as k_sample_rows walks its first window. When the kept set
+// ends inside the prefix the row's token is chosen here; otherwise the row
+// is left to the full sampler.
+__global__ __launch_bounds__(kArgmaxPartThreads) void k_top_walk(const float *logits, uint32_t count,
+                                                                 float temperature, float top_p,
+                                                                 const uint64_t *words, uint32_t *tokens,
+                                                                 uint32_t parts, const float *part_value,
+                                                                 const double *part_sum, uint32_t *top) {
+    __shared__ uint64_t cand[kWindow];
+    __shared__ double prob[kWindow];
+    uint32_t *state = top + static_cast<size_t>(blockIdx.x) * kTopRowWords;
+    const uint32_t n = state[kTopState + 1];
+    if (n == 0u) {
+        return;
+    }
+    const float *row = logits + static_cast<size_t>(blockIdx.x) * count;
+    const size_t base = static_cast<size_t>(blockIdx.x) * parts;
+    float m = -__builtin_huge_valf();
+    double denominator = 0.0;
+    for (uint32_t p = 0; p < parts; ++p) {
+        const float v = part_value[base + p];
+        m = v > m ? v : m;
+        denominator += part_sum[base + p];
+    }
+    const double maximum = static_cast<double>(m);
+    const double t = static_cast<double>(temperature);
+    uint32_t size = 1;
+    while (size < n) {
+        size <<= 1;
+    }
+    const uint64_t *src = reinterpret_cast<const uint64_t *>(state + kTopCand);
+    for (uint32_t k = threadIdx.x; k < size; k += blockDim.x) {
+        cand[k] = k < n ? src[k] : ~0ull;
+    }
+    // bitonic sort, ascending
+    for (uint32_t width = 2; width <= size; width <<= 1) {
+        for (uint32_t stride = width >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            for (uint32_t i = threadIdx.x; i < size; i += blockDim.x) {
+                const uint32_t j = i ^ stride;
+                if (j > i) {
+                    const uint64_t a = cand[i], b = cand[j];
+                    const bool up = (i & width) == 0u;
+                    if ((a > b) == up) {
+                        cand[i] = b;
+                        cand[j] = a;
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
+        const float logit = row[static_cast<uint32_t>(cand[k])];
+        prob[k] = exp((static_cast<double>(logit) - maximum) / t);
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) {
+        return;
+    }
+    // phase 1: the kept prefix and the sum of its p
+    double cumulative = 0.0, kept = 0.0;
+    uint32_t k = 0;
+    for (; k < n; ++k) {
+        cumulative += prob[k] / denominator;
+        kept += prob[k];
+        if (cumulative >= static_cast<double>(top_p)) {
+            break;
+        }
+    }
+    if (k == n) {
+        return;  // the kept set reaches past the prefix
+    }
+    const uint64_t last = cand[k];
+    // the draw, as k_sample_rows takes it
+    double u = static_cast<double>(words[blockIdx.x]) * 0x1p-64;
+    if (u >= 1.0) {
+        u = 0x1.fffffffffffffp-1;
+    }
+    const double target = u * kept;
+    // phase 2: the running p from the first token until it reaches target
+    double running = 0.0;
+    uint32_t token = static_cast<uint32_t>(last);
+    for (uint32_t j = 0; j <= k; ++j) {
+        running += prob[j];
+        if (target <= running) {
+            token = static_cast<uint32_t>(cand[j]);
+            break;
+        }
+        if (cand[j] == last) {
+            break;
+        }
+    }
+    tokens[blockIdx.x] = token;
+    state[kTopState + 2] = 1u;
+}
+
 }  // namespace
 }  // namespace adi_hip
 
@@ -700,7 +939,7 @@ int adi_hip_sample_rows(adi_hip_context *ctx, const float *logits, uint32_t rows
             launch(ctx, "sample", k_sample_rows, dim3(rows), dim3(kSampleThreads), 0, logits,
                    count, temperature, top_p, words, tokens, 0u,
                    static_cast<const float *>(nullptr), static_cast<const uint32_t *>(nullptr),
-                   static_cast<const double *>(nullptr));
+                   static_cast<const double *>(nullptr), static_cast<const uint32_t *>(nullptr));
             return;
         }
         // long rows: the maximum and the denominator over up to 64 blocks a row
@@ -710,18 +949,28 @@ int adi_hip_sample_rows(adi_hip_context *ctx, const float *logits, uint32_t rows
         auto &ws = ctx->workspace;
         ws.used = 0;
         ws.ensure(Workspace::round(size_t(rows) * parts * 4) * 2 +
-                  Workspace::round(size_t(rows) * parts * 8));
+                  Workspace::round(size_t(rows) * parts * 8) + Workspace::round(size_t(rows) * kTopRowWords * 4));
         float *part_value = ws.take<float>(size_t(rows) * parts);
         uint32_t *part_index = ws.take<uint32_t>(size_t(rows) * parts);
         double *part_sum = ws.take<double>(size_t(rows) * parts);
+        uint32_t *top = ws.take<uint32_t>(size_t(rows) * kTopRowWords);
         launch(ctx, "argmax_parts", k_argmax_parts, dim3(parts, rows), dim3(kArgmaxPartThreads), 0,
-               logits, count, span, part_value, part_index);
+               logits, count, span, part_value, part_index, top, kTopZeroWords, kTopRowWords);
         launch(ctx, "expsum_parts", k_expsum_parts, dim3(parts, rows), dim3(kArgmaxPartThreads), 0,
                logits, count, span, static_cast<const float *>(part_value),
-               static_cast<const uint32_t *>(part_index), temperature, part_sum);
+               static_cast<const uint32_t *>(part_index), temperature, part_sum, top);
+        // the short walk: the kept set of most rows ends in a short prefix of
+        // the sorted order; the full sampler then only runs for the rest
+        launch(ctx, "top_collect", k_top_collect, dim3(parts, rows), dim3(kArgmaxPartThreads), 0, logits,
+               count, span, static_cast<const uint32_t *>(part_index), static_cast<const double *>(part_sum),
+               top_p, top);
+        launch(ctx, "top_walk", k_top_walk, dim3(rows), dim3(kArgmaxPartThreads), 0, logits, count, temperature,
+               top_p, words, tokens, parts, static_cast<const float *>(part_value),
+               static_cast<const double *>(part_sum), top);
         launch(ctx, "sample", k_sample_rows, dim3(rows), dim3(kSampleThreads), 0, logits, count,
                temperature, top_p, words, tokens, parts, static_cast<const float *>(part_value),
-               static_cast<const uint32_t *>(part_index), static_cast<const double *>(part_sum));
+               static_cast<const uint32_t *>(part_index), static_cast<const double *>(part_sum),
+               static_cast<const uint32_t *>(top));
     });
 }
 
