@@ -2619,7 +2619,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_decode_few(MoeDecodeFew a)
 // transform over that half's sums.
 template <int VR>
 __device__ void ne_fused_rows(const NeFusedJob &job, float *ne_lds, const int8_t *sv_lds, uint32_t group,
-                              uint32_t halves, uint32_t batch, uint32_t w8, uint32_t lane, float *norm_sums,
+                              uint32_t halves, uint32_t batch, uint32_t w8, uint32_t lane, float (*norm_sums)[4],
                               float *norm_scale) {
     constexpr uint32_t R = 512u * VR, RH = R / 8u;
     // every sum of the half's input rows is in (first touch here, ordinary
@@ -2659,13 +2659,19 @@ __device__ void ne_fused_rows(const NeFusedJob &job, float *ne_lds, const int8_t
     }
     if constexpr (R <= 2048u) {
         if (job.tail_row != nullptr) {
-            // the residual add and the next RMS norm of the half's rows
-            for (uint32_t p = group; p < batch; p += halves) {
-                float *row = job.tail_row + static_cast<size_t>(p) * R;
-                const float *y = ne_lds + p * R;
+            // the residual add and the next RMS norm of the half's rows, two
+            // at a time (one on each 256-thread half of the block)
+            const uint32_t pair = threadIdx.x >> 8;
+            for (uint32_t i0 = 0; group + halves * i0 < batch; i0 += 2u) {
+                const uint32_t p = group + halves * (i0 + pair);
+                const bool live = p < batch;
+                const uint32_t q = live ? p : group;
+                float *row = job.tail_row + static_cast<size_t>(q) * R;
+                const float *y = ne_lds + q * R;
                 block_rms_norm([&](uint32_t e) { return row[e] + y[e] * static_cast<float>(sv_lds[e]); },
                                [&](uint32_t e, float v) { row[e] = v; }, job.tail_weight, R, 1.0f, 1.0e-6f,
-                               job.tail_out + static_cast<size_t>(p) * R, norm_sums, norm_scale, threadIdx.x);
+                               job.tail_out + static_cast<size_t>(q) * R, norm_sums[pair], &norm_scale[pair],
+                               live ? threadIdx.x & 255u : 256u);
             }
         }
     }
@@ -2678,7 +2684,7 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
     __shared__ uint32_t table[1024];
     __shared__ float part[kNeFusedMaxItems][16][kNeFusedRows];  // [item in tile row][row][input row]
     __shared__ uint32_t last;
-    __shared__ float norm_sums[4], norm_scale;  // block_rms_norm's block sums
+    __shared__ float norm_sums[2][4], norm_scale[2];  // block_rms_norm's block sums, two rows at a time
     __shared__ int8_t sv_lds[kNeFusedMaxRows];  // the output signs, staged by every block for whichever ends last
     constexpr uint32_t C = 512u * VC, CH = C / 8u;
     constexpr uint32_t tile_columns = C / kTile, per_row = tile_columns / 16u;
@@ -2729,12 +2735,17 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
     size_t x_stride = C;
     if constexpr (C == 2048u) {
         if (a.norm_row != nullptr) {
-            for (uint32_t p = group; p < a.batch; p += halves) {
-                const float *row = a.norm_row + static_cast<size_t>(p) * C;
-                const float *add = a.norm_add != nullptr ? a.norm_add + static_cast<size_t>(p) * C : nullptr;
+            // two rows at a time, one on each 256-thread half of the block
+            const uint32_t pair = threadIdx.x >> 8;
+            for (uint32_t i0 = 0; group + halves * i0 < a.batch; i0 += 2u) {
+                const uint32_t p = group + halves * (i0 + pair);
+                const bool live = p < a.batch;
+                const uint32_t q = live ? p : group;  // a row in range for the idle half's pointers
+                const float *row = a.norm_row + static_cast<size_t>(q) * C;
+                const float *add = a.norm_add != nullptr ? a.norm_add + static_cast<size_t>(q) * C : nullptr;
                 block_rms_norm([&](uint32_t e) { return add != nullptr ? row[e] + add[e] : row[e]; },
-                               [](uint32_t, float) {}, a.norm_weight, C, 1.0f, 1.0e-6f, ne_lds + p * C, norm_sums,
-                               &norm_scale, threadIdx.x);
+                               [](uint32_t, float) {}, a.norm_weight, C, 1.0f, 1.0e-6f, ne_lds + q * C,
+                               norm_sums[pair], &norm_scale[pair], live ? threadIdx.x & 255u : 256u);
             }
             __syncthreads();
             if (g == 0) {
@@ -2858,10 +2869,10 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
     if (last != 0u) {
         // the last block of the matrix and half: the row transform
         switch (R) {
-        case 512u: ne_fused_rows<1>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane, norm_sums, &norm_scale); break;
-        case 2048u: ne_fused_rows<4>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane, norm_sums, &norm_scale); break;
-        case 4096u: ne_fused_rows<8>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane, norm_sums, &norm_scale); break;
-        default: ne_fused_rows<16>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane, norm_sums, &norm_scale); break;
+        case 512u: ne_fused_rows<1>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane, norm_sums, norm_scale); break;
+        case 2048u: ne_fused_rows<4>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane, norm_sums, norm_scale); break;
+        case 4096u: ne_fused_rows<8>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane, norm_sums, norm_scale); break;
+        default: ne_fused_rows<16>(job, ne_lds, sv_lds, group, halves, a.batch, w8, lane, norm_sums, norm_scale); break;
         }
         if (threadIdx.x == 0) {
             coherent_store(ticket, 0u);
