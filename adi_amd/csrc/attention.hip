@@ -72,6 +72,35 @@ __host__ __device__ __forceinline__ uint32_t row_splits(uint32_t tokens, uint32_
     return s < 1u ? 1u : (s > cap ? cap : s);
 }
 
+// Blocks of the flash-decoding partial kernels (block b runs on XCD b % 8).
+// Under kPairSplits splits block b is query head b % 16 of split b / 16: all
+// splits of a head on one XCD, whose L2 then still holds them for the
+// combine. From kPairSplits splits the history is long and the eight query
+// heads of a KV head, which read the same cache entries, are dealt to one
+// XCD instead, so the entries pass through that XCD's L2 once rather than
+// once per XCD: block b (k = b / 8) takes pair g = 8 (k / 8) + b % 8,
+// g = kKvHeads split + kv, and query head 8 kv + k % 8; the grid of
+// partial_blocks(splits) covers every pair, and blocks of pairs past the
+// last split return at once.
+static_assert(kQueryHeads == 8 * kKvHeads, "eight query heads to a KV head");
+constexpr uint32_t kPairSplits = 32;
+__host__ __device__ __forceinline__ uint32_t partial_blocks(uint32_t splits) {
+    return splits < kPairSplits ? kQueryHeads * splits : (kKvHeads * splits + 7u) / 8u * 64u;
+}
+struct PartialBlock {
+    uint32_t head, split;
+    bool live;
+};
+__device__ __forceinline__ PartialBlock partial_block(uint32_t b, uint32_t splits) {
+    if (splits < kPairSplits) {
+        return {b % kQueryHeads, b / kQueryHeads, true};
+    }
+    const uint32_t k = b >> 3;
+    const uint32_t g = ((k >> 3) << 3) | (b & 7u);
+    const uint32_t kv = g % kKvHeads;
+    return {kv * 8u + (k & 7u), g / kKvHeads, g < kKvHeads * splits};
+}
+
 struct LinearRows {
     float *convolution[kRowGroup];
     float *recurrent[kRowGroup];
@@ -240,11 +269,11 @@ __device__ __forceinline__ void online_step(float score, float4 value, float &ma
 // (maximum -inf and denominator 0 when the split lies past the token).
 __device__ __forceinline__ void attention_partial_span(const float *query_gate, const float *keys,
                                                        const float *values, uint32_t tokens,
-                                                       uint32_t chunk, float *partial) {
+                                                       uint32_t chunk, float *partial, uint32_t h,
+                                                       uint32_t split, uint32_t splits) {
 #pragma clang fp contract(off)
     __shared__ __align__(16) float wave_acc[4][kHeadSize];
     __shared__ float wave_max[4], wave_den[4];
-    const uint32_t h = blockIdx.x, split = blockIdx.y, splits = gridDim.y;
     const uint32_t kv = h / (kQueryHeads / kKvHeads);
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const float4 q = reinterpret_cast<const float4 *>(query_gate + static_cast<size_t>(h) * kQueryStride)[lane];
@@ -253,12 +282,30 @@ __device__ __forceinline__ void attention_partial_span(const float *query_gate, 
     const uint32_t end = begin + chunk < tokens ? begin + chunk : tokens;
     float maximum = -__builtin_huge_valf(), denominator = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (uint32_t t = begin + wave; t < end; t += 4) {
-        const size_t at = (static_cast<size_t>(t) * kKvHeads + kv) * kHeadSize;
-        const float4 k = reinterpret_cast<const float4 *>(keys + at)[lane];
-        const float4 v = reinterpret_cast<const float4 *>(values + at)[lane];
-        const float dot = wave_sum(((q.x * k.x + q.y * k.y) + q.z * k.z) + q.w * k.w);
-        online_step(dot * score_scale, v, maximum, denominator, acc);
+    // the wave's tokens t0, t0 + 4, ... in batches of eight: the batch's
+    // entries are loaded together (a token past the span reloads t0, unused),
+    // its dot products reduced together, then the online updates in order
+    constexpr uint32_t kBatch = 8;
+    for (uint32_t t0 = begin + wave; t0 < end; t0 += 4u * kBatch) {
+        float4 k[kBatch], v[kBatch];
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; ++j) {
+            const uint32_t t = t0 + 4u * j < end ? t0 + 4u * j : t0;
+            const size_t at = (static_cast<size_t>(t) * kKvHeads + kv) * kHeadSize;
+            k[j] = reinterpret_cast<const float4 *>(keys + at)[lane];
+            v[j] = reinterpret_cast<const float4 *>(values + at)[lane];
+        }
+        float dot[kBatch];
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; ++j) {
+            dot[j] = wave_sum(((q.x * k[j].x + q.y * k[j].y) + q.z * k[j].z) + q.w * k[j].w);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; ++j) {
+            if (t0 + 4u * j < end) {
+                online_step(dot[j] * score_scale, v[j], maximum, denominator, acc);
+            }
+        }
     }
     reinterpret_cast<float4 *>(wave_acc[wave])[lane] = acc;
     if (lane == 0) {
@@ -290,11 +337,16 @@ __device__ __forceinline__ void attention_partial_span(const float *query_gate, 
 __global__ __launch_bounds__(256) void k_attention_partial(const float *query_gate,
                                                            const float *keys, const float *values,
                                                            uint32_t position, uint32_t chunk,
-                                                           float *partial) {
+                                                           uint32_t splits, float *partial) {
+    const PartialBlock pb = partial_block(blockIdx.x, splits);
+    if (!pb.live) {
+        return;
+    }
     const uint32_t b = blockIdx.z;
     attention_partial_span(query_gate + static_cast<size_t>(b) * kQueryHeads * kQueryStride, keys,
                            values, position + b + 1, chunk,
-                           partial + static_cast<size_t>(b) * kQueryHeads * gridDim.y * kPartialStride);
+                           partial + static_cast<size_t>(b) * kQueryHeads * splits * kPartialStride, pb.head,
+                           pb.split, splits);
 }
 
 // Row r of a decode step over sequences sees its own cache's entries
@@ -304,29 +356,33 @@ __global__ __launch_bounds__(256) void k_attention_partial(const float *query_ga
 __global__ __launch_bounds__(256) void k_attention_partial_rows(const float *query_gate,
                                                                 FullRows rows,
                                                                 const uint32_t *positions,
-                                                                uint32_t cap, float *partial) {
+                                                                uint32_t cap, uint32_t grid_splits,
+                                                                float *partial) {
+    const PartialBlock pb = partial_block(blockIdx.x, grid_splits);
+    if (!pb.live) {
+        return;
+    }
     const uint32_t r = blockIdx.z;
     const uint32_t tokens = positions[r] + 1;
     const uint32_t splits = row_splits(tokens, cap);
     attention_partial_span(query_gate + static_cast<size_t>(r) * kQueryHeads * kQueryStride,
                            rows.keys[r], rows.values[r], tokens, (tokens + splits - 1u) / splits,
-                           partial + static_cast<size_t>(r) * kQueryHeads * gridDim.y * kPartialStride);
+                           partial + static_cast<size_t>(r) * kQueryHeads * grid_splits * kPartialStride,
+                           pb.head, pb.split, grid_splits);
 }
 
-// Per query head: the splits merged, divided by the denominator, times the
-// head's sigmoid gate (src/executor.cpp:403-411).
-__global__ __launch_bounds__(kHeadSize) void k_attention_combine(const float *partial,
-                                                                 uint32_t splits,
-                                                                 const float *query_gate,
-                                                                 float *attended) {
+// The splits of one query head merged (splits <= N): every split's
+// accumulator, then the splits' maxima and denominators (through LDS),
+// loaded in one round, then the accumulators added in split order.
+template <uint32_t N>
+__device__ __forceinline__ void combine_splits(const float *p, uint32_t splits, uint32_t t, float *split_max,
+                                               float *split_den, float *split_factor, float &a, float &d) {
 #pragma clang fp contract(off)
-    const uint32_t h = blockIdx.x, t = threadIdx.x, b = blockIdx.y;
-    query_gate += static_cast<size_t>(b) * kQueryHeads * kQueryStride;
-    attended += static_cast<size_t>(b) * kQueryHeads * kHeadSize;
-    __shared__ float split_max[kMaxSplits], split_den[kMaxSplits], split_factor[kMaxSplits];
-    const float *p = partial + (static_cast<size_t>(b) * kQueryHeads + h) * splits * kPartialStride;
-    // the splits' maxima and denominators through LDS, so the loop below
-    // loads only the accumulators (splits <= kMaxSplits)
+    float acc[N];
+#pragma unroll
+    for (uint32_t s = 0; s < N; ++s) {
+        acc[s] = s < splits ? p[s * kPartialStride + t] : 0.0f;
+    }
     for (uint32_t s = t; s < splits; s += kHeadSize) {
         split_max[s] = p[s * kPartialStride + kHeadSize];
         split_den[s] = p[s * kPartialStride + kHeadSize + 1];
@@ -341,18 +397,39 @@ __global__ __launch_bounds__(kHeadSize) void k_attention_combine(const float *pa
         split_factor[s] = expf(split_max[s] - m);
     }
     __syncthreads();
-    float a = 0.0f, d = 0.0f;
-#pragma unroll 8
-    for (uint32_t s = 0; s < splits; ++s) {
-        const float den = split_den[s];
+    a = 0.0f;
+    d = 0.0f;
+#pragma unroll
+    for (uint32_t s = 0; s < N; ++s) {
+        const float den = s < splits ? split_den[s] : 0.0f;
         if (den == 0.0f) {
-            continue;  // a split past the token
+            continue;  // a split past the token (or past the splits)
         }
         const float f = split_factor[s];
-        a += p[s * kPartialStride + t] * f;
+        a += acc[s] * f;
         d += den * f;
     }
+}
+
+// Per query head: the splits merged, divided by the denominator, times the
+// head's sigmoid gate (src/executor.cpp:403-411).
+__global__ __launch_bounds__(kHeadSize) void k_attention_combine(const float *partial,
+                                                                 uint32_t splits,
+                                                                 const float *query_gate,
+                                                                 float *attended) {
+#pragma clang fp contract(off)
+    const uint32_t h = blockIdx.x, t = threadIdx.x, b = blockIdx.y;
+    query_gate += static_cast<size_t>(b) * kQueryHeads * kQueryStride;
+    attended += static_cast<size_t>(b) * kQueryHeads * kHeadSize;
+    __shared__ float split_max[kMaxSplits], split_den[kMaxSplits], split_factor[kMaxSplits];
+    const float *p = partial + (static_cast<size_t>(b) * kQueryHeads + h) * splits * kPartialStride;
     const float gate = query_gate[static_cast<size_t>(h) * kQueryStride + kHeadSize + t];
+    float a, d;
+    if (splits <= 16u) {
+        combine_splits<16>(p, splits, t, split_max, split_den, split_factor, a, d);
+    } else {
+        combine_splits<kMaxSplits>(p, splits, t, split_max, split_den, split_factor, a, d);
+    }
     attended[static_cast<size_t>(h) * kHeadSize + t] = a * (1.0f / d) * sigmoid_of(gate);
 }
 
@@ -681,9 +758,9 @@ void full_attention_chunk(adi_hip_context *ctx, const adi_hip_full_attention *L,
            dim3(kHeadSize), 0, query_gate, key, L->query_norm, L->key_norm,
            count == 1 ? rope_table(position) : RopeTable{},
            count == 1 ? nullptr : rope_rows(ctx, position + count), position);
-    launch(ctx, "attention_partial", k_attention_partial, dim3(kQueryHeads, splits, count),
+    launch(ctx, "attention_partial", k_attention_partial, dim3(partial_blocks(splits), 1, count),
            dim3(256), 0, static_cast<const float *>(query_gate), static_cast<const float *>(keys),
-           static_cast<const float *>(values), position, chunk, partial);
+           static_cast<const float *>(values), position, chunk, splits, partial);
     launch(ctx, "attention_combine", k_attention_combine, dim3(kQueryHeads, count),
            dim3(kHeadSize), 0, static_cast<const float *>(partial), splits,
            static_cast<const float *>(query_gate), attended);
@@ -870,8 +947,8 @@ void full_attention_rows(adi_hip_context *ctx, const adi_hip_full_attention *L, 
                static_cast<const float *>(value + static_cast<size_t>(first) * kKvHeads * kHeadSize),
                L->query_norm, L->key_norm, rope, table, row_positions);
         launch(ctx, "attention_partial_rows", k_attention_partial_rows,
-               dim3(kQueryHeads, splits, count), dim3(256), 0, static_cast<const float *>(qg), table,
-               row_positions, cap,
+               dim3(partial_blocks(splits), 1, count), dim3(256), 0, static_cast<const float *>(qg), table,
+               row_positions, cap, splits,
                partial + static_cast<size_t>(first) * kQueryHeads * splits * kPartialStride);
     }
     launch(ctx, "attention_combine", k_attention_combine, dim3(kQueryHeads, rows), dim3(kHeadSize),
