@@ -591,6 +591,168 @@ __global__ __launch_bounds__(256) void k_gated_delta_rows(const float *convolved
                              rows.recurrent[r], output + static_cast<size_t>(r) * kValueSize);
 }
 
+// The causal convolution and SiLU of channel c for one token whose three
+// earlier inputs are in `history` (src/executor.cpp:480-496): the output and
+// the channel's shifted state (h1, h2, x).
+struct ConvChannel {
+    float y, h1, h2, x;
+};
+__device__ __forceinline__ ConvChannel conv_channel(const float *qkv_row, const uint16_t *weights,
+                                                    const float *history, uint32_t c) {
+#pragma clang fp contract(off)
+    const uint2 packed = *reinterpret_cast<const uint2 *>(weights + static_cast<size_t>(c) * 4u);
+    const float w0 = bf16_bits_to_float(packed.x & 0xFFFFu), w1 = bf16_bits_to_float(packed.x >> 16);
+    const float w2 = bf16_bits_to_float(packed.y & 0xFFFFu), w3 = bf16_bits_to_float(packed.y >> 16);
+    const float h0 = history[0], h1 = history[1], h2 = history[2];
+    const float x = qkv_row[c];
+    float v = 0.0f;
+    v += h0 * w0;
+    v += h1 * w1;
+    v += h2 * w2;
+    v += x * w3;
+    return {silu_of(v), h1, h2, x};
+}
+
+// One decode token of each of up to kRowGroup sequences through the Gated
+// DeltaNet core in one launch: the convolution with the query and key L2
+// norms, the delta rule and the gated RMS norm (src/executor.cpp:480-550),
+// with the arithmetic of k_linear_conv_rows, k_gated_delta_rows and
+// k_linear_norm_gate. Block (value head h, row block y, sequence r):
+// - convolves the 128 query and 128 key channels of h's key head itself (the
+//   16 blocks of a key head each do, each sum in the 128-thread block's
+//   order) and its own 16 value channels, whose state only it shifts;
+// - updates its 16 state rows and writes their outputs through to memory;
+// - the last of the head's 8 blocks through the head's ticket reads the 128
+//   outputs back and writes the head's gated norm; the last of the key
+//   head's 16 blocks through its ticket shifts the query and key channels'
+//   state (every one of them has read it by then).
+// `tickets` holds 48 words a sequence (32 value heads, 16 key heads), zero
+// between calls: the last block through each ticket clears it.
+__global__ __launch_bounds__(256) void k_linear_core_rows(const float *qkv, const uint16_t *weights,
+                                                          LinearRows rows, const float *alpha,
+                                                          const float *beta, const uint16_t *alpha_bias,
+                                                          const uint16_t *a_log, const uint16_t *norm,
+                                                          const float *gate, float *recurrent_output,
+                                                          float *normalized, uint32_t *tickets) {
+#pragma clang fp contract(off)
+    constexpr uint32_t kRows = kDeltaRows / 4u;
+    constexpr uint32_t kHeadBlocks = kLinearHead / kDeltaRows;
+    __shared__ float qk[2][kLinearHead];
+    __shared__ float vv[kDeltaRows];
+    __shared__ float part[4];
+    __shared__ uint32_t last;
+    const uint32_t h = blockIdx.x, y = blockIdx.y, r = blockIdx.z;
+    const uint32_t kh = h / (kValueHeads / kKeyHeads);
+    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    const float *row = qkv + static_cast<size_t>(r) * kChannels;
+    float *history = rows.convolution[r];
+    const uint32_t row0 = y * kDeltaRows + wave * kRows;
+    // the state rows first, so that their loads overlap the convolution
+    float2 *state = reinterpret_cast<float2 *>(rows.recurrent[r] +
+                                               (static_cast<size_t>(h) * kLinearHead + row0) * kLinearHead);
+    float2 s[kRows];
+#pragma unroll
+    for (uint32_t j = 0; j < kRows; ++j) {
+        s[j] = state[j * (kLinearHead / 2u) + lane];
+    }
+    // threads 0-127 the query channels, 128-255 the key channels; each L2
+    // norm sums as a 128-thread block does: (0 + wave 0) + wave 1
+    const uint32_t half = t >> 7;
+    const uint32_t c = half * kQkSize + kh * kLinearHead + (t & (kLinearHead - 1u));
+    const ConvChannel cc = conv_channel(row, weights, history + static_cast<size_t>(c) * 3u, c);
+    const float sq = wave_sum(cc.y * cc.y);
+    if (lane == 0) {
+        part[wave] = sq;
+    }
+    if (t < kDeltaRows) {
+        const uint32_t cv = 2u * kQkSize + h * kLinearHead + y * kDeltaRows + t;
+        float *hv = history + static_cast<size_t>(cv) * 3u;
+        const ConvChannel v = conv_channel(row, weights, hv, cv);
+        vv[t] = v.y;
+        hv[0] = v.h1;
+        hv[1] = v.h2;
+        hv[2] = v.x;
+    }
+    __syncthreads();
+    float squares = 0.0f;
+    squares += part[2u * half];
+    squares += part[2u * half + 1u];
+    qk[half][t & (kLinearHead - 1u)] = cc.y * (1.0f / sqrtf(squares + kEpsilon));
+    __syncthreads();
+    // the delta rule on the block's rows (gated_delta_rows_of_head, one token)
+    {
+        const float2 q = make_float2(qk[0][2u * lane], qk[0][2u * lane + 1u]);
+        const float2 k = make_float2(qk[1][2u * lane], qk[1][2u * lane + 1u]);
+        const float bias = bf16_bits_to_float(alpha_bias[h]);
+        const float rate = expf(bf16_bits_to_float(a_log[h]));
+        const float output_scale = 1.0f / sqrtf(static_cast<float>(kLinearHead));
+        const float beta_value = sigmoid_of(beta[static_cast<size_t>(r) * kValueHeads + h]);
+        const float biased = alpha[static_cast<size_t>(r) * kValueHeads + h] + bias;
+        const float softplus = biased > 20.0f ? biased : log1pf(expf(biased));
+        const float decay = expf(-rate * softplus);
+        float *out = recurrent_output + static_cast<size_t>(r) * kValueSize + static_cast<size_t>(h) * kLinearHead;
+#pragma unroll
+        for (uint32_t j = 0; j < kRows; ++j) {
+            s[j].x *= decay;
+            s[j].y *= decay;
+            const float prediction = wave_sum(s[j].x * k.x + s[j].y * k.y);
+            const float delta = (vv[wave * kRows + j] - prediction) * beta_value;
+            s[j].x += k.x * delta;
+            s[j].y += k.y * delta;
+            const float attended = wave_sum(s[j].x * q.x + s[j].y * q.y);
+            if (lane == 0) {
+                coherent_store(out + row0 + j, attended * output_scale);
+            }
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kRows; ++j) {
+            state[j * (kLinearHead / 2u) + lane] = s[j];
+        }
+    }
+    uint32_t *ticket = tickets + static_cast<size_t>(r) * (kValueHeads + kKeyHeads);
+    wait_stores();
+    __syncthreads();
+    if (t == 0) {
+        last = coherent_add(ticket + h, 1u) + 1u == kHeadBlocks ? 1u : 0u;
+    }
+    __syncthreads();
+    if (last != 0u) {
+        // the head's gated RMS norm (k_linear_norm_gate's arithmetic on
+        // threads 0-127)
+        const size_t i = static_cast<size_t>(r) * kValueSize + static_cast<size_t>(h) * kLinearHead + t;
+        const float x = t < kLinearHead ? coherent_load(recurrent_output + i) : 0.0f;
+        const float sx = wave_sum(x * x);
+        if (lane == 0) {
+            part[wave] = sx;
+        }
+        __syncthreads();
+        if (t < kLinearHead) {
+            float total = 0.0f;
+            total += part[0];
+            total += part[1];
+            const float scale = 1.0f / sqrtf(total / static_cast<float>(kLinearHead) + kEpsilon);
+            normalized[i] = x * scale * (0.0f + bf16_bits_to_float(norm[t])) * silu_of(gate[i]);
+        }
+        if (t == 0) {
+            coherent_store(ticket + h, 0u);
+        }
+    }
+    __syncthreads();
+    if (t == 0) {
+        last = coherent_add(ticket + kValueHeads + kh, 1u) + 1u == 2u * kHeadBlocks ? 1u : 0u;
+    }
+    __syncthreads();
+    if (last != 0u) {
+        float *hc = history + static_cast<size_t>(c) * 3u;
+        hc[0] = cc.h1;
+        hc[1] = cc.h2;
+        hc[2] = cc.x;
+        if (t == 0) {
+            coherent_store(ticket + kValueHeads + kh, 0u);
+        }
+    }
+}
+
 // rms_norm (weight offset 0, src/kernels.cpp:1052-1073) of each value head,
 // times SiLU of the gate (src/executor.cpp:538-550).
 __global__ __launch_bounds__(kLinearHead) void k_linear_norm_gate(const float *recurrent_output,
@@ -767,6 +929,18 @@ void full_attention_chunk(adi_hip_context *ctx, const adi_hip_full_attention *L,
     project_output(ctx, &L->output, attended, count, outputs, norm_tail);
 }
 
+// The Gated DeltaNet core of one token of each of `count` (<= kRowGroup)
+// sequences in one launch (k_linear_core_rows).
+void launch_linear_core(adi_hip_context *ctx, const adi_hip_linear_attention *L, const float *qkv,
+                        const LinearRows &table, uint32_t count, const float *alpha, const float *beta,
+                        const float *gate, float *recurrent_output, float *normalized) {
+    static_assert(kRowGroup * (kValueHeads + kKeyHeads) <= kMoeSyncWords - kMoeSyncLinear,
+                  "the DeltaNet tickets fit their sync lines");
+    launch(ctx, "linear_core", k_linear_core_rows, dim3(kValueHeads, kLinearHead / kDeltaRows, count),
+           dim3(256), 0, qkv, L->convolution, table, alpha, beta, L->alpha_bias, L->a_log, L->norm, gate,
+           recurrent_output, normalized, ctx->moe_sync + kMoeSyncLinear);
+}
+
 // linear_attention_forward for `count` consecutive tokens.
 void linear_attention_chunk(adi_hip_context *ctx, const adi_hip_linear_attention *L,
                             uint32_t count, const float *inputs, float *outputs,
@@ -803,6 +977,14 @@ void linear_attention_chunk(adi_hip_context *ctx, const adi_hip_linear_attention
     project_qkv_gate(ctx, L, inputs, count, qkv, gate, norm_in);
     const float *x = norm_in != nullptr ? norm_in->out : inputs;  // the normalized rows
     project_decay(ctx, L, x, count, alpha, beta);
+    if (count == 1 && ctx->fused_moe) {
+        LinearRows table{};
+        table.convolution[0] = convolution_state;
+        table.recurrent[0] = recurrent_state;
+        launch_linear_core(ctx, L, qkv, table, 1, alpha, beta, gate, recurrent_output, normalized);
+        project_output(ctx, &L->output, normalized, count, outputs, norm_tail);
+        return;
+    }
     launch(ctx, "linear_conv", k_linear_conv, dim3(kChannels / kLinearHead, count),
            dim3(kLinearHead), 0, static_cast<const float *>(qkv), L->convolution,
            convolution_state, convolved);
@@ -1008,6 +1190,12 @@ void linear_attention_rows(adi_hip_context *ctx, const adi_hip_linear_attention 
             table.recurrent[i] = states[first + i]->recurrent;
         }
         const size_t at = static_cast<size_t>(first);
+        if (ctx->fused_moe) {
+            launch_linear_core(ctx, L, qkv + at * kChannels, table, count, alpha + at * kValueHeads,
+                               beta + at * kValueHeads, gate + at * kValueSize,
+                               recurrent_output + at * kValueSize, normalized + at * kValueSize);
+            continue;
+        }
         launch(ctx, "linear_conv_rows", k_linear_conv_rows, dim3(kChannels / kLinearHead, count),
                dim3(kLinearHead), 0, static_cast<const float *>(qkv + at * kChannels),
                L->convolution, table, convolved + at * kChannels);
@@ -1017,10 +1205,10 @@ void linear_attention_rows(adi_hip_context *ctx, const adi_hip_linear_attention 
                static_cast<const float *>(alpha + at * kValueHeads),
                static_cast<const float *>(beta + at * kValueHeads), L->alpha_bias, L->a_log, table,
                recurrent_output + at * kValueSize);
+        launch(ctx, "linear_norm_gate", k_linear_norm_gate, dim3(kValueHeads, count), dim3(kLinearHead),
+               0, static_cast<const float *>(recurrent_output + at * kValueSize), L->norm,
+               static_cast<const float *>(gate + at * kValueSize), normalized + at * kValueSize);
     }
-    launch(ctx, "linear_norm_gate", k_linear_norm_gate, dim3(kValueHeads, rows), dim3(kLinearHead),
-           0, static_cast<const float *>(recurrent_output), L->norm,
-           static_cast<const float *>(gate), normalized);
     project_output(ctx, &L->output, normalized, rows, outputs, norm_tail);
 }
 

@@ -1935,8 +1935,8 @@ constexpr uint32_t kLogits = 0,        // 8 group counters (block b adds to b % 
                    kCounters = kPosition + kFewMaxRows;
 }  // namespace few_sync
 static_assert(kMoeSyncFew >= (moe_sync::kParts + 18u) * kMoeSyncLine &&
-                  kMoeSyncFew + few_sync::kCounters * few_sync::kStride <= kMoeSyncWords,
-              "the few-row counters sit after the one-row block's lines, inside the sync buffer");
+                  kMoeSyncFew + few_sync::kCounters * few_sync::kStride <= kMoeSyncLinear,
+              "the few-row counters sit after the one-row block's lines, before the DeltaNet tickets");
 
 __device__ __forceinline__ uint32_t *few_word(uint32_t *sync, uint32_t i) {
     return sync + static_cast<size_t>(i) * few_sync::kStride;

@@ -113,6 +113,41 @@ def test_decode_batch_many_sequences_mixed_positions(gpu, oracle, parts, count):
         assert s.position == len(prompt) + 2
 
 
+@pytest.mark.parametrize("count", [3, 40])
+def test_decode_batch_one_launch_paths_equal_separate_launches(gpu, parts, count):
+    """A decode step's Gated DeltaNet core (convolution, delta rule, gated
+    norm) runs as one launch per 32 sequences, and up to 12 rows the MoE
+    block and up to 4 the NE projections are single launches too; with the
+    one-launch paths off every part is a launch of its own. Logits, caches
+    and states are bit-identical over three steps of sequences at different
+    positions (40 sequences: two groups of row pointers)."""
+    model = parts["one"]
+
+    def run(fused):
+        gpu.set_fused_decode(fused)
+        try:
+            seqs = [hip.Sequence(model, CAPACITY) for _ in range(count)]
+            for i, s in enumerate(seqs):
+                if i % 4:
+                    hip.prefill(gpu, model, [(3 * i + j) % VOCAB for j in range(i % 4)], s, None, ubatch=2)
+            tokens = [(5 * i + 1) % VOCAB for i in range(count)]
+            outs = []
+            for step in range(3):
+                print("decode_batch", count, fused, step, flush=True)
+                out = torch.empty((count, VOCAB), dtype=torch.float32, device="cuda")
+                hip.decode_batch(gpu, model, tokens, seqs, out)
+                outs.append(out.cpu().numpy())
+                tokens = [int(t) for t in np.argmax(outs[-1], axis=1)]
+            gpu.synchronize()
+            return outs + [t.cpu().numpy() for s in seqs for keep in s.tensors for t in keep]
+        finally:
+            gpu.set_fused_decode(True)
+
+    one, separate = run(True), run(False)
+    for i, (a, b) in enumerate(zip(one, separate)):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), i
+
+
 def test_fresh_sequences_batched_equal_decoded_alone(gpu, parts):
     """tests/model_batch_test.cpp:24-51: two new sequences decoded as one
     batch give the logits of each decoded alone, and both reach position 1.
