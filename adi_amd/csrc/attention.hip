@@ -628,8 +628,17 @@ __device__ __forceinline__ ConvChannel conv_channel(const float *qkv_row, const 
 //   state (every one of them has read it by then).
 // `tickets` holds 48 words a sequence (32 value heads, 16 key heads), zero
 // between calls: the last block through each ticket clears it.
+// With LANES 8 or 16 the block also computes its head's alpha and beta
+// (the bf16 matmuls of the normalized row `x`, in the CPU's LANES-lane order
+// as k_bf16_lds does): the row and the two weight rows staged in LDS, one
+// wave's lanes 0 .. 2 LANES - 1 running the chains. With LANES 0 they come
+// precomputed in alpha and beta.
+constexpr uint32_t kDecayColumns = 2048;  // the widest row staged for alpha and beta
+template <int LANES>
 __global__ __launch_bounds__(256) void k_linear_core_rows(const float *qkv, const uint16_t *weights,
-                                                          LinearRows rows, const float *alpha,
+                                                          LinearRows rows, const float *x,
+                                                          const uint16_t *alpha_w, const uint16_t *beta_w,
+                                                          uint32_t columns, const float *alpha,
                                                           const float *beta, const uint16_t *alpha_bias,
                                                           const uint16_t *a_log, const uint16_t *norm,
                                                           const float *gate, float *recurrent_output,
@@ -637,9 +646,13 @@ __global__ __launch_bounds__(256) void k_linear_core_rows(const float *qkv, cons
 #pragma clang fp contract(off)
     constexpr uint32_t kRows = kDeltaRows / 4u;
     constexpr uint32_t kHeadBlocks = kLinearHead / kDeltaRows;
+    constexpr uint32_t kStaged = LANES > 0 ? kDecayColumns : 4u;
     __shared__ float qk[2][kLinearHead];
     __shared__ float vv[kDeltaRows];
     __shared__ float part[4];
+    __shared__ float decay_in[2];
+    __shared__ __align__(16) float x_lds[kStaged];
+    __shared__ __align__(16) uint16_t w_lds[2][kStaged];
     __shared__ uint32_t last;
     const uint32_t h = blockIdx.x, y = blockIdx.y, r = blockIdx.z;
     const uint32_t kh = h / (kValueHeads / kKeyHeads);
@@ -654,6 +667,20 @@ __global__ __launch_bounds__(256) void k_linear_core_rows(const float *qkv, cons
 #pragma unroll
     for (uint32_t j = 0; j < kRows; ++j) {
         s[j] = state[j * (kLinearHead / 2u) + lane];
+    }
+    if constexpr (LANES > 0) {
+        // the row and the head's alpha and beta weight rows (columns <= 2048,
+        // a multiple of 256)
+        const float4 *xs = reinterpret_cast<const float4 *>(x + static_cast<size_t>(r) * columns);
+        for (uint32_t i = t; i < columns / 4u; i += 256u) {
+            reinterpret_cast<float4 *>(x_lds)[i] = xs[i];
+        }
+        const uint4 *wa = reinterpret_cast<const uint4 *>(alpha_w + static_cast<size_t>(h) * columns);
+        const uint4 *wb = reinterpret_cast<const uint4 *>(beta_w + static_cast<size_t>(h) * columns);
+        for (uint32_t i = t; i < columns / 8u; i += 256u) {
+            reinterpret_cast<uint4 *>(w_lds[0])[i] = wa[i];
+            reinterpret_cast<uint4 *>(w_lds[1])[i] = wb[i];
+        }
     }
     // threads 0-127 the query channels, 128-255 the key channels; each L2
     // norm sums as a 128-thread block does: (0 + wave 0) + wave 1
@@ -678,6 +705,20 @@ __global__ __launch_bounds__(256) void k_linear_core_rows(const float *qkv, cons
     squares += part[2u * half];
     squares += part[2u * half + 1u];
     qk[half][t & (kLinearHead - 1u)] = cc.y * (1.0f / sqrtf(squares + kEpsilon));
+    if constexpr (LANES > 0) {
+        if (wave == 3u) {
+            // lanes 0 .. LANES - 1 alpha's chains, LANES .. 2 LANES - 1 beta's
+            // (the lanes past them repeat those)
+            const uint32_t g = (lane / LANES) & 1u;
+            const float acc = router_chain<LANES>(w_lds[g], x_lds, columns, lane % LANES);
+            const float a = router_lane_sum<LANES>(acc, 0u);
+            const float b = router_lane_sum<LANES>(acc, 1u);
+            if (lane == 0) {
+                decay_in[0] = a;
+                decay_in[1] = b;
+            }
+        }
+    }
     __syncthreads();
     // the delta rule on the block's rows (gated_delta_rows_of_head, one token)
     {
@@ -686,8 +727,10 @@ __global__ __launch_bounds__(256) void k_linear_core_rows(const float *qkv, cons
         const float bias = bf16_bits_to_float(alpha_bias[h]);
         const float rate = expf(bf16_bits_to_float(a_log[h]));
         const float output_scale = 1.0f / sqrtf(static_cast<float>(kLinearHead));
-        const float beta_value = sigmoid_of(beta[static_cast<size_t>(r) * kValueHeads + h]);
-        const float biased = alpha[static_cast<size_t>(r) * kValueHeads + h] + bias;
+        const float alpha_in = LANES > 0 ? decay_in[0] : alpha[static_cast<size_t>(r) * kValueHeads + h];
+        const float beta_in = LANES > 0 ? decay_in[1] : beta[static_cast<size_t>(r) * kValueHeads + h];
+        const float beta_value = sigmoid_of(beta_in);
+        const float biased = alpha_in + bias;
         const float softplus = biased > 20.0f ? biased : log1pf(expf(biased));
         const float decay = expf(-rate * softplus);
         float *out = recurrent_output + static_cast<size_t>(r) * kValueSize + static_cast<size_t>(h) * kLinearHead;
@@ -929,16 +972,33 @@ void full_attention_chunk(adi_hip_context *ctx, const adi_hip_full_attention *L,
     project_output(ctx, &L->output, attended, count, outputs, norm_tail);
 }
 
+// Whether the Gated DeltaNet core launch computes alpha and beta itself from
+// the normalized rows x (8- or 16-lane order, rows of at most 2048 columns,
+// a multiple of 256, 16-byte aligned).
+bool core_takes_decay(const adi_hip_context *ctx, const adi_hip_linear_attention *L, const float *x) {
+    const uint32_t columns = L->alpha.columns;
+    return (ctx->isa_lanes == 8 || ctx->isa_lanes == 16) && columns <= kDecayColumns && columns % 256u == 0 &&
+           aligned_to(x, 16) && aligned_to(L->alpha.values, 16) && aligned_to(L->beta.values, 16);
+}
+
 // The Gated DeltaNet core of one token of each of `count` (<= kRowGroup)
-// sequences in one launch (k_linear_core_rows).
+// sequences in one launch (k_linear_core_rows): alpha and beta from the
+// normalized rows x when core_takes_decay holds, else from alpha and beta.
 void launch_linear_core(adi_hip_context *ctx, const adi_hip_linear_attention *L, const float *qkv,
-                        const LinearRows &table, uint32_t count, const float *alpha, const float *beta,
-                        const float *gate, float *recurrent_output, float *normalized) {
+                        const LinearRows &table, uint32_t count, const float *x, const float *alpha,
+                        const float *beta, const float *gate, float *recurrent_output, float *normalized) {
     static_assert(kRowGroup * (kValueHeads + kKeyHeads) <= kMoeSyncWords - kMoeSyncLinear,
                   "the DeltaNet tickets fit their sync lines");
-    launch(ctx, "linear_core", k_linear_core_rows, dim3(kValueHeads, kLinearHead / kDeltaRows, count),
-           dim3(256), 0, qkv, L->convolution, table, alpha, beta, L->alpha_bias, L->a_log, L->norm, gate,
-           recurrent_output, normalized, ctx->moe_sync + kMoeSyncLinear);
+    using Kernel = void (*)(const float *, const uint16_t *, LinearRows, const float *, const uint16_t *,
+                            const uint16_t *, uint32_t, const float *, const float *, const uint16_t *,
+                            const uint16_t *, const uint16_t *, const float *, float *, float *, uint32_t *);
+    Kernel kernel = k_linear_core_rows<0>;
+    if (core_takes_decay(ctx, L, x)) {
+        kernel = ctx->isa_lanes == 16 ? k_linear_core_rows<16> : k_linear_core_rows<8>;
+    }
+    launch(ctx, "linear_core", kernel, dim3(kValueHeads, kLinearHead / kDeltaRows, count), dim3(256), 0, qkv,
+           L->convolution, table, x, L->alpha.values, L->beta.values, L->alpha.columns, alpha, beta,
+           L->alpha_bias, L->a_log, L->norm, gate, recurrent_output, normalized, ctx->moe_sync + kMoeSyncLinear);
 }
 
 // linear_attention_forward for `count` consecutive tokens.
@@ -976,15 +1036,18 @@ void linear_attention_chunk(adi_hip_context *ctx, const adi_hip_linear_attention
     float *beta = ws.take<float>(n * kValueHeads);
     project_qkv_gate(ctx, L, inputs, count, qkv, gate, norm_in);
     const float *x = norm_in != nullptr ? norm_in->out : inputs;  // the normalized rows
-    project_decay(ctx, L, x, count, alpha, beta);
     if (count == 1 && ctx->fused_moe) {
+        if (!core_takes_decay(ctx, L, x)) {
+            project_decay(ctx, L, x, count, alpha, beta);
+        }
         LinearRows table{};
         table.convolution[0] = convolution_state;
         table.recurrent[0] = recurrent_state;
-        launch_linear_core(ctx, L, qkv, table, 1, alpha, beta, gate, recurrent_output, normalized);
+        launch_linear_core(ctx, L, qkv, table, 1, x, alpha, beta, gate, recurrent_output, normalized);
         project_output(ctx, &L->output, normalized, count, outputs, norm_tail);
         return;
     }
+    project_decay(ctx, L, x, count, alpha, beta);
     launch(ctx, "linear_conv", k_linear_conv, dim3(kChannels / kLinearHead, count),
            dim3(kLinearHead), 0, static_cast<const float *>(qkv), L->convolution,
            convolution_state, convolved);
@@ -1181,7 +1244,9 @@ void linear_attention_rows(adi_hip_context *ctx, const adi_hip_linear_attention 
     float *beta = ws.take<float>(n * kValueHeads);
     project_qkv_gate(ctx, L, inputs, rows, qkv, gate, norm_in);
     const float *x = norm_in != nullptr ? norm_in->out : inputs;  // the normalized rows
-    project_decay(ctx, L, x, rows, alpha, beta);
+    if (!ctx->fused_moe || !core_takes_decay(ctx, L, x)) {
+        project_decay(ctx, L, x, rows, alpha, beta);
+    }
     for (uint32_t first = 0; first < rows; first += kRowGroup) {
         const uint32_t count = rows - first < kRowGroup ? rows - first : kRowGroup;
         LinearRows table{};
@@ -1191,8 +1256,8 @@ void linear_attention_rows(adi_hip_context *ctx, const adi_hip_linear_attention 
         }
         const size_t at = static_cast<size_t>(first);
         if (ctx->fused_moe) {
-            launch_linear_core(ctx, L, qkv + at * kChannels, table, count, alpha + at * kValueHeads,
-                               beta + at * kValueHeads, gate + at * kValueSize,
+            launch_linear_core(ctx, L, qkv + at * kChannels, table, count, x + at * L->alpha.columns,
+                               alpha + at * kValueHeads, beta + at * kValueHeads, gate + at * kValueSize,
                                recurrent_output + at * kValueSize, normalized + at * kValueSize);
             continue;
         }

@@ -1284,51 +1284,6 @@ __device__ __forceinline__ void publish_flag(uint32_t *sync, uint32_t line) {
     }
 }
 
-// One router logit per LANES-lane group in the CPU's order (dense.hip): lane
-// j of the group adds columns j, j + LANES, ... of its row (fused multiply-add
-// for the 16-lane order, multiply then add for the 8-lane order), then the
-// group's lane sums are added in lane order from 0. w (bf16) and x in LDS.
-template <int LANES>
-__device__ __forceinline__ float router_chain(const uint16_t *w, const float *x, uint32_t columns,
-                                              uint32_t j) {
-#pragma clang fp contract(off)
-    constexpr uint32_t kBatch = 16;  // LDS reads of 16 steps issued before their adds
-    float acc = 0.0f;
-    for (uint32_t base = 0; base < columns; base += kBatch * LANES) {
-        float wk[kBatch], xk[kBatch];
-#pragma unroll
-        for (uint32_t u = 0; u < kBatch; ++u) {
-            const uint32_t k = base + u * LANES + j;
-            wk[u] = bf16_bits_to_float(w[k]);
-            xk[u] = x[k];
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < kBatch; ++u) {
-            if constexpr (LANES == 16) {
-                acc = fmaf(wk[u], xk[u], acc);
-            } else {
-                acc = acc + wk[u] * xk[u];
-            }
-        }
-    }
-    return acc;
-}
-
-// The lane sums of lanes group * LANES .. + LANES - 1, added in lane order
-// from 0 (every lane gets the sum).
-template <int LANES>
-__device__ __forceinline__ float router_lane_sum(float acc, uint32_t group) {
-#pragma clang fp contract(off)
-    float sum = 0.0f;
-#pragma unroll
-    for (uint32_t j = 0; j < LANES; ++j) {
-        sum = sum + __uint_as_float(static_cast<uint32_t>(
-                        __builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(acc)),
-                                                  static_cast<int>(group * LANES + j))));
-    }
-    return sum;
-}
-
 // The 2048-point transform of x * m by the eight GEMV waves of a block, in
 // two steps with a block barrier between them. Step one: wave w transforms
 // elements 256 w .. 256 w + 255 (index bits 0-7; element 64 i + lane of its
