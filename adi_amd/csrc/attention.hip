@@ -267,16 +267,24 @@ __device__ __forceinline__ void online_step(float score, float4 value, float &ma
 // every fourth. Lane l holds dimensions 4l..4l+3. Writes the split's
 // accumulator, maximum and denominator to the token's partial rows
 // (maximum -inf and denominator 0 when the split lies past the token).
-__device__ __forceinline__ void attention_partial_span(const float *query_gate, const float *keys,
+// With COHERENT the partial row is written through to memory (a later block
+// of the same launch reads it). The query head is at `query` (global or LDS);
+// entry `fresh` (when below `tokens`) is taken from fresh_key / fresh_value
+// (LDS) instead of the cache.
+template <bool COHERENT = false>
+__device__ __forceinline__ void attention_partial_span(const float *query, const float *keys,
                                                        const float *values, uint32_t tokens,
                                                        uint32_t chunk, float *partial, uint32_t h,
-                                                       uint32_t split, uint32_t splits) {
+                                                       uint32_t split, uint32_t splits,
+                                                       uint32_t fresh = 0xFFFFFFFFu,
+                                                       const float *fresh_key = nullptr,
+                                                       const float *fresh_value = nullptr) {
 #pragma clang fp contract(off)
     __shared__ __align__(16) float wave_acc[4][kHeadSize];
     __shared__ float wave_max[4], wave_den[4];
     const uint32_t kv = h / (kQueryHeads / kKvHeads);
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const float4 q = reinterpret_cast<const float4 *>(query_gate + static_cast<size_t>(h) * kQueryStride)[lane];
+    const float4 q = reinterpret_cast<const float4 *>(query)[lane];
     const float score_scale = 1.0f / 16.0f;  // 1 / sqrt(256)
     const uint32_t begin = split * chunk;
     const uint32_t end = begin + chunk < tokens ? begin + chunk : tokens;
@@ -292,8 +300,13 @@ __device__ __forceinline__ void attention_partial_span(const float *query_gate, 
         for (uint32_t j = 0; j < kBatch; ++j) {
             const uint32_t t = t0 + 4u * j < end ? t0 + 4u * j : t0;
             const size_t at = (static_cast<size_t>(t) * kKvHeads + kv) * kHeadSize;
-            k[j] = reinterpret_cast<const float4 *>(keys + at)[lane];
-            v[j] = reinterpret_cast<const float4 *>(values + at)[lane];
+            if (t == fresh) {  // wave-uniform
+                k[j] = reinterpret_cast<const float4 *>(fresh_key)[lane];
+                v[j] = reinterpret_cast<const float4 *>(fresh_value)[lane];
+            } else {
+                k[j] = reinterpret_cast<const float4 *>(keys + at)[lane];
+                v[j] = reinterpret_cast<const float4 *>(values + at)[lane];
+            }
         }
         float dot[kBatch];
 #pragma unroll
@@ -326,10 +339,18 @@ __device__ __forceinline__ void attention_partial_span(const float *query_gate, 
         }
     }
     float *out = partial + (static_cast<size_t>(h) * splits + split) * kPartialStride;
-    out[threadIdx.x] = a;
-    if (threadIdx.x == 0) {
-        out[kHeadSize] = m;
-        out[kHeadSize + 1] = d;
+    if constexpr (COHERENT) {
+        coherent_store(out + threadIdx.x, a);
+        if (threadIdx.x == 0) {
+            coherent_store(out + kHeadSize, m);
+            coherent_store(out + kHeadSize + 1, d);
+        }
+    } else {
+        out[threadIdx.x] = a;
+        if (threadIdx.x == 0) {
+            out[kHeadSize] = m;
+            out[kHeadSize + 1] = d;
+        }
     }
 }
 
@@ -343,7 +364,9 @@ __global__ __launch_bounds__(256) void k_attention_partial(const float *query_ga
         return;
     }
     const uint32_t b = blockIdx.z;
-    attention_partial_span(query_gate + static_cast<size_t>(b) * kQueryHeads * kQueryStride, keys,
+    attention_partial_span(query_gate + static_cast<size_t>(b) * kQueryHeads * kQueryStride +
+                               static_cast<size_t>(pb.head) * kQueryStride,
+                           keys,
                            values, position + b + 1, chunk,
                            partial + static_cast<size_t>(b) * kQueryHeads * splits * kPartialStride, pb.head,
                            pb.split, splits);
@@ -365,7 +388,8 @@ __global__ __launch_bounds__(256) void k_attention_partial_rows(const float *que
     const uint32_t r = blockIdx.z;
     const uint32_t tokens = positions[r] + 1;
     const uint32_t splits = row_splits(tokens, cap);
-    attention_partial_span(query_gate + static_cast<size_t>(r) * kQueryHeads * kQueryStride,
+    attention_partial_span(query_gate + static_cast<size_t>(r) * kQueryHeads * kQueryStride +
+                               static_cast<size_t>(pb.head) * kQueryStride,
                            rows.keys[r], rows.values[r], tokens, (tokens + splits - 1u) / splits,
                            partial + static_cast<size_t>(r) * kQueryHeads * grid_splits * kPartialStride,
                            pb.head, pb.split, grid_splits);
@@ -374,18 +398,19 @@ __global__ __launch_bounds__(256) void k_attention_partial_rows(const float *que
 // The splits of one query head merged (splits <= N): every split's
 // accumulator, then the splits' maxima and denominators (through LDS),
 // loaded in one round, then the accumulators added in split order.
-template <uint32_t N>
+template <uint32_t N, bool COHERENT = false>
 __device__ __forceinline__ void combine_splits(const float *p, uint32_t splits, uint32_t t, float *split_max,
                                                float *split_den, float *split_factor, float &a, float &d) {
 #pragma clang fp contract(off)
+    const auto load = [](const float *at) { return COHERENT ? coherent_load(at) : *at; };
     float acc[N];
 #pragma unroll
     for (uint32_t s = 0; s < N; ++s) {
-        acc[s] = s < splits ? p[s * kPartialStride + t] : 0.0f;
+        acc[s] = s < splits ? load(p + s * kPartialStride + t) : 0.0f;
     }
     for (uint32_t s = t; s < splits; s += kHeadSize) {
-        split_max[s] = p[s * kPartialStride + kHeadSize];
-        split_den[s] = p[s * kPartialStride + kHeadSize + 1];
+        split_max[s] = load(p + s * kPartialStride + kHeadSize);
+        split_den[s] = load(p + s * kPartialStride + kHeadSize + 1);
     }
     __syncthreads();
     // split 0 always holds token 0, so the maximum is finite
@@ -431,6 +456,93 @@ __global__ __launch_bounds__(kHeadSize) void k_attention_combine(const float *pa
         combine_splits<kMaxSplits>(p, splits, t, split_max, split_den, split_factor, a, d);
     }
     attended[static_cast<size_t>(h) * kHeadSize + t] = a * (1.0f / d) * sigmoid_of(gate);
+}
+
+// One decode token of each of up to kRowGroup sequences through full
+// attention's core in one launch, with the arithmetic of k_norm_rope_rows,
+// k_attention_partial_rows and k_attention_combine. Block (query head h,
+// split, sequence r), dealt as partial_block deals them:
+// - normalizes and rotates its query head into LDS itself (every split of a
+//   head does);
+// - the splits holding the row's new entry (position) normalize and rotate
+//   its key and take its value themselves, and one of them per KV head (the
+//   first query head of the KV head) writes both into the cache: no block
+//   reads that entry from the cache;
+// - writes its split's partial row through to memory; the last block of the
+//   head's grid_splits through the head's ticket merges them and applies the
+//   sigmoid gate.
+// `tickets` holds kQueryHeads words a sequence, zero between calls.
+__global__ __launch_bounds__(256) void k_attention_rows_one(const float *query_gate, const float *key,
+                                                            const float *value, const uint16_t *query_norm,
+                                                            const uint16_t *key_norm, const float *rope_rows,
+                                                            FullRows rows, const uint32_t *positions,
+                                                            uint32_t cap, uint32_t grid_splits, float *partial,
+                                                            float *attended, uint32_t *tickets) {
+    __shared__ float sums[16];
+    __shared__ float head[kHeadSize];
+    __shared__ __align__(16) float q_lds[kHeadSize];
+    __shared__ __align__(16) float key_lds[kHeadSize];
+    __shared__ __align__(16) float value_lds[kHeadSize];
+    __shared__ float split_max[kMaxSplits], split_den[kMaxSplits], split_factor[kMaxSplits];
+    __shared__ uint32_t last;
+    const PartialBlock pb = partial_block(blockIdx.x, grid_splits);
+    if (!pb.live) {
+        return;
+    }
+    const uint32_t r = blockIdx.z, t = threadIdx.x;
+    const uint32_t h = pb.head, split = pb.split, kv = h / (kQueryHeads / kKvHeads);
+    const uint32_t position = positions[r];
+    const uint32_t tokens = position + 1u;
+    const uint32_t splits = row_splits(tokens, cap);
+    const uint32_t chunk = (tokens + splits - 1u) / splits;
+    const uint32_t begin = split * chunk;
+    const bool fresh = begin <= position && position < begin + chunk;  // uniform over the block
+    const float *qg = query_gate + (static_cast<size_t>(r) * kQueryHeads + h) * kQueryStride;
+    float cosine = 0.0f, sine = 0.0f;
+    if (t < kRopeHalf) {
+        const float *row = rope_rows + static_cast<size_t>(position) * (2 * kRopeHalf);
+        cosine = row[t];
+        sine = row[kRopeHalf + t];
+    }
+    norm_rope_head(qg, q_lds, query_norm, cosine, sine, sums, head);
+    if (fresh) {
+        __syncthreads();  // head[] is free again
+        const size_t src = (static_cast<size_t>(r) * kKvHeads + kv) * kHeadSize;
+        norm_rope_head(key + src, key_lds, key_norm, cosine, sine, sums, head);
+        value_lds[t] = value[src + t];
+        __syncthreads();
+        if (h % (kQueryHeads / kKvHeads) == 0u) {
+            const size_t entry = (static_cast<size_t>(position) * kKvHeads + kv) * kHeadSize;
+            rows.keys[r][entry + t] = key_lds[t];
+            rows.values[r][entry + t] = value_lds[t];
+        }
+    }
+    __syncthreads();
+    float *p = partial + static_cast<size_t>(r) * kQueryHeads * grid_splits * kPartialStride;
+    attention_partial_span<true>(q_lds, rows.keys[r], rows.values[r], tokens, chunk, p, h, split, grid_splits,
+                                 position, key_lds, value_lds);
+    wait_stores();
+    __syncthreads();
+    uint32_t *ticket = tickets + static_cast<size_t>(r) * kQueryHeads + h;
+    if (t == 0) {
+        last = coherent_add(ticket, 1u) + 1u == grid_splits ? 1u : 0u;
+    }
+    __syncthreads();
+    if (last == 0u) {
+        return;
+    }
+    const float gate = qg[kHeadSize + t];
+    const float *ph = p + static_cast<size_t>(h) * grid_splits * kPartialStride;
+    float a, d;
+    if (grid_splits <= 16u) {
+        combine_splits<16, true>(ph, grid_splits, t, split_max, split_den, split_factor, a, d);
+    } else {
+        combine_splits<kMaxSplits, true>(ph, grid_splits, t, split_max, split_den, split_factor, a, d);
+    }
+    attended[(static_cast<size_t>(r) * kQueryHeads + h) * kHeadSize + t] = a * (1.0f / d) * sigmoid_of(gate);
+    if (t == 0) {
+        coherent_store(ticket, 0u);
+    }
 }
 
 // The causal convolution of 128 channels for token b of a chunk
@@ -1186,6 +1298,19 @@ void full_attention_rows(adi_hip_context *ctx, const adi_hip_full_attention *L, 
         }
         const uint32_t *row_positions = device_positions + first;
         float *qg = query_gate + static_cast<size_t>(first) * kQueryHeads * kQueryStride;
+        if (ctx->fused_moe) {
+            static_assert(kRowGroup * kQueryHeads <= kMoeSyncWords - kMoeSyncAttention,
+                          "the attention tickets fit their sync line");
+            launch(ctx, "attention_rows_one", k_attention_rows_one, dim3(partial_blocks(splits), 1, count),
+                   dim3(256), 0, static_cast<const float *>(qg),
+                   static_cast<const float *>(key + static_cast<size_t>(first) * kKvHeads * kHeadSize),
+                   static_cast<const float *>(value + static_cast<size_t>(first) * kKvHeads * kHeadSize),
+                   L->query_norm, L->key_norm, rope, table, row_positions, cap, splits,
+                   partial + static_cast<size_t>(first) * kQueryHeads * splits * kPartialStride,
+                   attended + static_cast<size_t>(first) * kQueryHeads * kHeadSize,
+                   ctx->moe_sync + kMoeSyncAttention);
+            continue;
+        }
         launch(ctx, "attention_norm_rope_rows", k_norm_rope_rows,
                dim3(kQueryHeads + 2 * kKvHeads, count), dim3(kHeadSize), 0, qg,
                static_cast<const float *>(key + static_cast<size_t>(first) * kKvHeads * kHeadSize),
@@ -1195,10 +1320,10 @@ void full_attention_rows(adi_hip_context *ctx, const adi_hip_full_attention *L, 
                dim3(partial_blocks(splits), 1, count), dim3(256), 0, static_cast<const float *>(qg), table,
                row_positions, cap, splits,
                partial + static_cast<size_t>(first) * kQueryHeads * splits * kPartialStride);
+        launch(ctx, "attention_combine", k_attention_combine, dim3(kQueryHeads, count), dim3(kHeadSize), 0,
+               static_cast<const float *>(partial + static_cast<size_t>(first) * kQueryHeads * splits * kPartialStride),
+               splits, static_cast<const float *>(qg), attended + static_cast<size_t>(first) * kQueryHeads * kHeadSize);
     }
-    launch(ctx, "attention_combine", k_attention_combine, dim3(kQueryHeads, rows), dim3(kHeadSize),
-           0, static_cast<const float *>(partial), splits, static_cast<const float *>(query_gate),
-           attended);
     project_output(ctx, &L->output, attended, rows, outputs, norm_tail);
 }
 

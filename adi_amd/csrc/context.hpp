@@ -151,17 +151,19 @@ struct adi_hip_context {
 
 namespace adi_hip {
 
-// adi_hip_context::moe_sync: 98 lines of kMoeSyncLine words. Lines 0-45
+// adi_hip_context::moe_sync: 99 lines of kMoeSyncLine words. Lines 0-45
 // hold the one-row MoE block's counters and flags, its logits, the NE
 // projection's ticket (43) and the error word (45); lines 46-63 the one-row
 // block's nine combine rows (data it leaves behind); lines 64-95 the few-row
-// block's counters; lines 96-97 the Gated DeltaNet core's tickets.
+// block's counters; lines 96-97 the Gated DeltaNet core's tickets; line 98
+// the full-attention decode launch's tickets.
 constexpr uint32_t kMoeSyncLine = 1024;
-constexpr uint32_t kMoeSyncWords = 98 * kMoeSyncLine;
+constexpr uint32_t kMoeSyncWords = 99 * kMoeSyncLine;
 constexpr uint32_t kMoeSyncError = 45 * kMoeSyncLine;
 constexpr uint32_t kMoeSyncNeTicket = 43 * kMoeSyncLine;  // the one-launch NE projection's ticket
 constexpr uint32_t kMoeSyncFew = 64 * kMoeSyncLine;       // the few-row MoE block's counters
 constexpr uint32_t kMoeSyncLinear = 96 * kMoeSyncLine;    // the Gated DeltaNet core's tickets
+constexpr uint32_t kMoeSyncAttention = 98 * kMoeSyncLine; // the full-attention decode launch's tickets
 
 // Selects the context's device for the duration of a call.
 class DeviceScope {
