@@ -69,7 +69,12 @@ int adi_hip_set_reduction_isa(adi_hip_context *ctx, uint32_t lanes);
  * routing, both projections of every route, shared expert and combine in
  * one persistent launch) and adi_hip_ne_matmul on up to 4 rows of the shapes
  * it is built for (x_hat, the NE items and the output transform in one
- * launch). The one-launch MoE block of 2 to 12 rows runs the decode-GEMV
+ * launch); in a decoder layer of 1 to 4 tokens, its RMS norms inside the
+ * projection launches; and for one token per sequence the Gated DeltaNet
+ * core (alpha/beta, convolution, delta rule, gated norm) and the full
+ * attention core (query/key norm and rotation, flash-decoding, split merge)
+ * as one launch each. All of these give results bit-identical to the
+ * separate launches. The one-launch MoE block of 2 to 12 rows runs the decode-GEMV
  * arithmetic; the separate launches take the MFMA GEMMs from 8 rows, except
  * with enabled 2 (separate launches, decode-GEMV up to 16 rows), which gives
  * results bit-identical to the one-launch block at every batch it runs; at
