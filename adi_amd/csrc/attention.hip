@@ -626,6 +626,8 @@ __global__ __launch_bounds__(256) void k_conv_history(const float *qkv, uint32_t
     }
 }
 
+constexpr uint32_t kDeltaTokens = 1024;  // tokens of one k_gated_delta launch, at most
+
 // gated_delta_head (src/executor.cpp:121-155) for state rows [16 y, 16 y +
 // 16) of value head x over `count` tokens in order: each wave keeps four
 // rows in registers through them, a lane holding two of a row's 128 values
@@ -651,28 +653,77 @@ __device__ __forceinline__ void gated_delta_rows_of_head(const float *convolved,
     for (uint32_t j = 0; j < kRows; ++j) {
         s[j] = state[j * (kLinearHead / 2u) + lane];
     }
-    for (uint32_t b = 0; b < count; ++b) {
-        const float *token = convolved + static_cast<size_t>(b) * kChannels;
-        const float2 q = reinterpret_cast<const float2 *>(token + static_cast<size_t>(kh) * kLinearHead)[lane];
-        const float2 k = reinterpret_cast<const float2 *>(token + kQkSize + static_cast<size_t>(kh) * kLinearHead)[lane];
-        const float *v = token + 2u * kQkSize + static_cast<size_t>(h) * kLinearHead;
-        const float beta_value = sigmoid_of(beta[static_cast<size_t>(b) * kValueHeads + h]);
+    // every token's decay and beta gate of the head, one thread a token
+    // (count <= kDeltaTokens), so the rows' loop does not wait on them
+    __shared__ float token_decay[kDeltaTokens], token_beta[kDeltaTokens];
+    for (uint32_t b = threadIdx.x; b < count; b += blockDim.x) {
+        token_beta[b] = sigmoid_of(beta[static_cast<size_t>(b) * kValueHeads + h]);
         const float biased = alpha[static_cast<size_t>(b) * kValueHeads + h] + bias;
         const float softplus = biased > 20.0f ? biased : log1pf(expf(biased));
-        const float decay = expf(-rate * softplus);
+        token_decay[b] = expf(-rate * softplus);
+    }
+    __syncthreads();
+    // a token's inputs, loaded kAhead tokens before its update (a ring of
+    // registers; a load past the last token reloads the last, unused)
+    struct TokenIn {
+        float2 q, k;
+        float v[kRows];
+    };
+    const auto load_token = [&](uint32_t b, TokenIn &in) {
+        const float *token = convolved + static_cast<size_t>(b) * kChannels;
+        in.q = reinterpret_cast<const float2 *>(token + static_cast<size_t>(kh) * kLinearHead)[lane];
+        in.k = reinterpret_cast<const float2 *>(token + kQkSize + static_cast<size_t>(kh) * kLinearHead)[lane];
+        const float *v = token + 2u * kQkSize + static_cast<size_t>(h) * kLinearHead + row0;
+#pragma unroll
+        for (uint32_t j = 0; j < kRows; ++j) {
+            in.v[j] = v[j];
+        }
+    };
+    const auto update = [&](uint32_t b, const TokenIn &in) {
+        const float beta_value = token_beta[b];
+        const float decay = token_decay[b];
+        // the rows' chains are independent: one block of code, one store
+        float attended[kRows];
 #pragma unroll
         for (uint32_t j = 0; j < kRows; ++j) {
             s[j].x *= decay;
             s[j].y *= decay;
-            const float prediction = wave_sum(s[j].x * k.x + s[j].y * k.y);
-            const float delta = (v[row0 + j] - prediction) * beta_value;
-            s[j].x += k.x * delta;
-            s[j].y += k.y * delta;
-            const float attended = wave_sum(s[j].x * q.x + s[j].y * q.y);
-            if (lane == 0) {
-                output[static_cast<size_t>(b) * kValueSize + static_cast<size_t>(h) * kLinearHead +
-                       row0 + j] = attended * output_scale;
-            }
+            const float prediction = wave_sum(s[j].x * in.k.x + s[j].y * in.k.y);
+            const float delta = (in.v[j] - prediction) * beta_value;
+            s[j].x += in.k.x * delta;
+            s[j].y += in.k.y * delta;
+            attended[j] = wave_sum(s[j].x * in.q.x + s[j].y * in.q.y) * output_scale;
+        }
+        static_assert(kRows == 4, "one float4 of outputs per token");
+        if (lane == 0) {
+            *reinterpret_cast<float4 *>(output + static_cast<size_t>(b) * kValueSize +
+                                        static_cast<size_t>(h) * kLinearHead + row0) =
+                make_float4(attended[0], attended[1], attended[2], attended[3]);
+        }
+    };
+    // ring slot u holds token b0 + u; each slot is refilled (kAhead tokens
+    // on) right after its token's update, in whole blocks of kAhead tokens
+    // with every slot index a constant, so no register of a load in flight
+    // is ever copied
+    constexpr uint32_t kAhead = 8;
+    TokenIn ring[kAhead];
+#pragma unroll
+    for (uint32_t u = 0; u < kAhead; ++u) {
+        load_token(u < count ? u : count - 1u, ring[u]);
+    }
+    uint32_t b0 = 0;
+    for (; b0 + kAhead <= count; b0 += kAhead) {
+#pragma unroll
+        for (uint32_t u = 0; u < kAhead; ++u) {
+            update(b0 + u, ring[u]);
+            const uint32_t next = b0 + u + kAhead;
+            load_token(next < count ? next : count - 1u, ring[u]);
+        }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kAhead; ++u) {
+        if (b0 + u < count) {
+            update(b0 + u, ring[u]);
         }
     }
 #pragma unroll
@@ -846,6 +897,7 @@ __global__ __launch_bounds__(256) void k_linear_core_rows(const float *qkv, cons
         const float softplus = biased > 20.0f ? biased : log1pf(expf(biased));
         const float decay = expf(-rate * softplus);
         float *out = recurrent_output + static_cast<size_t>(r) * kValueSize + static_cast<size_t>(h) * kLinearHead;
+        float attended[kRows];  // the rows' chains in one block of code
 #pragma unroll
         for (uint32_t j = 0; j < kRows; ++j) {
             s[j].x *= decay;
@@ -854,9 +906,12 @@ __global__ __launch_bounds__(256) void k_linear_core_rows(const float *qkv, cons
             const float delta = (vv[wave * kRows + j] - prediction) * beta_value;
             s[j].x += k.x * delta;
             s[j].y += k.y * delta;
-            const float attended = wave_sum(s[j].x * q.x + s[j].y * q.y);
-            if (lane == 0) {
-                coherent_store(out + row0 + j, attended * output_scale);
+            attended[j] = wave_sum(s[j].x * q.x + s[j].y * q.y) * output_scale;
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (uint32_t j = 0; j < kRows; ++j) {
+                coherent_store(out + row0 + j, attended[j]);
             }
         }
 #pragma unroll
@@ -1167,10 +1222,15 @@ void linear_attention_chunk(adi_hip_context *ctx, const adi_hip_linear_attention
         launch(ctx, "linear_conv_history", k_conv_history, dim3(kChannels / 256), dim3(256), 0,
                static_cast<const float *>(qkv), count, convolution_state);
     }
-    launch(ctx, "gated_delta", k_gated_delta, dim3(kValueHeads, kLinearHead / kDeltaRows),
-           dim3(256), 0, static_cast<const float *>(convolved), static_cast<const float *>(alpha),
-           static_cast<const float *>(beta), L->alpha_bias, L->a_log, count, recurrent_state,
-           recurrent_output);
+    // at most kDeltaTokens tokens a launch; the state carries over in order
+    for (uint32_t b0 = 0; b0 < count; b0 += kDeltaTokens) {
+        const uint32_t n = count - b0 < kDeltaTokens ? count - b0 : kDeltaTokens;
+        launch(ctx, "gated_delta", k_gated_delta, dim3(kValueHeads, kLinearHead / kDeltaRows), dim3(256), 0,
+               static_cast<const float *>(convolved + static_cast<size_t>(b0) * kChannels),
+               static_cast<const float *>(alpha + static_cast<size_t>(b0) * kValueHeads),
+               static_cast<const float *>(beta + static_cast<size_t>(b0) * kValueHeads), L->alpha_bias, L->a_log,
+               n, recurrent_state, recurrent_output + static_cast<size_t>(b0) * kValueSize);
+    }
     launch(ctx, "linear_norm_gate", k_linear_norm_gate, dim3(kValueHeads, count),
            dim3(kLinearHead), 0, static_cast<const float *>(recurrent_output), L->norm,
            static_cast<const float *>(gate), normalized);
