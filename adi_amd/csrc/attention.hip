@@ -632,13 +632,14 @@ constexpr uint32_t kDeltaTokens = 1024;  // tokens of one k_gated_delta launch, 
 // 16) of value head x over `count` tokens in order: each wave keeps four
 // rows in registers through them, a lane holding two of a row's 128 values
 // (src/simd.cpp:108-127); the state is read and written once.
+template <uint32_t WAVES>
 __device__ __forceinline__ void gated_delta_rows_of_head(const float *convolved, const float *alpha,
                                                          const float *beta,
                                                          const uint16_t *alpha_bias,
                                                          const uint16_t *a_log, uint32_t count,
                                                          float *recurrent, float *output) {
 #pragma clang fp contract(off)
-    constexpr uint32_t kRows = kDeltaRows / 4u;
+    constexpr uint32_t kRows = kDeltaRows / WAVES;  // rows of a wave
     const uint32_t h = blockIdx.x;
     const uint32_t kh = h / (kValueHeads / kKeyHeads);
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -694,11 +695,16 @@ __device__ __forceinline__ void gated_delta_rows_of_head(const float *convolved,
             s[j].y += in.k.y * delta;
             attended[j] = wave_sum(s[j].x * in.q.x + s[j].y * in.q.y) * output_scale;
         }
-        static_assert(kRows == 4, "one float4 of outputs per token");
         if (lane == 0) {
-            *reinterpret_cast<float4 *>(output + static_cast<size_t>(b) * kValueSize +
-                                        static_cast<size_t>(h) * kLinearHead + row0) =
-                make_float4(attended[0], attended[1], attended[2], attended[3]);
+            float *dst = output + static_cast<size_t>(b) * kValueSize + static_cast<size_t>(h) * kLinearHead + row0;
+            if constexpr (kRows == 4) {
+                *reinterpret_cast<float4 *>(dst) = make_float4(attended[0], attended[1], attended[2], attended[3]);
+            } else if constexpr (kRows == 2) {
+                *reinterpret_cast<float2 *>(dst) = make_float2(attended[0], attended[1]);
+            } else {
+                static_assert(kRows == 1, "one, two or four rows a wave");
+                dst[0] = attended[0];
+            }
         }
     };
     // ring slot u holds token b0 + u; each slot is refilled (kAhead tokens
@@ -732,12 +738,13 @@ __device__ __forceinline__ void gated_delta_rows_of_head(const float *convolved,
     }
 }
 
-// Block (value head, row block) over the chunk's `count` tokens.
-__global__ __launch_bounds__(256) void k_gated_delta(const float *convolved, const float *alpha,
+// Block (value head, row block) over the chunk's `count` tokens: sixteen
+// waves of one row (four waves a SIMD, each hiding the others' reductions).
+__global__ __launch_bounds__(1024) void k_gated_delta(const float *convolved, const float *alpha,
                                                      const float *beta, const uint16_t *alpha_bias,
                                                      const uint16_t *a_log, uint32_t count,
                                                      float *recurrent, float *output) {
-    gated_delta_rows_of_head(convolved, alpha, beta, alpha_bias, a_log, count, recurrent, output);
+    gated_delta_rows_of_head<16>(convolved, alpha, beta, alpha_bias, a_log, count, recurrent, output);
 }
 
 // Block (value head, row block, r): one token of sequence r with its own
@@ -748,7 +755,7 @@ __global__ __launch_bounds__(256) void k_gated_delta_rows(const float *convolved
                                                           const uint16_t *a_log, LinearRows rows,
                                                           float *output) {
     const uint32_t r = blockIdx.z;
-    gated_delta_rows_of_head(convolved + static_cast<size_t>(r) * kChannels,
+    gated_delta_rows_of_head<4>(convolved + static_cast<size_t>(r) * kChannels,
                              alpha + static_cast<size_t>(r) * kValueHeads,
                              beta + static_cast<size_t>(r) * kValueHeads, alpha_bias, a_log, 1,
                              rows.recurrent[r], output + static_cast<size_t>(r) * kValueSize);
@@ -1225,7 +1232,7 @@ void linear_attention_chunk(adi_hip_context *ctx, const adi_hip_linear_attention
     // at most kDeltaTokens tokens a launch; the state carries over in order
     for (uint32_t b0 = 0; b0 < count; b0 += kDeltaTokens) {
         const uint32_t n = count - b0 < kDeltaTokens ? count - b0 : kDeltaTokens;
-        launch(ctx, "gated_delta", k_gated_delta, dim3(kValueHeads, kLinearHead / kDeltaRows), dim3(256), 0,
+        launch(ctx, "gated_delta", k_gated_delta, dim3(kValueHeads, kLinearHead / kDeltaRows), dim3(1024), 0,
                static_cast<const float *>(convolved + static_cast<size_t>(b0) * kChannels),
                static_cast<const float *>(alpha + static_cast<size_t>(b0) * kValueHeads),
                static_cast<const float *>(beta + static_cast<size_t>(b0) * kValueHeads), L->alpha_bias, L->a_log,
