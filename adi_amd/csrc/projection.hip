@@ -466,9 +466,13 @@ __device__ __forceinline__ void expert_prefetch(const MoeGemv &m, const uint4 *s
             // their registers and nothing waits on them until the compute
             const uint32_t t = valid[g] ? tile[g] : 0u;
             const uint32_t *src = words + static_cast<size_t>(t) * 12u + quad * 3u;
-            st.d[g][0] = __builtin_nontemporal_load(src);
-            st.d[g][1] = __builtin_nontemporal_load(src + 1);
-            st.d[g][2] = __builtin_nontemporal_load(src + 2);
+            // the lane's three dwords in one 12-byte load (each load
+            // instruction takes the CU's address path once)
+            typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+            const u32x3 w = __builtin_nontemporal_load(reinterpret_cast<const u32x3 *>(src));
+            st.d[g][0] = w.x;
+            st.d[g][1] = w.y;
+            st.d[g][2] = w.z;
             const uint32_t tr = t >> a.tc_shift, tc = t & (tile_columns - 1u);
             st.gamma[g] = gamma_row[wave_slot(tr, tc, a.tile_rows, tile_columns)];
         }
@@ -1921,6 +1925,32 @@ __device__ __forceinline__ void few_wait_total(uint32_t *sync, uint32_t first, u
     }
 }
 
+// Waits until word(t) >= target(t) for every t < n (n <= 64): one lane a
+// counter, all of them polled in one round of loads (bounded like
+// wait_count, error bit `bit`). One wait before a run of prefetched items
+// instead of one per item: a coherent poll issued behind an item's prefetch
+// loads would wait for them too (vmcnt counts in order).
+template <typename Word, typename Target>
+__device__ __forceinline__ void few_wait_each(Word &&word, Target &&target, uint32_t n, uint32_t lane,
+                                              uint32_t *error, uint32_t bit) {
+    for (uint32_t spins = 0;; ++spins) {
+        bool ready = true;
+        if (lane < n) {
+            ready = coherent_load(word(lane)) >= target(lane);
+        }
+        if (__builtin_amdgcn_ballot_w64(!ready) == 0u) {
+            return;
+        }
+        if (spins >= kSpinLimit) {
+            if (lane == 0) {
+                __hip_atomic_fetch_or(error, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 // Two-level ticket over the grid from group counters `first` and top counter
 // `top`: true in the one caller that completes it.
 __device__ __forceinline__ bool few_ticket(uint32_t *sync, uint32_t first, uint32_t top, uint32_t b,
@@ -2332,11 +2362,16 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_decode_few(MoeDecodeFew a)
         const uint32_t which = il / a.gu.expert_items_per_slot;
         const uint32_t item = il % a.gu.expert_items_per_slot;
         auto index = [&](uint32_t t) { return ((which * a.gu.max_active + slot_of(t)) << a.gu.item_shift) + item; };
+        // every slot's x_hat rows of this entry (built in P1) before the
+        // first item, so no poll waits behind a prefetch
+        few_wait_each([&](uint32_t t) { return few_word(sync, few_sync::kXReady + 2u * slot_of(t) + which); },
+                      [&](uint32_t t) {
+                          const uint4 info = slots[slot_of(t)];
+                          return kGemvWaves * (info.z - info.y);
+                      },
+                      n_slots, lane, error, 4u);
         auto stage = [&](uint32_t t, ExpertStage &st) {
-            const uint32_t s = slot_of(t);
-            const uint4 info = slots[s];
             expert_prefetch(a.gu, slots, index(t), half, lane, st, nullptr, false);
-            wait_count(few_word(sync, few_sync::kXReady + 2u * s + which), kGemvWaves * (info.z - info.y), error, 4u);
             expert_load_x(a.gu, index(t), half, lane, st);
         };
         // plain stores: only this XCD's SwiGLU rows read these Z slices
