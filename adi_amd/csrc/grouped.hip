@@ -317,40 +317,6 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
             return __builtin_bit_cast(BChunk, __builtin_amdgcn_raw_buffer_load_b128(src, off, soff, 0));
         }
     };
-    // D register r of lane l: position 32 cb + l % 32, block row
-    // (r % 4) + 8 (r / 4) + 4 kh. An item's stores go out after the next
-    // item's first loads: vmcnt counts loads and stores in one queue, so
-    // stores issued first would hold the next item's first waits until
-    // they reach memory.
-    f32x16 acc[2][CB];
-    struct Pending {
-        float *z;
-        uint32_t rows, p0, end, tr0;
-        bool live;
-    } pending = {nullptr, 0u, 0u, 0u, 0u, false};
-    const auto store_pending = [&]() {
-        if (pending.z == nullptr) {
-            return;
-        }
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) {
-            const uint32_t p = pending.p0 + 32u * cb + m;
-            if (pending.live && p < pending.end) {
-#pragma unroll
-                for (int rb = 0; rb < 2; ++rb) {
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const uint32_t row = (pending.tr0 + 2u * rb) * kTile + 8u * g + 4u * kh;
-                        if (row < pending.rows) {
-                            *reinterpret_cast<f32x4 *>(pending.z + static_cast<size_t>(p) * pending.rows + row) =
-                                f32x4{acc[rb][cb][4 * g], acc[rb][cb][4 * g + 1], acc[rb][cb][4 * g + 2],
-                                      acc[rb][cb][4 * g + 3]};
-                        }
-                    }
-                }
-            }
-        }
-    };
     const uint32_t rounds = (total + kExpertGroups - 1u) / kExpertGroups;
     for (uint32_t round = worker; round < rounds; round += workers) {
         const uint32_t item_any = round * kExpertGroups + group;
@@ -372,15 +338,9 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
         const uint32_t within = local - starts[slot];
         const uint32_t rq = within % J.row_groups;
         const uint32_t pg = within / J.row_groups;
-        // the slot is uniform and the table does not change during the
-        // launch: its entry comes through the scalar cache (a vector load
-        // here would wait on every load and store still in flight)
-        uint4 info = make_uint4(0u, 0u, J.max_positions, 0u);
-        if (J.slot_info != nullptr) {
-            const u32x4 v = reinterpret_cast<const __attribute__((address_space(4))) u32x4 *>(
-                reinterpret_cast<uintptr_t>(J.slot_info))[slot];
-            info = make_uint4(v.x, v.y, v.z, v.w);
-        }
+        // the slot is uniform: its entry comes through the scalar cache
+        const uint4 info = J.slot_info != nullptr ? J.slot_info[slot]
+                                                  : make_uint4(0u, 0u, J.max_positions, 0u);
         const uint32_t first = __builtin_amdgcn_readfirstlane(info.y);
         const uint32_t mat = __builtin_amdgcn_readfirstlane(info.x);
         const uint32_t end = __builtin_amdgcn_readfirstlane(info.z);
@@ -422,44 +382,21 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
         wv.sh0 = 48u - pos;
         wv.sh1 = 36u - pos;
 
-        // gamma of the tile at anti-diagonal d = tr_block + e sits in wave
-        // slot R_t + C_t - 1 - d, one less past the main anti-diagonal
-        // (src/codec_cache.cpp:117-147); slots past the matrix read 0 and
-        // belong to tiles that are never stored
-        const uint32_t e = gthread;  // tile_columns + 35 <= 512
-        uint16_t g;
-        {
-            const __amdgpu_buffer_rsrc_t gbuf =
-                buffer_over(a.gamma + mat * a.gamma_stride, (a.tile_rows + tile_columns) * 2u);
-            const uint32_t top = a.tile_rows + tile_columns - 1u;
-            const uint32_t d = tr_block + e;
-            const uint32_t gslot = top - d - (d >= tile_columns ? 1u : 0u);
-            g = __builtin_amdgcn_raw_buffer_load_b16(gbuf, gslot * 2u, 0, 0);
-        }
-        // the K loop's first B and word loads (a K of at least kDepth steps):
-        // B of step s waits in bv[s % 4] (registers) until step s - 1 writes
-        // it to ring slot s % 2; the words of step s wait in ws[s % 4]
-        const bool pipelined = steps % kDepth == 0;
-        BChunk bv[kDepth];
-        ExpertWords ws[kDepth];
-        if (pipelined) {
-#pragma unroll
-            for (int u = 0; u < kDepth; ++u) {
-                __builtin_amdgcn_sched_barrier(0);
-                bv[u] = load_b(xsrc, b_off, u * 64u);
-                if (u < kDepth - 1) {
-                    expert_words(wv, u, ws[u]);
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        // the previous item's outputs, behind this item's first loads
-        store_pending();
-        __builtin_amdgcn_sched_barrier(0);
         // the previous item's readers of the gamma rows and the ring are done
         __syncthreads();
         {
+            // gamma of the tile at anti-diagonal d = tr_block + e sits in wave
+            // slot R_t + C_t - 1 - d, one less past the main anti-diagonal
+            // (src/codec_cache.cpp:117-147); slots past the matrix read 0 and
+            // belong to tiles that are never stored
+            const __amdgpu_buffer_rsrc_t gbuf =
+                buffer_over(a.gamma + mat * a.gamma_stride, (a.tile_rows + tile_columns) * 2u);
+            const uint32_t top = a.tile_rows + tile_columns - 1u;
             uint16_t *rows = reinterpret_cast<uint16_t *>(gamma_rows[group]);
+            const uint32_t e = gthread;  // tile_columns + 35 <= 512
+            const uint32_t d = tr_block + e;
+            const uint32_t gslot = top - d - (d >= tile_columns ? 1u : 0u);
+            const uint16_t g = __builtin_amdgcn_raw_buffer_load_b16(gbuf, gslot * 2u, 0, 0);
             if (e < tile_columns + kBlockTileRows + 3u) {
 #pragma unroll
                 for (uint32_t q = 0; q < 4u; ++q) {
@@ -470,6 +407,7 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
                 }
             }
         }
+        f32x16 acc[2][CB];
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
@@ -498,7 +436,7 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
         // and multiplied with every live block (the slot's later blocks skip
         // their MFMAs, not the decode)
         auto k_loop = [&]<int LIVE>() {
-            if (!pipelined) {
+            if (steps % kDepth != 0) {
                 // short K (under 4 steps): one step at a time
                 for (uint32_t kc = 0; kc < steps; ++kc) {
                     const BChunk bv = load_b(xsrc, b_off, kc * 64u);
@@ -514,9 +452,21 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
                     __syncthreads();
                 }
             } else {
-                // the first loads went out before the previous item's stores;
-                // loads past the last step reload it (in bounds, unused), so
-                // the loop body has no branch
+                // B of step s waits in bv[s % 4] (registers) until step s - 1
+                // writes it to ring slot s % 2; the words of step s wait in
+                // ws[s % 4]. Loads past the last step reload it (in bounds,
+                // unused), so the loop body has no branch.
+                BChunk bv[kDepth];
+                ExpertWords ws[kDepth];
+#pragma unroll
+                for (int u = 0; u < kDepth; ++u) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    bv[u] = load_b(xsrc, b_off, u * 64u);
+                    if (u < kDepth - 1) {
+                        expert_words(wv, u, ws[u]);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
                 *reinterpret_cast<BChunk *>(ring + b_store) = bv[0];
                 bv[0] = load_b(xsrc, b_off, min(static_cast<uint32_t>(kDepth), last) * 64u);
                 __syncthreads();
@@ -549,9 +499,28 @@ __global__ __launch_bounds__(512 * GROUPS) void k_expert_mfma(ExpertMfmaJobs J) 
         } else {
             k_loop.template operator()<1>();
         }
-        pending = {a.z + half * a.z_split_stride, a.rows, p0, end, tr0, live};
+        // D register r of lane l: position 32 cb + l % 32, block row
+        // (r % 4) + 8 (r / 4) + 4 kh
+        float *z = a.z + half * a.z_split_stride;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+            const uint32_t p = p0 + 32u * cb + m;
+            if (live && p < end) {
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const uint32_t row = (tr0 + 2u * rb) * kTile + 8u * g + 4u * kh;
+                        if (row < a.rows) {
+                            *reinterpret_cast<f32x4 *>(z + static_cast<size_t>(p) * a.rows + row) =
+                                f32x4{acc[rb][cb][4 * g], acc[rb][cb][4 * g + 1], acc[rb][cb][4 * g + 2],
+                                      acc[rb][cb][4 * g + 3]};
+                        }
+                    }
+                }
+            }
+        }
     }
-    store_pending();
 }
 
 // ---- NE -------------------------------------------------------------------
