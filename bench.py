@@ -794,8 +794,8 @@ def main():
         cpu_child(args)
         return
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is "
-                          "described in DESIGN.md but not built", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this benchmark runs on one GPU; sharding across GPUs is "
+                          "designed but not built", "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
     from adi_amd import hip

@@ -101,7 +101,7 @@ int adi_hip_set_workspace_limit(adi_hip_context *ctx, size_t bytes);
 /* Device buffers for callers that build descriptors without the HIP runtime
  * (a host-compiled Backend shim). No reference counterpart: the reference's
  * matrices are views into the mmap (include/adi/kernels.hpp:9-77), which
- * this build copies to HBM once. Copies are synchronous on the context's
+ * this library copies to HBM once. Copies are synchronous on the context's
  * stream. */
 int adi_hip_device_alloc(adi_hip_context *ctx, size_t bytes, void **out);
 void adi_hip_device_free(adi_hip_context *ctx, void *pointer);

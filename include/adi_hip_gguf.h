@@ -191,7 +191,7 @@ int adi_hip_gguf_upload_decoder_layer(adi_hip_context *ctx, const adi_hip_gguf *
  * |prot_rows i32 {n} with |prot_dense bf16 {hidden, n} (both or neither; rows
  * inside their chunk; finite); hf.model.language_model.norm.weight bf16
  * {hidden}. The vocabulary and hidden width are the embedding's
- * (mach.embedding.q_packed; this build takes any vocabulary divisible by 8,
+ * (mach.embedding.q_packed; this library takes any vocabulary divisible by 8,
  * where the reference accepts 248,320 only). The upload lays the chunks end
  * to end as one head of vocabulary rows, protected rows renumbered to it
  * (the logits are the chunks' in order), and returns the final norm's device

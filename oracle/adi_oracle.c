@@ -1,7 +1,7 @@
 /*
  * adi_oracle.c -- CPU restatement of ADI's packed-weight hot path.
  *
- * TEST INFRASTRUCTURE ONLY: this is the checker the HIP kernels are compared
+ * TEST INFRASTRUCTURE ONLY: the reference the HIP kernels are compared
  * against (tests, smoke check, benchmark CPU-baseline leg). Nothing in the
  * product links it.
  *

@@ -1,7 +1,7 @@
 // backend_driver.cpp -- TEST INFRASTRUCTURE ONLY.
 //
 // C entry points that run one adi::Backend entry, from either the reference's
-// cpu_backend() (src/backend.cpp:11-26) or this build's hip_backend(), on host
+// cpu_backend() (src/backend.cpp:11-26) or the HIP library's hip_backend(), on host
 // arrays, so the parity tests can drive the reference's own dispatch table.
 // Linked with the reference's compiled runtime into _ref/libadi_backend.so.
 // Every function returns 0, 1 for std::invalid_argument or 2 for any other

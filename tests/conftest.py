@@ -30,7 +30,7 @@ def ref():
 @pytest.fixture(scope="session")
 def gpu():
     """A context on cuda:0; fails loudly (no skip) when the library or the
-    GPU is missing, since GPU tests are selected only on a GPU box."""
+    GPU is missing, since GPU tests are selected only on a machine with one."""
     import torch
     from adi_amd import hip
     assert torch.cuda.is_available(), "GPU tests need an MI355X"

@@ -1,4 +1,4 @@
-"""Pins the oracle (oracle/adi_oracle.c) before it is trusted as the checker:
+"""Pins the oracle (oracle/adi_oracle.c) before the GPU tests compare against it:
 
 * against the golden vectors the compiled reference produced
   (tests/golden/golden.npz, written by tests/golden/make_golden.py);
