@@ -284,14 +284,14 @@ struct TiledShape {
 template <int LANES, bool FUSED, uint32_t BLOCK, uint32_t THREADS>
 __global__ __launch_bounds__(THREADS) void k_bf16_tiled(
     const uint16_t *__restrict__ w, uint32_t rows, const uint16_t *__restrict__ w_extra,
-    uint32_t columns, const float *__restrict__ x, uint32_t batch, float *__restrict__ out,
-    float *__restrict__ out_extra) {
+    uint32_t extra_rows, uint32_t columns, const float *__restrict__ x, uint32_t batch,
+    float *__restrict__ out, float *__restrict__ out_extra) {
 #pragma clang fp contract(off)
     using S = TiledShape<LANES, BLOCK, THREADS>;
     static_assert(S::T >= 1 && S::R >= 1 && S::T * S::token_groups == BLOCK, "tile shape");
     __shared__ float xs[BLOCK][LANES][S::pitch];
     __shared__ float ws[BLOCK][LANES][S::pitch];
-    const uint32_t total_rows = rows + (w_extra != nullptr ? 1u : 0u);
+    const uint32_t total_rows = rows + (w_extra != nullptr ? extra_rows : 0u);
     // XCD-aware tiles: blocks are dealt to the eight XCDs round robin, so
     // block id goes to XCD id % 8. With at least eight token tiles XCD x
     // takes token tiles x, x + 8, ... with every row tile, and its L2 holds
@@ -347,7 +347,8 @@ __global__ __launch_bounds__(THREADS) void k_bf16_tiled(
             const uint32_t idx = u * THREADS + threadIdx.x;  // rows x 32 uint4
             const uint32_t r = idx >> 5, k = (idx & 31u) * 8u;
             const uint32_t row = min(row0 + r, total_rows - 1u);
-            const uint16_t *src = row < rows ? w + static_cast<size_t>(row) * columns : w_extra;
+            const uint16_t *src = row < rows ? w + static_cast<size_t>(row) * columns
+                                             : w_extra + static_cast<size_t>(row - rows) * columns;
             wv[u] = *reinterpret_cast<const uint4 *>(src + c0 + k);
         }
     };
@@ -434,7 +435,7 @@ __global__ __launch_bounds__(THREADS) void k_bf16_tiled(
             if (row < rows) {
                 out[static_cast<size_t>(tok) * rows + row] = sum;
             } else {
-                out_extra[tok] = sum;
+                out_extra[static_cast<size_t>(tok) * extra_rows + (row - rows)] = sum;
             }
         }
     }
@@ -836,10 +837,10 @@ void launch_bf16_ordered_extra(adi_hip_context *ctx, const uint16_t *w, uint32_t
         const uint32_t threads = small ? 128u : kTiledLargeThreads;
         if (lanes == 8) {
             launch(ctx, "router", small ? k_bf16_tiled<8, false, 8, 128> : k_bf16_tiled<8, false, 16, kTiledLargeThreads>,
-                   grid, dim3(threads), 0, w, rows, w_extra, columns, x, batch, out, out_extra);
+                   grid, dim3(threads), 0, w, rows, w_extra, 1u, columns, x, batch, out, out_extra);
         } else {
             launch(ctx, "router", small ? k_bf16_tiled<16, true, 8, 128> : k_bf16_tiled<16, true, 16, kTiledLargeThreads>,
-                   grid, dim3(threads), 0, w, rows, w_extra, columns, x, batch, out, out_extra);
+                   grid, dim3(threads), 0, w, rows, w_extra, 1u, columns, x, batch, out, out_extra);
         }
         return;
     }
@@ -882,6 +883,24 @@ void launch_bf16_pair(adi_hip_context *ctx, const uint16_t *w0, uint32_t rows0, 
         } else {
             launch(ctx, "bf16_pair", batch == 1 ? k_bf16_lds<16, true, 8> : k_bf16_lds<16, true, 32>, grid,
                    dim3(64), lds, w0, rows0, w1, rows1, columns, x, batch, out0, out1);
+        }
+        return;
+    }
+    if ((lanes == 8 || lanes == 16) && batch >= kTiledBatch && columns % kTiledChunk == 0 &&
+        (addresses & 15u) == 0) {
+        // both matrices' rows in one launch of the register-tiled kernel
+        const bool small = batch <= kTiledSmallBatch;
+        const uint32_t block = small ? 8u : 16u;
+        const uint32_t token_tiles = ceil_div(batch, block), row_tiles = ceil_div(rows0 + rows1, block);
+        const dim3 grid(token_tiles >= 8u ? 8u * ceil_div(token_tiles, 8u) * row_tiles
+                                          : 8u * ceil_div(row_tiles, 8u) * token_tiles);
+        const uint32_t threads = small ? 128u : kTiledLargeThreads;
+        if (lanes == 8) {
+            launch(ctx, "bf16_pair", small ? k_bf16_tiled<8, false, 8, 128> : k_bf16_tiled<8, false, 16, kTiledLargeThreads>,
+                   grid, dim3(threads), 0, w0, rows0, w1, rows1, columns, x, batch, out0, out1);
+        } else {
+            launch(ctx, "bf16_pair", small ? k_bf16_tiled<16, true, 8, 128> : k_bf16_tiled<16, true, 16, kTiledLargeThreads>,
+                   grid, dim3(threads), 0, w0, rows0, w1, rows1, columns, x, batch, out0, out1);
         }
         return;
     }

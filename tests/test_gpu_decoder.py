@@ -92,14 +92,15 @@ def wide_layers(gpu):
             for i in (0, 3)]
 
 
-@pytest.mark.parametrize("count", [1, 2, 4])
+@pytest.mark.parametrize("count", [1, 2, 4, 40])
 def test_layer_norms_folded_equal_separate_launches(gpu, wide_layers, count):
     """At hidden 2048 a layer of 1-4 tokens runs its input RMS norm (with the
-    residual add) inside its first attention projection launch, the
-    post-attention norm inside its output projection launch, and the Gated
-    DeltaNet's alpha and beta matmuls as one launch; with the one-launch
-    paths off they are launches of their own. Hidden rows and every state
-    are bit-identical over three steps of both layers."""
+    residual add) inside its first attention projection launch and the
+    post-attention norm inside its output projection launch; at any token
+    count the Gated DeltaNet's alpha and beta matmuls are one launch (the
+    small-batch kernel below 32 tokens, the register-tiled one from 32). With
+    the one-launch paths off they are launches of their own. Hidden rows and
+    every state are bit-identical over three steps of both layers."""
     rng = syn.rng_for(51, count)
     x0 = syn.hidden_states(rng, count, 2048)
 
