@@ -3340,10 +3340,73 @@ void ne_matmul_group(adi_hip_context *ctx, const adi_hip_ne_matrix *const *m, ui
         launch_add_rms_norm(ctx, in->row, in->add, in->weight, m[0]->columns, batch, in->out);
         inputs = in->out;
     }
+    const uint32_t columns = m[0]->columns;
+    bool grouped = ctx->fused_moe && count > 1 && batch >= kNeMfmaBatch && columns >= 32 && wave_width(columns) &&
+                   size_t(batch) * columns * 2u < (size_t(1) << 32) && aligned_to(inputs, 16);
     for (uint32_t j = 0; j < count; ++j) {
-        const int status = adi_hip_ne_matmul(ctx, m[j], inputs, batch, outputs[j]);
-        if (status != ADI_HIP_OK) {
-            fail(status, ctx->last_error());
+        grouped = grouped && m[j]->columns == columns && m[j]->rows % kTile == 0;
+    }
+    if (grouped) {
+        // the MFMA path of adi_hip_ne_matmul for every matrix, with one
+        // prologue launch for all of their x_hat and one MFMA launch for two
+        // matrices of one shape and codebook (the same kernels and arithmetic)
+        auto &ws = ctx->workspace;
+        ws.used = 0;
+        uint32_t splits[kNeFusedJobs];
+        size_t bytes = 0;
+        for (uint32_t j = 0; j < count; ++j) {
+            splits[j] = ne_mfma_slices(m[j]->rows, columns, batch);
+            bytes += Workspace::round(size_t(batch) * columns * 4) +
+                     Workspace::round(size_t(splits[j]) * batch * m[j]->rows * 4);
+        }
+        ws.ensure(bytes);
+        uint16_t *hi[kNeFusedJobs], *lo[kNeFusedJobs];
+        float *z[kNeFusedJobs];
+        PrologueJobs jobs{};
+        jobs.segments = count;
+        jobs.n = columns;
+        for (uint32_t j = 0; j < count; ++j) {
+            hi[j] = reinterpret_cast<uint16_t *>(ws.take<float>(size_t(batch) * columns));
+            lo[j] = hi[j] + size_t(batch) * columns;
+            z[j] = ws.take<float>(size_t(splits[j]) * batch * m[j]->rows);
+            jobs.seg[j] = PrologueSegment{inputs, nullptr, nullptr, nullptr, m[j]->su, 0,
+                                          XhatOut{nullptr, hi[j], lo[j], 1, batch}, batch};
+        }
+        launch_prologues(ctx, jobs);
+        bool launched[kNeFusedJobs] = {};
+        for (uint32_t j = 0; j < count; ++j) {
+            if (launched[j]) {
+                continue;
+            }
+            NeMfmaJobs J{};
+            J.ne_book = m[j]->codebook->data;
+            for (uint32_t k = j; k < count && J.ne_count < 2u; ++k) {
+                if (launched[k] || m[k]->rows != m[j]->rows || m[k]->codebook->data != J.ne_book) {
+                    continue;
+                }
+                NeMfma &n = J.ne[J.ne_count++];
+                n.trellis = m[k]->trellis;
+                n.weight_scale = m[k]->weight_scale;
+                n.rows = m[k]->rows;
+                n.columns = columns;
+                n.x_hi = hi[k];
+                n.x_lo = lo[k];
+                n.batch = batch;
+                n.z = z[k];
+                launched[k] = true;
+            }
+            launch_ne_mfma(ctx, J);
+        }
+        for (uint32_t j = 0; j < count; ++j) {
+            launch_epilogue_any<int8_t>(ctx, z[j], splits[j], size_t(batch) * m[j]->rows, m[j]->rows, m[j]->sv,
+                                        batch, outputs[j]);
+        }
+    } else {
+        for (uint32_t j = 0; j < count; ++j) {
+            const int status = adi_hip_ne_matmul(ctx, m[j], inputs, batch, outputs[j]);
+            if (status != ADI_HIP_OK) {
+                fail(status, ctx->last_error());
+            }
         }
     }
     if (tail != nullptr) {

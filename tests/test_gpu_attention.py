@@ -141,13 +141,14 @@ def test_linear_attention_rejections(gpu, linear_layer):
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("count", [1, 2, 4])
+@pytest.mark.parametrize("count", [1, 2, 4, 40])
 def test_projection_group_equals_separate_launches(gpu, count):
     """At hidden 2048 the query, key and value projections (Gated DeltaNet:
-    qkv and gate) of 1-4 tokens run as one NE launch; with the one-launch
-    paths switched off they run one projection at a time. Outputs, caches and
-    states are bit-identical, on two calls in a row (the tickets the first
-    call cleared are reused)."""
+    qkv and gate) of 1-4 tokens run as one NE launch, and from 8 tokens they
+    share one prologue launch (key and value one MFMA launch too); with the
+    one-launch paths switched off they run one projection at a time. Outputs,
+    caches and states are bit-identical, on two calls in a row (the tickets
+    the first call cleared are reused)."""
     hidden = 2048
     rng = syn.rng_for(45, count)
     tlut = syn.ne_tlut(rng)
