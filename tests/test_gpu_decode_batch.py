@@ -148,6 +148,47 @@ def test_decode_batch_one_launch_paths_equal_separate_launches(gpu, parts, count
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), i
 
 
+def test_decode_batch_long_histories(gpu, parts):
+    """Two sequences past 1,000 entries decoded in one step: each row's
+    history then splits into 32 parts, where the flash-decoding blocks of
+    the eight query heads of a KV head share an XCD. The logits are
+    bit-identical with the one-launch paths off (norm/rotation, partial and
+    merge launches), and within 1e-3 of the same tokens taken through the
+    single-sequence chunk kernels (a one-token prefill each: 33-34 splits,
+    the kernels the attention tests hold to the oracle at histories up to
+    2,500 entries)."""
+    model = parts["one"]
+    capacity = 1100
+    rng = np.random.default_rng(2024)
+    prompts = [[int(t) for t in rng.integers(3, VOCAB, size=n)] for n in (1030, 1057)]
+
+    def prefilled():
+        seqs = [hip.Sequence(model, capacity) for _ in prompts]
+        for prompt, s in zip(prompts, seqs):
+            hip.prefill(gpu, model, prompt, s, None, ubatch=128)
+        return seqs
+
+    def run(fused):
+        gpu.set_fused_decode(fused)
+        try:
+            seqs = prefilled()
+            print("decode_batch long", fused, flush=True)
+            out = torch.empty((2, VOCAB), dtype=torch.float32, device="cuda")
+            hip.decode_batch(gpu, model, [5, 9], seqs, out)
+            gpu.synchronize()
+            return out.cpu().numpy()
+        finally:
+            gpu.set_fused_decode(True)
+
+    one, separate = run(True), run(False)
+    assert np.array_equal(one.view(np.uint32), separate.view(np.uint32))
+    seqs = prefilled()
+    for b, (s, token) in enumerate(zip(seqs, [5, 9])):
+        logits = torch.empty(VOCAB, dtype=torch.float32, device="cuda")
+        hip.prefill(gpu, model, [token], s, logits, ubatch=128)
+        assert max_rel_error(one[b], logits.cpu().numpy()) <= 1e-3, b
+
+
 def test_fresh_sequences_batched_equal_decoded_alone(gpu, parts):
     """tests/model_batch_test.cpp:24-51: two new sequences decoded as one
     batch give the logits of each decoded alone, and both reach position 1.
