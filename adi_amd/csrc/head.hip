@@ -458,19 +458,30 @@ __global__ __launch_bounds__(kHmThreads) void k_head_mfma(
                 scales + static_cast<size_t>(row_of(t, lane / 4u)) * kHmGroups + 8u * (lane % 4u));
             sreg = *src;
         };
+        // issued in the order the tile loop issues them (first quarter,
+        // scales, the other quarters), so that the loop's counted waits hold
+        // on entry as on every later tile; in another order the compiler can
+        // only wait for every load at the top of each tile
         if (tile < tiles) {
             if constexpr (COALESCED) {
                 load_raw(tile, 0, raw[0]);
+                load_scales(tile);
+                __builtin_amdgcn_sched_barrier(0);
                 load_raw(tile, 1, raw[1]);
+                __builtin_amdgcn_sched_barrier(0);
                 load_raw(tile, 2, raw[2]);
+                __builtin_amdgcn_sched_barrier(0);
                 load_raw(tile, 3, raw[3]);
             } else {
                 load_chunk(tile, 0, w[0]);
+                load_scales(tile);
+                __builtin_amdgcn_sched_barrier(0);
                 load_chunk(tile, 1, w[1]);
+                __builtin_amdgcn_sched_barrier(0);
                 load_chunk(tile, 2, w[2]);
+                __builtin_amdgcn_sched_barrier(0);
                 load_chunk(tile, 3, w[3]);
             }
-            load_scales(tile);
         }
         if (t0 > 0) {
             __syncthreads();  // the previous pass's readers are done with the tables
