@@ -383,6 +383,22 @@ __global__ __launch_bounds__(256) void k_hadamard_block(float *values, uint32_t 
 
 constexpr uint32_t kGemvThreads = 512;
 constexpr uint32_t kGemvWaves = kGemvThreads / kWave;
+
+// A thread's share of the 4 KiB NE table (threads 0 .. kGemvThreads - 1),
+// loaded into registers so that other loads can go out before it is stored.
+constexpr uint32_t kTableWords = 1024u / kGemvThreads;
+__device__ __forceinline__ void load_table_share(const uint32_t *src, uint32_t (&v)[kTableWords]) {
+#pragma unroll
+    for (uint32_t k = 0; k < kTableWords; ++k) {
+        v[k] = src[threadIdx.x + k * kGemvThreads];
+    }
+}
+__device__ __forceinline__ void store_table_share(const uint32_t (&v)[kTableWords], uint32_t *dst) {
+#pragma unroll
+    for (uint32_t k = 0; k < kTableWords; ++k) {
+        dst[threadIdx.x + k * kGemvThreads] = v[k];
+    }
+}
 constexpr size_t kPlaneBytes = size_t(kExpertRows) * 8;  // one component plane
 constexpr uint32_t kMaxSlots = 1024;                     // routed slots staged in LDS
 
@@ -902,6 +918,12 @@ __global__ __launch_bounds__(kGemvThreads) void k_trellis_gemv(MoeGemv m) {
         }
     }
     float *wave_x_lds = shared_x_lds + kFusedSwigluWidth * (1u + owner);
+    // the NE table's words load before the plane: the load counter completes
+    // in order, so the plane's wait covers them
+    uint32_t tab[kTableWords];
+    if (m.ne_count > 0) {
+        load_table_share(static_cast<const uint32_t *>(m.ne_book), tab);
+    }
     if (m.expert_count > 0) {
         // 8192 16-byte rows per plane, 16 per thread, all loads issued first
         constexpr uint32_t kPer = static_cast<uint32_t>(kPlaneBytes / 16) / kGemvThreads;
@@ -935,10 +957,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_trellis_gemv(MoeGemv m) {
         }
     }
     if (m.ne_count > 0) {
-        const uint32_t *src = static_cast<const uint32_t *>(m.ne_book);
-        for (uint32_t i = threadIdx.x; i < 1024u; i += kGemvThreads) {
-            ne_table[i] = src[i];
-        }
+        store_table_share(tab, ne_table);
     }
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63u;
@@ -1503,12 +1522,12 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode_one(MoeDecodeOne a
 
     // ---- P0 ----
     if (!helper) {
+        // the NE table's words go out first; the plane's wait covers them
+        uint32_t tab[kTableWords];
+        load_table_share(static_cast<const uint32_t *>(a.gu.ne_book), tab);
         fill_plane_share(static_cast<const uint4 *>(a.gu.expert_book) + half * (kPlaneBytes / 16),
                          plane_lds);
-        const uint32_t *src = static_cast<const uint32_t *>(a.gu.ne_book);
-        for (uint32_t i = threadIdx.x; i < 1024u; i += kGemvThreads) {
-            ne_table[i] = src[i];
-        }
+        store_table_share(tab, ne_table);
         if (lane == 0) {
             __hip_atomic_fetch_add(&flags[0], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
@@ -2156,13 +2175,13 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_decode_few(MoeDecodeFew a)
     if (threadIdx.x == 0) {
         coherent_add(few_word(sync, few_sync::kLogits + xcd), 1u);
     }
-    // the codebook plane and the NE table
-    fill_plane_share(static_cast<const uint4 *>(a.gu.expert_book) + half * (kPlaneBytes / 16), plane_lds);
+    // the codebook plane and the NE table (its words first; the plane's wait
+    // covers them)
     {
-        const uint32_t *src = static_cast<const uint32_t *>(a.gu.ne_book);
-        for (uint32_t i = threadIdx.x; i < 1024u; i += kGemvThreads) {
-            ne_table[i] = src[i];
-        }
+        uint32_t tab[kTableWords];
+        load_table_share(static_cast<const uint32_t *>(a.gu.ne_book), tab);
+        fill_plane_share(static_cast<const uint4 *>(a.gu.expert_book) + half * (kPlaneBytes / 16), plane_lds);
+        store_table_share(tab, ne_table);
     }
     // the shared expert's gate (blocks 0 .. B - 1) and up (B .. 2B - 1) x_hat of one row
     if (b < 2u * B) {
@@ -2712,19 +2731,52 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
             code[q][1] = __builtin_nontemporal_load(src + 1);
         }
     };
-    load_codes(b);
-    for (uint32_t i = threadIdx.x; i < 1024u; i += kNeFusedThreads) {
-        table[i] = job.table[i];
+    // The block's shares of the NE table and the output signs, and the x_hat
+    // inputs, load before the codes: the load counter completes in order, so
+    // the waits for them leave the codes in flight.
+    constexpr uint32_t kTablePer = 1024u / kNeFusedThreads;
+    constexpr uint32_t kSignPer = kNeFusedMaxRows / 4u / kNeFusedThreads;
+    const uint32_t sign_words = R / 4u;
+    const uint32_t *sv_words = reinterpret_cast<const uint32_t *>(job.sv);
+    uint32_t tab[kTablePer], signs[kSignPer];
+#pragma unroll
+    for (uint32_t k = 0; k < kTablePer; ++k) {
+        tab[k] = job.table[threadIdx.x + k * kNeFusedThreads];
     }
-    for (uint32_t i = threadIdx.x; i < R / 4u; i += kNeFusedThreads) {
-        reinterpret_cast<uint32_t *>(sv_lds)[i] = reinterpret_cast<const uint32_t *>(job.sv)[i];
+#pragma unroll
+    for (uint32_t k = 0; k < kSignPer; ++k) {
+        signs[k] = sv_words[min(threadIdx.x + k * kNeFusedThreads, sign_words - 1u)];
+    }
+    float xs[VC], xv[kMine][VC];
+    load_wave_sign<VC>(job.su + w8 * CH, lane, xs);
+    const bool normed = C == 2048u && a.norm_row != nullptr;
+    if (!normed) {
+#pragma unroll
+        for (uint32_t i = 0; i < kMine; ++i) {
+            const uint32_t p = group + halves * i;
+            if (p < a.batch) {
+                load_wave<VC>(a.x + static_cast<size_t>(p) * C + w8 * CH, lane, xv[i]);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_codes(b);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (uint32_t k = 0; k < kTablePer; ++k) {
+        table[threadIdx.x + k * kNeFusedThreads] = tab[k];
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kSignPer; ++k) {
+        const uint32_t i = threadIdx.x + k * kNeFusedThreads;
+        if (i < sign_words) {
+            reinterpret_cast<uint32_t *>(sv_lds)[i] = signs[k];
+        }
     }
     // with a norm the half's input rows are computed here, into the x_hat
     // rows' place; the first block of the half writes them out
-    const float *x = a.x;
-    size_t x_stride = C;
     if constexpr (C == 2048u) {
-        if (a.norm_row != nullptr) {
+        if (normed) {
             // two rows at a time, one on each 256-thread half of the block
             const uint32_t pair = threadIdx.x >> 8;
             for (uint32_t i0 = 0; group + halves * i0 < a.batch; i0 += 2u) {
@@ -2747,31 +2799,26 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
                 }
                 __syncthreads();  // copied before the x_hat rows overwrite them
             }
-            x = ne_lds;
+#pragma unroll
+            for (uint32_t i = 0; i < kMine; ++i) {
+                const uint32_t p = group + halves * i;
+                if (p < a.batch) {
+                    load_wave<VC>(ne_lds + p * C + w8 * CH, lane, xv[i]);
+                }
+            }
         }
     }
-    // x_hat of the half's input rows (their loads first)
-    {
-        float v[kMine][VC], s[VC];
-        load_wave_sign<VC>(job.su + w8 * CH, lane, s);
+    // x_hat of the half's input rows
 #pragma unroll
-        for (uint32_t i = 0; i < kMine; ++i) {
-            const uint32_t p = group + halves * i;
-            if (p < a.batch) {
-                load_wave<VC>(x + static_cast<size_t>(p) * x_stride + w8 * CH, lane, v[i]);
+    for (uint32_t i = 0; i < kMine; ++i) {
+        const uint32_t p = group + halves * i;
+        if (p < a.batch) {
+#pragma unroll
+            for (int e = 0; e < VC; ++e) {
+                xv[i][e] = xv[i][e] * xs[e];
             }
-        }
-#pragma unroll
-        for (uint32_t i = 0; i < kMine; ++i) {
-            const uint32_t p = group + halves * i;
-            if (p < a.batch) {
-#pragma unroll
-                for (int e = 0; e < VC; ++e) {
-                    v[i][e] = v[i][e] * s[e];
-                }
-                wave_hadamard<VC>(v[i], 1.0f, lane);
-                store_wave<VC>(ne_lds + p * C + w8 * CH, lane, v[i]);
-            }
+            wave_hadamard<VC>(xv[i], 1.0f, lane);
+            store_wave<VC>(ne_lds + p * C + w8 * CH, lane, xv[i]);
         }
     }
     __syncthreads();
