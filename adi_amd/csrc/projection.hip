@@ -2686,7 +2686,7 @@ __device__ void ne_fused_rows(const NeFusedJob &job, float *ne_lds, const int8_t
     }
 }
 
-template <int VC>
+template <int VC, int ROWS>
 __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
 #pragma clang fp contract(off)
     extern __shared__ float ne_lds[];  // x_hat [batch][C], then the outputs [batch][rows]
@@ -2718,17 +2718,29 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
     const uint32_t b = g - job.first_block, blocks = job.blocks;  // within the matrix and half
     uint32_t *ticket = a.ticket + 32u * (2u * j + group);
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    // the codes of the block's first tile row go out first
+    // A round takes ROWS of the block's tile rows (tr, tr + blocks, ...), so
+    // that a wave runs ROWS items between the round's barriers (their x_hat
+    // reads shared).
     constexpr uint32_t kWaveItems = per_row > 8u ? per_row / 8u : 1u;
-    u32x4 code[kWaveItems][2];
+    constexpr uint32_t kRoundRows = ROWS;
+    static_assert(kRoundRows * per_row <= kNeFusedMaxItems, "a round's items fit the partial sums");
+    u32x4 code[kRoundRows][kWaveItems][2];
+    // the codes of the round from tile row tr; a tile row past the matrix
+    // loads the block's first one again, unused (the loads stay unconditional
+    // so that the waits before the first round count them)
     auto load_codes = [&](uint32_t tr) {
 #pragma unroll
-        for (uint32_t q = 0; q < kWaveItems; ++q) {
-            const uint32_t i = w8 + 8u * q;
-            const uint32_t tile = (tr * per_row + (i < per_row ? i : 0u)) * 16u + tslot;
-            const u32x4 *src = reinterpret_cast<const u32x4 *>(job.trellis) + static_cast<size_t>(tile) * 8u + quad * 2u;
-            code[q][0] = __builtin_nontemporal_load(src);
-            code[q][1] = __builtin_nontemporal_load(src + 1);
+        for (uint32_t u = 0; u < kRoundRows; ++u) {
+            const uint32_t t = tr + u * blocks < tile_rows ? tr + u * blocks : b;
+#pragma unroll
+            for (uint32_t q = 0; q < kWaveItems; ++q) {
+                const uint32_t i = w8 + 8u * q;
+                const uint32_t tile = (t * per_row + (i < per_row ? i : 0u)) * 16u + tslot;
+                const u32x4 *src =
+                    reinterpret_cast<const u32x4 *>(job.trellis) + static_cast<size_t>(tile) * 8u + quad * 2u;
+                code[u][q][0] = __builtin_nontemporal_load(src);
+                code[u][q][1] = __builtin_nontemporal_load(src + 1);
+            }
         }
     };
     // The block's shares of the NE table and the output signs, and the x_hat
@@ -2826,20 +2838,27 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
         hadamard_cross_span<CH>(ne_lds + p * C, a.scale_columns, w8, lane);
     }
     __syncthreads();
-    for (uint32_t tr = b; tr < tile_rows; tr += blocks) {
+    for (uint32_t tr = b; tr < tile_rows; tr += kRoundRows * blocks) {
 #pragma unroll
         for (uint32_t q = 0; q < kWaveItems; ++q) {
             const uint32_t i8 = w8 + 8u * q;
             if (i8 < per_row) {
-                const uint32_t d[9] = {code[q][0].x, code[q][0].y, code[q][0].z, code[q][0].w,
-                                       code[q][1].x, code[q][1].y, code[q][1].z, code[q][1].w,
-                                       quad_next(code[q][0].x) & 0xFFFFu};
-                uint32_t idx[32];
-                decode_ne_quad(d, idx);
-                uint32_t w[32];
+                // the table values of the item in each of the round's tile rows
+                uint32_t w[kRoundRows][32];
 #pragma unroll
-                for (int k = 0; k < 32; ++k) {
-                    w[k] = table[idx[k]];
+                for (uint32_t u = 0; u < kRoundRows; ++u) {
+                    if (tr + u * blocks >= tile_rows) {
+                        break;
+                    }
+                    const uint32_t d[9] = {code[u][q][0].x, code[u][q][0].y, code[u][q][0].z, code[u][q][0].w,
+                                           code[u][q][1].x, code[u][q][1].y, code[u][q][1].z, code[u][q][1].w,
+                                           quad_next(code[u][q][0].x) & 0xFFFFu};
+                    uint32_t idx[32];
+                    decode_ne_quad(d, idx);
+#pragma unroll
+                    for (int k = 0; k < 32; ++k) {
+                        w[u][k] = table[idx[k]];
+                    }
                 }
                 const uint32_t column = (i8 * 16u + tslot) << 4;
 #pragma unroll
@@ -2858,42 +2877,51 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
                         x[4 * e + 2] = t.z;
                         x[4 * e + 3] = t.w;
                     }
-                    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                    for (int s = 0; s < 8; ++s) {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const float2 wv = half2_bits_to_float2(w[8 * r + s]);
-                            acc[r] = fmaf(wv.x, x[2 * s], acc[r]);
-                            acc[r] = fmaf(wv.y, x[2 * s + 1], acc[r]);
+                    for (uint32_t u = 0; u < kRoundRows; ++u) {
+                        if (tr + u * blocks >= tile_rows) {
+                            break;
                         }
-                    }
+                        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        acc[r] = sum_over_quads(acc[r], 16u);
-                    }
-                    if (tslot == 0) {
+                        for (int s = 0; s < 8; ++s) {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const float2 wv = half2_bits_to_float2(w[u][8 * r + s]);
+                                acc[r] = fmaf(wv.x, x[2 * s], acc[r]);
+                                acc[r] = fmaf(wv.y, x[2 * s + 1], acc[r]);
+                            }
+                        }
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            part[i8][quad * 4u + r][p] = acc[r] * job.weight_scale;
+                            acc[r] = sum_over_quads(acc[r], 16u);
+                        }
+                        if (tslot == 0) {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                part[u * per_row + i8][quad * 4u + r][p] = acc[r] * job.weight_scale;
+                            }
                         }
                     }
                 }
             }
         }
-        if (tr + blocks < tile_rows) {
-            load_codes(tr + blocks);
+        if (tr + kRoundRows * blocks < tile_rows) {
+            load_codes(tr + kRoundRows * blocks);
         }
         __syncthreads();
-        // the slice-order sum of the tile row's items: ((0 + item 0) + item 1) + ...
-        if (threadIdx.x < 16u * kMine && group + halves * (threadIdx.x >> 4) < a.batch) {
-            const uint32_t r = threadIdx.x & 15u, p = group + halves * (threadIdx.x >> 4);
-            float sum = 0.0f;
-            for (uint32_t i = 0; i < per_row; ++i) {
-                sum = sum + part[i][r][p];
+        // the slice-order sum of each tile row's items: ((0 + item 0) + item 1) + ...
+        {
+            const uint32_t r = threadIdx.x & 15u, i = (threadIdx.x >> 4) % kMine, u = (threadIdx.x >> 4) / kMine;
+            const uint32_t p = group + halves * i, t = tr + u * blocks;
+            if (u < kRoundRows && p < a.batch && t < tile_rows) {
+                float sum = 0.0f;
+                for (uint32_t k = 0; k < per_row; ++k) {
+                    sum = sum + part[u * per_row + k][r][p];
+                }
+                coherent_store(reinterpret_cast<uint32_t *>(job.zsum) + static_cast<size_t>(p) * R + t * kTile + r,
+                               __float_as_uint(sum));
             }
-            coherent_store(reinterpret_cast<uint32_t *>(job.zsum) + static_cast<size_t>(p) * R + tr * kTile + r,
-                           __float_as_uint(sum));
         }
         __syncthreads();
     }
@@ -2969,9 +2997,7 @@ bool launch_ne_fused(adi_hip_context *ctx, const adi_hip_ne_matrix *const *m, ui
         widest = std::max(widest, rows);
         tile_rows += rows / kTile;
     }
-    using Kernel = void (*)(NeFused);
-    Kernel kernel = columns == 2048u ? k_ne_fused<4> : (columns == 4096u ? k_ne_fused<8> : nullptr);
-    if (kernel == nullptr) {
+    if (columns != 2048u && columns != 4096u) {
         return false;
     }
     NeFused a{};
@@ -3002,6 +3028,11 @@ bool launch_ne_fused(adi_hip_context *ctx, const adi_hip_ne_matrix *const *m, ui
             break;
         }
     }
+    // two tile rows a round at 2048 columns (one item a wave each) when a
+    // block has more than one; a 4096-column tile row has two items a wave
+    using Kernel = void (*)(NeFused);
+    const Kernel kernel =
+        columns == 4096u ? k_ne_fused<8, 1> : (rounds > 1u ? k_ne_fused<4, 2> : k_ne_fused<4, 1>);
     float *sums = zsum;
     uint32_t first = 0;
     for (uint32_t j = 0; j < count; ++j) {
