@@ -239,20 +239,20 @@ __device__ __forceinline__ float lane_xor(float v) {
 // (xor 1 .. 32) and the four waves ((0 + 1) + (2 + 3)); dst[i] = v * scale *
 // (offset + w[i]). wave_sums (4 floats) and scale_shared are LDS. The same
 // values as the rms_norm launch.
-template <typename Value, typename Keep>
-__device__ __forceinline__ void block_rms_norm(Value &&value, Keep &&keep, const uint16_t *weight, uint32_t count,
-                                               float offset, float epsilon, float *dst, float *wave_sums,
-                                               float *scale_shared, uint32_t tid) {
+// block_rms_norm from the values a thread already holds: v[k] and the weights
+// w[k] (as floats) of indexes tid + 256 k, so that a caller can issue the
+// loads early. keep(i, v) sees each value once, first.
+template <typename Keep>
+__device__ __forceinline__ void block_rms_norm_held(const float (&v)[8], const float (&w)[8], Keep &&keep,
+                                                    uint32_t count, float offset, float epsilon, float *dst,
+                                                    float *wave_sums, float *scale_shared, uint32_t tid) {
 #pragma clang fp contract(off)
     constexpr uint32_t kHeld = 8, kThreads = 256;
-    float v[kHeld], w[kHeld];
     float squares = 0.0f;
     if (tid < kThreads) {
 #pragma unroll
         for (uint32_t k = 0; k < kHeld; ++k) {
             const uint32_t i = tid + k * kThreads;
-            v[k] = i < count ? value(i) : 0.0f;
-            w[k] = i < count ? bf16_bits_to_float(weight[i]) : 0.0f;
             if (i < count) {
                 keep(i, v[k]);
             }
@@ -289,6 +289,23 @@ __device__ __forceinline__ void block_rms_norm(Value &&value, Keep &&keep, const
             }
         }
     }
+}
+
+template <typename Value, typename Keep>
+__device__ __forceinline__ void block_rms_norm(Value &&value, Keep &&keep, const uint16_t *weight, uint32_t count,
+                                               float offset, float epsilon, float *dst, float *wave_sums,
+                                               float *scale_shared, uint32_t tid) {
+    constexpr uint32_t kHeld = 8, kThreads = 256;
+    float v[kHeld], w[kHeld];
+    if (tid < kThreads) {
+#pragma unroll
+        for (uint32_t k = 0; k < kHeld; ++k) {
+            const uint32_t i = tid + k * kThreads;
+            v[k] = i < count ? value(i) : 0.0f;
+            w[k] = i < count ? bf16_bits_to_float(weight[i]) : 0.0f;
+        }
+    }
+    block_rms_norm_held(v, w, keep, count, offset, epsilon, dst, wave_sums, scale_shared, tid);
 }
 
 // Value of the next lane of the lane's quad (lane 3 of a quad reads lane 0):

@@ -2686,7 +2686,7 @@ __device__ void ne_fused_rows(const NeFusedJob &job, float *ne_lds, const int8_t
     }
 }
 
-template <int VC, int ROWS>
+template <int VC, int ROWS, bool NORM>
 __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
 #pragma clang fp contract(off)
     extern __shared__ float ne_lds[];  // x_hat [batch][C], then the outputs [batch][rows]
@@ -2761,8 +2761,30 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
     }
     float xs[VC], xv[kMine][VC];
     load_wave_sign<VC>(job.su + w8 * CH, lane, xs);
-    const bool normed = C == 2048u && a.norm_row != nullptr;
-    if (!normed) {
+    // the input norm (a.norm_row set; 2048 columns only), known at compile
+    // time so that its loads go out with the others without a branch
+    constexpr bool normed = NORM;
+    static_assert(!NORM || C == 2048u, "the input norm runs at 2048 columns");
+    // With a norm: the half's input rows two at a time, one on each 256-thread
+    // half of the block (a half holds at most two rows: two halves from two
+    // rows on), thread t of a half holding columns t + 256 k of its row, the
+    // residual and the weights.
+    static_assert(kNeFusedRows <= 4u, "a half holds at most two input rows");
+    const uint32_t pair = threadIdx.x >> 8, t256 = threadIdx.x & 255u;
+    const uint32_t norm_p = group + halves * pair;
+    const uint32_t norm_q = norm_p < a.batch ? norm_p : group;  // a row in range for an idle half's loads
+    float norm_row[8], norm_add[8];
+    uint16_t norm_w[8];
+    if constexpr (normed) {
+        const float *row = a.norm_row + static_cast<size_t>(norm_q) * C;
+        const float *add = a.norm_add != nullptr ? a.norm_add + static_cast<size_t>(norm_q) * C : row;
+#pragma unroll
+        for (uint32_t k = 0; k < 8u; ++k) {
+            norm_row[k] = row[t256 + 256u * k];
+            norm_add[k] = add[t256 + 256u * k];
+            norm_w[k] = a.norm_weight[t256 + 256u * k];
+        }
+    } else {
 #pragma unroll
         for (uint32_t i = 0; i < kMine; ++i) {
             const uint32_t p = group + halves * i;
@@ -2787,20 +2809,16 @@ __global__ __launch_bounds__(kNeFusedThreads) void k_ne_fused(NeFused a) {
     }
     // with a norm the half's input rows are computed here, into the x_hat
     // rows' place; the first block of the half writes them out
-    if constexpr (C == 2048u) {
-        if (normed) {
-            // two rows at a time, one on each 256-thread half of the block
-            const uint32_t pair = threadIdx.x >> 8;
-            for (uint32_t i0 = 0; group + halves * i0 < a.batch; i0 += 2u) {
-                const uint32_t p = group + halves * (i0 + pair);
-                const bool live = p < a.batch;
-                const uint32_t q = live ? p : group;  // a row in range for the idle half's pointers
-                const float *row = a.norm_row + static_cast<size_t>(q) * C;
-                const float *add = a.norm_add != nullptr ? a.norm_add + static_cast<size_t>(q) * C : nullptr;
-                block_rms_norm([&](uint32_t e) { return add != nullptr ? row[e] + add[e] : row[e]; },
-                               [](uint32_t, float) {}, a.norm_weight, C, 1.0f, 1.0e-6f, ne_lds + q * C,
-                               norm_sums[pair], &norm_scale[pair], live ? threadIdx.x & 255u : 256u);
+    if constexpr (normed) {
+        {
+            float v[8], w[8];
+#pragma unroll
+            for (uint32_t k = 0; k < 8u; ++k) {
+                v[k] = a.norm_add != nullptr ? norm_row[k] + norm_add[k] : norm_row[k];
+                w[k] = bf16_bits_to_float(norm_w[k]);
             }
+            block_rms_norm_held(v, w, [](uint32_t, float) {}, C, 1.0f, 1.0e-6f, ne_lds + norm_q * C,
+                                norm_sums[pair], &norm_scale[pair], norm_p < a.batch ? t256 : 256u);
             __syncthreads();
             if (g == 0) {
                 for (uint32_t p = group; p < a.batch; p += halves) {
@@ -3031,8 +3049,11 @@ bool launch_ne_fused(adi_hip_context *ctx, const adi_hip_ne_matrix *const *m, ui
     // two tile rows a round at 2048 columns (one item a wave each) when a
     // block has more than one; a 4096-column tile row has two items a wave
     using Kernel = void (*)(NeFused);
+    const bool norm = in != nullptr;
     const Kernel kernel =
-        columns == 4096u ? k_ne_fused<8, 1> : (rounds > 1u ? k_ne_fused<4, 2> : k_ne_fused<4, 1>);
+        columns == 4096u ? k_ne_fused<8, 1, false>
+                         : (rounds > 1u ? (norm ? k_ne_fused<4, 2, true> : k_ne_fused<4, 2, false>)
+                                        : (norm ? k_ne_fused<4, 1, true> : k_ne_fused<4, 1, false>));
     float *sums = zsum;
     uint32_t first = 0;
     for (uint32_t j = 0; j < count; ++j) {
