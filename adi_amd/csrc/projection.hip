@@ -1355,6 +1355,38 @@ __device__ __forceinline__ void hadamard_cross_span(float *dst, float scale, uin
         }
     }
 }
+// hadamard_cross_span with the result times a sign row written to `out`
+// instead of back into `src`: out[i] = (u * scale) * signs[i], the values
+// the in-place transform and a sign pass over it give.
+template <uint32_t SPAN>
+__device__ __forceinline__ void hadamard_cross_span_out(const float *src, float scale, uint32_t wave, uint32_t lane,
+                                                        const int8_t *signs, float *out) {
+#pragma clang fp contract(off)
+    constexpr uint32_t per_wave = SPAN / 8u;
+    for (uint32_t j = per_wave * wave + lane; j < per_wave * (wave + 1u); j += 64u) {
+        float u[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            u[k] = src[SPAN * k + j];
+        }
+#pragma unroll
+        for (int stride = 1; stride < 8; stride <<= 1) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if ((k & stride) == 0) {
+                    const float p = u[k], q = u[k + stride];
+                    u[k] = p + q;
+                    u[k + stride] = p - q;
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float v = u[k] * scale;
+            out[SPAN * k + j] = v * static_cast<float>(signs[SPAN * k + j]);
+        }
+    }
+}
 __device__ __forceinline__ void hadamard_cross(float *dst, float scale, uint32_t wave, uint32_t lane) {
 #pragma clang fp contract(off)
     if (lane < 32) {
@@ -2631,6 +2663,15 @@ __device__ void ne_fused_rows(const NeFusedJob &job, float *ne_lds, const int8_t
                               uint32_t halves, uint32_t batch, uint32_t w8, uint32_t lane, float (*norm_sums)[4],
                               float *norm_scale) {
     constexpr uint32_t R = 512u * VR, RH = R / 8u;
+    // with the next norm (2048 rows): its residual rows and weights load
+    // after the sums, so that their latency runs under the transform; a
+    // half holds at most two rows, one on each 256-thread half of the block
+    const bool tail = R <= 2048u && job.tail_row != nullptr;
+    const uint32_t pair = threadIdx.x >> 8, t256 = threadIdx.x & 255u;
+    const uint32_t tail_p = group + halves * pair;
+    const uint32_t tail_q = tail_p < batch ? tail_p : group;
+    float tail_r[8];
+    uint16_t tail_w[8];
     // every sum of the half's input rows is in (first touch here, ordinary
     // loads; all the loads first)
     {
@@ -2640,6 +2681,14 @@ __device__ void ne_fused_rows(const NeFusedJob &job, float *ne_lds, const int8_t
             const uint32_t p = group + halves * i;
             if (p < batch) {
                 load_wave<VR>(job.zsum + static_cast<size_t>(p) * R + w8 * RH, lane, v[i]);
+            }
+        }
+        if (tail) {
+            const float *row = job.tail_row + static_cast<size_t>(tail_q) * R;
+#pragma unroll
+            for (uint32_t k = 0; k < 8u; ++k) {
+                tail_r[k] = row[t256 + 256u * k];
+                tail_w[k] = job.tail_weight[t256 + 256u * k];
             }
         }
 #pragma unroll
@@ -2652,6 +2701,13 @@ __device__ void ne_fused_rows(const NeFusedJob &job, float *ne_lds, const int8_t
         }
     }
     __syncthreads();
+    if (!tail) {
+        // the last butterflies write the outputs
+        for (uint32_t p = group; p < batch; p += halves) {
+            hadamard_cross_span_out<RH>(ne_lds + p * R, job.scale_rows, w8, lane, sv_lds, job.out + p * R);
+        }
+        return;
+    }
     for (uint32_t p = group; p < batch; p += halves) {
         hadamard_cross_span<RH>(ne_lds + p * R, job.scale_rows, w8, lane);
     }
@@ -2666,24 +2722,19 @@ __device__ void ne_fused_rows(const NeFusedJob &job, float *ne_lds, const int8_t
             }
         }
     }
-    if constexpr (R <= 2048u) {
-        if (job.tail_row != nullptr) {
-            // the residual add and the next RMS norm of the half's rows, two
-            // at a time (one on each 256-thread half of the block)
-            const uint32_t pair = threadIdx.x >> 8;
-            for (uint32_t i0 = 0; group + halves * i0 < batch; i0 += 2u) {
-                const uint32_t p = group + halves * (i0 + pair);
-                const bool live = p < batch;
-                const uint32_t q = live ? p : group;
-                float *row = job.tail_row + static_cast<size_t>(q) * R;
-                const float *y = ne_lds + q * R;
-                block_rms_norm([&](uint32_t e) { return row[e] + y[e] * static_cast<float>(sv_lds[e]); },
-                               [&](uint32_t e, float v) { row[e] = v; }, job.tail_weight, R, 1.0f, 1.0e-6f,
-                               job.tail_out + static_cast<size_t>(q) * R, norm_sums[pair], &norm_scale[pair],
-                               live ? threadIdx.x & 255u : 256u);
-            }
-        }
+    // the residual add and the next RMS norm of the half's rows
+    float *row = job.tail_row + static_cast<size_t>(tail_q) * R;
+    const float *y = ne_lds + tail_q * R;
+    float v[8], w[8];
+#pragma unroll
+    for (uint32_t k = 0; k < 8u; ++k) {
+        const uint32_t e = t256 + 256u * k;
+        v[k] = tail_r[k] + y[e] * static_cast<float>(sv_lds[e]);
+        w[k] = bf16_bits_to_float(tail_w[k]);
     }
+    block_rms_norm_held(v, w, [&](uint32_t e, float x) { row[e] = x; }, R, 1.0f, 1.0e-6f,
+                        job.tail_out + static_cast<size_t>(tail_q) * R, norm_sums[pair], &norm_scale[pair],
+                        tail_p < batch ? t256 : 256u);
 }
 
 template <int VC, int ROWS, bool NORM>
