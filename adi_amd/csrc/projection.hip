@@ -2032,6 +2032,59 @@ __device__ __forceinline__ void expert_load_x(const MoeGemv &m, uint32_t i, uint
     load_x_pair(a.x_hat, a.columns, st.info.y, column, 1u << a.group_shift, valid, st.x);
 }
 
+// expert_prefetch (without x_hat) and expert_load_x for G tile groups (the
+// matrix's), with every load issued: a slot past the active count reads
+// expert 0's first tile and x_hat row 0 and is never computed, and the items
+// of the one-launch geometry cover their matrices exactly (no tile past one).
+// With no branch around a load the compiler counts them, so the waits of the
+// item that runs meanwhile leave them in flight.
+template <uint32_t G>
+__device__ __forceinline__ void few_prefetch(const MoeGemv &m, const uint4 *slots, uint32_t i, uint32_t half,
+                                             uint32_t lane, ExpertStage &st) {
+    const ExpertItem it = expert_item_of(m, i);
+    const ExpertGemv &a = m.expert[it.which];
+    const uint4 info = slots[it.slot];
+    st.info = make_uint4(__builtin_amdgcn_readfirstlane(info.x), __builtin_amdgcn_readfirstlane(info.y),
+                         __builtin_amdgcn_readfirstlane(info.z), 0u);
+    const uint32_t quad = lane & 3u;
+    const uint32_t tile_columns = 1u << a.tc_shift;
+    const bool live = st.info.z > st.info.y;
+    uint32_t column[4], tile[4];
+    bool valid[4];
+    expert_tiles(a, it.item, half, lane, column, valid, tile);
+    const uint32_t expert = live ? st.info.x : 0u;
+    const uint32_t *words = reinterpret_cast<const uint32_t *>(a.trellis + expert * a.trellis_stride);
+    const uint16_t *gamma_row = a.gamma + expert * a.gamma_stride;
+#pragma unroll
+    for (uint32_t g = 0; g < G; ++g) {
+        const uint32_t t = valid[g] && live ? tile[g] : 0u;
+        typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+        const u32x3 w = __builtin_nontemporal_load(reinterpret_cast<const u32x3 *>(words + static_cast<size_t>(t) * 12u + quad * 3u));
+        st.d[g][0] = w.x;
+        st.d[g][1] = w.y;
+        st.d[g][2] = w.z;
+        const uint32_t tr = t >> a.tc_shift, tc = t & (tile_columns - 1u);
+        st.gamma[g] = gamma_row[wave_slot(tr, tc, a.tile_rows, tile_columns)];
+    }
+}
+template <uint32_t G>
+__device__ __forceinline__ void few_load_x(const MoeGemv &m, uint32_t i, uint32_t half, uint32_t lane,
+                                           ExpertStage &st) {
+    const ExpertItem it = expert_item_of(m, i);
+    const ExpertGemv &a = m.expert[it.which];
+    uint32_t column[4], tile[4];
+    bool valid[4];
+    expert_tiles(a, it.item, half, lane, column, valid, tile);
+    const bool live = st.info.z > st.info.y;
+    const float *row = a.x_hat + static_cast<size_t>(live ? st.info.y : 0u) * a.columns;
+#pragma unroll
+    for (uint32_t g = 0; g < G; ++g) {
+        const float *src = row + (valid[g] && live ? column[g] : 0u);
+        st.x[g][0] = *reinterpret_cast<const float4 *>(src);
+        st.x[g][1] = *reinterpret_cast<const float4 *>(src + 8);
+    }
+}
+
 // 256 consecutive floats (a wave's chunk, 4 a lane) written through to memory.
 __device__ __forceinline__ void store_chunk_through(float *dst, uint32_t lane, float4 v) {
     typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -2421,9 +2474,12 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_decode_few(MoeDecodeFew a)
                           return kGemvWaves * (info.z - info.y);
                       },
                       n_slots, lane, error, 4u);
+        // every slot's stage is issued, the one past the last staging the last
+        // again (unused): see few_prefetch
         auto stage = [&](uint32_t t, ExpertStage &st) {
-            expert_prefetch(a.gu, slots, index(t), half, lane, st, nullptr, false);
-            expert_load_x(a.gu, index(t), half, lane, st);
+            t = t < n_slots ? t : n_slots - 1u;
+            few_prefetch<kFewGuGroups>(a.gu, slots, index(t), half, lane, st);
+            few_load_x<kFewGuGroups>(a.gu, index(t), half, lane, st);
         };
         // plain stores: only this XCD's SwiGLU rows read these Z slices
         auto run = [&](uint32_t t, ExpertStage &st) {
@@ -2435,16 +2491,12 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_decode_few(MoeDecodeFew a)
             stage(0, s0);
         }
         for (uint32_t t = 0; t < n_slots; t += 2u) {
-            if (t + 1u < n_slots) {
-                stage(t + 1u, s1);
-            }
+            stage(t + 1u, s1);
             run(t, s0);
             if (t + 1u >= n_slots) {
                 break;
             }
-            if (t + 2u < n_slots) {
-                stage(t + 2u, s0);
-            }
+            stage(t + 2u, s0);
             run(t + 1u, s1);
         }
     }
@@ -2497,11 +2549,21 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_decode_few(MoeDecodeFew a)
     // next slot's codes and x_hat in flight during the arithmetic ----
     {
         auto index = [&](uint32_t t) { return (slot_of(t) << a.dn.item_shift) + il; };
+        // the slot's x_hat count is read before its codes go out: when it is
+        // already complete (the usual case), that read's wait leaves the codes
+        // in flight; otherwise the poll waits for everything
         auto stage = [&](uint32_t t, ExpertStage &st) {
+            t = t < n_slots ? t : n_slots - 1u;
             const uint4 info = slots[slot_of(t)];
-            expert_prefetch(a.dn, slots, index(t), half, lane, st, nullptr, false);
-            wait_count(few_word(sync, few_sync::kDownX + slot_of(t)), info.z - info.y, error, 4u);
-            expert_load_x(a.dn, index(t), half, lane, st);
+            uint32_t *word = few_word(sync, few_sync::kDownX + slot_of(t));
+            const uint32_t seen = coherent_load(word);
+            __builtin_amdgcn_sched_barrier(0);
+            few_prefetch<kFewDnGroups>(a.dn, slots, index(t), half, lane, st);
+            __builtin_amdgcn_sched_barrier(0);
+            if (__builtin_amdgcn_readfirstlane(seen) < info.z - info.y) {
+                wait_count(word, info.z - info.y, error, 4u);
+            }
+            few_load_x<kFewDnGroups>(a.dn, index(t), half, lane, st);
         };
         auto run = [&](uint32_t t, ExpertStage &st) {
             expert_compute<false>(a.dn, index(t), half, plane, lane, st);  // read on this XCD only
@@ -2512,16 +2574,12 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_decode_few(MoeDecodeFew a)
             stage(0, s0);
         }
         for (uint32_t t = 0; t < n_slots; t += 2u) {
-            if (t + 1u < n_slots) {
-                stage(t + 1u, s1);
-            }
+            stage(t + 1u, s1);
             run(t, s0);
             if (t + 1u >= n_slots) {
                 break;
             }
-            if (t + 2u < n_slots) {
-                stage(t + 2u, s0);
-            }
+            stage(t + 2u, s0);
             run(t + 1u, s1);
         }
     }
@@ -3408,6 +3466,14 @@ bool plan_moe_decode_few(adi_hip_context *ctx, MoeDecodeFew &a) {
     if (2u * a.gu.expert_items_per_slot != pair_waves || a.dn.expert_items_per_slot != pair_waves ||
         a.experts + 1 > 2 * blocks || a.gu.ne_items != 2 * a.gu.ne_items_per_matrix ||
         a.gu.ne_items_per_matrix > blocks || a.dn.ne_items != blocks || 2u * a.batch > blocks) {
+        return false;
+    }
+    // the items' tile groups are the ones the kernel stages, and the items
+    // cover each matrix exactly
+    if ((1u << a.gu.expert[0].group_shift) != kFewGuGroups || (1u << a.gu.expert[1].group_shift) != kFewGuGroups ||
+        (1u << d.group_shift) != kFewDnGroups ||
+        (g.tile_rows << g.tc_shift) != a.gu.expert_items_per_slot * 16u * kFewGuGroups ||
+        (d.tile_rows << d.tc_shift) != a.dn.expert_items_per_slot * 16u * kFewDnGroups) {
         return false;
     }
     a.expect_gu = 2u * a.gu.expert_count * a.gu.expert_items_per_slot;

@@ -243,6 +243,9 @@ constexpr uint32_t kFusedMaxExperts = 256;  // routed experts they handle
 // 164.8 us a layer) overtake the decode-GEMV items this launch runs.
 constexpr uint32_t kFewMaxRows = 12;
 constexpr uint32_t kFewMaxRoutes = 8 * kFewMaxRows;
+// tile groups of a gate/up and of a down item in that launch (item_groups of
+// 2048 and 512 columns)
+constexpr uint32_t kFewGuGroups = 4, kFewDnGroups = 2;
 struct MoeDecodeFew {
     MoeGemv gu;                       // routed gate/up (entries 0, 1), shared gate/up (NE 0, 1)
     MoeGemv dn;                       // routed down (entry 0), shared down (NE 0); dn.swiglu set
