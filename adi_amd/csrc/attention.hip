@@ -295,17 +295,23 @@ __device__ __forceinline__ void attention_partial_span(const float *query, const
     // its dot products reduced together, then the online updates in order
     constexpr uint32_t kBatch = 8;
     for (uint32_t t0 = begin + wave; t0 < end; t0 += 4u * kBatch) {
+        // every entry from the cache, with no branch around a load (so the
+        // batch's loads are counted and waited for once); the fresh entry's
+        // cache slot is read too and then replaced by its LDS copy
         float4 k[kBatch], v[kBatch];
 #pragma unroll
         for (uint32_t j = 0; j < kBatch; ++j) {
             const uint32_t t = t0 + 4u * j < end ? t0 + 4u * j : t0;
             const size_t at = (static_cast<size_t>(t) * kKvHeads + kv) * kHeadSize;
+            k[j] = reinterpret_cast<const float4 *>(keys + at)[lane];
+            v[j] = reinterpret_cast<const float4 *>(values + at)[lane];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; ++j) {
+            const uint32_t t = t0 + 4u * j < end ? t0 + 4u * j : t0;
             if (t == fresh) {  // wave-uniform
                 k[j] = reinterpret_cast<const float4 *>(fresh_key)[lane];
                 v[j] = reinterpret_cast<const float4 *>(fresh_value)[lane];
-            } else {
-                k[j] = reinterpret_cast<const float4 *>(keys + at)[lane];
-                v[j] = reinterpret_cast<const float4 *>(values + at)[lane];
             }
         }
         float dot[kBatch];
@@ -408,9 +414,14 @@ __device__ __forceinline__ void combine_splits(const float *p, uint32_t splits, 
     for (uint32_t s = 0; s < N; ++s) {
         acc[s] = s < splits ? load(p + s * kPartialStride + t) : 0.0f;
     }
-    for (uint32_t s = t; s < splits; s += kHeadSize) {
-        split_max[s] = load(p + s * kPartialStride + kHeadSize);
-        split_den[s] = load(p + s * kPartialStride + kHeadSize + 1);
+    static_assert(N <= kHeadSize, "a thread's split");
+    // both words of the thread's split loaded before either is stored (one
+    // round trip with the accumulators')
+    if (t < splits) {
+        const float mx = load(p + t * kPartialStride + kHeadSize);
+        const float dn = load(p + t * kPartialStride + kHeadSize + 1);
+        split_max[t] = mx;
+        split_den[t] = dn;
     }
     __syncthreads();
     // split 0 always holds token 0, so the maximum is finite
@@ -838,18 +849,40 @@ __global__ __launch_bounds__(256) void k_linear_core_rows(const float *qkv, cons
     for (uint32_t j = 0; j < kRows; ++j) {
         s[j] = state[j * (kLinearHead / 2u) + lane];
     }
+    // the row and the head's alpha and beta weight rows (columns <= 2048, a
+    // multiple of 256) into LDS: every load issued first (indexes past the
+    // row clamped), then the stores
+    constexpr uint32_t kX4 = LANES > 0 ? kDecayColumns / 4u / 256u : 1u;
+    constexpr uint32_t kW8 = LANES > 0 ? kDecayColumns / 8u / 256u : 1u;
+    float4 xv[kX4];
+    uint4 av[kW8], bv[kW8];
     if constexpr (LANES > 0) {
-        // the row and the head's alpha and beta weight rows (columns <= 2048,
-        // a multiple of 256)
         const float4 *xs = reinterpret_cast<const float4 *>(x + static_cast<size_t>(r) * columns);
-        for (uint32_t i = t; i < columns / 4u; i += 256u) {
-            reinterpret_cast<float4 *>(x_lds)[i] = xs[i];
+#pragma unroll
+        for (uint32_t k = 0; k < kX4; ++k) {
+            xv[k] = xs[min(t + 256u * k, columns / 4u - 1u)];
         }
         const uint4 *wa = reinterpret_cast<const uint4 *>(alpha_w + static_cast<size_t>(h) * columns);
         const uint4 *wb = reinterpret_cast<const uint4 *>(beta_w + static_cast<size_t>(h) * columns);
-        for (uint32_t i = t; i < columns / 8u; i += 256u) {
-            reinterpret_cast<uint4 *>(w_lds[0])[i] = wa[i];
-            reinterpret_cast<uint4 *>(w_lds[1])[i] = wb[i];
+#pragma unroll
+        for (uint32_t k = 0; k < kW8; ++k) {
+            av[k] = wa[min(t + 256u * k, columns / 8u - 1u)];
+            bv[k] = wb[min(t + 256u * k, columns / 8u - 1u)];
+        }
+    }
+    if constexpr (LANES > 0) {
+#pragma unroll
+        for (uint32_t k = 0; k < kX4; ++k) {
+            if (t + 256u * k < columns / 4u) {
+                reinterpret_cast<float4 *>(x_lds)[t + 256u * k] = xv[k];
+            }
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kW8; ++k) {
+            if (t + 256u * k < columns / 8u) {
+                reinterpret_cast<uint4 *>(w_lds[0])[t + 256u * k] = av[k];
+                reinterpret_cast<uint4 *>(w_lds[1])[t + 256u * k] = bv[k];
+            }
         }
     }
     // threads 0-127 the query channels, 128-255 the key channels; each L2
