@@ -1387,6 +1387,148 @@ __device__ __forceinline__ void hadamard_cross_span_out(const float *src, float 
         }
     }
 }
+// ---- block-per-vector prologue / epilogue (n = 2048, 4096) ---------------
+//
+// A launch of few vectors (a prefill chunk's attention projections: 128-384)
+// leaves most CUs idle with one wave a vector, each wave running a whole
+// 2048- or 4096-point transform. Here a vector takes a block of eight waves:
+// wave w transforms elements w n/8 .. (w + 1) n/8 - 1 (the index bits below
+// 8 or 9, in the wave layout of that chunk), then the waves run the last
+// three index bits across the chunks in LDS (hadamard_cross_span): every
+// butterfly is the one-wave transform's, in the same order, so the results
+// are bit-identical to the one-wave kernels'.
+constexpr uint32_t kBlockVectors = 512;  // vectors up to which a vector takes a block
+
+// x_hat of vector v from LDS (n values, already scaled) in out's layout, by
+// the block's 512 threads: f32 rows, f16 hi/lo rows, or the two codebook
+// planes of each 16-column tile (store_xhat's layouts).
+__device__ __forceinline__ void store_xhat_lds(const XhatOut &out, uint32_t v, const float *x, uint32_t n) {
+#pragma clang fp contract(off)
+    if (out.planes == 0) {
+        float4 *dst = reinterpret_cast<float4 *>(out.f32 + static_cast<size_t>(v) * n);
+        for (uint32_t i = threadIdx.x; i < n / 4u; i += 512u) {
+            dst[i] = reinterpret_cast<const float4 *>(x)[i];
+        }
+        return;
+    }
+    const auto split = [](float f, uint32_t &hi, uint32_t &lo) {
+        hi = f16_bits_rne(f);
+        lo = f16_bits_rne(f - half_bits_to_float(hi));
+    };
+    if (out.planes == 1) {
+        for (uint32_t i = threadIdx.x; i < n / 4u; i += 512u) {
+            const float4 q = reinterpret_cast<const float4 *>(x)[i];
+            uint32_t h[4], l[4];
+            split(q.x, h[0], l[0]);
+            split(q.y, h[1], l[1]);
+            split(q.z, h[2], l[2]);
+            split(q.w, h[3], l[3]);
+            *reinterpret_cast<uint2 *>(out.hi + static_cast<size_t>(v) * n + 4u * i) =
+                make_uint2(h[0] | h[1] << 16, h[2] | h[3] << 16);
+            *reinterpret_cast<uint2 *>(out.lo + static_cast<size_t>(v) * n + 4u * i) =
+                make_uint2(l[0] | l[1] << 16, l[2] | l[3] << 16);
+        }
+        return;
+    }
+    // (tile, plane) pairs: the plane's columns 4 p .. 4 p + 3 and 8 + 4 p ..
+    // 8 + 4 p + 3 of the tile, in that order, one 16-byte store each
+    for (uint32_t t = threadIdx.x; t < n / 8u; t += 512u) {
+        const uint32_t tile = t >> 1, plane = t & 1u, c = tile * 16u + 4u * plane;
+        const float4 a = *reinterpret_cast<const float4 *>(x + c);
+        const float4 b = *reinterpret_cast<const float4 *>(x + c + 8u);
+        const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        uint32_t h[8], l[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            split(f[k], h[k], l[k]);
+        }
+        const size_t at = static_cast<size_t>(plane) * out.vectors * (n / 2u) + static_cast<size_t>(v) * (n / 2u) +
+                          tile * 8u;
+        *reinterpret_cast<uint4 *>(out.hi + at) =
+            make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
+        *reinterpret_cast<uint4 *>(out.lo + at) =
+            make_uint4(l[0] | l[1] << 16, l[2] | l[3] << 16, l[4] | l[5] << 16, l[6] | l[7] << 16);
+    }
+}
+
+// prologue_vector for vector blockIdx.x by a block: x_hat = H_n(x[src] * su).
+template <int VC>
+__global__ __launch_bounds__(512) void k_prologue_block(PrologueJobs j) {
+#pragma clang fp contract(off)
+    constexpr uint32_t n = 512u * VC, CH = 64u * VC;
+    __shared__ __align__(16) float x_lds[n];
+    uint32_t v = blockIdx.x, s = 0;
+    while (s < j.segments && v >= j.seg[s].count) {
+        v -= j.seg[s].count;
+        ++s;
+    }
+    if (s >= j.segments) {
+        return;  // the whole block
+    }
+    const PrologueSegment &g = j.seg[s];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t src = g.source_row != nullptr ? g.source_row[v] : v;
+    const uint32_t mat = g.matrix_index != nullptr ? g.matrix_index[v] : 0u;
+    float val[VC], su[VC];
+    load_wave<VC>(g.x + static_cast<size_t>(src) * n + wave * CH, lane, val);
+    if (g.su_f16 != nullptr) {
+        load_wave_f16<VC>(g.su_f16 + static_cast<size_t>(mat) * g.su_stride + wave * CH, lane, su);
+    } else {
+        load_wave_sign<VC>(g.su_sign + wave * CH, lane, su);
+    }
+#pragma unroll
+    for (int i = 0; i < VC; ++i) {
+        val[i] = val[i] * su[i];
+    }
+    wave_hadamard<VC>(val, 1.0f, lane);
+    store_wave<VC>(x_lds + wave * CH, lane, val);
+    __syncthreads();
+    hadamard_cross_span<CH>(x_lds, j.scale, wave, lane);
+    __syncthreads();
+    store_xhat_lds(g.out, v, x_lds, n);
+}
+
+// k_epilogue_wave for vector blockIdx.x by a block: y = sv * H_n(sum over
+// splits of z), the last butterflies writing y.
+template <int VC, typename Scale>
+__global__ __launch_bounds__(512) void k_epilogue_block(const float *__restrict__ z, uint32_t splits,
+                                                        size_t split_stride, const Scale *__restrict__ sv,
+                                                        float scale, float *__restrict__ out) {
+#pragma clang fp contract(off)
+    constexpr uint32_t n = 512u * VC, CH = 64u * VC;
+    __shared__ __align__(16) float y_lds[n];
+    const uint32_t v = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    float val[VC];
+    sum_slices_deep<VC>(z + static_cast<size_t>(v) * n + wave * CH, split_stride, splits, lane, val);
+    wave_hadamard<VC>(val, 1.0f, lane);
+    store_wave<VC>(y_lds + wave * CH, lane, val);
+    __syncthreads();
+    float *dst = out + static_cast<size_t>(v) * n;
+    for (uint32_t jj = CH / 8u * wave + lane; jj < CH / 8u * (wave + 1u); jj += 64u) {
+        float u[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            u[k] = y_lds[CH * k + jj];
+        }
+#pragma unroll
+        for (int stride = 1; stride < 8; stride <<= 1) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if ((k & stride) == 0) {
+                    const float p = u[k], q = u[k + stride];
+                    u[k] = p + q;
+                    u[k + stride] = p - q;
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float w = u[k] * scale;
+            dst[CH * k + jj] = w * scale_value<Scale>(sv[CH * k + jj]);
+        }
+    }
+}
+
 __device__ __forceinline__ void hadamard_cross(float *dst, float scale, uint32_t wave, uint32_t lane) {
 #pragma clang fp contract(off)
     if (lane < 32) {
@@ -3211,6 +3353,14 @@ void launch_prologues(adi_hip_context *ctx, PrologueJobs &jobs) {
         vectors += jobs.seg[s].count;
     }
     prepare_prologues(jobs);
+    if ((jobs.n == 2048u || jobs.n == 4096u) && vectors <= kBlockVectors) {
+        if (jobs.n == 2048u) {
+            launch(ctx, "hadamard_prologue", k_prologue_block<4>, dim3(vectors), dim3(512), 0, jobs);
+        } else {
+            launch(ctx, "hadamard_prologue", k_prologue_block<8>, dim3(vectors), dim3(512), 0, jobs);
+        }
+        return;
+    }
     const dim3 grid(ceil_div(vectors, 4));
     switch (jobs.n) {
     case 64: launch(ctx, "hadamard_prologue", k_prologue_wave<1>, grid, dim3(256), 0, jobs); break;
@@ -3252,6 +3402,16 @@ void launch_epilogue_any(adi_hip_context *ctx, const float *z, uint32_t splits,
         launch(ctx, "reduce_slices", k_reduce_slices, dim3(ceil_div(count4, 64)), dim3(64), 0,
                const_cast<float *>(z), splits, split_stride, count4);
         splits = 1;
+    }
+    if ((n == 2048u || n == 4096u) && vectors <= kBlockVectors) {
+        if (n == 2048u) {
+            launch(ctx, "hadamard_epilogue", k_epilogue_block<4, Scale>, dim3(vectors), dim3(512), 0, z, splits,
+                   split_stride, sv, scale, out);
+        } else {
+            launch(ctx, "hadamard_epilogue", k_epilogue_block<8, Scale>, dim3(vectors), dim3(512), 0, z, splits,
+                   split_stride, sv, scale, out);
+        }
+        return;
     }
     const dim3 grid(ceil_div(vectors, 4));
     switch (n) {
