@@ -1387,7 +1387,7 @@ __device__ __forceinline__ void hadamard_cross_span_out(const float *src, float 
         }
     }
 }
-// ---- block-per-vector prologue / epilogue (n = 2048, 4096) ---------------
+// ---- block-per-vector prologue / epilogue (n = 2048, 4096; 8192 too) -----
 //
 // A launch of few vectors (a prefill chunk's attention projections: 128-384)
 // leaves most CUs idle with one wave a vector, each wave running a whole
@@ -1488,8 +1488,9 @@ __global__ __launch_bounds__(512) void k_prologue_block(PrologueJobs j) {
     store_xhat_lds(g.out, v, x_lds, n);
 }
 
-// k_epilogue_wave for vector blockIdx.x by a block: y = sv * H_n(sum over
-// splits of z), the last butterflies writing y.
+// k_epilogue_wave (k_epilogue_8192 at 8192 points) for vector blockIdx.x by
+// a block: y = sv * H_n(sum over splits of z), the last butterflies writing
+// y.
 template <int VC, typename Scale>
 __global__ __launch_bounds__(512) void k_epilogue_block(const float *__restrict__ z, uint32_t splits,
                                                         size_t split_stride, const Scale *__restrict__ sv,
@@ -3403,12 +3404,15 @@ void launch_epilogue_any(adi_hip_context *ctx, const float *z, uint32_t splits,
                const_cast<float *>(z), splits, split_stride, count4);
         splits = 1;
     }
-    if ((n == 2048u || n == 4096u) && vectors <= kBlockVectors) {
+    if ((n == 2048u || n == 4096u || n == 8192u) && vectors <= kBlockVectors) {
         if (n == 2048u) {
             launch(ctx, "hadamard_epilogue", k_epilogue_block<4, Scale>, dim3(vectors), dim3(512), 0, z, splits,
                    split_stride, sv, scale, out);
-        } else {
+        } else if (n == 4096u) {
             launch(ctx, "hadamard_epilogue", k_epilogue_block<8, Scale>, dim3(vectors), dim3(512), 0, z, splits,
+                   split_stride, sv, scale, out);
+        } else {
+            launch(ctx, "hadamard_epilogue", k_epilogue_block<16, Scale>, dim3(vectors), dim3(512), 0, z, splits,
                    split_stride, sv, scale, out);
         }
         return;
