@@ -298,11 +298,21 @@ __device__ __forceinline__ void block_rms_norm(Value &&value, Keep &&keep, const
     constexpr uint32_t kHeld = 8, kThreads = 256;
     float v[kHeld], w[kHeld];
     if (tid < kThreads) {
+        // every load issued with its index clamped into the row (count >= 1),
+        // the values past the row zeroed after: a branch around each load
+        // would make the compiler wait for each before issuing the next
 #pragma unroll
         for (uint32_t k = 0; k < kHeld; ++k) {
-            const uint32_t i = tid + k * kThreads;
-            v[k] = i < count ? value(i) : 0.0f;
-            w[k] = i < count ? bf16_bits_to_float(weight[i]) : 0.0f;
+            const uint32_t i = min(tid + k * kThreads, count - 1u);
+            v[k] = value(i);
+            w[k] = bf16_bits_to_float(weight[i]);
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kHeld; ++k) {
+            if (tid + k * kThreads >= count) {
+                v[k] = 0.0f;
+                w[k] = 0.0f;
+            }
         }
     }
     block_rms_norm_held(v, w, keep, count, offset, epsilon, dst, wave_sums, scale_shared, tid);
