@@ -646,14 +646,13 @@ __device__ __forceinline__ void ne_prefetch(const MoeGemv &m, uint32_t k, uint32
     uint32_t tile, column;
     bool valid;
     ne_tile(a, it.y, lane, tile, valid, column);
+    // no branch around the code loads (a lane past the matrix reads tile 0:
+    // its x_hat is zero, so its sums stay +0 whatever its codes), so that
+    // nothing waits for them here
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
-    if (valid) {
-        const u32x4 *src = reinterpret_cast<const u32x4 *>(a.trellis) +
-                           static_cast<size_t>(tile) * 8u + (lane & 3u) * 2u;
-        lo = __builtin_nontemporal_load(src);
-        hi = __builtin_nontemporal_load(src + 1);
-    }
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(a.trellis) +
+                       static_cast<size_t>(valid ? tile : 0u) * 8u + (lane & 3u) * 2u;
+    const u32x4 lo = __builtin_nontemporal_load(src), hi = __builtin_nontemporal_load(src + 1);
     st.d[0] = lo.x; st.d[1] = lo.y; st.d[2] = lo.z; st.d[3] = lo.w;
     st.d[4] = hi.x; st.d[5] = hi.y; st.d[6] = hi.z; st.d[7] = hi.w;
     if (x_lds != nullptr) {
@@ -671,13 +670,11 @@ __device__ __forceinline__ void ne_prefetch_codes(const MoeGemv &m, uint32_t k, 
     uint32_t tile, column;
     bool valid;
     ne_tile(a, it.y, lane, tile, valid, column);
+    // no branch around the loads, as in ne_prefetch
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
-    if (valid) {
-        const u32x4 *src = reinterpret_cast<const u32x4 *>(a.trellis) + static_cast<size_t>(tile) * 8u + (lane & 3u) * 2u;
-        lo = __builtin_nontemporal_load(src);
-        hi = __builtin_nontemporal_load(src + 1);
-    }
+    const u32x4 *src =
+        reinterpret_cast<const u32x4 *>(a.trellis) + static_cast<size_t>(valid ? tile : 0u) * 8u + (lane & 3u) * 2u;
+    const u32x4 lo = __builtin_nontemporal_load(src), hi = __builtin_nontemporal_load(src + 1);
     st.d[0] = lo.x; st.d[1] = lo.y; st.d[2] = lo.z; st.d[3] = lo.w;
     st.d[4] = hi.x; st.d[5] = hi.y; st.d[6] = hi.z; st.d[7] = hi.w;
 }
@@ -2326,9 +2323,6 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_decode_few(MoeDecodeFew a)
     const uint32_t gu_k = from_top % a.gu.ne_items, gu_first = (from_top / a.gu.ne_items) * gu_per;
     const uint32_t dn_k = from_top % a.dn.ne_items, dn_first = (from_top / a.dn.ne_items) * dn_per;
     NeStage gu_st;
-    if (gu_unit) {
-        ne_prefetch_codes(a.gu, gu_k, lane, gu_st);
-    }
     uint32_t barriers = 0;
     auto block_barrier = [&]() {
         __builtin_amdgcn_s_waitcnt(kWaitLds);
@@ -2402,6 +2396,11 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_decode_few(MoeDecodeFew a)
     __syncthreads();  // every chain's logits out; the staged rows are free
     if (threadIdx.x == 0) {
         coherent_add(few_word(sync, few_sync::kLogits + xcd), 1u);
+    }
+    // the shared gate/up unit's codes, needed after the routing (issued
+    // before the router chains, their wait held the chains back)
+    if (gu_unit) {
+        ne_prefetch_codes(a.gu, gu_k, lane, gu_st);
     }
     // the codebook plane and the NE table (its words first; the plane's wait
     // covers them)
